@@ -1,0 +1,239 @@
+"""Benchmark of the fused sequence-mixing kernels on one MI355X.
+
+Headline (one JSON line, BASELINE.json metric): the config-2 Mamba selective scan,
+forward + backward (B=8, T=2048, D=1536, N=16; u, dt, z bf16; A, B, C, D f32), as
+whole-step algorithmic HBM GB/s.  A "step" is one forward (writing the backward's
+state checkpoints) plus one backward over one batch of synthetic input already
+resident in HBM.  The other configs are reported under "configs" (not the value).
+
+Algorithmic bytes (per call, what roofline.achieved divides by):
+  selective scan fwd = 4*B*T*D*2 (u, dt, z, y) + 2*B*T*N*4 (B, C) + D*N*4 + D*4
+  selective scan bwd = 7*B*T*D*2 (u, dt, z, dy in; du, ddt, dz out) + 4*B*T*N*4 + 2*(D*N*4 + D*4)
+  MinGRU fwd = 3*B*T*H*s, bwd = 6*B*T*H*s (s = element size)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def ss_bytes(B, T, D, N):
+    fwd = 4 * B * T * D * 2 + 2 * B * T * N * 4 + D * N * 4 + D * 4
+    bwd = 7 * B * T * D * 2 + 4 * B * T * N * 4 + 2 * (D * N * 4 + D * 4)
+    return fwd, bwd
+
+
+class EventTimer:
+    """Accumulates the duration of enqueued work with HIP events on the current stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+
+    def __enter__(self):
+        self.s = self.torch.cuda.Event(enable_timing=True)
+        self.e = self.torch.cuda.Event(enable_timing=True)
+        self.s.record()
+        return self
+
+    def __exit__(self, *a):
+        self.e.record()
+        self.pairs.append((self.s, self.e))
+
+    def mean_ms(self):
+        self.torch.cuda.synchronize()
+        return float(np.mean([s.elapsed_time(e) for s, e in self.pairs]))
+
+
+def bench_selective_scan(torch, steps, warmup, B=8, T=2048, D=1536, N=16):
+    from edifice_amd import _native as nat
+    from edifice_amd import fused_scan as fs
+
+    g = torch.Generator(device="cuda").manual_seed(2000)
+    dev = "cuda"
+    bf, f32 = torch.bfloat16, torch.float32
+    x = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    dt = torch.nn.functional.softplus(torch.randn(B, T, D, device=dev, generator=g) - 4).to(bf)
+    A = -torch.exp(torch.rand(D, N, device=dev, generator=g) * np.log(16.0))
+    Bm = torch.randn(B, T, N, device=dev, generator=g)
+    Cm = torch.randn(B, T, N, device=dev, generator=g)
+    Dv = torch.randn(D, device=dev, generator=g)
+    z = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    dy = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    out = torch.empty_like(x)
+    states = torch.empty(nat.query("edf_selective_scan_states_bytes", B, T, D, N) // 4, dtype=f32, device=dev)
+    dx, ddt, dz = torch.empty_like(x), torch.empty_like(x), torch.empty_like(x)
+    dA = torch.empty(D, N, dtype=f32, device=dev)
+    dB = torch.empty(B, T, N, dtype=f32, device=dev)
+    dC = torch.empty(B, T, N, dtype=f32, device=dev)
+    dD = torch.empty(D, dtype=f32, device=dev)
+    wsb = nat.query("edf_selective_scan_backward_workspace_bytes", B, T, D, N, 0, 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_selective_scan", stream, P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(out),
+                 P(states), None, 0, B, T, D, N, 1, 0, 0)
+
+    def bwd():
+        nat.call("edf_fused_selective_scan_backward", stream, P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(dy),
+                 P(states), P(dx), P(ddt), P(dA), P(dB), P(dC), P(dD), P(dz), P(ws), wsb, B, T, D, N, 1, 0, 0)
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    tf, tb = EventTimer(torch), EventTimer(torch)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        with tf:
+            fwd()
+        with tb:
+            bwd()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    fb, bb = ss_bytes(B, T, D, N)
+    fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
+    _ = fs  # imported for its side effect of validating the package import
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, step_ms=wall * 1e3, fwd_bytes=fb, bwd_bytes=bb,
+                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6, step_gbs=(fb + bb) / (wall * 1e3) / 1e6)
+
+
+def bench_mingru(torch, steps, warmup, B, T, H, dtype):
+    from edifice_amd import _native as nat
+
+    dev = "cuda"
+    g = torch.Generator(device="cuda").manual_seed(1000)
+    gates = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
+    cand = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
+    dy = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
+    out, dg, dc = torch.empty_like(gates), torch.empty_like(gates), torch.empty_like(gates)
+    flag = 1 if dtype == torch.bfloat16 else 0
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_mingru", stream, P(gates), P(cand), P(out), B, T, H, flag)
+
+    def bwd():
+        nat.call("edf_mingru_backward", stream, P(gates), P(cand), P(out), P(dy), P(dg), P(dc), B, T, H, flag)
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    tf, tb = EventTimer(torch), EventTimer(torch)
+    for _ in range(steps):
+        with tf:
+            fwd()
+        with tb:
+            bwd()
+    s = gates.element_size()
+    fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
+    fb, bb = 3 * B * T * H * s, 6 * B * T * H * s
+    return dict(shape=[B, T, H], dtype=str(dtype).replace("torch.", ""), fwd_us=fwd_ms * 1e3, bwd_us=bwd_ms * 1e3,
+                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
+
+
+def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
+    """Time the C restatement (oracle/cref.c, OpenMP f32) on the config-2 selective-scan
+    workload (about 3 s per fwd+bwd step on 8 host cores); returns GB/s under the same
+    byte accounting as the GPU figure."""
+    from oracle import cbuild
+
+    lib = cbuild.lib()
+    rng = np.random.default_rng(7)
+    f32 = np.float32
+    x = rng.normal(size=(B, T, D)).astype(f32)
+    dt = np.log1p(np.exp(rng.normal(size=(B, T, D)) - 4)).astype(f32)
+    A = (-np.exp(rng.uniform(0, np.log(16), size=(D, N)))).astype(f32)
+    Bm, Cm = (rng.normal(size=(B, T, N)).astype(f32) for _ in range(2))
+    Dv = rng.normal(size=D).astype(f32)
+    z, dy = (rng.normal(size=(B, T, D)).astype(f32) for _ in range(2))
+    out, dx, ddt, dz = (np.empty_like(x) for _ in range(4))
+    dA, dB, dC, dD = np.zeros_like(A), np.zeros_like(Bm), np.zeros_like(Cm), np.zeros_like(Dv)
+    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        lib.cref_selective_scan_fwd(P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(out), B, T, D, N)
+        lib.cref_selective_scan_bwd(P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(dy), P(dx), P(ddt), P(dA),
+                                    P(dB), P(dC), P(dD), P(dz), B, T, D, N)
+        times.append(time.perf_counter() - t0)
+    fb, bb = ss_bytes(B, T, D, N)
+    t = float(np.median(times))
+    lib.cref_threads.restype = ctypes.c_int
+    return dict(value=(fb + bb) / t / 1e9, unit="GB/s", cores=int(lib.cref_threads()), kind="port",
+                sample=f"C restatement (Nx unavailable), selective scan fwd+bwd f32, B={B} T={T} D={D} N={N} "
+                       f"(the full config-2 workload), median of {reps}, {t:.2f} s per step")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, 'How it would shard')",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    only = set(filter(None, args.only.split(",")))
+    want = (lambda k: not only or k in only)  # noqa: E731
+    configs = {}
+    if want("mingru"):
+        configs["c1_mingru_f32_4x60x256"] = bench_mingru(torch, args.steps, args.warmup, 4, 60, 256, torch.float32)
+        for dt in (torch.bfloat16, torch.float32):
+            key = f"mingru_bw_{str(dt).replace('torch.', '')}_8x2048x1536"
+            configs[key] = bench_mingru(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
+    ss = bench_selective_scan(torch, args.steps, args.warmup)
+    configs["c2_selective_scan"] = ss
+    dominant = "ss_bwd" if ss["bwd_ms"] >= ss["fwd_ms"] else "ss_fwd"
+    dom_ms = max(ss["bwd_ms"], ss["fwd_ms"])
+    dom_bytes = ss["bwd_bytes"] if dominant == "ss_bwd" else ss["fwd_bytes"]
+    achieved = dom_bytes / dom_ms / 1e6
+    line = {
+        "metric": "scan HBM GB/s (% of peak); delta-rule & flash-attn fwd+bwd TFLOP/s (% MFMA)",
+        "value": round(ss["step_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ss["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 io / f32 math",
+        "data": "synthetic (config-2 distributions, seeded torch generator)",
+        "config": {"workload": "config 2: Mamba selective scan fwd+bwd, B=8 T=2048 D=1536 N=16, u/dt/z bf16, "
+                               "A/B/C/D f32, D skip + silu(z) gate", "batch": 8, "seq_len": 2048, "d_inner": 1536,
+                   "d_state": 16},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "configs": configs,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_selective_scan()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

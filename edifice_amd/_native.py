@@ -1,0 +1,69 @@
+"""ctypes binding of ``libedifice_hip.so`` (the C ABI in ``include/edifice_hip.h``).
+
+The library is loaded lazily; if it has not been built, every op raises
+``EdificeHipError`` — there is no CPU fallback on the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from .build import lib_path
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+S = ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/edifice_hip.h
+SIGNATURES = {
+    "edf_version": (I, []),
+    "edf_last_error": (ctypes.c_char_p, []),
+    "edf_fused_mingru_scan": (I, [P, P, P, P, P, I, I, I, I]),
+    "edf_fused_mingru_scan_backward": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I]),
+    "edf_mingru": (I, [P, P, P, P, I, I, I, I]),
+    "edf_mingru_backward": (I, [P, P, P, P, P, P, P, I, I, I, I]),
+    "edf_fused_minlstm_scan": (I, [P, P, P, P, P, P, I, I, I, I]),
+    "edf_fused_minlstm_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I]),
+    "edf_minlstm": (I, [P, P, P, P, P, I, I, I, I]),
+    "edf_minlstm_backward": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I]),
+    "edf_fused_selective_scan": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
+    "edf_selective_scan_states_bytes": (S, [I, I, I, I]),
+    "edf_selective_scan_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_selective_scan_backward": (
+        I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
+    "edf_selective_scan_backward_workspace_bytes": (S, [I, I, I, I, I, I]),
+}
+
+
+class EdificeHipError(RuntimeError):
+    """Raised when the HIP library is missing or an entry point returns an error."""
+
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = lib_path()
+        if not os.path.exists(path):
+            raise EdificeHipError(
+                f"{path} is not built; run `python -m edifice_amd.build` (edifice_amd has no CPU fallback)")
+        handle = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def call(name: str, *args) -> None:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().edf_last_error().decode(errors="replace")
+        raise EdificeHipError(f"{name} failed (code {rc}): {msg}")
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(lib(), name)(*args))

@@ -1,0 +1,51 @@
+// Shared device helpers for the gfx950 kernels of edifice_amd.
+//
+// Storage types: every tensor is either IEEE float32 or bfloat16 (raw __bf16).
+// Arithmetic is always float32 (bf16 is an I/O format only), matching the
+// reference contract "bf16 I/O, f32 math" (native/cuda/precision.cuh:18-23).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define EDF_DEVICE __device__ __forceinline__
+
+namespace edf {
+
+typedef __bf16 bf16;
+
+// ---- scalar load / store with conversion -----------------------------------
+EDF_DEVICE float to_f32(float v) { return v; }
+EDF_DEVICE float to_f32(bf16 v) { return (float)v; }
+
+template <typename T> EDF_DEVICE T from_f32(float v);
+template <> EDF_DEVICE float from_f32<float>(float v) { return v; }
+template <> EDF_DEVICE bf16 from_f32<bf16>(float v) { return (bf16)v; }  // RNE
+
+template <typename T> EDF_DEVICE float ld(const T* p, long i) { return to_f32(p[i]); }
+template <typename T> EDF_DEVICE void st(T* p, long i, float v) { p[i] = from_f32<T>(v); }
+
+// ---- math -------------------------------------------------------------------
+constexpr float LOG2E = 1.4426950408889634f;
+
+EDF_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+EDF_DEVICE float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)); exact reciprocal keeps f32 parity.
+EDF_DEVICE float sigmoidf(float x) { return 1.0f / (1.0f + fast_exp2(-x * LOG2E)); }
+
+EDF_DEVICE float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
+
+// ---- launch-shape helpers -----------------------------------------------------
+// MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs, each
+// with a private L2.  remap_xcd() turns the hardware id into a logical id such
+// that logical ids L, L+1, ... run on the same XCD, so neighbouring tiles that
+// share cache lines also share an L2.  Identity when the grid is not a multiple
+// of 8.
+EDF_DEVICE int remap_xcd(int id, int total) {
+  if ((total & 7) != 0) return id;
+  const int per = total >> 3;
+  return (id & 7) * per + (id >> 3);
+}
+
+}  // namespace edf

@@ -1,0 +1,193 @@
+"""Host-side mirror of ``Edifice.CUDA.FusedScan`` (lib/edifice/cuda/fused_scan.ex).
+
+Same op names, argument order and meaning as the Elixir module; tensors are torch
+tensors resident on the GPU (the role Nx/EXLA device buffers play in the
+reference).  Each op launches the HIP kernel through the C ABI on torch's current
+stream and is differentiable: the backward is the fused HIP backward kernel,
+which the reference only wires through ``Nx.Defn.Kernel.custom_grad``
+(e.g. fused_scan.ex:474-480, 2205-2209, 2606-2611, 3438-3442).
+
+There is no CPU or eager fallback: CPU tensors, unsupported dtypes or a missing
+library raise ``EdificeHipError`` (the reference's fallback tier is the parity
+oracle in ``oracle/``, which the product never calls).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _native as nat
+from ._native import EdificeHipError
+
+F32, BF16 = 0, 1
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+SS_DT_PER_CHANNEL, SS_DT_MEAN = 0, 1
+
+
+def dtype_flag(t: torch.Tensor) -> int:
+    """0 = f32, 1 = bf16, as ``dtype_flag/1`` (fused_scan.ex:39-44); other dtypes raise."""
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise EdificeHipError(f"unsupported dtype {t.dtype} (float32 or bfloat16)") from None
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise EdificeHipError("edifice_amd ops need GPU tensors (no CPU fallback)")
+        if not t.is_contiguous():
+            raise EdificeHipError("edifice_amd ops need contiguous tensors")
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _same(dtype_of, *ts):
+    for t in ts:
+        if t is not None and t.dtype != dtype_of.dtype:
+            raise EdificeHipError(f"dtype mismatch: {t.dtype} vs {dtype_of.dtype}")
+
+
+def _c(t):
+    return None if t is None else t.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# MinGRU / MinLSTM
+# ---------------------------------------------------------------------------
+
+class _MinGRU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gates, cand):
+        gates, cand = gates.contiguous(), cand.contiguous()
+        _dev(gates, cand)
+        _same(gates, cand)
+        bsz, seq, hid = gates.shape
+        out = torch.empty_like(gates)
+        nat.call("edf_mingru", _stream(), _p(gates), _p(cand), _p(out), bsz, seq, hid, dtype_flag(gates))
+        ctx.save_for_backward(gates, cand, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        gates, cand, out = ctx.saved_tensors
+        dy = dy.contiguous().to(gates.dtype)
+        bsz, seq, hid = gates.shape
+        dg = torch.empty_like(gates)
+        dc = torch.empty_like(cand)
+        nat.call("edf_mingru_backward", _stream(), _p(gates), _p(cand), _p(out), _p(dy), _p(dg), _p(dc),
+                 bsz, seq, hid, dtype_flag(gates))
+        return dg, dc
+
+
+def mingru(gates: torch.Tensor, candidates: torch.Tensor) -> torch.Tensor:
+    """``FusedScan.mingru/2`` (fused_scan.ex:60-74): gate logits [B,T,H], candidates [B,T,H].
+
+    z = sigmoid(gates) is fused into the kernel; h0 = 0; returns all hidden states.
+    """
+    return _MinGRU.apply(gates, candidates)
+
+
+class _MinLSTM(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, fg, ig, cand):
+        fg, ig, cand = fg.contiguous(), ig.contiguous(), cand.contiguous()
+        _dev(fg, ig, cand)
+        _same(fg, ig, cand)
+        bsz, seq, hid = fg.shape
+        out = torch.empty_like(fg)
+        nat.call("edf_minlstm", _stream(), _p(fg), _p(ig), _p(cand), _p(out), bsz, seq, hid, dtype_flag(fg))
+        ctx.save_for_backward(fg, ig, cand, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        fg, ig, cand, out = ctx.saved_tensors
+        dy = dy.contiguous().to(fg.dtype)
+        bsz, seq, hid = fg.shape
+        df, di, dc = torch.empty_like(fg), torch.empty_like(ig), torch.empty_like(cand)
+        nat.call("edf_minlstm_backward", _stream(), _p(fg), _p(ig), _p(cand), _p(out), _p(dy), _p(df), _p(di),
+                 _p(dc), bsz, seq, hid, dtype_flag(fg))
+        return df, di, dc
+
+
+def minlstm(forget_gates: torch.Tensor, input_gates: torch.Tensor, candidates: torch.Tensor) -> torch.Tensor:
+    """``FusedScan.minlstm/3`` (fused_scan.ex:77-91): gate logits, sigmoids fused, h0 = 0."""
+    return _MinLSTM.apply(forget_gates, input_gates, candidates)
+
+
+# ---------------------------------------------------------------------------
+# Selective scan
+# ---------------------------------------------------------------------------
+
+def _u8(nbytes, like):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=like.device)
+
+
+class _SelectiveScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, dt, A, B, C, D, z, mode):
+        x, dt, A, B, C, D, z = (_c(t) for t in (x, dt, A, B, C, D, z))
+        _dev(x, dt, A, B, C, D, z)
+        _same(x, dt, z)
+        _same(A, B, C, D)
+        bsz, seq, dim = x.shape
+        n = A.shape[1]
+        io, par = dtype_flag(x), dtype_flag(A)
+        out = torch.empty_like(x)
+        need_grad = any(ctx.needs_input_grad[:7])
+        states = None
+        if need_grad:
+            sb = nat.query("edf_selective_scan_states_bytes", bsz, seq, dim, n)
+            states = torch.empty(sb // 4, dtype=torch.float32, device=x.device)
+        wsb = nat.query("edf_selective_scan_workspace_bytes", bsz, seq, dim, n, mode)
+        ws = _u8(wsb, x) if wsb else None
+        nat.call("edf_fused_selective_scan", _stream(), _p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(out),
+                 _p(states), _p(ws), wsb, bsz, seq, dim, n, io, par, mode)
+        ctx.mode = mode
+        ctx.save_for_backward(x, dt, A, B, C, D, z, states)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, dt, A, B, C, D, z, states = ctx.saved_tensors
+        dout = dout.contiguous().to(x.dtype)
+        bsz, seq, dim = x.shape
+        n = A.shape[1]
+        io, par = dtype_flag(x), dtype_flag(A)
+        f32 = dict(dtype=torch.float32, device=x.device)
+        dx, ddt = torch.empty_like(x), torch.empty_like(dt)
+        dA = torch.empty((dim, n), **f32)
+        dB = torch.empty((bsz, seq, n), **f32)
+        dC = torch.empty((bsz, seq, n), **f32)
+        dD = torch.empty((dim,), **f32) if D is not None else None
+        dz = torch.empty_like(z) if z is not None else None
+        wsb = nat.query("edf_selective_scan_backward_workspace_bytes", bsz, seq, dim, n, ctx.mode,
+                        int(states is not None))
+        ws = _u8(wsb, x)
+        nat.call("edf_fused_selective_scan_backward", _stream(), _p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z),
+                 _p(dout), _p(states), _p(dx), _p(ddt), _p(dA), _p(dB), _p(dC), _p(dD), _p(dz), _p(ws), wsb,
+                 bsz, seq, dim, n, io, par, ctx.mode)
+        cast = (lambda t, like: None if t is None else t.to(like.dtype))
+        return dx, ddt, cast(dA, A), cast(dB, B), cast(dC, C), cast(dD, D), dz, None
+
+
+def selective_scan(x, dt, a, b, c, d=None, z=None, *, dt_mode: str = "channel"):
+    """``FusedScan.selective_scan/5`` (fused_scan.ex:370-384) plus optional D skip and silu(z) gate.
+
+    x, dt (and z): [B, T, D]; a: [D, N]; b, c: [B, T, N]; d: [D].  dt is clipped to
+    [1e-3, 0.1] inside the kernel.  dt_mode="channel" is the kernel semantics
+    (B_bar = dt B per channel, fused_selective_scan.cu:68-90); "mean" is the Mamba
+    block CPU semantics (B_bar = mean_d(dt) B, common.ex:402-445).
+    """
+    mode = {"channel": SS_DT_PER_CHANNEL, "mean": SS_DT_MEAN}[dt_mode]
+    return _SelectiveScan.apply(x, dt, a, b, c, d, z, mode)

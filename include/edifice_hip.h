@@ -1,0 +1,149 @@
+/*
+ * edifice_hip.h — C ABI of the MI355X (gfx950) fused sequence-mixing kernels.
+ *
+ * This is the drop-in boundary that replaces Edifice's CUDA NIF bridge
+ * (c_src/edifice_cuda_nif.c) and the kernel-library launch wrappers it dlsym's
+ * (`fused_<op>_launch`, typedefs at c_src/edifice_cuda_nif.c:31-438).  Every
+ * entry point below names the reference NIF it replaces (name/arity from the
+ * NIF table at c_src/edifice_cuda_nif.c:4458-4507, Elixir stubs in
+ * lib/edifice/cuda/nif.ex) and keeps that NIF's argument order and meaning.
+ *
+ * Conventions (differences from the reference are deliberate, see the notes):
+ *   - All tensor arguments are device pointers (what the reference receives as
+ *     u64 addresses from Nx.to_pointer(mode: :local)); sizes are plain ints.
+ *   - Outputs are CALLER-OWNED: the reference NIF allocated the output with
+ *     cudaMalloc per call; here the caller (the NIF shim, or any host) passes the
+ *     output buffer(s).  Backward ops take one pointer per gradient; passing
+ *     consecutive slices of one buffer reproduces the reference's concatenated
+ *     [d1 | d2 | ...] output layout.
+ *   - No allocation happens inside any entry point.  Ops that need scratch
+ *     memory take (workspace, workspace_bytes) and export a *_workspace_bytes
+ *     query.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream).  Kernels are
+ *     enqueued asynchronously; nothing synchronises the device (the reference
+ *     called cudaDeviceSynchronize after every launch).
+ *   - dtype: 0 = float32, 1 = bfloat16, the reference's dtype flag
+ *     (lib/edifice/cuda/fused_scan.ex:39-44).  Arithmetic is always float32.
+ *   - Return value: EDF_OK (0) or an EDF_ERR_* code; edf_last_error() returns
+ *     a thread-local message for the last failing call on this thread
+ *     (the reference returned {:error, "..."} strings).
+ */
+#ifndef EDIFICE_HIP_H
+#define EDIFICE_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EDF_ABI_VERSION 1
+
+enum {
+  EDF_OK = 0,
+  EDF_ERR_INVALID_ARG = 1, /* "dimensions must be positive", bad dtype, null pointer */
+  EDF_ERR_UNSUPPORTED = 2, /* shape / dtype combination this build does not implement */
+  EDF_ERR_LAUNCH = 3,      /* "... kernel launch failed" */
+  EDF_ERR_WORKSPACE = 4    /* workspace missing or smaller than the *_workspace_bytes query */
+};
+
+enum { EDF_F32 = 0, EDF_BF16 = 1 };
+
+/* selective-scan discretisation of B: per-channel dt (kernel semantics,
+ * native/cuda/fused_selective_scan.cu:68-90) or mean over channels
+ * (Mamba block CPU semantics, lib/edifice/ssm/common.ex:402-445). */
+enum { EDF_SS_DT_PER_CHANNEL = 0, EDF_SS_DT_MEAN = 1 };
+
+int edf_version(void);
+const char* edf_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * MinGRU   h_t = (1 - z_t) h_{t-1} + z_t cand_t        tensors [B, T, H], h0 [B, H]
+ * ------------------------------------------------------------------------ */
+
+/* Replaces fused_mingru_scan/7 (gates_ptr, cand_ptr, h0_ptr, batch, seq_len,
+ * hidden, dtype) — c_src/edifice_cuda_nif.c:630-704, nif.ex:29-30 — and
+ * fused_mingru_scan_launch (native/cuda/fused_mingru_scan.cu:82-101).
+ * z is post-sigmoid.  h0 may be NULL (zeros). */
+int edf_fused_mingru_scan(void* stream, const void* z, const void* cand, const void* h0, void* out, int batch,
+                          int seq_len, int hidden, int dtype);
+
+/* Replaces fused_mingru_scan_backward/9 (z, cand, h0, fwd, dy, batch, seq_len,
+ * hidden, dtype), c_src/edifice_cuda_nif.c:2508-2514; outputs dz (post-sigmoid),
+ * dcand, dh0 (grad_h0 may be NULL). */
+int edf_fused_mingru_scan_backward(void* stream, const void* z, const void* cand, const void* h0,
+                                   const void* forward_out, const void* grad_out, void* grad_z, void* grad_cand,
+                                   void* grad_h0, int batch, int seq_len, int hidden, int dtype);
+
+/* Whole FusedScan.mingru/2 (lib/edifice/cuda/fused_scan.ex:60-74): gate logits
+ * in, sigmoid fused, h0 = 0.  The backward returns d(gate logits), i.e. the chain
+ * rule dz z (1 - z) of fused_scan.ex:474-480 fused into the kernel. */
+int edf_mingru(void* stream, const void* gates, const void* cand, void* out, int batch, int seq_len, int hidden,
+               int dtype);
+int edf_mingru_backward(void* stream, const void* gates, const void* cand, const void* forward_out,
+                        const void* grad_out, void* grad_gates, void* grad_cand, int batch, int seq_len, int hidden,
+                        int dtype);
+
+/* ------------------------------------------------------------------------
+ * MinLSTM  c_t = f'_t c_{t-1} + i'_t cand_t,  f' = f/(f+i+1e-6), i' = i/(f+i+1e-6)
+ * ------------------------------------------------------------------------ */
+
+/* Replaces fused_minlstm_scan/8 (forget, input, cand, h0, batch, seq_len, hidden,
+ * dtype), nif.ex:33-34; gates post-sigmoid, h0 may be NULL. */
+int edf_fused_minlstm_scan(void* stream, const void* f, const void* i, const void* cand, const void* h0, void* out,
+                           int batch, int seq_len, int hidden, int dtype);
+
+/* Replaces fused_minlstm_scan_backward/10; outputs df, di (post-sigmoid),
+ * dcand, dh0 (grad_h0 may be NULL). */
+int edf_fused_minlstm_scan_backward(void* stream, const void* f, const void* i, const void* cand, const void* h0,
+                                    const void* forward_out, const void* grad_out, void* grad_f, void* grad_i,
+                                    void* grad_cand, void* grad_h0, int batch, int seq_len, int hidden, int dtype);
+
+/* Whole FusedScan.minlstm/3 (fused_scan.ex:77-91) with fused sigmoids; backward
+ * returns gradients w.r.t. the gate logits (fused_scan.ex:502-511). */
+int edf_minlstm(void* stream, const void* forget_gates, const void* input_gates, const void* cand, void* out,
+                int batch, int seq_len, int hidden, int dtype);
+int edf_minlstm_backward(void* stream, const void* forget_gates, const void* input_gates, const void* cand,
+                         const void* forward_out, const void* grad_out, void* grad_forget, void* grad_input,
+                         void* grad_cand, int batch, int seq_len, int hidden, int dtype);
+
+/* ------------------------------------------------------------------------
+ * Mamba selective scan
+ *   x, dt, z, out, grad_x, grad_dt, grad_z: [B, T, D] in io_dtype
+ *   A [D, N], B, C [B, T, N], D [D]: param_dtype; grad_A/B/C/D: float32
+ *   dt is clipped to [1e-3, 0.1]; ddt is zero where dt was clipped.
+ * ------------------------------------------------------------------------ */
+
+/* Replaces fused_selective_scan/10 (x, dt, A, B, C, batch, seq_len, hidden,
+ * state, dtype), c_src/edifice_cuda_nif.c:1470-1503, and
+ * fused_selective_scan_launch (native/cuda/fused_selective_scan.cu:105-123).
+ * Extensions: per-tensor dtypes (io vs param), optional D skip (NULL = none)
+ * and silu(z) gate (NULL = none), and `states`, an optional float32 buffer of
+ * edf_selective_scan_states_bytes() that receives checkpoints for the backward.
+ * state must be 1, 2, 4, 8, 16 or 32 (the reference allowed <= 32). */
+int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const void* A, const void* B, const void* C,
+                             const void* D, const void* z, void* out, void* states, void* workspace,
+                             size_t workspace_bytes, int batch, int seq_len, int hidden, int state, int io_dtype,
+                             int param_dtype, int mode);
+size_t edf_selective_scan_states_bytes(int batch, int seq_len, int hidden, int state);
+size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode);
+
+/* Replaces fused_selective_scan_backward/11 (x, dt, A, B, C, dy, batch, seq_len,
+ * hidden, state, dtype), whose concatenated output was [dx | ddt | dB | dC]
+ * (native/cuda/fused_selective_scan_backward.cu:198-238).  Adds grad_A, grad_D,
+ * grad_z (each may be NULL).  `states` may be NULL: the checkpoints are then
+ * recomputed into the workspace.  state must be 4, 8 or 16. */
+int edf_fused_selective_scan_backward(void* stream, const void* x, const void* dt, const void* A, const void* B,
+                                      const void* C, const void* D, const void* z, const void* grad_out,
+                                      const void* states, void* grad_x, void* grad_dt, void* grad_A, void* grad_B,
+                                      void* grad_C, void* grad_D, void* grad_z, void* workspace,
+                                      size_t workspace_bytes, int batch, int seq_len, int hidden, int state,
+                                      int io_dtype, int param_dtype, int mode);
+size_t edf_selective_scan_backward_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode,
+                                                   int have_states);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EDIFICE_HIP_H */

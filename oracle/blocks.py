@@ -1,0 +1,163 @@
+"""Block-level restatement of Edifice's sequence-mixing callers — TEST INFRASTRUCTURE ONLY.
+
+Used to pin the scan restatements (and, in GPU tests, the HIP kernels) against the
+reference's own model-level fixtures ``test/fixtures/numerical/*_random.safetensors``,
+which hold PyTorch-generated weights, inputs, expected outputs and (DeltaNet) the input
+gradient.  The models mirror the Edifice blocks:
+
+  MinGRU   lib/edifice/recurrent/min_gru.ex:272-295 (layer), :305-326 (scan)
+  DeltaNet lib/edifice/recurrent/delta_net.ex:197-219 (layer), :275-307 (projection split,
+           sigmoid beta, key L2 norm with eps 1e-6 inside the sqrt)
+  Mamba    lib/edifice/ssm/common.ex:210-279 (block), :333-373 (B/C/dt projections),
+           :402-471 (dt-mean discretisation and output)
+  GQA      causal grouped-query attention block, fed through the flash-attention op
+           (lib/edifice/blocks/sdpa.ex:74-91 routes causal self-attention to flash)
+
+Dense layers use the fixture's PyTorch layout (weight [out, in]).  Layer norm uses
+eps 1e-5, the value the fixtures were generated with.  The sequence-mixing op of each
+block is pluggable (``ops``) so the same model runs the numpy oracle or the HIP path;
+everything around it runs in float64 torch on the CPU (or the device of the input).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import scans
+
+LN_EPS = 1.0e-5
+
+
+def _np(t):
+    return t.detach().cpu().double().numpy()
+
+
+def _t(a, like):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device=like.device, dtype=like.dtype)
+
+
+class _OracleMinGRU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gates, cand):
+        ctx.save_for_backward(gates, cand)
+        return _t(scans.min_gru_scan(_np(gates), _np(cand)), gates)
+
+    @staticmethod
+    def backward(ctx, dy):
+        gates, cand = ctx.saved_tensors
+        dg, dc = scans.min_gru_scan_backward(_np(gates), _np(cand), _np(dy))
+        return _t(dg, gates), _t(dc, cand)
+
+
+class _OracleDelta(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, beta):
+        ctx.save_for_backward(q, k, v, beta)
+        return _t(scans.delta_rule(_np(q), _np(k), _np(v), _np(beta)), q)
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, beta = ctx.saved_tensors
+        g = scans.delta_rule_backward(_np(q), _np(k), _np(v), _np(beta), _np(do))
+        return _t(g["dq"], q), _t(g["dk"], k), _t(g["dv"], v), _t(g["dbeta"], beta)
+
+
+def oracle_ops():
+    """The numpy oracle as pluggable block ops (forward + hand-derived backward)."""
+    return {
+        "mingru": _OracleMinGRU.apply,
+        "delta_net": _OracleDelta.apply,
+        "selective_scan_mean": lambda x, dt, A, B, C: _t(
+            scans.selective_scan(_np(x), _np(dt), _np(A), _np(B), _np(C), mode="mean"), x),
+        "causal_attention": lambda q, k, v: _t(
+            scans.flash_attention(_np(q), _np(k), _np(v), causal=True), q),
+    }
+
+
+def load_fixture(path):
+    from safetensors.numpy import load_file
+
+    return {k: torch.from_numpy(v.astype(np.float64)) for k, v in load_file(path).items()}
+
+
+def _dense(w, prefix, x):
+    return F.linear(x, w[prefix + ".weight"], w[prefix + ".bias"])
+
+
+def _ln(w, prefix, x):
+    return F.layer_norm(x, (x.shape[-1],), w[prefix + ".weight"], w[prefix + ".bias"], LN_EPS)
+
+
+def min_gru_model(w, x, ops):
+    """MinGRU.build/1: input projection, 2 x (LN -> gate/candidate -> scan -> residual), final LN."""
+    h = _dense(w, "weight.input_projection", x)
+    for li in range(2):
+        p = f"weight.layers.{li}"
+        n = _ln(w, p + ".norm", h)
+        h = h + ops["mingru"](_dense(w, p + ".gate", n), _dense(w, p + ".candidate", n))
+    return _ln(w, "weight.final_norm", h)[:, -1]
+
+
+def delta_net_model(w, x, ops, num_heads=4):
+    """DeltaNet.build/1 with embed == hidden (no input projection), 2 layers, final LN."""
+    h = x
+    bsz, seq, hid = x.shape
+    hd = hid // num_heads
+    for li in range(2):
+        p = f"weight.layers.{li}"
+        n = _ln(w, p + ".norm", h)
+        proj = _dense(w, p + ".qkvb_proj", n)
+        q, k, v, bpre = torch.split(proj, hid, dim=-1)
+        shp = (bsz, seq, num_heads, hd)
+        q, k, v = q.reshape(shp), k.reshape(shp), v.reshape(shp)
+        beta = torch.sigmoid(bpre).reshape(shp)
+        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + scans.KEY_NORM_EPS)
+        o = ops["delta_net"](q, k, v, beta).reshape(bsz, seq, hid)
+        h = h + _dense(w, p + ".out_proj", o)
+    return _ln(w, "weight.final_norm", h)[:, -1]
+
+
+def mamba_model(w, x, ops, state_size=8, conv_size=4):
+    """Mamba.build/1 via Common.build_model: 2 residual blocks, last timestep (no final LN)."""
+    h = x
+    for li in range(2):
+        p = f"weight.blocks.{li}"
+        n = _ln(w, p + ".norm", h)
+        xz = _dense(w, p + ".in_proj", n)
+        inner = xz.shape[-1] // 2
+        xb, zb = xz[..., :inner], xz[..., inner:]
+        seq = xb.shape[1]
+        conv = F.conv1d(xb.transpose(1, 2), w[p + ".dw_conv.weight"], w[p + ".dw_conv.bias"],
+                        padding=conv_size - 1, groups=inner)[..., :seq].transpose(1, 2)
+        xa = F.silu(conv)
+        bc = _dense(w, p + ".bc_proj", xa)
+        Bm, Cm = bc[..., :state_size], bc[..., state_size:]
+        dt = F.softplus(_dense(w, p + ".dt_proj", _dense(w, p + ".dt_rank_proj", xa)))
+        A = -(torch.arange(state_size, dtype=x.dtype, device=x.device) + 1.0)
+        A = A[None, :].expand(inner, state_size).contiguous()
+        y = ops["selective_scan_mean"](xa, dt, A, Bm, Cm)
+        h = h + _dense(w, p + ".out_proj", y * F.silu(zb))
+    return h[:, -1]
+
+
+def gqa_model(w, x, ops, num_heads=4, num_kv_heads=2):
+    """Causal GQA transformer, 2 blocks (attention + GELU FFN), final LN, last timestep."""
+    h = x
+    bsz, seq, hid = x.shape
+    hd = hid // num_heads
+    grp = num_heads // num_kv_heads
+    for li in range(2):
+        p = f"weight.blocks.{li}"
+        n = _ln(w, p + ".attn_norm", h)
+        q = _dense(w, p + ".attn.q_proj", n).reshape(bsz, seq, num_heads, hd).transpose(1, 2)
+        k = _dense(w, p + ".attn.k_proj", n).reshape(bsz, seq, num_kv_heads, hd).transpose(1, 2)
+        v = _dense(w, p + ".attn.v_proj", n).reshape(bsz, seq, num_kv_heads, hd).transpose(1, 2)
+        k = k.repeat_interleave(grp, dim=1).contiguous()
+        v = v.repeat_interleave(grp, dim=1).contiguous()
+        o = ops["causal_attention"](q.contiguous(), k, v)
+        o = o.transpose(1, 2).reshape(bsz, seq, hid)
+        h = h + _dense(w, p + ".attn.out_proj", o)
+        f = _ln(w, p + ".ffn_norm", h)
+        h = h + _dense(w, p + ".ffn_down", F.gelu(_dense(w, p + ".ffn_up", f)))
+    return _ln(w, "weight.final_norm", h)[:, -1]

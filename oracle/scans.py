@@ -1,0 +1,424 @@
+"""numpy float64 restatement of Edifice's fused sequence-mixing ops — TEST INFRASTRUCTURE ONLY.
+
+Only tests, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg may use
+this module, as the checker.  Every function cites the reference file:line whose
+semantics it restates (paths relative to the Edifice repository root).
+
+Layouts follow the reference exactly:
+  scans / delta rule   [batch, seq, hidden]  and  [batch, seq, heads, head_dim]
+  attention            [batch, heads, seq, head_dim]
+
+Pinning (what independently checks each function; see tests/test_oracle_*.py):
+  mingru_scan / _backward       seq_len=1 known answer (backward_kernels_test.exs:271-287),
+                                min_gru_random.safetensors block fixture, z≡1 / z≡0
+                                closed forms, torch autograd + finite differences.
+  minlstm_scan / _backward      f'+i'≈1 invariant, i≡0 ⇒ constant state, closed form
+                                at T=1, torch autograd + finite differences.
+  selective_scan (channel mode) B≡0 ⇒ y≡0; N=1, A=0 ⇒ cumulative sum; torch autograd
+                                of an independent associative-scan formulation.
+  selective_scan (mean mode)    mamba_random.safetensors block fixture.
+  selective_scan_backward       torch autograd of the forward, finite differences,
+                                clip mask ⇒ ddt=0 outside [1e-3, 0.1].
+  delta_rule                    delta_net_random.safetensors (forward and input
+                                gradient), β≡0 ⇒ o≡0, α≡1 ⇒ DeltaNet, T=1 closed form.
+  delta_rule_backward           delta_net_random.safetensors gradient.input, torch
+                                autograd of the forward, finite differences.
+  flash_attention / _backward   torch.nn.functional.scaled_dot_product_attention and
+                                its autograd, gqa_random.safetensors block fixture,
+                                causal row 0 == V[0], identical keys ⇒ mean of V.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+DT_MIN = 1.0e-3  # fused_selective_scan.cu:30, fused_scan.ex:1469
+DT_MAX = 0.1  # fused_selective_scan.cu:31
+MINLSTM_EPS = 1.0e-6  # min_lstm.ex:83-84, fused_minlstm_scan.cu:27
+KEY_NORM_EPS = 1.0e-6  # delta_net.ex:297-298, gated_delta_net.ex:383-386
+
+
+def _f64(*xs):
+    return [None if x is None else np.asarray(x, dtype=np.float64) for x in xs]
+
+
+def sigmoid(x):
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * (1.0 + np.tanh(0.5 * x))
+
+
+def silu(x):
+    return x * sigmoid(x)
+
+
+def softplus(x):
+    x = np.asarray(x, dtype=np.float64)
+    return np.logaddexp(0.0, x)
+
+
+# ---------------------------------------------------------------------------
+# MinGRU   h_t = (1 - z_t) h_{t-1} + z_t h~_t
+# ---------------------------------------------------------------------------
+
+def mingru_scan(z, cand, h0=None):
+    """Forward with post-sigmoid gates and explicit h0.
+
+    Follows ``mingru_scan_fallback`` (lib/edifice/cuda/fused_scan.ex:516-528) and the
+    kernel contract of native/cuda/fused_mingru_scan.cu:38-65.
+    """
+    z, cand, h0 = _f64(z, cand, h0)
+    bsz, seq, hid = z.shape
+    h = np.zeros((bsz, hid)) if h0 is None else h0.copy()
+    out = np.empty_like(z)
+    for t in range(seq):
+        h = (1.0 - z[:, t]) * h + z[:, t] * cand[:, t]
+        out[:, t] = h
+    return out
+
+
+def mingru_scan_backward(z, cand, h0, fwd, dy):
+    """Reverse pass -> (dz, dcand, dh0).
+
+    Follows ``mingru_backward_fallback`` (fused_scan.ex:548-581): dh accumulates the
+    upstream gradient, dz = dh (h~_t - h_{t-1}), dcand = dh z_t, carry dh (1 - z_t).
+    """
+    z, cand, h0, fwd, dy = _f64(z, cand, h0, fwd, dy)
+    bsz, seq, hid = z.shape
+    if h0 is None:
+        h0 = np.zeros((bsz, hid))
+    dz = np.empty_like(z)
+    dc = np.empty_like(z)
+    carry = np.zeros((bsz, hid))
+    for t in range(seq - 1, -1, -1):
+        dh = dy[:, t] + carry
+        h_prev = h0 if t == 0 else fwd[:, t - 1]
+        dz[:, t] = dh * (cand[:, t] - h_prev)
+        dc[:, t] = dh * z[:, t]
+        carry = dh * (1.0 - z[:, t])
+    return dz, dc, carry
+
+
+def min_gru_scan(gates, cand):
+    """Logit-level MinGRU: sigmoid applied first, h0 = 0 (min_gru.ex:305-326)."""
+    return mingru_scan(sigmoid(gates), cand, None)
+
+
+def min_gru_scan_backward(gates, cand, dy):
+    """Gradients of ``min_gru_scan`` w.r.t. (gates, cand).
+
+    The post-sigmoid gradient comes from ``mingru_scan_backward``; the chain rule
+    dz * z (1 - z) follows fused_scan.ex:474-480.
+    """
+    z = sigmoid(gates)
+    fwd = mingru_scan(z, cand, None)
+    dz, dc, _ = mingru_scan_backward(z, cand, None, fwd, dy)
+    return dz * z * (1.0 - z), dc
+
+
+# ---------------------------------------------------------------------------
+# MinLSTM  c_t = f'_t c_{t-1} + i'_t h~_t,  f' = f/(f+i+eps), i' = i/(f+i+eps)
+# ---------------------------------------------------------------------------
+
+def minlstm_scan(f, i, cand, h0=None):
+    """Forward with post-sigmoid gates (fused_scan.ex:583-602, fused_minlstm_scan.cu:37-68)."""
+    f, i, cand, h0 = _f64(f, i, cand, h0)
+    bsz, seq, hid = f.shape
+    s = f + (i + MINLSTM_EPS)
+    fn, inn = f / s, i / s
+    c = np.zeros((bsz, hid)) if h0 is None else h0.copy()
+    out = np.empty_like(f)
+    for t in range(seq):
+        c = fn[:, t] * c + inn[:, t] * cand[:, t]
+        out[:, t] = c
+    return out
+
+
+def minlstm_scan_backward(f, i, cand, h0, fwd, dy):
+    """Reverse pass -> (df, di, dcand, dh0), quotient rule through the normalisation.
+
+    Follows ``minlstm_backward_fallback`` (fused_scan.ex:623-677).
+    """
+    f, i, cand, h0, fwd, dy = _f64(f, i, cand, h0, fwd, dy)
+    bsz, seq, hid = f.shape
+    if h0 is None:
+        h0 = np.zeros((bsz, hid))
+    df = np.empty_like(f)
+    di = np.empty_like(f)
+    dcand = np.empty_like(f)
+    carry = np.zeros((bsz, hid))
+    for t in range(seq - 1, -1, -1):
+        dc = dy[:, t] + carry
+        ft, it = f[:, t], i[:, t]
+        s = ft + (it + MINLSTM_EPS)
+        c_prev = h0 if t == 0 else fwd[:, t - 1]
+        df_n = dc * c_prev
+        di_n = dc * cand[:, t]
+        dcand[:, t] = dc * (it / s)
+        carry = dc * (ft / s)
+        s2 = s * s
+        df[:, t] = (df_n * (it + MINLSTM_EPS) - di_n * it) / s2
+        di[:, t] = (-df_n * ft + di_n * (ft + MINLSTM_EPS)) / s2
+    return df, di, dcand, carry
+
+
+def min_lstm_scan(forget_gates, input_gates, cand):
+    """Logit-level MinLSTM (min_lstm.ex:304-334)."""
+    return minlstm_scan(sigmoid(forget_gates), sigmoid(input_gates), cand, None)
+
+
+# ---------------------------------------------------------------------------
+# Selective scan (Mamba)
+# ---------------------------------------------------------------------------
+
+def selective_scan(x, dt, A, B, C, D=None, z=None, mode="channel", return_states=False):
+    """Mamba selective scan, forward.
+
+    mode="channel" — kernel semantics: dt clipped to [1e-3, 0.1], A_bar = exp(dt A[d,n]),
+      B_bar = dt B (native/cuda/fused_selective_scan.cu:41-91; restated in
+      test/edifice/cuda/backward_kernels_test.exs:1563-1586).
+    mode="mean" — block CPU semantics: B_bar = mean_d(clip(dt)) B
+      (lib/edifice/ssm/common.ex:402-445 discretize_ssm, :492-513 sequential_scan,
+      :462-471 compute_ssm_output, :661-668 selective_scan_fallback).
+    Optional extensions with no reference kernel counterpart (the Mamba block applies
+    the gate outside the scan, common.ex:270-278): y += D[d] x, then y *= silu(z).
+    """
+    x, dt, A, B, C, D, z = _f64(x, dt, A, B, C, D, z)
+    bsz, seq, hid = x.shape
+    n = A.shape[1]
+    dtc = np.clip(dt, DT_MIN, DT_MAX)
+    if mode == "mean":
+        dtb = np.broadcast_to(dtc.mean(axis=2, keepdims=True), dtc.shape)
+    elif mode == "channel":
+        dtb = dtc
+    else:
+        raise ValueError(mode)
+    h = np.zeros((bsz, hid, n))
+    y = np.empty_like(x)
+    states = []
+    for t in range(seq):
+        a_bar = np.exp(dtc[:, t, :, None] * A[None])
+        h = a_bar * h + (dtb[:, t, :, None] * B[:, t, None, :]) * x[:, t, :, None]
+        if return_states:
+            states.append(h.copy())
+        y[:, t] = np.einsum("bdn,bn->bd", h, C[:, t])
+    if D is not None:
+        y = y + D[None, None, :] * x
+    out = y * silu(z) if z is not None else y
+    if return_states:
+        return out, np.stack(states, axis=1)
+    return out
+
+
+def selective_scan_backward(x, dt, A, B, C, dout, D=None, z=None, mode="channel"):
+    """Reverse pass -> dict(dx, ddt, dA, dB, dC, dD, dz).
+
+    The scan part follows ``selective_scan_backward_fallback`` (fused_scan.ex:1453-1533):
+    dh += dy C; dC += sum_d dy h; dx += sum_n dh dt B; ddt += sum_n dh (h_prev A_bar A + B x),
+    zeroed where dt was clipped; dB += sum_d dh x dt; carry dh A_bar.  Extensions with no
+    reference counterpart: dA = sum_{b,t} dh h_prev A_bar dt (the reference kernel has
+    no dA output, fused_selective_scan_backward.cu:198-238), dD, dz (silu gate), and the
+    mean-mode dt coupling.
+    """
+    x, dt, A, B, C, dout, D, z = _f64(x, dt, A, B, C, dout, D, z)
+    bsz, seq, hid = x.shape
+    n = A.shape[1]
+    dtc = np.clip(dt, DT_MIN, DT_MAX)
+    in_range = (dt >= DT_MIN) & (dt <= DT_MAX)
+    mean_mode = mode == "mean"
+    dtb = np.broadcast_to(dtc.mean(axis=2, keepdims=True), dtc.shape) if mean_mode else dtc
+
+    # recompute forward states (h_prev for each t)
+    h = np.zeros((bsz, hid, n))
+    hprev = np.empty((bsz, seq, hid, n))
+    for t in range(seq):
+        hprev[:, t] = h
+        a_bar = np.exp(dtc[:, t, :, None] * A[None])
+        h = a_bar * h + (dtb[:, t, :, None] * B[:, t, None, :]) * x[:, t, :, None]
+
+    res = {}
+    if z is not None:
+        y_ssm = selective_scan(x, dt, A, B, C, D, None, mode)
+        sz = sigmoid(z)
+        dy = dout * z * sz
+        res["dz"] = dout * y_ssm * sz * (1.0 + z * (1.0 - sz))
+    else:
+        dy = dout
+        res["dz"] = None
+    dx = np.zeros_like(x)
+    if D is not None:
+        res["dD"] = np.einsum("btd,btd->d", dy, x)
+        dx += dy * D[None, None, :]
+    else:
+        res["dD"] = None
+    ddt = np.zeros_like(x)
+    dA = np.zeros_like(A)
+    dB = np.zeros_like(B)
+    dC = np.zeros_like(C)
+    dh = np.zeros((bsz, hid, n))
+    for t in range(seq - 1, -1, -1):
+        a_bar = np.exp(dtc[:, t, :, None] * A[None])
+        hp = hprev[:, t]
+        h_cur = a_bar * hp + (dtb[:, t, :, None] * B[:, t, None, :]) * x[:, t, :, None]
+        dh = dh + dy[:, t, :, None] * C[:, t, None, :]
+        dC[:, t] = np.einsum("bd,bdn->bn", dy[:, t], h_cur)
+        dx[:, t] += np.einsum("bdn,bd,bn->bd", dh, dtb[:, t], B[:, t])
+        g_a = np.einsum("bdn,bdn->bd", dh * hp, a_bar * A[None])
+        dA += np.einsum("bdn,bd->dn", dh * hp * a_bar, dtc[:, t])
+        g_b = np.einsum("bdn,bn,bd->bd", dh, B[:, t], x[:, t])
+        if mean_mode:
+            ddt[:, t] = g_a + g_b.sum(axis=1, keepdims=True) / hid
+            dB[:, t] = np.einsum("bdn,bd->bn", dh, x[:, t]) * dtb[:, t, 0][:, None]
+        else:
+            ddt[:, t] = g_a + g_b
+            dB[:, t] = np.einsum("bdn,bd,bd->bn", dh, x[:, t], dtc[:, t])
+        dh = dh * a_bar
+    ddt = np.where(in_range, ddt, 0.0)
+    res.update(dx=dx, ddt=ddt, dA=dA, dB=dB, dC=dC)
+    return res
+
+
+# ---------------------------------------------------------------------------
+# Delta rule (DeltaNet / GatedDeltaNet)
+# ---------------------------------------------------------------------------
+
+def _beta4(beta, shape):
+    beta = np.asarray(beta, dtype=np.float64)
+    if beta.ndim == 3:  # per-head beta [B,T,H] broadcast along the value rows
+        beta = np.broadcast_to(beta[..., None], shape)
+    return beta
+
+
+def l2_normalize_keys(k):
+    """k / sqrt(sum k^2 + 1e-6) over head_dim (delta_net.ex:297-298)."""
+    k = np.asarray(k, dtype=np.float64)
+    return k / np.sqrt((k * k).sum(axis=-1, keepdims=True) + KEY_NORM_EPS)
+
+
+def delta_rule(q, k, v, beta, alpha=None, return_states=False):
+    """o_t = S_t q_t with S_t = a_t S_{t-1} + diag(beta_t)(v_t - a_t S_{t-1} k_t) k_t^T.
+
+    S is [heads, d_v, d_k] per batch, retrieval S k contracts the key axis.
+    alpha=None is DeltaNet (delta_net.ex:231-273); otherwise GatedDeltaNet with a per
+    (b, t, head) scalar decay (gated_delta_net.ex:300-353).  beta is per element
+    [B,T,H,d] as in the reference, or per head [B,T,H] (broadcast along d).
+    No 1/sqrt(d) scaling of q (delta_net.ex:266-268).
+    """
+    q, k, v, alpha = _f64(q, k, v, alpha)
+    beta = _beta4(beta, v.shape)
+    bsz, seq, nh, d = q.shape
+    dv = v.shape[3]
+    S = np.zeros((bsz, nh, dv, d))
+    out = np.empty((bsz, seq, nh, dv))
+    states = []
+    for t in range(seq):
+        if alpha is not None:
+            S = alpha[:, t, :, None, None] * S
+        r = np.einsum("bhij,bhj->bhi", S, k[:, t])
+        err = beta[:, t] * (v[:, t] - r)
+        S = S + err[..., :, None] * k[:, t, :, None, :]
+        if return_states:
+            states.append(S.copy())
+        out[:, t] = np.einsum("bhij,bhj->bhi", S, q[:, t])
+    if return_states:
+        return out, np.stack(states, axis=1)
+    return out
+
+
+def delta_rule_backward(q, k, v, beta, do, alpha=None):
+    """Reverse pass -> dict(dq, dk, dv, dbeta, dalpha).
+
+    Follows ``delta_rule_backward_fallback`` (fused_scan.ex:1257-1328) and
+    ``gated_delta_net_backward_fallback`` (fused_scan.ex:1347-1431):
+      dS_total = dS + do q^T; dq = S_t^T do; ds_k = dS_total k;
+      dv = beta ds_k; dbeta = err ds_k;
+      dk = dS_total^T (beta err) - S_g^T (beta ds_k);
+      dalpha = sum(dS_to_decayed * S_prev); dS_prev = alpha dS_to_decayed.
+    For per-head beta the per-element dbeta is summed over the value rows.
+    """
+    q, k, v, do, alpha = _f64(q, k, v, do, alpha)
+    per_head_beta = np.asarray(beta).ndim == 3
+    beta = _beta4(beta, v.shape)
+    bsz, seq, nh, d = q.shape
+    dv_ = v.shape[3]
+    # forward states
+    S = np.zeros((bsz, nh, dv_, d))
+    s_prev = np.empty((bsz, seq, nh, dv_, d))
+    for t in range(seq):
+        s_prev[:, t] = S
+        sg = S if alpha is None else alpha[:, t, :, None, None] * S
+        r = np.einsum("bhij,bhj->bhi", sg, k[:, t])
+        S = sg + (beta[:, t] * (v[:, t] - r))[..., :, None] * k[:, t, :, None, :]
+    dq = np.empty_like(q)
+    dk = np.empty_like(k)
+    dvv = np.empty_like(v)
+    dbeta = np.empty_like(v)
+    dalpha = np.empty((bsz, seq, nh)) if alpha is not None else None
+    dS = np.zeros((bsz, nh, dv_, d))
+    for t in range(seq - 1, -1, -1):
+        sp = s_prev[:, t]
+        a = None if alpha is None else alpha[:, t, :, None, None]
+        sg = sp if a is None else a * sp
+        kt, qt, bt = k[:, t], q[:, t], beta[:, t]
+        err = v[:, t] - np.einsum("bhij,bhj->bhi", sg, kt)
+        s_new = sg + (bt * err)[..., :, None] * kt[..., None, :]
+        dtot = dS + do[:, t][..., :, None] * qt[..., None, :]
+        dq[:, t] = np.einsum("bhij,bhi->bhj", s_new, do[:, t])
+        ds_k = np.einsum("bhij,bhj->bhi", dtot, kt)
+        d_dec = dtot - (bt * ds_k)[..., :, None] * kt[..., None, :]
+        dvv[:, t] = bt * ds_k
+        dbeta[:, t] = err * ds_k
+        dk[:, t] = (np.einsum("bhij,bhi->bhj", dtot, bt * err)
+                    - np.einsum("bhij,bhi->bhj", sg, bt * ds_k))
+        if a is None:
+            dS = d_dec
+        else:
+            dalpha[:, t] = (d_dec * sp).sum(axis=(2, 3))
+            dS = a * d_dec
+    if per_head_beta:
+        dbeta = dbeta.sum(axis=3)
+    return dict(dq=dq, dk=dk, dv=dvv, dbeta=dbeta, dalpha=dalpha)
+
+
+# ---------------------------------------------------------------------------
+# Flash attention
+# ---------------------------------------------------------------------------
+
+def _scores(q, k, causal):
+    d = q.shape[-1]
+    s = np.einsum("bhid,bhjd->bhij", q, k) / np.sqrt(d)
+    if causal:
+        tq, tk = s.shape[-2:]
+        mask = np.arange(tq)[:, None] >= np.arange(tk)[None, :]
+        s = np.where(mask, s, -np.inf)
+    return s
+
+
+def flash_attention(q, k, v, causal=False, return_lse=False):
+    """softmax(Q K^T / sqrt(d) + causal -inf) V (fused_scan.ex:3476-3508).
+
+    Causal mask keeps key j <= query i (rows >= cols).  Optionally also returns the
+    row log-sum-exp of the scaled scores (natural log).
+    """
+    q, k, v = _f64(q, k, v)
+    s = _scores(q, k, causal)
+    m = s.max(axis=-1, keepdims=True)
+    w = np.exp(s - m)
+    l = w.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhij,bhjd->bhid", w / l, v)
+    if return_lse:
+        return o, (m + np.log(l))[..., 0]
+    return o
+
+
+def flash_attention_backward(q, k, v, do, causal=False):
+    """-> (dq, dk, dv) following ``flash_attention_backward_fallback`` (fused_scan.ex:3527-3570)."""
+    q, k, v, do = _f64(q, k, v, do)
+    d = q.shape[-1]
+    s = _scores(q, k, causal)
+    w = np.exp(s - s.max(axis=-1, keepdims=True))
+    w = w / w.sum(axis=-1, keepdims=True)
+    dv = np.einsum("bhij,bhid->bhjd", w, do)
+    dw = np.einsum("bhid,bhjd->bhij", do, v)
+    ds = w * (dw - (dw * w).sum(axis=-1, keepdims=True)) / np.sqrt(d)
+    dq = np.einsum("bhij,bhjd->bhid", ds, k)
+    dk = np.einsum("bhij,bhid->bhjd", ds, q)
+    return dq, dk, dv

@@ -1,0 +1,134 @@
+"""GPU parity: MinGRU / MinLSTM scans (HIP, through the C ABI) vs the CPU oracle."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import scans
+from tests.conftest import assert_close
+from tests.gpu_util import TOL, announce, host, rounded, to_dev
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1, 2), (4, 60, 256), (2, 37, 100), (3, 129, 64), (2, 700, 130), (1, 2048, 96)]
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+def _sig(x):
+    return 1 / (1 + np.exp(-x))
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mingru_logits_fwd_bwd(shape, dtype, rng):
+    from edifice_amd import fused_scan as fs
+    announce("mingru_logits", shape=shape, dtype=dtype)
+    g = rng.normal(size=shape)
+    c = rng.normal(size=shape)
+    dy = rng.normal(size=shape)
+    tg, tc = to_dev(g, dtype).requires_grad_(), to_dev(c, dtype).requires_grad_()
+    out = fs.mingru(tg, tc)
+    out.backward(to_dev(dy, dtype))
+    gr, cr, dyr = rounded(g, dtype), rounded(c, dtype), rounded(dy, dtype)
+    assert_close(host(out), scans.min_gru_scan(gr, cr), TOL[dtype], "h")
+    dg, dc = scans.min_gru_scan_backward(gr, cr, dyr)
+    assert_close(host(tg.grad), dg, TOL[dtype], "dgates")
+    assert_close(host(tc.grad), dc, TOL[dtype], "dcand")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_minlstm_logits_fwd_bwd(shape, dtype, rng):
+    from edifice_amd import fused_scan as fs
+    announce("minlstm_logits", shape=shape, dtype=dtype)
+    fg, ig, c, dy = (rng.normal(size=shape) for _ in range(4))
+    tf, ti, tc = (to_dev(a, dtype).requires_grad_() for a in (fg, ig, c))
+    out = fs.minlstm(tf, ti, tc)
+    out.backward(to_dev(dy, dtype))
+    fr, ir, cr, dyr = (rounded(a, dtype) for a in (fg, ig, c, dy))
+    f, i = _sig(fr), _sig(ir)
+    fwd = scans.minlstm_scan(f, i, cr)
+    assert_close(host(out), fwd, TOL[dtype], "c")
+    df, di, dc, _ = scans.minlstm_scan_backward(f, i, cr, None, fwd, dyr)
+    assert_close(host(tf.grad), df * f * (1 - f), TOL[dtype], "dforget")
+    assert_close(host(ti.grad), di * i * (1 - i), TOL[dtype], "dinput")
+    assert_close(host(tc.grad), dc, TOL[dtype], "dcand")
+
+
+def _call(name, *args):
+    from edifice_amd import _native as nat
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ptrs = [ctypes.c_void_p(a.data_ptr()) if isinstance(a, torch.Tensor) else a for a in args]
+    nat.call(name, stream, *ptrs)
+
+
+@pytest.mark.parametrize("shape", [(4, 60, 256), (2, 33, 70)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_reference_shaped_entry_points(shape, dtype, rng):
+    """edf_fused_mingru_scan / _backward and the MinLSTM pair: post-sigmoid gates, explicit h0."""
+    announce("nif_shaped", shape=shape, dtype=dtype)
+    bsz, seq, hid = shape
+    flag = 1 if dtype == torch.bfloat16 else 0
+    z = rng.uniform(0.02, 0.98, size=shape)
+    i = rng.uniform(0.02, 0.98, size=shape)
+    c, dy = rng.normal(size=shape), rng.normal(size=shape)
+    h0 = rng.normal(size=(bsz, hid))
+    tz, ti, tc, tdy, th0 = (to_dev(a, dtype) for a in (z, i, c, dy, h0))
+    zr, ir, cr, dyr, h0r = (rounded(a, dtype) for a in (z, i, c, dy, h0))
+    tol = TOL[dtype]
+
+    out = torch.empty_like(tz)
+    _call("edf_fused_mingru_scan", tz, tc, th0, out, bsz, seq, hid, flag)
+    fwd = scans.mingru_scan(zr, cr, h0r)
+    assert_close(host(out), fwd, tol, "mingru h")
+    gz, gc, gh = torch.empty_like(tz), torch.empty_like(tz), torch.empty_like(th0)
+    _call("edf_fused_mingru_scan_backward", tz, tc, th0, out, tdy, gz, gc, gh, bsz, seq, hid, flag)
+    ez, ec, eh = scans.mingru_scan_backward(zr, cr, h0r, host(out), dyr)
+    assert_close(host(gz), ez, tol, "dz")
+    assert_close(host(gc), ec, tol, "dcand")
+    assert_close(host(gh), eh, tol, "dh0")
+
+    out = torch.empty_like(tz)
+    _call("edf_fused_minlstm_scan", tz, ti, tc, th0, out, bsz, seq, hid, flag)
+    fwd = scans.minlstm_scan(zr, ir, cr, h0r)
+    assert_close(host(out), fwd, tol, "minlstm c")
+    gf, gi, gc, gh = (torch.empty_like(t) for t in (tz, tz, tz, th0))
+    _call("edf_fused_minlstm_scan_backward", tz, ti, tc, th0, out, tdy, gf, gi, gc, gh, bsz, seq, hid, flag)
+    ef, ei, ec, eh = scans.minlstm_scan_backward(zr, ir, cr, h0r, host(out), dyr)
+    for a, e, n in ((gf, ef, "df"), (gi, ei, "di"), (gc, ec, "dcand"), (gh, eh, "dh0")):
+        assert_close(host(a), e, tol, n)
+
+
+def test_mingru_seq1_known_answer():
+    """backward_kernels_test.exs:271-287 through the HIP entry points."""
+    announce("mingru_known_answer")
+    f32 = dict(dtype=torch.float32, device="cuda")
+    z = torch.tensor([[[0.3, 0.7]]], **f32)
+    c = torch.tensor([[[2.0, -1.0]]], **f32)
+    h0 = torch.zeros(1, 2, **f32)
+    out = torch.empty_like(z)
+    _call("edf_fused_mingru_scan", z, c, h0, out, 1, 1, 2, 0)
+    assert torch.allclose(out, torch.tensor([[[0.6, -0.7]]], **f32), atol=1e-6)
+    gz, gc, gh = torch.empty_like(z), torch.empty_like(z), torch.empty_like(h0)
+    _call("edf_fused_mingru_scan_backward", z, c, h0, out, torch.ones_like(z), gz, gc, gh, 1, 1, 2, 0)
+    assert torch.allclose(gz.cpu(), torch.tensor([[[2.0, -1.0]]]), atol=1e-6)
+    assert torch.allclose(gc.cpu(), torch.tensor([[[0.3, 0.7]]]), atol=1e-6)
+    assert torch.allclose(gh.cpu(), torch.tensor([[0.7, 0.3]]), atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mingru_bandwidth_shape_full_size(dtype, rng):
+    """The MinGRU bandwidth row (B=8, T=2048, H=1536) against the oracle at full size."""
+    from edifice_amd import fused_scan as fs
+    shape = (8, 2048, 1536)
+    announce("mingru_full", shape=shape, dtype=dtype)
+    g = rng.normal(size=shape).astype(np.float32)
+    c = rng.normal(size=shape).astype(np.float32)
+    tg, tc = to_dev(g, dtype).requires_grad_(), to_dev(c, dtype).requires_grad_()
+    out = fs.mingru(tg, tc)
+    gr, cr = rounded(g, dtype), rounded(c, dtype)
+    assert_close(host(out), scans.min_gru_scan(gr, cr), TOL[dtype], "h full")
+    # z -> 1 (large logits): h == cand exactly up to storage rounding
+    big = torch.full_like(tg, 30.0)
+    assert torch.allclose(fs.mingru(big, tc).float(), tc.float(), rtol=0, atol=1e-6)

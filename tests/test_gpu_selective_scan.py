@@ -1,0 +1,85 @@
+"""GPU parity: Mamba selective scan (HIP) vs the CPU oracle, forward and backward."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import scans
+from tests.conftest import assert_close
+from tests.gpu_util import TOL, announce, host, rounded, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def make_inputs(rng, bsz, T, D, N):
+    """Config-2 distributions at a chosen shape."""
+    x = rng.normal(size=(bsz, T, D))
+    dt = np.log1p(np.exp(rng.normal(size=(bsz, T, D)) - 4.0))  # softplus(N(0,1) - 4)
+    A = -np.exp(rng.uniform(np.log(1.0), np.log(16.0), size=(D, N)))
+    B = rng.normal(size=(bsz, T, N))
+    C = rng.normal(size=(bsz, T, N))
+    Dv = rng.normal(size=D)
+    z = rng.normal(size=(bsz, T, D))
+    return x, dt, A, B, C, Dv, z
+
+
+CASES = [
+    # (bsz, T, D, N, io dtype, param dtype, with D/z, dt mode)
+    (2, 70, 48, 16, torch.float32, torch.float32, False, "channel"),
+    (2, 70, 48, 16, torch.float32, torch.float32, True, "channel"),
+    (2, 96, 40, 8, torch.float32, torch.float32, True, "channel"),
+    (1, 33, 20, 4, torch.float32, torch.float32, True, "channel"),
+    (2, 64, 48, 16, torch.bfloat16, torch.float32, True, "channel"),
+    (2, 50, 24, 16, torch.bfloat16, torch.bfloat16, False, "channel"),
+    (2, 45, 32, 8, torch.float32, torch.float32, False, "mean"),
+    (2, 45, 32, 16, torch.float32, torch.float32, True, "mean"),
+    (1, 1, 16, 16, torch.float32, torch.float32, True, "channel"),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_selective_scan_fwd_bwd(case, rng):
+    from edifice_amd import fused_scan as fs
+    bsz, T, D, N, io, par, extras, mode = case
+    announce("selective_scan", case=case)
+    x, dt, A, B, C, Dv, z = make_inputs(rng, bsz, T, D, N)
+    if not extras:
+        Dv = z = None
+    dy = rng.normal(size=x.shape)
+    tx, tdt = to_dev(x, io).requires_grad_(), to_dev(dt, io).requires_grad_()
+    tz = to_dev(z, io).requires_grad_() if extras else None
+    tA, tB, tC = (to_dev(a, par).requires_grad_() for a in (A, B, C))
+    tD = to_dev(Dv, par).requires_grad_() if extras else None
+    out = fs.selective_scan(tx, tdt, tA, tB, tC, tD, tz, dt_mode=mode)
+    out.backward(to_dev(dy, io))
+
+    xr, dtr, zr, dyr = (None if a is None else rounded(a, io) for a in (x, dt, z, dy))
+    Ar, Br, Cr, Dr = (None if a is None else rounded(a, par) for a in (A, B, C, Dv))
+    tol = max(TOL[io], TOL[par])
+    assert_close(host(out), scans.selective_scan(xr, dtr, Ar, Br, Cr, Dr, zr, mode), tol, "y")
+    g = scans.selective_scan_backward(xr, dtr, Ar, Br, Cr, dyr, Dr, zr, mode)
+    pairs = [("dx", tx), ("ddt", tdt), ("dA", tA), ("dB", tB), ("dC", tC)]
+    if extras:
+        pairs += [("dD", tD), ("dz", tz)]
+    for name, t in pairs:
+        assert_close(host(t.grad), g[name], tol, name)
+
+
+def test_selective_scan_config2_full_size_properties(rng):
+    """C2 shape (B=8, T=2048, D=1536, N=16, bf16 u/dt/z, f32 A/B/C/D): B == 0 gives
+    y == D x silu(z) exactly (size-independent closed form), and one batch row agrees
+    with the oracle over the whole sequence."""
+    from edifice_amd import fused_scan as fs
+    bsz, T, D, N = 8, 2048, 1536, 16
+    announce("selective_scan_c2_full")
+    x, dt, A, B, C, Dv, z = make_inputs(rng, bsz, T, D, N)
+    tx, tdt, tz = (to_dev(a, torch.bfloat16) for a in (x, dt, z))
+    tA, tB, tC, tD = (to_dev(a, torch.float32) for a in (A, B, C, Dv))
+    y0 = fs.selective_scan(tx, tdt, tA, torch.zeros_like(tB), tC, tD, tz)
+    xr, zr = rounded(x, torch.bfloat16), rounded(z, torch.bfloat16)
+    expect = Dv * xr * zr / (1 + np.exp(-zr))
+    assert_close(host(y0), expect, TOL[torch.bfloat16], "B=0 closed form")
+    y = fs.selective_scan(tx, tdt, tA, tB, tC, tD, tz)
+    b = 3
+    ref = scans.selective_scan(xr[b:b + 1, :, :256], rounded(dt, torch.bfloat16)[b:b + 1, :, :256], A[:256],
+                               B[b:b + 1], C[b:b + 1], Dv[:256], zr[b:b + 1, :, :256])
+    assert_close(host(y)[b:b + 1, :, :256], ref, TOL[torch.bfloat16], "row 3 vs oracle")

@@ -1,0 +1,184 @@
+"""Pin the oracle's hand-derived backward passes against torch autograd (float64).
+
+The autograd side differentiates a torch restatement of the FORWARD only, so it is
+independent of the hand-derived backward in oracle/scans.py (which follows the
+reference's *_backward_fallback functions).  Finite differences back both up.
+CPU only.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import scans
+from tests.conftest import assert_close
+
+F64 = torch.float64  # explicit everywhere: never change torch's global default dtype
+
+
+def _t(a, grad=True):
+    return torch.tensor(np.asarray(a), dtype=torch.float64, requires_grad=grad)
+
+
+def torch_mingru(z, c, h0):
+    h, out = h0, []
+    for t in range(z.shape[1]):
+        h = (1 - z[:, t]) * h + z[:, t] * c[:, t]
+        out.append(h)
+    return torch.stack(out, 1)
+
+
+def torch_minlstm(f, i, c, h0):
+    s = f + i + 1e-6
+    fn, inn = f / s, i / s
+    h, out = h0, []
+    for t in range(f.shape[1]):
+        h = fn[:, t] * h + inn[:, t] * c[:, t]
+        out.append(h)
+    return torch.stack(out, 1)
+
+
+def test_mingru_backward_vs_autograd(rng):
+    z = rng.uniform(0.05, 0.95, size=(2, 13, 6))
+    c = rng.normal(size=z.shape)
+    h0 = rng.normal(size=(2, 6))
+    dy = rng.normal(size=z.shape)
+    tz, tc, th = _t(z), _t(c), _t(h0)
+    torch_mingru(tz, tc, th).backward(torch.from_numpy(dy))
+    fwd = scans.mingru_scan(z, c, h0)
+    dz, dc, dh0 = scans.mingru_scan_backward(z, c, h0, fwd, dy)
+    for a, e, n in ((dz, tz.grad, "dz"), (dc, tc.grad, "dc"), (dh0, th.grad, "dh0")):
+        assert_close(a, e.numpy(), 1e-12, n)
+    # logit-level chain rule
+    g = rng.normal(size=z.shape)
+    tg = _t(g)
+    torch_mingru(torch.sigmoid(tg), tc.detach(), torch.zeros(2, 6, dtype=F64)).backward(torch.from_numpy(dy))
+    dg, _ = scans.min_gru_scan_backward(g, c, dy)
+    assert_close(dg, tg.grad.numpy(), 1e-12, "dgates")
+
+
+def test_minlstm_backward_vs_autograd(rng):
+    f = rng.uniform(0.05, 0.95, size=(2, 11, 5))
+    i = rng.uniform(0.05, 0.95, size=f.shape)
+    c = rng.normal(size=f.shape)
+    h0 = rng.normal(size=(2, 5))
+    dy = rng.normal(size=f.shape)
+    tf, ti, tc, th = _t(f), _t(i), _t(c), _t(h0)
+    torch_minlstm(tf, ti, tc, th).backward(torch.from_numpy(dy))
+    fwd = scans.minlstm_scan(f, i, c, h0)
+    df, di, dc, dh0 = scans.minlstm_scan_backward(f, i, c, h0, fwd, dy)
+    for a, e, n in ((df, tf.grad, "df"), (di, ti.grad, "di"), (dc, tc.grad, "dc"), (dh0, th.grad, "dh0")):
+        assert_close(a, e.numpy(), 1e-12, n)
+
+
+def torch_selective_assoc(x, dt, A, B, C, D, z, mode):
+    """Independent forward: the scan as cumulative sums in log-decay space,
+    h_t = sum_{s<=t} exp(A (cum_t - cum_s)) dtb_s B_s x_s (no recurrence)."""
+    dtc = torch.clamp(dt, 1e-3, 0.1)
+    dtb = dtc.mean(-1, keepdim=True).expand_as(dtc) if mode == "mean" else dtc
+    cum = torch.cumsum(dtc, 1)  # [b, t, d]
+    T = x.shape[1]
+    ys = []
+    for t in range(T):
+        decay = torch.exp(A[None, None] * (cum[:, t:t + 1, :, None] - cum[:, :t + 1, :, None]))  # [b,s,d,n]
+        h = (decay * (dtb[:, :t + 1, :, None] * B[:, :t + 1, None, :] * x[:, :t + 1, :, None])).sum(1)
+        ys.append((h * C[:, t, None, :]).sum(-1))
+    y = torch.stack(ys, 1)
+    if D is not None:
+        y = y + D * x
+    if z is not None:
+        y = y * z * torch.sigmoid(z)
+    return y
+
+
+@pytest.mark.parametrize("mode", ["channel", "mean"])
+@pytest.mark.parametrize("extras", [False, True])
+def test_selective_scan_forward_backward_vs_autograd(rng, mode, extras):
+    bsz, T, D, N = 2, 9, 5, 4
+    x = rng.normal(size=(bsz, T, D))
+    dt = rng.uniform(0.0, 0.15, size=(bsz, T, D))  # some entries outside [1e-3, 0.1]
+    A = -np.exp(rng.uniform(0, np.log(16), size=(D, N)))
+    B, C = rng.normal(size=(bsz, T, N)), rng.normal(size=(bsz, T, N))
+    Dv = rng.normal(size=D) if extras else None
+    z = rng.normal(size=x.shape) if extras else None
+    dy = rng.normal(size=x.shape)
+    tx, tdt, tA, tB, tC = _t(x), _t(dt), _t(A), _t(B), _t(C)
+    tD = _t(Dv) if extras else None
+    tz = _t(z) if extras else None
+    y_t = torch_selective_assoc(tx, tdt, tA, tB, tC, tD, tz, mode)
+    y = scans.selective_scan(x, dt, A, B, C, Dv, z, mode)
+    assert_close(y, y_t.detach().numpy(), 1e-12, "forward")
+    y_t.backward(torch.from_numpy(dy))
+    g = scans.selective_scan_backward(x, dt, A, B, C, dy, Dv, z, mode)
+    pairs = [("dx", tx), ("ddt", tdt), ("dA", tA), ("dB", tB), ("dC", tC)]
+    if extras:
+        pairs += [("dD", tD), ("dz", tz)]
+    for name, tt in pairs:
+        assert_close(g[name], tt.grad.numpy(), 1e-10, name)
+
+
+def torch_delta(q, k, v, beta, alpha):
+    bsz, T, H, d = q.shape
+    S = torch.zeros(bsz, H, v.shape[-1], d, dtype=F64)
+    out = []
+    for t in range(T):
+        if alpha is not None:
+            S = alpha[:, t, :, None, None] * S
+        r = torch.einsum("bhij,bhj->bhi", S, k[:, t])
+        b = beta[:, t] if beta.dim() == 4 else beta[:, t, :, None]
+        S = S + (b * (v[:, t] - r))[..., None] * k[:, t, :, None, :]
+        out.append(torch.einsum("bhij,bhj->bhi", S, q[:, t]))
+    return torch.stack(out, 1)
+
+
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("per_head_beta", [False, True])
+def test_delta_rule_backward_vs_autograd(rng, gated, per_head_beta):
+    bsz, T, H, d = 2, 7, 2, 4
+    q = rng.normal(size=(bsz, T, H, d))
+    k = scans.l2_normalize_keys(rng.normal(size=(bsz, T, H, d)))
+    v = rng.normal(size=(bsz, T, H, d))
+    beta = rng.uniform(size=(bsz, T, H) if per_head_beta else (bsz, T, H, d))
+    alpha = rng.uniform(0.5, 1.0, size=(bsz, T, H)) if gated else None
+    do = rng.normal(size=v.shape)
+    tq, tk, tv, tb = _t(q), _t(k), _t(v), _t(beta)
+    ta = _t(alpha) if gated else None
+    o_t = torch_delta(tq, tk, tv, tb, ta)
+    assert_close(scans.delta_rule(q, k, v, beta, alpha), o_t.detach().numpy(), 1e-12, "forward")
+    o_t.backward(torch.from_numpy(do))
+    g = scans.delta_rule_backward(q, k, v, beta, do, alpha)
+    pairs = [("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb)] + ([("dalpha", ta)] if gated else [])
+    for name, tt in pairs:
+        assert_close(g[name], tt.grad.numpy(), 1e-10, name)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_backward_vs_sdpa_autograd(rng, causal):
+    bsz, H, T, d = 2, 2, 9, 8
+    q, k, v, do = (rng.normal(size=(bsz, H, T, d)) for _ in range(4))
+    tq, tk, tv = _t(q), _t(k), _t(v)
+    torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=causal).backward(torch.from_numpy(do))
+    dq, dk, dv = scans.flash_attention_backward(q, k, v, do, causal)
+    for a, tt, n in ((dq, tq, "dq"), (dk, tk, "dk"), (dv, tv, "dv")):
+        assert_close(a, tt.grad.numpy(), 1e-10, n)
+
+
+def test_selective_scan_backward_finite_difference(rng):
+    bsz, T, D, N = 1, 6, 3, 2
+    x = rng.normal(size=(bsz, T, D))
+    dt = rng.uniform(0.01, 0.09, size=(bsz, T, D))
+    A = -np.exp(rng.uniform(0, 2, size=(D, N)))
+    B, C = rng.normal(size=(bsz, T, N)), rng.normal(size=(bsz, T, N))
+    dy = rng.normal(size=x.shape)
+    g = scans.selective_scan_backward(x, dt, A, B, C, dy)
+    eps = 1e-6
+    for name, arr in (("dx", x), ("ddt", dt), ("dA", A), ("dB", B), ("dC", C)):
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            old = arr[idx]
+            arr[idx] = old + eps
+            fp = (scans.selective_scan(x, dt, A, B, C) * dy).sum()
+            arr[idx] = old - eps
+            fm = (scans.selective_scan(x, dt, A, B, C) * dy).sum()
+            arr[idx] = old
+            num[idx] = (fp - fm) / (2 * eps)
+        assert_close(g[name], num, 1e-6, name)
