@@ -32,6 +32,10 @@ SIGNATURES = {
     "edf_fused_selective_scan_backward": (
         I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
     "edf_selective_scan_backward_workspace_bytes": (S, [I, I, I, I, I, I]),
+    "edf_fused_flash_attention": (I, [P, P, P, P, P, P, I, I, I, I, I, I]),
+    "edf_fused_flash_attention_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
+    "edf_flash_attention_backward_workspace_bytes": (S, [I, I, I, I]),
+    "edf_debug_mfma_32x32x16_bf16": (I, [P, P, P, P]),
 }
 
 

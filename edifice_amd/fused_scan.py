@@ -181,6 +181,44 @@ class _SelectiveScan(torch.autograd.Function):
         return dx, ddt, cast(dA, A), cast(dB, B), cast(dC, C), cast(dD, D), dz, None
 
 
+class _FlashAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, causal):
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        _dev(q, k, v)
+        _same(q, k, v)
+        bsz, nh, seq, hd = q.shape
+        if k.shape != q.shape or v.shape != q.shape:
+            raise EdificeHipError("flash_attention needs q, k, v of one shape [B, H, T, d] (self-attention)")
+        out = torch.empty_like(q)
+        lse = torch.empty((bsz, nh, seq), dtype=torch.float32, device=q.device)
+        nat.call("edf_fused_flash_attention", _stream(), _p(q), _p(k), _p(v), _p(out), _p(lse), bsz, nh, seq, hd,
+                 int(causal), dtype_flag(q))
+        ctx.causal = int(causal)
+        ctx.save_for_backward(q, k, v, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        dout = dout.contiguous().to(q.dtype)
+        bsz, nh, seq, hd = q.shape
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        wsb = nat.query("edf_flash_attention_backward_workspace_bytes", bsz, nh, seq, hd)
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_flash_attention_backward", _stream(), _p(q), _p(k), _p(v), _p(out), _p(dout), _p(lse),
+                 _p(dq), _p(dk), _p(dv), _p(ws), wsb, bsz, nh, seq, hd, ctx.causal, dtype_flag(q))
+        return dq, dk, dv, None
+
+
+def flash_attention(q, k, v, causal: bool = False):
+    """``FusedScan.flash_attention/4`` (fused_scan.ex:3398-3414): q, k, v [B, H, T, d].
+
+    Scale 1/sqrt(d); causal keeps keys j <= i.  Differentiable (fused HIP backward).
+    """
+    return _FlashAttention.apply(q, k, v, bool(causal))
+
+
 def selective_scan(x, dt, a, b, c, d=None, z=None, *, dt_mode: str = "channel"):
     """``FusedScan.selective_scan/5`` (fused_scan.ex:370-384) plus optional D skip and silu(z) gate.
 

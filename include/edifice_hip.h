@@ -142,6 +142,35 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
 size_t edf_selective_scan_backward_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode,
                                                    int have_states);
 
+/* ------------------------------------------------------------------------
+ * Flash attention   O = softmax(Q K^T / sqrt(d) [+ causal -inf]) V
+ *   q, k, v, out, grads: [B, H, T, d] in dtype; lse: float32 [B, H, T] (natural log)
+ * ------------------------------------------------------------------------ */
+
+/* Replaces fused_flash_attention/9 (q, k, v, batch, heads, seq_len, head_dim,
+ * causal, dtype), nif.ex fused_flash_attention, and fused_flash_attention_launch
+ * (native/cuda/fused_flash_attention.cu:168-191).  Extension: `lse` (may be NULL)
+ * receives the row log-sum-exp for the backward.  bf16 with head_dim 32, 64 or 128
+ * runs on MFMA; other head_dim (<= 256) and float32 run a wave-per-row kernel. */
+int edf_fused_flash_attention(void* stream, const void* q, const void* k, const void* v, void* out, float* lse,
+                              int batch, int num_heads, int seq_len, int head_dim, int causal, int dtype);
+
+/* Replaces fused_flash_attention_backward/11 (q, k, v, out, dO, batch, heads,
+ * seq_len, head_dim, causal, dtype), whose concatenated output was [dQ | dK | dV]
+ * (native/cuda/fused_flash_attention_backward.cu:355-408; that code cudaMalloc'ed D
+ * and lse per call).  Takes the forward's lse; the workspace holds
+ * D = rowsum(dO * O), edf_flash_attention_backward_workspace_bytes() bytes. */
+int edf_fused_flash_attention_backward(void* stream, const void* q, const void* k, const void* v, const void* out,
+                                       const void* grad_out, const float* lse, void* grad_q, void* grad_k,
+                                       void* grad_v, void* workspace, size_t workspace_bytes, int batch,
+                                       int num_heads, int seq_len, int head_dim, int causal, int dtype);
+size_t edf_flash_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim);
+
+/* Diagnostic: C[32][32] = A[32][16] * B[16][32] (bf16 in, f32 out, row-major) with one
+ * v_mfma_f32_32x32x16_bf16, using the lane layout the attention and delta-rule kernels
+ * assume.  No reference counterpart; used by the GPU tests to pin that layout. */
+int edf_debug_mfma_32x32x16_bf16(void* stream, const void* A, const void* B, float* C);
+
 #ifdef __cplusplus
 }
 #endif
