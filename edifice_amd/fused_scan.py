@@ -219,6 +219,72 @@ def flash_attention(q, k, v, causal: bool = False):
     return _FlashAttention.apply(q, k, v, bool(causal))
 
 
+BETA_PER_ELEMENT, BETA_PER_HEAD = 0, 1
+
+
+class _DeltaRule(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, beta, alpha):
+        q, k, v, beta, alpha = (_c(t) for t in (q, k, v, beta, alpha))
+        _dev(q, k, v, beta, alpha)
+        _same(q, k, v, beta, alpha)
+        bsz, seq, nh, hd = q.shape
+        if k.shape != q.shape or v.shape != q.shape:
+            raise EdificeHipError("delta rule needs q, k, v of one shape [B, T, H, d]")
+        if beta.shape == q.shape:
+            mode = BETA_PER_ELEMENT
+        elif beta.shape == q.shape[:3]:
+            mode = BETA_PER_HEAD
+        else:
+            raise EdificeHipError(f"beta must be [B,T,H,d] or [B,T,H], got {tuple(beta.shape)}")
+        if alpha is not None and alpha.shape != q.shape[:3]:
+            raise EdificeHipError(f"alpha must be [B,T,H], got {tuple(alpha.shape)}")
+        dt = dtype_flag(q)
+        out = torch.empty_like(v)
+        wsb = nat.query("edf_delta_rule_workspace_bytes", bsz, seq, nh, hd, dt, mode)
+        ws = _u8(wsb, q) if wsb else None
+        if alpha is None:
+            nat.call("edf_fused_delta_net_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(ws), wsb,
+                     bsz, seq, nh, hd, dt, mode)
+        else:
+            nat.call("edf_fused_gated_delta_net_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(alpha),
+                     _p(out), _p(ws), wsb, bsz, seq, nh, hd, dt, mode)
+        ctx.mode = mode
+        ctx.save_for_backward(q, k, v, beta, alpha, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, beta, alpha, out = ctx.saved_tensors
+        do = do.contiguous().to(q.dtype)
+        bsz, seq, nh, hd = q.shape
+        dt = dtype_flag(q)
+        dq, dk, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
+        wsb = nat.query("edf_delta_rule_backward_workspace_bytes", bsz, seq, nh, hd, dt, ctx.mode)
+        ws = _u8(wsb, q)
+        if alpha is None:
+            nat.call("edf_fused_delta_rule_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out),
+                     _p(do), _p(dq), _p(dk), _p(dv), _p(db), _p(ws), wsb, bsz, seq, nh, hd, dt, ctx.mode)
+            return dq, dk, dv, db, None
+        da = torch.empty_like(alpha)
+        nat.call("edf_fused_gated_delta_net_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(alpha),
+                 _p(out), _p(do), _p(dq), _p(dk), _p(dv), _p(db), _p(da), _p(ws), wsb, bsz, seq, nh, hd, dt,
+                 ctx.mode)
+        return dq, dk, dv, db, da
+
+
+def delta_net_scan(q, k, v, beta):
+    """``FusedScan.delta_net_scan/4`` (fused_scan.ex:195-209): q, k, v [B, T, H, d]; k
+    L2-normalised, beta post-sigmoid, per element [B, T, H, d] or per head [B, T, H]."""
+    return _DeltaRule.apply(q, k, v, beta, None)
+
+
+def gated_delta_net_scan(q, k, v, beta, alpha):
+    """``FusedScan.gated_delta_net_scan/5`` (fused_scan.ex:219-233): as delta_net_scan with a
+    per-(b, t, head) decay alpha [B, T, H] applied to the state before each update."""
+    return _DeltaRule.apply(q, k, v, beta, alpha)
+
+
 def selective_scan(x, dt, a, b, c, d=None, z=None, *, dt_mode: str = "channel"):
     """``FusedScan.selective_scan/5`` (fused_scan.ex:370-384) plus optional D skip and silu(z) gate.
 

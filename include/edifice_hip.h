@@ -166,6 +166,56 @@ int edf_fused_flash_attention_backward(void* stream, const void* q, const void* 
                                        int num_heads, int seq_len, int head_dim, int causal, int dtype);
 size_t edf_flash_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim);
 
+/* ------------------------------------------------------------------------
+ * Delta rule (DeltaNet / GatedDeltaNet)
+ *   q, k, v, out, grads: [B, T, H, d] in dtype (k L2-normalised by the caller, no
+ *   q scaling); S is [d x d] per (b, h):
+ *     S_g = alpha_t S;  S = S_g + diag(beta_t)(v_t - S_g k_t) k_t^T;  o_t = S q_t
+ *   beta: [B, T, H, d] (EDF_BETA_PER_ELEMENT, the reference's layout) or [B, T, H]
+ *   (EDF_BETA_PER_HEAD); alpha: [B, T, H] (gated only).  head_dim <= 128.
+ *   bf16 + per-head beta + head_dim 128 + seq_len >= 64 runs the chunked MFMA forward
+ *   when the workspace (edf_delta_rule_workspace_bytes) is supplied; everything else
+ *   runs the exact per-step kernels.
+ * ------------------------------------------------------------------------ */
+enum { EDF_BETA_PER_ELEMENT = 0, EDF_BETA_PER_HEAD = 1 };
+
+size_t edf_delta_rule_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                      int beta_mode);
+size_t edf_delta_rule_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                               int beta_mode);
+
+/* Replaces fused_delta_net_scan/9 (q, k, v, beta, batch, seq_len, heads, head_dim,
+ * dtype), c_src/edifice_cuda_nif.c, and fused_delta_net_scan_launch
+ * (native/cuda/fused_delta_rule_scan.cu:234-245). */
+int edf_fused_delta_net_scan(void* stream, const void* q, const void* k, const void* v, const void* beta, void* out,
+                             void* workspace, size_t workspace_bytes, int batch, int seq_len, int num_heads,
+                             int head_dim, int dtype, int beta_mode);
+
+/* Replaces fused_gated_delta_net_scan/10 (+ alpha) and
+ * fused_gated_delta_net_scan_launch (native/cuda/fused_delta_rule_scan.cu:247-258). */
+int edf_fused_gated_delta_net_scan(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                                   const void* alpha, void* out, void* workspace, size_t workspace_bytes, int batch,
+                                   int seq_len, int num_heads, int head_dim, int dtype, int beta_mode);
+
+/* Replaces fused_delta_rule_scan_backward/11 (q, k, v, beta, fwd, dy, ...), whose
+ * concatenated output was [dq | dk | dv | dbeta]
+ * (native/cuda/fused_delta_rule_scan_backward.cu:277-320).  grad_beta has beta's
+ * layout.  forward_out is accepted and unused, as in the reference. */
+int edf_fused_delta_rule_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                                       const void* forward_out, const void* grad_out, void* grad_q, void* grad_k,
+                                       void* grad_v, void* grad_beta, void* workspace, size_t workspace_bytes,
+                                       int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                       int beta_mode);
+
+/* Replaces fused_gated_delta_net_scan_backward/12, output [dq | dk | dv | dbeta | dalpha]
+ * (native/cuda/fused_gated_delta_net_scan_backward.cu:348-390). */
+int edf_fused_gated_delta_net_scan_backward(void* stream, const void* q, const void* k, const void* v,
+                                            const void* beta, const void* alpha, const void* forward_out,
+                                            const void* grad_out, void* grad_q, void* grad_k, void* grad_v,
+                                            void* grad_beta, void* grad_alpha, void* workspace,
+                                            size_t workspace_bytes, int batch, int seq_len, int num_heads,
+                                            int head_dim, int dtype, int beta_mode);
+
 /* Diagnostic: C[32][32] = A[32][16] * B[16][32] (bf16 in, f32 out, row-major) with one
  * v_mfma_f32_32x32x16_bf16, using the lane layout the attention and delta-rule kernels
  * assume.  No reference counterpart; used by the GPU tests to pin that layout. */
