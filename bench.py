@@ -149,6 +149,96 @@ def bench_mingru(torch, steps, warmup, B, T, H, dtype):
                 fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
 
 
+def _time_pair(torch, steps, warmup, fwd, bwd):
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    tf, tb = EventTimer(torch), EventTimer(torch)
+    for _ in range(steps):
+        with tf:
+            fwd()
+        with tb:
+            bwd()
+    return tf.mean_ms(), tb.mean_ms()
+
+
+def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
+    """Config 3: gated delta rule, bf16 I/O, per-head beta, f32 state.
+    Algorithmic flops (chunked-form convention): fwd 2 (5 C d + 3 d^2) per token-head, bwd 2x fwd."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(3000)
+    dev, bf = "cuda", torch.bfloat16
+
+    def l2n(x):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+
+    q = l2n(torch.randn(B, T, H, d, device=dev, generator=g)).to(bf)
+    k = l2n(torch.randn(B, T, H, d, device=dev, generator=g)).to(bf)
+    v = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    beta = torch.sigmoid(torch.randn(B, T, H, device=dev, generator=g)).to(bf)
+    alpha = torch.exp(-torch.nn.functional.softplus(torch.randn(B, T, H, device=dev, generator=g))).to(bf)
+    do = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    out = torch.empty_like(v)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    db, da = torch.empty_like(beta), torch.empty_like(alpha)
+    wsf = nat.query("edf_delta_rule_workspace_bytes", B, T, H, d, 1, 1)
+    wsb = nat.query("edf_delta_rule_backward_workspace_bytes", B, T, H, d, 1, 1)
+    ws1 = torch.empty(max(wsf, 1), dtype=torch.uint8, device=dev)
+    ws2 = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_gated_delta_net_scan", stream, P(q), P(k), P(v), P(beta), P(alpha), P(out), P(ws1), wsf,
+                 B, T, H, d, 1, 1)
+
+    def bwd():
+        nat.call("edf_fused_gated_delta_net_scan_backward", stream, P(q), P(k), P(v), P(beta), P(alpha), P(out),
+                 P(do), P(dq), P(dk), P(dv), P(db), P(da), P(ws2), wsb, B, T, H, d, 1, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, max(2, steps // 4), 1, fwd, bwd)
+    fflops = 2 * (5 * C * d + 3 * d * d) * B * H * T
+    bflops = 2 * fflops
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, fwd_tflops=fflops / fwd_ms / 1e9, bwd_tflops=bflops / bwd_ms / 1e9,
+                fwd_bwd_tflops=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9,
+                fwd_bwd_mfma_frac=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+                shape=dict(B=B, H=H, T=T, d=d, chunk=C))
+
+
+def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128):
+    """Config 4: causal flash attention, bf16.  Flops: fwd 4 B H T^2 d / 2, bwd 2.5x fwd."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(4000)
+    dev, bf = "cuda", torch.bfloat16
+    std = d ** -0.25
+    q, k, v, do = (torch.randn(B, H, T, d, device=dev, generator=g).mul_(std).to(bf) for _ in range(4))
+    out = torch.empty_like(q)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    wsb = nat.query("edf_flash_attention_backward_workspace_bytes", B, H, T, d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_flash_attention", stream, P(q), P(k), P(v), P(out), P(lse), B, H, T, d, 1, 1)
+
+    def bwd():
+        nat.call("edf_fused_flash_attention_backward", stream, P(q), P(k), P(v), P(out), P(do), P(lse), P(dq),
+                 P(dk), P(dv), P(ws), wsb, B, H, T, d, 1, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
+    fflops = 4 * B * H * T * T * d / 2
+    bflops = 2.5 * fflops
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, fwd_tflops=fflops / fwd_ms / 1e9, bwd_tflops=bflops / bwd_ms / 1e9,
+                fwd_bwd_tflops=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9,
+                fwd_bwd_mfma_frac=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+                shape=dict(B=B, H=H, T=T, d=d, causal=True))
+
+
 def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
     """Time the C restatement (oracle/cref.c, OpenMP f32) on the config-2 selective-scan
     workload (about 3 s per fwd+bwd step on 8 host cores); returns GB/s under the same
@@ -206,6 +296,10 @@ def main():
             configs[key] = bench_mingru(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
     ss = bench_selective_scan(torch, args.steps, args.warmup)
     configs["c2_selective_scan"] = ss
+    if want("delta"):
+        configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
+    if want("flash"):
+        configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
     dominant = "ss_bwd" if ss["bwd_ms"] >= ss["fwd_ms"] else "ss_fwd"
     dom_ms = max(ss["bwd_ms"], ss["fwd_ms"])
     dom_bytes = ss["bwd_bytes"] if dominant == "ss_bwd" else ss["fwd_bytes"]

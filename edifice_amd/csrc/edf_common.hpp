@@ -25,6 +25,14 @@ template <> EDF_DEVICE bf16 from_f32<bf16>(float v) { return (bf16)v; }  // RNE
 template <typename T> EDF_DEVICE float ld(const T* p, long i) { return to_f32(p[i]); }
 template <typename T> EDF_DEVICE void st(T* p, long i, float v) { p[i] = from_f32<T>(v); }
 
+// Branch-free guarded load: always reads p[ok ? i : safe] (an in-bounds element the
+// caller names) and returns 0 when !ok.  Keeping loads out of divergent branches lets
+// the compiler issue a whole block of them before the first wait.
+template <typename T> EDF_DEVICE float ld_or0(const T* p, long i, bool ok, long safe = 0) {
+  const float v = to_f32(p[ok ? i : safe]);
+  return ok ? v : 0.0f;
+}
+
 // ---- math -------------------------------------------------------------------
 constexpr float LOG2E = 1.4426950408889634f;
 

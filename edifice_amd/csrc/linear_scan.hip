@@ -61,7 +61,7 @@ __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict
   const int b = blockIdx.y;
   const int c = blockIdx.x * 64 + lane;
   const bool valid = c < hid;
-  const long base = (long)b * seq * hid + c;
+  const long base = (long)b * seq * hid + min(c, hid - 1);  // loads stay in bounds; stores are guarded
 
   float h = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c) : 0.0f;
   const int steps = (seq + W * L - 1) / (W * L);
@@ -71,16 +71,12 @@ __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict
 #pragma unroll
     for (int j = 0; j < L; ++j) {
       const int t = t0 + j;
-      if (valid && t < seq) {
-        const long idx = base + (long)t * hid;
-        Step<OP, LOGITS> s;
-        s.make(ld(g1, idx), OP == OP_MINLSTM ? ld(g2, idx) : 0.0f, ld(cand, idx));
-        a[j] = s.a;
-        bb[j] = s.b;
-      } else {
-        a[j] = 1.0f;
-        bb[j] = 0.0f;
-      }
+      const long idx = base + (long)min(t, seq - 1) * hid;
+      Step<OP, LOGITS> s;
+      s.make(ld(g1, idx), OP == OP_MINLSTM ? ld(g2, idx) : 0.0f, ld(cand, idx));
+      const bool ok = valid && t < seq;  // padding steps are the identity map
+      a[j] = ok ? s.a : 1.0f;
+      bb[j] = ok ? s.b : 0.0f;
     }
     float A = 1.0f, B = 0.0f;
 #pragma unroll
@@ -122,7 +118,7 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
   const int b = blockIdx.y;
   const int c = blockIdx.x * 64 + lane;
   const bool valid = c < hid;
-  const long base = (long)b * seq * hid + c;
+  const long base = (long)b * seq * hid + min(c, hid - 1);  // loads stay in bounds; stores are guarded
   const float h0v = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c) : 0.0f;
 
   float u = 0.0f;  // u_{t+1} entering the macro-step from the right
@@ -135,20 +131,19 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
 #pragma unroll
     for (int j = 0; j < L; ++j) {
       const int t = t0 + j;
-      if (valid && t < seq) {
-        const long idx = base + (long)t * hid;
-        x1[j] = ld(g1, idx);
-        x2[j] = OP == OP_MINLSTM ? ld(g2, idx) : 0.0f;
-        cc[j] = ld(cand, idx);
-        hp[j] = t > 0 ? ld(fwd, idx - hid) : h0v;
-        gy[j] = ld(dy, idx);
-      } else {
-        x1[j] = 0.0f;
-        x2[j] = 0.0f;
-        cc[j] = 0.0f;
-        hp[j] = 0.0f;
-        gy[j] = 0.0f;
-      }
+      const bool ok = valid && t < seq;
+      const long idx = base + (long)min(t, seq - 1) * hid;
+      const long pidx = base + (long)max(min(t, seq - 1) - 1, 0) * hid;
+      const float v1 = ld(g1, idx);
+      const float v2 = OP == OP_MINLSTM ? ld(g2, idx) : 0.0f;
+      const float vc = ld(cand, idx);
+      const float vh = ld(fwd, pidx);
+      const float vy = ld(dy, idx);
+      x1[j] = ok ? v1 : 0.0f;
+      x2[j] = ok ? v2 : 0.0f;
+      cc[j] = ok ? vc : 0.0f;
+      hp[j] = ok ? (t > 0 ? vh : h0v) : 0.0f;
+      gy[j] = ok ? vy : 0.0f;
     }
     // per-step decay a_t (1 for padding)
     float a[L];

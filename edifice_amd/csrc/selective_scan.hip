@@ -86,12 +86,14 @@ __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ d
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename TI, typename TP, int N, int NT>
+template <typename TI, typename TP, int N, int NT, bool MEAN, bool HAS_Z>
 __global__ __launch_bounds__(NT) void ss_fwd_kernel(const SSArgs p) {
   using G = Geo<N, NT>;
   constexpr int LPC = G::LPC, SPL = G::SPL, CPW = G::CPW;
   constexpr int TS = 16;
-  constexpr int PT = TS + 4;  // row stride of [.][t] tiles (16 B aligned rows)
+  constexpr int PT = TS + 1;  // odd row stride: row writes and column reads hit distinct banks
+  constexpr int EPT = CPW * TS / NT;              // staged (t, channel) elements per thread
+  constexpr int BPT = (N * TS + NT - 1) / NT;     // staged (t, n) elements per thread
   __shared__ float s_x[CPW][PT], s_dtc[CPW][PT], s_dtx[CPW][PT], s_z[CPW][PT];
   __shared__ float s_B[N][TS + 1], s_C[N][TS + 1];
   __shared__ float s_p[NT][PT];
@@ -123,37 +125,59 @@ __global__ __launch_bounds__(NT) void ss_fwd_kernel(const SSArgs p) {
   const float Dc = (Dv != nullptr && cvalid) ? ld(Dv, c) : 0.0f;
   const long rowbase = (long)b * seq * dim;
 
+  // Raw values of the next block, loaded one block ahead from clamped (in-bounds)
+  // indices so no load sits behind a divergent branch.
+  // Kept in the storage type: converting at load time would force a wait on the load.
+  TI px[EPT], pdt[EPT], pz[EPT];
+  TP pb[BPT], pc[BPT];
+  float pm[EPT];
+  auto fetch = [&](int t0) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * NT;
+      const int t = min(t0 + e / CPW, seq - 1), cc = min(c0 + e % CPW, dim - 1);
+      const long idx = rowbase + (long)t * dim + cc;
+      px[k] = x[idx];
+      pdt[k] = dt[idx];
+      if (HAS_Z) pz[k] = z[idx];
+      pm[k] = MEAN ? p.dtmean[(long)b * seq + t] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < BPT; ++k) {
+      const int e = min(tid + k * NT, N * TS - 1);
+      const long idx = ((long)b * seq + min(t0 + e / N, seq - 1)) * N + e % N;
+      pb[k] = Bm[idx];
+      pc[k] = Cm[idx];
+    }
+  };
+  fetch(0);
+
   const int nblk = (seq + TS - 1) / TS;
   for (int blk = 0; blk < nblk; ++blk) {
     const int t0 = blk * TS;
-    for (int e = tid; e < CPW * TS; e += NT) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * NT;
       const int tt = e / CPW, ch = e % CPW;
-      const int t = t0 + tt, cc = c0 + ch;
-      float xv = 0.0f, dtc = 0.0f, dtx = 0.0f, zv = 0.0f;
-      if (t < seq && cc < dim) {
-        const long idx = rowbase + (long)t * dim + cc;
-        xv = ld(x, idx);
-        dtc = clampf(ld(dt, idx), DT_MIN, DT_MAX);
-        dtx = (p.dtmean != nullptr ? p.dtmean[(long)b * seq + t] : dtc) * xv;
-        if (z != nullptr) zv = ld(z, idx);
-      }
-      s_x[ch][tt] = xv;
+      const bool ok = (t0 + tt < seq) && (c0 + ch < dim);
+      const float xv = to_f32(px[k]);
+      const float dtc = ok ? clampf(to_f32(pdt[k]), DT_MIN, DT_MAX) : 0.0f;
+      s_x[ch][tt] = ok ? xv : 0.0f;
       s_dtc[ch][tt] = dtc;
-      s_dtx[ch][tt] = dtx;
-      s_z[ch][tt] = zv;
+      s_dtx[ch][tt] = ok ? (MEAN ? pm[k] : dtc) * xv : 0.0f;
+      s_z[ch][tt] = (ok && HAS_Z) ? to_f32(pz[k]) : 0.0f;
     }
-    for (int e = tid; e < N * TS; e += NT) {
-      const int tt = e / N, nn = e % N;
-      const int t = t0 + tt;
-      float bv = 0.0f, cv = 0.0f;
-      if (t < seq) {
-        const long idx = ((long)b * seq + t) * N + nn;
-        bv = ld(Bm, idx);
-        cv = ld(Cm, idx);
+#pragma unroll
+    for (int k = 0; k < BPT; ++k) {
+      const int e = tid + k * NT;
+      if (e < N * TS) {
+        const int tt = e / N, nn = e % N;
+        const bool ok = t0 + tt < seq;
+        s_B[nn][tt] = ok ? to_f32(pb[k]) : 0.0f;
+        s_C[nn][tt] = ok ? to_f32(pc[k]) : 0.0f;
       }
-      s_B[nn][tt] = bv;
-      s_C[nn][tt] = cv;
     }
+    if (t0 + TS < seq) fetch(t0 + TS);
     __syncthreads();
 
     float pr[TS];
@@ -186,7 +210,7 @@ __global__ __launch_bounds__(NT) void ss_fwd_kernel(const SSArgs p) {
 #pragma unroll
       for (int m = 0; m < LPC; ++m) y += s_p[cl * LPC + m][tt];
       y = fmaf(Dc, s_x[cl][tt], y);
-      if (z != nullptr) {
+      if (HAS_Z) {
         const float zv = s_z[cl][tt];
         y *= zv * sigmoidf(zv);
       }
@@ -212,7 +236,7 @@ __global__ __launch_bounds__(NT) void ss_bwd_kernel(const SSArgs p) {
   constexpr int LPC = G::LPC, SPL = G::SPL, CPW = G::CPW;
   static_assert(SPL == 1, "backward keeps one state per lane");
   constexpr int TS = 8;  // reduction block (timesteps)
-  constexpr int PC = CK + 4;
+  constexpr int PC = CK + 1;  // odd row stride: conflict-free staging writes
   // chunk tiles [channel][t]
   __shared__ float s_x[CPW][PC], s_dtc[CPW][PC], s_dtb[CPW][PC], s_rng[CPW][PC], s_dy[CPW][PC];
   __shared__ float s_B[N][CK + 1], s_C[N][CK + 1];
@@ -250,42 +274,63 @@ __global__ __launch_bounds__(NT) void ss_bwd_kernel(const SSArgs p) {
   float dD = 0.0f;
   const long rowbase = (long)b * seq * dim;
 
+  // Raw values of the next chunk (in reverse order), fetched one chunk ahead from
+  // clamped in-bounds indices so the loads are never behind a divergent branch.
+  constexpr int EPT = CPW * CK / NT;
+  constexpr int BPT = (N * CK + NT - 1) / NT;
+  TI px[EPT], pdt[EPT], pgo[EPT], pz[EPT];
+  TP pb[BPT], pc[BPT];
+  float pm[EPT];
+  auto fetch = [&](int ts) {
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const int e = tid + q * NT;
+      const int t = min(ts + e / CPW, seq - 1), cc = min(c0 + e % CPW, dim - 1);
+      const long idx = rowbase + (long)t * dim + cc;
+      px[q] = x[idx];
+      pdt[q] = dt[idx];
+      pgo[q] = dout[idx];
+      pz[q] = z != nullptr ? z[idx] : px[q];
+      pm[q] = mean_mode ? p.dtmean[(long)b * seq + t] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      const int e = min(tid + q * NT, N * CK - 1);
+      const long idx = ((long)b * seq + min(ts + e / N, seq - 1)) * N + e % N;
+      pb[q] = Bm[idx];
+      pc[q] = Cm[idx];
+    }
+  };
+  fetch((p.nck - 1) * CK);
+
   for (int k = p.nck - 1; k >= 0; --k) {
     const int ts = k * CK;
     // ---- stage the chunk ------------------------------------------------
-    for (int e = tid; e < CPW * CK; e += NT) {
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const int e = tid + q * NT;
       const int tt = e / CPW, ch = e % CPW;
-      const int t = ts + tt, cc = c0 + ch;
-      float xv = 0.0f, dtc = 0.0f, dtb = 0.0f, rng = 0.0f, go = 0.0f, zv = 0.0f;
-      if (t < seq && cc < dim) {
-        const long idx = rowbase + (long)t * dim + cc;
-        xv = ld(x, idx);
-        const float dtr = ld(dt, idx);
-        dtc = clampf(dtr, DT_MIN, DT_MAX);
-        rng = (dtr >= DT_MIN && dtr <= DT_MAX) ? 1.0f : 0.0f;
-        dtb = mean_mode ? p.dtmean[(long)b * seq + t] : dtc;
-        go = ld(dout, idx);
-        if (z != nullptr) zv = ld(z, idx);
-      }
-      s_x[ch][tt] = xv;
+      const bool ok = (ts + tt < seq) && (c0 + ch < dim);
+      const float dtr = to_f32(pdt[q]);
+      const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
+      s_x[ch][tt] = ok ? to_f32(px[q]) : 0.0f;
       s_dtc[ch][tt] = dtc;
-      s_dtb[ch][tt] = dtb;
-      s_rng[ch][tt] = rng;
-      s_dy[ch][tt] = go;      // raw upstream gradient; gated below if z is present
-      s_o[0][tt][ch] = zv;    // raw z, consumed by the recompute epilogue
+      s_dtb[ch][tt] = ok ? (mean_mode ? pm[q] : dtc) : 0.0f;
+      s_rng[ch][tt] = (ok && dtr >= DT_MIN && dtr <= DT_MAX) ? 1.0f : 0.0f;
+      s_dy[ch][tt] = ok ? to_f32(pgo[q]) : 0.0f;  // raw upstream gradient; gated below if z is present
+      s_o[0][tt][ch] = ok ? to_f32(pz[q]) : 0.0f;  // raw z, consumed by the recompute epilogue
     }
-    for (int e = tid; e < N * CK; e += NT) {
-      const int tt = e / N, nn = e % N;
-      const int t = ts + tt;
-      float bv = 0.0f, cv = 0.0f;
-      if (t < seq) {
-        const long idx = ((long)b * seq + t) * N + nn;
-        bv = ld(Bm, idx);
-        cv = ld(Cm, idx);
+#pragma unroll
+    for (int q = 0; q < BPT; ++q) {
+      const int e = tid + q * NT;
+      if (e < N * CK) {
+        const int tt = e / N, nn = e % N;
+        const bool ok = ts + tt < seq;
+        s_B[nn][tt] = ok ? to_f32(pb[q]) : 0.0f;
+        s_C[nn][tt] = ok ? to_f32(pc[q]) : 0.0f;
       }
-      s_B[nn][tt] = bv;
-      s_C[nn][tt] = cv;
     }
+    if (k > 0) fetch((k - 1) * CK);
     __syncthreads();
 
     // ---- recompute the chunk's states ------------------------------------
@@ -545,7 +590,11 @@ inline WsLayout bwd_layout(int batch, int seq, int dim, int N, bool need_ckpt, b
 template <typename TI, typename TP, int N>
 void launch_fwd_t(hipStream_t s, const SSArgs& a) {
   const int grid = a.batch * a.ntile;
-  ss_fwd_kernel<TI, TP, N, FWD_NT><<<grid, FWD_NT, 0, s>>>(a);
+  const bool mean = a.dtmean != nullptr, hz = a.z != nullptr;
+  if (mean && hz) ss_fwd_kernel<TI, TP, N, FWD_NT, true, true><<<grid, FWD_NT, 0, s>>>(a);
+  else if (mean) ss_fwd_kernel<TI, TP, N, FWD_NT, true, false><<<grid, FWD_NT, 0, s>>>(a);
+  else if (hz) ss_fwd_kernel<TI, TP, N, FWD_NT, false, true><<<grid, FWD_NT, 0, s>>>(a);
+  else ss_fwd_kernel<TI, TP, N, FWD_NT, false, false><<<grid, FWD_NT, 0, s>>>(a);
 }
 
 template <typename TI, typename TP>

@@ -1,0 +1,82 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the public
+header declares, and rejects invalid arguments with the reference's error messages
+before touching the device."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+
+def _declared():
+    names = set()
+    for hdr in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(hdr).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(edf_\w+)\s*\(", text))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from edifice_amd import _native
+
+    return _native.lib()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for must in ("edf_fused_mingru_scan", "edf_fused_selective_scan", "edf_fused_flash_attention",
+                 "edf_fused_delta_net_scan", "edf_fused_gated_delta_net_scan_backward"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_ctypes_table_covers_header():
+    from edifice_amd import _native
+
+    assert set(_declared()) <= set(_native.SIGNATURES), set(_declared()) - set(_native.SIGNATURES)
+
+
+def test_version(lib):
+    assert lib.edf_version() == 1
+
+
+@pytest.mark.parametrize("call", [
+    lambda L: L.edf_fused_mingru_scan(None, None, None, None, None, 0, 4, 4, 0),
+    lambda L: L.edf_fused_minlstm_scan(None, None, None, None, None, None, 2, -1, 4, 0),
+    lambda L: L.edf_fused_selective_scan(None, None, None, None, None, None, None, None, None, None, None, 0,
+                                         1, 0, 4, 16, 1, 0, 0),
+    lambda L: L.edf_fused_flash_attention(None, None, None, None, None, None, 1, 1, 0, 128, 1, 1),
+    lambda L: L.edf_fused_delta_net_scan(None, None, None, None, None, None, None, 0, 0, 4, 2, 4, 0, 0),
+])
+def test_nonpositive_dims_rejected(lib, call):
+    """The reference NIFs return {:error, "dimensions must be positive"} (c_src/edifice_cuda_nif.c:657)."""
+    rc = call(lib)
+    assert rc == 1
+    assert lib.edf_last_error() == b"dimensions must be positive"
+
+
+def test_bad_dtype_and_unsupported_shapes(lib):
+    assert lib.edf_fused_mingru_scan(None, None, None, None, None, 1, 1, 1, 7) == 1
+    assert b"dtype" in lib.edf_last_error()
+    # selective-scan backward supports state sizes 4, 8, 16
+    rc = lib.edf_fused_selective_scan_backward(*([None] * 18), 0, 1, 8, 8, 32, 0, 0, 0)
+    assert rc == 2 and b"state size" in lib.edf_last_error()
+    # a missing workspace is reported, not dereferenced
+    rc = lib.edf_fused_flash_attention_backward(*([ctypes.c_void_p(16)] * 10), None, 0, 1, 1, 8, 64, 1, 1)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+
+
+def test_workspace_queries(lib):
+    assert lib.edf_selective_scan_states_bytes(8, 2048, 1536, 16) == 8 * 1536 * 64 * 16 * 4
+    assert lib.edf_flash_attention_backward_workspace_bytes(4, 32, 4096, 128) == 4 * 32 * 4096 * 4
+    assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 1, 1) > 0  # chunked path
+    assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 0, 1) == 0  # f32: step path
