@@ -149,6 +149,21 @@ def bench_mingru(torch, steps, warmup, B, T, H, dtype):
                 fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
 
 
+def profiled_traffic(kernels, path=os.path.join(ROOT, "profiles", "selective_scan_c2.md")):
+    """HBM bytes per launch of the named kernels, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel reference there); None if absent."""
+    import re
+
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    found = dict((k, int(v)) for k, v in re.findall(r"traffic_bytes\[(\w+)\] = (\d+)", text))
+    if not all(k in found for k in kernels):
+        return None
+    return sum(found[k] for k in kernels)
+
+
 def _time_pair(torch, steps, warmup, fwd, bwd):
     for _ in range(warmup):
         fwd()
@@ -279,6 +294,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain 256 MiB device copy (scale reference for rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, 'How it would shard')",
@@ -300,10 +317,13 @@ def main():
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
-    dominant = "ss_bwd" if ss["bwd_ms"] >= ss["fwd_ms"] else "ss_fwd"
+    bwd_dom = ss["bwd_ms"] >= ss["fwd_ms"]
+    dominant = ("edf_fused_selective_scan_backward (ss_bwd_kernel + dB/dC, dA/dD reductions)" if bwd_dom
+                else "edf_fused_selective_scan (ss_fwd_kernel)")
     dom_ms = max(ss["bwd_ms"], ss["fwd_ms"])
-    dom_bytes = ss["bwd_bytes"] if dominant == "ss_bwd" else ss["fwd_bytes"]
+    dom_bytes = ss["bwd_bytes"] if bwd_dom else ss["fwd_bytes"]
     achieved = dom_bytes / dom_ms / 1e6
+    traffic = profiled_traffic(["ss_bwd_kernel", "ss_reduce_bc_kernel"] if bwd_dom else ["ss_fwd_kernel"])
     line = {
         "metric": "scan HBM GB/s (% of peak); delta-rule & flash-attn fwd+bwd TFLOP/s (% MFMA)",
         "value": round(ss["step_gbs"], 2),
@@ -321,11 +341,17 @@ def main():
                                "A/B/C/D f32, D skip + silu(z) gate", "batch": 8, "seq_len": 2048, "d_inner": 1536,
                    "d_state": 16},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "configs": configs,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_selective_scan()
+    if args.copy_probe:
+        src = torch.ones(64 * 2 ** 20, dtype=torch.float32, device="cuda")  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(line))
 
 
