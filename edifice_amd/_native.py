@@ -43,6 +43,7 @@ SIGNATURES = {
     "edf_fused_gated_delta_net_scan_backward": (
         I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_debug_mfma_32x32x16_bf16": (I, [P, P, P, P]),
+    "edf_debug_acc_kfrag_bf16": (I, [P, P, P]),
 }
 
 

@@ -1,6 +1,7 @@
 // C-ABI entry points of the delta rule (DeltaNet / GatedDeltaNet), forward and backward.
-// Dispatch: the exact per-step kernels (delta_rule_seq.hip) serve every case; the
-// chunked MFMA kernels (delta_rule_chunk.hip) take bf16, per-head beta, head_dim 128.
+// Dispatch: the chunked MFMA kernels (delta_rule_chunk.hip) take bf16, per-head beta,
+// head_dim 128, seq >= 64 (forward and backward); the exact per-step kernels
+// (delta_rule_seq.hip) serve every other case.
 #include "edf_abi.hpp"
 
 namespace edf {
@@ -15,6 +16,10 @@ bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head);
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d);
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
                  void* out, void* workspace, int batch, int seq, int heads, int d);
+size_t dr_chunk_backward_workspace_bytes(int batch, int seq, int heads, int d);
+int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                          const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
+                          void* dalpha, void* workspace, int batch, int seq, int heads, int d);
 
 namespace {
 int check_dr(int batch, int seq, int heads, int d, int dtype, int beta_mode) {
@@ -47,6 +52,13 @@ int bwd(void* stream, const void* q, const void* k, const void* v, const void* b
   if (rc) return rc;
   EDF_REQUIRE(q && k && v && beta && grad_out && dq && dk && dv && dbeta, EDF_ERR_INVALID_ARG,
               "null tensor pointer");
+  const int per_head = beta_mode == EDF_BETA_PER_HEAD;
+  if (dr_chunk_eligible(seq, d, dtype, per_head)) {
+    const size_t need = dr_chunk_backward_workspace_bytes(batch, seq, heads, d);
+    EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+    return dr_chunk_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
+                                 seq, heads, d);
+  }
   const size_t need = dr_seq_backward_workspace_bytes(batch, heads, seq, d);
   EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
   return dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
@@ -68,6 +80,8 @@ size_t edf_delta_rule_workspace_bytes(int batch, int seq_len, int num_heads, int
 size_t edf_delta_rule_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
                                                int beta_mode) {
   if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  if (edf::dr_chunk_eligible(seq_len, head_dim, dtype, beta_mode == EDF_BETA_PER_HEAD))
+    return edf::dr_chunk_backward_workspace_bytes(batch, seq_len, num_heads, head_dim);
   return edf::dr_seq_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
 }
 

@@ -1,25 +1,36 @@
-// Chunked (WY / UT-transform) gated delta rule forward on bf16 MFMA, per-head beta.
+// Chunked (WY / UT-transform) gated delta rule on bf16 MFMA, per-head beta, head_dim 128:
+// forward and backward.
 //
 // Same recurrence as the step path (delta_rule_seq.hip; reference
 // lib/edifice/recurrent/gated_delta_net.ex:300-353 with beta broadcast along the value
-// rows), rewritten per chunk of C = 64 steps with M = S^T [d_k x d_v], gamma_t the
-// cumulative decay inside the chunk and M0 the state entering it:
-//   A  = strict_lower(diag(beta) (Gamma o K K^T)),   Gamma_ts = gamma_t / gamma_s
-//   T  = (I + A)^-1
-//   R  = diag(beta) (V - diag(gamma) K M0)
-//   E  = T R                         (the per-step delta-rule corrections)
-//   O  = diag(gamma) Q M0 + (Q K^T o Gamma o tril) E
-//   M1 = gamma_C M0 + K^T diag(gamma_C / gamma) E
-// The R form folds the usual W = T diag(beta gamma) K into K M0, so the value-sliced
-// phase never needs a d_k-wide W.
+// rows).  With M = S^T [d_k x d_v], rows of Q, K, V the C = 64 steps of a chunk,
+// gamma_t the cumulative decay inside the chunk (lg = log gamma) and h the state
+// entering it:
+//   A     = strict_lower(diag(beta) (Gamma o K K^T)),  Gamma_ts = gamma_t / gamma_s
+//   T     = (I + A)^-1
+//   W     = T diag(beta gamma) K,   U = T diag(beta) V
+//   v_new = U - W h                               (the per-step delta-rule corrections)
+//   O     = diag(gamma) Q h + P v_new,            P = Q K^T o Gamma o tril
+//   h'    = gamma_C h + Kd^T v_new,               Kd = diag(gamma_C / gamma) K
 //
-// Phase 1 (one workgroup per (b, h, chunk), fully parallel): K K^T and Q K^T on MFMA,
-//   the decays, and T by blocked inversion (16x16 diagonal blocks by forward
-//   substitution, off-diagonal blocks by small products); T, the masked Q K^T and the
-//   log-decays go to the workspace (bf16 / f32).
-// Phase 2 (one workgroup per (b, h, 32-wide d_v slice), sequential over chunks): the
-//   f32 state slice lives in registers (one 32x32 MFMA tile per wave); K M0, Q M0, T R,
-//   P E and K^T E-tilde are 32x32x16 bf16 MFMAs with operands staged in LDS.
+// Forward:  prep (parallel over chunks: T, W, U, Kd^T)  ->  scan (sequential over
+//   chunks, one workgroup per (b, h, 32-wide d_v slice): h and v_new per chunk)  ->
+//   out (parallel over chunks: O).
+// Backward: prep, scan (recompute h, v_new)  ->  dlocal (parallel: P^T dO and
+//   Q^T diag(gamma) dO)  ->  reverse scan (dh per chunk, dv_new)  ->  grad (parallel:
+//   dQ, dK, dV, dbeta, dalpha).  With dR = T^T dv_new:
+//   dh_prev = gamma_C dh + Q^T diag(gamma) dO - W^T dv_new,  dv_new = P^T dO + Kd dh
+//   dQ = diag(gamma) dO h^T + dS K
+//   dK = diag(gamma_C/gamma) v_new dh^T - diag(beta gamma) dR h^T + dS^T Q + (dG + dG^T) K
+//   dV = diag(beta) dR,  dA = -dR v_new^T,  dS = dP o Gamma o tril,  dP = dO v_new^T,
+//   dG = diag(beta) dA o Gamma (strict lower),
+//   dbeta_t = <dR_t, V_t - gamma_t (K h)_t> + sum_s dA_ts (Gamma o K K^T)_ts,
+//   dlg collects every gamma above; dalpha_s = (sum_{t >= s} dlg_t) / alpha_s.
+//
+// Every product is a 32x32x16 bf16 MFMA with f32 accumulation.  Operands contract over
+// their contiguous dimension; results are stored with rows contiguous (store_rows) or
+// reused in registers through acc_kfrag, which is why the workspace keeps some tensors
+// in both orientations.
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 #include "edf_mfma.hpp"
@@ -27,29 +38,66 @@
 namespace edf {
 namespace {
 
-constexpr int CH = 64;   // chunk length
-constexpr int DK = 128;  // head dim handled by this path
-constexpr int VS = 32;   // d_v slice per phase-2 workgroup
+constexpr int CH = 64;      // chunk length
+constexpr int DK = 128;     // head dim handled by this path
+constexpr int VS = 32;      // d_v slice per scan workgroup
+constexpr int KS = DK + 8;  // LDS row stride (bf16) of [*][DK] tiles
+constexpr int TS = CH + 8;  // LDS row stride (bf16) of [*][CH] tiles
 
-struct ChunkArgs {
-  const bf16 *q, *k, *v, *beta, *alpha;
+struct CkArgs {
+  const bf16 *q, *k, *v, *beta, *alpha, *dout;
   bf16* out;
-  bf16* tbuf;   // [BH][nch][CH][CH]  T
-  bf16* pbuf;   // [BH][nch][CH][CH]  masked Q K^T o Gamma
-  float* lbuf;  // [BH][nch][CH]      inclusive log-decay inside the chunk
+  bf16 *dq, *dk, *dv, *dbeta, *dalpha;
+  float* lg;  // [ci][CH]       inclusive log-decay inside the chunk (ci = bh * nch + c)
+  bf16* W;    // [ci][CH][DK]   W = T diag(beta gamma) K
+  bf16* Wt;   // [ci][DK][CH]   W^T
+  bf16* Ut;   // [ci][DK][CH]   U^T
+  bf16* Kdt;  // [ci][DK][CH]   Kd^T
+  bf16* Tt;   // [ci][CH][CH]   T^T
+  bf16* hT;   // [ci][DK][DK]   state entering the chunk, [d_v][d_k]
+  bf16* hN;   // [ci][DK][DK]   same, [d_k][d_v]
+  bf16* vT;   // [ci][DK][CH]   v_new^T
+  bf16* vN;   // [ci][CH][DK]   v_new
+  bf16* dvl;  // [ci][DK][CH]   (P^T dO)^T
+  bf16* dhl;  // [ci][DK][DK]   (Q^T diag(gamma) dO)^T, [d_v][d_k]
+  bf16* dmN;  // [ci][DK][DK]   dL/d(state leaving the chunk), [d_k][d_v]
+  bf16* dvT;  // [ci][DK][CH]   (dL/dv_new)^T
   int H, T, nch;
 };
 
-EDF_DEVICE long row_off(const ChunkArgs& p, int b, int h, int t) { return (((long)b * p.T + t) * p.H + h) * DK; }
+EDF_DEVICE long row_off(const CkArgs& p, int b, int h, int t) { return (((long)b * p.T + t) * p.H + h) * DK; }
+EDF_DEVICE long head_off(const CkArgs& p, int b, int h, int t) { return ((long)b * p.T + t) * p.H + h; }
+
+// 8 bf16 of row t (zeros beyond the sequence); the load itself is always in bounds.
+EDF_DEVICE bf16x8 ld_row8(const bf16* base, const CkArgs& p, int b, int h, int t, int col) {
+  const bool ok = t < p.T;
+  const bf16x8 v = *(const bf16x8*)(base + row_off(p, b, h, ok ? t : p.T - 1) + col);
+  return ok ? v : bf16x8{};
+}
+
+// Transposed staging of a chunk of a [B,T,H,DK] tensor: dst[d * TS + t] = scale_t * src[t][d].
+// Lanes run along t so that the 2-byte LDS writes of a wave fill consecutive words.
+EDF_DEVICE void stage_t(bf16* dst, const bf16* src, const CkArgs& p, int b, int h, int t0, const float* scale) {
+  for (int e = threadIdx.x; e < CH * DK / 8; e += 256) {
+    const int t = e & (CH - 1), cb = (e >> 6) * 8;
+    const bf16x8 x = ld_row8(src, p, b, h, t0 + t, cb);
+    const float sc = scale != nullptr ? scale[t] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[(cb + i) * TS + t] = (bf16)((float)x[i] * sc);
+  }
+}
 
 // ---------------------------------------------------------------------------
-// phase 1
+// prep: decays, T = (I + A)^-1, W (and W^T), U^T, Kd^T (and T^T)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dr_chunk_prep_kernel(const ChunkArgs p) {
-  constexpr int KS = DK + 8;
+template <bool BWD>
+__global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   constexpr int AS = CH + 1;
   __shared__ __attribute__((aligned(16))) bf16 sK[CH * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sQ[CH * KS];
+  __shared__ __attribute__((aligned(16))) bf16 sV[CH * KS];
+  __shared__ __attribute__((aligned(16))) bf16 sKb[DK * TS];  // (diag(beta gamma) K)^T
+  __shared__ __attribute__((aligned(16))) bf16 sVb[DK * TS];  // (diag(beta) V)^T
+  __shared__ __attribute__((aligned(16))) bf16 sTb[CH * TS];  // T
   __shared__ float sA[CH * AS];
   __shared__ float sT[CH * AS];
   __shared__ float sX[16 * 17];
@@ -61,18 +109,17 @@ __global__ __launch_bounds__(256) void dr_chunk_prep_kernel(const ChunkArgs p) {
   const long bh = blockIdx.y;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   const int t0 = c * CH;
+  const long ci = bh * p.nch + c;
 
   for (int e = tid; e < CH * DK / 8; e += 256) {
-    const int row = e / (DK / 8), col = (e % (DK / 8)) * 8;
-    const int t = t0 + row;
-    const bool ok = t < p.T;
-    *(bf16x8*)(sK + row * KS + col) = ok ? *(const bf16x8*)(p.k + row_off(p, b, h, t) + col) : bf16x8{};
-    *(bf16x8*)(sQ + row * KS + col) = ok ? *(const bf16x8*)(p.q + row_off(p, b, h, t) + col) : bf16x8{};
+    const int row = e >> 4, col = (e & 15) * 8;
+    *(bf16x8*)(sK + row * KS + col) = ld_row8(p.k, p, b, h, t0 + row, col);
+    *(bf16x8*)(sV + row * KS + col) = ld_row8(p.v, p, b, h, t0 + row, col);
   }
   if (w == 0) {
     const int t = t0 + l;
     const bool ok = t < p.T;
-    const long hi = ((long)b * p.T + t) * p.H + h;
+    const long hi = head_off(p, b, h, ok ? t : p.T - 1);
     float la = (ok && p.alpha != nullptr) ? __logf(to_f32(p.alpha[hi])) : 0.0f;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -84,40 +131,29 @@ __global__ __launch_bounds__(256) void dr_chunk_prep_kernel(const ChunkArgs p) {
   }
   __syncthreads();
 
-  // K K^T and Q K^T tiles (I, J) of 32x32; the upper tile (0, 1) is all zero after masking
+  // A from the K K^T tiles (I, J); the tile above the diagonal is zero
   if (w != 1) {
     const int I = w >= 2 ? 1 : 0, J = (w == 3) ? 1 : 0;
-    f32x16 G = zero16(), QK = zero16();
+    f32x16 G = zero16();
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk) {
-      const bf16x8 bk = *(const bf16x8*)(sK + (J * 32 + li) * KS + kk * 16 + 8 * g);
-      const bf16x8 ak = *(const bf16x8*)(sK + (I * 32 + li) * KS + kk * 16 + 8 * g);
-      const bf16x8 aq = *(const bf16x8*)(sQ + (I * 32 + li) * KS + kk * 16 + 8 * g);
-      G = mfma32(ak, bk, G);
-      QK = mfma32(aq, bk, QK);
+      const bf16x8 a = *(const bf16x8*)(sK + (I * 32 + li) * KS + kk * 16 + 8 * g);
+      const bf16x8 bb = *(const bf16x8*)(sK + (J * 32 + li) * KS + kk * 16 + 8 * g);
+      G = mfma32(a, bb, G);
     }
     const int s = J * 32 + li;
-    bf16* prow = p.pbuf + (((long)bh * p.nch + c) * CH) * CH;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int t = I * 32 + d_row(r, g);
-      const float dec = __expf(lg[t] - lg[s]);
-      sA[t * AS + s] = s < t ? bt[t] * dec * G[r] : 0.0f;
-      prow[t * CH + s] = (bf16)(s <= t ? dec * QK[r] : 0.0f);
+      sA[t * AS + s] = s < t ? bt[t] * __expf(lg[t] - lg[s]) * G[r] : 0.0f;
     }
   } else {
-    // the zero upper tile of P and A
-    const int s = 32 + li;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int t = d_row(r, g);
-      sA[t * AS + s] = 0.0f;
-      p.pbuf[(((long)bh * p.nch + c) * CH + t) * CH + s] = (bf16)0.0f;
-    }
+    for (int r = 0; r < 16; ++r) sA[d_row(r, g) * AS + 32 + li] = 0.0f;
   }
   __syncthreads();
 
-  // diagonal 16x16 blocks of T = (I + A)^-1: wave w, lane j < 16 -> column 16w + j
+  // diagonal 16x16 blocks of T by forward substitution: wave w, lane j < 16 -> column 16w + j
   if (l < 16) {
     const int o = 16 * w;
     float x[16];
@@ -131,175 +167,665 @@ __global__ __launch_bounds__(256) void dr_chunk_prep_kernel(const ChunkArgs p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) sT[(o + i) * AS + o + l] = x[i];
   }
-  // zero the strict upper part of T
   for (int e = tid; e < CH * CH; e += 256) {
     const int i = e / CH, j = e % CH;
     if ((j >> 4) > (i >> 4)) sT[i * AS + j] = 0.0f;
   }
   __syncthreads();
-  // off-diagonal blocks, by distance from the diagonal: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj
-  const int ri = tid >> 4, cj = tid & 15;
-  for (int dist = 1; dist < 4; ++dist) {
-    for (int bj = 0; bj + dist < 4; ++bj) {
-      const int bi = bj + dist;
-      float xs = 0.0f;
-      for (int kb = bj; kb < bi; ++kb)
+  // off-diagonal blocks by distance from the diagonal: T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj
+  {
+    const int ri = tid >> 4, cj = tid & 15;
+    for (int dist = 1; dist < 4; ++dist) {
+      for (int bj = 0; bj + dist < 4; ++bj) {
+        const int bi = bj + dist;
+        float xs = 0.0f;
+        for (int kb = bj; kb < bi; ++kb)
 #pragma unroll
-        for (int m = 0; m < 16; ++m) xs = fmaf(sA[(16 * bi + ri) * AS + 16 * kb + m], sT[(16 * kb + m) * AS + 16 * bj + cj], xs);
-      sX[ri * 17 + cj] = xs;
-      __syncthreads();
-      float y = 0.0f;
+          for (int m = 0; m < 16; ++m)
+            xs = fmaf(sA[(16 * bi + ri) * AS + 16 * kb + m], sT[(16 * kb + m) * AS + 16 * bj + cj], xs);
+        sX[ri * 17 + cj] = xs;
+        __syncthreads();
+        float y = 0.0f;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) y = fmaf(sT[(16 * bi + ri) * AS + 16 * bi + m], sX[m * 17 + cj], y);
-      sT[(16 * bi + ri) * AS + 16 * bj + cj] = -y;
-      __syncthreads();
+        for (int m = 0; m < 16; ++m) y = fmaf(sT[(16 * bi + ri) * AS + 16 * bi + m], sX[m * 17 + cj], y);
+        sT[(16 * bi + ri) * AS + 16 * bj + cj] = -y;
+        __syncthreads();
+      }
     }
   }
-  bf16* tout = p.tbuf + (((long)bh * p.nch + c) * CH) * CH;
-  for (int e = tid; e < CH * CH; e += 256) tout[e] = (bf16)sT[(e / CH) * AS + (e % CH)];
-  if (tid < CH) p.lbuf[((long)bh * p.nch + c) * CH + tid] = lg[tid];
+
+  // bf16 operands: T, (beta gamma K)^T, (beta V)^T; Kd^T and T^T to the workspace
+  const float lgC = lg[CH - 1];
+  for (int e = tid; e < DK * CH / 8; e += 256) {
+    const int d = e >> 3, tb = (e & 7) * 8;
+    bf16x8 kb, vb, kd;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = tb + i;
+      const float kf = (float)sK[t * KS + d];
+      kb[i] = (bf16)(bt[t] * __expf(lg[t]) * kf);
+      vb[i] = (bf16)(bt[t] * (float)sV[t * KS + d]);
+      kd[i] = (bf16)(__expf(lgC - lg[t]) * kf);
+    }
+    *(bf16x8*)(sKb + d * TS + tb) = kb;
+    *(bf16x8*)(sVb + d * TS + tb) = vb;
+    *(bf16x8*)(p.Kdt + ci * DK * CH + d * CH + tb) = kd;
+  }
+  for (int e = tid; e < CH * CH / 8; e += 256) {
+    const int row = e >> 3, cb = (e & 7) * 8;
+    bf16x8 tv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tv[i] = (bf16)sT[row * AS + cb + i];
+    *(bf16x8*)(sTb + row * TS + cb) = tv;
+    if (BWD) {
+      bf16x8 tt;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tt[i] = (bf16)sT[(cb + i) * AS + row];
+      *(bf16x8*)(p.Tt + ci * CH * CH + row * CH + cb) = tt;
+    }
+  }
+  if (tid < CH) p.lg[ci * CH + tid] = lg[tid];
+  __syncthreads();
+
+  // T is lower triangular, so row tile 0 only reaches s < 32 (k-steps 0, 1)
+#pragma unroll
+  for (int J = 0; J < 2; ++J) {
+    // W^T: rows d_k = 32 w + .., columns t = 32 J + li  ->  W stored [t][d_k]
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 0; kk < 2 * (J + 1); ++kk) {
+      const bf16x8 a = *(const bf16x8*)(sKb + (32 * w + li) * TS + 16 * kk + 8 * g);
+      const bf16x8 bb = *(const bf16x8*)(sTb + (32 * J + li) * TS + 16 * kk + 8 * g);
+      X = mfma32(a, bb, X);
+    }
+    store_rows(p.W + ci * CH * DK + (long)(32 * J) * DK + 32 * w, DK, X, li, g);
+    // U: rows t = 32 J + .., columns d_v = 32 w + li  ->  U^T stored [d_v][t]
+    X = zero16();
+#pragma unroll
+    for (int kk = 0; kk < 2 * (J + 1); ++kk) {
+      const bf16x8 a = *(const bf16x8*)(sTb + (32 * J + li) * TS + 16 * kk + 8 * g);
+      const bf16x8 bb = *(const bf16x8*)(sVb + (32 * w + li) * TS + 16 * kk + 8 * g);
+      X = mfma32(a, bb, X);
+    }
+    store_rows(p.Ut + ci * DK * CH + (long)(32 * w) * CH + 32 * J, CH, X, li, g);
+    if (BWD) {
+      // W: rows t = 32 J + .., columns d_k = 32 w + li  ->  W^T stored [d_k][t]
+      X = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 2 * (J + 1); ++kk) {
+        const bf16x8 a = *(const bf16x8*)(sTb + (32 * J + li) * TS + 16 * kk + 8 * g);
+        const bf16x8 bb = *(const bf16x8*)(sKb + (32 * w + li) * TS + 16 * kk + 8 * g);
+        X = mfma32(a, bb, X);
+      }
+      store_rows(p.Wt + ci * DK * CH + (long)(32 * w) * CH + 32 * J, CH, X, li, g);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// phase 2
+// scan over chunks, one workgroup per (b, h, d_v slice); wave w owns state rows
+// d_k = 32 w .. 32 w + 31 of the slice as one f32 accumulator tile.
+//   MODE 0 / 1 (forward states):  v = U - W h;          h = gamma_C h + Kd^T v
+//   MODE 2 (reverse, gradients):   v = dvl + Kd dh;      dh = gamma_C dh + dhl - W^T v
+// MODE 0 stores h as [d_v][d_k] and v^T; MODE 1 stores h as [d_k][d_v] and v;
+// MODE 2 stores dh (the gradient of the state leaving each chunk) as [d_k][d_v] and v^T.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dr_chunk_state_kernel(const ChunkArgs p) {
-  constexpr int KS = DK + 8;  // [t][dk]
-  constexpr int TS = CH + 8;  // [*][t]
-  __shared__ __attribute__((aligned(16))) bf16 sK[CH * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sQ[CH * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sKt[DK * TS];
-  __shared__ __attribute__((aligned(16))) bf16 sT[CH * TS];
-  __shared__ __attribute__((aligned(16))) bf16 sP[CH * TS];
-  __shared__ __attribute__((aligned(16))) bf16 sMt[VS * KS];  // M0^T [dv][dk]
-  __shared__ __attribute__((aligned(16))) bf16 sRt[VS * TS];  // R^T  [dv][t]
-  __shared__ __attribute__((aligned(16))) bf16 sEt[VS * TS];  // E^T
-  __shared__ __attribute__((aligned(16))) bf16 sEs[VS * TS];  // (gamma_C / gamma) E, transposed
-  __shared__ float sV[CH * (VS + 1)];
-  __shared__ float lg[CH], bt[CH];
+template <int MODE>
+__global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
+  constexpr bool REV = MODE == 2;
+  __shared__ __attribute__((aligned(16))) bf16 sA1[2][CH * KS];  // W, or Kd in the reverse pass: [t][d_k]
+  __shared__ __attribute__((aligned(16))) bf16 sSt[2][VS * KS];  // state slice, [d_v][d_k]
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
-  const int nsl = DK / VS;
-  const long bh = blockIdx.x / nsl;
-  const int sl = blockIdx.x % nsl;
+  constexpr int NSL = DK / VS;
+  const int logical = remap_xcd(blockIdx.x, gridDim.x);  // the slices of one head share an XCD
+  const long bh = logical / NSL;
+  const int v0 = (logical % NSL) * VS;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-  const int v0 = sl * VS;
 
-  f32x16 M = zero16();  // rows dk = 32 w + d_row(r, g), column dv = li (within the slice)
-  for (int c = 0; c < p.nch; ++c) {
-    const int t0 = c * CH;
-    __syncthreads();
-    for (int e = tid; e < CH * DK / 8; e += 256) {
-      const int row = e / (DK / 8), col = (e % (DK / 8)) * 8;
-      const int t = t0 + row;
-      const bool ok = t < p.T;
-      const bf16x8 kv = ok ? *(const bf16x8*)(p.k + row_off(p, b, h, t) + col) : bf16x8{};
-      *(bf16x8*)(sK + row * KS + col) = kv;
-      *(bf16x8*)(sQ + row * KS + col) = ok ? *(const bf16x8*)(p.q + row_off(p, b, h, t) + col) : bf16x8{};
+  f32x16 S = zero16();  // rows d_k = 32 w + d_row(r, g), column d_v = v0 + li
+
+  // next chunk's operands, loaded one chunk ahead
+  bf16x8 pa1[4];
+  float pl1[4];
+  bf16x8 pa2[4];
+  bf16x4 px0[2][4];
+  bf16x4 py0[4];
+  float plgC = 0.0f;
+  auto fetch = [&](int c) {
+    const long ci = bh * p.nch + c;
 #pragma unroll
-      for (int e2 = 0; e2 < 8; ++e2) sKt[(col + e2) * TS + row] = kv[e2];
-    }
-    {
-      const bf16* tsrc = p.tbuf + (((long)bh * p.nch + c) * CH) * CH;
-      const bf16* psrc = p.pbuf + (((long)bh * p.nch + c) * CH) * CH;
-      for (int e = tid; e < CH * CH / 8; e += 256) {
-        const int row = e / (CH / 8), col = (e % (CH / 8)) * 8;
-        *(bf16x8*)(sT + row * TS + col) = *(const bf16x8*)(tsrc + row * CH + col);
-        *(bf16x8*)(sP + row * TS + col) = *(const bf16x8*)(psrc + row * CH + col);
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i;
+      const int row = e >> 4, col = (e & 15) * 8;
+      if (!REV) {
+        pa1[i] = *(const bf16x8*)(p.W + ci * CH * DK + row * DK + col);
+      } else {
+        pa1[i] = ld_row8(p.k, p, b, h, c * CH + row, col);
+        pl1[i] = p.lg[ci * CH + row];
       }
     }
-    for (int e = tid; e < CH * VS; e += 256) {
-      const int row = e / VS, col = e % VS;
-      const int t = t0 + row;
-      sV[row * (VS + 1) + col] = t < p.T ? to_f32(p.v[row_off(p, b, h, t) + v0 + col]) : 0.0f;
-    }
-    if (tid < CH) {
-      const int t = t0 + tid;
-      lg[tid] = p.lbuf[((long)bh * p.nch + c) * CH + tid];
-      bt[tid] = t < p.T ? to_f32(p.beta[((long)b * p.T + t) * p.H + h]) : 0.0f;
-    }
-    // M0^T tile of this wave -> LDS (bf16)
+    const bf16* a2 = (REV ? p.Wt : p.Kdt) + ci * DK * CH + (32 * w + li) * CH + 8 * g;
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      bf16x4 m4;
+    for (int kk = 0; kk < 4; ++kk) pa2[kk] = *(const bf16x8*)(a2 + 16 * kk);
+    const bf16* x0 = (REV ? p.dvl : p.Ut) + ci * DK * CH + (v0 + li) * CH + 4 * g;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) m4[e] = (bf16)M[rb * 4 + e];
-      *(bf16x4*)(sMt + li * KS + 32 * w + 8 * rb + 4 * g) = m4;
+    for (int T = 0; T < 2; ++T)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) px0[T][q] = *(const bf16x4*)(x0 + 32 * T + 8 * q);
+    if (REV) {
+      const bf16* y0 = p.dhl + ci * DK * DK + (v0 + li) * DK + 32 * w + 4 * g;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) py0[q] = *(const bf16x4*)(y0 + 8 * q);
     }
+    plgC = p.lg[ci * CH + CH - 1];
+  };
+  fetch(REV ? p.nch - 1 : 0);
+
+  for (int it = 0; it < p.nch; ++it) {
+    const int c = REV ? p.nch - 1 - it : it;
+    const long ci = bh * p.nch + c;
+    bf16* sa = sA1[it & 1];
+    bf16* ss = sSt[it & 1];
+    // publish the state entering (forward) / leaving (reverse) chunk c
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (bf16)S[4 * q + e];
+      *(bf16x4*)(ss + li * KS + 32 * w + 8 * q + 4 * g) = v;
+      if (MODE == 0) *(bf16x4*)(p.hT + ci * DK * DK + (long)(v0 + li) * DK + 32 * w + 8 * q + 4 * g) = v;
+    }
+    if (MODE != 0) {
+      bf16* dst = (MODE == 1 ? p.hN : p.dmN) + ci * DK * DK + v0 + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[(long)(32 * w + d_row(r, g)) * DK] = (bf16)S[r];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i;
+      const int row = e >> 4, col = (e & 15) * 8;
+      bf16x8 a = pa1[i];
+      if (REV) {
+        const float sc = __expf(plgC - pl1[i]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = (bf16)((float)a[j] * sc);
+      }
+      *(bf16x8*)(sa + row * KS + col) = a;
+    }
+    bf16x8 a2[4];
+    bf16x4 x0[2][4], y0[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) a2[kk] = pa2[kk];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      x0[0][q] = px0[0][q];
+      x0[1][q] = px0[1][q];
+      y0[q] = py0[q];
+    }
+    const float gC = __expf(plgC);
+    if (it + 1 < p.nch) fetch(REV ? c - 1 : c + 1);
     __syncthreads();
 
-    // K M0 (waves 0, 1) and Q M0 (waves 2, 3): rows t = 32 (w & 1) + d_row, column dv = li
-    const int tb = 32 * (w & 1);
-    const bf16* src = (w < 2) ? sK : sQ;
-    f32x16 X = zero16();
+    // X = A1 * state: rows t (two tiles), column d_v
+    f32x16 X[2];
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) {
-      const bf16x8 a = *(const bf16x8*)(src + (tb + li) * KS + kk * 16 + 8 * g);
-      const bf16x8 bm = *(const bf16x8*)(sMt + li * KS + kk * 16 + 8 * g);
-      X = mfma32(a, bm, X);
-    }
-    if (w < 2) {  // R = beta (V - gamma K M0), stored transposed
+    for (int T = 0; T < 2; ++T) {
+      X[T] = zero16();
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        bf16x4 r4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = tb + 8 * rb + 4 * g + e;
-          r4[e] = (bf16)(bt[t] * (sV[t * (VS + 1) + li] - __expf(lg[t]) * X[rb * 4 + e]));
-        }
-        *(bf16x4*)(sRt + li * TS + tb + 8 * rb + 4 * g) = r4;
-      }
-    }
-    __syncthreads();
-    if (w < 2) {  // E = T R (T lower triangular: s < 32 (w + 1))
-      f32x16 E = zero16();
-      const int send = 32 * (w + 1);
-      for (int s0 = 0; s0 < send; s0 += 16) {
-        const bf16x8 a = *(const bf16x8*)(sT + (tb + li) * TS + s0 + 8 * g);
-        const bf16x8 br = *(const bf16x8*)(sRt + li * TS + s0 + 8 * g);
-        E = mfma32(a, br, E);
-      }
-      const float lgC = lg[CH - 1];
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        bf16x4 e4, s4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = tb + 8 * rb + 4 * g + e;
-          e4[e] = (bf16)E[rb * 4 + e];
-          s4[e] = (bf16)(__expf(lgC - lg[t]) * E[rb * 4 + e]);
-        }
-        *(bf16x4*)(sEt + li * TS + tb + 8 * rb + 4 * g) = e4;
-        *(bf16x4*)(sEs + li * TS + tb + 8 * rb + 4 * g) = s4;
-      }
-    }
-    __syncthreads();
-    if (w >= 2) {  // O = gamma Q M0 + P E
-      f32x16 O = zero16();
-      const int send = 32 * ((w & 1) + 1);
-      for (int s0 = 0; s0 < send; s0 += 16) {
-        const bf16x8 a = *(const bf16x8*)(sP + (tb + li) * TS + s0 + 8 * g);
-        const bf16x8 be = *(const bf16x8*)(sEt + li * TS + s0 + 8 * g);
-        O = mfma32(a, be, O);
+      for (int kk = 0; kk < DK / 16; ++kk) {
+        const bf16x8 a = *(const bf16x8*)(sa + (32 * T + li) * KS + 16 * kk + 8 * g);
+        const bf16x8 bb = *(const bf16x8*)(ss + li * KS + 16 * kk + 8 * g);
+        X[T] = mfma32(a, bb, X[T]);
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int t = tb + d_row(r, g);
-        if (t0 + t < p.T) p.out[row_off(p, b, h, t0 + t) + v0 + li] = (bf16)fmaf(__expf(lg[t]), X[r], O[r]);
+        const float x0v = (float)x0[T][r >> 2][r & 3];
+        X[T][r] = REV ? x0v + X[T][r] : x0v - X[T][r];
       }
     }
-    // M1 = gamma_C M0 + K^T E-tilde  (this wave's 32 rows of d_k)
-    const float gC = __expf(lg[CH - 1]);
+    // store v (one tile per wave pair)
+    if (MODE != 1) {
+      bf16* dst = (REV ? p.dvT : p.vT) + ci * DK * CH + (long)v0 * CH;
+      if (w == 0) store_rows(dst, CH, X[0], li, g);
+      else if (w == 1) store_rows(dst + 32, CH, X[1], li, g);
+    } else if (w >= 2) {
+      bf16* dst = p.vN + ci * CH * DK + (long)(32 * (w - 2)) * DK + v0 + li;
+      const f32x16 Xw = w == 2 ? X[0] : X[1];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) M[r] *= gC;
+      for (int r = 0; r < 16; ++r) dst[(long)d_row(r, g) * DK] = (bf16)Xw[r];
+    }
+    // state update: Y = A2 * v, contracting over t with v taken straight from registers
+    f32x16 Y = zero16();
 #pragma unroll
-    for (int s0 = 0; s0 < CH; s0 += 16) {
-      const bf16x8 a = *(const bf16x8*)(sKt + (32 * w + li) * TS + s0 + 8 * g);
-      const bf16x8 be = *(const bf16x8*)(sEs + li * TS + s0 + 8 * g);
-      M = mfma32(a, be, M);
+    for (int kk = 0; kk < 4; ++kk) Y = mfma32(a2[kk], acc_kfrag(X[kk >> 1], kk & 1), Y);
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      S[r] = REV ? fmaf(gC, S[r], (float)y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out: O = diag(gamma) Q h + P v_new, computed as O^T so that rows of O store contiguously
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16 sP[CH * TS];  // P [t][s]
+  __shared__ float lg[CH];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int c = blockIdx.x;
+  const long bh = blockIdx.y;
+  const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  const int t0 = c * CH;
+  const long ci = bh * p.nch + c;
+  if (tid < CH) lg[tid] = p.lg[ci * CH + tid];
+  __syncthreads();
+
+  // S^T tiles (rows s = 32 I, columns t = 32 J): (0,0), (0,1), (1,1); P[t<32][s>=32] = 0
+  if (w < 3) {
+    const int I = w == 2 ? 1 : 0, J = w == 0 ? 0 : 1;
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      X = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
+                 ld_row8(p.q, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), X);
+    const int t = 32 * J + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int s = 32 * I + d_row(r, g);
+      X[r] = s <= t ? X[r] * __expf(lg[t] - lg[s]) : 0.0f;
+    }
+    store_rows(sP + (32 * J) * TS + 32 * I, TS, X, li, g);
+  } else {
+    store_rows(sP + 32, TS, zero16(), li, g);
+  }
+  __syncthreads();
+
+#pragma unroll
+  for (int J = 0; J < 2; ++J) {
+    const int t = 32 * J + li;
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      X = mfma32(*(const bf16x8*)(p.hT + ci * DK * DK + (long)(32 * w + li) * DK + 16 * kk + 8 * g),
+                 ld_row8(p.q, p, b, h, t0 + t, 16 * kk + 8 * g), X);
+    const float gm = __expf(lg[t]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) X[r] *= gm;
+#pragma unroll
+    for (int kk = 0; kk < 2 * (J + 1); ++kk)
+      X = mfma32(*(const bf16x8*)(p.vT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g),
+                 *(const bf16x8*)(sP + t * TS + 16 * kk + 8 * g), X);
+    if (t0 + t < p.T) store_rows(p.out + row_off(p, b, h, t0 + 32 * J) + 32 * w, (long)p.H * DK, X, li, g);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dlocal: dvl = (P^T dO)^T and dhl = (Q^T diag(gamma) dO)^T per chunk
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16 sPt[CH * TS];  // P^T [s][t]
+  __shared__ __attribute__((aligned(16))) bf16 sdOt[DK * TS];  // dO^T [d_v][t]
+  __shared__ __attribute__((aligned(16))) bf16 sQg[DK * TS];  // (diag(gamma) Q)^T [d_k][t]
+  __shared__ float lg[CH], gm[CH];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int c = blockIdx.x;
+  const long bh = blockIdx.y;
+  const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  const int t0 = c * CH;
+  const long ci = bh * p.nch + c;
+  if (tid < CH) {
+    lg[tid] = p.lg[ci * CH + tid];
+    gm[tid] = __expf(lg[tid]);
+  }
+  __syncthreads();
+  stage_t(sdOt, p.dout, p, b, h, t0, nullptr);
+  stage_t(sQg, p.q, p, b, h, t0, gm);
+
+  // S = Q K^T tile (rows t = 32 I, columns s = 32 J) -> P^T [s][t]
+  {
+    const int I = w >> 1, J = w & 1;
+    f32x16 X = zero16();
+    if (w != 1) {
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk)
+        X = mfma32(ld_row8(p.q, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
+                   ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), X);
+      const int s = 32 * J + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * I + d_row(r, g);
+        X[r] = s <= t ? X[r] * __expf(lg[t] - lg[s]) : 0.0f;
+      }
+    }
+    store_rows(sPt + (32 * J) * TS + 32 * I, TS, X, li, g);
+  }
+  __syncthreads();
+
+  // P^T dO: rows s (tile I), columns d_v = 32 w + li; P^T[s][t] = 0 for t < s
+#pragma unroll
+  for (int I = 0; I < 2; ++I) {
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 2 * I; kk < 4; ++kk)
+      X = mfma32(*(const bf16x8*)(sPt + (32 * I + li) * TS + 16 * kk + 8 * g),
+                 *(const bf16x8*)(sdOt + (32 * w + li) * TS + 16 * kk + 8 * g), X);
+    store_rows(p.dvl + ci * DK * CH + (long)(32 * w) * CH + 32 * I, CH, X, li, g);
+  }
+  // Q^T diag(gamma) dO: rows d_k (tile I), columns d_v = 32 w + li
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      X = mfma32(*(const bf16x8*)(sQg + (32 * I + li) * TS + 16 * kk + 8 * g),
+                 *(const bf16x8*)(sdOt + (32 * w + li) * TS + 16 * kk + 8 * g), X);
+    store_rows(p.dhl + ci * DK * DK + (long)(32 * w) * DK + 32 * I, DK, X, li, g);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// grad: dQ, dK, dV, dbeta, dalpha of one chunk
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
+  constexpr int ZS = CH + 1;
+  __shared__ __attribute__((aligned(16))) bf16 sQt[DK * TS];  // Q^T [d_k][t]
+  __shared__ __attribute__((aligned(16))) bf16 sKt[DK * TS];  // K^T [d_k][s]
+  __shared__ __attribute__((aligned(16))) bf16 sdR[CH * KS];  // dR [s][d_v]
+  __shared__ __attribute__((aligned(16))) bf16 sdS[CH * TS];  // dS [t][s]
+  __shared__ __attribute__((aligned(16))) bf16 sdSt[CH * TS];  // dS^T [s][t]
+  __shared__ __attribute__((aligned(16))) bf16 sdF[CH * TS];  // dG + dG^T
+  __shared__ float sZ[CH * ZS];  // dP P + dA A
+  __shared__ float sB[CH * ZS];  // dA Gamma (K K^T), s < t
+  __shared__ float lg[CH], bt[CH], dlg[CH], dbt[CH];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int c = blockIdx.x;
+  const long bh = blockIdx.y;
+  const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  const int t0 = c * CH;
+  const long ci = bh * p.nch + c;
+  const bf16* hN = p.hN + ci * DK * DK;
+  const bf16* vN = p.vN + ci * CH * DK;
+
+  if (tid < CH) {
+    const int t = t0 + tid;
+    lg[tid] = p.lg[ci * CH + tid];
+    bt[tid] = t < p.T ? to_f32(p.beta[head_off(p, b, h, t)]) : 0.0f;
+    dlg[tid] = 0.0f;
+    dbt[tid] = 0.0f;
+  }
+  stage_t(sQt, p.q, p, b, h, t0, nullptr);
+  stage_t(sKt, p.k, p, b, h, t0, nullptr);
+  __syncthreads();
+  const float lgC = lg[CH - 1];
+
+  // dR^T = dv_new^T T: rows d_v = 32 w + .., columns s = 32 J + li  (T[t][s] = 0 for t < s)
+#pragma unroll
+  for (int J = 0; J < 2; ++J) {
+    const int s = 32 * J + li;
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 2 * J; kk < 4; ++kk)
+      X = mfma32(*(const bf16x8*)(p.dvT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g),
+                 *(const bf16x8*)(p.Tt + ci * CH * CH + (long)s * CH + 16 * kk + 8 * g), X);
+    store_rows(sdR + (32 * J) * KS + 32 * w, KS, X, li, g);
+    // dV = beta dR;  dbeta += <dR_s, V_s>
+    const bool ok = t0 + s < p.T;
+    const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1) + 32 * w + 4 * g;
+    if (ok) store_rows(p.dv + row_off(p, b, h, t0 + 32 * J) + 32 * w, (long)p.H * DK, X, li, g, bt[s]);
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bf16x4 vv = *(const bf16x4*)(p.v + ro + 8 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fmaf(X[4 * q + e], (float)vv[e], acc);
+    }
+    acc += __shfl_xor(acc, 32);
+    if (g == 0) atomicAdd(&dbt[s], ok ? acc : 0.0f);
+  }
+
+  // S = Q K^T and G = K K^T on tile (I, J) = (w / 2, w % 2); tile (0, 1) is above the diagonal
+  const int I = w >> 1, J = w & 1;
+  f32x16 Sq = zero16(), Gk = zero16();
+  if (w != 1) {
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      const bf16x8 bk = ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g);
+      Sq = mfma32(ld_row8(p.q, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g), bk, Sq);
+      Gk = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g), bk, Gk);
     }
   }
+  __syncthreads();  // sdR complete
+
+  {
+    const int s = 32 * J + li;
+    f32x16 dS = zero16();
+    if (w != 1) {
+      f32x16 dA = zero16(), dP = zero16();
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk) {
+        const bf16x8 bv = *(const bf16x8*)(vN + (long)s * DK + 16 * kk + 8 * g);
+        dA = mfma32(*(const bf16x8*)(sdR + (32 * I + li) * KS + 16 * kk + 8 * g), bv, dA);
+        dP = mfma32(ld_row8(p.dout, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g), bv, dP);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = 32 * I + d_row(r, g);
+        const float gam = __expf(lg[t] - lg[s]);
+        const bool mP = s <= t, mA = s < t;
+        const float Pv = mP ? Sq[r] * gam : 0.0f;
+        const float GG = mA ? gam * Gk[r] : 0.0f;
+        const float dAv = -dA[r];
+        dS[r] = mP ? dP[r] * gam : 0.0f;
+        const float dG = mA ? bt[t] * dAv * gam : 0.0f;
+        sZ[t * ZS + s] = dP[r] * Pv + dAv * bt[t] * GG;
+        sB[t * ZS + s] = dAv * GG;
+        sdS[t * TS + s] = (bf16)dS[r];
+        if (mA) {
+          sdF[t * TS + s] = (bf16)dG;
+          sdF[s * TS + t] = (bf16)dG;
+        } else if (s == t) {
+          sdF[t * TS + t] = (bf16)0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int t = d_row(r, g);
+        sZ[t * ZS + s] = 0.0f;
+        sB[t * ZS + s] = 0.0f;
+        sdS[t * TS + s] = (bf16)0.0f;
+      }
+    }
+    store_rows(sdSt + (32 * J) * TS + 32 * I, TS, dS, li, g);
+  }
+  __syncthreads();
+
+  if (tid < CH) {
+    float acc = 0.0f;
+    for (int s = 0; s < CH; ++s) acc += sZ[tid * ZS + s] - sZ[s * ZS + tid];
+    atomicAdd(&dlg[tid], acc);
+  } else if (tid < 2 * CH) {
+    const int t = tid - CH;
+    float acc = 0.0f;
+    for (int s = 0; s < CH; ++s) acc += sB[t * ZS + s];
+    atomicAdd(&dbt[t], acc);
+  }
+
+  // dQ^T and dK^T: rows d_k = 32 w + .., columns t (or s) = 32 J + li
+  float dlgC = 0.0f;
+#pragma unroll
+  for (int J2 = 0; J2 < 2; ++J2) {
+    const int t = 32 * J2 + li;
+    const bool ok = t0 + t < p.T;
+    // dQ^T = gamma (h dO^T) + K^T dS^T
+    f32x16 X = zero16();
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      X = mfma32(*(const bf16x8*)(hN + (long)(32 * w + li) * DK + 16 * kk + 8 * g),
+                 ld_row8(p.dout, p, b, h, t0 + t, 16 * kk + 8 * g), X);
+    const float gmt = __expf(lg[t]);
+    float qx = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      qx = fmaf((float)sQt[(32 * w + d_row(r, g)) * TS + t], X[r], qx);
+      X[r] *= gmt;
+    }
+    qx += __shfl_xor(qx, 32);
+    if (g == 0) atomicAdd(&dlg[t], gmt * qx);
+#pragma unroll
+    for (int kk = 0; kk < 2 * (J2 + 1); ++kk)
+      X = mfma32(*(const bf16x8*)(sKt + (32 * w + li) * TS + 16 * kk + 8 * g),
+                 *(const bf16x8*)(sdS + t * TS + 16 * kk + 8 * g), X);
+    if (ok) store_rows(p.dq + row_off(p, b, h, t0 + 32 * J2) + 32 * w, (long)p.H * DK, X, li, g);
+
+    // dK^T = (gamma_C / gamma) dh v^T - (beta gamma) h dR^T + Q^T dS + K^T dF
+    f32x16 X1 = zero16(), X2 = zero16(), X3 = zero16();
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      const bf16x8 ah = *(const bf16x8*)(hN + (long)(32 * w + li) * DK + 16 * kk + 8 * g);
+      X1 = mfma32(*(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * w + li) * DK + 16 * kk + 8 * g),
+                  *(const bf16x8*)(vN + (long)t * DK + 16 * kk + 8 * g), X1);
+      X2 = mfma32(ah, *(const bf16x8*)(sdR + t * KS + 16 * kk + 8 * g), X2);
+    }
+#pragma unroll
+    for (int kk = 2 * J2; kk < 4; ++kk)
+      X3 = mfma32(*(const bf16x8*)(sQt + (32 * w + li) * TS + 16 * kk + 8 * g),
+                  *(const bf16x8*)(sdSt + t * TS + 16 * kk + 8 * g), X3);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      X3 = mfma32(*(const bf16x8*)(sKt + (32 * w + li) * TS + 16 * kk + 8 * g),
+                  *(const bf16x8*)(sdF + t * TS + 16 * kk + 8 * g), X3);
+    const float sc1 = __expf(lgC - lg[t]);
+    const float sc2 = bt[t] * gmt;
+    float k1 = 0.0f, k2 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float kv = (float)sKt[(32 * w + d_row(r, g)) * TS + t];
+      k1 = fmaf(kv, X1[r], k1);
+      k2 = fmaf(kv, X2[r], k2);
+      X3[r] += sc1 * X1[r] - sc2 * X2[r];
+    }
+    k1 += __shfl_xor(k1, 32);
+    k2 += __shfl_xor(k2, 32);
+    if (g == 0) {
+      atomicAdd(&dlg[t], -sc1 * k1 - sc2 * k2);
+      atomicAdd(&dbt[t], -gmt * k2);
+      dlgC += sc1 * k1;
+    }
+    if (ok) store_rows(p.dk + row_off(p, b, h, t0 + 32 * J2) + 32 * w, (long)p.H * DK, X3, li, g);
+  }
+  // gamma_C <dh, h> and the Kd terms enter the decay of the last step
+  {
+    const bf16* dm = p.dmN + ci * DK * DK;
+    float acc = 0.0f;
+    for (int e = tid; e < DK * DK / 8; e += 256) {
+      const bf16x8 x = *(const bf16x8*)(dm + 8 * e);
+      const bf16x8 y = *(const bf16x8*)(hN + 8 * e);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fmaf((float)x[i], (float)y[i], acc);
+    }
+    acc = acc * __expf(lgC) + dlgC;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    if (l == 0) atomicAdd(&dlg[CH - 1], acc);
+  }
+  __syncthreads();
+
+  if (w == 0) {
+    // dlog(alpha_s) = sum_{t >= s} dlg_t
+    float x = dlg[l];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_down(x, off);
+      if (l + off < 64) x += y;
+    }
+    const int t = t0 + l;
+    if (t < p.T) {
+      const long hi = head_off(p, b, h, t);
+      p.dbeta[hi] = (bf16)dbt[l];
+      if (p.dalpha != nullptr) p.dalpha[hi] = (bf16)(x / to_f32(p.alpha[hi]));
+    }
+  }
+}
+
+__global__ void dr_ck_debug_kfrag_kernel(const float* x, bf16* out) {
+  const int l = threadIdx.x, g = l >> 5, li = l & 31;
+  f32x16 t0, t1;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    t0[r] = x[d_row(r, g) * 32 + li];
+    t1[r] = x[(32 + d_row(r, g)) * 32 + li];
+  }
+  *(bf16x8*)(out + (l * 4 + 0) * 8) = acc_kfrag(t0, 0);
+  *(bf16x8*)(out + (l * 4 + 1) * 8) = acc_kfrag(t0, 1);
+  *(bf16x8*)(out + (l * 4 + 2) * 8) = acc_kfrag(t1, 0);
+  *(bf16x8*)(out + (l * 4 + 3) * 8) = acc_kfrag(t1, 1);
+}
+
+struct Layout {
+  size_t lg, W, Wt, Ut, Kdt, Tt, hT, hN, vT, vN, dvl, dhl, dmN, dvT, total;
+};
+
+inline size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+Layout layout(int batch, int seq, int heads, bool bwd) {
+  const size_t nci = (size_t)batch * heads * ((seq + CH - 1) / CH);
+  const size_t tile_ck = nci * CH * DK * sizeof(bf16), tile_kk = nci * DK * DK * sizeof(bf16);
+  Layout L{};
+  size_t off = 0;
+  auto take = [&](size_t& slot, size_t bytes, bool use) {
+    slot = use ? off : 0;
+    if (use) off += a256(bytes);
+  };
+  take(L.lg, nci * CH * sizeof(float), true);
+  take(L.W, tile_ck, true);
+  take(L.Wt, tile_ck, bwd);
+  take(L.Ut, tile_ck, true);
+  take(L.Kdt, tile_ck, true);
+  take(L.Tt, nci * CH * CH * sizeof(bf16), bwd);
+  take(L.hT, tile_kk, !bwd);
+  take(L.hN, tile_kk, bwd);
+  take(L.vT, tile_ck, !bwd);
+  take(L.vN, tile_ck, bwd);
+  take(L.dvl, tile_ck, bwd);
+  take(L.dhl, tile_kk, bwd);
+  take(L.dmN, tile_kk, bwd);
+  take(L.dvT, tile_ck, bwd);
+  L.total = off;
+  return L;
+}
+
+CkArgs make_args(const Layout& L, void* workspace, bool bwd, int seq, int heads) {
+  CkArgs a{};
+  char* ws = (char*)workspace;
+  a.lg = (float*)(ws + L.lg);
+  a.W = (bf16*)(ws + L.W);
+  a.Ut = (bf16*)(ws + L.Ut);
+  a.Kdt = (bf16*)(ws + L.Kdt);
+  if (bwd) {
+    a.Wt = (bf16*)(ws + L.Wt);
+    a.Tt = (bf16*)(ws + L.Tt);
+    a.hN = (bf16*)(ws + L.hN);
+    a.vN = (bf16*)(ws + L.vN);
+    a.dvl = (bf16*)(ws + L.dvl);
+    a.dhl = (bf16*)(ws + L.dhl);
+    a.dmN = (bf16*)(ws + L.dmN);
+    a.dvT = (bf16*)(ws + L.dvT);
+  } else {
+    a.hT = (bf16*)(ws + L.hT);
+    a.vT = (bf16*)(ws + L.vT);
+  }
+  a.H = heads;
+  a.T = seq;
+  a.nch = (seq + CH - 1) / CH;
+  return a;
 }
 
 }  // namespace
@@ -309,29 +835,65 @@ bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head) {
 }
 
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d) {
-  const size_t nch = (seq + CH - 1) / CH;
-  const size_t bh = (size_t)batch * heads;
-  return bh * nch * (2 * CH * CH * sizeof(bf16) + CH * sizeof(float));
+  (void)d;
+  return layout(batch, seq, heads, false).total;
+}
+
+size_t dr_chunk_backward_workspace_bytes(int batch, int seq, int heads, int d) {
+  (void)d;
+  return layout(batch, seq, heads, true).total;
 }
 
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
                  void* out, void* workspace, int batch, int seq, int heads, int d) {
   (void)d;
-  ChunkArgs a{};
+  CkArgs a = make_args(layout(batch, seq, heads, false), workspace, false, seq, heads);
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha; a.out = (bf16*)out;
-  a.H = heads; a.T = seq; a.nch = (seq + CH - 1) / CH;
-  const size_t bh = (size_t)batch * heads;
-  char* ws = (char*)workspace;
-  a.tbuf = (bf16*)ws;
-  a.pbuf = (bf16*)(ws + bh * a.nch * CH * CH * sizeof(bf16));
-  a.lbuf = (float*)(ws + 2 * bh * a.nch * CH * CH * sizeof(bf16));
+  const unsigned bh = (unsigned)batch * heads;
   hipStream_t s = as_stream(stream);
-  dr_chunk_prep_kernel<<<dim3(a.nch, (unsigned)bh), 256, 0, s>>>(a);
+  dr_ck_prep_kernel<false><<<dim3(a.nch, bh), 256, 0, s>>>(a);
   int rc = check_launch("delta rule chunk prep");
   if (rc) return rc;
-  dr_chunk_state_kernel<<<(unsigned)(bh * (DK / VS)), 256, 0, s>>>(a);
-  return check_launch("delta rule chunk state");
+  dr_ck_scan_kernel<0><<<bh * (DK / VS), 256, 0, s>>>(a);
+  rc = check_launch("delta rule chunk scan");
+  if (rc) return rc;
+  dr_ck_out_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  return check_launch("delta rule chunk output");
+}
+
+int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                          const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
+                          void* dalpha, void* workspace, int batch, int seq, int heads, int d) {
+  (void)d;
+  CkArgs a = make_args(layout(batch, seq, heads, true), workspace, true, seq, heads);
+  a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
+  a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha; a.dout = (const bf16*)grad_out;
+  a.dq = (bf16*)dq; a.dk = (bf16*)dk; a.dv = (bf16*)dv; a.dbeta = (bf16*)dbeta; a.dalpha = (bf16*)dalpha;
+  const unsigned bh = (unsigned)batch * heads;
+  hipStream_t s = as_stream(stream);
+  dr_ck_prep_kernel<true><<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  int rc = check_launch("delta rule chunk prep");
+  if (rc) return rc;
+  dr_ck_scan_kernel<1><<<bh * (DK / VS), 256, 0, s>>>(a);
+  rc = check_launch("delta rule chunk scan");
+  if (rc) return rc;
+  dr_ck_dlocal_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  rc = check_launch("delta rule chunk dlocal");
+  if (rc) return rc;
+  dr_ck_scan_kernel<2><<<bh * (DK / VS), 256, 0, s>>>(a);
+  rc = check_launch("delta rule chunk reverse scan");
+  if (rc) return rc;
+  dr_ck_grad_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  return check_launch("delta rule chunk grad");
 }
 
 }  // namespace edf
+
+extern "C" int edf_debug_acc_kfrag_bf16(void* stream, const float* x, void* out) {
+  using namespace edf;
+  clear_error();
+  EDF_REQUIRE(x != nullptr && out != nullptr, EDF_ERR_INVALID_ARG, "null pointer");
+  dr_ck_debug_kfrag_kernel<<<1, 64, 0, as_stream(stream)>>>(x, (bf16*)out);
+  return check_launch("acc_kfrag probe");
+}

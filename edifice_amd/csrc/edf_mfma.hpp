@@ -34,4 +34,44 @@ EDF_DEVICE f32x16 zero16() {
 // Row (within the 32-row tile) held by register r of a lane in half g.
 EDF_DEVICE constexpr int d_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+
+EDF_DEVICE unsigned pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (bf16)lo;
+  v[1] = (bf16)hi;
+  return __builtin_bit_cast(unsigned, v);
+}
+
+// An accumulator tile X (column = lane % 32) reused as an MFMA operand that contracts
+// over X's rows: the B fragment of X (B[k][j] = X[k][j]) and the A fragment of X^T are
+// the same 8 values, rows 16 m + 8 g .. 16 m + 7 + 8 g of column lane % 32.  Registers
+// 8m..8m+3 of half g hold rows 16m + 4g + 0..3 and registers 8m+4..8m+7 hold rows
+// 16m + 8 + 4g + 0..3, so one v_permlane32_swap per register pair (lanes 32..63 of the
+// first operand trade places with lanes 0..31 of the second) completes the fragment.
+// m is 0 or 1 and must be a compile-time constant after unrolling.
+EDF_DEVICE bf16x8 acc_kfrag(const f32x16& x, int m) {
+  const unsigned a0 = pack_bf16x2(x[8 * m + 0], x[8 * m + 1]);
+  const unsigned a1 = pack_bf16x2(x[8 * m + 2], x[8 * m + 3]);
+  const unsigned b0 = pack_bf16x2(x[8 * m + 4], x[8 * m + 5]);
+  const unsigned b1 = pack_bf16x2(x[8 * m + 6], x[8 * m + 7]);
+  const auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+  const u32x4 r = {s0[0], s1[0], s0[1], s1[1]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// Store an accumulator tile with its rows contiguous: dst[lane%32 * ld + row] (bf16),
+// four consecutive rows per 8-byte store; dst points at (row 0, column 0).
+EDF_DEVICE void store_rows(bf16* dst, long ld, const f32x16& x, int li, int g, float scale = 1.0f) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    bf16x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = (bf16)(x[4 * q + e] * scale);
+    *(bf16x4*)(dst + (long)li * ld + 8 * q + 4 * g) = v;
+  }
+}
+
 }  // namespace edf

@@ -221,6 +221,13 @@ int edf_fused_gated_delta_net_scan_backward(void* stream, const void* q, const v
  * assume.  No reference counterpart; used by the GPU tests to pin that layout. */
 int edf_debug_mfma_32x32x16_bf16(void* stream, const void* A, const void* B, float* C);
 
+/* Diagnostic: reuse of an MFMA accumulator as the next product's operand (one
+ * v_permlane32_swap per register pair).  x is a 64x32 f32 matrix (row-major) held as two
+ * 32x32 accumulator tiles; out[lane][kk][e] (bf16, 64 x 4 x 8) receives the operand
+ * fragment for k-step kk, which must equal x[16 kk + 8 (lane / 32) + e][lane % 32].
+ * No reference counterpart; used by the GPU tests to pin the chunked delta rule's layout. */
+int edf_debug_acc_kfrag_bf16(void* stream, const float* x, void* out);
+
 #ifdef __cplusplus
 }
 #endif

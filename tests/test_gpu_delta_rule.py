@@ -30,10 +30,11 @@ CASES = [
     (1, 37, 1, 128, torch.float32, True, False),
     (1, 48, 2, 128, torch.float32, False, True),
     (2, 20, 2, 32, torch.bfloat16, False, True),
-    # chunked MFMA forward (bf16, per-head beta, d=128, T >= 64)
+    # chunked MFMA forward and backward (bf16, per-head beta, d=128, T >= 64)
     (1, 64, 2, 128, torch.bfloat16, True, True),
-    (1, 200, 2, 128, torch.bfloat16, True, True),
+    (1, 200, 2, 128, torch.bfloat16, True, True),    # partial last chunk
     (2, 130, 1, 128, torch.bfloat16, True, False),
+    (1, 640, 2, 128, torch.bfloat16, True, True),    # ten chunks: state and gradient carried across
 ]
 
 

@@ -21,3 +21,20 @@ def test_mfma_32x32x16_layout(rng):
              ctypes.c_void_p(C.data_ptr()))
     expect = A.float().cpu().numpy() @ B.float().cpu().numpy()
     np.testing.assert_array_equal(C.cpu().numpy(), expect)  # small integers: exact
+
+
+def test_acc_kfrag_layout(rng):
+    """An accumulator tile reused as an operand over its rows (v_permlane32_swap)."""
+    from edifice_amd import _native as nat
+    announce("acc_kfrag_layout")
+    x = rng.integers(-64, 65, size=(64, 32)).astype(np.float32)  # exact in bf16
+    X = torch.from_numpy(x).cuda()
+    out = torch.empty(64, 4, 8, dtype=torch.bfloat16, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.call("edf_debug_acc_kfrag_bf16", stream, ctypes.c_void_p(X.data_ptr()), ctypes.c_void_p(out.data_ptr()))
+    got = out.float().cpu().numpy()
+    lane = np.arange(64)[:, None, None]
+    kk = np.arange(4)[None, :, None]
+    e = np.arange(8)[None, None, :]
+    expect = x[16 * kk + 8 * (lane // 32) + e, lane % 32]
+    np.testing.assert_array_equal(got, expect)
