@@ -77,8 +77,9 @@ EDF_DEVICE bf16x8 ld_row8(const bf16* base, const CkArgs& p, int b, int h, int t
 
 // Transposed staging of a chunk of a [B,T,H,DK] tensor: dst[d * TS + t] = scale_t * src[t][d].
 // Lanes run along t so that the 2-byte LDS writes of a wave fill consecutive words.
+template <int NT>
 EDF_DEVICE void stage_t(bf16* dst, const bf16* src, const CkArgs& p, int b, int h, int t0, const float* scale) {
-  for (int e = threadIdx.x; e < CH * DK / 8; e += 256) {
+  for (int e = threadIdx.x; e < CH * DK / 8; e += NT) {
     const int t = e & (CH - 1), cb = (e >> 6) * 8;
     const bf16x8 x = ld_row8(src, p, b, h, t0 + t, cb);
     const float sc = scale != nullptr ? scale[t] : 1.0f;
@@ -88,20 +89,21 @@ EDF_DEVICE void stage_t(bf16* dst, const bf16* src, const CkArgs& p, int b, int 
 }
 
 // ---------------------------------------------------------------------------
-// prep: decays, T = (I + A)^-1, W (and W^T), U^T, Kd^T (and T^T)
+// prep: decays, T = (I + A)^-1, W (and W^T), U^T, Kd^T (and T^T).
+// LDS is reused across phases (A then K^T, T then V^T) so three workgroups share a CU.
 // ---------------------------------------------------------------------------
 template <bool BWD>
 __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   constexpr int AS = CH + 1;
-  __shared__ __attribute__((aligned(16))) bf16 sK[CH * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sV[CH * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sKb[DK * TS];  // (diag(beta gamma) K)^T
-  __shared__ __attribute__((aligned(16))) bf16 sVb[DK * TS];  // (diag(beta) V)^T
+  __shared__ __attribute__((aligned(16))) char u1[DK * TS * sizeof(bf16)];
+  __shared__ __attribute__((aligned(16))) char u2[DK * TS * sizeof(bf16)];
   __shared__ __attribute__((aligned(16))) bf16 sTb[CH * TS];  // T
-  __shared__ float sA[CH * AS];
-  __shared__ float sT[CH * AS];
-  __shared__ float sX[16 * 17];
-  __shared__ float lg[CH], bt[CH];
+  __shared__ float lg[CH], bt[CH], kbs[CH], kds[CH];
+  float* sA = (float*)u1;      // [CH][AS]   A, during the inversion
+  float* sX = sA + CH * AS;    // [16][17]   substitution scratch
+  bf16* sKb = (bf16*)u1;       // [DK][TS]   (diag(beta gamma) K)^T, afterwards
+  float* sT = (float*)u2;      // [CH][AS]   T in f32, during the inversion
+  bf16* sVb = (bf16*)u2;       // [DK][TS]   (diag(beta) V)^T, afterwards
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -111,11 +113,6 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   const int t0 = c * CH;
   const long ci = bh * p.nch + c;
 
-  for (int e = tid; e < CH * DK / 8; e += 256) {
-    const int row = e >> 4, col = (e & 15) * 8;
-    *(bf16x8*)(sK + row * KS + col) = ld_row8(p.k, p, b, h, t0 + row, col);
-    *(bf16x8*)(sV + row * KS + col) = ld_row8(p.v, p, b, h, t0 + row, col);
-  }
   if (w == 0) {
     const int t = t0 + l;
     const bool ok = t < p.T;
@@ -126,21 +123,23 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
       const float y = __shfl_up(la, off);
       if (l >= off) la += y;
     }
+    const float lC = __shfl(la, 63);
+    const float bv = ok ? to_f32(p.beta[hi]) : 0.0f;
     lg[l] = la;
-    bt[l] = ok ? to_f32(p.beta[hi]) : 0.0f;
+    bt[l] = bv;
+    kbs[l] = bv * __expf(la);
+    kds[l] = __expf(lC - la);
   }
   __syncthreads();
 
-  // A from the K K^T tiles (I, J); the tile above the diagonal is zero
+  // A from the K K^T tiles (I, J), operands straight from global; the tile above the diagonal is zero
   if (w != 1) {
     const int I = w >= 2 ? 1 : 0, J = (w == 3) ? 1 : 0;
     f32x16 G = zero16();
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) {
-      const bf16x8 a = *(const bf16x8*)(sK + (I * 32 + li) * KS + kk * 16 + 8 * g);
-      const bf16x8 bb = *(const bf16x8*)(sK + (J * 32 + li) * KS + kk * 16 + 8 * g);
-      G = mfma32(a, bb, G);
-    }
+    for (int kk = 0; kk < DK / 16; ++kk)
+      G = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
+                 ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), G);
     const int s = J * 32 + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -194,23 +193,7 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
     }
   }
 
-  // bf16 operands: T, (beta gamma K)^T, (beta V)^T; Kd^T and T^T to the workspace
-  const float lgC = lg[CH - 1];
-  for (int e = tid; e < DK * CH / 8; e += 256) {
-    const int d = e >> 3, tb = (e & 7) * 8;
-    bf16x8 kb, vb, kd;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = tb + i;
-      const float kf = (float)sK[t * KS + d];
-      kb[i] = (bf16)(bt[t] * __expf(lg[t]) * kf);
-      vb[i] = (bf16)(bt[t] * (float)sV[t * KS + d]);
-      kd[i] = (bf16)(__expf(lgC - lg[t]) * kf);
-    }
-    *(bf16x8*)(sKb + d * TS + tb) = kb;
-    *(bf16x8*)(sVb + d * TS + tb) = vb;
-    *(bf16x8*)(p.Kdt + ci * DK * CH + d * CH + tb) = kd;
-  }
+  // T -> bf16 (and T^T to the workspace); then sA and sT are free
   for (int e = tid; e < CH * CH / 8; e += 256) {
     const int row = e >> 3, cb = (e & 7) * 8;
     bf16x8 tv;
@@ -225,6 +208,24 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
     }
   }
   if (tid < CH) p.lg[ci * CH + tid] = lg[tid];
+  __syncthreads();
+  stage_t<256>(sKb, p.k, p, b, h, t0, nullptr);
+  stage_t<256>(sVb, p.v, p, b, h, t0, bt);
+  __syncthreads();
+  // K^T -> Kd^T (workspace) and (diag(beta gamma) K)^T (in place)
+  for (int e = tid; e < DK * CH / 8; e += 256) {
+    const int d = e >> 3, tb = (e & 7) * 8;
+    const bf16x8 kv = *(const bf16x8*)(sKb + d * TS + tb);
+    bf16x8 kb, kd;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float kf = (float)kv[i];
+      kb[i] = (bf16)(kbs[tb + i] * kf);
+      kd[i] = (bf16)(kds[tb + i] * kf);
+    }
+    *(bf16x8*)(sKb + d * TS + tb) = kb;
+    *(bf16x8*)(p.Kdt + ci * DK * CH + d * CH + tb) = kd;
+  }
   __syncthreads();
 
   // T is lower triangular, so row tile 0 only reaches s < 32 (k-steps 0, 1)
@@ -286,45 +287,62 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 
   f32x16 S = zero16();  // rows d_k = 32 w + d_row(r, g), column d_v = v0 + li
 
-  // next chunk's operands, loaded one chunk ahead
-  bf16x8 pa1[4];
-  float pl1[4];
-  bf16x8 pa2[4];
-  bf16x4 px0[2][4];
-  bf16x4 py0[4];
-  float plgC = 0.0f;
-  auto fetch = [&](int c) {
+  // operands of the next two chunks, loaded ahead into two register sets (the loop is
+  // unrolled by two so that each set is addressed statically)
+  struct Pre {
+    bf16x8 a1[4];
+    float l1[4];
+    bf16x8 a2[4];
+    bf16x4 x0[2][4];
+    bf16x4 y0[4];
+    float lgC;
+  };
+  Pre pre0, pre1;
+  // A1 rows of chunk c (consumed first, into LDS)
+  auto fetch_a1 = [&](Pre& P, int c) {
     const long ci = bh * p.nch + c;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i;
       const int row = e >> 4, col = (e & 15) * 8;
       if (!REV) {
-        pa1[i] = *(const bf16x8*)(p.W + ci * CH * DK + row * DK + col);
+        P.a1[i] = *(const bf16x8*)(p.W + ci * CH * DK + row * DK + col);
       } else {
-        pa1[i] = ld_row8(p.k, p, b, h, c * CH + row, col);
-        pl1[i] = p.lg[ci * CH + row];
+        P.a1[i] = ld_row8(p.k, p, b, h, c * CH + row, col);
+        P.l1[i] = p.lg[ci * CH + row];
       }
     }
+  };
+  // the rest of chunk c (consumed at the end of its step)
+  auto fetch_rest = [&](Pre& P, int c) {
+    const long ci = bh * p.nch + c;
     const bf16* a2 = (REV ? p.Wt : p.Kdt) + ci * DK * CH + (32 * w + li) * CH + 8 * g;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) pa2[kk] = *(const bf16x8*)(a2 + 16 * kk);
+    for (int kk = 0; kk < 4; ++kk) P.a2[kk] = *(const bf16x8*)(a2 + 16 * kk);
     const bf16* x0 = (REV ? p.dvl : p.Ut) + ci * DK * CH + (v0 + li) * CH + 4 * g;
 #pragma unroll
     for (int T = 0; T < 2; ++T)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) px0[T][q] = *(const bf16x4*)(x0 + 32 * T + 8 * q);
+      for (int q = 0; q < 4; ++q) P.x0[T][q] = *(const bf16x4*)(x0 + 32 * T + 8 * q);
     if (REV) {
       const bf16* y0 = p.dhl + ci * DK * DK + (v0 + li) * DK + 32 * w + 4 * g;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) py0[q] = *(const bf16x4*)(y0 + 8 * q);
+      for (int q = 0; q < 4; ++q) P.y0[q] = *(const bf16x4*)(y0 + 8 * q);
     }
-    plgC = p.lg[ci * CH + CH - 1];
+    P.lgC = p.lg[ci * CH + CH - 1];
   };
-  fetch(REV ? p.nch - 1 : 0);
+  auto chunk_of = [&](int it) { return REV ? p.nch - 1 - it : it; };
+  fetch_a1(pre0, chunk_of(0));
+  fetch_rest(pre0, chunk_of(0));
+  if (p.nch > 1) {
+    fetch_a1(pre1, chunk_of(1));
+    fetch_rest(pre1, chunk_of(1));
+  }
 
-  for (int it = 0; it < p.nch; ++it) {
-    const int c = REV ? p.nch - 1 - it : it;
+  // Each register set is consumed in place and refilled (for the chunk two steps
+  // ahead) right after its last use, so no copy of an in-flight load is needed.
+  auto body = [&](int it, Pre& P) {
+    const int c = chunk_of(it);
     const long ci = bh * p.nch + c;
     bf16* sa = sA1[it & 1];
     bf16* ss = sSt[it & 1];
@@ -346,26 +364,16 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i;
       const int row = e >> 4, col = (e & 15) * 8;
-      bf16x8 a = pa1[i];
+      bf16x8 a = P.a1[i];
       if (REV) {
-        const float sc = __expf(plgC - pl1[i]);
+        const float sc = __expf(P.lgC - P.l1[i]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) a[j] = (bf16)((float)a[j] * sc);
       }
       *(bf16x8*)(sa + row * KS + col) = a;
     }
-    bf16x8 a2[4];
-    bf16x4 x0[2][4], y0[4];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) a2[kk] = pa2[kk];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      x0[0][q] = px0[0][q];
-      x0[1][q] = px0[1][q];
-      y0[q] = py0[q];
-    }
-    const float gC = __expf(plgC);
-    if (it + 1 < p.nch) fetch(REV ? c - 1 : c + 1);
+    const float gC = __expf(P.lgC);
+    if (it + 2 < p.nch) fetch_a1(P, chunk_of(it + 2));
     __syncthreads();
 
     // X = A1 * state: rows t (two tiles), column d_v
@@ -381,7 +389,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float x0v = (float)x0[T][r >> 2][r & 3];
+        const float x0v = (float)P.x0[T][r >> 2][r & 3];
         X[T][r] = REV ? x0v + X[T][r] : x0v - X[T][r];
       }
     }
@@ -399,10 +407,15 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     // state update: Y = A2 * v, contracting over t with v taken straight from registers
     f32x16 Y = zero16();
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) Y = mfma32(a2[kk], acc_kfrag(X[kk >> 1], kk & 1), Y);
+    for (int kk = 0; kk < 4; ++kk) Y = mfma32(P.a2[kk], acc_kfrag(X[kk >> 1], kk & 1), Y);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      S[r] = REV ? fmaf(gC, S[r], (float)y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
+      S[r] = REV ? fmaf(gC, S[r], (float)P.y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
+    if (it + 2 < p.nch) fetch_rest(P, chunk_of(it + 2));
+  };
+  for (int it = 0; it < p.nch; it += 2) {
+    body(it, pre0);
+    if (it + 1 < p.nch) body(it + 1, pre1);
   }
 }
 
@@ -483,8 +496,8 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
     gm[tid] = __expf(lg[tid]);
   }
   __syncthreads();
-  stage_t(sdOt, p.dout, p, b, h, t0, nullptr);
-  stage_t(sQg, p.q, p, b, h, t0, gm);
+  stage_t<256>(sdOt, p.dout, p, b, h, t0, nullptr);
+  stage_t<256>(sQg, p.q, p, b, h, t0, gm);
 
   // S = Q K^T tile (rows t = 32 I, columns s = 32 J) -> P^T [s][t]
   {
@@ -529,9 +542,10 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// grad: dQ, dK, dV, dbeta, dalpha of one chunk
+// grad: dQ, dK, dV, dbeta, dalpha of one chunk.  Eight waves: wave w works on the
+// 32-wide d tile (w & 3) and the 32-step tile (w >> 2) of each product.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
+__global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   constexpr int ZS = CH + 1;
   __shared__ __attribute__((aligned(16))) bf16 sQt[DK * TS];  // Q^T [d_k][t]
   __shared__ __attribute__((aligned(16))) bf16 sKt[DK * TS];  // K^T [d_k][s]
@@ -539,12 +553,14 @@ __global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sdS[CH * TS];  // dS [t][s]
   __shared__ __attribute__((aligned(16))) bf16 sdSt[CH * TS];  // dS^T [s][t]
   __shared__ __attribute__((aligned(16))) bf16 sdF[CH * TS];  // dG + dG^T
-  __shared__ float sZ[CH * ZS];  // dP P + dA A
-  __shared__ float sB[CH * ZS];  // dA Gamma (K K^T), s < t
+  __shared__ float sZp[CH * ZS];  // dP o P
+  __shared__ float sZa[CH * ZS];  // dA o A
+  __shared__ float sB[CH * ZS];   // dA o Gamma o (K K^T), s < t
   __shared__ float lg[CH], bt[CH], dlg[CH], dbt[CH];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int wd = w & 3, wt = w >> 2;
   const int c = blockIdx.x;
   const long bh = blockIdx.y;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -560,25 +576,26 @@ __global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
     dlg[tid] = 0.0f;
     dbt[tid] = 0.0f;
   }
-  stage_t(sQt, p.q, p, b, h, t0, nullptr);
-  stage_t(sKt, p.k, p, b, h, t0, nullptr);
+  stage_t<512>(sQt, p.q, p, b, h, t0, nullptr);
+  stage_t<512>(sKt, p.k, p, b, h, t0, nullptr);
   __syncthreads();
   const float lgC = lg[CH - 1];
 
-  // dR^T = dv_new^T T: rows d_v = 32 w + .., columns s = 32 J + li  (T[t][s] = 0 for t < s)
-#pragma unroll
-  for (int J = 0; J < 2; ++J) {
-    const int s = 32 * J + li;
+  // dR^T = dv_new^T T: rows d_v = 32 wd + .., columns s = 32 wt + li  (T[t][s] = 0 for t < s)
+  {
+    const int J = wt, s = 32 * J + li;
     f32x16 X = zero16();
 #pragma unroll
-    for (int kk = 2 * J; kk < 4; ++kk)
-      X = mfma32(*(const bf16x8*)(p.dvT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g),
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk < 2 * J) continue;
+      X = mfma32(*(const bf16x8*)(p.dvT + ci * DK * CH + (long)(32 * wd + li) * CH + 16 * kk + 8 * g),
                  *(const bf16x8*)(p.Tt + ci * CH * CH + (long)s * CH + 16 * kk + 8 * g), X);
-    store_rows(sdR + (32 * J) * KS + 32 * w, KS, X, li, g);
+    }
+    store_rows(sdR + (32 * J) * KS + 32 * wd, KS, X, li, g);
     // dV = beta dR;  dbeta += <dR_s, V_s>
     const bool ok = t0 + s < p.T;
-    const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1) + 32 * w + 4 * g;
-    if (ok) store_rows(p.dv + row_off(p, b, h, t0 + 32 * J) + 32 * w, (long)p.H * DK, X, li, g, bt[s]);
+    const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1) + 32 * wd + 4 * g;
+    if (ok) store_rows(p.dv + row_off(p, b, h, t0 + 32 * J) + 32 * wd, (long)p.H * DK, X, li, g, bt[s]);
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -590,66 +607,76 @@ __global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
     if (g == 0) atomicAdd(&dbt[s], ok ? acc : 0.0f);
   }
 
-  // S = Q K^T and G = K K^T on tile (I, J) = (w / 2, w % 2); tile (0, 1) is above the diagonal
-  const int I = w >> 1, J = w & 1;
-  f32x16 Sq = zero16(), Gk = zero16();
-  if (w != 1) {
+  // waves 0-3: S = Q K^T, then dP = dO v^T;  waves 4-7: G = K K^T, then dA = -dR v^T;
+  // tile (I, J) = (wd / 2, wd % 2); tile (0, 1) lies above the diagonal
+  const int I = wd >> 1, J = wd & 1;
+  const bool sq = w < 4;
+  const bool live = wd != 1;
+  f32x16 SG = zero16();
+  if (live) {
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) {
-      const bf16x8 bk = ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g);
-      Sq = mfma32(ld_row8(p.q, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g), bk, Sq);
-      Gk = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g), bk, Gk);
-    }
+    for (int kk = 0; kk < DK / 16; ++kk)
+      SG = mfma32(ld_row8(sq ? p.q : p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
+                  ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), SG);
   }
   __syncthreads();  // sdR complete
 
   {
     const int s = 32 * J + li;
     f32x16 dS = zero16();
-    if (w != 1) {
-      f32x16 dA = zero16(), dP = zero16();
+    if (live) {
+      f32x16 D = zero16();
 #pragma unroll
       for (int kk = 0; kk < DK / 16; ++kk) {
         const bf16x8 bv = *(const bf16x8*)(vN + (long)s * DK + 16 * kk + 8 * g);
-        dA = mfma32(*(const bf16x8*)(sdR + (32 * I + li) * KS + 16 * kk + 8 * g), bv, dA);
-        dP = mfma32(ld_row8(p.dout, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g), bv, dP);
+        const bf16x8 a = sq ? ld_row8(p.dout, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g)
+                            : *(const bf16x8*)(sdR + (32 * I + li) * KS + 16 * kk + 8 * g);
+        D = mfma32(a, bv, D);
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = 32 * I + d_row(r, g);
         const float gam = __expf(lg[t] - lg[s]);
-        const bool mP = s <= t, mA = s < t;
-        const float Pv = mP ? Sq[r] * gam : 0.0f;
-        const float GG = mA ? gam * Gk[r] : 0.0f;
-        const float dAv = -dA[r];
-        dS[r] = mP ? dP[r] * gam : 0.0f;
-        const float dG = mA ? bt[t] * dAv * gam : 0.0f;
-        sZ[t * ZS + s] = dP[r] * Pv + dAv * bt[t] * GG;
-        sB[t * ZS + s] = dAv * GG;
-        sdS[t * TS + s] = (bf16)dS[r];
-        if (mA) {
-          sdF[t * TS + s] = (bf16)dG;
-          sdF[s * TS + t] = (bf16)dG;
-        } else if (s == t) {
-          sdF[t * TS + t] = (bf16)0.0f;
+        if (sq) {
+          const bool mP = s <= t;
+          dS[r] = mP ? D[r] * gam : 0.0f;
+          sZp[t * ZS + s] = mP ? D[r] * SG[r] * gam : 0.0f;
+          sdS[t * TS + s] = (bf16)dS[r];
+        } else {
+          const bool mA = s < t;
+          const float GG = mA ? gam * SG[r] : 0.0f;
+          const float dAv = -D[r];
+          sZa[t * ZS + s] = dAv * bt[t] * GG;
+          sB[t * ZS + s] = dAv * GG;
+          const float dG = mA ? bt[t] * dAv * gam : 0.0f;
+          if (mA) {
+            sdF[t * TS + s] = (bf16)dG;
+            sdF[s * TS + t] = (bf16)dG;
+          } else if (s == t) {
+            sdF[t * TS + t] = (bf16)0.0f;
+          }
         }
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = d_row(r, g);
-        sZ[t * ZS + s] = 0.0f;
-        sB[t * ZS + s] = 0.0f;
-        sdS[t * TS + s] = (bf16)0.0f;
+        if (sq) {
+          sZp[t * ZS + s] = 0.0f;
+          sdS[t * TS + s] = (bf16)0.0f;
+        } else {
+          sZa[t * ZS + s] = 0.0f;
+          sB[t * ZS + s] = 0.0f;
+        }
       }
     }
-    store_rows(sdSt + (32 * J) * TS + 32 * I, TS, dS, li, g);
+    if (sq) store_rows(sdSt + (32 * J) * TS + 32 * I, TS, dS, li, g);
   }
   __syncthreads();
 
   if (tid < CH) {
     float acc = 0.0f;
-    for (int s = 0; s < CH; ++s) acc += sZ[tid * ZS + s] - sZ[s * ZS + tid];
+    for (int s = 0; s < CH; ++s) acc += sZp[tid * ZS + s] + sZa[tid * ZS + s] - sZp[s * ZS + tid] - sZa[s * ZS + tid];
     atomicAdd(&dlg[tid], acc);
   } else if (tid < 2 * CH) {
     const int t = tid - CH;
@@ -658,56 +685,59 @@ __global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
     atomicAdd(&dbt[t], acc);
   }
 
-  // dQ^T and dK^T: rows d_k = 32 w + .., columns t (or s) = 32 J + li
+  // dQ^T and dK^T: rows d_k = 32 wd + .., columns t (or s) = 32 wt + li
   float dlgC = 0.0f;
-#pragma unroll
-  for (int J2 = 0; J2 < 2; ++J2) {
-    const int t = 32 * J2 + li;
+  {
+    const int J2 = wt, t = 32 * J2 + li;
     const bool ok = t0 + t < p.T;
     // dQ^T = gamma (h dO^T) + K^T dS^T
     f32x16 X = zero16();
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk)
-      X = mfma32(*(const bf16x8*)(hN + (long)(32 * w + li) * DK + 16 * kk + 8 * g),
+      X = mfma32(*(const bf16x8*)(hN + (long)(32 * wd + li) * DK + 16 * kk + 8 * g),
                  ld_row8(p.dout, p, b, h, t0 + t, 16 * kk + 8 * g), X);
     const float gmt = __expf(lg[t]);
     float qx = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      qx = fmaf((float)sQt[(32 * w + d_row(r, g)) * TS + t], X[r], qx);
+      qx = fmaf((float)sQt[(32 * wd + d_row(r, g)) * TS + t], X[r], qx);
       X[r] *= gmt;
     }
     qx += __shfl_xor(qx, 32);
     if (g == 0) atomicAdd(&dlg[t], gmt * qx);
 #pragma unroll
-    for (int kk = 0; kk < 2 * (J2 + 1); ++kk)
-      X = mfma32(*(const bf16x8*)(sKt + (32 * w + li) * TS + 16 * kk + 8 * g),
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk >= 2 * (J2 + 1)) continue;
+      X = mfma32(*(const bf16x8*)(sKt + (32 * wd + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdS + t * TS + 16 * kk + 8 * g), X);
-    if (ok) store_rows(p.dq + row_off(p, b, h, t0 + 32 * J2) + 32 * w, (long)p.H * DK, X, li, g);
+    }
+    if (ok) store_rows(p.dq + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X, li, g);
 
     // dK^T = (gamma_C / gamma) dh v^T - (beta gamma) h dR^T + Q^T dS + K^T dF
     f32x16 X1 = zero16(), X2 = zero16(), X3 = zero16();
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk) {
-      const bf16x8 ah = *(const bf16x8*)(hN + (long)(32 * w + li) * DK + 16 * kk + 8 * g);
-      X1 = mfma32(*(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * w + li) * DK + 16 * kk + 8 * g),
+      X1 = mfma32(*(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * wd + li) * DK + 16 * kk + 8 * g),
                   *(const bf16x8*)(vN + (long)t * DK + 16 * kk + 8 * g), X1);
-      X2 = mfma32(ah, *(const bf16x8*)(sdR + t * KS + 16 * kk + 8 * g), X2);
+      X2 = mfma32(*(const bf16x8*)(hN + (long)(32 * wd + li) * DK + 16 * kk + 8 * g),
+                  *(const bf16x8*)(sdR + t * KS + 16 * kk + 8 * g), X2);
     }
 #pragma unroll
-    for (int kk = 2 * J2; kk < 4; ++kk)
-      X3 = mfma32(*(const bf16x8*)(sQt + (32 * w + li) * TS + 16 * kk + 8 * g),
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk < 2 * J2) continue;
+      X3 = mfma32(*(const bf16x8*)(sQt + (32 * wd + li) * TS + 16 * kk + 8 * g),
                   *(const bf16x8*)(sdSt + t * TS + 16 * kk + 8 * g), X3);
+    }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      X3 = mfma32(*(const bf16x8*)(sKt + (32 * w + li) * TS + 16 * kk + 8 * g),
+      X3 = mfma32(*(const bf16x8*)(sKt + (32 * wd + li) * TS + 16 * kk + 8 * g),
                   *(const bf16x8*)(sdF + t * TS + 16 * kk + 8 * g), X3);
     const float sc1 = __expf(lgC - lg[t]);
     const float sc2 = bt[t] * gmt;
     float k1 = 0.0f, k2 = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float kv = (float)sKt[(32 * w + d_row(r, g)) * TS + t];
+      const float kv = (float)sKt[(32 * wd + d_row(r, g)) * TS + t];
       k1 = fmaf(kv, X1[r], k1);
       k2 = fmaf(kv, X2[r], k2);
       X3[r] += sc1 * X1[r] - sc2 * X2[r];
@@ -717,15 +747,15 @@ __global__ __launch_bounds__(256) void dr_ck_grad_kernel(const CkArgs p) {
     if (g == 0) {
       atomicAdd(&dlg[t], -sc1 * k1 - sc2 * k2);
       atomicAdd(&dbt[t], -gmt * k2);
-      dlgC += sc1 * k1;
+      dlgC = sc1 * k1;
     }
-    if (ok) store_rows(p.dk + row_off(p, b, h, t0 + 32 * J2) + 32 * w, (long)p.H * DK, X3, li, g);
+    if (ok) store_rows(p.dk + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X3, li, g);
   }
   // gamma_C <dh, h> and the Kd terms enter the decay of the last step
   {
     const bf16* dm = p.dmN + ci * DK * DK;
     float acc = 0.0f;
-    for (int e = tid; e < DK * DK / 8; e += 256) {
+    for (int e = tid; e < DK * DK / 8; e += 512) {
       const bf16x8 x = *(const bf16x8*)(dm + 8 * e);
       const bf16x8 y = *(const bf16x8*)(hN + 8 * e);
 #pragma unroll
@@ -884,7 +914,7 @@ int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void
   dr_ck_scan_kernel<2><<<bh * (DK / VS), 256, 0, s>>>(a);
   rc = check_launch("delta rule chunk reverse scan");
   if (rc) return rc;
-  dr_ck_grad_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  dr_ck_grad_kernel<<<dim3(a.nch, bh), 512, 0, s>>>(a);
   return check_launch("delta rule chunk grad");
 }
 
