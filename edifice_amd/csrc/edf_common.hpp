@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #define EDF_DEVICE __device__ __forceinline__
 
 namespace edf {
@@ -43,6 +45,27 @@ EDF_DEVICE float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 EDF_DEVICE float sigmoidf(float x) { return 1.0f / (1.0f + fast_exp2(-x * LOG2E)); }
 
 EDF_DEVICE float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
+
+// ---- compile-time loops ------------------------------------------------------
+// static_for<N>(f) calls f(IC<0>{}), ..., f(IC<N-1>{}); inside f, decltype(i)::value is
+// a constant expression (needed for instruction immediates such as DPP controls).
+template <int J> struct IC { static constexpr int value = J; };
+template <typename F, int... Is>
+EDF_DEVICE void static_for_impl(std::integer_sequence<int, Is...>, F&& f) { (f(IC<Is>{}), ...); }
+template <int N, typename F>
+EDF_DEVICE void static_for(F&& f) { static_for_impl(std::make_integer_sequence<int, N>{}, f); }
+
+// ---- cross-lane ----------------------------------------------------------------
+// DPP row_newbcast:J (gfx90a and later): every lane receives lane J of its own 16-lane
+// row.  With the same 16 values replicated in the four rows of a wave this is a
+// wave-wide broadcast of value J, and the compiler folds it into the consuming VOP2
+// instruction (v_mul_f32_dpp) when old = 0 and bound_ctrl is set.
+template <int J>
+EDF_DEVICE float row_bcast(float v) {
+  static_assert(J >= 0 && J < 16, "lane within a row");
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + J, 0xF, 0xF,
+                                                               true));
+}
 
 // ---- launch-shape helpers -----------------------------------------------------
 // MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs, each

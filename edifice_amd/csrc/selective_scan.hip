@@ -11,22 +11,34 @@
 //   common.ex:270-278).
 //   Optional extensions: y += D[d] x, then y *= silu(z).
 //
-// Design (see the repository design notes for the roofline discussion):
-//   * lane = (channel d, state n); LPC = min(N,16) lanes per channel, SPL = N/LPC
-//     states per lane, so a channel's states live in one 16-lane DPP row and the
-//     grid has B*D*N/SPL lanes (3072 waves at B=8, D=1536, N=16) without splitting T;
-//   * inputs are staged per block of timesteps through LDS with coalesced row loads
-//     (x, dt, z: [t][channel] rows; B, C: [t][n] rows shared by the whole workgroup);
-//     clip(dt) and dt*x are computed once per (t, d) at staging time;
-//   * per (t, n) the lane does one v_exp_f32 and four VALU ops;
-//   * y = sum_n C h is a transpose-reduce through LDS (one add per (t, n));
-//   * workgroup ids are remapped so that tiles sharing 128 B lines share an XCD;
-//   * backward: the forward writes the state every CK timesteps ("checkpoints");
-//     backward walks chunks in reverse, recomputes the chunk's states and decays
-//     into registers, then runs the reverse recurrence.  Sums over channels
-//     (dB, dC) are reduced in LDS per workgroup and then across workgroups by a
-//     small deterministic reduction kernel; sums over states (dx, ddt) use the
-//     LDS transpose-reduce.
+// Design.  The op is VALU-bound: per (b, t, d, n) element the forward needs one
+// v_exp_f32 (about 10 cycles per wave on MI355X, measured) and four VALU ops, several
+// times the HBM time at config-2 size.  The layout minimises everything else:
+//   * lane = channel d (64 channels per wave) holding K = 2 states in registers;
+//     NW = N / K waves per workgroup cover one 64-channel tile's N states (8 waves at
+//     N = 16, 2 waves per SIMD: enough to hide LDS and transcendental latency, which
+//     four states per lane at 1 wave per SIMD did not);
+//   * the B[b, t, :] and C[b, t, :] values a wave needs are the same for all its lanes.
+//     Forward: a block's values are loaded into a few VGPRs (16 values per register,
+//     replicated over the four 16-lane rows) and broadcast with DPP row_newbcast, folded
+//     into v_mul_f32_dpp: no LDS traffic.  Backward: staged through LDS once per chunk
+//     and read as broadcasts.  (Scalar loads into SGPR operands were tried and are
+//     slower: every timestep waits on the scalar cache.)
+//   * x, dt (and z) are staged per block of timesteps through LDS from coalesced rows,
+//     clip(dt) and dt_b * x computed once per (t, d); the recurrence reads them as
+//     16-byte vectors;
+//   * y = sum_n C h: each lane sums its K states, the NW wave partials are added
+//     through LDS by the thread that staged that (t, d), which still holds x and z in
+//     registers for the D skip and the gate; double-buffered tiles need one barrier
+//     per block, and the raw inputs are prefetched four blocks ahead;
+//   * the forward writes the state every CK = 16 timesteps ("checkpoints", layout
+//     [b][chunk][n][d], coalesced over d);
+//   * backward: chunks are walked in reverse; each chunk's states and decays are
+//     recomputed from its checkpoint into registers, then the reverse recurrence runs
+//     with the same lane layout.  Sums over states (dx, ddt) are in-lane plus an LDS
+//     add over the NW waves; sums over channels (dB, dC) go through an LDS tile per
+//     block of 8 timesteps (conflict-free strides) into per-tile partials, summed over
+//     the tiles by a small deterministic kernel (no atomics).
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
@@ -35,6 +47,7 @@ namespace {
 
 constexpr float DT_MIN = 1.0e-3f;
 constexpr float DT_MAX = 0.1f;
+constexpr int SS_CK = 16;  // checkpoint interval (timesteps) = backward recompute chunk
 
 struct SSArgs {
   const void* x;
@@ -46,25 +59,30 @@ struct SSArgs {
   const void* z;
   const float* dtmean;  // [batch, seq] or null (per-channel dt_b)
   void* out;
-  float* ckpt;  // [batch, dim, nck, N] state after each chunk of ck timesteps
+  float* ckpt;  // [batch, nck, N, dim] state after each chunk of SS_CK timesteps
   // backward only
   const void* dout;
   void* dx;
   void* ddt;
   void* dz;
-  float* part_bc;  // [ntile, batch, seq, 2, N]
+  float* part_bc;  // [ntile, batch, seq, 2, N]  (qty 0 = dC, 1 = dB)
   float* part_a;   // [batch, dim, N]
   float* part_d;   // [batch, dim]
   float* part_m;   // [ntile, batch, seq] (mean mode)
-  int batch, seq, dim, ck, nck, ntile;
+  int batch, seq, dim, nck, ntile;
 };
 
-template <int N, int NT>
-struct Geo {
-  static constexpr int LPC = N < 16 ? N : 16;
-  static constexpr int SPL = N / LPC;
-  static constexpr int CPW = NT / LPC;  // channels per workgroup
+// lane = channel; K = min(N, KMAX) states per lane (at least N / 16, so a workgroup
+// has at most 16 waves); NW waves per workgroup cover the N states.
+template <int N, int KMAX = 4>
+struct SSGeo {
+  static constexpr int KLO = KMAX > N / 16 ? KMAX : N / 16;
+  static constexpr int K = N < KLO ? N : KLO;
+  static constexpr int NW = N / K;
+  static constexpr int NT = 64 * NW;
 };
+
+EDF_DEVICE int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // ---------------------------------------------------------------------------
 // dt mean over channels (block semantics), one wave per (b, t)
@@ -86,142 +104,155 @@ __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ d
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename TI, typename TP, int N, int NT, bool MEAN, bool HAS_Z>
-__global__ __launch_bounds__(NT) void ss_fwd_kernel(const SSArgs p) {
-  using G = Geo<N, NT>;
-  constexpr int LPC = G::LPC, SPL = G::SPL, CPW = G::CPW;
-  constexpr int TS = 16;
-  constexpr int PT = TS + 1;  // odd row stride: row writes and column reads hit distinct banks
-  constexpr int EPT = CPW * TS / NT;              // staged (t, channel) elements per thread
-  constexpr int BPT = (N * TS + NT - 1) / NT;     // staged (t, n) elements per thread
-  __shared__ float s_x[CPW][PT], s_dtc[CPW][PT], s_dtx[CPW][PT], s_z[CPW][PT];
-  __shared__ float s_B[N][TS + 1], s_C[N][TS + 1];
-  __shared__ float s_p[NT][PT];
-  __shared__ float s_y[TS][CPW + 1];
+template <typename TI, typename TP, int N, int KMAX, bool MEAN, bool HAS_Z, bool WRITE_Y>
+__global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSArgs p, const TP* __restrict__ Bm,
+                                                                    const TP* __restrict__ Cm) {
+  using G = SSGeo<N, KMAX>;
+  constexpr int K = G::K, NW = G::NW, NT = G::NT;
+  constexpr int TS = SS_CK;          // timesteps per staged block (one checkpoint per block)
+  constexpr int PS = TS + 4;         // [channel][t] row stride: 16-byte reads are conflict-free
+  constexpr int EPT = TS * 64 / NT;  // staged (t, channel) elements per thread
+  constexpr int R = TS * 2 * K / 16;  // VGPRs holding a block's B/C values (16 per row)
+  constexpr int PD = 4;                // prefetch distance (blocks)
+  static_assert(TS % 4 == 0 && EPT * NW == TS && PD % 2 == 0 && (TS * K) % 16 == 0, "staging layout");
+  __shared__ __align__(16) float s_dtc[2][64][PS];
+  __shared__ __align__(16) float s_dtx[2][64][PS];
+  __shared__ float s_yp[2][NW][TS][64];
 
-  const TI* x = (const TI*)p.x;
-  const TI* dt = (const TI*)p.dt;
-  const TI* z = (const TI*)p.z;
-  const TP* Am = (const TP*)p.A;
-  const TP* Bm = (const TP*)p.B;
-  const TP* Cm = (const TP*)p.C;
-  const TP* Dv = (const TP*)p.D;
-  TI* out = (TI*)p.out;
+  const TI* __restrict__ x = (const TI*)p.x;
+  const TI* __restrict__ dt = (const TI*)p.dt;
+  const TI* __restrict__ z = (const TI*)p.z;
+  const TP* __restrict__ Am = (const TP*)p.A;
+  const TP* __restrict__ Dv = (const TP*)p.D;
+  TI* __restrict__ out = (TI*)p.out;
   const int seq = p.seq, dim = p.dim;
 
-  const int tid = threadIdx.x;
-  const int n = tid % LPC, cl = tid / LPC;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);  // this wave's state group
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int b = logical / p.ntile, tile = logical % p.ntile;
-  const int c0 = tile * CPW, c = c0 + cl;
+  const int c = tile * 64 + lane;
   const bool cvalid = c < dim;
+  const int cc = min(c, dim - 1);
 
-  float A2[SPL], h[SPL];
+  float A2[K], h[K];
 #pragma unroll
-  for (int s = 0; s < SPL; ++s) {
-    A2[s] = cvalid ? ld(Am, (long)c * N + n * SPL + s) * LOG2E : 0.0f;
+  for (int s = 0; s < K; ++s) {
+    A2[s] = cvalid ? ld(Am, (long)c * N + w * K + s) * LOG2E : 0.0f;
     h[s] = 0.0f;
   }
   const float Dc = (Dv != nullptr && cvalid) ? ld(Dv, c) : 0.0f;
   const long rowbase = (long)b * seq * dim;
 
-  // Raw values of the next block, loaded one block ahead from clamped (in-bounds)
-  // indices so no load sits behind a divergent branch.
-  // Kept in the storage type: converting at load time would force a wait on the load.
-  TI px[EPT], pdt[EPT], pz[EPT];
-  TP pb[BPT], pc[BPT];
-  float pm[EPT];
-  auto fetch = [&](int t0) {
+  // Raw values of the blocks ahead, loaded PD blocks early from clamped (in-bounds)
+  // indices so no load sits behind a divergent branch and the HBM latency is covered by
+  // PD blocks of compute; kept in the storage type until staged.
+  // B/C: the wave needs B[t, wK..wK+K) and C[t, wK..wK+K) for the TS steps of a block,
+  // the same for every lane.  Value v = t K + s of B sits in lane v % 16 of every
+  // 16-lane row of register v / 16 (C likewise in registers R/2..R-1) and reaches all
+  // lanes through a DPP row broadcast (folded into v_mul_f32_dpp for B): no LDS traffic.
+  // Scalar loads into SGPR operands were tried and are slower: the scalar-cache latency
+  // and the 64-bit scalar address arithmetic are not hidden.
+  TI rx[PD][EPT], rdt[PD][EPT], rz[PD][EPT];
+  float rbc[PD][R];
+  float rm[PD][EPT];
+  float cx[EPT], cz[EPT], nx[EPT], nz[EPT];
+  auto fetch = [&](int slot, int t0) {
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      const int e = tid + k * NT;
-      const int t = min(t0 + e / CPW, seq - 1), cc = min(c0 + e % CPW, dim - 1);
-      const long idx = rowbase + (long)t * dim + cc;
-      px[k] = x[idx];
-      pdt[k] = dt[idx];
-      if (HAS_Z) pz[k] = z[idx];
-      pm[k] = MEAN ? p.dtmean[(long)b * seq + t] : 0.0f;
+    for (int i = 0; i < EPT; ++i) {
+      // uniform row pointer + 32-bit lane offset: SGPR-base addressing, no 64-bit VALU math
+      const long row = rowbase + (long)min(t0 + w + i * NW, seq - 1) * dim;
+      rx[slot][i] = (x + row)[cc];
+      rdt[slot][i] = (dt + row)[cc];
+      if (HAS_Z) rz[slot][i] = (z + row)[cc];
+      rm[slot][i] = MEAN ? p.dtmean[(long)b * seq + min(t0 + w + i * NW, seq - 1)] : 0.0f;
     }
+    const long bc0 = ((long)b * seq + t0) * N + w * K;
+    const int tmax = seq - 1 - t0;
 #pragma unroll
-    for (int k = 0; k < BPT; ++k) {
-      const int e = min(tid + k * NT, N * TS - 1);
-      const long idx = ((long)b * seq + min(t0 + e / N, seq - 1)) * N + e % N;
-      pb[k] = Bm[idx];
-      pc[k] = Cm[idx];
+    for (int r = 0; r < R; ++r) {
+      const int v = (16 * r + (lane & 15)) % (TS * K);
+      const int off = min(v / K, tmax) * N + v % K;
+      rbc[slot][r] = to_f32((r < R / 2 ? Bm : Cm)[bc0 + off]);
     }
   };
-  fetch(0);
+  auto stage = [&](int slot, int t0, int buf, float* xs, float* zs) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int tt = w + i * NW;
+      const bool ok = (t0 + tt < seq) && cvalid;
+      const float xv = to_f32(rx[slot][i]);
+      const float dtc = ok ? clampf(to_f32(rdt[slot][i]), DT_MIN, DT_MAX) : 0.0f;
+      s_dtc[buf][lane][tt] = dtc;
+      s_dtx[buf][lane][tt] = ok ? (MEAN ? rm[slot][i] : dtc) * xv : 0.0f;
+      xs[i] = xv;
+      zs[i] = HAS_Z ? to_f32(rz[slot][i]) : 0.0f;
+    }
+  };
 
+  // Pipeline: raw slot j holds block j mod PD.  Block blk is computed from LDS buffer
+  // blk & 1 and from its B/C values in slot blk % PD; then block blk + 1 is staged into
+  // the other LDS buffer and block blk + PD is fetched into slot blk % PD, which block
+  // blk no longer needs.
   const int nblk = (seq + TS - 1) / TS;
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int t0 = blk * TS;
 #pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-      const int e = tid + k * NT;
-      const int tt = e / CPW, ch = e % CPW;
-      const bool ok = (t0 + tt < seq) && (c0 + ch < dim);
-      const float xv = to_f32(px[k]);
-      const float dtc = ok ? clampf(to_f32(pdt[k]), DT_MIN, DT_MAX) : 0.0f;
-      s_x[ch][tt] = ok ? xv : 0.0f;
-      s_dtc[ch][tt] = dtc;
-      s_dtx[ch][tt] = ok ? (MEAN ? pm[k] : dtc) * xv : 0.0f;
-      s_z[ch][tt] = (ok && HAS_Z) ? to_f32(pz[k]) : 0.0f;
-    }
-#pragma unroll
-    for (int k = 0; k < BPT; ++k) {
-      const int e = tid + k * NT;
-      if (e < N * TS) {
-        const int tt = e / N, nn = e % N;
-        const bool ok = t0 + tt < seq;
-        s_B[nn][tt] = ok ? to_f32(pb[k]) : 0.0f;
-        s_C[nn][tt] = ok ? to_f32(pc[k]) : 0.0f;
-      }
-    }
-    if (t0 + TS < seq) fetch(t0 + TS);
-    __syncthreads();
+  for (int j = 0; j < PD; ++j)
+    if (j < nblk) fetch(j, j * TS);
+  stage(0, 0, 0, cx, cz);
+  __syncthreads();
 
-    float pr[TS];
+  for (int blk0 = 0; blk0 < nblk; blk0 += PD) {
 #pragma unroll
-    for (int tt = 0; tt < TS; ++tt) {
-      const float dtc = s_dtc[cl][tt];
-      const float dtx = s_dtx[cl][tt];
-      float acc = 0.0f;
+    for (int u = 0; u < PD; ++u) {
+      const int blk = blk0 + u;
+      if (blk >= nblk) break;
+      const int t0 = blk * TS, buf = u & 1;  // PD is even, so u & 1 == blk & 1
+      // ---- recurrence over the block ----
+      const float* bcr = rbc[u];  // this block's B/C values (slot blk % PD == u)
+      static_for<TS / 4>([&](auto qi) {
+        constexpr int q = decltype(qi)::value;
+        const float4 dc4 = *reinterpret_cast<const float4*>(&s_dtc[buf][lane][4 * q]);
+        const float4 dx4 = *reinterpret_cast<const float4*>(&s_dtx[buf][lane][4 * q]);
+        const float dcv[4] = {dc4.x, dc4.y, dc4.z, dc4.w};
+        const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+        static_for<4>([&](auto vi) {
+          constexpr int v = decltype(vi)::value, tt = 4 * q + v;
+          float acc = 0.0f;
+          static_for<K>([&](auto si) {
+            constexpr int s = decltype(si)::value;
+            constexpr int vb = tt * K + s, vc = vb + TS * K;  // B and C value indices
+            const float a = fast_exp2(dcv[v] * A2[s]);
+            h[s] = fmaf(a, h[s], row_bcast<vb % 16>(bcr[vb / 16]) * dxv[v]);
+            if (WRITE_Y) acc += row_bcast<vc % 16>(bcr[vc / 16]) * h[s];
+          });
+          if (WRITE_Y) s_yp[buf][w][tt][lane] = acc;
+        });
+      });
+      if (p.ckpt != nullptr && cvalid) {
+        float* ck = p.ckpt + (((long)b * p.nck + blk) * N + w * K) * dim + c;
 #pragma unroll
-      for (int s = 0; s < SPL; ++s) {
-        const int nn = n * SPL + s;
-        const float a = fast_exp2(dtc * A2[s]);
-        h[s] = fmaf(a, h[s], dtx * s_B[nn][tt]);
-        acc = fmaf(s_C[nn][tt], h[s], acc);
+        for (int s = 0; s < K; ++s) ck[(long)s * dim] = h[s];
       }
-      pr[tt] = acc;
-    }
-    if (p.ckpt != nullptr && cvalid && (((t0 + TS) % p.ck) == 0 || t0 + TS >= seq)) {
-      const int k = (min(t0 + TS, seq) - 1) / p.ck;
+      if (blk + 1 < nblk) stage((u + 1) % PD, t0 + TS, buf ^ 1, nx, nz);
+      if (blk + PD < nblk) fetch(u, t0 + PD * TS);
+      __syncthreads();
+      // ---- y for the (t, d) this thread staged: sum the wave partials, D skip, gate ----
+      if (WRITE_Y) {
 #pragma unroll
-      for (int s = 0; s < SPL; ++s) p.ckpt[(((long)b * dim + c) * p.nck + k) * N + n * SPL + s] = h[s];
-    }
+        for (int i = 0; i < EPT; ++i) {
+          const int tt = w + i * NW;
+          float y = 0.0f;
 #pragma unroll
-    for (int tt = 0; tt < TS; ++tt) s_p[tid][tt] = pr[tt];
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < TS / LPC; ++q) {
-      const int tt = n + q * LPC;
-      float y = 0.0f;
-#pragma unroll
-      for (int m = 0; m < LPC; ++m) y += s_p[cl * LPC + m][tt];
-      y = fmaf(Dc, s_x[cl][tt], y);
-      if (HAS_Z) {
-        const float zv = s_z[cl][tt];
-        y *= zv * sigmoidf(zv);
+          for (int v = 0; v < NW; ++v) y += s_yp[buf][v][tt][lane];
+          y = fmaf(Dc, cx[i], y);
+          if (HAS_Z) y *= cz[i] * sigmoidf(cz[i]);
+          if (t0 + tt < seq && cvalid) st(out, rowbase + (long)(t0 + tt) * dim + c, y);
+        }
       }
-      s_y[tt][cl] = y;
-    }
-    __syncthreads();
-    if (out != nullptr) {
-      for (int e = tid; e < CPW * TS; e += NT) {
-        const int tt = e / CPW, ch = e % CPW;
-        const int t = t0 + tt, cc = c0 + ch;
-        if (t < seq && cc < dim) st(out, rowbase + (long)t * dim + cc, s_y[tt][ch]);
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) {
+        cx[i] = nx[i];
+        cz[i] = nz[i];
       }
     }
   }
@@ -230,42 +261,51 @@ __global__ __launch_bounds__(NT) void ss_fwd_kernel(const SSArgs p) {
 // ---------------------------------------------------------------------------
 // backward
 // ---------------------------------------------------------------------------
-template <typename TI, typename TP, int N, int NT, int CK>
-__global__ __launch_bounds__(NT) void ss_bwd_kernel(const SSArgs p) {
-  using G = Geo<N, NT>;
-  constexpr int LPC = G::LPC, SPL = G::SPL, CPW = G::CPW;
-  static_assert(SPL == 1, "backward keeps one state per lane");
-  constexpr int TS = 8;  // reduction block (timesteps)
-  constexpr int PC = CK + 1;  // odd row stride: conflict-free staging writes
-  // chunk tiles [channel][t]
-  __shared__ float s_x[CPW][PC], s_dtc[CPW][PC], s_dtb[CPW][PC], s_rng[CPW][PC], s_dy[CPW][PC];
-  __shared__ float s_B[N][CK + 1], s_C[N][CK + 1];
-  // reduction scratch: [qty][lane][t]
-  __shared__ float s_r[4][NT][TS + 1];
-  __shared__ float s_o[2][CK][CPW + 1];  // staged dx / ddt (and dz) rows
+template <typename TI, typename TP, int N, int KMAX, bool MEAN, bool HAS_Z>
+__global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSArgs p, const TP* __restrict__ Bm,
+                                                                      const TP* __restrict__ Cm) {
+  using G = SSGeo<N, KMAX>;
+  constexpr int K = G::K, NW = G::NW, NT = G::NT;
+  static_assert(K == 2 || K == 4, "backward keeps two or four states per lane");
+  constexpr int CK = SS_CK;          // recompute chunk (= checkpoint interval)
+  constexpr int TS = 8;              // reduction block (timesteps)
+  constexpr int PS = CK + 4;         // [channel][t] row stride (16-byte reads conflict-free)
+  constexpr int EPT = CK * 64 / NT;  // staged (t, channel) elements per thread
+  constexpr int GS = 2 * K * TS + 4;  // per-lane stride of the dC/dB tile: b128 writes conflict-free
+  constexpr int GW = 64 * GS + 8;     // per-wave stride: the reduction's reads are conflict-free
+  constexpr int THR = NT / (TS * 2 * N);  // threads per dB/dC output (adjacent lanes)
+  static_assert(EPT * NW == CK && TS % NW == 0 && CK % TS == 0, "staging layout");
+  static_assert((THR == 1 || THR == 2) && THR * TS * 2 * N == NT, "dB/dC outputs per thread");
+  constexpr int BCT = CK * 2 * N / NT;  // staged B/C values per thread
+  __shared__ __align__(16) float s_bc[CK][2 * N];  // per t: B[0..N), C[0..N)
+  __shared__ __align__(16) float s_dtc[64][PS];
+  __shared__ __align__(16) float s_dtx[64][PS];
+  __shared__ __align__(16) float s_dy[64][PS];
+  __shared__ __align__(16) float s_g[NW * GW];
+  __shared__ float s_pp[2][NW][TS][64];
+  __shared__ float s_yp[HAS_Z ? NW : 1][CK][64];
+  __shared__ float s_m[MEAN ? TS : 1][64];
 
-  const TI* x = (const TI*)p.x;
-  const TI* dt = (const TI*)p.dt;
-  const TI* z = (const TI*)p.z;
-  const TI* dout = (const TI*)p.dout;
-  const TP* Am = (const TP*)p.A;
-  const TP* Bm = (const TP*)p.B;
-  const TP* Cm = (const TP*)p.C;
-  const TP* Dv = (const TP*)p.D;
+  const TI* __restrict__ x = (const TI*)p.x;
+  const TI* __restrict__ dt = (const TI*)p.dt;
+  const TI* __restrict__ z = (const TI*)p.z;
+  const TI* __restrict__ dout = (const TI*)p.dout;
+  const TP* __restrict__ Am = (const TP*)p.A;
+  const TP* __restrict__ Dv = (const TP*)p.D;
   const int seq = p.seq, dim = p.dim;
-  const bool mean_mode = p.dtmean != nullptr;
 
-  const int tid = threadIdx.x;
-  const int n = tid % LPC, cl = tid / LPC;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = uniform(tid >> 6);
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int b = logical / p.ntile, tile = logical % p.ntile;
-  const int c0 = tile * CPW, c = c0 + cl;
+  const int c = tile * 64 + lane;
   const bool cvalid = c < dim;
+  const int cc = min(c, dim - 1);
 
-  float A1[SPL], A2[SPL], dh[SPL], dA[SPL];
+  float A1[K], A2[K], dh[K], dA[K];
 #pragma unroll
-  for (int s = 0; s < SPL; ++s) {
-    A1[s] = cvalid ? ld(Am, (long)c * N + n * SPL + s) : 0.0f;
+  for (int s = 0; s < K; ++s) {
+    A1[s] = cvalid ? ld(Am, (long)c * N + w * K + s) : 0.0f;
     A2[s] = A1[s] * LOG2E;
     dh[s] = 0.0f;
     dA[s] = 0.0f;
@@ -274,218 +314,214 @@ __global__ __launch_bounds__(NT) void ss_bwd_kernel(const SSArgs p) {
   float dD = 0.0f;
   const long rowbase = (long)b * seq * dim;
 
-  // Raw values of the next chunk (in reverse order), fetched one chunk ahead from
-  // clamped in-bounds indices so the loads are never behind a divergent branch.
-  constexpr int EPT = CPW * CK / NT;
-  constexpr int BPT = (N * CK + NT - 1) / NT;
-  TI px[EPT], pdt[EPT], pgo[EPT], pz[EPT];
-  TP pb[BPT], pc[BPT];
-  float pm[EPT];
+  // raw values of the next chunk (in reverse order), loaded a chunk ahead
+  TI rx[EPT], rdt[EPT], rdo[EPT], rz[EPT];
+  TP rbc[BCT];
+  float rm[EPT];
+  // this thread's staged (t, d) values, kept for the per-(t, d) epilogues
+  float ex[EPT], edtb[EPT], emask[EPT], edy[EPT], ego[EPT], ez[EPT];
   auto fetch = [&](int ts) {
 #pragma unroll
-    for (int q = 0; q < EPT; ++q) {
-      const int e = tid + q * NT;
-      const int t = min(ts + e / CPW, seq - 1), cc = min(c0 + e % CPW, dim - 1);
+    for (int i = 0; i < EPT; ++i) {
+      const int t = min(ts + w + i * NW, seq - 1);
       const long idx = rowbase + (long)t * dim + cc;
-      px[q] = x[idx];
-      pdt[q] = dt[idx];
-      pgo[q] = dout[idx];
-      pz[q] = z != nullptr ? z[idx] : px[q];
-      pm[q] = mean_mode ? p.dtmean[(long)b * seq + t] : 0.0f;
+      rx[i] = x[idx];
+      rdt[i] = dt[idx];
+      rdo[i] = dout[idx];
+      if (HAS_Z) rz[i] = z[idx];
+      rm[i] = MEAN ? p.dtmean[(long)b * seq + t] : 0.0f;
     }
 #pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      const int e = min(tid + q * NT, N * CK - 1);
-      const long idx = ((long)b * seq + min(ts + e / N, seq - 1)) * N + e % N;
-      pb[q] = Bm[idx];
-      pc[q] = Cm[idx];
+    for (int i = 0; i < BCT; ++i) {
+      const int e = tid + i * NT;
+      const int r = e % (2 * N);
+      const long row = (long)b * seq + min(ts + e / (2 * N), seq - 1);
+      rbc[i] = (r < N ? Bm : Cm)[row * N + (r % N)];
     }
   };
-  fetch((p.nck - 1) * CK);
 
+  fetch((p.nck - 1) * CK);
   for (int k = p.nck - 1; k >= 0; --k) {
     const int ts = k * CK;
-    // ---- stage the chunk ------------------------------------------------
+    // ---- stage the chunk ---------------------------------------------------------
 #pragma unroll
-    for (int q = 0; q < EPT; ++q) {
-      const int e = tid + q * NT;
-      const int tt = e / CPW, ch = e % CPW;
-      const bool ok = (ts + tt < seq) && (c0 + ch < dim);
-      const float dtr = to_f32(pdt[q]);
-      const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
-      s_x[ch][tt] = ok ? to_f32(px[q]) : 0.0f;
-      s_dtc[ch][tt] = dtc;
-      s_dtb[ch][tt] = ok ? (mean_mode ? pm[q] : dtc) : 0.0f;
-      s_rng[ch][tt] = (ok && dtr >= DT_MIN && dtr <= DT_MAX) ? 1.0f : 0.0f;
-      s_dy[ch][tt] = ok ? to_f32(pgo[q]) : 0.0f;  // raw upstream gradient; gated below if z is present
-      s_o[0][tt][ch] = ok ? to_f32(pz[q]) : 0.0f;  // raw z, consumed by the recompute epilogue
+    for (int i = 0; i < BCT; ++i) {
+      const int e = tid + i * NT;
+      s_bc[e / (2 * N)][e % (2 * N)] = to_f32(rbc[i]);
     }
 #pragma unroll
-    for (int q = 0; q < BPT; ++q) {
-      const int e = tid + q * NT;
-      if (e < N * CK) {
-        const int tt = e / N, nn = e % N;
-        const bool ok = ts + tt < seq;
-        s_B[nn][tt] = ok ? to_f32(pb[q]) : 0.0f;
-        s_C[nn][tt] = ok ? to_f32(pc[q]) : 0.0f;
+    for (int i = 0; i < EPT; ++i) {
+      const int tt = w + i * NW;
+      const bool ok = (ts + tt < seq) && cvalid;
+      const float dtr = to_f32(rdt[i]);
+      const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
+      const float dtb = ok ? (MEAN ? rm[i] : dtc) : 0.0f;
+      const float xv = ok ? to_f32(rx[i]) : 0.0f;
+      ex[i] = xv;
+      edtb[i] = dtb;
+      emask[i] = (ok && dtr >= DT_MIN && dtr <= DT_MAX) ? 1.0f : 0.0f;
+      ego[i] = ok ? to_f32(rdo[i]) : 0.0f;
+      ez[i] = (HAS_Z && ok) ? to_f32(rz[i]) : 0.0f;
+      s_dtc[lane][tt] = dtc;
+      s_dtx[lane][tt] = dtb * xv;
+      if (!HAS_Z) {
+        edy[i] = ego[i];
+        s_dy[lane][tt] = ego[i];
       }
     }
     if (k > 0) fetch((k - 1) * CK);
     __syncthreads();
 
-    // ---- recompute the chunk's states ------------------------------------
-    float h0[SPL];
+    // ---- recompute the chunk's states and decays from its checkpoint ---------------
+    float h0[K], hs[CK][K], as[CK][K];
 #pragma unroll
-    for (int s = 0; s < SPL; ++s)
-      h0[s] = (k > 0 && cvalid) ? p.ckpt[(((long)b * dim + c) * p.nck + (k - 1)) * N + n * SPL + s] : 0.0f;
-    float hs[CK][SPL], as[CK][SPL];
+    for (int s = 0; s < K; ++s)
+      h0[s] = (k > 0 && cvalid) ? p.ckpt[(((long)b * p.nck + (k - 1)) * N + w * K + s) * dim + c] : 0.0f;
     {
-      float hh[SPL];
+      float hh[K];
 #pragma unroll
-      for (int s = 0; s < SPL; ++s) hh[s] = h0[s];
+      for (int s = 0; s < K; ++s) hh[s] = h0[s];
 #pragma unroll
-      for (int j = 0; j < CK; ++j) {
-        const float dtc = s_dtc[cl][j];
-        const float dtx = s_dtb[cl][j] * s_x[cl][j];
+      for (int q = 0; q < CK / 4; ++q) {
+        const float4 dc4 = *reinterpret_cast<const float4*>(&s_dtc[lane][4 * q]);
+        const float4 dx4 = *reinterpret_cast<const float4*>(&s_dtx[lane][4 * q]);
+        const float dcv[4] = {dc4.x, dc4.y, dc4.z, dc4.w};
+        const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
 #pragma unroll
-        for (int s = 0; s < SPL; ++s) {
-          const int nn = n * SPL + s;
-          const float a = fast_exp2(dtc * A2[s]);
-          hh[s] = fmaf(a, hh[s], dtx * s_B[nn][j]);
-          as[j][s] = a;
-          hs[j][s] = hh[s];
+        for (int u = 0; u < 4; ++u) {
+          const int j = 4 * q + u;
+          const float* bc = &s_bc[j][w * K];
+          float acc = 0.0f;
+#pragma unroll
+          for (int s = 0; s < K; ++s) {
+            const float a = fast_exp2(dcv[u] * A2[s]);
+            hh[s] = fmaf(a, hh[s], dxv[u] * bc[s]);
+            as[j][s] = a;
+            hs[j][s] = hh[s];
+            if (HAS_Z) acc = fmaf(bc[N + s], hh[s], acc);
+          }
+          if (HAS_Z) s_yp[w][j][lane] = acc;
         }
       }
     }
 
-    // ---- gate: dy = dout * silu(z); dz = dout * y * silu'(z) ---------------
-    if (z != nullptr) {
+    // ---- gate: dy = dout silu(z); dz = dout y silu'(z) (y before the gate) -----------
+    if (HAS_Z) {
+      __syncthreads();
 #pragma unroll
-      for (int jb = 0; jb < CK; jb += TS) {
+      for (int i = 0; i < EPT; ++i) {
+        const int tt = w + i * NW;
+        float y = 0.0f;
 #pragma unroll
-        for (int j = 0; j < TS; ++j) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int s = 0; s < SPL; ++s) acc = fmaf(s_C[n * SPL + s][jb + j], hs[jb + j][s], acc);
-          s_r[0][tid][j] = acc;
-        }
-        __syncthreads();
-        for (int q = n; q < TS; q += LPC) {
-          float y = 0.0f;
-#pragma unroll
-          for (int m = 0; m < LPC; ++m) y += s_r[0][cl * LPC + m][q];
-          const int j = jb + q;
-          y = fmaf(Dc, s_x[cl][j], y);
-          const float zv = s_o[0][j][cl];
-          const float sg = sigmoidf(zv);
-          const float go = s_dy[cl][j];
-          s_dy[cl][j] = go * zv * sg;
-          s_o[1][j][cl] = go * y * sg * (1.0f + zv * (1.0f - sg));
-        }
-        __syncthreads();
-      }
-      if (p.dz != nullptr) {
-        for (int e = tid; e < CPW * CK; e += NT) {
-          const int tt = e / CPW, ch = e % CPW;
-          const int t = ts + tt, cc = c0 + ch;
-          if (t < seq && cc < dim) st((TI*)p.dz, rowbase + (long)t * dim + cc, s_o[1][tt][ch]);
-        }
+        for (int v = 0; v < NW; ++v) y += s_yp[v][tt][lane];
+        y = fmaf(Dc, ex[i], y);
+        const float sg = sigmoidf(ez[i]);
+        edy[i] = ego[i] * ez[i] * sg;
+        s_dy[lane][tt] = edy[i];
+        if (p.dz != nullptr && ts + tt < seq && cvalid)
+          st((TI*)p.dz, rowbase + (long)(ts + tt) * dim + c, ego[i] * y * sg * (1.0f + ez[i] * (1.0f - sg)));
       }
       __syncthreads();
     }
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) dD = fmaf(edy[i], ex[i], dD);
 
-    // ---- reverse recurrence over the chunk ---------------------------------
+    // ---- reverse recurrence, in blocks of TS timesteps ------------------------------
 #pragma unroll
     for (int jb = CK - TS; jb >= 0; jb -= TS) {
+      float dyv[TS], dcv[TS], dxv[TS];
+#pragma unroll
+      for (int q = 0; q < TS / 4; ++q) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&s_dy[lane][jb + 4 * q]);
+        const float4 b4 = *reinterpret_cast<const float4*>(&s_dtc[lane][jb + 4 * q]);
+        const float4 c4 = *reinterpret_cast<const float4*>(&s_dtx[lane][jb + 4 * q]);
+        dyv[4 * q] = a4.x; dyv[4 * q + 1] = a4.y; dyv[4 * q + 2] = a4.z; dyv[4 * q + 3] = a4.w;
+        dcv[4 * q] = b4.x; dcv[4 * q + 1] = b4.y; dcv[4 * q + 2] = b4.z; dcv[4 * q + 3] = b4.w;
+        dxv[4 * q] = c4.x; dxv[4 * q + 1] = c4.y; dxv[4 * q + 2] = c4.z; dxv[4 * q + 3] = c4.w;
+      }
+      float* g = s_g + w * GW + lane * GS;
 #pragma unroll
       for (int j = TS - 1; j >= 0; --j) {
         const int jj = jb + j;
-        const float dyv = s_dy[cl][jj];
-        const float dtc = s_dtc[cl][jj];
-        const float dtx = s_dtb[cl][jj] * s_x[cl][jj];
-        float px = 0.0f, pa = 0.0f, gC = 0.0f, gB = 0.0f;
+        const float* bc = &s_bc[jj][w * K];
+        float px = 0.0f, pa = 0.0f, gC[K], gB[K];
 #pragma unroll
-        for (int s = 0; s < SPL; ++s) {
-          const int nn = n * SPL + s;
-          const float Bv = s_B[nn][jj];
-          const float Cv = s_C[nn][jj];
-          dh[s] = fmaf(dyv, Cv, dh[s]);
-          const float hp = jj > 0 ? hs[jj - 1][s] : h0[s];
-          gC = dyv * hs[jj][s];
-          gB = dh[s] * dtx;
+        for (int s = 0; s < K; ++s) {
+          const float Bv = bc[s];
+          const float Cv = bc[N + s];
+          dh[s] = fmaf(dyv[j], Cv, dh[s]);
+          gC[s] = dyv[j] * hs[jj][s];
+          gB[s] = dh[s] * dxv[j];
           px = fmaf(dh[s], Bv, px);
-          const float ga = dh[s] * hp * as[jj][s];
-          dA[s] = fmaf(ga, dtc, dA[s]);
-          pa = fmaf(ga, A1[s], pa);
           dh[s] *= as[jj][s];
+          const float ga = dh[s] * (jj > 0 ? hs[jj - 1][s] : h0[s]);
+          dA[s] = fmaf(ga, dcv[j], dA[s]);
+          pa = fmaf(ga, A1[s], pa);
         }
-        s_r[0][tid][j] = px;
-        s_r[1][tid][j] = pa;
-        s_r[2][tid][j] = gC;
-        s_r[3][tid][j] = gB;
+        if constexpr (K == 4) {
+          *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gC[2], gC[3]);
+          *reinterpret_cast<float4*>(g + j * 2 * K + K) = make_float4(gB[0], gB[1], gB[2], gB[3]);
+        } else {
+          *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gB[0], gB[1]);
+        }
+        s_pp[0][w][j][lane] = px;
+        s_pp[1][w][j][lane] = pa;
       }
       __syncthreads();
-      // sums over states: dx, ddt per (t, channel)
-      for (int q = n; q < TS; q += LPC) {
-        float px = 0.0f, pa = 0.0f;
-#pragma unroll
-        for (int m = 0; m < LPC; ++m) {
-          px += s_r[0][cl * LPC + m][q];
-          pa += s_r[1][cl * LPC + m][q];
-        }
-        const int jj = jb + q;
-        const float xv = s_x[cl][jj];
-        const float dyv = s_dy[cl][jj];
-        dD = fmaf(dyv, xv, dD);
-        s_o[0][jj][cl] = fmaf(px, s_dtb[cl][jj], dyv * Dc);
-        const float g = mean_mode ? pa : pa + px * xv;
-        s_o[1][jj][cl] = s_rng[cl][jj] * g;
-        if (mean_mode) s_r[0][cl * LPC + n][q] = px * xv;  // reused below for the dt-mean coupling
-      }
-      // sums over channels: dC (qty 0) and dB (qty 1) per (t, n) for this workgroup's tile
-      for (int e = tid; e < 2 * N * TS; e += NT) {
-        const int qty = e / (N * TS);
-        const int r = e % (N * TS);
-        const int nn = r / TS, q = r % TS;
+      // sums over the 64 channels: dC (qty 0) and dB (qty 1) per (t, n) of this tile;
+      // THR adjacent threads share an output, each summing every THR-th channel
+      {
+        const int o = tid / THR, hf = tid % THR;
+        const int n = o % N, qty = (o / N) % 2, j = o / (2 * N);
+        const float* src = s_g + (n / K) * GW + hf * GS + j * 2 * K + qty * K + (n % K);
         float acc = 0.0f;
-        for (int ch = 0; ch < CPW; ++ch) acc += s_r[2 + qty][ch * LPC + nn][q];
-        const int t = ts + jb + q;
-        if (t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + qty) * N + nn] = acc;
+#pragma unroll 16
+        for (int l = 0; l < 64 / THR; ++l) acc += src[l * THR * GS];
+        if (THR == 2) acc += __shfl_xor(acc, 1);
+        const int t = ts + jb + j;
+        if (hf == 0 && t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + qty) * N + n] = acc;
       }
-      __syncthreads();
-      if (mean_mode) {
-        for (int q = tid; q < TS; q += NT) {
+      // sums over the states: dx, ddt for the (t, d) this thread staged in this block
+#pragma unroll
+      for (int i = jb / NW; i < (jb + TS) / NW; ++i) {
+        const int tt = w + i * NW, j = tt - jb;
+        float pxs = 0.0f, pas = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) {
+          pxs += s_pp[0][v][j][lane];
+          pas += s_pp[1][v][j][lane];
+        }
+        if (ts + tt < seq && cvalid) {
+          const long idx = rowbase + (long)(ts + tt) * dim + c;
+          st((TI*)p.dx, idx, fmaf(pxs, edtb[i], edy[i] * Dc));
+          st((TI*)p.ddt, idx, emask[i] * (MEAN ? pas : fmaf(pxs, ex[i], pas)));
+        }
+        if (MEAN) s_m[j][lane] = pxs * ex[i];  // dt-mean coupling, summed over channels below
+      }
+      if (MEAN) {
+        __syncthreads();
+        if (tid < TS) {
           float acc = 0.0f;
-          for (int ch = 0; ch < CPW; ++ch) acc += s_r[0][ch * LPC + (q % LPC)][q];
-          const int t = ts + jb + q;
+          for (int l = 0; l < 64; ++l) acc += s_m[tid][l];
+          const int t = ts + jb + tid;
           if (t < seq) p.part_m[((long)tile * p.batch + b) * seq + t] = acc;
         }
-        __syncthreads();
       }
+      __syncthreads();
     }
-    // ---- write dx, ddt rows for the chunk ------------------------------------
-    for (int e = tid; e < CPW * CK; e += NT) {
-      const int tt = e / CPW, ch = e % CPW;
-      const int t = ts + tt, cc = c0 + ch;
-      if (t < seq && cc < dim) {
-        const long idx = rowbase + (long)t * dim + cc;
-        st((TI*)p.dx, idx, s_o[0][tt][ch]);
-        st((TI*)p.ddt, idx, s_o[1][tt][ch]);
-      }
-    }
-    __syncthreads();
   }
-  // dA partial per (b, d, n); dD partial per (b, d)
+  // dA partial per (b, d, n); dD partial per (b, d): the lanes of one channel in the
+  // NW waves hold disjoint timesteps
   if (cvalid) {
 #pragma unroll
-    for (int s = 0; s < SPL; ++s) p.part_a[((long)b * dim + c) * N + n * SPL + s] = dA[s];
+    for (int s = 0; s < K; ++s) p.part_a[((long)b * dim + c) * N + w * K + s] = dA[s];
   }
-  // dD: lanes of a channel hold disjoint timesteps; reduce over the LPC lanes
-  s_r[0][tid][0] = dD;
+  s_pp[0][w][0][lane] = dD;
   __syncthreads();
-  if (n == 0 && cvalid) {
+  if (w == 0 && cvalid) {
     float acc = 0.0f;
-    for (int m = 0; m < LPC; ++m) acc += s_r[0][cl * LPC + m][0];
+#pragma unroll
+    for (int v = 0; v < NW; ++v) acc += s_pp[0][v][0][lane];
     p.part_d[(long)b * dim + c] = acc;
   }
 }
@@ -546,18 +582,12 @@ __global__ __launch_bounds__(256) void ss_mean_fixup_kernel(const float* __restr
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-constexpr int FWD_NT = 256;
-constexpr int BWD_NT = 256;
-
-inline int ss_ck(int N) { return N <= 16 ? 32 : 16; }
-
 inline bool pow2_state(int N) { return N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32; }
 
-inline int ntiles(int dim, int N, int nt) {
-  const int lpc = N < 16 ? N : 16;
-  const int cpw = nt / lpc;
-  return (dim + cpw - 1) / cpw;
-}
+// one workgroup per (batch, 64-channel tile)
+inline int ntiles(int dim) { return (dim + 63) / 64; }
+
+inline long num_chunks(int seq) { return (seq + SS_CK - 1) / SS_CK; }
 
 struct WsLayout {
   size_t ckpt, dtmean, part_bc, part_a, part_d, part_m, total;
@@ -567,9 +597,8 @@ inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 inline WsLayout bwd_layout(int batch, int seq, int dim, int N, bool need_ckpt, bool mean_mode) {
   WsLayout w{};
-  const int ck = ss_ck(N);
-  const long nck = (seq + ck - 1) / ck;
-  const int nt = ntiles(dim, N, BWD_NT);
+  const long nck = num_chunks(seq);
+  const int nt = ntiles(dim);
   size_t off = 0;
   w.ckpt = off;
   if (need_ckpt) off += align256((size_t)batch * dim * nck * N * 4);
@@ -587,14 +616,35 @@ inline WsLayout bwd_layout(int batch, int seq, int dim, int N, bool need_ckpt, b
   return w;
 }
 
-template <typename TI, typename TP, int N>
-void launch_fwd_t(hipStream_t s, const SSArgs& a) {
+template <typename TI, typename TP, int N, int KMAX>
+void launch_fwd_k(hipStream_t s, const SSArgs& a) {
+  constexpr int NT = SSGeo<N, KMAX>::NT;
   const int grid = a.batch * a.ntile;
   const bool mean = a.dtmean != nullptr, hz = a.z != nullptr;
-  if (mean && hz) ss_fwd_kernel<TI, TP, N, FWD_NT, true, true><<<grid, FWD_NT, 0, s>>>(a);
-  else if (mean) ss_fwd_kernel<TI, TP, N, FWD_NT, true, false><<<grid, FWD_NT, 0, s>>>(a);
-  else if (hz) ss_fwd_kernel<TI, TP, N, FWD_NT, false, true><<<grid, FWD_NT, 0, s>>>(a);
-  else ss_fwd_kernel<TI, TP, N, FWD_NT, false, false><<<grid, FWD_NT, 0, s>>>(a);
+  const TP* Bp = (const TP*)a.B;
+  const TP* Cp = (const TP*)a.C;
+  if (a.out == nullptr) {  // checkpoints only (backward without saved states)
+    if (mean) ss_fwd_kernel<TI, TP, N, KMAX, true, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
+    else ss_fwd_kernel<TI, TP, N, KMAX, false, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  } else if (mean && hz) {
+    ss_fwd_kernel<TI, TP, N, KMAX, true, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  } else if (mean) {
+    ss_fwd_kernel<TI, TP, N, KMAX, true, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  } else if (hz) {
+    ss_fwd_kernel<TI, TP, N, KMAX, false, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  } else {
+    ss_fwd_kernel<TI, TP, N, KMAX, false, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  }
+}
+
+// Two states per lane: 2 waves per SIMD at config-2 size (192 workgroups of 8 waves), which
+// hides the LDS and exp latencies better than four states per lane at 1 wave per SIMD
+// (measured on MI355X: 209 vs 247 us forward, 722 vs 811 us backward).
+constexpr int SS_KMAX = 2;
+
+template <typename TI, typename TP, int N>
+void launch_fwd_t(hipStream_t s, const SSArgs& a) {
+  launch_fwd_k<TI, TP, N, SS_KMAX>(s, a);
 }
 
 template <typename TI, typename TP>
@@ -611,10 +661,22 @@ int launch_fwd_n(hipStream_t s, const SSArgs& a, int N) {
   return check_launch("selective scan");
 }
 
+template <typename TI, typename TP, int N, int KMAX>
+void launch_bwd_k(hipStream_t s, const SSArgs& a) {
+  constexpr int NT = SSGeo<N, KMAX>::NT;
+  const int grid = a.batch * a.ntile;
+  const bool mean = a.dtmean != nullptr, hz = a.z != nullptr;
+  const TP* Bp = (const TP*)a.B;
+  const TP* Cp = (const TP*)a.C;
+  if (mean && hz) ss_bwd_kernel<TI, TP, N, KMAX, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  else if (mean) ss_bwd_kernel<TI, TP, N, KMAX, true, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  else if (hz) ss_bwd_kernel<TI, TP, N, KMAX, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  else ss_bwd_kernel<TI, TP, N, KMAX, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
+}
+
 template <typename TI, typename TP, int N>
 void launch_bwd_t(hipStream_t s, const SSArgs& a) {
-  const int grid = a.batch * a.ntile;
-  ss_bwd_kernel<TI, TP, N, BWD_NT, 32><<<grid, BWD_NT, 0, s>>>(a);
+  launch_bwd_k<TI, TP, N, SS_KMAX>(s, a);
 }
 
 template <typename TI, typename TP>
@@ -662,9 +724,7 @@ extern "C" {
 
 size_t edf_selective_scan_states_bytes(int batch, int seq_len, int hidden, int state) {
   if (batch <= 0 || seq_len <= 0 || hidden <= 0 || state <= 0) return 0;
-  const int ck = edf::ss_ck(state);
-  const size_t nck = (size_t)(seq_len + ck - 1) / ck;
-  return (size_t)batch * hidden * nck * state * sizeof(float);
+  return (size_t)batch * edf::num_chunks(seq_len) * state * hidden * sizeof(float);
 }
 
 size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode) {
@@ -694,9 +754,8 @@ int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const 
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z; a.out = out;
   a.ckpt = (float*)states;
   a.batch = batch; a.seq = seq_len; a.dim = hidden;
-  a.ck = ss_ck(state);
-  a.nck = (seq_len + a.ck - 1) / a.ck;
-  a.ntile = ntiles(hidden, state, FWD_NT);
+  a.nck = (int)num_chunks(seq_len);
+  a.ntile = ntiles(hidden);
   if (mode == EDF_SS_DT_MEAN) {
     a.dtmean = (float*)workspace;
     rc = run_dtmean(s, dt, (float*)workspace, batch, seq_len, hidden, io_dtype);
@@ -730,8 +789,8 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   SSArgs a{};
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z;
   a.batch = batch; a.seq = seq_len; a.dim = hidden;
-  a.ck = ss_ck(state);
-  a.nck = (seq_len + a.ck - 1) / a.ck;
+  a.nck = (int)num_chunks(seq_len);
+  a.ntile = ntiles(hidden);
   if (mean_mode) {
     a.dtmean = (float*)(ws + L.dtmean);
     rc = run_dtmean(s, dt, (float*)(ws + L.dtmean), batch, seq_len, hidden, io_dtype);
@@ -741,7 +800,6 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   if (states == nullptr) {  // recompute checkpoints with a forward pass that writes no output
     SSArgs f = a;
     f.out = nullptr;
-    f.ntile = ntiles(hidden, state, FWD_NT);
     rc = by_dtypes(io_dtype, param_dtype, [&](auto* ti, auto* tp) {
       using TI = std::remove_pointer_t<decltype(ti)>;
       using TP = std::remove_pointer_t<decltype(tp)>;
@@ -757,7 +815,6 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   a.part_a = (float*)(ws + L.part_a);
   a.part_d = (float*)(ws + L.part_d);
   a.part_m = mean_mode ? (float*)(ws + L.part_m) : nullptr;
-  a.ntile = ntiles(hidden, state, BWD_NT);
   rc = by_dtypes(io_dtype, param_dtype, [&](auto* ti, auto* tp) {
     using TI = std::remove_pointer_t<decltype(ti)>;
     using TP = std::remove_pointer_t<decltype(tp)>;
