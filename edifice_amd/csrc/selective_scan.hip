@@ -271,20 +271,21 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   constexpr int TS = 8;              // reduction block (timesteps)
   constexpr int PS = CK + 4;         // [channel][t] row stride (16-byte reads conflict-free)
   constexpr int EPT = CK * 64 / NT;  // staged (t, channel) elements per thread
-  constexpr int GS = 2 * K * TS + 4;  // per-lane stride of the dC/dB tile: b128 writes conflict-free
-  constexpr int GW = 64 * GS + 8;     // per-wave stride: the reduction's reads are conflict-free
-  constexpr int THR = NT / (TS * 2 * N);  // threads per dB/dC output (adjacent lanes)
-  static_assert(EPT * NW == CK && TS % NW == 0 && CK % TS == 0, "staging layout");
-  static_assert((THR == 1 || THR == 2) && THR * TS * 2 * N == NT, "dB/dC outputs per thread");
+  constexpr int GS = 2 * K * TS + 4;  // per-lane stride of a wave's dC/dB tile: b128 writes conflict-free
+  constexpr int OPW = 2 * K * TS;     // dC/dB outputs per wave per block
+  constexpr int LPO = 64 / OPW;       // lanes per output (each sums 64 / LPO channels)
+  static_assert(EPT * NW == CK && CK % TS == 0 && (LPO == 1 || LPO == 2), "staging layout");
   constexpr int BCT = CK * 2 * N / NT;  // staged B/C values per thread
   __shared__ __align__(16) float s_bc[CK][2 * N];  // per t: B[0..N), C[0..N)
   __shared__ __align__(16) float s_dtc[64][PS];
   __shared__ __align__(16) float s_dtx[64][PS];
   __shared__ __align__(16) float s_dy[64][PS];
-  __shared__ __align__(16) float s_g[NW * GW];
-  __shared__ float s_pp[2][NW][TS][64];
-  __shared__ float s_yp[HAS_Z ? NW : 1][CK][64];
-  __shared__ float s_m[MEAN ? TS : 1][64];
+  // each wave's private dC/dB tile: [lane][t][qty][state], reduced by the wave itself
+  __shared__ __align__(16) float s_g[NW][64 * GS];
+  // per-(t, d) partial sums over each wave's states for the chunk, px and pa
+  // ([2][NW][CK][64]); the same memory first holds the gate's y partials ([NW][CK][64])
+  __shared__ float s_pp[2 * NW * CK * 64];
+  __shared__ float s_m[MEAN ? CK : 1][64];
 
   const TI* __restrict__ x = (const TI*)p.x;
   const TI* __restrict__ dt = (const TI*)p.dt;
@@ -301,6 +302,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   const int c = tile * 64 + lane;
   const bool cvalid = c < dim;
   const int cc = min(c, dim - 1);
+  auto pp = [&](int q, int v, int t) -> float& { return s_pp[((q * NW + v) * CK + t) * 64 + lane]; };
 
   float A1[K], A2[K], dh[K], dA[K];
 #pragma unroll
@@ -373,7 +375,9 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
     __syncthreads();
 
     // ---- recompute the chunk's states and decays from its checkpoint ---------------
-    float h0[K], hs[CK][K], as[CK][K];
+    // states, decays and this wave's B/C values of the chunk, kept in registers for the
+    // reverse pass (reading B/C from LDS once per chunk halves that LDS traffic)
+    float h0[K], hs[CK][K], as[CK][K], bB[CK][K], bC[CK][K];
 #pragma unroll
     for (int s = 0; s < K; ++s)
       h0[s] = (k > 0 && cvalid) ? p.ckpt[(((long)b * p.nck + (k - 1)) * N + w * K + s) * dim + c] : 0.0f;
@@ -394,13 +398,15 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
           float acc = 0.0f;
 #pragma unroll
           for (int s = 0; s < K; ++s) {
+            bB[j][s] = bc[s];
+            bC[j][s] = bc[N + s];
             const float a = fast_exp2(dcv[u] * A2[s]);
-            hh[s] = fmaf(a, hh[s], dxv[u] * bc[s]);
+            hh[s] = fmaf(a, hh[s], dxv[u] * bB[j][s]);
             as[j][s] = a;
             hs[j][s] = hh[s];
-            if (HAS_Z) acc = fmaf(bc[N + s], hh[s], acc);
+            if (HAS_Z) acc = fmaf(bC[j][s], hh[s], acc);
           }
-          if (HAS_Z) s_yp[w][j][lane] = acc;
+          if (HAS_Z) pp(0, w, j) = acc;
         }
       }
     }
@@ -413,7 +419,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         const int tt = w + i * NW;
         float y = 0.0f;
 #pragma unroll
-        for (int v = 0; v < NW; ++v) y += s_yp[v][tt][lane];
+        for (int v = 0; v < NW; ++v) y += pp(0, v, tt);
         y = fmaf(Dc, ex[i], y);
         const float sg = sigmoidf(ez[i]);
         edy[i] = ego[i] * ez[i] * sg;
@@ -439,16 +445,15 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         dcv[4 * q] = b4.x; dcv[4 * q + 1] = b4.y; dcv[4 * q + 2] = b4.z; dcv[4 * q + 3] = b4.w;
         dxv[4 * q] = c4.x; dxv[4 * q + 1] = c4.y; dxv[4 * q + 2] = c4.z; dxv[4 * q + 3] = c4.w;
       }
-      float* g = s_g + w * GW + lane * GS;
+      float* g = &s_g[w][lane * GS];
 #pragma unroll
       for (int j = TS - 1; j >= 0; --j) {
         const int jj = jb + j;
-        const float* bc = &s_bc[jj][w * K];
         float px = 0.0f, pa = 0.0f, gC[K], gB[K];
 #pragma unroll
         for (int s = 0; s < K; ++s) {
-          const float Bv = bc[s];
-          const float Cv = bc[N + s];
+          const float Bv = bB[jj][s];
+          const float Cv = bC[jj][s];
           dh[s] = fmaf(dyv[j], Cv, dh[s]);
           gC[s] = dyv[j] * hs[jj][s];
           gB[s] = dh[s] * dxv[j];
@@ -464,50 +469,53 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         } else {
           *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gB[0], gB[1]);
         }
-        s_pp[0][w][j][lane] = px;
-        s_pp[1][w][j][lane] = pa;
+        pp(0, w, jj) = px;
+        pp(1, w, jj) = pa;
       }
-      __syncthreads();
-      // sums over the 64 channels: dC (qty 0) and dB (qty 1) per (t, n) of this tile;
-      // THR adjacent threads share an output, each summing every THR-th channel
+      // sums over the 64 channels of this wave's dC (qty 0) and dB (qty 1) per (t, n):
+      // the tile is the wave's own, so LDS ordering within the wave replaces a barrier
+      // and other waves keep computing meanwhile.  Output o = (t, qty, state) is the
+      // o-th float of every lane row; LPO = 2 lanes share it (channels 0..31 / 32..63).
       {
-        const int o = tid / THR, hf = tid % THR;
-        const int n = o % N, qty = (o / N) % 2, j = o / (2 * N);
-        const float* src = s_g + (n / K) * GW + hf * GS + j * 2 * K + qty * K + (n % K);
+        __builtin_amdgcn_wave_barrier();  // keep the tile writes before the column reads
+        const int o = lane % OPW, hf = lane / OPW;
+        const float* src = &s_g[w][hf * (64 / LPO) * GS + o];
         float acc = 0.0f;
 #pragma unroll 16
-        for (int l = 0; l < 64 / THR; ++l) acc += src[l * THR * GS];
-        if (THR == 2) acc += __shfl_xor(acc, 1);
+        for (int l = 0; l < 64 / LPO; ++l) acc += src[l * GS];
+        __builtin_amdgcn_wave_barrier();  // and the reads before the next block's writes
+        if (LPO == 2) acc += __shfl_xor(acc, 32);
+        const int j = o / (2 * K), qty = (o / K) % 2, n = w * K + o % K;
         const int t = ts + jb + j;
         if (hf == 0 && t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + qty) * N + n] = acc;
       }
-      // sums over the states: dx, ddt for the (t, d) this thread staged in this block
+    }
+    // ---- sums over the states: dx, ddt for the (t, d) this thread staged --------------
+    __syncthreads();
 #pragma unroll
-      for (int i = jb / NW; i < (jb + TS) / NW; ++i) {
-        const int tt = w + i * NW, j = tt - jb;
-        float pxs = 0.0f, pas = 0.0f;
+    for (int i = 0; i < EPT; ++i) {
+      const int tt = w + i * NW;
+      float pxs = 0.0f, pas = 0.0f;
 #pragma unroll
-        for (int v = 0; v < NW; ++v) {
-          pxs += s_pp[0][v][j][lane];
-          pas += s_pp[1][v][j][lane];
-        }
-        if (ts + tt < seq && cvalid) {
-          const long idx = rowbase + (long)(ts + tt) * dim + c;
-          st((TI*)p.dx, idx, fmaf(pxs, edtb[i], edy[i] * Dc));
-          st((TI*)p.ddt, idx, emask[i] * (MEAN ? pas : fmaf(pxs, ex[i], pas)));
-        }
-        if (MEAN) s_m[j][lane] = pxs * ex[i];  // dt-mean coupling, summed over channels below
+      for (int v = 0; v < NW; ++v) {
+        pxs += pp(0, v, tt);
+        pas += pp(1, v, tt);
       }
-      if (MEAN) {
-        __syncthreads();
-        if (tid < TS) {
-          float acc = 0.0f;
-          for (int l = 0; l < 64; ++l) acc += s_m[tid][l];
-          const int t = ts + jb + tid;
-          if (t < seq) p.part_m[((long)tile * p.batch + b) * seq + t] = acc;
-        }
+      if (ts + tt < seq && cvalid) {
+        const long idx = rowbase + (long)(ts + tt) * dim + c;
+        st((TI*)p.dx, idx, fmaf(pxs, edtb[i], edy[i] * Dc));
+        st((TI*)p.ddt, idx, emask[i] * (MEAN ? pas : fmaf(pxs, ex[i], pas)));
       }
+      if (MEAN) s_m[tt][lane] = pxs * ex[i];  // dt-mean coupling, summed over channels below
+    }
+    if (MEAN) {
       __syncthreads();
+      if (tid < CK) {
+        float acc = 0.0f;
+        for (int l = 0; l < 64; ++l) acc += s_m[tid][l];
+        const int t = ts + tid;
+        if (t < seq) p.part_m[((long)tile * p.batch + b) * seq + t] = acc;
+      }
     }
   }
   // dA partial per (b, d, n); dD partial per (b, d): the lanes of one channel in the
@@ -516,12 +524,13 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 #pragma unroll
     for (int s = 0; s < K; ++s) p.part_a[((long)b * dim + c) * N + w * K + s] = dA[s];
   }
-  s_pp[0][w][0][lane] = dD;
+  __syncthreads();  // the last chunk's epilogue has read s_pp
+  pp(0, w, 0) = dD;
   __syncthreads();
   if (w == 0 && cvalid) {
     float acc = 0.0f;
 #pragma unroll
-    for (int v = 0; v < NW; ++v) acc += s_pp[0][v][0][lane];
+    for (int v = 0; v < NW; ++v) acc += pp(0, v, 0);
     p.part_d[(long)b * dim + c] = acc;
   }
 }
