@@ -44,6 +44,7 @@ SIGNATURES = {
         I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_debug_mfma_32x32x16_bf16": (I, [P, P, P, P]),
     "edf_debug_acc_kfrag_bf16": (I, [P, P, P]),
+    "edf_debug_lds_read_tr16": (I, [P, P, P]),
 }
 
 

@@ -74,4 +74,17 @@ EDF_DEVICE void store_rows(bf16* dst, long ld, const f32x16& x, int li, int g, f
   }
 }
 
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, with lane i supplying the
+// address A_i of four consecutive bf16, lane j = 4 a + b receives element b of
+// A_{a}, A_{a+4}, A_{a+8}, A_{a+12} (layout checked on the GPU by
+// tests/test_gpu_mfma_layout.py).  Pointing lane i at row r0 + i / 4, column
+// c0 + 4 (i % 4) of a row-major tile hands lane j the column c0 + j of rows r0..r0+3:
+// a transposed operand straight from a row-major LDS tile.
+EDF_DEVICE bf16x4 lds_read_tr16(const bf16* p) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+  return __builtin_bit_cast(bf16x4, v);
+}
+
 }  // namespace edf

@@ -32,16 +32,19 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
                                                              const bf16* __restrict__ V, bf16* __restrict__ O,
                                                              float* __restrict__ LSE, int T, float scale_log2) {
   constexpr int BM = 128, BN = 64;
-  constexpr int KS = HD + 8;  // sK row stride (elements)
-  constexpr int VS = BN + 4;  // sVt row stride (elements)
+  constexpr int KS = HD + 8;   // sK row stride (elements): 16-byte operand reads conflict-free
+  constexpr int VS = HD + 16;  // sV row stride: transposed 8-byte reads conflict-free
   constexpr int NKK = HD / 16, NDT = HD / 32;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BN * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[HD * VS];
+  constexpr int CPR = HD / 8;             // 16-byte chunks per row
+  constexpr int CPT = BN * CPR / 256;     // chunks per thread per tile (K and V each)
+  static_assert(CPT >= 1 && BN * CPR % 256 == 0, "tile staging");
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * KS];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * VS];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
   const long bh = blockIdx.y;
-  const int qb = CAUSAL ? (gridDim.x - 1 - blockIdx.x) : blockIdx.x;
+  const int qb = CAUSAL ? (gridDim.x - 1 - blockIdx.x) : blockIdx.x;  // heaviest blocks first
   const int q0 = qb * BM;
   const int qw = q0 + 32 * w;
   const int myq = qw + li;
@@ -49,51 +52,54 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
   const bf16* Kh = K + bh * T * HD;
   const bf16* Vh = V + bh * T * HD;
 
+  // Q^T as MFMA B fragments, kept in registers
   bf16x8 qf[NKK];
 #pragma unroll
-  for (int kk = 0; kk < NKK; ++kk) {
-    if (myq < T)
-      qf[kk] = *(const bf16x8*)(Qh + (long)myq * HD + kk * 16 + 8 * g);
-    else
-      qf[kk] = bf16x8{};
-  }
+  for (int kk = 0; kk < NKK; ++kk)
+    qf[kk] = myq < T ? *(const bf16x8*)(Qh + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
   f32x16 o[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = zero16();
-  float m = -INFINITY, lsum = 0.0f;
+  float m = -INFINITY, lsum = 0.0f;  // running max (unscaled score units) and sum
+
+  // K / V tiles: global -> registers one tile ahead, registers -> LDS double buffer
+  bf16x8 rk[CPT], rv[CPT];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
+      const int key = k0 + row;
+      rk[i] = key < T ? *(const bf16x8*)(Kh + (long)key * HD + col) : bf16x8{};
+      rv[i] = key < T ? *(const bf16x8*)(Vh + (long)key * HD + col) : bf16x8{};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
+      *(bf16x8*)(&sK[buf][row * KS + col]) = rk[i];
+      *(bf16x8*)(&sV[buf][row * VS + col]) = rv[i];
+    }
+  };
 
   const int kend = CAUSAL ? min(T, q0 + BM) : T;
   const int nkt = (kend + BN - 1) / BN;
+  gload(0);
+  sstore(0);
+  if (nkt > 1) gload(BN);
+  __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
-    const int k0 = kt * BN;
-    __syncthreads();
-    for (int c = tid; c < BN * HD / 8; c += 256) {
-      const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const int key = k0 + row;
-      bf16x8 v = key < T ? *(const bf16x8*)(Kh + (long)key * HD + col) : bf16x8{};
-      *(bf16x8*)(sK + row * KS + col) = v;
-    }
-    for (int c = tid; c < (BN / 2) * (HD / 8); c += 256) {
-      const int kp = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const int key = k0 + 2 * kp;
-      bf16x8 v0 = key < T ? *(const bf16x8*)(Vh + (long)key * HD + col) : bf16x8{};
-      bf16x8 v1 = key + 1 < T ? *(const bf16x8*)(Vh + (long)(key + 1) * HD + col) : bf16x8{};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-        bf16x2 pr = {v0[e], v1[e]};
-        *(bf16x2*)(sVt + (col + e) * VS + 2 * kp) = pr;
-      }
-    }
-    __syncthreads();
-
+    const int k0 = kt * BN, buf = kt & 1;
+    const bf16* sk = sK[buf];
+    const bf16* sv = sV[buf];
+    // S^T = K Q^T: lane owns query column li, rows are keys
     f32x16 s[2];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       s[h2] = zero16();
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) {
-        const bf16x8 a = *(const bf16x8*)(sK + (h2 * 32 + li) * KS + kk * 16 + 8 * g);
+        const bf16x8 a = *(const bf16x8*)(sk + (h2 * 32 + li) * KS + kk * 16 + 8 * g);
         s[h2] = mfma32(a, qf[kk], s[h2]);
       }
     }
@@ -103,51 +109,68 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
     for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float v = s[h2][r] * scale_log2;
         if (need_mask) {
           const int key = k0 + h2 * 32 + d_row(r, g);
-          if (key >= T || (CAUSAL && key > myq)) v = -INFINITY;
+          if (key >= T || (CAUSAL && key > myq)) s[h2][r] = -INFINITY;
         }
-        s[h2][r] = v;
-        mx = fmaxf(mx, v);
+        mx = fmaxf(mx, s[h2][r]);
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mnew = fmaxf(m, mx);
-    const float alpha = fast_exp2(m - mnew);
+    // scale folded into the exponent: p = 2^(s c - m c)
+    const float mns = mnew == -INFINITY ? 0.0f : mnew * scale_log2;
+    if (__any(mnew > m)) {  // rescale only when some row maximum grew
+      const float alpha = fast_exp2(m * scale_log2 - mns);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
+    m = mnew;
     float rs = 0.0f;
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(s[h2][r] - mnew);
-        s[h2][r] = p;
-        rs += p;
+        const float pv = fast_exp2(fmaf(s[h2][r], scale_log2, -mns));
+        s[h2][r] = pv;
+        rs += pv;
       }
     }
-    rs += __shfl_xor(rs, 32);
-    lsum = lsum * alpha + rs;
-    m = mnew;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    lsum += rs + __shfl_xor(rs, 32);
 
+    // P^T straight from the S^T registers: B fragment kc holds keys
+    // 16 kc + 4 g + {0..3} and 16 kc + 8 + 4 g + {0..3}
     bf16x8 pf[4];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
       for (int it = 0; it < 8; ++it) pf[kc][it] = (bf16)s[kc >> 1][8 * (kc & 1) + it];
 
+    // O^T += V^T P^T; the V^T A fragment (same key order) comes from two transposed
+    // reads of the row-major V tile: lane i of each 16-lane group addresses key row
+    // base + i / 4, columns d0 + 4 (i % 4)
+    {
+      const int grp = l >> 4, i16 = l & 15;
+      const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+      const int kr = 4 * (grp >> 1) + (i16 >> 2);
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const bf16* vrow = sVt + (dt * 32 + li) * VS + 4 * g;
+      for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const bf16x8 a = cat4(*(const bf16x4*)(vrow + kc * 16), *(const bf16x4*)(vrow + kc * 16 + 8));
-        o[dt] = mfma32(a, pf[kc], o[dt]);
+        for (int kc = 0; kc < 4; ++kc) {
+          const bf16* vp = sv + (16 * kc + kr) * VS + dt * 32 + d0;
+          const bf16x8 a = cat4(lds_read_tr16(vp), lds_read_tr16(vp + 8 * VS));
+          o[dt] = mfma32(a, pf[kc], o[dt]);
+        }
       }
     }
+    if (kt + 1 < nkt) {
+      sstore(buf ^ 1);
+      if (kt + 2 < nkt) gload((kt + 2) * BN);
+    }
+    __syncthreads();
   }
 
   if (myq < T) {
@@ -162,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
         for (int e = 0; e < 4; ++e) v[e] = (bf16)(o[dt][rb * 4 + e] * inv);
         *(bf16x4*)(orow + dt * 32 + 8 * rb + 4 * g) = v;
       }
-    if (g == 0 && LSE != nullptr) LSE[bh * T + myq] = (m + __log2f(lsum)) * LN2;
+    if (g == 0 && LSE != nullptr) LSE[bh * T + myq] = (m * scale_log2 + __log2f(lsum)) * LN2;
   }
 }
 
@@ -230,6 +253,17 @@ __global__ void debug_mfma_kernel(const bf16* A, const bf16* B, float* C) {
   for (int r = 0; r < 16; ++r) C[d_row(r, g) * 32 + li] = d[r];
 }
 
+__global__ void debug_tr16_kernel(const bf16* x, bf16* out) {
+  __shared__ __attribute__((aligned(16))) bf16 t[64 * 64];
+  const int l = threadIdx.x;
+  for (int i = l; i < 64 * 64; i += 64) t[i] = x[i];
+  __syncthreads();
+  const int grp = l >> 4, i16 = l & 15;
+  const int row = 4 * (grp >> 1) + (i16 >> 2), col = 16 * (grp & 1) + 4 * (i16 & 3);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) *(bf16x4*)(out + (l * 2 + rb) * 4) = lds_read_tr16(t + (8 * rb + row) * 64 + col);
+}
+
 template <int HD>
 void launch_mfma_fwd(hipStream_t s, const void* q, const void* k, const void* v, void* o, float* lse, int BH, int T,
                      int causal, float scale_log2) {
@@ -267,6 +301,12 @@ int edf_debug_mfma_32x32x16_bf16(void* stream, const void* A, const void* B, flo
   EDF_REQUIRE(A && B && C, EDF_ERR_INVALID_ARG, "null tensor pointer");
   edf::debug_mfma_kernel<<<1, 64, 0, edf::as_stream(stream)>>>((const edf::bf16*)A, (const edf::bf16*)B, C);
   return edf::check_launch("debug mfma");
+}
+
+int edf_debug_lds_read_tr16(void* stream, const void* x, void* out) {
+  EDF_REQUIRE(x && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  edf::debug_tr16_kernel<<<1, 64, 0, edf::as_stream(stream)>>>((const edf::bf16*)x, (edf::bf16*)out);
+  return edf::check_launch("debug lds transposed read");
 }
 
 int edf_fused_flash_attention(void* stream, const void* q, const void* k, const void* v, void* out, float* lse,

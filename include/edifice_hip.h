@@ -228,6 +228,14 @@ int edf_debug_mfma_32x32x16_bf16(void* stream, const void* A, const void* B, flo
  * No reference counterpart; used by the GPU tests to pin the chunked delta rule's layout. */
 int edf_debug_acc_kfrag_bf16(void* stream, const float* x, void* out);
 
+/* Diagnostic: the transposed LDS read (ds_read_b64_tr_b16) the attention kernels use for
+ * the V^T operand.  x is a 64x64 bf16 row-major tile; out[lane][rb][e] (bf16, 64 x 2 x 4)
+ * receives, for rb = 0 and 1, what lane `lane` reads when lane i of each 16-lane group
+ * addresses row 8 rb + 4 (group / 2) + i / 4, column 16 (group % 2) + 4 (i % 4); that must
+ * be x[8 rb + 4 (lane / 32) + e][lane % 32].  No reference counterpart; used by the GPU
+ * tests to pin that layout. */
+int edf_debug_lds_read_tr16(void* stream, const void* x, void* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,3 +38,20 @@ def test_acc_kfrag_layout(rng):
     e = np.arange(8)[None, None, :]
     expect = x[16 * kk + 8 * (lane // 32) + e, lane % 32]
     np.testing.assert_array_equal(got, expect)
+
+
+def test_lds_read_tr16_layout(rng):
+    """ds_read_b64_tr_b16: the transposed V^T operand read from a row-major LDS tile."""
+    from edifice_amd import _native as nat
+    announce("lds_read_tr16_layout")
+    x = rng.integers(-128, 128, size=(64, 64)).astype(np.float32)  # exact in bf16
+    X = torch.from_numpy(x).to("cuda", torch.bfloat16)
+    out = torch.empty(64, 2, 4, dtype=torch.bfloat16, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    nat.call("edf_debug_lds_read_tr16", stream, ctypes.c_void_p(X.data_ptr()), ctypes.c_void_p(out.data_ptr()))
+    got = out.float().cpu().numpy()
+    lane = np.arange(64)[:, None, None]
+    rb = np.arange(2)[None, :, None]
+    e = np.arange(4)[None, None, :]
+    expect = x[8 * rb + 4 * (lane // 32) + e, lane % 32]
+    np.testing.assert_array_equal(got, expect)
