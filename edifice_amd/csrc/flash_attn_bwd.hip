@@ -10,12 +10,14 @@
 // uses atomics:
 //   1. D = rowsum(dO * O) (float32, one 16-lane group per row);
 //   2. dK/dV: a workgroup owns 128 keys (32 per wave, K and V kept in registers as
-//      MFMA B fragments) and walks the query tiles; S = Q K^T puts one key per lane
-//      column, so P and dS feed dV += P^T dO and dK += dS^T Q directly from
-//      registers (Q and dO are staged in LDS both row-major and transposed);
+//      MFMA B fragments) and walks 64-query tiles; S = Q K^T puts one key per lane
+//      column, so P and dS feed dV^T += dO^T P and dK^T += Q^T dS directly from
+//      registers, and dO^T, Q^T come from the row-major LDS tiles through
+//      ds_read_b64_tr_b16 (no transposed staging);
 //   3. dQ: a workgroup owns 128 queries (32 per wave, Q and dO in registers) and
-//      walks the key tiles; S^T = K Q^T puts one query per lane, so dS feeds
-//      dQ += dS K from registers (K staged transposed in LDS).
+//      walks 64-key tiles; S^T = K Q^T puts one query per lane, so dS^T feeds
+//      dQ^T += K^T dS^T from registers (K^T by transposed reads).
+//   Tiles are double-buffered in LDS (one barrier per tile).
 //   Causal: only tiles on or below the diagonal are visited.
 // float32 or other head_dim: wave-per-row kernels (parity path).
 #include "edf_abi.hpp"
@@ -43,6 +45,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dot_kernel(const TT* __restrict__ 
 }
 
 // ---- dK / dV -------------------------------------------------------------------
+// A workgroup owns 128 keys (32 per wave: K and V stay in registers as the B fragments
+// of S = Q K^T and dP = dO V^T, so a lane owns one key column) and walks 64-query tiles
+// of Q, dO, LSE and D staged in a double-buffered LDS ring (one barrier per tile).
+// dV^T += dO^T P and dK^T += Q^T dS take P and dS straight from the accumulator
+// registers as B fragments (query order as the accumulator rows hold it) and the
+// transposed A operands from the row-major tiles with ds_read_b64_tr_b16.
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                              const bf16* __restrict__ V, const bf16* __restrict__ dO,
@@ -50,139 +58,162 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
                                                              const float* __restrict__ Dd, bf16* __restrict__ dK,
                                                              bf16* __restrict__ dV, int T, float scale_log2,
                                                              float scale) {
-  constexpr int BKEY = 128, BQ = 32;
+  constexpr int BKEY = 128, BQ = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
-  constexpr int RS = HD + 8;  // row-major tile stride
-  constexpr int TS = BQ + 4;  // transposed tile stride
-  __shared__ __attribute__((aligned(16))) bf16 sQ[BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sdO[BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sQt[HD * TS];
-  __shared__ __attribute__((aligned(16))) bf16 sdOt[HD * TS];
-  __shared__ __attribute__((aligned(16))) float sL[BQ];
-  __shared__ __attribute__((aligned(16))) float sD[BQ];
+  constexpr int RS = HD + 8;           // row stride: 16-byte row reads conflict-free
+  constexpr int CPR = HD / 8;          // 16-byte chunks per row
+  constexpr int CPT = BQ * CPR / 256;  // chunks per thread per tile and tensor
+  static_assert(CPT >= 1 && BQ * CPR % 256 == 0, "tile staging");
+  __shared__ __attribute__((aligned(16))) bf16 sQ[2][BQ * RS];
+  __shared__ __attribute__((aligned(16))) bf16 sdO[2][BQ * RS];
+  __shared__ __attribute__((aligned(16))) float sL[2][BQ];
+  __shared__ __attribute__((aligned(16))) float sD[2][BQ];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
   const long bh = blockIdx.y;
-  const int kb0 = blockIdx.x * BKEY;
+  const int kb0 = blockIdx.x * BKEY;  // causal: low key blocks see the most queries and run first
   const int kw = kb0 + 32 * w;
   const int mykey = kw + li;
   const long base = bh * T * HD;
 
-  // K, V as B fragments: B[k = dim][j = key] -> lane holds row `mykey`, 8 dims
   bf16x8 kf[NKK], vf[NKK];
 #pragma unroll
   for (int kk = 0; kk < NKK; ++kk) {
-    if (mykey < T) {
-      kf[kk] = *(const bf16x8*)(K + base + (long)mykey * HD + kk * 16 + 8 * g);
-      vf[kk] = *(const bf16x8*)(V + base + (long)mykey * HD + kk * 16 + 8 * g);
-    } else {
-      kf[kk] = bf16x8{};
-      vf[kk] = bf16x8{};
-    }
+    kf[kk] = mykey < T ? *(const bf16x8*)(K + base + (long)mykey * HD + kk * 16 + 8 * g) : bf16x8{};
+    vf[kk] = mykey < T ? *(const bf16x8*)(V + base + (long)mykey * HD + kk * 16 + 8 * g) : bf16x8{};
   }
-  f32x16 dk[NDT], dv[NDT];
+  f32x16 dkt[NDT], dvt[NDT];  // dK^T, dV^T: rows = dims, column = this lane's key
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
-    dk[dt] = zero16();
-    dv[dt] = zero16();
+    dkt[dt] = zero16();
+    dvt[dt] = zero16();
   }
 
-  const int qstart = CAUSAL ? (kb0 / BQ) * BQ : 0;
-  for (int q0 = qstart; q0 < T; q0 += BQ) {
-    __syncthreads();
-    for (int c = tid; c < BQ * HD / 8; c += 256) {
-      const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const int q = q0 + row;
-      bf16x8 a = q < T ? *(const bf16x8*)(Q + base + (long)q * HD + col) : bf16x8{};
-      bf16x8 b = q < T ? *(const bf16x8*)(dO + base + (long)q * HD + col) : bf16x8{};
-      *(bf16x8*)(sQ + row * RS + col) = a;
-      *(bf16x8*)(sdO + row * RS + col) = b;
-    }
-    for (int c = tid; c < (BQ / 2) * (HD / 8); c += 256) {
-      const int qp = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const int q = q0 + 2 * qp;
-      const bf16x8 a0 = q < T ? *(const bf16x8*)(Q + base + (long)q * HD + col) : bf16x8{};
-      const bf16x8 a1 = q + 1 < T ? *(const bf16x8*)(Q + base + (long)(q + 1) * HD + col) : bf16x8{};
-      const bf16x8 b0 = q < T ? *(const bf16x8*)(dO + base + (long)q * HD + col) : bf16x8{};
-      const bf16x8 b1 = q + 1 < T ? *(const bf16x8*)(dO + base + (long)(q + 1) * HD + col) : bf16x8{};
+  bf16x8 rq[CPT], ro[CPT];
+  float rl = 0.0f, rd = 0.0f;
+  auto gload = [&](int q0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        *(bf16x2*)(sQt + (col + e) * TS + 2 * qp) = bf16x2{a0[e], a1[e]};
-        *(bf16x2*)(sdOt + (col + e) * TS + 2 * qp) = bf16x2{b0[e], b1[e]};
-      }
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
+      const int q = q0 + row;
+      rq[i] = q < T ? *(const bf16x8*)(Q + base + (long)q * HD + col) : bf16x8{};
+      ro[i] = q < T ? *(const bf16x8*)(dO + base + (long)q * HD + col) : bf16x8{};
     }
     if (tid < BQ) {
       const int q = q0 + tid;
-      sL[tid] = q < T ? LSE[bh * T + q] * LOG2E : 0.0f;
-      sD[tid] = q < T ? Dd[bh * T + q] : 0.0f;
+      rl = q < T ? LSE[bh * T + q] * LOG2E : 0.0f;
+      rd = q < T ? Dd[bh * T + q] : 0.0f;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
+      *(bf16x8*)(&sQ[buf][row * RS + col]) = rq[i];
+      *(bf16x8*)(&sdO[buf][row * RS + col]) = ro[i];
+    }
+    if (tid < BQ) {
+      sL[buf][tid] = rl;
+      sD[buf][tid] = rd;
+    }
+  };
+
+  const int qstart = CAUSAL ? kb0 : 0;  // causal: queries before kb0 see none of these keys
+  const int ntile = qstart < T ? (T - qstart + BQ - 1) / BQ : 0;
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);  // transposed-read column within a 32-dim tile
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);     // and row within a 16-query chunk
+  if (ntile > 0) {
+    gload(qstart);
+    sstore(0);
+    if (ntile > 1) gload(qstart + BQ);
+  }
+  __syncthreads();
+  for (int it = 0; it < ntile; ++it) {
+    const int q0 = qstart + it * BQ, buf = it & 1;
+#pragma unroll
+    for (int sub = 0; sub < BQ / 32; ++sub) {
+      const int qs = q0 + 32 * sub;
+      if (CAUSAL && qs + 31 < kw) continue;  // every query of the sub-tile precedes this wave's keys
+      // S = Q K^T and dP = dO V^T (32 queries x 32 keys); lane owns key column
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) {
+        const bf16x8 aq = *(const bf16x8*)(&sQ[buf][(32 * sub + li) * RS + kk * 16 + 8 * g]);
+        const bf16x8 ao = *(const bf16x8*)(&sdO[buf][(32 * sub + li) * RS + kk * 16 + 8 * g]);
+        s = mfma32(aq, kf[kk], s);
+        dp = mfma32(ao, vf[kk], dp);
+      }
+      const bool mask = (qs + 32 > T) || (mykey >= T) || (CAUSAL && qs < kw + 31);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        const f32x4 lv = *(const f32x4*)(&sL[buf][32 * sub + 8 * rb + 4 * g]);
+        const f32x4 dv4 = *(const f32x4*)(&sD[buf][32 * sub + 8 * rb + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = rb * 4 + e;
+          float p = fast_exp2(fmaf(s[r], scale_log2, -lv[e]));
+          if (mask) {
+            const int q = qs + 8 * rb + 4 * g + e;
+            if (q >= T || mykey >= T || (CAUSAL && mykey > q)) p = 0.0f;
+          }
+          s[r] = p;
+          dp[r] = p * (dp[r] - dv4[e]) * scale;
+        }
+      }
+      // B fragments: queries 16 kc + 4 g + {0..3} and 16 kc + 8 + 4 g + {0..3}
+      bf16x8 pb[2], db[2];
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pb[kc][e] = (bf16)s[8 * kc + e];
+          db[kc][e] = (bf16)dp[8 * kc + e];
+        }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          const int off = (32 * sub + 16 * kc + kr) * RS + dt * 32 + d0;
+          const bf16x8 ao = cat4(lds_read_tr16(&sdO[buf][off]), lds_read_tr16(&sdO[buf][off + 8 * RS]));
+          const bf16x8 aq = cat4(lds_read_tr16(&sQ[buf][off]), lds_read_tr16(&sQ[buf][off + 8 * RS]));
+          dvt[dt] = mfma32(ao, pb[kc], dvt[dt]);
+          dkt[dt] = mfma32(aq, db[kc], dkt[dt]);
+        }
+      }
+    }
+    if (it + 1 < ntile) {
+      sstore(buf ^ 1);
+      if (it + 2 < ntile) gload(q0 + 2 * BQ);
     }
     __syncthreads();
-    if (CAUSAL && q0 + BQ - 1 < kw) continue;  // every query of the tile precedes this wave's keys
-
-    // S = Q K^T and dP = dO V^T (32 queries x 32 keys); lane owns key column
-    f32x16 s = zero16(), dp = zero16();
-#pragma unroll
-    for (int kk = 0; kk < NKK; ++kk) {
-      const bf16x8 aq = *(const bf16x8*)(sQ + li * RS + kk * 16 + 8 * g);
-      const bf16x8 ao = *(const bf16x8*)(sdO + li * RS + kk * 16 + 8 * g);
-      s = mfma32(aq, kf[kk], s);
-      dp = mfma32(ao, vf[kk], dp);
-    }
-    const bool mask = (q0 + BQ > T) || (mykey >= T) || (CAUSAL && q0 < kw + 31);
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
-      const f32x4 lv = *(const f32x4*)(sL + 8 * rb + 4 * g);
-      const f32x4 dv4 = *(const f32x4*)(sD + 8 * rb + 4 * g);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = rb * 4 + e;
-        float p = fast_exp2(s[r] * scale_log2 - lv[e]);
-        if (mask) {
-          const int q = q0 + 8 * rb + 4 * g + e;
-          if (q >= T || mykey >= T || (CAUSAL && mykey > q)) p = 0.0f;
-        }
-        s[r] = p;
-        dp[r] = p * (dp[r] - dv4[e]) * scale;
-      }
-    }
-    // A fragments of P^T and dS^T (rows = keys, k = queries in the permuted order)
-    bf16x8 pa[2], da[2];
-#pragma unroll
-    for (int kc = 0; kc < 2; ++kc)
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        pa[kc][it] = (bf16)s[8 * kc + it];
-        da[kc][it] = (bf16)dp[8 * kc + it];
-      }
-    // dV += P^T dO ; dK += dS^T Q   (B = dO / Q rows for 8 permuted queries, one dim)
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const bf16* orow = sdOt + (dt * 32 + li) * TS + 4 * g;
-      const bf16* qrow = sQt + (dt * 32 + li) * TS + 4 * g;
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const bf16x8 bo = cat4(*(const bf16x4*)(orow + kc * 16), *(const bf16x4*)(orow + kc * 16 + 8));
-        const bf16x8 bq = cat4(*(const bf16x4*)(qrow + kc * 16), *(const bf16x4*)(qrow + kc * 16 + 8));
-        dv[dt] = mfma32(pa[kc], bo, dv[dt]);
-        dk[dt] = mfma32(da[kc], bq, dk[dt]);
-      }
-    }
   }
-  // dK, dV: D[i = key][j = dim] -> lane owns dim column li of tile dt, rows = keys
+  // lane li owns key mykey; register r of tile dt holds dim dt * 32 + d_row(r, g)
+  if (mykey < T) {
+    bf16* krow = dK + base + (long)mykey * HD;
+    bf16* vrow = dV + base + (long)mykey * HD;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kw + d_row(r, g);
-      if (key < T) {
-        dK[base + (long)key * HD + dt * 32 + li] = (bf16)dk[dt][r];
-        dV[base + (long)key * HD + dt * 32 + li] = (bf16)dv[dt][r];
+      for (int rb = 0; rb < 4; ++rb) {
+        bf16x4 a, b;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] = (bf16)dkt[dt][rb * 4 + e];
+          b[e] = (bf16)dvt[dt][rb * 4 + e];
+        }
+        *(bf16x4*)(krow + dt * 32 + 8 * rb + 4 * g) = a;
+        *(bf16x4*)(vrow + dt * 32 + 8 * rb + 4 * g) = b;
       }
-    }
+  }
 }
 
 // ---- dQ -----------------------------------------------------------------------------
+// A workgroup owns 128 queries (32 per wave: Q and dO in registers as B fragments of
+// S^T = K Q^T and dP^T = V dO^T, so a lane owns one query column) and walks 64-key tiles
+// of K and V in a double-buffered LDS ring.  dQ^T += K^T dS^T takes dS^T from the
+// accumulator registers and K^T from the row-major K tile with transposed reads.
 template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                            const bf16* __restrict__ V, const bf16* __restrict__ dO,
@@ -192,15 +223,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
   constexpr int BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   constexpr int RS = HD + 8;
-  constexpr int TS = BN + 4;
-  __shared__ __attribute__((aligned(16))) bf16 sK[BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sV[BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sKt[HD * TS];
+  constexpr int CPR = HD / 8;
+  constexpr int CPT = BN * CPR / 256;
+  static_assert(CPT >= 1 && BN * CPR % 256 == 0, "tile staging");
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * RS];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * RS];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
   const long bh = blockIdx.y;
-  const int qb = CAUSAL ? (gridDim.x - 1 - blockIdx.x) : blockIdx.x;
+  const int qb = CAUSAL ? (gridDim.x - 1 - blockIdx.x) : blockIdx.x;  // heaviest blocks first
   const int q0 = qb * BM;
   const int qw = q0 + 32 * w;
   const int myq = qw + li;
@@ -209,87 +241,104 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
   bf16x8 qf[NKK], of[NKK];
 #pragma unroll
   for (int kk = 0; kk < NKK; ++kk) {
-    if (myq < T) {
-      qf[kk] = *(const bf16x8*)(Q + base + (long)myq * HD + kk * 16 + 8 * g);
-      of[kk] = *(const bf16x8*)(dO + base + (long)myq * HD + kk * 16 + 8 * g);
-    } else {
-      qf[kk] = bf16x8{};
-      of[kk] = bf16x8{};
-    }
+    qf[kk] = myq < T ? *(const bf16x8*)(Q + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
+    of[kk] = myq < T ? *(const bf16x8*)(dO + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
   }
   const float myl = myq < T ? LSE[bh * T + myq] * LOG2E : 0.0f;
   const float myd = myq < T ? Dd[bh * T + myq] : 0.0f;
-  f32x16 dq[NDT];
+  f32x16 dqt[NDT];  // dQ^T: rows = dims, column = this lane's query
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) dq[dt] = zero16();
+  for (int dt = 0; dt < NDT; ++dt) dqt[dt] = zero16();
+
+  bf16x8 rk[CPT], rv[CPT];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
+      const int key = k0 + row;
+      rk[i] = key < T ? *(const bf16x8*)(K + base + (long)key * HD + col) : bf16x8{};
+      rv[i] = key < T ? *(const bf16x8*)(V + base + (long)key * HD + col) : bf16x8{};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
+      *(bf16x8*)(&sK[buf][row * RS + col]) = rk[i];
+      *(bf16x8*)(&sV[buf][row * RS + col]) = rv[i];
+    }
+  };
 
   const int kend = CAUSAL ? min(T, q0 + BM) : T;
-  for (int k0 = 0; k0 < kend; k0 += BN) {
-    __syncthreads();
-    for (int c = tid; c < BN * HD / 8; c += 256) {
-      const int row = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const int key = k0 + row;
-      *(bf16x8*)(sK + row * RS + col) = key < T ? *(const bf16x8*)(K + base + (long)key * HD + col) : bf16x8{};
-      *(bf16x8*)(sV + row * RS + col) = key < T ? *(const bf16x8*)(V + base + (long)key * HD + col) : bf16x8{};
-    }
-    for (int c = tid; c < (BN / 2) * (HD / 8); c += 256) {
-      const int kp = c / (HD / 8), col = (c % (HD / 8)) * 8;
-      const int key = k0 + 2 * kp;
-      const bf16x8 a0 = key < T ? *(const bf16x8*)(K + base + (long)key * HD + col) : bf16x8{};
-      const bf16x8 a1 = key + 1 < T ? *(const bf16x8*)(K + base + (long)(key + 1) * HD + col) : bf16x8{};
+  const int nkt = (kend + BN - 1) / BN;
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);
+  gload(0);
+  sstore(0);
+  if (nkt > 1) gload(BN);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * BN, buf = kt & 1;
+    if (!(CAUSAL && k0 > qw + 31)) {  // some key of the tile is visible to this wave's queries
+      f32x16 s[2], dp[2];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) *(bf16x2*)(sKt + (col + e) * TS + 2 * kp) = bf16x2{a0[e], a1[e]};
-    }
-    __syncthreads();
-    if (CAUSAL && k0 > qw + 31) continue;
-
-    f32x16 s[2], dp[2];
+      for (int h2 = 0; h2 < 2; ++h2) {
+        s[h2] = zero16();
+        dp[h2] = zero16();
 #pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2) {
-      s[h2] = zero16();
-      dp[h2] = zero16();
-#pragma unroll
-      for (int kk = 0; kk < NKK; ++kk) {
-        const bf16x8 ak = *(const bf16x8*)(sK + (h2 * 32 + li) * RS + kk * 16 + 8 * g);
-        const bf16x8 av = *(const bf16x8*)(sV + (h2 * 32 + li) * RS + kk * 16 + 8 * g);
-        s[h2] = mfma32(ak, qf[kk], s[h2]);
-        dp[h2] = mfma32(av, of[kk], dp[h2]);
-      }
-    }
-    const bool mask = (k0 + BN > T) || (myq >= T) || (CAUSAL && k0 + BN - 1 > qw);
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(s[h2][r] * scale_log2 - myl);
-        if (mask) {
-          const int key = k0 + h2 * 32 + d_row(r, g);
-          if (key >= T || myq >= T || (CAUSAL && key > myq)) p = 0.0f;
+        for (int kk = 0; kk < NKK; ++kk) {
+          const bf16x8 ak = *(const bf16x8*)(&sK[buf][(h2 * 32 + li) * RS + kk * 16 + 8 * g]);
+          const bf16x8 av = *(const bf16x8*)(&sV[buf][(h2 * 32 + li) * RS + kk * 16 + 8 * g]);
+          s[h2] = mfma32(ak, qf[kk], s[h2]);
+          dp[h2] = mfma32(av, of[kk], dp[h2]);
         }
-        s[h2][r] = p * (dp[h2][r] - myd) * scale;  // dS^T
       }
-    bf16x8 da[4];
+      const bool mask = (k0 + BN > T) || (myq >= T) || (CAUSAL && k0 + BN - 1 > qw);
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc)
+      for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-      for (int it = 0; it < 8; ++it) da[kc][it] = (bf16)s[kc >> 1][8 * (kc & 1) + it];
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(fmaf(s[h2][r], scale_log2, -myl));
+          if (mask) {
+            const int key = k0 + h2 * 32 + d_row(r, g);
+            if (key >= T || myq >= T || (CAUSAL && key > myq)) p = 0.0f;
+          }
+          s[h2][r] = p * (dp[h2][r] - myd) * scale;  // dS^T
+        }
+      bf16x8 db[4];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const bf16* krow = sKt + (dt * 32 + li) * TS + 4 * g;
+      for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const bf16x8 b = cat4(*(const bf16x4*)(krow + kc * 16), *(const bf16x4*)(krow + kc * 16 + 8));
-        dq[dt] = mfma32(da[kc], b, dq[dt]);
+        for (int e = 0; e < 8; ++e) db[kc][e] = (bf16)s[kc >> 1][8 * (kc & 1) + e];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+          const int off = (16 * kc + kr) * RS + dt * 32 + d0;
+          const bf16x8 a = cat4(lds_read_tr16(&sK[buf][off]), lds_read_tr16(&sK[buf][off + 8 * RS]));
+          dqt[dt] = mfma32(a, db[kc], dqt[dt]);
+        }
       }
     }
+    if (kt + 1 < nkt) {
+      sstore(buf ^ 1);
+      if (kt + 2 < nkt) gload((kt + 2) * BN);
+    }
+    __syncthreads();
   }
+  if (myq < T) {
+    bf16* qrow = dQ + base + (long)myq * HD;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int q = qw + d_row(r, g);
-      if (q < T) dQ[base + (long)q * HD + dt * 32 + li] = (bf16)dq[dt][r];
-    }
+      for (int rb = 0; rb < 4; ++rb) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)dqt[dt][rb * 4 + e];
+        *(bf16x4*)(qrow + dt * 32 + 8 * rb + 4 * g) = v;
+      }
+  }
 }
 
 // ---- generic wave-per-row kernels (float32 / any head_dim) ------------------------
