@@ -87,4 +87,26 @@ EDF_DEVICE bf16x4 lds_read_tr16(const bf16* p) {
   return __builtin_bit_cast(bf16x4, v);
 }
 
+// LDS layout of a row-major bf16 tile with HD columns.  The LDS of gfx950 serves 64
+// four-byte banks per cycle (measured with SQ_LDS_BANK_CONFLICT); MFMA row-operand reads
+// take 16 bytes from each of 16 consecutive rows, transposed reads 8 bytes per lane from
+// 4 consecutive rows x 64 bytes (32 lanes per cycle).  No row padding serves both, so for
+// HD = 128 the rows are unpadded (256 bytes) and the 16-byte chunk c of row r is stored at
+// c ^ h(r), h(r) = 4 (r % 4) + (r / 4) % 4: h is a bijection over any 16 consecutive
+// rows, and 4 consecutive rows x 4 chunks land on 16 distinct chunk slots.  Other head
+// sizes (parity paths) use rows padded by 16 bytes.  col must be a multiple of 4.
+template <int HD>
+EDF_DEVICE int lds_off(int row, int col) {
+  if constexpr (HD == 128) {
+    const int h = ((row & 3) << 2) | ((row >> 2) & 3);
+    return row * 128 + (((col >> 3) ^ h) << 3) + (col & 7);
+  } else {
+    return row * (HD + 8) + col;
+  }
+}
+template <int HD>
+constexpr int lds_tile_elems(int rows) {
+  return HD == 128 ? rows * 128 : rows * (HD + 8);
+}
+
 }  // namespace edf

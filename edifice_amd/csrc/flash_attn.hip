@@ -22,6 +22,8 @@
 #include "edf_common.hpp"
 #include "edf_mfma.hpp"
 
+#include <type_traits>
+
 namespace edf {
 namespace {
 
@@ -32,14 +34,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
                                                              const bf16* __restrict__ V, bf16* __restrict__ O,
                                                              float* __restrict__ LSE, int T, float scale_log2) {
   constexpr int BM = 128, BN = 64;
-  constexpr int KS = HD + 8;   // sK row stride (elements): 16-byte operand reads conflict-free
-  constexpr int VS = HD + 16;  // sV row stride: transposed 8-byte reads conflict-free
   constexpr int NKK = HD / 16, NDT = HD / 32;
   constexpr int CPR = HD / 8;             // 16-byte chunks per row
   constexpr int CPT = BN * CPR / 256;     // chunks per thread per tile (K and V each)
   static_assert(CPT >= 1 && BN * CPR % 256 == 0, "tile staging");
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * VS];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][lds_tile_elems<HD>(BN)];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][lds_tile_elems<HD>(BN)];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -68,17 +68,18 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      const int key = k0 + row;
-      rk[i] = key < T ? *(const bf16x8*)(Kh + (long)key * HD + col) : bf16x8{};
-      rv[i] = key < T ? *(const bf16x8*)(Vh + (long)key * HD + col) : bf16x8{};
+      // rows past the end are clamped, not branched around: their scores are masked
+      const long key = min(k0 + row, T - 1);
+      rk[i] = *(const bf16x8*)(Kh + key * HD + col);
+      rv[i] = *(const bf16x8*)(Vh + key * HD + col);
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      *(bf16x8*)(&sK[buf][row * KS + col]) = rk[i];
-      *(bf16x8*)(&sV[buf][row * VS + col]) = rv[i];
+      *(bf16x8*)(&sK[buf][lds_off<HD>(row, col)]) = rk[i];
+      *(bf16x8*)(&sV[buf][lds_off<HD>(row, col)]) = rv[i];
     }
   };
 
@@ -92,6 +93,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
     const int k0 = kt * BN, buf = kt & 1;
     const bf16* sk = sK[buf];
     const bf16* sv = sV[buf];
+    // Tiles wholly inside the sequence and below the diagonal take the unmasked body;
+    // the rest select -inf per score without branching.
+    auto tile = [&](auto masked) {
+    constexpr bool MASK = decltype(masked)::value;
     // S^T = K Q^T: lane owns query column li, rows are keys
     f32x16 s[2];
 #pragma unroll
@@ -99,19 +104,18 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
       s[h2] = zero16();
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) {
-        const bf16x8 a = *(const bf16x8*)(sk + (h2 * 32 + li) * KS + kk * 16 + 8 * g);
+        const bf16x8 a = *(const bf16x8*)(sk + lds_off<HD>(h2 * 32 + li, kk * 16 + 8 * g));
         s[h2] = mfma32(a, qf[kk], s[h2]);
       }
     }
-    const bool need_mask = (k0 + BN > T) || (CAUSAL && k0 + BN - 1 > qw);
     float mx = -INFINITY;
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        if (need_mask) {
+        if constexpr (MASK) {
           const int key = k0 + h2 * 32 + d_row(r, g);
-          if (key >= T || (CAUSAL && key > myq)) s[h2][r] = -INFINITY;
+          s[h2][r] = (key >= T || (CAUSAL && key > myq)) ? -INFINITY : s[h2][r];
         }
         mx = fmaxf(mx, s[h2][r]);
       }
@@ -160,12 +164,15 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
       for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
-          const bf16* vp = sv + (16 * kc + kr) * VS + dt * 32 + d0;
-          const bf16x8 a = cat4(lds_read_tr16(vp), lds_read_tr16(vp + 8 * VS));
+          const int row = 16 * kc + kr, col = dt * 32 + d0;
+          const bf16x8 a = cat4(lds_read_tr16(sv + lds_off<HD>(row, col)), lds_read_tr16(sv + lds_off<HD>(row + 8, col)));
           o[dt] = mfma32(a, pf[kc], o[dt]);
         }
       }
     }
+    };
+    if ((k0 + BN > T) || (CAUSAL && k0 + BN - 1 > qw)) tile(std::true_type{});
+    else tile(std::false_type{});
     if (kt + 1 < nkt) {
       sstore(buf ^ 1);
       if (kt + 2 < nkt) gload((kt + 2) * BN);

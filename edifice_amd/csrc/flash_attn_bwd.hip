@@ -24,6 +24,8 @@
 #include "edf_common.hpp"
 #include "edf_mfma.hpp"
 
+#include <type_traits>
+
 namespace edf {
 namespace {
 
@@ -60,12 +62,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
                                                              float scale) {
   constexpr int BKEY = 128, BQ = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
-  constexpr int RS = HD + 8;           // row stride: 16-byte row reads conflict-free
   constexpr int CPR = HD / 8;          // 16-byte chunks per row
   constexpr int CPT = BQ * CPR / 256;  // chunks per thread per tile and tensor
   static_assert(CPT >= 1 && BQ * CPR % 256 == 0, "tile staging");
-  __shared__ __attribute__((aligned(16))) bf16 sQ[2][BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sdO[2][BQ * RS];
+  __shared__ __attribute__((aligned(16))) bf16 sQ[2][lds_tile_elems<HD>(BQ)];
+  __shared__ __attribute__((aligned(16))) bf16 sdO[2][lds_tile_elems<HD>(BQ)];
   __shared__ __attribute__((aligned(16))) float sL[2][BQ];
   __shared__ __attribute__((aligned(16))) float sD[2][BQ];
 
@@ -96,22 +97,23 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      const int q = q0 + row;
-      rq[i] = q < T ? *(const bf16x8*)(Q + base + (long)q * HD + col) : bf16x8{};
-      ro[i] = q < T ? *(const bf16x8*)(dO + base + (long)q * HD + col) : bf16x8{};
+      // rows past the end are clamped, not branched around: their P and dS are masked to 0
+      const long q = min(q0 + row, T - 1);
+      rq[i] = *(const bf16x8*)(Q + base + q * HD + col);
+      ro[i] = *(const bf16x8*)(dO + base + q * HD + col);
     }
     if (tid < BQ) {
-      const int q = q0 + tid;
-      rl = q < T ? LSE[bh * T + q] * LOG2E : 0.0f;
-      rd = q < T ? Dd[bh * T + q] : 0.0f;
+      const long q = min(q0 + tid, T - 1);
+      rl = LSE[bh * T + q] * LOG2E;
+      rd = Dd[bh * T + q];
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      *(bf16x8*)(&sQ[buf][row * RS + col]) = rq[i];
-      *(bf16x8*)(&sdO[buf][row * RS + col]) = ro[i];
+      *(bf16x8*)(&sQ[buf][lds_off<HD>(row, col)]) = rq[i];
+      *(bf16x8*)(&sdO[buf][lds_off<HD>(row, col)]) = ro[i];
     }
     if (tid < BQ) {
       sL[buf][tid] = rl;
@@ -136,16 +138,18 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
     for (int sub = 0; sub < BQ / 32; ++sub) {
       const int qs = q0 + 32 * sub;
       if (CAUSAL && qs + 31 < kw) continue;  // every query of the sub-tile precedes this wave's keys
+      auto subtile = [&](auto masked) {
+      constexpr bool MASK = decltype(masked)::value;
       // S = Q K^T and dP = dO V^T (32 queries x 32 keys); lane owns key column
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) {
-        const bf16x8 aq = *(const bf16x8*)(&sQ[buf][(32 * sub + li) * RS + kk * 16 + 8 * g]);
-        const bf16x8 ao = *(const bf16x8*)(&sdO[buf][(32 * sub + li) * RS + kk * 16 + 8 * g]);
+        const int off = lds_off<HD>(32 * sub + li, kk * 16 + 8 * g);
+        const bf16x8 aq = *(const bf16x8*)(&sQ[buf][off]);
+        const bf16x8 ao = *(const bf16x8*)(&sdO[buf][off]);
         s = mfma32(aq, kf[kk], s);
         dp = mfma32(ao, vf[kk], dp);
       }
-      const bool mask = (qs + 32 > T) || (mykey >= T) || (CAUSAL && qs < kw + 31);
 #pragma unroll
       for (int rb = 0; rb < 4; ++rb) {
         const f32x4 lv = *(const f32x4*)(&sL[buf][32 * sub + 8 * rb + 4 * g]);
@@ -154,9 +158,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
         for (int e = 0; e < 4; ++e) {
           const int r = rb * 4 + e;
           float p = fast_exp2(fmaf(s[r], scale_log2, -lv[e]));
-          if (mask) {
+          if constexpr (MASK) {
             const int q = qs + 8 * rb + 4 * g + e;
-            if (q >= T || mykey >= T || (CAUSAL && mykey > q)) p = 0.0f;
+            p = (q >= T || mykey >= T || (CAUSAL && mykey > q)) ? 0.0f : p;
           }
           s[r] = p;
           dp[r] = p * (dp[r] - dv4[e]) * scale;
@@ -175,13 +179,19 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
       for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-          const int off = (32 * sub + 16 * kc + kr) * RS + dt * 32 + d0;
-          const bf16x8 ao = cat4(lds_read_tr16(&sdO[buf][off]), lds_read_tr16(&sdO[buf][off + 8 * RS]));
-          const bf16x8 aq = cat4(lds_read_tr16(&sQ[buf][off]), lds_read_tr16(&sQ[buf][off + 8 * RS]));
+          const int row = 32 * sub + 16 * kc + kr, col = dt * 32 + d0;
+          const int o0 = lds_off<HD>(row, col), o1 = lds_off<HD>(row + 8, col);
+          const bf16x8 ao = cat4(lds_read_tr16(&sdO[buf][o0]), lds_read_tr16(&sdO[buf][o1]));
+          const bf16x8 aq = cat4(lds_read_tr16(&sQ[buf][o0]), lds_read_tr16(&sQ[buf][o1]));
           dvt[dt] = mfma32(ao, pb[kc], dvt[dt]);
           dkt[dt] = mfma32(aq, db[kc], dkt[dt]);
         }
       }
+      };
+      // sub-tiles inside the sequence for every query and key of the wave and wholly
+      // below the diagonal take the unmasked body
+      if ((qs + 32 > T) || (kw + 31 >= T) || (CAUSAL && qs < kw + 31)) subtile(std::true_type{});
+      else subtile(std::false_type{});
     }
     if (it + 1 < ntile) {
       sstore(buf ^ 1);
@@ -222,12 +232,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
                                                            float scale) {
   constexpr int BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
-  constexpr int RS = HD + 8;
   constexpr int CPR = HD / 8;
   constexpr int CPT = BN * CPR / 256;
   static_assert(CPT >= 1 && BN * CPR % 256 == 0, "tile staging");
-  __shared__ __attribute__((aligned(16))) bf16 sK[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][BN * RS];
+  __shared__ __attribute__((aligned(16))) bf16 sK[2][lds_tile_elems<HD>(BN)];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][lds_tile_elems<HD>(BN)];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -255,17 +264,18 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      const int key = k0 + row;
-      rk[i] = key < T ? *(const bf16x8*)(K + base + (long)key * HD + col) : bf16x8{};
-      rv[i] = key < T ? *(const bf16x8*)(V + base + (long)key * HD + col) : bf16x8{};
+      // rows past the end are clamped, not branched around: their P is masked to 0
+      const long key = min(k0 + row, T - 1);
+      rk[i] = *(const bf16x8*)(K + base + key * HD + col);
+      rv[i] = *(const bf16x8*)(V + base + key * HD + col);
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      *(bf16x8*)(&sK[buf][row * RS + col]) = rk[i];
-      *(bf16x8*)(&sV[buf][row * RS + col]) = rv[i];
+      *(bf16x8*)(&sK[buf][lds_off<HD>(row, col)]) = rk[i];
+      *(bf16x8*)(&sV[buf][lds_off<HD>(row, col)]) = rv[i];
     }
   };
 
@@ -280,7 +290,8 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
   __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
     const int k0 = kt * BN, buf = kt & 1;
-    if (!(CAUSAL && k0 > qw + 31)) {  // some key of the tile is visible to this wave's queries
+    auto tile = [&](auto masked) {
+      constexpr bool MASK = decltype(masked)::value;
       f32x16 s[2], dp[2];
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
@@ -288,21 +299,21 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
         dp[h2] = zero16();
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
-          const bf16x8 ak = *(const bf16x8*)(&sK[buf][(h2 * 32 + li) * RS + kk * 16 + 8 * g]);
-          const bf16x8 av = *(const bf16x8*)(&sV[buf][(h2 * 32 + li) * RS + kk * 16 + 8 * g]);
+          const int off = lds_off<HD>(h2 * 32 + li, kk * 16 + 8 * g);
+          const bf16x8 ak = *(const bf16x8*)(&sK[buf][off]);
+          const bf16x8 av = *(const bf16x8*)(&sV[buf][off]);
           s[h2] = mfma32(ak, qf[kk], s[h2]);
           dp[h2] = mfma32(av, of[kk], dp[h2]);
         }
       }
-      const bool mask = (k0 + BN > T) || (myq >= T) || (CAUSAL && k0 + BN - 1 > qw);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float p = fast_exp2(fmaf(s[h2][r], scale_log2, -myl));
-          if (mask) {
+          if constexpr (MASK) {
             const int key = k0 + h2 * 32 + d_row(r, g);
-            if (key >= T || myq >= T || (CAUSAL && key > myq)) p = 0.0f;
+            p = (key >= T || myq >= T || (CAUSAL && key > myq)) ? 0.0f : p;
           }
           s[h2][r] = p * (dp[h2][r] - myd) * scale;  // dS^T
         }
@@ -315,11 +326,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
       for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
-          const int off = (16 * kc + kr) * RS + dt * 32 + d0;
-          const bf16x8 a = cat4(lds_read_tr16(&sK[buf][off]), lds_read_tr16(&sK[buf][off + 8 * RS]));
+          const int row = 16 * kc + kr, col = dt * 32 + d0;
+          const bf16x8 a = cat4(lds_read_tr16(&sK[buf][lds_off<HD>(row, col)]),
+                                lds_read_tr16(&sK[buf][lds_off<HD>(row + 8, col)]));
           dqt[dt] = mfma32(a, db[kc], dqt[dt]);
         }
       }
+    };
+    if (!(CAUSAL && k0 > qw + 31)) {  // some key of the tile is visible to this wave's queries
+      if ((k0 + BN > T) || (qw + 31 >= T) || (CAUSAL && k0 + BN - 1 > qw)) tile(std::true_type{});
+      else tile(std::false_type{});
     }
     if (kt + 1 < nkt) {
       sstore(buf ^ 1);
