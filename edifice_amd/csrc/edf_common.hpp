@@ -79,4 +79,14 @@ EDF_DEVICE int remap_xcd(int id, int total) {
   return (id & 7) * per + (id >> 3);
 }
 
+// For a 2-D grid (x = block within a head, y = head): the (block, head) this workgroup
+// takes, remapped with remap_xcd so that all blocks of a head run on one XCD and share
+// its L2 (the K/V or Q/dO tiles every block of the head streams through).
+EDF_DEVICE void head_block(int& blk, long& head) {
+  const int nx = gridDim.x;
+  const int logical = remap_xcd(blockIdx.x + nx * blockIdx.y, nx * gridDim.y);
+  blk = logical % nx;
+  head = logical / nx;
+}
+
 }  // namespace edf

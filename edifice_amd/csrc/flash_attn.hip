@@ -43,8 +43,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
-  const long bh = blockIdx.y;
-  const int qb = CAUSAL ? (gridDim.x - 1 - blockIdx.x) : blockIdx.x;  // heaviest blocks first
+  int xb;
+  long bh;
+  head_block(xb, bh);
+  const int qb = CAUSAL ? (gridDim.x - 1 - xb) : xb;  // heaviest blocks first
   const int q0 = qb * BM;
   const int qw = q0 + 32 * w;
   const int myq = qw + li;

@@ -72,8 +72,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
-  const long bh = blockIdx.y;
-  const int kb0 = blockIdx.x * BKEY;  // causal: low key blocks see the most queries and run first
+  int xb;
+  long bh;
+  head_block(xb, bh);
+  const int kb0 = xb * BKEY;  // causal: low key blocks see the most queries and run first
   const int kw = kb0 + 32 * w;
   const int mykey = kw + li;
   const long base = bh * T * HD;
@@ -240,8 +242,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
-  const long bh = blockIdx.y;
-  const int qb = CAUSAL ? (gridDim.x - 1 - blockIdx.x) : blockIdx.x;  // heaviest blocks first
+  int xb;
+  long bh;
+  head_block(xb, bh);
+  const int qb = CAUSAL ? (gridDim.x - 1 - xb) : xb;  // heaviest blocks first
   const int q0 = qb * BM;
   const int qw = q0 + 32 * w;
   const int myq = qw + li;
