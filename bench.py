@@ -323,7 +323,8 @@ def main():
     dom_ms = max(ss["bwd_ms"], ss["fwd_ms"])
     dom_bytes = ss["bwd_bytes"] if bwd_dom else ss["fwd_bytes"]
     achieved = dom_bytes / dom_ms / 1e6
-    traffic = profiled_traffic(["ss_bwd_kernel", "ss_reduce_bc_kernel"] if bwd_dom else ["ss_fwd_kernel"])
+    traffic = profiled_traffic(["ss_bwd_kernel", "ss_reduce_bc_kernel", "ss_reduce_ad_kernel"] if bwd_dom
+                               else ["ss_fwd_kernel"])
     line = {
         "metric": "scan HBM GB/s (% of peak); delta-rule & flash-attn fwd+bwd TFLOP/s (% MFMA)",
         "value": round(ss["step_gbs"], 2),
