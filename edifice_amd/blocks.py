@@ -1,0 +1,256 @@
+"""Block-level callers of the fused ops: Edifice's sequence-mixing blocks as torch modules.
+
+Each block wires the projections, gates, normalisations and head reshapes of the
+reference block around one fused HIP op from :mod:`edifice_amd.fused_scan`, so a
+forward and backward through a block runs the HIP kernels for the recurrence and torch
+(rocBLAS / MIOpen) for the dense layers around it:
+
+  MinGRULayer        lib/edifice/recurrent/min_gru.ex:272-295 (pre-norm, gate and candidate
+                     projections, FusedScan.mingru, residual)
+  MambaBlock         lib/edifice/ssm/common.ex:210-279 (norm, in_proj to 2 x inner, x/z split,
+                     causal depthwise conv + SiLU, SSM, SiLU(z) gate, out_proj) with the SSM of
+                     common.ex:333-373 (B/C and low-rank dt projections, softplus) and the dt-mean
+                     discretisation of common.ex:402-471; A = -(1..N) per channel
+  DeltaNetLayer      lib/edifice/recurrent/delta_net.ex:197-219, 275-307 (qkvb projection,
+                     sigmoid beta, key L2 norm with eps inside the sqrt, per-head recurrence)
+  GatedDeltaNetLayer lib/edifice/recurrent/gated_delta_net.ex:230-290, 355-401 (optional short
+                     causal conv, 6 x hidden projection, per-head alpha = mean of sigmoid,
+                     swish output gate)
+  GQABlock           causal grouped-query attention routed to flash attention
+                     (lib/edifice/blocks/sdpa.ex:74-91) + GELU feed-forward
+
+``build(name, **opts)`` mirrors ``Edifice.build(name, opts)`` for these families and returns
+a model mapping [batch, seq, embed] to the last timestep's hidden state, as the reference's
+sequence models do.  Module attributes follow the reference layer names, so
+``load_reference_weights`` reads the reference's own weight files (``weight.<layer>...``
+keys, PyTorch layout) unchanged.
+
+There is no CPU path: the fused ops raise on CPU tensors.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import fused_scan as fs
+
+LN_EPS = 1.0e-5       # layer-norm epsilon the reference fixtures were generated with
+KEY_NORM_EPS = 1.0e-6  # inside the sqrt of the key L2 norm (delta_net.ex:291, gated_delta_net.ex:387)
+
+
+def _causal_depthwise_conv(conv: nn.Conv1d, x: torch.Tensor) -> torch.Tensor:
+    """[B, T, C] -> [B, T, C]: depthwise conv with conv_size - 1 steps of left padding."""
+    seq = x.shape[1]
+    return conv(x.transpose(1, 2))[..., :seq].transpose(1, 2)
+
+
+def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:
+    bsz, seq, hid = t.shape
+    return t.reshape(bsz, seq, num_heads, hid // num_heads).contiguous()
+
+
+def _l2norm_keys(k: torch.Tensor) -> torch.Tensor:
+    return k / torch.sqrt((k * k).sum(-1, keepdim=True) + KEY_NORM_EPS)
+
+
+class MinGRULayer(nn.Module):
+    """min_gru.ex:272-295: x + MinGRU(gate(norm x), candidate(norm x)); the gate's sigmoid
+    and its chain rule run inside the fused kernels."""
+
+    def __init__(self, hidden_size: int):
+        super().__init__()
+        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.gate = nn.Linear(hidden_size, hidden_size)
+        self.candidate = nn.Linear(hidden_size, hidden_size)
+
+    def forward(self, x):
+        n = self.norm(x)
+        return x + fs.mingru(self.gate(n).contiguous(), self.candidate(n).contiguous())
+
+
+class MambaBlock(nn.Module):
+    """common.ex:210-279 (block) around the selective SSM of common.ex:333-471.
+
+    The scan runs the fused kernel in dt-mean mode (the block's CPU semantics) with the
+    SiLU(z) gate fused in; B, C and A are float32 (the reference's parameter precision),
+    x, dt and z keep the model dtype.  Returns the block output without the residual
+    (the model adds it, as Common.build_model does)."""
+
+    def __init__(self, hidden_size: int, state_size: int = 16, expand_factor: int = 2, conv_size: int = 4):
+        super().__init__()
+        inner = hidden_size * expand_factor
+        dt_rank = max(hidden_size // 16, 1)  # common.ex:221
+        self.inner, self.state_size = inner, state_size
+        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.in_proj = nn.Linear(hidden_size, 2 * inner)
+        self.dw_conv = nn.Conv1d(inner, inner, conv_size, padding=conv_size - 1, groups=inner)
+        self.bc_proj = nn.Linear(inner, 2 * state_size)
+        self.dt_rank_proj = nn.Linear(inner, dt_rank)
+        self.dt_proj = nn.Linear(dt_rank, inner)
+        self.out_proj = nn.Linear(inner, hidden_size)
+        a = -(torch.arange(state_size, dtype=torch.float32) + 1.0)
+        self.register_buffer("A", a[None, :].expand(inner, state_size).contiguous(), persistent=False)
+
+    def forward(self, x):
+        xz = self.in_proj(self.norm(x))
+        xb, zb = xz[..., : self.inner], xz[..., self.inner:]
+        xa = F.silu(_causal_depthwise_conv(self.dw_conv, xb))
+        bc = self.bc_proj(xa).float()
+        b, c = bc[..., : self.state_size].contiguous(), bc[..., self.state_size:].contiguous()
+        dt = F.softplus(self.dt_proj(self.dt_rank_proj(xa)))
+        y = fs.selective_scan(xa.contiguous(), dt.contiguous(), self.A.float(), b, c, None, zb.contiguous(),
+                              dt_mode="mean")
+        return self.out_proj(y)
+
+
+class DeltaNetLayer(nn.Module):
+    """delta_net.ex:197-219 and :275-307: x + out_proj(DeltaRule(q, l2norm(k), v, sigmoid(b)))."""
+
+    def __init__(self, hidden_size: int, num_heads: int):
+        super().__init__()
+        self.hidden, self.num_heads = hidden_size, num_heads
+        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.qkvb_proj = nn.Linear(hidden_size, 4 * hidden_size)
+        self.out_proj = nn.Linear(hidden_size, hidden_size)
+
+    def forward(self, x):
+        bsz, seq, hid = x.shape
+        q, k, v, bpre = torch.split(self.qkvb_proj(self.norm(x)), hid, dim=-1)
+        nh = self.num_heads
+        o = fs.delta_net_scan(_heads(q, nh), _l2norm_keys(_heads(k, nh)), _heads(v, nh),
+                              _heads(torch.sigmoid(bpre), nh))
+        return x + self.out_proj(o.reshape(bsz, seq, hid))
+
+
+class GatedDeltaNetLayer(nn.Module):
+    """gated_delta_net.ex:230-290 and :355-401: optional short causal conv (+ SiLU), a
+    6 x hidden projection to q, k, v, beta, alpha, gate; alpha is the head mean of
+    sigmoid(alpha_pre); the output is swish(gate)-gated before out_proj; residual."""
+
+    def __init__(self, hidden_size: int, num_heads: int, use_short_conv: bool = True, conv_size: int = 4):
+        super().__init__()
+        self.hidden, self.num_heads = hidden_size, num_heads
+        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.short_conv = (nn.Conv1d(hidden_size, hidden_size, conv_size, padding=conv_size - 1,
+                                     groups=hidden_size) if use_short_conv else None)
+        self.qkvbag_proj = nn.Linear(hidden_size, 6 * hidden_size)
+        self.out_proj = nn.Linear(hidden_size, hidden_size)
+
+    def forward(self, x):
+        bsz, seq, hid = x.shape
+        h = self.norm(x)
+        if self.short_conv is not None:
+            h = F.silu(_causal_depthwise_conv(self.short_conv, h))
+        q, k, v, bpre, apre, gpre = torch.split(self.qkvbag_proj(h), hid, dim=-1)
+        nh = self.num_heads
+        alpha = _heads(torch.sigmoid(apre), nh).mean(-1).contiguous()
+        o = fs.gated_delta_net_scan(_heads(q, nh), _l2norm_keys(_heads(k, nh)), _heads(v, nh),
+                                    _heads(torch.sigmoid(bpre), nh), alpha)
+        return x + self.out_proj(o.reshape(bsz, seq, hid) * F.silu(gpre))
+
+
+class GQAttention(nn.Module):
+    """Causal grouped-query self-attention on the fused flash kernel; the KV heads are
+    repeated to the query heads before the kernel."""
+
+    def __init__(self, hidden_size: int, num_heads: int, num_kv_heads: int):
+        super().__init__()
+        self.num_heads, self.num_kv_heads = num_heads, num_kv_heads
+        hd = hidden_size // num_heads
+        self.q_proj = nn.Linear(hidden_size, hidden_size)
+        self.k_proj = nn.Linear(hidden_size, num_kv_heads * hd)
+        self.v_proj = nn.Linear(hidden_size, num_kv_heads * hd)
+        self.out_proj = nn.Linear(hidden_size, hidden_size)
+
+    def forward(self, x):
+        bsz, seq, hid = x.shape
+        nh, nkv = self.num_heads, self.num_kv_heads
+        hd = hid // nh
+        q = self.q_proj(x).reshape(bsz, seq, nh, hd).transpose(1, 2).contiguous()
+        k = self.k_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
+        v = self.v_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
+        k = k.repeat_interleave(nh // nkv, dim=1).contiguous()
+        v = v.repeat_interleave(nh // nkv, dim=1).contiguous()
+        o = fs.flash_attention(q, k, v, causal=True)
+        return self.out_proj(o.transpose(1, 2).reshape(bsz, seq, hid))
+
+
+class GQABlock(nn.Module):
+    """Pre-norm transformer block: x + attn(norm x), then + ffn_down(gelu(ffn_up(norm x)))."""
+
+    def __init__(self, hidden_size: int, num_heads: int, num_kv_heads: int, ffn_mult: int = 4):
+        super().__init__()
+        self.attn_norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.attn = GQAttention(hidden_size, num_heads, num_kv_heads)
+        self.ffn_norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.ffn_up = nn.Linear(hidden_size, ffn_mult * hidden_size)
+        self.ffn_down = nn.Linear(ffn_mult * hidden_size, hidden_size)
+
+    def forward(self, x):
+        x = x + self.attn(self.attn_norm(x))
+        return x + self.ffn_down(F.gelu(self.ffn_up(self.ffn_norm(x))))
+
+
+class SequenceModel(nn.Module):
+    """[batch, seq, embed] -> the last timestep's hidden state [batch, hidden]: an optional
+    input projection, a stack of blocks, an optional final layer norm (the shape of the
+    reference's MinGRU / DeltaNet / Mamba / GQA builders)."""
+
+    def __init__(self, blocks_name: str, blocks, input_projection=None, final_norm=None, residual=False):
+        super().__init__()
+        if input_projection is not None:
+            self.input_projection = input_projection
+        setattr(self, blocks_name, nn.ModuleList(blocks))
+        self._blocks_name = blocks_name
+        if final_norm is not None:
+            self.final_norm = final_norm
+        self._residual = residual
+
+    def sequence(self, x):
+        """Hidden states of every timestep, [batch, seq, hidden]."""
+        h = self.input_projection(x) if hasattr(self, "input_projection") else x
+        for blk in getattr(self, self._blocks_name):
+            h = h + blk(h) if self._residual else blk(h)
+        return self.final_norm(h) if hasattr(self, "final_norm") else h
+
+    def forward(self, x):
+        return self.sequence(x)[:, -1]
+
+    def load_reference_weights(self, weights: dict):
+        """Load a reference weight file's ``weight.<layer>.<param>`` tensors (PyTorch layout)."""
+        sd = {k[len("weight."):]: v for k, v in weights.items() if k.startswith("weight.")}
+        ref = self.state_dict()
+        missing = sorted(set(ref) - set(sd))
+        extra = sorted(set(sd) - set(ref))
+        if missing or extra:
+            raise KeyError(f"weight keys do not match the model: missing {missing}, unexpected {extra}")
+        self.load_state_dict({k: v.to(ref[k].dtype) for k, v in sd.items()})
+        return self
+
+
+def build(name: str, *, embed_size: int, hidden_size: int | None = None, num_layers: int = 2,
+          num_heads: int = 4, num_kv_heads: int | None = None, state_size: int = 16, expand_factor: int = 2,
+          conv_size: int = 4, use_short_conv: bool = True) -> SequenceModel:
+    """``Edifice.build(name, opts)`` for the sequence-mixing families on the fused path.
+
+    name: "min_gru", "mamba", "delta_net", "gated_delta_net" or "gqa".  hidden_size defaults
+    to embed_size; an input projection is added when they differ."""
+    hidden = hidden_size or embed_size
+    proj = nn.Linear(embed_size, hidden) if hidden != embed_size else None
+    if name == "min_gru":
+        return SequenceModel("layers", [MinGRULayer(hidden) for _ in range(num_layers)], proj,
+                             nn.LayerNorm(hidden, eps=LN_EPS))
+    if name == "delta_net":
+        return SequenceModel("layers", [DeltaNetLayer(hidden, num_heads) for _ in range(num_layers)], proj,
+                             nn.LayerNorm(hidden, eps=LN_EPS))
+    if name == "gated_delta_net":
+        return SequenceModel("layers", [GatedDeltaNetLayer(hidden, num_heads, use_short_conv, conv_size)
+                                        for _ in range(num_layers)], proj, nn.LayerNorm(hidden, eps=LN_EPS))
+    if name == "mamba":
+        return SequenceModel("blocks", [MambaBlock(hidden, state_size, expand_factor, conv_size)
+                                        for _ in range(num_layers)], proj, None, residual=True)
+    if name == "gqa":
+        return SequenceModel("blocks", [GQABlock(hidden, num_heads, num_kv_heads or num_heads)
+                                        for _ in range(num_layers)], proj, nn.LayerNorm(hidden, eps=LN_EPS))
+    raise ValueError(f"unknown block family {name!r}")

@@ -63,6 +63,60 @@ class _OracleDelta(torch.autograd.Function):
         return _t(g["dq"], q), _t(g["dk"], k), _t(g["dv"], v), _t(g["dbeta"], beta)
 
 
+class _OracleSelectiveScanMean(torch.autograd.Function):
+    """Mean-mode selective scan with the silu(z) gate (the Mamba block's scan), forward and
+    the hand-derived backward of scans.selective_scan_backward."""
+
+    @staticmethod
+    def forward(ctx, x, dt, A, B, C, z):
+        ctx.save_for_backward(x, dt, A, B, C, z)
+        return _t(scans.selective_scan(_np(x), _np(dt), _np(A), _np(B), _np(C), None, _np(z), mode="mean"), x)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, dt, A, B, C, z = ctx.saved_tensors
+        g = scans.selective_scan_backward(_np(x), _np(dt), _np(A), _np(B), _np(C), _np(dy), None, _np(z), mode="mean")
+        return (_t(g["dx"], x), _t(g["ddt"], dt), _t(g["dA"], A), _t(g["dB"], B), _t(g["dC"], C), _t(g["dz"], z))
+
+
+class _OracleCausalAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v):
+        ctx.save_for_backward(q, k, v)
+        return _t(scans.flash_attention(_np(q), _np(k), _np(v), causal=True), q)
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v = ctx.saved_tensors
+        dq, dk, dv = scans.flash_attention_backward(_np(q), _np(k), _np(v), _np(do), causal=True)
+        return _t(dq, q), _t(dk, k), _t(dv, v)
+
+
+class _OracleGatedDelta(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, beta, alpha):
+        ctx.save_for_backward(q, k, v, beta, alpha)
+        return _t(scans.delta_rule(_np(q), _np(k), _np(v), _np(beta), _np(alpha)), q)
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, beta, alpha = ctx.saved_tensors
+        g = scans.delta_rule_backward(_np(q), _np(k), _np(v), _np(beta), _np(do), _np(alpha))
+        return _t(g["dq"], q), _t(g["dk"], k), _t(g["dv"], v), _t(g["dbeta"], beta), _t(g["dalpha"], alpha)
+
+
+def differentiable_oracle_ops():
+    """Every block op as a numpy-oracle autograd Function (forward + hand-derived backward),
+    for gradient checks of whole blocks; the Mamba scan takes the z gate inside."""
+    return {
+        "mingru": _OracleMinGRU.apply,
+        "delta_net": _OracleDelta.apply,
+        "gated_delta_net": _OracleGatedDelta.apply,
+        "selective_scan_mean_gated": _OracleSelectiveScanMean.apply,
+        "causal_attention": _OracleCausalAttention.apply,
+    }
+
+
 def oracle_ops():
     """The numpy oracle as pluggable block ops (forward + hand-derived backward)."""
     return {
@@ -118,6 +172,29 @@ def delta_net_model(w, x, ops, num_heads=4):
     return _ln(w, "weight.final_norm", h)[:, -1]
 
 
+def gated_delta_net_model(w, x, ops, num_heads=4, conv_size=4):
+    """GatedDeltaNet.build with embed == hidden: per layer LN, short causal depthwise conv +
+    SiLU, 6 x hidden projection split into q, k, v, beta, alpha, gate
+    (gated_delta_net.ex:230-290, 355-401); alpha = head mean of sigmoid; swish output gate;
+    residual; final LN; last timestep.  No reference fixture exists for this family."""
+    h = x
+    bsz, seq, hid = x.shape
+    hd = hid // num_heads
+    shp = (bsz, seq, num_heads, hd)
+    for li in range(2):
+        p = f"weight.layers.{li}"
+        n = _ln(w, p + ".norm", h)
+        n = F.silu(F.conv1d(n.transpose(1, 2), w[p + ".short_conv.weight"], w[p + ".short_conv.bias"],
+                            padding=conv_size - 1, groups=hid)[..., :seq].transpose(1, 2))
+        q, k, v, bpre, apre, gpre = torch.split(_dense(w, p + ".qkvbag_proj", n), hid, dim=-1)
+        k = k.reshape(shp)
+        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + scans.KEY_NORM_EPS)
+        alpha = torch.sigmoid(apre).reshape(shp).mean(-1)
+        o = ops["gated_delta_net"](q.reshape(shp), k, v.reshape(shp), torch.sigmoid(bpre).reshape(shp), alpha)
+        h = h + _dense(w, p + ".out_proj", o.reshape(bsz, seq, hid) * F.silu(gpre))
+    return _ln(w, "weight.final_norm", h)[:, -1]
+
+
 def mamba_model(w, x, ops, state_size=8, conv_size=4):
     """Mamba.build/1 via Common.build_model: 2 residual blocks, last timestep (no final LN)."""
     h = x
@@ -136,8 +213,11 @@ def mamba_model(w, x, ops, state_size=8, conv_size=4):
         dt = F.softplus(_dense(w, p + ".dt_proj", _dense(w, p + ".dt_rank_proj", xa)))
         A = -(torch.arange(state_size, dtype=x.dtype, device=x.device) + 1.0)
         A = A[None, :].expand(inner, state_size).contiguous()
-        y = ops["selective_scan_mean"](xa, dt, A, Bm, Cm)
-        h = h + _dense(w, p + ".out_proj", y * F.silu(zb))
+        if "selective_scan_mean_gated" in ops:
+            y = ops["selective_scan_mean_gated"](xa, dt, A, Bm, Cm, zb)
+        else:
+            y = ops["selective_scan_mean"](xa, dt, A, Bm, Cm) * F.silu(zb)
+        h = h + _dense(w, p + ".out_proj", y)
     return h[:, -1]
 
 
