@@ -254,6 +254,36 @@ def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128):
                 shape=dict(B=B, H=H, T=T, d=d, causal=True))
 
 
+def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
+    """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
+    activations, random init, synthetic token ids uniform over the vocabulary; one step = the
+    forward and backward of the next-token loss (no optimizer step, as the metric states)."""
+    from edifice_amd import blocks
+
+    torch.manual_seed(5000)
+    model = blocks.HybridDecoder(vocab, embed).to("cuda", torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(5001)
+    tokens = torch.randint(0, vocab, (B, T + 1), device="cuda", generator=g)
+
+    def step():
+        for p in model.parameters():
+            p.grad = None
+        model.loss(tokens).backward()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record()
+    for _ in range(steps):
+        step()
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / steps
+    return dict(step_ms=ms, tokens_per_s=B * T / ms * 1e3,
+                shape=dict(batch=B, seq=T, vocab=vocab, embed=embed, layers="4 mamba + 2 delta_net + 2 attention"))
+
+
 def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
     """Time the C restatement (oracle/cref.c, OpenMP f32) on the config-2 selective-scan
     workload (about 3 s per fwd+bwd step on 8 host cores); returns GB/s under the same
@@ -317,6 +347,8 @@ def main():
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
+    if want("hybrid"):
+        configs["c5_hybrid_decoder"] = bench_hybrid(torch, max(2, args.steps // 5), 1)
     bwd_dom = ss["bwd_ms"] >= ss["fwd_ms"]
     dominant = ("edf_fused_selective_scan_backward (ss_bwd_kernel + dB/dC, dA/dD reductions)" if bwd_dom
                 else "edf_fused_selective_scan (ss_fwd_kernel)")

@@ -254,3 +254,36 @@ def build(name: str, *, embed_size: int, hidden_size: int | None = None, num_lay
         return SequenceModel("blocks", [GQABlock(hidden, num_heads, num_kv_heads or num_heads)
                                         for _ in range(num_layers)], proj, nn.LayerNorm(hidden, eps=LN_EPS))
     raise ValueError(f"unknown block family {name!r}")
+
+
+class HybridDecoder(nn.Module):
+    """Decoder stack mixing the three fused paths (the hybrid of the benchmark's config 5):
+    token embedding -> Mamba blocks (residual) -> DeltaNet layers -> causal attention + FFN
+    blocks -> final layer norm -> LM head, with a next-token cross-entropy ``loss``."""
+
+    def __init__(self, vocab_size: int = 32000, embed_size: int = 1024, mamba_layers: int = 4,
+                 delta_layers: int = 2, attn_layers: int = 2, num_heads: int = 8, state_size: int = 16,
+                 expand_factor: int = 2, conv_size: int = 4):
+        super().__init__()
+        self.embed = nn.Embedding(vocab_size, embed_size)
+        self.mamba = nn.ModuleList(MambaBlock(embed_size, state_size, expand_factor, conv_size)
+                                   for _ in range(mamba_layers))
+        self.delta = nn.ModuleList(DeltaNetLayer(embed_size, num_heads) for _ in range(delta_layers))
+        self.attn = nn.ModuleList(GQABlock(embed_size, num_heads, num_heads) for _ in range(attn_layers))
+        self.final_norm = nn.LayerNorm(embed_size, eps=LN_EPS)
+        self.lm_head = nn.Linear(embed_size, vocab_size, bias=False)
+
+    def forward(self, tokens: torch.Tensor) -> torch.Tensor:
+        h = self.embed(tokens)
+        for blk in self.mamba:
+            h = h + blk(h)
+        for blk in self.delta:
+            h = blk(h)
+        for blk in self.attn:
+            h = blk(h)
+        return self.lm_head(self.final_norm(h))
+
+    def loss(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Mean next-token cross entropy over tokens[:, 1:] (logits reduced in float32)."""
+        logits = self.forward(tokens[:, :-1])
+        return F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1))
