@@ -35,6 +35,43 @@ template <typename T> EDF_DEVICE float ld_or0(const T* p, long i, bool ok, long 
   return ok ? v : 0.0f;
 }
 
+// ---- raw buffer access ---------------------------------------------------------
+// A raw buffer resource (V#) over [base, base + bytes), bytes < 2^31.  The hardware
+// range-checks every access against it: a load at an offset >= bytes returns 0 and a
+// store there is dropped, so kernels address padding lanes and steps with OOB_OFF
+// instead of branching around the access.  The SGPR base plus a 32-bit VGPR offset
+// also keeps 64-bit address arithmetic out of the vector registers.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr unsigned OOB_OFF = 0x80000000u;
+constexpr int BUF_DWORD3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
+EDF_DEVICE rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, BUF_DWORD3);
+}
+
+// storage-type bits of one element (T = float or bf16) and their conversions
+template <typename T> struct Bits;
+template <> struct Bits<float> { typedef unsigned type; };
+template <> struct Bits<bf16> { typedef unsigned short type; };
+
+template <typename T> EDF_DEVICE typename Bits<T>::type bload(rsrc_t r, unsigned off);
+template <> EDF_DEVICE unsigned bload<float>(rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+template <> EDF_DEVICE unsigned short bload<bf16>(rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+EDF_DEVICE float bits_f32(unsigned v) { return __builtin_bit_cast(float, v); }
+EDF_DEVICE float bits_f32(unsigned short v) { return __builtin_bit_cast(float, (unsigned)v << 16); }
+
+template <typename T> EDF_DEVICE void bstore(rsrc_t r, unsigned off, float v);
+template <> EDF_DEVICE void bstore<float>(rsrc_t r, unsigned off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)off, 0, 0);
+}
+template <> EDF_DEVICE void bstore<bf16>(rsrc_t r, unsigned off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)v), r, (int)off, 0, 0);
+}
+
 // ---- math -------------------------------------------------------------------
 constexpr float LOG2E = 1.4426950408889634f;
 

@@ -20,7 +20,11 @@
 //     (A, B) in LDS, and after one barrier composes the maps of the earlier waves
 //     with the carry of the previous macro-step (a carry-propagating scan over W
 //     waves; no second read of the inputs);
-//   * backward runs the same scan in reverse time on u_t = a_t (g_t + u_{t+1}).
+//   * backward runs the same scan in reverse time on u_t = a_t (g_t + u_{t+1});
+//   * the raw inputs of the next macro-step are loaded into a register ring while the
+//     current one is composed and stored; every global access is a raw buffer access
+//     whose out-of-range offsets (padding steps, channels past hid) the hardware turns
+//     into zero loads and dropped stores, so the steady-state loop has no branch.
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
@@ -28,6 +32,11 @@ namespace edf {
 namespace {
 
 constexpr float MINLSTM_EPS = 1.0e-6f;
+// Long-sequence geometry (16 waves per workgroup), measured on MI355X at 8x2048x1536:
+// timesteps per wave per macro-step (L) and register-ring depth in macro-steps (P).
+// Deeper rings (P = 3, 4) were slower for both directions.
+constexpr int LIN_LF = 8, LIN_PF = 2;  // forward
+constexpr int LIN_LB = 4, LIN_PB = 2;  // backward (five inputs per step)
 
 enum { OP_MINGRU = 0, OP_MINLSTM = 1 };
 
@@ -50,157 +59,229 @@ struct Step {
   }
 };
 
-template <typename T, int OP, bool LOGITS, int L, int W>
+// Raw inputs of P macro-steps are kept in a register ring: the slot of macro-step ms is
+// refilled with macro-step ms + P as soon as its values are consumed, so P - 1 macro-steps
+// of loads are in flight while the barrier, the composition and the stores of the current
+// one run.  All global accesses are raw buffer accesses (per-batch resources): steps past
+// the sequence and channels past hid use an out-of-range offset, so the loads return 0 and
+// the stores are dropped by the hardware, and the loop body has no branch around a memory
+// access (which would make the compiler drain the whole ring at the loop head).  The
+// macro-step count is padded to a multiple of P with such empty steps.
+template <typename T, int OP, bool LOGITS, int L, int W, int P>
 __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
                                                              const T* __restrict__ cand, const T* __restrict__ h0,
                                                              T* __restrict__ out, int seq, int hid) {
+  typedef typename Bits<T>::type RB;
+  constexpr unsigned ES = sizeof(T);
   __shared__ float sA[2][W][64];
   __shared__ float sB[2][W][64];
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int b = blockIdx.y;
   const int c = blockIdx.x * 64 + lane;
   const bool valid = c < hid;
-  const long base = (long)b * seq * hid + min(c, hid - 1);  // loads stay in bounds; stores are guarded
+  const long slab = (long)b * seq * hid;
+  const unsigned bytes = (unsigned)((long)seq * hid * ES);
+  const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
+  const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
+  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RO = make_rsrc(out + slab, bytes);
+  auto off = [&](int t) -> unsigned {
+    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
+  };
+
+  RB r1[P][L], r2[P][L], rc[P][L];
+  auto fetch = [&](int slot, int ms) {
+    const int t0 = (ms * W + w) * L;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const unsigned o = off(t0 + j);
+      r1[slot][j] = bload<T>(R1, o);
+      if (OP == OP_MINLSTM) r2[slot][j] = bload<T>(R2, o);
+      rc[slot][j] = bload<T>(RC, o);
+    }
+  };
 
   float h = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c) : 0.0f;
   const int steps = (seq + W * L - 1) / (W * L);
-  for (int ms = 0; ms < steps; ++ms) {
-    const int t0 = ms * W * L + w * L;
-    float a[L], bb[L];
+  const int npad = (steps + P - 1) / P * P;
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      const int t = t0 + j;
-      const long idx = base + (long)min(t, seq - 1) * hid;
-      Step<OP, LOGITS> s;
-      s.make(ld(g1, idx), OP == OP_MINLSTM ? ld(g2, idx) : 0.0f, ld(cand, idx));
-      const bool ok = valid && t < seq;  // padding steps are the identity map
-      a[j] = ok ? s.a : 1.0f;
-      bb[j] = ok ? s.b : 0.0f;
-    }
-    float A = 1.0f, B = 0.0f;
+  for (int j = 0; j < P; ++j) fetch(j, j);
+  for (int ms0 = 0; ms0 < npad; ms0 += P) {
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      B = fmaf(a[j], B, bb[j]);
-      A *= a[j];
-    }
-    const int buf = ms & 1;
-    sA[buf][w][lane] = A;
-    sB[buf][w][lane] = B;
-    __syncthreads();
-    float hin = h;
-    for (int v = 0; v < w; ++v) hin = fmaf(sA[buf][v][lane], hin, sB[buf][v][lane]);
-    float hend = fmaf(A, hin, B);
-    for (int v = w + 1; v < W; ++v) hend = fmaf(sA[buf][v][lane], hend, sB[buf][v][lane]);
-    float hh = hin;
+    for (int u = 0; u < P; ++u) {
+      const int ms = ms0 + u;
+      const int t0 = (ms * W + w) * L;
+      float a[L], bb[L];
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      hh = fmaf(a[j], hh, bb[j]);
-      const int t = t0 + j;
-      if (valid && t < seq) st(out, base + (long)t * hid, hh);
+      for (int j = 0; j < L; ++j) {
+        Step<OP, LOGITS> s;
+        s.make(bits_f32(r1[u][j]), OP == OP_MINLSTM ? bits_f32(r2[u][j]) : 0.0f, bits_f32(rc[u][j]));
+        const bool ok = valid && t0 + j < seq;  // padding steps are the identity map
+        a[j] = ok ? s.a : 1.0f;
+        bb[j] = ok ? s.b : 0.0f;
+      }
+      fetch(u, ms + P);
+      float A = 1.0f, B = 0.0f;
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        B = fmaf(a[j], B, bb[j]);
+        A *= a[j];
+      }
+      const int buf = ms & 1;
+      sA[buf][w][lane] = A;
+      sB[buf][w][lane] = B;
+      __syncthreads();
+      // compose the W wave maps in time order (all 2W LDS reads issued together; a loop
+      // over the preceding waves only is a chain of dependent reads and measured slower);
+      // this wave starts from the prefix before it
+      float x = h, hh = h;
+#pragma unroll
+      for (int v = 0; v < W; ++v) {
+        if (v == w) hh = x;
+        x = fmaf(sA[buf][v][lane], x, sB[buf][v][lane]);
+      }
+      h = x;
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        hh = fmaf(a[j], hh, bb[j]);
+        bstore<T>(RO, off(t0 + j), hh);
+      }
     }
-    h = hend;
   }
 }
 
 // Backward: reverse scan u_t = a_t (g_t + u_{t+1}), dh_t = g_t + u_{t+1}, dh0 = u_0.
-template <typename T, int OP, bool LOGITS, int L, int W>
+// Same register ring and buffer addressing as the forward, walking macro-steps from the
+// end of the (padded) sequence.
+template <typename T, int OP, bool LOGITS, int L, int W, int P>
 __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
                                                              const T* __restrict__ cand, const T* __restrict__ h0,
                                                              const T* __restrict__ fwd, const T* __restrict__ dy,
                                                              T* __restrict__ d1, T* __restrict__ d2,
                                                              T* __restrict__ dcand, T* __restrict__ dh0, int seq,
                                                              int hid) {
+  typedef typename Bits<T>::type RB;
+  constexpr unsigned ES = sizeof(T);
   __shared__ float sA[2][W][64];
   __shared__ float sB[2][W][64];
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int b = blockIdx.y;
   const int c = blockIdx.x * 64 + lane;
   const bool valid = c < hid;
-  const long base = (long)b * seq * hid + min(c, hid - 1);  // loads stay in bounds; stores are guarded
+  const long slab = (long)b * seq * hid;
+  const unsigned bytes = (unsigned)((long)seq * hid * ES);
+  const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
+  const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
+  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RH = make_rsrc(fwd + slab, bytes);
+  const rsrc_t RY = make_rsrc(dy + slab, bytes);
+  const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
+  const rsrc_t W2 = make_rsrc((OP == OP_MINLSTM ? d2 : d1) + slab, bytes);
+  const rsrc_t WC = make_rsrc(dcand + slab, bytes);
+  auto off = [&](int t) -> unsigned {
+    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
+  };
+  // h_{t-1}: the forward output one row up; t = 0 reads out of range (0) and takes h0
+  auto offp = [&](int t) -> unsigned {
+    return (valid && t < seq && t > 0) ? ((unsigned)(t - 1) * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
+  };
   const float h0v = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c) : 0.0f;
 
-  float u = 0.0f;  // u_{t+1} entering the macro-step from the right
   const int steps = (seq + W * L - 1) / (W * L);
-  const int tpad = steps * W * L;
-  for (int ms = 0; ms < steps; ++ms) {
-    // wave 0 owns the latest L timesteps of this macro-step
-    const int t0 = tpad - (ms + 1) * W * L + (W - 1 - w) * L;
-    float x1[L], x2[L], cc[L], hp[L], gy[L];
+  const int npad = (steps + P - 1) / P * P;
+  const int tpad = npad * W * L;
+  // wave 0 owns the latest L timesteps of each macro-step
+  auto first_t = [&](int ms) { return tpad - (ms + 1) * W * L + (W - 1 - w) * L; };
+  RB r1[P][L], r2[P][L], rc[P][L], rh[P][L], ry[P][L];
+  auto fetch = [&](int slot, int ms) {
+    const int t0 = first_t(ms);
 #pragma unroll
     for (int j = 0; j < L; ++j) {
-      const int t = t0 + j;
-      const bool ok = valid && t < seq;
-      const long idx = base + (long)min(t, seq - 1) * hid;
-      const long pidx = base + (long)max(min(t, seq - 1) - 1, 0) * hid;
-      const float v1 = ld(g1, idx);
-      const float v2 = OP == OP_MINLSTM ? ld(g2, idx) : 0.0f;
-      const float vc = ld(cand, idx);
-      const float vh = ld(fwd, pidx);
-      const float vy = ld(dy, idx);
-      x1[j] = ok ? v1 : 0.0f;
-      x2[j] = ok ? v2 : 0.0f;
-      cc[j] = ok ? vc : 0.0f;
-      hp[j] = ok ? (t > 0 ? vh : h0v) : 0.0f;
-      gy[j] = ok ? vy : 0.0f;
+      const unsigned o = off(t0 + j);
+      r1[slot][j] = bload<T>(R1, o);
+      if (OP == OP_MINLSTM) r2[slot][j] = bload<T>(R2, o);
+      rc[slot][j] = bload<T>(RC, o);
+      rh[slot][j] = bload<T>(RH, offp(t0 + j));
+      ry[slot][j] = bload<T>(RY, o);
     }
-    // per-step decay a_t (1 for padding)
-    float a[L];
+  };
+
+  float u = 0.0f;  // u_{t+1} entering the macro-step from the right
 #pragma unroll
-    for (int j = 0; j < L; ++j) {
-      const int t = t0 + j;
-      Step<OP, LOGITS> s;
-      s.make(x1[j], x2[j], cc[j]);
-      a[j] = (valid && t < seq) ? s.a : 1.0f;
-    }
-    float A = 1.0f, B = 0.0f;
+  for (int j = 0; j < P; ++j) fetch(j, j);
+  for (int ms0 = 0; ms0 < npad; ms0 += P) {
 #pragma unroll
-    for (int j = L - 1; j >= 0; --j) {
-      B = a[j] * (gy[j] + B);
-      A *= a[j];
-    }
-    const int buf = ms & 1;
-    sA[buf][w][lane] = A;
-    sB[buf][w][lane] = B;
-    __syncthreads();
-    float uin = u;
-    for (int v = 0; v < w; ++v) uin = fmaf(sA[buf][v][lane], uin, sB[buf][v][lane]);
-    float uend = fmaf(A, uin, B);
-    for (int v = w + 1; v < W; ++v) uend = fmaf(sA[buf][v][lane], uend, sB[buf][v][lane]);
+    for (int sl = 0; sl < P; ++sl) {
+      const int ms = ms0 + sl;
+      const int t0 = first_t(ms);
+      // Per step only the decay a, the input gradient g and the coefficients that map
+      // dh_t to each output gradient are kept; the ring slot is refilled right after.
+      //   MinGRU:  dz = dh (c - h_{t-1}) [z (1 - z)],  dc = dh z
+      //   MinLSTM: df = dh (h_{t-1} (i + eps) - c i) / s^2 [f (1 - f)],
+      //            di = dh (c (f + eps) - h_{t-1} f) / s^2 [i (1 - i)],  dc = dh i / s
+      float a[L], gy[L], k1[L], k2[L], kc[L];
 #pragma unroll
-    for (int j = L - 1; j >= 0; --j) {
-      const int t = t0 + j;
-      const float dh = gy[j] + uin;
-      uin = a[j] * dh;
-      if (!(valid && t < seq)) continue;
-      const long idx = base + (long)t * hid;
-      if (OP == OP_MINGRU) {
-        const float z = LOGITS ? sigmoidf(x1[j]) : x1[j];
-        float dz = dh * (cc[j] - hp[j]);
-        if (LOGITS) dz *= z * (1.0f - z);
-        st(d1, idx, dz);
-        st(dcand, idx, dh * z);
-      } else {
-        const float f = LOGITS ? sigmoidf(x1[j]) : x1[j];
-        const float i = LOGITS ? sigmoidf(x2[j]) : x2[j];
-        const float s = f + (i + MINLSTM_EPS);
-        const float r = 1.0f / s;
-        const float dfn = dh * hp[j];
-        const float din = dh * cc[j];
-        const float r2 = r * r;
-        float df = (dfn * (i + MINLSTM_EPS) - din * i) * r2;
-        float di = (din * (f + MINLSTM_EPS) - dfn * f) * r2;
-        if (LOGITS) {
-          df *= f * (1.0f - f);
-          di *= i * (1.0f - i);
+      for (int j = 0; j < L; ++j) {
+        const int t = t0 + j;
+        const bool ok = valid && t < seq;
+        const float x1 = bits_f32(r1[sl][j]);
+        const float x2 = OP == OP_MINLSTM ? bits_f32(r2[sl][j]) : 0.0f;
+        const float cv = bits_f32(rc[sl][j]);
+        const float hp = t > 0 ? bits_f32(rh[sl][j]) : h0v;
+        gy[j] = bits_f32(ry[sl][j]);  // 0 outside the sequence
+        if (OP == OP_MINGRU) {
+          const float z = LOGITS ? sigmoidf(x1) : x1;
+          a[j] = ok ? 1.0f - z : 1.0f;  // padding steps are the identity map
+          k1[j] = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
+          k2[j] = 0.0f;
+          kc[j] = z;
+        } else {
+          const float f = LOGITS ? sigmoidf(x1) : x1;
+          const float i = LOGITS ? sigmoidf(x2) : x2;
+          const float r = 1.0f / (f + (i + MINLSTM_EPS));
+          const float r2 = r * r;
+          a[j] = ok ? f * r : 1.0f;
+          float c1 = (hp * (i + MINLSTM_EPS) - cv * i) * r2;
+          float c2 = (cv * (f + MINLSTM_EPS) - hp * f) * r2;
+          if (LOGITS) {
+            c1 *= f * (1.0f - f);
+            c2 *= i * (1.0f - i);
+          }
+          k1[j] = c1;
+          k2[j] = c2;
+          kc[j] = i * r;
         }
-        st(d1, idx, df);
-        st(d2, idx, di);
-        st(dcand, idx, dh * (i * r));
+      }
+      fetch(sl, ms + P);
+      float A = 1.0f, B = 0.0f;
+#pragma unroll
+      for (int j = L - 1; j >= 0; --j) {
+        B = a[j] * (gy[j] + B);
+        A *= a[j];
+      }
+      const int buf = ms & 1;
+      sA[buf][w][lane] = A;
+      sB[buf][w][lane] = B;
+      __syncthreads();
+      float x = u, uin = u;
+#pragma unroll
+      for (int v = 0; v < W; ++v) {
+        if (v == w) uin = x;
+        x = fmaf(sA[buf][v][lane], x, sB[buf][v][lane]);
+      }
+      u = x;
+#pragma unroll
+      for (int j = L - 1; j >= 0; --j) {
+        const unsigned o = off(t0 + j);
+        const float dh = gy[j] + uin;
+        uin = a[j] * dh;
+        bstore<T>(W1, o, dh * k1[j]);
+        if (OP == OP_MINLSTM) bstore<T>(W2, o, dh * k2[j]);
+        bstore<T>(WC, o, dh * kc[j]);
       }
     }
-    u = uend;
   }
   if (valid && w == 0 && dh0 != nullptr) st(dh0, (long)b * hid + c, u);
 }
@@ -208,15 +289,15 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
 template <typename T, int OP, bool LOGITS>
 int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, const void* h0, void* out, int bsz,
                int seq, int hid) {
-  constexpr int L = 8;
+  constexpr int L = LIN_LF;
   const dim3 grid((hid + 63) / 64, bsz);
   if (seq >= 512) {
     constexpr int W = 16;
-    linscan_fwd_kernel<T, OP, LOGITS, L, W><<<grid, 64 * W, 0, s>>>((const T*)g1, (const T*)g2, (const T*)cand,
+    linscan_fwd_kernel<T, OP, LOGITS, L, W, LIN_PF><<<grid, 64 * W, 0, s>>>((const T*)g1, (const T*)g2, (const T*)cand,
                                                                     (const T*)h0, (T*)out, seq, hid);
   } else {
     constexpr int W = 4;
-    linscan_fwd_kernel<T, OP, LOGITS, L, W><<<grid, 64 * W, 0, s>>>((const T*)g1, (const T*)g2, (const T*)cand,
+    linscan_fwd_kernel<T, OP, LOGITS, L, W, 2><<<grid, 64 * W, 0, s>>>((const T*)g1, (const T*)g2, (const T*)cand,
                                                                     (const T*)h0, (T*)out, seq, hid);
   }
   return check_launch(OP == OP_MINGRU ? "mingru scan" : "minlstm scan");
@@ -225,16 +306,16 @@ int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
 template <typename T, int OP, bool LOGITS>
 int launch_bwd(hipStream_t s, const void* g1, const void* g2, const void* cand, const void* h0, const void* fwd,
                const void* dy, void* d1, void* d2, void* dcand, void* dh0, int bsz, int seq, int hid) {
-  constexpr int L = 8;
+  constexpr int L = LIN_LB;
   const dim3 grid((hid + 63) / 64, bsz);
   if (seq >= 512) {
     constexpr int W = 16;
-    linscan_bwd_kernel<T, OP, LOGITS, L, W><<<grid, 64 * W, 0, s>>>(
+    linscan_bwd_kernel<T, OP, LOGITS, L, W, LIN_PB><<<grid, 64 * W, 0, s>>>(
         (const T*)g1, (const T*)g2, (const T*)cand, (const T*)h0, (const T*)fwd, (const T*)dy, (T*)d1, (T*)d2,
         (T*)dcand, (T*)dh0, seq, hid);
   } else {
     constexpr int W = 4;
-    linscan_bwd_kernel<T, OP, LOGITS, L, W><<<grid, 64 * W, 0, s>>>(
+    linscan_bwd_kernel<T, OP, LOGITS, L, W, 2><<<grid, 64 * W, 0, s>>>(
         (const T*)g1, (const T*)g2, (const T*)cand, (const T*)h0, (const T*)fwd, (const T*)dy, (T*)d1, (T*)d2,
         (T*)dcand, (T*)dh0, seq, hid);
   }
@@ -245,6 +326,8 @@ template <int OP, bool LOGITS>
 int fwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand, const void* h0, void* out, int bsz,
                  int seq, int hid, int dtype) {
   EDF_REQUIRE(bsz > 0 && seq > 0 && hid > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
+  EDF_REQUIRE((long)seq * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row must stay below 2 GiB)");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(g1 && cand && out && (OP == OP_MINGRU || g2), EDF_ERR_INVALID_ARG, "null tensor pointer");
   if (dtype == EDF_BF16) return launch_fwd<bf16, OP, LOGITS>(as_stream(stream), g1, g2, cand, h0, out, bsz, seq, hid);
@@ -255,6 +338,8 @@ template <int OP, bool LOGITS>
 int bwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand, const void* h0, const void* fwd,
                  const void* dy, void* d1, void* d2, void* dcand, void* dh0, int bsz, int seq, int hid, int dtype) {
   EDF_REQUIRE(bsz > 0 && seq > 0 && hid > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
+  EDF_REQUIRE((long)seq * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row must stay below 2 GiB)");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(g1 && cand && fwd && dy && d1 && dcand && (OP == OP_MINGRU || (g2 && d2)), EDF_ERR_INVALID_ARG,
               "null tensor pointer");
