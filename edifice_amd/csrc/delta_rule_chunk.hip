@@ -373,7 +373,10 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
       *(bf16x8*)(sa + row * KS + col) = a;
     }
     const float gC = __expf(P.lgC);
-    if (it + 2 < p.nch) fetch_a1(P, chunk_of(it + 2));
+    // Prefetches are unconditional (past the last chunk they reload it): a conditional
+    // one makes the compiler copy the loaded registers at the loop latch behind a full
+    // vmcnt(0) drain, which serialises every step on an HBM round trip.
+    fetch_a1(P, chunk_of(min(it + 2, p.nch - 1)));
     __syncthreads();
 
     // X = A1 * state: rows t (two tiles), column d_v
@@ -411,12 +414,16 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       S[r] = REV ? fmaf(gC, S[r], (float)P.y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
-    if (it + 2 < p.nch) fetch_rest(P, chunk_of(it + 2));
+    fetch_rest(P, chunk_of(min(it + 2, p.nch - 1)));
   };
-  for (int it = 0; it < p.nch; it += 2) {
+  // both bodies of the unrolled pair run unconditionally inside the loop (an odd last
+  // chunk is peeled), for the same reason as the unconditional prefetches
+  int it = 0;
+  for (; it + 1 < p.nch; it += 2) {
     body(it, pre0);
-    if (it + 1 < p.nch) body(it + 1, pre1);
+    body(it + 1, pre1);
   }
+  if (it < p.nch) body(it, pre0);
 }
 
 // ---------------------------------------------------------------------------

@@ -194,18 +194,21 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
   // blk & 1 and from its B/C values in slot blk % PD; then block blk + 1 is staged into
   // the other LDS buffer and block blk + PD is fetched into slot blk % PD, which block
   // blk no longer needs.
+  // Every fetch and stage is unconditional (block indices clamped to the last block, and
+  // the block count padded to a multiple of PD with empty blocks whose staged dt is 0,
+  // i.e. identity steps): a conditional refill makes the compiler drain the whole ring
+  // (vmcnt(0)) at the loop head.  Only stores are guarded.
   const int nblk = (seq + TS - 1) / TS;
+  const int npad = (nblk + PD - 1) / PD * PD;
 #pragma unroll
-  for (int j = 0; j < PD; ++j)
-    if (j < nblk) fetch(j, j * TS);
+  for (int j = 0; j < PD; ++j) fetch(j, min(j, nblk - 1) * TS);
   stage(0, 0, 0, cx, cz);
   __syncthreads();
 
-  for (int blk0 = 0; blk0 < nblk; blk0 += PD) {
+  for (int blk0 = 0; blk0 < npad; blk0 += PD) {
 #pragma unroll
     for (int u = 0; u < PD; ++u) {
       const int blk = blk0 + u;
-      if (blk >= nblk) break;
       const int t0 = blk * TS, buf = u & 1;  // PD is even, so u & 1 == blk & 1
       // ---- recurrence over the block ----
       const float* bcr = rbc[u];  // this block's B/C values (slot blk % PD == u)
@@ -223,18 +226,20 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
             constexpr int vb = tt * K + s, vc = vb + TS * K;  // B and C value indices
             const float a = fast_exp2(dcv[v] * A2[s]);
             h[s] = fmaf(a, h[s], row_bcast<vb % 16>(bcr[vb / 16]) * dxv[v]);
-            if (WRITE_Y) acc += row_bcast<vc % 16>(bcr[vc / 16]) * h[s];
+            // the first state's C h is a DPP-folded multiply, not a broadcast + fma with 0
+            if (WRITE_Y) acc = s == 0 ? row_bcast<vc % 16>(bcr[vc / 16]) * h[s]
+                                      : fmaf(row_bcast<vc % 16>(bcr[vc / 16]), h[s], acc);
           });
           if (WRITE_Y) s_yp[buf][w][tt][lane] = acc;
         });
       });
-      if (p.ckpt != nullptr && cvalid) {
+      if (p.ckpt != nullptr && cvalid && blk < nblk) {
         float* ck = p.ckpt + (((long)b * p.nck + blk) * N + w * K) * dim + c;
 #pragma unroll
         for (int s = 0; s < K; ++s) ck[(long)s * dim] = h[s];
       }
-      if (blk + 1 < nblk) stage((u + 1) % PD, t0 + TS, buf ^ 1, nx, nz);
-      if (blk + PD < nblk) fetch(u, t0 + PD * TS);
+      stage((u + 1) % PD, t0 + TS, buf ^ 1, nx, nz);
+      fetch(u, min(blk + PD, nblk - 1) * TS);
       __syncthreads();
       // ---- y for the (t, d) this thread staged: sum the wave partials, D skip, gate ----
       if (WRITE_Y) {
@@ -320,6 +325,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   TI rx[EPT], rdt[EPT], rdo[EPT], rz[EPT];
   TP rbc[BCT];
   float rm[EPT];
+  float rck[K];  // the checkpoint the fetched chunk starts from (its predecessor's state)
   // this thread's staged (t, d) values, kept for the per-(t, d) epilogues
   float ex[EPT], edtb[EPT], emask[EPT], edy[EPT], ego[EPT], ez[EPT];
   auto fetch = [&](int ts) {
@@ -340,8 +346,14 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
       const long row = (long)b * seq + min(ts + e / (2 * N), seq - 1);
       rbc[i] = (r < N ? Bm : Cm)[row * N + (r % N)];
     }
+    const int kp = max(ts / CK - 1, 0);  // chunk 0 starts from zero (selected at use)
+#pragma unroll
+    for (int s = 0; s < K; ++s) rck[s] = p.ckpt[(((long)b * p.nck + kp) * N + w * K + s) * dim + cc];
   };
 
+  // The next chunk's inputs and checkpoint are fetched one chunk ahead, unconditionally
+  // (chunk 0 fetches itself again): a conditional fetch makes the compiler drain every
+  // outstanding load at the loop latch.
   fetch((p.nck - 1) * CK);
   for (int k = p.nck - 1; k >= 0; --k) {
     const int ts = k * CK;
@@ -371,7 +383,10 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         s_dy[lane][tt] = ego[i];
       }
     }
-    if (k > 0) fetch((k - 1) * CK);
+    float ck0[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) ck0[s] = rck[s];
+    fetch(max(k - 1, 0) * CK);
     __syncthreads();
 
     // ---- recompute the chunk's states and decays from its checkpoint ---------------
@@ -380,7 +395,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
     float h0[K], hs[CK][K], as[CK][K], bB[CK][K], bC[CK][K];
 #pragma unroll
     for (int s = 0; s < K; ++s)
-      h0[s] = (k > 0 && cvalid) ? p.ckpt[(((long)b * p.nck + (k - 1)) * N + w * K + s) * dim + c] : 0.0f;
+      h0[s] = (k > 0 && cvalid) ? ck0[s] : 0.0f;
     {
       float hh[K];
 #pragma unroll
