@@ -7,13 +7,12 @@
 //
 // bf16 path (the performance path), per workgroup of 4 waves and 128 queries:
 //   * each wave owns 32 queries; Q^T stays in registers as MFMA B fragments;
-//   * K and V tiles of BN keys (32 at head_dim 128, measured faster than 64: fewer
-//     live score registers; 64 otherwise) are staged in LDS, double-buffered;
+//   * K and V tiles of 64 keys are staged in LDS (K row-major, V transposed to
+//     [dim][key] so the MFMA A operand of V^T is a contiguous LDS read), rows padded
+//     against bank conflicts;
 //   * S^T = K Q^T with v_mfma_f32_32x32x16_bf16: every lane owns one query column,
 //     so the online-softmax max/sum are lane-local plus one exchange between the two
-//     wave halves; the reference maximum is only raised when a row maximum exceeds it by
-//     more than 2^8 (P <= 256), so the O rescale runs on few tiles, and row sums are
-//     v_dot2_f32_bf16 over the packed bf16 P fragments (the weights O actually uses);
+//     wave halves;
 //   * O^T += V^T P^T reuses the S^T result registers directly as the B operand
 //     (keys permuted consistently in the V^T reads), so P never goes through LDS;
 //   * causal: key tiles above the diagonal are skipped, only diagonal tiles are
@@ -34,8 +33,7 @@ template <int HD, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                              const bf16* __restrict__ V, bf16* __restrict__ O,
                                                              float* __restrict__ LSE, int T, float scale_log2) {
-  constexpr int BM = 128, BN = HD == 128 ? 32 : 64;
-  constexpr int NH2 = BN / 32;  // 32-key blocks per tile
+  constexpr int BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   constexpr int CPR = HD / 8;             // 16-byte chunks per row
   constexpr int CPT = BN * CPR / 256;     // chunks per thread per tile (K and V each)
@@ -102,9 +100,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
     auto tile = [&](auto masked) {
     constexpr bool MASK = decltype(masked)::value;
     // S^T = K Q^T: lane owns query column li, rows are keys
-    f32x16 s[NH2];
+    f32x16 s[2];
 #pragma unroll
-    for (int h2 = 0; h2 < NH2; ++h2) {
+    for (int h2 = 0; h2 < 2; ++h2) {
       s[h2] = zero16();
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) {
@@ -114,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int h2 = 0; h2 < NH2; ++h2) {
+    for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         if constexpr (MASK) {
@@ -125,46 +123,37 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
       }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Lazy rescaling: the reference maximum m moves only when a row's maximum exceeds it
-    // by more than 8 (log2 units), so p = 2^(s c - m c) <= 256 (exact enough in bf16 and
-    // f32) and the O rescale runs on a few tiles instead of nearly every one.
-    if (__any((mx - m) * scale_log2 > 8.0f)) {
-      const float mnew = fmaxf(m, mx);
-      const float alpha = mnew == -INFINITY ? 1.0f : fast_exp2((m - mnew) * scale_log2);
-      m = mnew;
+    const float mnew = fmaxf(m, mx);
+    // scale folded into the exponent: p = 2^(s c - m c)
+    const float mns = mnew == -INFINITY ? 0.0f : mnew * scale_log2;
+    if (__any(mnew > m)) {  // rescale only when some row maximum grew
+      const float alpha = fast_exp2(m * scale_log2 - mns);
       lsum *= alpha;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
     }
-    const float mns = m == -INFINITY ? 0.0f : m * scale_log2;
+    m = mnew;
+    float rs = 0.0f;
 #pragma unroll
-    for (int h2 = 0; h2 < NH2; ++h2) {
+    for (int h2 = 0; h2 < 2; ++h2) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[h2][r] = fast_exp2(fmaf(s[h2][r], scale_log2, -mns));
+      for (int r = 0; r < 16; ++r) {
+        const float pv = fast_exp2(fmaf(s[h2][r], scale_log2, -mns));
+        s[h2][r] = pv;
+        rs += pv;
+      }
     }
+    lsum += rs + __shfl_xor(rs, 32);
 
     // P^T straight from the S^T registers: B fragment kc holds keys
     // 16 kc + 4 g + {0..3} and 16 kc + 8 + 4 g + {0..3}
-    bf16x8 pf[2 * NH2];
+    bf16x8 pf[4];
 #pragma unroll
-    for (int kc = 0; kc < 2 * NH2; ++kc)
+    for (int kc = 0; kc < 4; ++kc)
 #pragma unroll
       for (int it = 0; it < 8; ++it) pf[kc][it] = (bf16)s[kc >> 1][8 * (kc & 1) + it];
-    // row sum of the bf16 P actually multiplied into O: v_dot2_f32_bf16 against (1, 1)
-    {
-      float rs = 0.0f;
-      const bf16x2 one2 = {(bf16)1.0f, (bf16)1.0f};
-#pragma unroll
-      for (int kc = 0; kc < 2 * NH2; ++kc)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bf16x2 pr = {pf[kc][2 * e], pf[kc][2 * e + 1]};
-          rs = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, rs, false);
-        }
-      lsum += rs + __shfl_xor(rs, 32);
-    }
 
     // O^T += V^T P^T; the V^T A fragment (same key order) comes from two transposed
     // reads of the row-major V tile: lane i of each 16-lane group addresses key row
@@ -176,7 +165,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-        for (int kc = 0; kc < 2 * NH2; ++kc) {
+        for (int kc = 0; kc < 4; ++kc) {
           const int row = 16 * kc + kr, col = dt * 32 + d0;
           const bf16x8 a = cat4(lds_read_tr16(sv + lds_off<HD>(row, col)), lds_read_tr16(sv + lds_off<HD>(row + 8, col)));
           o[dt] = mfma32(a, pf[kc], o[dt]);
