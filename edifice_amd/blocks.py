@@ -40,9 +40,24 @@ KEY_NORM_EPS = 1.0e-6  # inside the sqrt of the key L2 norm (delta_net.ex:291, g
 
 
 def _causal_depthwise_conv(conv: nn.Conv1d, x: torch.Tensor) -> torch.Tensor:
-    """[B, T, C] -> [B, T, C]: depthwise conv with conv_size - 1 steps of left padding."""
-    seq = x.shape[1]
-    return conv(x.transpose(1, 2))[..., :seq].transpose(1, 2)
+    """[B, T, C] -> [B, T, C]: depthwise conv with conv_size - 1 steps of left padding,
+    y[t, c] = bias[c] + sum_j w[c, j] x[t - (K - 1) + j, c].
+
+    Computed as K shifted multiply-adds in (at least) float32 over the channel-contiguous layout
+    (bandwidth-bound elementwise work) rather than through the convolution library,
+    whose depthwise bf16 path falls back to naive kernels; the result is cast back to the
+    input dtype.  Same parameters (the nn.Conv1d's weight [C, 1, K] and bias) and the
+    same arithmetic as the reference's padded depthwise conv."""
+    seq, ksz = x.shape[1], conv.kernel_size[0]
+    acc = torch.promote_types(x.dtype, torch.float32)
+    w = conv.weight[:, 0, :].to(acc)  # [C, K]
+    xp = F.pad(x.to(acc), (0, 0, ksz - 1, 0))  # left-pad time
+    y = xp[:, ksz - 1:ksz - 1 + seq] * w[:, ksz - 1]
+    for j in range(ksz - 1):
+        y = y + xp[:, j:j + seq] * w[:, j]
+    if conv.bias is not None:
+        y = y + conv.bias.to(acc)
+    return y.to(x.dtype)
 
 
 def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:

@@ -12,12 +12,17 @@
 //
 // This is the exact per-step path: it supports per-element beta (where each row of S
 // has its own gate, so the chunked UT form of the per-head path does not apply),
-// float32 I/O and any head_dim <= 128.  One workgroup of 256 lanes owns one
-// (batch, head) state; lane (tr, tc) holds S[tr + 16 a][tc + 16 c], so row sums are
-// reductions inside a 16-lane DPP row and column sums go through LDS.
+// float32 I/O and any head_dim <= 128.
+//
+// Rows of S evolve independently given k, q, alpha and the row's beta, so a workgroup
+// owns one block of RB = 16 rows of one (batch, head) state (DP / 16 workgroups per
+// head): lane (tr, tc) holds S[16 rb + tr][tc + 16 c], row sums are reductions inside a
+// 16-lane DPP row, and only the backward's sums over rows (dq, dk, dalpha and a per-head
+// dbeta) cross workgroups: each row block writes its partial sums and a small kernel adds
+// the DP / 16 partials in a fixed order (deterministic, no atomics).
 // The backward does not invert the update (the reference divides by alpha): the
-// forward states are checkpointed every CK steps into the workspace and each chunk's
-// CK states are recomputed into a per-(batch, head) workspace slab.
+// forward states are checkpointed every CK steps and each chunk's CK states are
+// recomputed into registers (16 x DP/16 floats per lane) before its reverse sweep.
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
@@ -25,12 +30,16 @@ namespace edf {
 namespace {
 
 constexpr int CK = 16;  // steps per staged chunk / checkpoint interval
+constexpr int RB = 16;  // state rows per workgroup
 
 struct DRArgs {
   const void *q, *k, *v, *beta, *alpha, *dout;
   void *out, *dq, *dk, *dv, *dbeta, *dalpha;
-  float* ckpt;  // [BH][nck][DP*DP]
-  float* slab;  // [BH][CK][DP*DP]
+  float* ckpt;    // [BH][nck][DP*DP] state after each chunk
+  float* part_q;  // [nrb][B*T*H][d]   per-row-block partial dq
+  float* part_k;  // [nrb][B*T*H][d]   per-row-block partial dk
+  float* part_a;  // [nrb][B*T*H]      per-row-block partial dalpha
+  float* part_b;  // [nrb][B*T*H]      per-row-block partial per-head dbeta
   int H, T, d, beta_per_head, nck;
 };
 
@@ -40,15 +49,17 @@ EDF_DEVICE float row16_sum(float x) {
   return x;
 }
 
-template <typename TT, int DP>
+// One chunk of inputs: k and q over all DP columns, v, beta (and dout) for this
+// workgroup's RB rows, alpha per step; zero beyond T and beyond d, alpha 1 beyond T, so
+// padding steps are identities of the recurrence and of its adjoint.
+template <int DP>
 struct Stage {
-  float k[CK][DP], q[CK][DP], v[CK][DP], b[CK][DP], go[CK][DP];
+  float k[CK][DP], q[CK][DP], v[CK][RB], b[CK][RB], go[CK][RB];
   float a[CK];
 };
 
-// Stage CK steps of the per-(b,h) inputs (zero-padded beyond T and beyond d).
 template <typename TT, int DP>
-EDF_DEVICE void stage_chunk(Stage<TT, DP>& sm, const DRArgs& p, long bh, int t0, bool with_dout) {
+EDF_DEVICE void stage_chunk(Stage<DP>& sm, const DRArgs& p, long bh, int rb, int t0, bool with_dout) {
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   const int d = p.d;
   for (int e = threadIdx.x; e < CK * DP; e += 256) {
@@ -58,11 +69,17 @@ EDF_DEVICE void stage_chunk(Stage<TT, DP>& sm, const DRArgs& p, long bh, int t0,
     const long idx = (((long)b * p.T + t) * p.H + h) * d + j;
     sm.k[tt][j] = ok ? ld((const TT*)p.k, idx) : 0.0f;
     sm.q[tt][j] = ok ? ld((const TT*)p.q, idx) : 0.0f;
-    sm.v[tt][j] = ok ? ld((const TT*)p.v, idx) : 0.0f;
+  }
+  for (int e = threadIdx.x; e < CK * RB; e += 256) {
+    const int tt = e / RB, ii = e % RB, i = rb * RB + ii;
+    const int t = t0 + tt;
+    const bool ok = t < p.T && i < d;
+    const long idx = (((long)b * p.T + t) * p.H + h) * d + i;
+    sm.v[tt][ii] = ok ? ld((const TT*)p.v, idx) : 0.0f;
     float bv = 0.0f;
     if (ok) bv = p.beta_per_head ? ld((const TT*)p.beta, ((long)b * p.T + t) * p.H + h) : ld((const TT*)p.beta, idx);
-    sm.b[tt][j] = bv;
-    if (with_dout) sm.go[tt][j] = ok ? ld((const TT*)p.dout, idx) : 0.0f;
+    sm.b[tt][ii] = bv;
+    if (with_dout) sm.go[tt][ii] = ok ? ld((const TT*)p.dout, idx) : 0.0f;
   }
   for (int tt = threadIdx.x; tt < CK; tt += 256) {
     const int t = t0 + tt;
@@ -70,196 +87,179 @@ EDF_DEVICE void stage_chunk(Stage<TT, DP>& sm, const DRArgs& p, long bh, int t0,
   }
 }
 
-// One forward step on the lane's tile; returns nothing, updates S in place.
+// One forward step of the lane's row segment: S = a S + beta (v - a S k) k^T.
 template <int DP>
-EDF_DEVICE void fwd_step(float (&S)[DP / 16][DP / 16], const float* kt, const float* vt, const float* bt, float at,
-                         int tr, int tc, float* r_out) {
-  constexpr int NA = DP / 16;
+EDF_DEVICE void fwd_step(float (&S)[DP / 16], const Stage<DP>& sm, int tt, int tr, int tc) {
+  constexpr int NC = DP / 16;
+  const float at = sm.a[tt];
+  float r = 0.0f;
 #pragma unroll
-  for (int a = 0; a < NA; ++a) {
-    float r = 0.0f;
+  for (int c = 0; c < NC; ++c) r = fmaf(S[c], sm.k[tt][tc + 16 * c], r);
+  r = row16_sum(r) * at;
+  const float e = sm.b[tt][tr] * (sm.v[tt][tr] - r);
 #pragma unroll
-    for (int c = 0; c < NA; ++c) r = fmaf(S[a][c], kt[tc + 16 * c], r);
-    r = row16_sum(r) * at;
-    const int i = tr + 16 * a;
-    const float e = bt[i] * (vt[i] - r);
-    if (r_out) r_out[a] = r;
-#pragma unroll
-    for (int c = 0; c < NA; ++c) S[a][c] = fmaf(e, kt[tc + 16 * c], at * S[a][c]);
-  }
+  for (int c = 0; c < NC; ++c) S[c] = fmaf(e, sm.k[tt][tc + 16 * c], at * S[c]);
 }
 
 template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
-  constexpr int NA = DP / 16;
-  __shared__ Stage<TT, DP> sm;
+  constexpr int NC = DP / 16;
+  __shared__ Stage<DP> sm;
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
+  const int rb = blockIdx.y, i = rb * RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-  float S[NA][NA];
+  float S[NC];
 #pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int c = 0; c < NA; ++c) S[a][c] = 0.0f;
+  for (int c = 0; c < NC; ++c) S[c] = 0.0f;
   for (int t0 = 0; t0 < p.T; t0 += CK) {
     __syncthreads();
-    stage_chunk<TT, DP>(sm, p, bh, t0, false);
+    stage_chunk<TT, DP>(sm, p, bh, rb, t0, false);
     __syncthreads();
     for (int tt = 0; tt < CK && t0 + tt < p.T; ++tt) {
-      fwd_step<DP>(S, sm.k[tt], sm.v[tt], sm.b[tt], sm.a[tt], tr, tc, nullptr);
-      // o_i = sum_j S[i][j] q_j
-#pragma unroll
-      for (int a = 0; a < NA; ++a) {
+      fwd_step<DP>(S, sm, tt, tr, tc);
+      if (p.out != nullptr) {  // o_i = sum_j S[i][j] q_j
         float o = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NA; ++c) o = fmaf(S[a][c], sm.q[tt][tc + 16 * c], o);
+        for (int c = 0; c < NC; ++c) o = fmaf(S[c], sm.q[tt][tc + 16 * c], o);
         o = row16_sum(o);
-        const int i = tr + 16 * a;
-        if (p.out != nullptr && tc == a && i < p.d) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
+        if (tc == 0 && i < p.d) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
       }
     }
     if (p.ckpt != nullptr) {
-      float* cp = p.ckpt + ((long)bh * p.nck + t0 / CK) * DP * DP;
+      float* cp = p.ckpt + ((long)bh * p.nck + t0 / CK) * DP * DP + (long)i * DP + tc;
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int c = 0; c < NA; ++c) cp[(tr + 16 * a) * DP + tc + 16 * c] = S[a][c];
+      for (int c = 0; c < NC; ++c) cp[16 * c] = S[c];
     }
   }
 }
 
+// Backward over chunks in reverse.  Per step t (S_p the state before it, S_g = a S_p,
+// S_t = S_g + be k^T, dtot = dS + do q^T):  dq = S_t^T do, dv = beta ds_k,
+// dbeta = err ds_k, dk = dtot^T be - S_g^T (beta ds_k), dalpha = sum((dtot - beta ds_k k^T) o S_p),
+// dS <- a (dtot - beta ds_k k^T), with err = v - S_g k, be = beta err, ds_k = dtot k.
 template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
-  constexpr int NA = DP / 16;
-  __shared__ Stage<TT, DP> sm;
-  __shared__ float red[2][16][DP + 1];  // column partials: [qty][tr][j]
-  __shared__ float reda[16 * 16];
+  constexpr int NC = DP / 16;
+  __shared__ Stage<DP> sm;
+  __shared__ float red[2][RB][DP + 1];  // per-row column partials: [qty][tr][j]
+  __shared__ float reda[2][RB];
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
+  const int rb = blockIdx.y, i = rb * RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-  float* slab = p.slab + bh * CK * DP * DP;
-  float dS[NA][NA];
+  const long nbth = (long)gridDim.x * p.T;  // B * T * H
+  float dS[NC];
 #pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int c = 0; c < NA; ++c) dS[a][c] = 0.0f;
+  for (int c = 0; c < NC; ++c) dS[c] = 0.0f;
 
   for (int ck = p.nck - 1; ck >= 0; --ck) {
     const int t0 = ck * CK;
     __syncthreads();
-    stage_chunk<TT, DP>(sm, p, bh, t0, true);
+    stage_chunk<TT, DP>(sm, p, bh, rb, t0, true);
     __syncthreads();
-    // recompute the chunk: slab[tt] = state before step t0 + tt
+    // recompute the chunk's states into registers: Sl[tt] = state before step t0 + tt
+    float Sl[CK][NC];
     {
-      float S[NA][NA];
+      float S[NC];
+      // chunk 0 starts from zero; its (unused) load address stays in bounds
+      const float* cp = p.ckpt + ((long)bh * p.nck + max(ck - 1, 0)) * DP * DP + (long)i * DP + tc;
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
+      for (int c = 0; c < NC; ++c) S[c] = ck > 0 ? cp[16 * c] : 0.0f;
 #pragma unroll
-        for (int c = 0; c < NA; ++c)
-          S[a][c] = ck > 0 ? p.ckpt[((long)bh * p.nck + (ck - 1)) * DP * DP + (tr + 16 * a) * DP + tc + 16 * c] : 0.0f;
       for (int tt = 0; tt < CK; ++tt) {
 #pragma unroll
-        for (int a = 0; a < NA; ++a)
-#pragma unroll
-          for (int c = 0; c < NA; ++c) slab[(long)tt * DP * DP + (tr + 16 * a) * DP + tc + 16 * c] = S[a][c];
-        fwd_step<DP>(S, sm.k[tt], sm.v[tt], sm.b[tt], sm.a[tt], tr, tc, nullptr);
+        for (int c = 0; c < NC; ++c) Sl[tt][c] = S[c];
+        fwd_step<DP>(S, sm, tt, tr, tc);
       }
     }
+#pragma unroll
     for (int tt = CK - 1; tt >= 0; --tt) {
       const int t = t0 + tt;
-      if (t >= p.T) continue;
       const float at = sm.a[tt];
-      const float* kt = sm.k[tt];
-      const float* qt = sm.q[tt];
-      const float* bt = sm.b[tt];
-      const float* got = sm.go[tt];
-      float Sp[NA][NA];
+      const float goi = sm.go[tt][tr], bi = sm.b[tt][tr];
+      float r = 0.0f, sk = 0.0f;
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int c = 0; c < NA; ++c) Sp[a][c] = slab[(long)tt * DP * DP + (tr + 16 * a) * DP + tc + 16 * c];
-      float err[NA], be[NA], bdk[NA], dsk[NA];
-      float pq[NA], pk[NA], pa = 0.0f;
-#pragma unroll
-      for (int c = 0; c < NA; ++c) {
-        pq[c] = 0.0f;
-        pk[c] = 0.0f;
+      for (int c = 0; c < NC; ++c) {
+        const float kj = sm.k[tt][tc + 16 * c];
+        r = fmaf(Sl[tt][c], kj, r);
+        sk = fmaf(fmaf(goi, sm.q[tt][tc + 16 * c], dS[c]), kj, sk);
       }
+      r = row16_sum(r) * at;
+      sk = row16_sum(sk);
+      const float err = sm.v[tt][tr] - r;
+      const float be = bi * err, bdk = bi * sk;
+      float pq[NC], pk[NC], pa = 0.0f;
 #pragma unroll
-      for (int a = 0; a < NA; ++a) {
-        const int i = tr + 16 * a;
-        float r = 0.0f, sk = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NA; ++c) {
-          r = fmaf(Sp[a][c], kt[tc + 16 * c], r);
-          sk = fmaf(fmaf(got[i], qt[tc + 16 * c], dS[a][c]), kt[tc + 16 * c], sk);
-        }
-        r = row16_sum(r) * at;
-        sk = row16_sum(sk);
-        err[a] = sm.v[tt][i] - r;
-        be[a] = bt[i] * err[a];
-        dsk[a] = sk;
-        bdk[a] = bt[i] * sk;
+      for (int c = 0; c < NC; ++c) {
+        const float kj = sm.k[tt][tc + 16 * c], qj = sm.q[tt][tc + 16 * c];
+        const float sg = at * Sl[tt][c];
+        const float snew = fmaf(be, kj, sg);
+        const float dtot = fmaf(goi, qj, dS[c]);
+        pq[c] = snew * goi;
+        pk[c] = fmaf(dtot, be, -sg * bdk);
+        const float ddec = fmaf(-bdk, kj, dtot);
+        pa = fmaf(ddec, Sl[tt][c], pa);
+        dS[c] = at * ddec;
       }
-#pragma unroll
-      for (int a = 0; a < NA; ++a) {
-        const int i = tr + 16 * a;
-#pragma unroll
-        for (int c = 0; c < NA; ++c) {
-          const int j = tc + 16 * c;
-          const float sg = at * Sp[a][c];
-          const float snew = fmaf(be[a], kt[j], sg);
-          const float dtot = fmaf(got[i], qt[j], dS[a][c]);
-          pq[c] = fmaf(snew, got[i], pq[c]);
-          pk[c] = fmaf(dtot, be[a], fmaf(-sg, bdk[a], pk[c]));
-          const float ddec = fmaf(-bdk[a], kt[j], dtot);
-          pa = fmaf(ddec, Sp[a][c], pa);
-          dS[a][c] = at * ddec;
-        }
+      const bool live = t < p.T;
+      const long bth = ((long)b * p.T + t) * p.H + h;
+      if (live && tc == 0 && i < p.d) {  // per-row outputs: dv, per-element dbeta
+        st((TT*)p.dv, bth * p.d + i, bdk);
+        if (!p.beta_per_head) st((TT*)p.dbeta, bth * p.d + i, err * sk);
       }
-      // per-row outputs: dv, dbeta
-      const long rowbase = (((long)b * p.T + t) * p.H + h) * p.d;
-      float dbh = 0.0f;
+      // sums over this block's rows (dq, dk, dalpha, per-head dbeta) through LDS
 #pragma unroll
-      for (int a = 0; a < NA; ++a) {
-        const int i = tr + 16 * a;
-        if (tc == 0 && i < p.d) {
-          st((TT*)p.dv, rowbase + i, bdk[a]);
-          if (!p.beta_per_head) st((TT*)p.dbeta, rowbase + i, err[a] * dsk[a]);
-        }
-        dbh += (i < p.d) ? err[a] * dsk[a] : 0.0f;
-      }
-      // column sums (dq, dk) and the full sums (dalpha, per-head dbeta) through LDS
-#pragma unroll
-      for (int c = 0; c < NA; ++c) {
+      for (int c = 0; c < NC; ++c) {
         red[0][tr][tc + 16 * c] = pq[c];
         red[1][tr][tc + 16 * c] = pk[c];
       }
       pa = row16_sum(pa);
       if (tc == 0) {
-        reda[tr] = pa;
-        reda[16 + tr] = dbh;
+        reda[0][tr] = pa;
+        reda[1][tr] = i < p.d ? err * sk : 0.0f;
       }
       __syncthreads();
-      for (int e = tid; e < 2 * DP; e += 256) {
-        const int qty = e / DP, j = e % DP;
-        float s = 0.0f;
+      if (live) {
+        for (int e = tid; e < 2 * DP; e += 256) {
+          const int qty = e / DP, j = e % DP;
+          float acc = 0.0f;
 #pragma unroll
-        for (int m = 0; m < 16; ++m) s += red[qty][m][j];
-        if (j < p.d) st((TT*)(qty == 0 ? p.dq : p.dk), rowbase + j, s);
-      }
-      if (tid == 0) {
-        float sa = 0.0f, sb = 0.0f;
-        for (int m = 0; m < 16; ++m) {
-          sa += reda[m];
-          sb += reda[16 + m];
+          for (int m = 0; m < RB; ++m) acc += red[qty][m][j];
+          if (j < p.d) (qty == 0 ? p.part_q : p.part_k)[((long)rb * nbth + bth) * p.d + j] = acc;
         }
-        const long hidx = ((long)b * p.T + t) * p.H + h;
-        if (p.dalpha != nullptr) st((TT*)p.dalpha, hidx, sa);
-        if (p.beta_per_head) st((TT*)p.dbeta, hidx, sb);
+        if (tid < 2) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int m = 0; m < RB; ++m) acc += reda[tid][m];
+          (tid == 0 ? p.part_a : p.part_b)[(long)rb * nbth + bth] = acc;
+        }
       }
       __syncthreads();
     }
+  }
+}
+
+// dq, dk (and dalpha, per-head dbeta) = the row-block partials added in block order.
+template <typename TT>
+__global__ __launch_bounds__(256) void dr_seq_reduce_kernel(const DRArgs p, long nbth, int nrb) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  const long nvec = nbth * p.d;
+  if (e < 2 * nvec) {
+    const int qty = e >= nvec;
+    const long o = e - qty * nvec;
+    const float* part = qty ? p.part_k : p.part_q;
+    float acc = 0.0f;
+    for (int r = 0; r < nrb; ++r) acc += part[r * nvec + o];
+    st((TT*)(qty ? p.dk : p.dq), o, acc);
+  } else if (e < 2 * nvec + 2 * nbth) {
+    const int qty = e >= 2 * nvec + nbth;
+    const long o = e - 2 * nvec - qty * nbth;
+    const float* part = qty ? p.part_b : p.part_a;
+    float acc = 0.0f;
+    for (int r = 0; r < nrb; ++r) acc += part[r * nbth + o];
+    if (qty == 0 && p.dalpha != nullptr) st((TT*)p.dalpha, o, acc);
+    if (qty == 1 && p.beta_per_head) st((TT*)p.dbeta, o, acc);
   }
 }
 
@@ -268,10 +268,11 @@ int launch_seq(hipStream_t s, const DRArgs& a, bool bwd, int BH) {
   const int d = a.d;
 #define EDF_DR_LAUNCH(DP)                                              \
   do {                                                                 \
+    const dim3 grid(BH, DP / RB);                                      \
     if (bwd)                                                           \
-      dr_seq_bwd_kernel<TT, DP><<<BH, 256, 0, s>>>(a);                 \
+      dr_seq_bwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);               \
     else                                                               \
-      dr_seq_fwd_kernel<TT, DP><<<BH, 256, 0, s>>>(a);                 \
+      dr_seq_fwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);               \
   } while (0)
   if (d <= 16)
     EDF_DR_LAUNCH(16);
@@ -287,13 +288,36 @@ int launch_seq(hipStream_t s, const DRArgs& a, bool bwd, int BH) {
 
 inline int pad_dim(int d) { return d <= 16 ? 16 : d <= 32 ? 32 : d <= 64 ? 64 : 128; }
 
+struct SeqWs {
+  size_t ckpt, part_q, part_k, part_a, part_b, total;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+inline SeqWs seq_ws(int batch, int heads, int seq, int d) {
+  const size_t dp = pad_dim(d), nrb = dp / RB;
+  const size_t nck = (seq + CK - 1) / CK;
+  const size_t bh = (size_t)batch * heads, nbth = bh * seq;
+  SeqWs w{};
+  size_t off = 0;
+  w.ckpt = off;
+  off += align256(bh * nck * dp * dp * 4);
+  w.part_q = off;
+  off += align256(nrb * nbth * d * 4);
+  w.part_k = off;
+  off += align256(nrb * nbth * d * 4);
+  w.part_a = off;
+  off += align256(nrb * nbth * 4);
+  w.part_b = off;
+  off += align256(nrb * nbth * 4);
+  w.total = off;
+  return w;
+}
+
 }  // namespace
 
 size_t dr_seq_backward_workspace_bytes(int batch, int heads, int seq, int d) {
-  const size_t dp = pad_dim(d);
-  const size_t nck = (seq + CK - 1) / CK;
-  const size_t bh = (size_t)batch * heads;
-  return bh * nck * dp * dp * 4 + bh * CK * dp * dp * 4;
+  return seq_ws(batch, heads, seq, d).total;
 }
 
 int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
@@ -316,23 +340,37 @@ int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* 
   a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta; a.dalpha = dalpha;
   a.H = heads; a.T = seq; a.d = d; a.beta_per_head = beta_per_head;
   a.nck = (seq + CK - 1) / CK;
-  const size_t dp = pad_dim(d);
-  const size_t bh = (size_t)batch * heads;
-  a.ckpt = (float*)workspace;
-  a.slab = (float*)((char*)workspace + bh * a.nck * dp * dp * 4);
+  const SeqWs w = seq_ws(batch, heads, seq, d);
+  char* ws = (char*)workspace;
+  a.ckpt = (float*)(ws + w.ckpt);
+  a.part_q = (float*)(ws + w.part_q);
+  a.part_k = (float*)(ws + w.part_k);
+  a.part_a = (float*)(ws + w.part_a);
+  a.part_b = (float*)(ws + w.part_b);
+  const int bh = batch * heads;
+  const long nbth = (long)bh * seq;
+  const int nrb = pad_dim(d) / RB;
   hipStream_t s = as_stream(stream);
-  // forward pass that only writes the checkpoints (output goes to the slab area, unused)
+  // forward pass that only writes the checkpoints
   DRArgs f = a;
   f.out = nullptr;
+  const long nred = 2 * nbth * d + 2 * nbth;
+  const unsigned gred = (unsigned)((nred + 255) / 256);
   int rc;
   if (dtype == EDF_BF16) {
-    rc = launch_seq<bf16>(s, f, false, (int)bh);
+    rc = launch_seq<bf16>(s, f, false, bh);
     if (rc) return rc;
-    return launch_seq<bf16>(s, a, true, (int)bh);
+    rc = launch_seq<bf16>(s, a, true, bh);
+    if (rc) return rc;
+    dr_seq_reduce_kernel<bf16><<<gred, 256, 0, s>>>(a, nbth, nrb);
+  } else {
+    rc = launch_seq<float>(s, f, false, bh);
+    if (rc) return rc;
+    rc = launch_seq<float>(s, a, true, bh);
+    if (rc) return rc;
+    dr_seq_reduce_kernel<float><<<gred, 256, 0, s>>>(a, nbth, nrb);
   }
-  rc = launch_seq<float>(s, f, false, (int)bh);
-  if (rc) return rc;
-  return launch_seq<float>(s, a, true, (int)bh);
+  return check_launch("delta rule backward reduction");
 }
 
 }  // namespace edf
