@@ -43,12 +43,6 @@ struct DRArgs {
   int H, T, d, beta_per_head, nck;
 };
 
-EDF_DEVICE float row16_sum(float x) {
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) x += __shfl_xor(x, off, 16);
-  return x;
-}
-
 // One chunk of inputs: k and q over all DP columns, v, beta (and dout) for this
 // workgroup's RB rows, alpha per step; zero beyond T and beyond d, alpha 1 beyond T, so
 // padding steps are identities of the recurrence and of its adjoint.

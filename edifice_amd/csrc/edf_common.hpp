@@ -104,6 +104,21 @@ EDF_DEVICE float row_bcast(float v) {
                                                                true));
 }
 
+// Sum over the 16 lanes of each DPP row, returned in every lane of the row: a rotation
+// butterfly (row_ror 8, 4, 2, 1) of VALU DPP adds.  At each step a lane and its partner
+// already hold equal values, so all 16 lanes end with the bitwise-same sum.
+template <int CTRL>
+EDF_DEVICE float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+EDF_DEVICE float row16_sum(float x) {
+  x += dpp_f32<0x128>(x);  // row_ror:8
+  x += dpp_f32<0x124>(x);  // row_ror:4
+  x += dpp_f32<0x122>(x);  // row_ror:2
+  x += dpp_f32<0x121>(x);  // row_ror:1
+  return x;
+}
+
 // ---- launch-shape helpers -----------------------------------------------------
 // MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs, each
 // with a private L2.  remap_xcd() turns the hardware id into a logical id such

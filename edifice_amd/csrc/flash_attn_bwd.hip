@@ -41,8 +41,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dot_kernel(const TT* __restrict__ 
   float acc = 0.0f;
   if (row < rows)
     for (int d = sub; d < HD; d += 16) acc = fmaf(ld(O, row * HD + d), ld(dO, row * HD + d), acc);
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  acc = row16_sum(acc);  // the 16 lanes of a row group are one DPP row
   if (row < rows && sub == 0) Dv[row] = acc;
 }
 
