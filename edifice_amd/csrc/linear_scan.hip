@@ -28,6 +28,8 @@
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
+#include <type_traits>
+
 namespace edf {
 namespace {
 
@@ -37,6 +39,8 @@ constexpr float MINLSTM_EPS = 1.0e-6f;
 // Deeper rings (P = 3, 4) were slower for both directions.
 constexpr int LIN_LF = 8, LIN_PF = 2;  // forward
 constexpr int LIN_LB = 4, LIN_PB = 2;  // backward (five inputs per step)
+// two channels per lane (bf16): 8 waves = 16 virtual waves of L steps (more waves spill)
+constexpr int LIN2_LF = 8, LIN2_LB = 4, LIN2_W = 8;
 
 enum { OP_MINGRU = 0, OP_MINLSTM = 1 };
 
@@ -286,39 +290,371 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
   if (valid && w == 0 && dh0 != nullptr) st(dh0, (long)b * hid + c, u);
 }
 
+// ---------------------------------------------------------------------------------
+// Two channels per lane (bf16, even hidden sizes): each access moves a bf16 pair (4 bytes
+// per lane, 256 bytes per wave instruction instead of 128; for float32 the same layout with
+// 8-byte pairs measured no faster than one channel per lane), and each
+// wave is two 32-lane "virtual waves" (lanes 0-31 and 32-63) that own consecutive time
+// segments of L steps, so the 64-channel tile keeps its 2W segments per macro-step.  The
+// lower half's affine maps reach the upper half through v_permlane32_swap (VALU); the
+// upper half forms the wave's map, the waves' maps are composed through LDS as above.
+// ---------------------------------------------------------------------------------
+template <typename T> struct Pair;
+template <> struct Pair<bf16> {
+  typedef unsigned type;
+  static EDF_DEVICE type load(rsrc_t r, unsigned off) { return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0); }
+  static EDF_DEVICE float lo(type v) { return __builtin_bit_cast(float, v << 16); }
+  static EDF_DEVICE float hi(type v) { return __builtin_bit_cast(float, v & 0xffff0000u); }
+  static EDF_DEVICE void store(rsrc_t r, unsigned off, float a, float b) {
+    const unsigned v = (unsigned)__builtin_bit_cast(unsigned short, (bf16)a) |
+                       ((unsigned)__builtin_bit_cast(unsigned short, (bf16)b) << 16);
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, (int)off, 0, 0);
+  }
+};
+
+// Value of x held by lane l - 32, delivered to lanes 32..63 (lanes 0..31 get y's upper
+// half, unused).  The second operand must be a different register from the first.
+EDF_DEVICE float from_lower(float y, float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, y), __builtin_bit_cast(unsigned, x),
+                                                  false, false);
+  return __builtin_bit_cast(float, s[0]);
+}
+
+template <typename T, int OP, bool LOGITS, int L, int W, int P>
+__global__ __launch_bounds__(64 * W) void linscan2_fwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
+                                                              const T* __restrict__ cand, const T* __restrict__ h0,
+                                                              T* __restrict__ out, int seq, int hid) {
+  typedef Pair<T> PR;
+  typedef typename PR::type PB;
+  constexpr unsigned ES = sizeof(T);
+  __shared__ float sA[2][W][64];
+  __shared__ float sB[2][W][64];
+  const int lane = threadIdx.x & 63, pi = lane & 31, hf = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int vw = 2 * w + hf;  // virtual wave: time-segment index within a macro-step
+  const int b = blockIdx.y;
+  const int c = blockIdx.x * 64 + 2 * pi;  // the lane's channels c, c + 1 (hid is even)
+  const bool valid = c < hid;
+  const long slab = (long)b * seq * hid;
+  const unsigned bytes = (unsigned)((long)seq * hid * ES);
+  const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
+  const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
+  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RO = make_rsrc(out + slab, bytes);
+  auto off = [&](int t) -> unsigned {
+    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
+  };
+
+  PB r1[P][L], r2[P][L], rc[P][L];
+  auto fetch = [&](int slot, int ms) {
+    const int t0 = (ms * 2 * W + vw) * L;
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const unsigned o = off(t0 + j);
+      r1[slot][j] = PR::load(R1, o);
+      if (OP == OP_MINLSTM) r2[slot][j] = PR::load(R2, o);
+      rc[slot][j] = PR::load(RC, o);
+    }
+  };
+
+  float h[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) h[k] = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c + k) : 0.0f;
+  const int steps = (seq + 2 * W * L - 1) / (2 * W * L);
+  const int npad = (steps + P - 1) / P * P;
+#pragma unroll
+  for (int j = 0; j < P; ++j) fetch(j, j);
+  for (int ms0 = 0; ms0 < npad; ms0 += P) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      const int ms = ms0 + u;
+      const int t0 = (ms * 2 * W + vw) * L;
+      float a[L][2], bb[L][2];
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        const bool ok = valid && t0 + j < seq;  // padding steps are the identity map
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          Step<OP, LOGITS> st;
+          const float x1 = k ? PR::hi(r1[u][j]) : PR::lo(r1[u][j]);
+          const float x2 = OP == OP_MINLSTM ? (k ? PR::hi(r2[u][j]) : PR::lo(r2[u][j])) : 0.0f;
+          const float xc = k ? PR::hi(rc[u][j]) : PR::lo(rc[u][j]);
+          st.make(x1, x2, xc);
+          a[j][k] = ok ? st.a : 1.0f;
+          bb[j][k] = ok ? st.b : 0.0f;
+        }
+      }
+      fetch(u, ms + P);
+      float A[2], B[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        A[k] = 1.0f;
+        B[k] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+          B[k] = fmaf(a[j][k], B[k], bb[j][k]);
+          A[k] *= a[j][k];
+        }
+      }
+      // the lower half's maps (the earlier segment) in the upper half's lanes
+      float Al[2], Bl[2];
+      Al[0] = from_lower(A[1], A[0]);
+      Al[1] = from_lower(A[0], A[1]);
+      Bl[0] = from_lower(B[1], B[0]);
+      Bl[1] = from_lower(B[0], B[1]);
+      const int buf = ms & 1;
+      if (hf) {  // the wave's map: upper segment after lower segment
+        *reinterpret_cast<float2*>(&sA[buf][w][2 * pi]) = make_float2(A[0] * Al[0], A[1] * Al[1]);
+        *reinterpret_cast<float2*>(&sB[buf][w][2 * pi]) = make_float2(fmaf(A[0], Bl[0], B[0]), fmaf(A[1], Bl[1], B[1]));
+      }
+      __syncthreads();
+      float x[2] = {h[0], h[1]}, hin[2] = {h[0], h[1]};
+#pragma unroll
+      for (int v = 0; v < W; ++v) {
+        if (v == w) {
+          hin[0] = x[0];
+          hin[1] = x[1];
+        }
+        const float2 av = *reinterpret_cast<const float2*>(&sA[buf][v][2 * pi]);
+        const float2 bv = *reinterpret_cast<const float2*>(&sB[buf][v][2 * pi]);
+        x[0] = fmaf(av.x, x[0], bv.x);
+        x[1] = fmaf(av.y, x[1], bv.y);
+      }
+      h[0] = x[0];
+      h[1] = x[1];
+      float hh[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) hh[k] = hf ? fmaf(Al[k], hin[k], Bl[k]) : hin[k];
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        hh[0] = fmaf(a[j][0], hh[0], bb[j][0]);
+        hh[1] = fmaf(a[j][1], hh[1], bb[j][1]);
+        PR::store(RO, off(t0 + j), hh[0], hh[1]);
+      }
+    }
+  }
+}
+
+// Backward with the same layout, walking macro-steps from the end of the padded sequence;
+// virtual wave 0 (the lower half of wave 0) owns the latest segment of each macro-step.
+template <typename T, int OP, bool LOGITS, int L, int W, int P>
+__global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
+                                                              const T* __restrict__ cand, const T* __restrict__ h0,
+                                                              const T* __restrict__ fwd, const T* __restrict__ dy,
+                                                              T* __restrict__ d1, T* __restrict__ d2,
+                                                              T* __restrict__ dcand, T* __restrict__ dh0, int seq,
+                                                              int hid) {
+  typedef Pair<T> PR;
+  typedef typename PR::type PB;
+  constexpr unsigned ES = sizeof(T);
+  __shared__ float sA[2][W][64];
+  __shared__ float sB[2][W][64];
+  const int lane = threadIdx.x & 63, pi = lane & 31, hf = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int vw = 2 * w + hf;
+  const int b = blockIdx.y;
+  const int c = blockIdx.x * 64 + 2 * pi;
+  const bool valid = c < hid;
+  const long slab = (long)b * seq * hid;
+  const unsigned bytes = (unsigned)((long)seq * hid * ES);
+  const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
+  const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
+  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RH = make_rsrc(fwd + slab, bytes);
+  const rsrc_t RY = make_rsrc(dy + slab, bytes);
+  const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
+  const rsrc_t W2 = make_rsrc((OP == OP_MINLSTM ? d2 : d1) + slab, bytes);
+  const rsrc_t WC = make_rsrc(dcand + slab, bytes);
+  auto off = [&](int t) -> unsigned {
+    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
+  };
+  auto offp = [&](int t) -> unsigned {  // h_{t-1}; t = 0 reads out of range (0) and takes h0
+    return (valid && t < seq && t > 0) ? ((unsigned)(t - 1) * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
+  };
+  float h0v[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) h0v[k] = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c + k) : 0.0f;
+
+  const int steps = (seq + 2 * W * L - 1) / (2 * W * L);
+  const int npad = (steps + P - 1) / P * P;
+  const int tpad = npad * 2 * W * L;
+  auto first_t = [&](int ms) { return tpad - (ms + 1) * 2 * W * L + (2 * W - 1 - vw) * L; };
+  PB r1[P][L], r2[P][L], rc[P][L], rh[P][L], ry[P][L];
+  auto fetch = [&](int slot, int ms) {
+    const int t0 = first_t(ms);
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const unsigned o = off(t0 + j);
+      r1[slot][j] = PR::load(R1, o);
+      if (OP == OP_MINLSTM) r2[slot][j] = PR::load(R2, o);
+      rc[slot][j] = PR::load(RC, o);
+      rh[slot][j] = PR::load(RH, offp(t0 + j));
+      ry[slot][j] = PR::load(RY, o);
+    }
+  };
+
+  float u[2] = {0.0f, 0.0f};  // u_{t+1} entering the macro-step from the right
+#pragma unroll
+  for (int j = 0; j < P; ++j) fetch(j, j);
+  for (int ms0 = 0; ms0 < npad; ms0 += P) {
+#pragma unroll
+    for (int sl = 0; sl < P; ++sl) {
+      const int ms = ms0 + sl;
+      const int t0 = first_t(ms);
+      // per step and channel: decay a, input gradient g and the dh -> output coefficients
+      float a[L][2], gy[L][2], k1[L][2], k2[L][2], kc[L][2];
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        const int t = t0 + j;
+        const bool ok = valid && t < seq;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const float x1 = k ? PR::hi(r1[sl][j]) : PR::lo(r1[sl][j]);
+          const float x2 = OP == OP_MINLSTM ? (k ? PR::hi(r2[sl][j]) : PR::lo(r2[sl][j])) : 0.0f;
+          const float cv = k ? PR::hi(rc[sl][j]) : PR::lo(rc[sl][j]);
+          const float hp = t > 0 ? (k ? PR::hi(rh[sl][j]) : PR::lo(rh[sl][j])) : h0v[k];
+          gy[j][k] = k ? PR::hi(ry[sl][j]) : PR::lo(ry[sl][j]);  // 0 outside the sequence
+          if (OP == OP_MINGRU) {
+            const float z = LOGITS ? sigmoidf(x1) : x1;
+            a[j][k] = ok ? 1.0f - z : 1.0f;
+            k1[j][k] = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
+            k2[j][k] = 0.0f;
+            kc[j][k] = z;
+          } else {
+            const float f = LOGITS ? sigmoidf(x1) : x1;
+            const float i = LOGITS ? sigmoidf(x2) : x2;
+            const float r = 1.0f / (f + (i + MINLSTM_EPS));
+            const float r2v = r * r;
+            a[j][k] = ok ? f * r : 1.0f;
+            float c1 = (hp * (i + MINLSTM_EPS) - cv * i) * r2v;
+            float c2 = (cv * (f + MINLSTM_EPS) - hp * f) * r2v;
+            if (LOGITS) {
+              c1 *= f * (1.0f - f);
+              c2 *= i * (1.0f - i);
+            }
+            k1[j][k] = c1;
+            k2[j][k] = c2;
+            kc[j][k] = i * r;
+          }
+        }
+      }
+      fetch(sl, ms + P);
+      float A[2], B[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        A[k] = 1.0f;
+        B[k] = 0.0f;
+#pragma unroll
+        for (int j = L - 1; j >= 0; --j) {
+          B[k] = a[j][k] * (gy[j][k] + B[k]);
+          A[k] *= a[j][k];
+        }
+      }
+      float Al[2], Bl[2];
+      Al[0] = from_lower(A[1], A[0]);
+      Al[1] = from_lower(A[0], A[1]);
+      Bl[0] = from_lower(B[1], B[0]);
+      Bl[1] = from_lower(B[0], B[1]);
+      const int buf = ms & 1;
+      if (hf) {
+        *reinterpret_cast<float2*>(&sA[buf][w][2 * pi]) = make_float2(A[0] * Al[0], A[1] * Al[1]);
+        *reinterpret_cast<float2*>(&sB[buf][w][2 * pi]) = make_float2(fmaf(A[0], Bl[0], B[0]), fmaf(A[1], Bl[1], B[1]));
+      }
+      __syncthreads();
+      float x[2] = {u[0], u[1]}, uin[2] = {u[0], u[1]};
+#pragma unroll
+      for (int v = 0; v < W; ++v) {
+        if (v == w) {
+          uin[0] = x[0];
+          uin[1] = x[1];
+        }
+        const float2 av = *reinterpret_cast<const float2*>(&sA[buf][v][2 * pi]);
+        const float2 bv = *reinterpret_cast<const float2*>(&sB[buf][v][2 * pi]);
+        x[0] = fmaf(av.x, x[0], bv.x);
+        x[1] = fmaf(av.y, x[1], bv.y);
+      }
+      u[0] = x[0];
+      u[1] = x[1];
+      float uu[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) uu[k] = hf ? fmaf(Al[k], uin[k], Bl[k]) : uin[k];
+#pragma unroll
+      for (int j = L - 1; j >= 0; --j) {
+        const unsigned o = off(t0 + j);
+        float dh[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          dh[k] = gy[j][k] + uu[k];
+          uu[k] = a[j][k] * dh[k];
+        }
+        PR::store(W1, o, dh[0] * k1[j][0], dh[1] * k1[j][1]);
+        if (OP == OP_MINLSTM) PR::store(W2, o, dh[0] * k2[j][0], dh[1] * k2[j][1]);
+        PR::store(WC, o, dh[0] * kc[j][0], dh[1] * kc[j][1]);
+      }
+    }
+  }
+  if (valid && w == 0 && hf == 0 && dh0 != nullptr) {
+    st(dh0, (long)b * hid + c, u[0]);
+    st(dh0, (long)b * hid + c + 1, u[1]);
+  }
+}
+
 template <typename T, int OP, bool LOGITS>
 int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, const void* h0, void* out, int bsz,
                int seq, int hid) {
-  constexpr int L = LIN_LF;
   const dim3 grid((hid + 63) / 64, bsz);
-  if (seq >= 512) {
-    constexpr int W = 16;
-    linscan_fwd_kernel<T, OP, LOGITS, L, W, LIN_PF><<<grid, 64 * W, 0, s>>>((const T*)g1, (const T*)g2, (const T*)cand,
-                                                                    (const T*)h0, (T*)out, seq, hid);
-  } else {
-    constexpr int W = 4;
-    linscan_fwd_kernel<T, OP, LOGITS, L, W, 2><<<grid, 64 * W, 0, s>>>((const T*)g1, (const T*)g2, (const T*)cand,
-                                                                    (const T*)h0, (T*)out, seq, hid);
+  const T* a = (const T*)g1;
+  const T* b = (const T*)g2;
+  const T* c = (const T*)cand;
+  const T* i = (const T*)h0;
+  T* o = (T*)out;
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (hid % 2 == 0) {  // two channels per lane
+      if (seq >= 512)
+        linscan2_fwd_kernel<T, OP, LOGITS, LIN2_LF, LIN2_W, LIN_PF><<<grid, 64 * LIN2_W, 0, s>>>(a, b, c, i, o, seq,
+                                                                                                hid);
+      else
+        linscan2_fwd_kernel<T, OP, LOGITS, LIN2_LF, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, o, seq, hid);
+      return check_launch(OP == OP_MINGRU ? "mingru scan" : "minlstm scan");
+    }
   }
+  if (seq >= 512)
+    linscan_fwd_kernel<T, OP, LOGITS, LIN_LF, 16, LIN_PF><<<grid, 64 * 16, 0, s>>>(a, b, c, i, o, seq, hid);
+  else
+    linscan_fwd_kernel<T, OP, LOGITS, LIN_LF, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, o, seq, hid);
   return check_launch(OP == OP_MINGRU ? "mingru scan" : "minlstm scan");
 }
 
 template <typename T, int OP, bool LOGITS>
 int launch_bwd(hipStream_t s, const void* g1, const void* g2, const void* cand, const void* h0, const void* fwd,
                const void* dy, void* d1, void* d2, void* dcand, void* dh0, int bsz, int seq, int hid) {
-  constexpr int L = LIN_LB;
   const dim3 grid((hid + 63) / 64, bsz);
-  if (seq >= 512) {
-    constexpr int W = 16;
-    linscan_bwd_kernel<T, OP, LOGITS, L, W, LIN_PB><<<grid, 64 * W, 0, s>>>(
-        (const T*)g1, (const T*)g2, (const T*)cand, (const T*)h0, (const T*)fwd, (const T*)dy, (T*)d1, (T*)d2,
-        (T*)dcand, (T*)dh0, seq, hid);
-  } else {
-    constexpr int W = 4;
-    linscan_bwd_kernel<T, OP, LOGITS, L, W, 2><<<grid, 64 * W, 0, s>>>(
-        (const T*)g1, (const T*)g2, (const T*)cand, (const T*)h0, (const T*)fwd, (const T*)dy, (T*)d1, (T*)d2,
-        (T*)dcand, (T*)dh0, seq, hid);
+  const T* a = (const T*)g1;
+  const T* b = (const T*)g2;
+  const T* c = (const T*)cand;
+  const T* i = (const T*)h0;
+  const T* f = (const T*)fwd;
+  const T* y = (const T*)dy;
+  T* o1 = (T*)d1;
+  T* o2 = (T*)d2;
+  T* oc = (T*)dcand;
+  T* oh = (T*)dh0;
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (hid % 2 == 0) {  // two channels per lane
+      if (seq >= 512)
+        linscan2_bwd_kernel<T, OP, LOGITS, LIN2_LB, LIN2_W, LIN_PB><<<grid, 64 * LIN2_W, 0, s>>>(a, b, c, i, f, y, o1,
+                                                                                                  o2, oc, oh, seq, hid);
+      else
+        linscan2_bwd_kernel<T, OP, LOGITS, LIN2_LB, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq,
+                                                                                   hid);
+      return check_launch(OP == OP_MINGRU ? "mingru scan backward" : "minlstm scan backward");
+    }
   }
+  if (seq >= 512)
+    linscan_bwd_kernel<T, OP, LOGITS, LIN_LB, 16, LIN_PB><<<grid, 64 * 16, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh,
+                                                                                    seq, hid);
+  else
+    linscan_bwd_kernel<T, OP, LOGITS, LIN_LB, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq, hid);
   return check_launch(OP == OP_MINGRU ? "mingru scan backward" : "minlstm scan backward");
 }
 
