@@ -164,7 +164,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
             p = (q >= T || mykey >= T || (CAUSAL && mykey > q)) ? 0.0f : p;
           }
           s[r] = p;
-          dp[r] = p * (dp[r] - dv4[e]) * scale;
+          dp[r] = p * (dp[r] - dv4[e]);  // dS / scale: 1/sqrt(d) is applied to dK once at the end
         }
       }
       // B fragments: queries 16 kc + 4 g + {0..3} and 16 kc + 8 + 4 g + {0..3}
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
         bf16x4 a, b;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          a[e] = (bf16)dkt[dt][rb * 4 + e];
+          a[e] = (bf16)(dkt[dt][rb * 4 + e] * scale);
           b[e] = (bf16)dvt[dt][rb * 4 + e];
         }
         *(bf16x4*)(krow + dt * 32 + 8 * rb + 4 * g) = a;
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
             const int key = k0 + h2 * 32 + d_row(r, g);
             p = (key >= T || myq >= T || (CAUSAL && key > myq)) ? 0.0f : p;
           }
-          s[h2][r] = p * (dp[h2][r] - myd) * scale;  // dS^T
+          s[h2][r] = p * (dp[h2][r] - myd);  // dS^T / scale: 1/sqrt(d) is applied to dQ at the end
         }
       bf16x8 db[4];
 #pragma unroll
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
       for (int rb = 0; rb < 4; ++rb) {
         bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (bf16)dqt[dt][rb * 4 + e];
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqt[dt][rb * 4 + e] * scale);
         *(bf16x4*)(qrow + dt * 32 + 8 * rb + 4 * g) = v;
       }
   }
