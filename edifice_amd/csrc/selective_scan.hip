@@ -14,10 +14,10 @@
 // Design.  The op is VALU-bound: per (b, t, d, n) element the forward needs one
 // v_exp_f32 (about 10 cycles per wave on MI355X, measured) and four VALU ops, several
 // times the HBM time at config-2 size.  The layout minimises everything else:
-//   * lane = channel d (64 channels per wave) holding K = 2 states in registers;
-//     NW = N / K waves per workgroup cover one 64-channel tile's N states (8 waves at
-//     N = 16, 2 waves per SIMD: enough to hide LDS and transcendental latency, which
-//     four states per lane at 1 wave per SIMD did not);
+//   * lane = channel d (64 channels per wave) holding K states in registers (one in the
+//     forward, two in the backward); NW = N / K waves per workgroup cover one 64-channel
+//     tile's N states (16 or 8 waves at N = 16: 4 or 2 waves per SIMD hide the LDS and
+//     transcendental latency, which four states per lane at 1 wave per SIMD did not);
 //   * the B[b, t, :] and C[b, t, :] values a wave needs are the same for all its lanes.
 //     Forward: a block's values are loaded into a few VGPRs (16 values per register,
 //     replicated over the four 16-lane rows) and broadcast with DPP row_newbcast, folded
@@ -661,14 +661,16 @@ void launch_fwd_k(hipStream_t s, const SSArgs& a) {
   }
 }
 
-// Two states per lane: 2 waves per SIMD at config-2 size (192 workgroups of 8 waves), which
-// hides the LDS and exp latencies better than four states per lane at 1 wave per SIMD
-// (measured on MI355X: 209 vs 247 us forward, 722 vs 811 us backward).
+// States per lane.  Backward: two (2 waves per SIMD at config-2 size, 192 workgroups of 8
+// waves), which hides the LDS and exp latencies better than four states per lane at 1 wave
+// per SIMD (measured on MI355X: 722 vs 811 us).  Forward: one (16 waves per workgroup, 4 per
+// SIMD; 190 vs 200 us with two states per lane, interleaved A/B).
 constexpr int SS_KMAX = 2;
+constexpr int SS_KMAX_FWD = 1;
 
 template <typename TI, typename TP, int N>
 void launch_fwd_t(hipStream_t s, const SSArgs& a) {
-  launch_fwd_k<TI, TP, N, SS_KMAX>(s, a);
+  launch_fwd_k<TI, TP, N, SS_KMAX_FWD>(s, a);
 }
 
 template <typename TI, typename TP>
