@@ -321,9 +321,22 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   float dD = 0.0f;
   const long rowbase = (long)b * seq * dim;
 
-  // raw values of the next chunk (in reverse order), loaded a chunk ahead
-  TI rx[EPT], rdt[EPT], rdo[EPT], rz[EPT];
-  TP rbc[BCT];
+  // raw values of the next chunk (in reverse order), loaded a chunk ahead through buffer
+  // resources on this batch row (SGPR base, 32-bit offsets: no 64-bit address VALU)
+  typedef typename Bits<TI>::type RI;
+  typedef typename Bits<TP>::type RP;
+  const unsigned rowbytes = (unsigned)((long)seq * dim * sizeof(TI));
+  const rsrc_t r_x = make_rsrc(x + rowbase, rowbytes), r_dt = make_rsrc(dt + rowbase, rowbytes);
+  const rsrc_t r_do = make_rsrc(dout + rowbase, rowbytes);
+  const rsrc_t r_z = make_rsrc(HAS_Z ? z + rowbase : x + rowbase, rowbytes);
+  const unsigned bcbytes = (unsigned)((long)seq * N * sizeof(TP));
+  const rsrc_t r_B = make_rsrc(Bm + (long)b * seq * N, bcbytes), r_C = make_rsrc(Cm + (long)b * seq * N, bcbytes);
+  const rsrc_t r_m =
+      make_rsrc(MEAN ? (const void*)(p.dtmean + (long)b * seq) : (const void*)x, (unsigned)(seq * sizeof(float)));
+  const rsrc_t r_dx = make_rsrc((TI*)p.dx + rowbase, rowbytes), r_ddt = make_rsrc((TI*)p.ddt + rowbase, rowbytes);
+  const rsrc_t r_dz = make_rsrc(p.dz != nullptr ? (TI*)p.dz + rowbase : (TI*)p.dx + rowbase, rowbytes);
+  RI rx[EPT], rdt[EPT], rdo[EPT], rz[EPT];
+  RP rbc[BCT];
   float rm[EPT];
   float rck[K];  // the checkpoint the fetched chunk starts from (its predecessor's state)
   // this thread's staged (t, d) values, kept for the per-(t, d) epilogues
@@ -332,19 +345,20 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int t = min(ts + w + i * NW, seq - 1);
-      const long idx = rowbase + (long)t * dim + cc;
-      rx[i] = x[idx];
-      rdt[i] = dt[idx];
-      rdo[i] = dout[idx];
-      if (HAS_Z) rz[i] = z[idx];
-      rm[i] = MEAN ? p.dtmean[(long)b * seq + t] : 0.0f;
+      const unsigned off = ((unsigned)t * dim + cc) * (unsigned)sizeof(TI);
+      rx[i] = bload<TI>(r_x, off);
+      rdt[i] = bload<TI>(r_dt, off);
+      rdo[i] = bload<TI>(r_do, off);
+      if (HAS_Z) rz[i] = bload<TI>(r_z, off);
+      rm[i] = MEAN ? bits_f32(bload<float>(r_m, (unsigned)t * 4u)) : 0.0f;
     }
 #pragma unroll
     for (int i = 0; i < BCT; ++i) {
       const int e = tid + i * NT;
       const int r = e % (2 * N);
-      const long row = (long)b * seq + min(ts + e / (2 * N), seq - 1);
-      rbc[i] = (r < N ? Bm : Cm)[row * N + (r % N)];
+      const unsigned off = ((unsigned)min(ts + e / (2 * N), seq - 1) * N + (r % N)) * (unsigned)sizeof(TP);
+      // lanes split between B and C: both loads issue, the other one out of bounds reads 0
+      rbc[i] = bload<TP>(r_B, r < N ? off : OOB_OFF) | bload<TP>(r_C, r < N ? OOB_OFF : off);
     }
     const int kp = max(ts / CK - 1, 0);  // chunk 0 starts from zero (selected at use)
 #pragma unroll
@@ -361,21 +375,21 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 #pragma unroll
     for (int i = 0; i < BCT; ++i) {
       const int e = tid + i * NT;
-      s_bc[e / (2 * N)][e % (2 * N)] = to_f32(rbc[i]);
+      s_bc[e / (2 * N)][e % (2 * N)] = bits_f32(rbc[i]);
     }
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int tt = w + i * NW;
       const bool ok = (ts + tt < seq) && cvalid;
-      const float dtr = to_f32(rdt[i]);
+      const float dtr = bits_f32(rdt[i]);
       const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
       const float dtb = ok ? (MEAN ? rm[i] : dtc) : 0.0f;
-      const float xv = ok ? to_f32(rx[i]) : 0.0f;
+      const float xv = ok ? bits_f32(rx[i]) : 0.0f;
       ex[i] = xv;
       edtb[i] = dtb;
       emask[i] = (ok && dtr >= DT_MIN && dtr <= DT_MAX) ? 1.0f : 0.0f;
-      ego[i] = ok ? to_f32(rdo[i]) : 0.0f;
-      ez[i] = (HAS_Z && ok) ? to_f32(rz[i]) : 0.0f;
+      ego[i] = ok ? bits_f32(rdo[i]) : 0.0f;
+      ez[i] = (HAS_Z && ok) ? bits_f32(rz[i]) : 0.0f;
       s_dtc[lane][tt] = dtc;
       s_dtx[lane][tt] = dtb * xv;
       if (!HAS_Z) {
@@ -439,8 +453,9 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         const float sg = sigmoidf(ez[i]);
         edy[i] = ego[i] * ez[i] * sg;
         s_dy[lane][tt] = edy[i];
-        if (p.dz != nullptr && ts + tt < seq && cvalid)
-          st((TI*)p.dz, rowbase + (long)(ts + tt) * dim + c, ego[i] * y * sg * (1.0f + ez[i] * (1.0f - sg)));
+        if (p.dz != nullptr)
+          bstore<TI>(r_dz, (ts + tt < seq && cvalid) ? ((unsigned)(ts + tt) * dim + c) * (unsigned)sizeof(TI) : OOB_OFF,
+                     ego[i] * y * sg * (1.0f + ez[i] * (1.0f - sg)));
       }
       __syncthreads();
     }
@@ -516,10 +531,10 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         pxs += pp(0, v, tt);
         pas += pp(1, v, tt);
       }
-      if (ts + tt < seq && cvalid) {
-        const long idx = rowbase + (long)(ts + tt) * dim + c;
-        st((TI*)p.dx, idx, fmaf(pxs, edtb[i], edy[i] * Dc));
-        st((TI*)p.ddt, idx, emask[i] * (MEAN ? pas : fmaf(pxs, ex[i], pas)));
+      {
+        const unsigned off = (ts + tt < seq && cvalid) ? ((unsigned)(ts + tt) * dim + c) * (unsigned)sizeof(TI) : OOB_OFF;
+        bstore<TI>(r_dx, off, fmaf(pxs, edtb[i], edy[i] * Dc));
+        bstore<TI>(r_ddt, off, emask[i] * (MEAN ? pas : fmaf(pxs, ex[i], pas)));
       }
       if (MEAN) s_m[tt][lane] = pxs * ex[i];  // dt-mean coupling, summed over channels below
     }
@@ -806,6 +821,11 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   EDF_REQUIRE(state == 4 || state == 8 || state == 16, EDF_ERR_UNSUPPORTED,
               "backward state size %d unsupported (4, 8 or 16)", state);
   EDF_REQUIRE(x && dt && A && B && C && grad_out && grad_x && grad_dt, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  // the backward kernel addresses one batch row of x, dt, dy, z, dx, ddt, dz (and of B, C)
+  // through a buffer resource with 32-bit byte offsets
+  EDF_REQUIRE((long)seq_len * hidden * (io_dtype == EDF_BF16 ? 2 : 4) < (1L << 31) &&
+                  (long)seq_len * (state > 1 ? state : 1) * 4 < (1L << 31),
+              EDF_ERR_UNSUPPORTED, "backward needs seq_len * hidden elements of one batch row below 2 GiB");
   const bool mean_mode = mode == EDF_SS_DT_MEAN;
   const WsLayout L = bwd_layout(batch, seq_len, hidden, state, states == nullptr, mean_mode);
   EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
