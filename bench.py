@@ -10,8 +10,9 @@ Algorithmic bytes (per call, what roofline.achieved divides by):
   selective scan fwd = 4*B*T*D*2 (u, dt, z, y) + 2*B*T*N*4 (B, C) + D*N*4 + D*4
   selective scan bwd = 7*B*T*D*2 (u, dt, z, dy in; du, ddt, dz out) + 4*B*T*N*4 + 2*(D*N*4 + D*4)
   MinGRU fwd = 3*B*T*H*s, bwd = 6*B*T*H*s (s = element size)
+  linear scan fwd = 3*B*T*H*s (a, b in; h out), bwd = 5*B*T*H*s (a, h, dy in; da, db out)
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru,linear]
 """
 from __future__ import annotations
 
@@ -145,6 +146,44 @@ def bench_mingru(torch, steps, warmup, B, T, H, dtype):
     s = gates.element_size()
     fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
     fb, bb = 3 * B * T * H * s, 6 * B * T * H * s
+    return dict(shape=[B, T, H], dtype=str(dtype).replace("torch.", ""), fwd_us=fwd_ms * 1e3, bwd_us=bwd_ms * 1e3,
+                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
+
+
+def bench_linear_scan(torch, steps, warmup, B, T, H, dtype):
+    """Generic linear scan h_t = a_t h_{t-1} + b_t (fwd reads a, b, writes h; bwd reads a,
+    h, dy, writes da, db)."""
+    from edifice_amd import _native as nat
+
+    dev = "cuda"
+    g = torch.Generator(device="cuda").manual_seed(1001)
+    a = torch.rand(B, T, H, device=dev, generator=g).to(dtype)
+    b = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
+    dy = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
+    out, da, db = torch.empty_like(a), torch.empty_like(a), torch.empty_like(a)
+    flag = 1 if dtype == torch.bfloat16 else 0
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_linear_scan", stream, P(a), P(b), None, P(out), B, T, H, flag)
+
+    def bwd():
+        nat.call("edf_fused_linear_scan_backward", stream, P(a), None, P(out), P(dy), P(da), P(db), None, B, T, H,
+                 flag)
+
+    for _ in range(warmup):
+        fwd()
+        bwd()
+    tf, tb = EventTimer(torch), EventTimer(torch)
+    for _ in range(steps):
+        with tf:
+            fwd()
+        with tb:
+            bwd()
+    s = a.element_size()
+    fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
+    fb, bb = 3 * B * T * H * s, 5 * B * T * H * s
     return dict(shape=[B, T, H], dtype=str(dtype).replace("torch.", ""), fwd_us=fwd_ms * 1e3, bwd_us=bwd_ms * 1e3,
                 fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
 
@@ -341,6 +380,10 @@ def main():
         for dt in (torch.bfloat16, torch.float32):
             key = f"mingru_bw_{str(dt).replace('torch.', '')}_8x2048x1536"
             configs[key] = bench_mingru(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
+    if want("linear"):
+        for dt in (torch.bfloat16, torch.float32):
+            key = f"linear_scan_{str(dt).replace('torch.', '')}_8x2048x1536"
+            configs[key] = bench_linear_scan(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
     ss = bench_selective_scan(torch, args.steps, args.warmup)
     configs["c2_selective_scan"] = ss
     if want("delta"):

@@ -26,6 +26,8 @@ SIGNATURES = {
     "edf_fused_minlstm_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I]),
     "edf_minlstm": (I, [P, P, P, P, P, I, I, I, I]),
     "edf_minlstm_backward": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I]),
+    "edf_fused_linear_scan": (I, [P, P, P, P, P, I, I, I, I]),
+    "edf_fused_linear_scan_backward": (I, [P, P, P, P, P, P, P, P, I, I, I, I]),
     "edf_fused_selective_scan": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
     "edf_selective_scan_states_bytes": (S, [I, I, I, I]),
     "edf_selective_scan_workspace_bytes": (S, [I, I, I, I, I]),

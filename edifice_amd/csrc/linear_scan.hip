@@ -1,6 +1,10 @@
-// MinGRU / MinLSTM linear scans, forward and backward, for gfx950.
+// MinGRU / MinLSTM and generic linear scans, forward and backward, for gfx950.
 //
 // Semantics (reference):
+//   linear  h_t = a_t h_{t-1} + b_t   (a, b given; Griffin, MEGA, GSS, MambaVision, ...)
+//           native/cuda/fused_linear_scan.cu:42-64, fused_scan.ex:171-185, 4429-4443
+//           backward fused_linear_scan_backward.cu:42-80, fused_scan.ex:884-910
+//           (da = dh h_{t-1}, db = dh, dh0 = a_0 dh_0)
 //   MinGRU  h_t = (1 - z_t) h_{t-1} + z_t c_t
 //           native/cuda/fused_mingru_scan.cu:38-65, lib/edifice/cuda/fused_scan.ex:516-528
 //           backward fused_scan.ex:548-581 (dz = dh (c - h_{t-1}), dc = dh z, dh0)
@@ -42,14 +46,17 @@ constexpr int LIN_LB = 4, LIN_PB = 2;  // backward (five inputs per step)
 // two channels per lane (bf16): 8 waves = 16 virtual waves of L steps (more waves spill)
 constexpr int LIN2_LF = 8, LIN2_LB = 4, LIN2_W = 8;
 
-enum { OP_MINGRU = 0, OP_MINLSTM = 1 };
+enum { OP_MINGRU = 0, OP_MINLSTM = 1, OP_LINEAR = 2 };  // OP_LINEAR: a, b given directly
 
 // Coefficients of step t: h_t = a h_{t-1} + b.
 template <int OP, bool LOGITS>
 struct Step {
   float a, b;
   EDF_DEVICE void make(float g1, float g2, float c) {
-    if (OP == OP_MINGRU) {
+    if (OP == OP_LINEAR) {
+      a = g1;
+      b = c;
+    } else if (OP == OP_MINGRU) {
       const float z = LOGITS ? sigmoidf(g1) : g1;
       a = 1.0f - z;
       b = z * c;
@@ -178,7 +185,7 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
   const unsigned bytes = (unsigned)((long)seq * hid * ES);
   const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
   const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
-  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RC = make_rsrc((OP == OP_LINEAR ? g1 : cand) + slab, bytes);  // b is not needed
   const rsrc_t RH = make_rsrc(fwd + slab, bytes);
   const rsrc_t RY = make_rsrc(dy + slab, bytes);
   const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
@@ -206,7 +213,7 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
       const unsigned o = off(t0 + j);
       r1[slot][j] = bload<T>(R1, o);
       if (OP == OP_MINLSTM) r2[slot][j] = bload<T>(R2, o);
-      rc[slot][j] = bload<T>(RC, o);
+      if (OP != OP_LINEAR) rc[slot][j] = bload<T>(RC, o);
       rh[slot][j] = bload<T>(RH, offp(t0 + j));
       ry[slot][j] = bload<T>(RY, o);
     }
@@ -222,6 +229,7 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
       const int t0 = first_t(ms);
       // Per step only the decay a, the input gradient g and the coefficients that map
       // dh_t to each output gradient are kept; the ring slot is refilled right after.
+      //   linear:  da = dh h_{t-1},  db = dh
       //   MinGRU:  dz = dh (c - h_{t-1}) [z (1 - z)],  dc = dh z
       //   MinLSTM: df = dh (h_{t-1} (i + eps) - c i) / s^2 [f (1 - f)],
       //            di = dh (c (f + eps) - h_{t-1} f) / s^2 [i (1 - i)],  dc = dh i / s
@@ -232,10 +240,15 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
         const bool ok = valid && t < seq;
         const float x1 = bits_f32(r1[sl][j]);
         const float x2 = OP == OP_MINLSTM ? bits_f32(r2[sl][j]) : 0.0f;
-        const float cv = bits_f32(rc[sl][j]);
+        const float cv = OP == OP_LINEAR ? 0.0f : bits_f32(rc[sl][j]);
         const float hp = t > 0 ? bits_f32(rh[sl][j]) : h0v;
         gy[j] = bits_f32(ry[sl][j]);  // 0 outside the sequence
-        if (OP == OP_MINGRU) {
+        if (OP == OP_LINEAR) {
+          a[j] = ok ? x1 : 1.0f;
+          k1[j] = hp;
+          k2[j] = 0.0f;
+          kc[j] = 1.0f;
+        } else if (OP == OP_MINGRU) {
           const float z = LOGITS ? sigmoidf(x1) : x1;
           a[j] = ok ? 1.0f - z : 1.0f;  // padding steps are the identity map
           k1[j] = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
@@ -459,7 +472,7 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
   const unsigned bytes = (unsigned)((long)seq * hid * ES);
   const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
   const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
-  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RC = make_rsrc((OP == OP_LINEAR ? g1 : cand) + slab, bytes);  // b is not needed
   const rsrc_t RH = make_rsrc(fwd + slab, bytes);
   const rsrc_t RY = make_rsrc(dy + slab, bytes);
   const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
@@ -487,7 +500,7 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
       const unsigned o = off(t0 + j);
       r1[slot][j] = PR::load(R1, o);
       if (OP == OP_MINLSTM) r2[slot][j] = PR::load(R2, o);
-      rc[slot][j] = PR::load(RC, o);
+      if (OP != OP_LINEAR) rc[slot][j] = PR::load(RC, o);
       rh[slot][j] = PR::load(RH, offp(t0 + j));
       ry[slot][j] = PR::load(RY, o);
     }
@@ -511,10 +524,15 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
         for (int k = 0; k < 2; ++k) {
           const float x1 = k ? PR::hi(r1[sl][j]) : PR::lo(r1[sl][j]);
           const float x2 = OP == OP_MINLSTM ? (k ? PR::hi(r2[sl][j]) : PR::lo(r2[sl][j])) : 0.0f;
-          const float cv = k ? PR::hi(rc[sl][j]) : PR::lo(rc[sl][j]);
+          const float cv = OP == OP_LINEAR ? 0.0f : (k ? PR::hi(rc[sl][j]) : PR::lo(rc[sl][j]));
           const float hp = t > 0 ? (k ? PR::hi(rh[sl][j]) : PR::lo(rh[sl][j])) : h0v[k];
           gy[j][k] = k ? PR::hi(ry[sl][j]) : PR::lo(ry[sl][j]);  // 0 outside the sequence
-          if (OP == OP_MINGRU) {
+          if (OP == OP_LINEAR) {
+            a[j][k] = ok ? x1 : 1.0f;
+            k1[j][k] = hp;
+            k2[j][k] = 0.0f;
+            kc[j][k] = 1.0f;
+          } else if (OP == OP_MINGRU) {
             const float z = LOGITS ? sigmoidf(x1) : x1;
             a[j][k] = ok ? 1.0f - z : 1.0f;
             k1[j][k] = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
@@ -599,6 +617,13 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
   }
 }
 
+inline const char* op_name(int op, bool backward = false) {
+  static const char* const names[3][2] = {{"mingru scan", "mingru scan backward"},
+                                          {"minlstm scan", "minlstm scan backward"},
+                                          {"linear scan", "linear scan backward"}};
+  return names[op][backward ? 1 : 0];
+}
+
 template <typename T, int OP, bool LOGITS>
 int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, const void* h0, void* out, int bsz,
                int seq, int hid) {
@@ -615,14 +640,14 @@ int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
                                                                                                 hid);
       else
         linscan2_fwd_kernel<T, OP, LOGITS, LIN2_LF, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, o, seq, hid);
-      return check_launch(OP == OP_MINGRU ? "mingru scan" : "minlstm scan");
+      return check_launch(op_name(OP));
     }
   }
   if (seq >= 512)
     linscan_fwd_kernel<T, OP, LOGITS, LIN_LF, 16, LIN_PF><<<grid, 64 * 16, 0, s>>>(a, b, c, i, o, seq, hid);
   else
     linscan_fwd_kernel<T, OP, LOGITS, LIN_LF, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, o, seq, hid);
-  return check_launch(OP == OP_MINGRU ? "mingru scan" : "minlstm scan");
+  return check_launch(op_name(OP));
 }
 
 template <typename T, int OP, bool LOGITS>
@@ -647,7 +672,7 @@ int launch_bwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
       else
         linscan2_bwd_kernel<T, OP, LOGITS, LIN2_LB, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq,
                                                                                    hid);
-      return check_launch(OP == OP_MINGRU ? "mingru scan backward" : "minlstm scan backward");
+      return check_launch(op_name(OP, true));
     }
   }
   if (seq >= 512)
@@ -655,7 +680,7 @@ int launch_bwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
                                                                                     seq, hid);
   else
     linscan_bwd_kernel<T, OP, LOGITS, LIN_LB, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq, hid);
-  return check_launch(OP == OP_MINGRU ? "mingru scan backward" : "minlstm scan backward");
+  return check_launch(op_name(OP, true));
 }
 
 template <int OP, bool LOGITS>
@@ -665,7 +690,7 @@ int fwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand,
   EDF_REQUIRE((long)seq * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
               "seq_len * hidden too large (one batch row must stay below 2 GiB)");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
-  EDF_REQUIRE(g1 && cand && out && (OP == OP_MINGRU || g2), EDF_ERR_INVALID_ARG, "null tensor pointer");
+  EDF_REQUIRE(g1 && cand && out && (OP != OP_MINLSTM || g2), EDF_ERR_INVALID_ARG, "null tensor pointer");
   if (dtype == EDF_BF16) return launch_fwd<bf16, OP, LOGITS>(as_stream(stream), g1, g2, cand, h0, out, bsz, seq, hid);
   return launch_fwd<float, OP, LOGITS>(as_stream(stream), g1, g2, cand, h0, out, bsz, seq, hid);
 }
@@ -677,8 +702,8 @@ int bwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand,
   EDF_REQUIRE((long)seq * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
               "seq_len * hidden too large (one batch row must stay below 2 GiB)");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
-  EDF_REQUIRE(g1 && cand && fwd && dy && d1 && dcand && (OP == OP_MINGRU || (g2 && d2)), EDF_ERR_INVALID_ARG,
-              "null tensor pointer");
+  EDF_REQUIRE(g1 && (OP == OP_LINEAR || cand) && fwd && dy && d1 && dcand && (OP != OP_MINLSTM || (g2 && d2)),
+              EDF_ERR_INVALID_ARG, "null tensor pointer");
   if (dtype == EDF_BF16)
     return launch_bwd<bf16, OP, LOGITS>(as_stream(stream), g1, g2, cand, h0, fwd, dy, d1, d2, dcand, dh0, bsz, seq,
                                         hid);
@@ -741,6 +766,18 @@ int edf_minlstm_backward(void* stream, const void* forget_gates, const void* inp
   return edf::bwd_dispatch<edf::OP_MINLSTM, true>(stream, forget_gates, input_gates, cand, nullptr, forward_out,
                                                   grad_out, grad_forget, grad_input, grad_cand, nullptr, batch,
                                                   seq_len, hidden, dtype);
+}
+
+int edf_fused_linear_scan(void* stream, const void* a, const void* b, const void* h0, void* out, int batch,
+                          int seq_len, int hidden, int dtype) {
+  return edf::fwd_dispatch<edf::OP_LINEAR, false>(stream, a, nullptr, b, h0, out, batch, seq_len, hidden, dtype);
+}
+
+int edf_fused_linear_scan_backward(void* stream, const void* a, const void* h0, const void* forward_out,
+                                   const void* grad_out, void* grad_a, void* grad_b, void* grad_h0, int batch,
+                                   int seq_len, int hidden, int dtype) {
+  return edf::bwd_dispatch<edf::OP_LINEAR, false>(stream, a, nullptr, nullptr, h0, forward_out, grad_out, grad_a,
+                                                  nullptr, grad_b, grad_h0, batch, seq_len, hidden, dtype);
 }
 
 }  // extern "C"

@@ -126,6 +126,58 @@ def minlstm(forget_gates: torch.Tensor, input_gates: torch.Tensor, candidates: t
 
 
 # ---------------------------------------------------------------------------
+# Generic linear scan
+# ---------------------------------------------------------------------------
+
+class _LinearScan(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, a, b):
+        a, b = a.contiguous(), b.contiguous()
+        _dev(a, b)
+        _same(a, b)
+        bsz, seq, hid = a.shape
+        if b.shape != a.shape:
+            raise EdificeHipError(f"shape mismatch: a {tuple(a.shape)} vs b {tuple(b.shape)}")
+        out = torch.empty_like(a)
+        nat.call("edf_fused_linear_scan", _stream(), _p(a), _p(b), None, _p(out), bsz, seq, hid, dtype_flag(a))
+        ctx.save_for_backward(a, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        a, out = ctx.saved_tensors
+        da, db, _ = linear_scan_backward(a, None, out, dy.contiguous().to(a.dtype))
+        return da, db
+
+
+def linear_scan(a_vals: torch.Tensor, b_vals: torch.Tensor) -> torch.Tensor:
+    """``FusedScan.linear_scan/2`` (fused_scan.ex:171-185): h_t = a_t h_{t-1} + b_t, h0 = 0.
+
+    a_vals, b_vals: [B, T, H] precomputed coefficients (no activation inside);
+    returns all hidden states.  The backward is the fused reverse scan
+    (``linear_scan_backward``), as the reference's custom_grad (fused_scan.ex:834-849).
+    """
+    return _LinearScan.apply(a_vals, b_vals)
+
+
+def linear_scan_backward(a_vals, h0, forward_out, grad_output):
+    """``linear_scan_backward_fallback/4`` (fused_scan.ex:884-915) on the GPU -> (da, db, dh0).
+
+    h0 may be None (zeros).  da = dh h_{t-1}, db = dh, dh0 = a_0 dh_0.
+    """
+    a_vals, forward_out, grad_output = a_vals.contiguous(), forward_out.contiguous(), grad_output.contiguous()
+    h0 = _c(h0)
+    _dev(a_vals, h0, forward_out, grad_output)
+    _same(a_vals, h0, forward_out, grad_output)
+    bsz, seq, hid = a_vals.shape
+    da, db = torch.empty_like(a_vals), torch.empty_like(a_vals)
+    dh0 = torch.empty((bsz, hid), dtype=a_vals.dtype, device=a_vals.device)
+    nat.call("edf_fused_linear_scan_backward", _stream(), _p(a_vals), _p(h0), _p(forward_out), _p(grad_output),
+             _p(da), _p(db), _p(dh0), bsz, seq, hid, dtype_flag(a_vals))
+    return da, db, dh0
+
+
+# ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------
 

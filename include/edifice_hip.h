@@ -108,6 +108,25 @@ int edf_minlstm_backward(void* stream, const void* forget_gates, const void* inp
                          void* grad_cand, int batch, int seq_len, int hidden, int dtype);
 
 /* ------------------------------------------------------------------------
+ * Generic linear scan  h_t = a_t h_{t-1} + b_t   (a, b precomputed by the caller)
+ * ------------------------------------------------------------------------ */
+
+/* Replaces fused_linear_scan/7 (a_ptr, b_ptr, h0_ptr, batch, seq_len, hidden, dtype),
+ * c_src/edifice_cuda_nif.c:891-899 -> fused_linear_scan_launch
+ * (native/cuda/fused_linear_scan.cu:77-95); h0 may be NULL (zeros, as
+ * fused_scan.ex:2950-2957 passes). */
+int edf_fused_linear_scan(void* stream, const void* a, const void* b, const void* h0, void* out, int batch,
+                          int seq_len, int hidden, int dtype);
+
+/* Replaces fused_linear_scan_backward/8 (a_ptr, h0_ptr, fwd_ptr, grad_ptr, batch,
+ * seq_len, hidden, dtype), c_src/edifice_cuda_nif.c:2414-2474, whose single output
+ * buffer [grad_a | grad_b | grad_h0] becomes three pointers here (grad_h0 may be NULL);
+ * da = dh h_{t-1}, db = dh, dh0 = a_0 dh_0 (fused_linear_scan_backward.cu:42-80). */
+int edf_fused_linear_scan_backward(void* stream, const void* a, const void* h0, const void* forward_out,
+                                   const void* grad_out, void* grad_a, void* grad_b, void* grad_h0, int batch,
+                                   int seq_len, int hidden, int dtype);
+
+/* ------------------------------------------------------------------------
  * Mamba selective scan
  *   x, dt, z, out, grad_x, grad_dt, grad_z: [B, T, D] in io_dtype
  *   A [D, N], B, C [B, T, N], D [D]: param_dtype; grad_A/B/C/D: float32

@@ -9,6 +9,10 @@ Layouts follow the reference exactly:
   attention            [batch, heads, seq, head_dim]
 
 Pinning (what independently checks each function; see tests/test_oracle_*.py):
+  linear_scan / _backward       seq_len=1 known answer (backward_kernels_test.exs:76-95),
+                                a≡1 ⇒ cumulative sum, a≡0 ⇒ b, a = 1 - z, b = z h~ ⇒
+                                mingru_scan, torch autograd of a closed-form
+                                (cumulative-product) forward, finite differences.
   mingru_scan / _backward       seq_len=1 known answer (backward_kernels_test.exs:271-287),
                                 min_gru_random.safetensors block fixture, z≡1 / z≡0
                                 closed forms, torch autograd + finite differences.
@@ -112,6 +116,50 @@ def min_gru_scan_backward(gates, cand, dy):
     fwd = mingru_scan(z, cand, None)
     dz, dc, _ = mingru_scan_backward(z, cand, None, fwd, dy)
     return dz * z * (1.0 - z), dc
+
+
+# ---------------------------------------------------------------------------
+# Generic linear scan  h_t = a_t h_{t-1} + b_t
+# ---------------------------------------------------------------------------
+
+def linear_scan(a, b, h0=None):
+    """Forward -> all hidden states.
+
+    Follows ``linear_scan_cc_fallback`` / ``linear_scan_fallback``
+    (lib/edifice/cuda/fused_scan.ex:869-881, 4429-4443) and the kernel contract of
+    native/cuda/fused_linear_scan.cu:42-64; h0 = None means zeros.
+    """
+    a, b, h0 = _f64(a, b, h0)
+    bsz, seq, hid = a.shape
+    h = np.zeros((bsz, hid)) if h0 is None else h0.copy()
+    out = np.empty_like(a)
+    for t in range(seq):
+        h = a[:, t] * h + b[:, t]
+        out[:, t] = h
+    return out
+
+
+def linear_scan_backward(a, h0, fwd, dy):
+    """Reverse pass -> (da, db, dh0).
+
+    Follows ``linear_scan_backward_fallback`` (fused_scan.ex:884-915) and
+    native/cuda/fused_linear_scan_backward.cu:42-80: dh = dy_t + carry,
+    da_t = dh h_{t-1}, db_t = dh, carry = dh a_t; dh0 is the final carry.
+    """
+    a, h0, fwd, dy = _f64(a, h0, fwd, dy)
+    bsz, seq, hid = a.shape
+    if h0 is None:
+        h0 = np.zeros((bsz, hid))
+    da = np.empty_like(a)
+    db = np.empty_like(a)
+    carry = np.zeros((bsz, hid))
+    for t in range(seq - 1, -1, -1):
+        dh = dy[:, t] + carry
+        h_prev = h0 if t == 0 else fwd[:, t - 1]
+        da[:, t] = dh * h_prev
+        db[:, t] = dh
+        carry = dh * a[:, t]
+    return da, db, carry
 
 
 # ---------------------------------------------------------------------------

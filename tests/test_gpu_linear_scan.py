@@ -1,4 +1,4 @@
-"""GPU parity: MinGRU / MinLSTM scans (HIP, through the C ABI) vs the CPU oracle."""
+"""GPU parity: MinGRU / MinLSTM / generic linear scans (HIP, through the C ABI) vs the CPU oracle."""
 import ctypes
 
 import numpy as np
@@ -11,7 +11,8 @@ from tests.gpu_util import TOL, announce, host, rounded, to_dev
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1, 1, 2), (4, 60, 256), (2, 37, 100), (3, 129, 64), (2, 700, 130), (1, 2048, 96)]
+# odd hidden sizes take the one-channel-per-lane bf16 kernels, even ones the channel-pair kernels
+SHAPES = [(1, 1, 2), (4, 60, 256), (2, 37, 100), (3, 129, 64), (2, 700, 130), (1, 2048, 96), (2, 45, 77)]
 DTYPES = [torch.float32, torch.bfloat16]
 
 
@@ -132,3 +133,81 @@ def test_mingru_bandwidth_shape_full_size(dtype, rng):
     # z -> 1 (large logits): h == cand exactly up to storage rounding
     big = torch.full_like(tg, 30.0)
     assert torch.allclose(fs.mingru(big, tc).float(), tc.float(), rtol=0, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# generic linear scan  h_t = a_t h_{t-1} + b_t
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_scan_fwd_bwd(shape, dtype, rng):
+    """FusedScan.linear_scan/2 with its custom_grad backward (h0 = 0)."""
+    from edifice_amd import fused_scan as fs
+    announce("linear_scan", shape=shape, dtype=dtype)
+    a = rng.uniform(-0.99, 0.99, size=shape)
+    b, dy = rng.normal(size=shape), rng.normal(size=shape)
+    ta, tb = to_dev(a, dtype).requires_grad_(), to_dev(b, dtype).requires_grad_()
+    out = fs.linear_scan(ta, tb)
+    out.backward(to_dev(dy, dtype))
+    ar, br, dyr = rounded(a, dtype), rounded(b, dtype), rounded(dy, dtype)
+    fwd = scans.linear_scan(ar, br)
+    assert_close(host(out), fwd, TOL[dtype], "h")
+    da, db, _ = scans.linear_scan_backward(ar, None, rounded(host(out), dtype), dyr)
+    assert_close(host(ta.grad), da, TOL[dtype], "da")
+    assert_close(host(tb.grad), db, TOL[dtype], "db")
+
+
+@pytest.mark.parametrize("shape", [(4, 60, 256), (2, 33, 70), (3, 50, 31)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_scan_reference_shaped_entry_points(shape, dtype, rng):
+    """edf_fused_linear_scan / _backward with an explicit h0 (and with h0 = NULL)."""
+    announce("linear_nif_shaped", shape=shape, dtype=dtype)
+    bsz, seq, hid = shape
+    flag = 1 if dtype == torch.bfloat16 else 0
+    a = rng.uniform(-1.0, 1.0, size=shape)
+    b, dy = rng.normal(size=shape), rng.normal(size=shape)
+    h0 = rng.normal(size=(bsz, hid))
+    ta, tb, tdy, th0 = (to_dev(x, dtype) for x in (a, b, dy, h0))
+    ar, br, dyr, h0r = (rounded(x, dtype) for x in (a, b, dy, h0))
+    tol = TOL[dtype]
+    for with_h0 in (True, False):
+        out = torch.empty_like(ta)
+        _call("edf_fused_linear_scan", ta, tb, th0 if with_h0 else None, out, bsz, seq, hid, flag)
+        assert_close(host(out), scans.linear_scan(ar, br, h0r if with_h0 else None), tol, "h")
+        ga, gb, gh = torch.empty_like(ta), torch.empty_like(ta), torch.empty_like(th0)
+        _call("edf_fused_linear_scan_backward", ta, th0 if with_h0 else None, out, tdy, ga, gb, gh, bsz, seq, hid,
+              flag)
+        ea, eb, eh = scans.linear_scan_backward(ar, h0r if with_h0 else None, rounded(host(out), dtype), dyr)
+        for x, e, n in ((ga, ea, "da"), (gb, eb, "db"), (gh, eh, "dh0")):
+            assert_close(host(x), e, tol, n)
+
+
+def test_linear_scan_seq1_known_answer():
+    """backward_kernels_test.exs:76-95 through the HIP entry points: a = 0.5, b = 1."""
+    announce("linear_known_answer")
+    f32 = dict(dtype=torch.float32, device="cuda")
+    a, b, h0 = torch.full((1, 1, 1), 0.5, **f32), torch.ones(1, 1, 1, **f32), torch.zeros(1, 1, **f32)
+    out = torch.empty_like(a)
+    _call("edf_fused_linear_scan", a, b, h0, out, 1, 1, 1, 0)
+    assert out.item() == 1.0
+    ga, gb, gh = torch.empty_like(a), torch.empty_like(a), torch.empty_like(h0)
+    _call("edf_fused_linear_scan_backward", a, h0, out, torch.ones_like(a), ga, gb, gh, 1, 1, 1, 0)
+    assert (ga.item(), gb.item(), gh.item()) == (0.0, 1.0, 0.5)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_linear_scan_full_size(dtype, rng):
+    """B=8, T=2048, H=1536 against the oracle, plus the a = 1 (cumulative sum) and a = 0 cases."""
+    from edifice_amd import fused_scan as fs
+    shape = (8, 2048, 1536)
+    announce("linear_full", shape=shape, dtype=dtype)
+    a = rng.uniform(0.0, 1.0, size=shape).astype(np.float32)
+    b = rng.normal(size=shape).astype(np.float32)
+    ta, tb = to_dev(a, dtype), to_dev(b, dtype)
+    out = fs.linear_scan(ta, tb)
+    assert_close(host(out), scans.linear_scan(rounded(a, dtype), rounded(b, dtype)), TOL[dtype], "h full")
+    assert torch.equal(fs.linear_scan(torch.zeros_like(ta), tb), tb)
+    cs = fs.linear_scan(torch.ones_like(ta), tb).float()
+    ref = torch.cumsum(tb.float(), dim=1)
+    assert ((cs - ref).abs().max() / ref.abs().max()).item() < (1e-5 if dtype == torch.float32 else 2e-2)

@@ -56,6 +56,55 @@ def test_mingru_backward_vs_autograd(rng):
     assert_close(dg, tg.grad.numpy(), 1e-12, "dgates")
 
 
+def torch_linear_closed_form(a, b, h0):
+    """h_t = sum_{s<=t} (prod_{s<r<=t} a_r) b_s + (prod_{r<=t} a_r) h0, built from
+    cumulative products (not the recurrence the oracle restates)."""
+    T = a.shape[1]
+    out = []
+    for t in range(T):
+        h = torch.prod(a[:, :t + 1], dim=1) * h0
+        for s in range(t + 1):
+            h = h + torch.prod(a[:, s + 1:t + 1], dim=1) * b[:, s]
+        out.append(h)
+    return torch.stack(out, 1)
+
+
+def test_linear_scan_forward_backward_vs_autograd(rng):
+    a = rng.uniform(-1.1, 1.1, size=(2, 9, 4))
+    b = rng.normal(size=a.shape)
+    h0 = rng.normal(size=(2, 4))
+    dy = rng.normal(size=a.shape)
+    ta, tb, th = _t(a), _t(b), _t(h0)
+    out = torch_linear_closed_form(ta, tb, th)
+    fwd = scans.linear_scan(a, b, h0)
+    assert_close(fwd, out.detach().numpy(), 1e-12, "h")
+    out.backward(torch.from_numpy(dy))
+    da, db, dh0 = scans.linear_scan_backward(a, h0, fwd, dy)
+    for x, e, n in ((da, ta.grad, "da"), (db, tb.grad, "db"), (dh0, th.grad, "dh0")):
+        assert_close(x, e.numpy(), 1e-12, n)
+
+
+def test_linear_scan_backward_finite_difference(rng):
+    """backward_kernels_test.exs:52-74 (finite differences of sum(forward))."""
+    a = rng.uniform(0.2, 0.8, size=(1, 5, 3))
+    b = rng.uniform(-0.5, 0.5, size=a.shape)
+    h0 = rng.normal(size=(1, 3))
+    dy = rng.normal(size=a.shape)
+    da, db, dh0 = scans.linear_scan_backward(a, h0, scans.linear_scan(a, b, h0), dy)
+    eps = 1e-6
+    for name, arr, g in (("da", a, da), ("db", b, db), ("dh0", h0, dh0)):
+        num = np.zeros_like(arr)
+        for idx in np.ndindex(arr.shape):
+            old = arr[idx]
+            arr[idx] = old + eps
+            fp = (scans.linear_scan(a, b, h0) * dy).sum()
+            arr[idx] = old - eps
+            fm = (scans.linear_scan(a, b, h0) * dy).sum()
+            arr[idx] = old
+            num[idx] = (fp - fm) / (2 * eps)
+        assert_close(g, num, 1e-7, name)
+
+
 def test_minlstm_backward_vs_autograd(rng):
     f = rng.uniform(0.05, 0.95, size=(2, 11, 5))
     i = rng.uniform(0.05, 0.95, size=f.shape)

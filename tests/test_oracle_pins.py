@@ -97,6 +97,16 @@ def test_linear_scan_seq1_known_answer_via_mingru():
     assert dc[0, 0, 0] / z[0, 0, 0] == pytest.approx(1.0)
 
 
+def test_linear_scan_seq1_known_answer():
+    """backward_kernels_test.exs:76-95: a = 0.5, b = 1, h0 = 0 -> h = 1, da = 0, db = 1,
+    dh0 = 0.5."""
+    a, b, h0 = np.array([[[0.5]]]), np.array([[[1.0]]]), np.zeros((1, 1))
+    fwd = scans.linear_scan(a, b, h0)
+    assert fwd[0, 0, 0] == 1.0
+    da, db, dh0 = scans.linear_scan_backward(a, h0, fwd, np.ones((1, 1, 1)))
+    assert (da[0, 0, 0], db[0, 0, 0], dh0[0, 0]) == (0.0, 1.0, 0.5)
+
+
 # ---------------------------------------------------------------------------
 # invariants / closed forms
 # ---------------------------------------------------------------------------
@@ -115,6 +125,30 @@ def test_mingru_invariants(rng):
     for s in range(T):
         expect = expect + np.prod(1 - z[:, s + 1:], axis=1) * z[:, s] * cand[:, s]
     np.testing.assert_allclose(h[:, -1], expect, rtol=1e-12)
+
+
+def test_linear_scan_invariants(rng):
+    b = rng.normal(size=(2, 9, 5))
+    h0 = rng.normal(size=(2, 5))
+    # a = 1: cumulative sum from h0;  a = 0: h_t = b_t
+    np.testing.assert_allclose(scans.linear_scan(np.ones_like(b), b, h0), h0[:, None] + np.cumsum(b, axis=1),
+                               rtol=1e-12)
+    np.testing.assert_allclose(scans.linear_scan(np.zeros_like(b), b, h0), b)
+    # a constant alpha, b constant beta, h0 = 0: h_t = beta (1 - alpha^(t+1)) / (1 - alpha)
+    alpha, beta = 0.7, -1.3
+    out = scans.linear_scan(np.full((1, 12, 1), alpha), np.full((1, 12, 1), beta))
+    t = np.arange(12)
+    np.testing.assert_allclose(out[0, :, 0], beta * (1 - alpha ** (t + 1)) / (1 - alpha), rtol=1e-12)
+    # a = 1 - z, b = z c is MinGRU (forward and backward)
+    z = rng.uniform(0.05, 0.95, size=b.shape)
+    fwd = scans.linear_scan(1 - z, z * b, h0)
+    np.testing.assert_allclose(fwd, scans.mingru_scan(z, b, h0), rtol=1e-12)
+    dy = rng.normal(size=b.shape)
+    da, db, dh0 = scans.linear_scan_backward(1 - z, h0, fwd, dy)
+    dz, dc, dh0_g = scans.mingru_scan_backward(z, b, h0, fwd, dy)
+    np.testing.assert_allclose(db * z, dc, rtol=1e-12)  # d/dc = db dz c/dc
+    np.testing.assert_allclose(-da + db * b, dz, rtol=1e-10, atol=1e-12)  # d/dz = -da + db c
+    np.testing.assert_allclose(dh0, dh0_g, rtol=1e-12)
 
 
 def test_minlstm_invariants(rng):
