@@ -270,12 +270,22 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
 //   MODE 2 (reverse, gradients):   v = dvl + Kd dh;      dh = gamma_C dh + dhl - W^T v
 // MODE 0 stores h as [d_v][d_k] and v^T; MODE 1 stores h as [d_k][d_v] and v;
 // MODE 2 stores dh (the gradient of the state leaving each chunk) as [d_k][d_v] and v^T.
+// Every stored tile is first staged in LDS in its global layout and then written by all
+// threads as contiguous 16-byte rows (the slice of one chunk is one 8 KB / 4 KB block, or
+// 64-byte row segments): storing straight from the accumulator layout scatters each
+// instruction over 32 rows, and those stores alone took half of the scan's time.  The v
+// tile of a step is written out after the next step's barrier.
 // ---------------------------------------------------------------------------
+constexpr int NS = VS + 8;  // LDS row stride (bf16) of [*][VS] tiles
+
 template <int MODE>
 __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
   constexpr bool REV = MODE == 2;
   __shared__ __attribute__((aligned(16))) bf16 sA1[2][CH * KS];  // W, or Kd in the reverse pass: [t][d_k]
   __shared__ __attribute__((aligned(16))) bf16 sSt[2][VS * KS];  // state slice, [d_v][d_k]
+  // the state slice as [d_k][d_v] (MODE 1, 2) and v as [d_v][t] (MODE 0, 2) or [t][d_v]
+  __shared__ __attribute__((aligned(16))) bf16 sN[MODE == 0 ? 1 : 2][MODE == 0 ? 8 : DK * NS];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][MODE == 1 ? CH * NS : VS * TS];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -284,8 +294,30 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
   const long bh = logical / NSL;
   const int v0 = (logical % NSL) * VS;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  auto chunk_of_ = [&](int it) { return REV ? p.nch - 1 - it : it; };
 
   f32x16 S = zero16();  // rows d_k = 32 w + d_row(r, g), column d_v = v0 + li
+
+  // output regions of this head (buffer resources: a dropped store needs no branch)
+  const long hbytes = (long)p.nch * DK * DK * 2, vbytes = (long)p.nch * DK * CH * 2;
+  const rsrc_t rH = make_rsrc((MODE == 0 ? p.hT : MODE == 1 ? p.hN : p.dmN) + bh * p.nch * DK * DK, (unsigned)hbytes);
+  const rsrc_t rV = make_rsrc((MODE == 0 ? p.vT : MODE == 1 ? p.vN : p.dvT) + bh * p.nch * DK * CH, (unsigned)vbytes);
+  auto st16 = [&](const rsrc_t& r, unsigned off, const bf16* src) {
+    __builtin_amdgcn_raw_buffer_store_b128(*(const u32x4*)src, r, (int)off, 0, 0);
+  };
+  // the v tile staged by step it - 1 (chunk cp); nothing is stored when it == 0
+  auto copy_v = [&](int it) {
+    const int cp = chunk_of_(it - 1);
+    if constexpr (MODE == 1) {  // v as [t][d_v]: 64 rows of 64 bytes
+      const int row = tid >> 2, ch = tid & 3;
+      const unsigned off = it > 0 ? (unsigned)(((cp * CH + row) * DK + v0 + 8 * ch) * 2) : OOB_OFF;
+      st16(rV, off, sV[(it - 1) & 1] + row * NS + 8 * ch);
+    } else {  // v^T as [d_v][t]: 32 rows of 128 bytes
+      const int row = tid >> 3, ch = tid & 7;
+      const unsigned off = it > 0 ? (unsigned)(((cp * DK + v0 + row) * CH + 8 * ch) * 2) : OOB_OFF;
+      st16(rV, off, sV[(it - 1) & 1] + row * TS + 8 * ch);
+    }
+  };
 
   // operands of the next two chunks, loaded ahead into two register sets (the loop is
   // unrolled by two so that each set is addressed statically)
@@ -331,7 +363,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     }
     P.lgC = p.lg[ci * CH + CH - 1];
   };
-  auto chunk_of = [&](int it) { return REV ? p.nch - 1 - it : it; };
+  auto chunk_of = chunk_of_;
   fetch_a1(pre0, chunk_of(0));
   fetch_rest(pre0, chunk_of(0));
   if (p.nch > 1) {
@@ -353,12 +385,11 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = (bf16)S[4 * q + e];
       *(bf16x4*)(ss + li * KS + 32 * w + 8 * q + 4 * g) = v;
-      if (MODE == 0) *(bf16x4*)(p.hT + ci * DK * DK + (long)(v0 + li) * DK + 32 * w + 8 * q + 4 * g) = v;
     }
-    if (MODE != 0) {
-      bf16* dst = (MODE == 1 ? p.hN : p.dmN) + ci * DK * DK + v0 + li;
+    if constexpr (MODE != 0) {
+      bf16* sn = sN[it & 1];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dst[(long)(32 * w + d_row(r, g)) * DK] = (bf16)S[r];
+      for (int r = 0; r < 16; ++r) sn[(32 * w + d_row(r, g)) * NS + li] = (bf16)S[r];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -396,16 +427,14 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
         X[T][r] = REV ? x0v + X[T][r] : x0v - X[T][r];
       }
     }
-    // store v (one tile per wave pair)
-    if (MODE != 1) {
-      bf16* dst = (REV ? p.dvT : p.vT) + ci * DK * CH + (long)v0 * CH;
-      if (w == 0) store_rows(dst, CH, X[0], li, g);
-      else if (w == 1) store_rows(dst + 32, CH, X[1], li, g);
+    // stage v for the next step's store (one tile per wave of a pair)
+    if constexpr (MODE != 1) {
+      if (w < 2) store_rows(sV[it & 1] + 32 * w, TS, w == 0 ? X[0] : X[1], li, g);
     } else if (w >= 2) {
-      bf16* dst = p.vN + ci * CH * DK + (long)(32 * (w - 2)) * DK + v0 + li;
+      bf16* dst = sV[it & 1] + (32 * (w - 2)) * NS + li;
       const f32x16 Xw = w == 2 ? X[0] : X[1];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dst[(long)d_row(r, g) * DK] = (bf16)Xw[r];
+      for (int r = 0; r < 16; ++r) dst[d_row(r, g) * NS] = (bf16)Xw[r];
     }
     // state update: Y = A2 * v, contracting over t with v taken straight from registers
     f32x16 Y = zero16();
@@ -414,6 +443,20 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       S[r] = REV ? fmaf(gC, S[r], (float)P.y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
+    // coalesced stores, off the step's dependency chain: the state this step started
+    // from (staged before its barrier) and the v of the previous step
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i;
+      if constexpr (MODE == 0) {  // [d_v][d_k]: the slice is 32 whole rows of 256 bytes
+        const int row = e >> 4, ch = e & 15;
+        st16(rH, (unsigned)(((c * DK + v0 + row) * DK + 8 * ch) * 2), ss + row * KS + 8 * ch);
+      } else {  // [d_k][d_v]: 128 rows of 64 bytes
+        const int row = e >> 2, ch = e & 3;
+        st16(rH, (unsigned)(((c * DK + row) * DK + v0 + 8 * ch) * 2), sN[it & 1] + row * NS + 8 * ch);
+      }
+    }
+    copy_v(it);
     fetch_rest(P, chunk_of(min(it + 2, p.nch - 1)));
   };
   // both bodies of the unrolled pair run unconditionally inside the loop (an odd last
@@ -424,6 +467,8 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     body(it + 1, pre1);
   }
   if (it < p.nch) body(it, pre0);
+  __syncthreads();
+  copy_v(p.nch);  // the last chunk's v
 }
 
 // ---------------------------------------------------------------------------
@@ -868,7 +913,8 @@ CkArgs make_args(const Layout& L, void* workspace, bool bwd, int seq, int heads)
 }  // namespace
 
 bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head) {
-  return dtype == EDF_BF16 && beta_per_head && d == DK && seq >= CH;
+  // seq bound: the scan addresses one head's per-chunk tiles with 32-bit byte offsets
+  return dtype == EDF_BF16 && beta_per_head && d == DK && seq >= CH && seq <= (1 << 21);
 }
 
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d) {
