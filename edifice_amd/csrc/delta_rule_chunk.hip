@@ -477,6 +477,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sP[CH * TS];  // P [t][s]
   __shared__ float lg[CH];
+  __shared__ __attribute__((aligned(16))) bf16 sScr[4][SCR_ELEMS];  // per-wave store staging
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -523,7 +524,8 @@ __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
     for (int kk = 0; kk < 2 * (J + 1); ++kk)
       X = mfma32(*(const bf16x8*)(p.vT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g),
                  *(const bf16x8*)(sP + t * TS + 16 * kk + 8 * g), X);
-    if (t0 + t < p.T) store_rows(p.out + row_off(p, b, h, t0 + 32 * J) + 32 * w, (long)p.H * DK, X, li, g);
+    store_rows_staged(p.out + row_off(p, b, h, t0 + 32 * J) + 32 * w, (long)p.H * DK, X, l, sScr[w],
+                      p.T - t0 - 32 * J);
   }
 }
 
@@ -535,6 +537,7 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sdOt[DK * TS];  // dO^T [d_v][t]
   __shared__ __attribute__((aligned(16))) bf16 sQg[DK * TS];  // (diag(gamma) Q)^T [d_k][t]
   __shared__ float lg[CH], gm[CH];
+  __shared__ __attribute__((aligned(16))) bf16 sScr[4][SCR_ELEMS];  // per-wave store staging
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -579,7 +582,7 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
     for (int kk = 2 * I; kk < 4; ++kk)
       X = mfma32(*(const bf16x8*)(sPt + (32 * I + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdOt + (32 * w + li) * TS + 16 * kk + 8 * g), X);
-    store_rows(p.dvl + ci * DK * CH + (long)(32 * w) * CH + 32 * I, CH, X, li, g);
+    store_rows_staged(p.dvl + ci * DK * CH + (long)(32 * w) * CH + 32 * I, CH, X, l, sScr[w]);
   }
   // Q^T diag(gamma) dO: rows d_k (tile I), columns d_v = 32 w + li
 #pragma unroll
@@ -589,7 +592,7 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
     for (int kk = 0; kk < 4; ++kk)
       X = mfma32(*(const bf16x8*)(sQg + (32 * I + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdOt + (32 * w + li) * TS + 16 * kk + 8 * g), X);
-    store_rows(p.dhl + ci * DK * DK + (long)(32 * w) * DK + 32 * I, DK, X, li, g);
+    store_rows_staged(p.dhl + ci * DK * DK + (long)(32 * w) * DK + 32 * I, DK, X, l, sScr[w]);
   }
 }
 
@@ -609,6 +612,7 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   __shared__ float sZa[CH * ZS];  // dA o A
   __shared__ float sB[CH * ZS];   // dA o Gamma o (K K^T), s < t
   __shared__ float lg[CH], bt[CH], dlg[CH], dbt[CH];
+  __shared__ __attribute__((aligned(16))) bf16 sScr[8][SCR_ELEMS];  // per-wave store staging
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -647,7 +651,8 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
     // dV = beta dR;  dbeta += <dR_s, V_s>
     const bool ok = t0 + s < p.T;
     const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1) + 32 * wd + 4 * g;
-    if (ok) store_rows(p.dv + row_off(p, b, h, t0 + 32 * J) + 32 * wd, (long)p.H * DK, X, li, g, bt[s]);
+    store_rows_staged(p.dv + row_off(p, b, h, t0 + 32 * J) + 32 * wd, (long)p.H * DK, X, l, sScr[w],
+                      p.T - t0 - 32 * J, bt[s]);
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -741,7 +746,6 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   float dlgC = 0.0f;
   {
     const int J2 = wt, t = 32 * J2 + li;
-    const bool ok = t0 + t < p.T;
     // dQ^T = gamma (h dO^T) + K^T dS^T
     f32x16 X = zero16();
 #pragma unroll
@@ -763,7 +767,8 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
       X = mfma32(*(const bf16x8*)(sKt + (32 * wd + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdS + t * TS + 16 * kk + 8 * g), X);
     }
-    if (ok) store_rows(p.dq + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X, li, g);
+    store_rows_staged(p.dq + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X, l, sScr[w],
+                      p.T - t0 - 32 * J2);
 
     // dK^T = (gamma_C / gamma) dh v^T - (beta gamma) h dR^T + Q^T dS + K^T dF
     f32x16 X1 = zero16(), X2 = zero16(), X3 = zero16();
@@ -801,7 +806,8 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
       atomicAdd(&dbt[t], -gmt * k2);
       dlgC = sc1 * k1;
     }
-    if (ok) store_rows(p.dk + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X3, li, g);
+    store_rows_staged(p.dk + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X3, l, sScr[w],
+                      p.T - t0 - 32 * J2);
   }
   // gamma_C <dh, h> and the Kd terms enter the decay of the last step
   {
