@@ -228,38 +228,65 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   }
   __syncthreads();
 
-  // T is lower triangular, so row tile 0 only reaches s < 32 (k-steps 0, 1)
-#pragma unroll
-  for (int J = 0; J < 2; ++J) {
-    // W^T: rows d_k = 32 w + .., columns t = 32 J + li  ->  W stored [t][d_k]
+  // T is lower triangular, so row tile 0 only reaches s < 32 (k-steps 0, 1).
+  // W^T tile: rows d_k = 32 w + .., columns t = 32 J + li  ->  W stored [t][d_k]
+  // U tile:   rows t = 32 J + .., columns d_v = 32 w + li  ->  U^T stored [d_v][t]
+  // W tile:   rows t = 32 J + .., columns d_k = 32 w + li  ->  W^T stored [d_k][t] (backward)
+  auto product = [&](const bf16* A, const bf16* Bm, int J) {
     f32x16 X = zero16();
 #pragma unroll
-    for (int kk = 0; kk < 2 * (J + 1); ++kk) {
-      const bf16x8 a = *(const bf16x8*)(sKb + (32 * w + li) * TS + 16 * kk + 8 * g);
-      const bf16x8 bb = *(const bf16x8*)(sTb + (32 * J + li) * TS + 16 * kk + 8 * g);
-      X = mfma32(a, bb, X);
-    }
-    store_rows(p.W + ci * CH * DK + (long)(32 * J) * DK + 32 * w, DK, X, li, g);
-    // U: rows t = 32 J + .., columns d_v = 32 w + li  ->  U^T stored [d_v][t]
-    X = zero16();
+    for (int kk = 0; kk < 2 * (J + 1); ++kk)
+      X = mfma32(*(const bf16x8*)(A + li * TS + 16 * kk + 8 * g), *(const bf16x8*)(Bm + li * TS + 16 * kk + 8 * g), X);
+    return X;
+  };
+  f32x16 XW[2], XU[2];
 #pragma unroll
-    for (int kk = 0; kk < 2 * (J + 1); ++kk) {
-      const bf16x8 a = *(const bf16x8*)(sTb + (32 * J + li) * TS + 16 * kk + 8 * g);
-      const bf16x8 bb = *(const bf16x8*)(sVb + (32 * w + li) * TS + 16 * kk + 8 * g);
-      X = mfma32(a, bb, X);
-    }
-    store_rows(p.Ut + ci * DK * CH + (long)(32 * w) * CH + 32 * J, CH, X, li, g);
-    if (BWD) {
-      // W: rows t = 32 J + .., columns d_k = 32 w + li  ->  W^T stored [d_k][t]
-      X = zero16();
+  for (int J = 0; J < 2; ++J) {
+    XW[J] = product(sKb + (32 * w) * TS, sTb + (32 * J) * TS, J);
+    XU[J] = product(sTb + (32 * J) * TS, sVb + (32 * w) * TS, J);
+  }
+  // The results of the chunk are contiguous 16 KB blocks of the workspace: they are staged
+  // in operand tiles that are no longer read and written as whole rows, 16 bytes per lane
+  // (stores straight from the accumulator layout scatter each instruction over 32 rows).
+  bf16* sW = (bf16*)u1;  // [t][d_k], row stride KS (over K^T once that is consumed)
+  bf16* sU = (bf16*)u2;  // [d_v][t] or [d_k][t], row stride TS (over V^T)
+  auto copy_w = [&]() {
 #pragma unroll
-      for (int kk = 0; kk < 2 * (J + 1); ++kk) {
-        const bf16x8 a = *(const bf16x8*)(sTb + (32 * J + li) * TS + 16 * kk + 8 * g);
-        const bf16x8 bb = *(const bf16x8*)(sKb + (32 * w + li) * TS + 16 * kk + 8 * g);
-        X = mfma32(a, bb, X);
-      }
-      store_rows(p.Wt + ci * DK * CH + (long)(32 * w) * CH + 32 * J, CH, X, li, g);
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, row = e >> 4, ch = e & 15;  // 64 rows of 256 bytes
+      *(bf16x8*)(p.W + ci * CH * DK + row * DK + 8 * ch) = *(const bf16x8*)(sW + row * KS + 8 * ch);
     }
+  };
+  auto copy_u = [&](bf16* dst) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, row = e >> 3, ch = e & 7;  // 128 rows of 128 bytes
+      *(bf16x8*)(dst + ci * DK * CH + row * CH + 8 * ch) = *(const bf16x8*)(sU + row * TS + 8 * ch);
+    }
+  };
+  __syncthreads();  // V^T consumed
+#pragma unroll
+  for (int J = 0; J < 2; ++J) store_rows(sU + (32 * w) * TS + 32 * J, TS, XU[J], li, g);
+  if constexpr (!BWD) {
+#pragma unroll
+    for (int J = 0; J < 2; ++J) store_rows(sW + (32 * J) * KS + 32 * w, KS, XW[J], li, g);
+    __syncthreads();
+    copy_u(p.Ut);
+    copy_w();
+  } else {
+    f32x16 XWt[2];
+#pragma unroll
+    for (int J = 0; J < 2; ++J) XWt[J] = product(sTb + (32 * J) * TS, sKb + (32 * w) * TS, J);
+    __syncthreads();  // U^T staged, K^T consumed
+    copy_u(p.Ut);
+#pragma unroll
+    for (int J = 0; J < 2; ++J) store_rows(sW + (32 * J) * KS + 32 * w, KS, XW[J], li, g);
+    __syncthreads();  // W staged, U^T copied
+    copy_w();
+#pragma unroll
+    for (int J = 0; J < 2; ++J) store_rows(sU + (32 * w) * TS + 32 * J, TS, XWt[J], li, g);
+    __syncthreads();
+    copy_u(p.Wt);
   }
 }
 
