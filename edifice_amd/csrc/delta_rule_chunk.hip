@@ -504,7 +504,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sP[CH * TS];  // P [t][s]
   __shared__ float lg[CH];
-  __shared__ __attribute__((aligned(16))) bf16 sScr[4][SCR_ELEMS];  // per-wave store staging
+  __shared__ __attribute__((aligned(16))) bf16 sO[CH * KS];  // O staged as [t][d] rows
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -551,8 +551,15 @@ __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
     for (int kk = 0; kk < 2 * (J + 1); ++kk)
       X = mfma32(*(const bf16x8*)(p.vT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g),
                  *(const bf16x8*)(sP + t * TS + 16 * kk + 8 * g), X);
-    store_rows_staged(p.out + row_off(p, b, h, t0 + 32 * J) + 32 * w, (long)p.H * DK, X, l, sScr[w],
-                      p.T - t0 - 32 * J);
+    store_rows(sO + (32 * J) * KS + 32 * w, KS, X, li, g);
+  }
+  // whole 256-byte rows of out (stores straight from the accumulator layout scatter each
+  // instruction over 32 rows)
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + 256 * i, row = e >> 4, ch = e & 15;
+    if (t0 + row < p.T) *(bf16x8*)(p.out + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(sO + row * KS + 8 * ch);
   }
 }
 
@@ -635,11 +642,13 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sdS[CH * TS];  // dS [t][s]
   __shared__ __attribute__((aligned(16))) bf16 sdSt[CH * TS];  // dS^T [s][t]
   __shared__ __attribute__((aligned(16))) bf16 sdF[CH * TS];  // dG + dG^T
-  __shared__ float sZp[CH * ZS];  // dP o P
-  __shared__ float sZa[CH * ZS];  // dA o A
-  __shared__ float sB[CH * ZS];   // dA o Gamma o (K K^T), s < t
+  __shared__ __attribute__((aligned(16))) float sZ[3 * CH * ZS];
+  float* sZp = sZ;               // dP o P
+  float* sZa = sZ + CH * ZS;     // dA o A
+  float* sB = sZ + 2 * CH * ZS;  // dA o Gamma o (K K^T), s < t
   __shared__ float lg[CH], bt[CH], dlg[CH], dbt[CH];
-  __shared__ __attribute__((aligned(16))) bf16 sScr[8][SCR_ELEMS];  // per-wave store staging
+  // dV, then dQ, staged as [t][d] rows (dK goes over sZ once that is consumed)
+  __shared__ __attribute__((aligned(16))) bf16 sO[CH * KS];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -651,6 +660,15 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   const long ci = bh * p.nch + c;
   const bf16* hN = p.hN + ci * DK * DK;
   const bf16* vN = p.vN + ci * CH * DK;
+  // a staged [t][d] tile of the chunk, written as whole 256-byte rows of a [B,T,H,D] tensor
+  // (stores straight from the accumulator layout scatter each instruction over 32 rows)
+  auto copy_rows = [&](bf16* dst, const bf16* src) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 512 * i, row = e >> 4, ch = e & 15;
+      if (t0 + row < p.T) *(bf16x8*)(dst + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(src + row * KS + 8 * ch);
+    }
+  };
 
   if (tid < CH) {
     const int t = t0 + tid;
@@ -678,8 +696,7 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
     // dV = beta dR;  dbeta += <dR_s, V_s>
     const bool ok = t0 + s < p.T;
     const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1) + 32 * wd + 4 * g;
-    store_rows_staged(p.dv + row_off(p, b, h, t0 + 32 * J) + 32 * wd, (long)p.H * DK, X, l, sScr[w],
-                      p.T - t0 - 32 * J, bt[s]);
+    store_rows(sO + (32 * J) * KS + 32 * wd, KS, X, li, g, bt[s]);
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -703,7 +720,8 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
       SG = mfma32(ld_row8(sq ? p.q : p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
                   ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), SG);
   }
-  __syncthreads();  // sdR complete
+  __syncthreads();  // sdR and the dV tile complete
+  copy_rows(p.dv, sO);
 
   {
     const int s = 32 * J + li;
@@ -771,6 +789,7 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
 
   // dQ^T and dK^T: rows d_k = 32 wd + .., columns t (or s) = 32 wt + li
   float dlgC = 0.0f;
+  f32x16 XdK;
   {
     const int J2 = wt, t = 32 * J2 + li;
     // dQ^T = gamma (h dO^T) + K^T dS^T
@@ -794,8 +813,7 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
       X = mfma32(*(const bf16x8*)(sKt + (32 * wd + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdS + t * TS + 16 * kk + 8 * g), X);
     }
-    store_rows_staged(p.dq + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X, l, sScr[w],
-                      p.T - t0 - 32 * J2);
+    store_rows(sO + (32 * J2) * KS + 32 * wd, KS, X, li, g);
 
     // dK^T = (gamma_C / gamma) dh v^T - (beta gamma) h dR^T + Q^T dS + K^T dF
     f32x16 X1 = zero16(), X2 = zero16(), X3 = zero16();
@@ -833,8 +851,7 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
       atomicAdd(&dbt[t], -gmt * k2);
       dlgC = sc1 * k1;
     }
-    store_rows_staged(p.dk + row_off(p, b, h, t0 + 32 * J2) + 32 * wd, (long)p.H * DK, X3, l, sScr[w],
-                      p.T - t0 - 32 * J2);
+    XdK = X3;
   }
   // gamma_C <dh, h> and the Kd terms enter the decay of the last step
   {
@@ -852,6 +869,12 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
     if (l == 0) atomicAdd(&dlg[CH - 1], acc);
   }
   __syncthreads();
+  // dQ is staged; sZ is consumed: stage dK over it
+  bf16* sK2 = (bf16*)sZ;
+  store_rows(sK2 + (32 * wt) * KS + 32 * wd, KS, XdK, li, g);
+  copy_rows(p.dq, sO);
+  __syncthreads();
+  copy_rows(p.dk, sK2);
 
   if (w == 0) {
     // dlog(alpha_s) = sum_{t >= s} dlg_t
