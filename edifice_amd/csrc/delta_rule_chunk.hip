@@ -292,7 +292,10 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
 
 // ---------------------------------------------------------------------------
 // scan over chunks, one workgroup per (b, h, d_v slice); wave w owns state rows
-// d_k = 32 w .. 32 w + 31 of the slice as one f32 accumulator tile.
+// d_k = 32 w .. 32 w + 31 of the slice as one f32 accumulator tile.  Per chunk, waves 0
+// and 1 compute the two 32-step tiles of v (reading A1 and the published state from
+// LDS) and publish v; after a second barrier every wave updates its state rows with v
+// read from LDS.  (Each wave computing all of v itself reads four times the LDS bytes.)
 //   MODE 0 / 1 (forward states):  v = U - W h;          h = gamma_C h + Kd^T v
 //   MODE 2 (reverse, gradients):   v = dvl + Kd dh;      dh = gamma_C dh + dhl - W^T v
 // MODE 0 stores h as [d_v][d_k] and v^T; MODE 1 stores h as [d_k][d_v] and v;
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
 // threads as contiguous 16-byte rows (the slice of one chunk is one 8 KB / 4 KB block, or
 // 64-byte row segments): storing straight from the accumulator layout scatters each
 // instruction over 32 rows, and those stores alone took half of the scan's time.  The v
-// tile of a step is written out after the next step's barrier.
+// tile of a step is written out at the end of the step.
 // ---------------------------------------------------------------------------
 constexpr int NS = VS + 8;  // LDS row stride (bf16) of [*][VS] tiles
 
@@ -310,12 +313,13 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
   constexpr bool REV = MODE == 2;
   __shared__ __attribute__((aligned(16))) bf16 sA1[2][CH * KS];  // W, or Kd in the reverse pass: [t][d_k]
   __shared__ __attribute__((aligned(16))) bf16 sSt[2][VS * KS];  // state slice, [d_v][d_k]
-  // the state slice as [d_k][d_v] (MODE 1, 2) and v as [d_v][t] (MODE 0, 2) or [t][d_v]
+  // the state slice as [d_k][d_v] (MODE 1, 2), v as [d_v][t] and (MODE 1) as [t][d_v]
   __shared__ __attribute__((aligned(16))) bf16 sN[MODE == 0 ? 1 : 2][MODE == 0 ? 8 : DK * NS];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][MODE == 1 ? CH * NS : VS * TS];
+  __shared__ __attribute__((aligned(16))) bf16 sV[2][VS * TS];
+  __shared__ __attribute__((aligned(16))) bf16 sV2[MODE == 1 ? 2 : 1][MODE == 1 ? CH * NS : 8];
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 5, li = l & 31;
   constexpr int NSL = DK / VS;
   const int logical = remap_xcd(blockIdx.x, gridDim.x);  // the slices of one head share an XCD
   const long bh = logical / NSL;
@@ -332,17 +336,14 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
   auto st16 = [&](const rsrc_t& r, unsigned off, const bf16* src) {
     __builtin_amdgcn_raw_buffer_store_b128(*(const u32x4*)src, r, (int)off, 0, 0);
   };
-  // the v tile staged by step it - 1 (chunk cp); nothing is stored when it == 0
-  auto copy_v = [&](int it) {
-    const int cp = chunk_of_(it - 1);
+  // the v tile of step it (chunk c)
+  auto copy_v = [&](int it, int c) {
     if constexpr (MODE == 1) {  // v as [t][d_v]: 64 rows of 64 bytes
       const int row = tid >> 2, ch = tid & 3;
-      const unsigned off = it > 0 ? (unsigned)(((cp * CH + row) * DK + v0 + 8 * ch) * 2) : OOB_OFF;
-      st16(rV, off, sV[(it - 1) & 1] + row * NS + 8 * ch);
+      st16(rV, (unsigned)(((c * CH + row) * DK + v0 + 8 * ch) * 2), sV2[it & 1] + row * NS + 8 * ch);
     } else {  // v^T as [d_v][t]: 32 rows of 128 bytes
       const int row = tid >> 3, ch = tid & 7;
-      const unsigned off = it > 0 ? (unsigned)(((cp * DK + v0 + row) * CH + 8 * ch) * 2) : OOB_OFF;
-      st16(rV, off, sV[(it - 1) & 1] + row * TS + 8 * ch);
+      st16(rV, (unsigned)(((c * DK + v0 + row) * CH + 8 * ch) * 2), sV[it & 1] + row * TS + 8 * ch);
     }
   };
 
@@ -352,7 +353,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     bf16x8 a1[4];
     float l1[4];
     bf16x8 a2[4];
-    bf16x4 x0[2][4];
+    bf16x4 x0[4];  // this wave's t tile (w & 1) of U^T or dvl
     bf16x4 y0[4];
     float lgC;
   };
@@ -380,9 +381,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     for (int kk = 0; kk < 4; ++kk) P.a2[kk] = *(const bf16x8*)(a2 + 16 * kk);
     const bf16* x0 = (REV ? p.dvl : p.Ut) + ci * DK * CH + (v0 + li) * CH + 4 * g;
 #pragma unroll
-    for (int T = 0; T < 2; ++T)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) P.x0[T][q] = *(const bf16x4*)(x0 + 32 * T + 8 * q);
+    for (int q = 0; q < 4; ++q) P.x0[q] = *(const bf16x4*)(x0 + 32 * (w & 1) + 8 * q);
     if (REV) {
       const bf16* y0 = p.dhl + ci * DK * DK + (v0 + li) * DK + 32 * w + 4 * g;
 #pragma unroll
@@ -437,41 +436,38 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     fetch_a1(P, chunk_of(min(it + 2, p.nch - 1)));
     __syncthreads();
 
-    // X = A1 * state: rows t (two tiles), column d_v
-    f32x16 X[2];
-#pragma unroll
-    for (int T = 0; T < 2; ++T) {
-      X[T] = zero16();
+    // v for the t tile w = 0, 1: X = A1 * state (rows t, column d_v), published as [d_v][t]
+    bf16* sv = sV[it & 1];
+    if (w < 2) {
+      f32x16 X = zero16();
 #pragma unroll
       for (int kk = 0; kk < DK / 16; ++kk) {
-        const bf16x8 a = *(const bf16x8*)(sa + (32 * T + li) * KS + 16 * kk + 8 * g);
+        const bf16x8 a = *(const bf16x8*)(sa + (32 * w + li) * KS + 16 * kk + 8 * g);
         const bf16x8 bb = *(const bf16x8*)(ss + li * KS + 16 * kk + 8 * g);
-        X[T] = mfma32(a, bb, X[T]);
+        X = mfma32(a, bb, X);
       }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float x0v = (float)P.x0[T][r >> 2][r & 3];
-        X[T][r] = REV ? x0v + X[T][r] : x0v - X[T][r];
+        const float x0v = (float)P.x0[r >> 2][r & 3];
+        X[r] = REV ? x0v + X[r] : x0v - X[r];
+      }
+      store_rows(sv + 32 * w, TS, X, li, g);
+      if constexpr (MODE == 1) {  // and as [t][d_v] for the store of v
+        bf16* dst = sV2[it & 1] + (32 * w) * NS + li;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[d_row(r, g) * NS] = (bf16)X[r];
       }
     }
-    // stage v for the next step's store (one tile per wave of a pair)
-    if constexpr (MODE != 1) {
-      if (w < 2) store_rows(sV[it & 1] + 32 * w, TS, w == 0 ? X[0] : X[1], li, g);
-    } else if (w >= 2) {
-      bf16* dst = sV[it & 1] + (32 * (w - 2)) * NS + li;
-      const f32x16 Xw = w == 2 ? X[0] : X[1];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dst[d_row(r, g) * NS] = (bf16)Xw[r];
-    }
-    // state update: Y = A2 * v, contracting over t with v taken straight from registers
+    __syncthreads();
+    // state update: Y = A2 * v, contracting over t
     f32x16 Y = zero16();
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) Y = mfma32(P.a2[kk], acc_kfrag(X[kk >> 1], kk & 1), Y);
+    for (int kk = 0; kk < 4; ++kk) Y = mfma32(P.a2[kk], *(const bf16x8*)(sv + li * TS + 16 * kk + 8 * g), Y);
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       S[r] = REV ? fmaf(gC, S[r], (float)P.y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
     // coalesced stores, off the step's dependency chain: the state this step started
-    // from (staged before its barrier) and the v of the previous step
+    // from and its v
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int e = tid + 256 * i;
@@ -483,7 +479,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
         st16(rH, (unsigned)(((c * DK + row) * DK + v0 + 8 * ch) * 2), sN[it & 1] + row * NS + 8 * ch);
       }
     }
-    copy_v(it);
+    copy_v(it, c);
     fetch_rest(P, chunk_of(min(it + 2, p.nch - 1)));
   };
   // both bodies of the unrolled pair run unconditionally inside the loop (an odd last
@@ -494,8 +490,6 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     body(it + 1, pre1);
   }
   if (it < p.nch) body(it, pre0);
-  __syncthreads();
-  copy_v(p.nch);  // the last chunk's v
 }
 
 // ---------------------------------------------------------------------------
