@@ -91,14 +91,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
   sstore(0);
   if (nkt > 1) gload(BN);
   __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
+  // One key tile; the masked body selects -inf per score without branching.
+  auto tile = [&](int kt, auto masked) {
+    constexpr bool MASK = decltype(masked)::value;
     const int k0 = kt * BN, buf = kt & 1;
     const bf16* sk = sK[buf];
     const bf16* sv = sV[buf];
-    // Tiles wholly inside the sequence and below the diagonal take the unmasked body;
-    // the rest select -inf per score without branching.
-    auto tile = [&](auto masked) {
-    constexpr bool MASK = decltype(masked)::value;
     // S^T = K Q^T: lane owns query column li, rows are keys
     f32x16 s[2];
 #pragma unroll
@@ -172,30 +170,53 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
         }
       }
     }
-    };
-    if ((k0 + BN > T) || (CAUSAL && k0 + BN - 1 > qw)) tile(std::true_type{});
-    else tile(std::false_type{});
+  };
+  // the next tile into the other LDS buffer, the one after it into registers
+  auto advance = [&](int kt) {
     if (kt + 1 < nkt) {
-      sstore(buf ^ 1);
+      sstore((kt & 1) ^ 1);
       if (kt + 2 < nkt) gload((kt + 2) * BN);
     }
     __syncthreads();
+  };
+  // A wave's unmasked tiles (inside the sequence and, causal, wholly at or below its
+  // queries' diagonal) come first: two loops with one tile body each (both bodies behind
+  // a branch in one loop spilled registers).  ksplit is wave-uniform; every wave runs nkt
+  // steps, so the barriers stay matched.
+  const int ksplit = min(min(T / BN, nkt), CAUSAL ? (qw + 1) / BN : nkt);
+  int kt = 0;
+  for (; kt < ksplit; ++kt) {
+    tile(kt, std::false_type{});
+    advance(kt);
+  }
+  for (; kt < nkt; ++kt) {
+    tile(kt, std::true_type{});
+    advance(kt);
   }
 
-  if (myq < T) {
-    const float inv = 1.0f / lsum;
-    bf16* orow = O + bh * T * HD + (long)myq * HD;
+  // O goes through the (now free) K tiles, each wave's 32 rows privately, and is written as
+  // whole rows: a lane holds one query row, so storing from registers would touch 32 rows
+  // per instruction in 16-byte pieces.
+  bf16* so = &sK[0][0];
+  static_assert(2 * lds_tile_elems<HD>(BN) >= lds_tile_elems<HD>(BM), "O staging");
+  const float inv = myq < T ? 1.0f / lsum : 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        bf16x4 v;
+    for (int rb = 0; rb < 4; ++rb) {
+      bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (bf16)(o[dt][rb * 4 + e] * inv);
-        *(bf16x4*)(orow + dt * 32 + 8 * rb + 4 * g) = v;
-      }
-    if (g == 0 && LSE != nullptr) LSE[bh * T + myq] = (m * scale_log2 + __log2f(lsum)) * LN2;
+      for (int e = 0; e < 4; ++e) v[e] = (bf16)(o[dt][rb * 4 + e] * inv);
+      *(bf16x4*)(so + lds_off<HD>(32 * w + li, dt * 32 + 8 * rb + 4 * g)) = v;
+    }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < 32 * CPR / 64; ++i) {
+    const int e = l + 64 * i, row = e / CPR, ch = e % CPR;
+    if (qw + row < T)
+      *(bf16x8*)(O + bh * T * HD + (long)(qw + row) * HD + 8 * ch) = *(const bf16x8*)(so + lds_off<HD>(32 * w + row, 8 * ch));
   }
+  if (myq < T && g == 0 && LSE != nullptr) LSE[bh * T + myq] = (m * scale_log2 + __log2f(lsum)) * LN2;
 }
 
 // Generic path: one wave per query row, lanes over head_dim (any dtype, any head_dim <= 256).
