@@ -261,8 +261,8 @@ def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
                 shape=dict(B=B, H=H, T=T, d=d, chunk=C))
 
 
-def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128):
-    """Config 4: causal flash attention, bf16.  Flops: fwd 4 B H T^2 d / 2, bwd 2.5x fwd."""
+def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128, causal=True):
+    """Config 4: causal flash attention, bf16.  Flops: fwd 4 B H T^2 d (/ 2 when causal), bwd 2.5x fwd."""
     from edifice_amd import _native as nat
 
     g = torch.Generator(device="cuda").manual_seed(4000)
@@ -278,19 +278,19 @@ def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128):
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
     def fwd():
-        nat.call("edf_fused_flash_attention", stream, P(q), P(k), P(v), P(out), P(lse), B, H, T, d, 1, 1)
+        nat.call("edf_fused_flash_attention", stream, P(q), P(k), P(v), P(out), P(lse), B, H, T, d, int(causal), 1)
 
     def bwd():
         nat.call("edf_fused_flash_attention_backward", stream, P(q), P(k), P(v), P(out), P(do), P(lse), P(dq),
-                 P(dk), P(dv), P(ws), wsb, B, H, T, d, 1, 1)
+                 P(dk), P(dv), P(ws), wsb, B, H, T, d, int(causal), 1)
 
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
-    fflops = 4 * B * H * T * T * d / 2
+    fflops = 4 * B * H * T * T * d / (2 if causal else 1)
     bflops = 2.5 * fflops
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, fwd_tflops=fflops / fwd_ms / 1e9, bwd_tflops=bflops / bwd_ms / 1e9,
                 fwd_bwd_tflops=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9,
                 fwd_bwd_mfma_frac=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9 / MFMA_BF16_PEAK_TFLOPS,
-                shape=dict(B=B, H=H, T=T, d=d, causal=True))
+                shape=dict(B=B, H=H, T=T, d=d, causal=causal))
 
 
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
@@ -390,6 +390,8 @@ def main():
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
+        configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,
+                                                                         causal=False)
     if want("hybrid"):
         configs["c5_hybrid_decoder"] = bench_hybrid(torch, max(2, args.steps // 5), 1)
     bwd_dom = ss["bwd_ms"] >= ss["fwd_ms"]
