@@ -98,14 +98,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
-      // rows past the end are clamped, not branched around: their P and dS are masked to 0
+      // rows past the end are clamped, not branched around: their P and dS are 0
       const long q = min(q0 + row, T - 1);
       rq[i] = *(const bf16x8*)(Q + base + q * HD + col);
       ro[i] = *(const bf16x8*)(dO + base + q * HD + col);
     }
     if (tid < BQ) {
       const long q = min(q0 + tid, T - 1);
-      rl = LSE[bh * T + q] * LOG2E;
+      const float lv = LSE[bh * T + q];
+      // a query past the end gets an infinite LSE, so its P and dS are 0 in every body
+      rl = q0 + tid < T ? lv * LOG2E : INFINITY;
       rd = Dd[bh * T + q];
     }
   };
@@ -189,9 +191,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
         }
       }
       };
-      // sub-tiles inside the sequence for every query and key of the wave and wholly
-      // below the diagonal take the unmasked body
-      if ((qs + 32 > T) || (kw + 31 >= T) || (CAUSAL && qs < kw + 31)) subtile(std::true_type{});
+      // Only sub-tiles on the causal diagonal need the masked body: queries past the end
+      // have P = 0 by their LSE, and keys past the end only feed their own (unstored) dK,
+      // dV columns.  The non-causal kernel thus has a single body.
+      if (CAUSAL && qs < kw + 31) subtile(std::true_type{});
       else subtile(std::false_type{});
     }
     if (it + 1 < ntile) {
@@ -291,10 +294,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
   sstore(0);
   if (nkt > 1) gload(BN);
   __syncthreads();
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int k0 = kt * BN, buf = kt & 1;
-    auto tile = [&](auto masked) {
+  auto tile = [&](int kt, auto masked) {
       constexpr bool MASK = decltype(masked)::value;
+      const int k0 = kt * BN, buf = kt & 1;
       f32x16 s[2], dp[2];
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
@@ -335,16 +337,27 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
           dqt[dt] = mfma32(a, db[kc], dqt[dt]);
         }
       }
-    };
-    if (!(CAUSAL && k0 > qw + 31)) {  // some key of the tile is visible to this wave's queries
-      if ((k0 + BN > T) || (qw + 31 >= T) || (CAUSAL && k0 + BN - 1 > qw)) tile(std::true_type{});
-      else tile(std::false_type{});
-    }
+  };
+  auto advance = [&](int kt) {
     if (kt + 1 < nkt) {
-      sstore(buf ^ 1);
+      sstore((kt & 1) ^ 1);
       if (kt + 2 < nkt) gload((kt + 2) * BN);
     }
     __syncthreads();
+  };
+  // A wave's unmasked tiles (inside the sequence for its keys and queries and, causal,
+  // wholly at or below its queries' diagonal) come first: two loops with one tile body
+  // each (a branch between the bodies inside one loop costs registers).  ksplit is
+  // wave-uniform and every wave runs nkt steps, so the barriers stay matched.
+  const int ksplit = qw + 31 >= T ? 0 : min(min(T / BN, nkt), CAUSAL ? (qw + 1) / BN : nkt);
+  int kt = 0;
+  for (; kt < ksplit; ++kt) {
+    tile(kt, std::false_type{});
+    advance(kt);
+  }
+  for (; kt < nkt; ++kt) {
+    if (!(CAUSAL && kt * BN > qw + 31)) tile(kt, std::true_type{});  // some key visible to the wave
+    advance(kt);
   }
   if (myq < T) {
     bf16* qrow = dQ + base + (long)myq * HD;
