@@ -12,7 +12,7 @@ Algorithmic bytes (per call, what roofline.achieved divides by):
   MinGRU fwd = 3*B*T*H*s, bwd = 6*B*T*H*s (s = element size)
   linear scan fwd = 3*B*T*H*s (a, b in; h out), bwd = 5*B*T*H*s (a, h, dy in; da, db out)
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru,linear]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru,linear,block]
 """
 from __future__ import annotations
 
@@ -186,6 +186,36 @@ def bench_linear_scan(torch, steps, warmup, B, T, H, dtype):
     fb, bb = 3 * B * T * H * s, 5 * B * T * H * s
     return dict(shape=[B, T, H], dtype=str(dtype).replace("torch.", ""), fwd_us=fwd_ms * 1e3, bwd_us=bwd_ms * 1e3,
                 fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
+
+
+def bench_mingru_block(torch, steps, warmup, B, T, H, L, dtype):
+    """Multi-layer MinGRU block inference (FusedScan.mingru_block/4): per layer LayerNorm,
+    gate and candidate projections (4 B T H^2 flops), MinGRU scan, residual."""
+    from edifice_amd import _native as nat
+
+    dev = "cuda"
+    g = torch.Generator(device="cuda").manual_seed(1002)
+    x = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
+    w = (torch.randn(L * (2 * H * H + 4 * H), device=dev, generator=g) * H ** -0.5).to(dtype)
+    out = torch.empty_like(x)
+    flag = 1 if dtype == torch.bfloat16 else 0
+    wsb = nat.query("edf_mingru_block_workspace_bytes", B, T, H, L, flag)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_mingru_block_scan", stream, P(x), P(w), None, P(out), P(ws), wsb, B, T, H, L, flag)
+
+    for _ in range(warmup):
+        fwd()
+    tf = EventTimer(torch)
+    for _ in range(steps):
+        with tf:
+            fwd()
+    ms = tf.mean_ms()
+    return dict(shape=[B, T, H], layers=L, dtype=str(dtype).replace("torch.", ""), ms=ms,
+                tokens_per_s=B * T / ms * 1e3, projection_tflops=4 * B * T * H * H * L / ms / 1e9)
 
 
 def profiled_traffic(kernels, path=os.path.join(ROOT, "profiles", "selective_scan_c2.md")):
@@ -380,6 +410,10 @@ def main():
         for dt in (torch.bfloat16, torch.float32):
             key = f"mingru_bw_{str(dt).replace('torch.', '')}_8x2048x1536"
             configs[key] = bench_mingru(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
+    if want("block"):
+        for dt in (torch.float32, torch.bfloat16):
+            key = f"mingru_block_{str(dt).replace('torch.', '')}_8x2048x256_L4"
+            configs[key] = bench_mingru_block(torch, args.steps, args.warmup, 8, 2048, 256, 4, dt)
     if want("linear"):
         for dt in (torch.bfloat16, torch.float32):
             key = f"linear_scan_{str(dt).replace('torch.', '')}_8x2048x1536"

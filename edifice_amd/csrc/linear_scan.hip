@@ -711,10 +711,212 @@ int bwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand,
                                        hid);
 }
 
+// ---------------------------------------------------------------------------------
+// Multi-layer MinGRU block, inference (reference native/cuda/fused_mingru_block_scan.cu:
+// 45-140; fallback lib/edifice/cuda/fused_scan.ex:4521-4571).  Per layer l, with x_0 the
+// input:  n = LayerNorm(x_l) (eps 1e-5, gamma, beta);  z = sigmoid(n W_z + b_z);
+// c = n W_h + b_h;  h_t = (1 - z_t) h_{t-1} + z_t c_t from h0[:, l];  x_{l+1} = x_l + h.
+// The reference walks timesteps and layers one by one in one workgroup per batch row
+// (every step a matrix-vector product).  The gates depend on x only, so here each layer is
+// one parallel pass over all (b, t) rows: a projection kernel (the previous layer's
+// residual, the LayerNorm and both products on f32 MFMA, 32 rows per workgroup) and the
+// MinGRU scan above with the sigmoid fused; activations stay in f32 between layers, as in
+// the reference's registers.  Packed weights per layer: W_z [H][H] (input-major), b_z,
+// W_h, b_h, gamma, beta, in the I/O dtype.
+// ---------------------------------------------------------------------------------
+constexpr int MGB_ROWS = 32;                // rows (b, t) per projection workgroup
+constexpr int MGB_HMAX = 256;
+constexpr int MGB_LD = MGB_HMAX + 2;        // LDS row stride: the A-operand reads are conflict-free
+constexpr float MGB_LN_EPS = 1.0e-5f;
+
+typedef __attribute__((ext_vector_type(16))) float mgb_f32x16;
+
+// Layer input x_l (the input for l = 0, else x_{l-1} + h_{l-1}) written back to X, its
+// LayerNorm, and Z = n W_z + b_z (gate logits), C = n W_h + b_h.
+template <typename T>
+__global__ __launch_bounds__(256) void mgb_proj_kernel(const T* __restrict__ input, float* __restrict__ X,
+                                                       const float* __restrict__ Hprev, const T* __restrict__ Wl,
+                                                       float* __restrict__ Z, float* __restrict__ C, long rows,
+                                                       int H, int first) {
+  __shared__ float sn[MGB_ROWS * MGB_LD];  // normalized rows, zero-padded to an even H
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const long row0 = (long)blockIdx.x * MGB_ROWS;
+  const T* Wz = Wl;
+  const T* bz = Wl + (long)H * H;
+  const T* Wh = bz + H;
+  const T* bh = Wh + (long)H * H;
+  const T* gamma = bh + H;
+  const T* beta = gamma + H;
+  // ---- residual + LayerNorm: wave w normalizes rows 8 w .. 8 w + 7 ----
+  for (int rr = 0; rr < MGB_ROWS / 4; ++rr) {
+    const int r = w * (MGB_ROWS / 4) + rr;
+    const long row = row0 + r;
+    const bool rok = row < rows;
+    float x[MGB_HMAX / 64];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MGB_HMAX / 64; ++j) {
+      const int c = lane + 64 * j;
+      const bool ok = rok && c < H;
+      const long idx = ok ? row * H + c : 0;
+      const float v = first ? to_f32(input[idx]) : X[idx] + Hprev[idx];
+      x[j] = ok ? v : 0.0f;
+      if (ok) X[idx] = x[j];
+      sum += x[j];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum / (float)H;
+    float var = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MGB_HMAX / 64; ++j) {
+      const float d = (lane + 64 * j < H) ? x[j] - mean : 0.0f;
+      var = fmaf(d, d, var);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) var += __shfl_xor(var, off);
+    const float inv = 1.0f / sqrtf(var / (float)H + MGB_LN_EPS);
+#pragma unroll
+    for (int j = 0; j < MGB_HMAX / 64; ++j) {
+      const int c = lane + 64 * j;
+      if (c < H) sn[r * MGB_LD + c] = fmaf((x[j] - mean) * inv, to_f32(gamma[c]), to_f32(beta[c]));
+      else if (c < MGB_LD) sn[r * MGB_LD + c] = 0.0f;
+    }
+  }
+  __syncthreads();
+  // ---- [32 rows] x [2H columns] on v_mfma_f32_32x32x2_f32: wave w takes column tiles w, w+4, ..;
+  // lane (li, g) supplies A[row li][k = 2 kk + g] and B[k][column li] for k step kk.  The W
+  // column values of 16 k steps are loaded a chunk ahead into one of two register sets.
+  const int li = lane & 31, g = lane >> 5;
+  const int ntile = (2 * H + 31) / 32, nch = ((H + 1) / 2 + 15) / 16;
+  for (int nt = w; nt < ntile; nt += 4) {
+    const int n = nt * 32 + li;  // this lane's output column: gate (n < H) or candidate
+    const bool nok = n < 2 * H;
+    const int nc = min(n, 2 * H - 1);
+    const T* Wc = nc < H ? Wz + nc : Wh + (nc - H);
+    float b0[16], b1[16];
+    auto ldb = [&](float* bb, int ch) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int k = 2 * (16 * ch + i) + g;
+        const float v = to_f32(Wc[(long)min(k, H - 1) * H]);
+        bb[i] = (nok && k < H) ? v : 0.0f;  // zero past H: the zero-padded A rows meet zero B
+      }
+    };
+    mgb_f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    auto mm = [&](const float* bb, int ch) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(sn[li * MGB_LD + 2 * (16 * ch + i) + g], bb[i], acc, 0, 0, 0);
+    };
+    ldb(b0, 0);
+    ldb(b1, min(1, nch - 1));
+    int ch = 0;
+    for (; ch + 1 < nch; ch += 2) {
+      mm(b0, ch);
+      ldb(b0, min(ch + 2, nch - 1));
+      mm(b1, ch + 1);
+      ldb(b1, min(ch + 3, nch - 1));
+    }
+    if (ch < nch) mm(b0, ch);
+    if (nok) {
+      const float bias = to_f32(n < H ? bz[n] : bh[n - H]);
+      float* dst = n < H ? Z + n : C + (n - H);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const long row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (row < rows) dst[row * H] = acc[r] + bias;
+      }
+    }
+  }
+}
+
+// h0[:, l, :] (or zeros) as a contiguous f32 [B, H] initial state
+template <typename T>
+__global__ __launch_bounds__(256) void mgb_h0_kernel(const T* __restrict__ h0, float* __restrict__ dst, int B, int L,
+                                                     int l, int H) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= B * H) return;
+  const int b = e / H, c = e % H;
+  dst[e] = h0 != nullptr ? to_f32(h0[((long)b * L + l) * H + c]) : 0.0f;
+}
+
+// output = x_{L-1} + h_{L-1}
+template <typename T>
+__global__ __launch_bounds__(256) void mgb_out_kernel(const float* __restrict__ X, const float* __restrict__ Hs,
+                                                      T* __restrict__ out, long n) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e < n) out[e] = (T)(X[e] + Hs[e]);
+}
+
+struct MgbWs {
+  float *X, *Z, *C, *Hs, *h0s;
+  size_t total;
+};
+inline MgbWs mgb_layout(void* base, long bth, int B, int H) {
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  MgbWs L{};
+  size_t off = 0;
+  char* p = (char*)base;
+  L.X = (float*)(p + off); off += up(bth * 4);
+  L.Z = (float*)(p + off); off += up(bth * 4);
+  L.C = (float*)(p + off); off += up(bth * 4);
+  L.Hs = (float*)(p + off); off += up(bth * 4);
+  L.h0s = (float*)(p + off); off += up((size_t)B * H * 4);
+  L.total = off;
+  return L;
+}
+
+template <typename T>
+int mgb_run(hipStream_t s, const void* input, const void* weights, const void* h0, void* out, const MgbWs& ws,
+            int B, int Tn, int H, int L) {
+  const long bth = (long)B * Tn * H, rows = (long)B * Tn;
+  const long lstride = 2L * H * H + 4L * H;
+  for (int l = 0; l < L; ++l) {
+    mgb_proj_kernel<T><<<(unsigned)((rows + MGB_ROWS - 1) / MGB_ROWS), 256, 0, s>>>(
+        (const T*)input, ws.X, ws.Hs, (const T*)weights + l * lstride, ws.Z, ws.C, rows, H, l == 0 ? 1 : 0);
+    if (int rc = check_launch("mingru block projection")) return rc;
+    mgb_h0_kernel<T><<<(B * H + 255) / 256, 256, 0, s>>>((const T*)h0, ws.h0s, B, L, l, H);
+    if (int rc = check_launch("mingru block h0")) return rc;
+    if (int rc = launch_fwd<float, OP_MINGRU, true>(s, ws.Z, nullptr, ws.C, ws.h0s, ws.Hs, B, Tn, H)) return rc;
+  }
+  mgb_out_kernel<T><<<(unsigned)((bth + 255) / 256), 256, 0, s>>>(ws.X, ws.Hs, (T*)out, bth);
+  return check_launch("mingru block output");
+}
+
 }  // namespace
 }  // namespace edf
 
 extern "C" {
+
+size_t edf_mingru_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype) {
+  (void)num_layers;
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || hidden <= 0) return 0;
+  return edf::mgb_layout(nullptr, (long)batch * seq_len * hidden, batch, hidden).total;
+}
+
+int edf_fused_mingru_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                                void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                                int num_layers, int dtype) {
+  using namespace edf;
+  EDF_REQUIRE(batch > 0 && seq_len > 0 && hidden > 0 && num_layers > 0, EDF_ERR_INVALID_ARG,
+              "dimensions and num_layers must be positive");
+  EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
+  EDF_REQUIRE(hidden <= MGB_HMAX, EDF_ERR_UNSUPPORTED, "hidden %d unsupported (the block scan takes H <= %d)",
+              hidden, MGB_HMAX);
+  EDF_REQUIRE((long)seq_len * hidden * 4 < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row of f32 activations must stay below 2 GiB)");
+  EDF_REQUIRE(input && weights && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const MgbWs L = mgb_layout(workspace, (long)batch * seq_len * hidden, batch, hidden);
+  EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
+              L.total);
+  if (dtype == EDF_BF16)
+    return mgb_run<bf16>(as_stream(stream), input, weights, h0, out, L, batch, seq_len, hidden, num_layers);
+  return mgb_run<float>(as_stream(stream), input, weights, h0, out, L, batch, seq_len, hidden, num_layers);
+}
 
 int edf_fused_mingru_scan(void* stream, const void* z, const void* cand, const void* h0, void* out, int batch,
                           int seq_len, int hidden, int dtype) {

@@ -177,6 +177,33 @@ def linear_scan_backward(a_vals, h0, forward_out, grad_output):
     return da, db, dh0
 
 
+def mingru_block(input, weights, h0, num_layers: int):
+    """``FusedScan.mingru_block/4`` (fused_scan.ex:4465-4479): multi-layer MinGRU inference.
+
+    input [B, T, H]; weights the flat per-layer packing of min_gru.ex:217-241
+    (W_z [H][H] input-major, b_z, W_h, b_h, gamma, beta) in input's dtype; h0
+    [B, num_layers, H] or None (zeros); H <= 256.  Returns the last layer's output
+    [B, T, H].  Inference only (the reference has no backward for it).
+    """
+    input, weights = input.contiguous(), weights.contiguous()
+    h0 = _c(h0)
+    _dev(input, weights, h0)
+    _same(input, weights, h0)
+    bsz, seq, hid = input.shape
+    per_layer = 2 * hid * hid + 4 * hid
+    if weights.numel() != num_layers * per_layer:
+        raise EdificeHipError(f"weights hold {weights.numel()} values, expected {num_layers} x {per_layer}")
+    if h0 is not None and tuple(h0.shape) != (bsz, num_layers, hid):
+        raise EdificeHipError(f"h0 must be [B, num_layers, H] = {(bsz, num_layers, hid)}")
+    out = torch.empty_like(input)
+    flag = dtype_flag(input)
+    wsb = nat.query("edf_mingru_block_workspace_bytes", bsz, seq, hid, num_layers, flag)
+    ws = _u8(wsb, input)
+    nat.call("edf_fused_mingru_block_scan", _stream(), _p(input), _p(weights), _p(h0), _p(out), _p(ws), wsb,
+             bsz, seq, hid, num_layers, flag)
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------

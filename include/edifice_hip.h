@@ -127,6 +127,24 @@ int edf_fused_linear_scan_backward(void* stream, const void* a, const void* h0, 
                                    int seq_len, int hidden, int dtype);
 
 /* ------------------------------------------------------------------------
+ * Multi-layer MinGRU block, inference: per layer LayerNorm -> gate / candidate
+ * projections -> sigmoid -> MinGRU scan -> residual
+ * ------------------------------------------------------------------------ */
+
+/* Replaces fused_mingru_block_scan/8 (input_ptr, weights_ptr, h0_ptr, batch, seq_len,
+ * hidden, num_layers, dtype), lib/edifice/cuda/nif.ex:127 -> fused_mingru_block_scan_launch
+ * (native/cuda/fused_mingru_block_scan.cu:45-140, 160-180).  input, out [B, T, H];
+ * weights packed per layer as W_z [H][H] (input-major), b_z [H], W_h [H][H], b_h [H],
+ * gamma [H], beta [H] in the I/O dtype (lib/edifice/recurrent/min_gru.ex:217-241);
+ * h0 [B, num_layers, H] or NULL (zeros); H <= 256.  Unlike the reference launch it takes
+ * a caller-provided workspace of edf_mingru_block_workspace_bytes() bytes (f32
+ * activations between the layers). */
+size_t edf_mingru_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype);
+int edf_fused_mingru_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                                void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                                int num_layers, int dtype);
+
+/* ------------------------------------------------------------------------
  * Mamba selective scan
  *   x, dt, z, out, grad_x, grad_dt, grad_z: [B, T, D] in io_dtype
  *   A [D, N], B, C [B, T, N], D [D]: param_dtype; grad_A/B/C/D: float32

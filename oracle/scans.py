@@ -13,6 +13,10 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 a≡1 ⇒ cumulative sum, a≡0 ⇒ b, a = 1 - z, b = z h~ ⇒
                                 mingru_scan, torch autograd of a closed-form
                                 (cumulative-product) forward, finite differences.
+  mingru_block                  the per-timestep restatement of the reference kernel
+                                (mingru_block_stepwise), one layer == LayerNorm + dense +
+                                mingru_scan + residual written out, W = 0 with a closed
+                                form, layers compose (L layers == 1 layer applied L times).
   mingru_scan / _backward       seq_len=1 known answer (backward_kernels_test.exs:271-287),
                                 min_gru_random.safetensors block fixture, z≡1 / z≡0
                                 closed forms, torch autograd + finite differences.
@@ -160,6 +164,68 @@ def linear_scan_backward(a, h0, fwd, dy):
         db[:, t] = dh
         carry = dh * a[:, t]
     return da, db, carry
+
+
+# ---------------------------------------------------------------------------
+# Multi-layer MinGRU block (inference)
+# ---------------------------------------------------------------------------
+
+BLOCK_LN_EPS = 1.0e-5  # fused_mingru_block_scan.cu:110, fused_scan.ex:4544
+
+
+def _mingru_block_layer_weights(weights, layer, hid):
+    """Slices of the per-layer packing W_z [H][H], b_z, W_h [H][H], b_h, gamma, beta
+    (min_gru.ex:217-241, fused_scan.ex:4525-4540)."""
+    w = np.asarray(weights, dtype=np.float64).reshape(-1)
+    off = layer * (2 * hid * hid + 4 * hid)
+    parts = []
+    for n in (hid * hid, hid, hid * hid, hid, hid, hid):
+        parts.append(w[off:off + n])
+        off += n
+    wz, bz, wh, bh, gamma, beta = parts
+    return wz.reshape(hid, hid), bz, wh.reshape(hid, hid), bh, gamma, beta
+
+
+def mingru_block(x, weights, h0, num_layers):
+    """Layer by layer over the whole sequence, as ``mingru_block_fallback``
+    (lib/edifice/cuda/fused_scan.ex:4521-4571): LayerNorm (biased variance, eps 1e-5,
+    gamma, beta), z = sigmoid(n W_z + b_z), c = n W_h + b_h, MinGRU scan from h0[:, l],
+    residual x + h.  h0 = None means zeros."""
+    x = np.asarray(x, dtype=np.float64)
+    bsz, seq, hid = x.shape
+    h0 = np.zeros((bsz, num_layers, hid)) if h0 is None else np.asarray(h0, dtype=np.float64)
+    for layer in range(num_layers):
+        wz, bz, wh, bh, gamma, beta = _mingru_block_layer_weights(weights, layer, hid)
+        mean = x.mean(-1, keepdims=True)
+        var = ((x - mean) ** 2).mean(-1, keepdims=True)
+        n = (x - mean) / np.sqrt(var + BLOCK_LN_EPS) * gamma + beta
+        z = sigmoid(n @ wz + bz)
+        c = n @ wh + bh
+        x = x + mingru_scan(z, c, h0[:, layer])
+    return x
+
+
+def mingru_block_stepwise(x, weights, h0, num_layers):
+    """Timestep by timestep, every layer per step, as the reference kernel walks it
+    (native/cuda/fused_mingru_block_scan.cu:73-135); an independent formulation of
+    ``mingru_block``."""
+    x = np.asarray(x, dtype=np.float64)
+    bsz, seq, hid = x.shape
+    h = np.zeros((bsz, num_layers, hid)) if h0 is None else np.array(h0, dtype=np.float64)
+    lw = [_mingru_block_layer_weights(weights, layer, hid) for layer in range(num_layers)]
+    out = np.empty_like(x)
+    for t in range(seq):
+        xv = x[:, t].copy()
+        for layer, (wz, bz, wh, bh, gamma, beta) in enumerate(lw):
+            mean = xv.mean(-1, keepdims=True)
+            var = ((xv - mean) ** 2).mean(-1, keepdims=True)
+            n = (xv - mean) / np.sqrt(var + BLOCK_LN_EPS) * gamma + beta
+            z = sigmoid(n @ wz + bz)
+            c = n @ wh + bh
+            h[:, layer] = (1.0 - z) * h[:, layer] + z * c
+            xv = xv + h[:, layer]
+        out[:, t] = xv
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -73,6 +73,13 @@ def test_bad_dtype_and_unsupported_shapes(lib):
     # a missing workspace is reported, not dereferenced
     rc = lib.edf_fused_flash_attention_backward(*([ctypes.c_void_p(16)] * 10), None, 0, 1, 1, 8, 64, 1, 1)
     assert rc == 4 and b"workspace" in lib.edf_last_error()
+    # the MinGRU block takes H <= 256 and needs its workspace
+    p = ctypes.c_void_p(16)
+    rc = lib.edf_fused_mingru_block_scan(None, p, p, None, p, p, 1 << 30, 2, 4, 257, 1, 0)
+    assert rc == 2 and b"hidden" in lib.edf_last_error()
+    rc = lib.edf_fused_mingru_block_scan(None, p, p, None, p, None, 0, 2, 4, 64, 1, 0)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+    assert lib.edf_mingru_block_workspace_bytes(2, 4, 64, 3, 0) >= 4 * 2 * 4 * 64 * 4 + 2 * 64 * 4
 
 
 def test_workspace_queries(lib):

@@ -211,3 +211,37 @@ def test_linear_scan_full_size(dtype, rng):
     cs = fs.linear_scan(torch.ones_like(ta), tb).float()
     ref = torch.cumsum(tb.float(), dim=1)
     assert ((cs - ref).abs().max() / ref.abs().max()).item() < (1e-5 if dtype == torch.float32 else 2e-2)
+
+
+# ---------------------------------------------------------------------------
+# multi-layer MinGRU block (inference)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bsz,seq,hid,layers", [(1, 5, 8, 1), (2, 37, 64, 2), (3, 130, 100, 3), (2, 64, 256, 2),
+                                                 (1, 33, 77, 4)])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mingru_block(bsz, seq, hid, layers, dtype, rng):
+    """FusedScan.mingru_block/4 against the layer-parallel oracle (itself pinned to the
+    per-timestep walk of fused_mingru_block_scan.cu)."""
+    from edifice_amd import fused_scan as fs
+    announce("mingru_block", shape=(bsz, seq, hid), layers=layers, dtype=dtype)
+    x = rng.normal(size=(bsz, seq, hid))
+    w = rng.normal(scale=hid ** -0.5, size=layers * (2 * hid * hid + 4 * hid))
+    h0 = rng.normal(scale=0.5, size=(bsz, layers, hid))
+    out = fs.mingru_block(to_dev(x, dtype), to_dev(w, dtype), to_dev(h0, dtype), layers)
+    expect = scans.mingru_block(rounded(x, dtype), rounded(w, dtype), rounded(h0, dtype), layers)
+    assert_close(host(out), expect, TOL[dtype], "block out")
+    out0 = fs.mingru_block(to_dev(x, dtype), to_dev(w, dtype), None, layers)
+    expect0 = scans.mingru_block(rounded(x, dtype), rounded(w, dtype), None, layers)
+    assert_close(host(out0), expect0, TOL[dtype], "block out, h0 = 0")
+
+
+def test_mingru_block_full_size(rng):
+    """B=8, T=2048, H=256, 4 layers (the bench shape), float32, against the oracle."""
+    from edifice_amd import fused_scan as fs
+    bsz, seq, hid, layers = 8, 2048, 256, 4
+    announce("mingru_block_full", shape=(bsz, seq, hid), layers=layers)
+    x = rng.normal(size=(bsz, seq, hid)).astype(np.float32)
+    w = rng.normal(scale=hid ** -0.5, size=layers * (2 * hid * hid + 4 * hid)).astype(np.float32)
+    out = fs.mingru_block(to_dev(x, torch.float32), to_dev(w, torch.float32), None, layers)
+    assert_close(host(out), scans.mingru_block(x, w, None, layers), TOL[torch.float32], "block full")

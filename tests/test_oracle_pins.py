@@ -151,6 +151,56 @@ def test_linear_scan_invariants(rng):
     np.testing.assert_allclose(dh0, dh0_g, rtol=1e-12)
 
 
+def _block_weights(rng, hid, layers, scale=0.3):
+    return rng.normal(scale=scale, size=layers * (2 * hid * hid + 4 * hid))
+
+
+def test_mingru_block_formulations_agree(rng):
+    """Layer-parallel restatement (fused_scan.ex:4521-4571) == the per-timestep walk of the
+    reference kernel (fused_mingru_block_scan.cu:73-135)."""
+    x = rng.normal(size=(2, 7, 6))
+    w = _block_weights(rng, 6, 3)
+    h0 = rng.normal(size=(2, 3, 6))
+    np.testing.assert_allclose(scans.mingru_block(x, w, h0, 3), scans.mingru_block_stepwise(x, w, h0, 3),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_mingru_block_one_layer_written_out(rng):
+    x = rng.normal(size=(2, 5, 4))
+    w = _block_weights(rng, 4, 1)
+    h0 = rng.normal(size=(2, 1, 4))
+    wz, bz, wh, bh, gamma, beta = (w[0:16].reshape(4, 4), w[16:20], w[20:36].reshape(4, 4), w[36:40], w[40:44],
+                                   w[44:48])
+    mean = x.mean(-1, keepdims=True)
+    sd = np.sqrt(x.var(-1, keepdims=True) + 1e-5)
+    n = (x - mean) / sd * gamma + beta
+    expect = x + scans.mingru_scan(scans.sigmoid(n @ wz + bz), n @ wh + bh, h0[:, 0])
+    np.testing.assert_allclose(scans.mingru_block(x, w, h0, 1), expect, rtol=1e-12)
+    # L layers == one layer applied L times with that layer's slice of weights and h0
+    w2 = _block_weights(rng, 4, 2)
+    h02 = rng.normal(size=(2, 2, 4))
+    y = scans.mingru_block(x, w2[:48], h02[:, :1], 1)
+    y = scans.mingru_block(y, w2[48:], h02[:, 1:], 1)
+    np.testing.assert_allclose(scans.mingru_block(x, w2, h02, 2), y, rtol=1e-12)
+
+
+def test_mingru_block_zero_projection_closed_form(rng):
+    """W = 0: z = sigmoid(b_z), c = b_h for every step, so one layer gives
+    h_t = b_h + (1 - z)^(t+1) (h0 - b_h) and out = x + h."""
+    hid = 3
+    x = rng.normal(size=(1, 6, hid))
+    w = np.zeros(2 * hid * hid + 4 * hid)
+    bz, bh = rng.normal(size=hid), rng.normal(size=hid)
+    w[hid * hid:hid * hid + hid] = bz
+    w[2 * hid * hid + hid:2 * hid * hid + 2 * hid] = bh
+    w[2 * hid * hid + 2 * hid:2 * hid * hid + 3 * hid] = 1.0  # gamma
+    h0 = rng.normal(size=(1, 1, hid))
+    z = scans.sigmoid(bz)
+    t = np.arange(6)[:, None]
+    h = bh + (1 - z) ** (t + 1) * (h0[0, 0] - bh)
+    np.testing.assert_allclose(scans.mingru_block(x, w, h0, 1)[0], x[0] + h, rtol=1e-12)
+
+
 def test_minlstm_invariants(rng):
     f = rng.uniform(0.05, 1, size=(2, 7, 4))
     i = rng.uniform(0.05, 1, size=(2, 7, 4))
