@@ -188,24 +188,25 @@ def bench_linear_scan(torch, steps, warmup, B, T, H, dtype):
                 fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
 
 
-def bench_mingru_block(torch, steps, warmup, B, T, H, L, dtype):
-    """Multi-layer MinGRU block inference (FusedScan.mingru_block/4): per layer LayerNorm,
-    gate and candidate projections (4 B T H^2 flops), MinGRU scan, residual."""
+def bench_block(torch, steps, warmup, B, T, H, L, dtype, kind="mingru"):
+    """Multi-layer block inference (FusedScan.{mingru,minlstm,linear}_block/4): per layer
+    LayerNorm, P projections (2 P B T H^2 flops; P = 3 for MinLSTM, else 2), scan, residual."""
     from edifice_amd import _native as nat
 
     dev = "cuda"
     g = torch.Generator(device="cuda").manual_seed(1002)
     x = torch.randn(B, T, H, device=dev, generator=g).to(dtype)
-    w = (torch.randn(L * (2 * H * H + 4 * H), device=dev, generator=g) * H ** -0.5).to(dtype)
+    nproj = 3 if kind == "minlstm" else 2
+    w = (torch.randn(L * (nproj * (H * H + H) + 2 * H), device=dev, generator=g) * H ** -0.5).to(dtype)
     out = torch.empty_like(x)
     flag = 1 if dtype == torch.bfloat16 else 0
-    wsb = nat.query("edf_mingru_block_workspace_bytes", B, T, H, L, flag)
+    wsb = nat.query(f"edf_{kind}_block_workspace_bytes", B, T, H, L, flag)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
     def fwd():
-        nat.call("edf_fused_mingru_block_scan", stream, P(x), P(w), None, P(out), P(ws), wsb, B, T, H, L, flag)
+        nat.call(f"edf_fused_{kind}_block_scan", stream, P(x), P(w), None, P(out), P(ws), wsb, B, T, H, L, flag)
 
     for _ in range(warmup):
         fwd()
@@ -215,7 +216,7 @@ def bench_mingru_block(torch, steps, warmup, B, T, H, L, dtype):
             fwd()
     ms = tf.mean_ms()
     return dict(shape=[B, T, H], layers=L, dtype=str(dtype).replace("torch.", ""), ms=ms,
-                tokens_per_s=B * T / ms * 1e3, projection_tflops=4 * B * T * H * H * L / ms / 1e9)
+                tokens_per_s=B * T / ms * 1e3, projection_tflops=2 * nproj * B * T * H * H * L / ms / 1e9)
 
 
 def profiled_traffic(kernels, path=os.path.join(ROOT, "profiles", "selective_scan_c2.md")):
@@ -411,9 +412,10 @@ def main():
             key = f"mingru_bw_{str(dt).replace('torch.', '')}_8x2048x1536"
             configs[key] = bench_mingru(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
     if want("block"):
-        for dt in (torch.float32, torch.bfloat16):
-            key = f"mingru_block_{str(dt).replace('torch.', '')}_8x2048x256_L4"
-            configs[key] = bench_mingru_block(torch, args.steps, args.warmup, 8, 2048, 256, 4, dt)
+        for kind, dt in (("mingru", torch.float32), ("mingru", torch.bfloat16), ("minlstm", torch.float32),
+                         ("linear", torch.float32)):
+            key = f"{kind}_block_{str(dt).replace('torch.', '')}_8x2048x256_L4"
+            configs[key] = bench_block(torch, args.steps, args.warmup, 8, 2048, 256, 4, dt, kind)
     if want("linear"):
         for dt in (torch.bfloat16, torch.float32):
             key = f"linear_scan_{str(dt).replace('torch.', '')}_8x2048x1536"

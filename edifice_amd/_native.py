@@ -30,6 +30,10 @@ SIGNATURES = {
     "edf_fused_linear_scan_backward": (I, [P, P, P, P, P, P, P, P, I, I, I, I]),
     "edf_mingru_block_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_mingru_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
+    "edf_minlstm_block_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_minlstm_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
+    "edf_linear_block_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_linear_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_fused_selective_scan": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
     "edf_selective_scan_states_bytes": (S, [I, I, I, I]),
     "edf_selective_scan_workspace_bytes": (S, [I, I, I, I, I]),

@@ -712,17 +712,22 @@ int bwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand,
 }
 
 // ---------------------------------------------------------------------------------
-// Multi-layer MinGRU block, inference (reference native/cuda/fused_mingru_block_scan.cu:
-// 45-140; fallback lib/edifice/cuda/fused_scan.ex:4521-4571).  Per layer l, with x_0 the
-// input:  n = LayerNorm(x_l) (eps 1e-5, gamma, beta);  z = sigmoid(n W_z + b_z);
-// c = n W_h + b_h;  h_t = (1 - z_t) h_{t-1} + z_t c_t from h0[:, l];  x_{l+1} = x_l + h.
+// Multi-layer blocks, inference.  Per layer l, with x_0 the input and n = LayerNorm(x_l)
+// (biased variance, eps 1e-5, gamma, beta), P projections p_k = n W_k + b_k feed one scan
+// from h0[:, l] and x_{l+1} = x_l + h:
+//   MinGRU  (P = 2: z, c)     h = (1 - sigmoid(z)) h + sigmoid(z) c
+//           native/cuda/fused_mingru_block_scan.cu:45-140, fused_scan.ex:4521-4571
+//   MinLSTM (P = 3: f, i, c)  h = f' h + i' c, f' = s(f) / (s(f) + s(i) + 1e-6), ...
+//           fused_minlstm_block_scan.cu:59-140, fused_scan.ex:4647-4705
+//   linear  (P = 2: a, b)     h = a h + b
+//           fused_linear_block_scan.cu:100-126, fused_scan.ex:4785-4835
 // The reference walks timesteps and layers one by one in one workgroup per batch row
-// (every step a matrix-vector product).  The gates depend on x only, so here each layer is
-// one parallel pass over all (b, t) rows: a projection kernel (the previous layer's
-// residual, the LayerNorm and both products on f32 MFMA, 32 rows per workgroup) and the
-// MinGRU scan above with the sigmoid fused; activations stay in f32 between layers, as in
-// the reference's registers.  Packed weights per layer: W_z [H][H] (input-major), b_z,
-// W_h, b_h, gamma, beta, in the I/O dtype.
+// (every step a matrix-vector product).  The projections depend on x only, so here each
+// layer is one parallel pass over all (b, t) rows: a projection kernel (the previous
+// layer's residual, the LayerNorm and the P products on f32 MFMA, 32 rows per workgroup)
+// and the scan above (sigmoids fused); activations stay in f32 between layers, as in the
+// reference's registers.  Packed weights per layer: W_1 [H][H] (input-major), b_1, ..,
+// W_P, b_P, gamma, beta, in the I/O dtype.
 // ---------------------------------------------------------------------------------
 constexpr int MGB_ROWS = 32;                // rows (b, t) per projection workgroup
 constexpr int MGB_HMAX = 256;
@@ -731,21 +736,21 @@ constexpr float MGB_LN_EPS = 1.0e-5f;
 
 typedef __attribute__((ext_vector_type(16))) float mgb_f32x16;
 
+struct MgbOut {
+  float* p[3];  // the P projection outputs, [rows][H] each
+};
+
 // Layer input x_l (the input for l = 0, else x_{l-1} + h_{l-1}) written back to X, its
-// LayerNorm, and Z = n W_z + b_z (gate logits), C = n W_h + b_h.
-template <typename T>
+// LayerNorm, and the P projections n W_k + b_k.
+template <typename T, int P>
 __global__ __launch_bounds__(256) void mgb_proj_kernel(const T* __restrict__ input, float* __restrict__ X,
                                                        const float* __restrict__ Hprev, const T* __restrict__ Wl,
-                                                       float* __restrict__ Z, float* __restrict__ C, long rows,
-                                                       int H, int first) {
+                                                       const MgbOut po, long rows, int H, int first) {
   __shared__ float sn[MGB_ROWS * MGB_LD];  // normalized rows, zero-padded to an even H
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const long row0 = (long)blockIdx.x * MGB_ROWS;
-  const T* Wz = Wl;
-  const T* bz = Wl + (long)H * H;
-  const T* Wh = bz + H;
-  const T* bh = Wh + (long)H * H;
-  const T* gamma = bh + H;
+  const long pstride = (long)H * H + H;  // W_k [H][H] then b_k [H]
+  const T* gamma = Wl + P * pstride;
   const T* beta = gamma + H;
   // ---- residual + LayerNorm: wave w normalizes rows 8 w .. 8 w + 7 ----
   for (int rr = 0; rr < MGB_ROWS / 4; ++rr) {
@@ -784,16 +789,16 @@ __global__ __launch_bounds__(256) void mgb_proj_kernel(const T* __restrict__ inp
     }
   }
   __syncthreads();
-  // ---- [32 rows] x [2H columns] on v_mfma_f32_32x32x2_f32: wave w takes column tiles w, w+4, ..;
+  // ---- [32 rows] x [P H columns] on v_mfma_f32_32x32x2_f32: wave w takes column tiles w, w+4, ..;
   // lane (li, g) supplies A[row li][k = 2 kk + g] and B[k][column li] for k step kk.  The W
   // column values of 16 k steps are loaded a chunk ahead into one of two register sets.
   const int li = lane & 31, g = lane >> 5;
-  const int ntile = (2 * H + 31) / 32, nch = ((H + 1) / 2 + 15) / 16;
+  const int ntile = (P * H + 31) / 32, nch = ((H + 1) / 2 + 15) / 16;
   for (int nt = w; nt < ntile; nt += 4) {
-    const int n = nt * 32 + li;  // this lane's output column: gate (n < H) or candidate
-    const bool nok = n < 2 * H;
-    const int nc = min(n, 2 * H - 1);
-    const T* Wc = nc < H ? Wz + nc : Wh + (nc - H);
+    const int n = nt * 32 + li;  // this lane's output column: projection n / H, column n % H
+    const bool nok = n < P * H;
+    const int nc = min(n, P * H - 1), pj = nc / H, cj = nc % H;
+    const T* Wc = Wl + pj * pstride + cj;
     float b0[16], b1[16];
     auto ldb = [&](float* bb, int ch) {
 #pragma unroll
@@ -822,8 +827,8 @@ __global__ __launch_bounds__(256) void mgb_proj_kernel(const T* __restrict__ inp
     }
     if (ch < nch) mm(b0, ch);
     if (nok) {
-      const float bias = to_f32(n < H ? bz[n] : bh[n - H]);
-      float* dst = n < H ? Z + n : C + (n - H);
+      const float bias = to_f32(Wl[pj * pstride + (long)H * H + cj]);
+      float* dst = (pj == 0 ? po.p[0] : pj == 1 ? po.p[1] : po.p[2]) + cj;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const long row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -852,38 +857,77 @@ __global__ __launch_bounds__(256) void mgb_out_kernel(const float* __restrict__ 
 }
 
 struct MgbWs {
-  float *X, *Z, *C, *Hs, *h0s;
+  float *X, *Hs, *h0s;
+  float* p[3];
   size_t total;
 };
-inline MgbWs mgb_layout(void* base, long bth, int B, int H) {
+inline MgbWs mgb_layout(void* base, long bth, int B, int H, int P) {
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   MgbWs L{};
   size_t off = 0;
-  char* p = (char*)base;
-  L.X = (float*)(p + off); off += up(bth * 4);
-  L.Z = (float*)(p + off); off += up(bth * 4);
-  L.C = (float*)(p + off); off += up(bth * 4);
-  L.Hs = (float*)(p + off); off += up(bth * 4);
-  L.h0s = (float*)(p + off); off += up((size_t)B * H * 4);
+  char* c = (char*)base;
+  L.X = (float*)(c + off); off += up(bth * 4);
+  L.Hs = (float*)(c + off); off += up(bth * 4);
+  for (int k = 0; k < P; ++k) {
+    L.p[k] = (float*)(c + off);
+    off += up(bth * 4);
+  }
+  L.h0s = (float*)(c + off); off += up((size_t)B * H * 4);
   L.total = off;
   return L;
 }
 
-template <typename T>
+enum { BLK_MINGRU = 0, BLK_MINLSTM = 1, BLK_LINEAR = 2 };
+constexpr int blk_projections(int kind) { return kind == BLK_MINLSTM ? 3 : 2; }
+
+template <typename T, int KIND>
 int mgb_run(hipStream_t s, const void* input, const void* weights, const void* h0, void* out, const MgbWs& ws,
             int B, int Tn, int H, int L) {
+  constexpr int P = blk_projections(KIND);
   const long bth = (long)B * Tn * H, rows = (long)B * Tn;
-  const long lstride = 2L * H * H + 4L * H;
+  const long lstride = P * ((long)H * H + H) + 2L * H;
+  const MgbOut po{{ws.p[0], ws.p[1], ws.p[P - 1]}};
   for (int l = 0; l < L; ++l) {
-    mgb_proj_kernel<T><<<(unsigned)((rows + MGB_ROWS - 1) / MGB_ROWS), 256, 0, s>>>(
-        (const T*)input, ws.X, ws.Hs, (const T*)weights + l * lstride, ws.Z, ws.C, rows, H, l == 0 ? 1 : 0);
-    if (int rc = check_launch("mingru block projection")) return rc;
+    mgb_proj_kernel<T, P><<<(unsigned)((rows + MGB_ROWS - 1) / MGB_ROWS), 256, 0, s>>>(
+        (const T*)input, ws.X, ws.Hs, (const T*)weights + l * lstride, po, rows, H, l == 0 ? 1 : 0);
+    if (int rc = check_launch("block projection")) return rc;
     mgb_h0_kernel<T><<<(B * H + 255) / 256, 256, 0, s>>>((const T*)h0, ws.h0s, B, L, l, H);
-    if (int rc = check_launch("mingru block h0")) return rc;
-    if (int rc = launch_fwd<float, OP_MINGRU, true>(s, ws.Z, nullptr, ws.C, ws.h0s, ws.Hs, B, Tn, H)) return rc;
+    if (int rc = check_launch("block h0")) return rc;
+    int rc;
+    if constexpr (KIND == BLK_MINGRU)
+      rc = launch_fwd<float, OP_MINGRU, true>(s, ws.p[0], nullptr, ws.p[1], ws.h0s, ws.Hs, B, Tn, H);
+    else if constexpr (KIND == BLK_MINLSTM)
+      rc = launch_fwd<float, OP_MINLSTM, true>(s, ws.p[0], ws.p[1], ws.p[2], ws.h0s, ws.Hs, B, Tn, H);
+    else
+      rc = launch_fwd<float, OP_LINEAR, false>(s, ws.p[0], nullptr, ws.p[1], ws.h0s, ws.Hs, B, Tn, H);
+    if (rc) return rc;
   }
   mgb_out_kernel<T><<<(unsigned)((bth + 255) / 256), 256, 0, s>>>(ws.X, ws.Hs, (T*)out, bth);
-  return check_launch("mingru block output");
+  return check_launch("block output");
+}
+
+template <int KIND>
+int block_dispatch(void* stream, const void* input, const void* weights, const void* h0, void* out, void* workspace,
+                   size_t workspace_bytes, int batch, int seq_len, int hidden, int num_layers, int dtype) {
+  EDF_REQUIRE(batch > 0 && seq_len > 0 && hidden > 0 && num_layers > 0, EDF_ERR_INVALID_ARG,
+              "dimensions and num_layers must be positive");
+  EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
+  EDF_REQUIRE(hidden <= MGB_HMAX, EDF_ERR_UNSUPPORTED, "hidden %d unsupported (the block scans take H <= %d)",
+              hidden, MGB_HMAX);
+  EDF_REQUIRE((long)seq_len * hidden * 4 < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row of f32 activations must stay below 2 GiB)");
+  EDF_REQUIRE(input && weights && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const MgbWs L = mgb_layout(workspace, (long)batch * seq_len * hidden, batch, hidden, blk_projections(KIND));
+  EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
+              L.total);
+  if (dtype == EDF_BF16)
+    return mgb_run<bf16, KIND>(as_stream(stream), input, weights, h0, out, L, batch, seq_len, hidden, num_layers);
+  return mgb_run<float, KIND>(as_stream(stream), input, weights, h0, out, L, batch, seq_len, hidden, num_layers);
+}
+
+inline size_t block_ws_bytes(int batch, int seq_len, int hidden, int kind) {
+  if (batch <= 0 || seq_len <= 0 || hidden <= 0) return 0;
+  return mgb_layout(nullptr, (long)batch * seq_len * hidden, batch, hidden, blk_projections(kind)).total;
 }
 
 }  // namespace
@@ -894,28 +938,40 @@ extern "C" {
 size_t edf_mingru_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype) {
   (void)num_layers;
   (void)dtype;
-  if (batch <= 0 || seq_len <= 0 || hidden <= 0) return 0;
-  return edf::mgb_layout(nullptr, (long)batch * seq_len * hidden, batch, hidden).total;
+  return edf::block_ws_bytes(batch, seq_len, hidden, edf::BLK_MINGRU);
 }
 
 int edf_fused_mingru_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
                                 void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
                                 int num_layers, int dtype) {
-  using namespace edf;
-  EDF_REQUIRE(batch > 0 && seq_len > 0 && hidden > 0 && num_layers > 0, EDF_ERR_INVALID_ARG,
-              "dimensions and num_layers must be positive");
-  EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
-  EDF_REQUIRE(hidden <= MGB_HMAX, EDF_ERR_UNSUPPORTED, "hidden %d unsupported (the block scan takes H <= %d)",
-              hidden, MGB_HMAX);
-  EDF_REQUIRE((long)seq_len * hidden * 4 < (1L << 31), EDF_ERR_UNSUPPORTED,
-              "seq_len * hidden too large (one batch row of f32 activations must stay below 2 GiB)");
-  EDF_REQUIRE(input && weights && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
-  const MgbWs L = mgb_layout(workspace, (long)batch * seq_len * hidden, batch, hidden);
-  EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
-              L.total);
-  if (dtype == EDF_BF16)
-    return mgb_run<bf16>(as_stream(stream), input, weights, h0, out, L, batch, seq_len, hidden, num_layers);
-  return mgb_run<float>(as_stream(stream), input, weights, h0, out, L, batch, seq_len, hidden, num_layers);
+  return edf::block_dispatch<edf::BLK_MINGRU>(stream, input, weights, h0, out, workspace, workspace_bytes, batch,
+                                              seq_len, hidden, num_layers, dtype);
+}
+
+size_t edf_minlstm_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype) {
+  (void)num_layers;
+  (void)dtype;
+  return edf::block_ws_bytes(batch, seq_len, hidden, edf::BLK_MINLSTM);
+}
+
+int edf_fused_minlstm_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                                 void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                                 int num_layers, int dtype) {
+  return edf::block_dispatch<edf::BLK_MINLSTM>(stream, input, weights, h0, out, workspace, workspace_bytes, batch,
+                                               seq_len, hidden, num_layers, dtype);
+}
+
+size_t edf_linear_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype) {
+  (void)num_layers;
+  (void)dtype;
+  return edf::block_ws_bytes(batch, seq_len, hidden, edf::BLK_LINEAR);
+}
+
+int edf_fused_linear_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                                void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                                int num_layers, int dtype) {
+  return edf::block_dispatch<edf::BLK_LINEAR>(stream, input, weights, h0, out, workspace, workspace_bytes, batch,
+                                              seq_len, hidden, num_layers, dtype);
 }
 
 int edf_fused_mingru_scan(void* stream, const void* z, const void* cand, const void* h0, void* out, int batch,

@@ -177,6 +177,29 @@ def linear_scan_backward(a_vals, h0, forward_out, grad_output):
     return da, db, dh0
 
 
+_BLOCK_PROJ = {"mingru": 2, "minlstm": 3, "linear": 2}
+
+
+def _block(kind, input, weights, h0, num_layers):
+    input, weights = input.contiguous(), weights.contiguous()
+    h0 = _c(h0)
+    _dev(input, weights, h0)
+    _same(input, weights, h0)
+    bsz, seq, hid = input.shape
+    per_layer = _BLOCK_PROJ[kind] * (hid * hid + hid) + 2 * hid
+    if weights.numel() != num_layers * per_layer:
+        raise EdificeHipError(f"weights hold {weights.numel()} values, expected {num_layers} x {per_layer}")
+    if h0 is not None and tuple(h0.shape) != (bsz, num_layers, hid):
+        raise EdificeHipError(f"h0 must be [B, num_layers, H] = {(bsz, num_layers, hid)}")
+    out = torch.empty_like(input)
+    flag = dtype_flag(input)
+    wsb = nat.query(f"edf_{kind}_block_workspace_bytes", bsz, seq, hid, num_layers, flag)
+    ws = _u8(wsb, input)
+    nat.call(f"edf_fused_{kind}_block_scan", _stream(), _p(input), _p(weights), _p(h0), _p(out), _p(ws), wsb,
+             bsz, seq, hid, num_layers, flag)
+    return out
+
+
 def mingru_block(input, weights, h0, num_layers: int):
     """``FusedScan.mingru_block/4`` (fused_scan.ex:4465-4479): multi-layer MinGRU inference.
 
@@ -185,23 +208,19 @@ def mingru_block(input, weights, h0, num_layers: int):
     [B, num_layers, H] or None (zeros); H <= 256.  Returns the last layer's output
     [B, T, H].  Inference only (the reference has no backward for it).
     """
-    input, weights = input.contiguous(), weights.contiguous()
-    h0 = _c(h0)
-    _dev(input, weights, h0)
-    _same(input, weights, h0)
-    bsz, seq, hid = input.shape
-    per_layer = 2 * hid * hid + 4 * hid
-    if weights.numel() != num_layers * per_layer:
-        raise EdificeHipError(f"weights hold {weights.numel()} values, expected {num_layers} x {per_layer}")
-    if h0 is not None and tuple(h0.shape) != (bsz, num_layers, hid):
-        raise EdificeHipError(f"h0 must be [B, num_layers, H] = {(bsz, num_layers, hid)}")
-    out = torch.empty_like(input)
-    flag = dtype_flag(input)
-    wsb = nat.query("edf_mingru_block_workspace_bytes", bsz, seq, hid, num_layers, flag)
-    ws = _u8(wsb, input)
-    nat.call("edf_fused_mingru_block_scan", _stream(), _p(input), _p(weights), _p(h0), _p(out), _p(ws), wsb,
-             bsz, seq, hid, num_layers, flag)
-    return out
+    return _block("mingru", input, weights, h0, num_layers)
+
+
+def minlstm_block(input, weights, h0, num_layers: int):
+    """``FusedScan.minlstm_block/4`` (fused_scan.ex:4591-4605): as ``mingru_block`` with
+    three projections per layer (W_f, b_f, W_i, b_i, W_h, b_h, gamma, beta)."""
+    return _block("minlstm", input, weights, h0, num_layers)
+
+
+def linear_block(input, weights, h0, num_layers: int):
+    """``FusedScan.linear_block/4`` (fused_scan.ex:4729-4743): projections a, b per layer
+    (W_a, b_a, W_b, b_b, gamma, beta), h = a h + b, residual."""
+    return _block("linear", input, weights, h0, num_layers)
 
 
 # ---------------------------------------------------------------------------

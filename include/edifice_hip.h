@@ -144,6 +144,24 @@ int edf_fused_mingru_block_scan(void* stream, const void* input, const void* wei
                                 void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
                                 int num_layers, int dtype);
 
+/* Replaces fused_minlstm_block_scan/8, lib/edifice/cuda/nif.ex:131 ->
+ * fused_minlstm_block_scan_launch (native/cuda/fused_minlstm_block_scan.cu:59-140): as the
+ * MinGRU block with three projections f, i, c per layer (packing W_f, b_f, W_i, b_i, W_h,
+ * b_h, gamma, beta) and h = f' h + i' c, f' = s(f) / (s(f) + s(i) + 1e-6). */
+size_t edf_minlstm_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype);
+int edf_fused_minlstm_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                                 void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                                 int num_layers, int dtype);
+
+/* Replaces fused_linear_block_scan/8, lib/edifice/cuda/nif.ex:135 ->
+ * fused_linear_block_scan_launch (native/cuda/fused_linear_block_scan.cu:100-126): two
+ * projections a, b per layer (packing W_a, b_a, W_b, b_b, gamma, beta), no activation,
+ * h = a h + b. */
+size_t edf_linear_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype);
+int edf_fused_linear_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                                void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                                int num_layers, int dtype);
+
 /* ------------------------------------------------------------------------
  * Mamba selective scan
  *   x, dt, z, out, grad_x, grad_dt, grad_z: [B, T, D] in io_dtype

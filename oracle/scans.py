@@ -13,9 +13,10 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 a≡1 ⇒ cumulative sum, a≡0 ⇒ b, a = 1 - z, b = z h~ ⇒
                                 mingru_scan, torch autograd of a closed-form
                                 (cumulative-product) forward, finite differences.
-  mingru_block                  the per-timestep restatement of the reference kernel
-                                (mingru_block_stepwise), one layer == LayerNorm + dense +
-                                mingru_scan + residual written out, W = 0 with a closed
+  block (mingru/minlstm/linear) the per-timestep restatement of the reference kernels
+                                (block_stepwise), one MinGRU / MinLSTM / linear layer ==
+                                LayerNorm + dense + mingru_scan / minlstm_scan /
+                                linear_scan + residual written out, W = 0 with a closed
                                 form, layers compose (L layers == 1 layer applied L times).
   mingru_scan / _backward       seq_len=1 known answer (backward_kernels_test.exs:271-287),
                                 min_gru_random.safetensors block fixture, z≡1 / z≡0
@@ -173,59 +174,89 @@ def linear_scan_backward(a, h0, fwd, dy):
 BLOCK_LN_EPS = 1.0e-5  # fused_mingru_block_scan.cu:110, fused_scan.ex:4544
 
 
-def _mingru_block_layer_weights(weights, layer, hid):
-    """Slices of the per-layer packing W_z [H][H], b_z, W_h [H][H], b_h, gamma, beta
-    (min_gru.ex:217-241, fused_scan.ex:4525-4540)."""
+BLOCK_PROJECTIONS = {"mingru": 2, "minlstm": 3, "linear": 2}
+
+
+def _block_layer_weights(weights, layer, hid, nproj):
+    """Slices of the per-layer packing W_1 [H][H], b_1, .., W_P, b_P, gamma, beta
+    (min_gru.ex:217-241; fused_scan.ex:4525-4540, 4653-4672, 4789-4802)."""
     w = np.asarray(weights, dtype=np.float64).reshape(-1)
-    off = layer * (2 * hid * hid + 4 * hid)
-    parts = []
-    for n in (hid * hid, hid, hid * hid, hid, hid, hid):
-        parts.append(w[off:off + n])
-        off += n
-    wz, bz, wh, bh, gamma, beta = parts
-    return wz.reshape(hid, hid), bz, wh.reshape(hid, hid), bh, gamma, beta
+    off = layer * (nproj * (hid * hid + hid) + 2 * hid)
+    proj = []
+    for _ in range(nproj):
+        proj.append((w[off:off + hid * hid].reshape(hid, hid), w[off + hid * hid:off + hid * hid + hid]))
+        off += hid * hid + hid
+    return proj, w[off:off + hid], w[off + hid:off + 2 * hid]
 
 
-def mingru_block(x, weights, h0, num_layers):
-    """Layer by layer over the whole sequence, as ``mingru_block_fallback``
-    (lib/edifice/cuda/fused_scan.ex:4521-4571): LayerNorm (biased variance, eps 1e-5,
-    gamma, beta), z = sigmoid(n W_z + b_z), c = n W_h + b_h, MinGRU scan from h0[:, l],
+def _block_norm(x, gamma, beta):
+    mean = x.mean(-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(-1, keepdims=True)
+    return (x - mean) / np.sqrt(var + BLOCK_LN_EPS) * gamma + beta
+
+
+def _block_step_coeffs(kind, p):
+    """(a, b) of h = a h + b from the layer's projections (fused_mingru_block_scan.cu:127-131,
+    fused_minlstm_block_scan.cu:128-137, fused_linear_block_scan.cu:112-123)."""
+    if kind == "mingru":
+        z = sigmoid(p[0])
+        return 1.0 - z, z * p[1]
+    if kind == "minlstm":
+        sf, si = sigmoid(p[0]), sigmoid(p[1])
+        s = sf + si + MINLSTM_EPS
+        return sf / s, si / s * p[2]
+    return p[0], p[1]
+
+
+def block(kind, x, weights, h0, num_layers):
+    """Layer by layer over the whole sequence, as the reference fallbacks
+    ``mingru_block_fallback`` / ``minlstm_block_fallback`` / ``linear_block_fallback``
+    (lib/edifice/cuda/fused_scan.ex:4521-4571, 4647-4705, 4785-4835): LayerNorm (biased
+    variance, eps 1e-5, gamma, beta), the projections, the layer's scan from h0[:, l],
     residual x + h.  h0 = None means zeros."""
     x = np.asarray(x, dtype=np.float64)
     bsz, seq, hid = x.shape
     h0 = np.zeros((bsz, num_layers, hid)) if h0 is None else np.asarray(h0, dtype=np.float64)
     for layer in range(num_layers):
-        wz, bz, wh, bh, gamma, beta = _mingru_block_layer_weights(weights, layer, hid)
-        mean = x.mean(-1, keepdims=True)
-        var = ((x - mean) ** 2).mean(-1, keepdims=True)
-        n = (x - mean) / np.sqrt(var + BLOCK_LN_EPS) * gamma + beta
-        z = sigmoid(n @ wz + bz)
-        c = n @ wh + bh
-        x = x + mingru_scan(z, c, h0[:, layer])
+        proj, gamma, beta = _block_layer_weights(weights, layer, hid, BLOCK_PROJECTIONS[kind])
+        n = _block_norm(x, gamma, beta)
+        a, b = _block_step_coeffs(kind, [n @ w + bias for w, bias in proj])
+        h = h0[:, layer].copy()
+        hs = np.empty_like(x)
+        for t in range(seq):
+            h = a[:, t] * h + b[:, t]
+            hs[:, t] = h
+        x = x + hs
     return x
 
 
-def mingru_block_stepwise(x, weights, h0, num_layers):
-    """Timestep by timestep, every layer per step, as the reference kernel walks it
-    (native/cuda/fused_mingru_block_scan.cu:73-135); an independent formulation of
-    ``mingru_block``."""
+def block_stepwise(kind, x, weights, h0, num_layers):
+    """Timestep by timestep, every layer per step, as the reference kernels walk it
+    (fused_mingru_block_scan.cu:73-135, fused_minlstm_block_scan.cu:66-144,
+    fused_linear_block_scan.cu:68-130); an independent formulation of ``block``."""
     x = np.asarray(x, dtype=np.float64)
     bsz, seq, hid = x.shape
     h = np.zeros((bsz, num_layers, hid)) if h0 is None else np.array(h0, dtype=np.float64)
-    lw = [_mingru_block_layer_weights(weights, layer, hid) for layer in range(num_layers)]
+    lw = [_block_layer_weights(weights, layer, hid, BLOCK_PROJECTIONS[kind]) for layer in range(num_layers)]
     out = np.empty_like(x)
     for t in range(seq):
         xv = x[:, t].copy()
-        for layer, (wz, bz, wh, bh, gamma, beta) in enumerate(lw):
-            mean = xv.mean(-1, keepdims=True)
-            var = ((xv - mean) ** 2).mean(-1, keepdims=True)
-            n = (xv - mean) / np.sqrt(var + BLOCK_LN_EPS) * gamma + beta
-            z = sigmoid(n @ wz + bz)
-            c = n @ wh + bh
-            h[:, layer] = (1.0 - z) * h[:, layer] + z * c
+        for layer, (proj, gamma, beta) in enumerate(lw):
+            n = _block_norm(xv, gamma, beta)
+            a, b = _block_step_coeffs(kind, [n @ w + bias for w, bias in proj])
+            h[:, layer] = a * h[:, layer] + b
             xv = xv + h[:, layer]
         out[:, t] = xv
     return out
+
+
+def mingru_block(x, weights, h0, num_layers):
+    """``block("mingru", ...)``: the multi-layer MinGRU block (fused_scan.ex:4521-4571)."""
+    return block("mingru", x, weights, h0, num_layers)
+
+
+def mingru_block_stepwise(x, weights, h0, num_layers):
+    return block_stepwise("mingru", x, weights, h0, num_layers)
 
 
 # ---------------------------------------------------------------------------

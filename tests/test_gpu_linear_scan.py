@@ -220,19 +220,27 @@ def test_linear_scan_full_size(dtype, rng):
 @pytest.mark.parametrize("bsz,seq,hid,layers", [(1, 5, 8, 1), (2, 37, 64, 2), (3, 130, 100, 3), (2, 64, 256, 2),
                                                  (1, 33, 77, 4)])
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_mingru_block(bsz, seq, hid, layers, dtype, rng):
-    """FusedScan.mingru_block/4 against the layer-parallel oracle (itself pinned to the
-    per-timestep walk of fused_mingru_block_scan.cu)."""
+@pytest.mark.parametrize("kind", ["mingru", "minlstm", "linear"])
+def test_block(kind, bsz, seq, hid, layers, dtype, rng):
+    """FusedScan.{mingru,minlstm,linear}_block/4 against the layer-parallel oracle (itself
+    pinned to the per-timestep walk of the reference kernels)."""
     from edifice_amd import fused_scan as fs
-    announce("mingru_block", shape=(bsz, seq, hid), layers=layers, dtype=dtype)
+    announce(f"{kind}_block", shape=(bsz, seq, hid), layers=layers, dtype=dtype)
+    nproj = scans.BLOCK_PROJECTIONS[kind]
     x = rng.normal(size=(bsz, seq, hid))
-    w = rng.normal(scale=hid ** -0.5, size=layers * (2 * hid * hid + 4 * hid))
+    w = rng.normal(scale=hid ** -0.5, size=layers * (nproj * (hid * hid + hid) + 2 * hid))
+    if kind == "linear":  # keep |a| < 1 so the recurrence stays bounded: a = n W_a + b_a, b_a = 0.5
+        wl = w.reshape(layers, -1)
+        wl[:, :hid * hid] *= 0.1
+        wl[:, hid * hid:hid * hid + hid] = 0.5
+        w = wl.reshape(-1)
     h0 = rng.normal(scale=0.5, size=(bsz, layers, hid))
-    out = fs.mingru_block(to_dev(x, dtype), to_dev(w, dtype), to_dev(h0, dtype), layers)
-    expect = scans.mingru_block(rounded(x, dtype), rounded(w, dtype), rounded(h0, dtype), layers)
+    op = getattr(fs, f"{kind}_block")
+    out = op(to_dev(x, dtype), to_dev(w, dtype), to_dev(h0, dtype), layers)
+    expect = scans.block(kind, rounded(x, dtype), rounded(w, dtype), rounded(h0, dtype), layers)
     assert_close(host(out), expect, TOL[dtype], "block out")
-    out0 = fs.mingru_block(to_dev(x, dtype), to_dev(w, dtype), None, layers)
-    expect0 = scans.mingru_block(rounded(x, dtype), rounded(w, dtype), None, layers)
+    out0 = op(to_dev(x, dtype), to_dev(w, dtype), None, layers)
+    expect0 = scans.block(kind, rounded(x, dtype), rounded(w, dtype), None, layers)
     assert_close(host(out0), expect0, TOL[dtype], "block out, h0 = 0")
 
 

@@ -151,18 +151,44 @@ def test_linear_scan_invariants(rng):
     np.testing.assert_allclose(dh0, dh0_g, rtol=1e-12)
 
 
-def _block_weights(rng, hid, layers, scale=0.3):
-    return rng.normal(scale=scale, size=layers * (2 * hid * hid + 4 * hid))
+def _block_weights(rng, hid, layers, scale=0.3, nproj=2):
+    return rng.normal(scale=scale, size=layers * (nproj * (hid * hid + hid) + 2 * hid))
 
 
-def test_mingru_block_formulations_agree(rng):
-    """Layer-parallel restatement (fused_scan.ex:4521-4571) == the per-timestep walk of the
-    reference kernel (fused_mingru_block_scan.cu:73-135)."""
+@pytest.mark.parametrize("kind", ["mingru", "minlstm", "linear"])
+def test_block_formulations_agree(rng, kind):
+    """Layer-parallel restatement (the reference fallbacks) == the per-timestep walk of the
+    reference kernels (fused_*_block_scan.cu)."""
     x = rng.normal(size=(2, 7, 6))
-    w = _block_weights(rng, 6, 3)
+    w = _block_weights(rng, 6, 3, nproj=scans.BLOCK_PROJECTIONS[kind])
     h0 = rng.normal(size=(2, 3, 6))
-    np.testing.assert_allclose(scans.mingru_block(x, w, h0, 3), scans.mingru_block_stepwise(x, w, h0, 3),
+    np.testing.assert_allclose(scans.block(kind, x, w, h0, 3), scans.block_stepwise(kind, x, w, h0, 3),
                                rtol=1e-12, atol=1e-12)
+
+
+def test_minlstm_and_linear_block_one_layer_written_out(rng):
+    hid = 4
+    x = rng.normal(size=(2, 5, hid))
+    h0 = rng.normal(size=(2, 1, hid))
+    mean = x.mean(-1, keepdims=True)
+    sd = np.sqrt(x.var(-1, keepdims=True) + 1e-5)
+
+    def proj(w, k):
+        o = k * (hid * hid + hid)
+        return w[o:o + hid * hid].reshape(hid, hid), w[o + hid * hid:o + hid * hid + hid]
+
+    w3 = _block_weights(rng, hid, 1, nproj=3)
+    gamma, beta = w3[3 * 20:3 * 20 + hid], w3[3 * 20 + hid:]
+    n = (x - mean) / sd * gamma + beta
+    (wf, bf), (wi, bi), (wh, bh) = proj(w3, 0), proj(w3, 1), proj(w3, 2)
+    expect = x + scans.minlstm_scan(scans.sigmoid(n @ wf + bf), scans.sigmoid(n @ wi + bi), n @ wh + bh, h0[:, 0])
+    np.testing.assert_allclose(scans.block("minlstm", x, w3, h0, 1), expect, rtol=1e-12)
+    w2 = _block_weights(rng, hid, 1, nproj=2)
+    gamma, beta = w2[2 * 20:2 * 20 + hid], w2[2 * 20 + hid:]
+    n = (x - mean) / sd * gamma + beta
+    (wa, ba), (wb, bb) = proj(w2, 0), proj(w2, 1)
+    expect = x + scans.linear_scan(n @ wa + ba, n @ wb + bb, h0[:, 0])
+    np.testing.assert_allclose(scans.block("linear", x, w2, h0, 1), expect, rtol=1e-12)
 
 
 def test_mingru_block_one_layer_written_out(rng):
