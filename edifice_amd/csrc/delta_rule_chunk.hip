@@ -565,7 +565,9 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sdOt[DK * TS];  // dO^T [d_v][t]
   __shared__ __attribute__((aligned(16))) bf16 sQg[DK * TS];  // (diag(gamma) Q)^T [d_k][t]
   __shared__ float lg[CH], gm[CH];
-  __shared__ __attribute__((aligned(16))) bf16 sScr[4][SCR_ELEMS];  // per-wave store staging
+  // each wave's 32 output rows (d_v = 32 w + ..) staged whole: dvl rows of 64 t, then dhl
+  // rows of 128 d_k, written as full rows (128 / 256 contiguous bytes)
+  __shared__ __attribute__((aligned(16))) bf16 sRow[4][32 * KS];
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -610,8 +612,16 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
     for (int kk = 2 * I; kk < 4; ++kk)
       X = mfma32(*(const bf16x8*)(sPt + (32 * I + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdOt + (32 * w + li) * TS + 16 * kk + 8 * g), X);
-    store_rows_staged(p.dvl + ci * DK * CH + (long)(32 * w) * CH + 32 * I, CH, X, l, sScr[w]);
+    store_rows(sRow[w] + 32 * I, TS, X, li, g);
   }
+  // this wave's rows are private: no workgroup barrier, the rows are a contiguous block
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {  // 32 rows x 128 bytes
+    const int e = l + 64 * i, row = e >> 3, ch = e & 7;
+    *(bf16x8*)(p.dvl + ci * DK * CH + (long)(32 * w + row) * CH + 8 * ch) = *(const bf16x8*)(sRow[w] + row * TS + 8 * ch);
+  }
+  __builtin_amdgcn_wave_barrier();
   // Q^T diag(gamma) dO: rows d_k (tile I), columns d_v = 32 w + li
 #pragma unroll
   for (int I = 0; I < 4; ++I) {
@@ -620,7 +630,13 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
     for (int kk = 0; kk < 4; ++kk)
       X = mfma32(*(const bf16x8*)(sQg + (32 * I + li) * TS + 16 * kk + 8 * g),
                  *(const bf16x8*)(sdOt + (32 * w + li) * TS + 16 * kk + 8 * g), X);
-    store_rows_staged(p.dhl + ci * DK * DK + (long)(32 * w) * DK + 32 * I, DK, X, l, sScr[w]);
+    store_rows(sRow[w] + 32 * I, KS, X, li, g);
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {  // 32 rows x 256 bytes
+    const int e = l + 64 * i, row = e >> 4, ch = e & 15;
+    *(bf16x8*)(p.dhl + ci * DK * DK + (long)(32 * w + row) * DK + 8 * ch) = *(const bf16x8*)(sRow[w] + row * KS + 8 * ch);
   }
 }
 

@@ -74,25 +74,6 @@ EDF_DEVICE void store_rows(bf16* dst, long ld, const f32x16& x, int li, int g, f
   }
 }
 
-// store_rows through a per-wave LDS tile (SCR_ELEMS bf16 owned by the calling wave): the
-// same result for the first nrows output rows, but each store instruction then writes 16
-// whole 64-byte row segments instead of 16-byte pieces of 32 rows, which the memory pipeline
-// absorbs several times faster.
-constexpr int SCR_LD = 40;  // 80-byte rows: 16-byte aligned reads
-constexpr int SCR_ELEMS = 32 * SCR_LD;
-EDF_DEVICE void store_rows_staged(bf16* dst, long ld, const f32x16& x, int lane, bf16* scratch, int nrows = 32,
-                                  float scale = 1.0f) {
-  store_rows(scratch, SCR_LD, x, lane & 31, lane >> 5, scale);
-  __builtin_amdgcn_wave_barrier();  // the tile writes before the row reads
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = 16 * i + (lane >> 2), ch = lane & 3;
-    const bf16x8 v = *(const bf16x8*)(scratch + row * SCR_LD + 8 * ch);
-    if (row < nrows) *(bf16x8*)(dst + (long)row * ld + 8 * ch) = v;
-  }
-  __builtin_amdgcn_wave_barrier();  // and the reads before the next tile's writes
-}
-
 // ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, with lane i supplying the
 // address A_i of four consecutive bf16, lane j = 4 a + b receives element b of
 // A_{a}, A_{a+4}, A_{a+8}, A_{a+12} (layout checked on the GPU by
