@@ -324,6 +324,39 @@ def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128, causal=True):
                 shape=dict(B=B, H=H, T=T, d=d, causal=causal))
 
 
+def bench_fox(torch, steps, warmup, B=4, H=32, T=4096, d=128):
+    """FoX (forgetting) attention at the config-4 shape, bf16, causal: flops as config 4."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(4001)
+    dev, bf = "cuda", torch.bfloat16
+    std = d ** -0.25
+    q, k, v, do = (torch.randn(B, H, T, d, device=dev, generator=g).mul_(std).to(bf) for _ in range(4))
+    cs = torch.cumsum(torch.nn.functional.logsigmoid(torch.randn(B, H, T, device=dev, generator=g) + 2.0), -1).to(bf)
+    out = torch.empty_like(q)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    dq, dk, dv, dcs = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(cs)
+    wsb = nat.query("edf_fox_attention_backward_workspace_bytes", B, H, T, d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_fox_attention", stream, P(q), P(k), P(v), P(cs), P(out), P(lse), B, H, T, d, 1)
+
+    def bwd():
+        nat.call("edf_fused_fox_attention_backward", stream, P(q), P(k), P(v), P(cs), P(out), P(do), P(lse), P(dq),
+                 P(dk), P(dv), P(dcs), P(ws), wsb, B, H, T, d, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
+    fflops = 4 * B * H * T * T * d / 2
+    bflops = 2.5 * fflops
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, fwd_tflops=fflops / fwd_ms / 1e9, bwd_tflops=bflops / bwd_ms / 1e9,
+                fwd_bwd_tflops=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9,
+                fwd_bwd_mfma_frac=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9 / MFMA_BF16_PEAK_TFLOPS,
+                shape=dict(B=B, H=H, T=T, d=d, causal=True))
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
@@ -428,6 +461,7 @@ def main():
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
         configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,
                                                                          causal=False)
+        configs["fox_attention_4x32x4096x128"] = bench_fox(torch, args.steps, args.warmup)
     if want("hybrid"):
         configs["c5_hybrid_decoder"] = bench_hybrid(torch, max(2, args.steps // 5), 1)
     bwd_dom = ss["bwd_ms"] >= ss["fwd_ms"]

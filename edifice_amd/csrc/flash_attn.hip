@@ -28,11 +28,17 @@ namespace edf {
 namespace {
 
 constexpr float LN2 = 0.6931471805599453f;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
 
-template <int HD, bool CAUSAL>
+// FOX: the forgetting-attention bias cs_q - cs_k (CS [BH][T], cumulative log forget
+// gates; reference native/cuda/fused_fox_attention.cu:1-14, fused_scan.ex:3860-3905) is
+// added to every score; scores are kept unscaled, so the bias enters as
+// (cs_q - cs_k) sqrt(d) (sqd).
+template <int HD, bool CAUSAL, bool FOX = false>
 __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                              const bf16* __restrict__ V, bf16* __restrict__ O,
-                                                             float* __restrict__ LSE, int T, float scale_log2) {
+                                                             float* __restrict__ LSE, int T, float scale_log2,
+                                                             const bf16* __restrict__ CS, float sqd) {
   constexpr int BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   constexpr int CPR = HD / 8;             // 16-byte chunks per row
@@ -40,6 +46,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
   static_assert(CPT >= 1 && BN * CPR % 256 == 0, "tile staging");
   __shared__ __attribute__((aligned(16))) bf16 sK[2][lds_tile_elems<HD>(BN)];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][lds_tile_elems<HD>(BN)];
+  __shared__ __attribute__((aligned(16))) float sCS[FOX ? 2 : 1][FOX ? BN : 4];  // cs of the tile's keys
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -66,6 +73,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
 
   // K / V tiles: global -> registers one tile ahead, registers -> LDS double buffer
   bf16x8 rk[CPT], rv[CPT];
+  float rcs = 0.0f;
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -75,6 +83,9 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
       rk[i] = *(const bf16x8*)(Kh + key * HD + col);
       rv[i] = *(const bf16x8*)(Vh + key * HD + col);
     }
+    if constexpr (FOX) {
+      if (tid < BN) rcs = to_f32(CS[bh * T + min(k0 + tid, T - 1)]);
+    }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
@@ -83,7 +94,11 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
       *(bf16x8*)(&sK[buf][lds_off<HD>(row, col)]) = rk[i];
       *(bf16x8*)(&sV[buf][lds_off<HD>(row, col)]) = rv[i];
     }
+    if constexpr (FOX) {
+      if (tid < BN) sCS[buf][tid] = rcs;
+    }
   };
+  const float csq = FOX && myq < T ? to_f32(CS[bh * T + myq]) * sqd : 0.0f;
 
   const int kend = CAUSAL ? min(T, q0 + BM) : T;
   const int nkt = (kend + BN - 1) / BN;
@@ -107,6 +122,16 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
         const bf16x8 a = *(const bf16x8*)(sk + lds_off<HD>(h2 * 32 + li, kk * 16 + 8 * g));
         s[h2] = mfma32(a, qf[kk], s[h2]);
       }
+    }
+    if constexpr (FOX) {  // + (cs_q - cs_key) sqrt(d); key h2 * 32 + 8 rb + 4 g + e
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          const f32x4 ck = *(const f32x4*)(&sCS[buf][h2 * 32 + 8 * rb + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[h2][4 * rb + e] += fmaf(-ck[e], sqd, csq);
+        }
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -224,7 +249,8 @@ template <typename TT, int DPL>
 __global__ __launch_bounds__(256) void fa_fwd_wave_kernel(const TT* __restrict__ Q, const TT* __restrict__ K,
                                                           const TT* __restrict__ V, TT* __restrict__ O,
                                                           float* __restrict__ LSE, int BH, int T, int HD,
-                                                          float scale_log2, int causal) {
+                                                          float scale_log2, int causal, const TT* __restrict__ CS,
+                                                          float sqd) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= BH * T) return;
@@ -238,6 +264,7 @@ __global__ __launch_bounds__(256) void fa_fwd_wave_kernel(const TT* __restrict__
     o[e] = 0.0f;
   }
   float m = -INFINITY, lsum = 0.0f;
+  const float csi = CS != nullptr ? ld(CS, bh * T + i) * sqd : 0.0f;
   const int jend = causal ? i + 1 : T;
   for (int j = 0; j < jend; ++j) {
     const long kb = (bh * T + j) * HD;
@@ -249,6 +276,7 @@ __global__ __launch_bounds__(256) void fa_fwd_wave_kernel(const TT* __restrict__
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (CS != nullptr) s += fmaf(-ld(CS, bh * T + j), sqd, csi);  // FoX bias (cs_i - cs_j) sqrt(d)
     s *= scale_log2;
     const float mnew = fmaxf(m, s);
     const float alpha = fast_exp2(m - mnew);
@@ -296,30 +324,31 @@ __global__ void debug_tr16_kernel(const bf16* x, bf16* out) {
 
 template <int HD>
 void launch_mfma_fwd(hipStream_t s, const void* q, const void* k, const void* v, void* o, float* lse, int BH, int T,
-                     int causal, float scale_log2) {
+                     int causal, float scale_log2, const void* cs = nullptr, float sqd = 0.0f) {
   const dim3 grid((T + 127) / 128, BH);
-  if (causal)
-    fa_fwd_mfma_kernel<HD, true><<<grid, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)o, lse,
-                                                      T, scale_log2);
+  const bf16 *Q = (const bf16*)q, *K = (const bf16*)k, *V = (const bf16*)v, *CS = (const bf16*)cs;
+  if (cs != nullptr)  // FoX attention is causal
+    fa_fwd_mfma_kernel<HD, true, true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, CS, sqd);
+  else if (causal)
+    fa_fwd_mfma_kernel<HD, true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
   else
-    fa_fwd_mfma_kernel<HD, false><<<grid, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)o, lse,
-                                                       T, scale_log2);
+    fa_fwd_mfma_kernel<HD, false><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
 }
 
 template <typename TT>
 void launch_wave_fwd(hipStream_t s, const void* q, const void* k, const void* v, void* o, float* lse, int BH, int T,
-                     int HD, int causal, float scale_log2) {
+                     int HD, int causal, float scale_log2, const void* cs = nullptr, float sqd = 0.0f) {
   const long rows = (long)BH * T;
   const unsigned grid = (unsigned)((rows + 3) / 4);
   if (HD <= 64)
     fa_fwd_wave_kernel<TT, 1><<<grid, 256, 0, s>>>((const TT*)q, (const TT*)k, (const TT*)v, (TT*)o, lse, BH, T, HD,
-                                                   scale_log2, causal);
+                                                   scale_log2, causal, (const TT*)cs, sqd);
   else if (HD <= 128)
     fa_fwd_wave_kernel<TT, 2><<<grid, 256, 0, s>>>((const TT*)q, (const TT*)k, (const TT*)v, (TT*)o, lse, BH, T, HD,
-                                                   scale_log2, causal);
+                                                   scale_log2, causal, (const TT*)cs, sqd);
   else
     fa_fwd_wave_kernel<TT, 4><<<grid, 256, 0, s>>>((const TT*)q, (const TT*)k, (const TT*)v, (TT*)o, lse, BH, T, HD,
-                                                   scale_log2, causal);
+                                                   scale_log2, causal, (const TT*)cs, sqd);
 }
 
 }  // namespace
@@ -363,6 +392,33 @@ int edf_fused_flash_attention(void* stream, const void* q, const void* k, const 
     launch_wave_fwd<float>(s, q, k, v, out, lse, BH, seq_len, head_dim, causal, scale_log2);
   }
   return check_launch("flash attention");
+}
+
+int edf_fused_fox_attention(void* stream, const void* q, const void* k, const void* v, const void* cs, void* out,
+                            float* lse, int batch, int num_heads, int seq_len, int head_dim, int dtype) {
+  using namespace edf;
+  EDF_REQUIRE(batch > 0 && num_heads > 0 && seq_len > 0 && head_dim > 0, EDF_ERR_INVALID_ARG,
+              "dimensions must be positive");
+  EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
+  EDF_REQUIRE(head_dim <= 256, EDF_ERR_UNSUPPORTED, "head_dim %d > 256 unsupported", head_dim);
+  EDF_REQUIRE(q && k && v && cs && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  hipStream_t s = as_stream(stream);
+  const int BH = batch * num_heads;
+  const float scale_log2 = LOG2E / sqrtf((float)head_dim);
+  const float sqd = sqrtf((float)head_dim);
+  if (dtype == EDF_BF16 && (head_dim == 32 || head_dim == 64 || head_dim == 128)) {
+    if (head_dim == 128)
+      launch_mfma_fwd<128>(s, q, k, v, out, lse, BH, seq_len, 1, scale_log2, cs, sqd);
+    else if (head_dim == 64)
+      launch_mfma_fwd<64>(s, q, k, v, out, lse, BH, seq_len, 1, scale_log2, cs, sqd);
+    else
+      launch_mfma_fwd<32>(s, q, k, v, out, lse, BH, seq_len, 1, scale_log2, cs, sqd);
+  } else if (dtype == EDF_BF16) {
+    launch_wave_fwd<bf16>(s, q, k, v, out, lse, BH, seq_len, head_dim, 1, scale_log2, cs, sqd);
+  } else {
+    launch_wave_fwd<float>(s, q, k, v, out, lse, BH, seq_len, head_dim, 1, scale_log2, cs, sqd);
+  }
+  return check_launch("fox attention");
 }
 
 }  // extern "C"

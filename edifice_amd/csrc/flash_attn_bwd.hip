@@ -52,13 +52,16 @@ __global__ __launch_bounds__(256) void fa_bwd_dot_kernel(const TT* __restrict__ 
 // dV^T += dO^T P and dK^T += Q^T dS take P and dS straight from the accumulator
 // registers as B fragments (query order as the accumulator rows hold it) and the
 // transposed A operands from the row-major tiles with ds_read_b64_tr_b16.
-template <int HD, bool CAUSAL>
+// FOX (forgetting attention, causal): scores carry + (cs_q - cs_k) sqrt(d) (sqd); this
+// kernel also writes -sum_q dS_qk, the key side of d cs, to DCSK (f32 [BH][T]).
+template <int HD, bool CAUSAL, bool FOX = false>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                              const bf16* __restrict__ V, const bf16* __restrict__ dO,
                                                              const float* __restrict__ LSE,
                                                              const float* __restrict__ Dd, bf16* __restrict__ dK,
                                                              bf16* __restrict__ dV, int T, float scale_log2,
-                                                             float scale) {
+                                                             float scale, const bf16* __restrict__ CS,
+                                                             float* __restrict__ DCSK, float sqd) {
   constexpr int BKEY = 128, BQ = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   constexpr int CPR = HD / 8;          // 16-byte chunks per row
@@ -68,6 +71,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
   __shared__ __attribute__((aligned(16))) bf16 sdO[2][lds_tile_elems<HD>(BQ)];
   __shared__ __attribute__((aligned(16))) float sL[2][BQ];
   __shared__ __attribute__((aligned(16))) float sD[2][BQ];
+  __shared__ __attribute__((aligned(16))) float sC[FOX ? 2 : 1][FOX ? BQ : 4];  // cs of the tile's queries
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -93,7 +97,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
   }
 
   bf16x8 rq[CPT], ro[CPT];
-  float rl = 0.0f, rd = 0.0f;
+  float rl = 0.0f, rd = 0.0f, rc = 0.0f;
+  const float csk = FOX && mykey < T ? to_f32(CS[bh * T + mykey]) * sqd : 0.0f;
+  float colacc = 0.0f;  // FOX: sum over queries of this lane's key's dS
   auto gload = [&](int q0) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -109,6 +115,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
       // a query past the end gets an infinite LSE, so its P and dS are 0 in every body
       rl = q0 + tid < T ? lv * LOG2E : INFINITY;
       rd = Dd[bh * T + q];
+      if constexpr (FOX) rc = to_f32(CS[bh * T + q]);
     }
   };
   auto sstore = [&](int buf) {
@@ -121,6 +128,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
     if (tid < BQ) {
       sL[buf][tid] = rl;
       sD[buf][tid] = rd;
+      if constexpr (FOX) sC[buf][tid] = rc;
     }
   };
 
@@ -157,9 +165,12 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
       for (int rb = 0; rb < 4; ++rb) {
         const f32x4 lv = *(const f32x4*)(&sL[buf][32 * sub + 8 * rb + 4 * g]);
         const f32x4 dv4 = *(const f32x4*)(&sD[buf][32 * sub + 8 * rb + 4 * g]);
+        f32x4 cq4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (FOX) cq4 = *(const f32x4*)(&sC[buf][32 * sub + 8 * rb + 4 * g]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = rb * 4 + e;
+          if constexpr (FOX) s[r] += fmaf(cq4[e], sqd, -csk);
           float p = fast_exp2(fmaf(s[r], scale_log2, -lv[e]));
           if constexpr (MASK) {
             const int q = qs + 8 * rb + 4 * g + e;
@@ -167,6 +178,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
           }
           s[r] = p;
           dp[r] = p * (dp[r] - dv4[e]);  // dS / scale: 1/sqrt(d) is applied to dK once at the end
+          if constexpr (FOX) colacc += dp[r];
         }
       }
       // B fragments: queries 16 kc + 4 g + {0..3} and 16 kc + 8 + 4 g + {0..3}
@@ -203,6 +215,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
     }
     __syncthreads();
   }
+  if constexpr (FOX) {
+    colacc += __shfl_xor(colacc, 32);  // the two lane halves hold the key's other queries
+    if (g == 0 && mykey < T) DCSK[bh * T + mykey] = -colacc;
+  }
   // lane li owns key mykey; register r of tile dt holds dim dt * 32 + d_row(r, g)
   if (mykey < T) {
     bf16* krow = dK + base + (long)mykey * HD;
@@ -228,12 +244,15 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dkdv_kernel(const bf16* __restr
 // S^T = K Q^T and dP^T = V dO^T, so a lane owns one query column) and walks 64-key tiles
 // of K and V in a double-buffered LDS ring.  dQ^T += K^T dS^T takes dS^T from the
 // accumulator registers and K^T from the row-major K tile with transposed reads.
-template <int HD, bool CAUSAL>
+// FOX: as the dK/dV kernel; writes d cs = sum_k dS_qk plus the key side DCSK to DCS.
+template <int HD, bool CAUSAL, bool FOX = false>
 __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                            const bf16* __restrict__ V, const bf16* __restrict__ dO,
                                                            const float* __restrict__ LSE, const float* __restrict__ Dd,
                                                            bf16* __restrict__ dQ, int T, float scale_log2,
-                                                           float scale) {
+                                                           float scale, const bf16* __restrict__ CS,
+                                                           const float* __restrict__ DCSK, bf16* __restrict__ DCS,
+                                                           float sqd) {
   constexpr int BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   constexpr int CPR = HD / 8;
@@ -261,6 +280,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
   }
   const float myl = myq < T ? LSE[bh * T + myq] * LOG2E : 0.0f;
   const float myd = myq < T ? Dd[bh * T + myq] : 0.0f;
+  __shared__ __attribute__((aligned(16))) float sCS[FOX ? 2 : 1][FOX ? BN : 4];  // cs of the tile's keys
+  const float csq = FOX && myq < T ? to_f32(CS[bh * T + myq]) * sqd : 0.0f;
+  float rowacc = 0.0f, rcs = 0.0f;  // FOX: sum over keys of this lane's query's dS
   f32x16 dqt[NDT];  // dQ^T: rows = dims, column = this lane's query
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) dqt[dt] = zero16();
@@ -275,6 +297,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
       rk[i] = *(const bf16x8*)(K + base + key * HD + col);
       rv[i] = *(const bf16x8*)(V + base + key * HD + col);
     }
+    if constexpr (FOX) {
+      if (tid < BN) rcs = to_f32(CS[bh * T + min(k0 + tid, T - 1)]);
+    }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
@@ -282,6 +307,9 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
       const int c = tid + 256 * i, row = c / CPR, col = (c % CPR) * 8;
       *(bf16x8*)(&sK[buf][lds_off<HD>(row, col)]) = rk[i];
       *(bf16x8*)(&sV[buf][lds_off<HD>(row, col)]) = rv[i];
+    }
+    if constexpr (FOX) {
+      if (tid < BN) sCS[buf][tid] = rcs;
     }
   };
 
@@ -311,6 +339,16 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
           dp[h2] = mfma32(av, of[kk], dp[h2]);
         }
       }
+      if constexpr (FOX) {  // + (cs_q - cs_key) sqrt(d); key h2 * 32 + 8 rb + 4 g + e
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int rb = 0; rb < 4; ++rb) {
+            const f32x4 ck = *(const f32x4*)(&sCS[buf][h2 * 32 + 8 * rb + 4 * g]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[h2][4 * rb + e] += fmaf(-ck[e], sqd, csq);
+          }
+      }
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
@@ -321,6 +359,7 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
             p = (key >= T || myq >= T || (CAUSAL && key > myq)) ? 0.0f : p;
           }
           s[h2][r] = p * (dp[h2][r] - myd);  // dS^T / scale: 1/sqrt(d) is applied to dQ at the end
+          if constexpr (FOX) rowacc += s[h2][r];
         }
       bf16x8 db[4];
 #pragma unroll
@@ -359,6 +398,10 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
     if (!(CAUSAL && kt * BN > qw + 31)) tile(kt, std::true_type{});  // some key visible to the wave
     advance(kt);
   }
+  if constexpr (FOX) {
+    rowacc += __shfl_xor(rowacc, 32);  // the two lane halves hold the query's other keys
+    if (g == 0 && myq < T) DCS[bh * T + myq] = (bf16)(rowacc + DCSK[bh * T + myq]);
+  }
   if (myq < T) {
     bf16* qrow = dQ + base + (long)myq * HD;
 #pragma unroll
@@ -380,7 +423,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_wave_kernel(const TT* __restric
                                                              const float* __restrict__ LSE,
                                                              const float* __restrict__ Dd, TT* __restrict__ dQ, int BH,
                                                              int T, int HD, float scale_log2, float scale,
-                                                             int causal) {
+                                                             int causal, const TT* __restrict__ CS,
+                                                             const float* __restrict__ DCSK, TT* __restrict__ DCS,
+                                                             float sqd) {
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= (long)BH * T) return;
@@ -395,6 +440,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_wave_kernel(const TT* __restric
     acc[e] = 0.0f;
   }
   const float lse2 = LSE[row] * LOG2E, Di = Dd[row];
+  const float csi = CS != nullptr ? ld(CS, row) * sqd : 0.0f;
+  float rowacc = 0.0f;  // FoX: sum over keys of dS
   const int jend = causal ? i + 1 : T;
   for (int j = 0; j < jend; ++j) {
     const long kb = (bh * T + j) * HD;
@@ -412,13 +459,17 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_wave_kernel(const TT* __restric
       s += __shfl_xor(s, off);
       dp += __shfl_xor(dp, off);
     }
-    const float ds = fast_exp2(s * scale_log2 - lse2) * (dp - Di) * scale;
+    if (CS != nullptr) s += fmaf(-ld(CS, bh * T + j), sqd, csi);  // FoX bias (cs_i - cs_j) sqrt(d)
+    const float g = fast_exp2(s * scale_log2 - lse2) * (dp - Di);
+    rowacc += g;
+    const float ds = g * scale;
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
       const int d = lane + 64 * e;
       if (d < HD) acc[e] = fmaf(ds, ld(K, kb + d), acc[e]);
     }
   }
+  if (CS != nullptr && lane == 0) st(DCS, row, rowacc + DCSK[row]);
 #pragma unroll
   for (int e = 0; e < DPL; ++e) {
     const int d = lane + 64 * e;
@@ -432,7 +483,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_wave_kernel(const TT* __restr
                                                                const float* __restrict__ LSE,
                                                                const float* __restrict__ Dd, TT* __restrict__ dK,
                                                                TT* __restrict__ dV, int BH, int T, int HD,
-                                                               float scale_log2, float scale, int causal) {
+                                                               float scale_log2, float scale, int causal,
+                                                               const TT* __restrict__ CS, float* __restrict__ DCSK,
+                                                               float sqd) {
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= (long)BH * T) return;
@@ -446,6 +499,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_wave_kernel(const TT* __restr
     vv[e] = d < HD ? ld(V, row * HD + d) : 0.0f;
     ak[e] = av[e] = 0.0f;
   }
+  const float csj = CS != nullptr ? ld(CS, row) * sqd : 0.0f;
+  float colacc = 0.0f;  // FoX: sum over queries of dS
   for (int i = causal ? j : 0; i < T; ++i) {
     const long qb = (bh * T + i) * HD;
     float s = 0.0f, dp = 0.0f;
@@ -462,8 +517,11 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_wave_kernel(const TT* __restr
       s += __shfl_xor(s, off);
       dp += __shfl_xor(dp, off);
     }
+    if (CS != nullptr) s += fmaf(ld(CS, bh * T + i), sqd, -csj);  // FoX bias (cs_i - cs_j) sqrt(d)
     const float p = fast_exp2(s * scale_log2 - LSE[bh * T + i] * LOG2E);
-    const float ds = p * (dp - Dd[bh * T + i]) * scale;
+    const float gq = p * (dp - Dd[bh * T + i]);
+    colacc += gq;
+    const float ds = gq * scale;
 #pragma unroll
     for (int e = 0; e < DPL; ++e) {
       const int d = lane + 64 * e;
@@ -481,39 +539,49 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_wave_kernel(const TT* __restr
       st(dV, row * HD + d, av[e]);
     }
   }
+  if (CS != nullptr && lane == 0) DCSK[row] = -colacc;
 }
 
 template <int HD>
 void launch_mfma_bwd(hipStream_t s, const void* q, const void* k, const void* v, const void* go, const float* lse,
                      const float* Dd, void* dq, void* dk, void* dv, int BH, int T, int causal, float scale_log2,
-                     float scale) {
+                     float scale, const void* cs = nullptr, float* dcsk = nullptr, void* dcs = nullptr,
+                     float sqd = 0.0f) {
   const dim3 g1((T + 127) / 128, BH);
-  if (causal) {
-    fa_bwd_dkdv_kernel<HD, true><<<g1, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)go,
-                                                    lse, Dd, (bf16*)dk, (bf16*)dv, T, scale_log2, scale);
-    fa_bwd_dq_kernel<HD, true><<<g1, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)go,
-                                                  lse, Dd, (bf16*)dq, T, scale_log2, scale);
+  const bf16 *Q = (const bf16*)q, *K = (const bf16*)k, *V = (const bf16*)v, *G = (const bf16*)go;
+  const bf16* CS = (const bf16*)cs;
+  if (cs != nullptr) {  // FoX attention is causal; dK/dV first: dQ adds its key-side d cs
+    fa_bwd_dkdv_kernel<HD, true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dk, (bf16*)dv, T, scale_log2,
+                                                          scale, CS, dcsk, sqd);
+    fa_bwd_dq_kernel<HD, true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dq, T, scale_log2, scale, CS, dcsk,
+                                                        (bf16*)dcs, sqd);
+  } else if (causal) {
+    fa_bwd_dkdv_kernel<HD, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dk, (bf16*)dv, T, scale_log2, scale,
+                                                    nullptr, nullptr, 0.0f);
+    fa_bwd_dq_kernel<HD, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dq, T, scale_log2, scale, nullptr,
+                                                  nullptr, nullptr, 0.0f);
   } else {
-    fa_bwd_dkdv_kernel<HD, false><<<g1, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v,
-                                                     (const bf16*)go, lse, Dd, (bf16*)dk, (bf16*)dv, T, scale_log2,
-                                                     scale);
-    fa_bwd_dq_kernel<HD, false><<<g1, 256, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)go,
-                                                   lse, Dd, (bf16*)dq, T, scale_log2, scale);
+    fa_bwd_dkdv_kernel<HD, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dk, (bf16*)dv, T, scale_log2, scale,
+                                                     nullptr, nullptr, 0.0f);
+    fa_bwd_dq_kernel<HD, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dq, T, scale_log2, scale, nullptr,
+                                                   nullptr, nullptr, 0.0f);
   }
 }
 
 template <typename TT>
 void launch_wave_bwd(hipStream_t s, const void* q, const void* k, const void* v, const void* go, const float* lse,
                      const float* Dd, void* dq, void* dk, void* dv, int BH, int T, int HD, int causal,
-                     float scale_log2, float scale) {
+                     float scale_log2, float scale, const void* cs = nullptr, float* dcsk = nullptr,
+                     void* dcs = nullptr, float sqd = 0.0f) {
   const long rows = (long)BH * T;
   const unsigned grid = (unsigned)((rows + 3) / 4);
-#define EDF_FA_WAVE_BWD(DPL)                                                                                      \
-  fa_bwd_dq_wave_kernel<TT, DPL><<<grid, 256, 0, s>>>((const TT*)q, (const TT*)k, (const TT*)v, (const TT*)go, lse, \
-                                                      Dd, (TT*)dq, BH, T, HD, scale_log2, scale, causal);          \
-  fa_bwd_dkdv_wave_kernel<TT, DPL><<<grid, 256, 0, s>>>((const TT*)q, (const TT*)k, (const TT*)v, (const TT*)go,    \
-                                                        lse, Dd, (TT*)dk, (TT*)dv, BH, T, HD, scale_log2, scale,   \
-                                                        causal)
+  const TT *Q = (const TT*)q, *K = (const TT*)k, *V = (const TT*)v, *G = (const TT*)go, *CS = (const TT*)cs;
+  // dK/dV first: with FoX the dQ kernel adds the key side of d cs that it writes
+#define EDF_FA_WAVE_BWD(DPL)                                                                                        \
+  fa_bwd_dkdv_wave_kernel<TT, DPL><<<grid, 256, 0, s>>>(Q, K, V, G, lse, Dd, (TT*)dk, (TT*)dv, BH, T, HD, scale_log2, \
+                                                        scale, causal, CS, dcsk, sqd);                               \
+  fa_bwd_dq_wave_kernel<TT, DPL><<<grid, 256, 0, s>>>(Q, K, V, G, lse, Dd, (TT*)dq, BH, T, HD, scale_log2, scale,     \
+                                                      causal, CS, dcsk, (TT*)dcs, sqd)
   if (HD <= 64) {
     EDF_FA_WAVE_BWD(1);
   } else if (HD <= 128) {
@@ -578,6 +646,61 @@ int edf_fused_flash_attention_backward(void* stream, const void* q, const void* 
                            scale_log2, scale);
   }
   return check_launch("flash attention backward");
+}
+
+size_t edf_fox_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim) {
+  if (batch <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return 0;
+  const size_t rows = (size_t)batch * num_heads * seq_len;
+  return ((rows * sizeof(float) + 255) & ~(size_t)255) + rows * sizeof(float);  // D, then the key side of d cs
+}
+
+int edf_fused_fox_attention_backward(void* stream, const void* q, const void* k, const void* v, const void* cs,
+                                     const void* out, const void* grad_out, const float* lse, void* grad_q,
+                                     void* grad_k, void* grad_v, void* grad_cs, void* workspace,
+                                     size_t workspace_bytes, int batch, int num_heads, int seq_len, int head_dim,
+                                     int dtype) {
+  using namespace edf;
+  EDF_REQUIRE(batch > 0 && num_heads > 0 && seq_len > 0 && head_dim > 0, EDF_ERR_INVALID_ARG,
+              "dimensions must be positive");
+  EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
+  EDF_REQUIRE(head_dim <= 256, EDF_ERR_UNSUPPORTED, "head_dim %d > 256 unsupported", head_dim);
+  EDF_REQUIRE(q && k && v && cs && out && grad_out && lse && grad_q && grad_k && grad_v && grad_cs,
+              EDF_ERR_INVALID_ARG, "null tensor pointer (the forward's lse is required)");
+  const size_t need = edf_fox_attention_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(workspace && workspace_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  hipStream_t s = as_stream(stream);
+  const int BH = batch * num_heads;
+  const long rows = (long)BH * seq_len;
+  float* Dd = (float*)workspace;
+  float* dcsk = (float*)((char*)workspace + ((rows * sizeof(float) + 255) & ~(size_t)255));
+  const unsigned gd = (unsigned)((rows + 15) / 16);
+  if (dtype == EDF_BF16)
+    fa_bwd_dot_kernel<bf16><<<gd, 256, 0, s>>>((const bf16*)out, (const bf16*)grad_out, Dd, rows, head_dim);
+  else
+    fa_bwd_dot_kernel<float><<<gd, 256, 0, s>>>((const float*)out, (const float*)grad_out, Dd, rows, head_dim);
+  int rc = check_launch("fox attention backward rowsum");
+  if (rc) return rc;
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  const float scale_log2 = scale * LOG2E;
+  const float sqd = sqrtf((float)head_dim);
+  if (dtype == EDF_BF16 && (head_dim == 32 || head_dim == 64 || head_dim == 128)) {
+    if (head_dim == 128)
+      launch_mfma_bwd<128>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, 1, scale_log2, scale,
+                           cs, dcsk, grad_cs, sqd);
+    else if (head_dim == 64)
+      launch_mfma_bwd<64>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, 1, scale_log2, scale,
+                          cs, dcsk, grad_cs, sqd);
+    else
+      launch_mfma_bwd<32>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, 1, scale_log2, scale,
+                          cs, dcsk, grad_cs, sqd);
+  } else if (dtype == EDF_BF16) {
+    launch_wave_bwd<bf16>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, head_dim, 1,
+                          scale_log2, scale, cs, dcsk, grad_cs, sqd);
+  } else {
+    launch_wave_bwd<float>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, head_dim, 1,
+                           scale_log2, scale, cs, dcsk, grad_cs, sqd);
+  }
+  return check_launch("fox attention backward");
 }
 
 }  // extern "C"

@@ -309,6 +309,42 @@ class _FlashAttention(torch.autograd.Function):
         return dq, dk, dv, None
 
 
+class _FoxAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cs):
+        q, k, v, cs = q.contiguous(), k.contiguous(), v.contiguous(), cs.contiguous()
+        _dev(q, k, v, cs)
+        _same(q, k, v, cs)
+        bsz, nh, seq, hd = q.shape
+        if k.shape != q.shape or v.shape != q.shape or tuple(cs.shape) != (bsz, nh, seq):
+            raise EdificeHipError("fox_attention needs q, k, v [B, H, T, d] and cs [B, H, T]")
+        out = torch.empty_like(q)
+        lse = torch.empty((bsz, nh, seq), dtype=torch.float32, device=q.device)
+        nat.call("edf_fused_fox_attention", _stream(), _p(q), _p(k), _p(v), _p(cs), _p(out), _p(lse), bsz, nh, seq,
+                 hd, dtype_flag(q))
+        ctx.save_for_backward(q, k, v, cs, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, cs, out, lse = ctx.saved_tensors
+        dout = dout.contiguous().to(q.dtype)
+        bsz, nh, seq, hd = q.shape
+        dq, dk, dv, dcs = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(cs)
+        wsb = nat.query("edf_fox_attention_backward_workspace_bytes", bsz, nh, seq, hd)
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_fox_attention_backward", _stream(), _p(q), _p(k), _p(v), _p(cs), _p(out), _p(dout),
+                 _p(lse), _p(dq), _p(dk), _p(dv), _p(dcs), _p(ws), wsb, bsz, nh, seq, hd, dtype_flag(q))
+        return dq, dk, dv, dcs
+
+
+def fox_attention(q, k, v, cs):
+    """``FusedScan.fox_attention/4`` (fused_scan.ex:3796-3810): causal attention with the
+    forget bias cs_i - cs_j added to the scaled scores (fused_scan.ex:3860-3905); q, k, v
+    [B, H, T, d], cs [B, H, T] (cumulative log forget gates).  Differentiable in all four."""
+    return _FoxAttention.apply(q, k, v, cs)
+
+
 def flash_attention(q, k, v, causal: bool = False):
     """``FusedScan.flash_attention/4`` (fused_scan.ex:3398-3414): q, k, v [B, H, T, d].
 

@@ -221,6 +221,24 @@ int edf_fused_flash_attention_backward(void* stream, const void* q, const void* 
                                        int num_heads, int seq_len, int head_dim, int causal, int dtype);
 size_t edf_flash_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim);
 
+/* FoX (forgetting) attention, always causal: scores QK^T/sqrt(d) + (cs_i - cs_j) with
+ * cs [B, H, T] the cumulative log forget gate.  Replaces fused_fox_attention/9 (q, k, v,
+ * cs, batch, heads, seq, head_dim, dtype), lib/edifice/cuda/nif.ex:106 ->
+ * native/cuda/fused_fox_attention.cu (semantics fused_scan.ex:3860-3905); lse (may be NULL)
+ * is the forward's per-row log-sum-exp, required by the backward. */
+int edf_fused_fox_attention(void* stream, const void* q, const void* k, const void* v, const void* cs, void* out,
+                            float* lse, int batch, int num_heads, int seq_len, int head_dim, int dtype);
+
+/* Replaces fused_fox_attention_backward/11 (q, k, v, cs, o, grad_o, ...), nif.ex:227 ->
+ * native/cuda/fused_fox_attention_backward.cu: dq, dk, dv and d cs = sum_j dS_ij -
+ * sum_j dS_ji; workspace edf_fox_attention_backward_workspace_bytes() bytes. */
+int edf_fused_fox_attention_backward(void* stream, const void* q, const void* k, const void* v, const void* cs,
+                                     const void* out, const void* grad_out, const float* lse, void* grad_q,
+                                     void* grad_k, void* grad_v, void* grad_cs, void* workspace,
+                                     size_t workspace_bytes, int batch, int num_heads, int seq_len, int head_dim,
+                                     int dtype);
+size_t edf_fox_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim);
+
 /* ------------------------------------------------------------------------
  * Delta rule (DeltaNet / GatedDeltaNet)
  *   q, k, v, out, grads: [B, T, H, d] in dtype (k L2-normalised by the caller, no

@@ -32,6 +32,9 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 gradient), β≡0 ⇒ o≡0, α≡1 ⇒ DeltaNet, T=1 closed form.
   delta_rule_backward           delta_net_random.safetensors gradient.input, torch
                                 autograd of the forward, finite differences.
+  fox_attention / _backward     cs = const ==> causal flash_attention; torch autograd of an
+                                independent torch forward; d cs sums to zero; shift
+                                invariance in cs.
   flash_attention / _backward   torch.nn.functional.scaled_dot_product_attention and
                                 its autograd, gqa_random.safetensors block fixture,
                                 causal row 0 == V[0], identical keys ⇒ mean of V.
@@ -567,3 +570,47 @@ def flash_attention_backward(q, k, v, do, causal=False):
     dq = np.einsum("bhij,bhjd->bhid", ds, k)
     dk = np.einsum("bhij,bhid->bhjd", ds, q)
     return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# FoX (forgetting) attention
+# ---------------------------------------------------------------------------
+
+def _fox_scores(q, k, cs):
+    """Q K^T / sqrt(d) + (cs_i - cs_j), causal (fused_scan.ex:3860-3900; the diagonal
+    bias the reference zeroes explicitly is cs_i - cs_i = 0)."""
+    s = _scores(q, k, True)
+    return s + (cs[..., :, None] - cs[..., None, :])
+
+
+def fox_attention(q, k, v, cs, return_lse=False):
+    """softmax(Q K^T / sqrt(d) + cs_i - cs_j, causal) V (``fox_attention_fallback``,
+    fused_scan.ex:3860-3907; kernel native/cuda/fused_fox_attention.cu:1-14)."""
+    q, k, v, cs = _f64(q, k, v, cs)
+    s = _fox_scores(q, k, cs)
+    m = s.max(axis=-1, keepdims=True)
+    w = np.exp(s - m)
+    l = w.sum(axis=-1, keepdims=True)
+    o = np.einsum("bhij,bhjd->bhid", w / l, v)
+    if return_lse:
+        return o, (m + np.log(l))[..., 0]
+    return o
+
+
+def fox_attention_backward(q, k, v, cs, do):
+    """-> (dq, dk, dv, dcs) following ``fox_attention_backward_fallback``
+    (fused_scan.ex:3926-3984): the attention backward with the bias, and
+    dcs_i = sum_j dS_ij - sum_j dS_ji (dS the gradient of the biased scores)."""
+    q, k, v, cs, do = _f64(q, k, v, cs, do)
+    d = q.shape[-1]
+    s = _fox_scores(q, k, cs)
+    w = np.exp(s - s.max(axis=-1, keepdims=True))
+    w = w / w.sum(axis=-1, keepdims=True)
+    dv = np.einsum("bhij,bhid->bhjd", w, do)
+    dw = np.einsum("bhid,bhjd->bhij", do, v)
+    g = w * (dw - (dw * w).sum(axis=-1, keepdims=True))
+    dq = np.einsum("bhij,bhjd->bhid", g, k) / np.sqrt(d)
+    dk = np.einsum("bhij,bhid->bhjd", g, q) / np.sqrt(d)
+    dcs = g.sum(axis=-1) - g.sum(axis=-2)
+    return dq, dk, dv, dcs
+

@@ -83,3 +83,50 @@ def test_flash_attention_config4_head_slice(rng):
     assert_close(host(tq.grad), dq, tol, "dQ")
     assert_close(host(tk.grad), dk, tol, "dK")
     assert_close(host(tv.grad), dv, tol, "dV")
+
+
+FOX_CASES = [
+    # (B, H, T, d, dtype): the MFMA path (bf16, d = 32/64/128) and the wave-per-row path
+    (2, 2, 64, 32, torch.bfloat16),
+    (1, 2, 200, 64, torch.bfloat16),
+    (2, 1, 256, 128, torch.bfloat16),
+    (1, 2, 130, 128, torch.bfloat16),
+    (1, 1, 1, 128, torch.bfloat16),
+    (1, 3, 33, 24, torch.bfloat16),
+    (2, 2, 40, 16, torch.float32),
+    (1, 1, 96, 128, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", FOX_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_fox_attention_fwd_bwd(case, rng):
+    """FusedScan.fox_attention/4 and its backward (dq, dk, dv, d cs) against the oracle."""
+    from edifice_amd import fused_scan as fs
+    B, H, T, d, dtype = case
+    announce("fox_attention", case=case)
+    std = d ** -0.25
+    q, k, v, do = (rng.normal(scale=std, size=(B, H, T, d)) for _ in range(4))
+    # cumulative log forget gates, as FoX builds them (sigmoid of logits around +2)
+    cs = np.cumsum(-np.log1p(np.exp(-(rng.normal(size=(B, H, T)) + 2.0))), axis=-1)
+    tq, tk, tv, tc = (to_dev(a, dtype).requires_grad_() for a in (q, k, v, cs))
+    out = fs.fox_attention(tq, tk, tv, tc)
+    out.backward(to_dev(do, dtype))
+    qr, kr, vr, cr, dor = (rounded(a, dtype) for a in (q, k, v, cs, do))
+    tol = TOL[dtype]
+    assert_close(host(out), scans.fox_attention(qr, kr, vr, cr), tol, "O")
+    dq, dk, dv, dcs = scans.fox_attention_backward(qr, kr, vr, cr, dor)
+    assert_close(host(tq.grad), dq, tol, "dQ")
+    assert_close(host(tk.grad), dk, tol, "dK")
+    assert_close(host(tv.grad), dv, tol, "dV")
+    assert_close(host(tc.grad), dcs, tol, "dcs")
+
+
+def test_fox_with_constant_cs_is_causal_flash(rng):
+    """cs constant: the bias vanishes and FoX equals causal flash attention exactly (same
+    kernels, bias 0)."""
+    from edifice_amd import fused_scan as fs
+    announce("fox_constant_cs")
+    B, H, T, d = 1, 2, 192, 128
+    q, k, v = (to_dev(rng.normal(scale=d ** -0.25, size=(B, H, T, d)), torch.bfloat16) for _ in range(3))
+    cs = torch.zeros(B, H, T, dtype=torch.bfloat16, device="cuda")
+    assert torch.equal(fs.fox_attention(q, k, v, cs), fs.flash_attention(q, k, v, causal=True))

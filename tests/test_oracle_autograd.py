@@ -231,3 +231,22 @@ def test_selective_scan_backward_finite_difference(rng):
             arr[idx] = old
             num[idx] = (fp - fm) / (2 * eps)
         assert_close(g[name], num, 1e-6, name)
+
+
+def test_fox_attention_vs_torch_autograd(rng):
+    """FoX forward and backward against torch autograd of an independent torch forward
+    (scores + cs_i - cs_j, causal softmax)."""
+    b, h, t, d = 1, 2, 9, 4
+    q, k, v, do = (rng.normal(size=(b, h, t, d)) for _ in range(4))
+    cs = np.cumsum(np.log(1 / (1 + np.exp(-rng.normal(size=(b, h, t))))), axis=-1)
+    tq, tk, tv, tc = _t(q), _t(k), _t(v), _t(cs)
+    sc = tq @ tk.transpose(-1, -2) / np.sqrt(d) + tc[..., :, None] - tc[..., None, :]
+    mask = torch.ones(t, t, dtype=torch.bool).tril()
+    sc = sc.masked_fill(~mask, float("-inf"))
+    out = torch.softmax(sc, -1) @ tv
+    out.backward(torch.from_numpy(do))
+    assert_close(scans.fox_attention(q, k, v, cs), out.detach().numpy(), 1e-12, "o")
+    dq, dk, dv, dcs = scans.fox_attention_backward(q, k, v, cs, do)
+    for a, e, n in ((dq, tq.grad, "dq"), (dk, tk.grad, "dk"), (dv, tv.grad, "dv"), (dcs, tc.grad, "dcs")):
+        assert_close(a, e.numpy(), 1e-10, n)
+

@@ -316,3 +316,17 @@ def test_flash_attention_matches_sdpa_and_invariants(rng):
     _, lse = scans.flash_attention(q, k, v, True, return_lse=True)
     s = np.einsum("bhid,bhjd->bhij", q, k) / np.sqrt(d)
     np.testing.assert_allclose(lse[:, :, 0], s[:, :, 0, 0])
+
+
+def test_fox_attention_invariants(rng):
+    """cs constant ==> causal attention; a shift of cs changes nothing; d cs sums to zero
+    over the sequence (every score's gradient enters once with + and once with -)."""
+    b, h, t, d = 1, 2, 7, 4
+    q, k, v, do = (rng.normal(size=(b, h, t, d)) for _ in range(4))
+    cs = np.cumsum(-np.abs(rng.normal(size=(b, h, t))), axis=-1)
+    np.testing.assert_allclose(scans.fox_attention(q, k, v, np.full((b, h, t), 3.0)),
+                               scans.flash_attention(q, k, v, causal=True), rtol=1e-12)
+    np.testing.assert_allclose(scans.fox_attention(q, k, v, cs + 5.0), scans.fox_attention(q, k, v, cs), rtol=1e-12)
+    dcs = scans.fox_attention_backward(q, k, v, cs, do)[3]
+    np.testing.assert_allclose(dcs.sum(-1), 0.0, atol=1e-12)
+
