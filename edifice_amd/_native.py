@@ -46,6 +46,10 @@ SIGNATURES = {
     "edf_fused_fox_attention": (I, [P, P, P, P, P, P, P, I, I, I, I, I]),
     "edf_fused_fox_attention_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_fox_attention_backward_workspace_bytes": (S, [I, I, I, I]),
+    "edf_laser_attention_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_laser_attention": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
+    "edf_laser_attention_backward_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_laser_attention_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_delta_rule_workspace_bytes": (S, [I, I, I, I, I, I]),
     "edf_delta_rule_backward_workspace_bytes": (S, [I, I, I, I, I, I]),
     "edf_fused_delta_net_scan": (I, [P, P, P, P, P, P, P, S, I, I, I, I, I, I]),

@@ -345,6 +345,48 @@ def fox_attention(q, k, v, cs):
     return _FoxAttention.apply(q, k, v, cs)
 
 
+class _LaserAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, vmax, causal):
+        q, k, v, vmax = q.contiguous(), k.contiguous(), v.contiguous(), vmax.contiguous()
+        _dev(q, k, v, vmax)
+        _same(q, k, v, vmax)
+        bsz, nh, seq, hd = q.shape
+        if k.shape != q.shape or v.shape != q.shape or tuple(vmax.shape) != (bsz, nh, 1, hd):
+            raise EdificeHipError("laser_attention needs q, k, v [B, H, T, d] and vmax [B, H, 1, d]")
+        out = torch.empty_like(q)
+        lse = torch.empty((bsz, nh, seq), dtype=torch.float32, device=q.device)
+        flag = dtype_flag(q)
+        wsb = nat.query("edf_laser_attention_workspace_bytes", bsz, nh, seq, hd, flag)
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_laser_attention", _stream(), _p(q), _p(k), _p(v), _p(vmax), _p(out), _p(lse), _p(ws), wsb,
+                 bsz, nh, seq, hd, int(causal), flag)
+        ctx.causal = int(causal)
+        ctx.save_for_backward(q, k, v, vmax, out, lse)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, vmax, out, lse = ctx.saved_tensors
+        dout = dout.contiguous().to(q.dtype)
+        bsz, nh, seq, hd = q.shape
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        flag = dtype_flag(q)
+        wsb = nat.query("edf_laser_attention_backward_workspace_bytes", bsz, nh, seq, hd, flag)
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_laser_attention_backward", _stream(), _p(q), _p(k), _p(v), _p(vmax), _p(out), _p(dout),
+                 _p(lse), _p(dq), _p(dk), _p(dv), _p(ws), wsb, bsz, nh, seq, hd, ctx.causal, flag)
+        return dq, dk, dv, None, None
+
+
+def laser_attention(q, k, v, causal: bool = True):
+    """``FusedScan.laser_attention/4`` (fused_scan.ex:3593-3613): log(softmax(Q K^T / sqrt(d))
+    exp(V - vmax)) + vmax with vmax = max over the sequence of V (computed here, as the
+    reference wrapper does, and held constant in the backward)."""
+    vmax = v.detach().amax(dim=2, keepdim=True)
+    return _LaserAttention.apply(q, k, v, vmax, causal)
+
+
 def flash_attention(q, k, v, causal: bool = False):
     """``FusedScan.flash_attention/4`` (fused_scan.ex:3398-3414): q, k, v [B, H, T, d].
 

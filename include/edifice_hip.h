@@ -239,6 +239,24 @@ int edf_fused_fox_attention_backward(void* stream, const void* q, const void* k,
                                      int dtype);
 size_t edf_fox_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim);
 
+/* LASER attention: O = log(max(softmax(Q K^T / sqrt(d)) exp(V - vmax), 1e-7)) + vmax, vmax
+ * [B, H, 1, d] the per-column max of V.  Replaces fused_laser_attention/10 (q, k, v, v_max,
+ * batch, heads, seq, head_dim, causal, dtype), lib/edifice/cuda/nif.ex:102 ->
+ * native/cuda/fused_laser_attention.cu (semantics fused_scan.ex:3667-3704); lse (may be
+ * NULL) is needed by the backward; workspace edf_laser_attention_workspace_bytes(). */
+size_t edf_laser_attention_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim, int dtype);
+int edf_fused_laser_attention(void* stream, const void* q, const void* k, const void* v, const void* v_max,
+                              void* out, float* lse, void* workspace, size_t workspace_bytes, int batch,
+                              int num_heads, int seq_len, int head_dim, int causal, int dtype);
+
+/* Replaces fused_laser_attention_backward/12 (q, k, v, vmax, o, grad_o, ...), nif.ex:223:
+ * dq, dk, dv (vmax held constant, as fused_scan.ex:3720-3771). */
+size_t edf_laser_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim, int dtype);
+int edf_fused_laser_attention_backward(void* stream, const void* q, const void* k, const void* v, const void* v_max,
+                                       const void* out, const void* grad_out, const float* lse, void* grad_q,
+                                       void* grad_k, void* grad_v, void* workspace, size_t workspace_bytes,
+                                       int batch, int num_heads, int seq_len, int head_dim, int causal, int dtype);
+
 /* ------------------------------------------------------------------------
  * Delta rule (DeltaNet / GatedDeltaNet)
  *   q, k, v, out, grads: [B, T, H, d] in dtype (k L2-normalised by the caller, no

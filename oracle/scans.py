@@ -32,6 +32,8 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 gradient), β≡0 ⇒ o≡0, α≡1 ⇒ DeltaNet, T=1 closed form.
   delta_rule_backward           delta_net_random.safetensors gradient.input, torch
                                 autograd of the forward, finite differences.
+  laser_attention / _backward   identical value rows ==> O = that row; torch autograd of an
+                                independent torch forward (vmax held constant).
   fox_attention / _backward     cs = const ==> causal flash_attention; torch autograd of an
                                 independent torch forward; d cs sums to zero; shift
                                 invariance in cs.
@@ -613,4 +615,44 @@ def fox_attention_backward(q, k, v, cs, do):
     dk = np.einsum("bhij,bhid->bhjd", g, q) / np.sqrt(d)
     dcs = g.sum(axis=-1) - g.sum(axis=-2)
     return dq, dk, dv, dcs
+
+
+# ---------------------------------------------------------------------------
+# LASER attention
+# ---------------------------------------------------------------------------
+
+LASER_CLAMP = 1.0e-7  # fused_scan.ex:3703
+
+
+def laser_attention(q, k, v, causal=True):
+    """log(max(softmax(Q K^T / sqrt(d)) exp(V - vmax), 1e-7)) + vmax, vmax the per-column
+    max of V over the sequence (``laser_attention`` / ``laser_attention_fallback``,
+    fused_scan.ex:3593-3600, 3667-3704)."""
+    q, k, v = _f64(q, k, v)
+    vmax = v.max(axis=2, keepdims=True)
+    s = _scores(q, k, causal)
+    w = np.exp(s - s.max(axis=-1, keepdims=True))
+    w = w / w.sum(axis=-1, keepdims=True)
+    return np.log(np.maximum(w @ np.exp(v - vmax), LASER_CLAMP)) + vmax
+
+
+def laser_attention_backward(q, k, v, do, causal=True):
+    """-> (dq, dk, dv) following ``laser_attention_backward_fallback`` (fused_scan.ex:3720-3771):
+    dR = dO exp(vmax - O), dV = (P^T dR) exp(V - vmax), dS from dR exp(V - vmax)^T; vmax is
+    held constant."""
+    q, k, v, do = _f64(q, k, v, do)
+    d = q.shape[-1]
+    vmax = v.max(axis=2, keepdims=True)
+    ev = np.exp(v - vmax)
+    s = _scores(q, k, causal)
+    w = np.exp(s - s.max(axis=-1, keepdims=True))
+    w = w / w.sum(axis=-1, keepdims=True)
+    o = np.log(np.maximum(w @ ev, LASER_CLAMP)) + vmax
+    dr = do * np.exp(vmax - o)
+    dv = np.einsum("bhij,bhid->bhjd", w, dr) * ev
+    dw = np.einsum("bhid,bhjd->bhij", dr, ev)
+    ds = w * (dw - (dw * w).sum(axis=-1, keepdims=True)) / np.sqrt(d)
+    dq = np.einsum("bhij,bhjd->bhid", ds, k)
+    dk = np.einsum("bhij,bhid->bhjd", ds, q)
+    return dq, dk, dv
 

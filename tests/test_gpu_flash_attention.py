@@ -130,3 +130,38 @@ def test_fox_with_constant_cs_is_causal_flash(rng):
     q, k, v = (to_dev(rng.normal(scale=d ** -0.25, size=(B, H, T, d)), torch.bfloat16) for _ in range(3))
     cs = torch.zeros(B, H, T, dtype=torch.bfloat16, device="cuda")
     assert torch.equal(fs.fox_attention(q, k, v, cs), fs.flash_attention(q, k, v, causal=True))
+
+
+LASER_CASES = [
+    # (B, H, T, d, dtype, causal)
+    (2, 2, 64, 32, torch.bfloat16, True),
+    (1, 2, 200, 128, torch.bfloat16, True),
+    (1, 2, 130, 64, torch.bfloat16, False),
+    (1, 3, 33, 24, torch.bfloat16, True),
+    (2, 2, 40, 16, torch.float32, True),
+    (1, 1, 96, 128, torch.float32, False),
+]
+
+
+@pytest.mark.parametrize("case", LASER_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_laser_attention_fwd_bwd(case, rng):
+    """FusedScan.laser_attention and its backward against the oracle."""
+    from edifice_amd import fused_scan as fs
+    B, H, T, d, dtype, causal = case
+    announce("laser_attention", case=case)
+    std = d ** -0.25
+    q, k, do = (rng.normal(scale=std, size=(B, H, T, d)) for _ in range(3))
+    # unit-scale values: with values of scale d^-1/4 and near-uniform attention every output
+    # is log(mean exp(v)) ~ 0.06, and the tolerance (relative to max |O|) would measure bf16
+    # rounding of a near-constant
+    v = rng.normal(size=(B, H, T, d))
+    tq, tk, tv = (to_dev(a, dtype).requires_grad_() for a in (q, k, v))
+    out = fs.laser_attention(tq, tk, tv, causal=causal)
+    out.backward(to_dev(do, dtype))
+    qr, kr, vr, dor = (rounded(a, dtype) for a in (q, k, v, do))
+    tol = TOL[dtype]
+    assert_close(host(out), scans.laser_attention(qr, kr, vr, causal), tol, "O")
+    dq, dk, dv = scans.laser_attention_backward(qr, kr, vr, dor, causal)
+    assert_close(host(tq.grad), dq, tol, "dQ")
+    assert_close(host(tk.grad), dk, tol, "dK")
+    assert_close(host(tv.grad), dv, tol, "dV")

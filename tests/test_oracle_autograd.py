@@ -250,3 +250,20 @@ def test_fox_attention_vs_torch_autograd(rng):
     for a, e, n in ((dq, tq.grad, "dq"), (dk, tk.grad, "dk"), (dv, tv.grad, "dv"), (dcs, tc.grad, "dcs")):
         assert_close(a, e.numpy(), 1e-10, n)
 
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_laser_attention_vs_torch_autograd(rng, causal):
+    b, h, t, d = 1, 2, 8, 4
+    q, k, v, do = (rng.normal(size=(b, h, t, d)) for _ in range(4))
+    tq, tk, tv = _t(q), _t(k), _t(v)
+    sc = tq @ tk.transpose(-1, -2) / np.sqrt(d)
+    if causal:
+        sc = sc.masked_fill(~torch.ones(t, t, dtype=torch.bool).tril(), float("-inf"))
+    vmax = tv.detach().amax(dim=2, keepdim=True)
+    out = torch.log(torch.softmax(sc, -1) @ torch.exp(tv - vmax)) + vmax
+    out.backward(torch.from_numpy(do))
+    assert_close(scans.laser_attention(q, k, v, causal), out.detach().numpy(), 1e-12, "o")
+    dq, dk, dv = scans.laser_attention_backward(q, k, v, do, causal)
+    for a, e, n in ((dq, tq.grad, "dq"), (dk, tk.grad, "dk"), (dv, tv.grad, "dv")):
+        assert_close(a, e.numpy(), 1e-10, n)
+

@@ -330,3 +330,12 @@ def test_fox_attention_invariants(rng):
     dcs = scans.fox_attention_backward(q, k, v, cs, do)[3]
     np.testing.assert_allclose(dcs.sum(-1), 0.0, atol=1e-12)
 
+
+def test_laser_attention_identical_rows(rng):
+    """All value rows equal c: exp(V - vmax) = 1 for every key, so O = c for any weights."""
+    b, h, t, d = 1, 1, 6, 3
+    q, k = rng.normal(size=(b, h, t, d)), rng.normal(size=(b, h, t, d))
+    row = rng.normal(size=d)
+    v = np.broadcast_to(row, (b, h, t, d)).copy()
+    np.testing.assert_allclose(scans.laser_attention(q, k, v, causal=True), v, rtol=1e-12, atol=1e-12)
+
