@@ -7,11 +7,11 @@
 namespace edf {
 size_t dr_seq_backward_workspace_bytes(int batch, int heads, int seq, int d);
 int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
-               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head);
+               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head, int alpha_per_row);
 int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
                         const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
                         void* dalpha, void* workspace, int batch, int seq, int heads, int d, int dtype,
-                        int beta_per_head);
+                        int beta_per_head, int alpha_per_row);
 bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head);
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d);
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
@@ -42,7 +42,7 @@ int fwd(void* stream, const void* q, const void* k, const void* v, const void* b
     if (workspace != nullptr && ws_bytes >= need)
       return dr_chunk_run(stream, q, k, v, beta, alpha, out, workspace, batch, seq, heads, d);
   }
-  return dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq, heads, d, dtype, per_head);
+  return dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq, heads, d, dtype, per_head, 0);
 }
 
 int bwd(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
@@ -62,7 +62,7 @@ int bwd(void* stream, const void* q, const void* k, const void* v, const void* b
   const size_t need = dr_seq_backward_workspace_bytes(batch, heads, seq, d);
   EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
   return dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
-                             seq, heads, d, dtype, beta_mode == EDF_BETA_PER_HEAD);
+                             seq, heads, d, dtype, beta_mode == EDF_BETA_PER_HEAD, 0);
 }
 }  // namespace
 }  // namespace edf
@@ -120,6 +120,38 @@ int edf_fused_gated_delta_net_scan_backward(void* stream, const void* q, const v
   EDF_REQUIRE(alpha != nullptr && grad_alpha != nullptr, EDF_ERR_INVALID_ARG, "null alpha / grad_alpha pointer");
   return edf::bwd(stream, q, k, v, beta, alpha, grad_out, grad_q, grad_k, grad_v, grad_beta, grad_alpha, workspace,
                   workspace_bytes, batch, seq_len, num_heads, head_dim, dtype, beta_mode);
+}
+
+// KDA: per-row log-space decay, per-head beta; always the exact per-step kernels (the
+// chunked form takes one decay per head).
+size_t edf_kda_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return edf::dr_seq_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+}
+
+int edf_fused_kda_scan(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                       const void* beta, void* out, int batch, int seq_len, int num_heads, int head_dim, int dtype) {
+  int rc = edf::check_dr(batch, seq_len, num_heads, head_dim, dtype, EDF_BETA_PER_HEAD);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && alpha && beta && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  return edf::dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq_len, num_heads, head_dim, dtype, 1, 1);
+}
+
+int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                const void* beta, const void* forward_out, const void* grad_out, void* grad_q,
+                                void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta, void* workspace,
+                                size_t workspace_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                                int dtype) {
+  (void)forward_out;
+  int rc = edf::check_dr(batch, seq_len, num_heads, head_dim, dtype, EDF_BETA_PER_HEAD);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && alpha && beta && grad_out && grad_q && grad_k && grad_v && grad_alpha && grad_beta,
+              EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const size_t need = edf::dr_seq_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(workspace && workspace_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  return edf::dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, grad_q, grad_k, grad_v, grad_beta,
+                                  grad_alpha, workspace, batch, seq_len, num_heads, head_dim, dtype, 1, 1);
 }
 
 }  // extern "C"

@@ -5,7 +5,9 @@
 //   S is [d_v x d_k] per (batch, head); beta per element [B,T,H,d] (one gate per value
 //   row, lib/edifice/recurrent/delta_net.ex:231-273, native/cuda/fused_delta_rule_scan.cu:146-154)
 //   or per head [B,T,H]; alpha per head [B,T,H] or absent
-//   (lib/edifice/recurrent/gated_delta_net.ex:300-353).
+//   (lib/edifice/recurrent/gated_delta_net.ex:300-353), or (KDA) a log-space decay per
+//   value row [B,T,H,d], S_g = diag(exp(alpha_t)) S (native/cuda/fused_kda_scan.cu:1-24,
+//   lib/edifice/cuda/fused_scan.ex:2632-2665; d alpha_i = exp(alpha_i) sum_j dS_g S_p).
 //   Backward: lib/edifice/cuda/fused_scan.ex:1257-1431 (dq = S_t^T do, ds_k = dS_tot k,
 //   dv = beta ds_k, dbeta = err ds_k, dk = dS_tot^T (beta err) - S_g^T (beta ds_k),
 //   dalpha = sum(dS_to_decayed * S_prev), dS_prev = alpha dS_to_decayed).
@@ -41,15 +43,16 @@ struct DRArgs {
   float* part_a;  // [nrb][B*T*H]      per-row-block partial dalpha
   float* part_b;  // [nrb][B*T*H]      per-row-block partial per-head dbeta
   int H, T, d, beta_per_head, nck;
+  int alpha_per_row;  // KDA: alpha [B,T,H,d] in log space, one decay per value row
 };
 
-// One chunk of inputs: k and q over all DP columns, v, beta (and dout) for this
-// workgroup's RB rows, alpha per step; zero beyond T and beyond d, alpha 1 beyond T, so
-// padding steps are identities of the recurrence and of its adjoint.
+// One chunk of inputs: k and q over all DP columns, v, beta, the decay (and dout) for this
+// workgroup's RB rows; zero beyond T and beyond d, decay 1 beyond T, so padding steps are
+// identities of the recurrence and of its adjoint.
 template <int DP>
 struct Stage {
   float k[CK][DP], q[CK][DP], v[CK][RB], b[CK][RB], go[CK][RB];
-  float a[CK];
+  float a[CK][RB];
 };
 
 template <typename TT, int DP>
@@ -74,10 +77,10 @@ EDF_DEVICE void stage_chunk(Stage<DP>& sm, const DRArgs& p, long bh, int rb, int
     if (ok) bv = p.beta_per_head ? ld((const TT*)p.beta, ((long)b * p.T + t) * p.H + h) : ld((const TT*)p.beta, idx);
     sm.b[tt][ii] = bv;
     if (with_dout) sm.go[tt][ii] = ok ? ld((const TT*)p.dout, idx) : 0.0f;
-  }
-  for (int tt = threadIdx.x; tt < CK; tt += 256) {
-    const int t = t0 + tt;
-    sm.a[tt] = (p.alpha != nullptr && t < p.T) ? ld((const TT*)p.alpha, ((long)b * p.T + t) * p.H + h) : 1.0f;
+    float av = 1.0f;
+    if (p.alpha != nullptr && ok)
+      av = p.alpha_per_row ? __expf(ld((const TT*)p.alpha, idx)) : ld((const TT*)p.alpha, ((long)b * p.T + t) * p.H + h);
+    sm.a[tt][ii] = av;
   }
 }
 
@@ -85,7 +88,7 @@ EDF_DEVICE void stage_chunk(Stage<DP>& sm, const DRArgs& p, long bh, int rb, int
 template <int DP>
 EDF_DEVICE void fwd_step(float (&S)[DP / 16], const Stage<DP>& sm, int tt, int tr, int tc) {
   constexpr int NC = DP / 16;
-  const float at = sm.a[tt];
+  const float at = sm.a[tt][tr];
   float r = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) r = fmaf(S[c], sm.k[tt][tc + 16 * c], r);
@@ -170,7 +173,7 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
 #pragma unroll
     for (int tt = CK - 1; tt >= 0; --tt) {
       const int t = t0 + tt;
-      const float at = sm.a[tt];
+      const float at = sm.a[tt][tr];
       const float goi = sm.go[tt][tr], bi = sm.b[tt][tr];
       float r = 0.0f, sk = 0.0f;
 #pragma unroll
@@ -212,6 +215,8 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
       if (tc == 0) {
         reda[0][tr] = pa;
         reda[1][tr] = i < p.d ? err * sk : 0.0f;
+        // KDA: the row's own decay gradient, in log space
+        if (p.alpha_per_row && live && i < p.d) st((TT*)p.dalpha, bth * p.d + i, pa * at);
       }
       __syncthreads();
       if (live) {
@@ -252,7 +257,7 @@ __global__ __launch_bounds__(256) void dr_seq_reduce_kernel(const DRArgs p, long
     const float* part = qty ? p.part_b : p.part_a;
     float acc = 0.0f;
     for (int r = 0; r < nrb; ++r) acc += part[r * nbth + o];
-    if (qty == 0 && p.dalpha != nullptr) st((TT*)p.dalpha, o, acc);
+    if (qty == 0 && p.dalpha != nullptr && !p.alpha_per_row) st((TT*)p.dalpha, o, acc);
     if (qty == 1 && p.beta_per_head) st((TT*)p.dbeta, o, acc);
   }
 }
@@ -315,10 +320,10 @@ size_t dr_seq_backward_workspace_bytes(int batch, int heads, int seq, int d) {
 }
 
 int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
-               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head) {
+               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head, int alpha_per_row) {
   DRArgs a{};
   a.q = q; a.k = k; a.v = v; a.beta = beta; a.alpha = alpha; a.out = out;
-  a.H = heads; a.T = seq; a.d = d; a.beta_per_head = beta_per_head;
+  a.H = heads; a.T = seq; a.d = d; a.beta_per_head = beta_per_head; a.alpha_per_row = alpha_per_row;
   a.nck = (seq + CK - 1) / CK;
   hipStream_t s = as_stream(stream);
   if (dtype == EDF_BF16) return launch_seq<bf16>(s, a, false, batch * heads);
@@ -328,11 +333,11 @@ int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const 
 int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
                         const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
                         void* dalpha, void* workspace, int batch, int seq, int heads, int d, int dtype,
-                        int beta_per_head) {
+                        int beta_per_head, int alpha_per_row) {
   DRArgs a{};
   a.q = q; a.k = k; a.v = v; a.beta = beta; a.alpha = alpha; a.dout = grad_out;
   a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta; a.dalpha = dalpha;
-  a.H = heads; a.T = seq; a.d = d; a.beta_per_head = beta_per_head;
+  a.H = heads; a.T = seq; a.d = d; a.beta_per_head = beta_per_head; a.alpha_per_row = alpha_per_row;
   a.nck = (seq + CK - 1) / CK;
   const SeqWs w = seq_ws(batch, heads, seq, d);
   char* ws = (char*)workspace;

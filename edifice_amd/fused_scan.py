@@ -449,6 +449,40 @@ class _DeltaRule(torch.autograd.Function):
         return dq, dk, dv, db, da
 
 
+class _KDA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, beta):
+        q, k, v, alpha, beta = (t.contiguous() for t in (q, k, v, alpha, beta))
+        _dev(q, k, v, alpha, beta)
+        _same(q, k, v, alpha, beta)
+        bsz, seq, nh, hd = q.shape
+        if alpha.shape != q.shape or tuple(beta.shape) != (bsz, seq, nh):
+            raise EdificeHipError("kda_scan needs alpha [B, T, H, d] and beta [B, T, H]")
+        out = torch.empty_like(v)
+        nat.call("edf_fused_kda_scan", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out), bsz, seq, nh,
+                 hd, dtype_flag(q))
+        ctx.save_for_backward(q, k, v, alpha, beta, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, alpha, beta, out = ctx.saved_tensors
+        do = do.contiguous().to(q.dtype)
+        bsz, seq, nh, hd = q.shape
+        dq, dk, dv, da, db = (torch.empty_like(t) for t in (q, k, v, alpha, beta))
+        wsb = nat.query("edf_kda_scan_backward_workspace_bytes", bsz, seq, nh, hd, dtype_flag(q))
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_kda_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out), _p(do),
+                 _p(dq), _p(dk), _p(dv), _p(da), _p(db), _p(ws), wsb, bsz, seq, nh, hd, dtype_flag(q))
+        return dq, dk, dv, da, db
+
+
+def kda_scan(q, k, v, alpha, beta):
+    """``FusedScan.kda_scan/5`` (fused_scan.ex:398-412): the delta rule with a log-space decay
+    per value row, S_g = diag(exp(alpha_t)) S; q, k, v, alpha [B, T, H, d], beta [B, T, H]."""
+    return _KDA.apply(q, k, v, alpha, beta)
+
+
 def delta_net_scan(q, k, v, beta):
     """``FusedScan.delta_net_scan/4`` (fused_scan.ex:195-209): q, k, v [B, T, H, d]; k
     L2-normalised, beta post-sigmoid, per element [B, T, H, d] or per head [B, T, H]."""

@@ -197,6 +197,24 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
 size_t edf_selective_scan_backward_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode,
                                                    int have_states);
 
+/* KDA (Kimi delta attention): the delta rule with a log-space decay per value row,
+ * S_g = diag(exp(alpha_t)) S, and a per-head beta.  Replaces fused_kda_scan/10 (q, k, v,
+ * alpha [B,T,H,d], beta [B,T,H], batch, seq, heads, head_dim, dtype), lib/edifice/cuda/
+ * nif.ex:90 -> native/cuda/fused_kda_scan.cu (semantics fused_scan.ex:2632-2665); head_dim
+ * <= 128; no workspace for the forward. */
+int edf_fused_kda_scan(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                       const void* beta, void* out, int batch, int seq_len, int num_heads, int head_dim, int dtype);
+
+/* Replaces fused_kda_scan_backward/12 (q, k, v, alpha, beta, fwd, grad, ...), nif.ex:206:
+ * dq, dk, dv, d alpha [B,T,H,d] (log space), d beta [B,T,H]; workspace
+ * edf_kda_scan_backward_workspace_bytes() bytes. */
+int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                const void* beta, const void* forward_out, const void* grad_out, void* grad_q,
+                                void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta, void* workspace,
+                                size_t workspace_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                                int dtype);
+size_t edf_kda_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
+
 /* ------------------------------------------------------------------------
  * Flash attention   O = softmax(Q K^T / sqrt(d) [+ causal -inf]) V
  *   q, k, v, out, grads: [B, H, T, d] in dtype; lse: float32 [B, H, T] (natural log)

@@ -30,6 +30,8 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 clip mask ⇒ ddt=0 outside [1e-3, 0.1].
   delta_rule                    delta_net_random.safetensors (forward and input
                                 gradient), β≡0 ⇒ o≡0, α≡1 ⇒ DeltaNet, T=1 closed form.
+  kda_scan / _backward          alpha = 0 ==> DeltaNet, rows sharing one decay ==>
+                                GatedDeltaNet, torch autograd of an independent forward.
   delta_rule_backward           delta_net_random.safetensors gradient.input, torch
                                 autograd of the forward, finite differences.
   laser_attention / _backward   identical value rows ==> O = that row; torch autograd of an
@@ -437,6 +439,15 @@ def _beta4(beta, shape):
     return beta
 
 
+def _decay4(alpha, shape):
+    """Per-row decay [B,T,H,d_v] from a per-head alpha [B,T,H] (broadcast along the rows) or
+    a per-row one; None stays None."""
+    if alpha is None:
+        return None
+    alpha = np.asarray(alpha, dtype=np.float64)
+    return np.broadcast_to(alpha[..., None], shape) if alpha.ndim == 3 else alpha
+
+
 def l2_normalize_keys(k):
     """k / sqrt(sum k^2 + 1e-6) over head_dim (delta_net.ex:297-298)."""
     k = np.asarray(k, dtype=np.float64)
@@ -448,11 +459,13 @@ def delta_rule(q, k, v, beta, alpha=None, return_states=False):
 
     S is [heads, d_v, d_k] per batch, retrieval S k contracts the key axis.
     alpha=None is DeltaNet (delta_net.ex:231-273); otherwise GatedDeltaNet with a per
-    (b, t, head) scalar decay (gated_delta_net.ex:300-353).  beta is per element
+    (b, t, head) scalar decay (gated_delta_net.ex:300-353), or a decay per value row
+    [B,T,H,d_v] (multiplicative; ``kda_scan`` passes exp of KDA's log decay).  beta is per element
     [B,T,H,d] as in the reference, or per head [B,T,H] (broadcast along d).
     No 1/sqrt(d) scaling of q (delta_net.ex:266-268).
     """
-    q, k, v, alpha = _f64(q, k, v, alpha)
+    q, k, v = _f64(q, k, v)
+    alpha = _decay4(alpha, v.shape)
     beta = _beta4(beta, v.shape)
     bsz, seq, nh, d = q.shape
     dv = v.shape[3]
@@ -461,7 +474,7 @@ def delta_rule(q, k, v, beta, alpha=None, return_states=False):
     states = []
     for t in range(seq):
         if alpha is not None:
-            S = alpha[:, t, :, None, None] * S
+            S = alpha[:, t, :, :, None] * S
         r = np.einsum("bhij,bhj->bhi", S, k[:, t])
         err = beta[:, t] * (v[:, t] - r)
         S = S + err[..., :, None] * k[:, t, :, None, :]
@@ -484,7 +497,9 @@ def delta_rule_backward(q, k, v, beta, do, alpha=None):
       dalpha = sum(dS_to_decayed * S_prev); dS_prev = alpha dS_to_decayed.
     For per-head beta the per-element dbeta is summed over the value rows.
     """
-    q, k, v, do, alpha = _f64(q, k, v, do, alpha)
+    q, k, v, do = _f64(q, k, v, do)
+    per_head_alpha = alpha is not None and np.asarray(alpha).ndim == 3
+    alpha = _decay4(alpha, v.shape)
     per_head_beta = np.asarray(beta).ndim == 3
     beta = _beta4(beta, v.shape)
     bsz, seq, nh, d = q.shape
@@ -494,18 +509,18 @@ def delta_rule_backward(q, k, v, beta, do, alpha=None):
     s_prev = np.empty((bsz, seq, nh, dv_, d))
     for t in range(seq):
         s_prev[:, t] = S
-        sg = S if alpha is None else alpha[:, t, :, None, None] * S
+        sg = S if alpha is None else alpha[:, t, :, :, None] * S
         r = np.einsum("bhij,bhj->bhi", sg, k[:, t])
         S = sg + (beta[:, t] * (v[:, t] - r))[..., :, None] * k[:, t, :, None, :]
     dq = np.empty_like(q)
     dk = np.empty_like(k)
     dvv = np.empty_like(v)
     dbeta = np.empty_like(v)
-    dalpha = np.empty((bsz, seq, nh)) if alpha is not None else None
+    dalpha = np.empty((bsz, seq, nh, dv_)) if alpha is not None else None
     dS = np.zeros((bsz, nh, dv_, d))
     for t in range(seq - 1, -1, -1):
         sp = s_prev[:, t]
-        a = None if alpha is None else alpha[:, t, :, None, None]
+        a = None if alpha is None else alpha[:, t, :, :, None]
         sg = sp if a is None else a * sp
         kt, qt, bt = k[:, t], q[:, t], beta[:, t]
         err = v[:, t] - np.einsum("bhij,bhj->bhi", sg, kt)
@@ -521,11 +536,29 @@ def delta_rule_backward(q, k, v, beta, do, alpha=None):
         if a is None:
             dS = d_dec
         else:
-            dalpha[:, t] = (d_dec * sp).sum(axis=(2, 3))
+            dalpha[:, t] = (d_dec * sp).sum(axis=3)
             dS = a * d_dec
     if per_head_beta:
         dbeta = dbeta.sum(axis=3)
+    if per_head_alpha:
+        dalpha = dalpha.sum(axis=3)
     return dict(dq=dq, dk=dk, dv=dvv, dbeta=dbeta, dalpha=dalpha)
+
+
+def kda_scan(q, k, v, alpha, beta):
+    """KDA: the delta rule with decay exp(alpha_t) per value row and a per-head beta
+    (``kda_scan_fallback``, fused_scan.ex:2632-2665; kernel fused_kda_scan.cu:1-24)."""
+    return delta_rule(q, k, v, beta, np.exp(np.asarray(alpha, dtype=np.float64)))
+
+
+def kda_scan_backward(q, k, v, alpha, beta, do):
+    """-> dict(dq, dk, dv, dbeta [B,T,H], dalpha [B,T,H,d] in log space)
+    (``kda_backward_fallback``, fused_scan.ex:1552-1640): the decay gradient of
+    ``delta_rule_backward`` times exp(alpha)."""
+    dec = np.exp(np.asarray(alpha, dtype=np.float64))
+    g = delta_rule_backward(q, k, v, beta, do, dec)
+    g["dalpha"] = g["dalpha"] * dec
+    return g
 
 
 # ---------------------------------------------------------------------------

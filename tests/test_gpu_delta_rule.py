@@ -76,3 +76,28 @@ def test_delta_rule_invariants(rng):
     qr, kr, vr, br = (a[:, :1].astype(np.float32).astype(np.float64) for a in (q, k, v, beta))
     expect = (br[..., None] * vr) * (kr * qr).sum(-1, keepdims=True)
     assert_close(o1, expect, 1e-5, "T=1 closed form")
+
+
+@pytest.mark.parametrize("shape", [(2, 37, 2, 16), (1, 70, 3, 64), (1, 33, 2, 128), (2, 20, 1, 50)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_kda_fwd_bwd(shape, dtype, rng):
+    """FusedScan.kda_scan/5 and its backward (per-row log decay, per-head beta) against the oracle."""
+    from edifice_amd import fused_scan as fs
+    bsz, t, h, d = shape
+    announce("kda", shape=shape, dtype=dtype)
+    q = scans.l2_normalize_keys(rng.normal(size=shape))
+    k = scans.l2_normalize_keys(rng.normal(size=shape))
+    v = rng.normal(size=shape)
+    alpha = -rng.uniform(0.01, 0.3, size=shape)
+    beta = rng.uniform(0.1, 0.9, size=(bsz, t, h))
+    do = rng.normal(size=shape)
+    tq, tk, tv, ta, tb = (to_dev(a, dtype).requires_grad_() for a in (q, k, v, alpha, beta))
+    out = fs.kda_scan(tq, tk, tv, ta, tb)
+    out.backward(to_dev(do, dtype))
+    qr, kr, vr, ar, br, dor = (rounded(a, dtype) for a in (q, k, v, alpha, beta, do))
+    tol = TOL[dtype]
+    assert_close(host(out), scans.kda_scan(qr, kr, vr, ar, br), tol, "o")
+    g = scans.kda_scan_backward(qr, kr, vr, ar, br, dor)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb)):
+        assert_close(host(tt.grad), g[n], tol, n)
+

@@ -267,3 +267,25 @@ def test_laser_attention_vs_torch_autograd(rng, causal):
     for a, e, n in ((dq, tq.grad, "dq"), (dk, tk.grad, "dk"), (dv, tv.grad, "dv")):
         assert_close(a, e.numpy(), 1e-10, n)
 
+
+def test_kda_backward_vs_autograd(rng):
+    """KDA backward (oracle) against torch autograd of an independent torch forward."""
+    bsz, t, h, d = 1, 5, 2, 3
+    q, k, v, do = (rng.normal(size=(bsz, t, h, d)) for _ in range(4))
+    alpha = -rng.uniform(0.05, 0.6, size=(bsz, t, h, d))
+    beta = rng.uniform(0.1, 0.9, size=(bsz, t, h))
+    tq, tk, tv, ta, tb = _t(q), _t(k), _t(v), _t(alpha), _t(beta)
+    S = torch.zeros(bsz, h, d, d, dtype=F64)
+    outs = []
+    for s in range(t):
+        S = torch.exp(ta[:, s])[..., :, None] * S
+        err = tv[:, s] - torch.einsum("bhij,bhj->bhi", S, tk[:, s])
+        S = S + tb[:, s][..., None, None] * err[..., :, None] * tk[:, s][..., None, :]
+        outs.append(torch.einsum("bhij,bhj->bhi", S, tq[:, s]))
+    out = torch.stack(outs, 1)
+    out.backward(torch.from_numpy(do))
+    assert_close(scans.kda_scan(q, k, v, alpha, beta), out.detach().numpy(), 1e-12, "o")
+    g = scans.kda_scan_backward(q, k, v, alpha, beta, do)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb)):
+        assert_close(g[n], tt.grad.numpy(), 1e-10, n)
+

@@ -339,3 +339,16 @@ def test_laser_attention_identical_rows(rng):
     v = np.broadcast_to(row, (b, h, t, d)).copy()
     np.testing.assert_allclose(scans.laser_attention(q, k, v, causal=True), v, rtol=1e-12, atol=1e-12)
 
+
+def test_kda_reduces_to_deltanet_and_gated(rng):
+    """KDA with alpha = 0 is DeltaNet; with every row sharing log decay c it is
+    GatedDeltaNet with alpha = exp(c)."""
+    bsz, t, h, d = 1, 6, 2, 4
+    q, k, v = (rng.normal(size=(bsz, t, h, d)) for _ in range(3))
+    beta = rng.uniform(0.1, 0.9, size=(bsz, t, h))
+    np.testing.assert_allclose(scans.kda_scan(q, k, v, np.zeros((bsz, t, h, d)), beta),
+                               scans.delta_rule(q, k, v, beta), rtol=1e-12)
+    c = -rng.uniform(0.05, 0.5, size=(bsz, t, h))
+    np.testing.assert_allclose(scans.kda_scan(q, k, v, np.broadcast_to(c[..., None], (bsz, t, h, d)), beta),
+                               scans.delta_rule(q, k, v, beta, np.exp(c)), rtol=1e-12)
+
