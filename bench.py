@@ -357,6 +357,39 @@ def bench_fox(torch, steps, warmup, B=4, H=32, T=4096, d=128):
                 shape=dict(B=B, H=H, T=T, d=d, causal=True))
 
 
+def bench_kda(torch, steps, warmup, B=8, T=2048, H=8, d=128):
+    """KDA (per-row log decay, per-head beta), bf16, on the exact per-step kernels: fwd and bwd
+    time per call and tokens/s (B T per call)."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(3001)
+    dev, bf = "cuda", torch.bfloat16
+    l2n = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)  # noqa: E731
+    q = l2n(torch.randn(B, T, H, d, device=dev, generator=g)).to(bf)
+    k = l2n(torch.randn(B, T, H, d, device=dev, generator=g)).to(bf)
+    v = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    alpha = (-0.3 * torch.rand(B, T, H, d, device=dev, generator=g)).to(bf)
+    beta = torch.sigmoid(torch.randn(B, T, H, device=dev, generator=g)).to(bf)
+    do = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    out, dq, dk, dv, da = (torch.empty_like(v) for _ in range(5))
+    db = torch.empty_like(beta)
+    wsb = nat.query("edf_kda_scan_backward_workspace_bytes", B, T, H, d, 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_kda_scan", stream, P(q), P(k), P(v), P(alpha), P(beta), P(out), B, T, H, d, 1)
+
+    def bwd():
+        nat.call("edf_fused_kda_scan_backward", stream, P(q), P(k), P(v), P(alpha), P(beta), P(out), P(do), P(dq),
+                 P(dk), P(dv), P(da), P(db), P(ws), wsb, B, T, H, d, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,
+                shape=dict(B=B, T=T, H=H, d=d))
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
@@ -457,6 +490,7 @@ def main():
     configs["c2_selective_scan"] = ss
     if want("delta"):
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
+        configs["kda_8x2048x8x128"] = bench_kda(torch, args.steps, args.warmup)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
         configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,
