@@ -390,6 +390,40 @@ def bench_kda(torch, steps, warmup, B=8, T=2048, H=8, d=128):
                 shape=dict(B=B, T=T, H=H, d=d))
 
 
+def bench_delta_product(torch, steps, warmup, B=8, T=2048, NH=2, H=8, d=128):
+    """DeltaProduct (n_h = 2 sub-steps per token, raw keys normalized in the kernel), bf16:
+    fwd and bwd time per call and tokens/s (B T per call)."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(3002)
+    dev, bf = "cuda", torch.bfloat16
+    q = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    k = torch.randn(B, T, NH, H, d, device=dev, generator=g).to(bf)
+    v = torch.randn(B, T, NH, H, d, device=dev, generator=g).to(bf)
+    beta = torch.sigmoid(torch.randn(B, T, NH, H, device=dev, generator=g)).to(bf)
+    do = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    out, dq = torch.empty_like(q), torch.empty_like(q)
+    dk, dv, db = torch.empty_like(k), torch.empty_like(v), torch.empty_like(beta)
+    wsf = nat.query("edf_delta_product_workspace_bytes", B, T, NH, H, d, 1)
+    wsb = nat.query("edf_delta_product_backward_workspace_bytes", B, T, NH, H, d, 1)
+    ws1 = torch.empty(wsf, dtype=torch.uint8, device=dev)
+    ws2 = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_delta_product_scan", stream, P(q), P(k), P(v), P(beta), P(out), P(ws1), wsf,
+                 B, T, NH, H, d, 1)
+
+    def bwd():
+        nat.call("edf_fused_delta_product_scan_backward", stream, P(q), P(k), P(v), P(beta), P(out), P(do), P(dq),
+                 P(dk), P(dv), P(db), P(ws2), wsb, B, T, NH, H, d, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,
+                shape=dict(B=B, T=T, n_h=NH, H=H, d=d))
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
@@ -491,6 +525,7 @@ def main():
     if want("delta"):
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
         configs["kda_8x2048x8x128"] = bench_kda(torch, args.steps, args.warmup)
+        configs["delta_product_8x2048x2x8x128"] = bench_delta_product(torch, args.steps, args.warmup)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
         configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,

@@ -1,0 +1,470 @@
+// DeltaProduct: n_h generalized-Householder delta-rule sub-steps per token, forward and
+// backward (native/cuda/fused_delta_product_scan.cu, fused_delta_product_scan_backward.cu).
+//
+// Semantics, with S [d_v x d_k] per (batch, head) as in the delta rule kernels (the
+// reference keeps the transpose, S_ref[key][value]):
+//   per token t, for j in 0..n_h-1:  kn = k_tj / sqrt(|k_tj|^2 + 1e-6)
+//                                    S  = S + beta_tj (v_tj - S kn) kn^T
+//   o_raw[j] = sum_i S[i][j] q_t[i]  (the reference's S_ref q_t, a sum over value rows)
+//   o_t = o_raw / sqrt(mean(o_raw^2) + 1e-6)
+// k and v are [B, T, n_h, H, d], i.e. [B, T*n_h, H, d]: the sub-steps form one delta-rule
+// sequence of T*n_h steps whose every n_h-th step emits an output.
+//
+// Layout of the work: as in the per-step delta kernels, a workgroup owns RB = 16 value
+// rows of one head's state (lane (tr, tc) holds S[16 rb + tr][tc + 16 c]); the update
+// and the retrieval S kn are row-local.  The output sums over ALL rows, so each row
+// block writes a partial o_raw (summed over its rows through a wave shuffle and LDS) and
+// a small kernel adds the d/16 partials in block order and applies the RMS norm.
+// Backward: dO (the gradient at o_raw) is computed from the re-run forward's partials;
+// dq_t = S_t dO and dv are row-local, the key and beta gradients sum over rows (row-block
+// partials, reduced in order, then taken through the key normalization).  The forward
+// states are checkpointed every CK sub-steps and recomputed per chunk, never inverted.
+#include "edf_abi.hpp"
+#include "edf_common.hpp"
+
+namespace edf {
+namespace {
+
+constexpr int DPR_CK = 16;  // sub-steps per staged chunk / checkpoint interval
+constexpr int DPR_RB = 16;  // state rows per workgroup
+constexpr float DPR_EPS = 1.0e-6f;  // fused_delta_product_scan.cu:38
+
+struct DPArgs {
+  const void *q, *k, *v, *beta, *dout;
+  void *out, *dq, *dk, *dv, *dbeta;
+  float* dO;      // [B*T*H][d]        gradient at the raw output (backward)
+  float* ckpt;    // [BH][nck][DP*DP]  state after each chunk of sub-steps
+  float* part_o;  // [nrb][B*T*H][d]   per-row-block partial raw output
+  float* part_k;  // [nrb][B*TS*H][d]  per-row-block partial gradient of the normalized key
+  float* part_b;  // [nrb][B*TS*H]     per-row-block partial dbeta
+  int H, T, NH, TS, d, nck;  // TS = T * NH sub-steps
+};
+
+template <int DP>
+struct DPStage {
+  float k[DPR_CK][DP];          // normalized key per sub-step (0 beyond TS and d)
+  float g[DPR_CK][DP];          // backward: dO of the token a sub-step closes, else 0
+  float red[DPR_CK][4][DP];     // per-wave sums over its 4 rows: raw output / key gradient
+  float v[DPR_CK][DPR_RB];      // this block's value rows
+  float q[DPR_CK][DPR_RB];      // q rows of the token a sub-step closes, else 0
+  float b[DPR_CK];              // beta per sub-step
+  float redb[DPR_CK][4];        // per-wave beta-gradient sums
+};
+
+EDF_DEVICE bool closes_token(const DPArgs& p, int s) { return s < p.TS && s % p.NH == p.NH - 1; }
+
+// Sum over the 4 rows a wave holds (lanes l, l^16, l^32, l^48 share a column).
+EDF_DEVICE float rows4_sum(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+EDF_DEVICE float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+template <typename TT, int DP>
+EDF_DEVICE void stage(DPStage<DP>& sm, const DPArgs& p, long bh, int rb, int t0, bool grad) {
+  constexpr int NC = DP / 16;
+  const int b = (int)(bh / p.H), h = (int)(bh % p.H), d = p.d;
+  const int tid = threadIdx.x;
+  for (int e = tid; e < DPR_CK * DP; e += 256) {
+    const int tt = e / DP, j = e % DP, s = t0 + tt;
+    const bool ok = s < p.TS && j < d;
+    sm.k[tt][j] = ok ? ld((const TT*)p.k, (((long)b * p.TS + s) * p.H + h) * d + j) : 0.0f;
+    if (grad) {
+      const bool cl = closes_token(p, s) && j < d;
+      sm.g[tt][j] = cl ? p.dO[(((long)b * p.T + s / p.NH) * p.H + h) * d + j] : 0.0f;
+    }
+  }
+  for (int e = tid; e < DPR_CK * DPR_RB; e += 256) {
+    const int tt = e / DPR_RB, ii = e % DPR_RB, i = rb * DPR_RB + ii, s = t0 + tt;
+    const bool ok = s < p.TS && i < d;
+    sm.v[tt][ii] = ok ? ld((const TT*)p.v, (((long)b * p.TS + s) * p.H + h) * d + i) : 0.0f;
+    const bool cl = closes_token(p, s) && i < d;
+    sm.q[tt][ii] = cl ? ld((const TT*)p.q, (((long)b * p.T + s / p.NH) * p.H + h) * d + i) : 0.0f;
+  }
+  if (tid < DPR_CK) {
+    const int s = t0 + tid;
+    sm.b[tid] = s < p.TS ? ld((const TT*)p.beta, ((long)b * p.TS + s) * p.H + h) : 0.0f;
+  }
+  __syncthreads();
+  // key normalization: 16 lanes per sub-step, each over its own columns
+  {
+    const int tt = tid >> 4, l = tid & 15;
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) ss = fmaf(sm.k[tt][l + 16 * c], sm.k[tt][l + 16 * c], ss);
+    const float inv = 1.0f / sqrtf(row16_sum(ss) + DPR_EPS);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) sm.k[tt][l + 16 * c] *= inv;
+  }
+}
+
+// One sub-step of the lane's row segment: S = S + beta (v - S kn) kn^T.
+template <int DP>
+EDF_DEVICE void sub_step(float (&S)[DP / 16], const DPStage<DP>& sm, int tt, int tr, int tc) {
+  constexpr int NC = DP / 16;
+  float r = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) r = fmaf(S[c], sm.k[tt][tc + 16 * c], r);
+  const float e = sm.b[tt] * (sm.v[tt][tr] - row16_sum(r));
+#pragma unroll
+  for (int c = 0; c < NC; ++c) S[c] = fmaf(e, sm.k[tt][tc + 16 * c], S[c]);
+}
+
+template <typename TT, int DP>
+__global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
+  constexpr int NC = DP / 16;
+  __shared__ DPStage<DP> sm;
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15, w = tid >> 6, lane = tid & 63;
+  const long bh = blockIdx.x;
+  const int rb = blockIdx.y, i = rb * DPR_RB + tr;
+  const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  const long nbth = (long)gridDim.x * p.T;
+  float S[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) S[c] = 0.0f;
+  for (int t0 = 0; t0 < p.TS; t0 += DPR_CK) {
+    __syncthreads();
+    stage<TT, DP>(sm, p, bh, rb, t0, false);
+    __syncthreads();
+    for (int tt = 0; tt < DPR_CK && t0 + tt < p.TS; ++tt) {
+      sub_step<DP>(S, sm, tt, tr, tc);
+      if (p.part_o != nullptr && closes_token(p, t0 + tt)) {
+        const float qi = sm.q[tt][tr];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const float o = rows4_sum(S[c] * qi);
+          if (lane < 16) sm.red[tt][w][tc + 16 * c] = o;
+        }
+      }
+    }
+    if (p.ckpt != nullptr) {
+      float* cp = p.ckpt + ((long)bh * p.nck + t0 / DPR_CK) * DP * DP + (long)i * DP + tc;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) cp[16 * c] = S[c];
+    }
+    if (p.part_o != nullptr) {
+      __syncthreads();
+      for (int e = tid; e < DPR_CK * DP; e += 256) {
+        const int tt = e / DP, j = e % DP, s = t0 + tt;
+        if (j < p.d && closes_token(p, s)) {
+          const long bth = ((long)b * p.T + s / p.NH) * p.H + h;
+          p.part_o[((long)rb * nbth + bth) * p.d + j] =
+              (sm.red[tt][0][j] + sm.red[tt][1][j]) + (sm.red[tt][2][j] + sm.red[tt][3][j]);
+        }
+      }
+    }
+  }
+}
+
+// o_raw = the row-block partials added in block order; forward: out = RMS_norm(o_raw);
+// backward: dO = dout / r - o_raw (dout . o_raw) / (d r^3).  One wave per (b, t, h).
+template <typename TT>
+__global__ __launch_bounds__(256) void dp_finish_kernel(const DPArgs p, long nbth, int nrb, int backward) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= nbth) return;
+  const int lane = threadIdx.x & 63, d = p.d;
+  float o[2], g[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int j = lane + 64 * u;
+    float acc = 0.0f;
+    if (j < d)
+      for (int r = 0; r < nrb; ++r) acc += p.part_o[((long)r * nbth + row) * d + j];
+    o[u] = acc;
+    g[u] = backward && j < d ? ld((const TT*)p.dout, row * d + j) : 0.0f;
+  }
+  const float ms = wave_sum(o[0] * o[0] + o[1] * o[1]) / (float)d;
+  const float rinv = 1.0f / sqrtf(ms + DPR_EPS);
+  if (!backward) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      if (lane + 64 * u < d) st((TT*)p.out, row * d + lane + 64 * u, o[u] * rinv);
+    return;
+  }
+  const float dot = wave_sum(g[0] * o[0] + g[1] * o[1]);
+  const float c = dot * rinv * rinv * rinv / (float)d;
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (lane + 64 * u < d) p.dO[row * d + lane + 64 * u] = g[u] * rinv - o[u] * c;
+}
+
+// Backward over chunks of sub-steps in reverse.  Per sub-step (S_p the state before it,
+// S_n = S_p + be kn^T, dtot = dS + q dO^T on a token's last sub-step):
+//   dq = S_n dO (token's last sub-step), ds_k = dtot kn, dv = beta ds_k, dbeta = err . ds_k,
+//   dkn = dtot^T be - S_p^T (beta ds_k), dS <- dtot - beta ds_k kn^T, err = v - S_p kn, be = beta err.
+template <typename TT, int DP>
+__global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
+  constexpr int NC = DP / 16;
+  __shared__ DPStage<DP> sm;
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15, w = tid >> 6, lane = tid & 63;
+  const long bh = blockIdx.x;
+  const int rb = blockIdx.y, i = rb * DPR_RB + tr;
+  const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  const long nbts = (long)gridDim.x * p.TS;
+  float dS[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) dS[c] = 0.0f;
+
+  for (int ck = p.nck - 1; ck >= 0; --ck) {
+    const int t0 = ck * DPR_CK;
+    __syncthreads();
+    stage<TT, DP>(sm, p, bh, rb, t0, true);
+    __syncthreads();
+    float Sl[DPR_CK][NC];  // Sl[tt] = state before sub-step t0 + tt
+    {
+      float S[NC];
+      const float* cp = p.ckpt + ((long)bh * p.nck + max(ck - 1, 0)) * DP * DP + (long)i * DP + tc;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) S[c] = ck > 0 ? cp[16 * c] : 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < DPR_CK; ++tt) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) Sl[tt][c] = S[c];
+        sub_step<DP>(S, sm, tt, tr, tc);
+      }
+    }
+#pragma unroll
+    for (int tt = DPR_CK - 1; tt >= 0; --tt) {
+      const int s = t0 + tt;
+      const float qi = sm.q[tt][tr], bi = sm.b[tt];
+      float r = 0.0f, sk = 0.0f, dtot[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float kj = sm.k[tt][tc + 16 * c];
+        dtot[c] = fmaf(qi, sm.g[tt][tc + 16 * c], dS[c]);
+        r = fmaf(Sl[tt][c], kj, r);
+        sk = fmaf(dtot[c], kj, sk);
+      }
+      r = row16_sum(r);
+      sk = row16_sum(sk);
+      const float err = sm.v[tt][tr] - r;
+      const float be = bi * err, bdk = bi * sk;
+      float pq = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const float kj = sm.k[tt][tc + 16 * c];
+        pq = fmaf(fmaf(be, kj, Sl[tt][c]), sm.g[tt][tc + 16 * c], pq);
+        const float pk = rows4_sum(fmaf(dtot[c], be, -Sl[tt][c] * bdk));
+        if (lane < 16) sm.red[tt][w][tc + 16 * c] = pk;
+        dS[c] = fmaf(-bdk, kj, dtot[c]);
+      }
+      pq = row16_sum(pq);
+      const float pb = rows4_sum(tc == 0 ? err * sk : 0.0f);
+      if (lane == 0) sm.redb[tt][w] = pb;
+      if (s < p.TS && tc == 0 && i < p.d) {
+        st((TT*)p.dv, (((long)b * p.TS + s) * p.H + h) * p.d + i, bdk);
+        if (closes_token(p, s)) st((TT*)p.dq, (((long)b * p.T + s / p.NH) * p.H + h) * p.d + i, pq);
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < DPR_CK * DP; e += 256) {
+      const int tt = e / DP, j = e % DP, s = t0 + tt;
+      if (j < p.d && s < p.TS) {
+        const long bts = ((long)b * p.TS + s) * p.H + h;
+        p.part_k[((long)rb * nbts + bts) * p.d + j] =
+            (sm.red[tt][0][j] + sm.red[tt][1][j]) + (sm.red[tt][2][j] + sm.red[tt][3][j]);
+      }
+    }
+    if (tid < DPR_CK && t0 + tid < p.TS) {
+      const long bts = ((long)b * p.TS + t0 + tid) * p.H + h;
+      p.part_b[(long)rb * nbts + bts] =
+          (sm.redb[tid][0] + sm.redb[tid][1]) + (sm.redb[tid][2] + sm.redb[tid][3]);
+    }
+  }
+}
+
+// dk = the row-block partials of dkn added in block order, through the key normalization
+// dk = (dkn - kn (dkn . kn)) / sqrt(|k|^2 + 1e-6); dbeta likewise summed.  One wave per
+// (b, sub-step, h).
+template <typename TT>
+__global__ __launch_bounds__(256) void dp_reduce_kernel(const DPArgs p, long nbts, int nrb) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= nbts) return;
+  const int lane = threadIdx.x & 63, d = p.d;
+  float g[2], kv[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int j = lane + 64 * u;
+    float acc = 0.0f;
+    if (j < d)
+      for (int r = 0; r < nrb; ++r) acc += p.part_k[((long)r * nbts + row) * d + j];
+    g[u] = acc;
+    kv[u] = j < d ? ld((const TT*)p.k, row * d + j) : 0.0f;
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(kv[0] * kv[0] + kv[1] * kv[1]) + DPR_EPS);
+  const float dot = wave_sum(g[0] * kv[0] + g[1] * kv[1]) * inv;  // dkn . kn
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+    if (lane + 64 * u < d) st((TT*)p.dk, row * d + lane + 64 * u, (g[u] - kv[u] * inv * dot) * inv);
+  if (lane == 0) {
+    float acc = 0.0f;
+    for (int r = 0; r < nrb; ++r) acc += p.part_b[(long)r * nbts + row];
+    st((TT*)p.dbeta, row, acc);
+  }
+}
+
+inline int dp_pad(int d) { return d <= 16 ? 16 : d <= 32 ? 32 : d <= 64 ? 64 : 128; }
+inline size_t dp_align(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct DPWs {
+  size_t part_o, ckpt, dO, part_k, part_b, total;
+};
+
+inline DPWs dp_ws(int batch, int seq, int nh, int heads, int d, bool backward) {
+  const size_t dp = dp_pad(d), nrb = dp / DPR_RB, ts = (size_t)seq * nh;
+  const size_t bh = (size_t)batch * heads, nbth = bh * seq, nbts = bh * ts;
+  const size_t nck = (ts + DPR_CK - 1) / DPR_CK;
+  DPWs w{};
+  size_t off = 0;
+  w.part_o = off;
+  off += dp_align(nrb * nbth * d * 4);
+  if (backward) {
+    w.ckpt = off;
+    off += dp_align(bh * nck * dp * dp * 4);
+    w.dO = off;
+    off += dp_align(nbth * d * 4);
+    w.part_k = off;
+    off += dp_align(nrb * nbts * d * 4);
+    w.part_b = off;
+    off += dp_align(nrb * nbts * 4);
+  }
+  w.total = off;
+  return w;
+}
+
+template <typename TT>
+int dp_launch(hipStream_t s, const DPArgs& a, bool bwd, int BH) {
+  const int d = a.d;
+#define EDF_DP_LAUNCH(DP)                                       \
+  do {                                                          \
+    const dim3 grid(BH, DP / DPR_RB);                           \
+    if (bwd)                                                    \
+      dp_bwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);            \
+    else                                                        \
+      dp_fwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);            \
+  } while (0)
+  if (d <= 16)
+    EDF_DP_LAUNCH(16);
+  else if (d <= 32)
+    EDF_DP_LAUNCH(32);
+  else if (d <= 64)
+    EDF_DP_LAUNCH(64);
+  else
+    EDF_DP_LAUNCH(128);
+#undef EDF_DP_LAUNCH
+  return check_launch(bwd ? "delta product backward" : "delta product");
+}
+
+int check_dp(int batch, int seq, int nh, int heads, int d, int dtype) {
+  EDF_REQUIRE(batch > 0 && seq > 0 && nh > 0 && heads > 0 && d > 0, EDF_ERR_INVALID_ARG,
+              "dimensions must be positive");
+  EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
+  EDF_REQUIRE(d <= 128, EDF_ERR_UNSUPPORTED, "head_dim %d > 128 unsupported", d);
+  EDF_REQUIRE((long)seq * nh < (1L << 30), EDF_ERR_UNSUPPORTED, "seq_len * num_householder too large");
+  return EDF_OK;
+}
+
+DPArgs dp_args(const void* q, const void* k, const void* v, const void* beta, int seq, int nh, int heads, int d) {
+  DPArgs a{};
+  a.q = q; a.k = k; a.v = v; a.beta = beta;
+  a.H = heads; a.T = seq; a.NH = nh; a.TS = seq * nh; a.d = d;
+  a.nck = (a.TS + DPR_CK - 1) / DPR_CK;
+  return a;
+}
+
+}  // namespace
+}  // namespace edf
+
+extern "C" {
+
+size_t edf_delta_product_workspace_bytes(int batch, int seq_len, int num_householder, int num_heads, int head_dim,
+                                         int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || num_householder <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return edf::dp_ws(batch, seq_len, num_householder, num_heads, head_dim, false).total;
+}
+
+size_t edf_delta_product_backward_workspace_bytes(int batch, int seq_len, int num_householder, int num_heads,
+                                                  int head_dim, int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || num_householder <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return edf::dp_ws(batch, seq_len, num_householder, num_heads, head_dim, true).total;
+}
+
+int edf_fused_delta_product_scan(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                                 void* out, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                 int num_householder, int num_heads, int head_dim, int dtype) {
+  using namespace edf;
+  int rc = check_dp(batch, seq_len, num_householder, num_heads, head_dim, dtype);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && beta && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const DPWs w = dp_ws(batch, seq_len, num_householder, num_heads, head_dim, false);
+  EDF_REQUIRE(workspace && workspace_bytes >= w.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
+              w.total);
+  DPArgs a = dp_args(q, k, v, beta, seq_len, num_householder, num_heads, head_dim);
+  a.out = out;
+  a.part_o = (float*)((char*)workspace + w.part_o);
+  const int bh = batch * num_heads, nrb = dp_pad(head_dim) / DPR_RB;
+  const long nbth = (long)bh * seq_len;
+  hipStream_t s = as_stream(stream);
+  const unsigned grows = (unsigned)((nbth + 3) / 4);
+  if (dtype == EDF_BF16) {
+    rc = dp_launch<bf16>(s, a, false, bh);
+    if (rc) return rc;
+    dp_finish_kernel<bf16><<<grows, 256, 0, s>>>(a, nbth, nrb, 0);
+  } else {
+    rc = dp_launch<float>(s, a, false, bh);
+    if (rc) return rc;
+    dp_finish_kernel<float><<<grows, 256, 0, s>>>(a, nbth, nrb, 0);
+  }
+  return check_launch("delta product output norm");
+}
+
+int edf_fused_delta_product_scan_backward(void* stream, const void* q, const void* k, const void* v,
+                                          const void* beta, const void* forward_out, const void* grad_out,
+                                          void* grad_q, void* grad_k, void* grad_v, void* grad_beta, void* workspace,
+                                          size_t workspace_bytes, int batch, int seq_len, int num_householder,
+                                          int num_heads, int head_dim, int dtype) {
+  using namespace edf;
+  (void)forward_out;  // the raw output and its norm are recomputed from the inputs
+  int rc = check_dp(batch, seq_len, num_householder, num_heads, head_dim, dtype);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && beta && grad_out && grad_q && grad_k && grad_v && grad_beta, EDF_ERR_INVALID_ARG,
+              "null tensor pointer");
+  const DPWs w = dp_ws(batch, seq_len, num_householder, num_heads, head_dim, true);
+  EDF_REQUIRE(workspace && workspace_bytes >= w.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
+              w.total);
+  char* ws = (char*)workspace;
+  DPArgs a = dp_args(q, k, v, beta, seq_len, num_householder, num_heads, head_dim);
+  a.dout = grad_out;
+  a.dq = grad_q; a.dk = grad_k; a.dv = grad_v; a.dbeta = grad_beta;
+  a.part_o = (float*)(ws + w.part_o);
+  a.ckpt = (float*)(ws + w.ckpt);
+  a.dO = (float*)(ws + w.dO);
+  a.part_k = (float*)(ws + w.part_k);
+  a.part_b = (float*)(ws + w.part_b);
+  const int bh = batch * num_heads, nrb = dp_pad(head_dim) / DPR_RB;
+  const long nbth = (long)bh * seq_len, nbts = nbth * num_householder;
+  hipStream_t s = as_stream(stream);
+  const unsigned grows = (unsigned)((nbth + 3) / 4), gsub = (unsigned)((nbts + 3) / 4);
+  if (dtype == EDF_BF16) {
+    if ((rc = dp_launch<bf16>(s, a, false, bh))) return rc;
+    dp_finish_kernel<bf16><<<grows, 256, 0, s>>>(a, nbth, nrb, 1);
+    if ((rc = dp_launch<bf16>(s, a, true, bh))) return rc;
+    dp_reduce_kernel<bf16><<<gsub, 256, 0, s>>>(a, nbts, nrb);
+  } else {
+    if ((rc = dp_launch<float>(s, a, false, bh))) return rc;
+    dp_finish_kernel<float><<<grows, 256, 0, s>>>(a, nbth, nrb, 1);
+    if ((rc = dp_launch<float>(s, a, true, bh))) return rc;
+    dp_reduce_kernel<float><<<gsub, 256, 0, s>>>(a, nbts, nrb);
+  }
+  return check_launch("delta product backward reduction");
+}
+
+}  // extern "C"

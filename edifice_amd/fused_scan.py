@@ -483,6 +483,47 @@ def kda_scan(q, k, v, alpha, beta):
     return _KDA.apply(q, k, v, alpha, beta)
 
 
+class _DeltaProduct(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, beta):
+        q, k, v, beta = (t.contiguous() for t in (q, k, v, beta))
+        _dev(q, k, v, beta)
+        _same(q, k, v, beta)
+        bsz, seq, nh, hd = q.shape
+        if k.dim() != 5 or tuple(k.shape) != (bsz, seq, k.shape[2], nh, hd) or v.shape != k.shape \
+                or tuple(beta.shape) != (bsz, seq, k.shape[2], nh):
+            raise EdificeHipError("delta_product_scan needs q [B, T, H, d], k and v [B, T, n_h, H, d], "
+                                  "beta [B, T, n_h, H]")
+        nhh = k.shape[2]
+        out = torch.empty_like(q)
+        wsb = nat.query("edf_delta_product_workspace_bytes", bsz, seq, nhh, nh, hd, dtype_flag(q))
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_delta_product_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(ws), wsb,
+                 bsz, seq, nhh, nh, hd, dtype_flag(q))
+        ctx.save_for_backward(q, k, v, beta, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, beta, out = ctx.saved_tensors
+        do = do.contiguous().to(q.dtype)
+        bsz, seq, nh, hd = q.shape
+        nhh = k.shape[2]
+        dq, dk, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
+        wsb = nat.query("edf_delta_product_backward_workspace_bytes", bsz, seq, nhh, nh, hd, dtype_flag(q))
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_delta_product_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(do),
+                 _p(dq), _p(dk), _p(dv), _p(db), _p(ws), wsb, bsz, seq, nhh, nh, hd, dtype_flag(q))
+        return dq, dk, dv, db
+
+
+def delta_product_scan(q, k, v, beta):
+    """``FusedScan.delta_product_scan/4`` (fused_scan.ex:246-260): n_h delta-rule sub-steps per
+    token on L2-normalised keys, output RMS_norm of the state contracted with q over its
+    value rows; q [B, T, H, d], k and v [B, T, n_h, H, d], beta [B, T, n_h, H] (post-sigmoid)."""
+    return _DeltaProduct.apply(q, k, v, beta)
+
+
 def delta_net_scan(q, k, v, beta):
     """``FusedScan.delta_net_scan/4`` (fused_scan.ex:195-209): q, k, v [B, T, H, d]; k
     L2-normalised, beta post-sigmoid, per element [B, T, H, d] or per head [B, T, H]."""

@@ -215,6 +215,30 @@ int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, cons
                                 int dtype);
 size_t edf_kda_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
 
+/* DeltaProduct: n_h delta-rule sub-steps per token on L2-normalised keys, then the RMS-
+ * normalised contraction of the state with q over its value rows.  Replaces
+ * fused_delta_product_scan/10 (q [B,T,H,d], k, v [B,T,n_h,H,d], beta [B,T,n_h,H], batch,
+ * seq, n_h, heads, head_dim, dtype), lib/edifice/cuda/nif.ex:66 ->
+ * native/cuda/fused_delta_product_scan.cu (fallback delta_product.ex:287-347); head_dim
+ * <= 128; workspace edf_delta_product_workspace_bytes() bytes (row-block partial outputs). */
+int edf_fused_delta_product_scan(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                                 void* out, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                 int num_householder, int num_heads, int head_dim, int dtype);
+size_t edf_delta_product_workspace_bytes(int batch, int seq_len, int num_householder, int num_heads, int head_dim,
+                                         int dtype);
+
+/* Replaces fused_delta_product_scan_backward/12 (q, k, v, beta, fwd, grad, ...), nif.ex:193
+ * -> native/cuda/fused_delta_product_scan_backward.cu: dq [B,T,H,d], dk, dv [B,T,n_h,H,d],
+ * d beta [B,T,n_h,H]; workspace edf_delta_product_backward_workspace_bytes() bytes.  The
+ * reference kernel stops at seq 512 (MAX_SEQ_LEN); this one takes any length. */
+int edf_fused_delta_product_scan_backward(void* stream, const void* q, const void* k, const void* v,
+                                          const void* beta, const void* forward_out, const void* grad_out,
+                                          void* grad_q, void* grad_k, void* grad_v, void* grad_beta, void* workspace,
+                                          size_t workspace_bytes, int batch, int seq_len, int num_householder,
+                                          int num_heads, int head_dim, int dtype);
+size_t edf_delta_product_backward_workspace_bytes(int batch, int seq_len, int num_householder, int num_heads,
+                                                  int head_dim, int dtype);
+
 /* ------------------------------------------------------------------------
  * Flash attention   O = softmax(Q K^T / sqrt(d) [+ causal -inf]) V
  *   q, k, v, out, grads: [B, H, T, d] in dtype; lse: float32 [B, H, T] (natural log)

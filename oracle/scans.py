@@ -561,6 +561,95 @@ def kda_scan_backward(q, k, v, alpha, beta, do):
     return g
 
 
+DP_NORM_EPS = 1.0e-6  # fused_delta_product_scan.cu:38 (key L2 norm and output RMS norm)
+
+
+def _dp_states(k, v, beta, t, S):
+    """The n_h Householder sub-steps of token t from state S -> list of the n_h + 1 states
+    (S before each sub-step, then after the last)."""
+    kn = l2_normalize_keys(k[:, t])                     # [B, n_h, H, d]
+    out = [S]
+    for j in range(k.shape[2]):
+        r = np.einsum("bhij,bhj->bhi", S, kn[:, j])
+        err = beta[:, t, j][..., None] * (v[:, t, j] - r)
+        S = S + err[..., :, None] * kn[:, j][..., None, :]
+        out.append(S)
+    return out
+
+
+def delta_product(q, k, v, beta, return_raw=False):
+    """DeltaProduct: n_h delta-rule (generalized Householder) sub-steps per token,
+    then o_t = RMS_norm(contraction of S_t with q_t).
+
+    q [B,T,H,d]; k, v [B,T,n_h,H,d]; beta [B,T,n_h,H] (post-sigmoid, one gate per head
+    and sub-step).  Each sub-step normalizes its key, kn = k / sqrt(|k|^2 + 1e-6), and
+    applies S = S + beta (v - S kn) kn^T with S [H, d_v, d_k] as in ``delta_rule``.  The
+    reference keeps the transpose S_ref[key][value] and outputs S_ref q
+    (fused_delta_product_scan.cu:94-271 and 274-299; ``delta_product_scan_fallback``,
+    delta_product.ex:287-347), which here contracts the VALUE rows:
+    o_raw[j] = sum_i S[i][j] q[i]; out = o_raw / sqrt(mean(o_raw^2) + 1e-6).
+    """
+    q, k, v, beta = _f64(q, k, v, beta)
+    bsz, seq, nh, d = q.shape
+    S = np.zeros((bsz, nh, v.shape[-1], k.shape[-1]))
+    raw = np.empty((bsz, seq, nh, k.shape[-1]))
+    for t in range(seq):
+        S = _dp_states(k, v, beta, t, S)[-1]
+        raw[:, t] = np.einsum("bhij,bhi->bhj", S, q[:, t])
+    out = raw / np.sqrt((raw * raw).mean(axis=-1, keepdims=True) + DP_NORM_EPS)
+    return (out, raw) if return_raw else out
+
+
+def delta_product_backward(q, k, v, beta, do):
+    """Reverse pass -> dict(dq [B,T,H,d], dk, dv [B,T,n_h,H,d], dbeta [B,T,n_h,H]).
+
+    Per token t in reverse (structure of ``delta_product_backward_fallback``,
+    fused_scan.ex:1947-2090, and fused_delta_product_scan_backward.cu:165-361):
+      dO = do / r - o_raw (do . o_raw) / (d r^3)   (RMS norm; the fallback's o_raw / r^2
+      factor drops the 1/r that the CUDA kernel keeps, fused_delta_product_scan_backward.cu:188-202)
+      dq = S_t dO (contracts the key axis);  dS += q_t dO^T
+      per sub-step j in reverse (S_p the state before it): err = v - S_p kn, ds_k = dS kn,
+      dv = beta ds_k, dbeta = err . ds_k, dkn = dS^T (beta err) - S_p^T (beta ds_k),
+      dk = (dkn - kn (dkn . kn)) / sqrt(|k|^2 + 1e-6),  dS <- dS - beta ds_k kn^T.
+    """
+    q, k, v, beta, do = _f64(q, k, v, beta, do)
+    bsz, seq, nh, d = q.shape
+    nhh = k.shape[2]
+    S = np.zeros((bsz, nh, v.shape[-1], k.shape[-1]))
+    per_tok = []
+    for t in range(seq):
+        sts = _dp_states(k, v, beta, t, S)
+        per_tok.append(sts)
+        S = sts[-1]
+    dq = np.empty_like(q)
+    dk = np.empty_like(k)
+    dvv = np.empty_like(v)
+    dbeta = np.empty_like(beta)
+    dS = np.zeros_like(S)
+    for t in range(seq - 1, -1, -1):
+        sts = per_tok[t]
+        st_ = sts[-1]
+        raw = np.einsum("bhij,bhi->bhj", st_, q[:, t])
+        r = np.sqrt((raw * raw).mean(axis=-1, keepdims=True) + DP_NORM_EPS)
+        dO = do[:, t] / r - raw * (do[:, t] * raw).sum(axis=-1, keepdims=True) / (d * r ** 3)
+        dq[:, t] = np.einsum("bhij,bhj->bhi", st_, dO)
+        dS = dS + q[:, t][..., :, None] * dO[..., None, :]
+        kraw = k[:, t]
+        nrm = np.sqrt((kraw * kraw).sum(axis=-1, keepdims=True) + DP_NORM_EPS)
+        kn = kraw / nrm
+        for j in range(nhh - 1, -1, -1):
+            sp, bt, knj = sts[j], beta[:, t, j][..., None], kn[:, j]
+            err = v[:, t, j] - np.einsum("bhij,bhj->bhi", sp, knj)
+            ds_k = np.einsum("bhij,bhj->bhi", dS, knj)
+            dvv[:, t, j] = bt * ds_k
+            dbeta[:, t, j] = (err * ds_k).sum(axis=-1)
+            dkn = (np.einsum("bhij,bhi->bhj", dS, bt * err)
+                   - np.einsum("bhij,bhi->bhj", sp, bt * ds_k))
+            dk[:, t, j] = (dkn - knj * (dkn * knj).sum(axis=-1, keepdims=True)) / nrm[:, j]
+            dS = dS - (bt * ds_k)[..., :, None] * knj[..., None, :]
+    return dict(dq=dq, dk=dk, dv=dvv, dbeta=dbeta)
+
+
 # ---------------------------------------------------------------------------
 # Flash attention
 # ---------------------------------------------------------------------------

@@ -101,3 +101,37 @@ def test_kda_fwd_bwd(shape, dtype, rng):
     for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb)):
         assert_close(host(tt.grad), g[n], tol, n)
 
+
+
+DP_CASES = [
+    # (B, T, n_h, H, d, dtype)
+    (1, 2, 2, 2, 2, torch.float32),       # reference backward test sizes (head_dim 2)
+    (2, 9, 2, 2, 16, torch.float32),
+    (1, 37, 3, 2, 64, torch.float32),     # sub-steps not a multiple of the 16-step chunk
+    (1, 20, 1, 1, 128, torch.float32),    # n_h = 1
+    (2, 33, 2, 2, 50, torch.float32),     # head_dim off the padded widths
+    (1, 70, 4, 1, 32, torch.bfloat16),
+    (1, 40, 2, 2, 128, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", DP_CASES)
+def test_delta_product_fwd_bwd(case, rng):
+    """FusedScan.delta_product_scan/4 and its backward against the oracle (raw keys, the
+    kernel normalizes; beta up to 2 as with allow_neg_eigval)."""
+    from edifice_amd import fused_scan as fs
+    bsz, t, nhh, h, d, dtype = case
+    announce("delta_product", case=case)
+    q = rng.normal(size=(bsz, t, h, d))
+    k, v = rng.normal(size=(bsz, t, nhh, h, d)), rng.normal(size=(bsz, t, nhh, h, d))
+    beta = rng.uniform(0.1, 1.9, size=(bsz, t, nhh, h))
+    do = rng.normal(size=(bsz, t, h, d))
+    tq, tk, tv, tb = (to_dev(a, dtype).requires_grad_() for a in (q, k, v, beta))
+    out = fs.delta_product_scan(tq, tk, tv, tb)
+    out.backward(to_dev(do, dtype))
+    qr, kr, vr, br, dor = (rounded(a, dtype) for a in (q, k, v, beta, do))
+    tol = TOL[dtype]
+    assert_close(host(out), scans.delta_product(qr, kr, vr, br), tol, "o")
+    g = scans.delta_product_backward(qr, kr, vr, br, dor)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb)):
+        assert_close(host(tt.grad), g[n], tol, n)

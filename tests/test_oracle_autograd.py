@@ -289,3 +289,30 @@ def test_kda_backward_vs_autograd(rng):
     for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb)):
         assert_close(g[n], tt.grad.numpy(), 1e-10, n)
 
+
+
+def test_delta_product_backward_vs_autograd(rng):
+    """DeltaProduct backward (oracle) against torch autograd of the reference-convention
+    forward (state [key][value], matrix Householder form, RMS-normalized S q)."""
+    bsz, t, nhh, h, d = 1, 4, 2, 2, 3
+    q, do = rng.normal(size=(bsz, t, h, d)), rng.normal(size=(bsz, t, h, d))
+    k, v = rng.normal(size=(bsz, t, nhh, h, d)), rng.normal(size=(bsz, t, nhh, h, d))
+    beta = rng.uniform(0.1, 1.9, size=(bsz, t, nhh, h))
+    tq, tk, tv, tb = _t(q), _t(k), _t(v), _t(beta)
+    S = torch.zeros(bsz, h, d, d, dtype=F64)
+    eye = torch.eye(d, dtype=F64)
+    outs = []
+    for s in range(t):
+        for j in range(nhh):
+            kv = tk[:, s, j]
+            kn = kv / torch.sqrt((kv * kv).sum(-1, keepdim=True) + 1e-6)
+            be = tb[:, s, j][..., None, None]
+            S = (eye - be * kn[..., :, None] * kn[..., None, :]) @ S + be * kn[..., :, None] * tv[:, s, j][..., None, :]
+        o = (S @ tq[:, s][..., None])[..., 0]
+        outs.append(o / torch.sqrt((o * o).mean(-1, keepdim=True) + 1e-6))
+    out = torch.stack(outs, 1)
+    out.backward(torch.from_numpy(do))
+    assert_close(scans.delta_product(q, k, v, beta), out.detach().numpy(), 1e-12, "o")
+    g = scans.delta_product_backward(q, k, v, beta, do)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb)):
+        assert_close(g[n], tt.grad.numpy(), 1e-10, n)

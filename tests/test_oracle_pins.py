@@ -352,3 +352,63 @@ def test_kda_reduces_to_deltanet_and_gated(rng):
     np.testing.assert_allclose(scans.kda_scan(q, k, v, np.broadcast_to(c[..., None], (bsz, t, h, d)), beta),
                                scans.delta_rule(q, k, v, beta, np.exp(c)), rtol=1e-12)
 
+
+
+def _dp_reference_form(q, k, v, beta):
+    """DeltaProduct written literally as the reference states it, in its own [key][value]
+    state: S = (I - beta kn kn^T) S + beta kn v^T per sub-step, o = RMS_norm(S q)."""
+    bsz, t, nhh, h, d = k.shape
+    out = np.empty(q.shape)
+    for b in range(bsz):
+        for hh in range(h):
+            S = np.zeros((d, d))
+            for s in range(t):
+                for j in range(nhh):
+                    kv = k[b, s, j, hh]
+                    kn = kv / np.sqrt(kv @ kv + 1e-6)
+                    be = beta[b, s, j, hh]
+                    S = (np.eye(d) - be * np.outer(kn, kn)) @ S + be * np.outer(kn, v[b, s, j, hh])
+                o = S @ q[b, s, hh]
+                out[b, s, hh] = o / np.sqrt(np.mean(o * o) + 1e-6)
+    return out
+
+
+def test_delta_product_matches_reference_matrix_form(rng):
+    """The oracle's row-wise update in the [value][key] state against the reference's own
+    matrix statement (fused_delta_product_scan.cu:1-13, delta_product.ex:333-343)."""
+    bsz, t, nhh, h, d = 2, 5, 3, 2, 4
+    q = rng.normal(size=(bsz, t, h, d))
+    k, v = (rng.normal(size=(bsz, t, nhh, h, d)) for _ in range(2))
+    beta = rng.uniform(0.1, 1.9, size=(bsz, t, nhh, h))
+    np.testing.assert_allclose(scans.delta_product(q, k, v, beta), _dp_reference_form(q, k, v, beta),
+                               rtol=1e-11, atol=1e-12)
+
+
+def test_delta_product_one_step_closed_form(rng):
+    """One token, one sub-step from S = 0: S_ref = beta kn v^T, so S_ref q = beta (v . q) kn
+    and out = c kn / sqrt(c^2 mean(kn^2) + 1e-6) with c = beta (v . q): the output follows
+    the KEY, which a contraction over the wrong state axis would not give."""
+    d = 6
+    q, k, v = rng.normal(size=(1, 1, 1, d)), rng.normal(size=(1, 1, 1, 1, d)), rng.normal(size=(1, 1, 1, 1, d))
+    beta = np.full((1, 1, 1, 1), 0.7)
+    kn = k[0, 0, 0, 0] / np.sqrt(k[0, 0, 0, 0] @ k[0, 0, 0, 0] + 1e-6)
+    c = 0.7 * (v[0, 0, 0, 0] @ q[0, 0, 0])
+    np.testing.assert_allclose(scans.delta_product(q, k, v, beta)[0, 0, 0],
+                               c * kn / np.sqrt(c * c * np.mean(kn * kn) + 1e-6), rtol=1e-12)
+
+
+def test_delta_product_reduces_to_delta_rule(rng):
+    """n_h = 1 runs the delta rule's states (normalized keys, per-head beta); a second
+    sub-step with beta = 0 is the identity."""
+    bsz, t, h, d = 1, 6, 2, 4
+    q = rng.normal(size=(bsz, t, h, d))
+    k, v = rng.normal(size=(bsz, t, 1, h, d)), rng.normal(size=(bsz, t, 1, h, d))
+    beta = rng.uniform(0.1, 0.9, size=(bsz, t, 1, h))
+    _, states = scans.delta_rule(q, scans.l2_normalize_keys(k[:, :, 0]), v[:, :, 0], beta[:, :, 0],
+                                 return_states=True)
+    raw = np.einsum("bthij,bthi->bthj", states, q)
+    np.testing.assert_allclose(scans.delta_product(q, k, v, beta, return_raw=True)[1], raw, rtol=1e-12)
+    k2 = np.concatenate([k, rng.normal(size=k.shape)], axis=2)
+    v2 = np.concatenate([v, rng.normal(size=v.shape)], axis=2)
+    b2 = np.concatenate([beta, np.zeros_like(beta)], axis=2)
+    np.testing.assert_allclose(scans.delta_product(q, k2, v2, b2), scans.delta_product(q, k, v, beta), rtol=1e-12)
