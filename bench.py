@@ -424,6 +424,39 @@ def bench_delta_product(torch, steps, warmup, B=8, T=2048, NH=2, H=8, d=128):
                 shape=dict(B=B, T=T, n_h=NH, H=H, d=d))
 
 
+def bench_rla(torch, steps, warmup, variant, B=8, T=2048, H=8, d=128):
+    """RLA (variant 0) / RDN (variant 1), bf16, clip 1.0: fwd and bwd time per call and
+    tokens/s (B T per call)."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(3003)
+    dev, bf = "cuda", torch.bfloat16
+    l2n = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)  # noqa: E731
+    q = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    k = l2n(torch.randn(B, T, H, d, device=dev, generator=g)).to(bf)
+    v = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    alpha, beta, gamma = ((0.3 + 0.65 * torch.rand(B, T, H, device=dev, generator=g)).to(bf) for _ in range(3))
+    do = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
+    out, dq, dk, dv = (torch.empty_like(q) for _ in range(4))
+    da, db, dg = (torch.empty_like(alpha) for _ in range(3))
+    wsb = nat.query("edf_rla_scan_backward_workspace_bytes", B, T, H, d, 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_rla_scan", stream, P(q), P(k), P(v), P(alpha), P(beta), P(gamma), P(out),
+                 B, T, H, d, variant, 1.0, 1)
+
+    def bwd():
+        nat.call("edf_fused_rla_scan_backward", stream, P(q), P(k), P(v), P(alpha), P(beta), P(gamma), P(out),
+                 P(do), P(dq), P(dk), P(dv), P(da), P(db), P(dg), P(ws), wsb, B, T, H, d, variant, 1.0, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,
+                shape=dict(B=B, T=T, H=H, d=d))
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
@@ -526,6 +559,8 @@ def main():
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
         configs["kda_8x2048x8x128"] = bench_kda(torch, args.steps, args.warmup)
         configs["delta_product_8x2048x2x8x128"] = bench_delta_product(torch, args.steps, args.warmup)
+        configs["rla_8x2048x8x128"] = bench_rla(torch, args.steps, args.warmup, 0)
+        configs["rdn_8x2048x8x128"] = bench_rla(torch, args.steps, args.warmup, 1)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
         configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,

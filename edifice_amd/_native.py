@@ -13,6 +13,7 @@ from .build import lib_path
 P = ctypes.c_void_p
 I = ctypes.c_int
 S = ctypes.c_size_t
+F = ctypes.c_float
 
 # name -> (restype, argtypes); must match include/edifice_hip.h
 SIGNATURES = {
@@ -64,6 +65,10 @@ SIGNATURES = {
     "edf_delta_product_workspace_bytes": (S, [I, I, I, I, I, I]),
     "edf_fused_delta_product_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_delta_product_backward_workspace_bytes": (S, [I, I, I, I, I, I]),
+    "edf_fused_rla_scan": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, F, I]),
+    "edf_fused_rla_scan_backward": (
+        I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, F, I]),
+    "edf_rla_scan_backward_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_debug_mfma_32x32x16_bf16": (I, [P, P, P, P]),
     "edf_debug_acc_kfrag_bf16": (I, [P, P, P]),
     "edf_debug_lds_read_tr16": (I, [P, P, P]),

@@ -524,6 +524,45 @@ def delta_product_scan(q, k, v, beta):
     return _DeltaProduct.apply(q, k, v, beta)
 
 
+class _RLA(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, alpha, beta, gamma, variant, clip):
+        q, k, v, alpha, beta, gamma = (t.contiguous() for t in (q, k, v, alpha, beta, gamma))
+        _dev(q, k, v, alpha, beta, gamma)
+        _same(q, k, v, alpha, beta, gamma)
+        bsz, seq, nh, hd = q.shape
+        if k.shape != q.shape or v.shape != q.shape or any(tuple(g.shape) != (bsz, seq, nh) for g in (alpha, beta, gamma)):
+            raise EdificeHipError("rla_scan needs q, k, v [B, T, H, d] and alpha, beta, gamma [B, T, H]")
+        out = torch.empty_like(q)
+        nat.call("edf_fused_rla_scan", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(gamma), _p(out),
+                 bsz, seq, nh, hd, variant, float(clip), dtype_flag(q))
+        ctx.save_for_backward(q, k, v, alpha, beta, gamma, out)
+        ctx.variant, ctx.clip = variant, float(clip)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, alpha, beta, gamma, out = ctx.saved_tensors
+        do = do.contiguous().to(q.dtype)
+        bsz, seq, nh, hd = q.shape
+        dq, dk, dv, da, db, dg = (torch.empty_like(t) for t in (q, k, v, alpha, beta, gamma))
+        wsb = nat.query("edf_rla_scan_backward_workspace_bytes", bsz, seq, nh, hd, dtype_flag(q))
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_rla_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(gamma),
+                 _p(out), _p(do), _p(dq), _p(dk), _p(dv), _p(da), _p(db), _p(dg), _p(ws), wsb, bsz, seq, nh, hd,
+                 ctx.variant, ctx.clip, dtype_flag(q))
+        return dq, dk, dv, da, db, dg, None, None
+
+
+def rla_scan(q, k, v, alpha, beta, gamma, variant="rla", clip_threshold=1.0):
+    """``FusedScan.rla_scan/7`` (fused_scan.ex:431-448): residual linear attention with base
+    state S and residual state R; q, k, v [B, T, H, d], alpha, beta, gamma [B, T, H];
+    variant "rla" (S += b v k^T) or "rdn" (delta-rule updates of both states); the residual
+    error is clipped to [-clip_threshold, clip_threshold]."""
+    var = {"rla": 0, "rdn": 1}[variant]
+    return _RLA.apply(q, k, v, alpha, beta, gamma, var, clip_threshold)
+
+
 def delta_net_scan(q, k, v, beta):
     """``FusedScan.delta_net_scan/4`` (fused_scan.ex:195-209): q, k, v [B, T, H, d]; k
     L2-normalised, beta post-sigmoid, per element [B, T, H, d] or per head [B, T, H]."""

@@ -239,6 +239,28 @@ int edf_fused_delta_product_scan_backward(void* stream, const void* q, const voi
 size_t edf_delta_product_backward_workspace_bytes(int batch, int seq_len, int num_householder, int num_heads,
                                                   int head_dim, int dtype);
 
+/* RLA / RDN (residual linear attention): base state S and residual state R, per-head
+ * alpha, beta, gamma [B,T,H]; variant 0 = RLA, 1 = RDN; clip_threshold >= 0 bounds the
+ * residual error.  Replaces fused_rla_scan/13 (q, k, v, alpha, beta, gamma, batch, seq,
+ * heads, head_dim, variant, clip, dtype), lib/edifice/cuda/nif.ex:94 ->
+ * native/cuda/fused_rla_scan.cu (fallback fused_scan.ex:2692-2768); head_dim <= 128; no
+ * workspace for the forward. */
+int edf_fused_rla_scan(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                       const void* beta, const void* gamma, void* out, int batch, int seq_len, int num_heads,
+                       int head_dim, int variant, float clip_threshold, int dtype);
+
+/* Replaces fused_rla_scan_backward/15 (q, k, v, alpha, beta, gamma, fwd, grad, ...),
+ * nif.ex:210 -> native/cuda/fused_rla_scan_backward.cu: dq, dk, dv [B,T,H,d], d alpha,
+ * d beta, d gamma [B,T,H]; workspace edf_rla_scan_backward_workspace_bytes() bytes.  The
+ * reference kernel keeps per-step history in fixed arrays (MAX_SEQ_LEN); this one takes
+ * any length. */
+int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                const void* beta, const void* gamma, const void* forward_out, const void* grad_out,
+                                void* grad_q, void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta,
+                                void* grad_gamma, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                int num_heads, int head_dim, int variant, float clip_threshold, int dtype);
+size_t edf_rla_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
+
 /* ------------------------------------------------------------------------
  * Flash attention   O = softmax(Q K^T / sqrt(d) [+ causal -inf]) V
  *   q, k, v, out, grads: [B, H, T, d] in dtype; lse: float32 [B, H, T] (natural log)

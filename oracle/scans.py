@@ -561,6 +561,95 @@ def kda_scan_backward(q, k, v, alpha, beta, do):
     return g
 
 
+RLA_VARIANTS = {"rla": 0, "rdn": 1}  # fused_scan.ex:425-433
+
+
+def _rla_step(S, R, kt, vt, a, b, g, variant, clip):
+    """One RLA / RDN step from (S, R) -> (S_t, R_t, e, re, rr) (fused_rla_scan.cu:114-165,
+    ``rla_scan_fallback`` fused_scan.ex:2692-2768).  a, b, g broadcast as [B, H, 1]."""
+    rs = np.einsum("bhij,bhj->bhi", S, kt)
+    e = vt - rs
+    re = np.clip(e, -clip, clip)
+    if variant == 0:   # RLA: S = a S + b v k^T, R = a R + g re k^T
+        rr = None
+        cs, cr = b * vt, g * re
+    else:              # RDN: S = a S + b (v - S k) k^T, R = a R + g (re - R k) k^T
+        rr = np.einsum("bhij,bhj->bhi", R, kt)
+        cs, cr = b * e, g * (re - rr)
+    S_t = a[..., None] * S + cs[..., :, None] * kt[..., None, :]
+    R_t = a[..., None] * R + cr[..., :, None] * kt[..., None, :]
+    return S_t, R_t, e, re, rr
+
+
+def rla_scan(q, k, v, alpha, beta, gamma, variant=0, clip=1.0):
+    """Residual linear attention: base state S and residual state R [H, d_v, d_k],
+    retrieval S_{t-1} k_t, residual error re = clip(v - S_{t-1} k_t, -c, c),
+    o_t = (S_t + R_t) q_t.  variant 0 (RLA) / 1 (RDN); alpha, beta, gamma per head [B,T,H]."""
+    q, k, v, alpha, beta, gamma = _f64(q, k, v, alpha, beta, gamma)
+    bsz, seq, nh, d = q.shape
+    S = np.zeros((bsz, nh, d, d))
+    R = np.zeros((bsz, nh, d, d))
+    out = np.empty_like(q)
+    for t in range(seq):
+        S, R, *_ = _rla_step(S, R, k[:, t], v[:, t], alpha[:, t, :, None], beta[:, t, :, None],
+                             gamma[:, t, :, None], variant, clip)
+        out[:, t] = np.einsum("bhij,bhj->bhi", S + R, q[:, t])
+    return out
+
+
+def rla_scan_backward(q, k, v, alpha, beta, gamma, do, variant=0, clip=1.0):
+    """Reverse pass -> dict(dq, dk, dv, dalpha, dbeta, dgamma) (the per-head gate gradients
+    [B,T,H]); structure of ``rla_backward_fallback`` (fused_scan.ex:1675-1812) and
+    fused_rla_scan_backward.cu:62-618, the clip passing gradient where |e| <= c
+    (fused_rla_scan_backward.cu:163).  Per step (S_p, R_p before it):
+      dS_tot = dS + do q^T, dR_tot = dR + do q^T, dq = (S_t + R_t)^T do,
+      ds_k = dS_tot k, dr_k = dR_tot k, m = [|e| <= c]; with cS, cR the row coefficients of
+      k^T in the two updates, dE_S = g dr_k m (RLA) or b ds_k + g dr_k m (RDN) and
+      dE_R = 0 (RLA) or g dr_k (RDN):
+      dv = b ds_k + g dr_k m,  dk = dS_tot^T cS + dR_tot^T cR - S_p^T dE_S - R_p^T dE_R,
+      dalpha = <dS_tot, S_p> + <dR_tot, R_p>, dbeta = ds_k . (v or e), dgamma = dr_k . cR / g,
+      dS <- a dS_tot - dE_S k^T, dR <- a dR_tot - dE_R k^T."""
+    q, k, v, alpha, beta, gamma, do = _f64(q, k, v, alpha, beta, gamma, do)
+    bsz, seq, nh, d = q.shape
+    S = np.zeros((bsz, nh, d, d))
+    R = np.zeros((bsz, nh, d, d))
+    hist = []
+    for t in range(seq):
+        hist.append((S, R))
+        S, R, *_ = _rla_step(S, R, k[:, t], v[:, t], alpha[:, t, :, None], beta[:, t, :, None],
+                             gamma[:, t, :, None], variant, clip)
+    g_ = {n: np.empty_like(x) for n, x in (("dq", q), ("dk", k), ("dv", v), ("dalpha", alpha),
+                                            ("dbeta", beta), ("dgamma", gamma))}
+    dS = np.zeros_like(S)
+    dR = np.zeros_like(R)
+    for t in range(seq - 1, -1, -1):
+        sp, rp = hist[t]
+        a, b, g = alpha[:, t, :, None], beta[:, t, :, None], gamma[:, t, :, None]
+        kt, vt, qt, dot = k[:, t], v[:, t], q[:, t], do[:, t]
+        s_t, r_t, e, re, rr = _rla_step(sp, rp, kt, vt, a, b, g, variant, clip)
+        m = (np.abs(e) <= clip).astype(np.float64)
+        outer = dot[..., :, None] * qt[..., None, :]
+        dst, drt = dS + outer, dR + outer
+        g_["dq"][:, t] = np.einsum("bhij,bhi->bhj", s_t + r_t, dot)
+        ds_k = np.einsum("bhij,bhj->bhi", dst, kt)
+        dr_k = np.einsum("bhij,bhj->bhi", drt, kt)
+        if variant == 0:
+            cs, cr, cb, cg = b * vt, g * re, vt, re
+            des, der = g * dr_k * m, np.zeros_like(dr_k)
+        else:
+            cs, cr, cb, cg = b * e, g * (re - rr), e, re - rr
+            des, der = b * ds_k + g * dr_k * m, g * dr_k
+        g_["dv"][:, t] = b * ds_k + g * dr_k * m
+        g_["dk"][:, t] = (np.einsum("bhij,bhi->bhj", dst, cs) + np.einsum("bhij,bhi->bhj", drt, cr)
+                          - np.einsum("bhij,bhi->bhj", sp, des) - np.einsum("bhij,bhi->bhj", rp, der))
+        g_["dalpha"][:, t] = (dst * sp).sum(axis=(2, 3)) + (drt * rp).sum(axis=(2, 3))
+        g_["dbeta"][:, t] = (ds_k * cb).sum(axis=-1)
+        g_["dgamma"][:, t] = (dr_k * cg).sum(axis=-1)
+        dS = a[..., None] * dst - des[..., :, None] * kt[..., None, :]
+        dR = a[..., None] * drt - der[..., :, None] * kt[..., None, :]
+    return g_
+
+
 DP_NORM_EPS = 1.0e-6  # fused_delta_product_scan.cu:38 (key L2 norm and output RMS norm)
 
 

@@ -135,3 +135,39 @@ def test_delta_product_fwd_bwd(case, rng):
     g = scans.delta_product_backward(qr, kr, vr, br, dor)
     for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb)):
         assert_close(host(tt.grad), g[n], tol, n)
+
+
+RLA_CASES = [
+    # (B, T, H, d, dtype, variant, clip)
+    (1, 5, 2, 3, torch.float32, "rla", 0.6),
+    (2, 21, 2, 16, torch.float32, "rdn", 0.6),
+    (1, 37, 2, 64, torch.float32, "rla", 1.0),    # T not a multiple of the 8-step chunk
+    (1, 30, 1, 128, torch.float32, "rdn", 1.0),
+    (2, 17, 2, 50, torch.float32, "rla", 0.3),    # head_dim off the padded widths
+    (1, 40, 2, 64, torch.bfloat16, "rdn", 1.0),
+    (1, 33, 1, 128, torch.bfloat16, "rla", 1.0),
+]
+
+
+@pytest.mark.parametrize("case", RLA_CASES)
+def test_rla_fwd_bwd(case, rng):
+    """FusedScan.rla_scan/7 (RLA and RDN) and its backward against the oracle; keys scaled
+    so that the retrievals stay O(1) and part of the residual errors clip."""
+    from edifice_amd import fused_scan as fs
+    bsz, t, h, d, dtype, variant, clip = case
+    announce("rla", case=case)
+    q = rng.normal(size=(bsz, t, h, d))
+    k = scans.l2_normalize_keys(rng.normal(size=(bsz, t, h, d)))
+    v = rng.normal(size=(bsz, t, h, d))
+    alpha, beta, gamma = (rng.uniform(0.3, 0.95, size=(bsz, t, h)) for _ in range(3))
+    do = rng.normal(size=(bsz, t, h, d))
+    tq, tk, tv, ta, tb, tg = (to_dev(x, dtype).requires_grad_() for x in (q, k, v, alpha, beta, gamma))
+    out = fs.rla_scan(tq, tk, tv, ta, tb, tg, variant, clip)
+    out.backward(to_dev(do, dtype))
+    xs = [rounded(x, dtype) for x in (q, k, v, alpha, beta, gamma)]
+    var = scans.RLA_VARIANTS[variant]
+    tol = TOL[dtype]
+    assert_close(host(out), scans.rla_scan(*xs, var, clip), tol, "o")
+    g = scans.rla_scan_backward(*xs, rounded(do, dtype), var, clip)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb), ("dgamma", tg)):
+        assert_close(host(tt.grad), g[n], tol, n)

@@ -316,3 +316,39 @@ def test_delta_product_backward_vs_autograd(rng):
     g = scans.delta_product_backward(q, k, v, beta, do)
     for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb)):
         assert_close(g[n], tt.grad.numpy(), 1e-10, n)
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_rla_backward_vs_autograd(rng, variant):
+    """RLA / RDN backward (oracle) against torch autograd of an independent forward written
+    from the reference's matrix statement (fused_rla_scan.cu:1-20); the threshold 0.6
+    clips part of the errors."""
+    bsz, t, h, d = 1, 5, 2, 3
+    q, k, v, do = (rng.normal(size=(bsz, t, h, d)) for _ in range(4))
+    alpha, beta, gamma = (rng.uniform(0.3, 0.95, size=(bsz, t, h)) for _ in range(3))
+    tq, tk, tv, ta, tb, tg = _t(q), _t(k), _t(v), _t(alpha), _t(beta), _t(gamma)
+    S = torch.zeros(bsz, h, d, d, dtype=F64)
+    R = torch.zeros(bsz, h, d, d, dtype=F64)
+    outs, clipped = [], 0
+    for s in range(t):
+        kk, vv = tk[:, s], tv[:, s]
+        a, b, g = (x[:, s][..., None, None] for x in (ta, tb, tg))
+        err = vv - (S @ kk[..., None])[..., 0]
+        clipped += int((err.abs() > 0.6).sum())
+        re = torch.clamp(err, -0.6, 0.6)
+        if variant == 0:
+            S2 = a * S + b * vv[..., :, None] * kk[..., None, :]
+            R2 = a * R + g * re[..., :, None] * kk[..., None, :]
+        else:
+            rr = (R @ kk[..., None])[..., 0]
+            S2 = a * S + b * err[..., :, None] * kk[..., None, :]
+            R2 = a * R + g * (re - rr)[..., :, None] * kk[..., None, :]
+        S, R = S2, R2
+        outs.append(((S + R) @ tq[:, s][..., None])[..., 0])
+    assert clipped > 0
+    out = torch.stack(outs, 1)
+    out.backward(torch.from_numpy(do))
+    assert_close(scans.rla_scan(q, k, v, alpha, beta, gamma, variant, 0.6), out.detach().numpy(), 1e-12, "o")
+    gr = scans.rla_scan_backward(q, k, v, alpha, beta, gamma, do, variant, 0.6)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb), ("dgamma", tg)):
+        assert_close(gr[n], tt.grad.numpy(), 1e-10, n)

@@ -412,3 +412,39 @@ def test_delta_product_reduces_to_delta_rule(rng):
     v2 = np.concatenate([v, rng.normal(size=v.shape)], axis=2)
     b2 = np.concatenate([beta, np.zeros_like(beta)], axis=2)
     np.testing.assert_allclose(scans.delta_product(q, k2, v2, b2), scans.delta_product(q, k, v, beta), rtol=1e-12)
+
+
+def _rla_inputs(rng, bsz=1, t=6, h=2, d=4):
+    q, k, v = (rng.normal(size=(bsz, t, h, d)) for _ in range(3))
+    alpha, beta, gamma = (rng.uniform(0.3, 0.95, size=(bsz, t, h)) for _ in range(3))
+    return q, k, v, alpha, beta, gamma
+
+
+def test_rla_without_residual_is_decayed_linear_attention(rng):
+    """RLA with gamma = 0 is S_t = a_t S + b_t v_t k_t^T, so
+    o_t = sum_{s<=t} (prod_{u=s+1..t} a_u) b_s (k_s . q_t) v_s."""
+    q, k, v, alpha, beta, _ = _rla_inputs(rng)
+    bsz, t, h, d = q.shape
+    want = np.zeros_like(q)
+    for tt in range(t):
+        for s in range(tt + 1):
+            w = np.prod(alpha[:, s + 1:tt + 1], axis=1) * beta[:, s] * (k[:, s] * q[:, tt]).sum(-1)
+            want[:, tt] += w[..., None] * v[:, s]
+    np.testing.assert_allclose(scans.rla_scan(q, k, v, alpha, beta, np.zeros_like(beta), 0), want, rtol=1e-12)
+
+
+def test_rdn_reduces_to_delta_rule(rng):
+    """RDN with alpha = 1 and gamma = 0 is DeltaNet with a per-head beta."""
+    q, k, v, _, beta, _ = _rla_inputs(rng)
+    np.testing.assert_allclose(scans.rla_scan(q, k, v, np.ones_like(beta), beta, np.zeros_like(beta), 1),
+                               scans.delta_rule(q, k, v, beta), rtol=1e-12)
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_rla_zero_clip_keeps_residual_empty(rng, variant):
+    """clip threshold 0: the residual error is 0, R stays 0 and the output is the gamma = 0
+    one; a huge threshold differs from it (the residual state is live)."""
+    q, k, v, alpha, beta, gamma = _rla_inputs(rng)
+    base = scans.rla_scan(q, k, v, alpha, beta, np.zeros_like(gamma), variant)
+    np.testing.assert_allclose(scans.rla_scan(q, k, v, alpha, beta, gamma, variant, clip=0.0), base, rtol=1e-12)
+    assert np.abs(scans.rla_scan(q, k, v, alpha, beta, gamma, variant, clip=1e9) - base).max() > 1e-3
