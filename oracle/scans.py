@@ -34,6 +34,12 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 GatedDeltaNet, torch autograd of an independent forward.
   delta_rule_backward           delta_net_random.safetensors gradient.input, torch
                                 autograd of the forward, finite differences.
+  delta_product / _backward     the reference's literal [key][value] matrix form, one-step
+                                closed form (output follows the key), n_h = 1 ==> the delta
+                                rule's states, beta = 0 sub-step ==> identity, torch autograd.
+  rla_scan / _backward          gamma = 0 RLA ==> decayed linear attention closed form, RDN
+                                with alpha = 1, gamma = 0 ==> DeltaNet, clip 0 ==> empty
+                                residual state, torch autograd (with clipped errors).
   laser_attention / _backward   identical value rows ==> O = that row; torch autograd of an
                                 independent torch forward (vmax held constant).
   fox_attention / _backward     cs = const ==> causal flash_attention; torch autograd of an
