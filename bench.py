@@ -457,6 +457,40 @@ def bench_rla(torch, steps, warmup, variant, B=8, T=2048, H=8, d=128):
                 shape=dict(B=B, T=T, H=H, d=d))
 
 
+def bench_ttt(torch, steps, warmup, B=8, T=2048, D=64):
+    """TTT-Linear (inner model D x D per batch element), bf16: fwd and bwd time per call and
+    tokens/s (B T per call).  One workgroup per batch element: the LayerNorm couples all rows
+    of W at every step."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(3004)
+    dev, bf = "cuda", torch.bfloat16
+    q = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    k = (torch.randn(B, T, D, device=dev, generator=g) / D ** 0.5).to(bf)
+    v = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    eta = (torch.sigmoid(torch.randn(B, T, D, device=dev, generator=g)) / D).to(bf)
+    w0 = (torch.randn(B, D, D, device=dev, generator=g) / D ** 0.5).to(bf)
+    lg, lb = torch.ones(D, device=dev, dtype=bf), torch.zeros(D, device=dev, dtype=bf)
+    do = torch.randn(B, T, D, device=dev, generator=g).to(bf)
+    out = torch.empty_like(q)
+    grads = [torch.empty_like(t) for t in (q, k, v, eta, w0, lg, lb)]
+    wsb = nat.query("edf_ttt_scan_backward_workspace_bytes", B, T, D, 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def fwd():
+        nat.call("edf_fused_ttt_scan", stream, P(q), P(k), P(v), P(eta), P(w0), P(lg), P(lb), P(out), B, T, D, 1)
+
+    def bwd():
+        nat.call("edf_fused_ttt_scan_backward", stream, P(q), P(k), P(v), P(eta), P(w0), P(lg), P(lb), P(do),
+                 *(P(t) for t in grads), P(ws), wsb, B, T, D, 1)
+
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,
+                shape=dict(B=B, T=T, D=D))
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
@@ -561,6 +595,7 @@ def main():
         configs["delta_product_8x2048x2x8x128"] = bench_delta_product(torch, args.steps, args.warmup)
         configs["rla_8x2048x8x128"] = bench_rla(torch, args.steps, args.warmup, 0)
         configs["rdn_8x2048x8x128"] = bench_rla(torch, args.steps, args.warmup, 1)
+        configs["ttt_8x2048x64"] = bench_ttt(torch, args.steps, args.warmup)
     if want("flash"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
         configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,

@@ -563,6 +563,42 @@ def rla_scan(q, k, v, alpha, beta, gamma, variant="rla", clip_threshold=1.0):
     return _RLA.apply(q, k, v, alpha, beta, gamma, var, clip_threshold)
 
 
+class _TTT(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, eta, w0, ln_g, ln_b):
+        q, k, v, eta, w0, ln_g, ln_b = (t.contiguous() for t in (q, k, v, eta, w0, ln_g, ln_b))
+        _dev(q, k, v, eta, w0, ln_g, ln_b)
+        _same(q, k, v, eta, w0, ln_g, ln_b)
+        bsz, seq, dd = q.shape
+        if any(t.shape != q.shape for t in (k, v, eta)) or tuple(w0.shape) != (bsz, dd, dd) \
+                or tuple(ln_g.shape) != (dd,) or tuple(ln_b.shape) != (dd,):
+            raise EdificeHipError("ttt_scan needs q, k, v, eta [B, T, D], w0 [B, D, D], ln_gamma, ln_beta [D]")
+        out = torch.empty_like(q)
+        nat.call("edf_fused_ttt_scan", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g), _p(ln_b), _p(out),
+                 bsz, seq, dd, dtype_flag(q))
+        ctx.save_for_backward(q, k, v, eta, w0, ln_g, ln_b)
+        return out
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, eta, w0, ln_g, ln_b = ctx.saved_tensors
+        do = do.contiguous().to(q.dtype)
+        bsz, seq, dd = q.shape
+        grads = [torch.empty_like(t) for t in (q, k, v, eta, w0, ln_g, ln_b)]
+        wsb = nat.query("edf_ttt_scan_backward_workspace_bytes", bsz, seq, dd, dtype_flag(q))
+        ws = _u8(wsb, q)
+        nat.call("edf_fused_ttt_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g), _p(ln_b),
+                 _p(do), *(_p(g) for g in grads), _p(ws), wsb, bsz, seq, dd, dtype_flag(q))
+        return tuple(grads)
+
+
+def ttt_scan(q, k, v, eta, w0, ln_gamma, ln_beta):
+    """``FusedScan.ttt_scan/7`` (fused_scan.ex:344-358): TTT-Linear with inner model W [B, D, D]
+    (initial w0) trained per step by one LayerNorm-ed reconstruction step; q, k, v, eta
+    (post-sigmoid learning rate) [B, T, D], ln_gamma, ln_beta [D]."""
+    return _TTT.apply(q, k, v, eta, w0, ln_gamma, ln_beta)
+
+
 def delta_net_scan(q, k, v, beta):
     """``FusedScan.delta_net_scan/4`` (fused_scan.ex:195-209): q, k, v [B, T, H, d]; k
     L2-normalised, beta post-sigmoid, per element [B, T, H, d] or per head [B, T, H]."""

@@ -261,6 +261,25 @@ int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, cons
                                 int num_heads, int head_dim, int variant, float clip_threshold, int dtype);
 size_t edf_rla_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
 
+/* TTT-Linear: an inner linear model W [B, D, D] (initial w0) updated every step by one
+ * LayerNorm-ed reconstruction step; q, k, v, eta [B,T,D], ln_g, ln_b [D].  Replaces
+ * fused_ttt_scan/11 (q, k, v, eta, w0, ln_g, ln_b, batch, seq, inner, dtype),
+ * lib/edifice/cuda/nif.ex:82 -> native/cuda/fused_ttt_scan.cu (fallback ttt.ex:369-404);
+ * inner_size <= 128; no workspace for the forward. */
+int edf_fused_ttt_scan(void* stream, const void* q, const void* k, const void* v, const void* eta, const void* w0,
+                       const void* ln_g, const void* ln_b, void* out, int batch, int seq_len, int inner_size,
+                       int dtype);
+
+/* Replaces fused_ttt_scan_backward/12 (q, k, v, eta, w0, ln_g, ln_b, grad, ...), nif.ex:214
+ * -> native/cuda/fused_ttt_scan_backward.cu: dq, dk, dv, d eta [B,T,D], d w0 [B,D,D],
+ * d ln_g, d ln_b [D]; workspace edf_ttt_scan_backward_workspace_bytes() bytes. */
+int edf_fused_ttt_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* eta,
+                                const void* w0, const void* ln_g, const void* ln_b, const void* grad_out,
+                                void* grad_q, void* grad_k, void* grad_v, void* grad_eta, void* grad_w0,
+                                void* grad_ln_g, void* grad_ln_b, void* workspace, size_t workspace_bytes,
+                                int batch, int seq_len, int inner_size, int dtype);
+size_t edf_ttt_scan_backward_workspace_bytes(int batch, int seq_len, int inner_size, int dtype);
+
 /* ------------------------------------------------------------------------
  * Flash attention   O = softmax(Q K^T / sqrt(d) [+ causal -inf]) V
  *   q, k, v, out, grads: [B, H, T, d] in dtype; lse: float32 [B, H, T] (natural log)

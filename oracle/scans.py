@@ -567,6 +567,73 @@ def kda_scan_backward(q, k, v, alpha, beta, do):
     return g
 
 
+TTT_LN_EPS = 1.0e-6  # fused_ttt_scan.cu:35
+
+
+def _ttt_fwd(q, k, v, eta, w0, ln_g, ln_b):
+    """-> (out, list of W before each step, x_hat, err, rstd)."""
+    bsz, seq, dd = q.shape
+    W = w0.copy()
+    out = np.empty_like(q)
+    ws, xh, er, rs = [], np.empty_like(q), np.empty_like(q), np.empty((bsz, seq))
+    for t in range(seq):
+        ws.append(W)
+        pred = np.einsum("bij,bj->bi", W, k[:, t])
+        mu = pred.mean(axis=-1, keepdims=True)
+        var = ((pred - mu) ** 2).mean(axis=-1, keepdims=True)
+        r = 1.0 / np.sqrt(var + TTT_LN_EPS)
+        x = (pred - mu) * r
+        err = ln_g * x + ln_b - v[:, t]
+        W = W - (eta[:, t] * err)[..., :, None] * k[:, t][:, None, :]
+        out[:, t] = np.einsum("bij,bj->bi", W, q[:, t])
+        xh[:, t], er[:, t], rs[:, t] = x, err, r[..., 0]
+    return out, ws, xh, er, rs
+
+
+def ttt_scan(q, k, v, eta, w0, ln_g, ln_b):
+    """TTT-Linear: an inner linear model W [B, D, D] (initial w0) trained at every step by one
+    LayerNorm-ed reconstruction step (fused_ttt_scan.cu:1-30 and 85-150; fallback
+    ``ttt_scan_fallback``, ttt.ex:369-404):
+      pred = W k;  x_hat = (pred - mean) / sqrt(var + 1e-6) (population variance over D);
+      err = ln_g x_hat + ln_b - v;  W = W - (eta err) k^T;  o = W q.
+    q, k, v, eta (post-sigmoid, per element) [B, T, D]; ln_g, ln_b [D]."""
+    q, k, v, eta, w0, ln_g, ln_b = _f64(q, k, v, eta, w0, ln_g, ln_b)
+    return _ttt_fwd(q, k, v, eta, w0, ln_g, ln_b)[0]
+
+
+def ttt_scan_backward(q, k, v, eta, w0, ln_g, ln_b, do):
+    """Reverse pass -> dict(dq, dk, dv, deta [B,T,D], dw0 [B,D,D], dln_g, dln_b [D])
+    (fused_ttt_scan_backward.cu:300-420 for the per-step math): with dW the adjoint after
+    step t, dW_t = dW + do q^T, dq = W_t^T do, d se = -dW_t k, deta = d se * err,
+    d err = d se * eta, dv = -d err, dln_g += d err x_hat, dln_b += d err,
+    dx = ln_g d err, d pred = rstd (dx - mean(dx) - x_hat mean(dx x_hat)),
+    dk = -dW_t^T se + W_p^T d pred, dW <- dW_t + d pred k^T; dw0 = the final dW."""
+    q, k, v, eta, w0, ln_g, ln_b, do = _f64(q, k, v, eta, w0, ln_g, ln_b, do)
+    bsz, seq, dd = q.shape
+    _, ws, xh, er, rs = _ttt_fwd(q, k, v, eta, w0, ln_g, ln_b)
+    dq, dk, dv, de = (np.empty_like(q) for _ in range(4))
+    dg, db = np.zeros(dd), np.zeros(dd)
+    dW = np.zeros_like(w0)
+    for t in range(seq - 1, -1, -1):
+        wp = ws[t]
+        se = eta[:, t] * er[:, t]
+        wt = wp - se[..., :, None] * k[:, t][:, None, :]
+        dwt = dW + do[:, t][..., :, None] * q[:, t][:, None, :]
+        dq[:, t] = np.einsum("bij,bi->bj", wt, do[:, t])
+        dse = -np.einsum("bij,bj->bi", dwt, k[:, t])
+        de[:, t] = dse * er[:, t]
+        derr = dse * eta[:, t]
+        dv[:, t] = -derr
+        dg += (derr * xh[:, t]).sum(axis=0)
+        db += derr.sum(axis=0)
+        dx = ln_g * derr
+        x = xh[:, t]
+        dpred = rs[:, t][:, None] * (dx - dx.mean(-1, keepdims=True) - x * (dx * x).mean(-1, keepdims=True))
+        dk[:, t] = -np.einsum("bij,bi->bj", dwt, se) + np.einsum("bij,bi->bj", wp, dpred)
+        dW = dwt + dpred[..., :, None] * k[:, t][:, None, :]
+    return dict(dq=dq, dk=dk, dv=dv, deta=de, dw0=dW, dln_g=dg, dln_b=db)
+
+
 RLA_VARIANTS = {"rla": 0, "rdn": 1}  # fused_scan.ex:425-433
 
 

@@ -171,3 +171,38 @@ def test_rla_fwd_bwd(case, rng):
     g = scans.rla_scan_backward(*xs, rounded(do, dtype), var, clip)
     for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb), ("dgamma", tg)):
         assert_close(host(tt.grad), g[n], tol, n)
+
+
+TTT_CASES = [
+    # (B, T, D, dtype)
+    (2, 5, 4, torch.float32),
+    (2, 37, 16, torch.float32),     # T not a multiple of the 8-step chunk
+    (3, 20, 50, torch.float32),     # D off the padded widths
+    (1, 30, 64, torch.float32),
+    (2, 24, 128, torch.float32),
+    (2, 33, 64, torch.bfloat16),
+    (1, 16, 128, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("case", TTT_CASES)
+def test_ttt_fwd_bwd(case, rng):
+    """FusedScan.ttt_scan/7 and its backward (dq, dk, dv, deta, dw0, dln_g, dln_b) against
+    the oracle; eta ~ sigmoid / D as the reference block feeds it."""
+    from edifice_amd import fused_scan as fs
+    bsz, t, d, dtype = case
+    announce("ttt", case=case)
+    q, k, v, do = (rng.normal(size=(bsz, t, d)) for _ in range(4))
+    k = k / np.sqrt(d)
+    eta = rng.uniform(0.2, 0.8, size=(bsz, t, d)) / d * 4
+    w0 = rng.normal(size=(bsz, d, d)) / np.sqrt(d)
+    g, b = 1 + 0.2 * rng.normal(size=d), 0.2 * rng.normal(size=d)
+    ts = [to_dev(x, dtype).requires_grad_() for x in (q, k, v, eta, w0, g, b)]
+    out = fs.ttt_scan(*ts)
+    out.backward(to_dev(do, dtype))
+    xs = [rounded(x, dtype) for x in (q, k, v, eta, w0, g, b)]
+    tol = TOL[dtype]
+    assert_close(host(out), scans.ttt_scan(*xs), tol, "o")
+    gr = scans.ttt_scan_backward(*xs, rounded(do, dtype))
+    for n, tt in zip(("dq", "dk", "dv", "deta", "dw0", "dln_g", "dln_b"), ts):
+        assert_close(host(tt.grad), gr[n], tol, n)

@@ -352,3 +352,27 @@ def test_rla_backward_vs_autograd(rng, variant):
     gr = scans.rla_scan_backward(q, k, v, alpha, beta, gamma, do, variant, 0.6)
     for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("dalpha", ta), ("dbeta", tb), ("dgamma", tg)):
         assert_close(gr[n], tt.grad.numpy(), 1e-10, n)
+
+
+def test_ttt_backward_vs_autograd(rng):
+    """TTT-Linear backward (oracle) against torch autograd of an independent forward using
+    torch.nn.functional.layer_norm (population variance, eps 1e-6)."""
+    bsz, t, d = 2, 4, 5
+    q, k, v, do = (rng.normal(size=(bsz, t, d)) for _ in range(4))
+    eta = rng.uniform(0.05, 0.3, size=(bsz, t, d))
+    w0 = 0.5 * rng.normal(size=(bsz, d, d))
+    g, b = 1 + 0.3 * rng.normal(size=d), 0.3 * rng.normal(size=d)
+    tq, tk, tv, te, tw, tg, tb = (_t(x) for x in (q, k, v, eta, w0, g, b))
+    W = tw
+    outs = []
+    for s in range(t):
+        pred = (W @ tk[:, s][..., None])[..., 0]
+        err = torch.nn.functional.layer_norm(pred, (d,), tg, tb, eps=1e-6) - tv[:, s]
+        W = W - (te[:, s] * err)[..., :, None] * tk[:, s][:, None, :]
+        outs.append((W @ tq[:, s][..., None])[..., 0])
+    out = torch.stack(outs, 1)
+    out.backward(torch.from_numpy(do))
+    assert_close(scans.ttt_scan(q, k, v, eta, w0, g, b), out.detach().numpy(), 1e-12, "o")
+    gr = scans.ttt_scan_backward(q, k, v, eta, w0, g, b, do)
+    for n, tt in (("dq", tq), ("dk", tk), ("dv", tv), ("deta", te), ("dw0", tw), ("dln_g", tg), ("dln_b", tb)):
+        assert_close(gr[n], tt.grad.numpy(), 1e-10, n)

@@ -448,3 +448,18 @@ def test_rla_zero_clip_keeps_residual_empty(rng, variant):
     base = scans.rla_scan(q, k, v, alpha, beta, np.zeros_like(gamma), variant)
     np.testing.assert_allclose(scans.rla_scan(q, k, v, alpha, beta, gamma, variant, clip=0.0), base, rtol=1e-12)
     assert np.abs(scans.rla_scan(q, k, v, alpha, beta, gamma, variant, clip=1e9) - base).max() > 1e-3
+
+
+def test_ttt_closed_forms(rng):
+    """eta = 0: W stays w0, so o_t = w0 q_t.  w0 = 0, one step: pred = 0 normalizes to 0,
+    so err = ln_b - v and o = -(eta (ln_b - v)) (k . q)."""
+    bsz, t, d = 2, 5, 6
+    q, k, v = (rng.normal(size=(bsz, t, d)) for _ in range(3))
+    w0 = rng.normal(size=(bsz, d, d))
+    g, b = rng.normal(size=d), rng.normal(size=d)
+    np.testing.assert_allclose(scans.ttt_scan(q, k, v, np.zeros((bsz, t, d)), w0, g, b),
+                               np.einsum("bij,btj->bti", w0, q), rtol=1e-12)
+    eta = rng.uniform(0.0, 0.1, size=(bsz, 1, d))
+    got = scans.ttt_scan(q[:, :1], k[:, :1], v[:, :1], eta, np.zeros((bsz, d, d)), g, b)
+    want = -(eta[:, 0] * (b - v[:, 0])) * (k[:, 0] * q[:, 0]).sum(-1, keepdims=True)
+    np.testing.assert_allclose(got[:, 0], want, rtol=1e-12)
