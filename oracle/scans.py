@@ -40,6 +40,8 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
   rla_scan / _backward          gamma = 0 RLA ==> decayed linear attention closed form, RDN
                                 with alpha = 1, gamma = 0 ==> DeltaNet, clip 0 ==> empty
                                 residual state, torch autograd (with clipped errors).
+  ttt_scan / _backward          eta = 0 ==> o = w0 q, w0 = 0 one-step closed form, torch
+                                autograd through torch.nn.functional.layer_norm.
   laser_attention / _backward   identical value rows ==> O = that row; torch autograd of an
                                 independent torch forward (vmax held constant).
   fox_attention / _backward     cs = const ==> causal flash_attention; torch autograd of an
