@@ -491,6 +491,48 @@ def bench_ttt(torch, steps, warmup, B=8, T=2048, D=64):
                 shape=dict(B=B, T=T, D=D))
 
 
+def bench_rnn_block(torch, steps, warmup, kind, dtype, B=8, T=2048, H=256, L=4):
+    """Multi-layer LSTM / GRU block (inference), random weights: ms per call and tokens/s."""
+    from edifice_amd import _native as nat
+
+    g = torch.Generator(device="cuda").manual_seed(3005)
+    G = 4 if kind == "lstm" else 3
+    sc = H ** -0.5
+    per = []
+    for _ in range(L):
+        per += [sc * torch.randn(H * G * H, device="cuda", generator=g), 0.1 * torch.randn(G * H, device="cuda", generator=g),
+                sc * torch.randn(H * G * H, device="cuda", generator=g), torch.ones(H, device="cuda"),
+                torch.zeros(H, device="cuda")]
+    w = torch.cat(per).to(dtype)
+    x = torch.randn(B, T, H, device="cuda", generator=g).to(dtype)
+    h0 = torch.zeros(B, L, H, device="cuda", dtype=dtype)
+    out = torch.empty_like(x)
+    flag = 1 if dtype == torch.bfloat16 else 0
+    wsb = nat.query(f"edf_{kind}_block_workspace_bytes", B, T, H, L, flag)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run():
+        if kind == "lstm":
+            nat.call("edf_fused_lstm_block_scan", stream, P(x), P(w), P(h0), P(h0), P(out), P(ws), wsb, B, T, H, L, flag)
+        else:
+            nat.call("edf_fused_gru_block_scan", stream, P(x), P(w), P(h0), P(out), P(ws), wsb, B, T, H, L, flag)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return dict(layers=L, dtype=str(dtype).replace("torch.", ""), ms=ms, tokens_per_s=B * T / ms * 1e3,
+                shape=dict(B=B, T=T, H=H))
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
@@ -583,6 +625,9 @@ def main():
                          ("linear", torch.float32)):
             key = f"{kind}_block_{str(dt).replace('torch.', '')}_8x2048x256_L4"
             configs[key] = bench_block(torch, args.steps, args.warmup, 8, 2048, 256, 4, dt, kind)
+        for kind in ("lstm", "gru"):
+            configs[f"{kind}_block_float32_8x2048x256_L4"] = bench_rnn_block(
+                torch, min(args.steps, 5), min(args.warmup, 2), kind, torch.float32)
     if want("linear"):
         for dt in (torch.bfloat16, torch.float32):
             key = f"linear_scan_{str(dt).replace('torch.', '')}_8x2048x1536"

@@ -35,6 +35,10 @@ SIGNATURES = {
     "edf_fused_minlstm_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_linear_block_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_linear_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
+    "edf_lstm_block_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_lstm_block_scan": (I, [P, P, P, P, P, P, P, S, I, I, I, I, I]),
+    "edf_gru_block_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_gru_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_fused_selective_scan": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
     "edf_selective_scan_states_bytes": (S, [I, I, I, I]),
     "edf_selective_scan_workspace_bytes": (S, [I, I, I, I, I]),

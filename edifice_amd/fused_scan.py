@@ -223,6 +223,51 @@ def linear_block(input, weights, h0, num_layers: int):
     return _block("linear", input, weights, h0, num_layers)
 
 
+_RNN_GATES = {"lstm": 4, "gru": 3}
+
+
+def _rnn_block(kind, input, weights, h0, c0, num_layers):
+    input, weights = input.contiguous(), weights.contiguous()
+    h0, c0 = _c(h0), _c(c0)
+    _dev(input, weights, h0, c0)
+    _same(input, weights, h0, c0)
+    bsz, seq, hid = input.shape
+    gh = _RNN_GATES[kind] * hid
+    per_layer = 2 * hid * gh + gh + 2 * hid
+    if weights.numel() != num_layers * per_layer:
+        raise EdificeHipError(f"weights hold {weights.numel()} values, expected {num_layers} x {per_layer}")
+    for name, t in (("h0", h0), ("c0", c0)):
+        if t is not None and tuple(t.shape) != (bsz, num_layers, hid):
+            raise EdificeHipError(f"{name} must be [B, num_layers, H] = {(bsz, num_layers, hid)}")
+    out = torch.empty_like(input)
+    flag = dtype_flag(input)
+    wsb = nat.query(f"edf_{kind}_block_workspace_bytes", bsz, seq, hid, num_layers, flag)
+    ws = _u8(wsb, input)
+    if kind == "lstm":
+        nat.call("edf_fused_lstm_block_scan", _stream(), _p(input), _p(weights), _p(h0), _p(c0), _p(out), _p(ws),
+                 wsb, bsz, seq, hid, num_layers, flag)
+    else:
+        nat.call("edf_fused_gru_block_scan", _stream(), _p(input), _p(weights), _p(h0), _p(out), _p(ws), wsb,
+                 bsz, seq, hid, num_layers, flag)
+    return out
+
+
+def lstm_block(input, weights, h0, c0, num_layers: int):
+    """``FusedScan.lstm_block/5`` (fused_scan.ex:4854-4868): multi-layer LSTM inference.
+
+    input [B, T, H]; weights the flat per-layer packing W_x [H, 4H] (gates i, f, g, o), b_x
+    [4H], R [H, 4H], gamma [H], beta [H] in input's dtype; h0, c0 [B, num_layers, H] or None
+    (zeros); H <= 256.  Returns the last layer's output [B, T, H].
+    """
+    return _rnn_block("lstm", input, weights, h0, c0, num_layers)
+
+
+def gru_block(input, weights, h0, num_layers: int):
+    """``FusedScan.gru_block/4`` (fused_scan.ex:4999-5013): multi-layer GRU inference, gates
+    r, z, n (W_x [H, 3H], b_x [3H], R [H, 3H], gamma, beta per layer), h = (1 - z) h + z n."""
+    return _rnn_block("gru", input, weights, h0, None, num_layers)
+
+
 # ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------

@@ -162,6 +162,25 @@ int edf_fused_linear_block_scan(void* stream, const void* input, const void* wei
                                 void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
                                 int num_layers, int dtype);
 
+/* Multi-layer LSTM block scan (inference).  Replaces fused_lstm_block_scan/9 (input,
+ * weights, h0, c0, batch, seq, hidden, layers, dtype), lib/edifice/cuda/nif.ex:139 ->
+ * native/cuda/fused_lstm_block_scan.cu (fallback fused_scan.ex:4911-4990).  Per-layer
+ * packing W_x [H, 4H] (gates i, f, g, o), b_x [4H], R [H, 4H], gamma [H], beta [H]; h0, c0
+ * [B, L, H] or NULL (zeros); H <= 256; workspace edf_lstm_block_workspace_bytes() bytes. */
+int edf_fused_lstm_block_scan(void* stream, const void* input, const void* weights, const void* h0, const void* c0,
+                              void* out, void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                              int num_layers, int dtype);
+size_t edf_lstm_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype);
+
+/* Multi-layer GRU block scan (inference).  Replaces fused_gru_block_scan/8 (input, weights,
+ * h0, batch, seq, hidden, layers, dtype), nif.ex:143 -> native/cuda/fused_gru_block_scan.cu
+ * (fallback fused_scan.ex:5055-5120); packing W_x [H, 3H] (gates r, z, n), b_x [3H],
+ * R [H, 3H], gamma, beta; workspace edf_gru_block_workspace_bytes() bytes. */
+int edf_fused_gru_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,
+                             void* workspace, size_t workspace_bytes, int batch, int seq_len, int hidden,
+                             int num_layers, int dtype);
+size_t edf_gru_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype);
+
 /* ------------------------------------------------------------------------
  * Mamba selective scan
  *   x, dt, z, out, grad_x, grad_dt, grad_z: [B, T, D] in io_dtype

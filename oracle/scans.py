@@ -265,6 +265,78 @@ def block_stepwise(kind, x, weights, h0, num_layers):
     return out
 
 
+RNN_BLOCK_GATES = {"lstm": 4, "gru": 3}
+
+
+def _rnn_layer_weights(weights, layer, hid, gates):
+    """Per-layer packing W_x [H, G H], b_x [G H], R [H, G H], gamma [H], beta [H]
+    (fused_lstm_block_scan.cu:14-16, fused_gru_block_scan.cu:14-16)."""
+    w = np.asarray(weights, dtype=np.float64)
+    gh = gates * hid
+    o = layer * (2 * hid * gh + gh + 2 * hid)
+    wx = w[o:o + hid * gh].reshape(hid, gh)
+    o += hid * gh
+    bx = w[o:o + gh]
+    o += gh
+    r = w[o:o + hid * gh].reshape(hid, gh)
+    o += hid * gh
+    return wx, bx, r, w[o:o + hid], w[o + hid:o + 2 * hid]
+
+
+def _rnn_cell(kind, xp, rh, h, c, hid):
+    """One LSTM (gates i, f, g, o) or GRU (r, z, n; reset on the recurrent part of n only,
+    h = (1 - z) h + z n) step from the input and recurrent projections."""
+    sl = [slice(k * hid, (k + 1) * hid) for k in range(RNN_BLOCK_GATES[kind])]
+    if kind == "lstm":
+        i, f, o = (sigmoid(xp[..., s] + rh[..., s]) for s in (sl[0], sl[1], sl[3]))
+        g = np.tanh(xp[..., sl[2]] + rh[..., sl[2]])
+        c = f * c + i * g
+        return o * np.tanh(c), c
+    r, z = (sigmoid(xp[..., s] + rh[..., s]) for s in (sl[0], sl[1]))
+    n = np.tanh(xp[..., sl[2]] + r * rh[..., sl[2]])
+    return (1.0 - z) * h + z * n, c
+
+
+def rnn_block(kind, x, weights, h0, c0, num_layers):
+    """Multi-layer LSTM / GRU block, layer by layer as ``lstm_block_fallback`` /
+    ``gru_block_fallback`` (fused_scan.ex:4911-4990, 5055-5120): LayerNorm (biased variance,
+    eps 1e-5), input projection n W_x + b_x for all steps, the recurrence with R h_{t-1} from
+    h0[:, l] (and c0[:, l]), residual x + h.  None initial states mean zeros."""
+    x = np.asarray(x, dtype=np.float64)
+    bsz, seq, hid = x.shape
+    h0 = np.zeros((bsz, num_layers, hid)) if h0 is None else np.asarray(h0, dtype=np.float64)
+    c0 = np.zeros((bsz, num_layers, hid)) if c0 is None else np.asarray(c0, dtype=np.float64)
+    for layer in range(num_layers):
+        wx, bx, r, gamma, beta = _rnn_layer_weights(weights, layer, hid, RNN_BLOCK_GATES[kind])
+        xp = _block_norm(x, gamma, beta) @ wx + bx
+        h, c = h0[:, layer].copy(), c0[:, layer].copy()
+        hs = np.empty_like(x)
+        for t in range(seq):
+            h, c = _rnn_cell(kind, xp[:, t], h @ r, h, c, hid)
+            hs[:, t] = h
+        x = x + hs
+    return x
+
+
+def rnn_block_stepwise(kind, x, weights, h0, c0, num_layers):
+    """Timestep by timestep, every layer per step, as the fused reference kernels walk it
+    (fused_lstm_block_scan.cu:80-170, fused_gru_block_scan.cu:75-165)."""
+    x = np.asarray(x, dtype=np.float64)
+    bsz, seq, hid = x.shape
+    h = np.zeros((bsz, num_layers, hid)) if h0 is None else np.array(h0, dtype=np.float64)
+    c = np.zeros((bsz, num_layers, hid)) if c0 is None else np.array(c0, dtype=np.float64)
+    lw = [_rnn_layer_weights(weights, layer, hid, RNN_BLOCK_GATES[kind]) for layer in range(num_layers)]
+    out = np.empty_like(x)
+    for t in range(seq):
+        xv = x[:, t].copy()
+        for layer, (wx, bx, r, gamma, beta) in enumerate(lw):
+            xp = _block_norm(xv, gamma, beta) @ wx + bx
+            h[:, layer], c[:, layer] = _rnn_cell(kind, xp, h[:, layer] @ r, h[:, layer], c[:, layer], hid)
+            xv = xv + h[:, layer]
+        out[:, t] = xv
+    return out
+
+
 def mingru_block(x, weights, h0, num_layers):
     """``block("mingru", ...)``: the multi-layer MinGRU block (fused_scan.ex:4521-4571)."""
     return block("mingru", x, weights, h0, num_layers)

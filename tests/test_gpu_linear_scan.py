@@ -253,3 +253,42 @@ def test_mingru_block_full_size(rng):
     w = rng.normal(scale=hid ** -0.5, size=layers * (2 * hid * hid + 4 * hid)).astype(np.float32)
     out = fs.mingru_block(to_dev(x, torch.float32), to_dev(w, torch.float32), None, layers)
     assert_close(host(out), scans.mingru_block(x, w, None, layers), TOL[torch.float32], "block full")
+
+
+RNN_BLOCK_CASES = [
+    # (kind, B, T, H, layers, dtype, initial states given)
+    ("lstm", 2, 9, 8, 2, torch.float32, True),
+    ("gru", 2, 9, 8, 2, torch.float32, True),
+    ("lstm", 3, 17, 50, 3, torch.float32, False),
+    ("gru", 9, 6, 33, 1, torch.float32, True),     # B past one 8-row step tile
+    ("lstm", 2, 12, 256, 2, torch.float32, True),   # reference maximum H
+    ("gru", 2, 12, 256, 2, torch.float32, False),
+    ("lstm", 1, 40, 128, 4, torch.bfloat16, True),
+    ("gru", 2, 70, 64, 2, torch.bfloat16, True),
+]
+
+
+@pytest.mark.parametrize("case", RNN_BLOCK_CASES)
+def test_rnn_block(case, rng):
+    """FusedScan.lstm_block/5 and gru_block/4 against the layer-by-layer oracle (itself pinned
+    to torch.nn.LSTM / torch.nn.GRU and to the step-by-step kernel order)."""
+    from edifice_amd import fused_scan as fs
+    kind, bsz, seq, hid, layers, dtype, init = case
+    announce("rnn_block", case=case)
+    gh = scans.RNN_BLOCK_GATES[kind] * hid
+    sc = 1 / np.sqrt(hid)
+    per = []
+    for _ in range(layers):
+        per += [sc * rng.normal(size=hid * gh), 0.3 * rng.normal(size=gh), sc * rng.normal(size=hid * gh),
+                1 + 0.2 * rng.normal(size=hid), 0.2 * rng.normal(size=hid)]
+    w = np.concatenate(per)
+    x = rng.normal(size=(bsz, seq, hid))
+    h0 = rng.normal(size=(bsz, layers, hid)) if init else None
+    c0 = rng.normal(size=(bsz, layers, hid)) if init and kind == "lstm" else None
+    tx, tw = to_dev(x, dtype), to_dev(w, dtype)
+    th0 = to_dev(h0, dtype) if h0 is not None else None
+    tc0 = to_dev(c0, dtype) if c0 is not None else None
+    out = fs.lstm_block(tx, tw, th0, tc0, layers) if kind == "lstm" else fs.gru_block(tx, tw, th0, layers)
+    r = lambda a: None if a is None else rounded(a, dtype)  # noqa: E731
+    want = scans.rnn_block(kind, r(x), r(w), r(h0), r(c0), layers)
+    assert_close(host(out), want, TOL[dtype], "out")

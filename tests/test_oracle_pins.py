@@ -463,3 +463,54 @@ def test_ttt_closed_forms(rng):
     got = scans.ttt_scan(q[:, :1], k[:, :1], v[:, :1], eta, np.zeros((bsz, d, d)), g, b)
     want = -(eta[:, 0] * (b - v[:, 0])) * (k[:, 0] * q[:, 0]).sum(-1, keepdims=True)
     np.testing.assert_allclose(got[:, 0], want, rtol=1e-12)
+
+
+def _rnn_weights(rng, kind, hid, layers, scale=0.3):
+    g = scans.RNN_BLOCK_GATES[kind] * hid
+    per = []
+    for _ in range(layers):
+        per += [scale * rng.normal(size=hid * g), scale * rng.normal(size=g), scale * rng.normal(size=hid * g),
+                1 + 0.2 * rng.normal(size=hid), 0.2 * rng.normal(size=hid)]
+    return np.concatenate(per)
+
+
+@pytest.mark.parametrize("kind", ["lstm", "gru"])
+def test_rnn_block_layerwise_equals_stepwise(rng, kind):
+    """The reference's two formulations (fallback layer by layer, kernel step by step) agree."""
+    bsz, t, hid, layers = 2, 7, 5, 3
+    x = rng.normal(size=(bsz, t, hid))
+    w = _rnn_weights(rng, kind, hid, layers)
+    h0, c0 = rng.normal(size=(bsz, layers, hid)), rng.normal(size=(bsz, layers, hid))
+    np.testing.assert_allclose(scans.rnn_block(kind, x, w, h0, c0, layers),
+                               scans.rnn_block_stepwise(kind, x, w, h0, c0, layers), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("kind", ["lstm", "gru"])
+def test_rnn_block_one_layer_is_torch_rnn(rng, kind):
+    """One layer = LayerNorm + torch.nn.LSTM / torch.nn.GRU (gate orders i,f,g,o and r,z,n;
+    weight_ih = W_x^T, weight_hh = R^T, no recurrent bias) + residual.  torch's GRU mixes
+    h' = (1 - z) n + z h, the reference (1 - z) h + z n, so the z rows are negated
+    (sigmoid(-a) = 1 - sigmoid(a))."""
+    bsz, t, hid = 2, 6, 4
+    x = rng.normal(size=(bsz, t, hid))
+    w = _rnn_weights(rng, kind, hid, 1)
+    h0, c0 = rng.normal(size=(bsz, 1, hid)), rng.normal(size=(bsz, 1, hid))
+    wx, bx, r, gamma, beta = scans._rnn_layer_weights(w, 0, hid, scans.RNN_BLOCK_GATES[kind])
+    n = scans._block_norm(x, gamma, beta)
+    wih, whh, bih = wx.T.copy(), r.T.copy(), bx.copy()
+    if kind == "gru":
+        for m in (wih, whh):
+            m[hid:2 * hid] *= -1
+        bih[hid:2 * hid] *= -1
+        net = torch.nn.GRU(hid, hid, batch_first=True).double()
+    else:
+        net = torch.nn.LSTM(hid, hid, batch_first=True).double()
+    with torch.no_grad():
+        net.weight_ih_l0.copy_(torch.from_numpy(wih))
+        net.weight_hh_l0.copy_(torch.from_numpy(whh))
+        net.bias_ih_l0.copy_(torch.from_numpy(bih))
+        net.bias_hh_l0.zero_()
+        hh = torch.from_numpy(h0.transpose(1, 0, 2).copy())
+        init = (hh, torch.from_numpy(c0.transpose(1, 0, 2).copy())) if kind == "lstm" else hh
+        y, _ = net(torch.from_numpy(n), init)
+    np.testing.assert_allclose(scans.rnn_block(kind, x, w, h0, c0, 1), x + y.numpy(), rtol=1e-10, atol=1e-12)
