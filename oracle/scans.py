@@ -18,6 +18,9 @@ Pinning (what independently checks each function; see tests/test_oracle_*.py):
                                 LayerNorm + dense + mingru_scan / minlstm_scan /
                                 linear_scan + residual written out, W = 0 with a closed
                                 form, layers compose (L layers == 1 layer applied L times).
+  rnn_block (lstm / gru)        one layer == LayerNorm + torch.nn.LSTM / torch.nn.GRU (z rows
+                                negated for torch's h' = (1 - z) n + z h) + residual; layer by
+                                layer == step by step (the fused kernels' order).
   mingru_scan / _backward       seq_len=1 known answer (backward_kernels_test.exs:271-287),
                                 min_gru_random.safetensors block fixture, z≡1 / z≡0
                                 closed forms, torch autograd + finite differences.
