@@ -11,9 +11,10 @@
 // per batch element streaming both weight matrices from memory at every step.  Here each
 // layer runs as (1) one MFMA kernel for LayerNorm + the input projection of ALL B T rows (the
 // residual add of the previous layer fused into its prologue), then (2) one small launch per
-// time step for the recurrence: the step's B x G H recurrent dot products spread over H / 8
-// workgroups, each holding 8 units of every gate for 8 batch rows: a workgroup stages its
-// R columns (H x 8 G floats) into LDS with independent loads, so R is read once per step from
+// time step for the recurrence: the step's B x G H recurrent dot products spread over H / 4
+// workgroups, each holding 4 units of every gate for 8 batch rows: a workgroup stages its
+// R columns (H x 4 G floats) into LDS with independent loads and splits each dot product over
+// a lane pair, so R is read once per step from
 // L2 by the whole grid, and the cell update needs no cross-workgroup exchange; the launch
 // boundary orders the steps (no grid-wide barrier inside a kernel).
 #include "edf_abi.hpp"
@@ -26,7 +27,7 @@ constexpr int RNB_ROWS = 32;   // rows per projection workgroup (one 32x32 MFMA 
 constexpr int RNB_HMAX = 256;  // reference limit (one thread per hidden unit)
 constexpr int RNB_LD = RNB_HMAX + 2;
 constexpr float RNB_LN_EPS = 1.0e-5f;  // fused_lstm_block_scan.cu:113
-constexpr int RNB_U = 8;   // hidden units per step workgroup
+constexpr int RNB_U = 4;   // hidden units per step workgroup
 constexpr int RNB_BS = 8;  // batch rows per step workgroup
 
 enum { RNB_LSTM = 4, RNB_GRU = 3 };  // value = number of gates
@@ -162,16 +163,22 @@ __global__ __launch_bounds__(256) void rnb_step_kernel(const T* __restrict__ R, 
     sh[bb][k] = v;
   }
   __syncthreads();
-  if (tid < RNB_BS * G * RNB_U) {
-    const int bb = tid / (G * RNB_U), gu = tid % (G * RNB_U);
+  // each dot product is split over a lane pair (even / odd k), combined with one swizzle
+  {
+    const int dot = tid >> 1, half = tid & 1;
+    const int bb = dot / (G * RNB_U), gu = dot % (G * RNB_U);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    int k = 0;
-    for (; k + 4 <= H; k += 4) {
+    if (dot < RNB_BS * G * RNB_U) {
+      int k = half;
+      for (; k + 6 < H; k += 8) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc[m] = fmaf(sh[bb][k + m], sR[k + m][gu], acc[m]);
+        for (int m = 0; m < 4; ++m) acc[m] = fmaf(sh[bb][k + 2 * m], sR[k + 2 * m][gu], acc[m]);
+      }
+      for (; k < H; k += 2) acc[0] = fmaf(sh[bb][k], sR[k][gu], acc[0]);
     }
-    for (; k < H; ++k) acc[0] = fmaf(sh[bb][k], sR[k][gu], acc[0]);
-    sd[bb][gu / RNB_U][gu % RNB_U] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    v += __shfl_xor(v, 1);
+    if (half == 0 && dot < RNB_BS * G * RNB_U) sd[bb][gu / RNB_U][gu % RNB_U] = v;
   }
   __syncthreads();
   if (tid < RNB_BS * RNB_U) {
