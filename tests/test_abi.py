@@ -89,3 +89,32 @@ def test_workspace_queries(lib):
     assert lib.edf_flash_attention_backward_workspace_bytes(4, 32, 4096, 128) == 4 * 32 * 4096 * 4
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 1, 1) > 0  # chunked path
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 0, 1) == 0  # f32: step path
+
+
+def test_variant_entry_points_validate_before_launch(lib):
+    """DeltaProduct, RLA, TTT and the LSTM / GRU blocks reject bad arguments with an error
+    code and message before any device work."""
+    p = ctypes.c_void_p(16)
+    rc = lib.edf_fused_delta_product_scan(None, p, p, p, p, p, p, 1 << 20, 1, 4, 0, 2, 16, 0)
+    assert rc == 1 and lib.edf_last_error() == b"dimensions must be positive"
+    rc = lib.edf_fused_delta_product_scan(None, p, p, p, p, p, p, 1 << 20, 1, 4, 2, 2, 129, 0)
+    assert rc == 2 and b"head_dim" in lib.edf_last_error()
+    rc = lib.edf_fused_delta_product_scan(None, p, p, p, p, p, None, 0, 1, 4, 2, 2, 64, 0)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+    rc = lib.edf_fused_rla_scan(None, p, p, p, p, p, p, p, 1, 4, 2, 16, 2, 1.0, 0)
+    assert rc == 1 and b"variant" in lib.edf_last_error()
+    rc = lib.edf_fused_rla_scan(None, p, p, p, p, p, p, p, 1, 4, 2, 16, 0, -0.5, 0)
+    assert rc == 1 and b"clip" in lib.edf_last_error()
+    rc = lib.edf_fused_rla_scan(None, p, p, p, p, p, p, p, 1, 4, 2, 16, 0, float("nan"), 0)
+    assert rc == 1 and b"clip" in lib.edf_last_error()
+    rc = lib.edf_fused_ttt_scan(None, p, p, p, p, p, p, p, p, 2, 4, 200, 0)
+    assert rc == 2 and b"inner_size" in lib.edf_last_error()
+    rc = lib.edf_fused_ttt_scan_backward(None, *([p] * 15), None, 0, 2, 4, 64, 0)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+    rc = lib.edf_fused_lstm_block_scan(None, p, p, None, None, p, p, 1 << 30, 2, 4, 300, 1, 0)
+    assert rc == 2 and b"hidden" in lib.edf_last_error()
+    rc = lib.edf_fused_gru_block_scan(None, p, p, None, p, None, 0, 2, 4, 64, 2, 1)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+    assert lib.edf_delta_product_backward_workspace_bytes(1, 5, 3, 2, 16, 0) > \
+        lib.edf_delta_product_workspace_bytes(1, 5, 3, 2, 16, 0) > 0
+    assert lib.edf_rla_scan_backward_workspace_bytes(0, 5, 2, 16, 0) == 0
