@@ -401,7 +401,6 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
   // ahead) right after its last use, so no copy of an in-flight load is needed.
   auto body = [&](int it, Pre& P) {
     const int c = chunk_of(it);
-    const long ci = bh * p.nch + c;
     bf16* sa = sA1[it & 1];
     bf16* ss = sSt[it & 1];
     // publish the state entering (forward) / leaving (reverse) chunk c

@@ -13,8 +13,8 @@
 // residual add of the previous layer fused into its prologue), then (2) one small launch per
 // time step for the recurrence: the step's B x G H recurrent dot products spread over H / 4
 // workgroups, each holding 4 units of every gate for 8 batch rows: a workgroup stages its
-// R columns (H x 4 G floats) into LDS with independent loads and splits each dot product over
-// a lane pair, so R is read once per step from
+// R columns (H x 4 G floats, laid out contiguously once per layer) into LDS and splits each
+// dot product over a lane pair, so R is read once per step from
 // L2 by the whole grid, and the cell update needs no cross-workgroup exchange; the launch
 // boundary orders the steps (no grid-wide barrier inside a kernel).
 #include "edf_abi.hpp"
@@ -142,19 +142,34 @@ __global__ __launch_bounds__(256) void rnb_init_kernel(const T* __restrict__ h0,
 }
 
 // One time step of one layer: gates = xp_t + R h_{t-1}, then the cell update.
+// R [H, G H] -> Rt [H / U groups][G U][H] f32: each step workgroup's columns become one
+// contiguous block (read with 16-byte loads every step instead of 16-byte pieces of
+// H rows).  Once per layer and call.
 template <typename T, int G>
-__global__ __launch_bounds__(256) void rnb_step_kernel(const T* __restrict__ R, const float* __restrict__ xp,
+__global__ __launch_bounds__(256) void rnb_rt_kernel(const T* __restrict__ R, float* __restrict__ Rt, int H) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  const int ngrp = (H + RNB_U - 1) / RNB_U;
+  if (e >= (long)ngrp * G * RNB_U * H) return;
+  const int k = (int)(e % H);
+  const long r = e / H;
+  const int gu = (int)(r % (G * RNB_U)), grp = (int)(r / (G * RNB_U));
+  const int g = gu / RNB_U, u = grp * RNB_U + gu % RNB_U;
+  Rt[e] = u < H ? to_f32(R[(long)k * G * H + g * H + u]) : 0.0f;
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void rnb_step_kernel(const float* __restrict__ Rt, const float* __restrict__ xp,
                                                        const float* __restrict__ hs0, float* __restrict__ Hs,
                                                        float* __restrict__ cs, int B, int Tn, int H, int t) {
   __shared__ float sh[RNB_BS][RNB_HMAX];
-  __shared__ float sR[RNB_HMAX][G * RNB_U];  // this workgroup's R columns, all H rows
+  constexpr int LDR = RNB_HMAX + 2;  // sR row stride: the lane pairs' reads hit distinct banks
+  __shared__ float sR[G * RNB_U * LDR];  // this workgroup's R columns [gate, unit][k]
   __shared__ float sd[RNB_BS][G][RNB_U];
   const int tid = threadIdx.x, GH = G * H;
   const int u0 = blockIdx.x * RNB_U, b0 = blockIdx.y * RNB_BS;
-  // independent loads (many in flight per lane) instead of a dependent walk down R's columns
-  for (int e = tid; e < H * G * RNB_U; e += 256) {
-    const int k = e / (G * RNB_U), gu = e % (G * RNB_U), g = gu / RNB_U, u = u0 + gu % RNB_U;
-    sR[k][gu] = u < H ? to_f32(R[(long)k * GH + g * H + u]) : 0.0f;
+  {
+    const float* src = Rt + (long)blockIdx.x * G * RNB_U * H;
+    for (int e = tid; e < G * RNB_U * H; e += 256) sR[(e / H) * LDR + e % H] = src[e];
   }
   for (int e = tid; e < RNB_BS * H; e += 256) {
     const int bb = e / H, k = e % H, b = b0 + bb;
@@ -172,9 +187,9 @@ __global__ __launch_bounds__(256) void rnb_step_kernel(const T* __restrict__ R, 
       int k = half;
       for (; k + 6 < H; k += 8) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) acc[m] = fmaf(sh[bb][k + 2 * m], sR[k + 2 * m][gu], acc[m]);
+        for (int m = 0; m < 4; ++m) acc[m] = fmaf(sh[bb][k + 2 * m], sR[gu * LDR + k + 2 * m], acc[m]);
       }
-      for (; k < H; k += 2) acc[0] = fmaf(sh[bb][k], sR[k][gu], acc[0]);
+      for (; k < H; k += 2) acc[0] = fmaf(sh[bb][k], sR[gu * LDR + k], acc[0]);
     }
     float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     v += __shfl_xor(v, 1);
@@ -213,7 +228,7 @@ __global__ __launch_bounds__(256) void rnb_out_kernel(const float* __restrict__ 
 }
 
 struct RnbWs {
-  float *X, *Hs, *xp, *hs0, *cs;
+  float *X, *Hs, *xp, *hs0, *cs, *Rt;
   size_t total;
 };
 
@@ -233,6 +248,8 @@ inline RnbWs rnb_layout(void* base, long bth, int B, int H, int G) {
   off += rnb_align((size_t)B * H * 4);
   w.cs = (float*)(p + off);
   off += rnb_align((size_t)B * H * 4);
+  w.Rt = (float*)(p + off);
+  off += rnb_align((size_t)((H + RNB_U - 1) / RNB_U) * RNB_U * G * H * 4);
   w.total = off;
   return w;
 }
@@ -252,7 +269,10 @@ int rnb_run(hipStream_t s, const void* input, const void* weights, const void* h
                                                            ws.hs0, ws.cs, B, L, l, H);
     if (int rc = check_launch("rnn block initial state")) return rc;
     const T* Rl = Wl + (long)H * G * H + (long)G * H;
-    for (int t = 0; t < Tn; ++t) rnb_step_kernel<T, G><<<gstep, 256, 0, s>>>(Rl, ws.xp, ws.hs0, ws.Hs, ws.cs, B, Tn, H, t);
+    const long nrt = (long)gstep.x * G * RNB_U * H;
+    rnb_rt_kernel<T, G><<<(unsigned)((nrt + 255) / 256), 256, 0, s>>>(Rl, ws.Rt, H);
+    if (int rc = check_launch("rnn block R layout")) return rc;
+    for (int t = 0; t < Tn; ++t) rnb_step_kernel<G><<<gstep, 256, 0, s>>>(ws.Rt, ws.xp, ws.hs0, ws.Hs, ws.cs, B, Tn, H, t);
     if (int rc = check_launch("rnn block step")) return rc;
   }
   rnb_out_kernel<T><<<(unsigned)((bth + 255) / 256), 256, 0, s>>>(ws.X, ws.Hs, (T*)out, bth);
