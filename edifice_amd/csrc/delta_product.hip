@@ -51,7 +51,27 @@ struct DPStage {
   float redb[DPR_CK][4];        // per-wave beta-gradient sums
 };
 
-EDF_DEVICE bool closes_token(const DPArgs& p, int s) { return s < p.TS && s % p.NH == p.NH - 1; }
+// The sub-steps of the chunk starting at t0 that close a token, as a bit mask over the
+// chunk (bit tt = sub-step t0 + tt), and the token index of the chunk's first closing
+// sub-step: one division per chunk (wave-uniform) instead of one per element or step.
+struct Closing {
+  unsigned mask;
+  int tok0;
+  EDF_DEVICE bool at(int tt) const { return (mask >> tt) & 1u; }
+  EDF_DEVICE int tok(int tt) const { return tok0 + __builtin_popcount(mask & ((1u << tt) - 1u)); }
+};
+
+EDF_DEVICE Closing closing(const DPArgs& p, int t0) {
+  Closing c;
+  c.tok0 = t0 / p.NH;
+  c.mask = 0u;
+  int r = t0 - c.tok0 * p.NH;
+  for (int tt = 0; tt < DPR_CK; ++tt) {
+    if (r == p.NH - 1 && t0 + tt < p.TS) c.mask |= 1u << tt;
+    r = r == p.NH - 1 ? 0 : r + 1;
+  }
+  return c;
+}
 
 // Sum over the 4 rows a wave holds (lanes l, l^16, l^32, l^48 share a column).
 EDF_DEVICE float rows4_sum(float x) {
@@ -71,21 +91,20 @@ EDF_DEVICE void stage(DPStage<DP>& sm, const DPArgs& p, long bh, int rb, int t0,
   constexpr int NC = DP / 16;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H), d = p.d;
   const int tid = threadIdx.x;
+  const Closing cl = closing(p, t0);
   for (int e = tid; e < DPR_CK * DP; e += 256) {
     const int tt = e / DP, j = e % DP, s = t0 + tt;
     const bool ok = s < p.TS && j < d;
     sm.k[tt][j] = ok ? ld((const TT*)p.k, (((long)b * p.TS + s) * p.H + h) * d + j) : 0.0f;
     if (grad) {
-      const bool cl = closes_token(p, s) && j < d;
-      sm.g[tt][j] = cl ? p.dO[(((long)b * p.T + s / p.NH) * p.H + h) * d + j] : 0.0f;
+      sm.g[tt][j] = cl.at(tt) && j < d ? p.dO[(((long)b * p.T + cl.tok(tt)) * p.H + h) * d + j] : 0.0f;
     }
   }
   for (int e = tid; e < DPR_CK * DPR_RB; e += 256) {
     const int tt = e / DPR_RB, ii = e % DPR_RB, i = rb * DPR_RB + ii, s = t0 + tt;
     const bool ok = s < p.TS && i < d;
     sm.v[tt][ii] = ok ? ld((const TT*)p.v, (((long)b * p.TS + s) * p.H + h) * d + i) : 0.0f;
-    const bool cl = closes_token(p, s) && i < d;
-    sm.q[tt][ii] = cl ? ld((const TT*)p.q, (((long)b * p.T + s / p.NH) * p.H + h) * d + i) : 0.0f;
+    sm.q[tt][ii] = cl.at(tt) && i < d ? ld((const TT*)p.q, (((long)b * p.T + cl.tok(tt)) * p.H + h) * d + i) : 0.0f;
   }
   if (tid < DPR_CK) {
     const int s = t0 + tid;
@@ -132,9 +151,10 @@ __global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
     __syncthreads();
     stage<TT, DP>(sm, p, bh, rb, t0, false);
     __syncthreads();
+    const Closing cl = closing(p, t0);
     for (int tt = 0; tt < DPR_CK && t0 + tt < p.TS; ++tt) {
       sub_step<DP>(S, sm, tt, tr, tc);
-      if (p.part_o != nullptr && closes_token(p, t0 + tt)) {
+      if (p.part_o != nullptr && cl.at(tt)) {
         const float qi = sm.q[tt][tr];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -151,9 +171,9 @@ __global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
     if (p.part_o != nullptr) {
       __syncthreads();
       for (int e = tid; e < DPR_CK * DP; e += 256) {
-        const int tt = e / DP, j = e % DP, s = t0 + tt;
-        if (j < p.d && closes_token(p, s)) {
-          const long bth = ((long)b * p.T + s / p.NH) * p.H + h;
+        const int tt = e / DP, j = e % DP;
+        if (j < p.d && cl.at(tt)) {
+          const long bth = ((long)b * p.T + cl.tok(tt)) * p.H + h;
           p.part_o[((long)rb * nbth + bth) * p.d + j] =
               (sm.red[tt][0][j] + sm.red[tt][1][j]) + (sm.red[tt][2][j] + sm.red[tt][3][j]);
         }
@@ -216,6 +236,7 @@ __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
     __syncthreads();
     stage<TT, DP>(sm, p, bh, rb, t0, true);
     __syncthreads();
+    const Closing cl = closing(p, t0);
     float Sl[DPR_CK][NC];  // Sl[tt] = state before sub-step t0 + tt
     {
       float S[NC];
@@ -259,7 +280,7 @@ __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
       if (lane == 0) sm.redb[tt][w] = pb;
       if (s < p.TS && tc == 0 && i < p.d) {
         st((TT*)p.dv, (((long)b * p.TS + s) * p.H + h) * p.d + i, bdk);
-        if (closes_token(p, s)) st((TT*)p.dq, (((long)b * p.T + s / p.NH) * p.H + h) * p.d + i, pq);
+        if (cl.at(tt)) st((TT*)p.dq, (((long)b * p.T + cl.tok(tt)) * p.H + h) * p.d + i, pq);
       }
     }
     __syncthreads();
