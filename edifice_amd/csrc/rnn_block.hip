@@ -6,147 +6,44 @@
 // Per-layer weight packing (as the reference): W_x [H, G H], b_x [G H], R [H, G H], gamma [H],
 // beta [H]; G = 4 (LSTM gates i, f, g, o) or 3 (GRU r, z, n).  LSTM: c = f c + i g,
 // h = o tanh(c).  GRU: n = tanh(x_n + r (R h)_n), h = (1 - z) h + z n.  LayerNorm eps 1e-5.
+// Layer l's input is x^l_t = input_t + sum_{m<l} h^m_t; the block returns x^L.
 //
-// Layout: the reference walks every layer inside one sequential loop over time, one block
-// per batch element streaming both weight matrices from memory at every step.  Here each
-// layer runs as (1) one MFMA kernel for LayerNorm + the input projection of ALL B T rows (the
-// residual add of the previous layer fused into its prologue), then (2) one small launch per
-// time step for the recurrence: the step's B x G H recurrent dot products spread over H / 4
-// workgroups, each holding 4 units of every gate for 8 batch rows: a workgroup stages its
-// R columns (H x 4 G floats, laid out contiguously once per layer) into LDS and splits each
-// dot product over a lane pair, so R is read once per step from
-// L2 by the whole grid, and the cell update needs no cross-workgroup exchange; the launch
-// boundary orders the steps (no grid-wide barrier inside a kernel).
+// Layout: both weight matrices of a layer (2 MB in f32 at H = 256) are too large to stay in
+// one CU, and every step of every layer depends on the step before it, so the recurrence
+// runs as one launch per anti-diagonal j of the (layer, step) grid: launch j computes step
+// t = j - l of every layer l at once (layer l's step t needs layer l-1's step t and its own
+// step t-1, both from launch j-1), T + L - 1 launches in all.  In a launch, H / 4
+// workgroups per layer each own 4 units of every gate for 8 batch rows: they stage their
+// W_x and R columns (laid out unit-major once per call, so each slice is one contiguous
+// block) into LDS, form and LayerNorm the x^l_t rows, take the input and recurrent dot
+// products (each split over a lane pair) and apply the cell update for their units.  The
+// launch boundary orders the diagonals: no grid-wide barrier runs inside a kernel.
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
 namespace edf {
 namespace {
 
-constexpr int RNB_ROWS = 32;   // rows per projection workgroup (one 32x32 MFMA tile height)
 constexpr int RNB_HMAX = 256;  // reference limit (one thread per hidden unit)
-constexpr int RNB_LD = RNB_HMAX + 2;
 constexpr float RNB_LN_EPS = 1.0e-5f;  // fused_lstm_block_scan.cu:113
-constexpr int RNB_U = 4;   // hidden units per step workgroup
-constexpr int RNB_BS = 8;  // batch rows per step workgroup
+constexpr int RNB_U = 4;   // hidden units per workgroup
+constexpr int RNB_BS = 8;  // batch rows per workgroup
+constexpr int RNB_LDR = RNB_HMAX + 2;  // LDS row stride of the weight slices (lane pairs hit distinct banks)
 
 enum { RNB_LSTM = 4, RNB_GRU = 3 };  // value = number of gates
 
-typedef float rnb_f32x16 __attribute__((ext_vector_type(16)));
+struct RnbArgs {
+  const void *input, *weights;
+  const float *Wt, *Rt;  // [L][ngrp][G U][H] unit-major copies of W_x and R
+  const float* hs0;      // [L][B][H] initial h
+  float* cs;             // [L][B][H] LSTM cell state
+  float* Hs;             // [L][B][T][H] every layer's h
+  int B, T, H, L, ngrp;
+};
 
-// Residual + LayerNorm of 32 rows into LDS, then [32 rows] x [G H columns] on
-// v_mfma_f32_32x32x2_f32 with W_x input-major: column n of row k at Wl[k G H + n].
+// M [H, G H] (row k, column g H + u) -> Mt [ngrp][G U][H] f32 for one layer.
 template <typename T, int G>
-__global__ __launch_bounds__(256) void rnb_proj_kernel(const T* __restrict__ input, float* __restrict__ X,
-                                                       const float* __restrict__ Hprev, const T* __restrict__ Wl,
-                                                       float* __restrict__ xp, long rows, int H, int first) {
-  __shared__ float sn[RNB_ROWS * RNB_LD];
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int GH = G * H;
-  const long row0 = (long)blockIdx.x * RNB_ROWS;
-  const T* gamma = Wl + 2L * H * GH + GH;
-  const T* beta = gamma + H;
-  for (int rr = 0; rr < RNB_ROWS / 4; ++rr) {
-    const int r = w * (RNB_ROWS / 4) + rr;
-    const long row = row0 + r;
-    const bool rok = row < rows;
-    float x[RNB_HMAX / 64];
-    float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < RNB_HMAX / 64; ++j) {
-      const int c = lane + 64 * j;
-      const bool ok = rok && c < H;
-      const long idx = ok ? row * H + c : 0;
-      const float v = first ? to_f32(input[idx]) : X[idx] + Hprev[idx];
-      x[j] = ok ? v : 0.0f;
-      if (ok) X[idx] = x[j];
-      sum += x[j];
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    const float mean = sum / (float)H;
-    float var = 0.0f;
-#pragma unroll
-    for (int j = 0; j < RNB_HMAX / 64; ++j) {
-      const float d = (lane + 64 * j < H) ? x[j] - mean : 0.0f;
-      var = fmaf(d, d, var);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) var += __shfl_xor(var, off);
-    const float inv = 1.0f / sqrtf(var / (float)H + RNB_LN_EPS);
-#pragma unroll
-    for (int j = 0; j < RNB_HMAX / 64; ++j) {
-      const int c = lane + 64 * j;
-      if (c < H) sn[r * RNB_LD + c] = fmaf((x[j] - mean) * inv, to_f32(gamma[c]), to_f32(beta[c]));
-      else if (c < RNB_LD) sn[r * RNB_LD + c] = 0.0f;
-    }
-  }
-  __syncthreads();
-  // wave w takes column tiles w, w + 4, ..; lane (li, g) supplies A[row li][k = 2 kk + g] and
-  // B[k][column li]; W values of 16 k steps are loaded a chunk ahead.
-  const int li = lane & 31, g = lane >> 5;
-  const int ntile = (GH + 31) / 32, nch = ((H + 1) / 2 + 15) / 16;
-  for (int nt = w; nt < ntile; nt += 4) {
-    const int n = nt * 32 + li;
-    const bool nok = n < GH;
-    const T* Wc = Wl + min(n, GH - 1);
-    float b0[16], b1[16];
-    auto ldb = [&](float* bb, int ch) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int k = 2 * (16 * ch + i) + g;
-        const float v = to_f32(Wc[(long)min(k, H - 1) * GH]);
-        bb[i] = (nok && k < H) ? v : 0.0f;
-      }
-    };
-    rnb_f32x16 acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    auto mm = [&](const float* bb, int ch) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(sn[li * RNB_LD + 2 * (16 * ch + i) + g], bb[i], acc, 0, 0, 0);
-    };
-    ldb(b0, 0);
-    ldb(b1, min(1, nch - 1));
-    int ch = 0;
-    for (; ch + 1 < nch; ch += 2) {
-      mm(b0, ch);
-      ldb(b0, min(ch + 2, nch - 1));
-      mm(b1, ch + 1);
-      ldb(b1, min(ch + 3, nch - 1));
-    }
-    if (ch < nch) mm(b0, ch);
-    if (nok) {
-      const float bias = to_f32(Wl[(long)H * GH + n]);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long row = row0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (row < rows) xp[row * GH + n] = acc[r] + bias;
-      }
-    }
-  }
-}
-
-// h0[:, l, :] and c0[:, l, :] (or zeros) into the f32 step states.
-template <typename T>
-__global__ __launch_bounds__(256) void rnb_init_kernel(const T* __restrict__ h0, const T* __restrict__ c0,
-                                                       float* __restrict__ hs0, float* __restrict__ cs, int B, int L,
-                                                       int l, int H) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= B * H) return;
-  const int b = e / H, u = e % H;
-  const long src = ((long)b * L + l) * H + u;
-  hs0[e] = h0 != nullptr ? to_f32(h0[src]) : 0.0f;
-  cs[e] = c0 != nullptr ? to_f32(c0[src]) : 0.0f;
-}
-
-// One time step of one layer: gates = xp_t + R h_{t-1}, then the cell update.
-// R [H, G H] -> Rt [H / U groups][G U][H] f32: each step workgroup's columns become one
-// contiguous block (read with 16-byte loads every step instead of 16-byte pieces of
-// H rows).  Once per layer and call.
-template <typename T, int G>
-__global__ __launch_bounds__(256) void rnb_rt_kernel(const T* __restrict__ R, float* __restrict__ Rt, int H) {
+__global__ __launch_bounds__(256) void rnb_rt_kernel(const T* __restrict__ M, float* __restrict__ Mt, int H) {
   const long e = (long)blockIdx.x * 256 + threadIdx.x;
   const int ngrp = (H + RNB_U - 1) / RNB_U;
   if (e >= (long)ngrp * G * RNB_U * H) return;
@@ -154,102 +51,169 @@ __global__ __launch_bounds__(256) void rnb_rt_kernel(const T* __restrict__ R, fl
   const long r = e / H;
   const int gu = (int)(r % (G * RNB_U)), grp = (int)(r / (G * RNB_U));
   const int g = gu / RNB_U, u = grp * RNB_U + gu % RNB_U;
-  Rt[e] = u < H ? to_f32(R[(long)k * G * H + g * H + u]) : 0.0f;
+  Mt[e] = u < H ? to_f32(M[(long)k * G * H + g * H + u]) : 0.0f;
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void rnb_step_kernel(const float* __restrict__ Rt, const float* __restrict__ xp,
-                                                       const float* __restrict__ hs0, float* __restrict__ Hs,
-                                                       float* __restrict__ cs, int B, int Tn, int H, int t) {
-  __shared__ float sh[RNB_BS][RNB_HMAX];
-  constexpr int LDR = RNB_HMAX + 2;  // sR row stride: the lane pairs' reads hit distinct banks
-  __shared__ float sR[G * RNB_U * LDR];  // this workgroup's R columns [gate, unit][k]
-  __shared__ float sd[RNB_BS][G][RNB_U];
-  const int tid = threadIdx.x, GH = G * H;
-  const int u0 = blockIdx.x * RNB_U, b0 = blockIdx.y * RNB_BS;
+// h0[:, l, :] and c0[:, l, :] (or zeros) for every layer, as [L][B][H] f32.
+template <typename T>
+__global__ __launch_bounds__(256) void rnb_init_kernel(const T* __restrict__ h0, const T* __restrict__ c0,
+                                                       float* __restrict__ hs0, float* __restrict__ cs, int B, int L,
+                                                       int H) {
+  const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (long)L * B * H) return;
+  const int u = (int)(e % H), b = (int)((e / H) % B), l = (int)(e / ((long)B * H));
+  const long src = ((long)b * L + l) * H + u;
+  hs0[e] = h0 != nullptr ? to_f32(h0[src]) : 0.0f;
+  cs[e] = c0 != nullptr ? to_f32(c0[src]) : 0.0f;
+}
+
+// Launch j: step t = j - l of layer l = blockIdx.z for units grp * U .. and batch rows
+// blockIdx.y * BS ...
+template <typename T, int G>
+__global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
+  const int l = blockIdx.z, t = j - l;
+  if (t < 0 || t >= p.T) return;  // whole workgroup: outside the (layer, step) grid
+  __shared__ float sW[G * RNB_U * RNB_LDR], sR[G * RNB_U * RNB_LDR];
+  __shared__ float sx[RNB_BS][RNB_HMAX], sh[RNB_BS][RNB_HMAX];
+  __shared__ float sd[2][RNB_BS][G * RNB_U];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, H = p.H, GH = G * H;
+  const int grp = blockIdx.x, u0 = grp * RNB_U, b0 = blockIdx.y * RNB_BS;
+  const long lstride = 2L * H * GH + GH + 2L * H;
+  const T* Wl = (const T*)p.weights + l * lstride;
   {
-    const float* src = Rt + (long)blockIdx.x * G * RNB_U * H;
-    for (int e = tid; e < G * RNB_U * H; e += 256) sR[(e / H) * LDR + e % H] = src[e];
+    const long off = ((long)l * p.ngrp + grp) * G * RNB_U * H;
+    for (int e = tid; e < G * RNB_U * H; e += 256) {
+      const int r = e / H, k = e % H;
+      sW[r * RNB_LDR + k] = p.Wt[off + e];
+      sR[r * RNB_LDR + k] = p.Rt[off + e];
+    }
   }
   for (int e = tid; e < RNB_BS * H; e += 256) {
     const int bb = e / H, k = e % H, b = b0 + bb;
-    float v = 0.0f;
-    if (b < B) v = t == 0 ? hs0[(long)b * H + k] : Hs[((long)b * Tn + t - 1) * H + k];
-    sh[bb][k] = v;
+    float hv = 0.0f, xv = 0.0f;
+    if (b < p.B) {
+      hv = t == 0 ? p.hs0[((long)l * p.B + b) * H + k] : p.Hs[(((long)l * p.B + b) * p.T + t - 1) * H + k];
+      xv = to_f32(((const T*)p.input)[((long)b * p.T + t) * H + k]);
+      for (int m = 0; m < l; ++m) xv += p.Hs[(((long)m * p.B + b) * p.T + t) * H + k];
+    }
+    sh[bb][k] = hv;
+    sx[bb][k] = xv;
   }
   __syncthreads();
-  // each dot product is split over a lane pair (even / odd k), combined with one swizzle
+  // LayerNorm of the 8 x rows: wave w normalizes rows 2 w and 2 w + 1 (biased variance)
+  {
+    const T* gamma = Wl + 2L * H * GH + GH;
+    const T* beta = gamma + H;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      float* row = sx[2 * w + rr];
+      float sum = 0.0f;
+      for (int k = lane; k < H; k += 64) sum += row[k];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+      const float mean = sum / (float)H;
+      float var = 0.0f;
+      for (int k = lane; k < H; k += 64) var = fmaf(row[k] - mean, row[k] - mean, var);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) var += __shfl_xor(var, off);
+      const float inv = 1.0f / sqrtf(var / (float)H + RNB_LN_EPS);
+      for (int k = lane; k < H; k += 64) row[k] = fmaf((row[k] - mean) * inv, to_f32(gamma[k]), to_f32(beta[k]));
+    }
+  }
+  __syncthreads();
+  // input and recurrent dot products, each split over a lane pair (even / odd k)
   {
     const int dot = tid >> 1, half = tid & 1;
     const int bb = dot / (G * RNB_U), gu = dot % (G * RNB_U);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ax[2] = {0.0f, 0.0f}, ar[2] = {0.0f, 0.0f};
     if (dot < RNB_BS * G * RNB_U) {
+      const float* wc = sW + gu * RNB_LDR;
+      const float* rc = sR + gu * RNB_LDR;
       int k = half;
-      for (; k + 6 < H; k += 8) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) acc[m] = fmaf(sh[bb][k + 2 * m], sR[gu * LDR + k + 2 * m], acc[m]);
+      for (; k + 2 < H; k += 4) {
+        ax[0] = fmaf(sx[bb][k], wc[k], ax[0]);
+        ar[0] = fmaf(sh[bb][k], rc[k], ar[0]);
+        ax[1] = fmaf(sx[bb][k + 2], wc[k + 2], ax[1]);
+        ar[1] = fmaf(sh[bb][k + 2], rc[k + 2], ar[1]);
       }
-      for (; k < H; k += 2) acc[0] = fmaf(sh[bb][k], sR[gu * LDR + k], acc[0]);
+      for (; k < H; k += 2) {
+        ax[0] = fmaf(sx[bb][k], wc[k], ax[0]);
+        ar[0] = fmaf(sh[bb][k], rc[k], ar[0]);
+      }
     }
-    float v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    v += __shfl_xor(v, 1);
-    if (half == 0 && dot < RNB_BS * G * RNB_U) sd[bb][gu / RNB_U][gu % RNB_U] = v;
+    float vx = ax[0] + ax[1], vr = ar[0] + ar[1];
+    vx += __shfl_xor(vx, 1);
+    vr += __shfl_xor(vr, 1);
+    if (half == 0 && dot < RNB_BS * G * RNB_U) {
+      sd[0][bb][gu] = vx;
+      sd[1][bb][gu] = vr;
+    }
   }
   __syncthreads();
   if (tid < RNB_BS * RNB_U) {
     const int bb = tid / RNB_U, uu = tid % RNB_U, b = b0 + bb, u = u0 + uu;
-    if (b >= B || u >= H) return;
-    const float* x = xp + ((long)b * Tn + t) * GH + u;
+    if (b >= p.B || u >= H) return;
+    const T* bx = Wl + (long)H * GH;
+    float xg[G], rg[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      xg[g] = sd[0][bb][g * RNB_U + uu] + to_f32(bx[g * H + u]);
+      rg[g] = sd[1][bb][g * RNB_U + uu];
+    }
+    const long si = ((long)l * p.B + b) * H + u;
     const float hp = sh[bb][u];
     float h;
     if constexpr (G == RNB_LSTM) {
-      const float ig = 1.0f / (1.0f + __expf(-(x[0] + sd[bb][0][uu])));
-      const float fg = 1.0f / (1.0f + __expf(-(x[H] + sd[bb][1][uu])));
-      const float gg = tanhf(x[2 * H] + sd[bb][2][uu]);
-      const float og = 1.0f / (1.0f + __expf(-(x[3 * H] + sd[bb][3][uu])));
-      const float c = fmaf(fg, cs[(long)b * H + u], ig * gg);
-      cs[(long)b * H + u] = c;
+      const float ig = 1.0f / (1.0f + __expf(-(xg[0] + rg[0])));
+      const float fg = 1.0f / (1.0f + __expf(-(xg[1] + rg[1])));
+      const float gg = tanhf(xg[2] + rg[2]);
+      const float og = 1.0f / (1.0f + __expf(-(xg[3] + rg[3])));
+      const float c = fmaf(fg, p.cs[si], ig * gg);
+      p.cs[si] = c;
       h = og * tanhf(c);
     } else {
-      const float rg = 1.0f / (1.0f + __expf(-(x[0] + sd[bb][0][uu])));
-      const float zg = 1.0f / (1.0f + __expf(-(x[H] + sd[bb][1][uu])));
-      const float ng = tanhf(fmaf(rg, sd[bb][2][uu], x[2 * H]));
-      h = fmaf(zg, ng - hp, hp);
+      const float r = 1.0f / (1.0f + __expf(-(xg[0] + rg[0])));
+      const float z = 1.0f / (1.0f + __expf(-(xg[1] + rg[1])));
+      const float n = tanhf(fmaf(r, rg[2], xg[2]));
+      h = fmaf(z, n - hp, hp);
     }
-    Hs[((long)b * Tn + t) * H + u] = h;
+    p.Hs[(((long)l * p.B + b) * p.T + t) * H + u] = h;
   }
 }
 
+// out = input + sum_l h^l (the last layer's residual stream).
 template <typename T>
-__global__ __launch_bounds__(256) void rnb_out_kernel(const float* __restrict__ X, const float* __restrict__ Hs,
-                                                      T* __restrict__ out, long n) {
+__global__ __launch_bounds__(256) void rnb_out_kernel(const RnbArgs p, T* __restrict__ out) {
   const long e = (long)blockIdx.x * 256 + threadIdx.x;
-  if (e < n) st(out, e, X[e] + Hs[e]);
+  const long n = (long)p.B * p.T * p.H;
+  if (e >= n) return;
+  float v = to_f32(((const T*)p.input)[e]);
+  for (int l = 0; l < p.L; ++l) v += p.Hs[(long)l * n + e];
+  st(out, e, v);
 }
 
 struct RnbWs {
-  float *X, *Hs, *xp, *hs0, *cs, *Rt;
+  float *Hs, *hs0, *cs, *Wt, *Rt;
   size_t total;
 };
 
 inline size_t rnb_align(size_t v) { return (v + 255) & ~(size_t)255; }
 
-inline RnbWs rnb_layout(void* base, long bth, int B, int H, int G) {
+inline RnbWs rnb_layout(void* base, int B, int Tn, int H, int L, int G) {
+  const size_t ngrp = (H + RNB_U - 1) / RNB_U, slice = ngrp * RNB_U * G * H;
   RnbWs w{};
   size_t off = 0;
   char* p = (char*)base;
-  w.X = (float*)(p + off);
-  off += rnb_align((size_t)bth * 4);
   w.Hs = (float*)(p + off);
-  off += rnb_align((size_t)bth * 4);
-  w.xp = (float*)(p + off);
-  off += rnb_align((size_t)bth * G * 4);
+  off += rnb_align((size_t)L * B * Tn * H * 4);
   w.hs0 = (float*)(p + off);
-  off += rnb_align((size_t)B * H * 4);
+  off += rnb_align((size_t)L * B * H * 4);
   w.cs = (float*)(p + off);
-  off += rnb_align((size_t)B * H * 4);
+  off += rnb_align((size_t)L * B * H * 4);
+  w.Wt = (float*)(p + off);
+  off += rnb_align((size_t)L * slice * 4);
   w.Rt = (float*)(p + off);
-  off += rnb_align((size_t)((H + RNB_U - 1) / RNB_U) * RNB_U * G * H * 4);
+  off += rnb_align((size_t)L * slice * 4);
   w.total = off;
   return w;
 }
@@ -257,25 +221,24 @@ inline RnbWs rnb_layout(void* base, long bth, int B, int H, int G) {
 template <typename T, int G>
 int rnb_run(hipStream_t s, const void* input, const void* weights, const void* h0, const void* c0, void* out,
             const RnbWs& ws, int B, int Tn, int H, int L) {
-  const long bth = (long)B * Tn * H, rows = (long)B * Tn;
-  const long lstride = 2L * H * G * H + (long)G * H + 2L * H;
-  const dim3 gstep((H + RNB_U - 1) / RNB_U, (B + RNB_BS - 1) / RNB_BS);
+  RnbArgs a{};
+  a.input = input; a.weights = weights; a.Wt = ws.Wt; a.Rt = ws.Rt; a.hs0 = ws.hs0; a.cs = ws.cs; a.Hs = ws.Hs;
+  a.B = B; a.T = Tn; a.H = H; a.L = L; a.ngrp = (H + RNB_U - 1) / RNB_U;
+  const long lstride = 2L * H * G * H + (long)G * H + 2L * H, slice = (long)a.ngrp * RNB_U * G * H;
+  const unsigned gslice = (unsigned)((slice + 255) / 256);
   for (int l = 0; l < L; ++l) {
     const T* Wl = (const T*)weights + l * lstride;
-    rnb_proj_kernel<T, G><<<(unsigned)((rows + RNB_ROWS - 1) / RNB_ROWS), 256, 0, s>>>(
-        (const T*)input, ws.X, ws.Hs, Wl, ws.xp, rows, H, l == 0 ? 1 : 0);
-    if (int rc = check_launch("rnn block projection")) return rc;
-    rnb_init_kernel<T><<<(B * H + 255) / 256, 256, 0, s>>>((const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr,
-                                                           ws.hs0, ws.cs, B, L, l, H);
-    if (int rc = check_launch("rnn block initial state")) return rc;
-    const T* Rl = Wl + (long)H * G * H + (long)G * H;
-    const long nrt = (long)gstep.x * G * RNB_U * H;
-    rnb_rt_kernel<T, G><<<(unsigned)((nrt + 255) / 256), 256, 0, s>>>(Rl, ws.Rt, H);
-    if (int rc = check_launch("rnn block R layout")) return rc;
-    for (int t = 0; t < Tn; ++t) rnb_step_kernel<G><<<gstep, 256, 0, s>>>(ws.Rt, ws.xp, ws.hs0, ws.Hs, ws.cs, B, Tn, H, t);
-    if (int rc = check_launch("rnn block step")) return rc;
+    rnb_rt_kernel<T, G><<<gslice, 256, 0, s>>>(Wl, ws.Wt + l * slice, H);
+    rnb_rt_kernel<T, G><<<gslice, 256, 0, s>>>(Wl + (long)H * G * H + (long)G * H, ws.Rt + l * slice, H);
   }
-  rnb_out_kernel<T><<<(unsigned)((bth + 255) / 256), 256, 0, s>>>(ws.X, ws.Hs, (T*)out, bth);
+  if (int rc = check_launch("rnn block weight layout")) return rc;
+  rnb_init_kernel<T><<<(unsigned)(((long)L * B * H + 255) / 256), 256, 0, s>>>(
+      (const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr, ws.hs0, ws.cs, B, L, H);
+  if (int rc = check_launch("rnn block initial state")) return rc;
+  const dim3 grid(a.ngrp, (B + RNB_BS - 1) / RNB_BS, L);
+  for (int j = 0; j < Tn + L - 1; ++j) rnb_diag_kernel<T, G><<<grid, 256, 0, s>>>(a, j);
+  if (int rc = check_launch("rnn block step")) return rc;
+  rnb_out_kernel<T><<<(unsigned)(((long)B * Tn * H + 255) / 256), 256, 0, s>>>(a, (T*)out);
   return check_launch("rnn block output");
 }
 
@@ -288,10 +251,9 @@ int rnb_dispatch(void* stream, const void* input, const void* weights, const voi
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(hidden <= RNB_HMAX, EDF_ERR_UNSUPPORTED, "hidden %d unsupported (the block scans take H <= %d)", hidden,
               RNB_HMAX);
-  EDF_REQUIRE((long)seq_len * hidden * G * 4 < (1L << 31), EDF_ERR_UNSUPPORTED,
-              "seq_len * hidden too large (one batch row of f32 gate projections must stay below 2 GiB)");
+  EDF_REQUIRE(num_layers <= 65535, EDF_ERR_UNSUPPORTED, "num_layers %d too large", num_layers);
   EDF_REQUIRE(input && weights && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
-  const RnbWs L = rnb_layout(workspace, (long)batch * seq_len * hidden, batch, hidden, G);
+  const RnbWs L = rnb_layout(workspace, batch, seq_len, hidden, num_layers, G);
   EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
               L.total);
   if (dtype == EDF_BF16)
@@ -299,9 +261,9 @@ int rnb_dispatch(void* stream, const void* input, const void* weights, const voi
   return rnb_run<float, G>(as_stream(stream), input, weights, h0, c0, out, L, batch, seq_len, hidden, num_layers);
 }
 
-inline size_t rnb_ws_bytes(int batch, int seq_len, int hidden, int G) {
-  if (batch <= 0 || seq_len <= 0 || hidden <= 0) return 0;
-  return rnb_layout(nullptr, (long)batch * seq_len * hidden, batch, hidden, G).total;
+inline size_t rnb_ws_bytes(int batch, int seq_len, int hidden, int num_layers, int G) {
+  if (batch <= 0 || seq_len <= 0 || hidden <= 0 || num_layers <= 0) return 0;
+  return rnb_layout(nullptr, batch, seq_len, hidden, num_layers, G).total;
 }
 
 }  // namespace
@@ -310,15 +272,13 @@ inline size_t rnb_ws_bytes(int batch, int seq_len, int hidden, int G) {
 extern "C" {
 
 size_t edf_lstm_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype) {
-  (void)num_layers;
   (void)dtype;
-  return edf::rnb_ws_bytes(batch, seq_len, hidden, edf::RNB_LSTM);
+  return edf::rnb_ws_bytes(batch, seq_len, hidden, num_layers, edf::RNB_LSTM);
 }
 
 size_t edf_gru_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype) {
-  (void)num_layers;
   (void)dtype;
-  return edf::rnb_ws_bytes(batch, seq_len, hidden, edf::RNB_GRU);
+  return edf::rnb_ws_bytes(batch, seq_len, hidden, num_layers, edf::RNB_GRU);
 }
 
 int edf_fused_lstm_block_scan(void* stream, const void* input, const void* weights, const void* h0, const void* c0,
