@@ -152,7 +152,8 @@ __global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
     stage<TT, DP>(sm, p, bh, rb, t0, false);
     __syncthreads();
     const Closing cl = closing(p, t0);
-    for (int tt = 0; tt < DPR_CK && t0 + tt < p.TS; ++tt) {
+#pragma unroll
+    for (int tt = 0; tt < DPR_CK; ++tt) {  // padding past TS: identity sub-steps, never closing
       sub_step<DP>(S, sm, tt, tr, tc);
       if (p.part_o != nullptr && cl.at(tt)) {
         const float qi = sm.q[tt][tr];

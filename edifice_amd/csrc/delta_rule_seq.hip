@@ -113,14 +113,17 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
     __syncthreads();
     stage_chunk<TT, DP>(sm, p, bh, rb, t0, false);
     __syncthreads();
-    for (int tt = 0; tt < CK && t0 + tt < p.T; ++tt) {
+    // all CK steps unrolled (the staged padding past T makes the extra steps identities), so
+    // the next step's LDS reads can be issued under the current step's arithmetic
+#pragma unroll
+    for (int tt = 0; tt < CK; ++tt) {
       fwd_step<DP>(S, sm, tt, tr, tc);
       if (p.out != nullptr) {  // o_i = sum_j S[i][j] q_j
         float o = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) o = fmaf(S[c], sm.q[tt][tc + 16 * c], o);
         o = row16_sum(o);
-        if (tc == 0 && i < p.d) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
+        if (tc == 0 && i < p.d && t0 + tt < p.T) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
       }
     }
     if (p.ckpt != nullptr) {

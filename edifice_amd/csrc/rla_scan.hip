@@ -127,14 +127,15 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
     __syncthreads();
     rla_stage<TT, CK, DP>(sm, p, bh, rb, t0, false);
     __syncthreads();
-    for (int tt = 0; tt < CK && t0 + tt < p.T; ++tt) {
+#pragma unroll
+    for (int tt = 0; tt < CK; ++tt) {  // padding past T: identity steps (a = 1, b = g = 0, k = 0)
       rla_step<CK, DP, VAR>(S, R, sm, tt, tr, tc, p.clip);
       if (p.out != nullptr) {
         float o = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) o = fmaf(S[c] + R[c], sm.q[tt][tc + 16 * c], o);
         o = row16_sum(o);
-        if (tc == 0 && i < p.d) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
+        if (tc == 0 && i < p.d && t0 + tt < p.T) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
       }
     }
     if (p.ckpt != nullptr) {
