@@ -12,11 +12,11 @@
 // one CU, and every step of every layer depends on the step before it, so the recurrence
 // runs as one launch per anti-diagonal j of the (layer, step) grid: launch j computes step
 // t = j - l of every layer l at once (layer l's step t needs layer l-1's step t and its own
-// step t-1, both from launch j-1), T + L - 1 launches in all.  In a launch, H / 4
-// workgroups per layer each own 4 units of every gate for 8 batch rows: they stage their
+// step t-1, both from launch j-1), T + L - 1 launches in all.  In a launch, H / 2
+// workgroups per layer each own 2 units of every gate for 8 batch rows: they stage their
 // W_x and R columns (laid out unit-major once per call, so each slice is one contiguous
 // block) into LDS, form and LayerNorm the x^l_t rows, take the input and recurrent dot
-// products (each split over a lane pair) and apply the cell update for their units.  The
+// products (each split over a lane quad) and apply the cell update for their units.  The
 // launch boundary orders the diagonals: no grid-wide barrier runs inside a kernel.
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
@@ -26,9 +26,9 @@ namespace {
 
 constexpr int RNB_HMAX = 256;  // reference limit (one thread per hidden unit)
 constexpr float RNB_LN_EPS = 1.0e-5f;  // fused_lstm_block_scan.cu:113
-constexpr int RNB_U = 4;   // hidden units per workgroup
+constexpr int RNB_U = 2;   // hidden units per workgroup
 constexpr int RNB_BS = 8;  // batch rows per workgroup
-constexpr int RNB_LDR = RNB_HMAX + 2;  // LDS row stride of the weight slices (lane pairs hit distinct banks)
+constexpr int RNB_LDR = RNB_HMAX + 4;  // LDS row stride: a wave's (row, k mod 4) reads hit distinct banks
 
 enum { RNB_LSTM = 4, RNB_GRU = 3 };  // value = number of gates
 
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
   const int l = blockIdx.z, t = j - l;
   if (t < 0 || t >= p.T) return;  // whole workgroup: outside the (layer, step) grid
   __shared__ float sW[G * RNB_U * RNB_LDR], sR[G * RNB_U * RNB_LDR];
-  __shared__ float sx[RNB_BS][RNB_HMAX], sh[RNB_BS][RNB_HMAX];
+  __shared__ float sx[RNB_BS][RNB_LDR], sh[RNB_BS][RNB_LDR];
   __shared__ float sd[2][RNB_BS][G * RNB_U];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, H = p.H, GH = G * H;
   const int grp = blockIdx.x, u0 = grp * RNB_U, b0 = blockIdx.y * RNB_BS;
@@ -121,22 +121,22 @@ __global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
     }
   }
   __syncthreads();
-  // input and recurrent dot products, each split over a lane pair (even / odd k)
+  // input and recurrent dot products, each split over a lane quad (k = q, q + 4, ...)
   {
-    const int dot = tid >> 1, half = tid & 1;
+    const int dot = tid >> 2, q = tid & 3;
     const int bb = dot / (G * RNB_U), gu = dot % (G * RNB_U);
     float ax[2] = {0.0f, 0.0f}, ar[2] = {0.0f, 0.0f};
     if (dot < RNB_BS * G * RNB_U) {
       const float* wc = sW + gu * RNB_LDR;
       const float* rc = sR + gu * RNB_LDR;
-      int k = half;
-      for (; k + 2 < H; k += 4) {
+      int k = q;
+      for (; k + 4 < H; k += 8) {
         ax[0] = fmaf(sx[bb][k], wc[k], ax[0]);
         ar[0] = fmaf(sh[bb][k], rc[k], ar[0]);
-        ax[1] = fmaf(sx[bb][k + 2], wc[k + 2], ax[1]);
-        ar[1] = fmaf(sh[bb][k + 2], rc[k + 2], ar[1]);
+        ax[1] = fmaf(sx[bb][k + 4], wc[k + 4], ax[1]);
+        ar[1] = fmaf(sh[bb][k + 4], rc[k + 4], ar[1]);
       }
-      for (; k < H; k += 2) {
+      for (; k < H; k += 4) {
         ax[0] = fmaf(sx[bb][k], wc[k], ax[0]);
         ar[0] = fmaf(sh[bb][k], rc[k], ar[0]);
       }
@@ -144,7 +144,9 @@ __global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
     float vx = ax[0] + ax[1], vr = ar[0] + ar[1];
     vx += __shfl_xor(vx, 1);
     vr += __shfl_xor(vr, 1);
-    if (half == 0 && dot < RNB_BS * G * RNB_U) {
+    vx += __shfl_xor(vx, 2);
+    vr += __shfl_xor(vr, 2);
+    if (q == 0 && dot < RNB_BS * G * RNB_U) {
       sd[0][bb][gu] = vx;
       sd[1][bb][gu] = vr;
     }
