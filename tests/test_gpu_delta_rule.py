@@ -106,6 +106,10 @@ def test_kda_fwd_bwd(shape, dtype, rng):
 DP_CASES = [
     # (B, T, n_h, H, d, dtype)
     (1, 2, 2, 2, 2, torch.float32),       # reference backward test sizes (head_dim 2)
+    # one token: two sub-steps (with one, o_raw = beta (v . q) kn from S = 0 and the RMS norm
+    # removes every dependence on q, v, beta but the 1e-6 one: those gradients are ~1e-4 of
+    # dk and f32 cancellation, not the kernel, sets their relative error)
+    (1, 1, 2, 1, 8, torch.float32),
     (2, 9, 2, 2, 16, torch.float32),
     (1, 37, 3, 2, 64, torch.float32),     # sub-steps not a multiple of the 16-step chunk
     (1, 20, 1, 1, 128, torch.float32),    # n_h = 1
@@ -140,6 +144,7 @@ def test_delta_product_fwd_bwd(case, rng):
 RLA_CASES = [
     # (B, T, H, d, dtype, variant, clip)
     (1, 5, 2, 3, torch.float32, "rla", 0.6),
+    (1, 1, 1, 8, torch.float32, "rdn", 0.6),      # one step
     (2, 21, 2, 16, torch.float32, "rdn", 0.6),
     (1, 37, 2, 64, torch.float32, "rla", 1.0),    # T not a multiple of the 8-step chunk
     (1, 30, 1, 128, torch.float32, "rdn", 1.0),
@@ -176,6 +181,7 @@ def test_rla_fwd_bwd(case, rng):
 TTT_CASES = [
     # (B, T, D, dtype)
     (2, 5, 4, torch.float32),
+    (1, 1, 8, torch.float32),       # one step
     (2, 37, 16, torch.float32),     # T not a multiple of the 8-step chunk
     (3, 20, 50, torch.float32),     # D off the padded widths
     (1, 30, 64, torch.float32),

@@ -258,6 +258,8 @@ def test_mingru_block_full_size(rng):
 RNN_BLOCK_CASES = [
     # (kind, B, T, H, layers, dtype, initial states given)
     ("lstm", 2, 9, 8, 2, torch.float32, True),
+    ("lstm", 1, 1, 16, 3, torch.float32, True),   # one step: every layer on one launch diagonal
+    ("gru", 3, 1, 16, 1, torch.float32, False),
     ("gru", 2, 9, 8, 2, torch.float32, True),
     ("lstm", 3, 17, 50, 3, torch.float32, False),
     ("gru", 9, 6, 33, 1, torch.float32, True),     # B past one 8-row step tile
