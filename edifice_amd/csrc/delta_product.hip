@@ -16,8 +16,9 @@
 // block writes a partial o_raw (summed over its rows through a wave shuffle and LDS) and
 // a small kernel adds the d/16 partials in block order and applies the RMS norm.
 // Backward: dO (the gradient at o_raw) is computed from the re-run forward's partials;
-// dq_t = S_t dO and dv are row-local, the key and beta gradients sum over rows (row-block
-// partials, reduced in order, then taken through the key normalization).  The forward
+// dq_t = S_t dO and dv are row-local, the key and beta gradients sum over rows (per step
+// through an LDS tile of the block's 16 rows, then row-block partials reduced in order and
+// taken through the key normalization).  The forward
 // states are checkpointed every CK sub-steps and recomputed per chunk, never inverted.
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
@@ -223,7 +224,9 @@ template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
   constexpr int NC = DP / 16;
   __shared__ DPStage<DP> sm;
-  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15, w = tid >> 6, lane = tid & 63;
+  __shared__ float redk[DPR_RB][DP + 1];  // this step's per-row key-gradient terms
+  __shared__ float redb[DPR_RB];
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * DPR_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -272,31 +275,33 @@ __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
       for (int c = 0; c < NC; ++c) {
         const float kj = sm.k[tt][tc + 16 * c];
         pq = fmaf(fmaf(be, kj, Sl[tt][c]), sm.g[tt][tc + 16 * c], pq);
-        const float pk = rows4_sum(fmaf(dtot[c], be, -Sl[tt][c] * bdk));
-        if (lane < 16) sm.red[tt][w][tc + 16 * c] = pk;
+        redk[tr][tc + 16 * c] = fmaf(dtot[c], be, -Sl[tt][c] * bdk);
         dS[c] = fmaf(-bdk, kj, dtot[c]);
       }
       pq = row16_sum(pq);
-      const float pb = rows4_sum(tc == 0 ? err * sk : 0.0f);
-      if (lane == 0) sm.redb[tt][w] = pb;
+      if (tc == 0) redb[tr] = i < p.d ? err * sk : 0.0f;
       if (s < p.TS && tc == 0 && i < p.d) {
         st((TT*)p.dv, (((long)b * p.TS + s) * p.H + h) * p.d + i, bdk);
         if (cl.at(tt)) st((TT*)p.dq, (((long)b * p.T + cl.tok(tt)) * p.H + h) * p.d + i, pq);
       }
-    }
-    __syncthreads();
-    for (int e = tid; e < DPR_CK * DP; e += 256) {
-      const int tt = e / DP, j = e % DP, s = t0 + tt;
-      if (j < p.d && s < p.TS) {
+      // the block's sums over its 16 rows, in row order, through LDS
+      __syncthreads();
+      if (s < p.TS) {
         const long bts = ((long)b * p.TS + s) * p.H + h;
-        p.part_k[((long)rb * nbts + bts) * p.d + j] =
-            (sm.red[tt][0][j] + sm.red[tt][1][j]) + (sm.red[tt][2][j] + sm.red[tt][3][j]);
+        for (int j = tid; j < DP; j += 256) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int m = 0; m < DPR_RB; ++m) acc += redk[m][j];
+          if (j < p.d) p.part_k[((long)rb * nbts + bts) * p.d + j] = acc;
+        }
+        if (tid == 255) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int m = 0; m < DPR_RB; ++m) acc += redb[m];
+          p.part_b[(long)rb * nbts + bts] = acc;
+        }
       }
-    }
-    if (tid < DPR_CK && t0 + tid < p.TS) {
-      const long bts = ((long)b * p.TS + t0 + tid) * p.H + h;
-      p.part_b[(long)rb * nbts + bts] =
-          (sm.redb[tid][0] + sm.redb[tid][1]) + (sm.redb[tid][2] + sm.redb[tid][3]);
+      __syncthreads();
     }
   }
 }
