@@ -13,7 +13,7 @@
 // one head, lane (tr, tc) holds columns tc + 16 c of row 16 rb + tr of each, and row sums
 // are 16-lane DPP reductions.  The forward is row-local end to end.  The backward's sums
 // over rows (dq, dk and the three per-head gate gradients) are formed per row block (a
-// 2-step lane shuffle over the wave's 4 rows, then the 4 waves in LDS once per chunk) and
+// per-step LDS tile of the block's 16 rows, summed in row order behind a barrier) and
 // added across blocks in a fixed order by a small kernel.  The forward states are
 // checkpointed every CK = 8 steps and recomputed per chunk (two states per lane, so half
 // the delta kernels' chunk keeps them in registers).
@@ -149,12 +149,6 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
   }
 }
 
-EDF_DEVICE float rla_rows4(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
-}
-
 // Backward over chunks in reverse.  Per step (S_p, R_p before it; dS, dR the adjoints after):
 //   dS_t = dS + do q^T, dR_t = dR + do q^T, dq = (S_n + R_n)^T do, ds_k = dS_t k, dr_k = dR_t k,
 //   m = [|e| <= c], dE_S = g dr_k m (RLA) | b ds_k + g dr_k m (RDN), dE_R = 0 | g dr_k,
@@ -165,9 +159,9 @@ template <typename TT, int DP, int VAR>
 __global__ __launch_bounds__(256) void rla_bwd_kernel(const RLAArgs p) {
   constexpr int NC = DP / 16, CK = RLA_CK;
   __shared__ RStage<CK, DP> sm;
-  __shared__ float red[CK][2][4][DP];  // per-wave sums over its 4 rows: dq, dk
-  __shared__ float reds[CK][3][4];     // per-wave dalpha, dbeta, dgamma
-  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15, w = tid >> 6, lane = tid & 63;
+  __shared__ float red[2][RLA_RB][DP + 1];  // this step's per-row dq and dk terms
+  __shared__ float reds[3][RLA_RB];         // and dalpha, dbeta, dgamma terms
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * RLA_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -231,45 +225,40 @@ __global__ __launch_bounds__(256) void rla_bwd_kernel(const RLAArgs p) {
       for (int c = 0; c < NC; ++c) {
         const float kj = sm.k[tt][tc + 16 * c];
         const float sn = fmaf(cs, kj, a * Sl[tt][c]), rn = fmaf(cr, kj, a * Rl[tt][c]);
-        const float pq = rla_rows4((sn + rn) * goi);
-        const float pk = rla_rows4(fmaf(dts[c], cs, dtr[c] * cr) - fmaf(Sl[tt][c], des, Rl[tt][c] * der));
-        if (lane < 16) {
-          red[tt][0][w][tc + 16 * c] = pq;
-          red[tt][1][w][tc + 16 * c] = pk;
-        }
+        red[0][tr][tc + 16 * c] = (sn + rn) * goi;
+        red[1][tr][tc + 16 * c] = fmaf(dts[c], cs, dtr[c] * cr) - fmaf(Sl[tt][c], des, Rl[tt][c] * der);
         pa = fmaf(dts[c], Sl[tt][c], fmaf(dtr[c], Rl[tt][c], pa));
         dS[c] = fmaf(-des, kj, a * dts[c]);
         dR[c] = fmaf(-der, kj, a * dtr[c]);
       }
       pa = row16_sum(pa);
       const bool row = tc == 0 && i < p.d;
-      const float sa = rla_rows4(row ? pa : 0.0f);
-      const float sb = rla_rows4(row ? dsk * (VAR == 0 ? vi : e) : 0.0f);
-      const float sg = rla_rows4(row ? drk * (VAR == 0 ? re : re - rr) : 0.0f);
-      if (lane == 0) {
-        reds[tt][0][w] = sa;
-        reds[tt][1][w] = sb;
-        reds[tt][2][w] = sg;
+      if (tc == 0) {
+        reds[0][tr] = row ? pa : 0.0f;
+        reds[1][tr] = row ? dsk * (VAR == 0 ? vi : e) : 0.0f;
+        reds[2][tr] = row ? drk * (VAR == 0 ? re : re - rr) : 0.0f;
       }
       if (t < p.T && row) st((TT*)p.dv, (((long)b * p.T + t) * p.H + h) * p.d + i, fmaf(bb, dsk, gm));
-    }
-    __syncthreads();
-    for (int e = tid; e < 2 * CK * DP; e += 256) {
-      const int qty = e / (CK * DP), tt = (e / DP) % CK, j = e % DP, t = t0 + tt;
-      if (j < p.d && t < p.T) {
-        const long bth = ((long)b * p.T + t) * p.H + h;
-        (qty == 0 ? p.part_q : p.part_k)[((long)rb * nbth + bth) * p.d + j] =
-            (red[tt][qty][0][j] + red[tt][qty][1][j]) + (red[tt][qty][2][j] + red[tt][qty][3][j]);
-      }
-    }
-    if (tid < 3 * CK) {
-      const int qty = tid / CK, tt = tid % CK, t = t0 + tt;
+      // the block's sums over its 16 rows, in row order, through LDS
+      __syncthreads();
       if (t < p.T) {
         const long bth = ((long)b * p.T + t) * p.H + h;
-        const int nrb = gridDim.y;
-        p.part_s[((long)qty * nrb + rb) * nbth + bth] =
-            (reds[tt][qty][0] + reds[tt][qty][1]) + (reds[tt][qty][2] + reds[tt][qty][3]);
+        for (int e2 = tid; e2 < 2 * DP; e2 += 256) {
+          const int qty = e2 / DP, j = e2 % DP;
+          float acc = 0.0f;
+#pragma unroll
+          for (int m = 0; m < RLA_RB; ++m) acc += red[qty][m][j];
+          if (j < p.d) (qty == 0 ? p.part_q : p.part_k)[((long)rb * nbth + bth) * p.d + j] = acc;
+        }
+        if (tid >= 253) {
+          const int qty = tid - 253, nrb = gridDim.y;
+          float acc = 0.0f;
+#pragma unroll
+          for (int m = 0; m < RLA_RB; ++m) acc += reds[qty][m];
+          p.part_s[((long)qty * nrb + rb) * nbth + bth] = acc;
+        }
       }
+      __syncthreads();
     }
   }
 }
