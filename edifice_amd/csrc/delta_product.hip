@@ -13,7 +13,7 @@
 // Layout of the work: as in the per-step delta kernels, a workgroup owns RB = 16 value
 // rows of one head's state (lane (tr, tc) holds S[16 rb + tr][tc + 16 c]); the update
 // and the retrieval S kn are row-local.  The output sums over ALL rows, so each row
-// block writes a partial o_raw (summed over its rows through a wave shuffle and LDS) and
+// block writes a partial o_raw (its 16 rows summed in row order through an LDS tile) and
 // a small kernel adds the d/16 partials in block order and applies the RMS norm.
 // Backward: dO (the gradient at o_raw) is computed from the re-run forward's partials;
 // dq_t = S_t dO and dv are row-local, the key and beta gradients sum over rows (per step
@@ -45,11 +45,9 @@ template <int DP>
 struct DPStage {
   float k[DPR_CK][DP];          // normalized key per sub-step (0 beyond TS and d)
   float g[DPR_CK][DP];          // backward: dO of the token a sub-step closes, else 0
-  float red[DPR_CK][4][DP];     // per-wave sums over its 4 rows: raw output / key gradient
   float v[DPR_CK][DPR_RB];      // this block's value rows
   float q[DPR_CK][DPR_RB];      // q rows of the token a sub-step closes, else 0
   float b[DPR_CK];              // beta per sub-step
-  float redb[DPR_CK][4];        // per-wave beta-gradient sums
 };
 
 // The sub-steps of the chunk starting at t0 that close a token, as a bit mask over the
@@ -72,13 +70,6 @@ EDF_DEVICE Closing closing(const DPArgs& p, int t0) {
     r = r == p.NH - 1 ? 0 : r + 1;
   }
   return c;
-}
-
-// Sum over the 4 rows a wave holds (lanes l, l^16, l^32, l^48 share a column).
-EDF_DEVICE float rows4_sum(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
 }
 
 EDF_DEVICE float wave_sum(float x) {
@@ -140,7 +131,8 @@ template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
   constexpr int NC = DP / 16;
   __shared__ DPStage<DP> sm;
-  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15, w = tid >> 6, lane = tid & 63;
+  __shared__ float redo[DPR_RB][DP + 1];  // a closing sub-step's per-row output terms
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * DPR_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -156,30 +148,25 @@ __global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
 #pragma unroll
     for (int tt = 0; tt < DPR_CK; ++tt) {  // padding past TS: identity sub-steps, never closing
       sub_step<DP>(S, sm, tt, tr, tc);
-      if (p.part_o != nullptr && cl.at(tt)) {
+      if (p.part_o != nullptr && cl.at(tt)) {  // the block's 16 rows summed in row order
         const float qi = sm.q[tt][tr];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const float o = rows4_sum(S[c] * qi);
-          if (lane < 16) sm.red[tt][w][tc + 16 * c] = o;
+        for (int c = 0; c < NC; ++c) redo[tr][tc + 16 * c] = S[c] * qi;
+        __syncthreads();
+        const long bth = ((long)b * p.T + cl.tok(tt)) * p.H + h;
+        for (int j = tid; j < p.d; j += 256) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int m = 0; m < DPR_RB; ++m) acc += redo[m][j];
+          p.part_o[((long)rb * nbth + bth) * p.d + j] = acc;
         }
+        __syncthreads();
       }
     }
     if (p.ckpt != nullptr) {
       float* cp = p.ckpt + ((long)bh * p.nck + t0 / DPR_CK) * DP * DP + (long)i * DP + tc;
 #pragma unroll
       for (int c = 0; c < NC; ++c) cp[16 * c] = S[c];
-    }
-    if (p.part_o != nullptr) {
-      __syncthreads();
-      for (int e = tid; e < DPR_CK * DP; e += 256) {
-        const int tt = e / DP, j = e % DP;
-        if (j < p.d && cl.at(tt)) {
-          const long bth = ((long)b * p.T + cl.tok(tt)) * p.H + h;
-          p.part_o[((long)rb * nbth + bth) * p.d + j] =
-              (sm.red[tt][0][j] + sm.red[tt][1][j]) + (sm.red[tt][2][j] + sm.red[tt][3][j]);
-        }
-      }
     }
   }
 }
