@@ -38,9 +38,11 @@ int fwd(void* stream, const void* q, const void* k, const void* v, const void* b
   EDF_REQUIRE(q && k && v && beta && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
   const int per_head = beta_mode == EDF_BETA_PER_HEAD;
   if (dr_chunk_eligible(seq, d, dtype, per_head)) {
+    // As the backward: a missing or short workspace is the caller's error, not a reason to
+    // run the (exact-state, ~10x slower) per-step kernels with different numerics.
     const size_t need = dr_chunk_workspace_bytes(batch, seq, heads, d);
-    if (workspace != nullptr && ws_bytes >= need)
-      return dr_chunk_run(stream, q, k, v, beta, alpha, out, workspace, batch, seq, heads, d);
+    EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+    return dr_chunk_run(stream, q, k, v, beta, alpha, out, workspace, batch, seq, heads, d);
   }
   return dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq, heads, d, dtype, per_head, 0);
 }

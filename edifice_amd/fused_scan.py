@@ -61,6 +61,18 @@ def _c(t):
     return None if t is None else t.contiguous()
 
 
+def _shape(name, t, want):
+    """Raise before any launch when ``t`` is not of shape ``want``: the kernels index every
+    operand by the leading tensor's sizes, so a mismatch would read or write out of bounds."""
+    if t is not None and tuple(t.shape) != tuple(want):
+        raise EdificeHipError(f"{name} must have shape {tuple(want)}, got {tuple(t.shape)}")
+
+
+def _rank(name, t, ndim):
+    if t.dim() != ndim:
+        raise EdificeHipError(f"{name} must be {ndim}-d, got shape {tuple(t.shape)}")
+
+
 # ---------------------------------------------------------------------------
 # MinGRU / MinLSTM
 # ---------------------------------------------------------------------------
@@ -69,6 +81,8 @@ class _MinGRU(torch.autograd.Function):
     @staticmethod
     def forward(ctx, gates, cand):
         gates, cand = gates.contiguous(), cand.contiguous()
+        _rank("gates", gates, 3)
+        _shape("candidates", cand, gates.shape)
         _dev(gates, cand)
         _same(gates, cand)
         bsz, seq, hid = gates.shape
@@ -101,6 +115,9 @@ class _MinLSTM(torch.autograd.Function):
     @staticmethod
     def forward(ctx, fg, ig, cand):
         fg, ig, cand = fg.contiguous(), ig.contiguous(), cand.contiguous()
+        _rank("forget_gates", fg, 3)
+        _shape("input_gates", ig, fg.shape)
+        _shape("candidates", cand, fg.shape)
         _dev(fg, ig, cand)
         _same(fg, ig, cand)
         bsz, seq, hid = fg.shape
@@ -280,11 +297,19 @@ class _SelectiveScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dt, A, B, C, D, z, mode):
         x, dt, A, B, C, D, z = (_c(t) for t in (x, dt, A, B, C, D, z))
+        _rank("x", x, 3)
+        _rank("A", A, 2)
+        bsz, seq, dim = x.shape
+        n = A.shape[1]
+        _shape("dt", dt, x.shape)
+        _shape("z", z, x.shape)
+        _shape("A", A, (dim, n))
+        _shape("B", B, (bsz, seq, n))
+        _shape("C", C, (bsz, seq, n))
+        _shape("D", D, (dim,))
         _dev(x, dt, A, B, C, D, z)
         _same(x, dt, z)
         _same(A, B, C, D)
-        bsz, seq, dim = x.shape
-        n = A.shape[1]
         io, par = dtype_flag(x), dtype_flag(A)
         out = torch.empty_like(x)
         need_grad = any(ctx.needs_input_grad[:7])

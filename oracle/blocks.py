@@ -136,7 +136,7 @@ def load_fixture(path):
 
 
 def _dense(w, prefix, x):
-    return F.linear(x, w[prefix + ".weight"], w[prefix + ".bias"])
+    return F.linear(x, w[prefix + ".weight"], w.get(prefix + ".bias"))
 
 
 def _ln(w, prefix, x):
@@ -153,22 +153,27 @@ def min_gru_model(w, x, ops):
     return _ln(w, "weight.final_norm", h)[:, -1]
 
 
+def delta_net_layer(w, p, h, ops, num_heads):
+    """One DeltaNet layer (delta_net.ex:197-219, :275-307) under key prefix ``p``, residual
+    included: h + out_proj(DeltaRule(q, l2norm(k), v, sigmoid(b)))."""
+    bsz, seq, hid = h.shape
+    hd = hid // num_heads
+    n = _ln(w, p + ".norm", h)
+    proj = _dense(w, p + ".qkvb_proj", n)
+    q, k, v, bpre = torch.split(proj, hid, dim=-1)
+    shp = (bsz, seq, num_heads, hd)
+    q, k, v = q.reshape(shp), k.reshape(shp), v.reshape(shp)
+    beta = torch.sigmoid(bpre).reshape(shp)
+    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + scans.KEY_NORM_EPS)
+    o = ops["delta_net"](q, k, v, beta).reshape(bsz, seq, hid)
+    return h + _dense(w, p + ".out_proj", o)
+
+
 def delta_net_model(w, x, ops, num_heads=4):
     """DeltaNet.build/1 with embed == hidden (no input projection), 2 layers, final LN."""
     h = x
-    bsz, seq, hid = x.shape
-    hd = hid // num_heads
     for li in range(2):
-        p = f"weight.layers.{li}"
-        n = _ln(w, p + ".norm", h)
-        proj = _dense(w, p + ".qkvb_proj", n)
-        q, k, v, bpre = torch.split(proj, hid, dim=-1)
-        shp = (bsz, seq, num_heads, hd)
-        q, k, v = q.reshape(shp), k.reshape(shp), v.reshape(shp)
-        beta = torch.sigmoid(bpre).reshape(shp)
-        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + scans.KEY_NORM_EPS)
-        o = ops["delta_net"](q, k, v, beta).reshape(bsz, seq, hid)
-        h = h + _dense(w, p + ".out_proj", o)
+        h = delta_net_layer(w, f"weight.layers.{li}", h, ops, num_heads)
     return _ln(w, "weight.final_norm", h)[:, -1]
 
 
@@ -195,49 +200,78 @@ def gated_delta_net_model(w, x, ops, num_heads=4, conv_size=4):
     return _ln(w, "weight.final_norm", h)[:, -1]
 
 
+def mamba_block(w, p, h, ops, state_size, conv_size=4):
+    """One Mamba block (common.ex:210-279, SSM :333-471) under key prefix ``p``, WITHOUT the
+    residual (Common.build_model adds it)."""
+    n = _ln(w, p + ".norm", h)
+    xz = _dense(w, p + ".in_proj", n)
+    inner = xz.shape[-1] // 2
+    xb, zb = xz[..., :inner], xz[..., inner:]
+    seq = xb.shape[1]
+    conv = F.conv1d(xb.transpose(1, 2), w[p + ".dw_conv.weight"], w[p + ".dw_conv.bias"],
+                    padding=conv_size - 1, groups=inner)[..., :seq].transpose(1, 2)
+    xa = F.silu(conv)
+    bc = _dense(w, p + ".bc_proj", xa)
+    Bm, Cm = bc[..., :state_size], bc[..., state_size:]
+    dt = F.softplus(_dense(w, p + ".dt_proj", _dense(w, p + ".dt_rank_proj", xa)))
+    A = -(torch.arange(state_size, dtype=h.dtype, device=h.device) + 1.0)
+    A = A[None, :].expand(inner, state_size).contiguous()
+    if "selective_scan_mean_gated" in ops:
+        y = ops["selective_scan_mean_gated"](xa, dt, A, Bm, Cm, zb)
+    else:
+        y = ops["selective_scan_mean"](xa, dt, A, Bm, Cm) * F.silu(zb)
+    return _dense(w, p + ".out_proj", y)
+
+
 def mamba_model(w, x, ops, state_size=8, conv_size=4):
     """Mamba.build/1 via Common.build_model: 2 residual blocks, last timestep (no final LN)."""
     h = x
     for li in range(2):
-        p = f"weight.blocks.{li}"
-        n = _ln(w, p + ".norm", h)
-        xz = _dense(w, p + ".in_proj", n)
-        inner = xz.shape[-1] // 2
-        xb, zb = xz[..., :inner], xz[..., inner:]
-        seq = xb.shape[1]
-        conv = F.conv1d(xb.transpose(1, 2), w[p + ".dw_conv.weight"], w[p + ".dw_conv.bias"],
-                        padding=conv_size - 1, groups=inner)[..., :seq].transpose(1, 2)
-        xa = F.silu(conv)
-        bc = _dense(w, p + ".bc_proj", xa)
-        Bm, Cm = bc[..., :state_size], bc[..., state_size:]
-        dt = F.softplus(_dense(w, p + ".dt_proj", _dense(w, p + ".dt_rank_proj", xa)))
-        A = -(torch.arange(state_size, dtype=x.dtype, device=x.device) + 1.0)
-        A = A[None, :].expand(inner, state_size).contiguous()
-        if "selective_scan_mean_gated" in ops:
-            y = ops["selective_scan_mean_gated"](xa, dt, A, Bm, Cm, zb)
-        else:
-            y = ops["selective_scan_mean"](xa, dt, A, Bm, Cm) * F.silu(zb)
-        h = h + _dense(w, p + ".out_proj", y)
+        h = h + mamba_block(w, f"weight.blocks.{li}", h, ops, state_size, conv_size)
     return h[:, -1]
+
+
+def gqa_block(w, p, h, ops, num_heads, num_kv_heads):
+    """One causal GQA transformer block (attention + GELU FFN, both pre-norm residual)
+    under key prefix ``p``."""
+    bsz, seq, hid = h.shape
+    hd = hid // num_heads
+    grp = num_heads // num_kv_heads
+    n = _ln(w, p + ".attn_norm", h)
+    q = _dense(w, p + ".attn.q_proj", n).reshape(bsz, seq, num_heads, hd).transpose(1, 2)
+    k = _dense(w, p + ".attn.k_proj", n).reshape(bsz, seq, num_kv_heads, hd).transpose(1, 2)
+    v = _dense(w, p + ".attn.v_proj", n).reshape(bsz, seq, num_kv_heads, hd).transpose(1, 2)
+    k = k.repeat_interleave(grp, dim=1).contiguous()
+    v = v.repeat_interleave(grp, dim=1).contiguous()
+    o = ops["causal_attention"](q.contiguous(), k, v)
+    o = o.transpose(1, 2).reshape(bsz, seq, hid)
+    h = h + _dense(w, p + ".attn.out_proj", o)
+    f = _ln(w, p + ".ffn_norm", h)
+    return h + _dense(w, p + ".ffn_down", F.gelu(_dense(w, p + ".ffn_up", f)))
 
 
 def gqa_model(w, x, ops, num_heads=4, num_kv_heads=2):
     """Causal GQA transformer, 2 blocks (attention + GELU FFN), final LN, last timestep."""
     h = x
-    bsz, seq, hid = x.shape
-    hd = hid // num_heads
-    grp = num_heads // num_kv_heads
     for li in range(2):
-        p = f"weight.blocks.{li}"
-        n = _ln(w, p + ".attn_norm", h)
-        q = _dense(w, p + ".attn.q_proj", n).reshape(bsz, seq, num_heads, hd).transpose(1, 2)
-        k = _dense(w, p + ".attn.k_proj", n).reshape(bsz, seq, num_kv_heads, hd).transpose(1, 2)
-        v = _dense(w, p + ".attn.v_proj", n).reshape(bsz, seq, num_kv_heads, hd).transpose(1, 2)
-        k = k.repeat_interleave(grp, dim=1).contiguous()
-        v = v.repeat_interleave(grp, dim=1).contiguous()
-        o = ops["causal_attention"](q.contiguous(), k, v)
-        o = o.transpose(1, 2).reshape(bsz, seq, hid)
-        h = h + _dense(w, p + ".attn.out_proj", o)
-        f = _ln(w, p + ".ffn_norm", h)
-        h = h + _dense(w, p + ".ffn_down", F.gelu(_dense(w, p + ".ffn_up", f)))
+        h = gqa_block(w, f"weight.blocks.{li}", h, ops, num_heads, num_kv_heads)
     return _ln(w, "weight.final_norm", h)[:, -1]
+
+
+def hybrid_decoder_loss(w, tokens, ops, num_heads, state_size=16, conv_size=4, layers=(4, 2, 2)):
+    """The config-5 decoder stack (SURVEY 3.5's assembly from blocks that reach the fused
+    kernels: ModelBuilder.build_sequence_model with output_mode :all, model_builder.ex:71-132):
+    embedding -> Mamba blocks (residual added here) -> DeltaNet layers -> causal attention +
+    FFN blocks -> final LN -> LM head (no bias) -> mean next-token cross entropy over
+    tokens[:, 1:] (the loss of recipes.ex:158-194).  Keys follow edifice_amd.blocks.HybridDecoder
+    under "weight." (embed, mamba.i, delta.i, attn.i, final_norm, lm_head)."""
+    n_mamba, n_delta, n_attn = layers
+    h = F.embedding(tokens[:, :-1], w["weight.embed.weight"])
+    for i in range(n_mamba):
+        h = h + mamba_block(w, f"weight.mamba.{i}", h, ops, state_size, conv_size)
+    for i in range(n_delta):
+        h = delta_net_layer(w, f"weight.delta.{i}", h, ops, num_heads)
+    for i in range(n_attn):
+        h = gqa_block(w, f"weight.attn.{i}", h, ops, num_heads, num_heads)
+    logits = _dense(w, "weight.lm_head", _ln(w, "weight.final_norm", h))
+    return F.cross_entropy(logits.reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1))

@@ -118,3 +118,56 @@ def test_variant_entry_points_validate_before_launch(lib):
     assert lib.edf_delta_product_backward_workspace_bytes(1, 5, 3, 2, 16, 0) > \
         lib.edf_delta_product_workspace_bytes(1, 5, 3, 2, 16, 0) > 0
     assert lib.edf_rla_scan_backward_workspace_bytes(0, 5, 2, 16, 0) == 0
+
+
+def _t(*shape):
+    import torch
+
+    return torch.zeros(shape, dtype=torch.float32)
+
+
+@pytest.mark.parametrize("call, msg", [
+    (lambda fs: fs.mingru(_t(2, 5, 8), _t(2, 5, 9)), "candidates"),
+    (lambda fs: fs.mingru(_t(2, 5), _t(2, 5)), "gates"),
+    (lambda fs: fs.minlstm(_t(2, 5, 8), _t(2, 4, 8), _t(2, 5, 8)), "input_gates"),
+    (lambda fs: fs.minlstm(_t(2, 5, 8), _t(2, 5, 8), _t(1, 5, 8)), "candidates"),
+    (lambda fs: fs.selective_scan(_t(2, 5, 8), _t(2, 5, 7), _t(8, 4), _t(2, 5, 4), _t(2, 5, 4)), "dt"),
+    (lambda fs: fs.selective_scan(_t(2, 5, 8), _t(2, 5, 8), _t(9, 4), _t(2, 5, 4), _t(2, 5, 4)), "A"),
+    (lambda fs: fs.selective_scan(_t(2, 5, 8), _t(2, 5, 8), _t(8, 4), _t(2, 5, 3), _t(2, 5, 4)), "B"),
+    (lambda fs: fs.selective_scan(_t(2, 5, 8), _t(2, 5, 8), _t(8, 4), _t(2, 5, 4), _t(2, 6, 4)), "C"),
+    (lambda fs: fs.selective_scan(_t(2, 5, 8), _t(2, 5, 8), _t(8, 4), _t(2, 5, 4), _t(2, 5, 4), _t(7)), "D"),
+    (lambda fs: fs.selective_scan(_t(2, 5, 8), _t(2, 5, 8), _t(8, 4), _t(2, 5, 4), _t(2, 5, 4), None,
+                                  _t(2, 5, 1)), "z"),
+])
+def test_wrappers_reject_mismatched_shapes_before_launch(call, msg):
+    """The kernels index every operand by the leading tensor's sizes, so the host mirror
+    checks shapes first: the error is raised before device checks or any launch (these
+    tensors are on the CPU, which would otherwise fail the device check)."""
+    from edifice_amd import fused_scan as fs
+    from edifice_amd._native import EdificeHipError
+
+    with pytest.raises(EdificeHipError, match=msg):
+        call(fs)
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_chunked_delta_rule_forward_requires_workspace(lib, gated):
+    """bf16 + per-head beta + head_dim 128 + seq >= 64 selects the chunked kernels: the
+    forward, like the backward, returns EDF_ERR_WORKSPACE (4) for a missing or short
+    workspace instead of silently running the per-step kernels.  The check precedes any
+    device call, so dummy host addresses are never dereferenced."""
+    from edifice_amd import _native
+
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    B, T, H, d, bf16, per_head = 1, 128, 2, 128, 1, 1
+    need = lib.edf_delta_rule_workspace_bytes(B, T, H, d, bf16, per_head)
+    assert need > 0
+    assert lib.edf_delta_rule_workspace_bytes(B, T, H, d, 0, per_head) == 0  # f32: per-step kernels
+    for ws, nbytes in ((None, 0), (p, need - 1)):
+        if gated:
+            rc = lib.edf_fused_gated_delta_net_scan(None, p, p, p, p, p, p, ws, nbytes, B, T, H, d, bf16, per_head)
+        else:
+            rc = lib.edf_fused_delta_net_scan(None, p, p, p, p, p, ws, nbytes, B, T, H, d, bf16, per_head)
+        assert rc == 4, rc
+        assert b"workspace too small" in _native.lib().edf_last_error()

@@ -300,6 +300,117 @@ def test_delta_rule_invariants(rng):
     np.testing.assert_allclose(o[:, 0], v[:, 0] * (k[:, 0] ** 2).sum(-1, keepdims=True), rtol=1e-12)
 
 
+def _gdn_two_step(q, k, v, beta, alpha):
+    """GatedDeltaNet at T = 2 written out from gated_delta_net.ex:322-344 (S0 = 0), in torch.
+
+    Step 1 stores S1 = (beta1 v1) k1^T (decaying the empty state does nothing).  Step 2
+    decays BEFORE the retrieval: s_gated = alpha2 S1 (:327), retrieval = s_gated k2
+    (:330-332), S2 = s_gated + (beta2 (v2 - retrieval)) k2^T (:335-338), o2 = S2 q2
+    (:341-344), so
+        o1 = beta1 v1 (k1.q1)
+        o2 = alpha2 beta1 v1 (k1.q2) + beta2 (v2 - alpha2 beta1 v1 (k1.k2)) (k2.q2).
+    q, k, v, beta: [B, 2, H, d] (beta may be [B, 2, H]); alpha: [B, 2, H]."""
+    if beta.dim() == 3:
+        beta = beta[..., None].expand(v.shape)
+
+    def dot(a, b):
+        return (a * b).sum(-1, keepdim=True)
+
+    q1, q2, k1, k2, v1, v2 = q[:, 0], q[:, 1], k[:, 0], k[:, 1], v[:, 0], v[:, 1]
+    b1, b2, a2 = beta[:, 0], beta[:, 1], alpha[:, 1, :, None]
+    o1 = b1 * v1 * dot(k1, q1)
+    o2 = a2 * b1 * v1 * dot(k1, q2) + b2 * (v2 - a2 * b1 * v1 * dot(k1, k2)) * dot(k2, q2)
+    return torch.stack([o1, o2], dim=1)
+
+
+@pytest.mark.parametrize("beta_per_head", [False, True])
+def test_gated_delta_rule_two_step_closed_form(rng, beta_per_head):
+    """Pins the GatedDeltaNet decay order (decay, then retrieve from the decayed state) and,
+    through torch autograd of the written-out closed form, every gradient of the oracle's
+    backward at T = 2.  alpha2 != 1 and per-element beta make the alternative orders
+    (retrieve from the undecayed state; decay after the update) differ visibly."""
+    bsz, H, d = 2, 3, 4
+    q, k, v = (rng.normal(size=(bsz, 2, H, d)) for _ in range(3))
+    beta = rng.uniform(0.2, 0.9, size=(bsz, 2, H) if beta_per_head else (bsz, 2, H, d))
+    alpha = rng.uniform(0.3, 0.7, size=(bsz, 2, H))
+    do = rng.normal(size=(bsz, 2, H, d))
+    tq, tk, tv, tb, ta = (torch.tensor(a, dtype=torch.float64, requires_grad=True)
+                          for a in (q, k, v, beta, alpha))
+    closed = _gdn_two_step(tq, tk, tv, tb, ta)
+    np.testing.assert_allclose(scans.delta_rule(q, k, v, beta, alpha), closed.detach().numpy(),
+                               rtol=1e-12, atol=1e-12)
+
+    # the closed form tells the orders apart: retrieval from the undecayed state differs
+    b4 = np.broadcast_to(beta[..., None], v.shape) if beta_per_head else beta
+    kk = (k[:, 0] * k[:, 1]).sum(-1, keepdims=True)
+    kq = (k[:, 1] * q[:, 1]).sum(-1, keepdims=True)
+    undecayed_retrieval = (alpha[:, 1, :, None] * b4[:, 0] * v[:, 0] * (k[:, 0] * q[:, 1]).sum(-1, keepdims=True)
+                           + b4[:, 1] * (v[:, 1] - b4[:, 0] * v[:, 0] * kk) * kq)
+    assert np.abs(undecayed_retrieval - closed.detach().numpy()[:, 1]).max() > 1e-2
+
+    closed.backward(torch.from_numpy(do))
+    g = scans.delta_rule_backward(q, k, v, beta, do, alpha)
+    for name, t in (("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb), ("dalpha", ta)):
+        np.testing.assert_allclose(g[name], t.grad.numpy(), rtol=1e-10, atol=1e-12, err_msg=name)
+
+
+def _ss_mean_two_step(x, dt, A, B, C):
+    """The block CPU (dt-mean) selective scan at T = 2 written out from common.ex:402-445
+    (discretize_ssm), :492-513 (sequential_scan, h[-1] = 0) and :462-471
+    (compute_ssm_output), in torch, with an arbitrary A[d, n] in place of the block's
+    fixed -(1..N):
+      clip first (:413): c = clip(dt, 1e-3, 0.1); m_t = mean_d c_t (:439-441)
+      h1 = m1 B1 x1;  h2 = exp(c2 A) h1 + m2 B2 x2;  y_t = sum_n C_t,n h_t,n
+    x, dt: [B, 2, D]; A: [D, N]; B, C: [B, 2, N]."""
+    c = dt.clamp(scans.DT_MIN, scans.DT_MAX)
+    m = c.mean(dim=2, keepdim=True)  # [B, 2, 1]
+    h1 = m[:, 0, :, None] * B[:, 0, None, :] * x[:, 0, :, None]  # [B, D, N]
+    h2 = torch.exp(c[:, 1, :, None] * A[None]) * h1 + m[:, 1, :, None] * B[:, 1, None, :] * x[:, 1, :, None]
+    y1 = (C[:, 0, None, :] * h1).sum(-1)
+    y2 = (C[:, 1, None, :] * h2).sum(-1)
+    return torch.stack([y1, y2], dim=1)
+
+
+def test_selective_scan_mean_mode_closed_forms(rng):
+    """Pins the dt-mean mode: (1) with A = 0, y_t,d = sum_n C_t,n sum_{s<=t} m_s B_s,n x_s,d
+    over a long sequence; (2) at T = 2 with A != 0, the decay uses each channel's own clipped
+    dt while the input term uses the channel mean of the clipped dt — forward and (torch
+    autograd of the written-out form) every gradient.  dt spreads over [1e-3, 0.1] with a few
+    values outside it, so the clip acts before the mean and mean mode differs from channel
+    mode."""
+    bsz, D, N = 2, 6, 3
+    # (1) A = 0 over T = 9
+    T = 9
+    x = rng.normal(size=(bsz, T, D))
+    dt = rng.uniform(0.002, 0.095, size=(bsz, T, D))
+    dt[0, 2, 1], dt[1, 4, 3] = 0.4, 1e-4  # clipped to 0.1 and 1e-3 before the mean
+    B, C = rng.normal(size=(bsz, T, N)), rng.normal(size=(bsz, T, N))
+    m = np.clip(dt, 1e-3, 0.1).mean(axis=2)  # [B, T]
+    acc = np.cumsum(m[:, :, None, None] * B[:, :, None, :] * x[:, :, :, None], axis=1)  # [B,T,D,N]
+    want = np.einsum("btdn,btn->btd", acc, C)
+    got = scans.selective_scan(x, dt, np.zeros((D, N)), B, C, mode="mean")
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    chan = scans.selective_scan(x, dt, np.zeros((D, N)), B, C, mode="channel")
+    assert np.abs(chan - got).max() > 1e-2 * np.abs(got).max()
+
+    # (2) T = 2, arbitrary negative A, forward and gradients
+    x2 = rng.normal(size=(bsz, 2, D))
+    dt2 = rng.uniform(0.002, 0.095, size=(bsz, 2, D))
+    dt2[0, 1, 2] = 0.3
+    A = -np.exp(rng.uniform(0.0, np.log(16.0), size=(D, N)))
+    B2, C2 = rng.normal(size=(bsz, 2, N)), rng.normal(size=(bsz, 2, N))
+    dy = rng.normal(size=(bsz, 2, D))
+    tx, tdt, tA, tB, tC = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (x2, dt2, A, B2, C2))
+    closed = _ss_mean_two_step(tx, tdt, tA, tB, tC)
+    np.testing.assert_allclose(scans.selective_scan(x2, dt2, A, B2, C2, mode="mean"),
+                               closed.detach().numpy(), rtol=1e-12, atol=1e-12)
+    closed.backward(torch.from_numpy(dy))
+    g = scans.selective_scan_backward(x2, dt2, A, B2, C2, dy, mode="mean")
+    for name, t in (("dx", tx), ("ddt", tdt), ("dA", tA), ("dB", tB), ("dC", tC)):
+        np.testing.assert_allclose(g[name], t.grad.numpy(), rtol=1e-10, atol=1e-12, err_msg=name)
+    assert g["ddt"][0, 1, 2] == 0.0  # clipped entry gets no gradient
+
+
 def test_flash_attention_matches_sdpa_and_invariants(rng):
     bsz, H, T, d = 2, 3, 7, 8
     q, k, v = (rng.normal(size=(bsz, H, T, d)) for _ in range(3))
