@@ -33,6 +33,10 @@
 //     per block, and the raw inputs are prefetched four blocks ahead;
 //   * the forward writes the state every CK = 16 timesteps ("checkpoints", layout
 //     [b][chunk][n][d], coalesced over d);
+//   * any state size 1..32 (the reference's limit): the kernels are compiled for the next
+//     power of two NP >= N and the states past N are padding, with A = B = C = 0 loaded
+//     for them, so they stay 0 and add nothing; A, B, C, dA, dB and dC keep the caller's
+//     stride N, checkpoints and partial sums the padded NP;
 //   * backward: chunks are walked in reverse; each chunk's states and decays are
 //     recomputed from its checkpoint into registers, then the reverse recurrence runs
 //     with the same lane layout.  Sums over states (dx, ddt) are in-lane plus an LDS
@@ -70,6 +74,7 @@ struct SSArgs {
   float* part_d;   // [batch, dim]
   float* part_m;   // [ntile, batch, seq] (mean mode)
   int batch, seq, dim, nck, ntile;
+  int nst;  // the caller's state count N (<= the kernel's padded NP): stride of A, B, C rows
 };
 
 // lane = channel; K = min(N, KMAX) states per lane (at least N / 16, so a workgroup
@@ -135,10 +140,11 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
   const bool cvalid = c < dim;
   const int cc = min(c, dim - 1);
 
+  const int ns = p.nst;
   float A2[K], h[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) {
-    A2[s] = cvalid ? ld(Am, (long)c * N + w * K + s) * LOG2E : 0.0f;
+    A2[s] = (cvalid && w * K + s < ns) ? ld(Am, (long)c * ns + w * K + s) * LOG2E : 0.0f;
     h[s] = 0.0f;
   }
   const float Dc = (Dv != nullptr && cvalid) ? ld(Dv, c) : 0.0f;
@@ -167,13 +173,15 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
       if (HAS_Z) rz[slot][i] = (z + row)[cc];
       rm[slot][i] = MEAN ? p.dtmean[(long)b * seq + min(t0 + w + i * NW, seq - 1)] : 0.0f;
     }
-    const long bc0 = ((long)b * seq + t0) * N + w * K;
+    const long bc0 = ((long)b * seq + t0) * ns;
     const int tmax = seq - 1 - t0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int v = (16 * r + (lane & 15)) % (TS * K);
-      const int off = min(v / K, tmax) * N + v % K;
-      rbc[slot][r] = to_f32((r < R / 2 ? Bm : Cm)[bc0 + off]);
+      const int st = w * K + v % K;  // padding states (st >= ns) load index 0 and use 0
+      const int off = st < ns ? min(v / K, tmax) * ns + st : 0;
+      const float val = to_f32((r < R / 2 ? Bm : Cm)[bc0 + off]);
+      rbc[slot][r] = st < ns ? val : 0.0f;
     }
   };
   auto stage = [&](int slot, int t0, int buf, float* xs, float* zs) {
@@ -271,16 +279,18 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
                                                                       const TP* __restrict__ Cm) {
   using G = SSGeo<N, KMAX>;
   constexpr int K = G::K, NW = G::NW, NT = G::NT;
-  static_assert(K == 2 || K == 4, "backward keeps two or four states per lane");
+  static_assert(K == 1 || K == 2 || K == 4, "backward keeps one, two or four states per lane");
   constexpr int CK = SS_CK;          // recompute chunk (= checkpoint interval)
-  constexpr int TS = 8;              // reduction block (timesteps)
+  constexpr int TS = 16 / K;         // reduction block (timesteps): 2 K TS = 32 outputs per wave
+  constexpr bool BC_REG = K <= 2;    // the chunk's B/C values held in registers (else read from LDS)
   constexpr int PS = CK + 4;         // [channel][t] row stride (16-byte reads conflict-free)
   constexpr int EPT = CK * 64 / NT;  // staged (t, channel) elements per thread
   constexpr int GS = 2 * K * TS + 4;  // per-lane stride of a wave's dC/dB tile: b128 writes conflict-free
   constexpr int OPW = 2 * K * TS;     // dC/dB outputs per wave per block
   constexpr int LPO = 64 / OPW;       // lanes per output (each sums 64 / LPO channels)
-  static_assert(EPT * NW == CK && CK % TS == 0 && (LPO == 1 || LPO == 2), "staging layout");
-  constexpr int BCT = CK * 2 * N / NT;  // staged B/C values per thread
+  static_assert(EPT * NW == CK && CK % TS == 0 && LPO == 2, "staging layout");
+  constexpr int BCN = CK * 2 * N;               // B/C values staged per chunk
+  constexpr int BCT = (BCN + NT - 1) / NT;      // per thread (the last round partly idle)
   __shared__ __align__(16) float s_bc[CK][2 * N];  // per t: B[0..N), C[0..N)
   __shared__ __align__(16) float s_dtc[64][PS];
   __shared__ __align__(16) float s_dtx[64][PS];
@@ -309,10 +319,11 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   const int cc = min(c, dim - 1);
   auto pp = [&](int q, int v, int t) -> float& { return s_pp[((q * NW + v) * CK + t) * 64 + lane]; };
 
+  const int ns = p.nst;
   float A1[K], A2[K], dh[K], dA[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) {
-    A1[s] = cvalid ? ld(Am, (long)c * N + w * K + s) : 0.0f;
+    A1[s] = (cvalid && w * K + s < ns) ? ld(Am, (long)c * ns + w * K + s) : 0.0f;
     A2[s] = A1[s] * LOG2E;
     dh[s] = 0.0f;
     dA[s] = 0.0f;
@@ -329,8 +340,8 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   const rsrc_t r_x = make_rsrc(x + rowbase, rowbytes), r_dt = make_rsrc(dt + rowbase, rowbytes);
   const rsrc_t r_do = make_rsrc(dout + rowbase, rowbytes);
   const rsrc_t r_z = make_rsrc(HAS_Z ? z + rowbase : x + rowbase, rowbytes);
-  const unsigned bcbytes = (unsigned)((long)seq * N * sizeof(TP));
-  const rsrc_t r_B = make_rsrc(Bm + (long)b * seq * N, bcbytes), r_C = make_rsrc(Cm + (long)b * seq * N, bcbytes);
+  const unsigned bcbytes = (unsigned)((long)seq * ns * sizeof(TP));
+  const rsrc_t r_B = make_rsrc(Bm + (long)b * seq * ns, bcbytes), r_C = make_rsrc(Cm + (long)b * seq * ns, bcbytes);
   const rsrc_t r_m =
       make_rsrc(MEAN ? (const void*)(p.dtmean + (long)b * seq) : (const void*)x, (unsigned)(seq * sizeof(float)));
   const rsrc_t r_dx = make_rsrc((TI*)p.dx + rowbase, rowbytes), r_ddt = make_rsrc((TI*)p.ddt + rowbase, rowbytes);
@@ -354,9 +365,11 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
     }
 #pragma unroll
     for (int i = 0; i < BCT; ++i) {
-      const int e = tid + i * NT;
+      const int e = min(tid + i * NT, BCN - 1);  // clamped: the load stays unconditional
       const int r = e % (2 * N);
-      const unsigned off = ((unsigned)min(ts + e / (2 * N), seq - 1) * N + (r % N)) * (unsigned)sizeof(TP);
+      // padding states (r % N >= ns) read 0 through an out-of-range offset
+      const unsigned off = r % N < ns ? ((unsigned)min(ts + e / (2 * N), seq - 1) * ns + (r % N)) * (unsigned)sizeof(TP)
+                                      : OOB_OFF;
       // lanes split between B and C: both loads issue, the other one out of bounds reads 0
       rbc[i] = bload<TP>(r_B, r < N ? off : OOB_OFF) | bload<TP>(r_C, r < N ? OOB_OFF : off);
     }
@@ -375,7 +388,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 #pragma unroll
     for (int i = 0; i < BCT; ++i) {
       const int e = tid + i * NT;
-      s_bc[e / (2 * N)][e % (2 * N)] = bits_f32(rbc[i]);
+      if (BCN % NT == 0 || e < BCN) s_bc[e / (2 * N)][e % (2 * N)] = bits_f32(rbc[i]);
     }
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
@@ -406,7 +419,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
     // ---- recompute the chunk's states and decays from its checkpoint ---------------
     // states, decays and this wave's B/C values of the chunk, kept in registers for the
     // reverse pass (reading B/C from LDS once per chunk halves that LDS traffic)
-    float h0[K], hs[CK][K], as[CK][K], bB[CK][K], bC[CK][K];
+    float h0[K], hs[CK][K], as[CK][K], bB[BC_REG ? CK : 1][K], bC[BC_REG ? CK : 1][K];
 #pragma unroll
     for (int s = 0; s < K; ++s)
       h0[s] = (k > 0 && cvalid) ? ck0[s] : 0.0f;
@@ -427,13 +440,15 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
           float acc = 0.0f;
 #pragma unroll
           for (int s = 0; s < K; ++s) {
-            bB[j][s] = bc[s];
-            bC[j][s] = bc[N + s];
+            if constexpr (BC_REG) {
+              bB[j][s] = bc[s];
+              bC[j][s] = bc[N + s];
+            }
             const float a = fast_exp2(dcv[u] * A2[s]);
-            hh[s] = fmaf(a, hh[s], dxv[u] * bB[j][s]);
+            hh[s] = fmaf(a, hh[s], dxv[u] * bc[s]);
             as[j][s] = a;
             hs[j][s] = hh[s];
-            if (HAS_Z) acc = fmaf(bC[j][s], hh[s], acc);
+            if (HAS_Z) acc = fmaf(bc[N + s], hh[s], acc);
           }
           if (HAS_Z) pp(0, w, j) = acc;
         }
@@ -482,8 +497,8 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         float px = 0.0f, pa = 0.0f, gC[K], gB[K];
 #pragma unroll
         for (int s = 0; s < K; ++s) {
-          const float Bv = bB[jj][s];
-          const float Cv = bC[jj][s];
+          const float Bv = BC_REG ? bB[BC_REG ? jj : 0][s] : s_bc[jj][w * K + s];
+          const float Cv = BC_REG ? bC[BC_REG ? jj : 0][s] : s_bc[jj][N + w * K + s];
           dh[s] = fmaf(dyv[j], Cv, dh[s]);
           gC[s] = dyv[j] * hs[jj][s];
           gB[s] = dh[s] * dxv[j];
@@ -496,8 +511,10 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
         if constexpr (K == 4) {
           *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gC[2], gC[3]);
           *reinterpret_cast<float4*>(g + j * 2 * K + K) = make_float4(gB[0], gB[1], gB[2], gB[3]);
-        } else {
+        } else if constexpr (K == 2) {
           *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gB[0], gB[1]);
+        } else {
+          *reinterpret_cast<float2*>(g + j * 2 * K) = make_float2(gC[0], gB[0]);
         }
         pp(0, w, jj) = px;
         pp(1, w, jj) = pa;
@@ -514,7 +531,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 #pragma unroll 16
         for (int l = 0; l < 64 / LPO; ++l) acc += src[l * GS];
         __builtin_amdgcn_wave_barrier();  // and the reads before the next block's writes
-        if (LPO == 2) acc += __shfl_xor(acc, 32);
+        acc += __shfl_xor(acc, 32);
         const int j = o / (2 * K), qty = (o / K) % 2, n = w * K + o % K;
         const int t = ts + jb + j;
         if (hf == 0 && t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + qty) * N + n] = acc;
@@ -565,34 +582,40 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
   }
 }
 
-// dB, dC = sum over channel tiles
+// dB, dC = sum over channel tiles; partials carry NP (padded) states, outputs ns
 __global__ __launch_bounds__(256) void ss_reduce_bc_kernel(const float* __restrict__ part, float* __restrict__ dB,
-                                                           float* __restrict__ dC, int ntile, long rows, int N) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // over rows * 2N
-  const long total = rows * 2 * N;
+                                                           float* __restrict__ dC, int ntile, long rows, int NP,
+                                                           int ns) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // over rows * 2NP
+  const long total = rows * 2 * NP;
   if (i >= total) return;
+  const long row = i / (2 * NP);
+  const int r = (int)(i % (2 * NP));
+  const int qty = r / NP, nn = r % NP;
+  if (nn >= ns) return;
   float acc = 0.0f;
   for (int tl = 0; tl < ntile; ++tl) acc += part[(long)tl * total + i];
-  const long row = i / (2 * N);
-  const int r = (int)(i % (2 * N));
-  const int qty = r / N, nn = r % N;
   if (qty == 0) {
-    if (dC) dC[row * N + nn] = acc;
+    if (dC) dC[row * ns + nn] = acc;
   } else {
-    if (dB) dB[row * N + nn] = acc;
+    if (dB) dB[row * ns + nn] = acc;
   }
 }
 
-// dA[d, n] = sum_b part_a; dD[d] = sum_b part_d
+// dA[d, n] = sum_b part_a (NP padded states per channel); dD[d] = sum_b part_d
 __global__ __launch_bounds__(256) void ss_reduce_ad_kernel(const float* __restrict__ part_a,
                                                            const float* __restrict__ part_d, float* __restrict__ dA,
-                                                           float* __restrict__ dD, int batch, int dim, int N) {
+                                                           float* __restrict__ dD, int batch, int dim, int NP,
+                                                           int ns) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
-  const long na = (long)dim * N;
+  const long na = (long)dim * NP;
   if (i < na) {
+    const long d = i / NP;
+    const int n = (int)(i % NP);
+    if (n >= ns) return;
     float acc = 0.0f;
     for (int bb = 0; bb < batch; ++bb) acc += part_a[(long)bb * na + i];
-    if (dA) dA[i] = acc;
+    if (dA) dA[d * ns + n] = acc;
   } else if (i < na + dim) {
     const long d = i - na;
     float acc = 0.0f;
@@ -621,7 +644,14 @@ __global__ __launch_bounds__(256) void ss_mean_fixup_kernel(const float* __restr
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-inline bool pow2_state(int N) { return N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32; }
+constexpr int SS_MAX_STATE = 32;  // the reference's limit (fused_selective_scan.cu:57-76, _backward.cu:59)
+
+// the power of two the kernels are compiled for: NP >= N, the states past N are padding
+inline int padded_state(int N) {
+  int np = 1;
+  while (np < N) np *= 2;
+  return np;
+}
 
 // one workgroup per (batch, 64-channel tile)
 inline int ntiles(int dim) { return (dim + 63) / 64; }
@@ -634,7 +664,8 @@ struct WsLayout {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-inline WsLayout bwd_layout(int batch, int seq, int dim, int N, bool need_ckpt, bool mean_mode) {
+inline WsLayout bwd_layout(int batch, int seq, int dim, int nst, bool need_ckpt, bool mean_mode) {
+  const int N = padded_state(nst);
   WsLayout w{};
   const long nck = num_chunks(seq);
   const int nt = ntiles(dim);
@@ -678,9 +709,10 @@ void launch_fwd_k(hipStream_t s, const SSArgs& a) {
 
 // States per lane.  Backward: two (2 waves per SIMD at config-2 size, 192 workgroups of 8
 // waves), which hides the LDS and exp latencies better than four states per lane at 1 wave
-// per SIMD (measured on MI355X: 722 vs 811 us).  Forward: one (16 waves per workgroup, 4 per
-// SIMD; 190 vs 200 us with two states per lane, interleaved A/B).
-constexpr int SS_KMAX = 2;
+// per SIMD (measured on MI355X: 722 vs 811 us); at NP = 32 four (8 waves), since 16 waves'
+// dC/dB tiles and state-sum partials do not fit the 160 KB of LDS.  Forward: one (16 waves
+// per workgroup, 4 per SIMD; 190 vs 200 us with two states per lane, interleaved A/B).
+template <int N> constexpr int ss_kmax_bwd() { return N >= 32 ? 4 : 2; }
 constexpr int SS_KMAX_FWD = 1;
 
 template <typename TI, typename TP, int N>
@@ -689,15 +721,15 @@ void launch_fwd_t(hipStream_t s, const SSArgs& a) {
 }
 
 template <typename TI, typename TP>
-int launch_fwd_n(hipStream_t s, const SSArgs& a, int N) {
-  switch (N) {
+int launch_fwd_n(hipStream_t s, const SSArgs& a, int nst) {
+  switch (padded_state(nst)) {
     case 1: launch_fwd_t<TI, TP, 1>(s, a); break;
     case 2: launch_fwd_t<TI, TP, 2>(s, a); break;
     case 4: launch_fwd_t<TI, TP, 4>(s, a); break;
     case 8: launch_fwd_t<TI, TP, 8>(s, a); break;
     case 16: launch_fwd_t<TI, TP, 16>(s, a); break;
     case 32: launch_fwd_t<TI, TP, 32>(s, a); break;
-    default: return set_error(EDF_ERR_UNSUPPORTED, "state size %d unsupported (1, 2, 4, 8, 16 or 32)", N);
+    default: return set_error(EDF_ERR_UNSUPPORTED, "state size %d unsupported (1..32)", nst);
   }
   return check_launch("selective scan");
 }
@@ -717,16 +749,19 @@ void launch_bwd_k(hipStream_t s, const SSArgs& a) {
 
 template <typename TI, typename TP, int N>
 void launch_bwd_t(hipStream_t s, const SSArgs& a) {
-  launch_bwd_k<TI, TP, N, SS_KMAX>(s, a);
+  launch_bwd_k<TI, TP, N, ss_kmax_bwd<N>()>(s, a);
 }
 
 template <typename TI, typename TP>
-int launch_bwd_n(hipStream_t s, const SSArgs& a, int N) {
-  switch (N) {
+int launch_bwd_n(hipStream_t s, const SSArgs& a, int nst) {
+  switch (padded_state(nst)) {
+    case 1: launch_bwd_t<TI, TP, 1>(s, a); break;
+    case 2: launch_bwd_t<TI, TP, 2>(s, a); break;
     case 4: launch_bwd_t<TI, TP, 4>(s, a); break;
     case 8: launch_bwd_t<TI, TP, 8>(s, a); break;
     case 16: launch_bwd_t<TI, TP, 16>(s, a); break;
-    default: return set_error(EDF_ERR_UNSUPPORTED, "backward state size %d unsupported (4, 8 or 16)", N);
+    case 32: launch_bwd_t<TI, TP, 32>(s, a); break;
+    default: return set_error(EDF_ERR_UNSUPPORTED, "state size %d unsupported (1..32)", nst);
   }
   return check_launch("selective scan backward");
 }
@@ -742,7 +777,7 @@ int by_dtypes(int io, int par, F&& f) {
 int check_common(int batch, int seq, int dim, int N, int io, int par, int mode) {
   EDF_REQUIRE(batch > 0 && seq > 0 && dim > 0 && N > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
   EDF_REQUIRE(valid_dtype(io) && valid_dtype(par), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
-  EDF_REQUIRE(pow2_state(N), EDF_ERR_UNSUPPORTED, "state size %d unsupported (1, 2, 4, 8, 16 or 32)", N);
+  EDF_REQUIRE(N <= SS_MAX_STATE, EDF_ERR_UNSUPPORTED, "state size %d unsupported (1..%d)", N, SS_MAX_STATE);
   EDF_REQUIRE(mode == EDF_SS_DT_PER_CHANNEL || mode == EDF_SS_DT_MEAN, EDF_ERR_INVALID_ARG, "unknown dt mode %d",
               mode);
   return EDF_OK;
@@ -765,7 +800,7 @@ extern "C" {
 
 size_t edf_selective_scan_states_bytes(int batch, int seq_len, int hidden, int state) {
   if (batch <= 0 || seq_len <= 0 || hidden <= 0 || state <= 0) return 0;
-  return (size_t)batch * edf::num_chunks(seq_len) * state * hidden * sizeof(float);
+  return (size_t)batch * edf::num_chunks(seq_len) * edf::padded_state(state) * hidden * sizeof(float);
 }
 
 size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode) {
@@ -794,7 +829,7 @@ int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const 
   SSArgs a{};
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z; a.out = out;
   a.ckpt = (float*)states;
-  a.batch = batch; a.seq = seq_len; a.dim = hidden;
+  a.batch = batch; a.seq = seq_len; a.dim = hidden; a.nst = state;
   a.nck = (int)num_chunks(seq_len);
   a.ntile = ntiles(hidden);
   if (mode == EDF_SS_DT_MEAN) {
@@ -818,8 +853,6 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   using namespace edf;
   int rc = check_common(batch, seq_len, hidden, state, io_dtype, param_dtype, mode);
   if (rc) return rc;
-  EDF_REQUIRE(state == 4 || state == 8 || state == 16, EDF_ERR_UNSUPPORTED,
-              "backward state size %d unsupported (4, 8 or 16)", state);
   EDF_REQUIRE(x && dt && A && B && C && grad_out && grad_x && grad_dt, EDF_ERR_INVALID_ARG, "null tensor pointer");
   // the backward kernel addresses one batch row of x, dt, dy, z, dx, ddt, dz (and of B, C)
   // through a buffer resource with 32-bit byte offsets
@@ -834,7 +867,7 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   char* ws = (char*)workspace;
   SSArgs a{};
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z;
-  a.batch = batch; a.seq = seq_len; a.dim = hidden;
+  a.batch = batch; a.seq = seq_len; a.dim = hidden; a.nst = state;
   a.nck = (int)num_chunks(seq_len);
   a.ntile = ntiles(hidden);
   if (mean_mode) {
@@ -868,17 +901,18 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   });
   if (rc) return rc;
   const long rows = (long)batch * seq_len;
+  const int np = padded_state(state);
   if (grad_B || grad_C) {
-    const long total = rows * 2 * state;
+    const long total = rows * 2 * np;
     ss_reduce_bc_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(a.part_bc, (float*)grad_B, (float*)grad_C,
-                                                                        a.ntile, rows, state);
+                                                                        a.ntile, rows, np, state);
     rc = check_launch("selective scan dB/dC reduction");
     if (rc) return rc;
   }
   if (grad_A || grad_D) {
-    const long total = (long)hidden * state + hidden;
+    const long total = (long)hidden * np + hidden;
     ss_reduce_ad_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(a.part_a, a.part_d, (float*)grad_A,
-                                                                        (float*)grad_D, batch, hidden, state);
+                                                                        (float*)grad_D, batch, hidden, np, state);
     rc = check_launch("selective scan dA/dD reduction");
     if (rc) return rc;
   }

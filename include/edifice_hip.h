@@ -194,7 +194,7 @@ size_t edf_gru_block_workspace_bytes(int batch, int seq_len, int hidden, int num
  * Extensions: per-tensor dtypes (io vs param), optional D skip (NULL = none)
  * and silu(z) gate (NULL = none), and `states`, an optional float32 buffer of
  * edf_selective_scan_states_bytes() that receives checkpoints for the backward.
- * state must be 1, 2, 4, 8, 16 or 32 (the reference allowed <= 32). */
+ * state: 1..32, as the reference (fused_selective_scan.cu:57-76 keeps h_state[32]). */
 int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const void* A, const void* B, const void* C,
                              const void* D, const void* z, void* out, void* states, void* workspace,
                              size_t workspace_bytes, int batch, int seq_len, int hidden, int state, int io_dtype,
@@ -206,7 +206,8 @@ size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, in
  * hidden, state, dtype), whose concatenated output was [dx | ddt | dB | dC]
  * (native/cuda/fused_selective_scan_backward.cu:198-238).  Adds grad_A, grad_D,
  * grad_z (each may be NULL).  `states` may be NULL: the checkpoints are then
- * recomputed into the workspace.  state must be 4, 8 or 16. */
+ * recomputed into the workspace.  state: 1..32, as the reference (MAX_STATE 32,
+ * fused_selective_scan_backward.cu:59). */
 int edf_fused_selective_scan_backward(void* stream, const void* x, const void* dt, const void* A, const void* B,
                                       const void* C, const void* D, const void* z, const void* grad_out,
                                       const void* states, void* grad_x, void* grad_dt, void* grad_A, void* grad_B,

@@ -67,9 +67,10 @@ def test_nonpositive_dims_rejected(lib, call):
 def test_bad_dtype_and_unsupported_shapes(lib):
     assert lib.edf_fused_mingru_scan(None, None, None, None, None, 1, 1, 1, 7) == 1
     assert b"dtype" in lib.edf_last_error()
-    # selective-scan backward supports state sizes 4, 8, 16
-    rc = lib.edf_fused_selective_scan_backward(*([None] * 18), 0, 1, 8, 8, 32, 0, 0, 0)
-    assert rc == 2 and b"state size" in lib.edf_last_error()
+    # the selective scan takes state sizes 1..32, as the reference (MAX_STATE 32)
+    for fn, nargs in ((lib.edf_fused_selective_scan_backward, 18), (lib.edf_fused_selective_scan, 11)):
+        rc = fn(*([None] * nargs), 0, 1, 8, 8, 33, 0, 0, 0)
+        assert rc == 2 and b"state size" in lib.edf_last_error()
     # a missing workspace is reported, not dereferenced
     rc = lib.edf_fused_flash_attention_backward(*([ctypes.c_void_p(16)] * 10), None, 0, 1, 1, 8, 64, 1, 1)
     assert rc == 4 and b"workspace" in lib.edf_last_error()
@@ -86,6 +87,9 @@ def test_workspace_queries(lib):
     # one float32 state per (b, chunk of 16 timesteps, n, d)
     assert lib.edf_selective_scan_states_bytes(8, 2048, 1536, 16) == 8 * 128 * 16 * 1536 * 4
     assert lib.edf_selective_scan_states_bytes(1, 17, 3, 4) == 2 * 4 * 3 * 4
+    # other state sizes are held padded to the next power of two
+    assert lib.edf_selective_scan_states_bytes(1, 17, 3, 12) == 2 * 16 * 3 * 4
+    assert lib.edf_selective_scan_states_bytes(1, 16, 3, 32) == 1 * 32 * 3 * 4
     assert lib.edf_flash_attention_backward_workspace_bytes(4, 32, 4096, 128) == 4 * 32 * 4096 * 4
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 1, 1) > 0  # chunked path
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 0, 1) == 0  # f32: step path

@@ -33,6 +33,17 @@ CASES = [
     (2, 45, 32, 8, torch.float32, torch.float32, False, "mean"),
     (2, 45, 32, 16, torch.float32, torch.float32, True, "mean"),
     (1, 1, 16, 16, torch.float32, torch.float32, True, "channel"),
+    # every state size up to the reference's 32, powers of two or not (padded inside)
+    (2, 40, 24, 1, torch.float32, torch.float32, True, "channel"),
+    (2, 40, 24, 2, torch.float32, torch.float32, False, "channel"),
+    (2, 37, 24, 3, torch.float32, torch.float32, True, "channel"),
+    (2, 50, 40, 12, torch.float32, torch.float32, True, "channel"),
+    (1, 45, 72, 12, torch.bfloat16, torch.float32, True, "channel"),
+    (2, 33, 24, 12, torch.float32, torch.float32, True, "mean"),
+    (2, 41, 24, 24, torch.float32, torch.float32, True, "channel"),
+    (2, 70, 48, 32, torch.float32, torch.float32, True, "channel"),
+    (1, 64, 80, 32, torch.bfloat16, torch.float32, True, "channel"),
+    (2, 35, 24, 32, torch.float32, torch.float32, False, "mean"),
 ]
 
 
