@@ -48,6 +48,7 @@ SIGNATURES = {
     "edf_fused_flash_attention": (I, [P, P, P, P, P, P, I, I, I, I, I, I]),
     "edf_fused_flash_attention_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_flash_attention_backward_workspace_bytes": (S, [I, I, I, I]),
+    "edf_fused_flash_attention_backward_noalloc": (I, [P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I]),
     "edf_fused_fox_attention": (I, [P, P, P, P, P, P, P, I, I, I, I, I]),
     "edf_fused_fox_attention_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_fox_attention_backward_workspace_bytes": (S, [I, I, I, I]),

@@ -24,6 +24,7 @@
 #include "edf_common.hpp"
 #include "edf_mfma.hpp"
 
+#include <mutex>
 #include <type_traits>
 
 namespace edf {
@@ -592,33 +593,28 @@ void launch_wave_bwd(hipStream_t s, const void* q, const void* k, const void* v,
 #undef EDF_FA_WAVE_BWD
 }
 
-}  // namespace
-}  // namespace edf
-
-extern "C" {
-
-size_t edf_flash_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim) {
-  if (batch <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return 0;
-  return (size_t)batch * num_heads * seq_len * sizeof(float);
-}
-
-int edf_fused_flash_attention_backward(void* stream, const void* q, const void* k, const void* v, const void* out,
-                                       const void* grad_out, const float* lse, void* grad_q, void* grad_k,
-                                       void* grad_v, void* workspace, size_t workspace_bytes, int batch,
-                                       int num_heads, int seq_len, int head_dim, int causal, int dtype) {
-  using namespace edf;
+// ---------------------------------------------------------------------------
+// host side: argument checks and the launch sequence shared by the entry points
+// ---------------------------------------------------------------------------
+int fa_bwd_check(const void* q, const void* k, const void* v, const void* out, const void* grad_out, const float* lse,
+                 const void* grad_q, const void* grad_k, const void* grad_v, int batch, int num_heads, int seq_len,
+                 int head_dim, int dtype) {
   EDF_REQUIRE(batch > 0 && num_heads > 0 && seq_len > 0 && head_dim > 0, EDF_ERR_INVALID_ARG,
               "dimensions must be positive");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(head_dim <= 256, EDF_ERR_UNSUPPORTED, "head_dim %d > 256 unsupported", head_dim);
   EDF_REQUIRE(q && k && v && out && grad_out && lse && grad_q && grad_k && grad_v, EDF_ERR_INVALID_ARG,
               "null tensor pointer (the forward's lse is required)");
-  const size_t need = edf_flash_attention_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
-  EDF_REQUIRE(workspace && workspace_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
-  hipStream_t s = as_stream(stream);
+  return EDF_OK;
+}
+
+// D = rowsum(dO o O) into Dd [B*H*T] (every entry written before it is read), then the dK/dV
+// and dQ kernels.
+int fa_bwd_run(hipStream_t s, const void* q, const void* k, const void* v, const void* out, const void* grad_out,
+               const float* lse, void* grad_q, void* grad_k, void* grad_v, float* Dd, int batch, int num_heads,
+               int seq_len, int head_dim, int causal, int dtype) {
   const int BH = batch * num_heads;
   const long rows = (long)BH * seq_len;
-  float* Dd = (float*)workspace;
   const unsigned gd = (unsigned)((rows + 15) / 16);
   if (dtype == EDF_BF16)
     fa_bwd_dot_kernel<bf16><<<gd, 256, 0, s>>>((const bf16*)out, (const bf16*)grad_out, Dd, rows, head_dim);
@@ -646,6 +642,95 @@ int edf_fused_flash_attention_backward(void* stream, const void* q, const void* 
                            scale_log2, scale);
   }
   return check_launch("flash attention backward");
+}
+
+// ---------------------------------------------------------------------------
+// Scratch for the allocation-free backward: D lives in a file-scope device array of
+// EDF_FA_NOALLOC_SCRATCH_BYTES, of which each GPU holds its own copy (from module load until
+// the process ends).  In host code `scratch` names a host-side stand-in, not a device address,
+// so kernels get the device address that hipGetSymbolAddress returns, looked up once per
+// device with that device current and cached.  Calls on one GPU share its copy: calls that
+// overlap in time on one GPU (two streams) race on it.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[EDF_FA_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int FA_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[FA_MAX_DEVICES] = {};
+
+int scratch_address(hipStream_t s, float** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return set_error(EDF_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  int dev = cur;
+  if (s != nullptr) {  // the stream's device (the kernels run there), not only the current one
+    e = hipStreamGetDevice(s, &dev);
+    if (e != hipSuccess) return set_error(EDF_ERR_LAUNCH, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+  }
+  EDF_REQUIRE(dev >= 0 && dev < FA_MAX_DEVICES, EDF_ERR_UNSUPPORTED, "device %d beyond %d", dev, FA_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return set_error(EDF_ERR_LAUNCH, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(e));
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t back = hipSetDevice(cur);
+      if (e == hipSuccess && back != hipSuccess)
+        return set_error(EDF_ERR_LAUNCH, "hipSetDevice(%d) failed: %s", cur, hipGetErrorString(back));
+    }
+    if (e != hipSuccess || p == nullptr)
+      return set_error(EDF_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return EDF_OK;
+}
+
+}  // namespace
+}  // namespace edf
+
+extern "C" {
+
+
+size_t edf_flash_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim) {
+  if (batch <= 0 || num_heads <= 0 || seq_len <= 0 || head_dim <= 0) return 0;
+  return (size_t)batch * num_heads * seq_len * sizeof(float);
+}
+
+int edf_fused_flash_attention_backward(void* stream, const void* q, const void* k, const void* v, const void* out,
+                                       const void* grad_out, const float* lse, void* grad_q, void* grad_k,
+                                       void* grad_v, void* workspace, size_t workspace_bytes, int batch,
+                                       int num_heads, int seq_len, int head_dim, int causal, int dtype) {
+  using namespace edf;
+  int rc = fa_bwd_check(q, k, v, out, grad_out, lse, grad_q, grad_k, grad_v, batch, num_heads, seq_len, head_dim,
+                        dtype);
+  if (rc) return rc;
+  const size_t need = edf_flash_attention_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(workspace && workspace_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  return fa_bwd_run(as_stream(stream), q, k, v, out, grad_out, lse, grad_q, grad_k, grad_v, (float*)workspace, batch,
+                    num_heads, seq_len, head_dim, causal, dtype);
+}
+
+int edf_fused_flash_attention_backward_noalloc(void* stream, const void* q, const void* k, const void* v,
+                                               const void* out, const void* grad_out, const float* lse,
+                                               void* grad_q, void* grad_k, void* grad_v, int batch, int num_heads,
+                                               int seq_len, int head_dim, int causal, int dtype) {
+  using namespace edf;
+  int rc = fa_bwd_check(q, k, v, out, grad_out, lse, grad_q, grad_k, grad_v, batch, num_heads, seq_len, head_dim,
+                        dtype);
+  if (rc) return rc;
+  const size_t need = edf_flash_attention_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(need <= EDF_FA_NOALLOC_SCRATCH_BYTES, EDF_ERR_UNSUPPORTED,
+              "batch * heads * seq_len = %zu exceeds the no-alloc scratch (%zu rows, %d MiB)", need / sizeof(float),
+              (size_t)EDF_FA_NOALLOC_SCRATCH_BYTES / sizeof(float), (int)(EDF_FA_NOALLOC_SCRATCH_BYTES >> 20));
+  hipStream_t s = as_stream(stream);
+  float* Dd = nullptr;
+  rc = scratch_address(s, &Dd);
+  if (rc) return rc;
+  return fa_bwd_run(s, q, k, v, out, grad_out, lse, grad_q, grad_k, grad_v, Dd, batch, num_heads, seq_len, head_dim,
+                    causal, dtype);
 }
 
 size_t edf_fox_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim) {

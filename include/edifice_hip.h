@@ -324,6 +324,21 @@ int edf_fused_flash_attention_backward(void* stream, const void* q, const void* 
                                        int num_heads, int seq_len, int head_dim, int causal, int dtype);
 size_t edf_flash_attention_backward_workspace_bytes(int batch, int num_heads, int seq_len, int head_dim);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * flash-attention backward above with no workspace argument.  D lives in a library-owned
+ * device array of EDF_FA_NOALLOC_SCRATCH_BYTES that every GPU the library runs on holds
+ * until the process ends, so batch * num_heads * seq_len must not exceed
+ * EDF_FA_NOALLOC_SCRATCH_BYTES / 4 (EDF_ERR_UNSUPPORTED otherwise).  Nothing is allocated
+ * per call.  All calls on one GPU share that array: calls that overlap in time on one GPU
+ * (e.g. on two streams) race and must be serialised by the caller.  Results are identical to
+ * edf_fused_flash_attention_backward's. */
+#define EDF_FA_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int edf_fused_flash_attention_backward_noalloc(void* stream, const void* q, const void* k, const void* v,
+                                               const void* out, const void* grad_out, const float* lse,
+                                               void* grad_q, void* grad_k, void* grad_v, int batch, int num_heads,
+                                               int seq_len, int head_dim, int causal, int dtype);
+
 /* FoX (forgetting) attention, always causal: scores QK^T/sqrt(d) + (cs_i - cs_j) with
  * cs [B, H, T] the cumulative log forget gate.  Replaces fused_fox_attention/9 (q, k, v,
  * cs, batch, heads, seq, head_dim, dtype), lib/edifice/cuda/nif.ex:106 ->

@@ -175,3 +175,13 @@ def test_chunked_delta_rule_forward_requires_workspace(lib, gated):
             rc = lib.edf_fused_delta_net_scan(None, p, p, p, p, p, ws, nbytes, B, T, H, d, bf16, per_head)
         assert rc == 4, rc
         assert b"workspace too small" in _native.lib().edf_last_error()
+
+
+def test_noalloc_flash_backward_rejects_sizes_beyond_its_scratch(lib):
+    """The allocation-free flash backward holds D in a fixed library-owned array of
+    EDF_FA_NOALLOC_SCRATCH_BYTES (16 MiB = 4M rows of batch * heads * seq_len): larger calls get
+    EDF_ERR_UNSUPPORTED (2) from the host-side check, before any device work."""
+    p = ctypes.c_void_p(16)
+    rows_max = (16 << 20) // 4
+    rc = lib.edf_fused_flash_attention_backward_noalloc(None, *([p] * 9), 1, 1, rows_max + 1, 64, 1, 1)
+    assert rc == 2 and b"no-alloc scratch" in lib.edf_last_error()
