@@ -12,6 +12,12 @@ Algorithmic bytes (per call, what roofline.achieved divides by):
   MinGRU fwd = 3*B*T*H*s, bwd = 6*B*T*H*s (s = element size)
   linear scan fwd = 3*B*T*H*s (a, b in; h out), bwd = 5*B*T*H*s (a, h, dy in; da, db out)
 
+Timing: the headline value times exactly K fwd+bwd steps (after W warm-ups) with host
+synchronisation on both sides; every per-kernel figure (and each config's roofline) is the
+median of max(K, 50) HIP-event timed runs after max(W, 10) warm-ups, events recorded on the
+stream the kernels are launched on; the scan rows evict the caches before each timed run with
+a 256 MiB fill (the 256 MB MALL could otherwise hold a whole scan's inputs).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru,linear,block]
 """
 from __future__ import annotations
@@ -38,26 +44,49 @@ def ss_bytes(B, T, D, N):
     return fwd, bwd
 
 
-class EventTimer:
-    """Accumulates the duration of enqueued work with HIP events on the current stream."""
+MIN_RUNS, MIN_WARMUP = 50, 10
+
+
+class Flush:
+    """Cache eviction between timed runs: a 256 MiB fill kernel on the current stream."""
 
     def __init__(self, torch):
-        self.torch = torch
-        self.pairs = []
+        self.buf = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
 
-    def __enter__(self):
-        self.s = self.torch.cuda.Event(enable_timing=True)
-        self.e = self.torch.cuda.Event(enable_timing=True)
-        self.s.record()
-        return self
+    def __call__(self):
+        self.buf.fill_(1.0)
 
-    def __exit__(self, *a):
-        self.e.record()
-        self.pairs.append((self.s, self.e))
 
-    def mean_ms(self):
-        self.torch.cuda.synchronize()
-        return float(np.mean([s.elapsed_time(e) for s, e in self.pairs]))
+def median_ms(torch, fn, runs, warmup, flush=None):
+    """Median duration (ms) of one call of ``fn`` over ``runs`` timed runs after ``warmup``
+    untimed ones, from HIP events on torch's current stream (the stream every entry point here
+    launches on); ``flush`` runs before each timed call, outside the events."""
+    for _ in range(warmup):
+        fn()
+    pairs = []
+    for _ in range(runs):
+        if flush is not None:
+            flush()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        pairs.append((s, e))
+    torch.cuda.synchronize()
+    return float(np.median([s.elapsed_time(e) for s, e in pairs]))
+
+
+def roofline(bound, work, ms, kernels=None, profile=None):
+    """Roofline dict for ``work`` algorithmic bytes ("hbm") or flops ("mfma") done in ``ms``;
+    ``traffic`` is the HBM bytes of the named kernels per call from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary ``profiles/<profile>`` (None when not profiled)."""
+    if bound == "hbm":
+        achieved, peak, unit = work / ms / 1e6, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = work / ms / 1e9, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s"
+    traffic = profiled_traffic(kernels, os.path.join(ROOT, "profiles", profile)) if kernels and profile else None
+    return {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
 def bench_selective_scan(torch, steps, warmup, B=8, T=2048, D=1536, N=16):
@@ -95,24 +124,28 @@ def bench_selective_scan(torch, steps, warmup, B=8, T=2048, D=1536, N=16):
         nat.call("edf_fused_selective_scan_backward", stream, P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(dy),
                  P(states), P(dx), P(ddt), P(dA), P(dB), P(dC), P(dD), P(dz), P(ws), wsb, B, T, D, N, 1, 0, 0)
 
+    # the headline step: exactly `steps` fwd+bwd steps after `warmup`, host-synchronised
     for _ in range(warmup):
         fwd()
         bwd()
     torch.cuda.synchronize()
-    tf, tb = EventTimer(torch), EventTimer(torch)
     t0 = time.perf_counter()
     for _ in range(steps):
-        with tf:
-            fwd()
-        with tb:
-            bwd()
+        fwd()
+        bwd()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
+    # per-kernel medians (caches evicted before each run)
+    runs, wu, fl = max(steps, MIN_RUNS), max(warmup, MIN_WARMUP), Flush(torch)
+    fwd_ms = median_ms(torch, fwd, runs, wu, fl)
+    bwd_ms = median_ms(torch, bwd, runs, wu, fl)
     fb, bb = ss_bytes(B, T, D, N)
-    fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
     _ = fs  # imported for its side effect of validating the package import
-    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, step_ms=wall * 1e3, fwd_bytes=fb, bwd_bytes=bb,
-                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6, step_gbs=(fb + bb) / (wall * 1e3) / 1e6)
+    return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, step_ms=wall * 1e3, fwd_bytes=fb, bwd_bytes=bb, runs=runs,
+                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6, step_gbs=(fb + bb) / (wall * 1e3) / 1e6,
+                roofline=roofline("hbm", fb + bb, fwd_ms + bwd_ms,
+                                  ["ss_fwd_kernel", "ss_bwd_kernel", "ss_reduce_bc_kernel", "ss_reduce_ad_kernel"],
+                                  "selective_scan_c2.md"))
 
 
 def bench_mingru(torch, steps, warmup, B, T, H, dtype):
@@ -134,20 +167,14 @@ def bench_mingru(torch, steps, warmup, B, T, H, dtype):
     def bwd():
         nat.call("edf_mingru_backward", stream, P(gates), P(cand), P(out), P(dy), P(dg), P(dc), B, T, H, flag)
 
-    for _ in range(warmup):
-        fwd()
-        bwd()
-    tf, tb = EventTimer(torch), EventTimer(torch)
-    for _ in range(steps):
-        with tf:
-            fwd()
-        with tb:
-            bwd()
+    runs, wu, fl = max(steps, MIN_RUNS), max(warmup, MIN_WARMUP), Flush(torch)
+    fwd_ms, bwd_ms = median_ms(torch, fwd, runs, wu, fl), median_ms(torch, bwd, runs, wu, fl)
     s = gates.element_size()
-    fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
     fb, bb = 3 * B * T * H * s, 6 * B * T * H * s
+    prof = "linear_scans_8x2048x1536.md" if (B, T, H) == (8, 2048, 1536) else None
     return dict(shape=[B, T, H], dtype=str(dtype).replace("torch.", ""), fwd_us=fwd_ms * 1e3, bwd_us=bwd_ms * 1e3,
-                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
+                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6, runs=runs,
+                roofline=roofline("hbm", fb + bb, fwd_ms + bwd_ms, None, prof))
 
 
 def bench_linear_scan(torch, steps, warmup, B, T, H, dtype):
@@ -172,20 +199,13 @@ def bench_linear_scan(torch, steps, warmup, B, T, H, dtype):
         nat.call("edf_fused_linear_scan_backward", stream, P(a), None, P(out), P(dy), P(da), P(db), None, B, T, H,
                  flag)
 
-    for _ in range(warmup):
-        fwd()
-        bwd()
-    tf, tb = EventTimer(torch), EventTimer(torch)
-    for _ in range(steps):
-        with tf:
-            fwd()
-        with tb:
-            bwd()
+    runs, wu, fl = max(steps, MIN_RUNS), max(warmup, MIN_WARMUP), Flush(torch)
+    fwd_ms, bwd_ms = median_ms(torch, fwd, runs, wu, fl), median_ms(torch, bwd, runs, wu, fl)
     s = a.element_size()
-    fwd_ms, bwd_ms = tf.mean_ms(), tb.mean_ms()
     fb, bb = 3 * B * T * H * s, 5 * B * T * H * s
     return dict(shape=[B, T, H], dtype=str(dtype).replace("torch.", ""), fwd_us=fwd_ms * 1e3, bwd_us=bwd_ms * 1e3,
-                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6)
+                fwd_gbs=fb / fwd_ms / 1e6, bwd_gbs=bb / bwd_ms / 1e6, runs=runs,
+                roofline=roofline("hbm", fb + bb, fwd_ms + bwd_ms))
 
 
 def bench_block(torch, steps, warmup, B, T, H, L, dtype, kind="mingru"):
@@ -208,13 +228,7 @@ def bench_block(torch, steps, warmup, B, T, H, L, dtype, kind="mingru"):
     def fwd():
         nat.call(f"edf_fused_{kind}_block_scan", stream, P(x), P(w), None, P(out), P(ws), wsb, B, T, H, L, flag)
 
-    for _ in range(warmup):
-        fwd()
-    tf = EventTimer(torch)
-    for _ in range(steps):
-        with tf:
-            fwd()
-    ms = tf.mean_ms()
+    ms = median_ms(torch, fwd, max(steps, MIN_RUNS), max(warmup, MIN_WARMUP))
     return dict(shape=[B, T, H], layers=L, dtype=str(dtype).replace("torch.", ""), ms=ms,
                 tokens_per_s=B * T / ms * 1e3, projection_tflops=2 * nproj * B * T * H * H * L / ms / 1e9)
 
@@ -229,23 +243,19 @@ def profiled_traffic(kernels, path=os.path.join(ROOT, "profiles", "selective_sca
     except OSError:
         return None
     found = dict((k, int(v)) for k, v in re.findall(r"traffic_bytes\[(\w+)\] = (\d+)", text))
+    if kernels == ["*"]:
+        return sum(found.values()) if found else None
     if not all(k in found for k in kernels):
         return None
     return sum(found[k] for k in kernels)
 
 
-def _time_pair(torch, steps, warmup, fwd, bwd):
-    for _ in range(warmup):
-        fwd()
-        bwd()
-    torch.cuda.synchronize()
-    tf, tb = EventTimer(torch), EventTimer(torch)
-    for _ in range(steps):
-        with tf:
-            fwd()
-        with tb:
-            bwd()
-    return tf.mean_ms(), tb.mean_ms()
+def _time_pair(torch, steps, warmup, fwd, bwd, runs=None):
+    """Medians of the forward and the backward entry point (no cache eviction: these rows are
+    compute-bound)."""
+    runs = runs or max(steps, MIN_RUNS)
+    wu = max(warmup, MIN_WARMUP)
+    return median_ms(torch, fwd, runs, wu), median_ms(torch, bwd, runs, wu)
 
 
 def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
@@ -283,13 +293,14 @@ def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
         nat.call("edf_fused_gated_delta_net_scan_backward", stream, P(q), P(k), P(v), P(beta), P(alpha), P(out),
                  P(do), P(dq), P(dk), P(dv), P(db), P(da), P(ws2), wsb, B, T, H, d, 1, 1)
 
-    fwd_ms, bwd_ms = _time_pair(torch, max(2, steps // 4), 1, fwd, bwd)
+    fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     fflops = 2 * (5 * C * d + 3 * d * d) * B * H * T
     bflops = 2 * fflops
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, fwd_tflops=fflops / fwd_ms / 1e9, bwd_tflops=bflops / bwd_ms / 1e9,
                 fwd_bwd_tflops=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9,
                 fwd_bwd_mfma_frac=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9 / MFMA_BF16_PEAK_TFLOPS,
-                shape=dict(B=B, H=H, T=T, d=d, chunk=C))
+                runs=max(steps, MIN_RUNS), shape=dict(B=B, H=H, T=T, d=d, chunk=C),
+                roofline=roofline("mfma", fflops + bflops, fwd_ms + bwd_ms, ["*"], "delta_rule_c3.md"))
 
 
 def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128, causal=True):
@@ -318,10 +329,12 @@ def bench_flash(torch, steps, warmup, B=4, H=32, T=4096, d=128, causal=True):
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     fflops = 4 * B * H * T * T * d / (2 if causal else 1)
     bflops = 2.5 * fflops
+    prof = "flash_c4.md" if (causal and (B, H, T, d) == (4, 32, 4096, 128)) else None
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, fwd_tflops=fflops / fwd_ms / 1e9, bwd_tflops=bflops / bwd_ms / 1e9,
                 fwd_bwd_tflops=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9,
                 fwd_bwd_mfma_frac=(fflops + bflops) / (fwd_ms + bwd_ms) / 1e9 / MFMA_BF16_PEAK_TFLOPS,
-                shape=dict(B=B, H=H, T=T, d=d, causal=causal))
+                runs=max(steps, MIN_RUNS), shape=dict(B=B, H=H, T=T, d=d, causal=causal),
+                roofline=roofline("mfma", fflops + bflops, fwd_ms + bwd_ms, ["*"], prof))
 
 
 def bench_fox(torch, steps, warmup, B=4, H=32, T=4096, d=128):
@@ -519,16 +532,7 @@ def bench_rnn_block(torch, steps, warmup, kind, dtype, B=8, T=2048, H=256, L=4):
         else:
             nat.call("edf_fused_gru_block_scan", stream, P(x), P(w), P(h0), P(out), P(ws), wsb, B, T, H, L, flag)
 
-    for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms = median_ms(torch, run, steps, warmup)
     return dict(layers=L, dtype=str(dtype).replace("torch.", ""), ms=ms, tokens_per_s=B * T / ms * 1e3,
                 shape=dict(B=B, T=T, H=H))
 
@@ -563,6 +567,18 @@ def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
                 shape=dict(batch=B, seq=T, vocab=vocab, embed=embed, layers="4 mamba + 2 delta_net + 2 attention"))
 
 
+def cpu_model():
+    """The host CPU's model name (the line lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
     """Time the C restatement (oracle/cref.c, OpenMP f32) on the config-2 selective-scan
     workload (about 3 s per fwd+bwd step on 8 host cores); returns GB/s under the same
@@ -592,6 +608,7 @@ def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
     t = float(np.median(times))
     lib.cref_threads.restype = ctypes.c_int
     return dict(value=(fb + bb) / t / 1e9, unit="GB/s", cores=int(lib.cref_threads()), kind="port",
+                cpu_model=cpu_model(), host_cpus=os.cpu_count(),
                 sample=f"C restatement (Nx unavailable), selective scan fwd+bwd f32, B={B} T={T} D={D} N={N} "
                        f"(the full config-2 workload), median of {reps}, {t:.2f} s per step")
 

@@ -19,10 +19,18 @@
 static float clampf(float x, float lo, float hi) { return x < lo ? lo : (x > hi ? hi : x); }
 static float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+/* The number of threads the parallel regions below actually run with (the team size of a
+ * parallel region under the same settings). */
 int cref_threads(void) {
 #ifdef _OPENMP
-  extern int omp_get_max_threads(void);
-  return omp_get_max_threads();
+  extern int omp_get_num_threads(void);
+  int n = 1;
+#pragma omp parallel
+  {
+#pragma omp single
+    n = omp_get_num_threads();
+  }
+  return n;
 #else
   return 1;
 #endif
