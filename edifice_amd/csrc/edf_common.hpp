@@ -81,6 +81,10 @@ EDF_DEVICE float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)); exact reciprocal keeps f32 parity.
 EDF_DEVICE float sigmoidf(float x) { return 1.0f / (1.0f + fast_exp2(-x * LOG2E)); }
 
+// sigmoid with the hardware reciprocal (1 ulp) instead of an IEEE division: for gates on
+// f32 math whose results are checked at 1e-4; 2^(-x log2 e) -> inf gives rcp(inf) = 0.
+EDF_DEVICE float sigmoid_rcp(float x) { return fast_rcp(1.0f + fast_exp2(-x * LOG2E)); }
+
 EDF_DEVICE float clampf(float x, float lo, float hi) { return fminf(fmaxf(x, lo), hi); }
 
 // ---- compile-time loops ------------------------------------------------------

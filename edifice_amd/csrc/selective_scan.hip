@@ -149,6 +149,21 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
   }
   const float Dc = (Dv != nullptr && cvalid) ? ld(Dv, c) : 0.0f;
   const long rowbase = (long)b * seq * dim;
+  // every global access goes through a buffer resource on this batch row: SGPR base plus a
+  // 32-bit offset (no 64-bit address VALU), out-of-range offsets load 0 / drop the store
+  typedef typename Bits<TI>::type RI;
+  typedef typename Bits<TP>::type RP;
+  const unsigned rowbytes = (unsigned)((long)seq * dim * sizeof(TI));
+  const rsrc_t r_x = make_rsrc(x + rowbase, rowbytes), r_dt = make_rsrc(dt + rowbase, rowbytes);
+  const rsrc_t r_z = make_rsrc(HAS_Z ? z + rowbase : x + rowbase, rowbytes);
+  const rsrc_t r_y = make_rsrc(WRITE_Y ? out + rowbase : x + rowbase, WRITE_Y ? rowbytes : 0u);
+  const unsigned bcbytes = (unsigned)((long)seq * ns * sizeof(TP));
+  const rsrc_t r_B = make_rsrc(Bm + (long)b * seq * ns, bcbytes), r_C = make_rsrc(Cm + (long)b * seq * ns, bcbytes);
+  const rsrc_t r_m =
+      make_rsrc(MEAN ? (const void*)(p.dtmean + (long)b * seq) : (const void*)x, (unsigned)(seq * sizeof(float)));
+  const unsigned ckbytes = (unsigned)((long)p.nck * N * dim * sizeof(float));
+  const rsrc_t r_ck = make_rsrc(p.ckpt != nullptr ? (const void*)(p.ckpt + (long)b * p.nck * N * dim) : (const void*)x,
+                                p.ckpt != nullptr ? ckbytes : 0u);
 
   // Raw values of the blocks ahead, loaded PD blocks early from clamped (in-bounds)
   // indices so no load sits behind a divergent branch and the HBM latency is covered by
@@ -159,29 +174,28 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
   // lanes through a DPP row broadcast (folded into v_mul_f32_dpp for B): no LDS traffic.
   // Scalar loads into SGPR operands were tried and are slower: the scalar-cache latency
   // and the 64-bit scalar address arithmetic are not hidden.
-  TI rx[PD][EPT], rdt[PD][EPT], rz[PD][EPT];
-  float rbc[PD][R];
+  RI rx[PD][EPT], rdt[PD][EPT], rz[PD][EPT];
+  RP rbc[PD][R];
   float rm[PD][EPT];
   float cx[EPT], cz[EPT], nx[EPT], nz[EPT];
   auto fetch = [&](int slot, int t0) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      // uniform row pointer + 32-bit lane offset: SGPR-base addressing, no 64-bit VALU math
-      const long row = rowbase + (long)min(t0 + w + i * NW, seq - 1) * dim;
-      rx[slot][i] = (x + row)[cc];
-      rdt[slot][i] = (dt + row)[cc];
-      if (HAS_Z) rz[slot][i] = (z + row)[cc];
-      rm[slot][i] = MEAN ? p.dtmean[(long)b * seq + min(t0 + w + i * NW, seq - 1)] : 0.0f;
+      const int t = min(t0 + w + i * NW, seq - 1);
+      const unsigned off = ((unsigned)t * dim + cc) * (unsigned)sizeof(TI);
+      rx[slot][i] = bload<TI>(r_x, off);
+      rdt[slot][i] = bload<TI>(r_dt, off);
+      if (HAS_Z) rz[slot][i] = bload<TI>(r_z, off);
+      rm[slot][i] = MEAN ? bits_f32(bload<float>(r_m, (unsigned)t * 4u)) : 0.0f;
     }
-    const long bc0 = ((long)b * seq + t0) * ns;
     const int tmax = seq - 1 - t0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int v = (16 * r + (lane & 15)) % (TS * K);
-      const int st = w * K + v % K;  // padding states (st >= ns) load index 0 and use 0
-      const int off = st < ns ? min(v / K, tmax) * ns + st : 0;
-      const float val = to_f32((r < R / 2 ? Bm : Cm)[bc0 + off]);
-      rbc[slot][r] = st < ns ? val : 0.0f;
+      const int st = w * K + v % K;  // padding states (st >= ns) read 0 through an out-of-range offset
+      const unsigned off =
+          st < ns ? ((unsigned)(t0 + min(v / K, tmax)) * ns + st) * (unsigned)sizeof(TP) : OOB_OFF;
+      rbc[slot][r] = bload<TP>(r < R / 2 ? r_B : r_C, off);
     }
   };
   auto stage = [&](int slot, int t0, int buf, float* xs, float* zs) {
@@ -189,12 +203,12 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
     for (int i = 0; i < EPT; ++i) {
       const int tt = w + i * NW;
       const bool ok = (t0 + tt < seq) && cvalid;
-      const float xv = to_f32(rx[slot][i]);
-      const float dtc = ok ? clampf(to_f32(rdt[slot][i]), DT_MIN, DT_MAX) : 0.0f;
+      const float xv = bits_f32(rx[slot][i]);
+      const float dtc = ok ? clampf(bits_f32(rdt[slot][i]), DT_MIN, DT_MAX) : 0.0f;
       s_dtc[buf][lane][tt] = dtc;
       s_dtx[buf][lane][tt] = ok ? (MEAN ? rm[slot][i] : dtc) * xv : 0.0f;
       xs[i] = xv;
-      zs[i] = HAS_Z ? to_f32(rz[slot][i]) : 0.0f;
+      zs[i] = HAS_Z ? bits_f32(rz[slot][i]) : 0.0f;
     }
   };
 
@@ -219,7 +233,9 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
       const int blk = blk0 + u;
       const int t0 = blk * TS, buf = u & 1;  // PD is even, so u & 1 == blk & 1
       // ---- recurrence over the block ----
-      const float* bcr = rbc[u];  // this block's B/C values (slot blk % PD == u)
+      float bcr[R];  // this block's B/C values (slot blk % PD == u)
+#pragma unroll
+      for (int r = 0; r < R; ++r) bcr[r] = bits_f32(rbc[u][r]);
       static_for<TS / 4>([&](auto qi) {
         constexpr int q = decltype(qi)::value;
         const float4 dc4 = *reinterpret_cast<const float4*>(&s_dtc[buf][lane][4 * q]);
@@ -241,10 +257,11 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
           if (WRITE_Y) s_yp[buf][w][tt][lane] = acc;
         });
       });
-      if (p.ckpt != nullptr && cvalid && blk < nblk) {
-        float* ck = p.ckpt + (((long)b * p.nck + blk) * N + w * K) * dim + c;
+      if (p.ckpt != nullptr) {
+        const bool ok = cvalid && blk < nblk;
 #pragma unroll
-        for (int s = 0; s < K; ++s) ck[(long)s * dim] = h[s];
+        for (int s = 0; s < K; ++s)
+          bstore<float>(r_ck, ok ? (((unsigned)blk * N + w * K + s) * dim + c) * 4u : OOB_OFF, h[s]);
       }
       stage((u + 1) % PD, t0 + TS, buf ^ 1, nx, nz);
       fetch(u, min(blk + PD, nblk - 1) * TS);
@@ -258,8 +275,9 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
 #pragma unroll
           for (int v = 0; v < NW; ++v) y += s_yp[buf][v][tt][lane];
           y = fmaf(Dc, cx[i], y);
-          if (HAS_Z) y *= cz[i] * sigmoidf(cz[i]);
-          if (t0 + tt < seq && cvalid) st(out, rowbase + (long)(t0 + tt) * dim + c, y);
+          if (HAS_Z) y *= cz[i] * sigmoid_rcp(cz[i]);
+          bstore<TI>(r_y, (t0 + tt < seq && cvalid) ? ((unsigned)(t0 + tt) * dim + c) * (unsigned)sizeof(TI) : OOB_OFF,
+                     y);
         }
       }
 #pragma unroll
@@ -465,7 +483,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 #pragma unroll
         for (int v = 0; v < NW; ++v) y += pp(0, v, tt);
         y = fmaf(Dc, ex[i], y);
-        const float sg = sigmoidf(ez[i]);
+        const float sg = sigmoid_rcp(ez[i]);
         edy[i] = ego[i] * ez[i] * sg;
         s_dy[lane][tt] = edy[i];
         if (p.dz != nullptr)
@@ -822,6 +840,11 @@ int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const 
   int rc = check_common(batch, seq_len, hidden, state, io_dtype, param_dtype, mode);
   if (rc) return rc;
   EDF_REQUIRE(x && dt && A && B && C && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  // the kernels address one batch row of x, dt, z, y (and of B, C and the checkpoints)
+  // through buffer resources with 32-bit byte offsets
+  EDF_REQUIRE((long)seq_len * hidden * (io_dtype == EDF_BF16 ? 2 : 4) < (1L << 31) &&
+                  num_chunks(seq_len) * padded_state(state) * hidden * 4 < (1L << 31),
+              EDF_ERR_UNSUPPORTED, "one batch row of seq_len * hidden elements (and its checkpoints) must stay below 2 GiB");
   const size_t need = edf_selective_scan_workspace_bytes(batch, seq_len, hidden, state, mode);
   EDF_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), EDF_ERR_WORKSPACE,
               "workspace too small: need %zu bytes", need);
