@@ -15,10 +15,13 @@ Algorithmic bytes (per call, what roofline.achieved divides by):
 Timing: the headline value times exactly K fwd+bwd steps (after W warm-ups) with host
 synchronisation on both sides; every per-kernel figure (and each config's roofline) is the
 median of max(K, 50) HIP-event timed runs after max(W, 10) warm-ups, events recorded on the
-stream the kernels are launched on; the scan rows evict the caches before each timed run with
-a 256 MiB fill (the 256 MB MALL could otherwise hold a whole scan's inputs).
+stream the kernels are launched on; the scan rows evict the caches before each timed run by
+reading a 512 MiB buffer (the 256 MB MALL could otherwise hold a whole scan's inputs; a read
+leaves no dirty lines to be written back during the timed run, see --flush).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only c2,mingru,linear,block]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only mingru,block,linear,c3,delta,c4,flash,hybrid]
+       [--flush read|write|none] [--copy-probe]
+(the config-2 headline always runs; --only selects the other rows)
 """
 from __future__ import annotations
 
@@ -48,13 +51,24 @@ MIN_RUNS, MIN_WARMUP = 50, 10
 
 
 class Flush:
-    """Cache eviction between timed runs: a 256 MiB fill kernel on the current stream."""
+    """Cache eviction between timed runs.  The default ("read") sums a 512 MiB buffer: twice
+    the 256 MB MALL, so the next run's inputs come from HBM, and the evicting lines are clean.
+    "write" fills 256 MiB instead; the dirty lines it leaves in L2 / MALL are written back
+    during the next timed run and bill that run for up to 256 MiB of extra HBM writes.
+    "none" times back-to-back runs."""
+
+    mode = "read"
 
     def __init__(self, torch):
-        self.buf = torch.empty(64 * 2 ** 20, dtype=torch.float32, device="cuda")
+        self.torch = torch
+        n = (128 if self.mode == "read" else 64) * 2 ** 20
+        self.buf = torch.ones(n, dtype=torch.float32, device="cuda") if self.mode != "none" else None
 
     def __call__(self):
-        self.buf.fill_(1.0)
+        if self.mode == "read":
+            self.torch.sum(self.buf)
+        elif self.mode == "write":
+            self.buf.fill_(1.0)
 
 
 def median_ms(torch, fn, runs, warmup, flush=None):
@@ -620,6 +634,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="")
+    ap.add_argument("--flush", choices=("read", "write", "none"), default="read",
+                    help="cache eviction before each timed scan-row run (default: read 512 MiB)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain 256 MiB device copy (scale reference for rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -629,6 +645,7 @@ def main():
         sys.exit(2)
     import torch
 
+    Flush.mode = args.flush
     only = set(filter(None, args.only.split(",")))
     want = (lambda k: not only or k in only)  # noqa: E731
     configs = {}
@@ -651,15 +668,17 @@ def main():
             configs[key] = bench_linear_scan(torch, args.steps, args.warmup, 8, 2048, 1536, dt)
     ss = bench_selective_scan(torch, args.steps, args.warmup)
     configs["c2_selective_scan"] = ss
-    if want("delta"):
+    if want("delta") or want("c3"):
         configs["c3_gated_delta_rule"] = bench_delta_rule(torch, args.steps, args.warmup)
+    if want("delta"):
         configs["kda_8x2048x8x128"] = bench_kda(torch, args.steps, args.warmup)
         configs["delta_product_8x2048x2x8x128"] = bench_delta_product(torch, args.steps, args.warmup)
         configs["rla_8x2048x8x128"] = bench_rla(torch, args.steps, args.warmup, 0)
         configs["rdn_8x2048x8x128"] = bench_rla(torch, args.steps, args.warmup, 1)
         configs["ttt_8x2048x64"] = bench_ttt(torch, args.steps, args.warmup)
-    if want("flash"):
+    if want("flash") or want("c4"):
         configs["c4_flash_attention"] = bench_flash(torch, args.steps, args.warmup)
+    if want("flash"):
         configs["flash_attention_noncausal_4x32x2048x128"] = bench_flash(torch, args.steps, args.warmup, T=2048,
                                                                          causal=False)
         configs["fox_attention_4x32x4096x128"] = bench_fox(torch, args.steps, args.warmup)
