@@ -12,37 +12,41 @@
 //   Optional extensions: y += D[d] x, then y *= silu(z).
 //
 // Design.  The op is VALU-bound: per (b, t, d, n) element the forward needs one
-// v_exp_f32 (about 10 cycles per wave on MI355X, measured) and four VALU ops, several
-// times the HBM time at config-2 size.  The layout minimises everything else:
-//   * lane = channel d (64 channels per wave) holding K states in registers (one in the
-//     forward, two in the backward); NW = N / K waves per workgroup cover one 64-channel
-//     tile's N states (16 or 8 waves at N = 16: 4 or 2 waves per SIMD hide the LDS and
-//     transcendental latency, which four states per lane at 1 wave per SIMD did not);
-//   * the B[b, t, :] and C[b, t, :] values a wave needs are the same for all its lanes.
-//     Forward: a block's values are loaded into a few VGPRs (16 values per register,
-//     replicated over the four 16-lane rows) and broadcast with DPP row_newbcast, folded
-//     into v_mul_f32_dpp: no LDS traffic.  Backward: staged through LDS once per chunk
-//     and read as broadcasts.  (Scalar loads into SGPR operands were tried and are
-//     slower: every timestep waits on the scalar cache.)
-//   * x, dt (and z) are staged per block of timesteps through LDS from coalesced rows,
-//     clip(dt) and dt_b * x computed once per (t, d); the recurrence reads them as
-//     16-byte vectors;
-//   * y = sum_n C h: each lane sums its K states, the NW wave partials are added
-//     through LDS by the thread that staged that (t, d), which still holds x and z in
-//     registers for the D skip and the gate; double-buffered tiles need one barrier
-//     per block, and the raw inputs are prefetched four blocks ahead;
+// v_exp_f32 and four other VALU ops, several times the HBM time at config-2 size, so the
+// layout is chosen to keep every SIMD busy and to spend little else per element:
+//   * one state per lane.  A wave holds SW = 4 states (one per 16-lane DPP row) of
+//     CW = 16 channels (fewer states, more channels when N < 4); a workgroup holds G
+//     such channel groups and all N states of them (G N / SW waves).  At config 2
+//     (B = 8, D = 1536, N = 16) G = 3 gives 256 workgroups of 12 waves: every CU gets one,
+//     3 waves per SIMD.  (One workgroup per (b, 64-channel tile) gave 192 workgroups: 64
+//     CUs idle.)  The host picks G from the grid it would produce;
+//   * B[b, t, n] and C[b, t, n] are the same for the 16 lanes of a row: a block of 16
+//     timesteps sits in one VGPR (lane i of the row holds step i of the row's state) and
+//     reaches the row through DPP row_newbcast, folded into v_mul_f32_dpp: no LDS traffic;
+//   * x, dt (and z) are staged per block of 16 timesteps through LDS from coalesced rows,
+//     clip(dt) and dt_b x computed once per (t, d); the recurrence reads them as 16-byte
+//     vectors (the four rows of a wave read the same addresses);
+//   * y = sum_n C h: every lane writes C h for its (state, t, d) to an LDS tile and the
+//     thread that staged (t, d) adds the N values, applies the D skip and the gate and
+//     stores y; double-buffered tiles need one barrier per block; raw inputs are
+//     prefetched four blocks ahead;
 //   * the forward writes the state every CK = 16 timesteps ("checkpoints", layout
-//     [b][chunk][n][d], coalesced over d);
+//     [b][chunk][n][d], coalesced over d) and, with a gate, the pre-gate y (for dz) into
+//     the same caller buffer, so the backward recomputes neither;
 //   * any state size 1..32 (the reference's limit): the kernels are compiled for the next
 //     power of two NP >= N and the states past N are padding, with A = B = C = 0 loaded
 //     for them, so they stay 0 and add nothing; A, B, C, dA, dB and dC keep the caller's
 //     stride N, checkpoints and partial sums the padded NP;
-//   * backward: chunks are walked in reverse; each chunk's states and decays are
-//     recomputed from its checkpoint into registers, then the reverse recurrence runs
-//     with the same lane layout.  Sums over states (dx, ddt) are in-lane plus an LDS
-//     add over the NW waves; sums over channels (dB, dC) go through an LDS tile per
-//     block of 8 timesteps (conflict-free strides) into per-tile partials, summed over
-//     the tiles by a small deterministic kernel (no atomics).
+//   * backward: chunks of 16 steps in reverse, each chunk's states and decays recomputed
+//     from its checkpoint into registers, then the reverse recurrence in two halves of 8
+//     steps.  Every lane writes its four per-element terms (dx and ddt terms summed over
+//     states, dC and dB terms summed over channels) to LDS tiles; after a barrier all
+//     threads reduce them: (t, d, quantity) sums over the N states -> dx, ddt; (t, n,
+//     quantity, channel group) sums over 16 channels, added over the G groups one half
+//     later into one partial per workgroup, summed over the workgroups by a small
+//     deterministic kernel (no atomics).
+#include <algorithm>
+
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
@@ -51,7 +55,7 @@ namespace {
 
 constexpr float DT_MIN = 1.0e-3f;
 constexpr float DT_MAX = 0.1f;
-constexpr int SS_CK = 16;  // checkpoint interval (timesteps) = backward recompute chunk
+constexpr int SS_CK = 16;  // checkpoint interval (timesteps) = recompute chunk = lanes per DPP row
 
 struct SSArgs {
   const void* x;
@@ -64,6 +68,7 @@ struct SSArgs {
   const float* dtmean;  // [batch, seq] or null (per-channel dt_b)
   void* out;
   float* ckpt;  // [batch, nck, N, dim] state after each chunk of SS_CK timesteps
+  void* ypre;   // [batch, seq, dim] y before the gate (io type), written with a gate
   // backward only
   const void* dout;
   void* dx;
@@ -77,17 +82,28 @@ struct SSArgs {
   int nst;  // the caller's state count N (<= the kernel's padded NP): stride of A, B, C rows
 };
 
-// lane = channel; K = min(N, KMAX) states per lane (at least N / 16, so a workgroup
-// has at most 16 waves); NW waves per workgroup cover the N states.
-template <int N, int KMAX = 4>
-struct SSGeo {
-  static constexpr int KLO = KMAX > N / 16 ? KMAX : N / 16;
-  static constexpr int K = N < KLO ? N : KLO;
-  static constexpr int NW = N / K;
+// Lane layout: one state per lane; a wave holds SW states (each on 64 / SW lanes, whole
+// 16-lane DPP rows) of CW channels; a workgroup holds G channel groups x all N states.
+template <int N, int G>
+struct RGeo {
+  static constexpr int SW = N < 4 ? N : 4;  // states per wave
+  static constexpr int CW = 64 / SW;        // channels per wave
+  static constexpr int NSG = N / SW;        // state groups
+  static constexpr int NW = G * NSG;        // waves per workgroup
   static constexpr int NT = 64 * NW;
+  static constexpr int CT = G * CW;         // channels per workgroup
+  static_assert(NW <= 16, "at most 16 waves per workgroup");
 };
 
+// the wide channel-group count compiled per state size (the narrow one is G = 1)
+template <int N> constexpr int ss_gwide() { return N >= 32 ? 1 : (N == 16 ? 3 : (N >= 4 ? 4 : 1)); }
+
 EDF_DEVICE int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// DPP quad_perm [1, 0, 3, 2]: the value of the neighbouring lane of a lane pair
+EDF_DEVICE float pair_swap(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
 
 // ---------------------------------------------------------------------------
 // dt mean over channels (block semantics), one wave per (b, t)
@@ -106,48 +122,68 @@ __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ d
   if (lane == 0) dtm[row] = s / (float)dim;
 }
 
+// Padded length of an LDS row holding the N states of one (t, channel): one wave's writes
+// (16 channels x 4 states) and the 16-byte reads of consecutive channels are conflict-free.
+template <int N> constexpr int ss_pn() { return N == 4 ? 12 : N + 4; }
+constexpr int mod64_to(int v, int r) { return v + ((r - v % 64) % 64 + 64) % 64; }  // smallest >= v, = r mod 64
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename TI, typename TP, int N, int KMAX, bool MEAN, bool HAS_Z, bool WRITE_Y>
-__global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSArgs p, const TP* __restrict__ Bm,
-                                                                    const TP* __restrict__ Cm) {
-  using G = SSGeo<N, KMAX>;
-  constexpr int K = G::K, NW = G::NW, NT = G::NT;
-  constexpr int TS = SS_CK;          // timesteps per staged block (one checkpoint per block)
-  constexpr int PS = TS + 4;         // [channel][t] row stride: 16-byte reads are conflict-free
-  constexpr int EPT = TS * 64 / NT;  // staged (t, channel) elements per thread
-  constexpr int R = TS * 2 * K / 16;  // VGPRs holding a block's B/C values (16 per row)
-  constexpr int PD = 4;                // prefetch distance (blocks)
-  static_assert(TS % 4 == 0 && EPT * NW == TS && PD % 2 == 0 && (TS * K) % 16 == 0, "staging layout");
-  __shared__ __align__(16) float s_dtc[2][64][PS];
-  __shared__ __align__(16) float s_dtx[2][64][PS];
-  __shared__ float s_yp[2][NW][TS][64];
+// WRITE_Y: store the gated output.  With a gate, y before the gate is stored into p.ypre
+// (through a zero-length resource, i.e. dropped, when p.ypre is null); without WRITE_Y
+// and without a gate only the checkpoints are written.
+template <typename TI, typename TP, int N, int G, bool MEAN, bool HAS_Z, bool WRITE_Y>
+__global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_fwd_kernel(const SSArgs p, const TP* __restrict__ Bm,
+                                                                const TP* __restrict__ Cm) {
+  using Geo = RGeo<N, G>;
+  constexpr int SW = Geo::SW, CW = Geo::CW, NT = Geo::NT, CT = Geo::CT;
+  constexpr int TS = SS_CK;                 // timesteps per block (one checkpoint per block)
+  constexpr int PS = TS + 4;                // [channel][t] row stride: 16-byte reads are conflict-free
+  constexpr int NE = TS * CT;               // staged (t, channel) elements per block
+  constexpr int EPT = (NE + NT - 1) / NT;   // per thread
+  constexpr bool SAVE_YP = HAS_Z;
+  constexpr bool YSUM = WRITE_Y || SAVE_YP;
+  constexpr int PN = ss_pn<N>();            // C h tile [t][channel][state], rows of PN floats
+  constexpr int PD = N >= 8 ? 4 : 2;        // prefetch distance (blocks)
+  static_assert(PD % 2 == 0, "the LDS buffer parity follows the ring slot");
+  __shared__ __align__(16) float s_dtc[2][CT][PS];
+  __shared__ __align__(16) float s_dtx[2][CT][PS];
+  __shared__ __align__(16) float s_yp[YSUM ? 2 : 1][YSUM ? TS * CT * PN : 1];
 
   const TI* __restrict__ x = (const TI*)p.x;
   const TI* __restrict__ dt = (const TI*)p.dt;
   const TI* __restrict__ z = (const TI*)p.z;
   const TP* __restrict__ Am = (const TP*)p.A;
   const TP* __restrict__ Dv = (const TP*)p.D;
-  TI* __restrict__ out = (TI*)p.out;
   const int seq = p.seq, dim = p.dim;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = uniform(tid >> 6);  // this wave's state group
+  const int w = uniform(tid >> 6);
+  const int g = w % G, sg = w / G;          // this wave's channel group and state group
+  const int s = sg * SW + lane / CW;        // this lane's state
+  const int cl = g * CW + lane % CW;        // this lane's channel within the tile
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int b = logical / p.ntile, tile = logical % p.ntile;
-  const int c = tile * 64 + lane;
+  const int c = tile * CT + cl;
   const bool cvalid = c < dim;
-  const int cc = min(c, dim - 1);
 
   const int ns = p.nst;
-  float A2[K], h[K];
+  const float A2 = (cvalid && s < ns) ? ld(Am, (long)c * ns + s) * LOG2E : 0.0f;
+  float h = 0.0f;
+
+  // the (t, channel) elements this thread stages and finishes: e = tid + i NT
+  int et[EPT], ec[EPT];
+  bool ev[EPT];
+  float eD[EPT];
 #pragma unroll
-  for (int s = 0; s < K; ++s) {
-    A2[s] = (cvalid && w * K + s < ns) ? ld(Am, (long)c * ns + w * K + s) * LOG2E : 0.0f;
-    h[s] = 0.0f;
+  for (int i = 0; i < EPT; ++i) {
+    const int e = tid + i * NT;
+    et[i] = e / CT;
+    ec[i] = e % CT;
+    ev[i] = e < NE && tile * CT + ec[i] < dim;
+    eD[i] = (Dv != nullptr && ev[i]) ? ld(Dv, tile * CT + ec[i]) : 0.0f;
   }
-  const float Dc = (Dv != nullptr && cvalid) ? ld(Dv, c) : 0.0f;
   const long rowbase = (long)b * seq * dim;
   // every global access goes through a buffer resource on this batch row: SGPR base plus a
   // 32-bit offset (no 64-bit address VALU), out-of-range offsets load 0 / drop the store
@@ -156,7 +192,9 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
   const unsigned rowbytes = (unsigned)((long)seq * dim * sizeof(TI));
   const rsrc_t r_x = make_rsrc(x + rowbase, rowbytes), r_dt = make_rsrc(dt + rowbase, rowbytes);
   const rsrc_t r_z = make_rsrc(HAS_Z ? z + rowbase : x + rowbase, rowbytes);
-  const rsrc_t r_y = make_rsrc(WRITE_Y ? out + rowbase : x + rowbase, WRITE_Y ? rowbytes : 0u);
+  const rsrc_t r_y = make_rsrc(WRITE_Y ? (TI*)p.out + rowbase : x + rowbase, WRITE_Y ? rowbytes : 0u);
+  const rsrc_t r_yp = make_rsrc(SAVE_YP && p.ypre != nullptr ? (TI*)p.ypre + rowbase : x + rowbase,
+                                SAVE_YP && p.ypre != nullptr ? rowbytes : 0u);
   const unsigned bcbytes = (unsigned)((long)seq * ns * sizeof(TP));
   const rsrc_t r_B = make_rsrc(Bm + (long)b * seq * ns, bcbytes), r_C = make_rsrc(Cm + (long)b * seq * ns, bcbytes);
   const rsrc_t r_m =
@@ -166,47 +204,38 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
                                 p.ckpt != nullptr ? ckbytes : 0u);
 
   // Raw values of the blocks ahead, loaded PD blocks early from clamped (in-bounds)
-  // indices so no load sits behind a divergent branch and the HBM latency is covered by
-  // PD blocks of compute; kept in the storage type until staged.
-  // B/C: the wave needs B[t, wK..wK+K) and C[t, wK..wK+K) for the TS steps of a block,
-  // the same for every lane.  Value v = t K + s of B sits in lane v % 16 of every
-  // 16-lane row of register v / 16 (C likewise in registers R/2..R-1) and reaches all
-  // lanes through a DPP row broadcast (folded into v_mul_f32_dpp for B): no LDS traffic.
-  // Scalar loads into SGPR operands were tried and are slower: the scalar-cache latency
-  // and the 64-bit scalar address arithmetic are not hidden.
+  // indices so no load sits behind a divergent branch; kept in the storage type until
+  // staged.  B/C: lane i of each 16-lane row loads step t0 + i of the row's state.
   RI rx[PD][EPT], rdt[PD][EPT], rz[PD][EPT];
-  RP rbc[PD][R];
+  RP rB[PD], rC[PD];
   float rm[PD][EPT];
   float cx[EPT], cz[EPT], nx[EPT], nz[EPT];
   auto fetch = [&](int slot, int t0) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      const int t = min(t0 + w + i * NW, seq - 1);
-      const unsigned off = ((unsigned)t * dim + cc) * (unsigned)sizeof(TI);
+      const int t = min(t0 + et[i], seq - 1);
+      const unsigned off = ev[i] ? ((unsigned)t * dim + tile * CT + ec[i]) * (unsigned)sizeof(TI) : OOB_OFF;
       rx[slot][i] = bload<TI>(r_x, off);
       rdt[slot][i] = bload<TI>(r_dt, off);
       if (HAS_Z) rz[slot][i] = bload<TI>(r_z, off);
       rm[slot][i] = MEAN ? bits_f32(bload<float>(r_m, (unsigned)t * 4u)) : 0.0f;
     }
-    const int tmax = seq - 1 - t0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int v = (16 * r + (lane & 15)) % (TS * K);
-      const int st = w * K + v % K;  // padding states (st >= ns) read 0 through an out-of-range offset
-      const unsigned off =
-          st < ns ? ((unsigned)(t0 + min(v / K, tmax)) * ns + st) * (unsigned)sizeof(TP) : OOB_OFF;
-      rbc[slot][r] = bload<TP>(r < R / 2 ? r_B : r_C, off);
-    }
+    // padding states (s >= ns) read 0 through an out-of-range offset
+    const unsigned off = s < ns ? ((unsigned)(t0 + min(lane & 15, seq - 1 - t0)) * ns + s) * (unsigned)sizeof(TP)
+                                : OOB_OFF;
+    rB[slot] = bload<TP>(r_B, off);
+    rC[slot] = bload<TP>(r_C, off);
   };
   auto stage = [&](int slot, int t0, int buf, float* xs, float* zs) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      const int tt = w + i * NW;
-      const bool ok = (t0 + tt < seq) && cvalid;
+      const bool ok = ev[i] && t0 + et[i] < seq;
       const float xv = bits_f32(rx[slot][i]);
       const float dtc = ok ? clampf(bits_f32(rdt[slot][i]), DT_MIN, DT_MAX) : 0.0f;
-      s_dtc[buf][lane][tt] = dtc;
-      s_dtx[buf][lane][tt] = ok ? (MEAN ? rm[slot][i] : dtc) * xv : 0.0f;
+      if (NE % NT == 0 || tid + i * NT < NE) {
+        s_dtc[buf][ec[i]][et[i]] = dtc;
+        s_dtx[buf][ec[i]][et[i]] = ok ? (MEAN ? rm[slot][i] : dtc) * xv : 0.0f;
+      }
       xs[i] = xv;
       zs[i] = HAS_Z ? bits_f32(rz[slot][i]) : 0.0f;
     }
@@ -223,7 +252,7 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
   const int nblk = (seq + TS - 1) / TS;
   const int npad = (nblk + PD - 1) / PD * PD;
 #pragma unroll
-  for (int j = 0; j < PD; ++j) fetch(j, min(j, nblk - 1) * TS);
+  for (int jb = 0; jb < PD; ++jb) fetch(jb, min(jb, nblk - 1) * TS);
   stage(0, 0, 0, cx, cz);
   __syncthreads();
 
@@ -233,51 +262,52 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
       const int blk = blk0 + u;
       const int t0 = blk * TS, buf = u & 1;  // PD is even, so u & 1 == blk & 1
       // ---- recurrence over the block ----
-      float bcr[R];  // this block's B/C values (slot blk % PD == u)
-#pragma unroll
-      for (int r = 0; r < R; ++r) bcr[r] = bits_f32(rbc[u][r]);
+      const float rb = bits_f32(rB[u]), rc = bits_f32(rC[u]);
       static_for<TS / 4>([&](auto qi) {
         constexpr int q = decltype(qi)::value;
-        const float4 dc4 = *reinterpret_cast<const float4*>(&s_dtc[buf][lane][4 * q]);
-        const float4 dx4 = *reinterpret_cast<const float4*>(&s_dtx[buf][lane][4 * q]);
+        const float4 dc4 = *reinterpret_cast<const float4*>(&s_dtc[buf][cl][4 * q]);
+        const float4 dx4 = *reinterpret_cast<const float4*>(&s_dtx[buf][cl][4 * q]);
         const float dcv[4] = {dc4.x, dc4.y, dc4.z, dc4.w};
         const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
         static_for<4>([&](auto vi) {
           constexpr int v = decltype(vi)::value, tt = 4 * q + v;
-          float acc = 0.0f;
-          static_for<K>([&](auto si) {
-            constexpr int s = decltype(si)::value;
-            constexpr int vb = tt * K + s, vc = vb + TS * K;  // B and C value indices
-            const float a = fast_exp2(dcv[v] * A2[s]);
-            h[s] = fmaf(a, h[s], row_bcast<vb % 16>(bcr[vb / 16]) * dxv[v]);
-            // the first state's C h is a DPP-folded multiply, not a broadcast + fma with 0
-            if (WRITE_Y) acc = s == 0 ? row_bcast<vc % 16>(bcr[vc / 16]) * h[s]
-                                      : fmaf(row_bcast<vc % 16>(bcr[vc / 16]), h[s], acc);
-          });
-          if (WRITE_Y) s_yp[buf][w][tt][lane] = acc;
+          const float a = fast_exp2(dcv[v] * A2);
+          h = fmaf(a, h, row_bcast<tt>(rb) * dxv[v]);
+          if (YSUM) s_yp[buf][(tt * CT + cl) * PN + s] = row_bcast<tt>(rc) * h;
         });
       });
-      if (p.ckpt != nullptr) {
-        const bool ok = cvalid && blk < nblk;
-#pragma unroll
-        for (int s = 0; s < K; ++s)
-          bstore<float>(r_ck, ok ? (((unsigned)blk * N + w * K + s) * dim + c) * 4u : OOB_OFF, h[s]);
-      }
+      if (p.ckpt != nullptr)
+        bstore<float>(r_ck, (cvalid && blk < nblk) ? (((unsigned)blk * N + s) * dim + c) * 4u : OOB_OFF, h);
       stage((u + 1) % PD, t0 + TS, buf ^ 1, nx, nz);
       fetch(u, min(blk + PD, nblk - 1) * TS);
       __syncthreads();
-      // ---- y for the (t, d) this thread staged: sum the wave partials, D skip, gate ----
-      if (WRITE_Y) {
+      // ---- y for the (t, d) this thread staged: sum over the states, D skip, gate ----
+      if (YSUM) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
-          const int tt = w + i * NW;
-          float y = 0.0f;
+          if (NE % NT != 0 && tid + i * NT >= NE) continue;
+          const float* src = &s_yp[buf][(et[i] * CT + ec[i]) * PN];
+          float y;
+          if constexpr (PN % 4 == 0) {
+            const float4 f0 = *reinterpret_cast<const float4*>(src);
+            y = (f0.x + f0.y) + (f0.z + f0.w);
 #pragma unroll
-          for (int v = 0; v < NW; ++v) y += s_yp[buf][v][tt][lane];
-          y = fmaf(Dc, cx[i], y);
+            for (int v = 4; v < N; v += 4) {
+              const float4 f = *reinterpret_cast<const float4*>(src + v);
+              y += (f.x + f.y) + (f.z + f.w);
+            }
+          } else {
+            y = src[0];
+#pragma unroll
+            for (int v = 1; v < N; ++v) y += src[v];
+          }
+          y = fmaf(eD[i], cx[i], y);
+          const unsigned off =
+              (ev[i] && t0 + et[i] < seq) ? ((unsigned)(t0 + et[i]) * dim + tile * CT + ec[i]) * (unsigned)sizeof(TI)
+                                          : OOB_OFF;
+          if (SAVE_YP) bstore<TI>(r_yp, off, y);
           if (HAS_Z) y *= cz[i] * sigmoid_rcp(cz[i]);
-          bstore<TI>(r_y, (t0 + tt < seq && cvalid) ? ((unsigned)(t0 + tt) * dim + c) * (unsigned)sizeof(TI) : OOB_OFF,
-                     y);
+          if (WRITE_Y) bstore<TI>(r_y, off, y);
         }
       }
 #pragma unroll
@@ -292,33 +322,39 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_fwd_kernel(const SSAr
 // ---------------------------------------------------------------------------
 // backward
 // ---------------------------------------------------------------------------
-template <typename TI, typename TP, int N, int KMAX, bool MEAN, bool HAS_Z>
-__global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSArgs p, const TP* __restrict__ Bm,
-                                                                      const TP* __restrict__ Cm) {
-  using G = SSGeo<N, KMAX>;
-  constexpr int K = G::K, NW = G::NW, NT = G::NT;
-  static_assert(K == 1 || K == 2 || K == 4, "backward keeps one, two or four states per lane");
-  constexpr int CK = SS_CK;          // recompute chunk (= checkpoint interval)
-  constexpr int TS = 16 / K;         // reduction block (timesteps): 2 K TS = 32 outputs per wave
-  constexpr bool BC_REG = K <= 2;    // the chunk's B/C values held in registers (else read from LDS)
-  constexpr int PS = CK + 4;         // [channel][t] row stride (16-byte reads conflict-free)
-  constexpr int EPT = CK * 64 / NT;  // staged (t, channel) elements per thread
-  constexpr int GS = 2 * K * TS + 4;  // per-lane stride of a wave's dC/dB tile: b128 writes conflict-free
-  constexpr int OPW = 2 * K * TS;     // dC/dB outputs per wave per block
-  constexpr int LPO = 64 / OPW;       // lanes per output (each sums 64 / LPO channels)
-  static_assert(EPT * NW == CK && CK % TS == 0 && LPO == 2, "staging layout");
-  constexpr int BCN = CK * 2 * N;               // B/C values staged per chunk
-  constexpr int BCT = (BCN + NT - 1) / NT;      // per thread (the last round partly idle)
-  __shared__ __align__(16) float s_bc[CK][2 * N];  // per t: B[0..N), C[0..N)
-  __shared__ __align__(16) float s_dtc[64][PS];
-  __shared__ __align__(16) float s_dtx[64][PS];
-  __shared__ __align__(16) float s_dy[64][PS];
-  // each wave's private dC/dB tile: [lane][t][qty][state], reduced by the wave itself
-  __shared__ __align__(16) float s_g[NW][64 * GS];
-  // per-(t, d) partial sums over each wave's states for the chunk, px and pa
-  // ([2][NW][CK][64]); the same memory first holds the gate's y partials ([NW][CK][64])
-  __shared__ float s_pp[2 * NW * CK * 64];
-  __shared__ float s_m[MEAN ? CK : 1][64];
+template <typename TI, typename TP, int N, int G, bool MEAN, bool HAS_Z>
+__global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p, const TP* __restrict__ Bm,
+                                                                  const TP* __restrict__ Cm) {
+  using Geo = RGeo<N, G>;
+  constexpr int SW = Geo::SW, CW = Geo::CW, NT = Geo::NT, CT = Geo::CT;
+  constexpr int CK = SS_CK;                 // recompute chunk (= checkpoint interval)
+  constexpr int TS = N >= 32 ? 4 : 8;       // reverse steps per reduction round
+  constexpr int NSB = CK / TS;
+  constexpr int PS = CK + 4;                // [channel][t] row stride of the staged values
+  constexpr int NE = CK * CT;               // staged (t, channel) elements per chunk
+  constexpr int EPT = (NE + NT - 1) / NT;
+  // px / pa tile [qty][t][channel][state]: a lane's state-sum item reads one contiguous row;
+  // PN makes the rows of one wave's writes and the 16-byte reads of consecutive channels
+  // conflict-free, QP puts the two quantities of one (t, channel) on different banks
+  constexpr int PN = ss_pn<N>();
+  constexpr int QP = mod64_to(TS * CT * PN, 32);
+  // dC / dB tile [qty][state][t][group][CW + 4]: a channel-group item reads one contiguous
+  // run of CW values; SSR puts a wave's state rows on different banks
+  constexpr int CWP = CW + 4, CTP = G * CWP;
+  constexpr int SSR = mod64_to(TS * CTP, CW % 64);
+  constexpr int NA = 2 * TS * CT;           // state sums per round: (t, channel, dx | ddt term)
+  constexpr int NB = 2 * TS * N * G;        // channel-group sums per round: (qty, t, state, group)
+  constexpr int NC = 2 * TS * N;            // partials per round: (qty, t, state)
+  static_assert(NT % CT == 0, "a thread's staged elements share one channel");
+  // staged per chunk, double-buffered: clip(dt) with the sign bit set where the raw dt lies
+  // outside [DT_MIN, DT_MAX] (no gradient), dt_b x, dy (after the gate)
+  __shared__ __align__(16) float s_st[2][3][CT][PS];
+  __shared__ float s_dtm[MEAN ? 2 : 1][CK];
+  __shared__ __align__(16) float s_pq[2 * QP];
+  __shared__ __align__(16) float s_bc[2 * N * SSR];
+  __shared__ float s_red[2][2][TS][N][G];
+  __shared__ float s_m[MEAN ? 2 : 1][MEAN ? TS : 1][CT];
+  __shared__ float s_Dv[CT];
 
   const TI* __restrict__ x = (const TI*)p.x;
   const TI* __restrict__ dt = (const TI*)p.dt;
@@ -330,273 +366,269 @@ __global__ __launch_bounds__((SSGeo<N, KMAX>::NT)) void ss_bwd_kernel(const SSAr
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = uniform(tid >> 6);
+  const int g = w % G, sg = w / G;
+  const int s = sg * SW + lane / CW;
+  const int cl = g * CW + lane % CW;
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int b = logical / p.ntile, tile = logical % p.ntile;
-  const int c = tile * 64 + lane;
+  const int c = tile * CT + cl;
   const bool cvalid = c < dim;
-  const int cc = min(c, dim - 1);
-  auto pp = [&](int q, int v, int t) -> float& { return s_pp[((q * NW + v) * CK + t) * 64 + lane]; };
 
   const int ns = p.nst;
-  float A1[K], A2[K], dh[K], dA[K];
-#pragma unroll
-  for (int s = 0; s < K; ++s) {
-    A1[s] = (cvalid && w * K + s < ns) ? ld(Am, (long)c * ns + w * K + s) : 0.0f;
-    A2[s] = A1[s] * LOG2E;
-    dh[s] = 0.0f;
-    dA[s] = 0.0f;
-  }
-  const float Dc = (Dv != nullptr && cvalid) ? ld(Dv, c) : 0.0f;
-  float dD = 0.0f;
-  const long rowbase = (long)b * seq * dim;
+  const float A1 = (cvalid && s < ns) ? ld(Am, (long)c * ns + s) : 0.0f;
+  const float A2 = A1 * LOG2E;
+  float dh = 0.0f, dA = 0.0f;
 
-  // raw values of the next chunk (in reverse order), loaded a chunk ahead through buffer
-  // resources on this batch row (SGPR base, 32-bit offsets: no 64-bit address VALU)
+  // staged elements (t, channel): e = tid + i NT
+  int et[EPT], ec[EPT];
+  bool ev[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = tid + i * NT;
+    et[i] = e / CT;
+    ec[i] = e % CT;
+    ev[i] = e < NE && tile * CT + ec[i] < dim;
+  }
+  // D per channel of the tile; dD accumulates over the elements this thread stages (all
+  // of one channel, since NT is a multiple of CT)
+  if (tid < CT) s_Dv[tid] = (Dv != nullptr && tile * CT + tid < dim) ? ld(Dv, tile * CT + tid) : 0.0f;
+  const int aq = tid & 1;  // the quantity of this thread's state-sum items (NT is even)
+  float dD = 0.0f;
+
+  const long rowbase = (long)b * seq * dim;
   typedef typename Bits<TI>::type RI;
   typedef typename Bits<TP>::type RP;
   const unsigned rowbytes = (unsigned)((long)seq * dim * sizeof(TI));
   const rsrc_t r_x = make_rsrc(x + rowbase, rowbytes), r_dt = make_rsrc(dt + rowbase, rowbytes);
   const rsrc_t r_do = make_rsrc(dout + rowbase, rowbytes);
   const rsrc_t r_z = make_rsrc(HAS_Z ? z + rowbase : x + rowbase, rowbytes);
+  const rsrc_t r_yp = make_rsrc(HAS_Z ? (const TI*)p.ypre + rowbase : x + rowbase, rowbytes);
   const unsigned bcbytes = (unsigned)((long)seq * ns * sizeof(TP));
   const rsrc_t r_B = make_rsrc(Bm + (long)b * seq * ns, bcbytes), r_C = make_rsrc(Cm + (long)b * seq * ns, bcbytes);
   const rsrc_t r_m =
       make_rsrc(MEAN ? (const void*)(p.dtmean + (long)b * seq) : (const void*)x, (unsigned)(seq * sizeof(float)));
   const rsrc_t r_dx = make_rsrc((TI*)p.dx + rowbase, rowbytes), r_ddt = make_rsrc((TI*)p.ddt + rowbase, rowbytes);
-  const rsrc_t r_dz = make_rsrc(p.dz != nullptr ? (TI*)p.dz + rowbase : (TI*)p.dx + rowbase, rowbytes);
-  RI rx[EPT], rdt[EPT], rdo[EPT], rz[EPT];
-  RP rbc[BCT];
+  const rsrc_t r_dz = make_rsrc(p.dz != nullptr ? (TI*)p.dz + rowbase : (TI*)p.dx + rowbase,
+                                p.dz != nullptr ? rowbytes : 0u);
+  const rsrc_t r_ck = make_rsrc(p.ckpt + (long)b * p.nck * N * dim, (unsigned)((long)p.nck * N * dim * 4));
+
+  // raw values of the next chunk (in reverse order), loaded a chunk ahead
+  RI rx[EPT], rdt[EPT], rdo[EPT], rz[EPT], ryp[EPT];
   float rm[EPT];
-  float rck[K];  // the checkpoint the fetched chunk starts from (its predecessor's state)
-  // this thread's staged (t, d) values, kept for the per-(t, d) epilogues
-  float ex[EPT], edtb[EPT], emask[EPT], edy[EPT], ego[EPT], ez[EPT];
+  RP rB, rC;
+  float rck;  // the state the fetched chunk starts from (its predecessor's checkpoint)
+  // B/C values and starting state of the staged chunk, moved from the fetch registers
+  float cB, cC, cck;
   auto fetch = [&](int ts) {
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      const int t = min(ts + w + i * NW, seq - 1);
-      const unsigned off = ((unsigned)t * dim + cc) * (unsigned)sizeof(TI);
+      const int t = min(ts + et[i], seq - 1);
+      const unsigned off = ev[i] ? ((unsigned)t * dim + tile * CT + ec[i]) * (unsigned)sizeof(TI) : OOB_OFF;
       rx[i] = bload<TI>(r_x, off);
       rdt[i] = bload<TI>(r_dt, off);
       rdo[i] = bload<TI>(r_do, off);
-      if (HAS_Z) rz[i] = bload<TI>(r_z, off);
+      if (HAS_Z) {
+        rz[i] = bload<TI>(r_z, off);
+        ryp[i] = bload<TI>(r_yp, off);
+      }
       rm[i] = MEAN ? bits_f32(bload<float>(r_m, (unsigned)t * 4u)) : 0.0f;
     }
-#pragma unroll
-    for (int i = 0; i < BCT; ++i) {
-      const int e = min(tid + i * NT, BCN - 1);  // clamped: the load stays unconditional
-      const int r = e % (2 * N);
-      // padding states (r % N >= ns) read 0 through an out-of-range offset
-      const unsigned off = r % N < ns ? ((unsigned)min(ts + e / (2 * N), seq - 1) * ns + (r % N)) * (unsigned)sizeof(TP)
-                                      : OOB_OFF;
-      // lanes split between B and C: both loads issue, the other one out of bounds reads 0
-      rbc[i] = bload<TP>(r_B, r < N ? off : OOB_OFF) | bload<TP>(r_C, r < N ? OOB_OFF : off);
-    }
-    const int kp = max(ts / CK - 1, 0);  // chunk 0 starts from zero (selected at use)
-#pragma unroll
-    for (int s = 0; s < K; ++s) rck[s] = p.ckpt[(((long)b * p.nck + kp) * N + w * K + s) * dim + cc];
+    const unsigned off = s < ns ? ((unsigned)(ts + min(lane & 15, seq - 1 - ts)) * ns + s) * (unsigned)sizeof(TP)
+                                : OOB_OFF;
+    rB = bload<TP>(r_B, off);
+    rC = bload<TP>(r_C, off);
+    // chunk 0 starts from zero (selected at use); the load stays unconditional
+    const int kp = max(ts / CK - 1, 0);
+    rck = bits_f32(bload<float>(r_ck, cvalid ? (((unsigned)kp * N + s) * dim + c) * 4u : OOB_OFF));
   };
-
-  // The next chunk's inputs and checkpoint are fetched one chunk ahead, unconditionally
-  // (chunk 0 fetches itself again): a conditional fetch makes the compiler drain every
-  // outstanding load at the loop latch.
-  fetch((p.nck - 1) * CK);
-  for (int k = p.nck - 1; k >= 0; --k) {
-    const int ts = k * CK;
-    // ---- stage the chunk ---------------------------------------------------------
-#pragma unroll
-    for (int i = 0; i < BCT; ++i) {
-      const int e = tid + i * NT;
-      if (BCN % NT == 0 || e < BCN) s_bc[e / (2 * N)][e % (2 * N)] = bits_f32(rbc[i]);
-    }
+  // stage the fetched chunk (first step ts) into buffer sb; the gate's dz is stored here;
+  // wgt = 0 when the chunk was staged before (dD counts each element once)
+  auto stage = [&](int ts, int sb, float wgt) {
+    cB = bits_f32(rB);
+    cC = bits_f32(rC);
+    cck = rck;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-      const int tt = w + i * NW;
-      const bool ok = (ts + tt < seq) && cvalid;
+      if (NE % NT != 0 && tid + i * NT >= NE) continue;
+      const bool ok = ev[i] && ts + et[i] < seq;
       const float dtr = bits_f32(rdt[i]);
       const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
       const float dtb = ok ? (MEAN ? rm[i] : dtc) : 0.0f;
       const float xv = ok ? bits_f32(rx[i]) : 0.0f;
-      ex[i] = xv;
-      edtb[i] = dtb;
-      emask[i] = (ok && dtr >= DT_MIN && dtr <= DT_MAX) ? 1.0f : 0.0f;
-      ego[i] = ok ? bits_f32(rdo[i]) : 0.0f;
-      ez[i] = (HAS_Z && ok) ? bits_f32(rz[i]) : 0.0f;
-      s_dtc[lane][tt] = dtc;
-      s_dtx[lane][tt] = dtb * xv;
-      if (!HAS_Z) {
-        edy[i] = ego[i];
-        s_dy[lane][tt] = ego[i];
+      const float go = ok ? bits_f32(rdo[i]) : 0.0f;
+      float dyp = go;
+      if (HAS_Z) {
+        const float zv = bits_f32(rz[i]);
+        const float sgm = sigmoid_rcp(zv);
+        dyp = go * zv * sgm;
+        const unsigned off = ok ? ((unsigned)(ts + et[i]) * dim + tile * CT + ec[i]) * (unsigned)sizeof(TI) : OOB_OFF;
+        bstore<TI>(r_dz, off, go * bits_f32(ryp[i]) * sgm * (1.0f + zv * (1.0f - sgm)));
       }
+      dD = fmaf(wgt * dyp, xv, dD);
+      s_st[sb][0][ec[i]][et[i]] = (dtr >= DT_MIN && dtr <= DT_MAX) ? dtc : -dtc;
+      s_st[sb][1][ec[i]][et[i]] = dtb * xv;
+      s_st[sb][2][ec[i]][et[i]] = dyp;
+      if (MEAN && ec[i] == 0) s_dtm[sb][et[i]] = ok ? rm[i] : 0.0f;
     }
-    float ck0[K];
-#pragma unroll
-    for (int s = 0; s < K; ++s) ck0[s] = rck[s];
-    fetch(max(k - 1, 0) * CK);
-    __syncthreads();
+  };
 
-    // ---- recompute the chunk's states and decays from its checkpoint ---------------
-    // states, decays and this wave's B/C values of the chunk, kept in registers for the
-    // reverse pass (reading B/C from LDS once per chunk halves that LDS traffic)
-    float h0[K], hs[CK][K], as[CK][K], bB[BC_REG ? CK : 1][K], bC[BC_REG ? CK : 1][K];
+  // channel-group sums of the previous round -> this workgroup's dC/dB partial; dt-mean
+  // coupling of the previous round -> its partial
+  auto finish_round = [&](int par, int ts0) {
+#pragma unroll 1
+    for (int it = tid; it < NC + (MEAN ? TS : 0); it += NT) {
+      if (it < NC) {
+        const int sn = it % N, tl = (it / N) % TS, q = it / (N * TS);
+        float v = s_red[par][q][tl][sn][0];
 #pragma unroll
-    for (int s = 0; s < K; ++s)
-      h0[s] = (k > 0 && cvalid) ? ck0[s] : 0.0f;
-    {
-      float hh[K];
-#pragma unroll
-      for (int s = 0; s < K; ++s) hh[s] = h0[s];
-#pragma unroll
-      for (int q = 0; q < CK / 4; ++q) {
-        const float4 dc4 = *reinterpret_cast<const float4*>(&s_dtc[lane][4 * q]);
-        const float4 dx4 = *reinterpret_cast<const float4*>(&s_dtx[lane][4 * q]);
-        const float dcv[4] = {dc4.x, dc4.y, dc4.z, dc4.w};
-        const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int j = 4 * q + u;
-          const float* bc = &s_bc[j][w * K];
-          float acc = 0.0f;
-#pragma unroll
-          for (int s = 0; s < K; ++s) {
-            if constexpr (BC_REG) {
-              bB[j][s] = bc[s];
-              bC[j][s] = bc[N + s];
-            }
-            const float a = fast_exp2(dcv[u] * A2[s]);
-            hh[s] = fmaf(a, hh[s], dxv[u] * bc[s]);
-            as[j][s] = a;
-            hs[j][s] = hh[s];
-            if (HAS_Z) acc = fmaf(bc[N + s], hh[s], acc);
-          }
-          if (HAS_Z) pp(0, w, j) = acc;
-        }
+        for (int gg = 1; gg < G; ++gg) v += s_red[par][q][tl][sn][gg];
+        const int t = ts0 + tl;
+        if (t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + q) * N + sn] = v;
+      } else if (MEAN) {
+        const int tl = it - NC;
+        float v = 0.0f;
+        for (int cc = 0; cc < CT; ++cc) v += s_m[MEAN ? par : 0][MEAN ? tl : 0][cc];
+        const int t = ts0 + tl;
+        if (t < seq) p.part_m[((long)tile * p.batch + b) * seq + t] = v;
       }
     }
+  };
 
-    // ---- gate: dy = dout silu(z); dz = dout y silu'(z) (y before the gate) -----------
-    if (HAS_Z) {
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < EPT; ++i) {
-        const int tt = w + i * NW;
-        float y = 0.0f;
-#pragma unroll
-        for (int v = 0; v < NW; ++v) y += pp(0, v, tt);
-        y = fmaf(Dc, ex[i], y);
-        const float sg = sigmoid_rcp(ez[i]);
-        edy[i] = ego[i] * ez[i] * sg;
-        s_dy[lane][tt] = edy[i];
-        if (p.dz != nullptr)
-          bstore<TI>(r_dz, (ts + tt < seq && cvalid) ? ((unsigned)(ts + tt) * dim + c) * (unsigned)sizeof(TI) : OOB_OFF,
-                     ego[i] * y * sg * (1.0f + ez[i] * (1.0f - sg)));
-      }
-      __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) dD = fmaf(edy[i], ex[i], dD);
-
-    // ---- reverse recurrence, in blocks of TS timesteps ------------------------------
-#pragma unroll
-    for (int jb = CK - TS; jb >= 0; jb -= TS) {
-      float dyv[TS], dcv[TS], dxv[TS];
-#pragma unroll
-      for (int q = 0; q < TS / 4; ++q) {
-        const float4 a4 = *reinterpret_cast<const float4*>(&s_dy[lane][jb + 4 * q]);
-        const float4 b4 = *reinterpret_cast<const float4*>(&s_dtc[lane][jb + 4 * q]);
-        const float4 c4 = *reinterpret_cast<const float4*>(&s_dtx[lane][jb + 4 * q]);
-        dyv[4 * q] = a4.x; dyv[4 * q + 1] = a4.y; dyv[4 * q + 2] = a4.z; dyv[4 * q + 3] = a4.w;
-        dcv[4 * q] = b4.x; dcv[4 * q + 1] = b4.y; dcv[4 * q + 2] = b4.z; dcv[4 * q + 3] = b4.w;
-        dxv[4 * q] = c4.x; dxv[4 * q + 1] = c4.y; dxv[4 * q + 2] = c4.z; dxv[4 * q + 3] = c4.w;
-      }
-      float* g = &s_g[w][lane * GS];
-#pragma unroll
-      for (int j = TS - 1; j >= 0; --j) {
-        const int jj = jb + j;
-        float px = 0.0f, pa = 0.0f, gC[K], gB[K];
-#pragma unroll
-        for (int s = 0; s < K; ++s) {
-          const float Bv = BC_REG ? bB[BC_REG ? jj : 0][s] : s_bc[jj][w * K + s];
-          const float Cv = BC_REG ? bC[BC_REG ? jj : 0][s] : s_bc[jj][N + w * K + s];
-          dh[s] = fmaf(dyv[j], Cv, dh[s]);
-          gC[s] = dyv[j] * hs[jj][s];
-          gB[s] = dh[s] * dxv[j];
-          px = fmaf(dh[s], Bv, px);
-          dh[s] *= as[jj][s];
-          const float ga = dh[s] * (jj > 0 ? hs[jj - 1][s] : h0[s]);
-          dA[s] = fmaf(ga, dcv[j], dA[s]);
-          pa = fmaf(ga, A1[s], pa);
-        }
-        if constexpr (K == 4) {
-          *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gC[2], gC[3]);
-          *reinterpret_cast<float4*>(g + j * 2 * K + K) = make_float4(gB[0], gB[1], gB[2], gB[3]);
-        } else if constexpr (K == 2) {
-          *reinterpret_cast<float4*>(g + j * 2 * K) = make_float4(gC[0], gC[1], gB[0], gB[1]);
-        } else {
-          *reinterpret_cast<float2*>(g + j * 2 * K) = make_float2(gC[0], gB[0]);
-        }
-        pp(0, w, jj) = px;
-        pp(1, w, jj) = pa;
-      }
-      // sums over the 64 channels of this wave's dC (qty 0) and dB (qty 1) per (t, n):
-      // the tile is the wave's own, so LDS ordering within the wave replaces a barrier
-      // and other waves keep computing meanwhile.  Output o = (t, qty, state) is the
-      // o-th float of every lane row; LPO = 2 lanes share it (channels 0..31 / 32..63).
-      {
-        __builtin_amdgcn_wave_barrier();  // keep the tile writes before the column reads
-        const int o = lane % OPW, hf = lane / OPW;
-        const float* src = &s_g[w][hf * (64 / LPO) * GS + o];
-        float acc = 0.0f;
-#pragma unroll 16
-        for (int l = 0; l < 64 / LPO; ++l) acc += src[l * GS];
-        __builtin_amdgcn_wave_barrier();  // and the reads before the next block's writes
-        acc += __shfl_xor(acc, 32);
-        const int j = o / (2 * K), qty = (o / K) % 2, n = w * K + o % K;
-        const int t = ts + jb + j;
-        if (hf == 0 && t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + qty) * N + n] = acc;
-      }
-    }
-    // ---- sums over the states: dx, ddt for the (t, d) this thread staged --------------
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      const int tt = w + i * NW;
-      float pxs = 0.0f, pas = 0.0f;
-#pragma unroll
-      for (int v = 0; v < NW; ++v) {
-        pxs += pp(0, v, tt);
-        pas += pp(1, v, tt);
-      }
-      {
-        const unsigned off = (ts + tt < seq && cvalid) ? ((unsigned)(ts + tt) * dim + c) * (unsigned)sizeof(TI) : OOB_OFF;
-        bstore<TI>(r_dx, off, fmaf(pxs, edtb[i], edy[i] * Dc));
-        bstore<TI>(r_ddt, off, emask[i] * (MEAN ? pas : fmaf(pxs, ex[i], pas)));
-      }
-      if (MEAN) s_m[tt][lane] = pxs * ex[i];  // dt-mean coupling, summed over channels below
-    }
-    if (MEAN) {
-      __syncthreads();
-      if (tid < CK) {
-        float acc = 0.0f;
-        for (int l = 0; l < 64; ++l) acc += s_m[tid][l];
-        const int t = ts + tid;
-        if (t < seq) p.part_m[((long)tile * p.batch + b) * seq + t] = acc;
-      }
-    }
-  }
-  // dA partial per (b, d, n); dD partial per (b, d): the lanes of one channel in the
-  // NW waves hold disjoint timesteps
-  if (cvalid) {
-#pragma unroll
-    for (int s = 0; s < K; ++s) p.part_a[((long)b * dim + c) * N + w * K + s] = dA[s];
-  }
-  __syncthreads();  // the last chunk's epilogue has read s_pp
-  pp(0, w, 0) = dD;
+  fetch((p.nck - 1) * CK);
+  stage((p.nck - 1) * CK, (p.nck - 1) & 1, 1.0f);
+  fetch(max(p.nck - 2, 0) * CK);
   __syncthreads();
-  if (w == 0 && cvalid) {
-    float acc = 0.0f;
+  int prev_par = -1, prev_ts = 0, par = 0;
+
+  for (int k = p.nck - 1; k >= 0; --k) {
+    const int ts = k * CK, sb = k & 1;
+    // the chunk's B/C values and starting state (moved out of the fetch registers when the
+    // chunk was staged).  The reverse pass broadcasts B from a separate copy: the
+    // compiler would otherwise share one broadcast between the two passes and fold it into
+    // neither multiply.
+    const float rb = cB, rc = cC;
+    float rb2;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(rb2) : "v"(rb));
+    const float h0 = (k > 0 && cvalid) ? cck : 0.0f;
+    // ---- recompute the chunk's states and decays from its checkpoint; the chunk's staged
+    // dt values stay in registers for the reverse pass ---------------------------------
+    float hs[CK], as[CK], dcs[CK], dxs[CK];
+    {
+      float hh = h0;
+      static_for<CK / 4>([&](auto qi) {
+        constexpr int q = decltype(qi)::value;
+        const float4 dc4 = *reinterpret_cast<const float4*>(&s_st[sb][0][cl][4 * q]);
+        const float4 dx4 = *reinterpret_cast<const float4*>(&s_st[sb][1][cl][4 * q]);
+        dcs[4 * q] = dc4.x; dcs[4 * q + 1] = dc4.y; dcs[4 * q + 2] = dc4.z; dcs[4 * q + 3] = dc4.w;
+        dxs[4 * q] = dx4.x; dxs[4 * q + 1] = dx4.y; dxs[4 * q + 2] = dx4.z; dxs[4 * q + 3] = dx4.w;
+        static_for<4>([&](auto vi) {
+          constexpr int tt = 4 * q + decltype(vi)::value;
+          const float a = fast_exp2(fabsf(dcs[tt]) * A2);
+          hh = fmaf(a, hh, row_bcast<tt>(rb) * dxs[tt]);
+          as[tt] = a;
+          hs[tt] = hh;
+        });
+      });
+    }
+    // ---- reverse recurrence in rounds of TS steps --------------------------------
+    static_for<NSB>([&](auto ui) {
+      constexpr int u = NSB - 1 - decltype(ui)::value;  // round u covers steps u TS .. u TS + TS - 1
+      static_for<TS / 4>([&](auto qi) {
+        constexpr int q = TS / 4 - 1 - decltype(qi)::value;
+        constexpr int tq = u * TS + 4 * q;
+        const float4 dy4 = *reinterpret_cast<const float4*>(&s_st[sb][2][cl][tq]);
+        const float dyv[4] = {dy4.x, dy4.y, dy4.z, dy4.w};
+        static_for<4>([&](auto vi) {
+          constexpr int v = 3 - decltype(vi)::value, tt = tq + v, tl = tt - u * TS;
+          dh = fmaf(dyv[v], row_bcast<tt>(rc), dh);
+          const float gC = dyv[v] * hs[tt];
+          const float gB = dh * dxs[tt];
+          const float px = dh * row_bcast<tt>(rb2);
+          dh *= as[tt];
+          const float ga = dh * (tt > 0 ? hs[tt > 0 ? tt - 1 : 0] : h0);
+          dA = fmaf(ga, fabsf(dcs[tt]), dA);
+          s_pq[(tl * CT + cl) * PN + s] = px;
+          s_pq[QP + (tl * CT + cl) * PN + s] = ga * A1;
+          s_bc[s * SSR + tl * CTP + g * CWP + lane % CW] = gC;
+          s_bc[N * SSR + s * SSR + tl * CTP + g * CWP + lane % CW] = gB;
+        });
+      });
+      if (u == 0) {
+        // the next chunk's inputs into the other staging buffer (last read by the chunk
+        // before this one), and the chunk after it into the registers; unconditional
+        // (chunk 0 stages itself again, counted with weight 0): a conditional fetch makes
+        // the compiler drain every outstanding load
+        stage(max(k - 1, 0) * CK, sb ^ 1, k > 0 ? 1.0f : 0.0f);
+        fetch(max(k - 2, 0) * CK);
+      }
+      __syncthreads();
+      // ---- state sums -> dx, ddt; channel-group sums -> s_red ----------------------
+#pragma unroll 1
+      for (int it = tid; it < NA; it += NT) {
+        const int tl = (it >> 1) / CT, tt = u * TS + tl, ac = (it >> 1) % CT;
+        const float* src = &s_pq[aq * QP + (tl * CT + ac) * PN];
+        float v;
+        if constexpr (PN % 4 == 0) {
+          const float4 f0 = *reinterpret_cast<const float4*>(src);
+          v = (f0.x + f0.y) + (f0.z + f0.w);
 #pragma unroll
-    for (int v = 0; v < NW; ++v) acc += pp(0, v, 0);
-    p.part_d[(long)b * dim + c] = acc;
+          for (int sn = 4; sn < N; sn += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(src + sn);
+            v += (f.x + f.y) + (f.z + f.w);
+          }
+        } else {
+          v = src[0];
+#pragma unroll
+          for (int sn = 1; sn < N; ++sn) v += src[sn];
+        }
+        const float other = pair_swap(v);
+        const float pxs = aq ? other : v, pas = aq ? v : other;
+        const float dcr = s_st[sb][0][ac][tt], dtx = s_st[sb][1][ac][tt], dyp = s_st[sb][2][ac][tt];
+        const float dtb = MEAN ? s_dtm[MEAN ? sb : 0][tt] : fabsf(dcr);
+        // x = dt_b x / dt_b (dt_b >= DT_MIN wherever the element is inside the tensor)
+        const float xv = dtb > 0.0f ? dtx * fast_rcp(dtb) : 0.0f;
+        const bool ok = tile * CT + ac < dim && ts + tt < seq;
+        const unsigned off = ok ? ((unsigned)(ts + tt) * dim + tile * CT + ac) * (unsigned)sizeof(TI) : OOB_OFF;
+        if (aq == 0) {
+          bstore<TI>(r_dx, off, fmaf(pxs, dtb, dyp * s_Dv[ac]));
+          if (MEAN) s_m[MEAN ? par : 0][MEAN ? tl : 0][ac] = pxs * xv;
+        } else {
+          const float mk = dcr > 0.0f ? 1.0f : 0.0f;
+          bstore<TI>(r_ddt, off, mk * (MEAN ? pas : fmaf(pxs, xv, pas)));
+        }
+      }
+#pragma unroll 1
+      for (int it = tid; it < NB; it += NT) {
+        const int gg = it % G, tl = (it / G) % TS, sn = (it / (G * TS)) % N, q = it / (G * TS * N);
+        const float* src = &s_bc[(q * N + sn) * SSR + tl * CTP + gg * CWP];
+        const float4 f0 = *reinterpret_cast<const float4*>(src);
+        float v = (f0.x + f0.y) + (f0.z + f0.w);
+#pragma unroll
+        for (int cc = 4; cc < CW; cc += 4) {
+          const float4 f = *reinterpret_cast<const float4*>(src + cc);
+          v += (f.x + f.y) + (f.z + f.w);
+        }
+        s_red[par][q][tl][sn][gg] = v;
+      }
+      if (prev_par >= 0) finish_round(prev_par, prev_ts);
+      prev_par = par;
+      prev_ts = ts + u * TS;
+      par ^= 1;
+      __syncthreads();  // the tiles are rewritten by the next round
+    });
+  }
+  finish_round(prev_par, prev_ts);
+  // dA partial per (b, d, n); dD partial per (b, d): threads with the same channel hold
+  // disjoint timesteps
+  if (cvalid) p.part_a[((long)b * dim + c) * N + s] = dA;
+  float* s_dd = s_pq;
+  s_dd[tid] = dD;
+  __syncthreads();
+  if (tid < CT && tile * CT + tid < dim) {
+    float acc = 0.0f;
+#pragma unroll 1
+    for (int kk = 0; kk < NT / CT; ++kk) acc += s_dd[kk * CT + tid];
+    p.part_d[(long)b * dim + tile * CT + tid] = acc;
   }
 }
 
@@ -671,25 +703,78 @@ inline int padded_state(int N) {
   return np;
 }
 
-// one workgroup per (batch, 64-channel tile)
-inline int ntiles(int dim) { return (dim + 63) / 64; }
-
 inline long num_chunks(int seq) { return (seq + SS_CK - 1) / SS_CK; }
 
-struct WsLayout {
-  size_t ckpt, dtmean, part_bc, part_a, part_d, part_m, total;
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Channel groups per workgroup.  The kernels are compiled for G = 1 and for a wide G per
+// state size; the host takes the one whose grid loads the busiest CU with the fewest
+// waves (workgroups spread evenly over 256 CUs, at most as many per CU as LDS and the
+// 32 waves per CU allow), the wide one on a tie (fewer dC/dB partials, longer rows).
+struct SSPlan {
+  int G, CT, ntile;
 };
 
-inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+inline int wide_groups(int NP) { return NP >= 32 ? 1 : (NP == 16 ? 3 : (NP >= 4 ? 4 : 1)); }
+
+// LDS bytes of one workgroup (mirrors the kernels' __shared__ declarations)
+inline size_t fwd_lds(int NP, int G) {
+  const int SW = NP < 4 ? NP : 4, CW = 64 / SW, CT = G * CW, PN = NP == 4 ? 12 : NP + 4;
+  return (size_t)2 * 2 * CT * (SS_CK + 4) * 4 + (size_t)2 * SS_CK * CT * PN * 4;
+}
+inline int mod64_up(int v, int r) { return v + ((r - v % 64) % 64 + 64) % 64; }
+inline size_t bwd_lds(int NP, int G) {
+  const int SW = NP < 4 ? NP : 4, CW = 64 / SW, CT = G * CW, TS = NP >= 32 ? 4 : 8;
+  const int PN = NP == 4 ? 12 : NP + 4, QP = mod64_up(TS * CT * PN, 32), SSR = mod64_up(TS * G * (CW + 4), CW % 64);
+  return (size_t)2 * 3 * CT * (SS_CK + 4) * 4 + 2 * SS_CK * 4 + (size_t)2 * QP * 4 + (size_t)2 * NP * SSR * 4 +
+         (size_t)2 * 2 * TS * NP * G * 4 + (size_t)2 * TS * CT * 4 + CT * 4;
+}
+
+inline SSPlan choose_plan(int batch, int dim, int NP, bool bwd) {
+  const int SW = NP < 4 ? NP : 4, CW = 64 / SW, NSG = NP / SW;
+  const int gw = wide_groups(NP);
+  SSPlan best{gw, gw * CW, (dim + gw * CW - 1) / (gw * CW)};
+#if defined(EDF_SS_FORCE_G)
+  if (EDF_SS_FORCE_G == 1) return SSPlan{1, CW, (dim + CW - 1) / CW};
+  return best;
+#endif
+  double best_score = 1e30;
+  const int cands[2] = {gw, 1};
+  for (int G : cands) {
+    const int CT = G * CW, nt = (dim + CT - 1) / CT, nw = G * NSG;
+    const long nwg = (long)batch * nt;
+    const size_t lds = bwd ? bwd_lds(NP, G) : fwd_lds(NP, G);
+    const long occ = std::max(1L, std::min((long)(163840 / lds), (long)(32 / nw)));
+    const long per_cu = (nwg + 255) / 256;
+    const long rounds = (per_cu + occ - 1) / occ;
+    const double score = (double)rounds * (double)std::min(per_cu, occ) * nw;
+    if (score < best_score) {
+      best_score = score;
+      best = SSPlan{G, CT, nt};
+    }
+  }
+  return best;
+}
+
+// caller-owned "states" buffer: checkpoints [batch][nck][NP][dim] float32, then y before the
+// gate [batch][seq][dim] (io type, written when the gate z is given)
+inline size_t ckpt_bytes(int batch, int seq, int dim, int nst) {
+  return align256((size_t)batch * num_chunks(seq) * padded_state(nst) * dim * sizeof(float));
+}
+
+struct WsLayout {
+  size_t ckpt, ypre, dtmean, part_bc, part_a, part_d, part_m, total;
+};
 
 inline WsLayout bwd_layout(int batch, int seq, int dim, int nst, bool need_ckpt, bool mean_mode) {
   const int N = padded_state(nst);
   WsLayout w{};
-  const long nck = num_chunks(seq);
-  const int nt = ntiles(dim);
+  const int nt = choose_plan(batch, dim, N, true).ntile;
   size_t off = 0;
   w.ckpt = off;
-  if (need_ckpt) off += align256((size_t)batch * dim * nck * N * 4);
+  if (need_ckpt) off += ckpt_bytes(batch, seq, dim, nst);
+  w.ypre = off;
+  if (need_ckpt) off += align256((size_t)batch * seq * dim * sizeof(float));
   w.dtmean = off;
   if (mean_mode) off += align256((size_t)batch * seq * 4);
   w.part_bc = off;
@@ -704,38 +789,37 @@ inline WsLayout bwd_layout(int batch, int seq, int dim, int nst, bool need_ckpt,
   return w;
 }
 
-template <typename TI, typename TP, int N, int KMAX>
-void launch_fwd_k(hipStream_t s, const SSArgs& a) {
-  constexpr int NT = SSGeo<N, KMAX>::NT;
+template <typename TI, typename TP, int N, int G>
+void launch_fwd_g(hipStream_t s, const SSArgs& a) {
+  constexpr int NT = RGeo<N, G>::NT;
   const int grid = a.batch * a.ntile;
-  const bool mean = a.dtmean != nullptr, hz = a.z != nullptr;
+  const bool mean = a.dtmean != nullptr, hz = a.z != nullptr, wy = a.out != nullptr;
   const TP* Bp = (const TP*)a.B;
   const TP* Cp = (const TP*)a.C;
-  if (a.out == nullptr) {  // checkpoints only (backward without saved states)
-    if (mean) ss_fwd_kernel<TI, TP, N, KMAX, true, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
-    else ss_fwd_kernel<TI, TP, N, KMAX, false, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  } else if (mean && hz) {
-    ss_fwd_kernel<TI, TP, N, KMAX, true, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  } else if (mean) {
-    ss_fwd_kernel<TI, TP, N, KMAX, true, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  } else if (hz) {
-    ss_fwd_kernel<TI, TP, N, KMAX, false, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  } else {
-    ss_fwd_kernel<TI, TP, N, KMAX, false, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+#define EDF_SS_FWD(M, Z, Y) ss_fwd_kernel<TI, TP, N, G, M, Z, Y><<<grid, NT, 0, s>>>(a, Bp, Cp)
+  if (wy) {
+    if (mean && hz) EDF_SS_FWD(true, true, true);
+    else if (mean) EDF_SS_FWD(true, false, true);
+    else if (hz) EDF_SS_FWD(false, true, true);
+    else EDF_SS_FWD(false, false, true);
+  } else {  // checkpoints (and y before the gate) only: the backward without saved states
+    if (mean && hz) EDF_SS_FWD(true, true, false);
+    else if (mean) EDF_SS_FWD(true, false, false);
+    else if (hz) EDF_SS_FWD(false, true, false);
+    else EDF_SS_FWD(false, false, false);
   }
+#undef EDF_SS_FWD
 }
 
-// States per lane.  Backward: two (2 waves per SIMD at config-2 size, 192 workgroups of 8
-// waves), which hides the LDS and exp latencies better than four states per lane at 1 wave
-// per SIMD (measured on MI355X: 722 vs 811 us); at NP = 32 four (8 waves), since 16 waves'
-// dC/dB tiles and state-sum partials do not fit the 160 KB of LDS.  Forward: one (16 waves
-// per workgroup, 4 per SIMD; 190 vs 200 us with two states per lane, interleaved A/B).
-template <int N> constexpr int ss_kmax_bwd() { return N >= 32 ? 4 : 2; }
-constexpr int SS_KMAX_FWD = 1;
-
 template <typename TI, typename TP, int N>
-void launch_fwd_t(hipStream_t s, const SSArgs& a) {
-  launch_fwd_k<TI, TP, N, SS_KMAX_FWD>(s, a);
+void launch_fwd_t(hipStream_t s, SSArgs a) {
+  const SSPlan pl = choose_plan(a.batch, a.dim, N, false);
+  a.ntile = pl.ntile;
+  constexpr int GW = ss_gwide<N>();
+  if constexpr (GW != 1) {
+    if (pl.G == GW) return launch_fwd_g<TI, TP, N, GW>(s, a);
+  }
+  launch_fwd_g<TI, TP, N, 1>(s, a);
 }
 
 template <typename TI, typename TP>
@@ -752,22 +836,27 @@ int launch_fwd_n(hipStream_t s, const SSArgs& a, int nst) {
   return check_launch("selective scan");
 }
 
-template <typename TI, typename TP, int N, int KMAX>
-void launch_bwd_k(hipStream_t s, const SSArgs& a) {
-  constexpr int NT = SSGeo<N, KMAX>::NT;
+template <typename TI, typename TP, int N, int G>
+void launch_bwd_g(hipStream_t s, const SSArgs& a) {
+  constexpr int NT = RGeo<N, G>::NT;
   const int grid = a.batch * a.ntile;
   const bool mean = a.dtmean != nullptr, hz = a.z != nullptr;
   const TP* Bp = (const TP*)a.B;
   const TP* Cp = (const TP*)a.C;
-  if (mean && hz) ss_bwd_kernel<TI, TP, N, KMAX, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  else if (mean) ss_bwd_kernel<TI, TP, N, KMAX, true, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  else if (hz) ss_bwd_kernel<TI, TP, N, KMAX, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
-  else ss_bwd_kernel<TI, TP, N, KMAX, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  if (mean && hz) ss_bwd_kernel<TI, TP, N, G, true, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  else if (mean) ss_bwd_kernel<TI, TP, N, G, true, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  else if (hz) ss_bwd_kernel<TI, TP, N, G, false, true><<<grid, NT, 0, s>>>(a, Bp, Cp);
+  else ss_bwd_kernel<TI, TP, N, G, false, false><<<grid, NT, 0, s>>>(a, Bp, Cp);
 }
 
 template <typename TI, typename TP, int N>
 void launch_bwd_t(hipStream_t s, const SSArgs& a) {
-  launch_bwd_k<TI, TP, N, ss_kmax_bwd<N>()>(s, a);
+  // a.ntile (and the partial buffers sized from it) come from the same plan
+  constexpr int GW = ss_gwide<N>();
+  if constexpr (GW != 1) {
+    if (choose_plan(a.batch, a.dim, N, true).G == GW) return launch_bwd_g<TI, TP, N, GW>(s, a);
+  }
+  launch_bwd_g<TI, TP, N, 1>(s, a);
 }
 
 template <typename TI, typename TP>
@@ -798,6 +887,12 @@ int check_common(int batch, int seq, int dim, int N, int io, int par, int mode) 
   EDF_REQUIRE(N <= SS_MAX_STATE, EDF_ERR_UNSUPPORTED, "state size %d unsupported (1..%d)", N, SS_MAX_STATE);
   EDF_REQUIRE(mode == EDF_SS_DT_PER_CHANNEL || mode == EDF_SS_DT_MEAN, EDF_ERR_INVALID_ARG, "unknown dt mode %d",
               mode);
+  // the kernels address one batch row of x, dt, z, y, dy, dx, ddt, dz (and of B, C and the
+  // checkpoints) through buffer resources with 32-bit byte offsets
+  EDF_REQUIRE((long)seq * dim * 4 < (1L << 31) && num_chunks(seq) * padded_state(N) * dim * 4 < (1L << 31) &&
+                  (long)seq * N * 4 < (1L << 31),
+              EDF_ERR_UNSUPPORTED,
+              "one batch row of seq_len * hidden elements (and its checkpoints) must stay below 2 GiB");
   return EDF_OK;
 }
 
@@ -818,7 +913,7 @@ extern "C" {
 
 size_t edf_selective_scan_states_bytes(int batch, int seq_len, int hidden, int state) {
   if (batch <= 0 || seq_len <= 0 || hidden <= 0 || state <= 0) return 0;
-  return (size_t)batch * edf::num_chunks(seq_len) * edf::padded_state(state) * hidden * sizeof(float);
+  return edf::ckpt_bytes(batch, seq_len, hidden, state) + (size_t)batch * seq_len * hidden * sizeof(float);
 }
 
 size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode) {
@@ -828,7 +923,7 @@ size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, in
 
 size_t edf_selective_scan_backward_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode,
                                                    int have_states) {
-  if (batch <= 0 || seq_len <= 0 || hidden <= 0 || state <= 0) return 0;
+  if (batch <= 0 || seq_len <= 0 || hidden <= 0 || state <= 0 || state > edf::SS_MAX_STATE) return 0;
   return edf::bwd_layout(batch, seq_len, hidden, state, !have_states, mode == EDF_SS_DT_MEAN).total;
 }
 
@@ -840,11 +935,6 @@ int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const 
   int rc = check_common(batch, seq_len, hidden, state, io_dtype, param_dtype, mode);
   if (rc) return rc;
   EDF_REQUIRE(x && dt && A && B && C && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
-  // the kernels address one batch row of x, dt, z, y (and of B, C and the checkpoints)
-  // through buffer resources with 32-bit byte offsets
-  EDF_REQUIRE((long)seq_len * hidden * (io_dtype == EDF_BF16 ? 2 : 4) < (1L << 31) &&
-                  num_chunks(seq_len) * padded_state(state) * hidden * 4 < (1L << 31),
-              EDF_ERR_UNSUPPORTED, "one batch row of seq_len * hidden elements (and its checkpoints) must stay below 2 GiB");
   const size_t need = edf_selective_scan_workspace_bytes(batch, seq_len, hidden, state, mode);
   EDF_REQUIRE(workspace_bytes >= need && (need == 0 || workspace), EDF_ERR_WORKSPACE,
               "workspace too small: need %zu bytes", need);
@@ -852,9 +942,9 @@ int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const 
   SSArgs a{};
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z; a.out = out;
   a.ckpt = (float*)states;
+  a.ypre = states != nullptr ? (char*)states + ckpt_bytes(batch, seq_len, hidden, state) : nullptr;
   a.batch = batch; a.seq = seq_len; a.dim = hidden; a.nst = state;
   a.nck = (int)num_chunks(seq_len);
-  a.ntile = ntiles(hidden);
   if (mode == EDF_SS_DT_MEAN) {
     a.dtmean = (float*)workspace;
     rc = run_dtmean(s, dt, (float*)workspace, batch, seq_len, hidden, io_dtype);
@@ -877,11 +967,6 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   int rc = check_common(batch, seq_len, hidden, state, io_dtype, param_dtype, mode);
   if (rc) return rc;
   EDF_REQUIRE(x && dt && A && B && C && grad_out && grad_x && grad_dt, EDF_ERR_INVALID_ARG, "null tensor pointer");
-  // the backward kernel addresses one batch row of x, dt, dy, z, dx, ddt, dz (and of B, C)
-  // through a buffer resource with 32-bit byte offsets
-  EDF_REQUIRE((long)seq_len * hidden * (io_dtype == EDF_BF16 ? 2 : 4) < (1L << 31) &&
-                  (long)seq_len * (state > 1 ? state : 1) * 4 < (1L << 31),
-              EDF_ERR_UNSUPPORTED, "backward needs seq_len * hidden elements of one batch row below 2 GiB");
   const bool mean_mode = mode == EDF_SS_DT_MEAN;
   const WsLayout L = bwd_layout(batch, seq_len, hidden, state, states == nullptr, mean_mode);
   EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
@@ -892,14 +977,17 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z;
   a.batch = batch; a.seq = seq_len; a.dim = hidden; a.nst = state;
   a.nck = (int)num_chunks(seq_len);
-  a.ntile = ntiles(hidden);
   if (mean_mode) {
     a.dtmean = (float*)(ws + L.dtmean);
     rc = run_dtmean(s, dt, (float*)(ws + L.dtmean), batch, seq_len, hidden, io_dtype);
     if (rc) return rc;
   }
-  a.ckpt = states ? (float*)states : (float*)(ws + L.ckpt);
-  if (states == nullptr) {  // recompute checkpoints with a forward pass that writes no output
+  if (states != nullptr) {
+    a.ckpt = (float*)states;
+    a.ypre = (char*)states + ckpt_bytes(batch, seq_len, hidden, state);
+  } else {  // recompute checkpoints (and y before the gate) with a forward pass that writes no output
+    a.ckpt = (float*)(ws + L.ckpt);
+    a.ypre = ws + L.ypre;
     SSArgs f = a;
     f.out = nullptr;
     rc = by_dtypes(io_dtype, param_dtype, [&](auto* ti, auto* tp) {
@@ -909,6 +997,7 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
     });
     if (rc) return rc;
   }
+  a.ntile = choose_plan(batch, hidden, padded_state(state), true).ntile;
   a.dout = grad_out;
   a.dx = grad_x;
   a.ddt = grad_dt;

@@ -84,12 +84,14 @@ def test_bad_dtype_and_unsupported_shapes(lib):
 
 
 def test_workspace_queries(lib):
-    # one float32 state per (b, chunk of 16 timesteps, n, d)
-    assert lib.edf_selective_scan_states_bytes(8, 2048, 1536, 16) == 8 * 128 * 16 * 1536 * 4
-    assert lib.edf_selective_scan_states_bytes(1, 17, 3, 4) == 2 * 4 * 3 * 4
+    # one float32 state per (b, chunk of 16 timesteps, n, d), padded to 256 bytes, then room
+    # for y before the gate (one float32 per (b, t, d))
+    a256 = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    assert lib.edf_selective_scan_states_bytes(8, 2048, 1536, 16) == 8 * 128 * 16 * 1536 * 4 + 8 * 2048 * 1536 * 4
+    assert lib.edf_selective_scan_states_bytes(1, 17, 3, 4) == a256(2 * 4 * 3 * 4) + 17 * 3 * 4
     # other state sizes are held padded to the next power of two
-    assert lib.edf_selective_scan_states_bytes(1, 17, 3, 12) == 2 * 16 * 3 * 4
-    assert lib.edf_selective_scan_states_bytes(1, 16, 3, 32) == 1 * 32 * 3 * 4
+    assert lib.edf_selective_scan_states_bytes(1, 17, 3, 12) == a256(2 * 16 * 3 * 4) + 17 * 3 * 4
+    assert lib.edf_selective_scan_states_bytes(1, 16, 3, 32) == a256(1 * 32 * 3 * 4) + 16 * 3 * 4
     assert lib.edf_flash_attention_backward_workspace_bytes(4, 32, 4096, 128) == 4 * 32 * 4096 * 4
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 1, 1) > 0  # chunked path
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 0, 1) == 0  # f32: step path
