@@ -394,6 +394,18 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   if (tid < CT) s_Dv[tid] = (Dv != nullptr && tile * CT + tid < dim) ? ld(Dv, tile * CT + tid) : 0.0f;
   const int aq = tid & 1;  // the quantity of this thread's state-sum items (NT is even)
   float dD = 0.0f;
+  // The ddt term sums A[d, n] ga over the states.  For N >= 2 a thread's state-sum items
+  // share one channel (NT is a multiple of 2 CT), so the multiply by A moves out of the
+  // per-element reverse pass into the sum: weights A[d, :] for quantity 1, ones for 0.
+  constexpr bool AW = N >= 2 && N <= 16;
+  float aw[AW ? N : 1];
+  if constexpr (AW) {
+    static_assert(NT % (2 * CT) == 0, "state-sum items of a thread share one channel");
+    const int wc = tile * CT + (tid >> 1) % CT;
+#pragma unroll
+    for (int sn = 0; sn < N; ++sn)
+      aw[sn] = aq == 0 ? 1.0f : ((wc < dim && sn < ns) ? ld(Am, (long)wc * ns + sn) : 0.0f);
+  }
 
   const long rowbase = (long)b * seq * dim;
   typedef typename Bits<TI>::type RI;
@@ -548,7 +560,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
           const float ga = dh * (tt > 0 ? hs[tt > 0 ? tt - 1 : 0] : h0);
           dA = fmaf(ga, fabsf(dcs[tt]), dA);
           s_pq[(tl * CT + cl) * PN + s] = px;
-          s_pq[QP + (tl * CT + cl) * PN + s] = ga * A1;
+          s_pq[QP + (tl * CT + cl) * PN + s] = AW ? ga : ga * A1;
           s_bc[s * SSR + tl * CTP + g * CWP + lane % CW] = gC;
           s_bc[N * SSR + s * SSR + tl * CTP + g * CWP + lane % CW] = gB;
         });
@@ -568,7 +580,19 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
         const int tl = (it >> 1) / CT, tt = u * TS + tl, ac = (it >> 1) % CT;
         const float* src = &s_pq[aq * QP + (tl * CT + ac) * PN];
         float v;
-        if constexpr (PN % 4 == 0) {
+        if constexpr (AW && PN % 4 == 0) {
+          const float4 f0 = *reinterpret_cast<const float4*>(src);
+          v = fmaf(f0.w, aw[3], fmaf(f0.z, aw[2], fmaf(f0.y, aw[1], f0.x * aw[0])));
+#pragma unroll
+          for (int sn = 4; sn < N; sn += 4) {
+            const float4 f = *reinterpret_cast<const float4*>(src + sn);
+            v = fmaf(f.w, aw[sn + 3], fmaf(f.z, aw[sn + 2], fmaf(f.y, aw[sn + 1], fmaf(f.x, aw[sn], v))));
+          }
+        } else if constexpr (AW) {
+          v = src[0] * aw[0];
+#pragma unroll
+          for (int sn = 1; sn < N; ++sn) v = fmaf(src[sn], aw[sn], v);
+        } else if constexpr (PN % 4 == 0) {
           const float4 f0 = *reinterpret_cast<const float4*>(src);
           v = (f0.x + f0.y) + (f0.z + f0.w);
 #pragma unroll

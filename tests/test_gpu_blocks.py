@@ -81,4 +81,5 @@ def test_block_model_bf16_forward(name):
     model = blocks.build(name, **FIXTURE_OPTS[name]).load_reference_weights(w).to("cuda", torch.bfloat16)
     with torch.no_grad():
         out = model(w["input.state_sequence"].cuda().to(torch.bfloat16)).float().cpu().numpy()
-    assert_close(out, w["expected_output"].numpy(), 2e-2, f"{name} bf16 forward")
+    # a whole bf16 model against the float32 fixture: normalised max-abs only (see assert_close)
+    assert_close(out, w["expected_output"].numpy(), 2e-2, f"{name} bf16 forward", elementwise=False)

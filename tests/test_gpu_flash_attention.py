@@ -162,6 +162,10 @@ def test_laser_attention_fwd_bwd(case, rng):
     tol = TOL[dtype]
     assert_close(host(out), scans.laser_attention(qr, kr, vr, causal), tol, "O")
     dq, dk, dv = scans.laser_attention_backward(qr, kr, vr, dor, causal)
-    assert_close(host(tq.grad), dq, tol, "dQ")
-    assert_close(host(tk.grad), dk, tol, "dK")
-    assert_close(host(tv.grad), dv, tol, "dV")
+    # bf16 gradients pass through one more bf16 rounding than the flash ones (E = exp(V - vmax)
+    # is an MFMA operand): element-wise 3e-2, still tighter than the reference's own bf16
+    # LASER gradient check (absolute 0.05, attention_backward_test.exs:227-229)
+    et = 3e-2 if dtype == torch.bfloat16 else None
+    assert_close(host(tq.grad), dq, tol, "dQ", elem_tol=et)
+    assert_close(host(tk.grad), dk, tol, "dK", elem_tol=et)
+    assert_close(host(tv.grad), dv, tol, "dV", elem_tol=et)
