@@ -273,7 +273,8 @@ def _time_pair(torch, steps, warmup, fwd, bwd, runs=None):
 
 
 def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
-    """Config 3: gated delta rule, bf16 I/O, per-head beta, f32 state.
+    """Config 3: gated delta rule, bf16 I/O, per-head beta, f32 state.  The backward is the
+    one the autograd path runs: from the per-chunk context the forward left in its workspace.
     Algorithmic flops (chunked-form convention): fwd 2 (5 C d + 3 d^2) per token-head, bwd 2x fwd."""
     from edifice_amd import _native as nat
 
@@ -293,7 +294,7 @@ def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     db, da = torch.empty_like(beta), torch.empty_like(alpha)
     wsf = nat.query("edf_delta_rule_workspace_bytes", B, T, H, d, 1, 1)
-    wsb = nat.query("edf_delta_rule_backward_workspace_bytes", B, T, H, d, 1, 1)
+    wsb = nat.query("edf_delta_rule_saved_backward_workspace_bytes", B, T, H, d, 1, 1)
     ws1 = torch.empty(max(wsf, 1), dtype=torch.uint8, device=dev)
     ws2 = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
@@ -303,9 +304,9 @@ def bench_delta_rule(torch, steps, warmup, B=4, H=16, T=4096, d=128, C=64):
         nat.call("edf_fused_gated_delta_net_scan", stream, P(q), P(k), P(v), P(beta), P(alpha), P(out), P(ws1), wsf,
                  B, T, H, d, 1, 1)
 
-    def bwd():
-        nat.call("edf_fused_gated_delta_net_scan_backward", stream, P(q), P(k), P(v), P(beta), P(alpha), P(out),
-                 P(do), P(dq), P(dk), P(dv), P(db), P(da), P(ws2), wsb, B, T, H, d, 1, 1)
+    def bwd():  # from the context the forward left in its workspace (as fused_scan's autograd does)
+        nat.call("edf_fused_delta_rule_scan_backward_saved", stream, P(q), P(k), P(v), P(beta), P(alpha), P(do),
+                 P(dq), P(dk), P(dv), P(db), P(da), P(ws1), wsf, P(ws2), wsb, B, T, H, d, 1, 1)
 
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     fflops = 2 * (5 * C * d + 3 * d * d) * B * H * T

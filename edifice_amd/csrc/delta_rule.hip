@@ -17,6 +17,11 @@ size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d);
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
                  void* out, void* workspace, int batch, int seq, int heads, int d);
 size_t dr_chunk_backward_workspace_bytes(int batch, int seq, int heads, int d);
+size_t dr_chunk_saved_backward_workspace_bytes(int batch, int seq, int heads, int d);
+int dr_chunk_saved_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                                const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
+                                void* dalpha, const void* fwd_workspace, void* workspace, int batch, int seq,
+                                int heads, int d);
 int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
                           const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
                           void* dalpha, void* workspace, int batch, int seq, int heads, int d);
@@ -66,10 +71,56 @@ int bwd(void* stream, const void* q, const void* k, const void* v, const void* b
   return dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
                              seq, heads, d, dtype, beta_mode == EDF_BETA_PER_HEAD, 0);
 }
+int bwd_saved(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
+              const void* grad_out, void* dq, void* dk, void* dv, void* dbeta, void* dalpha, const void* fwd_ws,
+              size_t fwd_ws_bytes, void* workspace, size_t ws_bytes, int batch, int seq, int heads, int d, int dtype,
+              int beta_mode) {
+  int rc = check_dr(batch, seq, heads, d, dtype, beta_mode);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && beta && grad_out && dq && dk && dv && dbeta, EDF_ERR_INVALID_ARG,
+              "null tensor pointer");
+  EDF_REQUIRE((alpha == nullptr) == (dalpha == nullptr), EDF_ERR_INVALID_ARG,
+              "alpha and grad_alpha must both be given (gated) or both be null");
+  const int per_head = beta_mode == EDF_BETA_PER_HEAD;
+  if (dr_chunk_eligible(seq, d, dtype, per_head)) {
+    const size_t need_f = dr_chunk_workspace_bytes(batch, seq, heads, d);
+    EDF_REQUIRE(fwd_ws && fwd_ws_bytes >= need_f, EDF_ERR_WORKSPACE,
+                "forward workspace too small: need the %zu bytes the forward filled", need_f);
+    const size_t need = dr_chunk_saved_backward_workspace_bytes(batch, seq, heads, d);
+    EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+    return dr_chunk_saved_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, fwd_ws,
+                                       workspace, batch, seq, heads, d);
+  }
+  // the per-step path keeps no forward context: its backward recomputes
+  const size_t need = dr_seq_backward_workspace_bytes(batch, heads, seq, d);
+  EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  return dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
+                             seq, heads, d, dtype, per_head, 0);
+}
 }  // namespace
 }  // namespace edf
 
 extern "C" {
+
+size_t edf_delta_rule_saved_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                                     int beta_mode) {
+  if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  if (edf::dr_chunk_eligible(seq_len, head_dim, dtype, beta_mode == EDF_BETA_PER_HEAD))
+    return edf::dr_chunk_saved_backward_workspace_bytes(batch, seq_len, num_heads, head_dim);
+  return edf::dr_seq_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+}
+
+int edf_fused_delta_rule_scan_backward_saved(void* stream, const void* q, const void* k, const void* v,
+                                             const void* beta, const void* alpha, const void* grad_out,
+                                             void* grad_q, void* grad_k, void* grad_v, void* grad_beta,
+                                             void* grad_alpha, const void* forward_workspace,
+                                             size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes,
+                                             int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                             int beta_mode) {
+  return edf::bwd_saved(stream, q, k, v, beta, alpha, grad_out, grad_q, grad_k, grad_v, grad_beta, grad_alpha,
+                        forward_workspace, forward_workspace_bytes, workspace, workspace_bytes, batch, seq_len,
+                        num_heads, head_dim, dtype, beta_mode);
+}
 
 size_t edf_delta_rule_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
                                       int beta_mode) {

@@ -54,9 +54,8 @@ struct CkArgs {
   bf16* Ut;   // [ci][DK][CH]   U^T
   bf16* Kdt;  // [ci][DK][CH]   Kd^T
   bf16* Tt;   // [ci][CH][CH]   T^T
-  bf16* hT;   // [ci][DK][DK]   state entering the chunk, [d_v][d_k]
+  bf16* P;    // [ci][CH][CH]   P = Q K^T o Gamma o tril, [t][s] (forward with fused output)
   bf16* hN;   // [ci][DK][DK]   same, [d_k][d_v]
-  bf16* vT;   // [ci][DK][CH]   v_new^T
   bf16* vN;   // [ci][CH][DK]   v_new
   bf16* dvl;  // [ci][DK][CH]   (P^T dO)^T
   bf16* dhl;  // [ci][DK][DK]   (Q^T diag(gamma) dO)^T, [d_v][d_k]
@@ -92,7 +91,9 @@ EDF_DEVICE void stage_t(bf16* dst, const bf16* src, const CkArgs& p, int b, int 
 // prep: decays, T = (I + A)^-1, W (and W^T), U^T, Kd^T (and T^T).
 // LDS is reused across phases (A then K^T, T then V^T) so three workgroups share a CU.
 // ---------------------------------------------------------------------------
-template <bool BWD>
+// BWD: also store T^T and W^T (the backward's context); OUT_P: also store P for the
+// scan's fused output.
+template <bool BWD, bool OUT_P>
 __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   constexpr int AS = CH + 1;
   __shared__ __attribute__((aligned(16))) char u1[DK * TS * sizeof(bf16)];
@@ -131,6 +132,33 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
     kds[l] = __expf(lC - la);
   }
   __syncthreads();
+
+  if constexpr (OUT_P) {
+    // P tiles X[s][t] = K Q^T (rows s = 32 I, columns t = 32 J, s <= t), staged as [t][s]
+    // in the T buffer (free until the inversion ends) and written as whole 128-byte rows
+    const int I = w == 3 ? 1 : 0, J = w >= 2 ? 1 : 0;
+    f32x16 X = zero16();
+    if (w != 1) {
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk)
+        X = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
+                   ld_row8(p.q, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), X);
+      const int t = 32 * J + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int sidx = 32 * I + d_row(r, g);
+        X[r] = sidx <= t ? X[r] * __expf(lg[t] - lg[sidx]) : 0.0f;
+      }
+    }
+    // w == 1 stores the zero tile s >= 32, t < 32
+    store_rows(sTb + (32 * (w == 1 ? 0 : J)) * TS + 32 * (w == 1 ? 1 : I), TS, X, li, g);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + 256 * i, row = e >> 3, ch = e & 7;  // 64 rows of 128 bytes
+      *(bf16x8*)(p.P + ci * CH * CH + row * CH + 8 * ch) = *(const bf16x8*)(sTb + row * TS + 8 * ch);
+    }
+  }
 
   // A from the K K^T tiles (I, J), operands straight from global; the tile above the diagonal is zero
   if (w != 1) {
@@ -296,9 +324,12 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
 // and 1 compute the two 32-step tiles of v (reading A1 and the published state from
 // LDS) and publish v; after a second barrier every wave updates its state rows with v
 // read from LDS.  (Each wave computing all of v itself reads four times the LDS bytes.)
-//   MODE 0 / 1 (forward states):  v = U - W h;          h = gamma_C h + Kd^T v
+//   MODE 1 / 3 (forward states):  v = U - W h;          h = gamma_C h + Kd^T v
 //   MODE 2 (reverse, gradients):   v = dvl + Kd dh;      dh = gamma_C dh + dhl - W^T v
-// MODE 0 stores h as [d_v][d_k] and v^T; MODE 1 stores h as [d_k][d_v] and v;
+// MODE 1 stores h as [d_k][d_v] and v (the backward's context); MODE 3 stores the same
+// and also forms the output of the slice, O = diag(gamma) Q h + P v: waves 2 and 3 (idle
+// while waves 0 and 1 form v) take one 32-step tile each, the Q h part before the v
+// barrier and the P v part after it, and write their O rows themselves;
 // MODE 2 stores dh (the gradient of the state leaving each chunk) as [d_k][d_v] and v^T.
 // Every stored tile is first staged in LDS in its global layout and then written by all
 // threads as contiguous 16-byte rows (the slice of one chunk is one 8 KB / 4 KB block, or
@@ -310,13 +341,18 @@ constexpr int NS = VS + 8;  // LDS row stride (bf16) of [*][VS] tiles
 
 template <int MODE>
 __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
+  static_assert(MODE >= 1 && MODE <= 3, "scan mode");
   constexpr bool REV = MODE == 2;
+  constexpr bool OUT = MODE == 3;
+  constexpr bool FWD_CTX = MODE == 1 || MODE == 3;  // store h as [d_k][d_v] and v as [t][d_v]
   __shared__ __attribute__((aligned(16))) bf16 sA1[2][CH * KS];  // W, or Kd in the reverse pass: [t][d_k]
   __shared__ __attribute__((aligned(16))) bf16 sSt[2][VS * KS];  // state slice, [d_v][d_k]
-  // the state slice as [d_k][d_v] (MODE 1, 2), v as [d_v][t] and (MODE 1) as [t][d_v]
-  __shared__ __attribute__((aligned(16))) bf16 sN[MODE == 0 ? 1 : 2][MODE == 0 ? 8 : DK * NS];
+  // the state slice as [d_k][d_v], v as [d_v][t] and (forward) as [t][d_v]
+  __shared__ __attribute__((aligned(16))) bf16 sN[2][DK * NS];
   __shared__ __attribute__((aligned(16))) bf16 sV[2][VS * TS];
-  __shared__ __attribute__((aligned(16))) bf16 sV2[MODE == 1 ? 2 : 1][MODE == 1 ? CH * NS : 8];
+  __shared__ __attribute__((aligned(16))) bf16 sV2[FWD_CTX ? 2 : 1][FWD_CTX ? CH * NS : 8];
+  // the output rows of waves 2 and 3 ([t][d_v], 32 rows each), written out by the wave
+  __shared__ __attribute__((aligned(16))) bf16 sO[OUT ? 2 : 1][OUT ? 32 * NS : 8];
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 5, li = l & 31;
@@ -331,14 +367,14 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 
   // output regions of this head (buffer resources: a dropped store needs no branch)
   const long hbytes = (long)p.nch * DK * DK * 2, vbytes = (long)p.nch * DK * CH * 2;
-  const rsrc_t rH = make_rsrc((MODE == 0 ? p.hT : MODE == 1 ? p.hN : p.dmN) + bh * p.nch * DK * DK, (unsigned)hbytes);
-  const rsrc_t rV = make_rsrc((MODE == 0 ? p.vT : MODE == 1 ? p.vN : p.dvT) + bh * p.nch * DK * CH, (unsigned)vbytes);
+  const rsrc_t rH = make_rsrc((FWD_CTX ? p.hN : p.dmN) + bh * p.nch * DK * DK, (unsigned)hbytes);
+  const rsrc_t rV = make_rsrc((FWD_CTX ? p.vN : p.dvT) + bh * p.nch * DK * CH, (unsigned)vbytes);
   auto st16 = [&](const rsrc_t& r, unsigned off, const bf16* src) {
     __builtin_amdgcn_raw_buffer_store_b128(*(const u32x4*)src, r, (int)off, 0, 0);
   };
   // the v tile of step it (chunk c)
   auto copy_v = [&](int it, int c) {
-    if constexpr (MODE == 1) {  // v as [t][d_v]: 64 rows of 64 bytes
+    if constexpr (FWD_CTX) {  // v as [t][d_v]: 64 rows of 64 bytes
       const int row = tid >> 2, ch = tid & 3;
       st16(rV, (unsigned)(((c * CH + row) * DK + v0 + 8 * ch) * 2), sV2[it & 1] + row * NS + 8 * ch);
     } else {  // v^T as [d_v][t]: 32 rows of 128 bytes
@@ -356,6 +392,10 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
     bf16x4 x0[4];  // this wave's t tile (w & 1) of U^T or dvl
     bf16x4 y0[4];
     float lgC;
+    // output (waves 2, 3): this lane's row t = 32 (w - 2) + li of Q and of P, log-decay at t
+    bf16x8 qo[OUT ? DK / 16 : 1];
+    bf16x8 po[OUT ? CH / 16 : 1];
+    float lgo;
   };
   Pre pre0, pre1;
   // A1 rows of chunk c (consumed first, into LDS)
@@ -388,6 +428,16 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
       for (int q = 0; q < 4; ++q) P.y0[q] = *(const bf16x4*)(y0 + 8 * q);
     }
     P.lgC = p.lg[ci * CH + CH - 1];
+    if constexpr (OUT) {
+      // every wave loads (waves 0, 1 a valid row they do not use): no wave-dependent branch
+      // around the loads
+      const int t = 32 * (w & 1) + li;
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk) P.qo[kk] = ld_row8(p.q, p, b, h, c * CH + t, 16 * kk + 8 * g);
+#pragma unroll
+      for (int kk = 0; kk < CH / 16; ++kk) P.po[kk] = *(const bf16x8*)(p.P + ci * CH * CH + t * CH + 16 * kk + 8 * g);
+      P.lgo = p.lg[ci * CH + t];
+    }
   };
   auto chunk_of = chunk_of_;
   fetch_a1(pre0, chunk_of(0));
@@ -411,7 +461,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
       for (int e = 0; e < 4; ++e) v[e] = (bf16)S[4 * q + e];
       *(bf16x4*)(ss + li * KS + 32 * w + 8 * q + 4 * g) = v;
     }
-    if constexpr (MODE != 0) {
+    {
       bf16* sn = sN[it & 1];
 #pragma unroll
       for (int r = 0; r < 16; ++r) sn[(32 * w + d_row(r, g)) * NS + li] = (bf16)S[r];
@@ -437,6 +487,15 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 
     // v for the t tile w = 0, 1: X = A1 * state (rows t, column d_v), published as [d_v][t]
     bf16* sv = sV[it & 1];
+    f32x16 XO = zero16();  // output tile of waves 2, 3: O^T rows d_v, column t = 32 (w - 2) + li
+    if (OUT && w >= 2) {
+      // diag(gamma) Q h while waves 0 and 1 form v
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk) XO = mfma32(*(const bf16x8*)(ss + li * KS + 16 * kk + 8 * g), P.qo[kk], XO);
+      const float gt = __expf(P.lgo);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) XO[r] *= gt;
+    }
     if (w < 2) {
       f32x16 X = zero16();
 #pragma unroll
@@ -451,7 +510,7 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
         X[r] = REV ? x0v + X[r] : x0v - X[r];
       }
       store_rows(sv + 32 * w, TS, X, li, g);
-      if constexpr (MODE == 1) {  // and as [t][d_v] for the store of v
+      if constexpr (FWD_CTX) {  // and as [t][d_v] for the store of v
         bf16* dst = sV2[it & 1] + (32 * w) * NS + li;
 #pragma unroll
         for (int r = 0; r < 16; ++r) dst[d_row(r, g) * NS] = (bf16)X[r];
@@ -465,18 +524,35 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
       S[r] = REV ? fmaf(gC, S[r], (float)P.y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
+    if (OUT && w >= 2) {
+      // + P v (P[t][s] = 0 for s > t: the first tile needs s < 32 only), staged as [t][d_v]
+      // rows of this wave and written out as 64-byte row segments
+      const int J = w - 2;
+#pragma unroll
+      for (int kk = 0; kk < CH / 16; ++kk) {
+        if (kk >= 2 * (J + 1)) continue;
+        XO = mfma32(*(const bf16x8*)(sv + li * TS + 16 * kk + 8 * g), P.po[kk], XO);
+      }
+      bf16* so = sO[J];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) so[li * NS + d_row(r, g)] = (bf16)XO[r];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = l + 64 * i, row = e >> 2, ch = e & 3;  // 32 rows x 64 bytes
+        const int t = c * CH + 32 * J + row;
+        if (t < p.T) *(bf16x8*)(p.out + row_off(p, b, h, t) + v0 + 8 * ch) = *(const bf16x8*)(so + row * NS + 8 * ch);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
     // coalesced stores, off the step's dependency chain: the state this step started
     // from and its v
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int e = tid + 256 * i;
-      if constexpr (MODE == 0) {  // [d_v][d_k]: the slice is 32 whole rows of 256 bytes
-        const int row = e >> 4, ch = e & 15;
-        st16(rH, (unsigned)(((c * DK + v0 + row) * DK + 8 * ch) * 2), ss + row * KS + 8 * ch);
-      } else {  // [d_k][d_v]: 128 rows of 64 bytes
-        const int row = e >> 2, ch = e & 3;
-        st16(rH, (unsigned)(((c * DK + row) * DK + v0 + 8 * ch) * 2), sN[it & 1] + row * NS + 8 * ch);
-      }
+      // [d_k][d_v]: 128 rows of 64 bytes
+      const int row = e >> 2, ch = e & 3;
+      st16(rH, (unsigned)(((c * DK + row) * DK + v0 + 8 * ch) * 2), sN[it & 1] + row * NS + 8 * ch);
     }
     copy_v(it, c);
     fetch_rest(P, chunk_of(min(it + 2, p.nch - 1)));
@@ -492,12 +568,20 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// out: O = diag(gamma) Q h + P v_new, computed as O^T so that rows of O store contiguously
+// out: O = diag(gamma) Q h + P v_new per chunk, from the state h ([d_k][d_v]) and v_new
+// ([t][d_v]) the forward scan stores for the backward.  Computed as O^T tiles (rows d_v,
+// column t per lane) so that O rows store contiguously; the h^T and v_new^T A fragments
+// come from transposed reads of the row-major tiles (ds_read_b64_tr_b16), which hand each
+// lane rows 4g..4g+3 and 8+4g..8+4g+3 of a 16-row step, so the B fragments (Q rows, P rows)
+// are read in that same order.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
-  __shared__ __attribute__((aligned(16))) bf16 sP[CH * TS];  // P [t][s]
+  __shared__ __attribute__((aligned(16))) bf16 sH[DK * DK];  // h [d_k][d_v], swizzled rows
+  __shared__ __attribute__((aligned(16))) bf16 sVn[CH * DK];  // v_new [t][d_v], swizzled rows
+  __shared__ __attribute__((aligned(16))) bf16 sQ[CH * KS];   // Q [t][d_k]
+  __shared__ __attribute__((aligned(16))) bf16 sP[CH * TS];   // P [t][s]
   __shared__ float lg[CH];
-  __shared__ __attribute__((aligned(16))) bf16 sO[CH * KS];  // O staged as [t][d] rows
+  bf16* sO = sH;  // O rows [t][d] (KS stride), over h once that is consumed
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
@@ -507,47 +591,72 @@ __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
   const int t0 = c * CH;
   const long ci = bh * p.nch + c;
   if (tid < CH) lg[tid] = p.lg[ci * CH + tid];
-  __syncthreads();
-
-  // S^T tiles (rows s = 32 I, columns t = 32 J): (0,0), (0,1), (1,1); P[t<32][s>=32] = 0
-  if (w < 3) {
-    const int I = w == 2 ? 1 : 0, J = w == 0 ? 0 : 1;
-    f32x16 X = zero16();
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk)
-      X = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
-                 ld_row8(p.q, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), X);
-    const int t = 32 * J + li;
+  for (int i = 0; i < 8; ++i) {  // h: 128 rows x 16 chunks
+    const int e = tid + 256 * i, row = e >> 4, col = (e & 15) * 8;
+    *(bf16x8*)(sH + lds_off<DK>(row, col)) = *(const bf16x8*)(p.hN + ci * DK * DK + row * DK + col);
+  }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int s = 32 * I + d_row(r, g);
-      X[r] = s <= t ? X[r] * __expf(lg[t] - lg[s]) : 0.0f;
-    }
-    store_rows(sP + (32 * J) * TS + 32 * I, TS, X, li, g);
-  } else {
-    store_rows(sP + 32, TS, zero16(), li, g);
+  for (int i = 0; i < 4; ++i) {  // v_new and Q: 64 rows x 16 chunks
+    const int e = tid + 256 * i, row = e >> 4, col = (e & 15) * 8;
+    *(bf16x8*)(sVn + lds_off<DK>(row, col)) = *(const bf16x8*)(p.vN + ci * CH * DK + row * DK + col);
+    *(bf16x8*)(sQ + row * KS + col) = ld_row8(p.q, p, b, h, t0 + row, col);
   }
   __syncthreads();
 
+  // P^T tiles X[s][t] = K Q^T (rows s = 32 I, columns t = 32 J, s <= t) -> sP [t][s]
+  {
+    const int I = w == 3 ? 1 : 0, J = w >= 2 ? 1 : 0;
+    f32x16 X = zero16();
+    if (w != 1) {
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk)
+        X = mfma32(ld_row8(p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
+                   *(const bf16x8*)(sQ + (32 * J + li) * KS + 16 * kk + 8 * g), X);
+      const int t = 32 * J + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int sidx = 32 * I + d_row(r, g);
+        X[r] = sidx <= t ? X[r] * __expf(lg[t] - lg[sidx]) : 0.0f;
+      }
+    }
+    store_rows(sP + (32 * (w == 1 ? 0 : J)) * TS + 32 * (w == 1 ? 1 : I), TS, X, li, g);
+  }
+  __syncthreads();
+
+  // transposed-read addressing: lane i of each 16-lane group reads row base + i / 4,
+  // columns 32 w + d0 .. + 3 and receives column 32 w + li of rows 4 g .. 4 g + 3
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);
+  f32x16 XO[2];
 #pragma unroll
   for (int J = 0; J < 2; ++J) {
     const int t = 32 * J + li;
     f32x16 X = zero16();
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk)
-      X = mfma32(*(const bf16x8*)(p.hT + ci * DK * DK + (long)(32 * w + li) * DK + 16 * kk + 8 * g),
-                 ld_row8(p.q, p, b, h, t0 + t, 16 * kk + 8 * g), X);
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      const int row = 16 * kk + kr, col = 32 * w + d0;
+      const bf16x8 a = cat4(lds_read_tr16(sH + lds_off<DK>(row, col)), lds_read_tr16(sH + lds_off<DK>(row + 8, col)));
+      const bf16* qr = sQ + t * KS + 16 * kk + 4 * g;
+      X = mfma32(a, cat4(*(const bf16x4*)qr, *(const bf16x4*)(qr + 8)), X);
+    }
     const float gm = __expf(lg[t]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) X[r] *= gm;
 #pragma unroll
-    for (int kk = 0; kk < 2 * (J + 1); ++kk)
-      X = mfma32(*(const bf16x8*)(p.vT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g),
-                 *(const bf16x8*)(sP + t * TS + 16 * kk + 8 * g), X);
-    store_rows(sO + (32 * J) * KS + 32 * w, KS, X, li, g);
+    for (int kc = 0; kc < CH / 16; ++kc) {
+      if (kc >= 2 * (J + 1)) continue;  // P[t][s] = 0 for s > t
+      const int row = 16 * kc + kr, col = 32 * w + d0;
+      const bf16x8 a = cat4(lds_read_tr16(sVn + lds_off<DK>(row, col)), lds_read_tr16(sVn + lds_off<DK>(row + 8, col)));
+      const bf16* pr = sP + t * TS + 16 * kc + 4 * g;
+      X = mfma32(a, cat4(*(const bf16x4*)pr, *(const bf16x4*)(pr + 8)), X);
+    }
+    XO[J] = X;
   }
-  // whole 256-byte rows of out (stores straight from the accumulator layout scatter each
-  // instruction over 32 rows)
+  __syncthreads();  // h consumed: O goes over it
+#pragma unroll
+  for (int J = 0; J < 2; ++J) store_rows(sO + (32 * J) * KS + 32 * w, KS, XO[J], li, g);
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -917,57 +1026,63 @@ __global__ void dr_ck_debug_kfrag_kernel(const float* x, bf16* out) {
 }
 
 struct Layout {
-  size_t lg, W, Wt, Ut, Kdt, Tt, hT, hN, vT, vN, dvl, dhl, dmN, dvT, total;
+  size_t lg, W, Wt, Ut, Kdt, Tt, P, hN, vN, dvl, dhl, dmN, dvT, total;
 };
 
 inline size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-Layout layout(int batch, int seq, int heads, bool bwd) {
+// Workspace regions.  The forward's (FWD) hold, on return, the per-chunk context the
+// backward reads (lg, W, W^T, U^T, Kd^T, T^T, h, v_new; P only for the fused output); the
+// backward's own (BWD) hold its reverse-pass tiles.  The recomputing backward takes both in
+// one workspace (ALL).
+enum LayoutKind { FWD, BWD, ALL };
+
+Layout layout(int batch, int seq, int heads, LayoutKind kind) {
   const size_t nci = (size_t)batch * heads * ((seq + CH - 1) / CH);
   const size_t tile_ck = nci * CH * DK * sizeof(bf16), tile_kk = nci * DK * DK * sizeof(bf16);
+  const bool ctx = kind != BWD, rev = kind != FWD;
   Layout L{};
   size_t off = 0;
   auto take = [&](size_t& slot, size_t bytes, bool use) {
     slot = use ? off : 0;
     if (use) off += a256(bytes);
   };
-  take(L.lg, nci * CH * sizeof(float), true);
-  take(L.W, tile_ck, true);
-  take(L.Wt, tile_ck, bwd);
-  take(L.Ut, tile_ck, true);
-  take(L.Kdt, tile_ck, true);
-  take(L.Tt, nci * CH * CH * sizeof(bf16), bwd);
-  take(L.hT, tile_kk, !bwd);
-  take(L.hN, tile_kk, bwd);
-  take(L.vT, tile_ck, !bwd);
-  take(L.vN, tile_ck, bwd);
-  take(L.dvl, tile_ck, bwd);
-  take(L.dhl, tile_kk, bwd);
-  take(L.dmN, tile_kk, bwd);
-  take(L.dvT, tile_ck, bwd);
+  take(L.lg, nci * CH * sizeof(float), ctx);
+  take(L.W, tile_ck, ctx);
+  take(L.Wt, tile_ck, ctx);
+  take(L.Ut, tile_ck, ctx);
+  take(L.Kdt, tile_ck, ctx);
+  take(L.Tt, nci * CH * CH * sizeof(bf16), ctx);
+  take(L.P, nci * CH * CH * sizeof(bf16), false);
+  take(L.hN, tile_kk, ctx);
+  take(L.vN, tile_ck, ctx);
+  take(L.dvl, tile_ck, rev);
+  take(L.dhl, tile_kk, rev);
+  take(L.dmN, tile_kk, rev);
+  take(L.dvT, tile_ck, rev);
   L.total = off;
   return L;
 }
 
-CkArgs make_args(const Layout& L, void* workspace, bool bwd, int seq, int heads) {
+// pointers into the context workspace (forward regions) and the reverse-pass workspace
+CkArgs make_args(const Layout& Lc, void* ctx_ws, const Layout& Lr, void* rev_ws, int seq, int heads) {
   CkArgs a{};
-  char* ws = (char*)workspace;
-  a.lg = (float*)(ws + L.lg);
-  a.W = (bf16*)(ws + L.W);
-  a.Ut = (bf16*)(ws + L.Ut);
-  a.Kdt = (bf16*)(ws + L.Kdt);
-  if (bwd) {
-    a.Wt = (bf16*)(ws + L.Wt);
-    a.Tt = (bf16*)(ws + L.Tt);
-    a.hN = (bf16*)(ws + L.hN);
-    a.vN = (bf16*)(ws + L.vN);
-    a.dvl = (bf16*)(ws + L.dvl);
-    a.dhl = (bf16*)(ws + L.dhl);
-    a.dmN = (bf16*)(ws + L.dmN);
-    a.dvT = (bf16*)(ws + L.dvT);
-  } else {
-    a.hT = (bf16*)(ws + L.hT);
-    a.vT = (bf16*)(ws + L.vT);
+  char* wc = (char*)ctx_ws;
+  char* wr = (char*)rev_ws;
+  a.lg = (float*)(wc + Lc.lg);
+  a.W = (bf16*)(wc + Lc.W);
+  a.Wt = (bf16*)(wc + Lc.Wt);
+  a.Ut = (bf16*)(wc + Lc.Ut);
+  a.Kdt = (bf16*)(wc + Lc.Kdt);
+  a.Tt = (bf16*)(wc + Lc.Tt);
+  a.P = Lc.P ? (bf16*)(wc + Lc.P) : nullptr;
+  a.hN = (bf16*)(wc + Lc.hN);
+  a.vN = (bf16*)(wc + Lc.vN);
+  if (rev_ws != nullptr) {
+    a.dvl = (bf16*)(wr + Lr.dvl);
+    a.dhl = (bf16*)(wr + Lr.dhl);
+    a.dmN = (bf16*)(wr + Lr.dmN);
+    a.dvT = (bf16*)(wr + Lr.dvT);
   }
   a.H = heads;
   a.T = seq;
@@ -984,56 +1099,86 @@ bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head) {
 
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d) {
   (void)d;
-  return layout(batch, seq, heads, false).total;
+  return layout(batch, seq, heads, FWD).total;
 }
 
 size_t dr_chunk_backward_workspace_bytes(int batch, int seq, int heads, int d) {
   (void)d;
-  return layout(batch, seq, heads, true).total;
+  return layout(batch, seq, heads, ALL).total;
 }
 
+size_t dr_chunk_saved_backward_workspace_bytes(int batch, int seq, int heads, int d) {
+  (void)d;
+  return layout(batch, seq, heads, BWD).total;
+}
+
+// forward: prep (T, W, U, Kd and the backward's context), the scan (states, v_new), the
+// output; the workspace keeps the context for dr_chunk_saved_backward_run
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
                  void* out, void* workspace, int batch, int seq, int heads, int d) {
   (void)d;
-  CkArgs a = make_args(layout(batch, seq, heads, false), workspace, false, seq, heads);
+  const Layout L = layout(batch, seq, heads, FWD);
+  CkArgs a = make_args(L, workspace, L, nullptr, seq, heads);
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha; a.out = (bf16*)out;
   const unsigned bh = (unsigned)batch * heads;
   hipStream_t s = as_stream(stream);
-  dr_ck_prep_kernel<false><<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  dr_ck_prep_kernel<true, false><<<dim3(a.nch, bh), 256, 0, s>>>(a);
   int rc = check_launch("delta rule chunk prep");
   if (rc) return rc;
-  dr_ck_scan_kernel<0><<<bh * (DK / VS), 256, 0, s>>>(a);
+  dr_ck_scan_kernel<1><<<bh * (DK / VS), 256, 0, s>>>(a);
   rc = check_launch("delta rule chunk scan");
   if (rc) return rc;
   dr_ck_out_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
   return check_launch("delta rule chunk output");
 }
 
-int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
-                          const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
-                          void* dalpha, void* workspace, int batch, int seq, int heads, int d) {
-  (void)d;
-  CkArgs a = make_args(layout(batch, seq, heads, true), workspace, true, seq, heads);
-  a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
-  a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha; a.dout = (const bf16*)grad_out;
+// the reverse pass from a complete context: dlocal, reverse scan, gradients
+int reverse_pass(hipStream_t s, CkArgs& a, unsigned bh, const void* grad_out, void* dq, void* dk, void* dv,
+                 void* dbeta, void* dalpha) {
+  a.dout = (const bf16*)grad_out;
   a.dq = (bf16*)dq; a.dk = (bf16*)dk; a.dv = (bf16*)dv; a.dbeta = (bf16*)dbeta; a.dalpha = (bf16*)dalpha;
-  const unsigned bh = (unsigned)batch * heads;
-  hipStream_t s = as_stream(stream);
-  dr_ck_prep_kernel<true><<<dim3(a.nch, bh), 256, 0, s>>>(a);
-  int rc = check_launch("delta rule chunk prep");
-  if (rc) return rc;
-  dr_ck_scan_kernel<1><<<bh * (DK / VS), 256, 0, s>>>(a);
-  rc = check_launch("delta rule chunk scan");
-  if (rc) return rc;
   dr_ck_dlocal_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
-  rc = check_launch("delta rule chunk dlocal");
+  int rc = check_launch("delta rule chunk dlocal");
   if (rc) return rc;
   dr_ck_scan_kernel<2><<<bh * (DK / VS), 256, 0, s>>>(a);
   rc = check_launch("delta rule chunk reverse scan");
   if (rc) return rc;
   dr_ck_grad_kernel<<<dim3(a.nch, bh), 512, 0, s>>>(a);
   return check_launch("delta rule chunk grad");
+}
+
+// backward that recomputes the context (prep, forward scan) into its own workspace
+int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                          const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
+                          void* dalpha, void* workspace, int batch, int seq, int heads, int d) {
+  (void)d;
+  const Layout L = layout(batch, seq, heads, ALL);
+  CkArgs a = make_args(L, workspace, L, workspace, seq, heads);
+  a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
+  a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha;
+  const unsigned bh = (unsigned)batch * heads;
+  hipStream_t s = as_stream(stream);
+  dr_ck_prep_kernel<true, false><<<dim3(a.nch, bh), 256, 0, s>>>(a);
+  int rc = check_launch("delta rule chunk prep");
+  if (rc) return rc;
+  dr_ck_scan_kernel<1><<<bh * (DK / VS), 256, 0, s>>>(a);
+  rc = check_launch("delta rule chunk scan");
+  if (rc) return rc;
+  return reverse_pass(s, a, bh, grad_out, dq, dk, dv, dbeta, dalpha);
+}
+
+// backward from the context a forward call left in its workspace (same inputs)
+int dr_chunk_saved_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                                const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
+                                void* dalpha, const void* fwd_workspace, void* workspace, int batch, int seq,
+                                int heads, int d) {
+  (void)d;
+  const Layout Lc = layout(batch, seq, heads, FWD), Lr = layout(batch, seq, heads, BWD);
+  CkArgs a = make_args(Lc, const_cast<void*>(fwd_workspace), Lr, workspace, seq, heads);
+  a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
+  a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha;
+  return reverse_pass(as_stream(stream), a, (unsigned)batch * heads, grad_out, dq, dk, dv, dbeta, dalpha);
 }
 
 }  // namespace edf

@@ -496,26 +496,25 @@ class _DeltaRule(torch.autograd.Function):
             nat.call("edf_fused_gated_delta_net_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(alpha),
                      _p(out), _p(ws), wsb, bsz, seq, nh, hd, dt, mode)
         ctx.mode = mode
-        ctx.save_for_backward(q, k, v, beta, alpha, out)
+        # the chunked path's workspace keeps the per-chunk context the backward reads
+        ctx.fwd_ws, ctx.fwd_wsb = ws, wsb
+        ctx.save_for_backward(q, k, v, beta, alpha)
         return out
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, beta, alpha, out = ctx.saved_tensors
+        q, k, v, beta, alpha = ctx.saved_tensors
         do = do.contiguous().to(q.dtype)
         bsz, seq, nh, hd = q.shape
         dt = dtype_flag(q)
         dq, dk, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
-        wsb = nat.query("edf_delta_rule_backward_workspace_bytes", bsz, seq, nh, hd, dt, ctx.mode)
+        da = torch.empty_like(alpha) if alpha is not None else None
+        wsb = nat.query("edf_delta_rule_saved_backward_workspace_bytes", bsz, seq, nh, hd, dt, ctx.mode)
         ws = _u8(wsb, q)
-        if alpha is None:
-            nat.call("edf_fused_delta_rule_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out),
-                     _p(do), _p(dq), _p(dk), _p(dv), _p(db), _p(ws), wsb, bsz, seq, nh, hd, dt, ctx.mode)
-            return dq, dk, dv, db, None
-        da = torch.empty_like(alpha)
-        nat.call("edf_fused_gated_delta_net_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(alpha),
-                 _p(out), _p(do), _p(dq), _p(dk), _p(dv), _p(db), _p(da), _p(ws), wsb, bsz, seq, nh, hd, dt,
-                 ctx.mode)
+        nat.call("edf_fused_delta_rule_scan_backward_saved", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(alpha),
+                 _p(do), _p(dq), _p(dk), _p(dv), _p(db), _p(da), _p(ctx.fwd_ws), ctx.fwd_wsb, _p(ws), wsb,
+                 bsz, seq, nh, hd, dt, ctx.mode)
+        ctx.fwd_ws = None
         return dq, dk, dv, db, da
 
 

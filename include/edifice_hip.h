@@ -426,6 +426,24 @@ int edf_fused_gated_delta_net_scan_backward(void* stream, const void* q, const v
                                             size_t workspace_bytes, int batch, int seq_len, int num_heads,
                                             int head_dim, int dtype, int beta_mode);
 
+/* No reference counterpart (the reference backward recomputes everything from its inputs):
+ * the backward of DeltaNet (alpha and grad_alpha NULL) or GatedDeltaNet from the per-chunk
+ * context its forward call left in `forward_workspace` (the workspace of the forward with the
+ * same q, k, v, beta, alpha, unchanged since).  On the chunked path (see above) this skips
+ * the forward's recomputation; `workspace` needs
+ * edf_delta_rule_saved_backward_workspace_bytes() bytes.  On the per-step path
+ * forward_workspace is not read and the backward recomputes, as
+ * edf_fused_gated_delta_net_scan_backward does. */
+size_t edf_delta_rule_saved_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                                     int beta_mode);
+int edf_fused_delta_rule_scan_backward_saved(void* stream, const void* q, const void* k, const void* v,
+                                             const void* beta, const void* alpha, const void* grad_out,
+                                             void* grad_q, void* grad_k, void* grad_v, void* grad_beta,
+                                             void* grad_alpha, const void* forward_workspace,
+                                             size_t forward_workspace_bytes, void* workspace, size_t workspace_bytes,
+                                             int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                             int beta_mode);
+
 /* Diagnostic: C[32][32] = A[32][16] * B[16][32] (bf16 in, f32 out, row-major) with one
  * v_mfma_f32_32x32x16_bf16, using the lane layout the attention and delta-rule kernels
  * assume.  No reference counterpart; used by the GPU tests to pin that layout. */

@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from oracle import scans
-from tests.conftest import assert_close
+from tests.conftest import assert_close, rel_err
 from tests.gpu_util import TOL, announce, host, rounded, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -57,6 +57,67 @@ def test_delta_rule_fwd_bwd(case, rng):
     pairs = [("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb)] + ([("dalpha", ta)] if gated else [])
     for name, t in pairs:
         assert_close(host(t.grad), g[name], tol, name)
+
+
+@pytest.mark.parametrize("case", [(1, 200, 2, 128, torch.bfloat16, True), (2, 130, 1, 128, torch.bfloat16, False),
+                                  (1, 40, 2, 32, torch.float32, True)],
+                         ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_delta_rule_backward_entry_points_agree(case, rng):
+    """The reference-shaped backward entry points (which recompute the forward context) and
+    edf_fused_delta_rule_scan_backward_saved (which reads the forward's workspace) give the
+    same gradients: chunked path (gated and not) and the per-step path.  The chunked
+    gradient kernel adds the dbeta and decay terms of a chunk with LDS atomics, whose order
+    varies between calls, so the agreement is to 1e-6 of each gradient's largest entry,
+    not bit for bit."""
+    import ctypes
+
+    from edifice_amd import _native as nat
+    B, T, H, d, dtype, gated = case
+    announce("delta_rule_entry_points", case=case)
+    q, k, v, beta, alpha = make_inputs(rng, B, T, H, d, True, gated)
+    do = rng.normal(size=v.shape)
+    tq, tk, tv, tb, tdo = (to_dev(a, dtype) for a in (q, k, v, beta, do))
+    ta = to_dev(alpha, dtype) if gated else None
+    P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dt = 1 if dtype == torch.bfloat16 else 0
+    wsf = nat.query("edf_delta_rule_workspace_bytes", B, T, H, d, dt, 1)
+    wsr = nat.query("edf_delta_rule_backward_workspace_bytes", B, T, H, d, dt, 1)
+    wss = nat.query("edf_delta_rule_saved_backward_workspace_bytes", B, T, H, d, dt, 1)
+    f_ws = torch.empty(max(wsf, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(tv)
+    if gated:
+        nat.call("edf_fused_gated_delta_net_scan", st, P(tq), P(tk), P(tv), P(tb), P(ta), P(out), P(f_ws), wsf,
+                 B, T, H, d, dt, 1)
+    else:
+        nat.call("edf_fused_delta_net_scan", st, P(tq), P(tk), P(tv), P(tb), P(out), P(f_ws), wsf, B, T, H, d, dt, 1)
+    grads = []
+    for saved in (False, True):
+        g = [torch.empty_like(t) for t in (tq, tk, tv, tb)] + ([torch.empty_like(ta)] if gated else [None])
+        if saved:
+            ws = torch.empty(max(wss, 1), dtype=torch.uint8, device="cuda")
+            nat.call("edf_fused_delta_rule_scan_backward_saved", st, P(tq), P(tk), P(tv), P(tb), P(ta), P(tdo),
+                     *(P(x) for x in g), P(f_ws), wsf, P(ws), wss, B, T, H, d, dt, 1)
+        elif gated:
+            ws = torch.empty(max(wsr, 1), dtype=torch.uint8, device="cuda")
+            nat.call("edf_fused_gated_delta_net_scan_backward", st, P(tq), P(tk), P(tv), P(tb), P(ta), P(out),
+                     P(tdo), *(P(x) for x in g), P(ws), wsr, B, T, H, d, dt, 1)
+        else:
+            ws = torch.empty(max(wsr, 1), dtype=torch.uint8, device="cuda")
+            nat.call("edf_fused_delta_rule_scan_backward", st, P(tq), P(tk), P(tv), P(tb), P(out), P(tdo),
+                     *(P(x) for x in g[:4]), P(ws), wsr, B, T, H, d, dt, 1)
+        torch.cuda.synchronize()
+        grads.append([None if x is None else host(x) for x in g])
+    for a, b_ in zip(*grads):
+        if a is not None:
+            assert rel_err(a, b_) <= 1e-6
+    # and the saved path against the oracle
+    qr, kr, vr, br, dor = (rounded(a, dtype) for a in (q, k, v, beta, do))
+    ar = rounded(alpha, dtype) if gated else None
+    ref = scans.delta_rule_backward(qr, kr, vr, br, dor, ar)
+    for name, x in zip(("dq", "dk", "dv", "dbeta", "dalpha"), grads[1]):
+        if x is not None:
+            assert_close(x, ref[name], TOL[dtype], name)
 
 
 def test_delta_rule_invariants(rng):
