@@ -698,16 +698,23 @@ __global__ __launch_bounds__(256) void ss_reduce_ad_kernel(const float* __restri
   }
 }
 
-// mean mode: ddt[b,t,d] += in_range * (sum over tiles part_m[b,t]) / dim
+// mean mode: ddt[b,t,d] += in_range * (sum over tiles part_m[b,t]) / dim.  One workgroup per
+// row: its threads split the tile partials (in tile order within each thread, then a fixed
+// tree), so the row total is formed once, not by every thread.
 template <typename TI>
 __global__ __launch_bounds__(256) void ss_mean_fixup_kernel(const float* __restrict__ part_m,
                                                             const TI* __restrict__ dt, TI* __restrict__ ddt,
                                                             int ntile, long rows, int dim) {
+  __shared__ float s_w[4];
   const long row = blockIdx.x;
   if (row >= rows) return;
   float tot = 0.0f;
-  for (int tl = 0; tl < ntile; ++tl) tot += part_m[(long)tl * rows + row];
-  tot /= (float)dim;
+  for (int tl = threadIdx.x; tl < ntile; tl += 256) tot += part_m[(long)tl * rows + row];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = tot;
+  __syncthreads();
+  tot = ((s_w[0] + s_w[1]) + (s_w[2] + s_w[3])) / (float)dim;
   for (int d = threadIdx.x; d < dim; d += 256) {
     const long idx = row * dim + d;
     const float dtr = ld(dt, idx);
