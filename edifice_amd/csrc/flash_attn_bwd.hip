@@ -417,6 +417,423 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
   }
 }
 
+// ---- head_dim 128: two workgroups per CU, tiles by direct global->LDS loads ----------
+// The kernels above keep their next tile in registers on its way to LDS and, at 320+
+// registers, run one wave per SIMD: each MFMA waits on the LDS read issued just before
+// it and the matrix core idles through the softmax.  These variants move the tiles with
+// 16-byte DMA loads (global_load_lds_dwordx4, no registers in flight), fit 256 registers
+// and run two workgroups (8 waves) per CU, so one wave's softmax and LDS waits overlap the
+// other's MFMAs.  Each ring buffer is its own __shared__ array and the loop is unrolled
+// over the two, so the compiler's wait for a DMA into one buffer never lands before the
+// reads of the other; every wave waits for its own DMA before the barrier that publishes
+// the tile.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte load per lane straight into LDS: lane l of the wave writes bytes
+// [16 l, 16 l + 16) after the wave-uniform address lds.
+EDF_DEVICE void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
+}
+
+// Column-major LDS tile of R rows x 128 bf16 columns (R a multiple of 32): the 16-byte
+// chunk c (columns 8 c .. 8 c + 7) of row r sits in slot c R + (r ^ 4 (c % 4)).  MFMA row
+// operands (16 rows of one chunk per 16 lanes) and transposed reads (4 rows x 4 chunks per
+// 32 lanes) each touch 64 distinct banks, and since the row XOR depends on c % 4 only,
+// every fragment address is one of two per-lane bases plus an immediate offset (the
+// row-major XOR swizzle needs a live address register per fragment instead).
+//
+// Rows r0 .. r0 + R - 1 of a row-major [T][128] bf16 head (rows past T - 1 repeat row
+// T - 1) into such a tile: the workgroup's R / 16 loads of 64 lanes fill slots in order,
+// load j slots 64 j .. 64 j + 63.
+template <int R>
+EDF_DEVICE void stage_cm(const bf16* src, bf16* dst, int r0, int T, int wu, int l) {
+  constexpr int IPW = R / 16;  // loads per wave
+  static_assert(R % 32 == 0, "whole 32-row groups");
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int j = wu * IPW + i;
+    const int slot = 64 * j + l;
+    const int c = slot / R;
+    const int row = (slot % R) ^ ((c & 3) << 2);
+    const long gr = min(r0 + row, T - 1);
+    dma16(src + gr * 128 + c * 8, dst + 512 * j);
+  }
+}
+
+// Per-lane bases (element offsets) into a column-major tile of R rows.  Row operand
+// (lane li reads row rb + li, chunk 2 kk + g, rb a multiple of 32):
+//   cm_row_base<R>(li, g, kk & 1) + (2 kk R + rb) * 8.
+template <int R>
+EDF_DEVICE int cm_row_base(int li, int g, int parity) {
+  return (((li ^ (4 * (2 * parity + g))) + g * R) << 3);
+}
+// Transposed read of rows rb + 16 kc + kr + 8 h, columns 32 dt + d0 (rb a multiple of 32,
+// kr < 8, d0 a multiple of 4 below 32):  cm_tr_base<R>(kr, d0, h) + (4 dt R + rb + 16 kc) * 8.
+template <int R>
+EDF_DEVICE int cm_tr_base(int kr, int d0, int h) {
+  const int cq = d0 >> 3;
+  return ((((kr + 8 * h) ^ (4 * cq)) + cq * R) << 3) + (d0 & 7);
+}
+
+// vmcnt(0) only: the DMA loads and the plain loads of this wave have landed.
+EDF_DEVICE void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// dK / dV, head_dim 128: 128 keys per workgroup, 32 per wave as in fa_bwd_dkdv_kernel,
+// with K as register B fragments but V read from an LDS copy of the workgroup's 128 x 128
+// tile (its fragments would not fit 256 registers beside the dK^T, dV^T accumulators) and
+// 32-query tiles of Q and dO (two workgroups' rings and V tiles fit the 160 KB LDS).
+template <bool CAUSAL, bool FOX>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
+                                                                const bf16* __restrict__ V,
+                                                                const bf16* __restrict__ dO,
+                                                                const float* __restrict__ LSE,
+                                                                const float* __restrict__ Dd, bf16* __restrict__ dK,
+                                                                bf16* __restrict__ dV, int T, float scale_log2,
+                                                                float scale, const bf16* __restrict__ CS,
+                                                                float* __restrict__ DCSK, float sqd) {
+  constexpr int HD = 128, BKEY = 128, BQ = 32;
+  constexpr int NKK = HD / 16, NDT = HD / 32;
+  __shared__ __attribute__((aligned(16))) bf16 sV[BKEY * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sQ0[BQ * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sQ1[BQ * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sO0[BQ * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sO1[BQ * HD];
+  __shared__ __attribute__((aligned(16))) float sL0[BQ], sL1[BQ], sD0[BQ], sD1[BQ];
+  __shared__ __attribute__((aligned(16))) float sC0[FOX ? BQ : 4], sC1[FOX ? BQ : 4];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  int xb;
+  long bh;
+  head_block(xb, bh);
+  const int kb0 = xb * BKEY;
+  const int kw = kb0 + 32 * w;
+  const int mykey = kw + li;
+  const long base = bh * T * HD;
+
+  // keys past the end read row T - 1 of V: they only feed their own dK, dV columns, never stored
+  stage_cm<BKEY>(V + base, sV, kb0, T, wu, l);
+  bf16x8 kf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk)
+    kf[kk] = mykey < T ? *(const bf16x8*)(K + base + (long)mykey * HD + kk * 16 + 8 * g) : bf16x8{};
+  f32x16 dkt[NDT], dvt[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    dkt[dt] = zero16();
+    dvt[dt] = zero16();
+  }
+  const float csk = FOX && mykey < T ? to_f32(CS[bh * T + mykey]) * sqd : 0.0f;
+  float colacc = 0.0f;
+  float rl = 0.0f, rd = 0.0f;
+  bf16 rc = {};
+
+  // Tile q0 into ring buffer B: Q and dO by DMA, the LSE, D and cs of its queries into
+  // registers of the first wave, which publish() converts (LSE to log2 units, +inf past
+  // the end) and writes to LDS once the tile's work is done; converting them here would
+  // wait for the DMA loads issued before them.
+  auto issue = [&](auto bt, int q0) {
+    constexpr int B = decltype(bt)::value;
+    stage_cm<BQ>(Q + base, B ? sQ1 : sQ0, q0, T, wu, l);
+    stage_cm<BQ>(dO + base, B ? sO1 : sO0, q0, T, wu, l);
+    if (tid < BQ) {
+      const long q = min(q0 + tid, T - 1);
+      rl = LSE[bh * T + q];
+      rd = Dd[bh * T + q];
+      if constexpr (FOX) rc = CS[bh * T + q];
+    }
+  };
+  auto publish = [&](auto bt, int q0) {
+    constexpr int B = decltype(bt)::value;
+    wait_vm();
+    if (tid < BQ) {
+      (B ? sL1 : sL0)[tid] = q0 + tid < T ? rl * LOG2E : INFINITY;
+      (B ? sD1 : sD0)[tid] = rd;
+      if constexpr (FOX) (B ? sC1 : sC0)[tid] = to_f32(rc);
+    }
+  };
+
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);
+  const int qrow[2] = {cm_row_base<BQ>(li, g, 0), cm_row_base<BQ>(li, g, 1)};
+  const int vrow[2] = {cm_row_base<BKEY>(li, g, 0) + 32 * w * 8, cm_row_base<BKEY>(li, g, 1) + 32 * w * 8};
+  const int qtr[2] = {cm_tr_base<BQ>(kr, d0, 0), cm_tr_base<BQ>(kr, d0, 1)};
+
+  auto subtile = [&](auto bt, int q0, int sub, auto masked) {
+    constexpr int B = decltype(bt)::value;
+    constexpr bool MASK = decltype(masked)::value;
+    const bf16* sQ = B ? sQ1 : sQ0;
+    const bf16* sO = B ? sO1 : sO0;
+    const float* sL = B ? sL1 : sL0;
+    const float* sD = B ? sD1 : sD0;
+    const float* sC = B ? sC1 : sC0;
+    const int qs = q0 + 32 * sub;
+    // The two bodies begin with the same LDS reads; distinct scheduling barriers keep the
+    // compiler from hoisting all 24 fragments above the branch (96 live registers, spills).
+    __builtin_amdgcn_sched_barrier(MASK ? 1 : 2);
+    f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const int off = qrow[kk & 1] + (2 * kk * BQ + 32 * sub) * 8;
+      const bf16x8 vf = *(const bf16x8*)(&sV[vrow[kk & 1] + 2 * kk * BKEY * 8]);
+      s = mfma32(*(const bf16x8*)(&sQ[off]), kf[kk], s);
+      dp = mfma32(*(const bf16x8*)(&sO[off]), vf, dp);
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const f32x4 lv = *(const f32x4*)(&sL[32 * sub + 8 * rb + 4 * g]);
+      const f32x4 dv4 = *(const f32x4*)(&sD[32 * sub + 8 * rb + 4 * g]);
+      f32x4 cq4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (FOX) cq4 = *(const f32x4*)(&sC[32 * sub + 8 * rb + 4 * g]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = rb * 4 + e;
+        if constexpr (FOX) s[r] += fmaf(cq4[e], sqd, -csk);
+        float p = fast_exp2(fmaf(s[r], scale_log2, -lv[e]));
+        if constexpr (MASK) {
+          const int q = qs + 8 * rb + 4 * g + e;
+          p = (q >= T || mykey >= T || (CAUSAL && mykey > q)) ? 0.0f : p;
+        }
+        s[r] = p;
+        dp[r] = p * (dp[r] - dv4[e]);
+        if constexpr (FOX) colacc += dp[r];
+      }
+    }
+    bf16x8 pb[2], db[2];
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pb[kc][e] = (bf16)s[8 * kc + e];
+        db[kc][e] = (bf16)dp[8 * kc + e];
+      }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) {
+        const int o0 = qtr[0] + (4 * dt * BQ + 32 * sub + 16 * kc) * 8;
+        const int o1 = qtr[1] + (4 * dt * BQ + 32 * sub + 16 * kc) * 8;
+        dvt[dt] = mfma32(cat4(lds_read_tr16(&sO[o0]), lds_read_tr16(&sO[o1])), pb[kc], dvt[dt]);
+        dkt[dt] = mfma32(cat4(lds_read_tr16(&sQ[o0]), lds_read_tr16(&sQ[o1])), db[kc], dkt[dt]);
+      }
+  };
+  auto tile = [&](auto bt, int q0) {
+#pragma unroll
+    for (int sub = 0; sub < BQ / 32; ++sub) {
+      const int qs = q0 + 32 * sub;
+      if (CAUSAL && qs + 31 < kw) continue;  // every query of the sub-tile precedes this wave's keys
+      // masked body on the causal diagonal and in a tile that runs past the end
+      if ((CAUSAL && qs < kw + 31) || q0 + BQ > T) subtile(bt, q0, sub, std::true_type{});
+      else subtile(bt, q0, sub, std::false_type{});
+    }
+  };
+
+  const int qstart = CAUSAL ? kb0 : 0;
+  const int ntile = qstart < T ? (T - qstart + BQ - 1) / BQ : 0;
+  const std::integral_constant<int, 0> b0{};
+  const std::integral_constant<int, 1> b1{};
+  if (ntile > 0) {
+    issue(b0, qstart);
+    publish(b0, qstart);
+  }
+  __syncthreads();
+  for (int it = 0; it < ntile; it += 2) {
+    const int q0 = qstart + it * BQ;
+    if (it + 1 < ntile) issue(b1, q0 + BQ);
+    tile(b0, q0);
+    if (it + 1 < ntile) publish(b1, q0 + BQ);
+    __syncthreads();
+    if (it + 1 >= ntile) break;
+    if (it + 2 < ntile) issue(b0, q0 + 2 * BQ);
+    tile(b1, q0 + BQ);
+    if (it + 2 < ntile) publish(b0, q0 + 2 * BQ);
+    __syncthreads();
+  }
+  if constexpr (FOX) {
+    colacc += __shfl_xor(colacc, 32);
+    if (g == 0 && mykey < T) DCSK[bh * T + mykey] = -colacc;
+  }
+  if (mykey < T) {
+    bf16* krow = dK + base + (long)mykey * HD;
+    bf16* vrow = dV + base + (long)mykey * HD;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        bf16x4 a, b;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a[e] = (bf16)(dkt[dt][rb * 4 + e] * scale);
+          b[e] = (bf16)dvt[dt][rb * 4 + e];
+        }
+        *(bf16x4*)(krow + dt * 32 + 8 * rb + 4 * g) = a;
+        *(bf16x4*)(vrow + dt * 32 + 8 * rb + 4 * g) = b;
+      }
+  }
+}
+
+// dQ, head_dim 128 (same decomposition as fa_bwd_dq_kernel: 128 queries per workgroup,
+// 32 per wave with Q and dO as register B fragments, 64-key tiles, each processed as two
+// 32-key halves so only one half's S^T / dP^T is live).
+template <bool CAUSAL, bool FOX>
+__global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
+                                                              const bf16* __restrict__ V, const bf16* __restrict__ dO,
+                                                              const float* __restrict__ LSE,
+                                                              const float* __restrict__ Dd, bf16* __restrict__ dQ,
+                                                              int T, float scale_log2, float scale,
+                                                              const bf16* __restrict__ CS,
+                                                              const float* __restrict__ DCSK, bf16* __restrict__ DCS,
+                                                              float sqd) {
+  constexpr int HD = 128, BM = 128, BN = 64;
+  constexpr int NKK = HD / 16, NDT = HD / 32;
+  __shared__ __attribute__((aligned(16))) bf16 sK0[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sK1[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sV0[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sV1[BN * HD];
+  __shared__ __attribute__((aligned(16))) float sCS0[FOX ? BN : 4], sCS1[FOX ? BN : 4];
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  int xb;
+  long bh;
+  head_block(xb, bh);
+  const int qb = CAUSAL ? (gridDim.x - 1 - xb) : xb;  // heaviest blocks first
+  const int q0 = qb * BM;
+  const int qw = q0 + 32 * w;
+  const int myq = qw + li;
+  const long base = bh * T * HD;
+
+  bf16x8 qf[NKK], of[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    qf[kk] = myq < T ? *(const bf16x8*)(Q + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
+    of[kk] = myq < T ? *(const bf16x8*)(dO + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
+  }
+  const float myl = myq < T ? LSE[bh * T + myq] * LOG2E : 0.0f;
+  const float myd = myq < T ? Dd[bh * T + myq] : 0.0f;
+  const float csq = FOX && myq < T ? to_f32(CS[bh * T + myq]) * sqd : 0.0f;
+  float rowacc = 0.0f;
+  bf16 rcs = {};
+  f32x16 dqt[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dqt[dt] = zero16();
+
+  auto issue = [&](auto bt, int k0) {
+    constexpr int B = decltype(bt)::value;
+    stage_cm<BN>(K + base, B ? sK1 : sK0, k0, T, wu, l);
+    stage_cm<BN>(V + base, B ? sV1 : sV0, k0, T, wu, l);
+    if constexpr (FOX) {
+      if (tid < BN) rcs = CS[bh * T + min(k0 + tid, T - 1)];  // converted by publish()
+    }
+  };
+  auto publish = [&](auto bt) {
+    constexpr int B = decltype(bt)::value;
+    wait_vm();
+    if constexpr (FOX) {
+      if (tid < BN) (B ? sCS1 : sCS0)[tid] = to_f32(rcs);
+    }
+  };
+
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);
+  const int krow[2] = {cm_row_base<BN>(li, g, 0), cm_row_base<BN>(li, g, 1)};
+  const int ktr[2] = {cm_tr_base<BN>(kr, d0, 0), cm_tr_base<BN>(kr, d0, 1)};
+  auto tile = [&](auto bt, int kt, auto masked) {
+    constexpr int B = decltype(bt)::value;
+    constexpr bool MASK = decltype(masked)::value;
+    const bf16* sK = B ? sK1 : sK0;
+    const bf16* sV = B ? sV1 : sV0;
+    const float* sCS = B ? sCS1 : sCS0;
+    const int k0 = kt * BN;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      if (MASK && CAUSAL && k0 + 32 * h2 > qw + 31) continue;  // the half is above the wave's diagonal
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) {
+        const int off = krow[kk & 1] + (2 * kk * BN + 32 * h2) * 8;
+        s = mfma32(*(const bf16x8*)(&sK[off]), qf[kk], s);
+        dp = mfma32(*(const bf16x8*)(&sV[off]), of[kk], dp);
+      }
+      if constexpr (FOX) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          const f32x4 ck = *(const f32x4*)(&sCS[h2 * 32 + 8 * rb + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[4 * rb + e] += fmaf(-ck[e], sqd, csq);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(s[r], scale_log2, -myl));
+        if constexpr (MASK) {
+          const int key = k0 + h2 * 32 + d_row(r, g);
+          p = (key >= T || myq >= T || (CAUSAL && key > myq)) ? 0.0f : p;
+        }
+        s[r] = p * (dp[r] - myd);
+        if constexpr (FOX) rowacc += s[r];
+      }
+      bf16x8 db[2];
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) db[kc][e] = (bf16)s[8 * kc + e];
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          const int o = (4 * dt * BN + 32 * h2 + 16 * kc) * 8;
+          const bf16x8 a = cat4(lds_read_tr16(&sK[ktr[0] + o]), lds_read_tr16(&sK[ktr[1] + o]));
+          dqt[dt] = mfma32(a, db[kc], dqt[dt]);
+        }
+    }
+  };
+
+  const int kend = CAUSAL ? min(T, q0 + BM) : T;
+  const int nkt = (kend + BN - 1) / BN;
+  // unmasked tiles: inside the sequence for the wave's keys and queries and, causal, wholly
+  // at or below its queries' diagonal (wave-uniform)
+  const int ksplit = qw + 31 >= T ? 0 : min(min(T / BN, nkt), CAUSAL ? (qw + 1) / BN : nkt);
+  auto step = [&](auto bt, int kt) {
+    constexpr int B = decltype(bt)::value;
+    const std::integral_constant<int, 1 - B> other{};
+    if (kt + 1 < nkt) issue(other, (kt + 1) * BN);
+    if (kt < ksplit) tile(bt, kt, std::false_type{});
+    else if (!(CAUSAL && kt * BN > qw + 31)) tile(bt, kt, std::true_type{});
+    if (kt + 1 < nkt) publish(other);
+    __syncthreads();
+  };
+  const std::integral_constant<int, 0> b0{};
+  const std::integral_constant<int, 1> b1{};
+  issue(b0, 0);
+  publish(b0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; kt += 2) {
+    step(b0, kt);
+    if (kt + 1 < nkt) step(b1, kt + 1);
+  }
+  if constexpr (FOX) {
+    rowacc += __shfl_xor(rowacc, 32);
+    if (g == 0 && myq < T) DCS[bh * T + myq] = (bf16)(rowacc + DCSK[bh * T + myq]);
+  }
+  if (myq < T) {
+    bf16* qrow = dQ + base + (long)myq * HD;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(dqt[dt][rb * 4 + e] * scale);
+        *(bf16x4*)(qrow + dt * 32 + 8 * rb + 4 * g) = v;
+      }
+  }
+}
+
 // ---- generic wave-per-row kernels (float32 / any head_dim) ------------------------
 template <typename TT, int DPL>
 __global__ __launch_bounds__(256) void fa_bwd_dq_wave_kernel(const TT* __restrict__ Q, const TT* __restrict__ K,
@@ -543,6 +960,29 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_wave_kernel(const TT* __restr
   if (CS != nullptr && lane == 0) DCSK[row] = -colacc;
 }
 
+// head_dim 128: the two-workgroups-per-CU kernels; FoX (cs != nullptr) is causal.
+void launch_mfma_bwd128(hipStream_t s, const bf16* Q, const bf16* K, const bf16* V, const bf16* G, const float* lse,
+                        const float* Dd, bf16* dq, bf16* dk, bf16* dv, int BH, int T, int causal, float scale_log2,
+                        float scale, const bf16* CS, float* dcsk, bf16* dcs, float sqd) {
+  const dim3 g1((T + 127) / 128, BH);
+  if (CS != nullptr) {  // dK/dV first: dQ adds its key-side d cs
+    fa_bwd_dkdv128_kernel<true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, CS, dcsk,
+                                                         sqd);
+    fa_bwd_dq128_kernel<true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dq, T, scale_log2, scale, CS, dcsk, dcs,
+                                                       sqd);
+  } else if (causal) {
+    fa_bwd_dkdv128_kernel<true, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, nullptr,
+                                                          nullptr, 0.0f);
+    fa_bwd_dq128_kernel<true, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dq, T, scale_log2, scale, nullptr,
+                                                        nullptr, nullptr, 0.0f);
+  } else {
+    fa_bwd_dkdv128_kernel<false, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale,
+                                                           nullptr, nullptr, 0.0f);
+    fa_bwd_dq128_kernel<false, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dq, T, scale_log2, scale, nullptr,
+                                                         nullptr, nullptr, 0.0f);
+  }
+}
+
 template <int HD>
 void launch_mfma_bwd(hipStream_t s, const void* q, const void* k, const void* v, const void* go, const float* lse,
                      const float* Dd, void* dq, void* dk, void* dv, int BH, int T, int causal, float scale_log2,
@@ -551,6 +991,11 @@ void launch_mfma_bwd(hipStream_t s, const void* q, const void* k, const void* v,
   const dim3 g1((T + 127) / 128, BH);
   const bf16 *Q = (const bf16*)q, *K = (const bf16*)k, *V = (const bf16*)v, *G = (const bf16*)go;
   const bf16* CS = (const bf16*)cs;
+  if constexpr (HD == 128) {
+    launch_mfma_bwd128(s, Q, K, V, G, lse, Dd, (bf16*)dq, (bf16*)dk, (bf16*)dv, BH, T, causal, scale_log2, scale, CS,
+                       dcsk, (bf16*)dcs, sqd);
+    return;
+  }
   if (cs != nullptr) {  // FoX attention is causal; dK/dV first: dQ adds its key-side d cs
     fa_bwd_dkdv_kernel<HD, true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, (bf16*)dk, (bf16*)dv, T, scale_log2,
                                                           scale, CS, dcsk, sqd);
