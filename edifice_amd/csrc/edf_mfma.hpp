@@ -109,4 +109,56 @@ constexpr int lds_tile_elems(int rows) {
   return HD == 128 ? rows * 128 : rows * (HD + 8);
 }
 
+// ---- direct global->LDS tiles (head_dim 128 attention kernels) ------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One 16-byte load per lane straight into LDS: lane l of the wave writes bytes
+// [16 l, 16 l + 16) after the wave-uniform address lds.
+EDF_DEVICE void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
+}
+
+// Column-major LDS tile of R rows x 128 bf16 columns (R a multiple of 32): the 16-byte
+// chunk c (columns 8 c .. 8 c + 7) of row r sits in slot c R + (r ^ 4 (c % 4)).  MFMA row
+// operands (16 rows of one chunk per 16 lanes) and transposed reads (4 rows x 4 chunks per
+// 32 lanes) each touch 64 distinct banks, and since the row XOR depends on c % 4 only,
+// every fragment address is one of two per-lane bases plus an immediate offset (the
+// row-major XOR swizzle needs a live address register per fragment instead).
+//
+// Rows r0 .. r0 + R - 1 of a row-major [T][128] bf16 head (rows past T - 1 repeat row
+// T - 1) into such a tile: the workgroup's R / 16 loads of 64 lanes fill slots in order,
+// load j slots 64 j .. 64 j + 63.
+template <int R>
+EDF_DEVICE void stage_cm(const bf16* src, bf16* dst, int r0, int T, int wu, int l) {
+  constexpr int IPW = R / 16;  // loads per wave
+  static_assert(R % 32 == 0, "whole 32-row groups");
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int j = wu * IPW + i;
+    const int slot = 64 * j + l;
+    const int c = slot / R;
+    const int row = (slot % R) ^ ((c & 3) << 2);
+    const long gr = min(r0 + row, T - 1);
+    dma16(src + gr * 128 + c * 8, dst + 512 * j);
+  }
+}
+
+// Per-lane bases (element offsets) into a column-major tile of R rows.  Row operand
+// (lane li reads row rb + li, chunk 2 kk + g, rb a multiple of 32):
+//   cm_row_base<R>(li, g, kk & 1) + (2 kk R + rb) * 8.
+template <int R>
+EDF_DEVICE int cm_row_base(int li, int g, int parity) {
+  return (((li ^ (4 * (2 * parity + g))) + g * R) << 3);
+}
+// Transposed read of rows rb + 16 kc + kr + 8 h, columns 32 dt + d0 (rb a multiple of 32,
+// kr < 8, d0 a multiple of 4 below 32):  cm_tr_base<R>(kr, d0, h) + (4 dt R + rb + 16 kc) * 8.
+template <int R>
+EDF_DEVICE int cm_tr_base(int kr, int d0, int h) {
+  const int cq = d0 >> 3;
+  return ((((kr + 8 * h) ^ (4 * cq)) + cq * R) << 3) + (d0 & 7);
+}
+
+// vmcnt(0) only: the DMA loads and the plain loads of this wave have landed.
+EDF_DEVICE void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace edf

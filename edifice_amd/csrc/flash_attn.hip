@@ -244,6 +244,216 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
   if (myq < T && g == 0 && LSE != nullptr) LSE[bh * T + myq] = (m * scale_log2 + __log2f(lsum)) * LN2;
 }
 
+// head_dim 128: the same decomposition (128 queries per workgroup, 32 per wave with Q^T as
+// register B fragments, 64-key tiles), with K and V moved by 16-byte DMA loads into
+// column-major LDS tiles (fragment addresses are bases plus immediates, no staging
+// registers), and K one tile ahead of V: iteration t issues the MFMAs of S(t + 1) before
+// the softmax of S(t), so the matrix core works on the next scores while the VALU turns
+// the current ones into P (the two rings stay two-deep: K(t) was consumed in iteration
+// t - 1).  Two workgroups per CU.
+template <bool CAUSAL, bool FOX = false>
+__global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
+                                                           const bf16* __restrict__ V, bf16* __restrict__ O,
+                                                           float* __restrict__ LSE, int T, float scale_log2,
+                                                           const bf16* __restrict__ CS, float sqd) {
+  constexpr int HD = 128, BM = 128, BN = 64;
+  constexpr int NKK = HD / 16, NDT = HD / 32;
+  __shared__ __attribute__((aligned(16))) bf16 sK0[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sK1[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sV0[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sV1[BN * HD];
+  __shared__ __attribute__((aligned(16))) float sC0[FOX ? BN : 4], sC1[FOX ? BN : 4];  // cs of a K tile's keys
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  int xb;
+  long bh;
+  head_block(xb, bh);
+  const int qb = CAUSAL ? (gridDim.x - 1 - xb) : xb;  // heaviest blocks first
+  const int q0 = qb * BM;
+  const int qw = q0 + 32 * w;
+  const int myq = qw + li;
+  const long base = bh * T * HD;
+
+  bf16x8 qf[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk)
+    qf[kk] = myq < T ? *(const bf16x8*)(Q + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
+  f32x16 o[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) o[dt] = zero16();
+  float m = -INFINITY, lsum = 0.0f;
+  const float csq = FOX && myq < T ? to_f32(CS[bh * T + myq]) * sqd : 0.0f;
+  bf16 rcs = {};
+
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);
+  const int krow[2] = {cm_row_base<BN>(li, g, 0), cm_row_base<BN>(li, g, 1)};
+  const int vtr[2] = {cm_tr_base<BN>(kr, d0, 0), cm_tr_base<BN>(kr, d0, 1)};
+
+  const int kend = CAUSAL ? min(T, q0 + BM) : T;
+  const int nkt = (kend + BN - 1) / BN;
+  // unmasked tiles of this wave: inside the sequence and, causal, at or below its diagonal
+  const int ksplit = min(min(T / BN, nkt), CAUSAL ? (qw + 1) / BN : nkt);
+  auto visible = [&](int t) { return !(CAUSAL && t * BN > qw + 31); };
+
+  auto issue_k = [&](auto bt, int t) {  // K tile t (and its cs) into K buffer B
+    constexpr int B = decltype(bt)::value;
+    stage_cm<BN>(K + base, B ? sK1 : sK0, t * BN, T, wu, l);
+    if constexpr (FOX) {
+      if (tid < BN) rcs = CS[bh * T + min(t * BN + tid, T - 1)];  // converted by publish_k()
+    }
+  };
+  auto issue_v = [&](auto bt, int t) {
+    constexpr int B = decltype(bt)::value;
+    stage_cm<BN>(V + base, B ? sV1 : sV0, t * BN, T, wu, l);
+  };
+  auto publish_k = [&](auto bt) {
+    constexpr int B = decltype(bt)::value;
+    if constexpr (FOX) {
+      if (tid < BN) (B ? sC1 : sC0)[tid] = to_f32(rcs);
+    }
+  };
+  // S^T of the K tile in buffer B: lane owns query column li, rows are the tile's keys
+  auto scores = [&](auto bt, f32x16* s) {
+    constexpr int B = decltype(bt)::value;
+    const bf16* sk = B ? sK1 : sK0;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      s[h2] = zero16();
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk)
+        s[h2] = mfma32(*(const bf16x8*)(&sk[krow[kk & 1] + (2 * kk * BN + 32 * h2) * 8]), qf[kk], s[h2]);
+    }
+    if constexpr (FOX) {  // + (cs_q - cs_key) sqrt(d); key h2 * 32 + 8 rb + 4 g + e
+      const float* sc = B ? sC1 : sC0;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          const f32x4 ck = *(const f32x4*)(&sc[h2 * 32 + 8 * rb + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[h2][4 * rb + e] += fmaf(-ck[e], sqd, csq);
+        }
+    }
+  };
+  // online softmax of tile t's scores and O^T += V^T P^T with V from buffer B
+  auto consume = [&](auto bt, f32x16* s, int t, auto masked) {
+    constexpr int B = decltype(bt)::value;
+    constexpr bool MASK = decltype(masked)::value;
+    const bf16* sv = B ? sV1 : sV0;
+    const int k0 = t * BN;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (MASK) {
+          const int key = k0 + h2 * 32 + d_row(r, g);
+          s[h2][r] = (key >= T || (CAUSAL && key > myq)) ? -INFINITY : s[h2][r];
+        }
+        mx = fmaxf(mx, s[h2][r]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(m, mx);
+    const float mns = mnew == -INFINITY ? 0.0f : mnew * scale_log2;
+    if (__any(mnew > m)) {  // rescale only when some row maximum grew
+      const float alpha = fast_exp2(m * scale_log2 - mns);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
+    m = mnew;
+    float rs = 0.0f;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = fast_exp2(fmaf(s[h2][r], scale_log2, -mns));
+        s[h2][r] = pv;
+        rs += pv;
+      }
+    lsum += rs + __shfl_xor(rs, 32);
+    bf16x8 pf[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int it = 0; it < 8; ++it) pf[kc][it] = (bf16)s[kc >> 1][8 * (kc & 1) + it];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const int o16 = (4 * dt * BN + 16 * kc) * 8;
+        o[dt] = mfma32(cat4(lds_read_tr16(&sv[vtr[0] + o16]), lds_read_tr16(&sv[vtr[1] + o16])), pf[kc], o[dt]);
+      }
+  };
+
+  const std::integral_constant<int, 0> b0{};
+  const std::integral_constant<int, 1> b1{};
+  f32x16 sc[2], sn[2];
+  // prologue: K(0), V(0), K(1) in; S(0); a barrier before iteration 0 reloads K buffer 0
+  issue_k(b0, 0);
+  issue_v(b0, 0);
+  wait_vm();
+  publish_k(b0);
+  if (nkt > 1) issue_k(b1, 1);
+  __syncthreads();  // K(0), its cs and V(0) visible
+  if (visible(0)) scores(b0, sc);
+  wait_vm();
+  if (nkt > 1) publish_k(b1);
+  __syncthreads();  // K(1) visible, K buffer 0 free
+  // iteration t (buffer parity B = t % 2): K(t + 2) into K buffer B, V(t + 1) into V buffer
+  // 1 - B; S(t + 1) from K buffer 1 - B; softmax of S(t) and O with V buffer B
+  auto step = [&](auto bt, int t) {
+    constexpr int B = decltype(bt)::value;
+    const std::integral_constant<int, 1 - B> ot{};
+    if (t + 2 < nkt) issue_k(bt, t + 2);
+    if (t + 1 < nkt) issue_v(ot, t + 1);
+    const bool nvis = t + 1 < nkt && visible(t + 1);
+    if (visible(t)) {
+      if (nvis) scores(ot, sn);
+      if (t < ksplit) consume(bt, sc, t, std::false_type{});
+      else consume(bt, sc, t, std::true_type{});
+    }
+    wait_vm();
+    if (t + 2 < nkt) publish_k(bt);
+    __syncthreads();
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) sc[h2] = sn[h2];
+  };
+  for (int t = 0; t < nkt; t += 2) {
+    step(b0, t);
+    if (t + 1 < nkt) step(b1, t + 1);
+  }
+
+  // O through the free K buffers (each wave its 32 rows, row-major swizzled), written as
+  // whole rows: a lane holds one query row, so storing from registers would touch 32 rows
+  // per instruction in 16-byte pieces.
+  bf16* so = (w < 2 ? sK0 : sK1) + (w & 1) * 32 * HD;
+  const float inv = myq < T ? 1.0f / lsum : 0.0f;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (bf16)(o[dt][rb * 4 + e] * inv);
+      *(bf16x4*)(so + lds_off<HD>(li, dt * 32 + 8 * rb + 4 * g)) = v;
+    }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < 32 * 16 / 64; ++i) {
+    const int e = l + 64 * i, row = e / 16, ch = e % 16;
+    if (qw + row < T)
+      *(bf16x8*)(O + base + (long)(qw + row) * HD + 8 * ch) = *(const bf16x8*)(so + lds_off<HD>(row, 8 * ch));
+  }
+  if (myq < T && g == 0 && LSE != nullptr) LSE[bh * T + myq] = (m * scale_log2 + __log2f(lsum)) * LN2;
+}
+
 // Generic path: one wave per query row, lanes over head_dim (any dtype, any head_dim <= 256).
 template <typename TT, int DPL>
 __global__ __launch_bounds__(256) void fa_fwd_wave_kernel(const TT* __restrict__ Q, const TT* __restrict__ K,
@@ -327,6 +537,15 @@ void launch_mfma_fwd(hipStream_t s, const void* q, const void* k, const void* v,
                      int causal, float scale_log2, const void* cs = nullptr, float sqd = 0.0f) {
   const dim3 grid((T + 127) / 128, BH);
   const bf16 *Q = (const bf16*)q, *K = (const bf16*)k, *V = (const bf16*)v, *CS = (const bf16*)cs;
+  if constexpr (HD == 128) {
+    if (cs != nullptr)  // FoX attention is causal
+      fa_fwd128_kernel<true, true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, CS, sqd);
+    else if (causal)
+      fa_fwd128_kernel<true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
+    else
+      fa_fwd128_kernel<false><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
+    return;
+  }
   if (cs != nullptr)  // FoX attention is causal
     fa_fwd_mfma_kernel<HD, true, true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, CS, sqd);
   else if (causal)

@@ -427,57 +427,6 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
 // over the two, so the compiler's wait for a DMA into one buffer never lands before the
 // reads of the other; every wave waits for its own DMA before the barrier that publishes
 // the tile.
-typedef __attribute__((address_space(3))) void lds_void;
-
-// One 16-byte load per lane straight into LDS: lane l of the wave writes bytes
-// [16 l, 16 l + 16) after the wave-uniform address lds.
-EDF_DEVICE void dma16(const void* src, void* lds) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
-}
-
-// Column-major LDS tile of R rows x 128 bf16 columns (R a multiple of 32): the 16-byte
-// chunk c (columns 8 c .. 8 c + 7) of row r sits in slot c R + (r ^ 4 (c % 4)).  MFMA row
-// operands (16 rows of one chunk per 16 lanes) and transposed reads (4 rows x 4 chunks per
-// 32 lanes) each touch 64 distinct banks, and since the row XOR depends on c % 4 only,
-// every fragment address is one of two per-lane bases plus an immediate offset (the
-// row-major XOR swizzle needs a live address register per fragment instead).
-//
-// Rows r0 .. r0 + R - 1 of a row-major [T][128] bf16 head (rows past T - 1 repeat row
-// T - 1) into such a tile: the workgroup's R / 16 loads of 64 lanes fill slots in order,
-// load j slots 64 j .. 64 j + 63.
-template <int R>
-EDF_DEVICE void stage_cm(const bf16* src, bf16* dst, int r0, int T, int wu, int l) {
-  constexpr int IPW = R / 16;  // loads per wave
-  static_assert(R % 32 == 0, "whole 32-row groups");
-#pragma unroll
-  for (int i = 0; i < IPW; ++i) {
-    const int j = wu * IPW + i;
-    const int slot = 64 * j + l;
-    const int c = slot / R;
-    const int row = (slot % R) ^ ((c & 3) << 2);
-    const long gr = min(r0 + row, T - 1);
-    dma16(src + gr * 128 + c * 8, dst + 512 * j);
-  }
-}
-
-// Per-lane bases (element offsets) into a column-major tile of R rows.  Row operand
-// (lane li reads row rb + li, chunk 2 kk + g, rb a multiple of 32):
-//   cm_row_base<R>(li, g, kk & 1) + (2 kk R + rb) * 8.
-template <int R>
-EDF_DEVICE int cm_row_base(int li, int g, int parity) {
-  return (((li ^ (4 * (2 * parity + g))) + g * R) << 3);
-}
-// Transposed read of rows rb + 16 kc + kr + 8 h, columns 32 dt + d0 (rb a multiple of 32,
-// kr < 8, d0 a multiple of 4 below 32):  cm_tr_base<R>(kr, d0, h) + (4 dt R + rb + 16 kc) * 8.
-template <int R>
-EDF_DEVICE int cm_tr_base(int kr, int d0, int h) {
-  const int cq = d0 >> 3;
-  return ((((kr + 8 * h) ^ (4 * cq)) + cq * R) << 3) + (d0 & 7);
-}
-
-// vmcnt(0) only: the DMA loads and the plain loads of this wave have landed.
-EDF_DEVICE void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // dK / dV, head_dim 128: 128 keys per workgroup, 32 per wave as in fa_bwd_dkdv_kernel,
 // with K as register B fragments but V read from an LDS copy of the workgroup's 128 x 128
 // tile (its fragments would not fit 256 registers beside the dK^T, dV^T accumulators) and
@@ -676,8 +625,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
 
 // dQ, head_dim 128 (same decomposition as fa_bwd_dq_kernel: 128 queries per workgroup,
 // 32 per wave with Q and dO as register B fragments, 64-key tiles, each processed as two
-// 32-key halves so only one half's S^T / dP^T is live).
-template <bool CAUSAL, bool FOX>
+// 32-key halves so only one half's S^T / dP^T is live).  OWN_D: the kernel forms
+// D = rowsum(dO o O) of its queries itself (O read in dO's fragment layout) and writes it
+// to Dw for the dK/dV kernel that runs after it; otherwise it reads D from Dd.
+template <bool CAUSAL, bool FOX, bool OWN_D = false>
 __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                               const bf16* __restrict__ V, const bf16* __restrict__ dO,
                                                               const float* __restrict__ LSE,
@@ -685,7 +636,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
                                                               int T, float scale_log2, float scale,
                                                               const bf16* __restrict__ CS,
                                                               const float* __restrict__ DCSK, bf16* __restrict__ DCS,
-                                                              float sqd) {
+                                                              float sqd, const bf16* __restrict__ O = nullptr,
+                                                              float* __restrict__ Dw = nullptr) {
   constexpr int HD = 128, BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   __shared__ __attribute__((aligned(16))) bf16 sK0[BN * HD];
@@ -713,7 +665,19 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
     of[kk] = myq < T ? *(const bf16x8*)(dO + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
   }
   const float myl = myq < T ? LSE[bh * T + myq] * LOG2E : 0.0f;
-  const float myd = myq < T ? Dd[bh * T + myq] : 0.0f;
+  float myd = 0.0f;
+  if constexpr (OWN_D) {  // the lane's 64 dims, then the other half's through the lane 32 apart
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk) {
+      const bf16x8 ov = myq < T ? *(const bf16x8*)(O + base + (long)myq * HD + kk * 16 + 8 * g) : bf16x8{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) myd = fmaf((float)of[kk][e], (float)ov[e], myd);
+    }
+    myd += __shfl_xor(myd, 32);
+    if (g == 0 && myq < T) Dw[bh * T + myq] = myd;
+  } else {
+    myd = myq < T ? Dd[bh * T + myq] : 0.0f;
+  }
   const float csq = FOX && myq < T ? to_f32(CS[bh * T + myq]) * sqd : 0.0f;
   float rowacc = 0.0f;
   bf16 rcs = {};
@@ -960,26 +924,28 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_wave_kernel(const TT* __restr
   if (CS != nullptr && lane == 0) DCSK[row] = -colacc;
 }
 
-// head_dim 128: the two-workgroups-per-CU kernels; FoX (cs != nullptr) is causal.
+// head_dim 128: the two-workgroups-per-CU kernels.  FoX (CS != nullptr, causal, D already
+// in Dd): dK/dV first, since dQ adds its key-side d cs.  Otherwise (O given, Dd not yet
+// written): dQ first, forming D of its queries into Dd, then dK/dV reading it.
 void launch_mfma_bwd128(hipStream_t s, const bf16* Q, const bf16* K, const bf16* V, const bf16* G, const float* lse,
-                        const float* Dd, bf16* dq, bf16* dk, bf16* dv, int BH, int T, int causal, float scale_log2,
-                        float scale, const bf16* CS, float* dcsk, bf16* dcs, float sqd) {
+                        float* Dd, bf16* dq, bf16* dk, bf16* dv, int BH, int T, int causal, float scale_log2,
+                        float scale, const bf16* CS, float* dcsk, bf16* dcs, float sqd, const bf16* O) {
   const dim3 g1((T + 127) / 128, BH);
-  if (CS != nullptr) {  // dK/dV first: dQ adds its key-side d cs
+  if (CS != nullptr) {
     fa_bwd_dkdv128_kernel<true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, CS, dcsk,
                                                          sqd);
     fa_bwd_dq128_kernel<true, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dq, T, scale_log2, scale, CS, dcsk, dcs,
                                                        sqd);
   } else if (causal) {
+    fa_bwd_dq128_kernel<true, false, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, nullptr, dq, T, scale_log2, scale,
+                                                              nullptr, nullptr, nullptr, 0.0f, O, Dd);
     fa_bwd_dkdv128_kernel<true, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, nullptr,
                                                           nullptr, 0.0f);
-    fa_bwd_dq128_kernel<true, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dq, T, scale_log2, scale, nullptr,
-                                                        nullptr, nullptr, 0.0f);
   } else {
+    fa_bwd_dq128_kernel<false, false, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, nullptr, dq, T, scale_log2, scale,
+                                                               nullptr, nullptr, nullptr, 0.0f, O, Dd);
     fa_bwd_dkdv128_kernel<false, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale,
                                                            nullptr, nullptr, 0.0f);
-    fa_bwd_dq128_kernel<false, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dq, T, scale_log2, scale, nullptr,
-                                                         nullptr, nullptr, 0.0f);
   }
 }
 
@@ -991,9 +957,9 @@ void launch_mfma_bwd(hipStream_t s, const void* q, const void* k, const void* v,
   const dim3 g1((T + 127) / 128, BH);
   const bf16 *Q = (const bf16*)q, *K = (const bf16*)k, *V = (const bf16*)v, *G = (const bf16*)go;
   const bf16* CS = (const bf16*)cs;
-  if constexpr (HD == 128) {
-    launch_mfma_bwd128(s, Q, K, V, G, lse, Dd, (bf16*)dq, (bf16*)dk, (bf16*)dv, BH, T, causal, scale_log2, scale, CS,
-                       dcsk, (bf16*)dcs, sqd);
+  if constexpr (HD == 128) {  // FoX only: plain attention goes through launch_mfma_bwd128 with O
+    launch_mfma_bwd128(s, Q, K, V, G, lse, (float*)Dd, (bf16*)dq, (bf16*)dk, (bf16*)dv, BH, T, causal, scale_log2,
+                       scale, CS, dcsk, (bf16*)dcs, sqd, nullptr);
     return;
   }
   if (cs != nullptr) {  // FoX attention is causal; dK/dV first: dQ adds its key-side d cs
@@ -1054,13 +1020,20 @@ int fa_bwd_check(const void* q, const void* k, const void* v, const void* out, c
 }
 
 // D = rowsum(dO o O) into Dd [B*H*T] (every entry written before it is read), then the dK/dV
-// and dQ kernels.
+// and dQ kernels; bf16 head_dim 128 forms D inside its dQ kernel.
 int fa_bwd_run(hipStream_t s, const void* q, const void* k, const void* v, const void* out, const void* grad_out,
                const float* lse, void* grad_q, void* grad_k, void* grad_v, float* Dd, int batch, int num_heads,
                int seq_len, int head_dim, int causal, int dtype) {
   const int BH = batch * num_heads;
   const long rows = (long)BH * seq_len;
   const unsigned gd = (unsigned)((rows + 15) / 16);
+  if (dtype == EDF_BF16 && head_dim == 128) {
+    const float scale = 1.0f / sqrtf(128.0f);
+    launch_mfma_bwd128(s, (const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)grad_out, lse, Dd,
+                       (bf16*)grad_q, (bf16*)grad_k, (bf16*)grad_v, BH, seq_len, causal, scale * LOG2E, scale,
+                       nullptr, nullptr, nullptr, 0.0f, (const bf16*)out);
+    return check_launch("flash attention backward");
+  }
   if (dtype == EDF_BF16)
     fa_bwd_dot_kernel<bf16><<<gd, 256, 0, s>>>((const bf16*)out, (const bf16*)grad_out, Dd, rows, head_dim);
   else
@@ -1069,11 +1042,8 @@ int fa_bwd_run(hipStream_t s, const void* q, const void* k, const void* v, const
   if (rc) return rc;
   const float scale = 1.0f / sqrtf((float)head_dim);
   const float scale_log2 = scale * LOG2E;
-  if (dtype == EDF_BF16 && (head_dim == 32 || head_dim == 64 || head_dim == 128)) {
-    if (head_dim == 128)
-      launch_mfma_bwd<128>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, causal, scale_log2,
-                           scale);
-    else if (head_dim == 64)
+  if (dtype == EDF_BF16 && (head_dim == 32 || head_dim == 64)) {
+    if (head_dim == 64)
       launch_mfma_bwd<64>(s, q, k, v, grad_out, lse, Dd, grad_q, grad_k, grad_v, BH, seq_len, causal, scale_log2,
                           scale);
     else

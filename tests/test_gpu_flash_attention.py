@@ -37,8 +37,17 @@ def test_flash_attention_fwd_bwd(case, rng):
     tol = TOL[dtype]
     assert_close(host(out), scans.flash_attention(qr, kr, vr, causal), tol, "O")
     dq, dk, dv = scans.flash_attention_backward(qr, kr, vr, dor, causal)
-    assert_close(host(tq.grad), dq, tol, "dQ")
-    assert_close(host(tk.grad), dk, tol, "dK")
+    if T == 1:
+        # One key: O = V[0] exactly, so dP - D = dO . (V[0] - O) = 0 and dQ = dK = 0
+        # analytically; the kernel's float32 dP and D (different summation orders) leave a
+        # rounding residue, bounded here by the tolerance times the size of one gradient
+        # term, sqrt(d) max|dO| max|V| max|K| (a ratio to max |expected| ~ 0 is undefined).
+        term = np.sqrt(d) * np.abs(dor).max() * np.abs(vr).max() * max(np.abs(kr).max(), np.abs(qr).max())
+        for name, got in (("dQ", host(tq.grad)), ("dK", host(tk.grad))):
+            assert np.abs(got).max() <= tol * term, f"{name}: |{name}| {np.abs(got).max():.3e} > {tol * term:.3e}"
+    else:
+        assert_close(host(tq.grad), dq, tol, "dQ")
+        assert_close(host(tk.grad), dk, tol, "dK")
     assert_close(host(tv.grad), dv, tol, "dV")
 
 
