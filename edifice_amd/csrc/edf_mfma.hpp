@@ -118,44 +118,51 @@ EDF_DEVICE void dma16(const void* src, void* lds) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
 }
 
-// Column-major LDS tile of R rows x 128 bf16 columns (R a multiple of 32): the 16-byte
-// chunk c (columns 8 c .. 8 c + 7) of row r sits in slot c R + (r ^ 4 (c % 4)).  MFMA row
-// operands (16 rows of one chunk per 16 lanes) and transposed reads (4 rows x 4 chunks per
-// 32 lanes) each touch 64 distinct banks, and since the row XOR depends on c % 4 only,
-// every fragment address is one of two per-lane bases plus an immediate offset (the
-// row-major XOR swizzle needs a live address register per fragment instead).
+// LDS tile of R rows x 128 bf16 columns (R a multiple of 16) in blocks of 64 16-byte slots:
+// block half * R / 8 + b8 holds rows 8 b8 .. 8 b8 + 7, chunks (of 8 columns) 8 half .. +7,
+// chunk c' and row r' of the block in slot (c' ^ (b8 % 2)) * 8 + (r' ^ 4 ((c' / 2) % 2)).
+// One DMA load fills one block from 8 half rows (8 cache lines); MFMA row operands (16 rows
+// of one chunk per 16 lanes) and transposed reads (4 rows x 4 chunks x 8 bytes per 32
+// lanes) each touch all 64 banks once; and every fragment address is one of two per-lane
+// bases plus an immediate (the row-major XOR swizzle needs an address register per
+// fragment, a column-major tile makes each DMA load touch 64 lines).
 //
 // Rows r0 .. r0 + R - 1 of a row-major [T][128] bf16 head (rows past T - 1 repeat row
-// T - 1) into such a tile: the workgroup's R / 16 loads of 64 lanes fill slots in order,
-// load j slots 64 j .. 64 j + 63.
+// T - 1) into such a tile: the workgroup's 4 waves issue R / 16 loads each, load j
+// filling block j.
 template <int R>
-EDF_DEVICE void stage_cm(const bf16* src, bf16* dst, int r0, int T, int wu, int l) {
+EDF_DEVICE void stage_hb(const bf16* src, bf16* dst, int r0, int T, int wu, int l) {
   constexpr int IPW = R / 16;  // loads per wave
-  static_assert(R % 32 == 0, "whole 32-row groups");
+  static_assert(R % 16 == 0, "whole 8-row blocks for 4 waves");
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
     const int j = wu * IPW + i;
-    const int slot = 64 * j + l;
-    const int c = slot / R;
-    const int row = (slot % R) ^ ((c & 3) << 2);
-    const long gr = min(r0 + row, T - 1);
-    dma16(src + gr * 128 + c * 8, dst + 512 * j);
+    const int half = j / (R / 8), b8 = j % (R / 8);
+    const int cp = (l >> 3) ^ (b8 & 1);
+    const int rp = (l & 7) ^ (4 * ((cp >> 1) & 1));
+    const long gr = min(r0 + 8 * b8 + rp, T - 1);
+    dma16(src + gr * 128 + (8 * half + cp) * 8, dst + 512 * j);
   }
 }
 
-// Per-lane bases (element offsets) into a column-major tile of R rows.  Row operand
-// (lane li reads row rb + li, chunk 2 kk + g, rb a multiple of 32):
-//   cm_row_base<R>(li, g, kk & 1) + (2 kk R + rb) * 8.
-template <int R>
-EDF_DEVICE int cm_row_base(int li, int g, int parity) {
-  return (((li ^ (4 * (2 * parity + g))) + g * R) << 3);
+// Element offsets into such a tile.  Row operand (lane li, half g reads row rb + li, chunk
+// 2 kk + g; rb a multiple of 32): hb_row_base(li, g, kk % 2) + hb_row_off<R>(kk, rb).
+EDF_DEVICE int hb_row_base(int li, int g, int parity) {
+  return ((li >> 3) * 64 + 8 * (g ^ ((li >> 3) & 1)) + ((li & 7) ^ (4 * parity))) << 3;
 }
-// Transposed read of rows rb + 16 kc + kr + 8 h, columns 32 dt + d0 (rb a multiple of 32,
-// kr < 8, d0 a multiple of 4 below 32):  cm_tr_base<R>(kr, d0, h) + (4 dt R + rb + 16 kc) * 8.
 template <int R>
-EDF_DEVICE int cm_tr_base(int kr, int d0, int h) {
+EDF_DEVICE constexpr int hb_row_off(int kk, int rb) {
+  return ((kk >> 2) * (R / 8) * 64 + 16 * (kk & 3) + (rb / 8) * 64) << 3;
+}
+// Transposed read of rows rb + 16 kc + kr + 8 h, columns 32 dt + d0 .. + 3 (rb a multiple
+// of 32, kr < 8, d0 a multiple of 4 below 32): hb_tr_base(kr, d0, h) + hb_tr_off<R>(dt, kc, rb).
+EDF_DEVICE int hb_tr_base(int kr, int d0, int h) {
   const int cq = d0 >> 3;
-  return ((((kr + 8 * h) ^ (4 * cq)) + cq * R) << 3) + (d0 & 7);
+  return ((h * 64 + (cq ^ h) * 8 + (kr ^ (4 * ((cq >> 1) & 1)))) << 3) + (d0 & 7);
+}
+template <int R>
+EDF_DEVICE constexpr int hb_tr_off(int dt, int kc, int rb) {
+  return ((dt >> 1) * (R / 8) * 64 + (rb / 8 + 2 * kc) * 64 + 32 * (dt & 1)) << 3;
 }
 
 // vmcnt(0) only: the DMA loads and the plain loads of this wave have landed.

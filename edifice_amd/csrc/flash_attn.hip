@@ -246,8 +246,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
 
 // head_dim 128: the same decomposition (128 queries per workgroup, 32 per wave with Q^T as
 // register B fragments, 64-key tiles), with K and V moved by 16-byte DMA loads into
-// column-major LDS tiles (fragment addresses are bases plus immediates, no staging
-// registers), and K one tile ahead of V: iteration t issues the MFMAs of S(t + 1) before
+// half-row-block LDS tiles (stage_hb: fragment addresses are bases plus immediates, no
+// staging registers), and K one tile ahead of V: iteration t issues the MFMAs of S(t + 1) before
 // the softmax of S(t), so the matrix core works on the next scores while the VALU turns
 // the current ones into P (the two rings stay two-deep: K(t) was consumed in iteration
 // t - 1).  Two workgroups per CU.
@@ -258,10 +258,11 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
                                                            const bf16* __restrict__ CS, float sqd) {
   constexpr int HD = 128, BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
-  __shared__ __attribute__((aligned(16))) bf16 sK0[BN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sK1[BN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sV0[BN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sV1[BN * HD];
+  // Two arrays, X0 = {K buffer 0, V buffer 1} and X1 = {K buffer 1, V buffer 0}: iteration t
+  // (parity B) writes only X_B and reads only X_(1-B), and each array's fixed address costs
+  // address registers (it is not folded into the LDS offset field).
+  __shared__ __attribute__((aligned(16))) bf16 sX0[2 * BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sX1[2 * BN * HD];
   __shared__ __attribute__((aligned(16))) float sC0[FOX ? BN : 4], sC1[FOX ? BN : 4];  // cs of a K tile's keys
 
   const int tid = threadIdx.x;
@@ -290,42 +291,42 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
   const int grp = l >> 4, i16 = l & 15;
   const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
   const int kr = 4 * (grp >> 1) + (i16 >> 2);
-  const int krow[2] = {cm_row_base<BN>(li, g, 0), cm_row_base<BN>(li, g, 1)};
-  const int vtr[2] = {cm_tr_base<BN>(kr, d0, 0), cm_tr_base<BN>(kr, d0, 1)};
+  const int krow[2] = {hb_row_base(li, g, 0), hb_row_base(li, g, 1)};
+  const int vtr[2] = {hb_tr_base(kr, d0, 0), hb_tr_base(kr, d0, 1)};
 
   const int kend = CAUSAL ? min(T, q0 + BM) : T;
   const int nkt = (kend + BN - 1) / BN;
   // unmasked tiles of this wave: inside the sequence and, causal, at or below its diagonal
   const int ksplit = min(min(T / BN, nkt), CAUSAL ? (qw + 1) / BN : nkt);
-  auto visible = [&](int t) { return !(CAUSAL && t * BN > qw + 31); };
+  auto visible = [&](int t) __attribute__((always_inline)) { return !(CAUSAL && t * BN > qw + 31); };
 
-  auto issue_k = [&](auto bt, int t) {  // K tile t (and its cs) into K buffer B
+  auto issue_k = [&](auto bt, int t) __attribute__((always_inline)) {  // K tile t (and its cs) into K buffer B
     constexpr int B = decltype(bt)::value;
-    stage_cm<BN>(K + base, B ? sK1 : sK0, t * BN, T, wu, l);
+    stage_hb<BN>(K + base, B ? sX1 : sX0, t * BN, T, wu, l);
     if constexpr (FOX) {
       if (tid < BN) rcs = CS[bh * T + min(t * BN + tid, T - 1)];  // converted by publish_k()
     }
   };
-  auto issue_v = [&](auto bt, int t) {
+  auto issue_v = [&](auto bt, int t) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
-    stage_cm<BN>(V + base, B ? sV1 : sV0, t * BN, T, wu, l);
+    stage_hb<BN>(V + base, (B ? sX0 : sX1) + BN * HD, t * BN, T, wu, l);
   };
-  auto publish_k = [&](auto bt) {
+  auto publish_k = [&](auto bt) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
     if constexpr (FOX) {
       if (tid < BN) (B ? sC1 : sC0)[tid] = to_f32(rcs);
     }
   };
   // S^T of the K tile in buffer B: lane owns query column li, rows are the tile's keys
-  auto scores = [&](auto bt, f32x16* s) {
+  auto scores = [&](auto bt, f32x16* s) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
-    const bf16* sk = B ? sK1 : sK0;
+    const bf16* sk = B ? sX1 : sX0;
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       s[h2] = zero16();
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk)
-        s[h2] = mfma32(*(const bf16x8*)(&sk[krow[kk & 1] + (2 * kk * BN + 32 * h2) * 8]), qf[kk], s[h2]);
+        s[h2] = mfma32(*(const bf16x8*)(&sk[krow[kk & 1] + hb_row_off<BN>(kk, 32 * h2)]), qf[kk], s[h2]);
     }
     if constexpr (FOX) {  // + (cs_q - cs_key) sqrt(d); key h2 * 32 + 8 rb + 4 g + e
       const float* sc = B ? sC1 : sC0;
@@ -339,11 +340,11 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
         }
     }
   };
-  // online softmax of tile t's scores and O^T += V^T P^T with V from buffer B
-  auto consume = [&](auto bt, f32x16* s, int t, auto masked) {
-    constexpr int B = decltype(bt)::value;
+  f32x16 sc[2], sn[2];  // scores of the current and the next tile
+  // Online softmax of tile t's scores, first half: mask, row maximum, rescale of O and the
+  // sum when a maximum grew; returns the new maximum in scaled log2 units.
+  auto softmax_max = [&](f32x16* s, int t, auto masked) __attribute__((always_inline)) {
     constexpr bool MASK = decltype(masked)::value;
-    const bf16* sv = B ? sV1 : sV0;
     const int k0 = t * BN;
     float mx = -INFINITY;
 #pragma unroll
@@ -357,44 +358,102 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
         mx = fmaxf(mx, s[h2][r]);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(m, mx);
-    const float mns = mnew == -INFINITY ? 0.0f : mnew * scale_log2;
-    if (__any(mnew > m)) {  // rescale only when some row maximum grew
-      const float alpha = fast_exp2(m * scale_log2 - mns);
+    // The exponentials are taken against a reference maximum m that is moved (and O and
+    // the sum rescaled) only when a score exceeds it by more than 2^8: p <= 256 is exact
+    // enough in float32 and bf16, and O, the sum and the LSE all refer to the same m.
+    if (__any(mx * scale_log2 > m * scale_log2 + 8.0f)) {
+      const float mnew = fmaxf(m, mx);
+      const float alpha = fast_exp2(m * scale_log2 - (mnew == -INFINITY ? 0.0f : mnew * scale_log2));
       lsum *= alpha;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      m = mnew;
     }
-    m = mnew;
-    float rs = 0.0f;
-#pragma unroll
-    for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(fmaf(s[h2][r], scale_log2, -mns));
-        s[h2][r] = pv;
-        rs += pv;
-      }
-    lsum += rs + __shfl_xor(rs, 32);
-    bf16x8 pf[4];
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc)
-#pragma unroll
-      for (int it = 0; it < 8; ++it) pf[kc][it] = (bf16)s[kc >> 1][8 * (kc & 1) + it];
+    return m == -INFINITY ? 0.0f : m * scale_log2;
+  };
+  // Second half for elements 2 j, 2 j + 1 of the 32: p = 2^(s c - m c) into the row sum and
+  // the bf16 B fragments of P^T (fragment kc holds keys 16 kc + 4 g + {0..3} and
+  // 16 kc + 8 + 4 g + {0..3}, the S^T registers' own order).
+  // pin: an empty volatile asm takes the pair and the sum, so the compiler cannot sink this
+  // arithmetic below the scheduling barrier of the step that issued it.
+  auto softmax_pair = [&](f32x16* s, int j, float mns, float& rs, bf16x8* pf, auto pin) __attribute__((always_inline)) {
+    const int h2 = j >> 3, r = (2 * j) & 15;
+    const float p0 = fast_exp2(fmaf(s[h2][r], scale_log2, -mns));
+    const float p1 = fast_exp2(fmaf(s[h2][r + 1], scale_log2, -mns));
+    unsigned pk = pack_bf16x2(p0, p1);
+    // the row sum of the bf16 P that the MFMA consumes, one dot2 per pair
+    rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), bf16x2{(bf16)1.0f, (bf16)1.0f}, rs, false);
+    if constexpr (decltype(pin)::value) asm volatile("" : "+v"(pk), "+v"(rs));
+    const int kc = 2 * h2 + (r >> 3), it = r & 7;
+    const bf16x2 pp = __builtin_bit_cast(bf16x2, pk);
+    pf[kc][it] = pp[0];
+    pf[kc][it + 1] = pp[1];
+  };
+  // O^T += V^T P^T with V from buffer B (transposed reads in the P^T key order)
+  auto pv_mma = [&](auto bt, const bf16x8* pf) __attribute__((always_inline)) {
+    constexpr int B = decltype(bt)::value;
+    const bf16* sv = (B ? sX0 : sX1) + BN * HD;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const int o16 = (4 * dt * BN + 16 * kc) * 8;
+        const int o16 = hb_tr_off<BN>(dt, kc, 0);
         o[dt] = mfma32(cat4(lds_read_tr16(&sv[vtr[0] + o16]), lds_read_tr16(&sv[vtr[1] + o16])), pf[kc], o[dt]);
       }
+  };
+  // Generic tile: softmax of s, then O with V buffer B.
+  auto consume = [&](auto bt, f32x16* s, int t, auto masked) __attribute__((always_inline)) {
+    const float mns = softmax_max(s, t, masked);
+    float rs = 0.0f;
+    bf16x8 pf[4];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) softmax_pair(s, j, mns, rs, pf, std::false_type{});
+    lsum += rs + __shfl_xor(rs, 32);
+    pv_mma(bt, pf);
+  };
+  // Unmasked tile t with a visible successor: the 16 MFMAs of S(t + 1) (K buffer 1 - B, its
+  // fragments read two steps ahead) alternate with the exponentials of S(t), two per MFMA,
+  // pinned by scheduling barriers so the matrix core and the VALU work at the same time.
+  auto fused = [&](auto bt, int t) __attribute__((always_inline)) {
+    constexpr int B = decltype(bt)::value;
+    const bf16* sk = B ? sX0 : sX1;  // K(t + 1) is in K buffer 1 - B
+    const float mns = softmax_max(sc, t, std::false_type{});
+    auto kfrag = [&](int i) __attribute__((always_inline)) {  // step i: keys 32 (i % 2) + li, dims of kk = i / 2
+      const int kk = i >> 1, h2 = i & 1;
+      return *(const bf16x8*)(&sk[krow[kk & 1] + hb_row_off<BN>(kk, 32 * h2)]);
+    };
+    bf16x8 fr[2] = {kfrag(0), kfrag(1)};
+    sn[0] = zero16();
+    sn[1] = zero16();
+    float rs = 0.0f;
+    bf16x8 pf[4];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sn[i & 1] = mfma32(fr[i & 1], qf[i >> 1], sn[i & 1]);
+      if (i + 2 < 16) fr[i & 1] = kfrag(i + 2);
+      softmax_pair(sc, i, mns, rs, pf, std::true_type{});
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (FOX) {  // + (cs_q - cs_key) sqrt(d) for the next tile's scores
+      const float* scs = B ? sC0 : sC1;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+          const f32x4 ck = *(const f32x4*)(&scs[h2 * 32 + 8 * rb + 4 * g]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sn[h2][4 * rb + e] += fmaf(-ck[e], sqd, csq);
+        }
+    }
+    lsum += rs + __shfl_xor(rs, 32);
+    pv_mma(bt, pf);
   };
 
   const std::integral_constant<int, 0> b0{};
   const std::integral_constant<int, 1> b1{};
-  f32x16 sc[2], sn[2];
   // prologue: K(0), V(0), K(1) in; S(0); a barrier before iteration 0 reloads K buffer 0
   issue_k(b0, 0);
   issue_v(b0, 0);
@@ -408,16 +467,20 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
   __syncthreads();  // K(1) visible, K buffer 0 free
   // iteration t (buffer parity B = t % 2): K(t + 2) into K buffer B, V(t + 1) into V buffer
   // 1 - B; S(t + 1) from K buffer 1 - B; softmax of S(t) and O with V buffer B
-  auto step = [&](auto bt, int t) {
+  auto step = [&](auto bt, int t) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
     const std::integral_constant<int, 1 - B> ot{};
     if (t + 2 < nkt) issue_k(bt, t + 2);
     if (t + 1 < nkt) issue_v(ot, t + 1);
     const bool nvis = t + 1 < nkt && visible(t + 1);
     if (visible(t)) {
-      if (nvis) scores(ot, sn);
-      if (t < ksplit) consume(bt, sc, t, std::false_type{});
-      else consume(bt, sc, t, std::true_type{});
+      if (t < ksplit && nvis) {
+        fused(bt, t);
+      } else {
+        if (nvis) scores(ot, sn);
+        if (t < ksplit) consume(bt, sc, t, std::false_type{});
+        else consume(bt, sc, t, std::true_type{});
+      }
     }
     wait_vm();
     if (t + 2 < nkt) publish_k(bt);
@@ -430,10 +493,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
     if (t + 1 < nkt) step(b1, t + 1);
   }
 
-  // O through the free K buffers (each wave its 32 rows, row-major swizzled), written as
+  // O through the free array X0 (each wave its 32 rows, row-major swizzled), written as
   // whole rows: a lane holds one query row, so storing from registers would touch 32 rows
   // per instruction in 16-byte pieces.
-  bf16* so = (w < 2 ? sK0 : sK1) + (w & 1) * 32 * HD;
+  bf16* so = sX0 + w * 32 * HD;
   const float inv = myq < T ? 1.0f / lsum : 0.0f;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)

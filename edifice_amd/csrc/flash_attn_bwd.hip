@@ -443,10 +443,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
   constexpr int HD = 128, BKEY = 128, BQ = 32;
   constexpr int NKK = HD / 16, NDT = HD / 32;
   __shared__ __attribute__((aligned(16))) bf16 sV[BKEY * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sQ0[BQ * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sQ1[BQ * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sO0[BQ * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sO1[BQ * HD];
+  // ring slot b: Q then dO (one array per slot: the compiler's fixed array addresses are
+  // not folded into the LDS offset field, so each array costs address registers)
+  __shared__ __attribute__((aligned(16))) bf16 sR0[2 * BQ * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sR1[2 * BQ * HD];
   __shared__ __attribute__((aligned(16))) float sL0[BQ], sL1[BQ], sD0[BQ], sD1[BQ];
   __shared__ __attribute__((aligned(16))) float sC0[FOX ? BQ : 4], sC1[FOX ? BQ : 4];
 
@@ -462,7 +462,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
   const long base = bh * T * HD;
 
   // keys past the end read row T - 1 of V: they only feed their own dK, dV columns, never stored
-  stage_cm<BKEY>(V + base, sV, kb0, T, wu, l);
+  stage_hb<BKEY>(V + base, sV, kb0, T, wu, l);
   bf16x8 kf[NKK];
 #pragma unroll
   for (int kk = 0; kk < NKK; ++kk)
@@ -484,8 +484,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
   // wait for the DMA loads issued before them.
   auto issue = [&](auto bt, int q0) {
     constexpr int B = decltype(bt)::value;
-    stage_cm<BQ>(Q + base, B ? sQ1 : sQ0, q0, T, wu, l);
-    stage_cm<BQ>(dO + base, B ? sO1 : sO0, q0, T, wu, l);
+    stage_hb<BQ>(Q + base, B ? sR1 : sR0, q0, T, wu, l);
+    stage_hb<BQ>(dO + base, (B ? sR1 : sR0) + BQ * HD, q0, T, wu, l);
     if (tid < BQ) {
       const long q = min(q0 + tid, T - 1);
       rl = LSE[bh * T + q];
@@ -506,15 +506,16 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
   const int grp = l >> 4, i16 = l & 15;
   const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
   const int kr = 4 * (grp >> 1) + (i16 >> 2);
-  const int qrow[2] = {cm_row_base<BQ>(li, g, 0), cm_row_base<BQ>(li, g, 1)};
-  const int vrow[2] = {cm_row_base<BKEY>(li, g, 0) + 32 * w * 8, cm_row_base<BKEY>(li, g, 1) + 32 * w * 8};
-  const int qtr[2] = {cm_tr_base<BQ>(kr, d0, 0), cm_tr_base<BQ>(kr, d0, 1)};
+  const int qrow[2] = {hb_row_base(li, g, 0), hb_row_base(li, g, 1)};
+  const int vrow[2] = {hb_row_base(li, g, 0) + hb_row_off<BKEY>(0, 32 * w),
+                       hb_row_base(li, g, 1) + hb_row_off<BKEY>(0, 32 * w)};
+  const int qtr[2] = {hb_tr_base(kr, d0, 0), hb_tr_base(kr, d0, 1)};
 
   auto subtile = [&](auto bt, int q0, int sub, auto masked) {
     constexpr int B = decltype(bt)::value;
     constexpr bool MASK = decltype(masked)::value;
-    const bf16* sQ = B ? sQ1 : sQ0;
-    const bf16* sO = B ? sO1 : sO0;
+    const bf16* sQ = B ? sR1 : sR0;
+    const bf16* sO = sQ + BQ * HD;
     const float* sL = B ? sL1 : sL0;
     const float* sD = B ? sD1 : sD0;
     const float* sC = B ? sC1 : sC0;
@@ -525,8 +526,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
     f32x16 s = zero16(), dp = zero16();
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk) {
-      const int off = qrow[kk & 1] + (2 * kk * BQ + 32 * sub) * 8;
-      const bf16x8 vf = *(const bf16x8*)(&sV[vrow[kk & 1] + 2 * kk * BKEY * 8]);
+      const int off = qrow[kk & 1] + hb_row_off<BQ>(kk, 32 * sub);
+      const bf16x8 vf = *(const bf16x8*)(&sV[vrow[kk & 1] + hb_row_off<BKEY>(kk, 0)]);
       s = mfma32(*(const bf16x8*)(&sQ[off]), kf[kk], s);
       dp = mfma32(*(const bf16x8*)(&sO[off]), vf, dp);
     }
@@ -562,8 +563,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int kc = 0; kc < 2; ++kc) {
-        const int o0 = qtr[0] + (4 * dt * BQ + 32 * sub + 16 * kc) * 8;
-        const int o1 = qtr[1] + (4 * dt * BQ + 32 * sub + 16 * kc) * 8;
+        const int o0 = qtr[0] + hb_tr_off<BQ>(dt, kc, 32 * sub);
+        const int o1 = qtr[1] + hb_tr_off<BQ>(dt, kc, 32 * sub);
         dvt[dt] = mfma32(cat4(lds_read_tr16(&sO[o0]), lds_read_tr16(&sO[o1])), pb[kc], dvt[dt]);
         dkt[dt] = mfma32(cat4(lds_read_tr16(&sQ[o0]), lds_read_tr16(&sQ[o1])), db[kc], dkt[dt]);
       }
@@ -640,10 +641,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
                                                               float* __restrict__ Dw = nullptr) {
   constexpr int HD = 128, BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
-  __shared__ __attribute__((aligned(16))) bf16 sK0[BN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sK1[BN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sV0[BN * HD];
-  __shared__ __attribute__((aligned(16))) bf16 sV1[BN * HD];
+  __shared__ __attribute__((aligned(16))) bf16 sR0[2 * BN * HD];  // ring slot: K then V
+  __shared__ __attribute__((aligned(16))) bf16 sR1[2 * BN * HD];
   __shared__ __attribute__((aligned(16))) float sCS0[FOX ? BN : 4], sCS1[FOX ? BN : 4];
 
   const int tid = threadIdx.x;
@@ -687,8 +686,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
 
   auto issue = [&](auto bt, int k0) {
     constexpr int B = decltype(bt)::value;
-    stage_cm<BN>(K + base, B ? sK1 : sK0, k0, T, wu, l);
-    stage_cm<BN>(V + base, B ? sV1 : sV0, k0, T, wu, l);
+    stage_hb<BN>(K + base, B ? sR1 : sR0, k0, T, wu, l);
+    stage_hb<BN>(V + base, (B ? sR1 : sR0) + BN * HD, k0, T, wu, l);
     if constexpr (FOX) {
       if (tid < BN) rcs = CS[bh * T + min(k0 + tid, T - 1)];  // converted by publish()
     }
@@ -704,13 +703,13 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
   const int grp = l >> 4, i16 = l & 15;
   const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
   const int kr = 4 * (grp >> 1) + (i16 >> 2);
-  const int krow[2] = {cm_row_base<BN>(li, g, 0), cm_row_base<BN>(li, g, 1)};
-  const int ktr[2] = {cm_tr_base<BN>(kr, d0, 0), cm_tr_base<BN>(kr, d0, 1)};
+  const int krow[2] = {hb_row_base(li, g, 0), hb_row_base(li, g, 1)};
+  const int ktr[2] = {hb_tr_base(kr, d0, 0), hb_tr_base(kr, d0, 1)};
   auto tile = [&](auto bt, int kt, auto masked) {
     constexpr int B = decltype(bt)::value;
     constexpr bool MASK = decltype(masked)::value;
-    const bf16* sK = B ? sK1 : sK0;
-    const bf16* sV = B ? sV1 : sV0;
+    const bf16* sK = B ? sR1 : sR0;
+    const bf16* sV = sK + BN * HD;
     const float* sCS = B ? sCS1 : sCS0;
     const int k0 = kt * BN;
 #pragma unroll
@@ -719,7 +718,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
       f32x16 s = zero16(), dp = zero16();
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) {
-        const int off = krow[kk & 1] + (2 * kk * BN + 32 * h2) * 8;
+        const int off = krow[kk & 1] + hb_row_off<BN>(kk, 32 * h2);
         s = mfma32(*(const bf16x8*)(&sK[off]), qf[kk], s);
         dp = mfma32(*(const bf16x8*)(&sV[off]), of[kk], dp);
       }
@@ -750,7 +749,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
-          const int o = (4 * dt * BN + 32 * h2 + 16 * kc) * 8;
+          const int o = hb_tr_off<BN>(dt, kc, 32 * h2);
           const bf16x8 a = cat4(lds_read_tr16(&sK[ktr[0] + o]), lds_read_tr16(&sK[ktr[1] + o]));
           dqt[dt] = mfma32(a, db[kc], dqt[dt]);
         }
