@@ -392,16 +392,22 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
     pf[kc][it + 1] = pp[1];
   };
   // O^T += V^T P^T with V from buffer B (transposed reads in the P^T key order)
+  // (step j: keys 16 (j / 4) .. of dims 32 (j % 4) ..; consecutive MFMAs go to different
+  // accumulators, and the transposed V fragments are read three steps ahead)
   auto pv_mma = [&](auto bt, const bf16x8* pf) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
     const bf16* sv = (B ? sX0 : sX1) + BN * HD;
+    auto vfrag = [&](int j) __attribute__((always_inline)) {
+      const int o16 = hb_tr_off<BN>(j & 3, j >> 2, 0);
+      return cat4(lds_read_tr16(&sv[vtr[0] + o16]), lds_read_tr16(&sv[vtr[1] + o16]));
+    };
+    bf16x8 a[3] = {vfrag(0), vfrag(1), vfrag(2)};
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const int o16 = hb_tr_off<BN>(dt, kc, 0);
-        o[dt] = mfma32(cat4(lds_read_tr16(&sv[vtr[0] + o16]), lds_read_tr16(&sv[vtr[1] + o16])), pf[kc], o[dt]);
-      }
+    for (int j = 0; j < 16; ++j) {
+      o[j & 3] = mfma32(a[j % 3], pf[j >> 2], o[j & 3]);
+      if (j + 3 < 16) a[j % 3] = vfrag(j + 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   // Generic tile: softmax of s, then O with V buffer B.
   auto consume = [&](auto bt, f32x16* s, int t, auto masked) __attribute__((always_inline)) {
@@ -414,7 +420,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
     pv_mma(bt, pf);
   };
   // Unmasked tile t with a visible successor: the 16 MFMAs of S(t + 1) (K buffer 1 - B, its
-  // fragments read two steps ahead) alternate with the exponentials of S(t), two per MFMA,
+  // fragments read four steps ahead) alternate with the exponentials of S(t), two per MFMA,
   // pinned by scheduling barriers so the matrix core and the VALU work at the same time.
   auto fused = [&](auto bt, int t) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
@@ -424,7 +430,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
       const int kk = i >> 1, h2 = i & 1;
       return *(const bf16x8*)(&sk[krow[kk & 1] + hb_row_off<BN>(kk, 32 * h2)]);
     };
-    bf16x8 fr[2] = {kfrag(0), kfrag(1)};
+    bf16x8 fr[4] = {kfrag(0), kfrag(1), kfrag(2), kfrag(3)};
     sn[0] = zero16();
     sn[1] = zero16();
     float rs = 0.0f;
@@ -432,8 +438,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      sn[i & 1] = mfma32(fr[i & 1], qf[i >> 1], sn[i & 1]);
-      if (i + 2 < 16) fr[i & 1] = kfrag(i + 2);
+      sn[i & 1] = mfma32(fr[i & 3], qf[i >> 1], sn[i & 1]);
+      if (i + 4 < 16) fr[i & 3] = kfrag(i + 4);
       softmax_pair(sc, i, mns, rs, pf, std::true_type{});
       __builtin_amdgcn_sched_barrier(0);
     }
