@@ -894,15 +894,16 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   }
   __syncthreads();
 
-  if (tid < CH) {
-    float acc = 0.0f;
-    for (int s = 0; s < CH; ++s) acc += sZp[tid * ZS + s] + sZa[tid * ZS + s] - sZp[s * ZS + tid] - sZa[s * ZS + tid];
-    atomicAdd(&dlg[tid], acc);
-  } else if (tid < 2 * CH) {
-    const int t = tid - CH;
-    float acc = 0.0f;
-    for (int s = 0; s < CH; ++s) acc += sB[t * ZS + s];
-    atomicAdd(&dbt[t], acc);
+  {  // row t = tid % 64 over the 8 columns s of part tid / 64 (all 512 threads)
+    const int t = tid & (CH - 1), s0 = 8 * (tid >> 6);
+    float a = 0.0f, bb = 0.0f;
+#pragma unroll
+    for (int s = s0; s < s0 + 8; ++s) {
+      a += sZp[t * ZS + s] + sZa[t * ZS + s] - sZp[s * ZS + t] - sZa[s * ZS + t];
+      bb += sB[t * ZS + s];
+    }
+    atomicAdd(&dlg[t], a);
+    atomicAdd(&dbt[t], bb);
   }
 
   // dQ^T and dK^T: rows d_k = 32 wd + .., columns t (or s) = 32 wt + li
@@ -910,12 +911,14 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   f32x16 XdK;
   {
     const int J2 = wt, t = 32 * J2 + li;
+    // rows d_k = 32 wd + li of h, the A operand of the dQ and dK products
+    bf16x8 hf[DK / 16];
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) hf[kk] = *(const bf16x8*)(hN + (long)(32 * wd + li) * DK + 16 * kk + 8 * g);
     // dQ^T = gamma (h dO^T) + K^T dS^T
     f32x16 X = zero16();
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk)
-      X = mfma32(*(const bf16x8*)(hN + (long)(32 * wd + li) * DK + 16 * kk + 8 * g),
-                 ld_row8(p.dout, p, b, h, t0 + t, 16 * kk + 8 * g), X);
+    for (int kk = 0; kk < DK / 16; ++kk) X = mfma32(hf[kk], ld_row8(p.dout, p, b, h, t0 + t, 16 * kk + 8 * g), X);
     const float gmt = __expf(lg[t]);
     float qx = 0.0f;
 #pragma unroll
@@ -935,12 +938,14 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
 
     // dK^T = (gamma_C / gamma) dh v^T - (beta gamma) h dR^T + Q^T dS + K^T dF
     f32x16 X1 = zero16(), X2 = zero16(), X3 = zero16();
+    float hdh = 0.0f;  // <dh, h> over this lane's fragments (waves with wt = 0 cover the matrix once)
 #pragma unroll
     for (int kk = 0; kk < DK / 16; ++kk) {
-      X1 = mfma32(*(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * wd + li) * DK + 16 * kk + 8 * g),
-                  *(const bf16x8*)(vN + (long)t * DK + 16 * kk + 8 * g), X1);
-      X2 = mfma32(*(const bf16x8*)(hN + (long)(32 * wd + li) * DK + 16 * kk + 8 * g),
-                  *(const bf16x8*)(sdR + t * KS + 16 * kk + 8 * g), X2);
+      const bf16x8 df = *(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * wd + li) * DK + 16 * kk + 8 * g);
+      X1 = mfma32(df, *(const bf16x8*)(vN + (long)t * DK + 16 * kk + 8 * g), X1);
+      X2 = mfma32(hf[kk], *(const bf16x8*)(sdR + t * KS + 16 * kk + 8 * g), X2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hdh = fmaf((float)df[e], (float)hf[kk][e], hdh);
     }
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -970,18 +975,8 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
       dlgC = sc1 * k1;
     }
     XdK = X3;
-  }
-  // gamma_C <dh, h> and the Kd terms enter the decay of the last step
-  {
-    const bf16* dm = p.dmN + ci * DK * DK;
-    float acc = 0.0f;
-    for (int e = tid; e < DK * DK / 8; e += 512) {
-      const bf16x8 x = *(const bf16x8*)(dm + 8 * e);
-      const bf16x8 y = *(const bf16x8*)(hN + 8 * e);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc = fmaf((float)x[i], (float)y[i], acc);
-    }
-    acc = acc * __expf(lgC) + dlgC;
+    // gamma_C <dh, h> and the Kd terms enter the decay of the last step
+    float acc = (wt == 0 ? hdh : 0.0f) * __expf(lgC) + dlgC;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
     if (l == 0) atomicAdd(&dlg[CH - 1], acc);
