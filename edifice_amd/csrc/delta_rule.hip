@@ -1,6 +1,7 @@
 // C-ABI entry points of the delta rule (DeltaNet / GatedDeltaNet), forward and backward.
 // Dispatch: the chunked MFMA kernels (delta_rule_chunk.hip) take bf16, per-head beta,
-// head_dim 128, seq >= 64 (forward and backward); the exact per-step kernels
+// head_dim 64 .. 128 (a multiple of 8; zero-padded to 128 inside), seq >= 64 (forward and
+// backward); the exact per-step kernels
 // (delta_rule_seq.hip) serve every other case.
 #include "edf_abi.hpp"
 

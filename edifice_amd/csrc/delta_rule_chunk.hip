@@ -1,5 +1,5 @@
-// Chunked (WY / UT-transform) gated delta rule on bf16 MFMA, per-head beta, head_dim 128:
-// forward and backward.
+// Chunked (WY / UT-transform) gated delta rule on bf16 MFMA, per-head beta, head_dim 128
+// (64 .. 128 in steps of 8, zero-padded to 128): forward and backward.
 //
 // Same recurrence as the step path (delta_rule_seq.hip; reference
 // lib/edifice/recurrent/gated_delta_net.ex:300-353 with beta broadcast along the value
@@ -62,15 +62,21 @@ struct CkArgs {
   bf16* dmN;  // [ci][DK][DK]   dL/d(state leaving the chunk), [d_k][d_v]
   bf16* dvT;  // [ci][DK][CH]   (dL/dv_new)^T
   int H, T, nch;
+  int D;  // head_dim of the [B,T,H,D] tensors, a multiple of 8 up to DK
 };
 
-EDF_DEVICE long row_off(const CkArgs& p, int b, int h, int t) { return (((long)b * p.T + t) * p.H + h) * DK; }
+// A head_dim D < DK is zero-padded to DK inside the kernels: the [B,T,H,D] tensors are read
+// through ld_row8 (zeros at columns >= D) and written only at columns < D.  Zero columns of
+// q, k and v stay zero through K K^T, T, W, U, the state and the outputs, so the first D
+// columns are the D-dimensional recurrence itself (at the cost of DK-wide tiles).
+EDF_DEVICE long row_off(const CkArgs& p, int b, int h, int t) { return (((long)b * p.T + t) * p.H + h) * p.D; }
 EDF_DEVICE long head_off(const CkArgs& p, int b, int h, int t) { return ((long)b * p.T + t) * p.H + h; }
 
-// 8 bf16 of row t (zeros beyond the sequence); the load itself is always in bounds.
+// 8 bf16 of row t, columns col .. col + 7 (zeros beyond the sequence or the head dim,
+// col a multiple of 8); the load itself is always in bounds.
 EDF_DEVICE bf16x8 ld_row8(const bf16* base, const CkArgs& p, int b, int h, int t, int col) {
-  const bool ok = t < p.T;
-  const bf16x8 v = *(const bf16x8*)(base + row_off(p, b, h, ok ? t : p.T - 1) + col);
+  const bool ok = t < p.T && col < p.D;
+  const bf16x8 v = *(const bf16x8*)(base + row_off(p, b, h, t < p.T ? t : p.T - 1) + (col < p.D ? col : 0));
   return ok ? v : bf16x8{};
 }
 
@@ -541,7 +547,8 @@ __global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
       for (int i = 0; i < 2; ++i) {
         const int e = l + 64 * i, row = e >> 2, ch = e & 3;  // 32 rows x 64 bytes
         const int t = c * CH + 32 * J + row;
-        if (t < p.T) *(bf16x8*)(p.out + row_off(p, b, h, t) + v0 + 8 * ch) = *(const bf16x8*)(so + row * NS + 8 * ch);
+        if (t < p.T && v0 + 8 * ch < p.D)
+          *(bf16x8*)(p.out + row_off(p, b, h, t) + v0 + 8 * ch) = *(const bf16x8*)(so + row * NS + 8 * ch);
       }
       __builtin_amdgcn_wave_barrier();
     }
@@ -661,7 +668,8 @@ __global__ __launch_bounds__(256) void dr_ck_out_kernel(const CkArgs p) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = tid + 256 * i, row = e >> 4, ch = e & 15;
-    if (t0 + row < p.T) *(bf16x8*)(p.out + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(sO + row * KS + 8 * ch);
+    if (t0 + row < p.T && 8 * ch < p.D)
+      *(bf16x8*)(p.out + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(sO + row * KS + 8 * ch);
   }
 }
 
@@ -784,7 +792,8 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int e = tid + 512 * i, row = e >> 4, ch = e & 15;
-      if (t0 + row < p.T) *(bf16x8*)(dst + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(src + row * KS + 8 * ch);
+      if (t0 + row < p.T && 8 * ch < p.D)
+        *(bf16x8*)(dst + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(src + row * KS + 8 * ch);
     }
   };
 
@@ -813,12 +822,13 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
     store_rows(sdR + (32 * J) * KS + 32 * wd, KS, X, li, g);
     // dV = beta dR;  dbeta += <dR_s, V_s>
     const bool ok = t0 + s < p.T;
-    const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1) + 32 * wd + 4 * g;
+    const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1);
     store_rows(sO + (32 * J) * KS + 32 * wd, KS, X, li, g, bt[s]);
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const bf16x4 vv = *(const bf16x4*)(p.v + ro + 8 * q);
+      const int col = 32 * wd + 8 * q + 4 * g;
+      const bf16x4 vv = col < p.D ? *(const bf16x4*)(p.v + ro + col) : bf16x4{};
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc = fmaf(X[4 * q + e], (float)vv[e], acc);
     }
@@ -1060,7 +1070,7 @@ Layout layout(int batch, int seq, int heads, LayoutKind kind) {
 }
 
 // pointers into the context workspace (forward regions) and the reverse-pass workspace
-CkArgs make_args(const Layout& Lc, void* ctx_ws, const Layout& Lr, void* rev_ws, int seq, int heads) {
+CkArgs make_args(const Layout& Lc, void* ctx_ws, const Layout& Lr, void* rev_ws, int seq, int heads, int d) {
   CkArgs a{};
   char* wc = (char*)ctx_ws;
   char* wr = (char*)rev_ws;
@@ -1082,14 +1092,18 @@ CkArgs make_args(const Layout& Lc, void* ctx_ws, const Layout& Lr, void* rev_ws,
   a.H = heads;
   a.T = seq;
   a.nch = (seq + CH - 1) / CH;
+  a.D = d;
   return a;
 }
 
 }  // namespace
 
 bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head) {
-  // seq bound: the scan addresses one head's per-chunk tiles with 32-bit byte offsets
-  return dtype == EDF_BF16 && beta_per_head && d == DK && seq >= CH && seq <= (1 << 21);
+  // seq bound: the scan addresses one head's per-chunk tiles with 32-bit byte offsets.
+  // head_dim 64 .. 128 (a multiple of 8) runs zero-padded to 128; below 64 the padding
+  // would cost more than the exact per-step kernels.
+  return dtype == EDF_BF16 && beta_per_head && d >= 64 && d <= DK && d % 8 == 0 && seq >= CH &&
+         seq <= (1 << 21);
 }
 
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d) {
@@ -1111,9 +1125,8 @@ size_t dr_chunk_saved_backward_workspace_bytes(int batch, int seq, int heads, in
 // output; the workspace keeps the context for dr_chunk_saved_backward_run
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
                  void* out, void* workspace, int batch, int seq, int heads, int d) {
-  (void)d;
   const Layout L = layout(batch, seq, heads, FWD);
-  CkArgs a = make_args(L, workspace, L, nullptr, seq, heads);
+  CkArgs a = make_args(L, workspace, L, nullptr, seq, heads, d);
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha; a.out = (bf16*)out;
   const unsigned bh = (unsigned)batch * heads;
@@ -1147,9 +1160,8 @@ int reverse_pass(hipStream_t s, CkArgs& a, unsigned bh, const void* grad_out, vo
 int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
                           const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
                           void* dalpha, void* workspace, int batch, int seq, int heads, int d) {
-  (void)d;
   const Layout L = layout(batch, seq, heads, ALL);
-  CkArgs a = make_args(L, workspace, L, workspace, seq, heads);
+  CkArgs a = make_args(L, workspace, L, workspace, seq, heads, d);
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha;
   const unsigned bh = (unsigned)batch * heads;
@@ -1170,7 +1182,7 @@ int dr_chunk_saved_backward_run(void* stream, const void* q, const void* k, cons
                                 int heads, int d) {
   (void)d;
   const Layout Lc = layout(batch, seq, heads, FWD), Lr = layout(batch, seq, heads, BWD);
-  CkArgs a = make_args(Lc, const_cast<void*>(fwd_workspace), Lr, workspace, seq, heads);
+  CkArgs a = make_args(Lc, const_cast<void*>(fwd_workspace), Lr, workspace, seq, heads, d);
   a.q = (const bf16*)q; a.k = (const bf16*)k; a.v = (const bf16*)v;
   a.beta = (const bf16*)beta; a.alpha = (const bf16*)alpha;
   return reverse_pass(as_stream(stream), a, (unsigned)batch * heads, grad_out, dq, dk, dv, dbeta, dalpha);

@@ -382,7 +382,8 @@ int edf_fused_laser_attention_backward(void* stream, const void* q, const void* 
  *     S_g = alpha_t S;  S = S_g + diag(beta_t)(v_t - S_g k_t) k_t^T;  o_t = S q_t
  *   beta: [B, T, H, d] (EDF_BETA_PER_ELEMENT, the reference's layout) or [B, T, H]
  *   (EDF_BETA_PER_HEAD); alpha: [B, T, H] (gated only).  head_dim <= 128.
- *   bf16 + per-head beta + head_dim 128 + seq_len >= 64 runs the chunked MFMA kernels,
+ *   bf16 + per-head beta + head_dim 64..128 (a multiple of 8; zero-padded to 128 inside the
+ *   kernels) + seq_len >= 64 runs the chunked MFMA kernels,
  *   forward and backward, and then requires the workspace the *_workspace_bytes queries
  *   return (EDF_ERR_WORKSPACE when it is missing or short; the forward query returns 0
  *   for every other case); everything else runs the exact per-step kernels.

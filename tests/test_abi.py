@@ -95,6 +95,12 @@ def test_workspace_queries(lib):
     assert lib.edf_flash_attention_backward_workspace_bytes(4, 32, 4096, 128) == 4 * 32 * 4096 * 4
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 1, 1) > 0  # chunked path
     assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, 128, 0, 1) == 0  # f32: step path
+    # head_dim 64 .. 128 in steps of 8 takes the chunked path (padded to 128, same workspace)
+    for d in (64, 96, 120):
+        assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, d, 1, 1) == lib.edf_delta_rule_workspace_bytes(
+            4, 4096, 16, 128, 1, 1)
+    for d in (32, 60, 100):  # below 64 or not a multiple of 8: step path
+        assert lib.edf_delta_rule_workspace_bytes(4, 4096, 16, d, 1, 1) == 0
 
 
 def test_variant_entry_points_validate_before_launch(lib):
@@ -158,7 +164,7 @@ def test_wrappers_reject_mismatched_shapes_before_launch(call, msg):
 
 @pytest.mark.parametrize("gated", [False, True])
 def test_chunked_delta_rule_forward_requires_workspace(lib, gated):
-    """bf16 + per-head beta + head_dim 128 + seq >= 64 selects the chunked kernels: the
+    """bf16 + per-head beta + head_dim 64..128 + seq >= 64 selects the chunked kernels: the
     forward, like the backward, returns EDF_ERR_WORKSPACE (4) for a missing or short
     workspace instead of silently running the per-step kernels.  The check precedes any
     device call, so dummy host addresses are never dereferenced."""

@@ -35,6 +35,10 @@ CASES = [
     (1, 200, 2, 128, torch.bfloat16, True, True),    # partial last chunk
     (2, 130, 1, 128, torch.bfloat16, True, False),
     (1, 640, 2, 128, torch.bfloat16, True, True),    # ten chunks: state and gradient carried across
+    # head_dim 64 and 96 on the chunked path (zero-padded to 128 inside the kernels)
+    (1, 200, 2, 64, torch.bfloat16, True, True),
+    (2, 130, 1, 64, torch.bfloat16, True, False),
+    (1, 192, 2, 96, torch.bfloat16, True, True),
 ]
 
 
@@ -60,7 +64,7 @@ def test_delta_rule_fwd_bwd(case, rng):
 
 
 @pytest.mark.parametrize("case", [(1, 200, 2, 128, torch.bfloat16, True), (2, 130, 1, 128, torch.bfloat16, False),
-                                  (1, 40, 2, 32, torch.float32, True)],
+                                  (1, 200, 2, 64, torch.bfloat16, True), (1, 40, 2, 32, torch.float32, True)],
                          ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
 def test_delta_rule_backward_entry_points_agree(case, rng):
     """The reference-shaped backward entry points (which recompute the forward context) and
