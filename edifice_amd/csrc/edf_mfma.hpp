@@ -127,11 +127,12 @@ EDF_DEVICE void dma16(const void* src, void* lds) {
 // bases plus an immediate (the row-major XOR swizzle needs an address register per
 // fragment, a column-major tile makes each DMA load touch 64 lines).
 //
-// Rows r0 .. r0 + R - 1 of a row-major [T][128] bf16 head (rows past T - 1 repeat row
-// T - 1) into such a tile: the workgroup's 4 waves issue R / 16 loads each, load j
-// filling block j.
+// Rows r0 .. r0 + R - 1 of a row-major [T][128] bf16 head into such a tile, through the
+// buffer resource r of the head (T * 256 bytes): rows past the end read as zeros.  The
+// workgroup's 4 waves issue R / 16 loads each, load j filling block j; a lane's byte offset
+// within the tile is loop-invariant and the tile's row offset is a scalar.
 template <int R>
-EDF_DEVICE void stage_hb(const bf16* src, bf16* dst, int r0, int T, int wu, int l) {
+EDF_DEVICE void stage_hb(rsrc_t r, bf16* dst, int r0, int wu, int l) {
   constexpr int IPW = R / 16;  // loads per wave
   static_assert(R % 16 == 0, "whole 8-row blocks for 4 waves");
 #pragma unroll
@@ -140,8 +141,8 @@ EDF_DEVICE void stage_hb(const bf16* src, bf16* dst, int r0, int T, int wu, int 
     const int half = j / (R / 8), b8 = j % (R / 8);
     const int cp = (l >> 3) ^ (b8 & 1);
     const int rp = (l & 7) ^ (4 * ((cp >> 1) & 1));
-    const long gr = min(r0 + 8 * b8 + rp, T - 1);
-    dma16(src + gr * 128 + (8 * half + cp) * 8, dst + 512 * j);
+    const unsigned off = (unsigned)(((8 * b8 + rp) * 128 + (8 * half + cp) * 8) * 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 512 * j), 16, off, r0 * 256, 0, 0);
   }
 }
 

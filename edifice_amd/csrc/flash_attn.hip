@@ -276,6 +276,8 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
   const int qw = q0 + 32 * w;
   const int myq = qw + li;
   const long base = bh * T * HD;
+  // per-head buffer resources: DMA rows past the end read as zeros (their scores are masked)
+  const rsrc_t rK = make_rsrc(K + base, (unsigned)T * HD * 2), rV = make_rsrc(V + base, (unsigned)T * HD * 2);
 
   bf16x8 qf[NKK];
 #pragma unroll
@@ -302,14 +304,14 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
 
   auto issue_k = [&](auto bt, int t) __attribute__((always_inline)) {  // K tile t (and its cs) into K buffer B
     constexpr int B = decltype(bt)::value;
-    stage_hb<BN>(K + base, B ? sX1 : sX0, t * BN, T, wu, l);
+    stage_hb<BN>(rK, B ? sX1 : sX0, t * BN, wu, l);
     if constexpr (FOX) {
       if (tid < BN) rcs = CS[bh * T + min(t * BN + tid, T - 1)];  // converted by publish_k()
     }
   };
   auto issue_v = [&](auto bt, int t) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;
-    stage_hb<BN>(V + base, (B ? sX0 : sX1) + BN * HD, t * BN, T, wu, l);
+    stage_hb<BN>(rV, (B ? sX0 : sX1) + BN * HD, t * BN, wu, l);
   };
   auto publish_k = [&](auto bt) __attribute__((always_inline)) {
     constexpr int B = decltype(bt)::value;

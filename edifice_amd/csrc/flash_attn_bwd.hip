@@ -461,8 +461,10 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
   const int mykey = kw + li;
   const long base = bh * T * HD;
 
-  // keys past the end read row T - 1 of V: they only feed their own dK, dV columns, never stored
-  stage_hb<BKEY>(V + base, sV, kb0, T, wu, l);
+  // per-head buffer resources: DMA rows past the end read as zeros
+  const rsrc_t rQ = make_rsrc(Q + base, (unsigned)T * HD * 2), rdO = make_rsrc(dO + base, (unsigned)T * HD * 2);
+  // keys past the end read zero rows of V: they only feed their own dK, dV columns, never stored
+  stage_hb<BKEY>(make_rsrc(V + base, (unsigned)T * HD * 2), sV, kb0, wu, l);
   bf16x8 kf[NKK];
 #pragma unroll
   for (int kk = 0; kk < NKK; ++kk)
@@ -484,8 +486,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
   // wait for the DMA loads issued before them.
   auto issue = [&](auto bt, int q0) {
     constexpr int B = decltype(bt)::value;
-    stage_hb<BQ>(Q + base, B ? sR1 : sR0, q0, T, wu, l);
-    stage_hb<BQ>(dO + base, (B ? sR1 : sR0) + BQ * HD, q0, T, wu, l);
+    stage_hb<BQ>(rQ, B ? sR1 : sR0, q0, wu, l);
+    stage_hb<BQ>(rdO, (B ? sR1 : sR0) + BQ * HD, q0, wu, l);
     if (tid < BQ) {
       const long q = min(q0 + tid, T - 1);
       rl = LSE[bh * T + q];
@@ -656,6 +658,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
   const int qw = q0 + 32 * w;
   const int myq = qw + li;
   const long base = bh * T * HD;
+  const rsrc_t rK = make_rsrc(K + base, (unsigned)T * HD * 2), rV = make_rsrc(V + base, (unsigned)T * HD * 2);
 
   bf16x8 qf[NKK], of[NKK];
 #pragma unroll
@@ -686,8 +689,8 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dq128_kernel(const bf16* __rest
 
   auto issue = [&](auto bt, int k0) {
     constexpr int B = decltype(bt)::value;
-    stage_hb<BN>(K + base, B ? sR1 : sR0, k0, T, wu, l);
-    stage_hb<BN>(V + base, (B ? sR1 : sR0) + BN * HD, k0, T, wu, l);
+    stage_hb<BN>(rK, B ? sR1 : sR0, k0, wu, l);
+    stage_hb<BN>(rV, (B ? sR1 : sR0) + BN * HD, k0, wu, l);
     if constexpr (FOX) {
       if (tid < BN) rcs = CS[bh * T + min(k0 + tid, T - 1)];  // converted by publish()
     }
@@ -943,8 +946,10 @@ void launch_mfma_bwd128(hipStream_t s, const bf16* Q, const bf16* K, const bf16*
   } else {
     fa_bwd_dq128_kernel<false, false, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, nullptr, dq, T, scale_log2, scale,
                                                                nullptr, nullptr, nullptr, 0.0f, O, Dd);
-    fa_bwd_dkdv128_kernel<false, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale,
-                                                           nullptr, nullptr, 0.0f);
+    // non-causal dK/dV: the one-wave-per-SIMD kernel (the two-workgroup variant's register
+    // allocation spills its K fragments when compiled without the causal branches)
+    fa_bwd_dkdv_kernel<128, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, nullptr,
+                                                      nullptr, 0.0f);
   }
 }
 
