@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from oracle import scans
-from tests.conftest import assert_close, rel_err
+from tests.conftest import assert_close
 from tests.gpu_util import TOL, announce, host, rounded, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -71,8 +71,9 @@ def test_delta_rule_backward_entry_points_agree(case, rng):
     edf_fused_delta_rule_scan_backward_saved (which reads the forward's workspace) give the
     same gradients: chunked path (gated and not) and the per-step path.  The chunked
     gradient kernel adds the dbeta and decay terms of a chunk with LDS atomics, whose order
-    varies between calls, so the agreement is to 1e-6 of each gradient's largest entry,
-    not bit for bit."""
+    varies between calls, so the agreement is not bit for bit: per element within 1e-6 of
+    the gradient's largest entry plus, for bf16 outputs, one bf16 unit of the element (a
+    float32 sum in a different order can round to the neighbouring bf16 value)."""
     import ctypes
 
     from edifice_amd import _native as nat
@@ -112,9 +113,11 @@ def test_delta_rule_backward_entry_points_agree(case, rng):
                      *(P(x) for x in g[:4]), P(ws), wsr, B, T, H, d, dt, 1)
         torch.cuda.synchronize()
         grads.append([None if x is None else host(x) for x in g])
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 0.0
     for a, b_ in zip(*grads):
         if a is not None:
-            assert rel_err(a, b_) <= 1e-6
+            bound = 1e-6 * np.abs(b_).max() + ulp * np.abs(b_)
+            assert np.all(np.abs(a - b_) <= bound), f"max excess {np.max(np.abs(a - b_) - bound):.3e}"
     # and the saved path against the oracle
     qr, kr, vr, br, dor = (rounded(a, dtype) for a in (q, k, v, beta, do))
     ar = rounded(alpha, dtype) if gated else None
