@@ -757,28 +757,54 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// grad: dQ, dK, dV, dbeta, dalpha of one chunk.  Eight waves: wave w works on the
-// 32-wide d tile (w & 3) and the 32-step tile (w >> 2) of each product.
+// grad: dQ, dK, dV, dbeta, dalpha of one chunk.  Four waves, two workgroups per CU: the
+// phases are short and separated by barriers and global loads, so while one workgroup
+// waits the other computes (one 8-wave workgroup per CU spent most of its time waiting).
+// Wave w owns the 32-wide d tile w of the [d][t] products (dR^T, dQ^T, dK^T) over both
+// 32-step tiles, and one or two of the six 32x32 (t, s) tiles of S | dP and G | dA.
+// LDS (67 KB): Q, K and dR as unpadded swizzled rows (lds_off); the transposed operands
+// K^T, Q^T and dS^T come from transposed reads (lds_read_tr16) of those rows and of the
+// dS tile; the row and column sums behind dlog-gamma and dbeta are formed in registers;
+// dV, dQ and dK are staged over tiles that are dead by then.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
-  constexpr int ZS = CH + 1;
-  __shared__ __attribute__((aligned(16))) bf16 sQt[DK * TS];  // Q^T [d_k][t]
-  __shared__ __attribute__((aligned(16))) bf16 sKt[DK * TS];  // K^T [d_k][s]
-  __shared__ __attribute__((aligned(16))) bf16 sdR[CH * KS];  // dR [s][d_v]
-  __shared__ __attribute__((aligned(16))) bf16 sdS[CH * TS];  // dS [t][s]
-  __shared__ __attribute__((aligned(16))) bf16 sdSt[CH * TS];  // dS^T [s][t]
-  __shared__ __attribute__((aligned(16))) bf16 sdF[CH * TS];  // dG + dG^T
-  __shared__ __attribute__((aligned(16))) float sZ[3 * CH * ZS];
-  float* sZp = sZ;               // dP o P
-  float* sZa = sZ + CH * ZS;     // dA o A
-  float* sB = sZ + 2 * CH * ZS;  // dA o Gamma o (K K^T), s < t
+
+// Sum over the 32 lanes of each half-wave of an accumulator tile's rows: afterwards lane li
+// holds the sum of register r = li / 2 (a reduce-scatter: each exchange halves the number
+// of registers still to be summed).
+EDF_DEVICE float rowsum32(const f32x16& x, int li) {
+  float a[8], b[4], c[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bool hi = li & 16;
+    a[j] = (hi ? x[j + 8] : x[j]) + __shfl_xor(hi ? x[j] : x[j + 8], 16);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool hi = li & 8;
+    b[j] = (hi ? a[j + 4] : a[j]) + __shfl_xor(hi ? a[j] : a[j + 4], 8);
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const bool hi = li & 4;
+    c[j] = (hi ? b[j + 2] : b[j]) + __shfl_xor(hi ? b[j] : b[j + 2], 4);
+  }
+  const bool hi = li & 2;
+  float d = (hi ? c[1] : c[0]) + __shfl_xor(hi ? c[0] : c[1], 2);
+  return d + __shfl_xor(d, 1);
+}
+
+__global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
+  __shared__ __attribute__((aligned(16))) bf16 sQ[CH * DK];         // Q [t][d_k]  (lds_off rows)
+  __shared__ __attribute__((aligned(16))) bf16 sK[CH * DK];         // K [s][d_k]
+  __shared__ __attribute__((aligned(16))) bf16 sdR[CH * DK];        // dR [s][d_v]
+  __shared__ __attribute__((aligned(16))) bf16 sdSF[2 * CH * TS];   // dS [t][s], dF = dG + dG^T [t][s]
   __shared__ float lg[CH], bt[CH], dlg[CH], dbt[CH];
-  // dV, then dQ, staged as [t][d] rows (dK goes over sZ once that is consumed)
-  __shared__ __attribute__((aligned(16))) bf16 sO[CH * KS];
+  bf16* sdS = sdSF;
+  bf16* sdF = sdSF + CH * TS;
+  bf16* sV = sdSF;  // dV [s][d_v] (lds_off rows), staged before dS and dF are formed
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
-  const int wd = w & 3, wt = w >> 2;
   const int c = blockIdx.x;
   const long bh = blockIdx.y;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -786,218 +812,295 @@ __global__ __launch_bounds__(512) void dr_ck_grad_kernel(const CkArgs p) {
   const long ci = bh * p.nch + c;
   const bf16* hN = p.hN + ci * DK * DK;
   const bf16* vN = p.vN + ci * CH * DK;
-  // a staged [t][d] tile of the chunk, written as whole 256-byte rows of a [B,T,H,D] tensor
-  // (stores straight from the accumulator layout scatter each instruction over 32 rows)
+  // transposed reads: lane i of each 16-lane group reads row r0 + kr, columns c0 + d0 .. + 3
+  // and receives column c0 + li of rows r0 + 4 g .. + 3 (twice, at r0 and r0 + 8, gives the
+  // 16-step operand in the order 4 g .. 4 g + 3, 8 + 4 g .. 8 + 4 g + 3)
+  const int grp = l >> 4, i16 = l & 15;
+  const int d0 = 16 * (grp & 1) + 4 * (i16 & 3);
+  const int kr = 4 * (grp >> 1) + (i16 >> 2);
+  auto tr_frag = [&](const bf16* tile, int r0, int c0) {
+    return cat4(lds_read_tr16(tile + lds_off<DK>(r0 + kr, c0 + d0)), lds_read_tr16(tile + lds_off<DK>(r0 + kr + 8, c0 + d0)));
+  };
+  auto tr_frag_ts = [&](const bf16* tile, int r0, int c0) {  // [*][TS] tiles
+    return cat4(lds_read_tr16(tile + (r0 + kr) * TS + c0 + d0), lds_read_tr16(tile + (r0 + kr + 8) * TS + c0 + d0));
+  };
+  // row t of a [*][TS] tile in the transposed-read order (B operand beside tr_frag)
+  auto row_frag_ts = [&](const bf16* tile, int t, int kk) {
+    const bf16* r = tile + t * TS + 16 * kk + 4 * g;
+    return cat4(*(const bf16x4*)r, *(const bf16x4*)(r + 8));
+  };
+  // staged [t][d] tile -> whole 256-byte rows of a [B,T,H,D] tensor
   auto copy_rows = [&](bf16* dst, const bf16* src) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + 512 * i, row = e >> 4, ch = e & 15;
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + 256 * i, row = e >> 4, ch = e & 15;
       if (t0 + row < p.T && 8 * ch < p.D)
-        *(bf16x8*)(dst + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(src + row * KS + 8 * ch);
+        *(bf16x8*)(dst + row_off(p, b, h, t0 + row) + 8 * ch) = *(const bf16x8*)(src + lds_off<DK>(row, 8 * ch));
+    }
+  };
+  // accumulator tile (rows d = 32 w + d_row(r, g), column j0 + li) -> row j0 + li of dst
+  auto put_rows = [&](bf16* dst, int j0, const f32x16& x, float scale) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (bf16)(x[4 * q + e] * scale);
+      *(bf16x4*)(dst + lds_off<DK>(j0 + li, 32 * w + 8 * q + 4 * g)) = v;
     }
   };
 
+  // ---- stage Q and K; the dR^T operands and V rows load meanwhile ----
+  const float lg0 = p.lg[ci * CH + (tid & (CH - 1))];
+  const bf16 bt0 = p.beta[head_off(p, b, h, min(t0 + (tid & (CH - 1)), p.T - 1))];
+  bf16x8 rq[4], rk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + 256 * i, row = e >> 4, col = (e & 15) * 8;
+    rq[i] = ld_row8(p.q, p, b, h, t0 + row, col);
+    rk[i] = ld_row8(p.k, p, b, h, t0 + row, col);
+  }
+  bf16x8 aD[4], aT[2][4];  // rows d_v = 32 w + li of dv_new^T; rows s of T^T (kk < 2 j multiply zeros of T)
+  bf16x4 vA[2][4];         // V rows s (dbeta), columns >= D masked at use
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) aD[kk] = *(const bf16x8*)(p.dvT + ci * DK * CH + (long)(32 * w + li) * CH + 16 * kk + 8 * g);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      aT[j][kk] = *(const bf16x8*)(p.Tt + ci * CH * CH + (long)(32 * j + li) * CH + 16 * kk + 8 * g);
+    const long ro = row_off(p, b, h, min(t0 + 32 * j + li, p.T - 1));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = 32 * w + 8 * q + 4 * g;
+      vA[j][q] = *(const bf16x4*)(p.v + ro + (col < p.D ? col : 0));
+    }
+  }
   if (tid < CH) {
-    const int t = t0 + tid;
-    lg[tid] = p.lg[ci * CH + tid];
-    bt[tid] = t < p.T ? to_f32(p.beta[head_off(p, b, h, t)]) : 0.0f;
+    lg[tid] = lg0;
+    bt[tid] = t0 + tid < p.T ? to_f32(bt0) : 0.0f;
     dlg[tid] = 0.0f;
     dbt[tid] = 0.0f;
   }
-  stage_t<512>(sQt, p.q, p, b, h, t0, nullptr);
-  stage_t<512>(sKt, p.k, p, b, h, t0, nullptr);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + 256 * i, row = e >> 4, col = (e & 15) * 8;
+    *(bf16x8*)(sQ + lds_off<DK>(row, col)) = rq[i];
+    *(bf16x8*)(sK + lds_off<DK>(row, col)) = rk[i];
+  }
   __syncthreads();
   const float lgC = lg[CH - 1];
 
-  // dR^T = dv_new^T T: rows d_v = 32 wd + .., columns s = 32 wt + li  (T[t][s] = 0 for t < s)
-  {
-    const int J = wt, s = 32 * J + li;
+  // ---- dR^T = dv_new^T T (rows d_v = 32 w + .., columns s): dR rows, dV = beta dR, dbeta ----
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int s = 32 * j + li;
     f32x16 X = zero16();
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      if (kk < 2 * J) continue;
-      X = mfma32(*(const bf16x8*)(p.dvT + ci * DK * CH + (long)(32 * wd + li) * CH + 16 * kk + 8 * g),
-                 *(const bf16x8*)(p.Tt + ci * CH * CH + (long)s * CH + 16 * kk + 8 * g), X);
+      if (kk < 2 * j) continue;
+      X = mfma32(aD[kk], aT[j][kk], X);
     }
-    store_rows(sdR + (32 * J) * KS + 32 * wd, KS, X, li, g);
-    // dV = beta dR;  dbeta += <dR_s, V_s>
-    const bool ok = t0 + s < p.T;
-    const long ro = row_off(p, b, h, ok ? t0 + s : p.T - 1);
-    store_rows(sO + (32 * J) * KS + 32 * wd, KS, X, li, g, bt[s]);
+    put_rows(sdR, 32 * j, X, 1.0f);
+    put_rows(sV, 32 * j, X, bt[s]);
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int col = 32 * wd + 8 * q + 4 * g;
-      const bf16x4 vv = col < p.D ? *(const bf16x4*)(p.v + ro + col) : bf16x4{};
+      const bool okc = 32 * w + 8 * q + 4 * g < p.D;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc = fmaf(X[4 * q + e], (float)vv[e], acc);
+      for (int e = 0; e < 4; ++e) acc = fmaf(X[4 * q + e], okc ? (float)vA[j][q][e] : 0.0f, acc);
     }
     acc += __shfl_xor(acc, 32);
-    if (g == 0) atomicAdd(&dbt[s], ok ? acc : 0.0f);
+    if (g == 0) atomicAdd(&dbt[s], t0 + s < p.T ? acc : 0.0f);
   }
+  __syncthreads();  // dR rows and the dV tile complete
+  copy_rows(p.dv, sV);
 
-  // waves 0-3: S = Q K^T, then dP = dO v^T;  waves 4-7: G = K K^T, then dA = -dR v^T;
-  // tile (I, J) = (wd / 2, wd % 2); tile (0, 1) lies above the diagonal
-  const int I = wd >> 1, J = wd & 1;
-  const bool sq = w < 4;
-  const bool live = wd != 1;
-  f32x16 SG = zero16();
-  if (live) {
+  // ---- the six (t, s) tiles: items 0-2 are S | dP, items 3-5 G | dA on tiles
+  // (0, 0), (1, 0), (1, 1); wave w takes items w and w + 4 ----
+  const int nit = w < 2 ? 2 : 1;
+  f32x16 SG[2], DD[2];
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk)
-      SG = mfma32(ld_row8(sq ? p.q : p.k, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g),
-                  ld_row8(p.k, p, b, h, t0 + 32 * J + li, 16 * kk + 8 * g), SG);
+  for (int u = 0; u < 2; ++u) {
+    if (u >= nit) break;
+    const int it = w + 4 * u, kind = it >= 3, tile = it % 3;
+    const int I = tile >= 1, J = tile == 2;
+    f32x16 A = zero16(), D = zero16();
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk) {
+      const bf16x8 vb = *(const bf16x8*)(vN + (long)(32 * J + li) * DK + 16 * kk + 8 * g);
+      const bf16x8 da = kind ? *(const bf16x8*)(sdR + lds_off<DK>(32 * I + li, 16 * kk + 8 * g))
+                             : ld_row8(p.dout, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g);
+      D = mfma32(da, vb, D);
+      A = mfma32(*(const bf16x8*)((kind ? sK : sQ) + lds_off<DK>(32 * I + li, 16 * kk + 8 * g)),
+                 *(const bf16x8*)(sK + lds_off<DK>(32 * J + li, 16 * kk + 8 * g)), A);
+    }
+    SG[u] = A;
+    DD[u] = D;
   }
-  __syncthreads();  // sdR and the dV tile complete
-  copy_rows(p.dv, sO);
-
-  {
+  __syncthreads();  // dV copied out: dS and dF go over it
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    if (u >= nit) break;
+    const int it = w + 4 * u, kind = it >= 3, tile = it % 3;
+    const int I = tile >= 1, J = tile == 2;
     const int s = 32 * J + li;
-    f32x16 dS = zero16();
-    if (live) {
-      f32x16 D = zero16();
-#pragma unroll
-      for (int kk = 0; kk < DK / 16; ++kk) {
-        const bf16x8 bv = *(const bf16x8*)(vN + (long)s * DK + 16 * kk + 8 * g);
-        const bf16x8 a = sq ? ld_row8(p.dout, p, b, h, t0 + 32 * I + li, 16 * kk + 8 * g)
-                            : *(const bf16x8*)(sdR + (32 * I + li) * KS + 16 * kk + 8 * g);
-        D = mfma32(a, bv, D);
-      }
+    const f32x16& S = SG[u];
+    const f32x16& D = DD[u];
+    f32x16 z, sb;
+    if (!kind) {  // dS = dP o Gamma o tril;  z = dP o S o Gamma (dlog-gamma)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int t = 32 * I + d_row(r, g);
         const float gam = __expf(lg[t] - lg[s]);
-        if (sq) {
-          const bool mP = s <= t;
-          dS[r] = mP ? D[r] * gam : 0.0f;
-          sZp[t * ZS + s] = mP ? D[r] * SG[r] * gam : 0.0f;
-          sdS[t * TS + s] = (bf16)dS[r];
-        } else {
-          const bool mA = s < t;
-          const float GG = mA ? gam * SG[r] : 0.0f;
-          const float dAv = -D[r];
-          sZa[t * ZS + s] = dAv * bt[t] * GG;
-          sB[t * ZS + s] = dAv * GG;
-          const float dG = mA ? bt[t] * dAv * gam : 0.0f;
-          if (mA) {
-            sdF[t * TS + s] = (bf16)dG;
-            sdF[s * TS + t] = (bf16)dG;
-          } else if (s == t) {
-            sdF[t * TS + t] = (bf16)0.0f;
-          }
-        }
+        const bool m = s <= t;
+        sdS[t * TS + s] = (bf16)(m ? D[r] * gam : 0.0f);
+        z[r] = m ? D[r] * S[r] * gam : 0.0f;
       }
-    } else {
+    } else {  // dA = -dR v_new^T;  dG = beta dA o Gamma (strict lower), dF = dG + dG^T
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int t = d_row(r, g);
-        if (sq) {
-          sZp[t * ZS + s] = 0.0f;
-          sdS[t * TS + s] = (bf16)0.0f;
-        } else {
-          sZa[t * ZS + s] = 0.0f;
-          sB[t * ZS + s] = 0.0f;
+        const int t = 32 * I + d_row(r, g);
+        const float gam = __expf(lg[t] - lg[s]);
+        const bool m = s < t;
+        const float GG = m ? gam * S[r] : 0.0f;
+        const float dAv = -D[r];
+        z[r] = dAv * bt[t] * GG;
+        sb[r] = dAv * GG;
+        const float dG = m ? bt[t] * dAv * gam : 0.0f;
+        if (m) {
+          sdF[t * TS + s] = (bf16)dG;
+          sdF[s * TS + t] = (bf16)dG;
+        } else if (s == t) {
+          sdF[t * TS + t] = (bf16)0.0f;
         }
       }
     }
-    if (sq) store_rows(sdSt + (32 * J) * TS + 32 * I, TS, dS, li, g);
-  }
-  __syncthreads();
-
-  {  // row t = tid % 64 over the 8 columns s of part tid / 64 (all 512 threads)
-    const int t = tid & (CH - 1), s0 = 8 * (tid >> 6);
-    float a = 0.0f, bb = 0.0f;
+    // dlog-gamma_t += sum_s z[t][s] - sum_s z[s][t];  dbeta_t += sum_s (dA o Gamma o G)[t][s]
+    float cs = 0.0f;
 #pragma unroll
-    for (int s = s0; s < s0 + 8; ++s) {
-      a += sZp[t * ZS + s] + sZa[t * ZS + s] - sZp[s * ZS + t] - sZa[s * ZS + t];
-      bb += sB[t * ZS + s];
+    for (int r = 0; r < 16; ++r) cs += z[r];
+    cs += __shfl_xor(cs, 32);
+    if (g == 0) atomicAdd(&dlg[s], -cs);
+    const int tr = 32 * I + d_row(li >> 1, g);
+    const float rs = rowsum32(z, li);
+    if ((li & 1) == 0) atomicAdd(&dlg[tr], rs);
+    if (kind) {
+      const float rb = rowsum32(sb, li);
+      if ((li & 1) == 0) atomicAdd(&dbt[tr], rb);
     }
-    atomicAdd(&dlg[t], a);
-    atomicAdd(&dbt[t], bb);
   }
+  // dh rows d_k = 32 w + li
+  bf16x8 fm[DK / 16];
+#pragma unroll
+  for (int kk = 0; kk < DK / 16; ++kk)
+    fm[kk] = *(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * w + li) * DK + 16 * kk + 8 * g);
+  __syncthreads();  // dS, dF and the sums complete
 
-  // dQ^T and dK^T: rows d_k = 32 wd + .., columns t (or s) = 32 wt + li
-  float dlgC = 0.0f;
-  f32x16 XdK;
+  // ---- dQ^T and dK^T: rows d_k = 32 w + .., columns t = 32 j + li, in three passes so that
+  // few operands are live at once ----
+  // (1) X1 = dh v_new^T
+  f32x16 X1[2], X2[2], XQ[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    X1[j] = zero16();
+#pragma unroll
+    for (int kk = 0; kk < DK / 16; ++kk)
+      X1[j] = mfma32(fm[kk], *(const bf16x8*)(vN + (long)(32 * j + li) * DK + 16 * kk + 8 * g), X1[j]);
+  }
+  // (2) h dO^T and h dR^T (h rows d_k = 32 w + li); <dh, h> over this wave's rows (the four
+  // waves cover the matrix once)
+  float hdh = 0.0f;
   {
-    const int J2 = wt, t = 32 * J2 + li;
-    // rows d_k = 32 wd + li of h, the A operand of the dQ and dK products
     bf16x8 hf[DK / 16];
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) hf[kk] = *(const bf16x8*)(hN + (long)(32 * wd + li) * DK + 16 * kk + 8 * g);
-    // dQ^T = gamma (h dO^T) + K^T dS^T
-    f32x16 X = zero16();
+    for (int kk = 0; kk < DK / 16; ++kk) hf[kk] = *(const bf16x8*)(hN + (long)(32 * w + li) * DK + 16 * kk + 8 * g);
 #pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) X = mfma32(hf[kk], ld_row8(p.dout, p, b, h, t0 + t, 16 * kk + 8 * g), X);
+    for (int kk = 0; kk < DK / 16; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hdh = fmaf((float)fm[kk][e], (float)hf[kk][e], hdh);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int t = 32 * j + li;
+      XQ[j] = zero16();
+      X2[j] = zero16();
+#pragma unroll
+      for (int kk = 0; kk < DK / 16; ++kk) {
+        XQ[j] = mfma32(hf[kk], ld_row8(p.dout, p, b, h, t0 + t, 16 * kk + 8 * g), XQ[j]);
+        X2[j] = mfma32(hf[kk], *(const bf16x8*)(sdR + lds_off<DK>(t, 16 * kk + 8 * g)), X2[j]);
+      }
+    }
+  }
+  // (3) dQ^T = gamma (h dO^T) + K^T dS^T;
+  //     dK^T = (gamma_C / gamma) dh v_new^T - (beta gamma) h dR^T + Q^T dS + K^T dF
+  float dlgC = 0.0f;
+  f32x16 XK[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int t = 32 * j + li;
+    f32x16 X = XQ[j];
     const float gmt = __expf(lg[t]);
-    float qx = 0.0f;
+    float qx = 0.0f, k1 = 0.0f, k2 = 0.0f;
+    bf16x4 qv[4], kv[4];  // Q[t][d], K[t][d] at this lane's rows d = 32 w + 8 q + 4 g + e
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      qv[q] = *(const bf16x4*)(sQ + lds_off<DK>(t, 32 * w + 8 * q + 4 * g));
+      kv[q] = *(const bf16x4*)(sK + lds_off<DK>(t, 32 * w + 8 * q + 4 * g));
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      qx = fmaf((float)sQt[(32 * wd + d_row(r, g)) * TS + t], X[r], qx);
+      qx = fmaf((float)qv[r >> 2][r & 3], X[r], qx);
       X[r] *= gmt;
     }
     qx += __shfl_xor(qx, 32);
     if (g == 0) atomicAdd(&dlg[t], gmt * qx);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      if (kk >= 2 * (J2 + 1)) continue;
-      X = mfma32(*(const bf16x8*)(sKt + (32 * wd + li) * TS + 16 * kk + 8 * g),
-                 *(const bf16x8*)(sdS + t * TS + 16 * kk + 8 * g), X);
+      if (kk >= 2 * (j + 1)) continue;  // dS[t][s] = 0 for s > t
+      X = mfma32(tr_frag(sK, 16 * kk, 32 * w), row_frag_ts(sdS, t, kk), X);
     }
-    store_rows(sO + (32 * J2) * KS + 32 * wd, KS, X, li, g);
+    XQ[j] = X;
 
-    // dK^T = (gamma_C / gamma) dh v^T - (beta gamma) h dR^T + Q^T dS + K^T dF
-    f32x16 X1 = zero16(), X2 = zero16(), X3 = zero16();
-    float hdh = 0.0f;  // <dh, h> over this lane's fragments (waves with wt = 0 cover the matrix once)
-#pragma unroll
-    for (int kk = 0; kk < DK / 16; ++kk) {
-      const bf16x8 df = *(const bf16x8*)(p.dmN + ci * DK * DK + (long)(32 * wd + li) * DK + 16 * kk + 8 * g);
-      X1 = mfma32(df, *(const bf16x8*)(vN + (long)t * DK + 16 * kk + 8 * g), X1);
-      X2 = mfma32(hf[kk], *(const bf16x8*)(sdR + t * KS + 16 * kk + 8 * g), X2);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) hdh = fmaf((float)df[e], (float)hf[kk][e], hdh);
-    }
+    f32x16 X3 = zero16();
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      if (kk < 2 * J2) continue;
-      X3 = mfma32(*(const bf16x8*)(sQt + (32 * wd + li) * TS + 16 * kk + 8 * g),
-                  *(const bf16x8*)(sdSt + t * TS + 16 * kk + 8 * g), X3);
+      if (kk < 2 * j) continue;  // dS[t'][s] = 0 for t' < s
+      X3 = mfma32(tr_frag(sQ, 16 * kk, 32 * w), tr_frag_ts(sdS, 16 * kk, 32 * j), X3);
     }
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      X3 = mfma32(*(const bf16x8*)(sKt + (32 * wd + li) * TS + 16 * kk + 8 * g),
-                  *(const bf16x8*)(sdF + t * TS + 16 * kk + 8 * g), X3);
+    for (int kk = 0; kk < 4; ++kk) X3 = mfma32(tr_frag(sK, 16 * kk, 32 * w), row_frag_ts(sdF, t, kk), X3);
     const float sc1 = __expf(lgC - lg[t]);
     const float sc2 = bt[t] * gmt;
-    float k1 = 0.0f, k2 = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float kv = (float)sKt[(32 * wd + d_row(r, g)) * TS + t];
-      k1 = fmaf(kv, X1[r], k1);
-      k2 = fmaf(kv, X2[r], k2);
-      X3[r] += sc1 * X1[r] - sc2 * X2[r];
+      const float kvr = (float)kv[r >> 2][r & 3];
+      k1 = fmaf(kvr, X1[j][r], k1);
+      k2 = fmaf(kvr, X2[j][r], k2);
+      X3[r] += sc1 * X1[j][r] - sc2 * X2[j][r];
     }
     k1 += __shfl_xor(k1, 32);
     k2 += __shfl_xor(k2, 32);
     if (g == 0) {
       atomicAdd(&dlg[t], -sc1 * k1 - sc2 * k2);
       atomicAdd(&dbt[t], -gmt * k2);
-      dlgC = sc1 * k1;
+      dlgC += sc1 * k1;
     }
-    XdK = X3;
-    // gamma_C <dh, h> and the Kd terms enter the decay of the last step
-    float acc = (wt == 0 ? hdh : 0.0f) * __expf(lgC) + dlgC;
+    XK[j] = X3;
+  }
+  {  // gamma_C <dh, h> and the Kd terms enter the decay of the last step
+    float acc = hdh * __expf(lgC) + dlgC;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
     if (l == 0) atomicAdd(&dlg[CH - 1], acc);
   }
+  __syncthreads();  // every read of sQ and sK done: dQ and dK go over them
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    put_rows(sQ, 32 * j, XQ[j], 1.0f);
+    put_rows(sK, 32 * j, XK[j], 1.0f);
+  }
   __syncthreads();
-  // dQ is staged; sZ is consumed: stage dK over it
-  bf16* sK2 = (bf16*)sZ;
-  store_rows(sK2 + (32 * wt) * KS + 32 * wd, KS, XdK, li, g);
-  copy_rows(p.dq, sO);
-  __syncthreads();
-  copy_rows(p.dk, sK2);
+  copy_rows(p.dq, sQ);
+  copy_rows(p.dk, sK);
 
   if (w == 0) {
     // dlog(alpha_s) = sum_{t >= s} dlg_t
@@ -1152,7 +1255,7 @@ int reverse_pass(hipStream_t s, CkArgs& a, unsigned bh, const void* grad_out, vo
   dr_ck_scan_kernel<2><<<bh * (DK / VS), 256, 0, s>>>(a);
   rc = check_launch("delta rule chunk reverse scan");
   if (rc) return rc;
-  dr_ck_grad_kernel<<<dim3(a.nch, bh), 512, 0, s>>>(a);
+  dr_ck_grad_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
   return check_launch("delta rule chunk grad");
 }
 
