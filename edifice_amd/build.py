@@ -48,8 +48,12 @@ def sources():
 # accumulators in AGPRs and moves them back and forth around every softmax step (about 40%
 # of the dQ kernel's VALU instructions).  The VGPR form of the MFMAs removes those moves
 # without spilling (measured: backward 3.01 -> 2.82 ms at config 4, identical results).
+# The chunked delta rule's kernels scale and convert their MFMA accumulators with VALU
+# work after every product; kept in VGPRs they need no v_accvgpr moves (config 3: output
+# kernel 84.6 -> 79.2 us, the others unchanged; identical results).
 PER_FILE_FLAGS = {
     "flash_attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "delta_rule_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 
