@@ -16,8 +16,16 @@
 // workgroups per layer each own 2 units of every gate for 8 batch rows: they stage their
 // W_x and R columns (laid out unit-major once per call, so each slice is one contiguous
 // block) into LDS, form and LayerNorm the x^l_t rows, take the input and recurrent dot
-// products (each split over a lane quad) and apply the cell update for their units.  The
-// launch boundary orders the diagonals: no grid-wide barrier runs inside a kernel.
+// products (each split over a lane quad) and apply the cell update for their units.
+// When the device can hold every workgroup at once, the recurrence is one cooperative
+// launch: each workgroup stages its weight slices once, keeps its LSTM cell state in a
+// register and walks all diagonals, a bounded grid barrier between them (per diagonal
+// launch it re-staged 16 KB of weights and paid a kernel boundary).  Otherwise one launch
+// per diagonal orders them.
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
@@ -31,6 +39,15 @@ constexpr int RNB_BS = 8;  // batch rows per workgroup
 constexpr int RNB_LDR = RNB_HMAX + 4;  // LDS row stride: a wave's (row, k mod 4) reads hit distinct banks
 
 enum { RNB_LSTM = 4, RNB_GRU = 3 };  // value = number of gates
+
+// grid barrier of the persistent kernel (rnb_grid_sync)
+constexpr unsigned RNB_SPIN_LIMIT = 1u << 16;
+constexpr int RNB_BAR_GROUPS = 16;
+constexpr int RNB_BAR_LINE = 32;  // words per 128-byte line: every counter on its own line
+// word offsets in the barrier area: root, abort, then the group counters and release words
+constexpr int RNB_BAR_ROOT = 0, RNB_BAR_ABORT = RNB_BAR_LINE, RNB_BAR_SUB = 2 * RNB_BAR_LINE,
+              RNB_BAR_GO = RNB_BAR_SUB + RNB_BAR_GROUPS * RNB_BAR_LINE,
+              RNB_BAR_WORDS = RNB_BAR_GO + RNB_BAR_GROUPS * RNB_BAR_LINE;
 
 struct RnbArgs {
   const void *input, *weights;
@@ -57,9 +74,10 @@ __global__ __launch_bounds__(256) void rnb_rt_kernel(const T* __restrict__ M, fl
 // h0[:, l, :] and c0[:, l, :] (or zeros) for every layer, as [L][B][H] f32.
 template <typename T>
 __global__ __launch_bounds__(256) void rnb_init_kernel(const T* __restrict__ h0, const T* __restrict__ c0,
-                                                       float* __restrict__ hs0, float* __restrict__ cs, int B, int L,
-                                                       int H) {
+                                                       float* __restrict__ hs0, float* __restrict__ cs,
+                                                       unsigned* __restrict__ bar, int B, int L, int H) {
   const long e = (long)blockIdx.x * 256 + threadIdx.x;
+  if (e < RNB_BAR_WORDS) bar[e] = 0u;
   if (e >= (long)L * B * H) return;
   const int u = (int)(e % H), b = (int)((e / H) % B), l = (int)(e / ((long)B * H));
   const long src = ((long)b * L + l) * H + u;
@@ -67,58 +85,94 @@ __global__ __launch_bounds__(256) void rnb_init_kernel(const T* __restrict__ h0,
   cs[e] = c0 != nullptr ? to_f32(c0[src]) : 0.0f;
 }
 
-// Launch j: step t = j - l of layer l = blockIdx.z for units grp * U .. and batch rows
-// blockIdx.y * BS ...
-template <typename T, int G>
-__global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
-  const int l = blockIdx.z, t = j - l;
-  if (t < 0 || t >= p.T) return;  // whole workgroup: outside the (layer, step) grid
-  __shared__ float sW[G * RNB_U * RNB_LDR], sR[G * RNB_U * RNB_LDR];
-  __shared__ float sx[RNB_BS][RNB_LDR], sh[RNB_BS][RNB_LDR];
-  __shared__ float sd[2][RNB_BS][G * RNB_U];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, H = p.H, GH = G * H;
-  const int grp = blockIdx.x, u0 = grp * RNB_U, b0 = blockIdx.y * RNB_BS;
-  const long lstride = 2L * H * GH + GH + 2L * H;
-  const T* Wl = (const T*)p.weights + l * lstride;
-  {
-    const long off = ((long)l * p.ngrp + grp) * G * RNB_U * H;
-    for (int e = tid; e < G * RNB_U * H; e += 256) {
-      const int r = e / H, k = e % H;
-      sW[r * RNB_LDR + k] = p.Wt[off + e];
-      sR[r * RNB_LDR + k] = p.Rt[off + e];
-    }
+// W_x and R columns of units grp * U .. for layer l into LDS (rows g U + uu, H wide).
+template <int G>
+EDF_DEVICE void rnb_stage_weights(const RnbArgs& p, int l, int grp, float* sW, float* sR) {
+  const int H = p.H;
+  const long off = ((long)l * p.ngrp + grp) * G * RNB_U * H;
+  for (int e = threadIdx.x; e < G * RNB_U * H; e += 256) {
+    const int r = e / H, k = e % H;
+    sW[r * RNB_LDR + k] = p.Wt[off + e];
+    sR[r * RNB_LDR + k] = p.Rt[off + e];
   }
-  for (int e = tid; e < RNB_BS * H; e += 256) {
-    const int bb = e / H, k = e % H, b = b0 + bb;
-    float hv = 0.0f, xv = 0.0f;
-    if (b < p.B) {
-      hv = t == 0 ? p.hs0[((long)l * p.B + b) * H + k] : p.Hs[(((long)l * p.B + b) * p.T + t - 1) * H + k];
-      xv = to_f32(((const T*)p.input)[((long)b * p.T + t) * H + k]);
-      for (int m = 0; m < l; ++m) xv += p.Hs[(((long)m * p.B + b) * p.T + t) * H + k];
+}
+
+// LayerNorm gamma / beta of layer l into LDS and the input-projection bias of the
+// thread's (batch row, unit) into registers (threads < BS U), once per kernel.
+template <typename T, int G>
+EDF_DEVICE void rnb_stage_consts(const RnbArgs& p, int l, int grp, float* sgam, float* sbet, float* xb) {
+  const int H = p.H, GH = G * H;
+  const T* Wl = (const T*)p.weights + l * (2L * H * GH + GH + 2L * H);
+  for (int k = threadIdx.x; k < H; k += 256) {
+    sgam[k] = to_f32(Wl[2L * H * GH + GH + k]);
+    sbet[k] = to_f32(Wl[2L * H * GH + GH + H + k]);
+  }
+  const int u = grp * RNB_U + threadIdx.x % RNB_U;
+#pragma unroll
+  for (int g = 0; g < G; ++g) xb[g] = u < H ? to_f32(Wl[(long)H * GH + g * H + u]) : 0.0f;
+}
+
+// Step t of layer l for units grp * U .. and batch rows b0 ..: form and LayerNorm the x rows,
+// the input and recurrent dot products, the cell update.  Every thread of the workgroup
+// runs it (no early return: the persistent kernel meets a grid barrier after it).  c holds
+// the LSTM cell state of the thread's (batch row, unit) (threads < BS U), xb its gate biases.
+template <typename T, int G>
+EDF_DEVICE void rnb_step(const RnbArgs& p, int l, int t, int grp, int b0, const float* sW, const float* sR,
+                         const float* sgam, const float* sbet, const float* xb, float (*sx)[RNB_LDR],
+                         float (*sh)[RNB_LDR], float (*sd)[RNB_BS][G * RNB_U], float& c) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, H = p.H;
+  const int u0 = grp * RNB_U;
+  // x^l_t = input_t + sum_{m<l} h^m_t and h^l_{t-1} rows of the 8 batch rows.  h rows of
+  // other workgroups are read at device scope (coherent across the XCDs: with H * 4 bytes
+  // below a cache line, the line of row t may have been cached while row t - 1 was read).
+  // A thread's up to 8 elements are loaded together from clamped addresses.
+  constexpr int EPT = RNB_BS * RNB_HMAX / 256;
+  auto hld = [&](const float* q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const long HT = (long)p.T * H;
+  const float* hprev = t == 0 ? p.hs0 + (long)l * p.B * H : p.Hs + (long)l * p.B * HT + (long)(t - 1) * H;
+  const long hstr = t == 0 ? H : HT;
+  int bk[EPT], kk[EPT];
+  bool ok[EPT];
+  float hv[EPT], xv[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = tid + 256 * i;
+    const int bb = e / H;
+    ok[i] = e < RNB_BS * H && b0 + bb < p.B;
+    bk[i] = ok[i] ? b0 + bb : 0;
+    kk[i] = ok[i] ? e % H : 0;
+    hv[i] = hld(hprev + bk[i] * hstr + kk[i]);
+    xv[i] = to_f32(((const T*)p.input)[((long)bk[i] * p.T + t) * H + kk[i]]);
+  }
+  for (int m = 0; m < l; ++m) {
+    const float* hm = p.Hs + (long)m * p.B * HT + (long)t * H;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) xv[i] += hld(hm + bk[i] * HT + kk[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const int e = tid + 256 * i;
+    if (e < RNB_BS * H) {
+      sh[e / H][e % H] = ok[i] ? hv[i] : 0.0f;
+      sx[e / H][e % H] = ok[i] ? xv[i] : 0.0f;
     }
-    sh[bb][k] = hv;
-    sx[bb][k] = xv;
   }
   __syncthreads();
   // LayerNorm of the 8 x rows: wave w normalizes rows 2 w and 2 w + 1 (biased variance)
-  {
-    const T* gamma = Wl + 2L * H * GH + GH;
-    const T* beta = gamma + H;
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-      float* row = sx[2 * w + rr];
-      float sum = 0.0f;
-      for (int k = lane; k < H; k += 64) sum += row[k];
+  for (int rr = 0; rr < 2; ++rr) {
+    float* row = sx[2 * w + rr];
+    float sum = 0.0f;
+    for (int k = lane; k < H; k += 64) sum += row[k];
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-      const float mean = sum / (float)H;
-      float var = 0.0f;
-      for (int k = lane; k < H; k += 64) var = fmaf(row[k] - mean, row[k] - mean, var);
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    const float mean = sum / (float)H;
+    float var = 0.0f;
+    for (int k = lane; k < H; k += 64) var = fmaf(row[k] - mean, row[k] - mean, var);
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) var += __shfl_xor(var, off);
-      const float inv = 1.0f / sqrtf(var / (float)H + RNB_LN_EPS);
-      for (int k = lane; k < H; k += 64) row[k] = fmaf((row[k] - mean) * inv, to_f32(gamma[k]), to_f32(beta[k]));
-    }
+    for (int off = 32; off > 0; off >>= 1) var += __shfl_xor(var, off);
+    const float inv = 1.0f / sqrtf(var / (float)H + RNB_LN_EPS);
+    for (int k = lane; k < H; k += 64) row[k] = fmaf((row[k] - mean) * inv, sgam[k], sbet[k]);
   }
   __syncthreads();
   // input and recurrent dot products, each split over a lane quad (k = q, q + 4, ...)
@@ -154,32 +208,125 @@ __global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
   __syncthreads();
   if (tid < RNB_BS * RNB_U) {
     const int bb = tid / RNB_U, uu = tid % RNB_U, b = b0 + bb, u = u0 + uu;
-    if (b >= p.B || u >= H) return;
-    const T* bx = Wl + (long)H * GH;
-    float xg[G], rg[G];
+    if (b < p.B && u < H) {
+      float xg[G], rg[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      xg[g] = sd[0][bb][g * RNB_U + uu] + to_f32(bx[g * H + u]);
-      rg[g] = sd[1][bb][g * RNB_U + uu];
+      for (int g = 0; g < G; ++g) {
+        xg[g] = sd[0][bb][g * RNB_U + uu] + xb[g];
+        rg[g] = sd[1][bb][g * RNB_U + uu];
+      }
+      const float hp = sh[bb][u];
+      float h;
+      if constexpr (G == RNB_LSTM) {
+        const float ig = 1.0f / (1.0f + __expf(-(xg[0] + rg[0])));
+        const float fg = 1.0f / (1.0f + __expf(-(xg[1] + rg[1])));
+        const float gg = tanhf(xg[2] + rg[2]);
+        const float og = 1.0f / (1.0f + __expf(-(xg[3] + rg[3])));
+        c = fmaf(fg, c, ig * gg);
+        h = og * tanhf(c);
+      } else {
+        const float r = 1.0f / (1.0f + __expf(-(xg[0] + rg[0])));
+        const float z = 1.0f / (1.0f + __expf(-(xg[1] + rg[1])));
+        const float n = tanhf(fmaf(r, rg[2], xg[2]));
+        h = fmaf(z, n - hp, hp);
+      }
+      // written through to the device coherence point (other XCDs read it next diagonal)
+      __hip_atomic_store(&p.Hs[(((long)l * p.B + b) * p.T + t) * H + u], h, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
-    const long si = ((long)l * p.B + b) * H + u;
-    const float hp = sh[bb][u];
-    float h;
-    if constexpr (G == RNB_LSTM) {
-      const float ig = 1.0f / (1.0f + __expf(-(xg[0] + rg[0])));
-      const float fg = 1.0f / (1.0f + __expf(-(xg[1] + rg[1])));
-      const float gg = tanhf(xg[2] + rg[2]);
-      const float og = 1.0f / (1.0f + __expf(-(xg[3] + rg[3])));
-      const float c = fmaf(fg, p.cs[si], ig * gg);
-      p.cs[si] = c;
-      h = og * tanhf(c);
-    } else {
-      const float r = 1.0f / (1.0f + __expf(-(xg[0] + rg[0])));
-      const float z = 1.0f / (1.0f + __expf(-(xg[1] + rg[1])));
-      const float n = tanhf(fmaf(r, rg[2], xg[2]));
-      h = fmaf(z, n - hp, hp);
+  }
+}
+
+// Launch j: step t = j - l of layer l = blockIdx.z for units grp * U .. and batch rows
+// blockIdx.y * BS ..  (the path when the persistent kernel cannot be co-scheduled).
+template <typename T, int G>
+__global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
+  const int l = blockIdx.z, t = j - l;
+  if (t < 0 || t >= p.T) return;  // whole workgroup: outside the (layer, step) grid
+  __shared__ float sW[G * RNB_U * RNB_LDR], sR[G * RNB_U * RNB_LDR];
+  __shared__ float sx[RNB_BS][RNB_LDR], sh[RNB_BS][RNB_LDR];
+  __shared__ float sd[2][RNB_BS][G * RNB_U];
+  __shared__ float sgam[RNB_HMAX], sbet[RNB_HMAX];
+  const int grp = blockIdx.x, b0 = blockIdx.y * RNB_BS, tid = threadIdx.x;
+  rnb_stage_weights<G>(p, l, grp, sW, sR);
+  float xb[G];
+  rnb_stage_consts<T, G>(p, l, grp, sgam, sbet, xb);
+  const long si = ((long)l * p.B + b0 + tid / RNB_U) * p.H + grp * RNB_U + tid % RNB_U;
+  const bool own = tid < RNB_BS * RNB_U && b0 + tid / RNB_U < p.B && grp * RNB_U + tid % RNB_U < p.H;
+  float c = (G == RNB_LSTM && own) ? p.cs[si] : 0.0f;
+  __syncthreads();
+  rnb_step<T, G>(p, l, t, grp, b0, sW, sR, sgam, sbet, xb, sx, sh, sd, c);
+  if (G == RNB_LSTM && own) p.cs[si] = c;
+}
+
+// Grid-wide barrier of the persistent kernel (a cooperative launch: every workgroup is
+// resident).  The h rows that cross it are stored and loaded at device scope (coherent
+// across the XCDs' L2s), so every wave waiting for its own stores before its workgroup
+// arrives orders them; no cache write-back or invalidation is needed (with them each
+// barrier cost ~85 us).  Arrivals go through a two-level tree of monotonic device-scope
+// counters, so no counter or flag serves more than 32 workgroups (one counter for all 512
+// workgroups of the config-size call serialised ~20 us of atomics per barrier): workgroup i
+// arrives at sub-counter i % 16; the last arrival of a group arrives at the root; the last
+// root arrival publishes the barrier's generation to the 16 groups' release words, which
+// the groups poll.  The wait is bounded: it cannot time out under a cooperative launch,
+// but if it ever did, the workgroup sets the abort word and every later wait of every
+// workgroup ends at once, so the kernel still finishes.
+EDF_DEVICE void rnb_grid_sync(unsigned* bar, unsigned gen, unsigned wg, unsigned nwg) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned grp = wg % RNB_BAR_GROUPS;
+    const unsigned members = nwg / RNB_BAR_GROUPS + (grp < nwg % RNB_BAR_GROUPS ? 1u : 0u);
+    const unsigned ngrp = nwg < RNB_BAR_GROUPS ? nwg : (unsigned)RNB_BAR_GROUPS;
+    unsigned* go = bar + RNB_BAR_GO + grp * RNB_BAR_LINE;
+    const unsigned sub = __hip_atomic_fetch_add(bar + RNB_BAR_SUB + grp * RNB_BAR_LINE, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    if (sub + 1 == gen * members) {
+      const unsigned root = __hip_atomic_fetch_add(bar + RNB_BAR_ROOT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (root + 1 == gen * ngrp)
+        for (unsigned i = 0; i < ngrp; ++i)
+          __hip_atomic_store(bar + RNB_BAR_GO + i * RNB_BAR_LINE, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    p.Hs[(((long)l * p.B + b) * p.T + t) * H + u] = h;
+    for (unsigned spin = 0;; ++spin) {
+      if (__hip_atomic_load(go, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= gen) break;
+      if (__hip_atomic_load(bar + RNB_BAR_ABORT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
+      if (spin >= RNB_SPIN_LIMIT) {
+        __hip_atomic_store(bar + RNB_BAR_ABORT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// The whole recurrence in one launch: each workgroup stages its weight slices once and
+// walks every anti-diagonal j, computing step t = j - l of its layer when that lies inside
+// the sequence; a grid barrier separates the diagonals (the launch boundary of the
+// per-diagonal path).  The barrier area starts zeroed.
+template <typename T, int G>
+__global__ __launch_bounds__(256) void rnb_persist_kernel(const RnbArgs p, unsigned* bar) {
+  __shared__ float sW[G * RNB_U * RNB_LDR], sR[G * RNB_U * RNB_LDR];
+  __shared__ float sx[RNB_BS][RNB_LDR], sh[RNB_BS][RNB_LDR];
+  __shared__ float sd[2][RNB_BS][G * RNB_U];
+  __shared__ float sgam[RNB_HMAX], sbet[RNB_HMAX];
+  const int l = blockIdx.z, grp = blockIdx.x, b0 = blockIdx.y * RNB_BS, tid = threadIdx.x;
+  const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
+  const unsigned wg = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  rnb_stage_weights<G>(p, l, grp, sW, sR);
+  float xb[G];
+  rnb_stage_consts<T, G>(p, l, grp, sgam, sbet, xb);
+  __syncthreads();
+  const long si = ((long)l * p.B + b0 + tid / RNB_U) * p.H + grp * RNB_U + tid % RNB_U;
+  const bool own = tid < RNB_BS * RNB_U && b0 + tid / RNB_U < p.B && grp * RNB_U + tid % RNB_U < p.H;
+  float c = (G == RNB_LSTM && own) ? p.cs[si] : 0.0f;
+  const int nd = p.T + p.L - 1;
+  for (int j = 0; j < nd; ++j) {
+    const int t = j - l;
+    if (t >= 0 && t < p.T) rnb_step<T, G>(p, l, t, grp, b0, sW, sR, sgam, sbet, xb, sx, sh, sd, c);
+    if (j + 1 < nd) rnb_grid_sync(bar, (unsigned)(j + 1), wg, nwg);
   }
 }
 
@@ -196,6 +343,7 @@ __global__ __launch_bounds__(256) void rnb_out_kernel(const RnbArgs p, T* __rest
 
 struct RnbWs {
   float *Hs, *hs0, *cs, *Wt, *Rt;
+  unsigned* bar;  // grid barrier counter and flag of the persistent kernel
   size_t total;
 };
 
@@ -216,6 +364,8 @@ inline RnbWs rnb_layout(void* base, int B, int Tn, int H, int L, int G) {
   off += rnb_align((size_t)L * slice * 4);
   w.Rt = (float*)(p + off);
   off += rnb_align((size_t)L * slice * 4);
+  w.bar = (unsigned*)(p + off);
+  off += rnb_align(RNB_BAR_WORDS * 4);
   w.total = off;
   return w;
 }
@@ -234,11 +384,33 @@ int rnb_run(hipStream_t s, const void* input, const void* weights, const void* h
     rnb_rt_kernel<T, G><<<gslice, 256, 0, s>>>(Wl + (long)H * G * H + (long)G * H, ws.Rt + l * slice, H);
   }
   if (int rc = check_launch("rnn block weight layout")) return rc;
-  rnb_init_kernel<T><<<(unsigned)(((long)L * B * H + 255) / 256), 256, 0, s>>>(
-      (const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr, ws.hs0, ws.cs, B, L, H);
+  rnb_init_kernel<T><<<(unsigned)((std::max((long)L * B * H, (long)RNB_BAR_WORDS) + 255) / 256), 256, 0, s>>>(
+      (const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr, ws.hs0, ws.cs, ws.bar, B, L, H);
   if (int rc = check_launch("rnn block initial state")) return rc;
   const dim3 grid(a.ngrp, (B + RNB_BS - 1) / RNB_BS, L);
-  for (int j = 0; j < Tn + L - 1; ++j) rnb_diag_kernel<T, G><<<grid, 256, 0, s>>>(a, j);
+  // one cooperative launch for the whole recurrence when every workgroup fits on the
+  // device at once (the runtime refuses it otherwise); else one launch per diagonal
+  // (EDF_RNN_BLOCK_PER_STEP=1 forces the per-diagonal path, so that tests cover both)
+  int coop = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
+    coop = 0;
+  const char* force = getenv("EDF_RNN_BLOCK_PER_STEP");
+  if (force != nullptr && force[0] == '1') coop = 0;
+  bool done = false;
+  if (coop) {
+    unsigned* bar = ws.bar;
+    void* args[] = {(void*)&a, (void*)&bar};
+    const hipError_t e = hipLaunchCooperativeKernel((const void*)rnb_persist_kernel<T, G>, grid, dim3(256), args, 0, s);
+    if (e == hipSuccess) {
+      done = true;
+    } else {
+      (void)hipGetLastError();  // not co-schedulable: clear and take the per-diagonal path
+    }
+  }
+  if (!done)
+    for (int j = 0; j < Tn + L - 1; ++j) rnb_diag_kernel<T, G><<<grid, 256, 0, s>>>(a, j);
   if (int rc = check_launch("rnn block step")) return rc;
   rnb_out_kernel<T><<<(unsigned)(((long)B * Tn * H + 255) / 256), 256, 0, s>>>(a, (T*)out);
   return check_launch("rnn block output");

@@ -294,3 +294,36 @@ def test_rnn_block(case, rng):
     r = lambda a: None if a is None else rounded(a, dtype)  # noqa: E731
     want = scans.rnn_block(kind, r(x), r(w), r(h0), r(c0), layers)
     assert_close(host(out), want, TOL[dtype], "out")
+
+
+@pytest.mark.parametrize("case", [RNN_BLOCK_CASES[3], RNN_BLOCK_CASES[6], RNN_BLOCK_CASES[8]])
+def test_rnn_block_paths_agree(case, rng, monkeypatch):
+    """The whole recurrence in one cooperative launch (grid barrier between diagonals) and
+    one launch per diagonal run the same arithmetic: bit-identical outputs, both against
+    the oracle."""
+    from edifice_amd import fused_scan as fs
+    kind, bsz, seq, hid, layers, dtype, init = case
+    announce("rnn_block_paths", case=case)
+    gh = scans.RNN_BLOCK_GATES[kind] * hid
+    sc = 1 / np.sqrt(hid)
+    per = []
+    for _ in range(layers):
+        per += [sc * rng.normal(size=hid * gh), 0.3 * rng.normal(size=gh), sc * rng.normal(size=hid * gh),
+                1 + 0.2 * rng.normal(size=hid), 0.2 * rng.normal(size=hid)]
+    w = np.concatenate(per)
+    x = rng.normal(size=(bsz, seq, hid))
+    h0 = rng.normal(size=(bsz, layers, hid)) if init else None
+    c0 = rng.normal(size=(bsz, layers, hid)) if init and kind == "lstm" else None
+    tx, tw = to_dev(x, dtype), to_dev(w, dtype)
+    th0 = to_dev(h0, dtype) if h0 is not None else None
+    tc0 = to_dev(c0, dtype) if c0 is not None else None
+
+    def run():
+        return host(fs.lstm_block(tx, tw, th0, tc0, layers) if kind == "lstm" else fs.gru_block(tx, tw, th0, layers))
+
+    whole = run()
+    monkeypatch.setenv("EDF_RNN_BLOCK_PER_STEP", "1")
+    stepwise = run()
+    assert np.array_equal(whole, stepwise)
+    r = lambda a: None if a is None else rounded(a, dtype)  # noqa: E731
+    assert_close(whole, scans.rnn_block(kind, r(x), r(w), r(h0), r(c0), layers), TOL[dtype], "out")
