@@ -768,29 +768,36 @@ __global__ __launch_bounds__(256) void dr_ck_dlocal_kernel(const CkArgs p) {
 // dV, dQ and dK are staged over tiles that are dead by then.
 // ---------------------------------------------------------------------------
 
-// Sum over the 32 lanes of each half-wave of an accumulator tile's rows: afterwards lane li
-// holds the sum of register r = li / 2 (a reduce-scatter: each exchange halves the number
-// of registers still to be summed).
+// Sum over the 32 lanes of each half-wave of an accumulator tile's rows: afterwards lanes li
+// and li ^ 16 hold the sum of register r = li & 15.  A reduce-scatter inside each 16-lane
+// row (each exchange halves the number of registers still to be summed) on DPP lane
+// exchanges - row_mirror (li ^ 15) and row_half_mirror (li ^ 7), valid pairings because
+// they come before the exchanges of the lower bits, then quad permutes (li ^ 2, li ^ 1) -
+// and one exchange between the two rows of the half-wave at the end.
+template <int CTRL>
+EDF_DEVICE float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 EDF_DEVICE float rowsum32(const f32x16& x, int li) {
   float a[8], b[4], c[2];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const bool hi = li & 16;
-    a[j] = (hi ? x[j + 8] : x[j]) + __shfl_xor(hi ? x[j] : x[j + 8], 16);
+    const bool hi = li & 8;
+    a[j] = (hi ? x[j + 8] : x[j]) + dpp<0x140>(hi ? x[j] : x[j + 8]);  // row_mirror
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const bool hi = li & 8;
-    b[j] = (hi ? a[j + 4] : a[j]) + __shfl_xor(hi ? a[j] : a[j + 4], 8);
+    const bool hi = li & 4;
+    b[j] = (hi ? a[j + 4] : a[j]) + dpp<0x141>(hi ? a[j] : a[j + 4]);  // row_half_mirror
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const bool hi = li & 4;
-    c[j] = (hi ? b[j + 2] : b[j]) + __shfl_xor(hi ? b[j] : b[j + 2], 4);
+    const bool hi = li & 2;
+    c[j] = (hi ? b[j + 2] : b[j]) + dpp<0x4E>(hi ? b[j] : b[j + 2]);  // quad_perm [2, 3, 0, 1]
   }
-  const bool hi = li & 2;
-  float d = (hi ? c[1] : c[0]) + __shfl_xor(hi ? c[0] : c[1], 2);
-  return d + __shfl_xor(d, 1);
+  const bool hi = li & 1;
+  const float d = (hi ? c[1] : c[0]) + dpp<0xB1>(hi ? c[0] : c[1]);  // quad_perm [1, 0, 3, 2]
+  return d + __shfl_xor(d, 16);
 }
 
 __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
@@ -981,12 +988,12 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
     for (int r = 0; r < 16; ++r) cs += z[r];
     cs += __shfl_xor(cs, 32);
     if (g == 0) atomicAdd(&dlg[s], -cs);
-    const int tr = 32 * I + d_row(li >> 1, g);
+    const int tr = 32 * I + d_row(li & 15, g);
     const float rs = rowsum32(z, li);
-    if ((li & 1) == 0) atomicAdd(&dlg[tr], rs);
+    if (li < 16) atomicAdd(&dlg[tr], rs);
     if (kind) {
       const float rb = rowsum32(sb, li);
-      if ((li & 1) == 0) atomicAdd(&dbt[tr], rb);
+      if (li < 16) atomicAdd(&dbt[tr], rb);
     }
   }
   // dh rows d_k = 32 w + li
