@@ -45,32 +45,69 @@ struct RStage {
   float a[CK], b[CK], g[CK];
 };
 
-// Zero beyond T and d; beyond T the gates are a = 1, b = g = 0, so a padding step is the
-// identity of the recurrence and of its adjoint.
+// A chunk's inputs loaded a chunk ahead into registers (raw values from clamped addresses:
+// no branch around a load, whose join would wait for it), then masked - zero beyond T and
+// d; beyond T the gates are a = 1, b = g = 0, so a padding step is the identity of the
+// recurrence and of its adjoint - and written to the other of two LDS stages once the
+// current chunk is done, so their latency hides under the chunk's steps (one barrier per
+// chunk).
 template <typename TT, int CK, int DP>
-EDF_DEVICE void rla_stage(RStage<CK, DP>& sm, const RLAArgs& p, long bh, int rb, int t0, bool grad) {
+struct RRegs {
+  static constexpr int EK = (CK * DP + 255) / 256;
+  static constexpr int EV = (CK * RLA_RB + 255) / 256;
+  TT k[EK], q[EK], v[EV], go[EV], a, b, g;
+};
+
+template <typename TT, int CK, int DP>
+EDF_DEVICE void rla_load(RRegs<TT, CK, DP>& R, const RLAArgs& p, long bh, int rb, int t0, bool grad) {
   const int b = (int)(bh / p.H), h = (int)(bh % p.H), d = p.d, tid = threadIdx.x;
-  for (int e = tid; e < CK * DP; e += 256) {
-    const int tt = e / DP, j = e % DP, t = t0 + tt;
-    const bool ok = t < p.T && j < d;
-    const long idx = (((long)b * p.T + t) * p.H + h) * d + j;
-    sm.k[tt][j] = ok ? ld((const TT*)p.k, idx) : 0.0f;
-    sm.q[tt][j] = ok ? ld((const TT*)p.q, idx) : 0.0f;
+#pragma unroll
+  for (int n = 0; n < RRegs<TT, CK, DP>::EK; ++n) {
+    const int e = min(tid + 256 * n, CK * DP - 1), tt = e / DP, j = e % DP;
+    const long idx = (((long)b * p.T + min(t0 + tt, p.T - 1)) * p.H + h) * d + min(j, d - 1);
+    R.k[n] = ((const TT*)p.k)[idx];
+    R.q[n] = ((const TT*)p.q)[idx];
   }
-  for (int e = tid; e < CK * RLA_RB; e += 256) {
-    const int tt = e / RLA_RB, ii = e % RLA_RB, i = rb * RLA_RB + ii, t = t0 + tt;
-    const bool ok = t < p.T && i < d;
-    const long idx = (((long)b * p.T + t) * p.H + h) * d + i;
-    sm.v[tt][ii] = ok ? ld((const TT*)p.v, idx) : 0.0f;
-    if (grad) sm.go[tt][ii] = ok ? ld((const TT*)p.dout, idx) : 0.0f;
+#pragma unroll
+  for (int n = 0; n < RRegs<TT, CK, DP>::EV; ++n) {
+    const int e = min(tid + 256 * n, CK * RLA_RB - 1), tt = e / RLA_RB, i = rb * RLA_RB + e % RLA_RB;
+    const long idx = (((long)b * p.T + min(t0 + tt, p.T - 1)) * p.H + h) * d + min(i, d - 1);
+    R.v[n] = ((const TT*)p.v)[idx];
+    if (grad) R.go[n] = ((const TT*)p.dout)[idx];
+  }
+  const long gi = ((long)b * p.T + min(t0 + tid % CK, p.T - 1)) * p.H + h;
+  R.a = ((const TT*)p.alpha)[gi];
+  R.b = ((const TT*)p.beta)[gi];
+  R.g = ((const TT*)p.gamma)[gi];
+}
+
+template <typename TT, int CK, int DP>
+EDF_DEVICE void rla_store(RStage<CK, DP>& sm, const RRegs<TT, CK, DP>& R, const RLAArgs& p, int rb, int t0,
+                          bool grad) {
+  const int d = p.d, tid = threadIdx.x;
+#pragma unroll
+  for (int n = 0; n < RRegs<TT, CK, DP>::EK; ++n) {
+    const int e = tid + 256 * n, tt = e / DP, j = e % DP;
+    if (e < CK * DP) {
+      const bool ok = t0 + tt < p.T && j < d;
+      sm.k[tt][j] = ok ? to_f32(R.k[n]) : 0.0f;
+      sm.q[tt][j] = ok ? to_f32(R.q[n]) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < RRegs<TT, CK, DP>::EV; ++n) {
+    const int e = tid + 256 * n, tt = e / RLA_RB, ii = e % RLA_RB, i = rb * RLA_RB + ii;
+    if (e < CK * RLA_RB) {
+      const bool ok = t0 + tt < p.T && i < d;
+      sm.v[tt][ii] = ok ? to_f32(R.v[n]) : 0.0f;
+      if (grad) sm.go[tt][ii] = ok ? to_f32(R.go[n]) : 0.0f;
+    }
   }
   if (tid < CK) {
-    const int t = t0 + tid;
-    const bool ok = t < p.T;
-    const long gi = ((long)b * p.T + t) * p.H + h;
-    sm.a[tid] = ok ? ld((const TT*)p.alpha, gi) : 1.0f;
-    sm.b[tid] = ok ? ld((const TT*)p.beta, gi) : 0.0f;
-    sm.g[tid] = ok ? ld((const TT*)p.gamma, gi) : 0.0f;
+    const bool ok = t0 + tid < p.T;
+    sm.a[tid] = ok ? to_f32(R.a) : 1.0f;
+    sm.b[tid] = ok ? to_f32(R.b) : 0.0f;
+    sm.g[tid] = ok ? to_f32(R.g) : 0.0f;
   }
 }
 
@@ -115,18 +152,23 @@ EDF_DEVICE void rla_step(float (&S)[DP / 16], float (&R)[DP / 16], const RStage<
 template <typename TT, int DP, int VAR, int CK>
 __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
   constexpr int NC = DP / 16;
-  __shared__ RStage<CK, DP> sm;
+  __shared__ RStage<CK, DP> sms[2];
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * RLA_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+  const int nch = (p.T + CK - 1) / CK;
   float S[NC], R[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) S[c] = R[c] = 0.0f;
-  for (int t0 = 0; t0 < p.T; t0 += CK) {
-    __syncthreads();
-    rla_stage<TT, CK, DP>(sm, p, bh, rb, t0, false);
-    __syncthreads();
+  RRegs<TT, CK, DP> G;
+  rla_load<TT, CK, DP>(G, p, bh, rb, 0, false);
+  rla_store<TT, CK, DP>(sms[0], G, p, rb, 0, false);
+  __syncthreads();
+  for (int chn = 0; chn < nch; ++chn) {
+    const int t0 = chn * CK;
+    const RStage<CK, DP>& sm = sms[chn & 1];
+    rla_load<TT, CK, DP>(G, p, bh, rb, min(t0 + CK, (nch - 1) * CK), false);  // next chunk (past the last: a reload)
 #pragma unroll
     for (int tt = 0; tt < CK; ++tt) {  // padding past T: identity steps (a = 1, b = g = 0, k = 0)
       rla_step<CK, DP, VAR>(S, R, sm, tt, tr, tc, p.clip);
@@ -146,6 +188,9 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
         cp[DP * DP + 16 * c] = R[c];
       }
     }
+    // the other stage was last read in the previous chunk, before the barrier below it
+    rla_store<TT, CK, DP>(sms[(chn + 1) & 1], G, p, rb, t0 + CK, false);
+    __syncthreads();
   }
 }
 
@@ -158,7 +203,7 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
 template <typename TT, int DP, int VAR>
 __global__ __launch_bounds__(256) void rla_bwd_kernel(const RLAArgs p) {
   constexpr int NC = DP / 16, CK = RLA_CK;
-  __shared__ RStage<CK, DP> sm;
+  __shared__ RStage<CK, DP> sms[2];
   __shared__ float red[2][RLA_RB][DP + 1];  // this step's per-row dq and dk terms
   __shared__ float reds[3][RLA_RB];         // and dalpha, dbeta, dgamma terms
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
@@ -171,20 +216,36 @@ __global__ __launch_bounds__(256) void rla_bwd_kernel(const RLAArgs p) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) dS[c] = dR[c] = 0.0f;
 
+  // chunk inputs and the checkpoints each chunk starts from, loaded a chunk ahead
+  RRegs<TT, CK, DP> G;
+  float cS[NC], cR[NC];
+  auto load_ck = [&](int ck) {
+    // chunk 0 starts from zero; its (unused) load address stays in bounds
+    const float* cp = p.ckpt + (((long)bh * p.nck + max(ck - 1, 0)) * 2) * DP * DP + (long)i * DP + tc;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      cS[c] = cp[16 * c];
+      cR[c] = cp[DP * DP + 16 * c];
+    }
+  };
+  rla_load<TT, CK, DP>(G, p, bh, rb, (p.nck - 1) * CK, true);
+  load_ck(p.nck - 1);
+  rla_store<TT, CK, DP>(sms[(p.nck - 1) & 1], G, p, rb, (p.nck - 1) * CK, true);
+  __syncthreads();
   for (int ck = p.nck - 1; ck >= 0; --ck) {
     const int t0 = ck * CK;
-    __syncthreads();
-    rla_stage<TT, CK, DP>(sm, p, bh, rb, t0, true);
-    __syncthreads();
+    const RStage<CK, DP>& sm = sms[ck & 1];
     float Sl[CK][NC], Rl[CK][NC];
     {
       float S[NC], R[NC];
-      const float* cp = p.ckpt + (((long)bh * p.nck + max(ck - 1, 0)) * 2) * DP * DP + (long)i * DP + tc;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        S[c] = ck > 0 ? cp[16 * c] : 0.0f;
-        R[c] = ck > 0 ? cp[DP * DP + 16 * c] : 0.0f;
+        S[c] = ck > 0 ? cS[c] : 0.0f;
+        R[c] = ck > 0 ? cR[c] : 0.0f;
       }
+      // the previous chunk's inputs and checkpoints load under this chunk's work
+      rla_load<TT, CK, DP>(G, p, bh, rb, max(ck - 1, 0) * CK, true);
+      load_ck(max(ck - 1, 0));
 #pragma unroll
       for (int tt = 0; tt < CK; ++tt) {
 #pragma unroll
@@ -260,6 +321,9 @@ __global__ __launch_bounds__(256) void rla_bwd_kernel(const RLAArgs p) {
       }
       __syncthreads();
     }
+    // the other stage was last read in the previous chunk, before this chunk's barriers
+    rla_store<TT, CK, DP>(sms[(ck + 1) & 1], G, p, rb, (ck - 1) * CK, true);
+    __syncthreads();
   }
 }
 
