@@ -39,18 +39,43 @@ struct TArgs {
   int T, D, nck;
 };
 
-template <typename TT, int DP>
-EDF_DEVICE void ttt_stage(float (*sx)[DP], const void* src, const TArgs& p, int b, int t0) {
-  for (int e = threadIdx.x; e < TTT_CK * DP; e += 256) {
-    const int tt = e / DP, j = e % DP, t = t0 + tt;
-    sx[tt][j] = t < p.T && j < p.D ? ld((const TT*)src, ((long)b * p.T + t) * p.D + j) : 0.0f;
-  }
+// Chunks of NA [B, T, D] inputs loaded a chunk ahead into registers (raw values from
+// clamped addresses: no branch around a load, whose join would wait for it), masked (zero
+// beyond T and D) and written to the other of two LDS stages once the current chunk is
+// done: their latency hides under the chunk's steps instead of sitting between two
+// barriers at its start.
+template <typename ST, int DP, int NA>
+struct TRegs {
+  static constexpr int E = (TTT_CK * DP + 255) / 256;
+  ST v[NA][E];
+};
+
+template <typename ST, int DP, int NA>
+EDF_DEVICE void ttt_load(TRegs<ST, DP, NA>& R, const void* const (&src)[NA], const TArgs& p, int b, int t0) {
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int n = 0; n < TRegs<ST, DP, NA>::E; ++n) {
+      const int e = min((int)threadIdx.x + 256 * n, TTT_CK * DP - 1), tt = e / DP, j = min(e % DP, p.D - 1);
+      R.v[a][n] = ((const ST*)src[a])[((long)b * p.T + min(t0 + tt, p.T - 1)) * p.D + j];
+    }
+}
+
+template <typename ST, int DP, int NA>
+EDF_DEVICE void ttt_store(float (*const (&dst)[NA])[DP], const TRegs<ST, DP, NA>& R, const TArgs& p, int t0) {
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int n = 0; n < TRegs<ST, DP, NA>::E; ++n) {
+      const int e = threadIdx.x + 256 * n, tt = e / DP, j = e % DP;
+      if (e < TTT_CK * DP) dst[a][tt][j] = t0 + tt < p.T && j < p.D ? to_f32(R.v[a][n]) : 0.0f;
+    }
 }
 
 template <typename TT, int DP>
 __global__ __launch_bounds__(256) void ttt_fwd_kernel(const TArgs p) {
   constexpr int NC = DP / 16, RPG = DP / 16;
-  __shared__ float sk[TTT_CK][DP], sq[TTT_CK][DP], sv[TTT_CK][DP], se[TTT_CK][DP];
+  __shared__ float stg[2][4][TTT_CK][DP];  // two stages of k, q, v, eta
   __shared__ float sg[DP], sb[DP];
   __shared__ float stat[2][16][3];  // per group: valid rows, mean, M2
   const int tid = threadIdx.x, g = tid >> 4, tc = tid & 15, b = blockIdx.x, D = p.D;
@@ -69,13 +94,22 @@ __global__ __launch_bounds__(256) void ttt_fwd_kernel(const TArgs p) {
     sg[j] = j < D ? ld((const TT*)p.ln_g, j) : 0.0f;
     sb[j] = j < D ? ld((const TT*)p.ln_b, j) : 0.0f;
   }
-  for (int t0 = 0; t0 < p.T; t0 += TTT_CK) {
-    __syncthreads();
-    ttt_stage<TT, DP>(sk, p.k, p, b, t0);
-    ttt_stage<TT, DP>(sq, p.q, p, b, t0);
-    ttt_stage<TT, DP>(sv, p.v, p, b, t0);
-    ttt_stage<TT, DP>(se, p.eta, p, b, t0);
-    __syncthreads();
+  const void* const srcs[4] = {p.k, p.q, p.v, p.eta};
+  TRegs<TT, DP, 4> R;
+  const int nch = (p.T + TTT_CK - 1) / TTT_CK;
+  {
+    float(*const d0[4])[DP] = {stg[0][0], stg[0][1], stg[0][2], stg[0][3]};
+    ttt_load<TT, DP, 4>(R, srcs, p, b, 0);
+    ttt_store<TT, DP, 4>(d0, R, p, 0);
+  }
+  __syncthreads();
+  for (int chn = 0; chn < nch; ++chn) {
+    const int t0 = chn * TTT_CK, cb = chn & 1;
+    float(*const sk)[DP] = stg[cb][0];
+    float(*const sq)[DP] = stg[cb][1];
+    float(*const sv)[DP] = stg[cb][2];
+    float(*const se)[DP] = stg[cb][3];
+    ttt_load<TT, DP, 4>(R, srcs, p, b, min(t0 + TTT_CK, (nch - 1) * TTT_CK));  // next chunk (past the last: a reload)
     for (int tt = 0; tt < TTT_CK && t0 + tt < p.T; ++tt) {
       const int t = t0 + tt, par = t & 1;
       float pred[RPG];
@@ -143,6 +177,13 @@ __global__ __launch_bounds__(256) void ttt_fwd_kernel(const TArgs p) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) cp[(g * RPG + rr) * DP + tc + 16 * c] = W[rr][c];
     }
+    // the other stage was last read in the previous chunk, before its steps' barriers
+    {
+      const int nb = cb ^ 1;
+      float(*const dn[4])[DP] = {stg[nb][0], stg[nb][1], stg[nb][2], stg[nb][3]};
+      ttt_store<TT, DP, 4>(dn, R, p, t0 + TTT_CK);
+    }
+    __syncthreads();
   }
 }
 
@@ -154,9 +195,8 @@ __global__ __launch_bounds__(256) void ttt_fwd_kernel(const TArgs p) {
 template <typename TT, int DP>
 __global__ __launch_bounds__(256) void ttt_bwd_kernel(const TArgs p) {
   constexpr int NC = DP / 16, RPG = DP / 16;
-  __shared__ float sk[TTT_CK][DP], sq[TTT_CK][DP], se[TTT_CK][DP], sdo[TTT_CK][DP], sx[TTT_CK][DP],
-      sr[TTT_CK][DP];
-  __shared__ float srs[TTT_CK];
+  __shared__ float stg[2][6][TTT_CK][DP];  // two stages of k, q, eta, dout, x_hat, err
+  __shared__ float srss[2][TTT_CK];
   __shared__ float sg[DP];
   __shared__ float stat[2][16][2];      // per group: sum dx, sum dx x_hat
   __shared__ float red[2][16][2][DP];   // per group: dq, dk partials
@@ -169,28 +209,59 @@ __global__ __launch_bounds__(256) void ttt_bwd_kernel(const TArgs p) {
     for (int c = 0; c < NC; ++c) dW[rr][c] = 0.0f;
   }
   for (int j = tid; j < DP; j += 256) sg[j] = j < D ? ld((const TT*)p.ln_g, j) : 0.0f;
+  // each chunk's inputs, per-step rstd and (DP <= 64: the registers allow it) the W it ends
+  // with load a chunk ahead
+  constexpr bool PRE_W = DP <= 64;
+  const void* const srct[4] = {p.k, p.q, p.eta, p.dout};
+  const void* const srcf[2] = {p.xh, p.err};
+  TRegs<TT, DP, 4> RT;
+  TRegs<float, DP, 2> RF;
+  float rsn = 0.0f, Wn[PRE_W ? RPG : 1][PRE_W ? NC : 1];
+  auto load_next = [&](int ck) {
+    ttt_load<TT, DP, 4>(RT, srct, p, b, ck * TTT_CK);
+    ttt_load<float, DP, 2>(RF, srcf, p, b, ck * TTT_CK);
+    rsn = p.rstd[(long)b * p.T + min(ck * TTT_CK + (int)(tid % TTT_CK), p.T - 1)];
+    if constexpr (PRE_W) {
+      const float* cp = p.ckpt + ((long)b * p.nck + ck) * DP * DP;
+#pragma unroll
+      for (int rr = 0; rr < RPG; ++rr)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) Wn[rr][c] = cp[(g * RPG + rr) * DP + tc + 16 * c];
+    }
+  };
+  auto store_next = [&](int ck, int sb) {
+    const int t0n = ck * TTT_CK;
+    float(*const dt[4])[DP] = {stg[sb][0], stg[sb][1], stg[sb][2], stg[sb][3]};
+    float(*const df[2])[DP] = {stg[sb][4], stg[sb][5]};
+    ttt_store<TT, DP, 4>(dt, RT, p, t0n);
+    ttt_store<float, DP, 2>(df, RF, p, t0n);
+    if (tid < TTT_CK) srss[sb][tid] = t0n + tid < p.T ? rsn : 0.0f;
+  };
+  load_next(p.nck - 1);
+  store_next(p.nck - 1, (p.nck - 1) & 1);
+  __syncthreads();
   for (int ck = p.nck - 1; ck >= 0; --ck) {
-    const int t0 = ck * TTT_CK;
-    {
+    const int t0 = ck * TTT_CK, cb = ck & 1;
+    float(*const sk)[DP] = stg[cb][0];
+    float(*const sq)[DP] = stg[cb][1];
+    float(*const se)[DP] = stg[cb][2];
+    float(*const sdo)[DP] = stg[cb][3];
+    float(*const sx)[DP] = stg[cb][4];
+    float(*const sr)[DP] = stg[cb][5];
+    const float* const srs = srss[cb];
+    if constexpr (PRE_W) {
+#pragma unroll
+      for (int rr = 0; rr < RPG; ++rr)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) W[rr][c] = Wn[rr][c];
+    } else {
       const float* cp = p.ckpt + ((long)b * p.nck + ck) * DP * DP;
 #pragma unroll
       for (int rr = 0; rr < RPG; ++rr)
 #pragma unroll
         for (int c = 0; c < NC; ++c) W[rr][c] = cp[(g * RPG + rr) * DP + tc + 16 * c];
     }
-    __syncthreads();
-    ttt_stage<TT, DP>(sk, p.k, p, b, t0);
-    ttt_stage<TT, DP>(sq, p.q, p, b, t0);
-    ttt_stage<TT, DP>(se, p.eta, p, b, t0);
-    ttt_stage<TT, DP>(sdo, p.dout, p, b, t0);
-    for (int e = tid; e < TTT_CK * DP; e += 256) {
-      const int tt = e / DP, j = e % DP, t = t0 + tt;
-      const bool ok = t < p.T && j < D;
-      sx[tt][j] = ok ? p.xh[((long)b * p.T + t) * D + j] : 0.0f;
-      sr[tt][j] = ok ? p.err[((long)b * p.T + t) * D + j] : 0.0f;
-    }
-    if (tid < TTT_CK) srs[tid] = t0 + tid < p.T ? p.rstd[(long)b * p.T + t0 + tid] : 0.0f;
-    __syncthreads();
+    load_next(max(ck - 1, 0));  // the previous chunk (for chunk 0, a reload)
     for (int tt = min(TTT_CK, p.T - t0) - 1; tt >= 0; --tt) {
       const int t = t0 + tt, par = t & 1;
       const long row0 = ((long)b * p.T + t) * D;
@@ -266,6 +337,9 @@ __global__ __launch_bounds__(256) void ttt_bwd_kernel(const TArgs p) {
         if (j < D) st((TT*)(qty == 0 ? p.dq : p.dk), row0 + j, acc);
       }
     }
+    // the other stage was last read in the previous chunk, before the barrier that ended it
+    store_next(max(ck - 1, 0), cb ^ 1);
+    __syncthreads();
   }
 #pragma unroll
   for (int rr = 0; rr < RPG; ++rr) {
