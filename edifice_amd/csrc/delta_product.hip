@@ -136,8 +136,10 @@ EDF_DEVICE void dp_normalize(DPStage<DP>& sm) {
   for (int c = 0; c < NC; ++c) sm.k[tt][l + 16 * c] *= inv;
 }
 
-// The backward stages each chunk at its start (its recomputed states hold too many
-// registers for the forward's loads a chunk ahead: they cost it an occupancy level).
+// The backward stages each chunk at its start. Its recomputed states hold too many
+// registers for the forward's loads a chunk ahead: at D = 128 they cost it an occupancy
+// level, and capped at two waves per SIMD (256 VGPRs, no spills) they gained nothing
+// (backward call 6.67 ms either way at 8x2048x2x8x128).
 template <typename TT, int DP>
 EDF_DEVICE void stage(DPStage<DP>& sm, const DPArgs& p, long bh, int rb, int t0, bool grad) {
   constexpr int NC = DP / 16;
