@@ -64,12 +64,16 @@ template <> EDF_DEVICE unsigned short bload<bf16>(rsrc_t r, unsigned off) {
 EDF_DEVICE float bits_f32(unsigned v) { return __builtin_bit_cast(float, v); }
 EDF_DEVICE float bits_f32(unsigned short v) { return __builtin_bit_cast(float, (unsigned)v << 16); }
 
-template <typename T> EDF_DEVICE void bstore(rsrc_t r, unsigned off, float v);
-template <> EDF_DEVICE void bstore<float>(rsrc_t r, unsigned off, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)off, 0, 0);
-}
-template <> EDF_DEVICE void bstore<bf16>(rsrc_t r, unsigned off, float v) {
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)v), r, (int)off, 0, 0);
+// AUX: the cache-policy immediate (BUF_NT marks a streaming store).  Two stores on the two
+// sides of a lane-divergent branch that differ only in their resource are merged by the
+// compiler into one store with a per-lane resource, which then runs once per distinct
+// resource in the wave; a different AUX keeps them apart.
+constexpr int BUF_NT = 2;
+template <typename T, int AUX = 0> EDF_DEVICE void bstore(rsrc_t r, unsigned off, float v) {
+  if constexpr (sizeof(T) == 4)
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, (int)off, 0, AUX);
+  else
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)v), r, (int)off, 0, AUX);
 }
 
 // ---- math -------------------------------------------------------------------

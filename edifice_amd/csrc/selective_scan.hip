@@ -122,9 +122,16 @@ __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ d
   if (lane == 0) dtm[row] = s / (float)dim;
 }
 
-// Padded length of an LDS row holding the N states of one (t, channel): one wave's writes
-// (16 channels x 4 states) and the 16-byte reads of consecutive channels are conflict-free.
+// Padded length of an LDS row holding the N states of one (t, channel): 16-byte reads of
+// the rows of 16 consecutive channels are conflict-free (PN / 4 odd), and so are one
+// wave's writes (16 channels x 4 states) with the slot swizzle below.
 template <int N> constexpr int ss_pn() { return N == 4 ? 12 : N + 4; }
+// A 32-lane half of a ds_write_b32 spreads over 32 banks (word address mod 32); the rows of
+// one wave's state-term writes (16 channels x states r, r + 1 per half) lie PN words apart,
+// and PN * 8 = 0 mod 32 for every PN above, so channels j and j + 8 would share a bank.
+// Channels with bit 3 set keep their states in the row at s ^ 2 (rows hold N >= 4 states;
+// sums over a whole row are unchanged).  16-byte reads of whole rows are untouched.
+template <int N> EDF_DEVICE int ss_swz(int cl) { return N >= 4 ? (cl & 8) >> 2 : 0; }
 constexpr int mod64_to(int v, int r) { return v + ((r - v % 64) % 64 + 64) % 64; }  // smallest >= v, = r mod 64
 
 // ---------------------------------------------------------------------------
@@ -163,6 +170,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_fwd_kernel(const SSArgs p
   const int g = w % G, sg = w / G;          // this wave's channel group and state group
   const int s = sg * SW + lane / CW;        // this lane's state
   const int cl = g * CW + lane % CW;        // this lane's channel within the tile
+  const int sx = s ^ ss_swz<N>(cl);         // its slot in a C h row
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int b = logical / p.ntile, tile = logical % p.ntile;
   const int c = tile * CT + cl;
@@ -273,7 +281,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_fwd_kernel(const SSArgs p
           constexpr int v = decltype(vi)::value, tt = 4 * q + v;
           const float a = fast_exp2(dcv[v] * A2);
           h = fmaf(a, h, row_bcast<tt>(rb) * dxv[v]);
-          if (YSUM) s_yp[buf][(tt * CT + cl) * PN + s] = row_bcast<tt>(rc) * h;
+          if (YSUM) s_yp[buf][(tt * CT + cl) * PN + sx] = row_bcast<tt>(rc) * h;
         });
       });
       if (p.ckpt != nullptr)
@@ -334,8 +342,8 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   constexpr int NE = CK * CT;               // staged (t, channel) elements per chunk
   constexpr int EPT = (NE + NT - 1) / NT;
   // px / pa tile [qty][t][channel][state]: a lane's state-sum item reads one contiguous row;
-  // PN makes the rows of one wave's writes and the 16-byte reads of consecutive channels
-  // conflict-free, QP puts the two quantities of one (t, channel) on different banks
+  // PN and the slot swizzle make one wave's writes and the 16-byte reads of consecutive
+  // channels conflict-free, QP puts the two quantities of one (t, channel) on different banks
   constexpr int PN = ss_pn<N>();
   constexpr int QP = mod64_to(TS * CT * PN, 32);
   // dC / dB tile [qty][state][t][group][CW + 4]: a channel-group item reads one contiguous
@@ -345,6 +353,12 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   constexpr int NA = 2 * TS * CT;           // state sums per round: (t, channel, dx | ddt term)
   constexpr int NB = 2 * TS * N * G;        // channel-group sums per round: (qty, t, state, group)
   constexpr int NC = 2 * TS * N;            // partials per round: (qty, t, state)
+  // A 16-lane group of 16-byte reads spreads over 64 banks; the runs of one row are CWP
+  // (= 4 mod 8) words apart, so 16 consecutive runs are conflict-free, but a group that
+  // crosses from one row into the next (SSR = 16 mod 32 words on, for the writes) is not
+  // when a row holds IPB = 8 mod 16 runs: those pair rows A and A + 2 instead.
+  constexpr int IPB = TS * G;
+  constexpr bool BC_PAIR = CW == 16 && IPB % 16 == 8 && N % 2 == 0;
   static_assert(NT % CT == 0, "a thread's staged elements share one channel");
   // staged per chunk, double-buffered: clip(dt) with the sign bit set where the raw dt lies
   // outside [DT_MIN, DT_MAX] (no gradient), dt_b x, dy (after the gate)
@@ -352,7 +366,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   __shared__ float s_dtm[MEAN ? 2 : 1][CK];
   __shared__ __align__(16) float s_pq[2 * QP];
   __shared__ __align__(16) float s_bc[2 * N * SSR];
-  __shared__ float s_red[2][2][TS][N][G];
+  __shared__ float s_red[2][2][N][TS][G];
   __shared__ float s_m[MEAN ? 2 : 1][MEAN ? TS : 1][CT];
   __shared__ float s_Dv[CT];
 
@@ -369,6 +383,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   const int g = w % G, sg = w / G;
   const int s = sg * SW + lane / CW;
   const int cl = g * CW + lane % CW;
+  const int sx = s ^ ss_swz<N>(cl);  // this lane's slot in a px / ga row
   const int logical = remap_xcd(blockIdx.x, gridDim.x);
   const int b = logical / p.ntile, tile = logical % p.ntile;
   const int c = tile * CT + cl;
@@ -401,10 +416,10 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   float aw[AW ? N : 1];
   if constexpr (AW) {
     static_assert(NT % (2 * CT) == 0, "state-sum items of a thread share one channel");
-    const int wc = tile * CT + (tid >> 1) % CT;
+    const int wl = (tid >> 1) % CT, wc = tile * CT + wl, wx = ss_swz<N>(wl);
 #pragma unroll
-    for (int sn = 0; sn < N; ++sn)
-      aw[sn] = aq == 0 ? 1.0f : ((wc < dim && sn < ns) ? ld(Am, (long)wc * ns + sn) : 0.0f);
+    for (int sn = 0; sn < N; ++sn)  // slot sn of the channel's row holds state sn ^ wx
+      aw[sn] = aq == 0 ? 1.0f : ((wc < dim && (sn ^ wx) < ns) ? ld(Am, (long)wc * ns + (sn ^ wx)) : 0.0f);
   }
 
   const long rowbase = (long)b * seq * dim;
@@ -491,9 +506,9 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
     for (int it = tid; it < NC + (MEAN ? TS : 0); it += NT) {
       if (it < NC) {
         const int sn = it % N, tl = (it / N) % TS, q = it / (N * TS);
-        float v = s_red[par][q][tl][sn][0];
+        float v = s_red[par][q][sn][tl][0];
 #pragma unroll
-        for (int gg = 1; gg < G; ++gg) v += s_red[par][q][tl][sn][gg];
+        for (int gg = 1; gg < G; ++gg) v += s_red[par][q][sn][tl][gg];
         const int t = ts0 + tl;
         if (t < seq) p.part_bc[((((long)tile * p.batch + b) * seq + t) * 2 + q) * N + sn] = v;
       } else if (MEAN) {
@@ -559,8 +574,8 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
           dh *= as[tt];
           const float ga = dh * (tt > 0 ? hs[tt > 0 ? tt - 1 : 0] : h0);
           dA = fmaf(ga, fabsf(dcs[tt]), dA);
-          s_pq[(tl * CT + cl) * PN + s] = px;
-          s_pq[QP + (tl * CT + cl) * PN + s] = AW ? ga : ga * A1;
+          s_pq[(tl * CT + cl) * PN + sx] = px;
+          s_pq[QP + (tl * CT + cl) * PN + sx] = AW ? ga : ga * A1;
           s_bc[s * SSR + tl * CTP + g * CWP + lane % CW] = gC;
           s_bc[N * SSR + s * SSR + tl * CTP + g * CWP + lane % CW] = gB;
         });
@@ -618,13 +633,34 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
           if (MEAN) s_m[MEAN ? par : 0][MEAN ? tl : 0][ac] = pxs * xv;
         } else {
           const float mk = dcr > 0.0f ? 1.0f : 0.0f;
-          bstore<TI>(r_ddt, off, mk * (MEAN ? pas : fmaf(pxs, xv, pas)));
+          bstore<TI, BUF_NT>(r_ddt, off, mk * (MEAN ? pas : fmaf(pxs, xv, pas)));
         }
       }
 #pragma unroll 1
       for (int it = tid; it < NB; it += NT) {
-        const int gg = it % G, tl = (it / G) % TS, sn = (it / (G * TS)) % N, q = it / (G * TS * N);
-        const float* src = &s_bc[(q * N + sn) * SSR + tl * CTP + gg * CWP];
+        int blk, i;  // item (blk = (qty, state) row of the tile, i = (t, group) run in it)
+        if constexpr (BC_PAIR) {
+          // 16-lane groups: rows A and A + 2 (2 SSR = 32 mod 64 words apart) each fill
+          // IPB / 16 whole groups, and their last 8 runs share one group
+          constexpr int F = IPB / 16;
+          const int pi = it / (2 * IPB), u = it % (2 * IPB);
+          const int A = 4 * (pi >> 1) + (pi & 1);
+          if (u < 16 * F) {
+            blk = A;
+            i = u;
+          } else if (u < 32 * F) {
+            blk = A + 2;
+            i = u - 16 * F;
+          } else {
+            blk = u - 32 * F < 8 ? A : A + 2;
+            i = 16 * F + (u & 7);
+          }
+        } else {
+          blk = it / IPB;
+          i = it % IPB;
+        }
+        const int q = blk / N, sn = blk % N, tl = i / G, gg = i % G;
+        const float* src = &s_bc[blk * SSR + tl * CTP + gg * CWP];
         const float4 f0 = *reinterpret_cast<const float4*>(src);
         float v = (f0.x + f0.y) + (f0.z + f0.w);
 #pragma unroll
@@ -632,7 +668,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
           const float4 f = *reinterpret_cast<const float4*>(src + cc);
           v += (f.x + f.y) + (f.z + f.w);
         }
-        s_red[par][q][tl][sn][gg] = v;
+        s_red[par][q][sn][tl][gg] = v;
       }
       if (prev_par >= 0) finish_round(prev_par, prev_ts);
       prev_par = par;
