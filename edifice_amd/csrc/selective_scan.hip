@@ -692,23 +692,38 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   }
 }
 
-// dB, dC = sum over channel tiles; partials carry NP (padded) states, outputs ns
+// dB, dC = sum over channel tiles, in tile order; partials carry NP (padded) states, outputs
+// ns.  VEC = 4 (NP >= 2, so 2 NP and the partial stride are multiples of 4): a thread sums
+// four consecutive (row, qty, n) entries with 16-byte loads, eight tiles' loads in flight.
+template <int VEC>
 __global__ __launch_bounds__(256) void ss_reduce_bc_kernel(const float* __restrict__ part, float* __restrict__ dB,
                                                            float* __restrict__ dC, int ntile, long rows, int NP,
                                                            int ns) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // over rows * 2NP
+  typedef float vec_t __attribute__((ext_vector_type(VEC)));
   const long total = rows * 2 * NP;
-  if (i >= total) return;
-  const long row = i / (2 * NP);
-  const int r = (int)(i % (2 * NP));
-  const int qty = r / NP, nn = r % NP;
-  if (nn >= ns) return;
-  float acc = 0.0f;
-  for (int tl = 0; tl < ntile; ++tl) acc += part[(long)tl * total + i];
-  if (qty == 0) {
-    if (dC) dC[row * ns + nn] = acc;
-  } else {
-    if (dB) dB[row * ns + nn] = acc;
+  const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * VEC;  // over rows * 2NP
+  if (i0 >= total) return;
+  const vec_t* p = reinterpret_cast<const vec_t*>(part + i0);
+  const long stride = total / VEC;
+  vec_t acc = (vec_t)0.0f;
+  int tl = 0;
+  for (; tl + 8 <= ntile; tl += 8) {
+    vec_t v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[(long)(tl + k) * stride];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc += v[k];
+  }
+  for (; tl < ntile; ++tl) acc += p[(long)tl * stride];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    const long i = i0 + k;
+    const long row = i / (2 * NP);
+    const int r = (int)(i % (2 * NP));
+    const int qty = r / NP, nn = r % NP;
+    if (nn >= ns) continue;
+    float* dst = qty == 0 ? dC : dB;
+    if (dst) dst[row * ns + nn] = acc[k];
   }
 }
 
@@ -1083,8 +1098,12 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   const int np = padded_state(state);
   if (grad_B || grad_C) {
     const long total = rows * 2 * np;
-    ss_reduce_bc_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(a.part_bc, (float*)grad_B, (float*)grad_C,
-                                                                        a.ntile, rows, np, state);
+    if (np >= 2 && ((uintptr_t)a.part_bc & 15) == 0)  // the caller's workspace may sit at any offset
+      ss_reduce_bc_kernel<4><<<(unsigned)((total / 4 + 255) / 256), 256, 0, s>>>(a.part_bc, (float*)grad_B,
+                                                                               (float*)grad_C, a.ntile, rows, np, state);
+    else
+      ss_reduce_bc_kernel<1><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(a.part_bc, (float*)grad_B,
+                                                                             (float*)grad_C, a.ntile, rows, np, state);
     rc = check_launch("selective scan dB/dC reduction");
     if (rc) return rc;
   }
