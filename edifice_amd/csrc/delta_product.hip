@@ -193,7 +193,7 @@ template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dp_fwd_kernel(const DPArgs p) {
   constexpr int NC = DP / 16;
   __shared__ DPStage<DP> sms[2];
-  __shared__ float redo[DPR_RB][DP + 1];  // a closing sub-step's per-row output terms
+  __shared__ float redo[DPR_RB][row16_stride(DP)];  // a closing sub-step's per-row output terms
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * DPR_RB + tr;
@@ -286,7 +286,7 @@ template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
   constexpr int NC = DP / 16;
   __shared__ DPStage<DP> sm;
-  __shared__ float redk[DPR_RB][DP + 1];  // this step's per-row key-gradient terms
+  __shared__ float redk[DPR_RB][row16_stride(DP)];  // this step's per-row key-gradient terms
   __shared__ float redb[DPR_RB];
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;

@@ -175,7 +175,7 @@ template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
   constexpr int NC = DP / 16;
   __shared__ Stage<DP> sms[2];
-  __shared__ float red[2][RB][DP + 1];  // per-row column partials: [qty][tr][j]
+  __shared__ float red[2][RB][row16_stride(DP)];  // per-row column partials: [qty][tr][j]
   __shared__ float reda[2][RB];
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;

@@ -76,6 +76,12 @@ template <typename T, int AUX = 0> EDF_DEVICE void bstore(rsrc_t r, unsigned off
     __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)v), r, (int)off, 0, AUX);
 }
 
+// Row stride (floats) of an LDS tile of 16 rows x dp columns that lanes write as (row =
+// tid / 16, column = tid % 16 + 16 c): a ds_write_b32 resolves 32 lanes at a time over 32
+// banks (word address mod 32), so the two rows of one half-wave sit 16 words apart mod 32;
+// reads along a row stay contiguous.
+constexpr int row16_stride(int dp) { return dp + (48 - dp % 32) % 32; }
+
 // ---- math -------------------------------------------------------------------
 constexpr float LOG2E = 1.4426950408889634f;
 

@@ -204,7 +204,7 @@ template <typename TT, int DP, int VAR>
 __global__ __launch_bounds__(256) void rla_bwd_kernel(const RLAArgs p) {
   constexpr int NC = DP / 16, CK = RLA_CK;
   __shared__ RStage<CK, DP> sms[2];
-  __shared__ float red[2][RLA_RB][DP + 1];  // this step's per-row dq and dk terms
+  __shared__ float red[2][RLA_RB][row16_stride(DP)];  // this step's per-row dq and dk terms
   __shared__ float reds[3][RLA_RB];         // and dalpha, dbeta, dgamma terms
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   const long bh = blockIdx.x;
