@@ -52,6 +52,9 @@ SIGNATURES = {
     "edf_fused_fox_attention": (I, [P, P, P, P, P, P, P, I, I, I, I, I]),
     "edf_fused_fox_attention_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_fox_attention_backward_workspace_bytes": (S, [I, I, I, I]),
+    "edf_causal_conv1d_silu": (I, [P, P, I, P, P, P, I, I, I, I, I]),
+    "edf_causal_conv1d_silu_backward_workspace_bytes": (S, [I, I, I, I]),
+    "edf_causal_conv1d_silu_backward": (I, [P, P, I, P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_laser_attention_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_laser_attention": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_laser_attention_backward_workspace_bytes": (S, [I, I, I, I, I]),

@@ -39,27 +39,6 @@ LN_EPS = 1.0e-5       # layer-norm epsilon the reference fixtures were generated
 KEY_NORM_EPS = 1.0e-6  # inside the sqrt of the key L2 norm (delta_net.ex:291, gated_delta_net.ex:387)
 
 
-def _causal_depthwise_conv(conv: nn.Conv1d, x: torch.Tensor) -> torch.Tensor:
-    """[B, T, C] -> [B, T, C]: depthwise conv with conv_size - 1 steps of left padding,
-    y[t, c] = bias[c] + sum_j w[c, j] x[t - (K - 1) + j, c].
-
-    Computed as K shifted multiply-adds in (at least) float32 over the channel-contiguous layout
-    (bandwidth-bound elementwise work) rather than through the convolution library,
-    whose depthwise bf16 path falls back to naive kernels; the result is cast back to the
-    input dtype.  Same parameters (the nn.Conv1d's weight [C, 1, K] and bias) and the
-    same arithmetic as the reference's padded depthwise conv."""
-    seq, ksz = x.shape[1], conv.kernel_size[0]
-    acc = torch.promote_types(x.dtype, torch.float32)
-    w = conv.weight[:, 0, :].to(acc)  # [C, K]
-    xp = F.pad(x.to(acc), (0, 0, ksz - 1, 0))  # left-pad time
-    y = xp[:, ksz - 1:ksz - 1 + seq] * w[:, ksz - 1]
-    for j in range(ksz - 1):
-        y = y + xp[:, j:j + seq] * w[:, j]
-    if conv.bias is not None:
-        y = y + conv.bias.to(acc)
-    return y.to(x.dtype)
-
-
 def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:
     bsz, seq, hid = t.shape
     return t.reshape(bsz, seq, num_heads, hid // num_heads).contiguous()
@@ -108,13 +87,17 @@ class MambaBlock(nn.Module):
         self.register_buffer("A", a[None, :].expand(inner, state_size).contiguous(), persistent=False)
 
     def forward(self, x):
-        xz = self.in_proj(self.norm(x))
-        xb, zb = xz[..., : self.inner], xz[..., self.inner:]
-        xa = F.silu(_causal_depthwise_conv(self.dw_conv, xb))
+        # in_proj's two halves as two products over its weight rows: x and z come out
+        # contiguous, and their gradients land in one buffer each (slices of one [.., 2 inner]
+        # output would each be scattered into a zero-filled full-size gradient)
+        n, w, bias = self.norm(x), self.in_proj.weight, self.in_proj.bias
+        xb = F.linear(n, w[: self.inner], None if bias is None else bias[: self.inner])
+        zb = F.linear(n, w[self.inner:], None if bias is None else bias[self.inner:])
+        xa = fs.causal_conv1d_silu(xb, self.dw_conv.weight, self.dw_conv.bias)
         bc = self.bc_proj(xa).float()
         b, c = bc[..., : self.state_size].contiguous(), bc[..., self.state_size:].contiguous()
         dt = F.softplus(self.dt_proj(self.dt_rank_proj(xa)))
-        y = fs.selective_scan(xa.contiguous(), dt.contiguous(), self.A.float(), b, c, None, zb.contiguous(),
+        y = fs.selective_scan(xa, dt.contiguous(), self.A.float(), b, c, None, zb,
                               dt_mode="mean")
         return self.out_proj(y)
 
@@ -156,7 +139,7 @@ class GatedDeltaNetLayer(nn.Module):
         bsz, seq, hid = x.shape
         h = self.norm(x)
         if self.short_conv is not None:
-            h = F.silu(_causal_depthwise_conv(self.short_conv, h))
+            h = fs.causal_conv1d_silu(h, self.short_conv.weight, self.short_conv.bias)
         q, k, v, bpre, apre, gpre = torch.split(self.qkvbag_proj(h), hid, dim=-1)
         nh = self.num_heads
         alpha = _heads(torch.sigmoid(apre), nh).mean(-1).contiguous()

@@ -286,6 +286,67 @@ def gru_block(input, weights, h0, num_layers: int):
 
 
 # ---------------------------------------------------------------------------
+# Causal depthwise conv1d + SiLU (block callers)
+# ---------------------------------------------------------------------------
+
+def _conv_operands(x, weight, bias):
+    if x.dim() != 3 or x.stride(2) != 1:
+        raise EdificeHipError(f"x must be [B, T, C] with contiguous channels, got shape {tuple(x.shape)}")
+    bsz, seq, ch = x.shape
+    if seq > 1 and x.stride(0) != seq * x.stride(1):
+        x = x.contiguous()  # rows of one batch element must be equally spaced across batches
+    w = weight.reshape(weight.shape[0], -1).contiguous()
+    _shape("weight", w, (ch, w.shape[1]))
+    b = _c(bias)
+    _shape("bias", b, (ch,))
+    _dev(w, b)
+    if not x.is_cuda:
+        raise EdificeHipError("edifice_amd ops need GPU tensors (no CPU fallback)")
+    _same(x, w, b)
+    return x, w, b, bsz, seq, ch, w.shape[1], (x.stride(1) if seq > 1 else ch)
+
+
+class _CausalConvSilu(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        x, w, b, bsz, seq, ch, k, xs = _conv_operands(x, weight, bias)
+        out = torch.empty((bsz, seq, ch), dtype=x.dtype, device=x.device)
+        nat.call("edf_causal_conv1d_silu", _stream(), _p(x), xs, _p(w), _p(b), _p(out), bsz, seq, ch, k,
+                 dtype_flag(x))
+        ctx.save_for_backward(x, w, b)
+        ctx.wshape, ctx.has_bias = weight.shape, bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, b = ctx.saved_tensors
+        bsz, seq, ch = x.shape
+        k = w.shape[1]
+        xs = x.stride(1) if seq > 1 else ch
+        dy = dy.contiguous().to(x.dtype)
+        dx = torch.empty((bsz, seq, ch), dtype=x.dtype, device=x.device)
+        dw = torch.empty_like(w)
+        db = torch.empty_like(b) if ctx.has_bias else None
+        wsb = nat.query("edf_causal_conv1d_silu_backward_workspace_bytes", bsz, seq, ch, k)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=x.device)
+        nat.call("edf_causal_conv1d_silu_backward", _stream(), _p(x), xs, _p(w), _p(b), _p(dy), _p(dx), _p(dw),
+                 _p(db), _p(ws), wsb, bsz, seq, ch, k, dtype_flag(x))
+        return dx, dw.reshape(ctx.wshape), db
+
+
+def causal_conv1d_silu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor = None) -> torch.Tensor:
+    """silu(causal depthwise conv1d(x)) over time: the Mamba block's x branch
+    (common.ex:251-252, ``build_depthwise_conv1d`` common.ex:298-309) and the GatedDeltaNet
+    short convolution (gated_delta_net.ex:239-245).
+
+    x: [B, T, C] with contiguous channels (a column slice of a wider projection is read in
+    place); weight: nn.Conv1d's [C, 1, K] (or [C, K]); bias: [C] or None; one dtype.
+    y[t] = silu(bias + sum_j w[j] x[t - (K - 1) + j]), x = 0 before t = 0, f32 inside.
+    """
+    return _CausalConvSilu.apply(x, weight, bias)
+
+
+# ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------
 

@@ -448,6 +448,29 @@ int edf_fused_delta_rule_scan_backward_saved(void* stream, const void* q, const 
                                              int batch, int seq_len, int num_heads, int head_dim, int dtype,
                                              int beta_mode);
 
+/* ------------------------------------------------------------------------
+ * Causal depthwise conv1d + bias + SiLU (block callers)
+ *   y[b, t, c] = silu(bias[c] + sum_{j < K} w[c, j] x[b, t - (K - 1) + j, c]), x = 0 before
+ *   t = 0; x [B, T, C] with row stride x_row_stride (>= C) elements, so a column slice of a
+ *   wider projection output needs no copy; out / grad_out / grad_x [B, T, C] contiguous;
+ *   weight [C, K] (nn.Conv1d's [C, 1, K]), bias [C] or NULL; all in dtype; 1 <= K <= 8.
+ *   Replaces the Mamba block's x-branch convolution and its activation,
+ *   Axon.conv(..., padding: [{K - 1, 0}], feature_group_size: C) + Axon.activation(:silu)
+ *   (lib/edifice/ssm/common.ex:251-252, 298-309), and the GatedDeltaNet short convolution
+ *   (lib/edifice/recurrent/gated_delta_net.ex:239-245).
+ * ------------------------------------------------------------------------ */
+int edf_causal_conv1d_silu(void* stream, const void* x, int x_row_stride, const void* weight, const void* bias,
+                           void* out, int batch, int seq_len, int channels, int kernel_size, int dtype);
+
+/* Gradients of edf_causal_conv1d_silu (the reference takes them by autodiff of the Axon
+ * layers): grad_x [B, T, C], grad_weight [C, K] and grad_bias [C] (either may be NULL),
+ * summed in a fixed order; workspace edf_causal_conv1d_silu_backward_workspace_bytes(). */
+size_t edf_causal_conv1d_silu_backward_workspace_bytes(int batch, int seq_len, int channels, int kernel_size);
+int edf_causal_conv1d_silu_backward(void* stream, const void* x, int x_row_stride, const void* weight,
+                                    const void* bias, const void* grad_out, void* grad_x, void* grad_weight,
+                                    void* grad_bias, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                    int channels, int kernel_size, int dtype);
+
 /* Diagnostic: C[32][32] = A[32][16] * B[16][32] (bf16 in, f32 out, row-major) with one
  * v_mfma_f32_32x32x16_bf16, using the lane layout the attention and delta-rule kernels
  * assume.  No reference counterpart; used by the GPU tests to pin that layout. */

@@ -177,6 +177,11 @@ class _OracleOps:
         assert causal
         return ob._OracleCausalAttention.apply(q, k, v)
 
+    @staticmethod
+    def causal_conv1d_silu(x, weight, bias=None):
+        from tests.gpu_util import torch_causal_conv_silu
+        return torch_causal_conv_silu(x, weight, bias)
+
 
 def test_c5_hybrid_decoder_bf16_matches_oracle_ops(monkeypatch):
     """Config 5's model at reduced size in bfloat16 (the benchmark's precision): the same bf16
