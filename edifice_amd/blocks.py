@@ -284,4 +284,4 @@ class HybridDecoder(nn.Module):
     def loss(self, tokens: torch.Tensor) -> torch.Tensor:
         """Mean next-token cross entropy over tokens[:, 1:] (logits reduced in float32)."""
         logits = self.forward(tokens[:, :-1])
-        return F.cross_entropy(logits.float().reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1))
+        return fs.cross_entropy(logits.reshape(-1, logits.shape[-1]), tokens[:, 1:].reshape(-1))

@@ -347,6 +347,47 @@ def causal_conv1d_silu(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
 
 
 # ---------------------------------------------------------------------------
+# Softmax cross entropy (block callers' loss)
+# ---------------------------------------------------------------------------
+
+class _CrossEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits, targets):
+        logits, targets = logits.contiguous(), targets.contiguous()
+        _dev(logits, targets)
+        _rank("logits", logits, 2)
+        rows, vocab = logits.shape
+        _shape("targets", targets, (rows,))
+        if targets.dtype != torch.int64:
+            raise EdificeHipError(f"targets must be int64, got {targets.dtype}")
+        loss_rows = torch.empty(rows, dtype=torch.float32, device=logits.device)
+        lse = torch.empty(rows, dtype=torch.float32, device=logits.device)
+        nat.call("edf_cross_entropy", _stream(), _p(logits), _p(targets), _p(loss_rows), _p(lse), rows, vocab,
+                 dtype_flag(logits))
+        ctx.save_for_backward(logits, targets, lse)
+        return loss_rows.mean()
+
+    @staticmethod
+    def backward(ctx, grad):
+        logits, targets, lse = ctx.saved_tensors
+        rows, vocab = logits.shape
+        grad = grad.reshape(1).to(torch.float32).contiguous()
+        dlogits = torch.empty_like(logits)
+        nat.call("edf_cross_entropy_backward", _stream(), _p(logits), _p(targets), _p(lse), _p(grad), 1.0 / rows,
+                 _p(dlogits), rows, vocab, dtype_flag(logits))
+        return dlogits, None
+
+
+def cross_entropy(logits: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+    """Mean softmax cross entropy of ``logits`` [N, V] (float32 or bfloat16, reduced in float32)
+    against int64 ``targets`` [N]: the decoder models' next-token loss, as
+    ``F.cross_entropy(logits.float(), targets)`` computes it, without a float32 copy of the
+    logits or of their gradient.  Targets outside [0, V) contribute 0 (the mean still divides
+    by N)."""
+    return _CrossEntropy.apply(logits, targets)
+
+
+# ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------
 

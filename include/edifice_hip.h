@@ -32,6 +32,7 @@
 #define EDIFICE_HIP_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -470,6 +471,20 @@ int edf_causal_conv1d_silu_backward(void* stream, const void* x, int x_row_strid
                                     const void* bias, const void* grad_out, void* grad_x, void* grad_weight,
                                     void* grad_bias, void* workspace, size_t workspace_bytes, int batch, int seq_len,
                                     int channels, int kernel_size, int dtype);
+
+/* ------------------------------------------------------------------------
+ * Softmax cross entropy over logits (block callers: the LM-head loss of the decoder
+ * models; the reference takes it from Axon's loss inside the compiled training step)
+ *   logits [rows, vocab] in dtype, targets [rows] int64; loss_rows[n] = lse[n] -
+ *   logits[n, targets[n]] and lse [rows] in f32 (rows whose target lies outside [0, vocab)
+ *   give loss 0 and gradient 0).  The backward writes grad_logits [rows, vocab] in dtype:
+ *   (softmax - onehot) * (*grad_loss) * inv_rows, with grad_loss a device scalar (f32).
+ * ------------------------------------------------------------------------ */
+int edf_cross_entropy(void* stream, const void* logits, const int64_t* targets, float* loss_rows, float* lse,
+                      int rows, int vocab, int dtype);
+int edf_cross_entropy_backward(void* stream, const void* logits, const int64_t* targets, const float* lse,
+                               const float* grad_loss, float inv_rows, void* grad_logits, int rows, int vocab,
+                               int dtype);
 
 /* Diagnostic: C[32][32] = A[32][16] * B[16][32] (bf16 in, f32 out, row-major) with one
  * v_mfma_f32_32x32x16_bf16, using the lane layout the attention and delta-rule kernels

@@ -178,6 +178,10 @@ class _OracleOps:
         return ob._OracleCausalAttention.apply(q, k, v)
 
     @staticmethod
+    def cross_entropy(logits, targets):
+        return torch.nn.functional.cross_entropy(logits.float(), targets)
+
+    @staticmethod
     def causal_conv1d_silu(x, weight, bias=None):
         from tests.gpu_util import torch_causal_conv_silu
         return torch_causal_conv_silu(x, weight, bias)
