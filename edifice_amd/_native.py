@@ -68,6 +68,7 @@ SIGNATURES = {
     "edf_fused_delta_rule_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_fused_gated_delta_net_scan_backward": (
         I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
+    "edf_delta_rule_forward_context_bytes": (S, [I, I, I, I, I, I]),
     "edf_delta_rule_saved_backward_workspace_bytes": (S, [I, I, I, I, I, I]),
     "edf_fused_delta_rule_scan_backward_saved": (
         I, [P, P, P, P, P, P, P, P, P, P, P, P, P, S, P, S, I, I, I, I, I, I]),

@@ -7,12 +7,14 @@
 
 namespace edf {
 size_t dr_seq_backward_workspace_bytes(int batch, int heads, int seq, int d);
+size_t dr_seq_context_bytes(int batch, int heads, int seq, int d);
 int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
-               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head, int alpha_per_row);
+               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head, int alpha_per_row,
+               float* context);
 int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
                         const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
                         void* dalpha, void* workspace, int batch, int seq, int heads, int d, int dtype,
-                        int beta_per_head, int alpha_per_row);
+                        int beta_per_head, int alpha_per_row, const float* context);
 bool dr_chunk_eligible(int seq, int d, int dtype, int beta_per_head);
 size_t dr_chunk_workspace_bytes(int batch, int seq, int heads, int d);
 int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
@@ -50,7 +52,11 @@ int fwd(void* stream, const void* q, const void* k, const void* v, const void* b
     EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
     return dr_chunk_run(stream, q, k, v, beta, alpha, out, workspace, batch, seq, heads, d);
   }
-  return dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq, heads, d, dtype, per_head, 0);
+  // per-step path: a workspace of edf_delta_rule_forward_context_bytes() (optional) also
+  // receives the states every 16 steps, which the saved backward then reads
+  const bool keep = workspace && ws_bytes >= dr_seq_context_bytes(batch, heads, seq, d);
+  return dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq, heads, d, dtype, per_head, 0,
+                    keep ? (float*)workspace : nullptr);
 }
 
 int bwd(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
@@ -70,7 +76,7 @@ int bwd(void* stream, const void* q, const void* k, const void* v, const void* b
   const size_t need = dr_seq_backward_workspace_bytes(batch, heads, seq, d);
   EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
   return dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
-                             seq, heads, d, dtype, beta_mode == EDF_BETA_PER_HEAD, 0);
+                             seq, heads, d, dtype, beta_mode == EDF_BETA_PER_HEAD, 0, nullptr);
 }
 int bwd_saved(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
               const void* grad_out, void* dq, void* dk, void* dv, void* dbeta, void* dalpha, const void* fwd_ws,
@@ -92,11 +98,13 @@ int bwd_saved(void* stream, const void* q, const void* k, const void* v, const v
     return dr_chunk_saved_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, fwd_ws,
                                        workspace, batch, seq, heads, d);
   }
-  // the per-step path keeps no forward context: its backward recomputes
+  // per-step path: the forward's stored states when its workspace held them, else the
+  // backward recomputes them
   const size_t need = dr_seq_backward_workspace_bytes(batch, heads, seq, d);
   EDF_REQUIRE(workspace && ws_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  const bool saved = fwd_ws && fwd_ws_bytes >= dr_seq_context_bytes(batch, heads, seq, d);
   return dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, dq, dk, dv, dbeta, dalpha, workspace, batch,
-                             seq, heads, d, dtype, per_head, 0);
+                             seq, heads, d, dtype, per_head, 0, saved ? (const float*)fwd_ws : nullptr);
 }
 }  // namespace
 }  // namespace edf
@@ -121,6 +129,14 @@ int edf_fused_delta_rule_scan_backward_saved(void* stream, const void* q, const 
   return edf::bwd_saved(stream, q, k, v, beta, alpha, grad_out, grad_q, grad_k, grad_v, grad_beta, grad_alpha,
                         forward_workspace, forward_workspace_bytes, workspace, workspace_bytes, batch, seq_len,
                         num_heads, head_dim, dtype, beta_mode);
+}
+
+size_t edf_delta_rule_forward_context_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                            int beta_mode) {
+  if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || head_dim <= 0 || head_dim > 128) return 0;
+  if (edf::dr_chunk_eligible(seq_len, head_dim, dtype, beta_mode == EDF_BETA_PER_HEAD))
+    return edf::dr_chunk_workspace_bytes(batch, seq_len, num_heads, head_dim);
+  return edf::dr_seq_context_bytes(batch, num_heads, seq_len, head_dim);
 }
 
 size_t edf_delta_rule_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
@@ -189,7 +205,8 @@ int edf_fused_kda_scan(void* stream, const void* q, const void* k, const void* v
   int rc = edf::check_dr(batch, seq_len, num_heads, head_dim, dtype, EDF_BETA_PER_HEAD);
   if (rc) return rc;
   EDF_REQUIRE(q && k && v && alpha && beta && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
-  return edf::dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq_len, num_heads, head_dim, dtype, 1, 1);
+  return edf::dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq_len, num_heads, head_dim, dtype, 1, 1,
+                         nullptr);
 }
 
 int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
@@ -205,7 +222,7 @@ int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, cons
   const size_t need = edf::dr_seq_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
   EDF_REQUIRE(workspace && workspace_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
   return edf::dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, grad_q, grad_k, grad_v, grad_beta,
-                                  grad_alpha, workspace, batch, seq_len, num_heads, head_dim, dtype, 1, 1);
+                                  grad_alpha, workspace, batch, seq_len, num_heads, head_dim, dtype, 1, 1, nullptr);
 }
 
 }  // extern "C"

@@ -371,10 +371,19 @@ size_t dr_seq_backward_workspace_bytes(int batch, int heads, int seq, int d) {
   return seq_ws(batch, heads, seq, d).total;
 }
 
+// the states the per-step forward can store for a later backward (the checkpoints the
+// backward would otherwise recompute with a forward pass of its own)
+size_t dr_seq_context_bytes(int batch, int heads, int seq, int d) {
+  const SeqWs w = seq_ws(batch, heads, seq, d);
+  return w.part_q - w.ckpt;
+}
+
 int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const void* beta, const void* alpha,
-               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head, int alpha_per_row) {
+               void* out, int batch, int seq, int heads, int d, int dtype, int beta_per_head, int alpha_per_row,
+               float* context) {
   DRArgs a{};
   a.q = q; a.k = k; a.v = v; a.beta = beta; a.alpha = alpha; a.out = out;
+  a.ckpt = context;  // also store the checkpoints (one pass writes both)
   a.H = heads; a.T = seq; a.d = d; a.beta_per_head = beta_per_head; a.alpha_per_row = alpha_per_row;
   a.nck = (seq + CK - 1) / CK;
   hipStream_t s = as_stream(stream);
@@ -385,7 +394,7 @@ int dr_seq_run(void* stream, const void* q, const void* k, const void* v, const 
 int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* v, const void* beta,
                         const void* alpha, const void* grad_out, void* dq, void* dk, void* dv, void* dbeta,
                         void* dalpha, void* workspace, int batch, int seq, int heads, int d, int dtype,
-                        int beta_per_head, int alpha_per_row) {
+                        int beta_per_head, int alpha_per_row, const float* context) {
   DRArgs a{};
   a.q = q; a.k = k; a.v = v; a.beta = beta; a.alpha = alpha; a.dout = grad_out;
   a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta; a.dalpha = dalpha;
@@ -393,7 +402,7 @@ int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* 
   a.nck = (seq + CK - 1) / CK;
   const SeqWs w = seq_ws(batch, heads, seq, d);
   char* ws = (char*)workspace;
-  a.ckpt = (float*)(ws + w.ckpt);
+  a.ckpt = context ? const_cast<float*>(context) : (float*)(ws + w.ckpt);
   a.part_q = (float*)(ws + w.part_q);
   a.part_k = (float*)(ws + w.part_k);
   a.part_a = (float*)(ws + w.part_a);
@@ -409,14 +418,18 @@ int dr_seq_backward_run(void* stream, const void* q, const void* k, const void* 
   const unsigned gred = (unsigned)((nred + 255) / 256);
   int rc;
   if (dtype == EDF_BF16) {
-    rc = launch_seq<bf16>(s, f, false, bh);
-    if (rc) return rc;
+    if (!context) {  // the forward's stored checkpoints, or a pass that writes only them
+      rc = launch_seq<bf16>(s, f, false, bh);
+      if (rc) return rc;
+    }
     rc = launch_seq<bf16>(s, a, true, bh);
     if (rc) return rc;
     dr_seq_reduce_kernel<bf16><<<gred, 256, 0, s>>>(a, nbth, nrb);
   } else {
-    rc = launch_seq<float>(s, f, false, bh);
-    if (rc) return rc;
+    if (!context) {
+      rc = launch_seq<float>(s, f, false, bh);
+      if (rc) return rc;
+    }
     rc = launch_seq<float>(s, a, true, bh);
     if (rc) return rc;
     dr_seq_reduce_kernel<float><<<gred, 256, 0, s>>>(a, nbth, nrb);

@@ -589,7 +589,11 @@ class _DeltaRule(torch.autograd.Function):
             raise EdificeHipError(f"alpha must be [B,T,H], got {tuple(alpha.shape)}")
         dt = dtype_flag(q)
         out = torch.empty_like(v)
-        wsb = nat.query("edf_delta_rule_workspace_bytes", bsz, seq, nh, hd, dt, mode)
+        # with gradients to come, a workspace that also keeps the states the backward reads
+        # (the chunked path's per-chunk context, or the per-step path's 16-step states)
+        query = ("edf_delta_rule_forward_context_bytes" if any(ctx.needs_input_grad)
+                 else "edf_delta_rule_workspace_bytes")
+        wsb = nat.query(query, bsz, seq, nh, hd, dt, mode)
         ws = _u8(wsb, q) if wsb else None
         if alpha is None:
             nat.call("edf_fused_delta_net_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(ws), wsb,
@@ -598,7 +602,6 @@ class _DeltaRule(torch.autograd.Function):
             nat.call("edf_fused_gated_delta_net_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(alpha),
                      _p(out), _p(ws), wsb, bsz, seq, nh, hd, dt, mode)
         ctx.mode = mode
-        # the chunked path's workspace keeps the per-chunk context the backward reads
         ctx.fwd_ws, ctx.fwd_wsb = ws, wsb
         ctx.save_for_backward(q, k, v, beta, alpha)
         return out

@@ -436,9 +436,16 @@ int edf_fused_gated_delta_net_scan_backward(void* stream, const void* q, const v
  * context its forward call left in `forward_workspace` (the workspace of the forward with the
  * same q, k, v, beta, alpha, unchanged since).  On the chunked path (see above) this skips
  * the forward's recomputation; `workspace` needs
- * edf_delta_rule_saved_backward_workspace_bytes() bytes.  On the per-step path
- * forward_workspace is not read and the backward recomputes, as
- * edf_fused_gated_delta_net_scan_backward does. */
+ * edf_delta_rule_saved_backward_workspace_bytes() bytes.  On the per-step path the forward's
+ * workspace is optional (edf_delta_rule_workspace_bytes() is 0 there); a forward workspace of
+ * edf_delta_rule_forward_context_bytes() also receives the states every 16 steps, which this
+ * backward then reads instead of recomputing them (bit-identical gradients); with a smaller
+ * or NULL forward_workspace it recomputes, as edf_fused_gated_delta_net_scan_backward does.
+ * edf_delta_rule_forward_context_bytes() is the chunked path's forward workspace on that
+ * path and the per-step states otherwise: the forward workspace a training caller
+ * allocates for the saved backward. */
+size_t edf_delta_rule_forward_context_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
+                                            int beta_mode);
 size_t edf_delta_rule_saved_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype,
                                                      int beta_mode);
 int edf_fused_delta_rule_scan_backward_saved(void* stream, const void* q, const void* k, const void* v,

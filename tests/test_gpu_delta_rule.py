@@ -63,13 +63,18 @@ def test_delta_rule_fwd_bwd(case, rng):
         assert_close(host(t.grad), g[name], tol, name)
 
 
-@pytest.mark.parametrize("case", [(1, 200, 2, 128, torch.bfloat16, True), (2, 130, 1, 128, torch.bfloat16, False),
-                                  (1, 200, 2, 64, torch.bfloat16, True), (1, 40, 2, 32, torch.float32, True)],
+@pytest.mark.parametrize("case", [(1, 200, 2, 128, torch.bfloat16, True, True),
+                                  (2, 130, 1, 128, torch.bfloat16, False, True),
+                                  (1, 200, 2, 64, torch.bfloat16, True, True), (1, 40, 2, 32, torch.float32, True, True),
+                                  (1, 70, 2, 128, torch.bfloat16, False, False),  # per-element beta (config 5)
+                                  (2, 45, 1, 40, torch.float32, True, False)],
                          ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
 def test_delta_rule_backward_entry_points_agree(case, rng):
     """The reference-shaped backward entry points (which recompute the forward context) and
     edf_fused_delta_rule_scan_backward_saved (which reads the forward's workspace) give the
-    same gradients: chunked path (gated and not) and the per-step path.  The chunked
+    same gradients: chunked path (gated and not) and the per-step path, whose forward workspace
+    of edf_delta_rule_forward_context_bytes() keeps the 16-step states the saved backward
+    reads instead of recomputing them (same kernels: bit-identical there).  The chunked
     gradient kernel adds the dbeta and decay terms of a chunk with LDS atomics, whose order
     varies between calls, so the agreement is not bit for bit: per element within 1e-6 of
     the gradient's largest entry plus, for bf16 outputs, one bf16 unit of the element (a
@@ -77,42 +82,49 @@ def test_delta_rule_backward_entry_points_agree(case, rng):
     import ctypes
 
     from edifice_amd import _native as nat
-    B, T, H, d, dtype, gated = case
+    B, T, H, d, dtype, gated, per_head = case
     announce("delta_rule_entry_points", case=case)
-    q, k, v, beta, alpha = make_inputs(rng, B, T, H, d, True, gated)
+    q, k, v, beta, alpha = make_inputs(rng, B, T, H, d, per_head, gated)
+    mode = 1 if per_head else 0
     do = rng.normal(size=v.shape)
     tq, tk, tv, tb, tdo = (to_dev(a, dtype) for a in (q, k, v, beta, do))
     ta = to_dev(alpha, dtype) if gated else None
     P = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     dt = 1 if dtype == torch.bfloat16 else 0
-    wsf = nat.query("edf_delta_rule_workspace_bytes", B, T, H, d, dt, 1)
-    wsr = nat.query("edf_delta_rule_backward_workspace_bytes", B, T, H, d, dt, 1)
-    wss = nat.query("edf_delta_rule_saved_backward_workspace_bytes", B, T, H, d, dt, 1)
+    wsf = nat.query("edf_delta_rule_forward_context_bytes", B, T, H, d, dt, mode)
+    wsr = nat.query("edf_delta_rule_backward_workspace_bytes", B, T, H, d, dt, mode)
+    wss = nat.query("edf_delta_rule_saved_backward_workspace_bytes", B, T, H, d, dt, mode)
+    chunked = nat.query("edf_delta_rule_workspace_bytes", B, T, H, d, dt, mode) > 0
     f_ws = torch.empty(max(wsf, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty_like(tv)
     if gated:
         nat.call("edf_fused_gated_delta_net_scan", st, P(tq), P(tk), P(tv), P(tb), P(ta), P(out), P(f_ws), wsf,
-                 B, T, H, d, dt, 1)
+                 B, T, H, d, dt, mode)
     else:
-        nat.call("edf_fused_delta_net_scan", st, P(tq), P(tk), P(tv), P(tb), P(out), P(f_ws), wsf, B, T, H, d, dt, 1)
+        nat.call("edf_fused_delta_net_scan", st, P(tq), P(tk), P(tv), P(tb), P(out), P(f_ws), wsf, B, T, H, d, dt,
+                 mode)
     grads = []
     for saved in (False, True):
         g = [torch.empty_like(t) for t in (tq, tk, tv, tb)] + ([torch.empty_like(ta)] if gated else [None])
         if saved:
             ws = torch.empty(max(wss, 1), dtype=torch.uint8, device="cuda")
             nat.call("edf_fused_delta_rule_scan_backward_saved", st, P(tq), P(tk), P(tv), P(tb), P(ta), P(tdo),
-                     *(P(x) for x in g), P(f_ws), wsf, P(ws), wss, B, T, H, d, dt, 1)
+                     *(P(x) for x in g), P(f_ws), wsf, P(ws), wss, B, T, H, d, dt, mode)
         elif gated:
             ws = torch.empty(max(wsr, 1), dtype=torch.uint8, device="cuda")
             nat.call("edf_fused_gated_delta_net_scan_backward", st, P(tq), P(tk), P(tv), P(tb), P(ta), P(out),
-                     P(tdo), *(P(x) for x in g), P(ws), wsr, B, T, H, d, dt, 1)
+                     P(tdo), *(P(x) for x in g), P(ws), wsr, B, T, H, d, dt, mode)
         else:
             ws = torch.empty(max(wsr, 1), dtype=torch.uint8, device="cuda")
             nat.call("edf_fused_delta_rule_scan_backward", st, P(tq), P(tk), P(tv), P(tb), P(out), P(tdo),
-                     *(P(x) for x in g[:4]), P(ws), wsr, B, T, H, d, dt, 1)
+                     *(P(x) for x in g[:4]), P(ws), wsr, B, T, H, d, dt, mode)
         torch.cuda.synchronize()
         grads.append([None if x is None else host(x) for x in g])
+    if not chunked:
+        for a, b_ in zip(*grads):
+            if a is not None:
+                assert np.array_equal(a, b_), "per-step: saved states and recomputed states disagree"
     ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 0.0
     for a, b_ in zip(*grads):
         if a is not None:
