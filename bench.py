@@ -504,15 +504,20 @@ def bench_ttt(torch, steps, warmup, B=8, T=2048, D=64):
     grads = [torch.empty_like(t) for t in (q, k, v, eta, w0, lg, lb)]
     wsb = nat.query("edf_ttt_scan_backward_workspace_bytes", B, T, D, 1)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    recb = nat.query("edf_ttt_scan_context_bytes", B, T, D, 1)
+    rec = torch.empty(recb, dtype=torch.uint8, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
+    # the training pair the autograd path runs: a forward that records the backward's context
+    # in the same pass, and the backward from that context
     def fwd():
-        nat.call("edf_fused_ttt_scan", stream, P(q), P(k), P(v), P(eta), P(w0), P(lg), P(lb), P(out), B, T, D, 1)
+        nat.call("edf_fused_ttt_scan_with_context", stream, P(q), P(k), P(v), P(eta), P(w0), P(lg), P(lb), P(out),
+                 P(rec), recb, B, T, D, 1)
 
     def bwd():
-        nat.call("edf_fused_ttt_scan_backward", stream, P(q), P(k), P(v), P(eta), P(w0), P(lg), P(lb), P(do),
-                 *(P(t) for t in grads), P(ws), wsb, B, T, D, 1)
+        nat.call("edf_fused_ttt_scan_backward_saved", stream, P(q), P(k), P(v), P(eta), P(w0), P(lg), P(lb), P(do),
+                 *(P(t) for t in grads), P(rec), recb, P(ws), wsb, B, T, D, 1)
 
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,

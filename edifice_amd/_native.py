@@ -86,6 +86,10 @@ SIGNATURES = {
     "edf_fused_ttt_scan": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I]),
     "edf_fused_ttt_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
     "edf_ttt_scan_backward_workspace_bytes": (S, [I, I, I, I]),
+    "edf_ttt_scan_context_bytes": (S, [I, I, I, I]),
+    "edf_fused_ttt_scan_with_context": (I, [P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
+    "edf_fused_ttt_scan_backward_saved": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, P, S, I, I,
+                                               I, I]),
     "edf_debug_mfma_32x32x16_bf16": (I, [P, P, P, P]),
     "edf_debug_acc_kfrag_bf16": (I, [P, P, P]),
     "edf_debug_lds_read_tr16": (I, [P, P, P]),

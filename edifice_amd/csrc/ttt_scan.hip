@@ -456,11 +456,13 @@ size_t edf_ttt_scan_backward_workspace_bytes(int batch, int seq_len, int inner_s
   return edf::ttt_ws(batch, seq_len, inner_size).total;
 }
 
-int edf_fused_ttt_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* eta,
-                                const void* w0, const void* ln_g, const void* ln_b, const void* grad_out,
-                                void* grad_q, void* grad_k, void* grad_v, void* grad_eta, void* grad_w0,
-                                void* grad_ln_g, void* grad_ln_b, void* workspace, size_t workspace_bytes,
-                                int batch, int seq_len, int inner_size, int dtype) {
+// the backward proper; `context` (nullable) holds what a recording forward stored (W every
+// TTT_CK steps, x_hat, err and 1/sigma per step), else a forward pass records it first
+static int ttt_backward(void* stream, const void* q, const void* k, const void* v, const void* eta, const void* w0,
+                        const void* ln_g, const void* ln_b, const void* grad_out, void* grad_q, void* grad_k,
+                        void* grad_v, void* grad_eta, void* grad_w0, void* grad_ln_g, void* grad_ln_b,
+                        const void* context, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                        int inner_size, int dtype) {
   using namespace edf;
   int rc = check_ttt(batch, seq_len, inner_size, dtype);
   if (rc) return rc;
@@ -471,11 +473,12 @@ int edf_fused_ttt_scan_backward(void* stream, const void* q, const void* k, cons
   EDF_REQUIRE(workspace && workspace_bytes >= w.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
               w.total);
   char* ws = (char*)workspace;
+  char* rec = context ? (char*)const_cast<void*>(context) : ws;  // the records: same layout either way
   TArgs a = ttt_args(q, k, v, eta, w0, ln_g, ln_b, seq_len, inner_size);
-  a.ckpt = (float*)(ws + w.ckpt);
-  a.xh = (float*)(ws + w.xh);
-  a.err = (float*)(ws + w.err);
-  a.rstd = (float*)(ws + w.rstd);
+  a.ckpt = (float*)(rec + w.ckpt);
+  a.xh = (float*)(rec + w.xh);
+  a.err = (float*)(rec + w.err);
+  a.rstd = (float*)(rec + w.rstd);
   a.part_g = (float*)(ws + w.part_g);
   a.part_b = (float*)(ws + w.part_b);
   TArgs f = a;  // forward re-run: checkpoints and per-step LayerNorm values, no output
@@ -485,15 +488,64 @@ int edf_fused_ttt_scan_backward(void* stream, const void* q, const void* k, cons
   hipStream_t s = as_stream(stream);
   const unsigned gred = (unsigned)((2 * inner_size + 255) / 256);
   if (dtype == EDF_BF16) {
-    if ((rc = ttt_launch<bf16>(s, f, false, batch))) return rc;
+    if (!context && (rc = ttt_launch<bf16>(s, f, false, batch))) return rc;
     if ((rc = ttt_launch<bf16>(s, a, true, batch))) return rc;
     ttt_ln_reduce_kernel<bf16><<<gred, 256, 0, s>>>(a, batch);
   } else {
-    if ((rc = ttt_launch<float>(s, f, false, batch))) return rc;
+    if (!context && (rc = ttt_launch<float>(s, f, false, batch))) return rc;
     if ((rc = ttt_launch<float>(s, a, true, batch))) return rc;
     ttt_ln_reduce_kernel<float><<<gred, 256, 0, s>>>(a, batch);
   }
   return check_launch("ttt backward reduction");
+}
+
+int edf_fused_ttt_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* eta,
+                                const void* w0, const void* ln_g, const void* ln_b, const void* grad_out,
+                                void* grad_q, void* grad_k, void* grad_v, void* grad_eta, void* grad_w0,
+                                void* grad_ln_g, void* grad_ln_b, void* workspace, size_t workspace_bytes,
+                                int batch, int seq_len, int inner_size, int dtype) {
+  return ttt_backward(stream, q, k, v, eta, w0, ln_g, ln_b, grad_out, grad_q, grad_k, grad_v, grad_eta, grad_w0,
+                      grad_ln_g, grad_ln_b, nullptr, workspace, workspace_bytes, batch, seq_len, inner_size, dtype);
+}
+
+size_t edf_ttt_scan_context_bytes(int batch, int seq_len, int inner_size, int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || inner_size <= 0) return 0;
+  return edf::ttt_ws(batch, seq_len, inner_size).part_g;
+}
+
+int edf_fused_ttt_scan_with_context(void* stream, const void* q, const void* k, const void* v, const void* eta,
+                                    const void* w0, const void* ln_g, const void* ln_b, void* out, void* context,
+                                    size_t context_bytes, int batch, int seq_len, int inner_size, int dtype) {
+  using namespace edf;
+  int rc = check_ttt(batch, seq_len, inner_size, dtype);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && eta && w0 && ln_g && ln_b && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const TWs w = ttt_ws(batch, seq_len, inner_size);
+  EDF_REQUIRE(context && context_bytes >= w.part_g, EDF_ERR_WORKSPACE, "context too small: need %zu bytes",
+              w.part_g);
+  char* rec = (char*)context;
+  TArgs a = ttt_args(q, k, v, eta, w0, ln_g, ln_b, seq_len, inner_size);
+  a.out = out;
+  a.ckpt = (float*)(rec + w.ckpt);
+  a.xh = (float*)(rec + w.xh);
+  a.err = (float*)(rec + w.err);
+  a.rstd = (float*)(rec + w.rstd);
+  hipStream_t s = as_stream(stream);
+  return dtype == EDF_BF16 ? ttt_launch<bf16>(s, a, false, batch) : ttt_launch<float>(s, a, false, batch);
+}
+
+int edf_fused_ttt_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* eta,
+                                      const void* w0, const void* ln_g, const void* ln_b, const void* grad_out,
+                                      void* grad_q, void* grad_k, void* grad_v, void* grad_eta, void* grad_w0,
+                                      void* grad_ln_g, void* grad_ln_b, const void* context, size_t context_bytes,
+                                      void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                      int inner_size, int dtype) {
+  const size_t need = edf_ttt_scan_context_bytes(batch, seq_len, inner_size, dtype);
+  EDF_REQUIRE(context && context_bytes >= need, EDF_ERR_WORKSPACE,
+              "context too small: need the %zu bytes the forward filled", need);
+  return ttt_backward(stream, q, k, v, eta, w0, ln_g, ln_b, grad_out, grad_q, grad_k, grad_v, grad_eta, grad_w0,
+                      grad_ln_g, grad_ln_b, context, workspace, workspace_bytes, batch, seq_len, inner_size, dtype);
 }
 
 }  // extern "C"

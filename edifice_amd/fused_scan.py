@@ -748,8 +748,15 @@ class _TTT(torch.autograd.Function):
                 or tuple(ln_g.shape) != (dd,) or tuple(ln_b.shape) != (dd,):
             raise EdificeHipError("ttt_scan needs q, k, v, eta [B, T, D], w0 [B, D, D], ln_gamma, ln_beta [D]")
         out = torch.empty_like(q)
-        nat.call("edf_fused_ttt_scan", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g), _p(ln_b), _p(out),
-                 bsz, seq, dd, dtype_flag(q))
+        ctx.rec, ctx.recb = None, 0
+        if any(ctx.needs_input_grad):  # record what the backward reads in the same pass
+            ctx.recb = nat.query("edf_ttt_scan_context_bytes", bsz, seq, dd, dtype_flag(q))
+            ctx.rec = _u8(ctx.recb, q)
+            nat.call("edf_fused_ttt_scan_with_context", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g),
+                     _p(ln_b), _p(out), _p(ctx.rec), ctx.recb, bsz, seq, dd, dtype_flag(q))
+        else:
+            nat.call("edf_fused_ttt_scan", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g), _p(ln_b),
+                     _p(out), bsz, seq, dd, dtype_flag(q))
         ctx.save_for_backward(q, k, v, eta, w0, ln_g, ln_b)
         return out
 
@@ -761,8 +768,10 @@ class _TTT(torch.autograd.Function):
         grads = [torch.empty_like(t) for t in (q, k, v, eta, w0, ln_g, ln_b)]
         wsb = nat.query("edf_ttt_scan_backward_workspace_bytes", bsz, seq, dd, dtype_flag(q))
         ws = _u8(wsb, q)
-        nat.call("edf_fused_ttt_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g), _p(ln_b),
-                 _p(do), *(_p(g) for g in grads), _p(ws), wsb, bsz, seq, dd, dtype_flag(q))
+        nat.call("edf_fused_ttt_scan_backward_saved", _stream(), _p(q), _p(k), _p(v), _p(eta), _p(w0), _p(ln_g),
+                 _p(ln_b), _p(do), *(_p(g) for g in grads), _p(ctx.rec), ctx.recb, _p(ws), wsb, bsz, seq, dd,
+                 dtype_flag(q))
+        ctx.rec = None
         return tuple(grads)
 
 

@@ -304,6 +304,23 @@ int edf_fused_ttt_scan_backward(void* stream, const void* q, const void* k, cons
                                 int batch, int seq_len, int inner_size, int dtype);
 size_t edf_ttt_scan_backward_workspace_bytes(int batch, int seq_len, int inner_size, int dtype);
 
+/* No reference counterpart (its backward re-runs the forward): a training forward that also
+ * records, into a caller-kept context of edf_ttt_scan_context_bytes() bytes, what the
+ * backward needs (W every 8 steps, x_hat, err and 1/sigma per step; one pass writes out and
+ * the records), and the backward from that context (unchanged since), which then skips its
+ * own recording forward; gradients bit-identical to edf_fused_ttt_scan_backward, workspace
+ * edf_ttt_scan_backward_workspace_bytes(). */
+size_t edf_ttt_scan_context_bytes(int batch, int seq_len, int inner_size, int dtype);
+int edf_fused_ttt_scan_with_context(void* stream, const void* q, const void* k, const void* v, const void* eta,
+                                    const void* w0, const void* ln_g, const void* ln_b, void* out, void* context,
+                                    size_t context_bytes, int batch, int seq_len, int inner_size, int dtype);
+int edf_fused_ttt_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* eta,
+                                      const void* w0, const void* ln_g, const void* ln_b, const void* grad_out,
+                                      void* grad_q, void* grad_k, void* grad_v, void* grad_eta, void* grad_w0,
+                                      void* grad_ln_g, void* grad_ln_b, const void* context, size_t context_bytes,
+                                      void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                      int inner_size, int dtype);
+
 /* ------------------------------------------------------------------------
  * Flash attention   O = softmax(Q K^T / sqrt(d) [+ causal -inf]) V
  *   q, k, v, out, grads: [B, H, T, d] in dtype; lse: float32 [B, H, T] (natural log)

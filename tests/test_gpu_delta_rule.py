@@ -292,3 +292,49 @@ def test_ttt_fwd_bwd(case, rng):
     gr = scans.ttt_scan_backward(*xs, rounded(do, dtype))
     for n, tt in zip(("dq", "dk", "dv", "deta", "dw0", "dln_g", "dln_b"), ts):
         assert_close(host(tt.grad), gr[n], tol, n)
+
+
+@pytest.mark.parametrize("case", [(2, 37, 16, torch.float32), (2, 33, 64, torch.bfloat16)],
+                         ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_ttt_context_entry_points_agree(case, rng):
+    """edf_fused_ttt_scan_with_context (the training forward, recording the backward's context
+    in the same pass) gives the plain forward's output, and edf_fused_ttt_scan_backward_saved
+    from that context gives the recomputing backward's gradients, bit for bit (same kernels)."""
+    import ctypes
+
+    from edifice_amd import _native as nat
+    bsz, t, d, dtype = case
+    announce("ttt_context", case=case)
+    q, k, v, do = (rng.normal(size=(bsz, t, d)) for _ in range(4))
+    eta = rng.uniform(0.2, 0.8, size=(bsz, t, d)) / d * 4
+    w0 = rng.normal(size=(bsz, d, d)) / np.sqrt(d)
+    g, b = 1 + 0.2 * rng.normal(size=d), 0.2 * rng.normal(size=d)
+    ins = [to_dev(x, dtype) for x in (q, k / np.sqrt(d), v, eta, w0, g, b)]
+    tdo = to_dev(do, dtype)
+    P = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dt = 1 if dtype == torch.bfloat16 else 0
+    wsb = nat.query("edf_ttt_scan_backward_workspace_bytes", bsz, t, d, dt)
+    recb = nat.query("edf_ttt_scan_context_bytes", bsz, t, d, dt)
+    rec = torch.empty(recb, dtype=torch.uint8, device="cuda")
+    outs, grads = [], []
+    for saved in (False, True):
+        out = torch.empty_like(ins[0])
+        if saved:
+            nat.call("edf_fused_ttt_scan_with_context", st, *(P(x) for x in ins), P(out), P(rec), recb, bsz, t, d, dt)
+        else:
+            nat.call("edf_fused_ttt_scan", st, *(P(x) for x in ins), P(out), bsz, t, d, dt)
+        gs = [torch.empty_like(x) for x in ins]
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        if saved:
+            nat.call("edf_fused_ttt_scan_backward_saved", st, *(P(x) for x in ins), P(tdo), *(P(x) for x in gs),
+                     P(rec), recb, P(ws), wsb, bsz, t, d, dt)
+        else:
+            nat.call("edf_fused_ttt_scan_backward", st, *(P(x) for x in ins), P(tdo), *(P(x) for x in gs), P(ws), wsb,
+                     bsz, t, d, dt)
+        torch.cuda.synchronize()
+        outs.append(out)
+        grads.append(gs)
+    assert torch.equal(outs[0], outs[1])
+    for a, c in zip(*grads):
+        assert torch.equal(a, c)
