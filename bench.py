@@ -432,20 +432,22 @@ def bench_delta_product(torch, steps, warmup, B=8, T=2048, NH=2, H=8, d=128):
     do = torch.randn(B, T, H, d, device=dev, generator=g).to(bf)
     out, dq = torch.empty_like(q), torch.empty_like(q)
     dk, dv, db = torch.empty_like(k), torch.empty_like(v), torch.empty_like(beta)
-    wsf = nat.query("edf_delta_product_workspace_bytes", B, T, NH, H, d, 1)
+    recb = nat.query("edf_delta_product_context_bytes", B, T, NH, H, d, 1)
     wsb = nat.query("edf_delta_product_backward_workspace_bytes", B, T, NH, H, d, 1)
-    ws1 = torch.empty(wsf, dtype=torch.uint8, device=dev)
+    rec = torch.empty(recb, dtype=torch.uint8, device=dev)
     ws2 = torch.empty(wsb, dtype=torch.uint8, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
+    # the training pair the autograd path runs: a forward that keeps the backward's context
+    # (row-block partials, 16-sub-step states) in the same pass, and the backward from it
     def fwd():
-        nat.call("edf_fused_delta_product_scan", stream, P(q), P(k), P(v), P(beta), P(out), P(ws1), wsf,
-                 B, T, NH, H, d, 1)
+        nat.call("edf_fused_delta_product_scan_with_context", stream, P(q), P(k), P(v), P(beta), P(out), P(rec),
+                 recb, B, T, NH, H, d, 1)
 
     def bwd():
-        nat.call("edf_fused_delta_product_scan_backward", stream, P(q), P(k), P(v), P(beta), P(out), P(do), P(dq),
-                 P(dk), P(dv), P(db), P(ws2), wsb, B, T, NH, H, d, 1)
+        nat.call("edf_fused_delta_product_scan_backward_saved", stream, P(q), P(k), P(v), P(beta), P(do), P(dq),
+                 P(dk), P(dv), P(db), P(rec), recb, P(ws2), wsb, B, T, NH, H, d, 1)
 
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,
@@ -469,16 +471,20 @@ def bench_rla(torch, steps, warmup, variant, B=8, T=2048, H=8, d=128):
     da, db, dg = (torch.empty_like(alpha) for _ in range(3))
     wsb = nat.query("edf_rla_scan_backward_workspace_bytes", B, T, H, d, 1)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    recb = nat.query("edf_rla_scan_context_bytes", B, T, H, d, 1)
+    rec = torch.empty(recb, dtype=torch.uint8, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
+    # the training pair the autograd path runs: a forward that keeps both states every 8 steps
+    # in the same pass, and the backward from them
     def fwd():
-        nat.call("edf_fused_rla_scan", stream, P(q), P(k), P(v), P(alpha), P(beta), P(gamma), P(out),
-                 B, T, H, d, variant, 1.0, 1)
+        nat.call("edf_fused_rla_scan_with_context", stream, P(q), P(k), P(v), P(alpha), P(beta), P(gamma), P(out),
+                 P(rec), recb, B, T, H, d, variant, 1.0, 1)
 
     def bwd():
-        nat.call("edf_fused_rla_scan_backward", stream, P(q), P(k), P(v), P(alpha), P(beta), P(gamma), P(out),
-                 P(do), P(dq), P(dk), P(dv), P(da), P(db), P(dg), P(ws), wsb, B, T, H, d, variant, 1.0, 1)
+        nat.call("edf_fused_rla_scan_backward_saved", stream, P(q), P(k), P(v), P(alpha), P(beta), P(gamma), P(do),
+                 P(dq), P(dk), P(dv), P(da), P(db), P(dg), P(rec), recb, P(ws), wsb, B, T, H, d, variant, 1.0, 1)
 
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,

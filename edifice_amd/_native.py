@@ -79,10 +79,18 @@ SIGNATURES = {
     "edf_delta_product_workspace_bytes": (S, [I, I, I, I, I, I]),
     "edf_fused_delta_product_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_delta_product_backward_workspace_bytes": (S, [I, I, I, I, I, I]),
+    "edf_delta_product_context_bytes": (S, [I, I, I, I, I, I]),
+    "edf_fused_delta_product_scan_with_context": (I, [P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
+    "edf_fused_delta_product_scan_backward_saved": (I, [P, P, P, P, P, P, P, P, P, P, P, S, P, S, I, I, I, I, I,
+                                                         I]),
     "edf_fused_rla_scan": (I, [P, P, P, P, P, P, P, P, I, I, I, I, I, F, I]),
     "edf_fused_rla_scan_backward": (
         I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, F, I]),
     "edf_rla_scan_backward_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_rla_scan_context_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_rla_scan_with_context": (I, [P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, F, I]),
+    "edf_fused_rla_scan_backward_saved": (
+        I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, P, S, I, I, I, I, I, F, I]),
     "edf_fused_ttt_scan": (I, [P, P, P, P, P, P, P, P, P, I, I, I, I]),
     "edf_fused_ttt_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
     "edf_ttt_scan_backward_workspace_bytes": (S, [I, I, I, I]),

@@ -515,13 +515,13 @@ int edf_fused_delta_product_scan(void* stream, const void* q, const void* k, con
   return check_launch("delta product output norm");
 }
 
-int edf_fused_delta_product_scan_backward(void* stream, const void* q, const void* k, const void* v,
-                                          const void* beta, const void* forward_out, const void* grad_out,
-                                          void* grad_q, void* grad_k, void* grad_v, void* grad_beta, void* workspace,
-                                          size_t workspace_bytes, int batch, int seq_len, int num_householder,
-                                          int num_heads, int head_dim, int dtype) {
+// the backward proper; `context` (nullable) holds the row-block output partials and the
+// state checkpoints a recording forward left, else a forward pass recomputes them
+static int dp_backward(void* stream, const void* q, const void* k, const void* v, const void* beta,
+                       const void* grad_out, void* grad_q, void* grad_k, void* grad_v, void* grad_beta,
+                       const void* context, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                       int num_householder, int num_heads, int head_dim, int dtype) {
   using namespace edf;
-  (void)forward_out;  // the raw output and its norm are recomputed from the inputs
   int rc = check_dp(batch, seq_len, num_householder, num_heads, head_dim, dtype);
   if (rc) return rc;
   EDF_REQUIRE(q && k && v && beta && grad_out && grad_q && grad_k && grad_v && grad_beta, EDF_ERR_INVALID_ARG,
@@ -530,11 +530,12 @@ int edf_fused_delta_product_scan_backward(void* stream, const void* q, const voi
   EDF_REQUIRE(workspace && workspace_bytes >= w.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
               w.total);
   char* ws = (char*)workspace;
+  char* rec = context ? (char*)const_cast<void*>(context) : ws;  // partials and checkpoints: same layout
   DPArgs a = dp_args(q, k, v, beta, seq_len, num_householder, num_heads, head_dim);
   a.dout = grad_out;
   a.dq = grad_q; a.dk = grad_k; a.dv = grad_v; a.dbeta = grad_beta;
-  a.part_o = (float*)(ws + w.part_o);
-  a.ckpt = (float*)(ws + w.ckpt);
+  a.part_o = (float*)(rec + w.part_o);
+  a.ckpt = (float*)(rec + w.ckpt);
   a.dO = (float*)(ws + w.dO);
   a.part_k = (float*)(ws + w.part_k);
   a.part_b = (float*)(ws + w.part_b);
@@ -543,17 +544,75 @@ int edf_fused_delta_product_scan_backward(void* stream, const void* q, const voi
   hipStream_t s = as_stream(stream);
   const unsigned grows = (unsigned)((nbth + 3) / 4), gsub = (unsigned)((nbts + 3) / 4);
   if (dtype == EDF_BF16) {
-    if ((rc = dp_launch<bf16>(s, a, false, bh))) return rc;
+    if (!context && (rc = dp_launch<bf16>(s, a, false, bh))) return rc;
     dp_finish_kernel<bf16><<<grows, 256, 0, s>>>(a, nbth, nrb, 1);
     if ((rc = dp_launch<bf16>(s, a, true, bh))) return rc;
     dp_reduce_kernel<bf16><<<gsub, 256, 0, s>>>(a, nbts, nrb);
   } else {
-    if ((rc = dp_launch<float>(s, a, false, bh))) return rc;
+    if (!context && (rc = dp_launch<float>(s, a, false, bh))) return rc;
     dp_finish_kernel<float><<<grows, 256, 0, s>>>(a, nbth, nrb, 1);
     if ((rc = dp_launch<float>(s, a, true, bh))) return rc;
     dp_reduce_kernel<float><<<gsub, 256, 0, s>>>(a, nbts, nrb);
   }
   return check_launch("delta product backward reduction");
+}
+
+int edf_fused_delta_product_scan_backward(void* stream, const void* q, const void* k, const void* v,
+                                          const void* beta, const void* forward_out, const void* grad_out,
+                                          void* grad_q, void* grad_k, void* grad_v, void* grad_beta, void* workspace,
+                                          size_t workspace_bytes, int batch, int seq_len, int num_householder,
+                                          int num_heads, int head_dim, int dtype) {
+  (void)forward_out;  // the raw output and its norm are recomputed from the inputs
+  return dp_backward(stream, q, k, v, beta, grad_out, grad_q, grad_k, grad_v, grad_beta, nullptr, workspace,
+                     workspace_bytes, batch, seq_len, num_householder, num_heads, head_dim, dtype);
+}
+
+size_t edf_delta_product_context_bytes(int batch, int seq_len, int num_householder, int num_heads, int head_dim,
+                                       int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || num_householder <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return edf::dp_ws(batch, seq_len, num_householder, num_heads, head_dim, true).dO;
+}
+
+int edf_fused_delta_product_scan_with_context(void* stream, const void* q, const void* k, const void* v,
+                                              const void* beta, void* out, void* context, size_t context_bytes,
+                                              int batch, int seq_len, int num_householder, int num_heads,
+                                              int head_dim, int dtype) {
+  using namespace edf;
+  int rc = check_dp(batch, seq_len, num_householder, num_heads, head_dim, dtype);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && beta && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const DPWs w = dp_ws(batch, seq_len, num_householder, num_heads, head_dim, true);
+  EDF_REQUIRE(context && context_bytes >= w.dO, EDF_ERR_WORKSPACE, "context too small: need %zu bytes", w.dO);
+  DPArgs a = dp_args(q, k, v, beta, seq_len, num_householder, num_heads, head_dim);
+  a.out = out;
+  a.part_o = (float*)((char*)context + w.part_o);
+  a.ckpt = (float*)((char*)context + w.ckpt);
+  const int bh = batch * num_heads, nrb = dp_pad(head_dim) / DPR_RB;
+  const long nbth = (long)bh * seq_len;
+  hipStream_t s = as_stream(stream);
+  const unsigned grows = (unsigned)((nbth + 3) / 4);
+  if (dtype == EDF_BF16) {
+    if ((rc = dp_launch<bf16>(s, a, false, bh))) return rc;
+    dp_finish_kernel<bf16><<<grows, 256, 0, s>>>(a, nbth, nrb, 0);
+  } else {
+    if ((rc = dp_launch<float>(s, a, false, bh))) return rc;
+    dp_finish_kernel<float><<<grows, 256, 0, s>>>(a, nbth, nrb, 0);
+  }
+  return check_launch("delta product output norm");
+}
+
+int edf_fused_delta_product_scan_backward_saved(void* stream, const void* q, const void* k, const void* v,
+                                                const void* beta, const void* grad_out, void* grad_q, void* grad_k,
+                                                void* grad_v, void* grad_beta, const void* context,
+                                                size_t context_bytes, void* workspace, size_t workspace_bytes,
+                                                int batch, int seq_len, int num_householder, int num_heads,
+                                                int head_dim, int dtype) {
+  const size_t need = edf_delta_product_context_bytes(batch, seq_len, num_householder, num_heads, head_dim, dtype);
+  EDF_REQUIRE(context && context_bytes >= need, EDF_ERR_WORKSPACE,
+              "context too small: need the %zu bytes the forward filled", need);
+  return dp_backward(stream, q, k, v, beta, grad_out, grad_q, grad_k, grad_v, grad_beta, context, workspace,
+                     workspace_bytes, batch, seq_len, num_householder, num_heads, head_dim, dtype);
 }
 
 }  // extern "C"

@@ -447,13 +447,14 @@ size_t edf_rla_scan_backward_workspace_bytes(int batch, int seq_len, int num_hea
   return edf::rla_ws(batch, seq_len, num_heads, head_dim).total;
 }
 
-int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
-                                const void* beta, const void* gamma, const void* forward_out, const void* grad_out,
-                                void* grad_q, void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta,
-                                void* grad_gamma, void* workspace, size_t workspace_bytes, int batch, int seq_len,
-                                int num_heads, int head_dim, int variant, float clip_threshold, int dtype) {
+// the backward proper; `context` (nullable) holds the states every RLA_CK steps a recording
+// forward left, else a checkpointing forward pass writes them first
+static int rla_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                        const void* beta, const void* gamma, const void* grad_out, void* grad_q, void* grad_k,
+                        void* grad_v, void* grad_alpha, void* grad_beta, void* grad_gamma, const void* context,
+                        void* workspace, size_t workspace_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                        int variant, float clip_threshold, int dtype) {
   using namespace edf;
-  (void)forward_out;  // states are recomputed from the inputs
   int rc = check_rla(batch, seq_len, num_heads, head_dim, variant, clip_threshold, dtype);
   if (rc) return rc;
   EDF_REQUIRE(q && k && v && alpha && beta && gamma && grad_out && grad_q && grad_k && grad_v && grad_alpha &&
@@ -467,7 +468,7 @@ int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, cons
   a.dout = grad_out;
   a.dq = grad_q; a.dk = grad_k; a.dv = grad_v;
   a.dalpha = grad_alpha; a.dbeta = grad_beta; a.dgamma = grad_gamma;
-  a.ckpt = (float*)(ws + w.ckpt);
+  a.ckpt = context ? (float*)const_cast<void*>(context) : (float*)(ws + w.ckpt);
   a.part_q = (float*)(ws + w.part_q);
   a.part_k = (float*)(ws + w.part_k);
   a.part_s = (float*)(ws + w.part_s);
@@ -476,15 +477,64 @@ int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, cons
   const unsigned gred = (unsigned)((2 * nbth * head_dim + 3 * nbth + 255) / 256);
   hipStream_t s = as_stream(stream);
   if (dtype == EDF_BF16) {
-    if ((rc = rla_launch_v<bf16>(s, a, 1, bh, variant))) return rc;
+    if (!context && (rc = rla_launch_v<bf16>(s, a, 1, bh, variant))) return rc;
     if ((rc = rla_launch_v<bf16>(s, a, 2, bh, variant))) return rc;
     rla_reduce_kernel<bf16><<<gred, 256, 0, s>>>(a, nbth, nrb);
   } else {
-    if ((rc = rla_launch_v<float>(s, a, 1, bh, variant))) return rc;
+    if (!context && (rc = rla_launch_v<float>(s, a, 1, bh, variant))) return rc;
     if ((rc = rla_launch_v<float>(s, a, 2, bh, variant))) return rc;
     rla_reduce_kernel<float><<<gred, 256, 0, s>>>(a, nbth, nrb);
   }
   return check_launch("rla backward reduction");
+}
+
+int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                const void* beta, const void* gamma, const void* forward_out, const void* grad_out,
+                                void* grad_q, void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta,
+                                void* grad_gamma, void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                                int num_heads, int head_dim, int variant, float clip_threshold, int dtype) {
+  (void)forward_out;  // states are recomputed from the inputs
+  return rla_backward(stream, q, k, v, alpha, beta, gamma, grad_out, grad_q, grad_k, grad_v, grad_alpha, grad_beta,
+                      grad_gamma, nullptr, workspace, workspace_bytes, batch, seq_len, num_heads, head_dim, variant,
+                      clip_threshold, dtype);
+}
+
+size_t edf_rla_scan_context_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || head_dim <= 0) return 0;
+  return edf::rla_ws(batch, seq_len, num_heads, head_dim).part_q;
+}
+
+int edf_fused_rla_scan_with_context(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                    const void* beta, const void* gamma, void* out, void* context,
+                                    size_t context_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                                    int variant, float clip_threshold, int dtype) {
+  using namespace edf;
+  int rc = check_rla(batch, seq_len, num_heads, head_dim, variant, clip_threshold, dtype);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && alpha && beta && gamma && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const size_t need = rla_ws(batch, seq_len, num_heads, head_dim).part_q;
+  EDF_REQUIRE(context && context_bytes >= need, EDF_ERR_WORKSPACE, "context too small: need %zu bytes", need);
+  RLAArgs a = rla_args(q, k, v, alpha, beta, gamma, seq_len, num_heads, head_dim, clip_threshold);
+  a.out = out;
+  a.ckpt = (float*)context;  // the checkpointing kernel writes the output too
+  hipStream_t s = as_stream(stream);
+  const int bh = batch * num_heads;
+  return dtype == EDF_BF16 ? rla_launch_v<bf16>(s, a, 1, bh, variant) : rla_launch_v<float>(s, a, 1, bh, variant);
+}
+
+int edf_fused_rla_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                      const void* beta, const void* gamma, const void* grad_out, void* grad_q,
+                                      void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta,
+                                      void* grad_gamma, const void* context, size_t context_bytes, void* workspace,
+                                      size_t workspace_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                                      int variant, float clip_threshold, int dtype) {
+  const size_t need = edf_rla_scan_context_bytes(batch, seq_len, num_heads, head_dim, dtype);
+  EDF_REQUIRE(context && context_bytes >= need, EDF_ERR_WORKSPACE,
+              "context too small: need the %zu bytes the forward filled", need);
+  return rla_backward(stream, q, k, v, alpha, beta, gamma, grad_out, grad_q, grad_k, grad_v, grad_alpha, grad_beta,
+                      grad_gamma, context, workspace, workspace_bytes, batch, seq_len, num_heads, head_dim, variant,
+                      clip_threshold, dtype);
 }
 
 }  // extern "C"

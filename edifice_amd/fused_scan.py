@@ -670,10 +670,17 @@ class _DeltaProduct(torch.autograd.Function):
                                   "beta [B, T, n_h, H]")
         nhh = k.shape[2]
         out = torch.empty_like(q)
-        wsb = nat.query("edf_delta_product_workspace_bytes", bsz, seq, nhh, nh, hd, dtype_flag(q))
-        ws = _u8(wsb, q)
-        nat.call("edf_fused_delta_product_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(ws), wsb,
-                 bsz, seq, nhh, nh, hd, dtype_flag(q))
+        ctx.rec, ctx.recb = None, 0
+        if any(ctx.needs_input_grad):  # keep the partials and states the backward reads
+            ctx.recb = nat.query("edf_delta_product_context_bytes", bsz, seq, nhh, nh, hd, dtype_flag(q))
+            ctx.rec = _u8(ctx.recb, q)
+            nat.call("edf_fused_delta_product_scan_with_context", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out),
+                     _p(ctx.rec), ctx.recb, bsz, seq, nhh, nh, hd, dtype_flag(q))
+        else:
+            wsb = nat.query("edf_delta_product_workspace_bytes", bsz, seq, nhh, nh, hd, dtype_flag(q))
+            ws = _u8(wsb, q)
+            nat.call("edf_fused_delta_product_scan", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(ws),
+                     wsb, bsz, seq, nhh, nh, hd, dtype_flag(q))
         ctx.save_for_backward(q, k, v, beta, out)
         return out
 
@@ -686,8 +693,10 @@ class _DeltaProduct(torch.autograd.Function):
         dq, dk, dv, db = (torch.empty_like(t) for t in (q, k, v, beta))
         wsb = nat.query("edf_delta_product_backward_workspace_bytes", bsz, seq, nhh, nh, hd, dtype_flag(q))
         ws = _u8(wsb, q)
-        nat.call("edf_fused_delta_product_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(out), _p(do),
-                 _p(dq), _p(dk), _p(dv), _p(db), _p(ws), wsb, bsz, seq, nhh, nh, hd, dtype_flag(q))
+        nat.call("edf_fused_delta_product_scan_backward_saved", _stream(), _p(q), _p(k), _p(v), _p(beta), _p(do),
+                 _p(dq), _p(dk), _p(dv), _p(db), _p(ctx.rec), ctx.recb, _p(ws), wsb, bsz, seq, nhh, nh, hd,
+                 dtype_flag(q))
+        ctx.rec = None
         return dq, dk, dv, db
 
 
@@ -708,8 +717,16 @@ class _RLA(torch.autograd.Function):
         if k.shape != q.shape or v.shape != q.shape or any(tuple(g.shape) != (bsz, seq, nh) for g in (alpha, beta, gamma)):
             raise EdificeHipError("rla_scan needs q, k, v [B, T, H, d] and alpha, beta, gamma [B, T, H]")
         out = torch.empty_like(q)
-        nat.call("edf_fused_rla_scan", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(gamma), _p(out),
-                 bsz, seq, nh, hd, variant, float(clip), dtype_flag(q))
+        ctx.rec, ctx.recb = None, 0
+        if any(ctx.needs_input_grad):  # keep the states the backward reads
+            ctx.recb = nat.query("edf_rla_scan_context_bytes", bsz, seq, nh, hd, dtype_flag(q))
+            ctx.rec = _u8(ctx.recb, q)
+            nat.call("edf_fused_rla_scan_with_context", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta),
+                     _p(gamma), _p(out), _p(ctx.rec), ctx.recb, bsz, seq, nh, hd, variant, float(clip),
+                     dtype_flag(q))
+        else:
+            nat.call("edf_fused_rla_scan", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(gamma), _p(out),
+                     bsz, seq, nh, hd, variant, float(clip), dtype_flag(q))
         ctx.save_for_backward(q, k, v, alpha, beta, gamma, out)
         ctx.variant, ctx.clip = variant, float(clip)
         return out
@@ -722,9 +739,10 @@ class _RLA(torch.autograd.Function):
         dq, dk, dv, da, db, dg = (torch.empty_like(t) for t in (q, k, v, alpha, beta, gamma))
         wsb = nat.query("edf_rla_scan_backward_workspace_bytes", bsz, seq, nh, hd, dtype_flag(q))
         ws = _u8(wsb, q)
-        nat.call("edf_fused_rla_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(gamma),
-                 _p(out), _p(do), _p(dq), _p(dk), _p(dv), _p(da), _p(db), _p(dg), _p(ws), wsb, bsz, seq, nh, hd,
-                 ctx.variant, ctx.clip, dtype_flag(q))
+        nat.call("edf_fused_rla_scan_backward_saved", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta),
+                 _p(gamma), _p(do), _p(dq), _p(dk), _p(dv), _p(da), _p(db), _p(dg), _p(ctx.rec), ctx.recb, _p(ws),
+                 wsb, bsz, seq, nh, hd, ctx.variant, ctx.clip, dtype_flag(q))
+        ctx.rec = None
         return dq, dk, dv, da, db, dg, None, None
 
 

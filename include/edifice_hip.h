@@ -263,6 +263,25 @@ int edf_fused_delta_product_scan_backward(void* stream, const void* q, const voi
 size_t edf_delta_product_backward_workspace_bytes(int batch, int seq_len, int num_householder, int num_heads,
                                                   int head_dim, int dtype);
 
+/* No reference counterpart (its backward re-runs the forward): a training forward that also
+ * keeps, in a caller-kept context of edf_delta_product_context_bytes() bytes, the row-block
+ * output partials and the state every 16 sub-steps (one pass writes out and both), and the
+ * backward from that context (unchanged since), which then skips its forward re-run;
+ * gradients bit-identical to edf_fused_delta_product_scan_backward, workspace
+ * edf_delta_product_backward_workspace_bytes(). */
+size_t edf_delta_product_context_bytes(int batch, int seq_len, int num_householder, int num_heads, int head_dim,
+                                       int dtype);
+int edf_fused_delta_product_scan_with_context(void* stream, const void* q, const void* k, const void* v,
+                                              const void* beta, void* out, void* context, size_t context_bytes,
+                                              int batch, int seq_len, int num_householder, int num_heads,
+                                              int head_dim, int dtype);
+int edf_fused_delta_product_scan_backward_saved(void* stream, const void* q, const void* k, const void* v,
+                                                const void* beta, const void* grad_out, void* grad_q, void* grad_k,
+                                                void* grad_v, void* grad_beta, const void* context,
+                                                size_t context_bytes, void* workspace, size_t workspace_bytes,
+                                                int batch, int seq_len, int num_householder, int num_heads,
+                                                int head_dim, int dtype);
+
 /* RLA / RDN (residual linear attention): base state S and residual state R, per-head
  * alpha, beta, gamma [B,T,H]; variant 0 = RLA, 1 = RDN; clip_threshold >= 0 bounds the
  * residual error.  Replaces fused_rla_scan/13 (q, k, v, alpha, beta, gamma, batch, seq,
@@ -284,6 +303,23 @@ int edf_fused_rla_scan_backward(void* stream, const void* q, const void* k, cons
                                 void* grad_gamma, void* workspace, size_t workspace_bytes, int batch, int seq_len,
                                 int num_heads, int head_dim, int variant, float clip_threshold, int dtype);
 size_t edf_rla_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
+
+/* No reference counterpart (its backward re-runs a checkpointing forward): a training
+ * forward that also keeps both states every 8 steps in a caller-kept context of
+ * edf_rla_scan_context_bytes() bytes (one pass writes out and the states), and the backward
+ * from that context (unchanged since), which then skips its forward re-run; gradients
+ * bit-identical to edf_fused_rla_scan_backward, workspace edf_rla_scan_backward_workspace_bytes(). */
+size_t edf_rla_scan_context_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
+int edf_fused_rla_scan_with_context(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                    const void* beta, const void* gamma, void* out, void* context,
+                                    size_t context_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                                    int variant, float clip_threshold, int dtype);
+int edf_fused_rla_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                      const void* beta, const void* gamma, const void* grad_out, void* grad_q,
+                                      void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta,
+                                      void* grad_gamma, const void* context, size_t context_bytes, void* workspace,
+                                      size_t workspace_bytes, int batch, int seq_len, int num_heads, int head_dim,
+                                      int variant, float clip_threshold, int dtype);
 
 /* TTT-Linear: an inner linear model W [B, D, D] (initial w0) updated every step by one
  * LayerNorm-ed reconstruction step; q, k, v, eta [B,T,D], ln_g, ln_b [D].  Replaces

@@ -338,3 +338,100 @@ def test_ttt_context_entry_points_agree(case, rng):
     assert torch.equal(outs[0], outs[1])
     for a, c in zip(*grads):
         assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("case", [(2, 13, 2, 2, 16, torch.float32), (1, 40, 3, 2, 128, torch.bfloat16)],
+                         ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_delta_product_context_entry_points_agree(case, rng):
+    """edf_fused_delta_product_scan_with_context gives the plain forward's output, and
+    edf_fused_delta_product_scan_backward_saved from its context the recomputing backward's
+    gradients, bit for bit (same kernels)."""
+    import ctypes
+
+    from edifice_amd import _native as nat
+    B, T, NH, H, d, dtype = case
+    announce("delta_product_context", case=case)
+    q = rng.normal(size=(B, T, H, d))
+    k = rng.normal(size=(B, T, NH, H, d))
+    v = rng.normal(size=(B, T, NH, H, d))
+    beta = 1 / (1 + np.exp(-rng.normal(size=(B, T, NH, H))))
+    do = rng.normal(size=(B, T, H, d))
+    tq, tk, tv, tb, tdo = (to_dev(x, dtype) for x in (q, k, v, beta, do))
+    P = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dt = 1 if dtype == torch.bfloat16 else 0
+    wsf = nat.query("edf_delta_product_workspace_bytes", B, T, NH, H, d, dt)
+    wsb = nat.query("edf_delta_product_backward_workspace_bytes", B, T, NH, H, d, dt)
+    recb = nat.query("edf_delta_product_context_bytes", B, T, NH, H, d, dt)
+    rec = torch.empty(recb, dtype=torch.uint8, device="cuda")
+    outs, grads = [], []
+    for saved in (False, True):
+        out = torch.empty_like(tq)
+        if saved:
+            nat.call("edf_fused_delta_product_scan_with_context", st, P(tq), P(tk), P(tv), P(tb), P(out), P(rec), recb,
+                     B, T, NH, H, d, dt)
+        else:
+            ws = torch.empty(wsf, dtype=torch.uint8, device="cuda")
+            nat.call("edf_fused_delta_product_scan", st, P(tq), P(tk), P(tv), P(tb), P(out), P(ws), wsf,
+                     B, T, NH, H, d, dt)
+        gs = [torch.empty_like(x) for x in (tq, tk, tv, tb)]
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        if saved:
+            nat.call("edf_fused_delta_product_scan_backward_saved", st, P(tq), P(tk), P(tv), P(tb), P(tdo),
+                     *(P(x) for x in gs), P(rec), recb, P(ws), wsb, B, T, NH, H, d, dt)
+        else:
+            nat.call("edf_fused_delta_product_scan_backward", st, P(tq), P(tk), P(tv), P(tb), P(out), P(tdo),
+                     *(P(x) for x in gs), P(ws), wsb, B, T, NH, H, d, dt)
+        torch.cuda.synchronize()
+        outs.append(out)
+        grads.append(gs)
+    assert torch.equal(outs[0], outs[1])
+    for a, c in zip(*grads):
+        assert torch.equal(a, c)
+
+
+@pytest.mark.parametrize("case", [(2, 21, 2, 16, torch.float32, 0), (1, 40, 2, 128, torch.bfloat16, 1)],
+                         ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_rla_context_entry_points_agree(case, rng):
+    """edf_fused_rla_scan_with_context gives the plain forward's output (within rounding: it
+    walks the sequence in 8-step chunks instead of 16, the same arithmetic per step) and
+    edf_fused_rla_scan_backward_saved from its context the recomputing backward's gradients bit
+    for bit (the same checkpointing pass writes the states)."""
+    import ctypes
+
+    from edifice_amd import _native as nat
+    B, T, H, d, dtype, variant = case
+    announce("rla_context", case=case)
+    q, k, v, do = (rng.normal(size=(B, T, H, d)) for _ in range(4))
+    k = scans.l2_normalize_keys(k)
+    alpha, beta, gamma = (1 / (1 + np.exp(-rng.normal(size=(B, T, H)))) for _ in range(3))
+    ins = [to_dev(x, dtype) for x in (q, k, v, alpha, beta, gamma)]
+    tdo = to_dev(do, dtype)
+    P = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dt = 1 if dtype == torch.bfloat16 else 0
+    wsb = nat.query("edf_rla_scan_backward_workspace_bytes", B, T, H, d, dt)
+    recb = nat.query("edf_rla_scan_context_bytes", B, T, H, d, dt)
+    rec = torch.empty(recb, dtype=torch.uint8, device="cuda")
+    outs, grads = [], []
+    for saved in (False, True):
+        out = torch.empty_like(ins[0])
+        if saved:
+            nat.call("edf_fused_rla_scan_with_context", st, *(P(x) for x in ins), P(out), P(rec), recb,
+                     B, T, H, d, variant, 1.0, dt)
+        else:
+            nat.call("edf_fused_rla_scan", st, *(P(x) for x in ins), P(out), B, T, H, d, variant, 1.0, dt)
+        gs = [torch.empty_like(x) for x in ins]
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        if saved:
+            nat.call("edf_fused_rla_scan_backward_saved", st, *(P(x) for x in ins), P(tdo), *(P(x) for x in gs),
+                     P(rec), recb, P(ws), wsb, B, T, H, d, variant, 1.0, dt)
+        else:
+            nat.call("edf_fused_rla_scan_backward", st, *(P(x) for x in ins), P(out), P(tdo), *(P(x) for x in gs),
+                     P(ws), wsb, B, T, H, d, variant, 1.0, dt)
+        torch.cuda.synchronize()
+        outs.append(host(out))
+        grads.append(gs)
+    assert_close(outs[1], outs[0], TOL[dtype], "o")
+    for a, c in zip(*grads):
+        assert torch.equal(a, c)
