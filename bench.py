@@ -403,15 +403,20 @@ def bench_kda(torch, steps, warmup, B=8, T=2048, H=8, d=128):
     db = torch.empty_like(beta)
     wsb = nat.query("edf_kda_scan_backward_workspace_bytes", B, T, H, d, 1)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    recb = nat.query("edf_kda_scan_context_bytes", B, T, H, d, 1)
+    rec = torch.empty(recb, dtype=torch.uint8, device=dev)
     P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
+    # the training pair the autograd path runs: a forward that keeps the 16-step states in the
+    # same pass, and the backward from them
     def fwd():
-        nat.call("edf_fused_kda_scan", stream, P(q), P(k), P(v), P(alpha), P(beta), P(out), B, T, H, d, 1)
+        nat.call("edf_fused_kda_scan_with_context", stream, P(q), P(k), P(v), P(alpha), P(beta), P(out), P(rec),
+                 recb, B, T, H, d, 1)
 
     def bwd():
-        nat.call("edf_fused_kda_scan_backward", stream, P(q), P(k), P(v), P(alpha), P(beta), P(out), P(do), P(dq),
-                 P(dk), P(dv), P(da), P(db), P(ws), wsb, B, T, H, d, 1)
+        nat.call("edf_fused_kda_scan_backward_saved", stream, P(q), P(k), P(v), P(alpha), P(beta), P(do), P(dq),
+                 P(dk), P(dv), P(da), P(db), P(rec), recb, P(ws), wsb, B, T, H, d, 1)
 
     fwd_ms, bwd_ms = _time_pair(torch, steps, warmup, fwd, bwd)
     return dict(fwd_ms=fwd_ms, bwd_ms=bwd_ms, tokens_per_s=B * T / (fwd_ms + bwd_ms) * 1e3,

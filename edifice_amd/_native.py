@@ -75,6 +75,9 @@ SIGNATURES = {
     "edf_fused_kda_scan": (I, [P, P, P, P, P, P, P, I, I, I, I, I]),
     "edf_fused_kda_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_kda_scan_backward_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_kda_scan_context_bytes": (S, [I, I, I, I, I]),
+    "edf_fused_kda_scan_with_context": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I]),
+    "edf_fused_kda_scan_backward_saved": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, S, P, S, I, I, I, I, I]),
     "edf_fused_delta_product_scan": (I, [P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_delta_product_workspace_bytes": (S, [I, I, I, I, I, I]),
     "edf_fused_delta_product_scan_backward": (I, [P, P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),

@@ -225,4 +225,41 @@ int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, cons
                                   grad_alpha, workspace, batch, seq_len, num_heads, head_dim, dtype, 1, 1, nullptr);
 }
 
+size_t edf_kda_scan_context_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype) {
+  (void)dtype;
+  if (batch <= 0 || seq_len <= 0 || num_heads <= 0 || head_dim <= 0 || head_dim > 128) return 0;
+  return edf::dr_seq_context_bytes(batch, num_heads, seq_len, head_dim);
+}
+
+int edf_fused_kda_scan_with_context(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                    const void* beta, void* out, void* context, size_t context_bytes, int batch,
+                                    int seq_len, int num_heads, int head_dim, int dtype) {
+  int rc = edf::check_dr(batch, seq_len, num_heads, head_dim, dtype, EDF_BETA_PER_HEAD);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && alpha && beta && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const size_t need = edf::dr_seq_context_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(context && context_bytes >= need, EDF_ERR_WORKSPACE, "context too small: need %zu bytes", need);
+  return edf::dr_seq_run(stream, q, k, v, beta, alpha, out, batch, seq_len, num_heads, head_dim, dtype, 1, 1,
+                         (float*)context);
+}
+
+int edf_fused_kda_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                      const void* beta, const void* grad_out, void* grad_q, void* grad_k,
+                                      void* grad_v, void* grad_alpha, void* grad_beta, const void* context,
+                                      size_t context_bytes, void* workspace, size_t workspace_bytes, int batch,
+                                      int seq_len, int num_heads, int head_dim, int dtype) {
+  int rc = edf::check_dr(batch, seq_len, num_heads, head_dim, dtype, EDF_BETA_PER_HEAD);
+  if (rc) return rc;
+  EDF_REQUIRE(q && k && v && alpha && beta && grad_out && grad_q && grad_k && grad_v && grad_alpha && grad_beta,
+              EDF_ERR_INVALID_ARG, "null tensor pointer");
+  const size_t needc = edf::dr_seq_context_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(context && context_bytes >= needc, EDF_ERR_WORKSPACE,
+              "context too small: need the %zu bytes the forward filled", needc);
+  const size_t need = edf::dr_seq_backward_workspace_bytes(batch, num_heads, seq_len, head_dim);
+  EDF_REQUIRE(workspace && workspace_bytes >= need, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes", need);
+  return edf::dr_seq_backward_run(stream, q, k, v, beta, alpha, grad_out, grad_q, grad_k, grad_v, grad_beta,
+                                  grad_alpha, workspace, batch, seq_len, num_heads, head_dim, dtype, 1, 1,
+                                  (const float*)context);
+}
+
 }  // extern "C"

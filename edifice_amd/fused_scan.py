@@ -633,8 +633,15 @@ class _KDA(torch.autograd.Function):
         if alpha.shape != q.shape or tuple(beta.shape) != (bsz, seq, nh):
             raise EdificeHipError("kda_scan needs alpha [B, T, H, d] and beta [B, T, H]")
         out = torch.empty_like(v)
-        nat.call("edf_fused_kda_scan", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out), bsz, seq, nh,
-                 hd, dtype_flag(q))
+        ctx.rec, ctx.recb = None, 0
+        if any(ctx.needs_input_grad):  # keep the 16-step states the backward reads
+            ctx.recb = nat.query("edf_kda_scan_context_bytes", bsz, seq, nh, hd, dtype_flag(q))
+            ctx.rec = _u8(ctx.recb, q)
+            nat.call("edf_fused_kda_scan_with_context", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out),
+                     _p(ctx.rec), ctx.recb, bsz, seq, nh, hd, dtype_flag(q))
+        else:
+            nat.call("edf_fused_kda_scan", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out), bsz, seq,
+                     nh, hd, dtype_flag(q))
         ctx.save_for_backward(q, k, v, alpha, beta, out)
         return out
 
@@ -646,8 +653,10 @@ class _KDA(torch.autograd.Function):
         dq, dk, dv, da, db = (torch.empty_like(t) for t in (q, k, v, alpha, beta))
         wsb = nat.query("edf_kda_scan_backward_workspace_bytes", bsz, seq, nh, hd, dtype_flag(q))
         ws = _u8(wsb, q)
-        nat.call("edf_fused_kda_scan_backward", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(out), _p(do),
-                 _p(dq), _p(dk), _p(dv), _p(da), _p(db), _p(ws), wsb, bsz, seq, nh, hd, dtype_flag(q))
+        nat.call("edf_fused_kda_scan_backward_saved", _stream(), _p(q), _p(k), _p(v), _p(alpha), _p(beta), _p(do),
+                 _p(dq), _p(dk), _p(dv), _p(da), _p(db), _p(ctx.rec), ctx.recb, _p(ws), wsb, bsz, seq, nh, hd,
+                 dtype_flag(q))
+        ctx.rec = None
         return dq, dk, dv, da, db
 
 

@@ -237,6 +237,21 @@ int edf_fused_kda_scan_backward(void* stream, const void* q, const void* k, cons
                                 void* grad_k, void* grad_v, void* grad_alpha, void* grad_beta, void* workspace,
                                 size_t workspace_bytes, int batch, int seq_len, int num_heads, int head_dim,
                                 int dtype);
+
+/* No reference counterpart (its backward re-runs a checkpointing forward): a training KDA
+ * forward that also keeps the states every 16 steps in a caller-kept context of
+ * edf_kda_scan_context_bytes() bytes (one pass writes out and the states), and the backward
+ * from that context (unchanged since), which then skips its forward re-run; gradients
+ * bit-identical to edf_fused_kda_scan_backward, workspace edf_kda_scan_backward_workspace_bytes(). */
+size_t edf_kda_scan_context_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
+int edf_fused_kda_scan_with_context(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                    const void* beta, void* out, void* context, size_t context_bytes, int batch,
+                                    int seq_len, int num_heads, int head_dim, int dtype);
+int edf_fused_kda_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* alpha,
+                                      const void* beta, const void* grad_out, void* grad_q, void* grad_k,
+                                      void* grad_v, void* grad_alpha, void* grad_beta, const void* context,
+                                      size_t context_bytes, void* workspace, size_t workspace_bytes, int batch,
+                                      int seq_len, int num_heads, int head_dim, int dtype);
 size_t edf_kda_scan_backward_workspace_bytes(int batch, int seq_len, int num_heads, int head_dim, int dtype);
 
 /* DeltaProduct: n_h delta-rule sub-steps per token on L2-normalised keys, then the RMS-

@@ -435,3 +435,46 @@ def test_rla_context_entry_points_agree(case, rng):
     assert_close(outs[1], outs[0], TOL[dtype], "o")
     for a, c in zip(*grads):
         assert torch.equal(a, c)
+
+
+def test_kda_context_entry_points_agree(rng):
+    """edf_fused_kda_scan_with_context gives the plain forward's output and
+    edf_fused_kda_scan_backward_saved from its context the recomputing backward's gradients,
+    bit for bit (same kernels)."""
+    import ctypes
+
+    from edifice_amd import _native as nat
+    B, T, H, d, dtype = 2, 45, 2, 64, torch.bfloat16
+    announce("kda_context")
+    q, k, v, do = (rng.normal(size=(B, T, H, d)) for _ in range(4))
+    k = scans.l2_normalize_keys(k)
+    alpha = -rng.uniform(0.01, 0.3, size=(B, T, H, d))  # log decay, as test_kda_fwd_bwd
+    beta = rng.uniform(0.1, 0.9, size=(B, T, H))
+    ins = [to_dev(x, dtype) for x in (q, k, v, alpha, beta)]
+    tdo = to_dev(do, dtype)
+    P = lambda x: ctypes.c_void_p(x.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    wsb = nat.query("edf_kda_scan_backward_workspace_bytes", B, T, H, d, 1)
+    recb = nat.query("edf_kda_scan_context_bytes", B, T, H, d, 1)
+    rec = torch.empty(recb, dtype=torch.uint8, device="cuda")
+    outs, grads = [], []
+    for saved in (False, True):
+        out = torch.empty_like(ins[0])
+        if saved:
+            nat.call("edf_fused_kda_scan_with_context", st, *(P(x) for x in ins), P(out), P(rec), recb, B, T, H, d, 1)
+        else:
+            nat.call("edf_fused_kda_scan", st, *(P(x) for x in ins), P(out), B, T, H, d, 1)
+        gs = [torch.empty_like(x) for x in ins]
+        ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+        if saved:
+            nat.call("edf_fused_kda_scan_backward_saved", st, *(P(x) for x in ins), P(tdo), *(P(x) for x in gs),
+                     P(rec), recb, P(ws), wsb, B, T, H, d, 1)
+        else:
+            nat.call("edf_fused_kda_scan_backward", st, *(P(x) for x in ins), P(out), P(tdo), *(P(x) for x in gs),
+                     P(ws), wsb, B, T, H, d, 1)
+        torch.cuda.synchronize()
+        outs.append(out)
+        grads.append(gs)
+    assert torch.equal(outs[0], outs[1])
+    for a, c in zip(*grads):
+        assert torch.equal(a, c)
