@@ -26,6 +26,7 @@ namespace {
 constexpr int RLA_RB = 16;  // state rows per workgroup
 constexpr int RLA_CKF = 16;  // forward staging chunk
 constexpr int RLA_CK = 8;    // backward chunk / checkpoint interval
+static_assert(RLA_CKF % RLA_CK == 0, "a forward chunk holds whole checkpoint intervals");
 
 struct RLAArgs {
   const void *q, *k, *v, *alpha, *beta, *gamma, *dout;
@@ -179,13 +180,15 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
         o = row16_sum(o);
         if (tc == 0 && i < p.d && t0 + tt < p.T) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
       }
-    }
-    if (p.ckpt != nullptr) {
-      float* cp = p.ckpt + (((long)bh * p.nck + t0 / CK) * 2) * DP * DP + (long)i * DP + tc;
+      // both states after every RLA_CK steps (a 16-step chunk writes two; none past the last)
+      const int ck = (t0 + tt) / RLA_CK;
+      if (tt % RLA_CK == RLA_CK - 1 && p.ckpt != nullptr && ck < p.nck) {
+        float* cp = p.ckpt + (((long)bh * p.nck + ck) * 2) * DP * DP + (long)i * DP + tc;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        cp[16 * c] = S[c];
-        cp[DP * DP + 16 * c] = R[c];
+        for (int c = 0; c < NC; ++c) {
+          cp[16 * c] = S[c];
+          cp[DP * DP + 16 * c] = R[c];
+        }
       }
     }
     // the other stage was last read in the previous chunk, before the barrier below it
@@ -517,10 +520,10 @@ int edf_fused_rla_scan_with_context(void* stream, const void* q, const void* k, 
   EDF_REQUIRE(context && context_bytes >= need, EDF_ERR_WORKSPACE, "context too small: need %zu bytes", need);
   RLAArgs a = rla_args(q, k, v, alpha, beta, gamma, seq_len, num_heads, head_dim, clip_threshold);
   a.out = out;
-  a.ckpt = (float*)context;  // the checkpointing kernel writes the output too
+  a.ckpt = (float*)context;  // the output kernel also writes the states every RLA_CK steps
   hipStream_t s = as_stream(stream);
   const int bh = batch * num_heads;
-  return dtype == EDF_BF16 ? rla_launch_v<bf16>(s, a, 1, bh, variant) : rla_launch_v<float>(s, a, 1, bh, variant);
+  return dtype == EDF_BF16 ? rla_launch_v<bf16>(s, a, 0, bh, variant) : rla_launch_v<float>(s, a, 0, bh, variant);
 }
 
 int edf_fused_rla_scan_backward_saved(void* stream, const void* q, const void* k, const void* v, const void* alpha,
