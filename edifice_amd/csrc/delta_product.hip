@@ -377,20 +377,35 @@ __global__ __launch_bounds__(256) void dp_reduce_kernel(const DPArgs p, long nbt
   if (row >= nbts) return;
   const int lane = threadIdx.x & 63, d = p.d;
   float g[2], kv[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int j = lane + 64 * u;
-    float acc = 0.0f;
+  if (d % 2 == 0) {  // lane owns columns 2 lane, 2 lane + 1: 8-byte loads, the same order of sums
+    const int j = 2 * lane;
+    float2 acc = make_float2(0.0f, 0.0f);
     if (j < d)
-      for (int r = 0; r < nrb; ++r) acc += p.part_k[((long)r * nbts + row) * d + j];
-    g[u] = acc;
-    kv[u] = j < d ? ld((const TT*)p.k, row * d + j) : 0.0f;
+      for (int r = 0; r < nrb; ++r) {
+        const float2 v = *reinterpret_cast<const float2*>(p.part_k + ((long)r * nbts + row) * d + j);
+        acc.x += v.x, acc.y += v.y;
+      }
+    g[0] = acc.x, g[1] = acc.y;
+    kv[0] = j < d ? ld((const TT*)p.k, row * d + j) : 0.0f;
+    kv[1] = j < d ? ld((const TT*)p.k, row * d + j + 1) : 0.0f;
+  } else {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = lane + 64 * u;
+      float acc = 0.0f;
+      if (j < d)
+        for (int r = 0; r < nrb; ++r) acc += p.part_k[((long)r * nbts + row) * d + j];
+      g[u] = acc;
+      kv[u] = j < d ? ld((const TT*)p.k, row * d + j) : 0.0f;
+    }
   }
   const float inv = 1.0f / sqrtf(wave_sum(kv[0] * kv[0] + kv[1] * kv[1]) + DPR_EPS);
   const float dot = wave_sum(g[0] * kv[0] + g[1] * kv[1]) * inv;  // dkn . kn
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
-    if (lane + 64 * u < d) st((TT*)p.dk, row * d + lane + 64 * u, (g[u] - kv[u] * inv * dot) * inv);
+  for (int u = 0; u < 2; ++u) {
+    const int j = d % 2 == 0 ? 2 * lane + u : lane + 64 * u;
+    if (j < d) st((TT*)p.dk, row * d + j, (g[u] - kv[u] * inv * dot) * inv);
+  }
   if (lane == 0) {
     float acc = 0.0f;
     for (int r = 0; r < nrb; ++r) acc += p.part_b[(long)r * nbts + row];
