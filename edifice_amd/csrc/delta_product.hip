@@ -253,29 +253,43 @@ __global__ __launch_bounds__(256) void dp_finish_kernel(const DPArgs p, long nbt
   const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= nbth) return;
   const int lane = threadIdx.x & 63, d = p.d;
+  // column of element u of this lane: 2 lane + u when d is even (8-byte loads of the
+  // partials), lane + 64 u otherwise; the row blocks are added in the same order either way
+  const bool pair = d % 2 == 0;
+  auto col = [&](int u) { return pair ? 2 * lane + u : lane + 64 * u; };
   float o[2], g[2];
+  if (pair) {
+    float2 acc = make_float2(0.0f, 0.0f);
+    if (2 * lane < d)
+      for (int r = 0; r < nrb; ++r) {
+        const float2 v = *reinterpret_cast<const float2*>(p.part_o + ((long)r * nbth + row) * d + 2 * lane);
+        acc.x += v.x, acc.y += v.y;
+      }
+    o[0] = acc.x, o[1] = acc.y;
+  } else {
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int j = lane + 64 * u;
-    float acc = 0.0f;
-    if (j < d)
-      for (int r = 0; r < nrb; ++r) acc += p.part_o[((long)r * nbth + row) * d + j];
-    o[u] = acc;
-    g[u] = backward && j < d ? ld((const TT*)p.dout, row * d + j) : 0.0f;
+    for (int u = 0; u < 2; ++u) {
+      float acc = 0.0f;
+      if (col(u) < d)
+        for (int r = 0; r < nrb; ++r) acc += p.part_o[((long)r * nbth + row) * d + col(u)];
+      o[u] = acc;
+    }
   }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) g[u] = backward && col(u) < d ? ld((const TT*)p.dout, row * d + col(u)) : 0.0f;
   const float ms = wave_sum(o[0] * o[0] + o[1] * o[1]) / (float)d;
   const float rinv = 1.0f / sqrtf(ms + DPR_EPS);
   if (!backward) {
 #pragma unroll
     for (int u = 0; u < 2; ++u)
-      if (lane + 64 * u < d) st((TT*)p.out, row * d + lane + 64 * u, o[u] * rinv);
+      if (col(u) < d) st((TT*)p.out, row * d + col(u), o[u] * rinv);
     return;
   }
   const float dot = wave_sum(g[0] * o[0] + g[1] * o[1]);
   const float c = dot * rinv * rinv * rinv / (float)d;
 #pragma unroll
   for (int u = 0; u < 2; ++u)
-    if (lane + 64 * u < d) p.dO[row * d + lane + 64 * u] = g[u] * rinv - o[u] * c;
+    if (col(u) < d) p.dO[row * d + col(u)] = g[u] * rinv - o[u] * c;
 }
 
 // Backward over chunks of sub-steps in reverse.  Per sub-step (S_p the state before it,
