@@ -252,13 +252,22 @@ __global__ __launch_bounds__(256) void cc_bwd_kernel(const CCArgs a) {
   }
 }
 
-// dw [C][K] and dbias [C] = the P workgroup partials added in order
+// dw [C][K] and dbias [C] = the P workgroup partials: 8 lanes per output each add a
+// contiguous eighth of them in order, then the eight sums are combined in a fixed tree
+// (deterministic; one thread per output would leave most of the chip idle)
 template <typename T, int K>
 __global__ __launch_bounds__(256) void cc_reduce_kernel(const float* __restrict__ part, T* dw, T* dbias, int C, long P) {
-  const long i = (long)blockIdx.x * 256 + threadIdx.x;  // over C (K + 1)
-  if (i >= (long)C * (K + 1)) return;
+  const long i = ((long)blockIdx.x * 256 + threadIdx.x) >> 3;  // over C (K + 1)
+  const int sub = threadIdx.x & 7;
+  const long n = (long)C * (K + 1);
+  const long p0 = (P * sub) / 8, p1 = (P * (sub + 1)) / 8;
   float s = 0.0f;
-  for (long p = 0; p < P; ++p) s += part[p * C * (K + 1) + i];
+  if (i < n)
+    for (long p = p0; p < p1; ++p) s += part[p * n + i];
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 4);
+  if (i >= n || sub != 0) return;
   const int c = (int)(i / (K + 1)), j = (int)(i % (K + 1));
   if (j < K) {
     if (dw) dw[(long)c * K + j] = (T)s;
@@ -285,7 +294,7 @@ int cc_launch(hipStream_t s, CCArgs& a, bool bwd, int vec, void* dw, void* dbias
   if (int rc = check_launch("causal conv backward")) return rc;
   if (dw || dbias) {
     const long n = (long)a.C * (K + 1);
-    cc_reduce_kernel<T, K><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(a.part, (T*)dw, (T*)dbias, a.C,
+    cc_reduce_kernel<T, K><<<(unsigned)((8 * n + 255) / 256), 256, 0, s>>>(a.part, (T*)dw, (T*)dbias, a.C,
                                                                        (long)a.B * a.nrb);
     return check_launch("causal conv dw reduction");
   }
