@@ -116,7 +116,17 @@ __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ d
   if (row >= rows) return;
   const TI* p = dt + (long)row * dim;
   float s = 0.0f;
-  for (int d = lane; d < dim; d += 64) s += clampf(ld(p, d), DT_MIN, DT_MAX);
+  constexpr int V = 16 / sizeof(TI);  // one 16-byte load per lane and step when the row allows it
+  if (dim % V == 0 && ((uintptr_t)dt & 15) == 0) {
+    for (int d0 = lane * V; d0 < dim; d0 += 64 * V) {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + d0);
+      const TI* e = reinterpret_cast<const TI*>(&u);
+#pragma unroll
+      for (int i = 0; i < V; ++i) s += clampf(to_f32(e[i]), DT_MIN, DT_MAX);
+    }
+  } else {
+    for (int d = lane; d < dim; d += 64) s += clampf(ld(p, d), DT_MIN, DT_MAX);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
   if (lane == 0) dtm[row] = s / (float)dim;
@@ -756,20 +766,52 @@ template <typename TI>
 __global__ __launch_bounds__(256) void ss_mean_fixup_kernel(const float* __restrict__ part_m,
                                                             const TI* __restrict__ dt, TI* __restrict__ ddt,
                                                             int ntile, long rows, int dim) {
-  __shared__ float s_w[4];
-  const long row = blockIdx.x;
-  if (row >= rows) return;
+  // 16 rows per workgroup.  The tile partials of a row sit `rows` apart (one per channel
+  // tile): 16 lanes take 16 consecutive rows and the 16 lane groups a sixteenth of the tiles
+  // each, combined in a fixed order; then each wave updates whole rows, 16-byte accesses.
+  constexpr int RW = 16;
+  __shared__ float s_part[RW][RW + 1];
+  __shared__ float s_tot[RW];
+  const long r0 = (long)blockIdx.x * RW;
+  const int rl = threadIdx.x & (RW - 1), grp = threadIdx.x / RW;
   float tot = 0.0f;
-  for (int tl = threadIdx.x; tl < ntile; tl += 256) tot += part_m[(long)tl * rows + row];
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off);
-  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = tot;
+  if (r0 + rl < rows)
+    for (int tl = grp; tl < ntile; tl += 256 / RW) tot += part_m[(long)tl * rows + r0 + rl];
+  s_part[rl][grp] = tot;
   __syncthreads();
-  tot = ((s_w[0] + s_w[1]) + (s_w[2] + s_w[3])) / (float)dim;
-  for (int d = threadIdx.x; d < dim; d += 256) {
-    const long idx = row * dim + d;
-    const float dtr = ld(dt, idx);
-    if (dtr >= DT_MIN && dtr <= DT_MAX) st(ddt, idx, ld(ddt, idx) + tot);
+  if (threadIdx.x < RW) {
+    float t = 0.0f;
+#pragma unroll
+    for (int g = 0; g < RW; ++g) t += s_part[threadIdx.x][g];
+    s_tot[threadIdx.x] = t / (float)dim;
+  }
+  __syncthreads();
+  constexpr int V = 16 / sizeof(TI);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nrow = (int)min((long)RW, rows - r0);
+  const bool vec = dim % V == 0 && ((uintptr_t)dt & 15) == 0 && ((uintptr_t)ddt & 15) == 0;
+  for (int r = w; r < nrow; r += 4) {
+    const float t = s_tot[r];
+    const long base = (r0 + r) * dim;
+    if (vec) {
+      for (int d0 = lane * V; d0 < dim; d0 += 64 * V) {
+        const uint4 ud = *reinterpret_cast<const uint4*>(dt + base + d0);
+        uint4 ug = *reinterpret_cast<const uint4*>(ddt + base + d0);
+        const TI* vd = reinterpret_cast<const TI*>(&ud);
+        TI* vg = reinterpret_cast<TI*>(&ug);
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+          const float dtr = to_f32(vd[i]);
+          if (dtr >= DT_MIN && dtr <= DT_MAX) vg[i] = (TI)(to_f32(vg[i]) + t);
+        }
+        *reinterpret_cast<uint4*>(ddt + base + d0) = ug;
+      }
+    } else {
+      for (int d = lane; d < dim; d += 64) {
+        const float dtr = ld(dt, base + d);
+        if (dtr >= DT_MIN && dtr <= DT_MAX) st(ddt, base + d, ld(ddt, base + d) + t);
+      }
+    }
   }
 }
 
@@ -1116,10 +1158,10 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   }
   if (mean_mode) {
     if (io_dtype == EDF_BF16)
-      ss_mean_fixup_kernel<bf16><<<(unsigned)rows, 256, 0, s>>>(a.part_m, (const bf16*)dt, (bf16*)grad_dt, a.ntile,
+      ss_mean_fixup_kernel<bf16><<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a.part_m, (const bf16*)dt, (bf16*)grad_dt, a.ntile,
                                                                 rows, hidden);
     else
-      ss_mean_fixup_kernel<float><<<(unsigned)rows, 256, 0, s>>>(a.part_m, (const float*)dt, (float*)grad_dt,
+      ss_mean_fixup_kernel<float><<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a.part_m, (const float*)dt, (float*)grad_dt,
                                                                  a.ntile, rows, hidden);
     rc = check_launch("selective scan dt-mean coupling");
     if (rc) return rc;
