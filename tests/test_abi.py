@@ -193,3 +193,53 @@ def test_noalloc_flash_backward_rejects_sizes_beyond_its_scratch(lib):
     rows_max = (16 << 20) // 4
     rc = lib.edf_fused_flash_attention_backward_noalloc(None, *([p] * 9), 1, 1, rows_max + 1, 64, 1, 1)
     assert rc == 2 and b"no-alloc scratch" in lib.edf_last_error()
+
+
+def test_context_and_glue_entry_points_validate_before_launch(lib):
+    """The training-context forwards and saved backwards, the causal conv and the cross
+    entropy reject bad arguments (sizes, null pointers, short contexts and workspaces) with an
+    error code and message before any device work."""
+    p = ctypes.c_void_p(16)
+    # a context smaller than its query: EDF_ERR_WORKSPACE, for every op that records one
+    need = lib.edf_ttt_scan_context_bytes(2, 9, 16, 0)
+    assert need > 0
+    rc = lib.edf_fused_ttt_scan_with_context(None, *([p] * 8), p, need - 1, 2, 9, 16, 0)
+    assert rc == 4 and b"context" in lib.edf_last_error()
+    rc = lib.edf_fused_ttt_scan_backward_saved(None, *([p] * 15), p, need - 1, p, 1 << 30, 2, 9, 16, 0)
+    assert rc == 4 and b"context" in lib.edf_last_error()
+    need = lib.edf_delta_product_context_bytes(1, 5, 2, 2, 16, 0)
+    rc = lib.edf_fused_delta_product_scan_with_context(None, *([p] * 5), p, need - 1, 1, 5, 2, 2, 16, 0)
+    assert rc == 4 and b"context" in lib.edf_last_error()
+    rc = lib.edf_fused_delta_product_scan_backward_saved(None, *([p] * 9), None, 0, p, 1 << 30, 1, 5, 2, 2, 16, 0)
+    assert rc == 4 and b"context" in lib.edf_last_error()
+    need = lib.edf_rla_scan_context_bytes(1, 9, 2, 16, 0)
+    rc = lib.edf_fused_rla_scan_with_context(None, *([p] * 7), p, need - 1, 1, 9, 2, 16, 0, 1.0, 0)
+    assert rc == 4 and b"context" in lib.edf_last_error()
+    rc = lib.edf_fused_rla_scan_with_context(None, *([p] * 7), p, need, 1, 9, 2, 16, 3, 1.0, 0)
+    assert rc == 1 and b"variant" in lib.edf_last_error()
+    need = lib.edf_kda_scan_context_bytes(1, 9, 2, 16, 0)
+    rc = lib.edf_fused_kda_scan_with_context(None, *([p] * 6), p, need - 1, 1, 9, 2, 16, 0)
+    assert rc == 4 and b"context" in lib.edf_last_error()
+    rc = lib.edf_fused_kda_scan_backward_saved(None, *([p] * 11), p, need, p, 0, 1, 9, 2, 16, 0)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+    # the per-step delta rule's training context is its 16-step states; the chunked path's is
+    # its forward workspace
+    assert lib.edf_delta_rule_forward_context_bytes(1, 40, 2, 32, 0, 0) > 0
+    assert lib.edf_delta_rule_workspace_bytes(1, 40, 2, 32, 0, 0) == 0
+    assert lib.edf_delta_rule_forward_context_bytes(1, 128, 2, 128, 1, 1) == \
+        lib.edf_delta_rule_workspace_bytes(1, 128, 2, 128, 1, 1) > 0
+    # causal conv: kernel size, row stride, workspace
+    rc = lib.edf_causal_conv1d_silu(None, p, 8, p, p, p, 2, 5, 8, 9, 0)
+    assert rc == 2 and b"kernel_size" in lib.edf_last_error()
+    rc = lib.edf_causal_conv1d_silu(None, p, 7, p, p, p, 2, 5, 8, 4, 0)
+    assert rc == 1 and b"x_row_stride" in lib.edf_last_error()
+    rc = lib.edf_causal_conv1d_silu(None, p, 8, p, p, p, 0, 5, 8, 4, 0)
+    assert rc == 1 and lib.edf_last_error() == b"dimensions must be positive"
+    rc = lib.edf_causal_conv1d_silu_backward(None, p, 8, p, p, p, p, p, p, None, 0, 2, 5, 8, 4, 1)
+    assert rc == 4 and b"workspace" in lib.edf_last_error()
+    assert lib.edf_causal_conv1d_silu_backward_workspace_bytes(2, 5, 8, 9) == 0
+    # cross entropy
+    rc = lib.edf_cross_entropy(None, p, p, p, None, 4, 10, 1)
+    assert rc == 1 and b"null" in lib.edf_last_error()
+    rc = lib.edf_cross_entropy_backward(None, p, p, p, p, 0.25, p, 4, 10, 3)
+    assert rc == 1 and b"dtype" in lib.edf_last_error()
