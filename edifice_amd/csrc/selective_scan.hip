@@ -871,7 +871,12 @@ inline SSPlan choose_plan(int batch, int dim, int NP, bool bwd) {
     const long occ = std::max(1L, std::min((long)(163840 / lds), (long)(32 / nw)));
     const long per_cu = (nwg + 255) / 256;
     const long rounds = (per_cu + occ - 1) / occ;
-    const double score = (double)rounds * (double)std::min(per_cu, occ) * nw;
+    // backward: waves the busiest CU runs in sequence (the narrow plan also multiplies its
+    // dB / dC partials); forward (no cross-tile partials): the channel work the busiest CU
+    // holds, slowed where its resident waves cannot fill 12 slots (three per SIMD)
+    const double waves = (double)std::min(per_cu, occ) * nw;
+    const double score = bwd ? (double)rounds * waves
+                             : (double)per_cu * CT / std::min(1.0, waves / 12.0);
     if (score < best_score) {
       best_score = score;
       best = SSPlan{G, CT, nt};
