@@ -143,6 +143,10 @@ template <int N> constexpr int ss_pn() { return N == 4 ? 12 : N + 4; }
 // sums over a whole row are unchanged).  16-byte reads of whole rows are untouched.
 template <int N> EDF_DEVICE int ss_swz(int cl) { return N >= 4 ? (cl & 8) >> 2 : 0; }
 constexpr int mod64_to(int v, int r) { return v + ((r - v % 64) % 64 + 64) % 64; }  // smallest >= v, = r mod 64
+// Row stride of the dC / dB tile's state rows: a 16-channel row pair of one 32-lane write
+// needs rows 16 apart mod 32 words; 2 SSR is then 32 mod 64, which the paired channel-sum
+// reads rely on.  Wider rows (N < 4) keep a 64-word residue of their channel count.
+constexpr int ss_ssr(int v, int cw) { return cw == 16 ? v + ((16 - v % 32) % 32 + 32) % 32 : mod64_to(v, cw % 64); }
 
 // ---------------------------------------------------------------------------
 // forward
@@ -359,7 +363,7 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
   // dC / dB tile [qty][state][t][group][CW + 4]: a channel-group item reads one contiguous
   // run of CW values; SSR puts a wave's state rows on different banks
   constexpr int CWP = CW + 4, CTP = G * CWP;
-  constexpr int SSR = mod64_to(TS * CTP, CW % 64);
+  constexpr int SSR = ss_ssr(TS * CTP, CW);
   constexpr int NA = 2 * TS * CT;           // state sums per round: (t, channel, dx | ddt term)
   constexpr int NB = 2 * TS * N * G;        // channel-group sums per round: (qty, t, state, group)
   constexpr int NC = 2 * TS * N;            // partials per round: (qty, t, state)
@@ -849,7 +853,7 @@ inline size_t fwd_lds(int NP, int G) {
 inline int mod64_up(int v, int r) { return v + ((r - v % 64) % 64 + 64) % 64; }
 inline size_t bwd_lds(int NP, int G) {
   const int SW = NP < 4 ? NP : 4, CW = 64 / SW, CT = G * CW, TS = NP >= 32 ? 4 : 8;
-  const int PN = NP == 4 ? 12 : NP + 4, QP = mod64_up(TS * CT * PN, 32), SSR = mod64_up(TS * G * (CW + 4), CW % 64);
+  const int PN = NP == 4 ? 12 : NP + 4, QP = mod64_up(TS * CT * PN, 32), SSR = ss_ssr(TS * G * (CW + 4), CW);
   return (size_t)2 * 3 * CT * (SS_CK + 4) * 4 + 2 * SS_CK * 4 + (size_t)2 * QP * 4 + (size_t)2 * NP * SSR * 4 +
          (size_t)2 * 2 * TS * NP * G * 4 + (size_t)2 * TS * CT * 4 + CT * 4;
 }
@@ -870,13 +874,10 @@ inline SSPlan choose_plan(int batch, int dim, int NP, bool bwd) {
     const size_t lds = bwd ? bwd_lds(NP, G) : fwd_lds(NP, G);
     const long occ = std::max(1L, std::min((long)(163840 / lds), (long)(32 / nw)));
     const long per_cu = (nwg + 255) / 256;
-    const long rounds = (per_cu + occ - 1) / occ;
-    // backward: waves the busiest CU runs in sequence (the narrow plan also multiplies its
-    // dB / dC partials); forward (no cross-tile partials): the channel work the busiest CU
-    // holds, slowed where its resident waves cannot fill 12 slots (three per SIMD)
+    // the channel work the busiest CU holds, slowed where its resident waves cannot fill 12
+    // slots (three per SIMD); a tie goes to the wide plan (fewer dB / dC partials)
     const double waves = (double)std::min(per_cu, occ) * nw;
-    const double score = bwd ? (double)rounds * waves
-                             : (double)per_cu * CT / std::min(1.0, waves / 12.0);
+    const double score = (double)per_cu * CT / std::min(1.0, waves / 12.0);
     if (score < best_score) {
       best_score = score;
       best = SSPlan{G, CT, nt};
