@@ -38,6 +38,8 @@ SIGNATURES = {
     "edf_lstm_block_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_lstm_block_scan": (I, [P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_gru_block_workspace_bytes": (S, [I, I, I, I, I]),
+    "edf_lstm_block_status": (I, [P, P, S, I, I, I, I]),
+    "edf_gru_block_status": (I, [P, P, S, I, I, I, I]),
     "edf_fused_gru_block_scan": (I, [P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_fused_selective_scan": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I, I, I, I]),
     "edf_selective_scan_states_bytes": (S, [I, I, I, I]),
@@ -101,9 +103,6 @@ SIGNATURES = {
     "edf_fused_ttt_scan_with_context": (I, [P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
     "edf_fused_ttt_scan_backward_saved": (I, [P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, P, S, P, S, I, I,
                                                I, I]),
-    "edf_debug_mfma_32x32x16_bf16": (I, [P, P, P, P]),
-    "edf_debug_acc_kfrag_bf16": (I, [P, P, P]),
-    "edf_debug_lds_read_tr16": (I, [P, P, P]),
 }
 
 

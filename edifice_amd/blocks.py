@@ -7,6 +7,8 @@ forward and backward through a block runs the HIP kernels for the recurrence and
 
   MinGRULayer        lib/edifice/recurrent/min_gru.ex:272-295 (pre-norm, gate and candidate
                      projections, FusedScan.mingru, residual)
+  MinLSTMLayer       lib/edifice/recurrent/min_lstm.ex:267-292 (pre-norm, forget, input and
+                     candidate projections, FusedScan.minlstm, residual)
   MambaBlock         lib/edifice/ssm/common.ex:210-279 (norm, in_proj to 2 x inner, x/z split,
                      causal depthwise conv + SiLU, SSM, SiLU(z) gate, out_proj) with the SSM of
                      common.ex:333-373 (B/C and low-rank dt projections, softplus) and the dt-mean
@@ -61,6 +63,24 @@ class MinGRULayer(nn.Module):
     def forward(self, x):
         n = self.norm(x)
         return x + fs.mingru(self.gate(n).contiguous(), self.candidate(n).contiguous())
+
+
+class MinLSTMLayer(nn.Module):
+    """min_lstm.ex:267-292: x + MinLSTM(forget(norm x), input(norm x), candidate(norm x)); the
+    two gate sigmoids, their normalisation f / (f + i + 1e-6) and its chain rule run inside
+    the fused kernels."""
+
+    def __init__(self, hidden_size: int):
+        super().__init__()
+        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.forget = nn.Linear(hidden_size, hidden_size)
+        self.input = nn.Linear(hidden_size, hidden_size)
+        self.candidate = nn.Linear(hidden_size, hidden_size)
+
+    def forward(self, x):
+        n = self.norm(x)
+        return x + fs.minlstm(self.forget(n).contiguous(), self.input(n).contiguous(),
+                              self.candidate(n).contiguous())
 
 
 class MambaBlock(nn.Module):
@@ -232,12 +252,15 @@ def build(name: str, *, embed_size: int, hidden_size: int | None = None, num_lay
           conv_size: int = 4, use_short_conv: bool = True) -> SequenceModel:
     """``Edifice.build(name, opts)`` for the sequence-mixing families on the fused path.
 
-    name: "min_gru", "mamba", "delta_net", "gated_delta_net" or "gqa".  hidden_size defaults
+    name: "min_gru", "min_lstm", "mamba", "delta_net", "gated_delta_net" or "gqa".  hidden_size defaults
     to embed_size; an input projection is added when they differ."""
     hidden = hidden_size or embed_size
     proj = nn.Linear(embed_size, hidden) if hidden != embed_size else None
     if name == "min_gru":
         return SequenceModel("layers", [MinGRULayer(hidden) for _ in range(num_layers)], proj,
+                             nn.LayerNorm(hidden, eps=LN_EPS))
+    if name == "min_lstm":  # min_lstm.ex:113-162 (the unfused layer stack)
+        return SequenceModel("layers", [MinLSTMLayer(hidden) for _ in range(num_layers)], proj,
                              nn.LayerNorm(hidden, eps=LN_EPS))
     if name == "delta_net":
         return SequenceModel("layers", [DeltaNetLayer(hidden, num_heads) for _ in range(num_layers)], proj,

@@ -75,9 +75,10 @@ __global__ __launch_bounds__(256) void rnb_rt_kernel(const T* __restrict__ M, fl
 template <typename T>
 __global__ __launch_bounds__(256) void rnb_init_kernel(const T* __restrict__ h0, const T* __restrict__ c0,
                                                        float* __restrict__ hs0, float* __restrict__ cs,
-                                                       unsigned* __restrict__ bar, int B, int L, int H) {
+                                                       unsigned* __restrict__ bar, unsigned abort0, int B, int L,
+                                                       int H) {
   const long e = (long)blockIdx.x * 256 + threadIdx.x;
-  if (e < RNB_BAR_WORDS) bar[e] = 0u;
+  if (e < RNB_BAR_WORDS) bar[e] = e == RNB_BAR_ABORT ? abort0 : 0u;
   if (e >= (long)L * B * H) return;
   const int u = (int)(e % H), b = (int)((e / H) % B), l = (int)(e / ((long)B * H));
   const long src = ((long)b * L + l) * H + u;
@@ -330,14 +331,18 @@ __global__ __launch_bounds__(256) void rnb_persist_kernel(const RnbArgs p, unsig
   }
 }
 
-// out = input + sum_l h^l (the last layer's residual stream).
+// out = input + sum_l h^l (the last layer's residual stream); NaN everywhere when the
+// persistent kernel's grid barrier gave up (the abort word), so a timed-out recurrence never
+// reaches the caller as numbers (edf_*_block_status reports it as an error).
 template <typename T>
-__global__ __launch_bounds__(256) void rnb_out_kernel(const RnbArgs p, T* __restrict__ out) {
+__global__ __launch_bounds__(256) void rnb_out_kernel(const RnbArgs p, const unsigned* __restrict__ bar,
+                                                      T* __restrict__ out) {
   const long e = (long)blockIdx.x * 256 + threadIdx.x;
   const long n = (long)p.B * p.T * p.H;
   if (e >= n) return;
   float v = to_f32(((const T*)p.input)[e]);
   for (int l = 0; l < p.L; ++l) v += p.Hs[(long)l * n + e];
+  if (bar[RNB_BAR_ABORT] != 0u) v = __builtin_nanf("");
   st(out, e, v);
 }
 
@@ -384,8 +389,13 @@ int rnb_run(hipStream_t s, const void* input, const void* weights, const void* h
     rnb_rt_kernel<T, G><<<gslice, 256, 0, s>>>(Wl + (long)H * G * H + (long)G * H, ws.Rt + l * slice, H);
   }
   if (int rc = check_launch("rnn block weight layout")) return rc;
+  // EDF_RNN_BLOCK_PRESET_ABORT=1 starts the recurrence with the abort word already set (a
+  // test hook): every grid-barrier wait then ends at once, the kernel finishes normally and
+  // the time-out path (NaN output, an error from the status query) runs without a time-out.
+  const char* preset = getenv("EDF_RNN_BLOCK_PRESET_ABORT");
+  const unsigned abort0 = (preset != nullptr && preset[0] == '1') ? 1u : 0u;
   rnb_init_kernel<T><<<(unsigned)((std::max((long)L * B * H, (long)RNB_BAR_WORDS) + 255) / 256), 256, 0, s>>>(
-      (const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr, ws.hs0, ws.cs, ws.bar, B, L, H);
+      (const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr, ws.hs0, ws.cs, ws.bar, abort0, B, L, H);
   if (int rc = check_launch("rnn block initial state")) return rc;
   const dim3 grid(a.ngrp, (B + RNB_BS - 1) / RNB_BS, L);
   // one cooperative launch for the whole recurrence when every workgroup fits on the
@@ -412,8 +422,25 @@ int rnb_run(hipStream_t s, const void* input, const void* weights, const void* h
   if (!done)
     for (int j = 0; j < Tn + L - 1; ++j) rnb_diag_kernel<T, G><<<grid, 256, 0, s>>>(a, j);
   if (int rc = check_launch("rnn block step")) return rc;
-  rnb_out_kernel<T><<<(unsigned)(((long)B * Tn * H + 255) / 256), 256, 0, s>>>(a, (T*)out);
+  rnb_out_kernel<T><<<(unsigned)(((long)B * Tn * H + 255) / 256), 256, 0, s>>>(a, ws.bar, (T*)out);
   return check_launch("rnn block output");
+}
+
+// Waits for the stream, then reads the abort word the last call on this workspace left.
+inline int rnb_status(void* stream, const void* workspace, size_t workspace_bytes, int B, int Tn, int H, int L,
+                      int G) {
+  EDF_REQUIRE(B > 0 && Tn > 0 && H > 0 && L > 0, EDF_ERR_INVALID_ARG, "dimensions and num_layers must be positive");
+  const RnbWs w = rnb_layout(const_cast<void*>(workspace), B, Tn, H, L, G);
+  EDF_REQUIRE(workspace && workspace_bytes >= w.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
+              w.total);
+  unsigned word = 0;
+  hipStream_t s = as_stream(stream);
+  if (hipMemcpyAsync(&word, w.bar + RNB_BAR_ABORT, sizeof(word), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return set_error(EDF_ERR_LAUNCH, "rnn block status: %s", hipGetErrorString(hipGetLastError()));
+  EDF_REQUIRE(word == 0u, EDF_ERR_LAUNCH,
+              "rnn block: the persistent kernel's grid barrier timed out; its output was written as NaN");
+  return EDF_OK;
 }
 
 template <int G>
@@ -460,6 +487,16 @@ int edf_fused_lstm_block_scan(void* stream, const void* input, const void* weigh
                               int num_layers, int dtype) {
   return edf::rnb_dispatch<edf::RNB_LSTM>(stream, input, weights, h0, c0, out, workspace, workspace_bytes, batch,
                                           seq_len, hidden, num_layers, dtype);
+}
+
+int edf_lstm_block_status(void* stream, const void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                          int hidden, int num_layers) {
+  return edf::rnb_status(stream, workspace, workspace_bytes, batch, seq_len, hidden, num_layers, edf::RNB_LSTM);
+}
+
+int edf_gru_block_status(void* stream, const void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                         int hidden, int num_layers) {
+  return edf::rnb_status(stream, workspace, workspace_bytes, batch, seq_len, hidden, num_layers, edf::RNB_GRU);
 }
 
 int edf_fused_gru_block_scan(void* stream, const void* input, const void* weights, const void* h0, void* out,

@@ -45,6 +45,9 @@
 //     quantity, channel group) sums over 16 channels, added over the G groups one half
 //     later into one partial per workgroup, summed over the workgroups by a small
 //     deterministic kernel (no atomics).
+#include <stdlib.h>
+#include <string.h>
+
 #include <algorithm>
 
 #include "edf_abi.hpp"
@@ -858,14 +861,24 @@ inline size_t bwd_lds(int NP, int G) {
          (size_t)2 * 2 * TS * NP * G * 4 + (size_t)2 * TS * CT * 4 + CT * 4;
 }
 
+// EDF_SS_PLAN=narrow | wide forces one of the two compiled plans (every call reads it, so
+// the workspace query and the launch that follows agree while it is unchanged); anything
+// else, or unset, lets the host choose.  Tests use it to run both plans at every state size.
+inline int forced_plan() {
+  const char* f = getenv("EDF_SS_PLAN");
+  if (!f) return 0;
+  if (!strcmp(f, "narrow")) return 1;
+  if (!strcmp(f, "wide")) return 2;
+  return 0;
+}
+
 inline SSPlan choose_plan(int batch, int dim, int NP, bool bwd) {
   const int SW = NP < 4 ? NP : 4, CW = 64 / SW, NSG = NP / SW;
   const int gw = wide_groups(NP);
   SSPlan best{gw, gw * CW, (dim + gw * CW - 1) / (gw * CW)};
-#if defined(EDF_SS_FORCE_G)
-  if (EDF_SS_FORCE_G == 1) return SSPlan{1, CW, (dim + CW - 1) / CW};
-  return best;
-#endif
+  const int force = forced_plan();
+  if (force == 1) return SSPlan{1, CW, (dim + CW - 1) / CW};
+  if (force == 2) return best;
   double best_score = 1e30;
   const int cands[2] = {gw, 1};
   for (int G : cands) {

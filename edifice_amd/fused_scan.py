@@ -266,6 +266,8 @@ def _rnn_block(kind, input, weights, h0, c0, num_layers):
     else:
         nat.call("edf_fused_gru_block_scan", _stream(), _p(input), _p(weights), _p(h0), _p(out), _p(ws), wsb,
                  bsz, seq, hid, num_layers, flag)
+    # a grid barrier that gave up raises here (the output then holds NaN); waits for the stream
+    nat.call(f"edf_{kind}_block_status", _stream(), _p(ws), wsb, bsz, seq, hid, num_layers)
     return out
 
 
@@ -293,8 +295,13 @@ def _conv_operands(x, weight, bias):
     if x.dim() != 3 or x.stride(2) != 1:
         raise EdificeHipError(f"x must be [B, T, C] with contiguous channels, got shape {tuple(x.shape)}")
     bsz, seq, ch = x.shape
-    if seq > 1 and x.stride(0) != seq * x.stride(1):
-        x = x.contiguous()  # rows of one batch element must be equally spaced across batches
+    # The kernels address row (b, t) at (b * seq + t) * row_stride: every row equally spaced,
+    # across batch elements too.  With one step the batch stride is the row stride; a size-1
+    # dimension's stride carries no meaning and is not used.
+    row_stride = x.stride(1) if seq > 1 else (x.stride(0) if bsz > 1 else ch)
+    if row_stride < ch or (seq > 1 and bsz > 1 and x.stride(0) != seq * row_stride):
+        x = x.contiguous()
+        row_stride = ch
     w = weight.reshape(weight.shape[0], -1).contiguous()
     _shape("weight", w, (ch, w.shape[1]))
     b = _c(bias)
@@ -303,7 +310,7 @@ def _conv_operands(x, weight, bias):
     if not x.is_cuda:
         raise EdificeHipError("edifice_amd ops need GPU tensors (no CPU fallback)")
     _same(x, w, b)
-    return x, w, b, bsz, seq, ch, w.shape[1], (x.stride(1) if seq > 1 else ch)
+    return x, w, b, bsz, seq, ch, w.shape[1], row_stride
 
 
 class _CausalConvSilu(torch.autograd.Function):
@@ -314,7 +321,7 @@ class _CausalConvSilu(torch.autograd.Function):
         nat.call("edf_causal_conv1d_silu", _stream(), _p(x), xs, _p(w), _p(b), _p(out), bsz, seq, ch, k,
                  dtype_flag(x))
         ctx.save_for_backward(x, w, b)
-        ctx.wshape, ctx.has_bias = weight.shape, bias is not None
+        ctx.wshape, ctx.has_bias, ctx.row_stride = weight.shape, bias is not None, xs
         return out
 
     @staticmethod
@@ -322,7 +329,7 @@ class _CausalConvSilu(torch.autograd.Function):
         x, w, b = ctx.saved_tensors
         bsz, seq, ch = x.shape
         k = w.shape[1]
-        xs = x.stride(1) if seq > 1 else ch
+        xs = ctx.row_stride
         dy = dy.contiguous().to(x.dtype)
         dx = torch.empty((bsz, seq, ch), dtype=x.dtype, device=x.device)
         dw = torch.empty_like(w)

@@ -185,6 +185,17 @@ int edf_fused_gru_block_scan(void* stream, const void* input, const void* weight
                              int num_layers, int dtype);
 size_t edf_gru_block_workspace_bytes(int batch, int seq_len, int hidden, int num_layers, int dtype);
 
+/* Status of the last LSTM / GRU block call on `workspace` (no reference counterpart: the
+ * reference kernels have no grid barrier).  Waits for `stream`, then returns EDF_OK, or
+ * EDF_ERR_LAUNCH when the persistent kernel's bounded grid-barrier wait gave up (it cannot
+ * under a cooperative launch; were it to, the kernel still finishes and writes NaN as the
+ * output).  Same shape arguments as the call it checks.  EDF_RNN_BLOCK_PRESET_ABORT=1 in the
+ * environment makes every call start in that state (a test hook for this path). */
+int edf_lstm_block_status(void* stream, const void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                          int hidden, int num_layers);
+int edf_gru_block_status(void* stream, const void* workspace, size_t workspace_bytes, int batch, int seq_len,
+                         int hidden, int num_layers);
+
 /* ------------------------------------------------------------------------
  * Mamba selective scan
  *   x, dt, z, out, grad_x, grad_dt, grad_z: [B, T, D] in io_dtype
@@ -560,26 +571,6 @@ int edf_cross_entropy(void* stream, const void* logits, const int64_t* targets, 
 int edf_cross_entropy_backward(void* stream, const void* logits, const int64_t* targets, const float* lse,
                                const float* grad_loss, float inv_rows, void* grad_logits, int rows, int vocab,
                                int dtype);
-
-/* Diagnostic: C[32][32] = A[32][16] * B[16][32] (bf16 in, f32 out, row-major) with one
- * v_mfma_f32_32x32x16_bf16, using the lane layout the attention and delta-rule kernels
- * assume.  No reference counterpart; used by the GPU tests to pin that layout. */
-int edf_debug_mfma_32x32x16_bf16(void* stream, const void* A, const void* B, float* C);
-
-/* Diagnostic: reuse of an MFMA accumulator as the next product's operand (one
- * v_permlane32_swap per register pair).  x is a 64x32 f32 matrix (row-major) held as two
- * 32x32 accumulator tiles; out[lane][kk][e] (bf16, 64 x 4 x 8) receives the operand
- * fragment for k-step kk, which must equal x[16 kk + 8 (lane / 32) + e][lane % 32].
- * No reference counterpart; used by the GPU tests to pin the chunked delta rule's layout. */
-int edf_debug_acc_kfrag_bf16(void* stream, const float* x, void* out);
-
-/* Diagnostic: the transposed LDS read (ds_read_b64_tr_b16) the attention kernels use for
- * the V^T operand.  x is a 64x64 bf16 row-major tile; out[lane][rb][e] (bf16, 64 x 2 x 4)
- * receives, for rb = 0 and 1, what lane `lane` reads when lane i of each 16-lane group
- * addresses row 8 rb + 4 (group / 2) + i / 4, column 16 (group % 2) + 4 (i % 4); that must
- * be x[8 rb + 4 (lane / 32) + e][lane % 32].  No reference counterpart; used by the GPU
- * tests to pin that layout. */
-int edf_debug_lds_read_tr16(void* stream, const void* x, void* out);
 
 #ifdef __cplusplus
 }

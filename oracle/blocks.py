@@ -6,6 +6,7 @@ which hold PyTorch-generated weights, inputs, expected outputs and (DeltaNet) th
 gradient.  The models mirror the Edifice blocks:
 
   MinGRU   lib/edifice/recurrent/min_gru.ex:272-295 (layer), :305-326 (scan)
+  MinLSTM  lib/edifice/recurrent/min_lstm.ex:267-292 (layer), :304-334 (scan); no fixture
   DeltaNet lib/edifice/recurrent/delta_net.ex:197-219 (layer), :275-307 (projection split,
            sigmoid beta, key L2 norm with eps 1e-6 inside the sqrt)
   Mamba    lib/edifice/ssm/common.ex:210-279 (block), :333-373 (B/C/dt projections),
@@ -48,6 +49,23 @@ class _OracleMinGRU(torch.autograd.Function):
         gates, cand = ctx.saved_tensors
         dg, dc = scans.min_gru_scan_backward(_np(gates), _np(cand), _np(dy))
         return _t(dg, gates), _t(dc, cand)
+
+
+class _OracleMinLSTM(torch.autograd.Function):
+    """Logit-level MinLSTM (sigmoids applied inside), forward and the hand-derived backward."""
+
+    @staticmethod
+    def forward(ctx, fg, ig, cand):
+        ctx.save_for_backward(fg, ig, cand)
+        return _t(scans.min_lstm_scan(_np(fg), _np(ig), _np(cand)), fg)
+
+    @staticmethod
+    def backward(ctx, dy):
+        fg, ig, cand = ctx.saved_tensors
+        f, i = scans.sigmoid(_np(fg)), scans.sigmoid(_np(ig))
+        fwd = scans.minlstm_scan(f, i, _np(cand))
+        df, di, dc, _ = scans.minlstm_scan_backward(f, i, _np(cand), None, fwd, _np(dy))
+        return _t(df * f * (1 - f), fg), _t(di * i * (1 - i), ig), _t(dc, cand)
 
 
 class _OracleDelta(torch.autograd.Function):
@@ -110,6 +128,7 @@ def differentiable_oracle_ops():
     for gradient checks of whole blocks; the Mamba scan takes the z gate inside."""
     return {
         "mingru": _OracleMinGRU.apply,
+        "minlstm": _OracleMinLSTM.apply,
         "delta_net": _OracleDelta.apply,
         "gated_delta_net": _OracleGatedDelta.apply,
         "selective_scan_mean_gated": _OracleSelectiveScanMean.apply,
@@ -150,6 +169,17 @@ def min_gru_model(w, x, ops):
         p = f"weight.layers.{li}"
         n = _ln(w, p + ".norm", h)
         h = h + ops["mingru"](_dense(w, p + ".gate", n), _dense(w, p + ".candidate", n))
+    return _ln(w, "weight.final_norm", h)[:, -1]
+
+
+def min_lstm_model(w, x, ops):
+    """MinLSTM.build/1 (min_lstm.ex:113-162) with embed == hidden: 2 x (LN -> forget, input,
+    candidate projections -> scan -> residual, min_lstm.ex:267-292), final LN, last timestep."""
+    h = x
+    for li in range(2):
+        p = f"weight.layers.{li}"
+        n = _ln(w, p + ".norm", h)
+        h = h + ops["minlstm"](_dense(w, p + ".forget", n), _dense(w, p + ".input", n), _dense(w, p + ".candidate", n))
     return _ln(w, "weight.final_norm", h)[:, -1]
 
 

@@ -11,9 +11,9 @@ import pytest
 from tests.conftest import ROOT
 
 
-def _declared():
+def _declared(pattern=os.path.join(ROOT, "include", "*.h")):
     names = set()
-    for hdr in glob.glob(os.path.join(ROOT, "include", "*.h")):
+    for hdr in glob.glob(pattern):
         text = open(hdr).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names.update(re.findall(r"\b(edf_\w+)\s*\(", text))
@@ -37,6 +37,13 @@ def test_header_declares_entry_points():
 def test_library_exports_every_declared_symbol(lib):
     missing = [n for n in _declared() if not hasattr(lib, n)]
     assert not missing, f"declared but not exported: {missing}"
+
+
+def test_layout_probes_stay_out_of_the_product_header(lib):
+    """The three layout probes live in the test-only header tests/edifice_hip_probes.h."""
+    probes = _declared(os.path.join(ROOT, "tests", "*.h"))
+    assert probes and not set(probes) & set(_declared())
+    assert all(hasattr(lib, n) for n in probes)
 
 
 def test_ctypes_table_covers_header():

@@ -62,3 +62,16 @@ def test_hybrid_decoder_oracle_covers_every_parameter():
     names = {k for k, _ in model.named_parameters()}
     assert {k[len("weight."):] for k in w} == names
     assert all(w["weight." + k].grad is not None and w["weight." + k].grad.abs().max() > 0 for k in names)
+
+
+def test_min_lstm_block_layout():
+    """min_lstm.ex:267-292: per layer a norm and three hidden x hidden projections named
+    forget, input, candidate (the names pack_block_weights reads, min_lstm.ex:212-219)."""
+    from edifice_amd import blocks
+    m = blocks.build("min_lstm", embed_size=24, hidden_size=32)
+    sd = m.state_dict()
+    assert tuple(sd["input_projection.weight"].shape) == (32, 24)
+    for proj in ("forget", "input", "candidate"):
+        assert tuple(sd[f"layers.1.{proj}.weight"].shape) == (32, 32)
+    assert {k for k in sd if k.startswith("layers.0.")} == {
+        f"layers.0.{n}.{p}" for n in ("norm", "forget", "input", "candidate") for p in ("weight", "bias")}

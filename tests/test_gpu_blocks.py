@@ -19,7 +19,7 @@ from tests.test_blocks import FIXTURE_OPTS
 pytestmark = pytest.mark.gpu
 
 ORACLE_MODELS = {"min_gru": ob.min_gru_model, "delta_net": ob.delta_net_model, "mamba": ob.mamba_model,
-                 "gqa": ob.gqa_model, "gated_delta_net": ob.gated_delta_net_model}
+                 "gqa": ob.gqa_model, "gated_delta_net": ob.gated_delta_net_model, "min_lstm": ob.min_lstm_model}
 
 
 def _grads_match(model, w_ref, x_gpu, x_ref, name, seed=7):
@@ -69,6 +69,25 @@ def test_gated_delta_net_block_matches_oracle():
         ref = ob.gated_delta_net_model({k: v.detach() for k, v in w_ref.items()}, xn, ob.differentiable_oracle_ops())
         assert_close(model(x).cpu().numpy(), ref.numpy(), 1e-4, "gated_delta_net forward")
     _grads_match(model, w_ref, x, x_ref, "gated_delta_net")
+
+
+def test_min_lstm_block_matches_oracle():
+    """No reference fixture covers MinLSTM: random weights (embed == hidden, two layers),
+    checked against the oracle block (pinned by a written-out T = 2 form on the CPU),
+    forward and every gradient."""
+    from edifice_amd import blocks
+    announce("block_min_lstm")
+    torch.manual_seed(4)
+    model = blocks.build("min_lstm", embed_size=48)
+    w_ref = {"weight." + k: v.detach().double().clone().requires_grad_() for k, v in model.state_dict().items()}
+    model = model.to("cuda", torch.float32)
+    xn = torch.randn(3, 37, 48, dtype=torch.float64)
+    x = xn.float().cuda().requires_grad_()
+    x_ref = xn.clone().requires_grad_()
+    with torch.no_grad():
+        ref = ob.min_lstm_model({k: v.detach() for k, v in w_ref.items()}, xn, ob.differentiable_oracle_ops())
+        assert_close(model(x).cpu().numpy(), ref.numpy(), 1e-4, "min_lstm forward")
+    _grads_match(model, w_ref, x, x_ref, "min_lstm")
 
 
 @pytest.mark.parametrize("name", ["min_gru", "mamba", "gqa"])

@@ -20,6 +20,9 @@ CASES = [
     (3, 64, 40, 1, torch.float32, True, False),    # K = 1
     (1, 97, 24, 8, torch.float32, True, True),     # K = 8, T off the 32-step runs
     (2, 300, 2048, 4, torch.bfloat16, True, True), # config-5 width, many workgroups
+    (2, 1, 16, 4, torch.bfloat16, True, True),     # one step (decode), strided: batch stride 2C
+    (3, 1, 24, 3, torch.float32, True, True),      # the same in f32, three batch elements
+    (2, 1, 16, 4, torch.float32, False, False),    # one step, contiguous
 ]
 
 

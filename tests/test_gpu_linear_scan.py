@@ -327,3 +327,52 @@ def test_rnn_block_paths_agree(case, rng, monkeypatch):
     assert np.array_equal(whole, stepwise)
     r = lambda a: None if a is None else rounded(a, dtype)  # noqa: E731
     assert_close(whole, scans.rnn_block(kind, r(x), r(w), r(h0), r(c0), layers), TOL[dtype], "out")
+
+
+@pytest.mark.parametrize("kind", ["lstm", "gru"])
+def test_rnn_block_barrier_timeout_surfaces(kind, rng, monkeypatch):
+    """The persistent kernel's bounded grid-barrier wait, had it given up, must not hand the
+    caller numbers with EDF_OK.  EDF_RNN_BLOCK_PRESET_ABORT=1 starts the call with the abort
+    word set (no wait times out: every wait ends at once and the kernel finishes normally):
+    the output is NaN, the status query returns EDF_ERR_LAUNCH and the Python op raises.  A
+    following ordinary call on the same workspace is clean again."""
+    from edifice_amd import _native as nat
+    from edifice_amd import fused_scan as fs
+    bsz, seq, hid, layers = 2, 12, 64, 2
+    announce("rnn_block_abort", kind=kind)
+    gh = scans.RNN_BLOCK_GATES[kind] * hid
+    sc = 1 / np.sqrt(hid)
+    per = []
+    for _ in range(layers):
+        per += [sc * rng.normal(size=hid * gh), 0.3 * rng.normal(size=gh), sc * rng.normal(size=hid * gh),
+                1 + 0.2 * rng.normal(size=hid), 0.2 * rng.normal(size=hid)]
+    tw = to_dev(np.concatenate(per), torch.float32)
+    tx = to_dev(rng.normal(size=(bsz, seq, hid)), torch.float32)
+    monkeypatch.delenv("EDF_RNN_BLOCK_PER_STEP", raising=False)
+    wsb = nat.query(f"edf_{kind}_block_workspace_bytes", bsz, seq, hid, layers, 0)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=tx.device)
+    out = torch.empty_like(tx)
+    L = nat.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        if kind == "lstm":
+            return L.edf_fused_lstm_block_scan(stream, tx.data_ptr(), tw.data_ptr(), None, None, out.data_ptr(),
+                                               ws.data_ptr(), wsb, bsz, seq, hid, layers, 0)
+        return L.edf_fused_gru_block_scan(stream, tx.data_ptr(), tw.data_ptr(), None, out.data_ptr(), ws.data_ptr(),
+                                          wsb, bsz, seq, hid, layers, 0)
+
+    status = getattr(L, f"edf_{kind}_block_status")
+    monkeypatch.setenv("EDF_RNN_BLOCK_PRESET_ABORT", "1")
+    assert launch() == 0
+    assert status(stream, ws.data_ptr(), wsb, bsz, seq, hid, layers) == 3  # EDF_ERR_LAUNCH
+    assert b"timed out" in L.edf_last_error()
+    assert torch.isnan(out).all()
+    with pytest.raises(nat.EdificeHipError, match="timed out"):
+        fs.lstm_block(tx, tw, None, None, layers) if kind == "lstm" else fs.gru_block(tx, tw, None, layers)
+    monkeypatch.delenv("EDF_RNN_BLOCK_PRESET_ABORT")
+    assert launch() == 0
+    assert status(stream, ws.data_ptr(), wsb, bsz, seq, hid, layers) == 0
+    want = scans.rnn_block(kind, rounded(tx.cpu().numpy(), torch.float32), rounded(tw.cpu().numpy(), torch.float32),
+                           None, None, layers)
+    assert_close(host(out), want, TOL[torch.float32], "clean call after the aborted one")

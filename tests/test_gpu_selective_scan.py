@@ -94,3 +94,95 @@ def test_selective_scan_config2_full_size_properties(rng):
     ref = scans.selective_scan(xr[b:b + 1, :, :256], rounded(dt, torch.bfloat16)[b:b + 1, :, :256], A[:256],
                                B[b:b + 1], C[b:b + 1], Dv[:256], zr[b:b + 1, :, :256])
     assert_close(host(y)[b:b + 1, :, :256], ref, TOL[torch.bfloat16], "row 3 vs oracle")
+
+
+# Every compiled (state size, channel groups) instantiation, forced through EDF_SS_PLAN: the
+# wide plan (G = 4 at N = 4 and 8, G = 3 at N = 16) and the narrow one (G = 1), forward and
+# backward, in both dt modes.  D = 100 spans several tiles of either plan with a ragged last
+# one; T = 70 ends off the 16-step checkpoint interval.
+PLAN_CASES = [
+    (n, plan, mode, io)
+    for n, io in ((3, torch.float32), (8, torch.float32), (16, torch.bfloat16), (16, torch.float32))
+    for plan in ("narrow", "wide")
+    for mode in ("channel", "mean")
+]
+
+
+@pytest.mark.parametrize("case", PLAN_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_selective_scan_each_plan(case, rng, monkeypatch):
+    from edifice_amd import fused_scan as fs
+    n, plan, mode, io = case
+    monkeypatch.setenv("EDF_SS_PLAN", plan)
+    announce("selective_scan_plan", n=n, plan=plan, mode=mode, io=io)
+    bsz, T, D = 2, 70, 100
+    x, dt, A, B, C, Dv, z = make_inputs(rng, bsz, T, D, n)
+    dy = rng.normal(size=x.shape)
+    par = torch.float32
+    tx, tdt, tz = (to_dev(a, io).requires_grad_() for a in (x, dt, z))
+    tA, tB, tC, tD = (to_dev(a, par).requires_grad_() for a in (A, B, C, Dv))
+    out = fs.selective_scan(tx, tdt, tA, tB, tC, tD, tz, dt_mode=mode)
+    out.backward(to_dev(dy, io))
+    xr, dtr, zr, dyr = (rounded(a, io) for a in (x, dt, z, dy))
+    tol = TOL[io]
+    assert_close(host(out), scans.selective_scan(xr, dtr, A, B, C, Dv, zr, mode), tol, "y")
+    g = scans.selective_scan_backward(xr, dtr, A, B, C, dyr, Dv, zr, mode)
+    for name, t in (("dx", tx), ("ddt", tdt), ("dA", tA), ("dB", tB), ("dC", tC), ("dD", tD), ("dz", tz)):
+        assert_close(host(t.grad), g[name], tol, name)
+
+
+def test_selective_scan_plans_agree_without_gate(rng, monkeypatch):
+    """No D, no gate: both plans give the oracle's result (the kernels' Z = false instances)."""
+    from edifice_amd import fused_scan as fs
+    x, dt, A, B, C, _, _ = make_inputs(rng, 2, 45, 72, 16)
+    dy = rng.normal(size=x.shape)
+    g = scans.selective_scan_backward(x, dt, A, B, C, dy)
+    for plan in ("narrow", "wide"):
+        monkeypatch.setenv("EDF_SS_PLAN", plan)
+        announce("selective_scan_plan_nogate", plan=plan)
+        tx, tdt, tA, tB, tC = (to_dev(a, torch.float32).requires_grad_() for a in (x, dt, A, B, C))
+        out = fs.selective_scan(tx, tdt, tA, tB, tC)
+        out.backward(to_dev(dy, torch.float32))
+        assert_close(host(out), scans.selective_scan(x, dt, A, B, C), TOL[torch.float32], f"y {plan}")
+        for name, t in (("dx", tx), ("ddt", tdt), ("dA", tA), ("dB", tB), ("dC", tC)):
+            assert_close(host(t.grad), g[name], TOL[torch.float32], f"{name} {plan}")
+
+
+def test_selective_scan_config5_width(rng, monkeypatch):
+    """The hybrid decoder's Mamba shape (config 5: B = 8, d_inner = 2048, N = 16, bf16 x, dt, z;
+    f32 A, B, C, D; dt-mean mode with the gate), at a short sequence.  The host's own choice
+    there is the narrow plan (G = 1: 1024 even workgroups against the wide plan's 344), which
+    the backward workspace size shows.  Row 5 is checked against the oracle over every
+    channel (its dt mean couples them all): y, dx, ddt, dz, dB, dC; dA and dD over channels
+    0-255, which x = 0 leaves to row 5 alone in the batch sums."""
+    from edifice_amd import fused_scan as fs
+    from edifice_amd import _native as nat
+    bsz, T, D, N, b0, W = 8, 136, 2048, 16, 5, 256
+    monkeypatch.delenv("EDF_SS_PLAN", raising=False)
+    auto = nat.query("edf_selective_scan_backward_workspace_bytes", bsz, T, D, N, 1, 1)
+    monkeypatch.setenv("EDF_SS_PLAN", "narrow")
+    narrow = nat.query("edf_selective_scan_backward_workspace_bytes", bsz, T, D, N, 1, 1)
+    monkeypatch.setenv("EDF_SS_PLAN", "wide")
+    wide = nat.query("edf_selective_scan_backward_workspace_bytes", bsz, T, D, N, 1, 1)
+    monkeypatch.delenv("EDF_SS_PLAN")
+    assert auto == narrow != wide, (auto, narrow, wide)
+    announce("selective_scan_c5_width", B=bsz, T=T, D=D, N=N)
+    x, dt, A, B, C, Dv, z = make_inputs(rng, bsz, T, D, N)
+    x[np.arange(bsz) != b0, :, :W] = 0.0
+    dy = rng.normal(size=x.shape)
+    tx, tdt, tz = (to_dev(a, torch.bfloat16).requires_grad_() for a in (x, dt, z))
+    tA, tB, tC, tD = (to_dev(a, torch.float32).requires_grad_() for a in (A, B, C, Dv))
+    y = fs.selective_scan(tx, tdt, tA, tB, tC, tD, tz, dt_mode="mean")
+    y.backward(to_dev(dy, torch.bfloat16))
+    torch.cuda.synchronize()
+    r = slice(b0, b0 + 1)
+    xr, dtr, zr, dyr = (rounded(a, torch.bfloat16)[r] for a in (x, dt, z, dy))
+    tol = TOL[torch.bfloat16]
+    assert_close(host(y)[r], scans.selective_scan(xr, dtr, A, B[r], C[r], Dv, zr, "mean"), tol, "y row 5")
+    g = scans.selective_scan_backward(xr, dtr, A, B[r], C[r], dyr, Dv, zr, "mean")
+    for name, t in (("dx", tx), ("ddt", tdt), ("dz", tz)):
+        assert_close(host(t.grad)[r], g[name], tol, f"{name} row 5")
+    assert_close(host(tB.grad)[r], g["dB"], tol, "dB row 5")
+    assert_close(host(tC.grad)[r], g["dC"], tol, "dC row 5")
+    # dA / dD: rows other than 5 hold x = 0 on channels 0-255, so only row 5 feeds those sums
+    assert_close(host(tA.grad)[:W], g["dA"][:W], tol, "dA channels 0-255")
+    assert_close(host(tD.grad)[:W], g["dD"][:W], tol, "dD channels 0-255")
