@@ -587,14 +587,16 @@ def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record()
-    for _ in range(steps):
+    for i in range(steps):
         step()
-    ev[1].record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    ms = ev[0].elapsed_time(ev[1]) / steps
-    return dict(step_ms=ms, tokens_per_s=B * T / ms * 1e3,
+    per_step = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    ms = float(np.median(per_step))
+    return dict(step_ms=ms, tokens_per_s=B * T / ms * 1e3, steps=steps, warmup=warmup,
+                step_ms_min=float(min(per_step)), step_ms_max=float(max(per_step)),
                 shape=dict(batch=B, seq=T, vocab=vocab, embed=embed, layers="4 mamba + 2 delta_net + 2 attention"))
 
 
@@ -610,14 +612,35 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
-    """Time the C restatement (oracle/cref.c, OpenMP f32) on the config-2 selective-scan
-    workload (about 3 s per fwd+bwd step on 8 host cores); returns GB/s under the same
-    byte accounting as the GPU figure."""
+def _cpu_median(fn, warmup=2, reps=5):
+    """Median wall time (s) of ``fn`` over ``reps`` runs after ``warmup`` untimed ones."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def _cpu_lib():
     from oracle import cbuild
 
     lib = cbuild.lib()
-    rng = np.random.default_rng(7)
+    lib.cref_threads.restype = ctypes.c_int
+    return lib
+
+
+def _cpu_entry(value, unit, lib, sample, **extra):
+    return dict(value=value, unit=unit, cores=int(lib.cref_threads()), kind="port", cpu_model=cpu_model(),
+                host_cpus=os.cpu_count(), sample=sample, **extra)
+
+
+CP = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+
+
+def _ss_cpu_inputs(rng, B, T, D, N):
     f32 = np.float32
     x = rng.normal(size=(B, T, D)).astype(f32)
     dt = np.log1p(np.exp(rng.normal(size=(B, T, D)) - 4)).astype(f32)
@@ -625,23 +648,139 @@ def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16, reps=3):
     Bm, Cm = (rng.normal(size=(B, T, N)).astype(f32) for _ in range(2))
     Dv = rng.normal(size=D).astype(f32)
     z, dy = (rng.normal(size=(B, T, D)).astype(f32) for _ in range(2))
+    return x, dt, A, Bm, Cm, Dv, z, dy
+
+
+def _ss_cpu_step(lib, ins, B, T, D, N):
+    x, dt, A, Bm, Cm, Dv, z, dy = ins
     out, dx, ddt, dz = (np.empty_like(x) for _ in range(4))
     dA, dB, dC, dD = np.zeros_like(A), np.zeros_like(Bm), np.zeros_like(Cm), np.zeros_like(Dv)
-    P = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        lib.cref_selective_scan_fwd(P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(out), B, T, D, N)
-        lib.cref_selective_scan_bwd(P(x), P(dt), P(A), P(Bm), P(Cm), P(Dv), P(z), P(dy), P(dx), P(ddt), P(dA),
-                                    P(dB), P(dC), P(dD), P(dz), B, T, D, N)
-        times.append(time.perf_counter() - t0)
+
+    def step():
+        lib.cref_selective_scan_fwd(CP(x), CP(dt), CP(A), CP(Bm), CP(Cm), CP(Dv), CP(z), CP(out), B, T, D, N)
+        lib.cref_selective_scan_bwd(CP(x), CP(dt), CP(A), CP(Bm), CP(Cm), CP(Dv), CP(z), CP(dy), CP(dx), CP(ddt),
+                                    CP(dA), CP(dB), CP(dC), CP(dD), CP(dz), B, T, D, N)
+    return step
+
+
+def cpu_baseline_selective_scan(B=8, T=2048, D=1536, N=16):
+    """Time the C restatement (oracle/cref.c, OpenMP f32) on the config-2 selective-scan
+    workload (the full configuration, a fraction of a second per fwd+bwd step on the host's
+    cores); returns GB/s under the same byte accounting as the GPU figure."""
+    lib = _cpu_lib()
+    t = _cpu_median(_ss_cpu_step(lib, _ss_cpu_inputs(np.random.default_rng(7), B, T, D, N), B, T, D, N))
     fb, bb = ss_bytes(B, T, D, N)
-    t = float(np.median(times))
-    lib.cref_threads.restype = ctypes.c_int
-    return dict(value=(fb + bb) / t / 1e9, unit="GB/s", cores=int(lib.cref_threads()), kind="port",
-                cpu_model=cpu_model(), host_cpus=os.cpu_count(),
-                sample=f"C restatement (Nx unavailable), selective scan fwd+bwd f32, B={B} T={T} D={D} N={N} "
-                       f"(the full config-2 workload), median of {reps}, {t:.2f} s per step")
+    return _cpu_entry((fb + bb) / t / 1e9, "GB/s", lib,
+                      f"C restatement (Nx unavailable), selective scan fwd+bwd f32, B={B} T={T} D={D} N={N} "
+                      f"(the full config-2 workload), median of 5 after 2 warm-ups, {t:.3f} s per step",
+                      s_per_step=t)
+
+
+def cpu_baseline_mingru(B=4, T=60, H=256):
+    """Config 1 (MinGRU f32 4x60x256, fwd+bwd) on the C restatement, GB/s under the GPU row's
+    byte accounting; the step is microseconds long, so each timed run is 200 steps."""
+    lib = _cpu_lib()
+    rng = np.random.default_rng(8)
+    f32 = np.float32
+    z = (1 / (1 + np.exp(-rng.normal(size=(B, T, H))))).astype(f32)
+    c, dy = (rng.normal(size=(B, T, H)).astype(f32) for _ in range(2))
+    out, dz, dc = (np.empty_like(z) for _ in range(3))
+    nul = ctypes.c_void_p(None)
+
+    def run():
+        for _ in range(200):
+            lib.cref_mingru_fwd(CP(z), CP(c), nul, CP(out), B, T, H)
+            lib.cref_mingru_bwd(CP(z), CP(c), nul, CP(out), CP(dy), CP(dz), CP(dc), nul, B, T, H)
+    t = _cpu_median(run) / 200
+    return _cpu_entry(9 * B * T * H * 4 / t / 1e9, "GB/s", lib,
+                      f"C restatement, MinGRU fwd+bwd f32 B={B} T={T} H={H} (the full config-1 workload), median of "
+                      f"5 runs of 200 steps after 2 warm-ups, {t * 1e6:.1f} us per step", s_per_step=t)
+
+
+def _delta_cpu(lib, B, T, H, d, per_head_beta, gated, seed):
+    rng = np.random.default_rng(seed)
+    f32 = np.float32
+    l2 = lambda a: (a / np.sqrt((a * a).sum(-1, keepdims=True) + 1e-6)).astype(f32)  # noqa: E731
+    q, k = l2(rng.normal(size=(B, T, H, d))), l2(rng.normal(size=(B, T, H, d)))
+    v, do = (rng.normal(size=(B, T, H, d)).astype(f32) for _ in range(2))
+    beta = (1 / (1 + np.exp(-rng.normal(size=(B, T, H) if per_head_beta else (B, T, H, d))))).astype(f32)
+    alpha = np.exp(-np.log1p(np.exp(rng.normal(size=(B, T, H))))).astype(f32) if gated else None
+    out, dq, dk, dv = (np.empty_like(q) for _ in range(4))
+    db = np.empty_like(beta)
+    da = np.empty((B, T, H), f32)
+    nul = ctypes.c_void_p(None)
+    ap, dap = (CP(alpha), CP(da)) if gated else (nul, nul)
+
+    def step():
+        lib.cref_delta_rule_fwd(CP(q), CP(k), CP(v), CP(beta), ap, CP(out), B, T, H, d, int(per_head_beta))
+        lib.cref_delta_rule_bwd(CP(q), CP(k), CP(v), CP(beta), ap, CP(do), CP(dq), CP(dk), CP(dv), CP(db), dap,
+                                B, T, H, d, int(per_head_beta))
+    return step
+
+
+def cpu_baseline_delta_rule(B=4, H=16, T=4096, d=128, C=64):
+    """Config 3 on the C restatement (recurrent form, f32, states checkpointed every 64 steps
+    for the backward), the full workload; TFLOP/s under the GPU row's chunked-form flop count."""
+    lib = _cpu_lib()
+    t = _cpu_median(_delta_cpu(lib, B, T, H, d, True, True, 9), warmup=1, reps=5)
+    flops = 3 * 2 * (5 * C * d + 3 * d * d) * B * H * T
+    return _cpu_entry(flops / t / 1e12, "TFLOP/s", lib,
+                      f"C restatement, gated delta rule fwd+bwd f32 (recurrent form), B={B} H={H} T={T} d={d} (the "
+                      f"full config-3 workload), median of 5 after 1 warm-up, {t:.3f} s per step", s_per_step=t)
+
+
+def _attn_cpu(lib, BH, T, d, causal, seed):
+    rng = np.random.default_rng(seed)
+    f32 = np.float32
+    q, k, v, do = (rng.normal(scale=d ** -0.25, size=(BH, T, d)).astype(f32) for _ in range(4))
+    out, dq, dk, dv = (np.empty_like(q) for _ in range(4))
+    lse = np.empty((BH, T), f32)
+
+    def step():
+        lib.cref_attention_fwd(CP(q), CP(k), CP(v), CP(out), CP(lse), BH, T, d, int(causal))
+        lib.cref_attention_bwd(CP(q), CP(k), CP(v), CP(out), CP(do), CP(lse), CP(dq), CP(dk), CP(dv), BH, T, d,
+                               int(causal))
+    return step
+
+
+def cpu_baseline_attention(B=4, H=32, T=4096, d=128, sample_heads=16):
+    """Config 4 on the C restatement (causal softmax attention, f32) over a bounded sample of
+    the (b, h) heads, which are independent and equal in cost; TFLOP/s under the GPU row's flop
+    count, and the full-step time scaled from the sample."""
+    lib = _cpu_lib()
+    t = _cpu_median(_attn_cpu(lib, sample_heads, T, d, True, 10), warmup=1, reps=5)
+    flops = 3.5 * 4 * sample_heads * T * T * d / 2
+    full = t * B * H / sample_heads
+    return _cpu_entry(flops / t / 1e12, "TFLOP/s", lib,
+                      f"C restatement, causal attention fwd+bwd f32 on {sample_heads} of the {B * H} heads "
+                      f"(T={T} d={d}), median of 5 after 1 warm-up, {t:.3f} s; full step scaled: {full:.2f} s",
+                      s_per_step=full)
+
+
+def cpu_baseline_hybrid(B=8, T=2048, embed=1024, sample_rows=1):
+    """Config 5's fused-op mix on the C restatement over a sample of its batch rows (rows are
+    independent and equal in cost): per row 4 Mamba selective scans (d_inner 2048, N 16), 2
+    DeltaNet rules (8 heads x 128, per-element beta) and 2 causal attentions (8 heads x 128),
+    forward and backward.  The dense layers, norms and loss are not timed (no CPU path here
+    runs them in the reference's form); tokens/s is the whole batch over the scaled op time."""
+    lib = _cpu_lib()
+    inner, N, H, d = 2 * embed, 16, 8, embed // 8
+    ss = _ss_cpu_step(lib, _ss_cpu_inputs(np.random.default_rng(11), sample_rows, T, inner, N), sample_rows, T,
+                      inner, N)
+    dr = _delta_cpu(lib, sample_rows, T, H, d, False, False, 12)
+    at = _attn_cpu(lib, sample_rows * H, T, d, True, 13)
+
+    def step():
+        for _ in range(4):
+            ss()
+        for _ in range(2):
+            dr()
+            at()
+    t = _cpu_median(step, warmup=1, reps=5) * B / sample_rows
+    return _cpu_entry(B * T / t, "tokens/s", lib,
+                      f"C restatement of config 5's fused ops only (4 selective scans, 2 delta rules, 2 causal "
+                      f"attentions, fwd+bwd, f32) on {sample_rows} of {B} batch rows (T={T}), median of 5 after 1 "
+                      f"warm-up, scaled to the batch: {t:.2f} s per step; dense layers excluded", s_per_step=t)
 
 
 def main():
@@ -700,7 +839,7 @@ def main():
                                                                          causal=False)
         configs["fox_attention_4x32x4096x128"] = bench_fox(torch, args.steps, args.warmup)
     if want("hybrid"):
-        configs["c5_hybrid_decoder"] = bench_hybrid(torch, max(2, args.steps // 5), 1)
+        configs["c5_hybrid_decoder"] = bench_hybrid(torch, max(5, args.steps // 4), 2)
     bwd_dom = ss["bwd_ms"] >= ss["fwd_ms"]
     dominant = ("edf_fused_selective_scan_backward (ss_bwd_kernel + dB/dC, dA/dD reductions)" if bwd_dom
                 else "edf_fused_selective_scan (ss_fwd_kernel)")
@@ -731,6 +870,18 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_selective_scan()
+        # the same C restatement on every other config (CPU time and speed-up per config)
+        cpu_rows = {"c1_mingru_f32_4x60x256": (cpu_baseline_mingru, "fwd_us", "bwd_us", 1e-6),
+                    "c3_gated_delta_rule": (cpu_baseline_delta_rule, "fwd_ms", "bwd_ms", 1e-3),
+                    "c4_flash_attention": (cpu_baseline_attention, "fwd_ms", "bwd_ms", 1e-3),
+                    "c5_hybrid_decoder": (cpu_baseline_hybrid, "step_ms", None, 1e-3)}
+        for key, (fn, f_key, b_key, unit_s) in cpu_rows.items():
+            if key in configs:
+                cb = fn()
+                row = configs[key]
+                gpu_s = (row[f_key] + (row[b_key] if b_key else 0.0)) * unit_s
+                cb["speedup_gpu_over_cpu"] = round(cb["s_per_step"] / gpu_s, 1)
+                row["cpu_baseline"] = cb
     if args.copy_probe:
         src = torch.ones(64 * 2 ** 20, dtype=torch.float32, device="cuda")  # 256 MiB
         dst = torch.empty_like(src)

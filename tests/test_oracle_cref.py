@@ -60,3 +60,45 @@ def test_cref_selective_scan(cref, rng, extras):
         pairs += [("dD", dD), ("dz", dz)]
     for n, a in pairs:
         assert_close(a, g[n], 1e-4, n)
+
+
+@pytest.mark.parametrize("gated,per_head", [(False, False), (True, True), (True, False)])
+def test_cref_delta_rule(cref, rng, gated, per_head):
+    """Forward and the checkpointed reverse pass (T spans three 64-step chunks, the last one
+    ragged) against the numpy oracle."""
+    B, T, H, d = 2, 150, 2, 12
+    f32 = np.float32
+    q, v, do = (rng.normal(size=(B, T, H, d)).astype(f32) for _ in range(3))
+    k = scans.l2_normalize_keys(rng.normal(size=(B, T, H, d))).astype(f32)
+    beta = rng.uniform(0.1, 0.9, size=(B, T, H) if per_head else (B, T, H, d)).astype(f32)
+    alpha = rng.uniform(0.8, 1.0, size=(B, T, H)).astype(f32) if gated else None
+    nul = ctypes.c_void_p(None)
+    out = np.empty_like(q)
+    cref.cref_delta_rule_fwd(P(q), P(k), P(v), P(beta), P(alpha) if gated else nul, P(out), B, T, H, d,
+                             int(per_head))
+    assert_close(out, scans.delta_rule(q, k, v, beta, alpha), 1e-4, "o")
+    dq, dk, dv = (np.empty_like(q) for _ in range(3))
+    dbeta = np.empty_like(beta)
+    dalpha = np.empty((B, T, H), f32)
+    cref.cref_delta_rule_bwd(P(q), P(k), P(v), P(beta), P(alpha) if gated else nul, P(do), P(dq), P(dk), P(dv),
+                             P(dbeta), P(dalpha) if gated else nul, B, T, H, d, int(per_head))
+    g = scans.delta_rule_backward(q, k, v, beta, do, alpha)
+    pairs = [("dq", dq), ("dk", dk), ("dv", dv), ("dbeta", dbeta)] + ([("dalpha", dalpha)] if gated else [])
+    for n, a in pairs:
+        assert_close(a, g[n], 1e-4, n)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_cref_attention(cref, rng, causal):
+    BH, T, d = 3, 45, 16
+    f32 = np.float32
+    q, k, v, do = (rng.normal(size=(1, BH, T, d)).astype(f32) for _ in range(4))
+    out, dq, dk, dv = (np.empty_like(q) for _ in range(4))
+    lse = np.empty((BH, T), f32)
+    cref.cref_attention_fwd(P(q), P(k), P(v), P(out), P(lse), BH, T, d, int(causal))
+    eo, el = scans.flash_attention(q, k, v, causal=causal, return_lse=True)
+    assert_close(out, eo, 1e-5, "o")
+    assert_close(lse, el[0], 1e-5, "lse")
+    cref.cref_attention_bwd(P(q), P(k), P(v), P(out), P(do), P(lse), P(dq), P(dk), P(dv), BH, T, d, int(causal))
+    for n, a, e in zip(("dq", "dk", "dv"), (dq, dk, dv), scans.flash_attention_backward(q, k, v, do, causal=causal)):
+        assert_close(a, e, 1e-4, n)
