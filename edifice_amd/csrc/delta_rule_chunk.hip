@@ -40,19 +40,26 @@ namespace {
 
 constexpr int CH = 64;      // chunk length
 constexpr int DK = 128;     // head dim handled by this path
-constexpr int VS = 32;      // d_v slice per scan workgroup
+constexpr int VS = 32;      // d_v slice per scan wave
 constexpr int KS = DK + 8;  // LDS row stride (bf16) of [*][DK] tiles
 constexpr int TS = CH + 8;  // LDS row stride (bf16) of [*][CH] tiles
+
+// W, W^T and Kd^T are stored for the scan with the contraction axis permuted within every
+// group of 16: stored position s holds logical position kperm(s) (elements 4..7 and 8..11
+// swapped), the order in which an MFMA accumulator tile holds the rows it hands on as an
+// operand (see the scan).
+EDF_DEVICE constexpr int kperm(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
 
 struct CkArgs {
   const bf16 *q, *k, *v, *beta, *alpha, *dout;
   bf16* out;
   bf16 *dq, *dk, *dv, *dbeta, *dalpha;
   float* lg;  // [ci][CH]       inclusive log-decay inside the chunk (ci = bh * nch + c)
-  bf16* W;    // [ci][CH][DK]   W = T diag(beta gamma) K
-  bf16* Wt;   // [ci][DK][CH]   W^T
+  bf16* W;    // [ci][CH][DK]   -W, W = T diag(beta gamma) K (d_k in kperm order)
+  bf16* Wt;   // [ci][DK][CH]   -W^T                         (t in kperm order)
   bf16* Ut;   // [ci][DK][CH]   U^T
-  bf16* Kdt;  // [ci][DK][CH]   Kd^T
+  bf16* Kdt;  // [ci][DK][CH]   Kd^T                         (t in kperm order)
+  bf16* Kd;   // [ci][CH][DK]   Kd                           (d_k in kperm order)
   bf16* Tt;   // [ci][CH][CH]   T^T
   bf16* P;    // [ci][CH][CH]   P = Q K^T o Gamma o tril, [t][s] (forward with fused output)
   bf16* hN;   // [ci][DK][DK]   same, [d_k][d_v]
@@ -166,6 +173,29 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
     }
   }
 
+  // Kd = diag(gamma_C / gamma) K as rows [t][d_k] in the scan's kperm order along d_k (the
+  // reverse scan's operand): stored chunk ch of row t holds logical columns 16 (ch / 2) +
+  // 4 (ch % 2) + 0..3 and 8 more on
+  if constexpr (BWD) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {  // 64 rows x 8 groups of 16 columns
+      const int e = tid + 256 * i, row = e >> 3, q = e & 7;
+      const bf16x8 lo = ld_row8(p.k, p, b, h, t0 + row, 16 * q), hi = ld_row8(p.k, p, b, h, t0 + row, 16 * q + 8);
+      const float sc = kds[row];
+      bf16x8 k0, k1;  // stored chunks 2 q (columns 0..3, 8..11 of the group) and 2 q + 1 (4..7, 12..15)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        k0[j] = (bf16)(sc * (float)lo[j]);
+        k0[4 + j] = (bf16)(sc * (float)hi[j]);
+        k1[j] = (bf16)(sc * (float)lo[4 + j]);
+        k1[4 + j] = (bf16)(sc * (float)hi[4 + j]);
+      }
+      bf16* dst = p.Kd + ci * CH * DK + row * DK + 16 * q;
+      *(bf16x8*)dst = k0;
+      *(bf16x8*)(dst + 8) = k1;
+    }
+  }
+
   // A from the K K^T tiles (I, J), operands straight from global; the tile above the diagonal is zero
   if (w != 1) {
     const int I = w >= 2 ? 1 : 0, J = (w == 3) ? 1 : 0;
@@ -246,19 +276,25 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   stage_t<256>(sKb, p.k, p, b, h, t0, nullptr);
   stage_t<256>(sVb, p.v, p, b, h, t0, bt);
   __syncthreads();
-  // K^T -> Kd^T (workspace) and (diag(beta gamma) K)^T (in place)
+  // K^T -> Kd^T (workspace, t in the scan's kperm order: logical t .. t + 3 of this chunk at
+  // stored kperm(t % 16), t + 4 .. t + 7 at kperm(t % 16 + 4)) and (diag(beta gamma) K)^T
+  // (in place)
   for (int e = tid; e < DK * CH / 8; e += 256) {
     const int d = e >> 3, tb = (e & 7) * 8;
     const bf16x8 kv = *(const bf16x8*)(sKb + d * TS + tb);
-    bf16x8 kb, kd;
+    bf16x8 kb;
+    bf16x4 kd0, kd1;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float kf = (float)kv[i];
       kb[i] = (bf16)(kbs[tb + i] * kf);
-      kd[i] = (bf16)(kds[tb + i] * kf);
+      if (i < 4) kd0[i] = (bf16)(kds[tb + i] * kf);
+      else kd1[i - 4] = (bf16)(kds[tb + i] * kf);
     }
     *(bf16x8*)(sKb + d * TS + tb) = kb;
-    *(bf16x8*)(p.Kdt + ci * DK * CH + d * CH + tb) = kd;
+    bf16* kdr = p.Kdt + ci * DK * CH + d * CH + (tb & ~15);
+    *(bf16x4*)(kdr + kperm(tb & 15)) = kd0;
+    *(bf16x4*)(kdr + kperm((tb & 15) + 4)) = kd1;
   }
   __syncthreads();
 
@@ -284,18 +320,26 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
   // (stores straight from the accumulator layout scatter each instruction over 32 rows).
   bf16* sW = (bf16*)u1;  // [t][d_k], row stride KS (over K^T once that is consumed)
   bf16* sU = (bf16*)u2;  // [d_v][t] or [d_k][t], row stride TS (over V^T)
-  auto copy_w = [&]() {
+  // stored 16-byte chunk ch of a kperm-ordered row: logical elements 16 (ch / 2) + 4 (ch % 2)
+  // + 0..3 and 8 more on
+  auto perm_chunk = [&](const bf16* row, int ch) {
+    const bf16* src = row + 16 * (ch >> 1) + 4 * (ch & 1);
+    return cat4(*(const bf16x4*)src, *(const bf16x4*)(src + 8));
+  };
+  auto copy_w = [&]() {  // -W in the scan's kperm order along d_k
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i, row = e >> 4, ch = e & 15;  // 64 rows of 256 bytes
-      *(bf16x8*)(p.W + ci * CH * DK + row * DK + 8 * ch) = *(const bf16x8*)(sW + row * KS + 8 * ch);
+      *(bf16x8*)(p.W + ci * CH * DK + row * DK + 8 * ch) = -perm_chunk(sW + row * KS, ch);
     }
   };
-  auto copy_u = [&](bf16* dst) {
+  // perm: -W^T, in the scan's kperm order along t; else U^T as staged
+  auto copy_u = [&](bf16* dst, bool perm) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = tid + 256 * i, row = e >> 3, ch = e & 7;  // 128 rows of 128 bytes
-      *(bf16x8*)(dst + ci * DK * CH + row * CH + 8 * ch) = *(const bf16x8*)(sU + row * TS + 8 * ch);
+      *(bf16x8*)(dst + ci * DK * CH + row * CH + 8 * ch) =
+          perm ? -perm_chunk(sU + row * TS, ch) : *(const bf16x8*)(sU + row * TS + 8 * ch);
     }
   };
   __syncthreads();  // V^T consumed
@@ -305,14 +349,14 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
 #pragma unroll
     for (int J = 0; J < 2; ++J) store_rows(sW + (32 * J) * KS + 32 * w, KS, XW[J], li, g);
     __syncthreads();
-    copy_u(p.Ut);
+    copy_u(p.Ut, false);
     copy_w();
   } else {
     f32x16 XWt[2];
 #pragma unroll
     for (int J = 0; J < 2; ++J) XWt[J] = product(sTb + (32 * J) * TS, sKb + (32 * w) * TS, J);
     __syncthreads();  // U^T staged, K^T consumed
-    copy_u(p.Ut);
+    copy_u(p.Ut, false);
 #pragma unroll
     for (int J = 0; J < 2; ++J) store_rows(sW + (32 * J) * KS + 32 * w, KS, XW[J], li, g);
     __syncthreads();  // W staged, U^T copied
@@ -320,258 +364,274 @@ __global__ __launch_bounds__(256) void dr_ck_prep_kernel(const CkArgs p) {
 #pragma unroll
     for (int J = 0; J < 2; ++J) store_rows(sU + (32 * w) * TS + 32 * J, TS, XWt[J], li, g);
     __syncthreads();
-    copy_u(p.Wt);
+    copy_u(p.Wt, true);
   }
 }
 
 // ---------------------------------------------------------------------------
-// scan over chunks, one workgroup per (b, h, d_v slice); wave w owns state rows
-// d_k = 32 w .. 32 w + 31 of the slice as one f32 accumulator tile.  Per chunk, waves 0
-// and 1 compute the two 32-step tiles of v (reading A1 and the published state from
-// LDS) and publish v; after a second barrier every wave updates its state rows with v
-// read from LDS.  (Each wave computing all of v itself reads four times the LDS bytes.)
-//   MODE 1 / 3 (forward states):  v = U - W h;          h = gamma_C h + Kd^T v
-//   MODE 2 (reverse, gradients):   v = dvl + Kd dh;      dh = gamma_C dh + dhl - W^T v
-// MODE 1 stores h as [d_k][d_v] and v (the backward's context); MODE 3 stores the same
-// and also forms the output of the slice, O = diag(gamma) Q h + P v: waves 2 and 3 (idle
-// while waves 0 and 1 form v) take one 32-step tile each, the Q h part before the v
-// barrier and the P v part after it, and write their O rows themselves;
-// MODE 2 stores dh (the gradient of the state leaving each chunk) as [d_k][d_v] and v^T.
-// Every stored tile is first staged in LDS in its global layout and then written by all
-// threads as contiguous 16-byte rows (the slice of one chunk is one 8 KB / 4 KB block, or
-// 64-byte row segments): storing straight from the accumulator layout scatters each
-// instruction over 32 rows, and those stores alone took half of the scan's time.  The v
-// tile of a step is written out at the end of the step.
+// scan over chunks, one wave per (b, h, 32-wide d_v slice), the state in registers.
+//   forward:  v = U - W h;           h = gamma_C h + Kd^T v         (stores h, v)
+//   reverse:  v = dvl + Kd dh;       dh = gamma_C dh + dhl - W^T v  (stores dh, v^T)
+// The d_v columns of the state evolve independently, so a wave owns its slice's whole
+// chain: the state is four 32x32 f32 accumulator tiles (rows d_k, lane = d_v column) and
+// v two (rows t); neither leaves the registers between the two products of a step.  An
+// accumulator tile is itself the B operand of a product that contracts over its rows,
+// with the contraction index in the order the accumulator holds it: lane half g of k-step
+// kk holds rows 16 kk + 4 g + 0..3 and 16 kk + 8 + 4 g + 0..3 (registers 8 kk' .. 8 kk' + 7).
+// The A operands read from memory use the same order: prep stores W, Kd^T and W^T in kperm
+// order along the contraction axis, so each A fragment is one 16-byte read; the reverse
+// pass's K rows come from k's own layout as two 8-byte reads.  Per chunk the operand tiles
+// (W or K, Kd^T or W^T: 32 KB; U^T or dvl's slice; the decays; in reverse dhl's slice) are
+// copied global -> LDS by DMA (no registers) one chunk ahead into the other of two buffers.
+// The stored h / dh ([d_k][d_v]) and v ([t][d_v]) leave through transposed LDS tiles: each
+// lane writes its accumulator column as 8-byte pieces of four consecutive rows, and
+// transposed reads (ds_read_b64_tr_b16) hand every lane 8 consecutive d_v of one row, one
+// 16-byte store; v^T ([d_v][t], reverse) is read back as plain rows.
 // ---------------------------------------------------------------------------
-constexpr int NS = VS + 8;  // LDS row stride (bf16) of [*][VS] tiles
+// 16-byte chunk slots of the scan's LDS tiles: 256-byte rows (16 chunks) XOR the row mod
+// 16, 128-byte rows (8 chunks) XOR (row / 2) mod 8.  A 16-lane read of one chunk of 16
+// consecutive rows then covers the 64 banks once.
+EDF_DEVICE int slot_k(int row, int c) { return row * 16 + (c ^ (row & 15)); }
+EDF_DEVICE int slot_t(int row, int c) { return row * 8 + (c ^ ((row >> 1) & 7)); }
+typedef __attribute__((address_space(3))) bf16 lbf16;
+typedef __attribute__((address_space(3))) float lf32;
+template <typename T> EDF_DEVICE T lds_ld(const lbf16* p) { return *(const __attribute__((address_space(3))) T*)p; }
+template <typename T> EDF_DEVICE void lds_st(lbf16* p, T v) { *(__attribute__((address_space(3))) T*)p = v; }
+EDF_DEVICE bf16x4 lds_tr16(const lbf16* p) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
 
-template <int MODE>
-__global__ __launch_bounds__(256) void dr_ck_scan_kernel(const CkArgs p) {
-  static_assert(MODE >= 1 && MODE <= 3, "scan mode");
-  constexpr bool REV = MODE == 2;
-  constexpr bool OUT = MODE == 3;
-  constexpr bool FWD_CTX = MODE == 1 || MODE == 3;  // store h as [d_k][d_v] and v as [t][d_v]
-  __shared__ __attribute__((aligned(16))) bf16 sA1[2][CH * KS];  // W, or Kd in the reverse pass: [t][d_k]
-  __shared__ __attribute__((aligned(16))) bf16 sSt[2][VS * KS];  // state slice, [d_v][d_k]
-  // the state slice as [d_k][d_v], v as [d_v][t] and (forward) as [t][d_v]
-  __shared__ __attribute__((aligned(16))) bf16 sN[2][DK * NS];
-  __shared__ __attribute__((aligned(16))) bf16 sV[2][VS * TS];
-  __shared__ __attribute__((aligned(16))) bf16 sV2[FWD_CTX ? 2 : 1][FWD_CTX ? CH * NS : 8];
-  // the output rows of waves 2 and 3 ([t][d_v], 32 rows each), written out by the wave
-  __shared__ __attribute__((aligned(16))) bf16 sO[OUT ? 2 : 1][OUT ? 32 * NS : 8];
+template <bool REV>
+__global__ __launch_bounds__(64) void dr_ck_scanw_kernel(const CkArgs p) {
+  // three buffers per chunk operand: chunk it + 2 is copied in while chunk it is used
+  __shared__ __attribute__((aligned(16))) bf16 sA1a[CH * DK];  // W (fwd) or K (rev) [t][d_k]
+  __shared__ __attribute__((aligned(16))) bf16 sA1b[CH * DK];
+  __shared__ __attribute__((aligned(16))) bf16 sA1c[CH * DK];
+  __shared__ __attribute__((aligned(16))) bf16 sA2a[DK * CH];  // Kd^T (fwd) or W^T (rev) [d_k][t]
+  __shared__ __attribute__((aligned(16))) bf16 sA2b[DK * CH];
+  __shared__ __attribute__((aligned(16))) bf16 sA2c[DK * CH];
+  __shared__ __attribute__((aligned(16))) bf16 sDa[REV ? 32 * DK : 8];  // dhl slice [32 d_v][d_k] (rev)
+  __shared__ __attribute__((aligned(16))) bf16 sDb[REV ? 32 * DK : 8];
+  __shared__ __attribute__((aligned(16))) bf16 sDc[REV ? 32 * DK : 8];
+  __shared__ __attribute__((aligned(16))) bf16 sXa[32 * CH];  // U^T (fwd) or dvl (rev) slice [32 d_v][t]
+  __shared__ __attribute__((aligned(16))) bf16 sXb[32 * CH];
+  __shared__ __attribute__((aligned(16))) bf16 sXc[32 * CH];
+  __shared__ __attribute__((aligned(16))) float sLa[CH];      // log-decays of the chunk
+  __shared__ __attribute__((aligned(16))) float sLb[CH];
+  __shared__ __attribute__((aligned(16))) float sLc[CH];
+  __shared__ __attribute__((aligned(16))) bf16 sHT[32 * DK];  // state slice transposed [32 d_v][d_k]
+  __shared__ __attribute__((aligned(16))) bf16 sVT[32 * CH];  // v slice transposed [32 d_v][t]
+  struct Buf {
+    lbf16 *a1, *a2, *dh, *xs;
+    lf32* lg;
+  };
+  const Buf B0{(lbf16*)sA1a, (lbf16*)sA2a, (lbf16*)sDa, (lbf16*)sXa, (lf32*)sLa};
+  const Buf B1{(lbf16*)sA1b, (lbf16*)sA2b, (lbf16*)sDb, (lbf16*)sXb, (lf32*)sLb};
+  const Buf B2{(lbf16*)sA1c, (lbf16*)sA2c, (lbf16*)sDc, (lbf16*)sXc, (lf32*)sLc};
+  lbf16 *const HT = (lbf16*)sHT, *const VT = (lbf16*)sVT;
 
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, g = l >> 5, li = l & 31;
-  constexpr int NSL = DK / VS;
+  const int l = threadIdx.x, g = l >> 5, li = l & 31;
+  constexpr int NSL = DK / 32;
   const int logical = remap_xcd(blockIdx.x, gridDim.x);  // the slices of one head share an XCD
   const long bh = logical / NSL;
-  const int v0 = (logical % NSL) * VS;
+  const int v0 = (logical % NSL) * 32;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-  auto chunk_of_ = [&](int it) { return REV ? p.nch - 1 - it : it; };
+  auto chunk_of = [&](int it) { return REV ? p.nch - 1 - it : it; };
 
-  f32x16 S = zero16();  // rows d_k = 32 w + d_row(r, g), column d_v = v0 + li
-
-  // output regions of this head (buffer resources: a dropped store needs no branch)
-  const long hbytes = (long)p.nch * DK * DK * 2, vbytes = (long)p.nch * DK * CH * 2;
-  const rsrc_t rH = make_rsrc((FWD_CTX ? p.hN : p.dmN) + bh * p.nch * DK * DK, (unsigned)hbytes);
-  const rsrc_t rV = make_rsrc((FWD_CTX ? p.vN : p.dvT) + bh * p.nch * DK * CH, (unsigned)vbytes);
-  auto st16 = [&](const rsrc_t& r, unsigned off, const bf16* src) {
-    __builtin_amdgcn_raw_buffer_store_b128(*(const u32x4*)src, r, (int)off, 0, 0);
-  };
-  // the v tile of step it (chunk c)
-  auto copy_v = [&](int it, int c) {
-    if constexpr (FWD_CTX) {  // v as [t][d_v]: 64 rows of 64 bytes
-      const int row = tid >> 2, ch = tid & 3;
-      st16(rV, (unsigned)(((c * CH + row) * DK + v0 + 8 * ch) * 2), sV2[it & 1] + row * NS + 8 * ch);
-    } else {  // v^T as [d_v][t]: 32 rows of 128 bytes
-      const int row = tid >> 3, ch = tid & 7;
-      st16(rV, (unsigned)(((c * DK + v0 + row) * CH + 8 * ch) * 2), sV[it & 1] + row * TS + 8 * ch);
-    }
-  };
-
-  // operands of the next two chunks, loaded ahead into two register sets (the loop is
-  // unrolled by two so that each set is addressed statically)
-  struct Pre {
-    bf16x8 a1[4];
-    float l1[4];
-    bf16x8 a2[4];
-    bf16x4 x0[4];  // this wave's t tile (w & 1) of U^T or dvl
-    bf16x4 y0[4];
-    float lgC;
-    // output (waves 2, 3): this lane's row t = 32 (w - 2) + li of Q and of P, log-decay at t
-    bf16x8 qo[OUT ? DK / 16 : 1];
-    bf16x8 po[OUT ? CH / 16 : 1];
-    float lgo;
-  };
-  Pre pre0, pre1;
-  // A1 rows of chunk c (consumed first, into LDS)
-  auto fetch_a1 = [&](Pre& P, int c) {
-    const long ci = bh * p.nch + c;
+  // Buffer resources over this head's regions; a DMA load's lane offset depends only on the
+  // lane and on j modulo the swizzle period (4 for 256-byte rows, 2 for 128-byte rows), the
+  // rest of every offset is scalar.
+  const long nchl = p.nch;
+  const rsrc_t rA1 = make_rsrc((REV ? p.Kd : p.W) + bh * nchl * CH * DK, (unsigned)(nchl * CH * DK * 2));
+  const rsrc_t rW = make_rsrc((REV ? p.Wt : p.W) + bh * nchl * CH * DK, (unsigned)(nchl * CH * DK * 2));
+  const rsrc_t rKd = make_rsrc(p.Kdt + bh * nchl * CH * DK, (unsigned)(nchl * CH * DK * 2));
+  const rsrc_t rDh = make_rsrc(REV ? p.dhl + bh * nchl * DK * DK : p.W, REV ? (unsigned)(nchl * DK * DK * 2) : 0u);
+  const rsrc_t rLg = make_rsrc(p.lg + bh * nchl * CH, (unsigned)(nchl * CH * 4));
+  const rsrc_t rX = make_rsrc((REV ? p.dvl : p.Ut) + bh * nchl * DK * CH, (unsigned)(nchl * DK * CH * 2));
+  const rsrc_t rH = make_rsrc((REV ? p.dmN : p.hN) + bh * nchl * DK * DK, (unsigned)(nchl * DK * DK * 2));
+  const rsrc_t rV = make_rsrc((REV ? p.dvT : p.vN) + bh * nchl * DK * CH, (unsigned)(nchl * DK * CH * 2));
+  unsigned o256[4], o128[2];  // DMA lane offsets (bytes) of the 256- and 128-byte-row tiles
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i;
-      const int row = e >> 4, col = (e & 15) * 8;
-      if (!REV) {
-        P.a1[i] = *(const bf16x8*)(p.W + ci * CH * DK + row * DK + col);
-      } else {
-        P.a1[i] = ld_row8(p.k, p, b, h, c * CH + row, col);
-        P.l1[i] = p.lg[ci * CH + row];
-      }
-    }
-  };
-  // the rest of chunk c (consumed at the end of its step)
-  auto fetch_rest = [&](Pre& P, int c) {
-    const long ci = bh * p.nch + c;
-    const bf16* a2 = (REV ? p.Wt : p.Kdt) + ci * DK * CH + (32 * w + li) * CH + 8 * g;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) P.a2[kk] = *(const bf16x8*)(a2 + 16 * kk);
-    const bf16* x0 = (REV ? p.dvl : p.Ut) + ci * DK * CH + (v0 + li) * CH + 4 * g;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) P.x0[q] = *(const bf16x4*)(x0 + 32 * (w & 1) + 8 * q);
-    if (REV) {
-      const bf16* y0 = p.dhl + ci * DK * DK + (v0 + li) * DK + 32 * w + 4 * g;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) P.y0[q] = *(const bf16x4*)(y0 + 8 * q);
-    }
-    P.lgC = p.lg[ci * CH + CH - 1];
-    if constexpr (OUT) {
-      // every wave loads (waves 0, 1 a valid row they do not use): no wave-dependent branch
-      // around the loads
-      const int t = 32 * (w & 1) + li;
-#pragma unroll
-      for (int kk = 0; kk < DK / 16; ++kk) P.qo[kk] = ld_row8(p.q, p, b, h, c * CH + t, 16 * kk + 8 * g);
-#pragma unroll
-      for (int kk = 0; kk < CH / 16; ++kk) P.po[kk] = *(const bf16x8*)(p.P + ci * CH * CH + t * CH + 16 * kk + 8 * g);
-      P.lgo = p.lg[ci * CH + t];
-    }
-  };
-  auto chunk_of = chunk_of_;
-  fetch_a1(pre0, chunk_of(0));
-  fetch_rest(pre0, chunk_of(0));
-  if (p.nch > 1) {
-    fetch_a1(pre1, chunk_of(1));
-    fetch_rest(pre1, chunk_of(1));
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * j + (l >> 4), lc = (l & 15) ^ (row & 15);
+    o256[j] = (unsigned)((row * DK + 8 * lc) * 2);
   }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = 8 * j + (l >> 3), lc = (l & 7) ^ ((row >> 1) & 7);
+    o128[j] = (unsigned)((row * CH + 8 * lc) * 2);
+  }
+  auto dma = [&](int c, const Buf& bf) {
+    lbf16 *a1 = bf.a1, *a2 = bf.a2, *dh = bf.dh, *xs = bf.xs;
+    lf32* lgs = bf.lg;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)  // -W (fwd) or Kd (rev): 4 rows of 256 bytes per load
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA1, (lds_void*)(a1 + 512 * j), 16, (int)o256[j & 3],
+                                               c * CH * DK * 2 + (j >> 2) * 4096, 0, 0);
+    if constexpr (REV) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)  // dhl rows d_v = v0 .. v0 + 31 ([d_v][d_k], 256-byte rows)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rDh, (lds_void*)(dh + 512 * j), 16, (int)o256[j & 3],
+                                                 (c * DK + v0) * DK * 2 + (j >> 2) * 4096, 0, 0);
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rLg, (lds_void*)lgs, 4, 4 * l, c * CH * 4, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)  // U^T (fwd) or dvl (rev) rows d_v = v0 .. v0 + 31 (128-byte rows)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, (lds_void*)(xs + 512 * j), 16, (int)o128[j & 1],
+                                               (c * DK + v0) * CH * 2 + (j >> 1) * 2048, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)  // Kd^T (fwd) or W^T (rev): 8 rows of 128 bytes per load
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(REV ? rW : rKd, (lds_void*)(a2 + 512 * j), 16, (int)o128[j & 1],
+                                               c * DK * CH * 2 + (j >> 1) * 2048, 0, 0);
+  };
 
-  // Each register set is consumed in place and refilled (for the chunk two steps
-  // ahead) right after its last use, so no copy of an in-flight load is needed.
-  auto body = [&](int it, Pre& P) {
+  f32x16 S[4];  // state slice: rows d_k = 32 m + d_row(r, g), column d_v = v0 + li
+#pragma unroll
+  for (int m = 0; m < 4; ++m) S[m] = zero16();
+
+  // transposed reads of the staging tiles: lane i of a 16-lane group G reads row (d_v)
+  // 8 G + 4 hf + i / 4, columns c0 + 4 (i % 4) .. + 3 and receives column c0 + i of rows
+  // 8 G + 4 hf .. + 3; two reads give 8 consecutive d_v of one row, stored at (row c0 + i,
+  // d_v v0 + 8 G ..)
+  const int G = l >> 4, i16 = l & 15;
+  const unsigned so = (unsigned)((i16 * DK + 8 * G) * 2);  // store offset in [rows][DK] layouts
+  const unsigned sor = (unsigned)(((l >> 3) * CH + 8 * (l & 7)) * 2);  // v^T rows (reverse)
+  auto tr_pair = [&](const lbf16* tile, bool k256, int c0) {
+    bf16x4 r[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int row = 8 * G + 4 * hf + (i16 >> 2), c = (c0 >> 3) + ((i16 & 3) >> 1);
+      r[hf] = lds_tr16(tile + 8 * (k256 ? slot_k(row, c) : slot_t(row, c)) + 4 * (i16 & 1));
+    }
+    return __builtin_bit_cast(u32x4, cat4(r[0], r[1]));
+  };
+
+  // Identity A fragments in the accumulator's contraction order: element e of lane (li, g) for
+  // k-step kk of a 32-row tile is 1 where its row 16 kk + 4 g + e (e < 4) or 16 kk + 8 + 4 g +
+  // e - 4 equals li.  A product with them adds a [rows][d_v] tile held as B fragments.
+  bf16x8 Id[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Id[kk][e] = (bf16)((16 * kk + (e < 4 ? 4 * g + e : 8 + 4 * g + e - 4)) == li ? 1.0f : 0.0f);
+  // B fragment of rows 32 tb + 16 kk + (accumulator order) of column li from a [32][cols]
+  // LDS tile holding the transpose (row li = column li of the operand)
+  auto bfrag_t = [&](const lbf16* tile, bool k256, int c0) {
+    const int c = c0 >> 3;
+    return k256 ? cat4(lds_ld<bf16x4>(tile + 8 * slot_k(li, c) + 4 * g), lds_ld<bf16x4>(tile + 8 * slot_k(li, c + 1) + 4 * g))
+                : cat4(lds_ld<bf16x4>(tile + 8 * slot_t(li, c) + 4 * g), lds_ld<bf16x4>(tile + 8 * slot_t(li, c + 1) + 4 * g));
+  };
+
+  auto body = [&](int it, const Buf& bf) {
+    const lbf16 *a1 = bf.a1, *a2 = bf.a2, *dh = bf.dh, *xs = bf.xs;
+    const lf32* lgs = bf.lg;
     const int c = chunk_of(it);
-    bf16* sa = sA1[it & 1];
-    bf16* ss = sSt[it & 1];
-    // publish the state entering (forward) / leaving (reverse) chunk c
+    // A fragments of the first product (rows t = 32 tb + li, 8 k-steps over d_k), all issued
+    // before the first MFMA so that their LDS latency overlaps
+    bf16x8 AX[2][8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      bf16x4 v;
+    for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (bf16)S[4 * q + e];
-      *(bf16x4*)(ss + li * KS + 32 * w + 8 * q + 4 * g) = v;
+      for (int tb = 0; tb < 2; ++tb) AX[tb][kk] = lds_ld<bf16x8>(a1 + 8 * slot_k(32 * tb + li, 2 * kk + g));
+    const float lgC = lgs[CH - 1];
+    // v = U + (-W) h (forward) or dvl + Kd dh (reverse): rows t = 32 tb + .., column d_v; the
+    // U / dvl tile enters through identity products
+    f32x16 V[2];
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      V[tb] = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) V[tb] = mfma32(Id[kk], bfrag_t(xs, false, 32 * tb + 16 * kk), V[tb]);
     }
-    {
-      bf16* sn = sN[it & 1];
+    // B fragments of the state (k = d_k) in bf16, staged transposed (four rows d_k of column
+    // li per 8-byte write)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sn[(32 * w + d_row(r, g)) * NS + li] = (bf16)S[r];
+    for (int kk = 0; kk < 8; ++kk) {
+      bf16x8 bs;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bs[e] = (bf16)S[kk >> 1][8 * (kk & 1) + e];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) V[tb] = mfma32(AX[tb][kk], bs, V[tb]);
+      // rows 16 kk + 4 g .. + 3 and 16 kk + 8 + 4 g .. + 3 of column li
+      lds_st(HT + 8 * slot_k(li, 2 * kk) + 4 * g, __builtin_shufflevector(bs, bs, 0, 1, 2, 3));
+      lds_st(HT + 8 * slot_k(li, 2 * kk + 1) + 4 * g, __builtin_shufflevector(bs, bs, 4, 5, 6, 7));
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // A fragments of the state update (rows d_k = 32 m + li, 4 k-steps over t)
+    bf16x8 AU[4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = tid + 256 * i;
-      const int row = e >> 4, col = (e & 15) * 8;
-      bf16x8 a = P.a1[i];
-      if (REV) {
-        const float sc = __expf(P.lgC - P.l1[i]);
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = (bf16)((float)a[j] * sc);
+      for (int kk = 0; kk < 4; ++kk) AU[m][kk] = lds_ld<bf16x8>(a2 + 8 * slot_t(32 * m + li, 2 * kk + g));
+    const float gC = __expf(lgC);
+    // B fragments of v (k = t); v itself is staged transposed ([d_v][t]: four rows t of
+    // column li per 8-byte write)
+    bf16x8 Bv[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Bv[kk][e] = (bf16)V[kk >> 1][8 * (kk & 1) + e];
+      lds_st(VT + 8 * slot_t(li, 2 * kk) + 4 * g, __builtin_shufflevector(Bv[kk], Bv[kk], 0, 1, 2, 3));
+      lds_st(VT + 8 * slot_t(li, 2 * kk + 1) + 4 * g, __builtin_shufflevector(Bv[kk], Bv[kk], 4, 5, 6, 7));
+    }
+    // state update over t: forward h = gamma_C h + Kd^T v; reverse dh = gamma_C dh + dhl +
+    // (-W^T) v, the dhl tile through identity products
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) S[m][r] *= gC;
+      if constexpr (REV) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) S[m] = mfma32(Id[kk], bfrag_t(dh, true, 32 * m + 16 * kk), S[m]);
       }
-      *(bf16x8*)(sa + row * KS + col) = a;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) S[m] = mfma32(AU[m][kk], Bv[kk], S[m]);
     }
-    const float gC = __expf(P.lgC);
-    // Prefetches are unconditional (past the last chunk they reload it): a conditional
-    // one makes the compiler copy the loaded registers at the loop latch behind a full
-    // vmcnt(0) drain, which serialises every step on an HBM round trip.
-    fetch_a1(P, chunk_of(min(it + 2, p.nch - 1)));
-    __syncthreads();
-
-    // v for the t tile w = 0, 1: X = A1 * state (rows t, column d_v), published as [d_v][t]
-    bf16* sv = sV[it & 1];
-    f32x16 XO = zero16();  // output tile of waves 2, 3: O^T rows d_v, column t = 32 (w - 2) + li
-    if (OUT && w >= 2) {
-      // diag(gamma) Q h while waves 0 and 1 form v
+    __builtin_amdgcn_sched_barrier(0);
+    // stored rows, 16 bytes per lane: the state [d_k][v0 .. v0 + 31] (eight transposed read
+    // pairs), then v [t][v0 ..] (forward, four pairs) or v^T [v0 .. v0 + 31][t] (reverse, rows)
 #pragma unroll
-      for (int kk = 0; kk < DK / 16; ++kk) XO = mfma32(*(const bf16x8*)(ss + li * KS + 16 * kk + 8 * g), P.qo[kk], XO);
-      const float gt = __expf(P.lgo);
+    for (int s = 0; s < 8; ++s)
+      __builtin_amdgcn_raw_buffer_store_b128(tr_pair(HT, true, 16 * s), rH, (int)so,
+                                             (c * DK * DK + 16 * s * DK + v0) * 2, 0);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) XO[r] *= gt;
-    }
-    if (w < 2) {
-      f32x16 X = zero16();
-#pragma unroll
-      for (int kk = 0; kk < DK / 16; ++kk) {
-        const bf16x8 a = *(const bf16x8*)(sa + (32 * w + li) * KS + 16 * kk + 8 * g);
-        const bf16x8 bb = *(const bf16x8*)(ss + li * KS + 16 * kk + 8 * g);
-        X = mfma32(a, bb, X);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float x0v = (float)P.x0[r >> 2][r & 3];
-        X[r] = REV ? x0v + X[r] : x0v - X[r];
-      }
-      store_rows(sv + 32 * w, TS, X, li, g);
-      if constexpr (FWD_CTX) {  // and as [t][d_v] for the store of v
-        bf16* dst = sV2[it & 1] + (32 * w) * NS + li;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dst[d_row(r, g) * NS] = (bf16)X[r];
+    for (int s = 0; s < 4; ++s) {
+      if constexpr (!REV) {
+        __builtin_amdgcn_raw_buffer_store_b128(tr_pair(VT, false, 16 * s), rV, (int)so,
+                                               (c * CH * DK + 16 * s * DK + v0) * 2, 0);
+      } else {  // rows d_v = 8 s + (l >> 3), chunk l & 7
+        const u32x4 d = lds_ld<u32x4>(VT + 8 * slot_t(8 * s + (l >> 3), l & 7));
+        __builtin_amdgcn_raw_buffer_store_b128(d, rV, (int)sor, (c * DK * CH + (v0 + 8 * s) * CH) * 2, 0);
       }
     }
-    __syncthreads();
-    // state update: Y = A2 * v, contracting over t
-    f32x16 Y = zero16();
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) Y = mfma32(P.a2[kk], *(const bf16x8*)(sv + li * TS + 16 * kk + 8 * g), Y);
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      S[r] = REV ? fmaf(gC, S[r], (float)P.y0[r >> 2][r & 3] - Y[r]) : fmaf(gC, S[r], Y[r]);
-    if (OUT && w >= 2) {
-      // + P v (P[t][s] = 0 for s > t: the first tile needs s < 32 only), staged as [t][d_v]
-      // rows of this wave and written out as 64-byte row segments
-      const int J = w - 2;
-#pragma unroll
-      for (int kk = 0; kk < CH / 16; ++kk) {
-        if (kk >= 2 * (J + 1)) continue;
-        XO = mfma32(*(const bf16x8*)(sv + li * TS + 16 * kk + 8 * g), P.po[kk], XO);
-      }
-      bf16* so = sO[J];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) so[li * NS + d_row(r, g)] = (bf16)XO[r];
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = l + 64 * i, row = e >> 2, ch = e & 3;  // 32 rows x 64 bytes
-        const int t = c * CH + 32 * J + row;
-        if (t < p.T && v0 + 8 * ch < p.D)
-          *(bf16x8*)(p.out + row_off(p, b, h, t) + v0 + 8 * ch) = *(const bf16x8*)(so + row * NS + 8 * ch);
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
-    // coalesced stores, off the step's dependency chain: the state this step started
-    // from and its v
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int e = tid + 256 * i;
-      // [d_k][d_v]: 128 rows of 64 bytes
-      const int row = e >> 2, ch = e & 3;
-      st16(rH, (unsigned)(((c * DK + row) * DK + v0 + 8 * ch) * 2), sN[it & 1] + row * NS + 8 * ch);
-    }
-    copy_v(it, c);
-    fetch_rest(P, chunk_of(min(it + 2, p.nch - 1)));
   };
-  // both bodies of the unrolled pair run unconditionally inside the loop (an odd last
-  // chunk is peeled), for the same reason as the unconditional prefetches
+
+  dma(chunk_of(0), B0);
+  dma(chunk_of(min(1, p.nch - 1)), B1);
+  // Step it reads buffer it % 3 after issuing chunk it + 2's copies into buffer (it + 2) % 3
+  // (unconditional: past the last chunk they reload it).  First it waits until its own
+  // copies have landed: issued after them are the stores of steps it - 2 and it - 1 (NST
+  // each) and chunk it + 1's copies (NDMA), more than the counter's 63 in reverse, where
+  // vmcnt(63) is the closest bound; and until every LDS access of step it - 1 has completed
+  // (the DMA overwrites what step it - 1 read).
+  constexpr int NST = 12;               // global stores per step (8 state rows + 4 v rows per lane)
+  constexpr int NDMA = REV ? 45 : 37;   // DMA loads per chunk
+  constexpr int WAITV = 2 * NST + NDMA < 63 ? 2 * NST + NDMA : 63;
+  auto step = [&](int it, const Buf& cur, const Buf& nxt2) {
+    __builtin_amdgcn_s_waitcnt(0x0070 | (WAITV & 15) | ((WAITV >> 4) << 14));  // vmcnt(WAITV) lgkmcnt(0)
+    dma(chunk_of(min(it + 2, p.nch - 1)), nxt2);
+    body(it, cur);
+  };
   int it = 0;
-  for (; it + 1 < p.nch; it += 2) {
-    body(it, pre0);
-    body(it + 1, pre1);
+  for (; it + 2 < p.nch; it += 3) {
+    step(it, B0, B2);
+    step(it + 1, B1, B0);
+    step(it + 2, B2, B1);
   }
-  if (it < p.nch) body(it, pre0);
+  if (it < p.nch) step(it, B0, B2);
+  if (it + 1 < p.nch) step(it + 1, B1, B0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1141,7 +1201,7 @@ __global__ void dr_ck_debug_kfrag_kernel(const float* x, bf16* out) {
 }
 
 struct Layout {
-  size_t lg, W, Wt, Ut, Kdt, Tt, P, hN, vN, dvl, dhl, dmN, dvT, total;
+  size_t lg, W, Wt, Ut, Kdt, Kd, Tt, P, hN, vN, dvl, dhl, dmN, dvT, total;
 };
 
 inline size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1167,6 +1227,7 @@ Layout layout(int batch, int seq, int heads, LayoutKind kind) {
   take(L.Wt, tile_ck, ctx);
   take(L.Ut, tile_ck, ctx);
   take(L.Kdt, tile_ck, ctx);
+  take(L.Kd, tile_ck, ctx);
   take(L.Tt, nci * CH * CH * sizeof(bf16), ctx);
   take(L.P, nci * CH * CH * sizeof(bf16), false);
   take(L.hN, tile_kk, ctx);
@@ -1189,6 +1250,7 @@ CkArgs make_args(const Layout& Lc, void* ctx_ws, const Layout& Lr, void* rev_ws,
   a.Wt = (bf16*)(wc + Lc.Wt);
   a.Ut = (bf16*)(wc + Lc.Ut);
   a.Kdt = (bf16*)(wc + Lc.Kdt);
+  a.Kd = (bf16*)(wc + Lc.Kd);
   a.Tt = (bf16*)(wc + Lc.Tt);
   a.P = Lc.P ? (bf16*)(wc + Lc.P) : nullptr;
   a.hN = (bf16*)(wc + Lc.hN);
@@ -1244,7 +1306,7 @@ int dr_chunk_run(void* stream, const void* q, const void* k, const void* v, cons
   dr_ck_prep_kernel<true, false><<<dim3(a.nch, bh), 256, 0, s>>>(a);
   int rc = check_launch("delta rule chunk prep");
   if (rc) return rc;
-  dr_ck_scan_kernel<1><<<bh * (DK / VS), 256, 0, s>>>(a);
+  dr_ck_scanw_kernel<false><<<bh * (DK / VS), 64, 0, s>>>(a);
   rc = check_launch("delta rule chunk scan");
   if (rc) return rc;
   dr_ck_out_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
@@ -1259,7 +1321,7 @@ int reverse_pass(hipStream_t s, CkArgs& a, unsigned bh, const void* grad_out, vo
   dr_ck_dlocal_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
   int rc = check_launch("delta rule chunk dlocal");
   if (rc) return rc;
-  dr_ck_scan_kernel<2><<<bh * (DK / VS), 256, 0, s>>>(a);
+  dr_ck_scanw_kernel<true><<<bh * (DK / VS), 64, 0, s>>>(a);
   rc = check_launch("delta rule chunk reverse scan");
   if (rc) return rc;
   dr_ck_grad_kernel<<<dim3(a.nch, bh), 256, 0, s>>>(a);
@@ -1279,7 +1341,7 @@ int dr_chunk_backward_run(void* stream, const void* q, const void* k, const void
   dr_ck_prep_kernel<true, false><<<dim3(a.nch, bh), 256, 0, s>>>(a);
   int rc = check_launch("delta rule chunk prep");
   if (rc) return rc;
-  dr_ck_scan_kernel<1><<<bh * (DK / VS), 256, 0, s>>>(a);
+  dr_ck_scanw_kernel<false><<<bh * (DK / VS), 64, 0, s>>>(a);
   rc = check_launch("delta rule chunk scan");
   if (rc) return rc;
   return reverse_pass(s, a, bh, grad_out, dq, dk, dv, dbeta, dalpha);
