@@ -191,6 +191,39 @@ def bench_mingru(torch, steps, warmup, B, T, H, dtype):
                 roofline=roofline("hbm", fb + bb, fwd_ms + bwd_ms, None, prof))
 
 
+def bench_hbm_ceiling(torch, steps, warmup, nbytes=8 * 2048 * 1536 * 2):
+    """The HBM rate a plain streaming kernel of this library reaches (edf_probe_stream, a
+    layout-free 16-byte-per-lane stream declared in tests/edifice_hip_probes.h): out = in0 + in1
+    over `nbytes` per stream (2 reads + 1 write, the MinGRU forward's traffic at the bandwidth
+    row's bf16 size) and out = in0 (1 read + 1 write), caches evicted before each run, over a
+    sweep of grid sizes; the best of the sweep is the ceiling the scan rows are read against."""
+    from edifice_amd import _native as nat
+
+    fn = nat.lib().edf_probe_stream
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_long, ctypes.c_int, ctypes.c_int]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    a = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    b, o = torch.ones_like(a), torch.empty_like(a)
+    runs, wu, fl = max(steps, MIN_RUNS), max(warmup, MIN_WARMUP), Flush(torch)
+    out = {}
+    for nin in (2, 1):
+        best = None
+        for blocks in (512, 1024, 2048, 4096, 8192):
+            def run():
+                rc = fn(stream, a.data_ptr(), b.data_ptr(), o.data_ptr(), nbytes, nin, blocks)
+                if rc != 0:
+                    raise RuntimeError(nat.lib().edf_last_error().decode())
+            ms = median_ms(torch, run, runs, wu, fl)
+            gbs = (nin + 1) * nbytes / ms / 1e6
+            if best is None or gbs > best[1]:
+                best = (blocks, gbs, ms)
+        key = "read2_write1" if nin == 2 else "read1_write1"
+        out[key] = dict(bytes=(nin + 1) * nbytes, us=round(best[2] * 1e3, 2), gbs=round(best[1], 1),
+                        frac_of_peak=round(best[1] / HBM_PEAK_GBS, 4), blocks=best[0])
+    return out
+
+
 def bench_linear_scan(torch, steps, warmup, B, T, H, dtype):
     """Generic linear scan h_t = a_t h_{t-1} + b_t (fwd reads a, b, writes h; bwd reads a,
     h, dy, writes da, db)."""
@@ -806,6 +839,7 @@ def main():
     want = (lambda k: not only or k in only)  # noqa: E731
     configs = {}
     if want("mingru"):
+        configs["hbm_ceiling_stream_probe"] = bench_hbm_ceiling(torch, args.steps, args.warmup)
         configs["c1_mingru_f32_4x60x256"] = bench_mingru(torch, args.steps, args.warmup, 4, 60, 256, torch.float32)
         for dt in (torch.bfloat16, torch.float32):
             key = f"mingru_bw_{str(dt).replace('torch.', '')}_8x2048x1536"

@@ -57,13 +57,13 @@ struct Step {
       a = g1;
       b = c;
     } else if (OP == OP_MINGRU) {
-      const float z = LOGITS ? sigmoidf(g1) : g1;
+      const float z = LOGITS ? sigmoid_rcp(g1) : g1;
       a = 1.0f - z;
       b = z * c;
     } else {
-      const float f = LOGITS ? sigmoidf(g1) : g1;
-      const float i = LOGITS ? sigmoidf(g2) : g2;
-      const float r = 1.0f / (f + (i + MINLSTM_EPS));
+      const float f = LOGITS ? sigmoid_rcp(g1) : g1;
+      const float i = LOGITS ? sigmoid_rcp(g2) : g2;
+      const float r = fast_rcp(f + (i + MINLSTM_EPS));
       a = f * r;
       b = (i * r) * c;
     }
@@ -78,7 +78,7 @@ struct Step {
 // the stores are dropped by the hardware, and the loop body has no branch around a memory
 // access (which would make the compiler drain the whole ring at the loop head).  The
 // macro-step count is padded to a multiple of P with such empty steps.
-template <typename T, int OP, bool LOGITS, int L, int W, int P>
+template <typename T, int OP, bool LOGITS, int L, int W, int P, bool PAD>
 __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
                                                              const T* __restrict__ cand, const T* __restrict__ h0,
                                                              T* __restrict__ out, int seq, int hid) {
@@ -97,9 +97,10 @@ __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict
   const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
   const rsrc_t RC = make_rsrc(cand + slab, bytes);
   const rsrc_t RO = make_rsrc(out + slab, bytes);
-  auto off = [&](int t) -> unsigned {
-    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
-  };
+  // a channel's base offset plus t rows: rows at and past seq lie beyond the resource (the
+  // hardware returns 0 / drops the store), channels past hid start out of range
+  const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
+  auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
 
   RB r1[P][L], r2[P][L], rc[P][L];
   auto fetch = [&](int slot, int ms) {
@@ -128,7 +129,7 @@ __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict
       for (int j = 0; j < L; ++j) {
         Step<OP, LOGITS> s;
         s.make(bits_f32(r1[u][j]), OP == OP_MINLSTM ? bits_f32(r2[u][j]) : 0.0f, bits_f32(rc[u][j]));
-        const bool ok = valid && t0 + j < seq;  // padding steps are the identity map
+        const bool ok = !PAD || (valid && t0 + j < seq);  // padding steps are the identity map
         a[j] = ok ? s.a : 1.0f;
         bb[j] = ok ? s.b : 0.0f;
       }
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(64 * W) void linscan_fwd_kernel(const T* __restrict
 // Backward: reverse scan u_t = a_t (g_t + u_{t+1}), dh_t = g_t + u_{t+1}, dh0 = u_0.
 // Same register ring and buffer addressing as the forward, walking macro-steps from the
 // end of the (padded) sequence.
-template <typename T, int OP, bool LOGITS, int L, int W, int P>
+template <typename T, int OP, bool LOGITS, int L, int W, int P, bool PAD>
 __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
                                                              const T* __restrict__ cand, const T* __restrict__ h0,
                                                              const T* __restrict__ fwd, const T* __restrict__ dy,
@@ -191,13 +192,13 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
   const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
   const rsrc_t W2 = make_rsrc((OP == OP_MINLSTM ? d2 : d1) + slab, bytes);
   const rsrc_t WC = make_rsrc(dcand + slab, bytes);
-  auto off = [&](int t) -> unsigned {
-    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
-  };
+  // a channel's base offset plus t rows: rows at and past seq lie beyond the resource (the
+  // hardware returns 0 / drops the store), channels past hid start out of range
+  const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
+  auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
   // h_{t-1}: the forward output one row up; t = 0 reads out of range (0) and takes h0
-  auto offp = [&](int t) -> unsigned {
-    return (valid && t < seq && t > 0) ? ((unsigned)(t - 1) * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
-  };
+  // h_{t-1}: t = 0 wraps below zero, out of range (0), and takes h0
+  auto offp = [&](int t) -> unsigned { return cb + (unsigned)(t - 1) * rowb; };
   const float h0v = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c) : 0.0f;
 
   const int steps = (seq + W * L - 1) / (W * L);
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
 #pragma unroll
       for (int j = 0; j < L; ++j) {
         const int t = t0 + j;
-        const bool ok = valid && t < seq;
+        const bool ok = !PAD || (valid && t < seq);
         const float x1 = bits_f32(r1[sl][j]);
         const float x2 = OP == OP_MINLSTM ? bits_f32(r2[sl][j]) : 0.0f;
         const float cv = OP == OP_LINEAR ? 0.0f : bits_f32(rc[sl][j]);
@@ -249,15 +250,15 @@ __global__ __launch_bounds__(64 * W) void linscan_bwd_kernel(const T* __restrict
           k2[j] = 0.0f;
           kc[j] = 1.0f;
         } else if (OP == OP_MINGRU) {
-          const float z = LOGITS ? sigmoidf(x1) : x1;
+          const float z = LOGITS ? sigmoid_rcp(x1) : x1;
           a[j] = ok ? 1.0f - z : 1.0f;  // padding steps are the identity map
           k1[j] = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
           k2[j] = 0.0f;
           kc[j] = z;
         } else {
-          const float f = LOGITS ? sigmoidf(x1) : x1;
-          const float i = LOGITS ? sigmoidf(x2) : x2;
-          const float r = 1.0f / (f + (i + MINLSTM_EPS));
+          const float f = LOGITS ? sigmoid_rcp(x1) : x1;
+          const float i = LOGITS ? sigmoid_rcp(x2) : x2;
+          const float r = fast_rcp(f + (i + MINLSTM_EPS));
           const float r2 = r * r;
           a[j] = ok ? f * r : 1.0f;
           float c1 = (hp * (i + MINLSTM_EPS) - cv * i) * r2;
@@ -333,7 +334,7 @@ EDF_DEVICE float from_lower(float y, float x) {
   return __builtin_bit_cast(float, s[0]);
 }
 
-template <typename T, int OP, bool LOGITS, int L, int W, int P>
+template <typename T, int OP, bool LOGITS, int L, int W, int P, bool PAD>
 __global__ __launch_bounds__(64 * W) void linscan2_fwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
                                                               const T* __restrict__ cand, const T* __restrict__ h0,
                                                               T* __restrict__ out, int seq, int hid) {
@@ -354,9 +355,10 @@ __global__ __launch_bounds__(64 * W) void linscan2_fwd_kernel(const T* __restric
   const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
   const rsrc_t RC = make_rsrc(cand + slab, bytes);
   const rsrc_t RO = make_rsrc(out + slab, bytes);
-  auto off = [&](int t) -> unsigned {
-    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
-  };
+  // a channel's base offset plus t rows: rows at and past seq lie beyond the resource (the
+  // hardware returns 0 / drops the store), channels past hid start out of range
+  const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
+  auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
 
   PB r1[P][L], r2[P][L], rc[P][L];
   auto fetch = [&](int slot, int ms) {
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(64 * W) void linscan2_fwd_kernel(const T* __restric
       float a[L][2], bb[L][2];
 #pragma unroll
       for (int j = 0; j < L; ++j) {
-        const bool ok = valid && t0 + j < seq;  // padding steps are the identity map
+        const bool ok = !PAD || (valid && t0 + j < seq);  // padding steps are the identity map
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           Step<OP, LOGITS> st;
@@ -450,7 +452,7 @@ __global__ __launch_bounds__(64 * W) void linscan2_fwd_kernel(const T* __restric
 
 // Backward with the same layout, walking macro-steps from the end of the padded sequence;
 // virtual wave 0 (the lower half of wave 0) owns the latest segment of each macro-step.
-template <typename T, int OP, bool LOGITS, int L, int W, int P>
+template <typename T, int OP, bool LOGITS, int L, int W, int P, bool PAD>
 __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
                                                               const T* __restrict__ cand, const T* __restrict__ h0,
                                                               const T* __restrict__ fwd, const T* __restrict__ dy,
@@ -478,12 +480,12 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
   const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
   const rsrc_t W2 = make_rsrc((OP == OP_MINLSTM ? d2 : d1) + slab, bytes);
   const rsrc_t WC = make_rsrc(dcand + slab, bytes);
-  auto off = [&](int t) -> unsigned {
-    return (valid && t < seq) ? ((unsigned)t * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
-  };
-  auto offp = [&](int t) -> unsigned {  // h_{t-1}; t = 0 reads out of range (0) and takes h0
-    return (valid && t < seq && t > 0) ? ((unsigned)(t - 1) * (unsigned)hid + (unsigned)c) * ES : OOB_OFF;
-  };
+  // a channel's base offset plus t rows: rows at and past seq lie beyond the resource (the
+  // hardware returns 0 / drops the store), channels past hid start out of range
+  const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
+  auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
+  // h_{t-1}: t = 0 wraps below zero, out of range (0), and takes h0
+  auto offp = [&](int t) -> unsigned { return cb + (unsigned)(t - 1) * rowb; };
   float h0v[2];
 #pragma unroll
   for (int k = 0; k < 2; ++k) h0v[k] = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c + k) : 0.0f;
@@ -519,7 +521,7 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
 #pragma unroll
       for (int j = 0; j < L; ++j) {
         const int t = t0 + j;
-        const bool ok = valid && t < seq;
+        const bool ok = !PAD || (valid && t < seq);
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           const float x1 = k ? PR::hi(r1[sl][j]) : PR::lo(r1[sl][j]);
@@ -533,15 +535,15 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
             k2[j][k] = 0.0f;
             kc[j][k] = 1.0f;
           } else if (OP == OP_MINGRU) {
-            const float z = LOGITS ? sigmoidf(x1) : x1;
+            const float z = LOGITS ? sigmoid_rcp(x1) : x1;
             a[j][k] = ok ? 1.0f - z : 1.0f;
             k1[j][k] = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
             k2[j][k] = 0.0f;
             kc[j][k] = z;
           } else {
-            const float f = LOGITS ? sigmoidf(x1) : x1;
-            const float i = LOGITS ? sigmoidf(x2) : x2;
-            const float r = 1.0f / (f + (i + MINLSTM_EPS));
+            const float f = LOGITS ? sigmoid_rcp(x1) : x1;
+            const float i = LOGITS ? sigmoid_rcp(x2) : x2;
+            const float r = fast_rcp(f + (i + MINLSTM_EPS));
             const float r2v = r * r;
             a[j][k] = ok ? f * r : 1.0f;
             float c1 = (hp * (i + MINLSTM_EPS) - cv * i) * r2v;
@@ -624,6 +626,15 @@ inline const char* op_name(int op, bool backward = false) {
   return names[op][backward ? 1 : 0];
 }
 
+// PAD: the launch has steps past the sequence inside a macro-step, or channels past hid;
+// those are masked into identity steps.  Without them the masks are compiled out (whole
+// padding macro-steps past the sequence only feed values that are never stored: zeros
+// entering the reverse scan, states past the end in the forward).
+template <int L, int W, bool PAIRS>
+inline bool needs_pad(int seq, int hid) {
+  return seq % ((PAIRS ? 2 : 1) * W * L) != 0 || hid % 64 != 0;
+}
+
 template <typename T, int OP, bool LOGITS>
 int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, const void* h0, void* out, int bsz,
                int seq, int hid) {
@@ -633,20 +644,23 @@ int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
   const T* c = (const T*)cand;
   const T* i = (const T*)h0;
   T* o = (T*)out;
+#define EDF_LIN_LAUNCH(KERNEL, L, W, P, PAIRS)                                                      \
+  do {                                                                                            \
+    if (needs_pad<L, W, PAIRS>(seq, hid))                                                         \
+      KERNEL<T, OP, LOGITS, L, W, P, true><<<grid, 64 * W, 0, s>>>(a, b, c, i, o, seq, hid);      \
+    else                                                                                          \
+      KERNEL<T, OP, LOGITS, L, W, P, false><<<grid, 64 * W, 0, s>>>(a, b, c, i, o, seq, hid);     \
+  } while (0)
   if constexpr (std::is_same<T, bf16>::value) {
     if (hid % 2 == 0) {  // two channels per lane
-      if (seq >= 512)
-        linscan2_fwd_kernel<T, OP, LOGITS, LIN2_LF, LIN2_W, LIN_PF><<<grid, 64 * LIN2_W, 0, s>>>(a, b, c, i, o, seq,
-                                                                                                hid);
-      else
-        linscan2_fwd_kernel<T, OP, LOGITS, LIN2_LF, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, o, seq, hid);
+      if (seq >= 512) EDF_LIN_LAUNCH(linscan2_fwd_kernel, LIN2_LF, LIN2_W, LIN_PF, true);
+      else EDF_LIN_LAUNCH(linscan2_fwd_kernel, LIN2_LF, 4, 2, true);
       return check_launch(op_name(OP));
     }
   }
-  if (seq >= 512)
-    linscan_fwd_kernel<T, OP, LOGITS, LIN_LF, 16, LIN_PF><<<grid, 64 * 16, 0, s>>>(a, b, c, i, o, seq, hid);
-  else
-    linscan_fwd_kernel<T, OP, LOGITS, LIN_LF, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, o, seq, hid);
+  if (seq >= 512) EDF_LIN_LAUNCH(linscan_fwd_kernel, LIN_LF, 16, LIN_PF, false);
+  else EDF_LIN_LAUNCH(linscan_fwd_kernel, LIN_LF, 4, 2, false);
+#undef EDF_LIN_LAUNCH
   return check_launch(op_name(OP));
 }
 
@@ -664,22 +678,23 @@ int launch_bwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
   T* o2 = (T*)d2;
   T* oc = (T*)dcand;
   T* oh = (T*)dh0;
+#define EDF_LIN_LAUNCH(KERNEL, L, W, P, PAIRS)                                                                 \
+  do {                                                                                                       \
+    if (needs_pad<L, W, PAIRS>(seq, hid))                                                                    \
+      KERNEL<T, OP, LOGITS, L, W, P, true><<<grid, 64 * W, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq, hid);  \
+    else                                                                                                     \
+      KERNEL<T, OP, LOGITS, L, W, P, false><<<grid, 64 * W, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq, hid); \
+  } while (0)
   if constexpr (std::is_same<T, bf16>::value) {
     if (hid % 2 == 0) {  // two channels per lane
-      if (seq >= 512)
-        linscan2_bwd_kernel<T, OP, LOGITS, LIN2_LB, LIN2_W, LIN_PB><<<grid, 64 * LIN2_W, 0, s>>>(a, b, c, i, f, y, o1,
-                                                                                                  o2, oc, oh, seq, hid);
-      else
-        linscan2_bwd_kernel<T, OP, LOGITS, LIN2_LB, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq,
-                                                                                   hid);
+      if (seq >= 512) EDF_LIN_LAUNCH(linscan2_bwd_kernel, LIN2_LB, LIN2_W, LIN_PB, true);
+      else EDF_LIN_LAUNCH(linscan2_bwd_kernel, LIN2_LB, 4, 2, true);
       return check_launch(op_name(OP, true));
     }
   }
-  if (seq >= 512)
-    linscan_bwd_kernel<T, OP, LOGITS, LIN_LB, 16, LIN_PB><<<grid, 64 * 16, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh,
-                                                                                    seq, hid);
-  else
-    linscan_bwd_kernel<T, OP, LOGITS, LIN_LB, 4, 2><<<grid, 64 * 4, 0, s>>>(a, b, c, i, f, y, o1, o2, oc, oh, seq, hid);
+  if (seq >= 512) EDF_LIN_LAUNCH(linscan_bwd_kernel, LIN_LB, 16, LIN_PB, false);
+  else EDF_LIN_LAUNCH(linscan_bwd_kernel, LIN_LB, 4, 2, false);
+#undef EDF_LIN_LAUNCH
   return check_launch(op_name(OP, true));
 }
 
@@ -687,8 +702,8 @@ template <int OP, bool LOGITS>
 int fwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand, const void* h0, void* out, int bsz,
                  int seq, int hid, int dtype) {
   EDF_REQUIRE(bsz > 0 && seq > 0 && hid > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
-  EDF_REQUIRE((long)seq * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
-              "seq_len * hidden too large (one batch row must stay below 2 GiB)");
+  EDF_REQUIRE((long)(seq + 512) * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row plus padding must stay below 2 GiB)");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(g1 && cand && out && (OP != OP_MINLSTM || g2), EDF_ERR_INVALID_ARG, "null tensor pointer");
   if (dtype == EDF_BF16) return launch_fwd<bf16, OP, LOGITS>(as_stream(stream), g1, g2, cand, h0, out, bsz, seq, hid);
@@ -699,8 +714,8 @@ template <int OP, bool LOGITS>
 int bwd_dispatch(void* stream, const void* g1, const void* g2, const void* cand, const void* h0, const void* fwd,
                  const void* dy, void* d1, void* d2, void* dcand, void* dh0, int bsz, int seq, int hid, int dtype) {
   EDF_REQUIRE(bsz > 0 && seq > 0 && hid > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
-  EDF_REQUIRE((long)seq * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
-              "seq_len * hidden too large (one batch row must stay below 2 GiB)");
+  EDF_REQUIRE((long)(seq + 512) * hid * (dtype == EDF_BF16 ? 2 : 4) < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row plus padding must stay below 2 GiB)");
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(g1 && (OP == OP_LINEAR || cand) && fwd && dy && d1 && dcand && (OP != OP_MINLSTM || (g2 && d2)),
               EDF_ERR_INVALID_ARG, "null tensor pointer");
@@ -914,8 +929,8 @@ int block_dispatch(void* stream, const void* input, const void* weights, const v
   EDF_REQUIRE(valid_dtype(dtype), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(hidden <= MGB_HMAX, EDF_ERR_UNSUPPORTED, "hidden %d unsupported (the block scans take H <= %d)",
               hidden, MGB_HMAX);
-  EDF_REQUIRE((long)seq_len * hidden * 4 < (1L << 31), EDF_ERR_UNSUPPORTED,
-              "seq_len * hidden too large (one batch row of f32 activations must stay below 2 GiB)");
+  EDF_REQUIRE((long)(seq_len + 512) * hidden * 4 < (1L << 31), EDF_ERR_UNSUPPORTED,
+              "seq_len * hidden too large (one batch row of f32 activations plus padding must stay below 2 GiB)");
   EDF_REQUIRE(input && weights && out, EDF_ERR_INVALID_ARG, "null tensor pointer");
   const MgbWs L = mgb_layout(workspace, (long)batch * seq_len * hidden, batch, hidden, blk_projections(KIND));
   EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",

@@ -30,6 +30,12 @@ int edf_debug_acc_kfrag_bf16(void* stream, const float* x, void* out);
  * tests to pin that layout. */
 int edf_debug_lds_read_tr16(void* stream, const void* x, void* out);
 
+/* Streaming probe: out = in0 + in1 (nin = 2, 32-bit integer lanes) or out = in0 (nin = 1)
+ * over n_bytes (a multiple of 16) with 16-byte accesses, `blocks` workgroups of 256 threads
+ * striding over the buffers: the HBM rate a plain streaming kernel reaches, against which
+ * bench.py reads the bandwidth-bound scans. */
+int edf_probe_stream(void* stream, const void* in0, const void* in1, void* out, long n_bytes, int nin, int blocks);
+
 #ifdef __cplusplus
 }
 #endif
