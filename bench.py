@@ -39,6 +39,16 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# VALU issue slots per second: 256 CUs x 4 SIMDs x 16 lanes at the 2.4 GHz shader clock
+# measured under load (a wave64 instruction occupies a SIMD for 4 cycles; v_exp_f32 for 4 of
+# those slots per lane, one quarter rate)
+VALU_PEAK_TSLOTS = 256 * 4 * 16 * 2.4e9 / 1e12
+# Selective scan, VALU issue slots per (b, t, d, n) element that the recurrence itself needs:
+#   forward  dt * A, exp (4 slots), dt_b x B, state update, C h into y           -> 8
+#   backward the forward's first four again (7), then dh += dy C, dy h, dh x dt_b,
+#            dh B, dh *= a, dh h_prev, dA (7) and the sums over states (dx, ddt) and
+#            over channels (dB, dC), one slot each (4)                            -> 18
+SS_VALU_SLOTS = (8, 18)
 
 
 def ss_bytes(B, T, D, N):
@@ -900,6 +910,13 @@ def main():
                    "d_state": 16},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        # the bound this kernel actually meets: its VALU issue slots per element (SS_VALU_SLOTS)
+        # over 8 x 2048 x 1536 x 16 elements, per second, against the VALU peak
+        "valu_roofline": {"kernel": dominant, "slots_per_element": SS_VALU_SLOTS[1 if bwd_dom else 0],
+                          "achieved": round(SS_VALU_SLOTS[1 if bwd_dom else 0] * 8 * 2048 * 1536 * 16 / dom_ms / 1e9, 2),
+                          "peak": round(VALU_PEAK_TSLOTS, 2), "unit": "T slots/s",
+                          "frac": round(SS_VALU_SLOTS[1 if bwd_dom else 0] * 8 * 2048 * 1536 * 16 / dom_ms / 1e9
+                                        / VALU_PEAK_TSLOTS, 4)},
         "configs": configs,
     }
     if not args.no_cpu:
