@@ -40,15 +40,15 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 # VALU issue slots per second: 256 CUs x 4 SIMDs x 16 lanes at the 2.4 GHz shader clock
-# measured under load (a wave64 instruction occupies a SIMD for 4 cycles; v_exp_f32 for 4 of
-# those slots per lane, one quarter rate)
+# measured under load (a wave64 FMA occupies a SIMD for 4 cycles = 64 lane slots)
 VALU_PEAK_TSLOTS = 256 * 4 * 16 * 2.4e9 / 1e12
-# Selective scan, VALU issue slots per (b, t, d, n) element that the recurrence itself needs:
-#   forward  dt * A, exp (4 slots), dt_b x B, state update, C h into y           -> 8
-#   backward the forward's first four again (7), then dh += dy C, dy h, dh x dt_b,
-#            dh B, dh *= a, dh h_prev, dA (7) and the sums over states (dx, ddt) and
-#            over channels (dB, dC), one slot each (4)                            -> 18
-SS_VALU_SLOTS = (8, 18)
+# Selective scan, VALU issue slots per (b, t, d, n) element that the recurrence itself needs,
+# v_exp_f32 counted as 2.5 (10 cycles per wave instruction, measured, against 4 for an FMA):
+#   forward  dt * A, exp, B * dt_b x, state update, C * h and its sum over the states   -> 7.5
+#   backward the forward's first four again (5.5); dh += dy C, dy h, dh dt_b x, dh B,
+#            dh *= a, dh h_prev, dA += ... (7); the sums over states (dx, ddt) and over
+#            channels (dB, dC), one add each (4)                                     -> 16.5
+SS_VALU_SLOTS = (7.5, 16.5)
 
 
 def ss_bytes(B, T, D, N):

@@ -17,7 +17,7 @@
 // W_x and R columns (laid out unit-major once per call, so each slice is one contiguous
 // block) into LDS, form and LayerNorm the x^l_t rows, take the input and recurrent dot
 // products (each split over a lane quad) and apply the cell update for their units.
-// When the device can hold every workgroup at once, the recurrence is one cooperative
+// When the device can hold every workgroup at once, the recurrence is one persistent
 // launch: each workgroup stages its weight slices once, keeps its LSTM cell state in a
 // register and walks all diagonals, a bounded grid barrier between them (per diagonal
 // launch it re-staged 16 KB of weights and paid a kernel boundary).  Otherwise one launch
@@ -260,8 +260,8 @@ __global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
   if (G == RNB_LSTM && own) p.cs[si] = c;
 }
 
-// Grid-wide barrier of the persistent kernel (a cooperative launch: every workgroup is
-// resident).  The h rows that cross it are stored and loaded at device scope (coherent
+// Grid-wide barrier of the persistent kernel (launched only when the occupancy limit holds
+// the whole grid, so every workgroup is resident).  The h rows that cross it are stored and loaded at device scope (coherent
 // across the XCDs' L2s), so every wave waiting for its own stores before its workgroup
 // arrives orders them; no cache write-back or invalidation is needed (with them each
 // barrier cost ~85 us).  Arrivals go through a two-level tree of monotonic device-scope
@@ -269,8 +269,8 @@ __global__ __launch_bounds__(256) void rnb_diag_kernel(const RnbArgs p, int j) {
 // workgroups of the config-size call serialised ~20 us of atomics per barrier): workgroup i
 // arrives at sub-counter i % 16; the last arrival of a group arrives at the root; the last
 // root arrival publishes the barrier's generation to the 16 groups' release words, which
-// the groups poll.  The wait is bounded: it cannot time out under a cooperative launch,
-// but if it ever did, the workgroup sets the abort word and every later wait of every
+// the groups poll.  The wait is bounded: if it times out (some workgroup not resident,
+// e.g. held back by another stream's kernels), the workgroup sets the abort word and every later wait of every
 // workgroup ends at once, so the kernel still finishes.
 EDF_DEVICE void rnb_grid_sync(unsigned* bar, unsigned gen, unsigned wg, unsigned nwg) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -398,28 +398,28 @@ int rnb_run(hipStream_t s, const void* input, const void* weights, const void* h
       (const T*)h0, G == RNB_LSTM ? (const T*)c0 : nullptr, ws.hs0, ws.cs, ws.bar, abort0, B, L, H);
   if (int rc = check_launch("rnn block initial state")) return rc;
   const dim3 grid(a.ngrp, (B + RNB_BS - 1) / RNB_BS, L);
-  // one cooperative launch for the whole recurrence when every workgroup fits on the
-  // device at once (the runtime refuses it otherwise); else one launch per diagonal
-  // (EDF_RNN_BLOCK_PER_STEP=1 forces the per-diagonal path, so that tests cover both)
-  int coop = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess)
-    coop = 0;
+  // One persistent launch for the whole recurrence when the occupancy query says every
+  // workgroup fits on the device at once; else one launch per diagonal
+  // (EDF_RNN_BLOCK_PER_STEP=1 forces the per-diagonal path, so that tests cover both).  The
+  // persistent launch is an ordinary one: `rocprofv3 --kernel-trace` runs of processes that
+  // had made a cooperative launch (hipLaunchCooperativeKernel, which the runtime serves
+  // through a separate cooperative dispatch path) ended in a segmentation fault at exit,
+  // after the tool's finalisation, and runs without one exited cleanly.  Co-residency
+  // follows from the grid fitting the occupancy limit when nothing else runs on the device;
+  // if another stream's kernels keep some workgroups waiting, the grid barrier's bounded
+  // wait gives up, the output is NaN and the status query reports the time-out.
+  int dev = 0, ncu = 0, per_cu = 0;
+  bool fits = hipGetDevice(&dev) == hipSuccess &&
+              hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+              hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)rnb_persist_kernel<T, G>, 256, 0) ==
+                  hipSuccess &&
+              (long)grid.x * grid.y * grid.z <= (long)per_cu * ncu;
+  (void)hipGetLastError();  // a failed query only selects the per-diagonal path
   const char* force = getenv("EDF_RNN_BLOCK_PER_STEP");
-  if (force != nullptr && force[0] == '1') coop = 0;
-  bool done = false;
-  if (coop) {
-    unsigned* bar = ws.bar;
-    void* args[] = {(void*)&a, (void*)&bar};
-    const hipError_t e = hipLaunchCooperativeKernel((const void*)rnb_persist_kernel<T, G>, grid, dim3(256), args, 0, s);
-    if (e == hipSuccess) {
-      done = true;
-    } else {
-      (void)hipGetLastError();  // not co-schedulable: clear and take the per-diagonal path
-    }
-  }
-  if (!done)
+  if (force != nullptr && force[0] == '1') fits = false;
+  if (fits)
+    rnb_persist_kernel<T, G><<<grid, 256, 0, s>>>(a, ws.bar);
+  else
     for (int j = 0; j < Tn + L - 1; ++j) rnb_diag_kernel<T, G><<<grid, 256, 0, s>>>(a, j);
   if (int rc = check_launch("rnn block step")) return rc;
   rnb_out_kernel<T><<<(unsigned)(((long)B * Tn * H + 255) / 256), 256, 0, s>>>(a, ws.bar, (T*)out);

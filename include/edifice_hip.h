@@ -168,7 +168,7 @@ int edf_fused_linear_block_scan(void* stream, const void* input, const void* wei
  * native/cuda/fused_lstm_block_scan.cu (fallback fused_scan.ex:4911-4990).  Per-layer
  * packing W_x [H, 4H] (gates i, f, g, o), b_x [4H], R [H, 4H], gamma [H], beta [H]; h0, c0
  * [B, L, H] or NULL (zeros); H <= 256; workspace edf_lstm_block_workspace_bytes() bytes.
- * The recurrence (LSTM and GRU) runs as one cooperative launch when the device can hold the
+ * The recurrence (LSTM and GRU) runs as one persistent launch when the device can hold the
  * whole grid at once (a grid barrier in the workspace between step diagonals), else as one
  * launch per diagonal; EDF_RNN_BLOCK_PER_STEP=1 in the environment forces the latter. */
 int edf_fused_lstm_block_scan(void* stream, const void* input, const void* weights, const void* h0, const void* c0,

@@ -298,7 +298,7 @@ def test_rnn_block(case, rng):
 
 @pytest.mark.parametrize("case", [RNN_BLOCK_CASES[3], RNN_BLOCK_CASES[6], RNN_BLOCK_CASES[8]])
 def test_rnn_block_paths_agree(case, rng, monkeypatch):
-    """The whole recurrence in one cooperative launch (grid barrier between diagonals) and
+    """The whole recurrence in one persistent launch (grid barrier between diagonals) and
     one launch per diagonal run the same arithmetic: bit-identical outputs, both against
     the oracle."""
     from edifice_amd import fused_scan as fs
