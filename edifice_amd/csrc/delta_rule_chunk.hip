@@ -437,7 +437,6 @@ __global__ __launch_bounds__(64) void dr_ck_scanw_kernel(const CkArgs p) {
   const int logical = remap_xcd(blockIdx.x, gridDim.x);  // the slices of one head share an XCD
   const long bh = logical / NSL;
   const int v0 = (logical % NSL) * 32;
-  const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   auto chunk_of = [&](int it) { return REV ? p.nch - 1 - it : it; };
 
   // Buffer resources over this head's regions; a DMA load's lane offset depends only on the
@@ -865,13 +864,19 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sK[CH * DK];         // K [s][d_k]
   __shared__ __attribute__((aligned(16))) bf16 sdR[CH * DK];        // dR [s][d_v]
   __shared__ __attribute__((aligned(16))) bf16 sdSF[2 * CH * TS];   // dS [t][s], dF = dG + dG^T [t][s]
-  __shared__ float lg[CH], bt[CH], dlg[CH], dbt[CH];
+  __shared__ float lg[CH], bt[CH];
+  // d log-gamma and dbeta per step: one row per wave, each added to only by its own wave (in
+  // program order), summed over the waves in a fixed order at the end, so the result is the
+  // same on every run (LDS atomics from four waves would add in arrival order)
+  __shared__ float dlgw[4][CH], dbtw[4][CH];
   bf16* sdS = sdSF;
   bf16* sdF = sdSF + CH * TS;
   bf16* sV = sdSF;  // dV [s][d_v] (lds_off rows), staged before dS and dF are formed
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
+  float* const dlg = dlgw[w];  // this wave's rows (plain read-modify-write: see above)
+  float* const dbt = dbtw[w];
   const int c = blockIdx.x;
   const long bh = blockIdx.y;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -945,8 +950,11 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
   if (tid < CH) {
     lg[tid] = lg0;
     bt[tid] = t0 + tid < p.T ? to_f32(bt0) : 0.0f;
-    dlg[tid] = 0.0f;
-    dbt[tid] = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      dlgw[ww][tid] = 0.0f;
+      dbtw[ww][tid] = 0.0f;
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -977,7 +985,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
       for (int e = 0; e < 4; ++e) acc = fmaf(X[4 * q + e], okc ? (float)vA[j][q][e] : 0.0f, acc);
     }
     acc += __shfl_xor(acc, 32);
-    if (g == 0) atomicAdd(&dbt[s], t0 + s < p.T ? acc : 0.0f);
+    if (g == 0) dbt[s] += t0 + s < p.T ? acc : 0.0f;
   }
   __syncthreads();  // dR rows and the dV tile complete
   copy_rows(p.dv, sV);
@@ -1047,13 +1055,13 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) cs += z[r];
     cs += __shfl_xor(cs, 32);
-    if (g == 0) atomicAdd(&dlg[s], -cs);
+    if (g == 0) dlg[s] += -cs;
     const int tr = 32 * I + d_row(li & 15, g);
     const float rs = rowsum32(z, li);
-    if (li < 16) atomicAdd(&dlg[tr], rs);
+    if (li < 16) dlg[tr] += rs;
     if (kind) {
       const float rb = rowsum32(sb, li);
-      if (li < 16) atomicAdd(&dbt[tr], rb);
+      if (li < 16) dbt[tr] += rb;
     }
   }
   // dh rows d_k = 32 w + li
@@ -1119,7 +1127,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
       X[r] *= gmt;
     }
     qx += __shfl_xor(qx, 32);
-    if (g == 0) atomicAdd(&dlg[t], gmt * qx);
+    if (g == 0) dlg[t] += gmt * qx;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk >= 2 * (j + 1)) continue;  // dS[t][s] = 0 for s > t
@@ -1147,8 +1155,8 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
     k1 += __shfl_xor(k1, 32);
     k2 += __shfl_xor(k2, 32);
     if (g == 0) {
-      atomicAdd(&dlg[t], -sc1 * k1 - sc2 * k2);
-      atomicAdd(&dbt[t], -gmt * k2);
+      dlg[t] += -sc1 * k1 - sc2 * k2;
+      dbt[t] += -gmt * k2;
       dlgC += sc1 * k1;
     }
     XK[j] = X3;
@@ -1157,7 +1165,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
     float acc = hdh * __expf(lgC) + dlgC;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (l == 0) atomicAdd(&dlg[CH - 1], acc);
+    if (l == 0) dlg[CH - 1] += acc;
   }
   __syncthreads();  // every read of sQ and sK done: dQ and dK go over them
 #pragma unroll
@@ -1171,7 +1179,8 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
 
   if (w == 0) {
     // dlog(alpha_s) = sum_{t >= s} dlg_t
-    float x = dlg[l];
+    float x = (dlgw[0][l] + dlgw[1][l]) + (dlgw[2][l] + dlgw[3][l]);
+    const float dbl = (dbtw[0][l] + dbtw[1][l]) + (dbtw[2][l] + dbtw[3][l]);
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float y = __shfl_down(x, off);
@@ -1180,7 +1189,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
     const int t = t0 + l;
     if (t < p.T) {
       const long hi = head_off(p, b, h, t);
-      p.dbeta[hi] = (bf16)dbt[l];
+      p.dbeta[hi] = (bf16)dbl;
       if (p.dalpha != nullptr) p.dalpha[hi] = (bf16)(x / to_f32(p.alpha[hi]));
     }
   }

@@ -32,14 +32,17 @@ def rel_err(actual, expected):
 
 
 # Element-wise floor of assert_close, as a fraction of max |e|: entries at least this large
-# are held to (about) the tolerance relative to themselves.  At the float32 tolerance 1%.
-# At bf16 tolerances (>= 1e-3) 25%: there the kernels round MFMA operands (P, dS, chunk
-# states) to bf16, and an output that sums many such terms carries an error of order
-# 2^-9 of the largest terms, whatever its own size; with the floor at a quarter of the
-# largest entry the near-zero outputs are held to 2e-2 * 0.25 = 5e-3 of it, about one
-# bf16 ulp.
+# are held to (about) the tolerance relative to themselves.  At the float32 tolerance 1%; at
+# the bf16 tolerance 5% (the scans, convolution and cross entropy compute in float32 and round
+# only their inputs and outputs).  Kernels that round MFMA operands to bf16 (attention's P and
+# dS, the chunked delta rule's states and chunk products) take mfma_bf16=True and a floor of
+# 25%: an output that sums many such terms carries an error of order 2^-9 of the largest
+# terms, whatever its own size, so near-zero outputs are held to 2e-2 * 0.25 = 5e-3 of the
+# largest entry, about one bf16 ulp.  (Measured on the GPU suite: every bf16 scan test holds at
+# a 5% floor; the MFMA-operand tests need about 20%.)
 ELEM_FLOOR = 1e-2
-ELEM_FLOOR_BF16 = 0.25
+ELEM_FLOOR_BF16 = 0.05
+ELEM_FLOOR_MFMA_BF16 = 0.25
 
 
 def elem_rel_err(actual, expected, floor=ELEM_FLOOR):
@@ -59,10 +62,11 @@ def elem_rel_err(actual, expected, floor=ELEM_FLOOR):
     return float((np.abs(a - e) / den).max())
 
 
-def assert_close(actual, expected, tol, what="", elementwise=True, elem_tol=None):
+def assert_close(actual, expected, tol, what="", elementwise=True, elem_tol=None, mfma_bf16=False):
     """Both criteria at the same tolerance: max |a - e| / max |e| <= tol and, element by
-    element, |a - e| <= tol (|e| + floor max |e|), floor ELEM_FLOOR (float32 tolerances)
-    or ELEM_FLOOR_BF16.
+    element, |a - e| <= tol (|e| + floor max |e|), floor ELEM_FLOOR (float32 tolerances),
+    ELEM_FLOOR_BF16, or ELEM_FLOOR_MFMA_BF16 for bf16 outputs of kernels that round MFMA
+    operands to bf16 (mfma_bf16=True).
 
     elementwise=False keeps only the first, for whole bf16 models compared with float32
     references: there every weight and activation of the block is rounded to bf16 (a
@@ -73,7 +77,8 @@ def assert_close(actual, expected, tol, what="", elementwise=True, elem_tol=None
     assert np.isfinite(err) and err <= tol, f"{what}: rel err {err:.3e} > {tol:.1e}"
     if elementwise:
         etol = tol if elem_tol is None else elem_tol
-        eerr = elem_rel_err(actual, expected, ELEM_FLOOR if tol < 1e-3 else ELEM_FLOOR_BF16)
+        floor = ELEM_FLOOR if tol < 1e-3 else (ELEM_FLOOR_MFMA_BF16 if mfma_bf16 else ELEM_FLOOR_BF16)
+        eerr = elem_rel_err(actual, expected, floor)
         assert np.isfinite(eerr) and eerr <= etol, f"{what}: element-wise rel err {eerr:.3e} > {etol:.1e}"
 
 

@@ -78,10 +78,10 @@ def test_c3_gated_delta_rule_full_size(rng):
         s4 = (slice(b, b + 1), slice(None), slice(h, h + 1))
         qr, kr, vr, dor = (rounded(a, BF16)[s4] for a in (q, k, v, do))
         br, ar = rounded(beta, BF16)[s4], rounded(alpha, BF16)[s4]
-        assert_close(host(out)[s4], scans.delta_rule(qr, kr, vr, br, ar), tol, f"o ({b},{h})")
+        assert_close(host(out)[s4], scans.delta_rule(qr, kr, vr, br, ar), tol, f"o ({b},{h})", mfma_bf16=True)
         g = scans.delta_rule_backward(qr, kr, vr, br, dor, ar)
         for name, t in (("dq", tq), ("dk", tk), ("dv", tv), ("dbeta", tb), ("dalpha", ta)):
-            assert_close(host(t.grad)[s4], g[name], tol, f"{name} ({b},{h})")
+            assert_close(host(t.grad)[s4], g[name], tol, f"{name} ({b},{h})", mfma_bf16=True)
 
 
 def test_c4_flash_attention_full_grid(rng):
@@ -101,10 +101,11 @@ def test_c4_flash_attention_full_grid(rng):
     for b, h in ((0, 0), (3, 31)):
         s = (slice(b, b + 1), slice(h, h + 1))
         qr, kr, vr, dor = (rounded(a, BF16)[s] for a in (q, k, v, do))
-        assert_close(host(out)[s], scans.flash_attention(qr, kr, vr, causal=True), tol, f"o ({b},{h})")
+        assert_close(host(out)[s], scans.flash_attention(qr, kr, vr, causal=True), tol, f"o ({b},{h})",
+                     mfma_bf16=True)
         dq, dk, dv = scans.flash_attention_backward(qr, kr, vr, dor, causal=True)
         for name, t, e in (("dq", tq, dq), ("dk", tk, dk), ("dv", tv, dv)):
-            assert_close(host(t.grad)[s], e, tol, f"{name} ({b},{h})")
+            assert_close(host(t.grad)[s], e, tol, f"{name} ({b},{h})", mfma_bf16=True)
 
 
 def _hybrid(dtype, seed=5):

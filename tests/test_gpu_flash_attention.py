@@ -35,7 +35,7 @@ def test_flash_attention_fwd_bwd(case, rng):
     out.backward(to_dev(do, dtype))
     qr, kr, vr, dor = (rounded(a, dtype) for a in (q, k, v, do))
     tol = TOL[dtype]
-    assert_close(host(out), scans.flash_attention(qr, kr, vr, causal), tol, "O")
+    assert_close(host(out), scans.flash_attention(qr, kr, vr, causal), tol, "O", mfma_bf16=True)
     dq, dk, dv = scans.flash_attention_backward(qr, kr, vr, dor, causal)
     if T == 1:
         # One key: O = V[0] exactly, so dP - D = dO . (V[0] - O) = 0 and dQ = dK = 0
@@ -46,9 +46,9 @@ def test_flash_attention_fwd_bwd(case, rng):
         for name, got in (("dQ", host(tq.grad)), ("dK", host(tk.grad))):
             assert np.abs(got).max() <= tol * term, f"{name}: |{name}| {np.abs(got).max():.3e} > {tol * term:.3e}"
     else:
-        assert_close(host(tq.grad), dq, tol, "dQ")
-        assert_close(host(tk.grad), dk, tol, "dK")
-    assert_close(host(tv.grad), dv, tol, "dV")
+        assert_close(host(tq.grad), dq, tol, "dQ", mfma_bf16=True)
+        assert_close(host(tk.grad), dk, tol, "dK", mfma_bf16=True)
+    assert_close(host(tv.grad), dv, tol, "dV", mfma_bf16=True)
 
 
 def test_flash_attention_lse_and_invariants(rng):
@@ -68,11 +68,11 @@ def test_flash_attention_lse_and_invariants(rng):
     qr, kr, vr = (rounded(a, torch.bfloat16) for a in (q, k, v))
     o_ref, lse_ref = scans.flash_attention(qr, kr, vr, True, return_lse=True)
     assert_close(host(lse), lse_ref, 1e-3, "lse")
-    assert_close(host(out)[:, :, 0], vr[:, :, 0], TOL[torch.bfloat16], "causal row 0")
+    assert_close(host(out)[:, :, 0], vr[:, :, 0], TOL[torch.bfloat16], "causal row 0", mfma_bf16=True)
     same_k = tk[:, :, :1].expand(-1, -1, T, -1).contiguous()
     nat.call("edf_fused_flash_attention", stream, P(tq), P(same_k), P(tv), P(out), P(lse), B, H, T, d, 0, 1)
     assert_close(host(out), np.broadcast_to(vr.mean(axis=2, keepdims=True), vr.shape), TOL[torch.bfloat16],
-                 "identical keys")
+                 "identical keys", mfma_bf16=True)
 
 
 def test_flash_attention_config4_head_slice(rng):
@@ -87,11 +87,11 @@ def test_flash_attention_config4_head_slice(rng):
     out.backward(to_dev(do, torch.bfloat16))
     qr, kr, vr, dor = (rounded(a, torch.bfloat16) for a in (q, k, v, do))
     tol = TOL[torch.bfloat16]
-    assert_close(host(out), scans.flash_attention(qr, kr, vr, True), tol, "O")
+    assert_close(host(out), scans.flash_attention(qr, kr, vr, True), tol, "O", mfma_bf16=True)
     dq, dk, dv = scans.flash_attention_backward(qr, kr, vr, dor, True)
-    assert_close(host(tq.grad), dq, tol, "dQ")
-    assert_close(host(tk.grad), dk, tol, "dK")
-    assert_close(host(tv.grad), dv, tol, "dV")
+    assert_close(host(tq.grad), dq, tol, "dQ", mfma_bf16=True)
+    assert_close(host(tk.grad), dk, tol, "dK", mfma_bf16=True)
+    assert_close(host(tv.grad), dv, tol, "dV", mfma_bf16=True)
 
 
 FOX_CASES = [
@@ -122,12 +122,12 @@ def test_fox_attention_fwd_bwd(case, rng):
     out.backward(to_dev(do, dtype))
     qr, kr, vr, cr, dor = (rounded(a, dtype) for a in (q, k, v, cs, do))
     tol = TOL[dtype]
-    assert_close(host(out), scans.fox_attention(qr, kr, vr, cr), tol, "O")
+    assert_close(host(out), scans.fox_attention(qr, kr, vr, cr), tol, "O", mfma_bf16=True)
     dq, dk, dv, dcs = scans.fox_attention_backward(qr, kr, vr, cr, dor)
-    assert_close(host(tq.grad), dq, tol, "dQ")
-    assert_close(host(tk.grad), dk, tol, "dK")
-    assert_close(host(tv.grad), dv, tol, "dV")
-    assert_close(host(tc.grad), dcs, tol, "dcs")
+    assert_close(host(tq.grad), dq, tol, "dQ", mfma_bf16=True)
+    assert_close(host(tk.grad), dk, tol, "dK", mfma_bf16=True)
+    assert_close(host(tv.grad), dv, tol, "dV", mfma_bf16=True)
+    assert_close(host(tc.grad), dcs, tol, "dcs", mfma_bf16=True)
 
 
 def test_fox_with_constant_cs_is_causal_flash(rng):
@@ -169,12 +169,12 @@ def test_laser_attention_fwd_bwd(case, rng):
     out.backward(to_dev(do, dtype))
     qr, kr, vr, dor = (rounded(a, dtype) for a in (q, k, v, do))
     tol = TOL[dtype]
-    assert_close(host(out), scans.laser_attention(qr, kr, vr, causal), tol, "O")
+    assert_close(host(out), scans.laser_attention(qr, kr, vr, causal), tol, "O", mfma_bf16=True)
     dq, dk, dv = scans.laser_attention_backward(qr, kr, vr, dor, causal)
     # bf16 gradients pass through one more bf16 rounding than the flash ones (E = exp(V - vmax)
     # is an MFMA operand): element-wise 3e-2, still tighter than the reference's own bf16
     # LASER gradient check (absolute 0.05, attention_backward_test.exs:227-229)
     et = 3e-2 if dtype == torch.bfloat16 else None
-    assert_close(host(tq.grad), dq, tol, "dQ", elem_tol=et)
-    assert_close(host(tk.grad), dk, tol, "dK", elem_tol=et)
-    assert_close(host(tv.grad), dv, tol, "dV", elem_tol=et)
+    assert_close(host(tq.grad), dq, tol, "dQ", elem_tol=et, mfma_bf16=True)
+    assert_close(host(tk.grad), dk, tol, "dK", elem_tol=et, mfma_bf16=True)
+    assert_close(host(tv.grad), dv, tol, "dV", elem_tol=et, mfma_bf16=True)
