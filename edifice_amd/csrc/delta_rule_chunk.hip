@@ -865,9 +865,10 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 sdR[CH * DK];        // dR [s][d_v]
   __shared__ __attribute__((aligned(16))) bf16 sdSF[2 * CH * TS];   // dS [t][s], dF = dG + dG^T [t][s]
   __shared__ float lg[CH], bt[CH];
-  // d log-gamma and dbeta per step: one row per wave, each added to only by its own wave (in
-  // program order), summed over the waves in a fixed order at the end, so the result is the
-  // same on every run (LDS atomics from four waves would add in arrival order)
+  // d log-gamma and dbeta per step: one row per wave, added to only by its own wave, so its LDS
+  // atomic adds (no return value, no wait) land in program order; the rows are summed over the
+  // waves in a fixed order at the end, so the result is the same on every run (one row shared
+  // by the four waves added in arrival order)
   __shared__ float dlgw[4][CH], dbtw[4][CH];
   bf16* sdS = sdSF;
   bf16* sdF = sdSF + CH * TS;
@@ -875,8 +876,15 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, g = l >> 5, li = l & 31;
-  float* const dlg = dlgw[w];  // this wave's rows (plain read-modify-write: see above)
-  float* const dbt = dbtw[w];
+  // this wave's row of dlgw / dbtw, chosen by a wave-uniform branch so that each add's LDS
+  // address keeps a constant row base (a per-wave row pointer cost registers and spills)
+  const int wrow = __builtin_amdgcn_readfirstlane(w);
+  auto add_row = [&](float (*rows)[CH], int i, float v) {
+    if (wrow == 0) atomicAdd(&rows[0][i], v);
+    else if (wrow == 1) atomicAdd(&rows[1][i], v);
+    else if (wrow == 2) atomicAdd(&rows[2][i], v);
+    else atomicAdd(&rows[3][i], v);
+  };
   const int c = blockIdx.x;
   const long bh = blockIdx.y;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -985,7 +993,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
       for (int e = 0; e < 4; ++e) acc = fmaf(X[4 * q + e], okc ? (float)vA[j][q][e] : 0.0f, acc);
     }
     acc += __shfl_xor(acc, 32);
-    if (g == 0) dbt[s] += t0 + s < p.T ? acc : 0.0f;
+    if (g == 0) add_row(dbtw, s, t0 + s < p.T ? acc : 0.0f);
   }
   __syncthreads();  // dR rows and the dV tile complete
   copy_rows(p.dv, sV);
@@ -1055,13 +1063,13 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) cs += z[r];
     cs += __shfl_xor(cs, 32);
-    if (g == 0) dlg[s] += -cs;
+    if (g == 0) add_row(dlgw, s, -cs);
     const int tr = 32 * I + d_row(li & 15, g);
     const float rs = rowsum32(z, li);
-    if (li < 16) dlg[tr] += rs;
+    if (li < 16) add_row(dlgw, tr, rs);
     if (kind) {
       const float rb = rowsum32(sb, li);
-      if (li < 16) dbt[tr] += rb;
+      if (li < 16) add_row(dbtw, tr, rb);
     }
   }
   // dh rows d_k = 32 w + li
@@ -1127,7 +1135,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
       X[r] *= gmt;
     }
     qx += __shfl_xor(qx, 32);
-    if (g == 0) dlg[t] += gmt * qx;
+    if (g == 0) add_row(dlgw, t, gmt * qx);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       if (kk >= 2 * (j + 1)) continue;  // dS[t][s] = 0 for s > t
@@ -1155,8 +1163,8 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
     k1 += __shfl_xor(k1, 32);
     k2 += __shfl_xor(k2, 32);
     if (g == 0) {
-      dlg[t] += -sc1 * k1 - sc2 * k2;
-      dbt[t] += -gmt * k2;
+      add_row(dlgw, t, -sc1 * k1 - sc2 * k2);
+      add_row(dbtw, t, -gmt * k2);
       dlgC += sc1 * k1;
     }
     XK[j] = X3;
@@ -1165,7 +1173,7 @@ __global__ __launch_bounds__(256, 2) void dr_ck_grad_kernel(const CkArgs p) {
     float acc = hdh * __expf(lgC) + dlgC;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-    if (l == 0) dlg[CH - 1] += acc;
+    if (l == 0) add_row(dlgw, CH - 1, acc);
   }
   __syncthreads();  // every read of sQ and sK done: dQ and dK go over them
 #pragma unroll
