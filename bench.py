@@ -765,11 +765,11 @@ def cpu_baseline_delta_rule(B=4, H=16, T=4096, d=128, C=64):
     """Config 3 on the C restatement (recurrent form, f32, states checkpointed every 64 steps
     for the backward), the full workload; TFLOP/s under the GPU row's chunked-form flop count."""
     lib = _cpu_lib()
-    t = _cpu_median(_delta_cpu(lib, B, T, H, d, True, True, 9), warmup=1, reps=5)
+    t = _cpu_median(_delta_cpu(lib, B, T, H, d, True, True, 9), warmup=2, reps=5)
     flops = 3 * 2 * (5 * C * d + 3 * d * d) * B * H * T
     return _cpu_entry(flops / t / 1e12, "TFLOP/s", lib,
                       f"C restatement, gated delta rule fwd+bwd f32 (recurrent form), B={B} H={H} T={T} d={d} (the "
-                      f"full config-3 workload), median of 5 after 1 warm-up, {t:.3f} s per step", s_per_step=t)
+                      f"full config-3 workload), median of 5 after 2 warm-ups, {t:.3f} s per step", s_per_step=t)
 
 
 def _attn_cpu(lib, BH, T, d, causal, seed):
@@ -791,12 +791,12 @@ def cpu_baseline_attention(B=4, H=32, T=4096, d=128, sample_heads=16):
     the (b, h) heads, which are independent and equal in cost; TFLOP/s under the GPU row's flop
     count, and the full-step time scaled from the sample."""
     lib = _cpu_lib()
-    t = _cpu_median(_attn_cpu(lib, sample_heads, T, d, True, 10), warmup=1, reps=5)
+    t = _cpu_median(_attn_cpu(lib, sample_heads, T, d, True, 10), warmup=2, reps=5)
     flops = 3.5 * 4 * sample_heads * T * T * d / 2
     full = t * B * H / sample_heads
     return _cpu_entry(flops / t / 1e12, "TFLOP/s", lib,
                       f"C restatement, causal attention fwd+bwd f32 on {sample_heads} of the {B * H} heads "
-                      f"(T={T} d={d}), median of 5 after 1 warm-up, {t:.3f} s; full step scaled: {full:.2f} s",
+                      f"(T={T} d={d}), median of 5 after 2 warm-ups, {t:.3f} s; full step scaled: {full:.2f} s",
                       s_per_step=full)
 
 
@@ -819,7 +819,7 @@ def cpu_baseline_hybrid(B=8, T=2048, embed=1024, sample_rows=1):
         for _ in range(2):
             dr()
             at()
-    t = _cpu_median(step, warmup=1, reps=5) * B / sample_rows
+    t = _cpu_median(step, warmup=2, reps=5) * B / sample_rows
     return _cpu_entry(B * T / t, "tokens/s", lib,
                       f"C restatement of config 5's fused ops only (4 selective scans, 2 delta rules, 2 causal "
                       f"attentions, fwd+bwd, f32) on {sample_rows} of {B} batch rows (T={T}), median of 5 after 1 "
