@@ -250,14 +250,17 @@ __global__ __launch_bounds__(256, 2) void fa_fwd_mfma_kernel(const bf16* __restr
 // staging registers), and K one tile ahead of V: iteration t issues the MFMAs of S(t + 1) before
 // the softmax of S(t), so the matrix core works on the next scores while the VALU turns
 // the current ones into P (the two rings stay two-deep: K(t) was consumed in iteration
-// t - 1).  Two workgroups per CU.
-template <bool CAUSAL, bool FOX = false>
+// t - 1).  Two workgroups per CU.  FULL (non-causal, T a multiple of the key tile): every
+// tile is inside the sequence and unmasked, so the masked body is not compiled (with it,
+// the non-causal instance spilled 49 registers).
+template <bool CAUSAL, bool FOX = false, bool FULL = false>
 __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                            const bf16* __restrict__ V, bf16* __restrict__ O,
                                                            float* __restrict__ LSE, int T, float scale_log2,
                                                            const bf16* __restrict__ CS, float sqd) {
   constexpr int HD = 128, BM = 128, BN = 64;
   constexpr int NKK = HD / 16, NDT = HD / 32;
+  static_assert(!(FULL && (CAUSAL || FOX)), "FULL is the unmasked non-causal instance");
   // Two arrays, X0 = {K buffer 0, V buffer 1} and X1 = {K buffer 1, V buffer 0}: iteration t
   // (parity B) writes only X_B and reads only X_(1-B), and each array's fixed address costs
   // address registers (it is not folded into the LDS offset field).
@@ -481,7 +484,10 @@ __global__ __launch_bounds__(256, 2) void fa_fwd128_kernel(const bf16* __restric
     if (t + 2 < nkt) issue_k(bt, t + 2);
     if (t + 1 < nkt) issue_v(ot, t + 1);
     const bool nvis = t + 1 < nkt && visible(t + 1);
-    if (visible(t)) {
+    if constexpr (FULL) {
+      if (nvis) fused(bt, t);
+      else consume(bt, sc, t, std::false_type{});
+    } else if (visible(t)) {
       if (t < ksplit && nvis) {
         fused(bt, t);
       } else {
@@ -613,6 +619,8 @@ void launch_mfma_fwd(hipStream_t s, const void* q, const void* k, const void* v,
       fa_fwd128_kernel<true, true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, CS, sqd);
     else if (causal)
       fa_fwd128_kernel<true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
+    else if (T % 64 == 0)
+      fa_fwd128_kernel<false, false, true><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
     else
       fa_fwd128_kernel<false><<<grid, 256, 0, s>>>(Q, K, V, (bf16*)o, lse, T, scale_log2, nullptr, 0.0f);
     return;

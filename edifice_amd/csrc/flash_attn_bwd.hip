@@ -431,7 +431,11 @@ __global__ __launch_bounds__(256, 1) void fa_bwd_dq_kernel(const bf16* __restric
 // with K as register B fragments but V read from an LDS copy of the workgroup's 128 x 128
 // tile (its fragments would not fit 256 registers beside the dK^T, dV^T accumulators) and
 // 32-query tiles of Q and dO (two workgroups' rings and V tiles fit the 160 KB LDS).
-template <bool CAUSAL, bool FOX>
+// FULL (non-causal, T a multiple of the query tile): no tile needs the mask, and only the
+// unmasked body is compiled (with both bodies the non-causal instance spills its K
+// fragments).  Keys past the end then get nonzero P and dS in their own columns, which are
+// never stored.
+template <bool CAUSAL, bool FOX, bool FULL = false>
 __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                                 const bf16* __restrict__ V,
                                                                 const bf16* __restrict__ dO,
@@ -442,6 +446,7 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
                                                                 float* __restrict__ DCSK, float sqd) {
   constexpr int HD = 128, BKEY = 128, BQ = 32;
   constexpr int NKK = HD / 16, NDT = HD / 32;
+  static_assert(!(FULL && (CAUSAL || FOX)), "FULL is the unmasked non-causal instance");
   __shared__ __attribute__((aligned(16))) bf16 sV[BKEY * HD];
   // ring slot b: Q then dO (one array per slot: the compiler's fixed array addresses are
   // not folded into the LDS offset field, so each array costs address registers)
@@ -571,13 +576,21 @@ __global__ __launch_bounds__(256, 2) void fa_bwd_dkdv128_kernel(const bf16* __re
         dkt[dt] = mfma32(cat4(lds_read_tr16(&sQ[o0]), lds_read_tr16(&sQ[o1])), db[kc], dkt[dt]);
       }
   };
+  // FULL: a skip test the compiler cannot resolve (opaque_lo is -1, no tile is skipped).
+  // With an unconditional tile body the register allocator spilled 129 registers (the K
+  // fragments among them, reloaded inside the loop); with the causal instance's shape of
+  // control flow it needs 250 and spills none.
+  int opaque_lo = -1;
+  if constexpr (FULL) asm volatile("" : "+s"(opaque_lo));
   auto tile = [&](auto bt, int q0) {
 #pragma unroll
     for (int sub = 0; sub < BQ / 32; ++sub) {
       const int qs = q0 + 32 * sub;
       if (CAUSAL && qs + 31 < kw) continue;  // every query of the sub-tile precedes this wave's keys
+      if (FULL && qs < opaque_lo) continue;
       // masked body on the causal diagonal and in a tile that runs past the end
-      if ((CAUSAL && qs < kw + 31) || q0 + BQ > T) subtile(bt, q0, sub, std::true_type{});
+      if constexpr (FULL) subtile(bt, q0, sub, std::false_type{});
+      else if ((CAUSAL && qs < kw + 31) || q0 + BQ > T) subtile(bt, q0, sub, std::true_type{});
       else subtile(bt, q0, sub, std::false_type{});
     }
   };
@@ -946,10 +959,15 @@ void launch_mfma_bwd128(hipStream_t s, const bf16* Q, const bf16* K, const bf16*
   } else {
     fa_bwd_dq128_kernel<false, false, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, nullptr, dq, T, scale_log2, scale,
                                                                nullptr, nullptr, nullptr, 0.0f, O, Dd);
-    // non-causal dK/dV: the one-wave-per-SIMD kernel (the two-workgroup variant's register
-    // allocation spills its K fragments when compiled without the causal branches)
-    fa_bwd_dkdv_kernel<128, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, nullptr,
-                                                      nullptr, 0.0f);
+    // non-causal dK/dV: the two-workgroup kernel's unmasked instance when every query tile
+    // is whole; otherwise the one-wave-per-SIMD kernel (the two-workgroup variant spills its
+    // K fragments when compiled with the masked body but without the causal branches)
+    if (T % 32 == 0)
+      fa_bwd_dkdv128_kernel<false, false, true><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale,
+                                                                   nullptr, nullptr, 0.0f);
+    else
+      fa_bwd_dkdv_kernel<128, false><<<g1, 256, 0, s>>>(Q, K, V, G, lse, Dd, dk, dv, T, scale_log2, scale, nullptr,
+                                                        nullptr, 0.0f);
   }
 }
 

@@ -14,6 +14,8 @@ CASES = [
     (2, 2, 64, 32, torch.bfloat16, True),
     (1, 2, 200, 64, torch.bfloat16, True),
     (1, 2, 130, 128, torch.bfloat16, False),
+    (2, 2, 256, 128, torch.bfloat16, False),  # whole key and query tiles: the unmasked instances
+    (1, 2, 160, 128, torch.bfloat16, False),  # whole 32-query tiles, a partial 64-key tile
     (2, 1, 256, 128, torch.bfloat16, True),
     (1, 1, 1, 128, torch.bfloat16, True),
     (1, 3, 33, 24, torch.bfloat16, True),     # odd head_dim: wave-per-row path
