@@ -171,13 +171,23 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
 // S_t = S_g + be k^T, dtot = dS + do q^T):  dq = S_t^T do, dv = beta ds_k,
 // dbeta = err ds_k, dk = dtot^T be - S_g^T (beta ds_k), dalpha = sum((dtot - beta ds_k k^T) o S_p),
 // dS <- a (dtot - beta ds_k k^T), with err = v - S_g k, be = beta err, ds_k = dtot k.
+//
+// The sums over the block's rows (dq, dk: one value per column; dalpha and a per-head
+// dbeta: one per row) leave the dependency chain of the steps: each wave sums its four
+// rows in registers (rows4_scatter: the lane of row r keeps the column sums of one value
+// in four) into a per-step slot of an LDS buffer, and every FS steps one barrier pair adds
+// the four waves' slots (in wave order) and stores the partials of those steps.
 template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
   constexpr int NC = DP / 16;
+  constexpr int FS = 8;                 // steps per flush of the row sums
+  constexpr int NG = (2 * NC + 3) / 4;  // rows4_scatter groups of the lane's 2 NC column values
+  static_assert(CK % FS == 0, "flushes split the chunk");
   __shared__ Stage<DP> sms[2];
-  __shared__ float red[2][RB][row16_stride(DP)];  // per-row column partials: [qty][tr][j]
-  __shared__ float reda[2][RB];
+  __shared__ float wsum[FS][4][NG][64];  // [step slot][wave][group][lane]: four-row sums
+  __shared__ float rsum[FS][2][RB];      // [step slot][dalpha | dbeta][row]
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  const int w = tid >> 6, lane = tid & 63;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -254,36 +264,46 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
         st((TT*)p.dv, bth * p.d + i, bdk);
         if (!p.beta_per_head) st((TT*)p.dbeta, bth * p.d + i, err * sk);
       }
-      // sums over this block's rows (dq, dk, dalpha, per-head dbeta) through LDS
+      // this wave's four rows summed per column: value k = qty NC + c (pq then pk), group
+      // k / 4; the lane of row r keeps item rows4_item(r) of each group
+      const int slot = tt % FS;
+      float vals[4 * NG];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        red[0][tr][tc + 16 * c] = pq[c];
-        red[1][tr][tc + 16 * c] = pk[c];
+        vals[c] = pq[c];
+        vals[NC + c] = pk[c];
       }
+#pragma unroll
+      for (int k = 2 * NC; k < 4 * NG; ++k) vals[k] = 0.0f;
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+        wsum[slot][w][g][lane] = rows4_scatter(vals[4 * g], vals[4 * g + 1], vals[4 * g + 2], vals[4 * g + 3]);
       pa = row16_sum(pa);
       if (tc == 0) {
-        reda[0][tr] = pa;
-        reda[1][tr] = i < p.d ? err * sk : 0.0f;
+        rsum[slot][0][tr] = pa;
+        rsum[slot][1][tr] = i < p.d ? err * sk : 0.0f;
         // KDA: the row's own decay gradient, in log space
         if (p.alpha_per_row && live && i < p.d) st((TT*)p.dalpha, bth * p.d + i, pa * at);
       }
-      __syncthreads();
-      if (live) {
-        for (int e = tid; e < 2 * DP; e += 256) {
-          const int qty = e / DP, j = e % DP;
+      if (slot == 0) {  // steps t .. t + FS - 1 are in the slots: sum the waves, store
+        __syncthreads();
+        for (int e = tid; e < FS * 2 * DP; e += 256) {
+          const int sl = e / (2 * DP), qty = (e / DP) & 1, j = e % DP;
+          const int k = qty * NC + (j >> 4), g = k >> 2, src = 16 * rows4_item(k & 3) + (j & 15);
+          const float acc = ((wsum[sl][0][g][src] + wsum[sl][1][g][src]) + wsum[sl][2][g][src]) + wsum[sl][3][g][src];
+          const int ts = t + sl;
+          if (ts < p.T && j < p.d)
+            (qty == 0 ? p.part_q : p.part_k)[((long)rb * nbth + ((long)b * p.T + ts) * p.H + h) * p.d + j] = acc;
+        }
+        if (tid < 2 * FS) {
+          const int sl = tid >> 1, qty = tid & 1, ts = t + sl;
           float acc = 0.0f;
 #pragma unroll
-          for (int m = 0; m < RB; ++m) acc += red[qty][m][j];
-          if (j < p.d) (qty == 0 ? p.part_q : p.part_k)[((long)rb * nbth + bth) * p.d + j] = acc;
+          for (int m = 0; m < RB; ++m) acc += rsum[sl][qty][m];
+          if (ts < p.T) (qty == 0 ? p.part_a : p.part_b)[(long)rb * nbth + ((long)b * p.T + ts) * p.H + h] = acc;
         }
-        if (tid < 2) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int m = 0; m < RB; ++m) acc += reda[tid][m];
-          (tid == 0 ? p.part_a : p.part_b)[(long)rb * nbth + bth] = acc;
-        }
+        __syncthreads();
       }
-      __syncthreads();
     }
     // the other buffer was last read in the previous chunk, before this chunk's barriers
     store_chunk<TT, DP>(sms[(ck + 1) & 1], R, p, rb, (ck - 1) * CK, true);

@@ -133,6 +133,27 @@ EDF_DEVICE float row16_sum(float x) {
   return x;
 }
 
+// Lane swaps between the four 16-lane rows of a wave.  Inline assembly: the compiler's
+// permlane swap builtins return the first register's new value in both halves of their
+// result when the second half is read through __builtin_bit_cast.  The s_nop covers the
+// wait states a VALU write needs before a permlane swap reads the register.
+EDF_DEVICE void swap16(float& a, float& b) {  // odd rows of a <-> even rows of b
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+EDF_DEVICE void swap32(float& a, float& b) {  // rows 2, 3 of a <-> rows 0, 1 of b
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// Reduce-scatter over the four rows: v[0..3] summed lane-wise over the rows, the lane in
+// row r receiving the sum of v[rows4_item(r)] (rows4_item is its own inverse).
+EDF_DEVICE constexpr int rows4_item(int r) { return 2 * (r & 1) + (r >> 1); }
+EDF_DEVICE float rows4_scatter(float v0, float v1, float v2, float v3) {
+  swap16(v0, v2);  // v0: rows 0, 2 keep v0, rows 1, 3 receive v2 of rows 0, 2
+  swap16(v1, v3);
+  float w0 = v0 + v2, w1 = v1 + v3;  // even rows: v0 / v1 of rows r, r + 1; odd rows: v2 / v3
+  swap32(w0, w1);
+  return w0 + w1;
+}
+
 // ---- launch-shape helpers -----------------------------------------------------
 // MI355X dispatches consecutive workgroup ids round-robin over its 8 XCDs, each
 // with a private L2.  remap_xcd() turns the hardware id into a logical id such
