@@ -32,6 +32,11 @@
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
 
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
 #include <type_traits>
 
 namespace edf {
@@ -619,6 +624,300 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
   }
 }
 
+// ---------------------------------------------------------------------------------
+// Look-back scan (long sequences): the sequence is split into parts of SR = 16 R steps, one
+// workgroup per (batch row, 64-lane channel tile, part), so that a bf16 tile of 128 channels
+// (two per lane) or an f32 tile of 64 is read as whole 256-byte row pieces by 16 waves x
+// (parts) workgroups.  A copy kernel of the bandwidth row's shape reads and writes at
+// 36 us with the one-workgroup-per-tile layout above and at 29.6 us with 256-byte pieces
+// over eight parts; the parts need the carry of the steps before them.
+//
+// Each workgroup loads its rows (R per wave) into registers, folds them into per-wave affine
+// maps, and its first wave composes them into the part's map (A, B) and publishes it.  The
+// part's carry is h0 taken through the maps of all earlier parts of its tile: its waves fetch
+// those maps together (wave v parts v, v + 16, ...), so the wait is for the earlier parts to
+// fold their own rows, not a chain of carries passed from part to part.
+//
+// Published values are 64-bit words {call epoch, f32 bits} written and read as device-scope
+// atomics (coherent across the XCDs' separate L2 caches); a word counts only when its epoch
+// is this call's, so words of earlier calls or of a call running at the same time on another
+// stream are never taken for this one's.  A wave that polls LB_SPIN times without finding a
+// part's words (overwritten by such a concurrent call, or a part not yet running) folds that
+// part's map from its rows itself: every workgroup finishes, whatever the dispatch order.
+// EDF_LIN_LOOKBACK_SPIN sets the poll limit (0 folds every map not published at the first
+// look, which the tests use to run that path).  Calls being captured into a graph use the
+// kernels above (a replay would repeat the captured epoch).
+// ---------------------------------------------------------------------------------
+constexpr int LB_W = 16;                // waves per workgroup
+constexpr int LB_R = 8;                 // steps per wave: parts of 128 steps (768 workgroups at
+                                        // the bandwidth row in bf16; two per CU fit)
+constexpr int LB_SPIN = 1 << 14;        // default polls of a part's words before folding them here
+constexpr int LB_MAXP = 32;             // parts per sequence
+constexpr size_t LB_WORDS = 1u << 20;   // published words per device (8 MiB)
+static __device__ __align__(256) unsigned long long lb_flags[LB_WORDS];
+
+EDF_DEVICE void lb_put(unsigned long long* p, unsigned epoch, float v) {
+  const unsigned long long x = ((unsigned long long)epoch << 32) | __builtin_bit_cast(unsigned, v);
+  __hip_atomic_store(p, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+EDF_DEVICE bool lb_get(unsigned long long* p, unsigned epoch, float& v) {
+  const unsigned long long x = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v = __builtin_bit_cast(float, (unsigned)x);
+  return (unsigned)(x >> 32) == epoch;
+}
+
+// 4 bytes per lane per row: a bf16 pair (two channels) or one f32 channel
+template <typename T> struct Lane4;
+template <> struct Lane4<bf16> {
+  static constexpr int C = 2;
+  static EDF_DEVICE unsigned load(rsrc_t r, unsigned off) { return Pair<bf16>::load(r, off); }
+  static EDF_DEVICE float get(unsigned v, int k) { return k ? Pair<bf16>::hi(v) : Pair<bf16>::lo(v); }
+  static EDF_DEVICE void store(rsrc_t r, unsigned off, const float* x) { Pair<bf16>::store(r, off, x[0], x[1]); }
+};
+template <> struct Lane4<float> {
+  static constexpr int C = 1;
+  static EDF_DEVICE unsigned load(rsrc_t r, unsigned off) { return bload<float>(r, off); }
+  static EDF_DEVICE float get(unsigned v, int) { return bits_f32(v); }
+  static EDF_DEVICE void store(rsrc_t r, unsigned off, const float* x) { bstore<float>(r, off, x[0]); }
+};
+
+// flags: [part][batch row x tile][A | B][channel of the lane][lane]
+template <typename T, int OP, bool LOGITS, int R>
+__global__ __launch_bounds__(64 * LB_W) void linscan_lb_fwd_kernel(const T* __restrict__ g1, const T* __restrict__ g2,
+                                                                   const T* __restrict__ cand, const T* __restrict__ h0,
+                                                                   T* __restrict__ out, int seq, int hid, int ntile,
+                                                                   unsigned long long* __restrict__ flags,
+                                                                   unsigned epoch, int spin_limit) {
+  typedef Lane4<T> LN;
+  constexpr int W = LB_W, C = LN::C, SR = W * R;
+  constexpr unsigned ES = sizeof(T);
+  __shared__ float sA[W][C][64];
+  __shared__ float sB[W][C][64];
+  __shared__ float sH[C][64];
+  __shared__ float sPA[LB_MAXP][C][64];  // the earlier parts' maps
+  __shared__ float sPB[LB_MAXP][C][64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int bt = blockIdx.x, nbt = gridDim.x, part = blockIdx.y, nparts = gridDim.y;
+  const int b = bt / ntile, tile = bt % ntile;
+  const int c = (tile * 64 + lane) * C;  // the lane's first channel (hid is a multiple of C)
+  const bool valid = c < hid;
+  const long slab = (long)b * seq * hid;
+  const unsigned bytes = (unsigned)((long)seq * hid * ES);
+  const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
+  const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
+  const rsrc_t RC = make_rsrc(cand + slab, bytes);
+  const rsrc_t RO = make_rsrc(out + slab, bytes);
+  const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
+  auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
+  // coefficients of channel k of a row from its raw values; steps past the sequence and
+  // channels past hid are identity maps
+  auto coef = [&](unsigned x1, unsigned x2, unsigned xc, int k, bool ok, float& a, float& bb) {
+    Step<OP, LOGITS> st;
+    st.make(LN::get(x1, k), OP == OP_MINLSTM ? LN::get(x2, k) : 0.0f, LN::get(xc, k));
+    a = ok ? st.a : 1.0f;
+    bb = ok ? st.b : 0.0f;
+  };
+
+  const int t0 = part * SR + w * R;
+  unsigned r1[R], r2[R], rc[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const unsigned o = off(t0 + j);
+    r1[j] = LN::load(R1, o);
+    if (OP == OP_MINLSTM) r2[j] = LN::load(R2, o);
+    rc[j] = LN::load(RC, o);
+  }
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    float A = 1.0f, B = 0.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      float a, bb;
+      coef(r1[j], OP == OP_MINLSTM ? r2[j] : 0u, rc[j], k, valid && t0 + j < seq, a, bb);
+      B = fmaf(a, B, bb);
+      A *= a;
+    }
+    sA[w][k][lane] = A;
+    sB[w][k][lane] = B;
+  }
+  __syncthreads();
+
+  // the part's map: wave 0 composes the 16 wave maps (in groups of four: issued all at once,
+  // their 4 C W LDS reads held the kernel's peak registers) and publishes it
+  auto words = [&](int pt) { return flags + (long)(pt * nbt + bt) * 2 * C * 64 + lane; };
+  if (w == 0 && part + 1 < nparts) {
+    float Ag[C], Bg[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      Ag[k] = 1.0f;
+      Bg[k] = 0.0f;
+    }
+#pragma unroll
+    for (int v0 = 0; v0 < W; v0 += 4) {
+#pragma unroll
+      for (int v = v0; v < v0 + 4; ++v)
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          Bg[k] = fmaf(sA[v][k][lane], Bg[k], sB[v][k][lane]);
+          Ag[k] *= sA[v][k][lane];
+        }
+      asm volatile("" ::: "memory");
+    }
+    unsigned long long* mine = words(part);
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      lb_put(mine + k * 64, epoch, Ag[k]);
+      lb_put(mine + (C + k) * 64, epoch, Bg[k]);
+    }
+  }
+  // the maps of the earlier parts, wave v fetching parts v, v + 16, ...: every part's map is
+  // published as soon as its own rows are folded, so the fetches of all predecessors wait
+  // together, not one after another
+  for (int j = w; j < part; j += W) {
+    unsigned long long* pj = words(j);
+    float av[C], bv[C];
+    for (int spins = 0;; ++spins) {
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        ok = lb_get(pj + k * 64, epoch, av[k]) && ok;
+        ok = lb_get(pj + (C + k) * 64, epoch, bv[k]) && ok;
+      }
+      if (__all(ok)) break;
+      if (spins >= spin_limit) {
+        // no words from part j: its map folded here from its rows
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          av[k] = 1.0f;
+          bv[k] = 0.0f;
+        }
+#pragma unroll 1
+        for (int t = j * SR; t < (j + 1) * SR; ++t) {
+          const unsigned o = off(t);
+          const unsigned y1 = LN::load(R1, o), y2 = OP == OP_MINLSTM ? LN::load(R2, o) : 0u, yc = LN::load(RC, o);
+#pragma unroll
+          for (int k = 0; k < C; ++k) {
+            float a, bb;
+            coef(y1, y2, yc, k, valid && t < seq, a, bb);
+            bv[k] = fmaf(a, bv[k], bb);
+            av[k] *= a;
+          }
+        }
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      sPA[j][k][lane] = av[k];
+      sPB[j][k][lane] = bv[k];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {  // the part's carry: h0 through the earlier parts' maps, in order
+    float x[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) x[k] = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c + k) : 0.0f;
+    for (int j = 0; j < part; ++j)
+#pragma unroll
+      for (int k = 0; k < C; ++k) x[k] = fmaf(sPA[j][k][lane], x[k], sPB[j][k][lane]);
+#pragma unroll
+    for (int k = 0; k < C; ++k) sH[k][lane] = x[k];
+  }
+  __syncthreads();
+
+  // the coefficients are formed again from the raw values (opaque to the compiler here, so
+  // that it does not keep the first pass's 2 C R coefficients live across the look-back)
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    asm volatile("" : "+v"(r1[j]), "+v"(rc[j]));
+    if (OP == OP_MINLSTM) asm volatile("" : "+v"(r2[j]));
+  }
+  // this wave's carry: the maps of the waves before it applied to the part's carry
+  float h[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) h[k] = sH[k][lane];
+#pragma unroll
+  for (int v0 = 0; v0 < W; v0 += 4) {
+#pragma unroll
+    for (int v = v0; v < v0 + 4; ++v)
+#pragma unroll
+      for (int k = 0; k < C; ++k)
+        if (v < w) h[k] = fmaf(sA[v][k][lane], h[k], sB[v][k][lane]);
+    asm volatile("" ::: "memory");
+  }
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      float a, bb;
+      coef(r1[j], OP == OP_MINLSTM ? r2[j] : 0u, rc[j], k, valid && t0 + j < seq, a, bb);
+      h[k] = fmaf(a, h[k], bb);
+    }
+    LN::store(RO, off(t0 + j), h);
+  }
+}
+
+constexpr int LB_MAX_DEVICES = 64;
+std::mutex g_lb_mu;
+unsigned long long* g_lb_ptr[LB_MAX_DEVICES] = {};
+std::atomic<unsigned> g_lb_epoch{0x6c620000u};
+
+// The device copy of lb_flags for the stream's device (nullptr if it cannot be found).
+unsigned long long* lb_flags_address(hipStream_t s) {
+  int cur = 0, dev = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return nullptr;
+  dev = cur;
+  if (s != nullptr && hipStreamGetDevice(s, &dev) != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= LB_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(g_lb_mu);
+  if (g_lb_ptr[dev] == nullptr) {
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return nullptr;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(lb_flags));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_lb_ptr[dev] = (unsigned long long*)p;
+  }
+  return g_lb_ptr[dev];
+}
+
+int lb_spin_limit() {
+  const char* env = getenv("EDF_LIN_LOOKBACK_SPIN");
+  return env != nullptr ? std::max(0, atoi(env)) : LB_SPIN;
+}
+
+unsigned lb_next_epoch() {
+  unsigned e;
+  do e = ++g_lb_epoch; while (e == 0);
+  return e;
+}
+
+// The look-back scan serves sequences of at least 512 steps whose words fit lb_flags, on a
+// stream that is not capturing; EDF_LIN_LOOKBACK=0 selects the one-workgroup-per-tile kernels.
+template <typename T>
+unsigned long long* lb_plan(hipStream_t s, int bsz, int seq, int hid, int& ntile, int& nparts) {
+  constexpr int C = Lane4<T>::C, SR = LB_W * LB_R;
+  const char* env = getenv("EDF_LIN_LOOKBACK");
+  if (env != nullptr && !strcmp(env, "0")) return nullptr;
+  if (hid % C != 0 || seq < 512) return nullptr;
+  ntile = (hid + 64 * C - 1) / (64 * C);
+  nparts = (seq + SR - 1) / SR;
+  const long words = (long)nparts * bsz * ntile * 2 * C * 64;
+  if (words > (long)LB_WORDS || nparts > LB_MAXP) return nullptr;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (st != hipStreamCaptureStatusNone) return nullptr;
+  return lb_flags_address(s);
+}
+
 inline const char* op_name(int op, bool backward = false) {
   static const char* const names[3][2] = {{"mingru scan", "mingru scan backward"},
                                           {"minlstm scan", "minlstm scan backward"},
@@ -644,6 +943,12 @@ int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
   const T* c = (const T*)cand;
   const T* i = (const T*)h0;
   T* o = (T*)out;
+  int ntile = 0, nparts = 0;
+  if (unsigned long long* flags = lb_plan<T>(s, bsz, seq, hid, ntile, nparts)) {
+    linscan_lb_fwd_kernel<T, OP, LOGITS, LB_R><<<dim3(bsz * ntile, nparts), 64 * LB_W, 0, s>>>(
+        a, b, c, i, o, seq, hid, ntile, flags, lb_next_epoch(), lb_spin_limit());
+    return check_launch(op_name(OP));
+  }
 #define EDF_LIN_LAUNCH(KERNEL, L, W, P, PAIRS)                                                      \
   do {                                                                                            \
     if (needs_pad<L, W, PAIRS>(seq, hid))                                                         \

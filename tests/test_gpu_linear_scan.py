@@ -64,7 +64,7 @@ def _call(name, *args):
     nat.call(name, stream, *ptrs)
 
 
-@pytest.mark.parametrize("shape", [(4, 60, 256), (2, 33, 70)])
+@pytest.mark.parametrize("shape", [(4, 60, 256), (2, 33, 70), (2, 1100, 262)])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_reference_shaped_entry_points(shape, dtype, rng):
     """edf_fused_mingru_scan / _backward and the MinLSTM pair: post-sigmoid gates, explicit h0."""
@@ -116,6 +116,31 @@ def test_mingru_seq1_known_answer():
     assert torch.allclose(gz.cpu(), torch.tensor([[[2.0, -1.0]]]), atol=1e-6)
     assert torch.allclose(gc.cpu(), torch.tensor([[[0.3, 0.7]]]), atol=1e-6)
     assert torch.allclose(gh.cpu(), torch.tensor([[0.7, 0.3]]), atol=1e-6)
+
+
+@pytest.mark.parametrize("spin", [None, "0"])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_lookback_forward_paths(dtype, spin, rng, monkeypatch):
+    """Sequences of at least 512 steps run the look-back forward (parts of 128 steps, each
+    part's carry from the parts before it); with a poll limit of 0 a part that finds no
+    published words at its first look recomputes its carry from the sequence start instead.
+    Every path against the oracle, and against the one-workgroup-per-tile kernels."""
+    from edifice_amd import fused_scan as fs
+    if spin is not None:
+        monkeypatch.setenv("EDF_LIN_LOOKBACK_SPIN", spin)
+    shape = (3, 1100, 262)  # a partial last part and a partial last channel tile
+    announce("lookback_paths", dtype=dtype, spin=spin)
+    g, c = rng.normal(size=shape), rng.normal(size=shape)
+    a = rng.uniform(0.0, 1.0, size=shape)
+    tg, tc, ta = (to_dev(x, dtype) for x in (g, c, a))
+    gr, cr, ar = (rounded(x, dtype) for x in (g, c, a))
+    out = fs.mingru(tg, tc)
+    assert_close(host(out), scans.min_gru_scan(gr, cr), TOL[dtype], "mingru h")
+    lin = fs.linear_scan(ta, tc)
+    assert_close(host(lin), scans.linear_scan(ar, cr), TOL[dtype], "linear h")
+    monkeypatch.setenv("EDF_LIN_LOOKBACK", "0")
+    assert_close(host(out), host(fs.mingru(tg, tc)), TOL[dtype], "mingru paths")
+    assert_close(host(lin), host(fs.linear_scan(ta, tc)), TOL[dtype], "linear paths")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
