@@ -651,7 +651,7 @@ __global__ __launch_bounds__(64 * W) void linscan2_bwd_kernel(const T* __restric
 constexpr int LB_W = 16;                // waves per workgroup
 constexpr int LB_R = 8;                 // steps per wave: parts of 128 steps (768 workgroups at
                                         // the bandwidth row in bf16; two per CU fit)
-constexpr int LB_SPIN = 1 << 14;        // default polls of a part's words before folding them here
+constexpr int LB_SPIN = 1 << 12;        // default polls of a part's words before folding them here
 constexpr int LB_MAXP = 32;             // parts per sequence
 constexpr size_t LB_WORDS = 1u << 20;   // published words per device (8 MiB)
 static __device__ __align__(256) unsigned long long lb_flags[LB_WORDS];
@@ -859,6 +859,241 @@ __global__ __launch_bounds__(64 * LB_W) void linscan_lb_fwd_kernel(const T* __re
   }
 }
 
+// Backward look-back: the reverse scan u_t = a_t (g_t + u_{t+1}) with the same parts, each
+// part's carry (u entering it from the right) from the maps of all later parts.
+template <typename T, int OP, bool LOGITS, int R>
+__global__ __launch_bounds__(64 * LB_W) void linscan_lb_bwd_kernel(
+    const T* __restrict__ g1, const T* __restrict__ g2, const T* __restrict__ cand, const T* __restrict__ h0,
+    const T* __restrict__ fwd, const T* __restrict__ dy, T* __restrict__ d1, T* __restrict__ d2,
+    T* __restrict__ dcand, T* __restrict__ dh0, int seq, int hid, int ntile, unsigned long long* __restrict__ flags,
+    unsigned epoch, int spin_limit) {
+  typedef Lane4<T> LN;
+  constexpr int W = LB_W, C = LN::C, SR = W * R;
+  constexpr unsigned ES = sizeof(T);
+  __shared__ float sA[W][C][64];
+  __shared__ float sB[W][C][64];
+  __shared__ float sU[C][64];
+  __shared__ float sPA[LB_MAXP][C][64];  // the later parts' maps
+  __shared__ float sPB[LB_MAXP][C][64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // the last parts first: workgroups are dispatched in id order, and a part waits for the
+  // parts after it
+  const int bt = blockIdx.x, nbt = gridDim.x, nparts = gridDim.y, part = nparts - 1 - (int)blockIdx.y;
+  const int b = bt / ntile, tile = bt % ntile;
+  const int c = (tile * 64 + lane) * C;
+  const bool valid = c < hid;
+  const long slab = (long)b * seq * hid;
+  const unsigned bytes = (unsigned)((long)seq * hid * ES);
+  const rsrc_t R1 = make_rsrc(g1 + slab, bytes);
+  const rsrc_t R2 = make_rsrc((OP == OP_MINLSTM ? g2 : g1) + slab, bytes);
+  const rsrc_t RC = make_rsrc((OP == OP_LINEAR ? g1 : cand) + slab, bytes);
+  const rsrc_t RH = make_rsrc(fwd + slab, bytes);
+  const rsrc_t RY = make_rsrc(dy + slab, bytes);
+  const rsrc_t W1 = make_rsrc(d1 + slab, bytes);
+  const rsrc_t W2 = make_rsrc((OP == OP_MINLSTM ? d2 : d1) + slab, bytes);
+  const rsrc_t WC = make_rsrc(dcand + slab, bytes);
+  const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
+  auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
+  // h_{t-1}: the forward output one row up; t = 0 wraps below zero, out of range (0), and
+  // takes h0
+  auto offp = [&](int t) -> unsigned { return cb + (unsigned)(t - 1) * rowb; };
+  float hz[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) hz[k] = (valid && h0 != nullptr) ? ld(h0, (long)b * hid + c + k) : 0.0f;
+  // per step and channel: the decay a, dy, and the factors that turn dh_t into each output
+  // gradient (as in linscan_bwd_kernel)
+  auto coef = [&](unsigned x1, unsigned x2, unsigned xc, unsigned xh, unsigned xy, int k, int t, float& a, float& gy,
+                  float& k1, float& k2, float& kc) {
+    const bool ok = valid && t < seq;
+    const float v1 = LN::get(x1, k);
+    const float v2 = OP == OP_MINLSTM ? LN::get(x2, k) : 0.0f;
+    const float cv = OP == OP_LINEAR ? 0.0f : LN::get(xc, k);
+    const float hp = t > 0 ? LN::get(xh, k) : hz[k];
+    gy = LN::get(xy, k);  // 0 outside the sequence
+    if (OP == OP_LINEAR) {
+      a = ok ? v1 : 1.0f;
+      k1 = hp;
+      k2 = 0.0f;
+      kc = 1.0f;
+    } else if (OP == OP_MINGRU) {
+      const float z = LOGITS ? sigmoid_rcp(v1) : v1;
+      a = ok ? 1.0f - z : 1.0f;
+      k1 = LOGITS ? (cv - hp) * (z * (1.0f - z)) : cv - hp;
+      k2 = 0.0f;
+      kc = z;
+    } else {
+      const float f = LOGITS ? sigmoid_rcp(v1) : v1;
+      const float i = LOGITS ? sigmoid_rcp(v2) : v2;
+      const float r = fast_rcp(f + (i + MINLSTM_EPS));
+      const float r2 = r * r;
+      a = ok ? f * r : 1.0f;
+      float c1 = (hp * (i + MINLSTM_EPS) - cv * i) * r2;
+      float c2 = (cv * (f + MINLSTM_EPS) - hp * f) * r2;
+      if (LOGITS) {
+        c1 *= f * (1.0f - f);
+        c2 *= i * (1.0f - i);
+      }
+      k1 = c1;
+      k2 = c2;
+      kc = i * r;
+    }
+  };
+
+  const int t0 = part * SR + w * R;
+  unsigned r1[R], r2[R], rc[R], rh[R], ry[R];
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const unsigned o = off(t0 + j);
+    r1[j] = LN::load(R1, o);
+    if (OP == OP_MINLSTM) r2[j] = LN::load(R2, o);
+    if (OP != OP_LINEAR) rc[j] = LN::load(RC, o);
+    rh[j] = LN::load(RH, offp(t0 + j));
+    ry[j] = LN::load(RY, o);
+  }
+  // this wave's reverse map: u entering its last step from the right -> u leaving its first
+#pragma unroll
+  for (int k = 0; k < C; ++k) {
+    float A = 1.0f, B = 0.0f;
+#pragma unroll
+    for (int j = R - 1; j >= 0; --j) {
+      float a, gy, k1, k2, kc;
+      coef(r1[j], OP == OP_MINLSTM ? r2[j] : 0u, OP != OP_LINEAR ? rc[j] : 0u, rh[j], ry[j], k, t0 + j, a, gy, k1, k2,
+           kc);
+      B = a * (gy + B);
+      A *= a;
+    }
+    sA[w][k][lane] = A;
+    sB[w][k][lane] = B;
+  }
+  __syncthreads();
+
+  auto words = [&](int pt) { return flags + (long)(pt * nbt + bt) * 2 * C * 64 + lane; };
+  if (w == 0 && part > 0) {  // the part's map, waves in reverse order, published for the parts before it
+    float Ag[C], Bg[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      Ag[k] = 1.0f;
+      Bg[k] = 0.0f;
+    }
+#pragma unroll
+    for (int v0 = W - 1; v0 >= 0; v0 -= 4) {
+#pragma unroll
+      for (int v = v0; v > v0 - 4; --v)
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          Bg[k] = fmaf(sA[v][k][lane], Bg[k], sB[v][k][lane]);
+          Ag[k] *= sA[v][k][lane];
+        }
+      asm volatile("" ::: "memory");
+    }
+    unsigned long long* mine = words(part);
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      lb_put(mine + k * 64, epoch, Ag[k]);
+      lb_put(mine + (C + k) * 64, epoch, Bg[k]);
+    }
+  }
+  // the maps of the later parts, wave v fetching parts part + 1 + v, part + 17 + v, ...
+  for (int j = part + 1 + w; j < nparts; j += W) {
+    unsigned long long* pj = words(j);
+    float av[C], bv[C];
+    for (int spins = 0;; ++spins) {
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        ok = lb_get(pj + k * 64, epoch, av[k]) && ok;
+        ok = lb_get(pj + (C + k) * 64, epoch, bv[k]) && ok;
+      }
+      if (__all(ok)) break;
+      if (spins >= spin_limit) {
+        // no words from part j: its reverse map folded here from its rows
+#pragma unroll
+        for (int k = 0; k < C; ++k) {
+          av[k] = 1.0f;
+          bv[k] = 0.0f;
+        }
+#pragma unroll 1
+        for (int t = (j + 1) * SR - 1; t >= j * SR; --t) {
+          const unsigned o = off(t);
+          const unsigned y1 = LN::load(R1, o), y2 = OP == OP_MINLSTM ? LN::load(R2, o) : 0u;
+          const unsigned yc = OP != OP_LINEAR ? LN::load(RC, o) : 0u, yh = LN::load(RH, offp(t)), yy = LN::load(RY, o);
+#pragma unroll
+          for (int k = 0; k < C; ++k) {
+            float a, gy, k1, k2, kc;
+            coef(y1, y2, yc, yh, yy, k, t, a, gy, k1, k2, kc);
+            bv[k] = a * (gy + bv[k]);
+            av[k] *= a;
+          }
+        }
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      sPA[j - part - 1][k][lane] = av[k];
+      sPB[j - part - 1][k][lane] = bv[k];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {  // the part's carry: 0 at the sequence end through the later parts' maps
+    float x[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) x[k] = 0.0f;
+    for (int j = nparts - 1; j > part; --j)
+#pragma unroll
+      for (int k = 0; k < C; ++k) x[k] = fmaf(sPA[j - part - 1][k][lane], x[k], sPB[j - part - 1][k][lane]);
+#pragma unroll
+    for (int k = 0; k < C; ++k) sU[k][lane] = x[k];
+  }
+  __syncthreads();
+
+  // coefficients formed again from the raw values (opaque here, as in the forward)
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    asm volatile("" : "+v"(r1[j]), "+v"(rh[j]), "+v"(ry[j]));
+    if (OP == OP_MINLSTM) asm volatile("" : "+v"(r2[j]));
+    if (OP != OP_LINEAR) asm volatile("" : "+v"(rc[j]));
+  }
+  // this wave's carry: the maps of the waves after it applied to the part's carry
+  float u[C];
+#pragma unroll
+  for (int k = 0; k < C; ++k) u[k] = sU[k][lane];
+#pragma unroll
+  for (int v0 = W - 1; v0 >= 0; v0 -= 4) {
+#pragma unroll
+    for (int v = v0; v > v0 - 4; --v)
+#pragma unroll
+      for (int k = 0; k < C; ++k)
+        if (v > w) u[k] = fmaf(sA[v][k][lane], u[k], sB[v][k][lane]);
+    asm volatile("" ::: "memory");
+  }
+#pragma unroll
+  for (int j = R - 1; j >= 0; --j) {
+    float o1[C], o2[C], oc[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      float a, gy, k1, k2, kc;
+      coef(r1[j], OP == OP_MINLSTM ? r2[j] : 0u, OP != OP_LINEAR ? rc[j] : 0u, rh[j], ry[j], k, t0 + j, a, gy, k1, k2,
+           kc);
+      const float dh = gy + u[k];
+      u[k] = a * dh;
+      o1[k] = dh * k1;
+      o2[k] = dh * k2;
+      oc[k] = dh * kc;
+    }
+    const unsigned o = off(t0 + j);
+    LN::store(W1, o, o1);
+    if (OP == OP_MINLSTM) LN::store(W2, o, o2);
+    LN::store(WC, o, oc);
+  }
+  if (valid && part == 0 && w == 0 && dh0 != nullptr) {
+#pragma unroll
+    for (int k = 0; k < C; ++k) st(dh0, (long)b * hid + c + k, u[k]);
+  }
+}
+
 constexpr int LB_MAX_DEVICES = 64;
 std::mutex g_lb_mu;
 unsigned long long* g_lb_ptr[LB_MAX_DEVICES] = {};
@@ -899,9 +1134,9 @@ unsigned lb_next_epoch() {
 
 // The look-back scan serves sequences of at least 512 steps whose words fit lb_flags, on a
 // stream that is not capturing; EDF_LIN_LOOKBACK=0 selects the one-workgroup-per-tile kernels.
-template <typename T>
+template <typename T, int R>
 unsigned long long* lb_plan(hipStream_t s, int bsz, int seq, int hid, int& ntile, int& nparts) {
-  constexpr int C = Lane4<T>::C, SR = LB_W * LB_R;
+  constexpr int C = Lane4<T>::C, SR = LB_W * R;
   const char* env = getenv("EDF_LIN_LOOKBACK");
   if (env != nullptr && !strcmp(env, "0")) return nullptr;
   if (hid % C != 0 || seq < 512) return nullptr;
@@ -944,10 +1179,14 @@ int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
   const T* i = (const T*)h0;
   T* o = (T*)out;
   int ntile = 0, nparts = 0;
-  if (unsigned long long* flags = lb_plan<T>(s, bsz, seq, hid, ntile, nparts)) {
-    linscan_lb_fwd_kernel<T, OP, LOGITS, LB_R><<<dim3(bsz * ntile, nparts), 64 * LB_W, 0, s>>>(
-        a, b, c, i, o, seq, hid, ntile, flags, lb_next_epoch(), lb_spin_limit());
-    return check_launch(op_name(OP));
+  // the forward look-back for f32 and the bf16 linear scan; the bf16 MinGRU / MinLSTM forward,
+  // which forms its gates' sigmoids twice there, measured no faster than the per-tile kernel
+  if constexpr (!std::is_same<T, bf16>::value || OP == OP_LINEAR) {
+    if (unsigned long long* flags = lb_plan<T, LB_R>(s, bsz, seq, hid, ntile, nparts)) {
+      linscan_lb_fwd_kernel<T, OP, LOGITS, LB_R><<<dim3(bsz * ntile, nparts), 64 * LB_W, 0, s>>>(
+          a, b, c, i, o, seq, hid, ntile, flags, lb_next_epoch(), lb_spin_limit());
+      return check_launch(op_name(OP));
+    }
   }
 #define EDF_LIN_LAUNCH(KERNEL, L, W, P, PAIRS)                                                      \
   do {                                                                                            \
@@ -983,6 +1222,12 @@ int launch_bwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
   T* o2 = (T*)d2;
   T* oc = (T*)dcand;
   T* oh = (T*)dh0;
+  int ntile = 0, nparts = 0;
+  if (unsigned long long* flags = lb_plan<T, LB_R>(s, bsz, seq, hid, ntile, nparts)) {
+    linscan_lb_bwd_kernel<T, OP, LOGITS, LB_R><<<dim3(bsz * ntile, nparts), 64 * LB_W, 0, s>>>(
+        a, b, c, i, f, y, o1, o2, oc, oh, seq, hid, ntile, flags, lb_next_epoch(), lb_spin_limit());
+    return check_launch(op_name(OP, true));
+  }
 #define EDF_LIN_LAUNCH(KERNEL, L, W, P, PAIRS)                                                                 \
   do {                                                                                                       \
     if (needs_pad<L, W, PAIRS>(seq, hid))                                                                    \

@@ -120,27 +120,43 @@ def test_mingru_seq1_known_answer():
 
 @pytest.mark.parametrize("spin", [None, "0"])
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_lookback_forward_paths(dtype, spin, rng, monkeypatch):
-    """Sequences of at least 512 steps run the look-back forward (parts of 128 steps, each
-    part's carry from the parts before it); with a poll limit of 0 a part that finds no
-    published words at its first look recomputes its carry from the sequence start instead.
-    Every path against the oracle, and against the one-workgroup-per-tile kernels."""
+def test_lookback_paths(dtype, spin, rng, monkeypatch):
+    """Sequences of at least 512 steps run the look-back scans (parts of 128 steps forward, 64
+    backward, each part's carry from the maps of the parts before / after it); with a poll
+    limit of 0 a part whose neighbours' maps are not published at the first look folds them
+    from their rows instead.  Every path against the oracle, and against the
+    one-workgroup-per-tile kernels (EDF_LIN_LOOKBACK=0)."""
     from edifice_amd import fused_scan as fs
     if spin is not None:
         monkeypatch.setenv("EDF_LIN_LOOKBACK_SPIN", spin)
     shape = (3, 1100, 262)  # a partial last part and a partial last channel tile
     announce("lookback_paths", dtype=dtype, spin=spin)
-    g, c = rng.normal(size=shape), rng.normal(size=shape)
+    g, c, dy = (rng.normal(size=shape) for _ in range(3))
     a = rng.uniform(0.0, 1.0, size=shape)
-    tg, tc, ta = (to_dev(x, dtype) for x in (g, c, a))
-    gr, cr, ar = (rounded(x, dtype) for x in (g, c, a))
-    out = fs.mingru(tg, tc)
-    assert_close(host(out), scans.min_gru_scan(gr, cr), TOL[dtype], "mingru h")
-    lin = fs.linear_scan(ta, tc)
-    assert_close(host(lin), scans.linear_scan(ar, cr), TOL[dtype], "linear h")
+    gr, cr, dyr, ar = (rounded(x, dtype) for x in (g, c, dy, a))
+
+    def run():
+        tg, tc, ta, tb = (to_dev(x, dtype).requires_grad_() for x in (g, c, a, c))
+        h = fs.mingru(tg, tc)
+        h.backward(to_dev(dy, dtype))
+        lin = fs.linear_scan(ta, tb)
+        lin.backward(to_dev(dy, dtype))
+        return [host(x) for x in (h, tg.grad, tc.grad, lin, ta.grad, tb.grad)]
+
+    got = run()
+    tol = TOL[dtype]
+    assert_close(got[0], scans.min_gru_scan(gr, cr), tol, "mingru h")
+    eg, ec = scans.min_gru_scan_backward(gr, cr, dyr)
+    assert_close(got[1], eg, tol, "mingru d gate")
+    assert_close(got[2], ec, tol, "mingru d cand")
+    lin = scans.linear_scan(ar, cr)
+    assert_close(got[3], lin, tol, "linear h")
+    da, db, _ = scans.linear_scan_backward(ar, None, rounded(got[3], dtype), dyr)
+    assert_close(got[4], da, tol, "linear da")
+    assert_close(got[5], db, tol, "linear db")
     monkeypatch.setenv("EDF_LIN_LOOKBACK", "0")
-    assert_close(host(out), host(fs.mingru(tg, tc)), TOL[dtype], "mingru paths")
-    assert_close(host(lin), host(fs.linear_scan(ta, tc)), TOL[dtype], "linear paths")
+    for x, y, name in zip(got, run(), ("h", "d gate", "d cand", "linear h", "da", "db")):
+        assert_close(x, y, tol, f"paths {name}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
