@@ -678,6 +678,7 @@ template <> struct Lane4<float> {
   static constexpr int C = 1;
   static EDF_DEVICE unsigned load(rsrc_t r, unsigned off) { return bload<float>(r, off); }
   static EDF_DEVICE float get(unsigned v, int) { return bits_f32(v); }
+  static EDF_DEVICE unsigned pack(float x0, float) { return __builtin_bit_cast(unsigned, x0); }
   static EDF_DEVICE void store(rsrc_t r, unsigned off, const float* x) { bstore<float>(r, off, x[0]); }
 };
 
@@ -710,10 +711,17 @@ __global__ __launch_bounds__(64 * LB_W) void linscan_lb_fwd_kernel(const T* __re
   const rsrc_t RO = make_rsrc(out + slab, bytes);
   const unsigned cb = valid ? (unsigned)c * ES : OOB_OFF, rowb = (unsigned)hid * ES;
   auto off = [&](int t) -> unsigned { return cb + (unsigned)t * rowb; };
-  // coefficients of channel k of a row from its raw values; steps past the sequence and
-  // channels past hid are identity maps
+  // gate logits -> gates, in place (f32: exactly; the gated bf16 forwards do not run here), so
+  // that both passes over the rows and a fold of another part's rows use one sigmoid per gate
+  static_assert(!LOGITS || std::is_same<T, float>::value, "gated forwards of bf16 pairs use the per-tile kernel");
+  auto gate = [&](unsigned x) -> unsigned {
+    if constexpr (LOGITS) return LN::pack(sigmoid_rcp(LN::get(x, 0)), 0.0f);
+    else return x;
+  };
+  // coefficients of channel k of a row from its gates; steps past the sequence and channels
+  // past hid are identity maps
   auto coef = [&](unsigned x1, unsigned x2, unsigned xc, int k, bool ok, float& a, float& bb) {
-    Step<OP, LOGITS> st;
+    Step<OP, false> st;
     st.make(LN::get(x1, k), OP == OP_MINLSTM ? LN::get(x2, k) : 0.0f, LN::get(xc, k));
     a = ok ? st.a : 1.0f;
     bb = ok ? st.b : 0.0f;
@@ -728,18 +736,30 @@ __global__ __launch_bounds__(64 * LB_W) void linscan_lb_fwd_kernel(const T* __re
     if (OP == OP_MINLSTM) r2[j] = LN::load(R2, o);
     rc[j] = LN::load(RC, o);
   }
+  {
+    float A[C], B[C];
 #pragma unroll
-  for (int k = 0; k < C; ++k) {
-    float A = 1.0f, B = 0.0f;
-#pragma unroll
-    for (int j = 0; j < R; ++j) {
-      float a, bb;
-      coef(r1[j], OP == OP_MINLSTM ? r2[j] : 0u, rc[j], k, valid && t0 + j < seq, a, bb);
-      B = fmaf(a, B, bb);
-      A *= a;
+    for (int k = 0; k < C; ++k) {
+      A[k] = 1.0f;
+      B[k] = 0.0f;
     }
-    sA[w][k][lane] = A;
-    sB[w][k][lane] = B;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {  // row by row: each row's gates formed as it is folded
+      r1[j] = gate(r1[j]);
+      if (OP == OP_MINLSTM) r2[j] = gate(r2[j]);
+#pragma unroll
+      for (int k = 0; k < C; ++k) {
+        float a, bb;
+        coef(r1[j], OP == OP_MINLSTM ? r2[j] : 0u, rc[j], k, valid && t0 + j < seq, a, bb);
+        B[k] = fmaf(a, B[k], bb);
+        A[k] *= a;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+      sA[w][k][lane] = A[k];
+      sB[w][k][lane] = B[k];
+    }
   }
   __syncthreads();
 
@@ -795,7 +815,8 @@ __global__ __launch_bounds__(64 * LB_W) void linscan_lb_fwd_kernel(const T* __re
 #pragma unroll 1
         for (int t = j * SR; t < (j + 1) * SR; ++t) {
           const unsigned o = off(t);
-          const unsigned y1 = LN::load(R1, o), y2 = OP == OP_MINLSTM ? LN::load(R2, o) : 0u, yc = LN::load(RC, o);
+          const unsigned y1 = gate(LN::load(R1, o)), y2 = OP == OP_MINLSTM ? gate(LN::load(R2, o)) : 0u;
+          const unsigned yc = LN::load(RC, o);
 #pragma unroll
           for (int k = 0; k < C; ++k) {
             float a, bb;
@@ -1179,8 +1200,10 @@ int launch_fwd(hipStream_t s, const void* g1, const void* g2, const void* cand, 
   const T* i = (const T*)h0;
   T* o = (T*)out;
   int ntile = 0, nparts = 0;
-  // the forward look-back for f32 and the bf16 linear scan; the bf16 MinGRU / MinLSTM forward,
-  // which forms its gates' sigmoids twice there, measured no faster than the per-tile kernel
+  // the forward look-back for f32 and the bf16 linear scan.  The bf16 MinGRU / MinLSTM forward
+  // keeps the per-tile kernel: it would form its gates' sigmoids a second time after the wait
+  // (measured no faster), and gates kept in place as bf16 pairs lose too much (3.6e-2
+  // element-wise against the oracle)
   if constexpr (!std::is_same<T, bf16>::value || OP == OP_LINEAR) {
     if (unsigned long long* flags = lb_plan<T, LB_R>(s, bsz, seq, hid, ntile, nparts)) {
       linscan_lb_fwd_kernel<T, OP, LOGITS, LB_R><<<dim3(bsz * ntile, nparts), 64 * LB_W, 0, s>>>(
