@@ -296,13 +296,23 @@ __global__ __launch_bounds__(256) void dp_finish_kernel(const DPArgs p, long nbt
 // S_n = S_p + be kn^T, dtot = dS + q dO^T on a token's last sub-step):
 //   dq = S_n dO (token's last sub-step), ds_k = dtot kn, dv = beta ds_k, dbeta = err . ds_k,
 //   dkn = dtot^T be - S_p^T (beta ds_k), dS <- dtot - beta ds_k kn^T, err = v - S_p kn, be = beta err.
+//
+// The sums over the block's rows (the key-gradient terms, one per column, and the per-head
+// dbeta term, one per row) leave the sub-steps' dependency chain as in the delta rule's
+// per-step backward: each wave adds its four rows' terms in registers (rows4_scatter) into a
+// per-sub-step slot of an LDS tile, and every FS sub-steps one barrier pair adds the four
+// waves' slots in wave order and stores the partials.
 template <typename TT, int DP>
 __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
   constexpr int NC = DP / 16;
+  constexpr int FS = 8;                 // sub-steps per flush of the row sums
+  constexpr int NG = (NC + 3) / 4;      // rows4_scatter groups of the lane's NC column terms
+  static_assert(DPR_CK % FS == 0, "flushes split the chunk");
   __shared__ DPStage<DP> sm;
-  __shared__ float redk[DPR_RB][row16_stride(DP)];  // this step's per-row key-gradient terms
-  __shared__ float redb[DPR_RB];
+  __shared__ float wsum[FS][4][NG][64];  // [slot][wave][group][lane]: four-row sums
+  __shared__ float redb[FS][DPR_RB];     // [slot][row]: dbeta terms
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  const int w = tid >> 6, lane = tid & 63;
   const long bh = blockIdx.x;
   const int rb = blockIdx.y, i = rb * DPR_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
@@ -346,38 +356,42 @@ __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
       sk = row16_sum(sk);
       const float err = sm.v[tt][tr] - r;
       const float be = bi * err, bdk = bi * sk;
-      float pq = 0.0f;
+      float pq = 0.0f, vals[4 * NG];
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const float kj = sm.k[tt][tc + 16 * c];
         pq = fmaf(fmaf(be, kj, Sl[tt][c]), sm.g[tt][tc + 16 * c], pq);
-        redk[tr][tc + 16 * c] = fmaf(dtot[c], be, -Sl[tt][c] * bdk);
+        vals[c] = fmaf(dtot[c], be, -Sl[tt][c] * bdk);
         dS[c] = fmaf(-bdk, kj, dtot[c]);
       }
+#pragma unroll
+      for (int k = NC; k < 4 * NG; ++k) vals[k] = 0.0f;
+      const int slot = tt % FS;
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+        wsum[slot][w][g][lane] = rows4_scatter(vals[4 * g], vals[4 * g + 1], vals[4 * g + 2], vals[4 * g + 3]);
       pq = row16_sum(pq);
-      if (tc == 0) redb[tr] = i < p.d ? err * sk : 0.0f;
+      if (tc == 0) redb[slot][tr] = i < p.d ? err * sk : 0.0f;
       if (s < p.TS && tc == 0 && i < p.d) {
         st((TT*)p.dv, (((long)b * p.TS + s) * p.H + h) * p.d + i, bdk);
         if (cl.at(tt)) st((TT*)p.dq, (((long)b * p.T + cl.tok(tt)) * p.H + h) * p.d + i, pq);
       }
-      // the block's sums over its 16 rows, in row order, through LDS
-      __syncthreads();
-      if (s < p.TS) {
-        const long bts = ((long)b * p.TS + s) * p.H + h;
-        for (int j = tid; j < DP; j += 256) {
+      if (slot == 0) {  // sub-steps s .. s + FS - 1 are in the slots: sum the waves, store
+        __syncthreads();
+        for (int e = tid; e < FS * DP; e += 256) {
+          const int sl = e / DP, j = e % DP;
+          const int g = (j >> 4) >> 2, src = 16 * rows4_item((j >> 4) & 3) + (j & 15);
+          const float acc = ((wsum[sl][0][g][src] + wsum[sl][1][g][src]) + wsum[sl][2][g][src]) + wsum[sl][3][g][src];
+          if (s + sl < p.TS && j < p.d) p.part_k[((long)rb * nbts + ((long)b * p.TS + s + sl) * p.H + h) * p.d + j] = acc;
+        }
+        if (tid < FS) {
           float acc = 0.0f;
 #pragma unroll
-          for (int m = 0; m < DPR_RB; ++m) acc += redk[m][j];
-          if (j < p.d) p.part_k[((long)rb * nbts + bts) * p.d + j] = acc;
+          for (int m = 0; m < DPR_RB; ++m) acc += redb[tid][m];
+          if (s + tid < p.TS) p.part_b[(long)rb * nbts + ((long)b * p.TS + s + tid) * p.H + h] = acc;
         }
-        if (tid == 255) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int m = 0; m < DPR_RB; ++m) acc += redb[m];
-          p.part_b[(long)rb * nbts + bts] = acc;
-        }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
 }
