@@ -108,11 +108,12 @@ EDF_DEVICE void store_chunk(Stage<DP>& sm, const StageRegs<TT, DP>& R, const DRA
   sm.a[tt][ii] = av;
 }
 
-// One forward step of the lane's row segment: S = a S + beta (v - a S k) k^T.
-template <int DP>
+// One forward step of the lane's row segment: S = a S + beta (v - a S k) k^T.  DECAY = false
+// (DeltaNet: no alpha, a = 1) compiles the decay multiplies out.
+template <int DP, bool DECAY>
 EDF_DEVICE void fwd_step(float (&S)[DP / 16], const Stage<DP>& sm, int tt, int tr, int tc) {
   constexpr int NC = DP / 16;
-  const float at = sm.a[tt][tr];
+  const float at = DECAY ? sm.a[tt][tr] : 1.0f;
   float r = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) r = fmaf(S[c], sm.k[tt][tc + 16 * c], r);
@@ -122,7 +123,7 @@ EDF_DEVICE void fwd_step(float (&S)[DP / 16], const Stage<DP>& sm, int tt, int t
   for (int c = 0; c < NC; ++c) S[c] = fmaf(e, sm.k[tt][tc + 16 * c], at * S[c]);
 }
 
-template <typename TT, int DP>
+template <typename TT, int DP, bool DECAY>
 __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
   constexpr int NC = DP / 16;
   __shared__ Stage<DP> sms[2];
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
     // the next step's LDS reads can be issued under the current step's arithmetic
 #pragma unroll
     for (int tt = 0; tt < CK; ++tt) {
-      fwd_step<DP>(S, sm, tt, tr, tc);
+      fwd_step<DP, DECAY>(S, sm, tt, tr, tc);
       if (p.out != nullptr) {  // o_i = sum_j S[i][j] q_j
         float o = 0.0f;
 #pragma unroll
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
 // rows in registers (rows4_scatter: the lane of row r keeps the column sums of one value
 // in four) into a per-step slot of an LDS buffer, and every FS steps one barrier pair adds
 // the four waves' slots (in wave order) and stores the partials of those steps.
-template <typename TT, int DP>
+template <typename TT, int DP, bool DECAY>
 __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
   constexpr int NC = DP / 16;
   constexpr int FS = 8;                 // steps per flush of the row sums
@@ -226,13 +227,13 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
       for (int tt = 0; tt < CK; ++tt) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) Sl[tt][c] = S[c];
-        fwd_step<DP>(S, sm, tt, tr, tc);
+        fwd_step<DP, DECAY>(S, sm, tt, tr, tc);
       }
     }
 #pragma unroll
     for (int tt = CK - 1; tt >= 0; --tt) {
       const int t = t0 + tt;
-      const float at = sm.a[tt][tr];
+      const float at = DECAY ? sm.a[tt][tr] : 1.0f;
       const float goi = sm.go[tt][tr], bi = sm.b[tt][tr];
       float r = 0.0f, sk = 0.0f;
 #pragma unroll
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
         pq[c] = snew * goi;
         pk[c] = fmaf(dtot, be, -sg * bdk);
         const float ddec = fmaf(-bdk, kj, dtot);
-        pa = fmaf(ddec, Sl[tt][c], pa);
+        if (DECAY) pa = fmaf(ddec, Sl[tt][c], pa);  // dalpha: no decay, no gradient
         dS[c] = at * ddec;
       }
       const bool live = t < p.T;
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
 #pragma unroll
       for (int g = 0; g < NG; ++g)
         wsum[slot][w][g][lane] = rows4_scatter(vals[4 * g], vals[4 * g + 1], vals[4 * g + 2], vals[4 * g + 3]);
-      pa = row16_sum(pa);
+      if (DECAY) pa = row16_sum(pa);
       if (tc == 0) {
         rsum[slot][0][tr] = pa;
         rsum[slot][1][tr] = i < p.d ? err * sk : 0.0f;
@@ -358,10 +359,14 @@ int launch_seq(hipStream_t s, const DRArgs& a, bool bwd, int BH) {
 #define EDF_DR_LAUNCH(DP)                                              \
   do {                                                                 \
     const dim3 grid(BH, DP / RB);                                      \
-    if (bwd)                                                           \
-      dr_seq_bwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);               \
+    if (bwd && a.alpha != nullptr)                                     \
+      dr_seq_bwd_kernel<TT, DP, true><<<grid, 256, 0, s>>>(a);         \
+    else if (bwd)                                                      \
+      dr_seq_bwd_kernel<TT, DP, false><<<grid, 256, 0, s>>>(a);        \
+    else if (a.alpha != nullptr)                                       \
+      dr_seq_fwd_kernel<TT, DP, true><<<grid, 256, 0, s>>>(a);         \
     else                                                               \
-      dr_seq_fwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);               \
+      dr_seq_fwd_kernel<TT, DP, false><<<grid, 256, 0, s>>>(a);        \
   } while (0)
   if (d <= 16)
     EDF_DR_LAUNCH(16);
