@@ -59,6 +59,9 @@ SIGNATURES = {
     "edf_causal_conv1d_silu_backward": (I, [P, P, I, P, P, P, P, P, P, P, S, I, I, I, I, I]),
     "edf_cross_entropy": (I, [P, P, P, P, P, I, I, I]),
     "edf_cross_entropy_backward": (I, [P, P, P, P, P, F, P, I, I, I]),
+    "edf_layer_norm": (I, [P, P, P, P, P, P, P, I, I, F, I, I]),
+    "edf_layer_norm_backward_workspace_bytes": (S, [I, I]),
+    "edf_layer_norm_backward": (I, [P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
     "edf_laser_attention_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_laser_attention": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_laser_attention_backward_workspace_bytes": (S, [I, I, I, I, I]),

@@ -46,6 +46,15 @@ def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:
     return t.reshape(bsz, seq, num_heads, hid // num_heads).contiguous()
 
 
+class LayerNorm(nn.LayerNorm):
+    """nn.LayerNorm over the last dimension (same parameters and state-dict names) run by the
+    HIP layer norm, ``fs.layer_norm``: Axon.layer_norm of the reference blocks
+    (common.ex:224, delta_net.ex:159,199, model_builder.ex:111,165)."""
+
+    def forward(self, x):
+        return fs.layer_norm(x, self.weight, self.bias, self.eps)
+
+
 def _l2norm_keys(k: torch.Tensor) -> torch.Tensor:
     return k / torch.sqrt((k * k).sum(-1, keepdim=True) + KEY_NORM_EPS)
 
@@ -56,7 +65,7 @@ class MinGRULayer(nn.Module):
 
     def __init__(self, hidden_size: int):
         super().__init__()
-        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.gate = nn.Linear(hidden_size, hidden_size)
         self.candidate = nn.Linear(hidden_size, hidden_size)
 
@@ -72,7 +81,7 @@ class MinLSTMLayer(nn.Module):
 
     def __init__(self, hidden_size: int):
         super().__init__()
-        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.forget = nn.Linear(hidden_size, hidden_size)
         self.input = nn.Linear(hidden_size, hidden_size)
         self.candidate = nn.Linear(hidden_size, hidden_size)
@@ -96,7 +105,7 @@ class MambaBlock(nn.Module):
         inner = hidden_size * expand_factor
         dt_rank = max(hidden_size // 16, 1)  # common.ex:221
         self.inner, self.state_size = inner, state_size
-        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.in_proj = nn.Linear(hidden_size, 2 * inner)
         self.dw_conv = nn.Conv1d(inner, inner, conv_size, padding=conv_size - 1, groups=inner)
         self.bc_proj = nn.Linear(inner, 2 * state_size)
@@ -128,7 +137,7 @@ class DeltaNetLayer(nn.Module):
     def __init__(self, hidden_size: int, num_heads: int):
         super().__init__()
         self.hidden, self.num_heads = hidden_size, num_heads
-        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.qkvb_proj = nn.Linear(hidden_size, 4 * hidden_size)
         self.out_proj = nn.Linear(hidden_size, hidden_size)
 
@@ -149,7 +158,7 @@ class GatedDeltaNetLayer(nn.Module):
     def __init__(self, hidden_size: int, num_heads: int, use_short_conv: bool = True, conv_size: int = 4):
         super().__init__()
         self.hidden, self.num_heads = hidden_size, num_heads
-        self.norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.short_conv = (nn.Conv1d(hidden_size, hidden_size, conv_size, padding=conv_size - 1,
                                      groups=hidden_size) if use_short_conv else None)
         self.qkvbag_proj = nn.Linear(hidden_size, 6 * hidden_size)
@@ -199,9 +208,9 @@ class GQABlock(nn.Module):
 
     def __init__(self, hidden_size: int, num_heads: int, num_kv_heads: int, ffn_mult: int = 4):
         super().__init__()
-        self.attn_norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.attn_norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.attn = GQAttention(hidden_size, num_heads, num_kv_heads)
-        self.ffn_norm = nn.LayerNorm(hidden_size, eps=LN_EPS)
+        self.ffn_norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.ffn_up = nn.Linear(hidden_size, ffn_mult * hidden_size)
         self.ffn_down = nn.Linear(ffn_mult * hidden_size, hidden_size)
 
@@ -258,22 +267,22 @@ def build(name: str, *, embed_size: int, hidden_size: int | None = None, num_lay
     proj = nn.Linear(embed_size, hidden) if hidden != embed_size else None
     if name == "min_gru":
         return SequenceModel("layers", [MinGRULayer(hidden) for _ in range(num_layers)], proj,
-                             nn.LayerNorm(hidden, eps=LN_EPS))
+                             LayerNorm(hidden, eps=LN_EPS))
     if name == "min_lstm":  # min_lstm.ex:113-162 (the unfused layer stack)
         return SequenceModel("layers", [MinLSTMLayer(hidden) for _ in range(num_layers)], proj,
-                             nn.LayerNorm(hidden, eps=LN_EPS))
+                             LayerNorm(hidden, eps=LN_EPS))
     if name == "delta_net":
         return SequenceModel("layers", [DeltaNetLayer(hidden, num_heads) for _ in range(num_layers)], proj,
-                             nn.LayerNorm(hidden, eps=LN_EPS))
+                             LayerNorm(hidden, eps=LN_EPS))
     if name == "gated_delta_net":
         return SequenceModel("layers", [GatedDeltaNetLayer(hidden, num_heads, use_short_conv, conv_size)
-                                        for _ in range(num_layers)], proj, nn.LayerNorm(hidden, eps=LN_EPS))
+                                        for _ in range(num_layers)], proj, LayerNorm(hidden, eps=LN_EPS))
     if name == "mamba":
         return SequenceModel("blocks", [MambaBlock(hidden, state_size, expand_factor, conv_size)
                                         for _ in range(num_layers)], proj, None, residual=True)
     if name == "gqa":
         return SequenceModel("blocks", [GQABlock(hidden, num_heads, num_kv_heads or num_heads)
-                                        for _ in range(num_layers)], proj, nn.LayerNorm(hidden, eps=LN_EPS))
+                                        for _ in range(num_layers)], proj, LayerNorm(hidden, eps=LN_EPS))
     raise ValueError(f"unknown block family {name!r}")
 
 
@@ -291,7 +300,7 @@ class HybridDecoder(nn.Module):
                                    for _ in range(mamba_layers))
         self.delta = nn.ModuleList(DeltaNetLayer(embed_size, num_heads) for _ in range(delta_layers))
         self.attn = nn.ModuleList(GQABlock(embed_size, num_heads, num_heads) for _ in range(attn_layers))
-        self.final_norm = nn.LayerNorm(embed_size, eps=LN_EPS)
+        self.final_norm = LayerNorm(embed_size, eps=LN_EPS)
         self.lm_head = nn.Linear(embed_size, vocab_size, bias=False)
 
     def forward(self, tokens: torch.Tensor) -> torch.Tensor:

@@ -395,6 +395,60 @@ def cross_entropy(logits: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# Layer normalisation (block callers' pre-norms and final norms)
+# ---------------------------------------------------------------------------
+
+class _LayerNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps):
+        x, weight, bias = _c(x), _c(weight), _c(bias)
+        _dev(x, weight, bias)
+        cols = x.shape[-1]
+        rows = x.numel() // max(cols, 1)
+        for name, t in (("weight", weight), ("bias", bias)):
+            if t is not None:
+                _shape(name, t, (cols,))
+        if weight is not None and bias is not None:
+            _same(weight, bias)
+        pt = weight if weight is not None else bias
+        y = torch.empty_like(x)
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+        nat.call("edf_layer_norm", _stream(), _p(x), _p(weight), _p(bias), _p(y), _p(mean), _p(rstd), rows, cols,
+                 float(eps), dtype_flag(x), dtype_flag(pt) if pt is not None else dtype_flag(x))
+        ctx.save_for_backward(x, weight, mean, rstd)
+        ctx.has_bias = bias is not None
+        ctx.pdtype = pt.dtype if pt is not None else x.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight, mean, rstd = ctx.saved_tensors
+        cols = x.shape[-1]
+        rows = x.numel() // max(cols, 1)
+        dy = dy.contiguous().to(x.dtype)
+        dx = torch.empty_like(x)
+        dw = torch.empty(cols, dtype=ctx.pdtype, device=x.device) if weight is not None else None
+        db = torch.empty(cols, dtype=ctx.pdtype, device=x.device) if ctx.has_bias else None
+        wsb = nat.query("edf_layer_norm_backward_workspace_bytes", rows, cols)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+        pflag = F32 if ctx.pdtype == torch.float32 else BF16
+        nat.call("edf_layer_norm_backward", _stream(), _p(x), _p(weight), _p(mean), _p(rstd), _p(dy), _p(dx),
+                 _p(dw), _p(db), _p(ws), wsb, rows, cols, dtype_flag(x), pflag)
+        return dx, dw, db, None
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor = None, bias: torch.Tensor = None,
+               eps: float = 1e-5) -> torch.Tensor:
+    """Layer normalisation over the last dimension, ``F.layer_norm(x, (C,), weight, bias, eps)``
+    (biased variance, eps inside the square root): the block models' pre-norms and final norms
+    (Axon.layer_norm, e.g. common.ex:224, delta_net.ex:159,199, model_builder.ex:111,165).
+    x float32 or bfloat16 with C <= 8192 columns; weight / bias [C] (float32 or bfloat16, one
+    dtype) or None; statistics and arithmetic in float32."""
+    return _LayerNorm.apply(x, weight, bias, eps)
+
+
+# ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------
 

@@ -572,6 +572,23 @@ int edf_cross_entropy_backward(void* stream, const void* logits, const int64_t* 
                                const float* grad_loss, float inv_rows, void* grad_logits, int rows, int vocab,
                                int dtype);
 
+/* ------------------------------------------------------------------------
+ * Layer normalisation over the last dimension (block callers: every block model's pre-norm
+ * and final norm; the reference's Axon.layer_norm, lib/edifice/ssm/common.ex:224,
+ * lib/edifice/recurrent/delta_net.ex:159,199, lib/edifice/blocks/model_builder.ex:111,165)
+ *   y[r, c] = (x[r, c] - mean_r) rstd_r gamma[c] + beta[c],  rstd_r = 1 / sqrt(var_r + eps)
+ *   (biased variance); x, y [rows, cols] in dtype; gamma, beta [cols] in param_dtype, either
+ *   NULL for 1 / 0; mean, rstd [rows] f32, written for the backward; 1 <= cols <= 8192.
+ * The backward writes grad_x [rows, cols] and, where not NULL, grad_gamma / grad_beta [cols]
+ * (summed over rows in a fixed order); workspace edf_layer_norm_backward_workspace_bytes().
+ * ------------------------------------------------------------------------ */
+int edf_layer_norm(void* stream, const void* x, const void* gamma, const void* beta, void* y, float* mean,
+                   float* rstd, int rows, int cols, float eps, int dtype, int param_dtype);
+size_t edf_layer_norm_backward_workspace_bytes(int rows, int cols);
+int edf_layer_norm_backward(void* stream, const void* x, const void* gamma, const float* mean, const float* rstd,
+                            const void* grad_y, void* grad_x, void* grad_gamma, void* grad_beta, void* workspace,
+                            size_t workspace_bytes, int rows, int cols, int dtype, int param_dtype);
+
 #ifdef __cplusplus
 }
 #endif

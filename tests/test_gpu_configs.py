@@ -187,12 +187,17 @@ class _OracleOps:
         from tests.gpu_util import torch_causal_conv_silu
         return torch_causal_conv_silu(x, weight, bias)
 
+    @staticmethod
+    def layer_norm(x, weight=None, bias=None, eps=1e-5):
+        return torch.nn.functional.layer_norm(x, (x.shape[-1],), weight, bias, eps)
+
 
 def test_c5_hybrid_decoder_bf16_matches_oracle_ops(monkeypatch):
     """Config 5's model at reduced size in bfloat16 (the benchmark's precision): the same bf16
-    model (same weights, the same torch bf16 GEMMs and norms) run once on the HIP ops and once
-    with the oracle ops swapped in, so the two runs differ only in the fused ops.  Loss and
-    every parameter gradient within the bf16 tolerance."""
+    model (same weights, the same torch bf16 GEMMs) run once on the HIP ops and once with the
+    oracle ops (and torch's layer norm, convolution and loss) swapped in, so the two runs
+    differ only in the ops edifice_amd fuses.  Loss and every parameter gradient within the
+    bf16 tolerance."""
     import copy
 
     from edifice_amd import blocks
