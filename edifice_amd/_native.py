@@ -14,6 +14,7 @@ P = ctypes.c_void_p
 I = ctypes.c_int
 S = ctypes.c_size_t
 F = ctypes.c_float
+L = ctypes.c_long
 
 # name -> (restype, argtypes); must match include/edifice_hip.h
 SIGNATURES = {
@@ -62,6 +63,8 @@ SIGNATURES = {
     "edf_layer_norm": (I, [P, P, P, P, P, P, P, I, I, F, I, I]),
     "edf_layer_norm_backward_workspace_bytes": (S, [I, I]),
     "edf_layer_norm_backward": (I, [P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
+    "edf_softplus": (I, [P, P, P, L, I]),
+    "edf_softplus_backward": (I, [P, P, P, P, L, I]),
     "edf_laser_attention_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_laser_attention": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_laser_attention_backward_workspace_bytes": (S, [I, I, I, I, I]),

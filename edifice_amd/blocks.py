@@ -125,7 +125,7 @@ class MambaBlock(nn.Module):
         xa = fs.causal_conv1d_silu(xb, self.dw_conv.weight, self.dw_conv.bias)
         bc = self.bc_proj(xa).float()
         b, c = bc[..., : self.state_size].contiguous(), bc[..., self.state_size:].contiguous()
-        dt = F.softplus(self.dt_proj(self.dt_rank_proj(xa)))
+        dt = fs.softplus(self.dt_proj(self.dt_rank_proj(xa)))
         y = fs.selective_scan(xa, dt.contiguous(), self.A.float(), b, c, None, zb,
                               dt_mode="mean")
         return self.out_proj(y)

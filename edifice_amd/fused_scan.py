@@ -448,6 +448,33 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor = None, bias: torch.Tensor 
     return _LayerNorm.apply(x, weight, bias, eps)
 
 
+class _Softplus(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        x = x.contiguous()
+        _dev(x)
+        y = torch.empty_like(x)
+        if x.numel():
+            nat.call("edf_softplus", _stream(), _p(x), _p(y), x.numel(), dtype_flag(x))
+        ctx.save_for_backward(x)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (x,) = ctx.saved_tensors
+        dy = dy.contiguous().to(x.dtype)
+        dx = torch.empty_like(x)
+        if x.numel():
+            nat.call("edf_softplus_backward", _stream(), _p(x), _p(dy), _p(dx), x.numel(), dtype_flag(x))
+        return dx
+
+
+def softplus(x: torch.Tensor) -> torch.Tensor:
+    """log(1 + e^x) elementwise (float32 or bfloat16, f32 inside), ``F.softplus(x)``: the Mamba
+    block's dt activation (Axon.activation(:softplus), common.ex:366)."""
+    return _Softplus.apply(x)
+
+
 # ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------

@@ -589,6 +589,14 @@ int edf_layer_norm_backward(void* stream, const void* x, const void* gamma, cons
                             const void* grad_y, void* grad_x, void* grad_gamma, void* grad_beta, void* workspace,
                             size_t workspace_bytes, int rows, int cols, int dtype, int param_dtype);
 
+/* ------------------------------------------------------------------------
+ * Softplus (block callers: the Mamba block's dt activation, Axon.activation(:softplus),
+ * lib/edifice/ssm/common.ex:366): y = log(1 + e^x) over n values of x in dtype (evaluated as
+ * max(x, 0) + log1p(e^-|x|), f32 inside); the backward writes grad_x = grad_y sigmoid(x).
+ * ------------------------------------------------------------------------ */
+int edf_softplus(void* stream, const void* x, void* y, long n, int dtype);
+int edf_softplus_backward(void* stream, const void* x, const void* grad_y, void* grad_x, long n, int dtype);
+
 #ifdef __cplusplus
 }
 #endif

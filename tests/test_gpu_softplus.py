@@ -1,0 +1,44 @@
+"""GPU parity: the HIP softplus (the Mamba block's dt activation) against float64 torch on the
+same (rounded) inputs, values and gradient."""
+import pytest
+import torch
+
+from tests.conftest import assert_close
+from tests.gpu_util import TOL, announce, host
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (shape, dtype, offset): offset 1 starts the tensor one element into a buffer (scalar path)
+    ((8, 2048, 64), torch.bfloat16, 0),   # the config-5 dt width, a slice of the batch
+    ((3, 70, 48), torch.float32, 0),
+    ((1001,), torch.bfloat16, 0),         # a tail past the last 16-byte vector
+    ((517,), torch.float32, 1),
+    ((5,), torch.bfloat16, 0),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_softplus(case):
+    from edifice_amd import fused_scan as fs
+    shape, dtype, off = case
+    announce("softplus", case=case)
+    g = torch.Generator().manual_seed(6)
+    n = 1
+    for d in shape:
+        n *= d
+    x = torch.randn(n, generator=g) * 4.0 - 2.0
+    x[:4] = torch.tensor([-100.0, 100.0, 0.0, 25.0])  # both saturated ends and the threshold region
+    x = x.to(dtype)
+    dy = torch.randn(n, generator=g).to(dtype)
+    buf = torch.zeros(n + off, dtype=dtype, device="cuda")
+    buf[off:] = x.cuda()
+    xd = buf[off:].view(shape).detach().requires_grad_()
+    y = fs.softplus(xd)
+    y.backward(dy.view(shape).cuda())
+    xr = x.double().view(shape).requires_grad_()
+    yr = torch.nn.functional.softplus(xr)
+    yr.backward(dy.double().view(shape))
+    assert y.dtype == dtype and torch.isfinite(y).all()
+    assert_close(host(y), yr.detach().numpy(), TOL[dtype], "y")
+    assert_close(host(xd.grad), xr.grad.numpy(), TOL[dtype], "dx")
