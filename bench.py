@@ -30,6 +30,7 @@ import ctypes
 import json
 import os
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -611,12 +612,35 @@ def bench_rnn_block(torch, steps, warmup, kind, dtype, B=8, T=2048, H=256, L=4):
                 shape=dict(B=B, T=T, H=H))
 
 
+GEMM_SOLUTIONS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "edifice_amd", "gemm_solutions_mi355x.csv")
+
+
+def use_tuned_gemms(torch):
+    """The config-5 model's torch GEMMs take the hipBLASLt / rocBLAS solutions that torch's
+    TunableOp measured fastest per shape on an MI355X (``edifice_amd/gemm_solutions_mi355x.csv``,
+    read before the model is built; no tuning runs here).  TunableOp checks the file's torch,
+    HIP, hipBLASLt, rocBLAS and architecture lines and ignores a file that does not match, and
+    shapes not in the file keep the library's default choice.  Returns what the GEMMs use."""
+    tun = getattr(torch.cuda, "tunable", None)
+    if tun is None or not os.path.exists(GEMM_SOLUTIONS):
+        return "library default"
+    tun.enable(True)
+    tun.tuning_enable(False)
+    tun.record_untuned_enable(False)
+    tun.set_filename(os.path.join(tempfile.gettempdir(), "edifice_tunableop_unused%d.csv"), True)
+    if not tun.read_file(GEMM_SOLUTIONS):
+        tun.enable(False)
+        return "library default (solution file not accepted)"
+    return "TunableOp file edifice_amd/gemm_solutions_mi355x.csv"
+
+
 def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     """Config 5: 4 Mamba + 2 DeltaNet + 2 causal-attention blocks, embed 1024, bf16 weights and
     activations, random init, synthetic token ids uniform over the vocabulary; one step = the
     forward and backward of the next-token loss (no optimizer step, as the metric states)."""
     from edifice_amd import blocks
 
+    gemm = use_tuned_gemms(torch)
     torch.manual_seed(5000)
     model = blocks.HybridDecoder(vocab, embed).to("cuda", torch.bfloat16)
     g = torch.Generator(device="cuda").manual_seed(5001)
@@ -638,7 +662,8 @@ def bench_hybrid(torch, steps, warmup, B=8, T=2048, vocab=32000, embed=1024):
     torch.cuda.synchronize()
     per_step = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
     ms = float(np.median(per_step))
-    return dict(step_ms=ms, tokens_per_s=B * T / ms * 1e3, steps=steps, warmup=warmup,
+    torch.cuda.tunable.enable(False)
+    return dict(step_ms=ms, tokens_per_s=B * T / ms * 1e3, steps=steps, warmup=warmup, gemm_solutions=gemm,
                 step_ms_min=float(min(per_step)), step_ms_max=float(max(per_step)),
                 shape=dict(batch=B, seq=T, vocab=vocab, embed=embed, layers="4 mamba + 2 delta_net + 2 attention"))
 
