@@ -46,6 +46,53 @@ def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:
     return t.reshape(bsz, seq, num_heads, hid // num_heads).contiguous()
 
 
+def _weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """dW = dy^T x over k rows.  For bf16 with many rows and a small [m, n] output the product
+    splits k into s slices, one batched product with float32 partials, summed and rounded once:
+    a single [m, n] product over k = 16 384 has too few output tiles for the GPU (the config-5
+    model's 1024 x 1024 weight gradients: 97-110 µs as one product, 57 µs in 8 slices)."""
+    k, m = dy.shape
+    n = x.shape[1]
+    s = 8 if m * n <= 1 << 20 else (4 if m * n <= 1 << 22 else 1)
+    if s == 1 or dy.dtype != torch.bfloat16 or k % s or k // s < 1024:
+        return dy.t().mm(x)
+    kc = k // s
+    a = dy.reshape(s, kc, m).transpose(1, 2)
+    b = x.reshape(s, kc, n).contiguous()  # the right operand stays a contiguous (non-transposed) tensor
+    return torch.bmm(a, b, out_dtype=torch.float32).sum(0).to(dy.dtype)
+
+
+class _LinearFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return F.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = dy2.mm(weight).view(x.shape)
+        if ctx.needs_input_grad[1]:
+            dw = _weight_grad(dy2, x.reshape(-1, x.shape[-1]))
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            # wide layers: the HIP column sum (torch's reduction reads [16384, 1024] bf16 at
+            # about 1.5 TB/s); narrow ones keep torch's
+            db = fs.column_sum(dy2) if dy2.shape[1] >= 256 and dy2.is_cuda else dy2.sum(0)
+        return dx, dw, db
+
+
+class Linear(nn.Linear):
+    """nn.Linear (same parameters and state-dict names; Axon.dense of the reference blocks)
+    whose weight gradient splits the row dimension when that pays (``_weight_grad``)."""
+
+    def forward(self, x):
+        return _LinearFn.apply(x, self.weight, self.bias)
+
+
 class LayerNorm(nn.LayerNorm):
     """nn.LayerNorm over the last dimension (same parameters and state-dict names) run by the
     HIP layer norm, ``fs.layer_norm``: Axon.layer_norm of the reference blocks
@@ -66,8 +113,8 @@ class MinGRULayer(nn.Module):
     def __init__(self, hidden_size: int):
         super().__init__()
         self.norm = LayerNorm(hidden_size, eps=LN_EPS)
-        self.gate = nn.Linear(hidden_size, hidden_size)
-        self.candidate = nn.Linear(hidden_size, hidden_size)
+        self.gate = Linear(hidden_size, hidden_size)
+        self.candidate = Linear(hidden_size, hidden_size)
 
     def forward(self, x):
         n = self.norm(x)
@@ -82,9 +129,9 @@ class MinLSTMLayer(nn.Module):
     def __init__(self, hidden_size: int):
         super().__init__()
         self.norm = LayerNorm(hidden_size, eps=LN_EPS)
-        self.forget = nn.Linear(hidden_size, hidden_size)
-        self.input = nn.Linear(hidden_size, hidden_size)
-        self.candidate = nn.Linear(hidden_size, hidden_size)
+        self.forget = Linear(hidden_size, hidden_size)
+        self.input = Linear(hidden_size, hidden_size)
+        self.candidate = Linear(hidden_size, hidden_size)
 
     def forward(self, x):
         n = self.norm(x)
@@ -106,12 +153,12 @@ class MambaBlock(nn.Module):
         dt_rank = max(hidden_size // 16, 1)  # common.ex:221
         self.inner, self.state_size = inner, state_size
         self.norm = LayerNorm(hidden_size, eps=LN_EPS)
-        self.in_proj = nn.Linear(hidden_size, 2 * inner)
+        self.in_proj = Linear(hidden_size, 2 * inner)
         self.dw_conv = nn.Conv1d(inner, inner, conv_size, padding=conv_size - 1, groups=inner)
-        self.bc_proj = nn.Linear(inner, 2 * state_size)
-        self.dt_rank_proj = nn.Linear(inner, dt_rank)
-        self.dt_proj = nn.Linear(dt_rank, inner)
-        self.out_proj = nn.Linear(inner, hidden_size)
+        self.bc_proj = Linear(inner, 2 * state_size)
+        self.dt_rank_proj = Linear(inner, dt_rank)
+        self.dt_proj = Linear(dt_rank, inner)
+        self.out_proj = Linear(inner, hidden_size)
         a = -(torch.arange(state_size, dtype=torch.float32) + 1.0)
         self.register_buffer("A", a[None, :].expand(inner, state_size).contiguous(), persistent=False)
 
@@ -120,8 +167,8 @@ class MambaBlock(nn.Module):
         # contiguous, and their gradients land in one buffer each (slices of one [.., 2 inner]
         # output would each be scattered into a zero-filled full-size gradient)
         n, w, bias = self.norm(x), self.in_proj.weight, self.in_proj.bias
-        xb = F.linear(n, w[: self.inner], None if bias is None else bias[: self.inner])
-        zb = F.linear(n, w[self.inner:], None if bias is None else bias[self.inner:])
+        xb = _LinearFn.apply(n, w[: self.inner], None if bias is None else bias[: self.inner])
+        zb = _LinearFn.apply(n, w[self.inner:], None if bias is None else bias[self.inner:])
         xa = fs.causal_conv1d_silu(xb, self.dw_conv.weight, self.dw_conv.bias)
         bc = self.bc_proj(xa).float()
         b, c = bc[..., : self.state_size].contiguous(), bc[..., self.state_size:].contiguous()
@@ -138,8 +185,8 @@ class DeltaNetLayer(nn.Module):
         super().__init__()
         self.hidden, self.num_heads = hidden_size, num_heads
         self.norm = LayerNorm(hidden_size, eps=LN_EPS)
-        self.qkvb_proj = nn.Linear(hidden_size, 4 * hidden_size)
-        self.out_proj = nn.Linear(hidden_size, hidden_size)
+        self.qkvb_proj = Linear(hidden_size, 4 * hidden_size)
+        self.out_proj = Linear(hidden_size, hidden_size)
 
     def forward(self, x):
         bsz, seq, hid = x.shape
@@ -161,8 +208,8 @@ class GatedDeltaNetLayer(nn.Module):
         self.norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.short_conv = (nn.Conv1d(hidden_size, hidden_size, conv_size, padding=conv_size - 1,
                                      groups=hidden_size) if use_short_conv else None)
-        self.qkvbag_proj = nn.Linear(hidden_size, 6 * hidden_size)
-        self.out_proj = nn.Linear(hidden_size, hidden_size)
+        self.qkvbag_proj = Linear(hidden_size, 6 * hidden_size)
+        self.out_proj = Linear(hidden_size, hidden_size)
 
     def forward(self, x):
         bsz, seq, hid = x.shape
@@ -185,10 +232,10 @@ class GQAttention(nn.Module):
         super().__init__()
         self.num_heads, self.num_kv_heads = num_heads, num_kv_heads
         hd = hidden_size // num_heads
-        self.q_proj = nn.Linear(hidden_size, hidden_size)
-        self.k_proj = nn.Linear(hidden_size, num_kv_heads * hd)
-        self.v_proj = nn.Linear(hidden_size, num_kv_heads * hd)
-        self.out_proj = nn.Linear(hidden_size, hidden_size)
+        self.q_proj = Linear(hidden_size, hidden_size)
+        self.k_proj = Linear(hidden_size, num_kv_heads * hd)
+        self.v_proj = Linear(hidden_size, num_kv_heads * hd)
+        self.out_proj = Linear(hidden_size, hidden_size)
 
     def forward(self, x):
         bsz, seq, hid = x.shape
@@ -211,8 +258,8 @@ class GQABlock(nn.Module):
         self.attn_norm = LayerNorm(hidden_size, eps=LN_EPS)
         self.attn = GQAttention(hidden_size, num_heads, num_kv_heads)
         self.ffn_norm = LayerNorm(hidden_size, eps=LN_EPS)
-        self.ffn_up = nn.Linear(hidden_size, ffn_mult * hidden_size)
-        self.ffn_down = nn.Linear(ffn_mult * hidden_size, hidden_size)
+        self.ffn_up = Linear(hidden_size, ffn_mult * hidden_size)
+        self.ffn_down = Linear(ffn_mult * hidden_size, hidden_size)
 
     def forward(self, x):
         x = x + self.attn(self.attn_norm(x))
@@ -264,7 +311,7 @@ def build(name: str, *, embed_size: int, hidden_size: int | None = None, num_lay
     name: "min_gru", "min_lstm", "mamba", "delta_net", "gated_delta_net" or "gqa".  hidden_size defaults
     to embed_size; an input projection is added when they differ."""
     hidden = hidden_size or embed_size
-    proj = nn.Linear(embed_size, hidden) if hidden != embed_size else None
+    proj = Linear(embed_size, hidden) if hidden != embed_size else None
     if name == "min_gru":
         return SequenceModel("layers", [MinGRULayer(hidden) for _ in range(num_layers)], proj,
                              LayerNorm(hidden, eps=LN_EPS))
@@ -301,7 +348,7 @@ class HybridDecoder(nn.Module):
         self.delta = nn.ModuleList(DeltaNetLayer(embed_size, num_heads) for _ in range(delta_layers))
         self.attn = nn.ModuleList(GQABlock(embed_size, num_heads, num_heads) for _ in range(attn_layers))
         self.final_norm = LayerNorm(embed_size, eps=LN_EPS)
-        self.lm_head = nn.Linear(embed_size, vocab_size, bias=False)
+        self.lm_head = Linear(embed_size, vocab_size, bias=False)
 
     def forward(self, tokens: torch.Tensor) -> torch.Tensor:
         h = self.embed(tokens)

@@ -475,6 +475,20 @@ def softplus(x: torch.Tensor) -> torch.Tensor:
     return _Softplus.apply(x)
 
 
+def column_sum(x: torch.Tensor, out_dtype: torch.dtype = None) -> torch.Tensor:
+    """Sum over the rows of a 2-D ``x`` (float32 or bfloat16, f32 inside, fixed order): the
+    dense layers' bias gradients.  Not differentiable (a backward helper)."""
+    x = x.contiguous()
+    _dev(x)
+    _rank("x", x, 2)
+    rows, cols = x.shape
+    out = torch.empty(cols, dtype=out_dtype or x.dtype, device=x.device)
+    wsb = nat.query("edf_column_sum_workspace_bytes", rows, cols)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    nat.call("edf_column_sum", _stream(), _p(x), _p(out), _p(ws), wsb, rows, cols, dtype_flag(x), dtype_flag(out))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Selective scan
 # ---------------------------------------------------------------------------

@@ -597,6 +597,16 @@ int edf_layer_norm_backward(void* stream, const void* x, const void* gamma, cons
 int edf_softplus(void* stream, const void* x, void* y, long n, int dtype);
 int edf_softplus_backward(void* stream, const void* x, const void* grad_y, void* grad_x, long n, int dtype);
 
+/* ------------------------------------------------------------------------
+ * Column sums (block callers: the bias gradients of the dense layers, sum over rows of the
+ * output gradient; in the reference XLA derives them for Axon.dense): out[c] = sum_r x[r, c],
+ * x [rows, cols] in dtype, out [cols] in out_dtype, f32 inside, summed in a fixed order;
+ * workspace edf_column_sum_workspace_bytes().
+ * ------------------------------------------------------------------------ */
+size_t edf_column_sum_workspace_bytes(long rows, int cols);
+int edf_column_sum(void* stream, const void* x, void* out, void* workspace, size_t workspace_bytes, long rows,
+                   int cols, int dtype, int out_dtype);
+
 #ifdef __cplusplus
 }
 #endif
