@@ -59,7 +59,9 @@ def _weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     kc = k // s
     a = dy.reshape(s, kc, m).transpose(1, 2)
     b = x.reshape(s, kc, n).contiguous()  # the right operand stays a contiguous (non-transposed) tensor
-    return torch.bmm(a, b, out_dtype=torch.float32).sum(0).to(dy.dtype)
+    part = torch.bmm(a, b, out_dtype=torch.float32)
+    # the s partials added in order and rounded to bf16 in one pass
+    return fs.column_sum(part.view(s, m * n), dy.dtype).view(m, n)
 
 
 class _LinearFn(torch.autograd.Function):

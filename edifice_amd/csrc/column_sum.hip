@@ -5,7 +5,8 @@
 // Two stages, summed in a fixed order (deterministic, no atomics): each workgroup sums a
 // slice of rows for 128 columns (a wave reads two adjacent elements per lane, the four waves
 // of a workgroup take interleaved rows and are added in LDS), one float32 partial per slice;
-// then four waves per 64 columns split the slices and are added in LDS.
+// then four waves per 64 columns split the slices and are added in LDS (with a single slice
+// the first stage writes the result).
 #include <stdint.h>
 
 #include <algorithm>
@@ -34,9 +35,10 @@ template <> EDF_DEVICE void ld2<float>(const float* p, float& a, float& b) {
 }
 
 // part [nslice][cols]: slice s covers rows [s * rps, (s + 1) * rps); PAIR: cols even and the
-// rows 2-element aligned, so a lane reads two adjacent columns at once
-template <typename T, bool PAIR>
-__global__ __launch_bounds__(CS_NT) void cs_part_kernel(const T* __restrict__ x, float* __restrict__ part, long rows,
+// rows 2-element aligned, so a lane reads two adjacent columns at once.  TO: with one slice
+// (few rows, e.g. the partials of a split product) the sums go straight to the output type.
+template <typename T, bool PAIR, typename TO = float>
+__global__ __launch_bounds__(CS_NT) void cs_part_kernel(const T* __restrict__ x, TO* __restrict__ part, long rows,
                                                        int cols, long rps) {
   __shared__ float s_acc[4][CS_CB];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(CS_NT) void cs_part_kernel(const T* __restrict__ x,
   if (threadIdx.x < CS_CB) {
     const int c = blockIdx.x * CS_CB + threadIdx.x;
     const float v = ((s_acc[0][threadIdx.x] + s_acc[1][threadIdx.x]) + s_acc[2][threadIdx.x]) + s_acc[3][threadIdx.x];
-    if (c < cols) part[(long)blockIdx.y * cols + c] = v;
+    if (c < cols) part[(long)blockIdx.y * cols + c] = from_f32<TO>(v);
   }
 }
 
@@ -92,6 +94,13 @@ int cs_run(hipStream_t s, const void* x, void* out, long rows, int cols, float* 
   const int nslice = (int)((rows + rps - 1) / rps);
   const dim3 g1((cols + CS_CB - 1) / CS_CB, nslice);
   const bool pair = cols % 2 == 0 && ((uintptr_t)x & (2 * sizeof(T) - 1)) == 0;
+  if (nslice == 1) {
+    if (pair)
+      cs_part_kernel<T, true, TO><<<g1, CS_NT, 0, s>>>((const T*)x, (TO*)out, rows, cols, rps);
+    else
+      cs_part_kernel<T, false, TO><<<g1, CS_NT, 0, s>>>((const T*)x, (TO*)out, rows, cols, rps);
+    return check_launch("column sum");
+  }
   if (pair)
     cs_part_kernel<T, true><<<g1, CS_NT, 0, s>>>((const T*)x, part, rows, cols, rps);
   else

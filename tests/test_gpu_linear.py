@@ -56,6 +56,7 @@ COLSUM_CASES = [
     (1000, 301, torch.float32, torch.float32, 0),      # odd width: one element per lane
     (70, 256, torch.bfloat16, torch.bfloat16, 1),      # fewer rows than a slice, misaligned
     (1, 5, torch.float32, torch.bfloat16, 0),
+    (8, 1 << 20, torch.float32, torch.bfloat16, 0),  # split-product partials: one slice, direct output
 ]
 
 
