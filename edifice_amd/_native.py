@@ -67,6 +67,8 @@ SIGNATURES = {
     "edf_softplus_backward": (I, [P, P, P, P, L, I]),
     "edf_column_sum_workspace_bytes": (S, [L, I]),
     "edf_column_sum": (I, [P, P, P, P, S, L, I, I, I]),
+    "edf_l2_normalize": (I, [P, P, P, L, I, F, I]),
+    "edf_l2_normalize_backward": (I, [P, P, P, P, L, I, F, I]),
     "edf_laser_attention_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_laser_attention": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_laser_attention_backward_workspace_bytes": (S, [I, I, I, I, I]),

@@ -105,7 +105,7 @@ class LayerNorm(nn.LayerNorm):
 
 
 def _l2norm_keys(k: torch.Tensor) -> torch.Tensor:
-    return k / torch.sqrt((k * k).sum(-1, keepdim=True) + KEY_NORM_EPS)
+    return fs.l2_normalize(k, KEY_NORM_EPS)
 
 
 class MinGRULayer(nn.Module):

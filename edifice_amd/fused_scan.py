@@ -475,6 +475,40 @@ def softplus(x: torch.Tensor) -> torch.Tensor:
     return _Softplus.apply(x)
 
 
+class _L2Normalize(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, eps):
+        x = x.contiguous()
+        _dev(x)
+        d = x.shape[-1]
+        rows = x.numel() // max(d, 1)
+        y = torch.empty_like(x)
+        if x.numel():
+            nat.call("edf_l2_normalize", _stream(), _p(x), _p(y), rows, d, float(eps), dtype_flag(x))
+        ctx.save_for_backward(x)
+        ctx.eps = eps
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        (x,) = ctx.saved_tensors
+        d = x.shape[-1]
+        rows = x.numel() // max(d, 1)
+        dy = dy.contiguous().to(x.dtype)
+        dx = torch.empty_like(x)
+        if x.numel():
+            nat.call("edf_l2_normalize_backward", _stream(), _p(x), _p(dy), _p(dx), rows, d, float(ctx.eps),
+                     dtype_flag(x))
+        return dx, None
+
+
+def l2_normalize(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """x / sqrt(sum x^2 + eps) over the last dimension (<= 1024 elements; float32 or bfloat16,
+    f32 inside): the DeltaNet / GatedDeltaNet key norm (delta_net.ex:291,
+    gated_delta_net.ex:387)."""
+    return _L2Normalize.apply(x, eps)
+
+
 def column_sum(x: torch.Tensor, out_dtype: torch.dtype = None) -> torch.Tensor:
     """Sum over the rows of a 2-D ``x`` (float32 or bfloat16, f32 inside, fixed order): the
     dense layers' bias gradients.  Not differentiable (a backward helper)."""

@@ -607,6 +607,16 @@ size_t edf_column_sum_workspace_bytes(long rows, int cols);
 int edf_column_sum(void* stream, const void* x, void* out, void* workspace, size_t workspace_bytes, long rows,
                    int cols, int dtype, int out_dtype);
 
+/* ------------------------------------------------------------------------
+ * L2 normalisation of rows (block callers: the DeltaNet / GatedDeltaNet key norm,
+ * lib/edifice/recurrent/delta_net.ex:291, gated_delta_net.ex:387):
+ *   y = x / sqrt(sum_j x_j^2 + eps) over rows of d <= 1024 elements of x [rows, d] in dtype
+ *   (f32 inside); the backward writes grad_x = (grad_y - y <y, grad_y>) / sqrt(sum x^2 + eps).
+ * ------------------------------------------------------------------------ */
+int edf_l2_normalize(void* stream, const void* x, void* y, long rows, int d, float eps, int dtype);
+int edf_l2_normalize_backward(void* stream, const void* x, const void* grad_y, void* grad_x, long rows, int d,
+                              float eps, int dtype);
+
 #ifdef __cplusplus
 }
 #endif

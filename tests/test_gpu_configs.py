@@ -199,13 +199,17 @@ class _OracleOps:
     def column_sum(x, out_dtype=None):
         return x.sum(0, dtype=out_dtype)
 
+    @staticmethod
+    def l2_normalize(x, eps=1e-6):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + eps)
+
 
 def test_c5_hybrid_decoder_bf16_matches_oracle_ops(monkeypatch):
     """Config 5's model at reduced size in bfloat16 (the benchmark's precision): the same bf16
     model (same weights, the same torch bf16 GEMMs) run once on the HIP ops and once with the
-    oracle ops (and torch's layer norm, softplus, convolution, bias-gradient sums and loss) swapped in, so the two runs
-    differ only in the ops edifice_amd fuses.  Loss and every parameter gradient within the
-    bf16 tolerance."""
+    oracle ops (and torch's layer norm, softplus, key norm, convolution, bias-gradient sums and
+    loss) swapped in, so the two runs differ only in the ops edifice_amd fuses.  Loss and every
+    parameter gradient within the bf16 tolerance."""
     import copy
 
     from edifice_amd import blocks

@@ -1,5 +1,5 @@
-"""GPU parity: the HIP softplus (the Mamba block's dt activation) against float64 torch on the
-same (rounded) inputs, values and gradient."""
+"""GPU parity: the HIP softplus (the Mamba block's dt activation) and row L2 normalisation (the
+DeltaNet key norm) against float64 torch on the same (rounded) inputs, values and gradient."""
 import pytest
 import torch
 
@@ -40,5 +40,41 @@ def test_softplus(case):
     yr = torch.nn.functional.softplus(xr)
     yr.backward(dy.double().view(shape))
     assert y.dtype == dtype and torch.isfinite(y).all()
+    assert_close(host(y), yr.detach().numpy(), TOL[dtype], "y")
+    assert_close(host(xd.grad), xr.grad.numpy(), TOL[dtype], "dx")
+
+
+L2_CASES = [
+    # (rows, d, dtype, offset)
+    (8 * 2048 * 8, 128, torch.bfloat16, 0),  # the config-5 DeltaNet keys
+    (300, 128, torch.float32, 0),
+    (77, 64, torch.bfloat16, 0),
+    (50, 1000, torch.float32, 0),          # beyond the vector path for f32
+    (31, 100, torch.bfloat16, 1),          # misaligned: one element per lane
+    (5, 8, torch.float32, 0),
+]
+
+
+@pytest.mark.parametrize("case", L2_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_l2_normalize(case):
+    """fs.l2_normalize (the DeltaNet key norm) against float64 torch: values and gradient, with
+    a zero row (eps keeps it finite)."""
+    from edifice_amd import fused_scan as fs
+    rows, d, dtype, off = case
+    announce("l2_normalize", case=case)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(rows, d, generator=g) * 3.0
+    x[0] = 0.0
+    x = x.to(dtype)
+    dy = torch.randn(rows, d, generator=g).to(dtype)
+    buf = torch.zeros(rows * d + off, dtype=dtype, device="cuda")
+    buf[off:] = x.cuda().reshape(-1)
+    xd = buf[off:].view(rows, d).detach().requires_grad_()
+    y = fs.l2_normalize(xd, 1e-6)
+    y.backward(dy.cuda())
+    xr = x.double().requires_grad_()
+    yr = xr / torch.sqrt((xr * xr).sum(-1, keepdim=True) + 1e-6)
+    yr.backward(dy.double())
+    assert torch.isfinite(y).all() and torch.isfinite(xd.grad).all()
     assert_close(host(y), yr.detach().numpy(), TOL[dtype], "y")
     assert_close(host(xd.grad), xr.grad.numpy(), TOL[dtype], "dx")
