@@ -123,7 +123,12 @@ EDF_DEVICE void fwd_step(float (&S)[DP / 16], const Stage<DP>& sm, int tt, int t
   for (int c = 0; c < NC; ++c) S[c] = fmaf(e, sm.k[tt][tc + 16 * c], at * S[c]);
 }
 
-template <typename TT, int DP, bool DECAY>
+// OUTM: 0 no output (p.out null), 1 output stored by the row's lane 0 (tensors of 2 GiB per
+// batch row and more), 2 output through a buffer resource over the batch row, every lane
+// storing (lanes other than the row's lane 0, rows past d and steps past T at an offset the
+// hardware drops): no branch in the unrolled steps, which a per-step branch splits into
+// basic blocks, each waiting for its own LDS reads.
+template <typename TT, int DP, bool DECAY, int OUTM>
 __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
   constexpr int NC = DP / 16;
   __shared__ Stage<DP> sms[2];
@@ -132,6 +137,15 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
   const int rb = blockIdx.y, i = rb * RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   const int nch = (p.T + CK - 1) / CK;
+  const long rowel = (long)p.T * p.H * p.d;  // output elements of one batch row
+  const rsrc_t r_out = make_rsrc(OUTM == 2 ? (const TT*)p.out + (long)b * rowel : (const TT*)p.k,
+                                 OUTM == 2 ? (unsigned)(rowel * sizeof(TT)) : 0u);
+  const bool orow = tc == 0 && i < p.d;
+  // OUTM 2: the lane's byte offset at step 0, out of bounds for lanes that store nothing; a
+  // step past T lands past the batch row (the host keeps (T + CK) H d elements under 2 GiB,
+  // so no offset wraps)
+  const unsigned obase = orow ? (unsigned)(((long)h * p.d + i) * sizeof(TT)) : OOB_OFF;
+  const unsigned ostep = (unsigned)((long)p.H * p.d * sizeof(TT));
   float S[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) S[c] = 0.0f;
@@ -149,12 +163,16 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
 #pragma unroll
     for (int tt = 0; tt < CK; ++tt) {
       fwd_step<DP, DECAY>(S, sm, tt, tr, tc);
-      if (p.out != nullptr) {  // o_i = sum_j S[i][j] q_j
+      if constexpr (OUTM != 0) {  // o_i = sum_j S[i][j] q_j
         float o = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) o = fmaf(S[c], sm.q[tt][tc + 16 * c], o);
         o = row16_sum(o);
-        if (tc == 0 && i < p.d && t0 + tt < p.T) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
+        if constexpr (OUTM == 2) {
+          bstore<TT>(r_out, obase + (unsigned)(t0 + tt) * ostep, o);
+        } else if (orow && t0 + tt < p.T) {
+          st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
+        }
       }
     }
     if (p.ckpt != nullptr) {
@@ -178,7 +196,10 @@ __global__ __launch_bounds__(256) void dr_seq_fwd_kernel(const DRArgs p) {
 // rows in registers (rows4_scatter: the lane of row r keeps the column sums of one value
 // in four) into a per-step slot of an LDS buffer, and every FS steps one barrier pair adds
 // the four waves' slots (in wave order) and stores the partials of those steps.
-template <typename TT, int DP, bool DECAY>
+// BUF: the per-row outputs (dv, per-element dbeta, KDA's dalpha) go through buffer resources
+// over the batch row, every lane storing at an offset the hardware drops where the lane
+// stores nothing (as the forward's OUTM 2), so the unrolled steps hold no branch.
+template <typename TT, int DP, bool DECAY, bool BUF>
 __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
   constexpr int NC = DP / 16;
   constexpr int FS = 8;                 // steps per flush of the row sums
@@ -193,6 +214,15 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
   const int rb = blockIdx.y, i = rb * RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   const long nbth = (long)gridDim.x * p.T;  // B * T * H
+  const long rowel = (long)p.T * p.H * p.d;  // per-row output elements of one batch row
+  const unsigned rbytes = (unsigned)(BUF ? rowel * sizeof(TT) : 0);
+  const rsrc_t r_dv = make_rsrc(BUF ? (const TT*)p.dv + (long)b * rowel : (const TT*)p.k, rbytes);
+  const rsrc_t r_db = make_rsrc(BUF && !p.beta_per_head ? (const TT*)p.dbeta + (long)b * rowel : (const TT*)p.k,
+                                BUF && !p.beta_per_head ? rbytes : 0u);
+  const rsrc_t r_da = make_rsrc(BUF && p.alpha_per_row ? (const TT*)p.dalpha + (long)b * rowel : (const TT*)p.k,
+                                BUF && p.alpha_per_row ? rbytes : 0u);
+  const unsigned obase = (tc == 0 && i < p.d) ? (unsigned)(((long)h * p.d + i) * sizeof(TT)) : OOB_OFF;
+  const unsigned ostep = (unsigned)((long)p.H * p.d * sizeof(TT));
   float dS[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) dS[c] = 0.0f;
@@ -261,7 +291,11 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
       }
       const bool live = t < p.T;
       const long bth = ((long)b * p.T + t) * p.H + h;
-      if (live && tc == 0 && i < p.d) {  // per-row outputs: dv, per-element dbeta
+      if constexpr (BUF) {  // per-row outputs: dv, per-element dbeta (steps past T land past the row)
+        const unsigned off = obase + (unsigned)t * ostep;
+        bstore<TT>(r_dv, off, bdk);
+        bstore<TT>(r_db, off, err * sk);
+      } else if (live && tc == 0 && i < p.d) {
         st((TT*)p.dv, bth * p.d + i, bdk);
         if (!p.beta_per_head) st((TT*)p.dbeta, bth * p.d + i, err * sk);
       }
@@ -280,10 +314,15 @@ __global__ __launch_bounds__(256) void dr_seq_bwd_kernel(const DRArgs p) {
       for (int g = 0; g < NG; ++g)
         wsum[slot][w][g][lane] = rows4_scatter(vals[4 * g], vals[4 * g + 1], vals[4 * g + 2], vals[4 * g + 3]);
       if (DECAY) pa = row16_sum(pa);
-      if (tc == 0) {
+      if constexpr (BUF) {
+        // every lane of the row holds the row sums: the 16 equal writes need no branch
         rsum[slot][0][tr] = pa;
         rsum[slot][1][tr] = i < p.d ? err * sk : 0.0f;
         // KDA: the row's own decay gradient, in log space
+        if constexpr (DECAY) bstore<TT>(r_da, obase + (unsigned)t * ostep, pa * at);
+      } else if (tc == 0) {
+        rsum[slot][0][tr] = pa;
+        rsum[slot][1][tr] = i < p.d ? err * sk : 0.0f;
         if (p.alpha_per_row && live && i < p.d) st((TT*)p.dalpha, bth * p.d + i, pa * at);
       }
       if (slot == 0) {  // steps t .. t + FS - 1 are in the slots: sum the waves, store
@@ -353,6 +392,24 @@ __global__ __launch_bounds__(256) void dr_seq_reduce_kernel(const DRArgs p, long
   }
 }
 
+template <typename TT, int DP, bool DECAY>
+void fwd_out(hipStream_t s, dim3 grid, const DRArgs& a) {
+  if (a.out == nullptr)
+    dr_seq_fwd_kernel<TT, DP, DECAY, 0><<<grid, 256, 0, s>>>(a);
+  else if ((long)(a.T + CK) * a.H * a.d * (long)sizeof(TT) < (1L << 31))
+    dr_seq_fwd_kernel<TT, DP, DECAY, 2><<<grid, 256, 0, s>>>(a);
+  else
+    dr_seq_fwd_kernel<TT, DP, DECAY, 1><<<grid, 256, 0, s>>>(a);
+}
+
+template <typename TT, int DP, bool DECAY>
+void bwd_out(hipStream_t s, dim3 grid, const DRArgs& a) {
+  if ((long)(a.T + CK) * a.H * a.d * (long)sizeof(TT) < (1L << 31))
+    dr_seq_bwd_kernel<TT, DP, DECAY, true><<<grid, 256, 0, s>>>(a);
+  else
+    dr_seq_bwd_kernel<TT, DP, DECAY, false><<<grid, 256, 0, s>>>(a);
+}
+
 template <typename TT>
 int launch_seq(hipStream_t s, const DRArgs& a, bool bwd, int BH) {
   const int d = a.d;
@@ -360,13 +417,13 @@ int launch_seq(hipStream_t s, const DRArgs& a, bool bwd, int BH) {
   do {                                                                 \
     const dim3 grid(BH, DP / RB);                                      \
     if (bwd && a.alpha != nullptr)                                     \
-      dr_seq_bwd_kernel<TT, DP, true><<<grid, 256, 0, s>>>(a);         \
+      bwd_out<TT, DP, true>(s, grid, a);                               \
     else if (bwd)                                                      \
-      dr_seq_bwd_kernel<TT, DP, false><<<grid, 256, 0, s>>>(a);        \
+      bwd_out<TT, DP, false>(s, grid, a);                              \
     else if (a.alpha != nullptr)                                       \
-      dr_seq_fwd_kernel<TT, DP, true><<<grid, 256, 0, s>>>(a);         \
+      fwd_out<TT, DP, true>(s, grid, a);                               \
     else                                                               \
-      dr_seq_fwd_kernel<TT, DP, false><<<grid, 256, 0, s>>>(a);        \
+      fwd_out<TT, DP, false>(s, grid, a);                              \
   } while (0)
   if (d <= 16)
     EDF_DR_LAUNCH(16);
