@@ -302,7 +302,10 @@ __global__ __launch_bounds__(256) void dp_finish_kernel(const DPArgs p, long nbt
 // per-step backward: each wave adds its four rows' terms in registers (rows4_scatter) into a
 // per-sub-step slot of an LDS tile, and every FS sub-steps one barrier pair adds the four
 // waves' slots in wave order and stores the partials.
-template <typename TT, int DP>
+// BUF: dv and dq go through buffer resources over the batch row, every lane storing at an
+// offset with bit 31 set where the lane or the sub-step stores nothing (OR, not add: no
+// offset wraps back into range), so the unrolled sub-steps hold no branch.
+template <typename TT, int DP, bool BUF>
 __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
   constexpr int NC = DP / 16;
   constexpr int FS = 8;                 // sub-steps per flush of the row sums
@@ -317,6 +320,14 @@ __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
   const int rb = blockIdx.y, i = rb * DPR_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   const long nbts = (long)gridDim.x * p.TS;
+  const long vrow = (long)p.TS * p.H * p.d, qrow = (long)p.T * p.H * p.d;  // elements per batch row
+  const rsrc_t r_dv = make_rsrc(BUF ? (const TT*)p.dv + (long)b * vrow : (const TT*)p.k,
+                                BUF ? (unsigned)(vrow * sizeof(TT)) : 0u);
+  const rsrc_t r_dq = make_rsrc(BUF ? (const TT*)p.dq + (long)b * qrow : (const TT*)p.k,
+                                BUF ? (unsigned)(qrow * sizeof(TT)) : 0u);
+  const unsigned lbase = (unsigned)(((long)h * p.d + i) * sizeof(TT));
+  const unsigned lpoison = (tc == 0 && i < p.d) ? 0u : OOB_OFF;
+  const unsigned ostep = (unsigned)((long)p.H * p.d * sizeof(TT));
   float dS[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) dS[c] = 0.0f;
@@ -371,10 +382,17 @@ __global__ __launch_bounds__(256) void dp_bwd_kernel(const DPArgs p) {
       for (int g = 0; g < NG; ++g)
         wsum[slot][w][g][lane] = rows4_scatter(vals[4 * g], vals[4 * g + 1], vals[4 * g + 2], vals[4 * g + 3]);
       pq = row16_sum(pq);
-      if (tc == 0) redb[slot][tr] = i < p.d ? err * sk : 0.0f;
-      if (s < p.TS && tc == 0 && i < p.d) {
-        st((TT*)p.dv, (((long)b * p.TS + s) * p.H + h) * p.d + i, bdk);
-        if (cl.at(tt)) st((TT*)p.dq, (((long)b * p.T + cl.tok(tt)) * p.H + h) * p.d + i, pq);
+      if constexpr (BUF) {
+        redb[slot][tr] = i < p.d ? err * sk : 0.0f;  // the row's 16 lanes hold the same value
+        // sub-steps past TS land past the batch row
+        bstore<TT>(r_dv, (lbase + (unsigned)s * ostep) | lpoison, bdk);
+        bstore<TT>(r_dq, (lbase + (unsigned)cl.tok(tt) * ostep) | lpoison | (cl.at(tt) ? 0u : OOB_OFF), pq);
+      } else {
+        if (tc == 0) redb[slot][tr] = i < p.d ? err * sk : 0.0f;
+        if (s < p.TS && tc == 0 && i < p.d) {
+          st((TT*)p.dv, (((long)b * p.TS + s) * p.H + h) * p.d + i, bdk);
+          if (cl.at(tt)) st((TT*)p.dq, (((long)b * p.T + cl.tok(tt)) * p.H + h) * p.d + i, pq);
+        }
       }
       if (slot == 0) {  // sub-steps s .. s + FS - 1 are in the slots: sum the waves, store
         __syncthreads();
@@ -476,8 +494,10 @@ int dp_launch(hipStream_t s, const DPArgs& a, bool bwd, int BH) {
 #define EDF_DP_LAUNCH(DP)                                       \
   do {                                                          \
     const dim3 grid(BH, DP / DPR_RB);                           \
-    if (bwd)                                                    \
-      dp_bwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);            \
+    if (bwd && (long)(a.TS + DPR_CK) * a.H * a.d * (long)sizeof(TT) < (1L << 31)) \
+      dp_bwd_kernel<TT, DP, true><<<grid, 256, 0, s>>>(a);      \
+    else if (bwd)                                               \
+      dp_bwd_kernel<TT, DP, false><<<grid, 256, 0, s>>>(a);     \
     else                                                        \
       dp_fwd_kernel<TT, DP><<<grid, 256, 0, s>>>(a);            \
   } while (0)
