@@ -150,7 +150,10 @@ EDF_DEVICE void rla_step(float (&S)[DP / 16], float (&R)[DP / 16], const RStage<
   }
 }
 
-template <typename TT, int DP, int VAR, int CK>
+// OB: p.out is set and stored through a buffer resource over the batch row by every lane (an
+// out-of-bounds offset where the lane stores nothing, steps past T past the row), so the
+// unrolled steps hold no branch around the store.
+template <typename TT, int DP, int VAR, int CK, bool OB>
 __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
   constexpr int NC = DP / 16;
   __shared__ RStage<CK, DP> sms[2];
@@ -159,6 +162,11 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
   const int rb = blockIdx.y, i = rb * RLA_RB + tr;
   const int b = (int)(bh / p.H), h = (int)(bh % p.H);
   const int nch = (p.T + CK - 1) / CK;
+  const long rowel = (long)p.T * p.H * p.d;
+  const rsrc_t r_out = make_rsrc(OB ? (const TT*)p.out + (long)b * rowel : (const TT*)p.k,
+                                 OB ? (unsigned)(rowel * sizeof(TT)) : 0u);
+  const unsigned obase = (tc == 0 && i < p.d) ? (unsigned)(((long)h * p.d + i) * sizeof(TT)) : OOB_OFF;
+  const unsigned ostep = (unsigned)((long)p.H * p.d * sizeof(TT));
   float S[NC], R[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) S[c] = R[c] = 0.0f;
@@ -173,12 +181,13 @@ __global__ __launch_bounds__(256) void rla_fwd_kernel(const RLAArgs p) {
 #pragma unroll
     for (int tt = 0; tt < CK; ++tt) {  // padding past T: identity steps (a = 1, b = g = 0, k = 0)
       rla_step<CK, DP, VAR>(S, R, sm, tt, tr, tc, p.clip);
-      if (p.out != nullptr) {
+      if (OB || p.out != nullptr) {
         float o = 0.0f;
 #pragma unroll
         for (int c = 0; c < NC; ++c) o = fmaf(S[c] + R[c], sm.q[tt][tc + 16 * c], o);
         o = row16_sum(o);
-        if (tc == 0 && i < p.d && t0 + tt < p.T) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
+        if constexpr (OB) bstore<TT>(r_out, obase + (unsigned)(t0 + tt) * ostep, o);
+        else if (tc == 0 && i < p.d && t0 + tt < p.T) st((TT*)p.out, (((long)b * p.T + t0 + tt) * p.H + h) * p.d + i, o);
       }
       // both states after every RLA_CK steps (a 16-step chunk writes two; none past the last)
       const int ck = (t0 + tt) / RLA_CK;
@@ -398,15 +407,20 @@ template <typename TT, int VAR>
 int rla_launch(hipStream_t s, const RLAArgs& a, int mode, int BH) {
   // mode 0: forward; 1: forward writing checkpoints every RLA_CK steps; 2: backward
   const int d = a.d;
+  const bool ob = a.out != nullptr && (long)(a.T + RLA_CKF) * a.H * a.d * (long)sizeof(TT) < (1L << 31);
 #define EDF_RLA_LAUNCH(DP)                                               \
   do {                                                                   \
     const dim3 grid(BH, DP / RLA_RB);                                    \
     if (mode == 2)                                                       \
       rla_bwd_kernel<TT, DP, VAR><<<grid, 256, 0, s>>>(a);               \
+    else if (mode == 1 && ob)                                            \
+      rla_fwd_kernel<TT, DP, VAR, RLA_CK, true><<<grid, 256, 0, s>>>(a); \
     else if (mode == 1)                                                  \
-      rla_fwd_kernel<TT, DP, VAR, RLA_CK><<<grid, 256, 0, s>>>(a);       \
+      rla_fwd_kernel<TT, DP, VAR, RLA_CK, false><<<grid, 256, 0, s>>>(a); \
+    else if (ob)                                                         \
+      rla_fwd_kernel<TT, DP, VAR, RLA_CKF, true><<<grid, 256, 0, s>>>(a); \
     else                                                                 \
-      rla_fwd_kernel<TT, DP, VAR, RLA_CKF><<<grid, 256, 0, s>>>(a);      \
+      rla_fwd_kernel<TT, DP, VAR, RLA_CKF, false><<<grid, 256, 0, s>>>(a); \
   } while (0)
   if (d <= 16)
     EDF_RLA_LAUNCH(16);
