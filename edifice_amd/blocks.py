@@ -172,9 +172,19 @@ class MambaBlock(nn.Module):
         xb = _LinearFn.apply(n, w[: self.inner], None if bias is None else bias[: self.inner])
         zb = _LinearFn.apply(n, w[self.inner:], None if bias is None else bias[self.inner:])
         xa = fs.causal_conv1d_silu(xb, self.dw_conv.weight, self.dw_conv.bias)
-        bc = self.bc_proj(xa).float()
+        # the B / C and low-rank dt projections as one product over their stacked weight rows:
+        # xa's gradient then gathers two contributions (this product and the scan), not three
+        n2 = 2 * self.state_size
+        w1, w2, b1, b2 = self.bc_proj.weight, self.dt_rank_proj.weight, self.bc_proj.bias, self.dt_rank_proj.bias
+        wcat = torch.cat([w1, w2], 0)
+        bcat = None
+        if b1 is not None or b2 is not None:  # a missing bias stacks as zeros
+            bcat = torch.cat([b1 if b1 is not None else w1.new_zeros(w1.shape[0]),
+                              b2 if b2 is not None else w2.new_zeros(w2.shape[0])], 0)
+        proj = _LinearFn.apply(xa, wcat, bcat)
+        bc = proj[..., :n2].float()
         b, c = bc[..., : self.state_size].contiguous(), bc[..., self.state_size:].contiguous()
-        dt = fs.softplus(self.dt_proj(self.dt_rank_proj(xa)))
+        dt = fs.softplus(self.dt_proj(proj[..., n2:]))
         y = fs.selective_scan(xa, dt.contiguous(), self.A.float(), b, c, None, zb,
                               dt_mode="mean")
         return self.out_proj(y)
