@@ -46,24 +46,6 @@ def _heads(t: torch.Tensor, num_heads: int) -> torch.Tensor:
     return t.reshape(bsz, seq, num_heads, hid // num_heads).contiguous()
 
 
-def _weight_grad(dy: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-    """dW = dy^T x over k rows.  For bf16 with many rows and a small [m, n] output the product
-    splits k into s slices, one batched product with float32 partials, summed and rounded once:
-    a single [m, n] product over k = 16 384 has too few output tiles for the GPU (the config-5
-    model's 1024 x 1024 weight gradients: 97-110 µs as one product, 57 µs in 8 slices)."""
-    k, m = dy.shape
-    n = x.shape[1]
-    s = 8 if m * n <= 1 << 20 else (4 if m * n <= 1 << 22 else 1)
-    if s == 1 or dy.dtype != torch.bfloat16 or k % s or k // s < 1024:
-        return dy.t().mm(x)
-    kc = k // s
-    a = dy.reshape(s, kc, m).transpose(1, 2)
-    b = x.reshape(s, kc, n).contiguous()  # the right operand stays a contiguous (non-transposed) tensor
-    part = torch.bmm(a, b, out_dtype=torch.float32)
-    # the s partials added in order and rounded to bf16 in one pass
-    return fs.column_sum(part.view(s, m * n), dy.dtype).view(m, n)
-
-
 class _LinearFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias):
@@ -79,12 +61,46 @@ class _LinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = dy2.mm(weight).view(x.shape)
         if ctx.needs_input_grad[1]:
-            dw = _weight_grad(dy2, x.reshape(-1, x.shape[-1]))
+            dw = fs.weight_grad(dy2, x.reshape(-1, x.shape[-1]))
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            # wide layers: the HIP column sum (torch's reduction reads [16384, 1024] bf16 at
-            # about 1.5 TB/s); narrow ones keep torch's
-            db = fs.column_sum(dy2) if dy2.shape[1] >= 256 and dy2.is_cuda else dy2.sum(0)
+            db = fs.bias_grad(dy2)
         return dx, dw, db
+
+
+class _LinearPair(torch.autograd.Function):
+    """y1, y2 = x W[:m1]^T + b[:m1], x W[m1:]^T + b[m1:]: one layer's output rows as two
+    products with contiguous outputs.  The backward adds the second product's input gradient
+    into the first's (addmm, no separate add) and writes the weight and bias gradients into
+    one buffer each (row slices of one output would each be scattered into a zero-filled
+    full-size gradient and added)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, m1):
+        b1, b2 = (None, None) if bias is None else (bias[:m1], bias[m1:])
+        ctx.save_for_backward(x, weight)
+        ctx.m1, ctx.has_bias = m1, bias is not None
+        return F.linear(x, weight[:m1], b1), F.linear(x, weight[m1:], b2)
+
+    @staticmethod
+    def backward(ctx, dy1, dy2):
+        x, weight = ctx.saved_tensors
+        m1 = ctx.m1
+        x2 = x.reshape(-1, x.shape[-1])
+        g1, g2 = dy1.reshape(-1, dy1.shape[-1]), dy2.reshape(-1, dy2.shape[-1])
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = g1.mm(weight[:m1])
+            dx.addmm_(g2, weight[m1:])
+            dx = dx.view(x.shape)
+        if ctx.needs_input_grad[1]:
+            dw = torch.empty_like(weight)
+            fs.weight_grad(g1, x2, out=dw[:m1])
+            fs.weight_grad(g2, x2, out=dw[m1:])
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            db = torch.empty(weight.shape[0], dtype=weight.dtype, device=weight.device)
+            fs.bias_grad(g1, out=db[:m1])
+            fs.bias_grad(g2, out=db[m1:])
+        return dx, dw, db, None
 
 
 class Linear(nn.Linear):
@@ -165,28 +181,18 @@ class MambaBlock(nn.Module):
         self.register_buffer("A", a[None, :].expand(inner, state_size).contiguous(), persistent=False)
 
     def forward(self, x):
-        # in_proj's two halves as two products over its weight rows: x and z come out
-        # contiguous, and their gradients land in one buffer each (slices of one [.., 2 inner]
-        # output would each be scattered into a zero-filled full-size gradient)
-        n, w, bias = self.norm(x), self.in_proj.weight, self.in_proj.bias
-        xb = _LinearFn.apply(n, w[: self.inner], None if bias is None else bias[: self.inner])
-        zb = _LinearFn.apply(n, w[self.inner:], None if bias is None else bias[self.inner:])
+        # in_proj's two halves as two products over its weight rows (x and z contiguous)
+        xb, zb = _LinearPair.apply(self.norm(x), self.in_proj.weight, self.in_proj.bias, self.inner)
         xa = fs.causal_conv1d_silu(xb, self.dw_conv.weight, self.dw_conv.bias)
-        # the B / C and low-rank dt projections as one product over their stacked weight rows:
-        # xa's gradient then gathers two contributions (this product and the scan), not three
-        n2 = 2 * self.state_size
+        # the B / C and low-rank dt projections as one product over their stacked weight rows
         w1, w2, b1, b2 = self.bc_proj.weight, self.dt_rank_proj.weight, self.bc_proj.bias, self.dt_rank_proj.bias
         wcat = torch.cat([w1, w2], 0)
         bcat = None
         if b1 is not None or b2 is not None:  # a missing bias stacks as zeros
             bcat = torch.cat([b1 if b1 is not None else w1.new_zeros(w1.shape[0]),
                               b2 if b2 is not None else w2.new_zeros(w2.shape[0])], 0)
-        proj = _LinearFn.apply(xa, wcat, bcat)
-        bc = proj[..., :n2].float()
-        b, c = bc[..., : self.state_size].contiguous(), bc[..., self.state_size:].contiguous()
-        dt = fs.softplus(self.dt_proj(proj[..., n2:]))
-        y = fs.selective_scan(xa, dt.contiguous(), self.A.float(), b, c, None, zb,
-                              dt_mode="mean")
+        y = fs.mamba_ssm(xa, wcat, bcat, self.dt_proj.weight, self.dt_proj.bias, self.A.float(), zb,
+                         self.state_size)
         return self.out_proj(y)
 
 
@@ -256,8 +262,9 @@ class GQAttention(nn.Module):
         q = self.q_proj(x).reshape(bsz, seq, nh, hd).transpose(1, 2).contiguous()
         k = self.k_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
         v = self.v_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
-        k = k.repeat_interleave(nh // nkv, dim=1).contiguous()
-        v = v.repeat_interleave(nh // nkv, dim=1).contiguous()
+        if nkv != nh:  # repeat_interleave copies even for one repeat
+            k, v = k.repeat_interleave(nh // nkv, dim=1), v.repeat_interleave(nh // nkv, dim=1)
+        k, v = k.contiguous(), v.contiguous()
         o = fs.flash_attention(q, k, v, causal=True)
         return self.out_proj(o.transpose(1, 2).reshape(bsz, seq, hid))
 

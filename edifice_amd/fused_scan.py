@@ -16,6 +16,7 @@ from __future__ import annotations
 import ctypes
 
 import torch
+import torch.nn.functional as F
 
 from . import _native as nat
 from ._native import EdificeHipError
@@ -448,25 +449,36 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor = None, bias: torch.Tensor 
     return _LayerNorm.apply(x, weight, bias, eps)
 
 
+def softplus_forward(x: torch.Tensor) -> torch.Tensor:
+    """softplus(x) by the HIP kernel, no autograd (``x`` made contiguous)."""
+    x = x.contiguous()
+    _dev(x)
+    y = torch.empty_like(x)
+    if x.numel():
+        nat.call("edf_softplus", _stream(), _p(x), _p(y), x.numel(), dtype_flag(x))
+    return y
+
+
+def softplus_backward(x: torch.Tensor, dy: torch.Tensor) -> torch.Tensor:
+    """dy sigmoid(x), the gradient of softplus at x (x contiguous, dy cast to x's dtype)."""
+    dy = dy.contiguous().to(x.dtype)
+    dx = torch.empty_like(x)
+    if x.numel():
+        nat.call("edf_softplus_backward", _stream(), _p(x), _p(dy), _p(dx), x.numel(), dtype_flag(x))
+    return dx
+
+
 class _Softplus(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x):
         x = x.contiguous()
-        _dev(x)
-        y = torch.empty_like(x)
-        if x.numel():
-            nat.call("edf_softplus", _stream(), _p(x), _p(y), x.numel(), dtype_flag(x))
         ctx.save_for_backward(x)
-        return y
+        return softplus_forward(x)
 
     @staticmethod
     def backward(ctx, dy):
         (x,) = ctx.saved_tensors
-        dy = dy.contiguous().to(x.dtype)
-        dx = torch.empty_like(x)
-        if x.numel():
-            nat.call("edf_softplus_backward", _stream(), _p(x), _p(dy), _p(dx), x.numel(), dtype_flag(x))
-        return dx
+        return softplus_backward(x, dy)
 
 
 def softplus(x: torch.Tensor) -> torch.Tensor:
@@ -509,14 +521,20 @@ def l2_normalize(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return _L2Normalize.apply(x, eps)
 
 
-def column_sum(x: torch.Tensor, out_dtype: torch.dtype = None) -> torch.Tensor:
+def column_sum(x: torch.Tensor, out_dtype: torch.dtype = None, out: torch.Tensor = None) -> torch.Tensor:
     """Sum over the rows of a 2-D ``x`` (float32 or bfloat16, f32 inside, fixed order): the
-    dense layers' bias gradients.  Not differentiable (a backward helper)."""
+    dense layers' bias gradients.  ``out``: a contiguous [cols] tensor to write (its dtype
+    then decides the output type).  Not differentiable (a backward helper)."""
     x = x.contiguous()
     _dev(x)
     _rank("x", x, 2)
     rows, cols = x.shape
-    out = torch.empty(cols, dtype=out_dtype or x.dtype, device=x.device)
+    if out is None:
+        out = torch.empty(cols, dtype=out_dtype or x.dtype, device=x.device)
+    elif out.shape != (cols,) or not out.is_contiguous() or out.dtype not in (torch.float32, torch.bfloat16):
+        raise EdificeHipError(f"column_sum: out must be a contiguous [{cols}] float32 or bfloat16 tensor")
+    else:
+        _dev(x, out)
     wsb = nat.query("edf_column_sum_workspace_bytes", rows, cols)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
     nat.call("edf_column_sum", _stream(), _p(x), _p(out), _p(ws), wsb, rows, cols, dtype_flag(x), dtype_flag(out))
@@ -531,34 +549,64 @@ def _u8(nbytes, like):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=like.device)
 
 
+def selective_scan_forward(x, dt, A, B, C, D, z, mode, keep_states):
+    """Run the fused selective scan (checked operands); returns (out, states), states the
+    per-chunk float32 carries the backward reads (None unless ``keep_states``)."""
+    x, dt, A, B, C, D, z = (_c(t) for t in (x, dt, A, B, C, D, z))
+    _rank("x", x, 3)
+    _rank("A", A, 2)
+    bsz, seq, dim = x.shape
+    n = A.shape[1]
+    _shape("dt", dt, x.shape)
+    _shape("z", z, x.shape)
+    _shape("A", A, (dim, n))
+    _shape("B", B, (bsz, seq, n))
+    _shape("C", C, (bsz, seq, n))
+    _shape("D", D, (dim,))
+    _dev(x, dt, A, B, C, D, z)
+    _same(x, dt, z)
+    _same(A, B, C, D)
+    io, par = dtype_flag(x), dtype_flag(A)
+    out = torch.empty_like(x)
+    states = None
+    if keep_states:
+        sb = nat.query("edf_selective_scan_states_bytes", bsz, seq, dim, n)
+        states = torch.empty(sb // 4, dtype=torch.float32, device=x.device)
+    wsb = nat.query("edf_selective_scan_workspace_bytes", bsz, seq, dim, n, mode)
+    ws = _u8(wsb, x) if wsb else None
+    nat.call("edf_fused_selective_scan", _stream(), _p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(out),
+             _p(states), _p(ws), wsb, bsz, seq, dim, n, io, par, mode)
+    return out, states
+
+
+def selective_scan_backward(x, dt, A, B, C, D, z, states, dout, mode):
+    """Gradients of the fused selective scan for the operands of ``selective_scan_forward``:
+    (dx, ddt, dA, dB, dC, dD, dz), dA / dB / dC / dD in float32, dD and dz None without D, z."""
+    dout = dout.contiguous().to(x.dtype)
+    bsz, seq, dim = x.shape
+    n = A.shape[1]
+    io, par = dtype_flag(x), dtype_flag(A)
+    f32 = dict(dtype=torch.float32, device=x.device)
+    dx, ddt = torch.empty_like(x), torch.empty_like(dt)
+    dA = torch.empty((dim, n), **f32)
+    dB = torch.empty((bsz, seq, n), **f32)
+    dC = torch.empty((bsz, seq, n), **f32)
+    dD = torch.empty((dim,), **f32) if D is not None else None
+    dz = torch.empty_like(z) if z is not None else None
+    wsb = nat.query("edf_selective_scan_backward_workspace_bytes", bsz, seq, dim, n, mode,
+                    int(states is not None))
+    ws = _u8(wsb, x)
+    nat.call("edf_fused_selective_scan_backward", _stream(), _p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z),
+             _p(dout), _p(states), _p(dx), _p(ddt), _p(dA), _p(dB), _p(dC), _p(dD), _p(dz), _p(ws), wsb,
+             bsz, seq, dim, n, io, par, mode)
+    return dx, ddt, dA, dB, dC, dD, dz
+
+
 class _SelectiveScan(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, dt, A, B, C, D, z, mode):
         x, dt, A, B, C, D, z = (_c(t) for t in (x, dt, A, B, C, D, z))
-        _rank("x", x, 3)
-        _rank("A", A, 2)
-        bsz, seq, dim = x.shape
-        n = A.shape[1]
-        _shape("dt", dt, x.shape)
-        _shape("z", z, x.shape)
-        _shape("A", A, (dim, n))
-        _shape("B", B, (bsz, seq, n))
-        _shape("C", C, (bsz, seq, n))
-        _shape("D", D, (dim,))
-        _dev(x, dt, A, B, C, D, z)
-        _same(x, dt, z)
-        _same(A, B, C, D)
-        io, par = dtype_flag(x), dtype_flag(A)
-        out = torch.empty_like(x)
-        need_grad = any(ctx.needs_input_grad[:7])
-        states = None
-        if need_grad:
-            sb = nat.query("edf_selective_scan_states_bytes", bsz, seq, dim, n)
-            states = torch.empty(sb // 4, dtype=torch.float32, device=x.device)
-        wsb = nat.query("edf_selective_scan_workspace_bytes", bsz, seq, dim, n, mode)
-        ws = _u8(wsb, x) if wsb else None
-        nat.call("edf_fused_selective_scan", _stream(), _p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z), _p(out),
-                 _p(states), _p(ws), wsb, bsz, seq, dim, n, io, par, mode)
+        out, states = selective_scan_forward(x, dt, A, B, C, D, z, mode, any(ctx.needs_input_grad[:7]))
         ctx.mode = mode
         ctx.save_for_backward(x, dt, A, B, C, D, z, states)
         return out
@@ -566,25 +614,93 @@ class _SelectiveScan(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         x, dt, A, B, C, D, z, states = ctx.saved_tensors
-        dout = dout.contiguous().to(x.dtype)
-        bsz, seq, dim = x.shape
-        n = A.shape[1]
-        io, par = dtype_flag(x), dtype_flag(A)
-        f32 = dict(dtype=torch.float32, device=x.device)
-        dx, ddt = torch.empty_like(x), torch.empty_like(dt)
-        dA = torch.empty((dim, n), **f32)
-        dB = torch.empty((bsz, seq, n), **f32)
-        dC = torch.empty((bsz, seq, n), **f32)
-        dD = torch.empty((dim,), **f32) if D is not None else None
-        dz = torch.empty_like(z) if z is not None else None
-        wsb = nat.query("edf_selective_scan_backward_workspace_bytes", bsz, seq, dim, n, ctx.mode,
-                        int(states is not None))
-        ws = _u8(wsb, x)
-        nat.call("edf_fused_selective_scan_backward", _stream(), _p(x), _p(dt), _p(A), _p(B), _p(C), _p(D), _p(z),
-                 _p(dout), _p(states), _p(dx), _p(ddt), _p(dA), _p(dB), _p(dC), _p(dD), _p(dz), _p(ws), wsb,
-                 bsz, seq, dim, n, io, par, ctx.mode)
+        dx, ddt, dA, dB, dC, dD, dz = selective_scan_backward(x, dt, A, B, C, D, z, states, dout, ctx.mode)
         cast = (lambda t, like: None if t is None else t.to(like.dtype))
         return dx, ddt, cast(dA, A), cast(dB, B), cast(dC, C), cast(dD, D), dz, None
+
+
+def weight_grad(dy: torch.Tensor, x: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """dW = dy^T x over k rows (into ``out``, a contiguous [m, n] tensor, when given).  For bf16
+    with many rows and a small [m, n] output the product splits k into s slices, one batched
+    product with float32 partials, summed and rounded once: a single [m, n] product over
+    k = 16 384 has too few output tiles for the GPU (the config-5 model's 1024 x 1024 weight
+    gradients: 97-110 µs as one product, 57 µs in 8 slices)."""
+    k, m = dy.shape
+    n = x.shape[1]
+    s = 8 if m * n <= 1 << 20 else (4 if m * n <= 1 << 22 else 1)
+    if s == 1 or dy.dtype != torch.bfloat16 or k % s or k // s < 1024:
+        return dy.t().mm(x) if out is None else torch.mm(dy.t(), x, out=out)
+    kc = k // s
+    a = dy.reshape(s, kc, m).transpose(1, 2)
+    b = x.reshape(s, kc, n).contiguous()  # the right operand stays a contiguous (non-transposed) tensor
+    part = torch.bmm(a, b, out_dtype=torch.float32)
+    # the s partials added in order and rounded to bf16 in one pass
+    return column_sum(part.view(s, m * n), dy.dtype, out=None if out is None else out.view(m * n)).view(m, n)
+
+
+def bias_grad(dy: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """Sum of dy's rows (the bias gradient), into ``out`` when given: wide layers take the HIP
+    column sum (torch's reduction reads [16384, 1024] bf16 at about 1.5 TB/s), narrow ones
+    keep torch's."""
+    if dy.is_cuda and dy.shape[1] >= 256:
+        return column_sum(dy, out=out)
+    r = dy.sum(0)
+    return r if out is None else out.copy_(r)
+
+
+class _MambaSSM(torch.autograd.Function):
+    """The Mamba block between its conv and out_proj (common.ex:333-471): one product of xa
+    over the stacked B / C and low-rank dt weights, B and C in float32, dt = softplus(dt_proj
+    (low-rank dt)), then the fused selective scan in dt-mean mode with the SiLU(z) gate.
+    One autograd node: the backward adds the projection's input gradient into the scan's
+    (addmm) and assembles the projection's output gradient in one buffer, where separate
+    torch ops would zero-fill and add a full-size gradient per slice."""
+
+    @staticmethod
+    def forward(ctx, xa, wcat, bcat, w_dt, b_dt, A, z, n_state):
+        bsz, seq, inner = xa.shape
+        x2 = xa.reshape(-1, inner)
+        proj = F.linear(x2, wcat, bcat)  # [rows, 2 N + dt_rank]
+        n2 = 2 * n_state
+        b = proj[:, :n_state].float().contiguous().view(bsz, seq, n_state)
+        c = proj[:, n_state:n2].float().contiguous().view(bsz, seq, n_state)
+        dt_pre = F.linear(proj[:, n2:], w_dt, b_dt)
+        dt = softplus_forward(dt_pre).view(bsz, seq, inner)
+        out, states = selective_scan_forward(xa, dt, A, b, c, None, z, SS_DT_MEAN, True)
+        ctx.save_for_backward(xa, wcat, proj, w_dt, dt_pre, dt, A, b, c, z, states)
+        ctx.n_state, ctx.has_bcat, ctx.has_bdt = n_state, bcat is not None, b_dt is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        xa, wcat, proj, w_dt, dt_pre, dt, A, b, c, z, states = ctx.saved_tensors
+        ns, n2 = ctx.n_state, 2 * ctx.n_state
+        rows, inner = dt_pre.shape
+        dxa, ddt, dA, dB, dC, _, dz = selective_scan_backward(xa, dt, A, b, c, None, z, states, dout,
+                                                                 SS_DT_MEAN)
+        ddt_pre = softplus_backward(dt_pre, ddt.view(rows, inner))
+        dproj = torch.empty_like(proj)
+        dproj[:, :ns].copy_(dB.view(rows, ns))
+        dproj[:, ns:n2].copy_(dC.view(rows, ns))
+        dproj[:, n2:].copy_(ddt_pre.mm(w_dt))
+        dxa.view(rows, inner).addmm_(dproj, wcat)
+        need = ctx.needs_input_grad
+        dwcat = weight_grad(dproj, xa.reshape(rows, inner)) if need[1] else None
+        dbcat = bias_grad(dproj) if ctx.has_bcat and need[2] else None
+        dw_dt = weight_grad(ddt_pre, proj[:, n2:]) if need[3] else None
+        db_dt = bias_grad(ddt_pre) if ctx.has_bdt and need[4] else None
+        dA = dA.to(A.dtype) if need[5] else None
+        return dxa, dwcat, dbcat, dw_dt, db_dt, dA, dz, None
+
+
+def mamba_ssm(xa, w_proj, b_proj, w_dt, b_dt, A, z, state_size: int):
+    """The Mamba block's selective SSM after its conv (common.ex:333-471, the B / C and dt
+    projections of :340-368 and the scan): xa [B, T, D] (model dtype); w_proj [2 N + R, D] the
+    stacked B, C and low-rank dt weights (b_proj [2 N + R] or None); w_dt [D, R] (b_dt [D] or
+    None) the dt up-projection; A [D, N] float32; z [B, T, D] the gate branch; N = state_size.
+    B and C are taken in float32, dt = softplus(dt_proj(.)), and the scan runs in dt-mean mode
+    with the SiLU(z) gate; returns y [B, T, D]."""
+    return _MambaSSM.apply(xa, w_proj, b_proj, w_dt, b_dt, A, z, state_size)
 
 
 class _FlashAttention(torch.autograd.Function):

@@ -162,12 +162,6 @@ class _OracleOps:
     by the oracle's autograd ops (float64 inside, inputs' dtypes outside)."""
 
     @staticmethod
-    def selective_scan(x, dt, a, b, c, d=None, z=None, *, dt_mode="channel"):
-        from oracle import blocks as ob
-        assert d is None and z is not None and dt_mode == "mean"
-        return ob._OracleSelectiveScanMean.apply(x, dt, a, b, c, z)
-
-    @staticmethod
     def delta_net_scan(q, k, v, beta):
         from oracle import blocks as ob
         return ob._OracleDelta.apply(q, k, v, beta)
@@ -192,12 +186,24 @@ class _OracleOps:
         return torch.nn.functional.layer_norm(x, (x.shape[-1],), weight, bias, eps)
 
     @staticmethod
-    def softplus(x):
-        return torch.nn.functional.softplus(x)
+    def mamba_ssm(xa, w_proj, b_proj, w_dt, b_dt, a, z, state_size):
+        from oracle import blocks as ob
+        proj = torch.nn.functional.linear(xa, w_proj, b_proj)
+        n2 = 2 * state_size
+        bc = proj[..., :n2].float()
+        b, c = bc[..., :state_size].contiguous(), bc[..., state_size:].contiguous()
+        dt = torch.nn.functional.softplus(torch.nn.functional.linear(proj[..., n2:], w_dt, b_dt))
+        return ob._OracleSelectiveScanMean.apply(xa, dt.contiguous(), a, b, c, z)
 
     @staticmethod
-    def column_sum(x, out_dtype=None):
-        return x.sum(0, dtype=out_dtype)
+    def weight_grad(dy, x, out=None):
+        r = dy.t().mm(x)
+        return r if out is None else out.copy_(r)
+
+    @staticmethod
+    def bias_grad(dy, out=None):
+        r = dy.sum(0)
+        return r if out is None else out.copy_(r)
 
     @staticmethod
     def l2_normalize(x, eps=1e-6):
@@ -207,8 +213,8 @@ class _OracleOps:
 def test_c5_hybrid_decoder_bf16_matches_oracle_ops(monkeypatch):
     """Config 5's model at reduced size in bfloat16 (the benchmark's precision): the same bf16
     model (same weights, the same torch bf16 GEMMs) run once on the HIP ops and once with the
-    oracle ops (and torch's layer norm, softplus, key norm, convolution, bias-gradient sums and
-    loss) swapped in, so the two runs differ only in the ops edifice_amd fuses.  Loss and every
+    oracle ops (and torch's layer norm, softplus, key norm, convolution, weight- and bias-gradient
+    products and loss) swapped in, so the two runs differ only in the ops edifice_amd fuses.  Loss and every
     parameter gradient within the bf16 tolerance."""
     import copy
 
