@@ -181,8 +181,12 @@ class MambaBlock(nn.Module):
         self.register_buffer("A", a[None, :].expand(inner, state_size).contiguous(), persistent=False)
 
     def forward(self, x):
+        return self.mix(self.norm(x))
+
+    def mix(self, n):
+        """The block after its norm: n = norm(x) -> the output the residual adds."""
         # in_proj's two halves as two products over its weight rows (x and z contiguous)
-        xb, zb = _LinearPair.apply(self.norm(x), self.in_proj.weight, self.in_proj.bias, self.inner)
+        xb, zb = _LinearPair.apply(n, self.in_proj.weight, self.in_proj.bias, self.inner)
         xa = fs.causal_conv1d_silu(xb, self.dw_conv.weight, self.dw_conv.bias)
         # the B / C and low-rank dt projections as one product over their stacked weight rows
         w1, w2, b1, b2 = self.bc_proj.weight, self.dt_rank_proj.weight, self.bc_proj.bias, self.dt_rank_proj.bias
@@ -207,12 +211,16 @@ class DeltaNetLayer(nn.Module):
         self.out_proj = Linear(hidden_size, hidden_size)
 
     def forward(self, x):
-        bsz, seq, hid = x.shape
-        q, k, v, bpre = torch.split(self.qkvb_proj(self.norm(x)), hid, dim=-1)
+        return x + self.mix(self.norm(x))
+
+    def mix(self, n):
+        """The layer after its norm: n = norm(x) -> the output the residual adds."""
+        bsz, seq, hid = n.shape
+        q, k, v, bpre = torch.split(self.qkvb_proj(n), hid, dim=-1)
         nh = self.num_heads
         o = fs.delta_net_scan(_heads(q, nh), _l2norm_keys(_heads(k, nh)), _heads(v, nh),
                               _heads(torch.sigmoid(bpre), nh))
-        return x + self.out_proj(o.reshape(bsz, seq, hid))
+        return self.out_proj(o.reshape(bsz, seq, hid))
 
 
 class GatedDeltaNetLayer(nn.Module):
@@ -282,7 +290,10 @@ class GQABlock(nn.Module):
 
     def forward(self, x):
         x = x + self.attn(self.attn_norm(x))
-        return x + self.ffn_down(F.gelu(self.ffn_up(self.ffn_norm(x))))
+        return x + self.ffn(self.ffn_norm(x))
+
+    def ffn(self, n):
+        return self.ffn_down(F.gelu(self.ffn_up(n)))
 
 
 class SequenceModel(nn.Module):
@@ -370,14 +381,17 @@ class HybridDecoder(nn.Module):
         self.lm_head = Linear(embed_size, vocab_size, bias=False)
 
     def forward(self, tokens: torch.Tensor) -> torch.Tensor:
+        # the stack as (norm, mix) stages h <- h + mix(norm h): each residual add runs with the
+        # next stage's norm (or the final norm) in one pass, fs.add_layer_norm
+        stages = [(b.norm, b.mix) for b in self.mamba] + [(b.norm, b.mix) for b in self.delta]
+        for b in self.attn:
+            stages += [(b.attn_norm, b.attn), (b.ffn_norm, b.ffn)]
         h = self.embed(tokens)
-        for blk in self.mamba:
-            h = h + blk(h)
-        for blk in self.delta:
-            h = blk(h)
-        for blk in self.attn:
-            h = blk(h)
-        return self.lm_head(self.final_norm(h))
+        n = stages[0][0](h)
+        for i, (_, mix) in enumerate(stages):
+            nxt = stages[i + 1][0] if i + 1 < len(stages) else self.final_norm
+            h, n = fs.add_layer_norm(h, mix(n), nxt.weight, nxt.bias, nxt.eps)
+        return self.lm_head(n)
 
     def loss(self, tokens: torch.Tensor) -> torch.Tensor:
         """Mean next-token cross entropy over tokens[:, 1:] (logits reduced in float32)."""

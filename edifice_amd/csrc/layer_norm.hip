@@ -18,6 +18,12 @@
 // pass.  The backward's waves keep per-column dgamma / dbeta sums in registers, summed over
 // the four waves of a workgroup in LDS into one partial per workgroup and over the
 // workgroups, in order, by two small kernels (deterministic, no atomics).
+//
+// Residual form (a pre-norm block stack's h' = h + f(norm h) followed by the next norm): the
+// forward takes the sum s = x + res rounded to the io dtype (what a separate add stores),
+// writes it and normalises it; the backward adds the gradient arriving at s from the residual
+// path to dx before its store (dx = LN'(dy) + grad_add, rounded once), so neither add is a pass
+// of its own.
 #include <math.h>
 #include <stdint.h>
 
@@ -73,10 +79,15 @@ EDF_DEVICE float wave_sum(float v) {
 // gamma / beta element c (1 / 0 when the parameter is absent)
 template <typename TP> EDF_DEVICE float pget(const TP* p, int c, float dflt) { return p ? to_f32(p[c]) : dflt; }
 
+// a + b rounded to T (the value a separate add in T stores), as f32
+template <typename T> EDF_DEVICE float add_rnd(float a, float b) { return to_f32(from_f32<T>(a + b)); }
+
 // ---- forward, row in registers: NV vectors of W elements per lane --------------------------
 // Each wave takes a stride of rows with gamma / beta of its columns in registers.
-template <typename T, typename TP, int NV>
-__global__ __launch_bounds__(LN_NT) void ln_fwd_kernel(const T* __restrict__ x, const TP* __restrict__ gamma,
+// RES: the row is x + res (rounded to T), also stored to sum
+template <typename T, typename TP, int NV, bool RES>
+__global__ __launch_bounds__(LN_NT) void ln_fwd_kernel(const T* __restrict__ x, const T* __restrict__ res,
+                                                      T* __restrict__ sum, const TP* __restrict__ gamma,
                                                       const TP* __restrict__ beta, T* __restrict__ y,
                                                       float* __restrict__ mean, float* __restrict__ rstd, int rows,
                                                       int cols, float eps) {
@@ -102,6 +113,13 @@ __global__ __launch_bounds__(LN_NT) void ln_fwd_kernel(const T* __restrict__ x, 
       const int c0 = (k * 64 + lane) * W;
       if (c0 < cols) {
         LnVec<T>::ld(xr + c0, v[k]);
+        if constexpr (RES) {
+          float rv[W];
+          LnVec<T>::ld(res + r * cols + c0, rv);
+#pragma unroll
+          for (int i = 0; i < W; ++i) v[k][i] = add_rnd<T>(v[k][i], rv[i]);
+          LnVec<T>::st(sum + r * cols + c0, v[k]);
+        }
       } else {
 #pragma unroll
         for (int i = 0; i < W; ++i) v[k][i] = 0.0f;
@@ -139,8 +157,10 @@ __global__ __launch_bounds__(LN_NT) void ln_fwd_kernel(const T* __restrict__ x, 
 }
 
 // ---- forward, any shape: one pass over memory per statistic --------------------------------
-template <typename T, typename TP>
-__global__ __launch_bounds__(LN_NT) void ln_fwd_any_kernel(const T* __restrict__ x, const TP* __restrict__ gamma,
+// RES: the sum x + res is formed and stored by the first pass, which the later passes read
+template <typename T, typename TP, bool RES>
+__global__ __launch_bounds__(LN_NT) void ln_fwd_any_kernel(const T* __restrict__ x, const T* __restrict__ res,
+                                                          T* __restrict__ sum, const TP* __restrict__ gamma,
                                                           const TP* __restrict__ beta, T* __restrict__ y,
                                                           float* __restrict__ mean, float* __restrict__ rstd, int rows,
                                                           int cols, float eps) {
@@ -149,7 +169,17 @@ __global__ __launch_bounds__(LN_NT) void ln_fwd_any_kernel(const T* __restrict__
   if (r >= rows) return;
   const T* xr = x + r * cols;
   float s = 0.0f;
-  for (int c = lane; c < cols; c += 64) s += to_f32(xr[c]);
+  if constexpr (RES) {
+    T* sr = sum + r * cols;
+    for (int c = lane; c < cols; c += 64) {
+      const T v = from_f32<T>(to_f32(xr[c]) + to_f32(res[r * cols + c]));
+      sr[c] = v;
+      s += to_f32(v);
+    }
+    xr = sr;  // each lane re-reads only the elements it wrote
+  } else {
+    for (int c = lane; c < cols; c += 64) s += to_f32(xr[c]);
+  }
   const float mu = wave_sum(s) / (float)cols;
   float q = 0.0f;
   for (int c = lane; c < cols; c += 64) {
@@ -168,11 +198,13 @@ __global__ __launch_bounds__(LN_NT) void ln_fwd_any_kernel(const T* __restrict__
 
 // ---- backward, row in registers -----------------------------------------------------------
 // part [LN_BWD_WG][2][cols]: this workgroup's dgamma (0) and dbeta (1) column sums
-template <typename T, typename TP, int NV>
+// GADD: dx = LN'(dy) + ga
+template <typename T, typename TP, int NV, bool GADD>
 __global__ __launch_bounds__(LN_NT) void ln_bwd_kernel(const T* __restrict__ x, const TP* __restrict__ gamma,
                                                       const float* __restrict__ mean, const float* __restrict__ rstd,
-                                                      const T* __restrict__ dy, T* __restrict__ dx,
-                                                      float* __restrict__ part, int rows, int cols) {
+                                                      const T* __restrict__ dy, const T* __restrict__ ga,
+                                                      T* __restrict__ dx, float* __restrict__ part, int rows,
+                                                      int cols) {
   constexpr int W = LnVec<T>::W;
   constexpr int NW = LN_NT / 64;
   __shared__ float s_acc[NW][2][NV * 64 * W];
@@ -223,6 +255,12 @@ __global__ __launch_bounds__(LN_NT) void ln_bwd_kernel(const T* __restrict__ x, 
       float o[W];
 #pragma unroll
       for (int i = 0; i < W; ++i) o[i] = rs * (g[k][i] - fmaf(xh[k][i], m2, m1));
+      if constexpr (GADD) {
+        float av[W];
+        LnVec<T>::ld(ga + r * cols + c0, av);
+#pragma unroll
+        for (int i = 0; i < W; ++i) o[i] += av[i];
+      }
       LnVec<T>::st(dr + c0, o);
     }
   }
@@ -246,12 +284,12 @@ __global__ __launch_bounds__(LN_NT) void ln_bwd_kernel(const T* __restrict__ x, 
 }
 
 // ---- backward, any shape ------------------------------------------------------------------
-template <typename T, typename TP>
+template <typename T, typename TP, bool GADD>
 __global__ __launch_bounds__(LN_NT) void ln_bwd_any_kernel(const T* __restrict__ x, const TP* __restrict__ gamma,
                                                           const float* __restrict__ mean,
                                                           const float* __restrict__ rstd, const T* __restrict__ dy,
-                                                          T* __restrict__ dx, float* __restrict__ part, int rows,
-                                                          int cols) {
+                                                          const T* __restrict__ ga, T* __restrict__ dx,
+                                                          float* __restrict__ part, int rows, int cols) {
   constexpr int NW = LN_NT / 64;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const float inv_c = 1.0f / (float)cols;
@@ -269,7 +307,8 @@ __global__ __launch_bounds__(LN_NT) void ln_bwd_any_kernel(const T* __restrict__
     T* dr = dx + r * cols;
     for (int c = lane; c < cols; c += 64) {
       const float g = to_f32(gr[c]) * pget(gamma, c, 1.0f);
-      dr[c] = from_f32<T>(rs * (g - fmaf((to_f32(xr[c]) - mu) * rs, m2, m1)));
+      const float o = rs * (g - fmaf((to_f32(xr[c]) - mu) * rs, m2, m1));
+      dr[c] = from_f32<T>(GADD ? o + to_f32(ga[r * cols + c]) : o);
     }
   }
   // column sums of this workgroup's rows (in row order per column)
@@ -327,44 +366,50 @@ int ln_nv(const void* x, const void* y, int cols) {
 
 inline int ln_bwd_groups(int rows) { return std::min((rows + LN_NT / 64 - 1) / (LN_NT / 64), LN_BWD_WG); }
 
-template <typename T, typename TP>
-int ln_fwd(hipStream_t s, const void* x, const void* gamma, const void* beta, void* y, float* mean, float* rstd,
-           int rows, int cols, float eps) {
+template <typename T, typename TP, bool RES>
+int ln_fwd(hipStream_t s, const void* x, const void* res, void* sum, const void* gamma, const void* beta, void* y,
+           float* mean, float* rstd, int rows, int cols, float eps) {
   const unsigned grid = (unsigned)((rows + LN_NT / 64 - 1) / (LN_NT / 64));
   const unsigned gridr = std::min(grid, (unsigned)LN_FWD_WG);
   const T* xp = (const T*)x;
+  const T* rp = (const T*)res;
+  T* sp = (T*)sum;
   const TP* gp = (const TP*)gamma;
   const TP* bp = (const TP*)beta;
   T* yp = (T*)y;
-  switch (ln_nv<T>(x, y, cols)) {
-    case 1: ln_fwd_kernel<T, TP, 1><<<gridr, LN_NT, 0, s>>>(xp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
-    case 2: ln_fwd_kernel<T, TP, 2><<<gridr, LN_NT, 0, s>>>(xp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
-    case 4: ln_fwd_kernel<T, TP, 4><<<gridr, LN_NT, 0, s>>>(xp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
+  const int nv = (RES && (((uintptr_t)res | (uintptr_t)sum) & 15)) ? 0 : ln_nv<T>(x, y, cols);
+  switch (nv) {
+    case 1: ln_fwd_kernel<T, TP, 1, RES><<<gridr, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
+    case 2: ln_fwd_kernel<T, TP, 2, RES><<<gridr, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
+    case 4: ln_fwd_kernel<T, TP, 4, RES><<<gridr, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
     case 8:
-      if constexpr (8 * LnVec<T>::W <= 32) ln_fwd_kernel<T, TP, 8><<<gridr, LN_NT, 0, s>>>(xp, gp, bp, yp, mean, rstd, rows, cols, eps);
+      if constexpr (8 * LnVec<T>::W <= 32)
+        ln_fwd_kernel<T, TP, 8, RES><<<gridr, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps);
       break;
-    default: ln_fwd_any_kernel<T, TP><<<grid, LN_NT, 0, s>>>(xp, gp, bp, yp, mean, rstd, rows, cols, eps);
+    default: ln_fwd_any_kernel<T, TP, RES><<<grid, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps);
   }
-  return check_launch("layer norm");
+  return check_launch(RES ? "add + layer norm" : "layer norm");
 }
 
-template <typename T, typename TP>
+template <typename T, typename TP, bool GADD>
 int ln_bwd(hipStream_t s, const void* x, const void* gamma, const float* mean, const float* rstd, const void* dy,
-           void* dx, void* dgamma, void* dbeta, float* part, int rows, int cols) {
+           const void* ga, void* dx, void* dgamma, void* dbeta, float* part, int rows, int cols) {
   const int nwg = ln_bwd_groups(rows);
   const T* xp = (const T*)x;
   const TP* gp = (const TP*)gamma;
   const T* dyp = (const T*)dy;
+  const T* gap = (const T*)ga;
   T* dxp = (T*)dx;
-  const int nv = ((uintptr_t)dy & 15) ? 0 : ln_nv<T>(x, dx, cols);
+  const int nv = (((uintptr_t)dy | (GADD ? (uintptr_t)ga : 0)) & 15) ? 0 : ln_nv<T>(x, dx, cols);
   switch (nv) {
-    case 1: ln_bwd_kernel<T, TP, 1><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, dxp, part, rows, cols); break;
-    case 2: ln_bwd_kernel<T, TP, 2><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, dxp, part, rows, cols); break;
-    case 4: ln_bwd_kernel<T, TP, 4><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, dxp, part, rows, cols); break;
+    case 1: ln_bwd_kernel<T, TP, 1, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols); break;
+    case 2: ln_bwd_kernel<T, TP, 2, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols); break;
+    case 4: ln_bwd_kernel<T, TP, 4, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols); break;
     case 8:
-      if constexpr (8 * LnVec<T>::W <= 32) ln_bwd_kernel<T, TP, 8><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, dxp, part, rows, cols);
+      if constexpr (8 * LnVec<T>::W <= 32)
+        ln_bwd_kernel<T, TP, 8, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols);
       break;
-    default: ln_bwd_any_kernel<T, TP><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, dxp, part, rows, cols);
+    default: ln_bwd_any_kernel<T, TP, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols);
   }
   int rc = check_launch("layer norm backward");
   if (rc || (!dgamma && !dbeta)) return rc;
@@ -406,7 +451,22 @@ int edf_layer_norm(void* stream, const void* x, const void* gamma, const void* b
   return ln_dtypes(dtype, param_dtype, [&](auto* ti, auto* tp) {
     using T = std::remove_pointer_t<decltype(ti)>;
     using TP = std::remove_pointer_t<decltype(tp)>;
-    return ln_fwd<T, TP>(s, x, gamma, beta, y, mean, rstd, rows, cols, eps);
+    return ln_fwd<T, TP, false>(s, x, nullptr, nullptr, gamma, beta, y, mean, rstd, rows, cols, eps);
+  });
+}
+
+int edf_add_layer_norm(void* stream, const void* x, const void* res, void* sum, const void* gamma, const void* beta,
+                       void* y, float* mean, float* rstd, int rows, int cols, float eps, int dtype, int param_dtype) {
+  using namespace edf;
+  int rc = ln_check(rows, cols, dtype, param_dtype);
+  if (rc) return rc;
+  EDF_REQUIRE(x && res && sum && y && mean && rstd, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  EDF_REQUIRE(eps >= 0.0f, EDF_ERR_INVALID_ARG, "eps must be non-negative");
+  hipStream_t s = as_stream(stream);
+  return ln_dtypes(dtype, param_dtype, [&](auto* ti, auto* tp) {
+    using T = std::remove_pointer_t<decltype(ti)>;
+    using TP = std::remove_pointer_t<decltype(tp)>;
+    return ln_fwd<T, TP, true>(s, x, res, sum, gamma, beta, y, mean, rstd, rows, cols, eps);
   });
 }
 
@@ -419,6 +479,14 @@ size_t edf_layer_norm_backward_workspace_bytes(int rows, int cols) {
 int edf_layer_norm_backward(void* stream, const void* x, const void* gamma, const float* mean, const float* rstd,
                             const void* grad_y, void* grad_x, void* grad_gamma, void* grad_beta, void* workspace,
                             size_t workspace_bytes, int rows, int cols, int dtype, int param_dtype) {
+  return edf_layer_norm_backward_add(stream, x, gamma, mean, rstd, grad_y, nullptr, grad_x, grad_gamma, grad_beta,
+                                     workspace, workspace_bytes, rows, cols, dtype, param_dtype);
+}
+
+int edf_layer_norm_backward_add(void* stream, const void* x, const void* gamma, const float* mean, const float* rstd,
+                                const void* grad_y, const void* grad_add, void* grad_x, void* grad_gamma,
+                                void* grad_beta, void* workspace, size_t workspace_bytes, int rows, int cols,
+                                int dtype, int param_dtype) {
   using namespace edf;
   int rc = ln_check(rows, cols, dtype, param_dtype);
   if (rc) return rc;
@@ -429,8 +497,10 @@ int edf_layer_norm_backward(void* stream, const void* x, const void* gamma, cons
   return ln_dtypes(dtype, param_dtype, [&](auto* ti, auto* tp) {
     using T = std::remove_pointer_t<decltype(ti)>;
     using TP = std::remove_pointer_t<decltype(tp)>;
-    return ln_bwd<T, TP>(s, x, gamma, mean, rstd, grad_y, grad_x, grad_gamma, grad_beta, (float*)workspace, rows,
-                         cols);
+    return grad_add ? ln_bwd<T, TP, true>(s, x, gamma, mean, rstd, grad_y, grad_add, grad_x, grad_gamma, grad_beta,
+                                          (float*)workspace, rows, cols)
+                    : ln_bwd<T, TP, false>(s, x, gamma, mean, rstd, grad_y, nullptr, grad_x, grad_gamma, grad_beta,
+                                           (float*)workspace, rows, cols);
   });
 }
 

@@ -449,6 +449,65 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor = None, bias: torch.Tensor 
     return _LayerNorm.apply(x, weight, bias, eps)
 
 
+class _AddLayerNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, res, weight, bias, eps):
+        x, res, weight, bias = _c(x), _c(res), _c(weight), _c(bias)
+        _dev(x, res, weight, bias)
+        _same(x, res)
+        if x.shape != res.shape:
+            raise EdificeHipError(f"add_layer_norm: x {tuple(x.shape)} and res {tuple(res.shape)} differ")
+        cols = x.shape[-1]
+        rows = x.numel() // max(cols, 1)
+        for name, t in (("weight", weight), ("bias", bias)):
+            if t is not None:
+                _shape(name, t, (cols,))
+        if weight is not None and bias is not None:
+            _same(weight, bias)
+        pt = weight if weight is not None else bias
+        total, y = torch.empty_like(x), torch.empty_like(x)
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+        nat.call("edf_add_layer_norm", _stream(), _p(x), _p(res), _p(total), _p(weight), _p(bias), _p(y), _p(mean),
+                 _p(rstd), rows, cols, float(eps), dtype_flag(x), dtype_flag(pt) if pt is not None else dtype_flag(x))
+        ctx.save_for_backward(total, weight, mean, rstd)
+        ctx.has_bias = bias is not None
+        ctx.pdtype = pt.dtype if pt is not None else x.dtype
+        ctx.set_materialize_grads(False)
+        return total, y
+
+    @staticmethod
+    def backward(ctx, dtotal, dy):
+        total, weight, mean, rstd = ctx.saved_tensors
+        cols = total.shape[-1]
+        rows = total.numel() // max(cols, 1)
+        if dy is None:  # the normalised output unused: the sum's gradient passes through
+            dx = torch.zeros_like(total) if dtotal is None else dtotal
+            zp = (lambda on: torch.zeros(cols, dtype=ctx.pdtype, device=total.device) if on else None)
+            return dx, dx, zp(weight is not None), zp(ctx.has_bias), None
+        dy = dy.contiguous().to(total.dtype)
+        ga = None if dtotal is None else dtotal.contiguous().to(total.dtype)
+        dx = torch.empty_like(total)
+        dw = torch.empty(cols, dtype=ctx.pdtype, device=total.device) if weight is not None else None
+        db = torch.empty(cols, dtype=ctx.pdtype, device=total.device) if ctx.has_bias else None
+        wsb = nat.query("edf_layer_norm_backward_workspace_bytes", rows, cols)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=total.device)
+        pflag = F32 if ctx.pdtype == torch.float32 else BF16
+        nat.call("edf_layer_norm_backward_add", _stream(), _p(total), _p(weight), _p(mean), _p(rstd), _p(dy), _p(ga),
+                 _p(dx), _p(dw), _p(db), _p(ws), wsb, rows, cols, dtype_flag(total), pflag)
+        return dx, dx, dw, db, None
+
+
+def add_layer_norm(x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor = None, bias: torch.Tensor = None,
+                   eps: float = 1e-5):
+    """(s, layer_norm(s)) with s = x + res: a pre-norm block stack's residual add and the next
+    block's norm in one pass (the residual adds of transformer_block.ex:118,144 and
+    common.ex:119 followed by Axon.layer_norm).  s is rounded to x's dtype as a separate add
+    stores it; the backward adds the gradient reaching s through the residual path into the
+    normalisation's input gradient in the same pass.  Shapes and dtypes as ``layer_norm``."""
+    return _AddLayerNorm.apply(x, res, weight, bias, eps)
+
+
 def softplus_forward(x: torch.Tensor) -> torch.Tensor:
     """softplus(x) by the HIP kernel, no autograd (``x`` made contiguous)."""
     x = x.contiguous()

@@ -588,6 +588,19 @@ size_t edf_layer_norm_backward_workspace_bytes(int rows, int cols);
 int edf_layer_norm_backward(void* stream, const void* x, const void* gamma, const float* mean, const float* rstd,
                             const void* grad_y, void* grad_x, void* grad_gamma, void* grad_beta, void* workspace,
                             size_t workspace_bytes, int rows, int cols, int dtype, int param_dtype);
+/* Residual form: the residual add in front of a pre-norm (transformer_block.ex:118,144,
+ * common.ex:119: h' = h + block(norm h), and the next block's norm of h').
+ * edf_add_layer_norm writes sum = x + res (rounded to dtype, as a separate add stores it; it may
+ * not alias x or res) and y = layer_norm(sum); mean / rstd as above, of sum.
+ * edf_layer_norm_backward_add is edf_layer_norm_backward (x = the sum) with grad_add [rows,
+ * cols] (the gradient reaching the sum through the residual path, may be NULL) added to
+ * grad_x before it is rounded and stored. */
+int edf_add_layer_norm(void* stream, const void* x, const void* res, void* sum, const void* gamma, const void* beta,
+                       void* y, float* mean, float* rstd, int rows, int cols, float eps, int dtype, int param_dtype);
+int edf_layer_norm_backward_add(void* stream, const void* x, const void* gamma, const float* mean, const float* rstd,
+                                const void* grad_y, const void* grad_add, void* grad_x, void* grad_gamma,
+                                void* grad_beta, void* workspace, size_t workspace_bytes, int rows, int cols,
+                                int dtype, int param_dtype);
 
 /* ------------------------------------------------------------------------
  * Softplus (block callers: the Mamba block's dt activation, Axon.activation(:softplus),

@@ -186,6 +186,11 @@ class _OracleOps:
         return torch.nn.functional.layer_norm(x, (x.shape[-1],), weight, bias, eps)
 
     @staticmethod
+    def add_layer_norm(x, res, weight=None, bias=None, eps=1e-5):
+        s = x + res
+        return s, torch.nn.functional.layer_norm(s, (s.shape[-1],), weight, bias, eps)
+
+    @staticmethod
     def mamba_ssm(xa, w_proj, b_proj, w_dt, b_dt, a, z, state_size):
         from oracle import blocks as ob
         proj = torch.nn.functional.linear(xa, w_proj, b_proj)

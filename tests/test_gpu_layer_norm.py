@@ -99,3 +99,67 @@ def test_layer_norm_matches_nn_layernorm_and_is_deterministic():
     assert_close(host(yv), host(torch.nn.functional.layer_norm(xv, (512,), w, None, 1e-5)), TOL[torch.float32],
                  "misaligned view")
     assert np.isfinite(host(yv)).all()
+
+
+ADD_CASES = [CASES[0], CASES[1], CASES[3], CASES[5], CASES[6], CASES[8]]
+
+
+@pytest.mark.parametrize("case", ADD_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_add_layer_norm(case):
+    """fs.add_layer_norm: the sum bit-identical to torch's add in the io dtype, y the float64
+    layer norm of that sum, and the input gradient LN'(dy) + (gradient reaching the sum), the
+    same for both addends; the parameter gradients as the plain layer norm's."""
+    from edifice_amd import fused_scan as fs
+    lead, cols, io, par, affine = case
+    announce("add_layer_norm", case=case)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(*lead, cols, generator=g) * 2.0 + 0.5).to(io)
+    r = torch.randn(*lead, cols, generator=g).to(io)
+    dy = torch.randn(*lead, cols, generator=g).to(io)
+    ds = torch.randn(*lead, cols, generator=g).to(io)
+    w = (1.0 + 0.3 * torch.randn(cols, generator=g)).to(par) if affine else None
+    b = (0.2 * torch.randn(cols, generator=g)).to(par) if affine else None
+    eps = 1e-5
+    xd, rd = x.cuda().requires_grad_(), r.cuda().requires_grad_()
+    wd = None if w is None else w.cuda().requires_grad_()
+    bd = None if b is None else b.cuda().requires_grad_()
+    s, y = fs.add_layer_norm(xd, rd, wd, bd, eps)
+    torch.autograd.backward([s, y], [ds.cuda(), dy.cuda()])
+    st = x + r  # torch's add in the io dtype
+    assert s.dtype == io and torch.equal(s.cpu(), st)
+    yr, dxr, dwr, dbr = _ref(st, w, b, dy, eps)
+    tol = max(TOL[io], TOL[par])
+    assert_close(host(y), yr.detach().numpy(), TOL[io], "y")
+    assert_close(host(xd.grad), (dxr + ds.double()).numpy(), TOL[io], "dx")
+    assert torch.equal(xd.grad, rd.grad)
+    if affine:
+        assert_close(host(wd.grad), dwr.numpy(), tol, "dgamma")
+        assert_close(host(bd.grad), dbr.numpy(), tol, "dbeta")
+
+
+def test_add_layer_norm_one_output_used():
+    """Only y used: dx is LN'(dy) alone; only the sum used: its gradient passes through and the
+    parameter gradients are zero.  A misaligned addend takes the any-shape kernels."""
+    from edifice_amd import fused_scan as fs
+    announce("add_layer_norm_one_output")
+    torch.manual_seed(6)
+    x = torch.randn(5, 256, device="cuda")
+    buf = torch.randn(1 + 5 * 256, device="cuda")
+    r = buf[1:].view(5, 256)  # not 16-byte aligned
+    w = torch.rand(256, device="cuda") + 0.5
+    dy = torch.randn(5, 256, device="cuda")
+    xd, rd, wd = x.clone().requires_grad_(), r.clone().requires_grad_(), w.clone().requires_grad_()
+    _, y = fs.add_layer_norm(xd, r, wd, None, 1e-5)
+    y.backward(dy)
+    xr, wr = (x + r).requires_grad_(), w.clone().requires_grad_()
+    yr = torch.nn.functional.layer_norm(xr, (256,), wr, None, 1e-5)
+    yr.backward(dy)
+    assert_close(host(y), host(yr), TOL[torch.float32], "y (misaligned addend)")
+    assert_close(host(xd.grad), host(xr.grad), TOL[torch.float32], "dx (y only)")
+    assert_close(host(wd.grad), host(wr.grad), TOL[torch.float32], "dgamma (y only)")
+    xd.grad = None
+    wd.grad = None
+    s, _ = fs.add_layer_norm(xd, rd, wd, None, 1e-5)
+    s.backward(dy)
+    assert torch.equal(xd.grad, dy) and torch.equal(rd.grad, dy)
+    assert torch.equal(wd.grad, torch.zeros_like(w))
