@@ -79,6 +79,28 @@ EDF_DEVICE float wave_sum(float v) {
 // gamma / beta element c (1 / 0 when the parameter is absent)
 template <typename TP> EDF_DEVICE float pget(const TP* p, int c, float dflt) { return p ? to_f32(p[c]) : dflt; }
 
+// W consecutive parameters from c0 (a 16-byte aligned parameter array, c0 a multiple of W) as
+// f32, or dflt for an absent parameter: one or two vector loads instead of W scalar ones
+template <typename TP, int W> EDF_DEVICE void pvec(const TP* p, int c0, float* o, float dflt) {
+  if (!p) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) o[i] = dflt;
+    return;
+  }
+  if constexpr (sizeof(TP) == 2) {
+    if constexpr (W == 8) {
+      LnVec<bf16>::ld(reinterpret_cast<const bf16*>(p) + c0, o);
+    } else {
+      const uint2 u = *reinterpret_cast<const uint2*>(p + c0);
+      o[0] = __builtin_bit_cast(float, u.x << 16), o[1] = __builtin_bit_cast(float, u.x & 0xffff0000u);
+      o[2] = __builtin_bit_cast(float, u.y << 16), o[3] = __builtin_bit_cast(float, u.y & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < W; j += 4) LnVec<float>::ld(reinterpret_cast<const float*>(p) + c0 + j, o + j);
+  }
+}
+
 // a + b rounded to T (the value a separate add in T stores), as f32
 template <typename T> EDF_DEVICE float add_rnd(float a, float b) { return to_f32(from_f32<T>(a + b)); }
 
@@ -96,13 +118,16 @@ __global__ __launch_bounds__(LN_NT) void ln_fwd_kernel(const T* __restrict__ x, 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float gm[NV][W], bt[NV][W];
 #pragma unroll
-  for (int k = 0; k < NV; ++k)
+  for (int k = 0; k < NV; ++k) {
+    const int c0 = (k * 64 + lane) * W;
+    if (c0 < cols) {
+      pvec<TP, W>(gamma, c0, gm[k], 1.0f);
+      pvec<TP, W>(beta, c0, bt[k], 0.0f);
+    } else {
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-      const int c = (k * 64 + lane) * W + i;
-      gm[k][i] = c < cols ? pget(gamma, c, 1.0f) : 0.0f;
-      bt[k][i] = c < cols ? pget(beta, c, 0.0f) : 0.0f;
+      for (int i = 0; i < W; ++i) gm[k][i] = bt[k][i] = 0.0f;
     }
+  }
   const float inv_c = 1.0f / (float)cols;
   for (long r = (long)blockIdx.x * NW + w; r < rows; r += (long)gridDim.x * NW) {
     const T* xr = x + r * cols;
@@ -211,13 +236,17 @@ __global__ __launch_bounds__(LN_NT) void ln_bwd_kernel(const T* __restrict__ x, 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float gm[NV][W], ag[NV][W], ab[NV][W];
 #pragma unroll
-  for (int k = 0; k < NV; ++k)
+  for (int k = 0; k < NV; ++k) {
+    const int c0 = (k * 64 + lane) * W;
+    if (c0 < cols) {
+      pvec<TP, W>(gamma, c0, gm[k], 1.0f);
+    } else {
 #pragma unroll
-    for (int i = 0; i < W; ++i) {
-      const int c = (k * 64 + lane) * W + i;
-      gm[k][i] = c < cols ? pget(gamma, c, 1.0f) : 0.0f;
-      ag[k][i] = ab[k][i] = 0.0f;
+      for (int i = 0; i < W; ++i) gm[k][i] = 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < W; ++i) ag[k][i] = ab[k][i] = 0.0f;
+  }
   const float inv_c = 1.0f / (float)cols;
   for (long r = (long)blockIdx.x * NW + w; r < rows; r += (long)gridDim.x * NW) {
     const T* xr = x + r * cols;
@@ -337,6 +366,7 @@ __global__ __launch_bounds__(256) void ln_reduce1_kernel(const float* __restrict
   if (e >= 2 * cols) return;
   const int k0 = blockIdx.y * LN_RS, k1 = min(nwg, k0 + LN_RS);
   float a = 0.0f;
+#pragma unroll 8
   for (int k = k0; k < k1; ++k) a += part[(long)k * 2 * cols + e];
   part2[(long)blockIdx.y * 2 * cols + e] = a;
 }
@@ -347,17 +377,18 @@ __global__ __launch_bounds__(256) void ln_reduce2_kernel(const float* __restrict
   const int e = blockIdx.x * 256 + threadIdx.x;
   if (e >= 2 * cols) return;
   float a = 0.0f;
+#pragma unroll 8
   for (int k = 0; k < nslice; ++k) a += part2[(long)k * 2 * cols + e];
   TP* dst = e < cols ? dgamma : dbeta;
   if (dst) dst[e < cols ? e : e - cols] = from_f32<TP>(a);
 }
 
 // vectors per lane for a row held in registers (at most 32 values per lane and array; 0:
-// the any-shape kernels)
+// the any-shape kernels); ptrs: every pointer the vector kernels read or write, OR-ed
 template <typename T>
-int ln_nv(const void* x, const void* y, int cols) {
+int ln_nv(uintptr_t ptrs, int cols) {
   constexpr int W = LnVec<T>::W;
-  if (cols % W != 0 || ((uintptr_t)x & 15) || ((uintptr_t)y & 15)) return 0;
+  if (cols % W != 0 || (ptrs & 15)) return 0;
   const int nvec = cols / W;
   for (int nv : {1, 2, 4, 8})
     if (nv * W <= 32 && nvec <= 64 * nv) return nv;
@@ -377,7 +408,8 @@ int ln_fwd(hipStream_t s, const void* x, const void* res, void* sum, const void*
   const TP* gp = (const TP*)gamma;
   const TP* bp = (const TP*)beta;
   T* yp = (T*)y;
-  const int nv = (RES && (((uintptr_t)res | (uintptr_t)sum) & 15)) ? 0 : ln_nv<T>(x, y, cols);
+  const int nv = ln_nv<T>((uintptr_t)x | (uintptr_t)y | (uintptr_t)res | (uintptr_t)sum | (uintptr_t)gamma |
+                             (uintptr_t)beta, cols);
   switch (nv) {
     case 1: ln_fwd_kernel<T, TP, 1, RES><<<gridr, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
     case 2: ln_fwd_kernel<T, TP, 2, RES><<<gridr, LN_NT, 0, s>>>(xp, rp, sp, gp, bp, yp, mean, rstd, rows, cols, eps); break;
@@ -400,7 +432,7 @@ int ln_bwd(hipStream_t s, const void* x, const void* gamma, const float* mean, c
   const T* dyp = (const T*)dy;
   const T* gap = (const T*)ga;
   T* dxp = (T*)dx;
-  const int nv = (((uintptr_t)dy | (GADD ? (uintptr_t)ga : 0)) & 15) ? 0 : ln_nv<T>(x, dx, cols);
+  const int nv = ln_nv<T>((uintptr_t)x | (uintptr_t)dx | (uintptr_t)dy | (uintptr_t)ga | (uintptr_t)gamma, cols);
   switch (nv) {
     case 1: ln_bwd_kernel<T, TP, 1, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols); break;
     case 2: ln_bwd_kernel<T, TP, 2, GADD><<<nwg, LN_NT, 0, s>>>(xp, gp, mean, rstd, dyp, gap, dxp, part, rows, cols); break;
