@@ -6,7 +6,9 @@
 // slice of rows for 128 columns (a wave reads two adjacent elements per lane, the four waves
 // of a workgroup take interleaved rows and are added in LDS), one float32 partial per slice;
 // then four waves per 64 columns split the slices and are added in LDS (with a single slice
-// the first stage writes the result).
+// the first stage writes the result).  Few rows (the float32 partials of a split product,
+// summed and rounded once): one pass, each thread summing 16 bytes of adjacent columns over
+// all rows in row order.
 #include <stdint.h>
 
 #include <algorithm>
@@ -21,6 +23,8 @@ constexpr int CS_NT = 256;
 constexpr int CS_CB = 128;        // columns per workgroup in stage 1 (two per lane)
 constexpr int CS_SLICES = 64;     // row slices at most (stage 2 reads 16 partials per thread)
 constexpr int CS_MIN_ROWS = 64;   // rows per slice at least
+constexpr int CS_FEW_ROWS = 32;   // at most this many rows: the one-pass column-vector kernel
+constexpr int CS_ROWS_WG = 8192;  // its workgroups at most (grid-stride beyond)
 
 template <typename T> EDF_DEVICE void ld2(const T* p, float& a, float& b);
 template <> EDF_DEVICE void ld2<bf16>(const bf16* p, float& a, float& b) {
@@ -69,6 +73,66 @@ __global__ __launch_bounds__(CS_NT) void cs_part_kernel(const T* __restrict__ x,
   }
 }
 
+// 16 bytes of T as f32 (VW = 16 / sizeof(T) values) and VW values stored as TO
+template <typename T> struct CsVec;
+template <> struct CsVec<float> {
+  static constexpr int VW = 4;
+  static EDF_DEVICE void ld(const float* p, float* a) {
+    const float4 f = *reinterpret_cast<const float4*>(p);
+    a[0] = f.x, a[1] = f.y, a[2] = f.z, a[3] = f.w;
+  }
+};
+template <> struct CsVec<bf16> {
+  static constexpr int VW = 8;
+  static EDF_DEVICE void ld(const bf16* p, float* a) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const unsigned w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      a[2 * i] = __builtin_bit_cast(float, w4[i] << 16);
+      a[2 * i + 1] = __builtin_bit_cast(float, w4[i] & 0xffff0000u);
+    }
+  }
+};
+template <typename TO, int VW> EDF_DEVICE void cs_stv(TO* p, const float* a) {
+  if constexpr (sizeof(TO) == 4) {
+#pragma unroll
+    for (int j = 0; j < VW; j += 4)
+      *reinterpret_cast<float4*>(p + j) = make_float4(a[j], a[j + 1], a[j + 2], a[j + 3]);
+  } else {
+    unsigned w[VW / 2];
+#pragma unroll
+    for (int i = 0; i < VW / 2; ++i)
+      w[i] = (unsigned)__builtin_bit_cast(unsigned short, (bf16)a[2 * i]) |
+             ((unsigned)__builtin_bit_cast(unsigned short, (bf16)a[2 * i + 1]) << 16);
+    if constexpr (VW == 8)
+      *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    else
+      *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+  }
+}
+
+// rows <= CS_FEW_ROWS, cols a multiple of VW, x and out 16-byte aligned: thread v sums columns
+// [v VW, (v + 1) VW) over rows 0, 1, ... in order
+template <typename T, typename TO>
+__global__ __launch_bounds__(CS_NT) void cs_rows_kernel(const T* __restrict__ x, TO* __restrict__ out, int rows,
+                                                       long cols) {
+  constexpr int VW = CsVec<T>::VW;
+  const long nvec = cols / VW;
+  for (long v = (long)blockIdx.x * CS_NT + threadIdx.x; v < nvec; v += (long)gridDim.x * CS_NT) {
+    float a[VW], b[VW];
+#pragma unroll
+    for (int i = 0; i < VW; ++i) a[i] = 0.0f;
+#pragma unroll 8
+    for (int r = 0; r < rows; ++r) {
+      CsVec<T>::ld(x + r * cols + v * VW, b);
+#pragma unroll
+      for (int i = 0; i < VW; ++i) a[i] += b[i];
+    }
+    cs_stv<TO, VW>(out + v * VW, a);
+  }
+}
+
 template <typename TO>
 __global__ __launch_bounds__(CS_NT) void cs_final_kernel(const float* __restrict__ part, TO* __restrict__ out,
                                                         int nslice, int cols) {
@@ -77,8 +141,10 @@ __global__ __launch_bounds__(CS_NT) void cs_final_kernel(const float* __restrict
   const int c = blockIdx.x * 64 + lane;
   const int per = (nslice + 3) / 4, k0 = w * per, k1 = std::min(nslice, k0 + per);
   float a = 0.0f;
-  if (c < cols)
+  if (c < cols) {
+#pragma unroll 8
     for (int k = k0; k < k1; ++k) a += part[(long)k * cols + c];
+  }
   s_acc[w][lane] = a;
   __syncthreads();
   if (w == 0 && c < cols) out[c] = from_f32<TO>(((s_acc[0][lane] + s_acc[1][lane]) + s_acc[2][lane]) + s_acc[3][lane]);
@@ -90,6 +156,13 @@ inline long cs_rows_per_slice(long rows, int /*cols*/) {
 
 template <typename T, typename TO>
 int cs_run(hipStream_t s, const void* x, void* out, long rows, int cols, float* part) {
+  constexpr int VW = CsVec<T>::VW;
+  if (rows <= CS_FEW_ROWS && cols % VW == 0 && !(((uintptr_t)x | (uintptr_t)out) & 15)) {
+    const long nvec = cols / VW;
+    const unsigned grid = (unsigned)std::min((nvec + CS_NT - 1) / CS_NT, (long)CS_ROWS_WG);
+    cs_rows_kernel<T, TO><<<grid, CS_NT, 0, s>>>((const T*)x, (TO*)out, (int)rows, cols);
+    return check_launch("column sum (few rows)");
+  }
   const long rps = cs_rows_per_slice(rows, cols);
   const int nslice = (int)((rows + rps - 1) / rps);
   const dim3 g1((cols + CS_CB - 1) / CS_CB, nslice);

@@ -56,7 +56,10 @@ COLSUM_CASES = [
     (1000, 301, torch.float32, torch.float32, 0),      # odd width: one element per lane
     (70, 256, torch.bfloat16, torch.bfloat16, 1),      # fewer rows than a slice, misaligned
     (1, 5, torch.float32, torch.bfloat16, 0),
-    (8, 1 << 20, torch.float32, torch.bfloat16, 0),  # split-product partials: one slice, direct output
+    (8, 1 << 20, torch.float32, torch.bfloat16, 0),  # split-product partials: the one-pass kernel
+    (4, 4096, torch.bfloat16, torch.float32, 0),     # one pass, bf16 in
+    (32, 1000, torch.float32, torch.float32, 0),     # one pass at its row limit
+    (3, 64, torch.float32, torch.bfloat16, 1),       # few rows but misaligned: the sliced kernels
 ]
 
 
