@@ -71,6 +71,8 @@ SIGNATURES = {
     "edf_column_sum": (I, [P, P, P, P, S, L, I, I, I]),
     "edf_l2_normalize": (I, [P, P, P, L, I, F, I]),
     "edf_l2_normalize_backward": (I, [P, P, P, P, L, I, F, I]),
+    "edf_delta_net_split": (I, [P, P, P, P, P, P, L, I, I, F, I]),
+    "edf_delta_net_split_backward": (I, [P, P, P, P, P, P, P, L, I, I, F, I]),
     "edf_laser_attention_workspace_bytes": (S, [I, I, I, I, I]),
     "edf_fused_laser_attention": (I, [P, P, P, P, P, P, P, P, S, I, I, I, I, I, I]),
     "edf_laser_attention_backward_workspace_bytes": (S, [I, I, I, I, I]),

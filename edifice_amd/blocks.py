@@ -216,10 +216,9 @@ class DeltaNetLayer(nn.Module):
     def mix(self, n):
         """The layer after its norm: n = norm(x) -> the output the residual adds."""
         bsz, seq, hid = n.shape
-        q, k, v, bpre = torch.split(self.qkvb_proj(n), hid, dim=-1)
-        nh = self.num_heads
-        o = fs.delta_net_scan(_heads(q, nh), _l2norm_keys(_heads(k, nh)), _heads(v, nh),
-                              _heads(torch.sigmoid(bpre), nh))
+        # q, l2norm(k), v, sigmoid(beta_pre) in the scan's head layout, one pass each way
+        q, k, v, beta = fs.delta_net_split(self.qkvb_proj(n), self.num_heads, KEY_NORM_EPS)
+        o = fs.delta_net_scan(q, k, v, beta)
         return self.out_proj(o.reshape(bsz, seq, hid))
 
 

@@ -6,10 +6,18 @@
 // (16-byte accesses: 8 bf16 or 4 f32 per lane and step, d up to 16 vectors per lane's share),
 // its sums by a row butterfly; rows whose length is not a multiple of the vector, or
 // misaligned tensors, take one element per lane and step.  The backward recomputes r from x.
+//
+// DeltaNet input split (delta_net.ex:274-300): the layer's projection [rows, 4 H d] holds
+// q | k | v | beta_pre per row; one pass writes q, the per-head L2-normalised k, v and
+// sigmoid(beta_pre) as [rows, H, d] tensors (the scan's layout), and the backward writes the
+// projection's gradient [rows, 4 H d] from dq, dk, dv, dbeta in one pass (k's norm and the
+// sigmoid recomputed from the projection), in place of head-layout copies, a separate norm,
+// a sigmoid and a concatenation.  One 16-lane row per (row, head).
 #include <math.h>
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "edf_abi.hpp"
 #include "edf_common.hpp"
@@ -146,6 +154,194 @@ int l2_run(hipStream_t s, const void* x, const void* dy, void* out, long rows, i
   return check_launch(BWD ? "l2 normalize backward" : "l2 normalize");
 }
 
+// 16 bytes copied unchanged
+EDF_DEVICE void cp16(const void* src, void* dst) {
+  *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+}
+
+// units = rows H (row, head) pairs, HD = H d; NV as l2_kernel (d <= 16 NV W), NV = 0: one
+// element per lane and step.  Forward: out[0..3] = q, k / |k|, v, sigmoid(beta_pre) [units, d].
+template <typename T, int NV>
+__global__ __launch_bounds__(L2_NT) void dnp_fwd_kernel(const T* __restrict__ proj, T* __restrict__ oq,
+                                                       T* __restrict__ ok, T* __restrict__ ov, T* __restrict__ ob,
+                                                       long units, int H, int d, float eps) {
+  constexpr int W = L2Vec<T>::W;
+  const int i16 = threadIdx.x & 15;
+  const long u = (long)blockIdx.x * (L2_NT / 16) + (threadIdx.x >> 4);
+  const bool live = u < units;  // dead rows compute on the last unit and store nothing
+  const long uu = live ? u : units - 1;
+  const long HD = (long)H * d;
+  const T* pr = proj + (uu / H) * 4 * HD + (uu % H) * d;  // this unit's q; k, v, beta_pre at +HD, +2HD, +3HD
+  const long ou = uu * d;
+  if constexpr (NV > 0) {
+    float kv[NV][W];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c0 = (k * 16 + i16) * W;
+      if (c0 < d) {
+        L2Vec<T>::ld(pr + HD + c0, kv[k]);
+        if (live) {
+          cp16(pr + c0, oq + ou + c0);
+          cp16(pr + 2 * HD + c0, ov + ou + c0);
+          float bv[W];
+          L2Vec<T>::ld(pr + 3 * HD + c0, bv);
+#pragma unroll
+          for (int i = 0; i < W; ++i) bv[i] = sigmoid_rcp(bv[i]);
+          L2Vec<T>::st(ob + ou + c0, bv);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) kv[k][i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < W; ++i) ss = fmaf(kv[k][i], kv[k][i], ss);
+    }
+    const float rn = 1.0f / sqrtf(row16_sum(ss) + eps);
+    if (!live) return;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c0 = (k * 16 + i16) * W;
+      if (c0 >= d) continue;
+      float o[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) o[i] = kv[k][i] * rn;
+      L2Vec<T>::st(ok + ou + c0, o);
+    }
+  } else {
+    float ss = 0.0f;
+    for (int c = i16; c < d; c += 16) {
+      const float a = to_f32(pr[HD + c]);
+      ss = fmaf(a, a, ss);
+    }
+    const float rn = 1.0f / sqrtf(row16_sum(ss) + eps);
+    if (!live) return;
+    for (int c = i16; c < d; c += 16) {
+      oq[ou + c] = pr[c];
+      ok[ou + c] = from_f32<T>(to_f32(pr[HD + c]) * rn);
+      ov[ou + c] = pr[2 * HD + c];
+      ob[ou + c] = from_f32<T>(sigmoid_rcp(to_f32(pr[3 * HD + c])));
+    }
+  }
+}
+
+// Backward: dproj [rows, 4 HD] from dq, dk, dv, dbeta [units, d]; dk through the norm
+// (dk_pre = r (dk - y <y, dk>), y = k r), dbeta through the sigmoid (dbeta s (1 - s)).
+template <typename T, int NV>
+__global__ __launch_bounds__(L2_NT) void dnp_bwd_kernel(const T* __restrict__ proj, const T* __restrict__ gq,
+                                                       const T* __restrict__ gk, const T* __restrict__ gv,
+                                                       const T* __restrict__ gb, T* __restrict__ dproj, long units,
+                                                       int H, int d, float eps) {
+  constexpr int W = L2Vec<T>::W;
+  const int i16 = threadIdx.x & 15;
+  const long u = (long)blockIdx.x * (L2_NT / 16) + (threadIdx.x >> 4);
+  const bool live = u < units;
+  const long uu = live ? u : units - 1;
+  const long HD = (long)H * d;
+  const long po = (uu / H) * 4 * HD + (uu % H) * d;
+  const T* pr = proj + po;
+  T* dr = dproj + po;
+  const long ou = uu * d;
+  if constexpr (NV > 0) {
+    float kv[NV][W], g[NV][W];
+    float ss = 0.0f, dot = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c0 = (k * 16 + i16) * W;
+      if (c0 < d) {
+        L2Vec<T>::ld(pr + HD + c0, kv[k]);
+        L2Vec<T>::ld(gk + ou + c0, g[k]);
+        if (live) {
+          cp16(gq + ou + c0, dr + c0);
+          cp16(gv + ou + c0, dr + 2 * HD + c0);
+          float bv[W], bg[W];
+          L2Vec<T>::ld(pr + 3 * HD + c0, bv);
+          L2Vec<T>::ld(gb + ou + c0, bg);
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            const float sg = sigmoid_rcp(bv[i]);
+            bv[i] = bg[i] * sg * (1.0f - sg);
+          }
+          L2Vec<T>::st(dr + 3 * HD + c0, bv);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) kv[k][i] = g[k][i] = 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        ss = fmaf(kv[k][i], kv[k][i], ss);
+        dot = fmaf(kv[k][i], g[k][i], dot);
+      }
+    }
+    const float rn = 1.0f / sqrtf(row16_sum(ss) + eps);
+    dot = row16_sum(dot) * rn;  // <y, dk>
+    if (!live) return;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int c0 = (k * 16 + i16) * W;
+      if (c0 >= d) continue;
+      float o[W];
+#pragma unroll
+      for (int i = 0; i < W; ++i) o[i] = rn * fmaf(-kv[k][i] * rn, dot, g[k][i]);
+      L2Vec<T>::st(dr + HD + c0, o);
+    }
+  } else {
+    float ss = 0.0f, dot = 0.0f;
+    for (int c = i16; c < d; c += 16) {
+      const float a = to_f32(pr[HD + c]);
+      ss = fmaf(a, a, ss);
+      dot = fmaf(a, to_f32(gk[ou + c]), dot);
+    }
+    const float rn = 1.0f / sqrtf(row16_sum(ss) + eps);
+    dot = row16_sum(dot) * rn;
+    if (!live) return;
+    for (int c = i16; c < d; c += 16) {
+      dr[c] = gq[ou + c];
+      dr[HD + c] = from_f32<T>(rn * fmaf(-to_f32(pr[HD + c]) * rn, dot, to_f32(gk[ou + c])));
+      dr[2 * HD + c] = gv[ou + c];
+      const float sg = sigmoid_rcp(to_f32(pr[3 * HD + c]));
+      dr[3 * HD + c] = from_f32<T>(to_f32(gb[ou + c]) * sg * (1.0f - sg));
+    }
+  }
+}
+
+// vectors per lane for a d-element row (0: one element per lane and step)
+template <typename T>
+int l2_nv(uintptr_t ptrs, int d) {
+  constexpr int W = L2Vec<T>::W;
+  if ((ptrs & 15) || d % W) return 0;
+  for (int c : {1, 2, 4, 8})
+    if (d / W <= 16 * c) return c;
+  return 0;
+}
+
+template <typename T>
+int dnp_run(hipStream_t s, bool bwd, const void* proj, const void* a0, const void* a1, const void* a2,
+            const void* a3, void* o0, void* o1, void* o2, void* o3, long rows, int H, int d, float eps) {
+  const long units = rows * H;
+  const unsigned grid = (unsigned)((units + L2_NT / 16 - 1) / (L2_NT / 16));
+  const uintptr_t ptrs = (uintptr_t)proj | (uintptr_t)a0 | (uintptr_t)a1 | (uintptr_t)a2 | (uintptr_t)a3 |
+                         (uintptr_t)o0 | (uintptr_t)o1 | (uintptr_t)o2 | (uintptr_t)o3;
+  const T* p = (const T*)proj;
+  auto launch = [&](auto nvc) {
+    constexpr int NV = decltype(nvc)::value;
+    if (bwd)
+      dnp_bwd_kernel<T, NV><<<grid, L2_NT, 0, s>>>(p, (const T*)a0, (const T*)a1, (const T*)a2, (const T*)a3,
+                                                   (T*)o0, units, H, d, eps);
+    else
+      dnp_fwd_kernel<T, NV><<<grid, L2_NT, 0, s>>>(p, (T*)o0, (T*)o1, (T*)o2, (T*)o3, units, H, d, eps);
+  };
+  switch (l2_nv<T>(ptrs, d)) {
+    case 1: launch(std::integral_constant<int, 1>{}); break;
+    case 2: launch(std::integral_constant<int, 2>{}); break;
+    case 4: launch(std::integral_constant<int, 4>{}); break;
+    case 8: launch(std::integral_constant<int, 8>{}); break;
+    default: launch(std::integral_constant<int, 0>{});
+  }
+  return check_launch(bwd ? "delta net split backward" : "delta net split");
+}
+
 int l2_check(long rows, int d, int dtype, float eps) {
   EDF_REQUIRE(rows > 0 && d > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
   EDF_REQUIRE(d <= L2_MAX_D, EDF_ERR_UNSUPPORTED, "rows of at most %d elements", L2_MAX_D);
@@ -178,6 +374,37 @@ int edf_l2_normalize_backward(void* stream, const void* x, const void* grad_y, v
   hipStream_t s = as_stream(stream);
   return dtype == EDF_BF16 ? l2_run<bf16, true>(s, x, grad_y, grad_x, rows, d, eps)
                            : l2_run<float, true>(s, x, grad_y, grad_x, rows, d, eps);
+}
+
+int edf_delta_net_split(void* stream, const void* proj, void* q, void* k, void* v, void* beta, long rows,
+                        int num_heads, int head_dim, float eps, int dtype) {
+  using namespace edf;
+  EDF_REQUIRE(num_heads > 0, EDF_ERR_INVALID_ARG, "num_heads must be positive");
+  int rc = l2_check(rows, head_dim, dtype, eps);
+  if (rc) return rc;
+  EDF_REQUIRE(proj && q && k && v && beta, EDF_ERR_INVALID_ARG, "null tensor pointer");
+  hipStream_t s = as_stream(stream);
+  return dtype == EDF_BF16
+             ? dnp_run<bf16>(s, false, proj, nullptr, nullptr, nullptr, nullptr, q, k, v, beta, rows, num_heads,
+                             head_dim, eps)
+             : dnp_run<float>(s, false, proj, nullptr, nullptr, nullptr, nullptr, q, k, v, beta, rows, num_heads,
+                              head_dim, eps);
+}
+
+int edf_delta_net_split_backward(void* stream, const void* proj, const void* grad_q, const void* grad_k,
+                                 const void* grad_v, const void* grad_beta, void* grad_proj, long rows,
+                                 int num_heads, int head_dim, float eps, int dtype) {
+  using namespace edf;
+  EDF_REQUIRE(num_heads > 0, EDF_ERR_INVALID_ARG, "num_heads must be positive");
+  int rc = l2_check(rows, head_dim, dtype, eps);
+  if (rc) return rc;
+  EDF_REQUIRE(proj && grad_q && grad_k && grad_v && grad_beta && grad_proj, EDF_ERR_INVALID_ARG,
+              "null tensor pointer");
+  hipStream_t s = as_stream(stream);
+  return dtype == EDF_BF16 ? dnp_run<bf16>(s, true, proj, grad_q, grad_k, grad_v, grad_beta, grad_proj, nullptr,
+                                           nullptr, nullptr, rows, num_heads, head_dim, eps)
+                           : dnp_run<float>(s, true, proj, grad_q, grad_k, grad_v, grad_beta, grad_proj, nullptr,
+                                            nullptr, nullptr, rows, num_heads, head_dim, eps);
 }
 
 }  // extern "C"

@@ -580,6 +580,43 @@ def l2_normalize(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return _L2Normalize.apply(x, eps)
 
 
+class _DeltaNetSplit(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, proj, num_heads, eps):
+        proj = proj.contiguous()
+        _dev(proj)
+        *lead, width = proj.shape
+        if width % (4 * num_heads):
+            raise EdificeHipError(f"delta_net_split: last dimension {width} is not 4 x num_heads x head_dim")
+        d = width // (4 * num_heads)
+        rows = proj.numel() // max(width, 1)
+        outs = [proj.new_empty(*lead, num_heads, d) for _ in range(4)]
+        if rows:
+            nat.call("edf_delta_net_split", _stream(), _p(proj), *(_p(t) for t in outs), rows, num_heads, d,
+                     float(eps), dtype_flag(proj))
+        ctx.save_for_backward(proj)
+        ctx.num_heads, ctx.d, ctx.eps = num_heads, d, eps
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv, db):
+        (proj,) = ctx.saved_tensors
+        rows = proj.numel() // max(proj.shape[-1], 1)
+        g = [t.contiguous().to(proj.dtype) for t in (dq, dk, dv, db)]
+        dproj = torch.empty_like(proj)
+        if rows:
+            nat.call("edf_delta_net_split_backward", _stream(), _p(proj), *(_p(t) for t in g), _p(dproj), rows,
+                     ctx.num_heads, ctx.d, float(ctx.eps), dtype_flag(proj))
+        return dproj, None, None
+
+
+def delta_net_split(proj: torch.Tensor, num_heads: int, eps: float = 1e-6):
+    """The DeltaNet layer's input split (delta_net.ex:274-300): proj [..., 4 H d] (the qkvb
+    projection, q | k | v | beta_pre) -> q, k / sqrt(sum_d k^2 + eps), v, sigmoid(beta_pre),
+    each [..., H, d], in one pass each way (float32 or bfloat16, f32 inside)."""
+    return _DeltaNetSplit.apply(proj, num_heads, eps)
+
+
 def column_sum(x: torch.Tensor, out_dtype: torch.dtype = None, out: torch.Tensor = None) -> torch.Tensor:
     """Sum over the rows of a 2-D ``x`` (float32 or bfloat16, f32 inside, fixed order): the
     dense layers' bias gradients.  ``out``: a contiguous [cols] tensor to write (its dtype

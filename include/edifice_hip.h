@@ -629,6 +629,16 @@ int edf_column_sum(void* stream, const void* x, void* out, void* workspace, size
 int edf_l2_normalize(void* stream, const void* x, void* y, long rows, int d, float eps, int dtype);
 int edf_l2_normalize_backward(void* stream, const void* x, const void* grad_y, void* grad_x, long rows, int d,
                               float eps, int dtype);
+/* DeltaNet input split (delta_net.ex:274-300): proj [rows, 4 H d] = q | k | v | beta_pre per
+ * row (the layer's qkvb projection); writes q, k / sqrt(sum_d k^2 + eps) per head, v and
+ * sigmoid(beta_pre), each [rows, H, d] (H = num_heads, d = head_dim <= 1024).  The backward
+ * writes grad_proj [rows, 4 H d] from the four [rows, H, d] gradients (k's norm and the sigmoid
+ * recomputed from proj). */
+int edf_delta_net_split(void* stream, const void* proj, void* q, void* k, void* v, void* beta, long rows,
+                        int num_heads, int head_dim, float eps, int dtype);
+int edf_delta_net_split_backward(void* stream, const void* proj, const void* grad_q, const void* grad_k,
+                                 const void* grad_v, const void* grad_beta, void* grad_proj, long rows,
+                                 int num_heads, int head_dim, float eps, int dtype);
 
 #ifdef __cplusplus
 }

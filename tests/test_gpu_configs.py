@@ -211,6 +211,13 @@ class _OracleOps:
         return r if out is None else out.copy_(r)
 
     @staticmethod
+    def delta_net_split(proj, num_heads, eps=1e-6):
+        q, k, v, bpre = torch.split(proj, proj.shape[-1] // 4, dim=-1)
+        heads = (lambda t: t.reshape(*t.shape[:-1], num_heads, -1).contiguous())
+        k = heads(k)
+        return heads(q), k / torch.sqrt((k * k).sum(-1, keepdim=True) + eps), heads(v), heads(torch.sigmoid(bpre))
+
+    @staticmethod
     def l2_normalize(x, eps=1e-6):
         return x / torch.sqrt((x * x).sum(-1, keepdim=True) + eps)
 

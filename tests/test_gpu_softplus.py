@@ -78,3 +78,46 @@ def test_l2_normalize(case):
     assert torch.isfinite(y).all() and torch.isfinite(xd.grad).all()
     assert_close(host(y), yr.detach().numpy(), TOL[dtype], "y")
     assert_close(host(xd.grad), xr.grad.numpy(), TOL[dtype], "dx")
+
+
+SPLIT_CASES = [
+    # (batch, seq, heads, head_dim, dtype, offset)
+    (2, 64, 8, 128, torch.bfloat16, 0),   # the config-5 layer's heads
+    (1, 37, 2, 64, torch.float32, 0),
+    (2, 9, 3, 256, torch.float32, 0),     # four vectors per lane
+    (1, 11, 2, 33, torch.float32, 0),     # off the vector: one element per lane
+    (1, 5, 2, 128, torch.bfloat16, 1),    # misaligned projection
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_delta_net_split(case):
+    """fs.delta_net_split against float64 torch (split, head reshape, per-head key L2 norm with eps
+    inside the square root, sigmoid of beta_pre): the four outputs and the projection's
+    gradient; q and v are copies (bit-identical) and so are their gradients."""
+    from edifice_amd import fused_scan as fs
+    bsz, seq, nh, d, dtype, off = case
+    announce("delta_net_split", case=case)
+    g = torch.Generator().manual_seed(21)
+    width = 4 * nh * d
+    p = torch.randn(bsz * seq * width, generator=g).to(dtype)
+    grads = [torch.randn(bsz, seq, nh, d, generator=g).to(dtype) for _ in range(4)]
+    buf = torch.zeros(p.numel() + off, dtype=dtype, device="cuda")
+    buf[off:] = p.cuda()
+    pd = buf[off:].view(bsz, seq, width).detach().requires_grad_()
+    outs = fs.delta_net_split(pd, nh, 1e-6)
+    torch.autograd.backward(outs, [t.cuda() for t in grads])
+    pr = p.double().view(bsz, seq, width).requires_grad_()
+    q, k, v, b = (t.reshape(bsz, seq, nh, d) for t in torch.split(pr, nh * d, dim=-1))
+    refs = (q, k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6), v, torch.sigmoid(b))
+    torch.autograd.backward(refs, [t.double() for t in grads])
+    for name, o, r in zip("qkvb", outs, refs):
+        assert o.shape == (bsz, seq, nh, d) and o.dtype == dtype
+        assert_close(host(o), r.detach().numpy(), TOL[dtype], name)
+    pv = p.view(bsz, seq, width)
+    assert torch.equal(outs[0].cpu(), pv[..., : nh * d].reshape(bsz, seq, nh, d))
+    assert torch.equal(outs[2].cpu(), pv[..., 2 * nh * d: 3 * nh * d].reshape(bsz, seq, nh, d))
+    assert_close(host(pd.grad), pr.grad.numpy(), TOL[dtype], "dproj")
+    gp = pd.grad.cpu()
+    assert torch.equal(gp[..., : nh * d], grads[0].reshape(bsz, seq, nh * d))
+    assert torch.equal(gp[..., 2 * nh * d: 3 * nh * d], grads[2].reshape(bsz, seq, nh * d))
