@@ -111,6 +111,16 @@ class Linear(nn.Linear):
         return _LinearFn.apply(x, self.weight, self.bias)
 
 
+class Embedding(nn.Embedding):
+    """nn.Embedding (same parameter and state-dict name) whose weight gradient is the HIP
+    kernel, ``fs.embedding`` (Axon.embedding of the reference language models)."""
+
+    def forward(self, ids):
+        if self.max_norm is not None or self.scale_grad_by_freq or self.sparse:
+            raise ValueError("Embedding: max_norm, scale_grad_by_freq and sparse are not supported")
+        return fs.embedding(ids, self.weight, self.padding_idx)
+
+
 class LayerNorm(nn.LayerNorm):
     """nn.LayerNorm over the last dimension (same parameters and state-dict names) run by the
     HIP layer norm, ``fs.layer_norm``: Axon.layer_norm of the reference blocks
@@ -371,7 +381,7 @@ class HybridDecoder(nn.Module):
                  delta_layers: int = 2, attn_layers: int = 2, num_heads: int = 8, state_size: int = 16,
                  expand_factor: int = 2, conv_size: int = 4):
         super().__init__()
-        self.embed = nn.Embedding(vocab_size, embed_size)
+        self.embed = Embedding(vocab_size, embed_size)
         self.mamba = nn.ModuleList(MambaBlock(embed_size, state_size, expand_factor, conv_size)
                                    for _ in range(mamba_layers))
         self.delta = nn.ModuleList(DeltaNetLayer(embed_size, num_heads) for _ in range(delta_layers))

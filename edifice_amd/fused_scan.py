@@ -617,6 +617,38 @@ def delta_net_split(proj: torch.Tensor, num_heads: int, eps: float = 1e-6):
     return _DeltaNetSplit.apply(proj, num_heads, eps)
 
 
+class _Embedding(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ids, weight, padding_idx):
+        out = torch.nn.functional.embedding(ids, weight, padding_idx)
+        ctx.save_for_backward(ids)
+        ctx.vocab, ctx.padding_idx = weight.shape[0], padding_idx
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        (ids,) = ctx.saved_tensors
+        dim = dy.shape[-1]
+        g = dy.contiguous().reshape(-1, dim)
+        flat = ids.contiguous().reshape(-1).to(torch.int64)
+        _dev(g, flat)
+        n = flat.numel()
+        dw = g.new_empty(ctx.vocab, dim)
+        wsb = nat.query("edf_embedding_backward_workspace_bytes", n, ctx.vocab)
+        ws = _u8(wsb, g)
+        pad = -1 if ctx.padding_idx is None else int(ctx.padding_idx) % ctx.vocab
+        nat.call("edf_embedding_backward", _stream(), _p(flat), _p(g), _p(dw), _p(ws), wsb, n, ctx.vocab, dim, pad,
+                 dtype_flag(g))
+        return None, dw, None
+
+
+def embedding(ids: torch.Tensor, weight: torch.Tensor, padding_idx: int = None) -> torch.Tensor:
+    """``F.embedding(ids, weight, padding_idx)`` whose weight gradient is the HIP kernel
+    (deterministic, every row written): the language models' token embedding (Axon.embedding,
+    e.g. show_o.ex:123).  weight float32 or bfloat16; no max_norm / scale_grad_by_freq."""
+    return _Embedding.apply(ids, weight, padding_idx)
+
+
 def column_sum(x: torch.Tensor, out_dtype: torch.dtype = None, out: torch.Tensor = None) -> torch.Tensor:
     """Sum over the rows of a 2-D ``x`` (float32 or bfloat16, f32 inside, fixed order): the
     dense layers' bias gradients.  ``out``: a contiguous [cols] tensor to write (its dtype

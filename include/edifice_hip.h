@@ -603,6 +603,19 @@ int edf_layer_norm_backward_add(void* stream, const void* x, const void* gamma, 
                                 int dtype, int param_dtype);
 
 /* ------------------------------------------------------------------------
+ * Token-embedding weight gradient (block callers: the language models' input embedding,
+ * Axon.embedding, e.g. lib/edifice/generative/show_o.ex:123):
+ *   grad_weight[v, :] = sum over positions p with ids[p] == v (ascending p) of grad[p, :]
+ * ids [n] int64, grad [n, dim] and grad_weight [vocab, dim] in dtype; every row of
+ * grad_weight is written (0 where no position names it, and for padding_idx; -1: none); ids
+ * outside [0, vocab) contribute nothing.  Deterministic (stable sort of the ids, fixed
+ * summation order); workspace edf_embedding_backward_workspace_bytes(n, vocab).
+ * ------------------------------------------------------------------------ */
+size_t edf_embedding_backward_workspace_bytes(long n, long vocab);
+int edf_embedding_backward(void* stream, const int64_t* ids, const void* grad, void* grad_weight, void* workspace,
+                           size_t workspace_bytes, long n, long vocab, int dim, long padding_idx, int dtype);
+
+/* ------------------------------------------------------------------------
  * Softplus (block callers: the Mamba block's dt activation, Axon.activation(:softplus),
  * lib/edifice/ssm/common.ex:366): y = log(1 + e^x) over n values of x in dtype (evaluated as
  * max(x, 0) + log1p(e^-|x|), f32 inside); the backward writes grad_x = grad_y sigmoid(x).

@@ -186,6 +186,10 @@ class _OracleOps:
         return torch.nn.functional.layer_norm(x, (x.shape[-1],), weight, bias, eps)
 
     @staticmethod
+    def embedding(ids, weight, padding_idx=None):
+        return torch.nn.functional.embedding(ids, weight, padding_idx)
+
+    @staticmethod
     def add_layer_norm(x, res, weight=None, bias=None, eps=1e-5):
         s = x + res
         return s, torch.nn.functional.layer_norm(s, (s.shape[-1],), weight, bias, eps)
