@@ -65,6 +65,8 @@ SIGNATURES = {
     "edf_layer_norm_backward": (I, [P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
     "edf_add_layer_norm": (I, [P, P, P, P, P, P, P, P, P, I, I, F, I, I]),
     "edf_layer_norm_backward_add": (I, [P, P, P, P, P, P, P, P, P, P, P, S, I, I, I, I]),
+    "edf_heads_split": (I, [P, P, P, L, L, I, I, I, I]),
+    "edf_heads_merge": (I, [P, P, P, L, L, I, I, I, I]),
     "edf_embedding_backward_workspace_bytes": (S, [L, L]),
     "edf_embedding_backward": (I, [P, P, P, P, P, S, L, L, I, L, I]),
     "edf_softplus": (I, [P, P, P, L, I]),

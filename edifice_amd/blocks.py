@@ -276,14 +276,23 @@ class GQAttention(nn.Module):
         bsz, seq, hid = x.shape
         nh, nkv = self.num_heads, self.num_kv_heads
         hd = hid // nh
-        q = self.q_proj(x).reshape(bsz, seq, nh, hd).transpose(1, 2).contiguous()
-        k = self.k_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
-        v = self.v_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
-        if nkv != nh:  # repeat_interleave copies even for one repeat
-            k, v = k.repeat_interleave(nh // nkv, dim=1), v.repeat_interleave(nh // nkv, dim=1)
-        k, v = k.contiguous(), v.contiguous()
+        if nkv == nh:
+            # q, k, v as one product over the stacked weights, split into the kernel's head
+            # layout in one pass (the backward merges dq, dk, dv into one gradient, no adds)
+            projs = (self.q_proj, self.k_proj, self.v_proj)
+            w = torch.cat([m.weight for m in projs], 0)
+            b = None
+            if any(m.bias is not None for m in projs):
+                b = torch.cat([m.bias if m.bias is not None else m.weight.new_zeros(hid) for m in projs], 0)
+            q, k, v = fs.split_heads(_LinearFn.apply(x, w, b), 3, nh)
+        else:
+            q = self.q_proj(x).reshape(bsz, seq, nh, hd).transpose(1, 2).contiguous()
+            k = self.k_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
+            v = self.v_proj(x).reshape(bsz, seq, nkv, hd).transpose(1, 2)
+            k = k.repeat_interleave(nh // nkv, dim=1).contiguous()
+            v = v.repeat_interleave(nh // nkv, dim=1).contiguous()
         o = fs.flash_attention(q, k, v, causal=True)
-        return self.out_proj(o.transpose(1, 2).reshape(bsz, seq, hid))
+        return self.out_proj(fs.merge_heads(o))
 
 
 class GQABlock(nn.Module):

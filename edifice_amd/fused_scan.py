@@ -617,6 +617,73 @@ def delta_net_split(proj: torch.Tensor, num_heads: int, eps: float = 1e-6):
     return _DeltaNetSplit.apply(proj, num_heads, eps)
 
 
+def _ptr_array(ts):
+    arr = (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+    return ctypes.cast(arr, ctypes.c_void_p), arr
+
+
+def _heads_split(x, parts, num_heads):
+    bsz, seq, width = x.shape
+    d = width // (parts * num_heads)
+    outs = [x.new_empty(bsz, num_heads, seq, d) for _ in range(parts)]
+    if x.numel():
+        ptr, keep = _ptr_array(outs)
+        nat.call("edf_heads_split", _stream(), _p(x), ptr, bsz, seq, parts, num_heads, d, dtype_flag(x))
+    return outs
+
+
+def _heads_merge(ts):
+    bsz, nh, seq, d = ts[0].shape
+    y = ts[0].new_empty(bsz, seq, len(ts) * nh * d)
+    if y.numel():
+        ptr, keep = _ptr_array(ts)
+        nat.call("edf_heads_merge", _stream(), ptr, _p(y), bsz, seq, len(ts), nh, d, dtype_flag(y))
+    return y
+
+
+class _SplitHeads(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, parts, num_heads):
+        x = x.contiguous()
+        _dev(x)
+        _rank("x", x, 3)
+        if x.shape[-1] % (parts * num_heads):
+            raise EdificeHipError(f"split_heads: last dimension {x.shape[-1]} is not parts x num_heads x head_dim")
+        return tuple(_heads_split(x, parts, num_heads))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        g = [t.contiguous() for t in grads]
+        _dev(*g)
+        return _heads_merge(g), None, None
+
+
+class _MergeHeads(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        x = x.contiguous()
+        _dev(x)
+        _rank("x", x, 4)
+        ctx.num_heads = x.shape[1]
+        return _heads_merge([x])
+
+    @staticmethod
+    def backward(ctx, dy):
+        return _heads_split(dy.contiguous(), 1, ctx.num_heads)[0]
+
+
+def split_heads(x: torch.Tensor, parts: int, num_heads: int):
+    """[B, T, P H d] (P stacked projections, e.g. q | k | v) -> P tensors [B, H, T, d], the
+    attention kernels' layout, in one pass (and its backward in one pass): the attention
+    blocks' head split (Nx reshape + transpose in the reference, e.g. transformer_block.ex:118)."""
+    return _SplitHeads.apply(x, parts, num_heads)
+
+
+def merge_heads(x: torch.Tensor) -> torch.Tensor:
+    """[B, H, T, d] -> [B, T, H d], one pass each way: the attention output's head merge."""
+    return _MergeHeads.apply(x)
+
+
 class _Embedding(torch.autograd.Function):
     @staticmethod
     def forward(ctx, ids, weight, padding_idx):

@@ -603,6 +603,18 @@ int edf_layer_norm_backward_add(void* stream, const void* x, const void* gamma, 
                                 int dtype, int param_dtype);
 
 /* ------------------------------------------------------------------------
+ * Head layout around the attention kernels (block callers: the attention blocks' head split
+ * and merge, Nx reshapes / transposes in the reference, e.g. transformer_block.ex:118):
+ *   edf_heads_split: x [batch, seq, P H d] -> parts[p] [batch, H, seq, d], p < P
+ *   edf_heads_merge: parts[p] [batch, H, seq, d] -> y [batch, seq, P H d]
+ * parts: a host array of num_parts (1..4) device pointers; H = num_heads, d = head_dim.
+ * ------------------------------------------------------------------------ */
+int edf_heads_split(void* stream, const void* x, void* const* parts, long batch, long seq, int num_parts,
+                    int num_heads, int head_dim, int dtype);
+int edf_heads_merge(void* stream, const void* const* parts, void* y, long batch, long seq, int num_parts,
+                    int num_heads, int head_dim, int dtype);
+
+/* ------------------------------------------------------------------------
  * Token-embedding weight gradient (block callers: the language models' input embedding,
  * Axon.embedding, e.g. lib/edifice/generative/show_o.ex:123):
  *   grad_weight[v, :] = sum over positions p with ids[p] == v (ascending p) of grad[p, :]

@@ -186,6 +186,15 @@ class _OracleOps:
         return torch.nn.functional.layer_norm(x, (x.shape[-1],), weight, bias, eps)
 
     @staticmethod
+    def split_heads(x, parts, num_heads):
+        bsz, seq, width = x.shape
+        return x.reshape(bsz, seq, parts, num_heads, -1).permute(2, 0, 3, 1, 4).contiguous().unbind(0)
+
+    @staticmethod
+    def merge_heads(x):
+        return x.transpose(1, 2).reshape(x.shape[0], x.shape[2], -1)
+
+    @staticmethod
     def embedding(ids, weight, padding_idx=None):
         return torch.nn.functional.embedding(ids, weight, padding_idx)
 

@@ -60,3 +60,4 @@ def test_embedding_module_in_model():
     m(ids).backward(dy)
     ref(ids).backward(dy)
     assert_close(host(m.weight.grad), host(ref.weight.grad), TOL[torch.float32], "dW vs nn.Embedding")
+
