@@ -9,7 +9,9 @@
 //   range, dB, dC), extended with dA, dD and the silu(z) gate, which have no reference
 //   kernel counterpart (the Mamba block applies them outside the scan,
 //   common.ex:270-278).
-//   Optional extensions: y += D[d] x, then y *= silu(z).
+//   Optional extensions: y += D[d] x, then y *= silu(z); in dt-mean mode, dt given before its
+//   softplus (the EDF_SS_DT_SOFTPLUS mode flag: softplus(dt) wherever dt is read, grad_dt
+//   with respect to the pre-activation).
 //
 // Design.  The op is VALU-bound: per (b, t, d, n) element the forward needs one
 // v_exp_f32 and four other VALU ops, several times the HBM time at config-2 size, so the
@@ -82,7 +84,8 @@ struct SSArgs {
   float* part_d;   // [batch, dim]
   float* part_m;   // [ntile, batch, seq] (mean mode)
   int batch, seq, dim, nck, ntile;
-  int nst;  // the caller's state count N (<= the kernel's padded NP): stride of A, B, C rows
+  int nst;    // the caller's state count N (<= the kernel's padded NP): stride of A, B, C rows
+  int dt_sp;  // dt holds the pre-activation: softplus(dt) is read, grad_dt is with respect to dt
 };
 
 // Lane layout: one state per lane; a wave holds SW states (each on 64 / SW lanes, whole
@@ -113,7 +116,7 @@ EDF_DEVICE float pair_swap(float v) {
 // ---------------------------------------------------------------------------
 template <typename TI>
 __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ dt, float* __restrict__ dtm, int rows,
-                                                        int dim) {
+                                                        int dim, int sp) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -125,10 +128,16 @@ __global__ __launch_bounds__(256) void ss_dtmean_kernel(const TI* __restrict__ d
       const uint4 u = *reinterpret_cast<const uint4*>(p + d0);
       const TI* e = reinterpret_cast<const TI*>(&u);
 #pragma unroll
-      for (int i = 0; i < V; ++i) s += clampf(to_f32(e[i]), DT_MIN, DT_MAX);
+      for (int i = 0; i < V; ++i) {
+        const float v = to_f32(e[i]);
+        s += clampf(sp ? softplus_f(v) : v, DT_MIN, DT_MAX);
+      }
     }
   } else {
-    for (int d = lane; d < dim; d += 64) s += clampf(ld(p, d), DT_MIN, DT_MAX);
+    for (int d = lane; d < dim; d += 64) {
+      const float v = ld(p, d);
+      s += clampf(sp ? softplus_f(v) : v, DT_MIN, DT_MAX);
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
@@ -256,7 +265,11 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_fwd_kernel(const SSArgs p
     for (int i = 0; i < EPT; ++i) {
       const bool ok = ev[i] && t0 + et[i] < seq;
       const float xv = bits_f32(rx[slot][i]);
-      const float dtc = ok ? clampf(bits_f32(rdt[slot][i]), DT_MIN, DT_MAX) : 0.0f;
+      float dtr = bits_f32(rdt[slot][i]);
+      if constexpr (MEAN) {  // the softplus flag exists in dt-mean mode only: C2's kernels stay as they were
+        if (p.dt_sp) dtr = softplus_f(dtr);
+      }
+      const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
       if (NE % NT == 0 || tid + i * NT < NE) {
         s_dtc[buf][ec[i]][et[i]] = dtc;
         s_dtx[buf][ec[i]][et[i]] = ok ? (MEAN ? rm[slot][i] : dtc) * xv : 0.0f;
@@ -495,7 +508,10 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
     for (int i = 0; i < EPT; ++i) {
       if (NE % NT != 0 && tid + i * NT >= NE) continue;
       const bool ok = ev[i] && ts + et[i] < seq;
-      const float dtr = bits_f32(rdt[i]);
+      float dtr = bits_f32(rdt[i]);
+      if constexpr (MEAN) {
+        if (p.dt_sp) dtr = softplus_f(dtr);
+      }
       const float dtc = ok ? clampf(dtr, DT_MIN, DT_MAX) : 0.0f;
       const float dtb = ok ? (MEAN ? rm[i] : dtc) : 0.0f;
       const float xv = ok ? bits_f32(rx[i]) : 0.0f;
@@ -649,6 +665,8 @@ __global__ __launch_bounds__((RGeo<N, G>::NT)) void ss_bwd_kernel(const SSArgs p
           bstore<TI>(r_dx, off, fmaf(pxs, dtb, dyp * s_Dv[ac]));
           if (MEAN) s_m[MEAN ? par : 0][MEAN ? tl : 0][ac] = pxs * xv;
         } else {
+          // with the softplus flag (mean mode) the fixup kernel adds the coupling term and
+          // applies the chain factor sigmoid(pre) to the sum
           const float mk = dcr > 0.0f ? 1.0f : 0.0f;
           bstore<TI, BUF_NT>(r_ddt, off, mk * (MEAN ? pas : fmaf(pxs, xv, pas)));
         }
@@ -768,11 +786,12 @@ __global__ __launch_bounds__(256) void ss_reduce_ad_kernel(const float* __restri
 
 // mean mode: ddt[b,t,d] += in_range * (sum over tiles part_m[b,t]) / dim.  One workgroup per
 // row: its threads split the tile partials (in tile order within each thread, then a fixed
-// tree), so the row total is formed once, not by every thread.
+// tree), so the row total is formed once, not by every thread.  sp: dt holds the
+// pre-activation, in_range tests softplus(dt) and the sum is scaled by sigmoid(dt).
 template <typename TI>
 __global__ __launch_bounds__(256) void ss_mean_fixup_kernel(const float* __restrict__ part_m,
                                                             const TI* __restrict__ dt, TI* __restrict__ ddt,
-                                                            int ntile, long rows, int dim) {
+                                                            int ntile, long rows, int dim, int sp) {
   // 16 rows per workgroup.  The tile partials of a row sit `rows` apart (one per channel
   // tile): 16 lanes take 16 consecutive rows and the 16 lane groups a sixteenth of the tiles
   // each, combined in a fixed order; then each wave updates whole rows, 16-byte accesses.
@@ -808,15 +827,18 @@ __global__ __launch_bounds__(256) void ss_mean_fixup_kernel(const float* __restr
         TI* vg = reinterpret_cast<TI*>(&ug);
 #pragma unroll
         for (int i = 0; i < V; ++i) {
-          const float dtr = to_f32(vd[i]);
-          if (dtr >= DT_MIN && dtr <= DT_MAX) vg[i] = (TI)(to_f32(vg[i]) + t);
+          const float raw = to_f32(vd[i]);
+          const float dtr = sp ? softplus_f(raw) : raw;
+          if (dtr >= DT_MIN && dtr <= DT_MAX) vg[i] = (TI)((to_f32(vg[i]) + t) * (sp ? sigmoid_rcp(raw) : 1.0f));
         }
         *reinterpret_cast<uint4*>(ddt + base + d0) = ug;
       }
     } else {
       for (int d = lane; d < dim; d += 64) {
-        const float dtr = ld(dt, base + d);
-        if (dtr >= DT_MIN && dtr <= DT_MAX) st(ddt, base + d, ld(ddt, base + d) + t);
+        const float raw = ld(dt, base + d);
+        const float dtr = sp ? softplus_f(raw) : raw;
+        if (dtr >= DT_MIN && dtr <= DT_MAX)
+          st(ddt, base + d, (ld(ddt, base + d) + t) * (sp ? sigmoid_rcp(raw) : 1.0f));
       }
     }
   }
@@ -1028,8 +1050,11 @@ int check_common(int batch, int seq, int dim, int N, int io, int par, int mode) 
   EDF_REQUIRE(batch > 0 && seq > 0 && dim > 0 && N > 0, EDF_ERR_INVALID_ARG, "dimensions must be positive");
   EDF_REQUIRE(valid_dtype(io) && valid_dtype(par), EDF_ERR_INVALID_ARG, "dtype must be 0 (f32) or 1 (bf16)");
   EDF_REQUIRE(N <= SS_MAX_STATE, EDF_ERR_UNSUPPORTED, "state size %d unsupported (1..%d)", N, SS_MAX_STATE);
-  EDF_REQUIRE(mode == EDF_SS_DT_PER_CHANNEL || mode == EDF_SS_DT_MEAN, EDF_ERR_INVALID_ARG, "unknown dt mode %d",
-              mode);
+  const int base_mode = mode & ~EDF_SS_DT_SOFTPLUS;
+  EDF_REQUIRE(base_mode == EDF_SS_DT_PER_CHANNEL || base_mode == EDF_SS_DT_MEAN, EDF_ERR_INVALID_ARG,
+              "unknown dt mode %d", mode);
+  EDF_REQUIRE(!(mode & EDF_SS_DT_SOFTPLUS) || base_mode == EDF_SS_DT_MEAN, EDF_ERR_UNSUPPORTED,
+              "the dt softplus flag is built for dt-mean mode (the Mamba block's form) only");
   // the kernels address one batch row of x, dt, z, y, dy, dx, ddt, dz (and of B, C and the
   // checkpoints) through buffer resources with 32-bit byte offsets
   EDF_REQUIRE((long)seq * dim * 4 < (1L << 31) && num_chunks(seq) * padded_state(N) * dim * 4 < (1L << 31) &&
@@ -1039,13 +1064,13 @@ int check_common(int batch, int seq, int dim, int N, int io, int par, int mode) 
   return EDF_OK;
 }
 
-int run_dtmean(hipStream_t s, const void* dt, float* dtm, int batch, int seq, int dim, int io) {
+int run_dtmean(hipStream_t s, const void* dt, float* dtm, int batch, int seq, int dim, int io, int sp) {
   const int rows = batch * seq;
   const int grid = (rows + 3) / 4;
   if (io == EDF_BF16)
-    ss_dtmean_kernel<bf16><<<grid, 256, 0, s>>>((const bf16*)dt, dtm, rows, dim);
+    ss_dtmean_kernel<bf16><<<grid, 256, 0, s>>>((const bf16*)dt, dtm, rows, dim, sp);
   else
-    ss_dtmean_kernel<float><<<grid, 256, 0, s>>>((const float*)dt, dtm, rows, dim);
+    ss_dtmean_kernel<float><<<grid, 256, 0, s>>>((const float*)dt, dtm, rows, dim, sp);
   return check_launch("selective scan dt mean");
 }
 
@@ -1061,13 +1086,13 @@ size_t edf_selective_scan_states_bytes(int batch, int seq_len, int hidden, int s
 
 size_t edf_selective_scan_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode) {
   if (batch <= 0 || seq_len <= 0) return 0;
-  return mode == EDF_SS_DT_MEAN ? edf::align256((size_t)batch * seq_len * 4) : 0;
+  return (mode & EDF_SS_DT_MEAN) ? edf::align256((size_t)batch * seq_len * 4) : 0;
 }
 
 size_t edf_selective_scan_backward_workspace_bytes(int batch, int seq_len, int hidden, int state, int mode,
                                                    int have_states) {
   if (batch <= 0 || seq_len <= 0 || hidden <= 0 || state <= 0 || state > edf::SS_MAX_STATE) return 0;
-  return edf::bwd_layout(batch, seq_len, hidden, state, !have_states, mode == EDF_SS_DT_MEAN).total;
+  return edf::bwd_layout(batch, seq_len, hidden, state, !have_states, (mode & EDF_SS_DT_MEAN) != 0).total;
 }
 
 int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const void* A, const void* B, const void* C,
@@ -1088,9 +1113,10 @@ int edf_fused_selective_scan(void* stream, const void* x, const void* dt, const 
   a.ypre = states != nullptr ? (char*)states + ckpt_bytes(batch, seq_len, hidden, state) : nullptr;
   a.batch = batch; a.seq = seq_len; a.dim = hidden; a.nst = state;
   a.nck = (int)num_chunks(seq_len);
-  if (mode == EDF_SS_DT_MEAN) {
+  a.dt_sp = (mode & EDF_SS_DT_SOFTPLUS) != 0;
+  if (mode & EDF_SS_DT_MEAN) {
     a.dtmean = (float*)workspace;
-    rc = run_dtmean(s, dt, (float*)workspace, batch, seq_len, hidden, io_dtype);
+    rc = run_dtmean(s, dt, (float*)workspace, batch, seq_len, hidden, io_dtype, a.dt_sp);
     if (rc) return rc;
   }
   return by_dtypes(io_dtype, param_dtype, [&](auto* ti, auto* tp) {
@@ -1110,7 +1136,7 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   int rc = check_common(batch, seq_len, hidden, state, io_dtype, param_dtype, mode);
   if (rc) return rc;
   EDF_REQUIRE(x && dt && A && B && C && grad_out && grad_x && grad_dt, EDF_ERR_INVALID_ARG, "null tensor pointer");
-  const bool mean_mode = mode == EDF_SS_DT_MEAN;
+  const bool mean_mode = (mode & EDF_SS_DT_MEAN) != 0;
   const WsLayout L = bwd_layout(batch, seq_len, hidden, state, states == nullptr, mean_mode);
   EDF_REQUIRE(workspace && workspace_bytes >= L.total, EDF_ERR_WORKSPACE, "workspace too small: need %zu bytes",
               L.total);
@@ -1120,9 +1146,10 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   a.x = x; a.dt = dt; a.A = A; a.B = B; a.C = C; a.D = D; a.z = z;
   a.batch = batch; a.seq = seq_len; a.dim = hidden; a.nst = state;
   a.nck = (int)num_chunks(seq_len);
+  a.dt_sp = (mode & EDF_SS_DT_SOFTPLUS) != 0;
   if (mean_mode) {
     a.dtmean = (float*)(ws + L.dtmean);
-    rc = run_dtmean(s, dt, (float*)(ws + L.dtmean), batch, seq_len, hidden, io_dtype);
+    rc = run_dtmean(s, dt, (float*)(ws + L.dtmean), batch, seq_len, hidden, io_dtype, a.dt_sp);
     if (rc) return rc;
   }
   if (states != nullptr) {
@@ -1177,11 +1204,11 @@ int edf_fused_selective_scan_backward(void* stream, const void* x, const void* d
   }
   if (mean_mode) {
     if (io_dtype == EDF_BF16)
-      ss_mean_fixup_kernel<bf16><<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a.part_m, (const bf16*)dt, (bf16*)grad_dt, a.ntile,
-                                                                rows, hidden);
+      ss_mean_fixup_kernel<bf16><<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(
+          a.part_m, (const bf16*)dt, (bf16*)grad_dt, a.ntile, rows, hidden, a.dt_sp);
     else
-      ss_mean_fixup_kernel<float><<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(a.part_m, (const float*)dt, (float*)grad_dt,
-                                                                 a.ntile, rows, hidden);
+      ss_mean_fixup_kernel<float><<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(
+          a.part_m, (const float*)dt, (float*)grad_dt, a.ntile, rows, hidden, a.dt_sp);
     rc = check_launch("selective scan dt-mean coupling");
     if (rc) return rc;
   }

@@ -48,15 +48,8 @@ template <> struct SpVec<float> {
   static EDF_DEVICE void st(float* p, const float* v) { *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]); }
 };
 
-// log1p(e^-|x|) from the hardware exp2 / log2: with t = e^-|x| in (0, 1], log2(1 + t) ln 2 for
-// t >= 2^-10 (1 + t is exact to 2^-24), and t (1 - t / 2) below, whose error t^3 / 3 is under
-// 2^-20 of the result; an IEEE log1pf made the pass compute-bound (101 us per 16.8 M values).
-EDF_DEVICE float softplus_f(float x) {
-  constexpr float LN2 = 0.6931471805599453f;
-  const float t = fast_exp2(-fabsf(x) * LOG2E);
-  const float lp = t < 0.0009765625f ? t * fmaf(-0.5f, t, 1.0f) : __builtin_amdgcn_logf(1.0f + t) * LN2;
-  return fmaxf(x, 0.0f) + lp;
-}
+// softplus_f (edf_common.hpp): log1p(e^-|x|) from the hardware exp2 / log2; an IEEE log1pf
+// made the pass compute-bound (101 us per 16.8 M values).
 EDF_DEVICE float sigmoid_f(float x) { return sigmoid_rcp(x); }
 
 // BWD: out = dy sigmoid(x), else out = softplus(x); VEC: 16-byte accesses over n / W vectors

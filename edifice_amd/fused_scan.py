@@ -24,6 +24,7 @@ from ._native import EdificeHipError
 F32, BF16 = 0, 1
 _DT = {torch.float32: F32, torch.bfloat16: BF16}
 SS_DT_PER_CHANNEL, SS_DT_MEAN = 0, 1
+SS_DT_SOFTPLUS = 2  # mode flag: dt is the pre-activation, the kernels take softplus(dt)
 
 
 def dtype_flag(t: torch.Tensor) -> int:
@@ -859,21 +860,22 @@ class _MambaSSM(torch.autograd.Function):
         n2 = 2 * n_state
         b = proj[:, :n_state].float().contiguous().view(bsz, seq, n_state)
         c = proj[:, n_state:n2].float().contiguous().view(bsz, seq, n_state)
-        dt_pre = F.linear(proj[:, n2:], w_dt, b_dt)
-        dt = softplus_forward(dt_pre).view(bsz, seq, inner)
-        out, states = selective_scan_forward(xa, dt, A, b, c, None, z, SS_DT_MEAN, True)
-        ctx.save_for_backward(xa, wcat, proj, w_dt, dt_pre, dt, A, b, c, z, states)
+        # dt = softplus(dt_proj(.)) is applied inside the scan (mode flag): no dt tensor
+        dt_pre = F.linear(proj[:, n2:], w_dt, b_dt).view(bsz, seq, inner)
+        out, states = selective_scan_forward(xa, dt_pre, A, b, c, None, z, SS_DT_MEAN | SS_DT_SOFTPLUS, True)
+        ctx.save_for_backward(xa, wcat, proj, w_dt, dt_pre, A, b, c, z, states)
         ctx.n_state, ctx.has_bcat, ctx.has_bdt = n_state, bcat is not None, b_dt is not None
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        xa, wcat, proj, w_dt, dt_pre, dt, A, b, c, z, states = ctx.saved_tensors
+        xa, wcat, proj, w_dt, dt_pre, A, b, c, z, states = ctx.saved_tensors
         ns, n2 = ctx.n_state, 2 * ctx.n_state
-        rows, inner = dt_pre.shape
-        dxa, ddt, dA, dB, dC, _, dz = selective_scan_backward(xa, dt, A, b, c, None, z, states, dout,
-                                                                 SS_DT_MEAN)
-        ddt_pre = softplus_backward(dt_pre, ddt.view(rows, inner))
+        bsz, seq, inner = dt_pre.shape
+        rows = bsz * seq
+        dxa, ddt, dA, dB, dC, _, dz = selective_scan_backward(xa, dt_pre, A, b, c, None, z, states, dout,
+                                                              SS_DT_MEAN | SS_DT_SOFTPLUS)
+        ddt_pre = ddt.view(rows, inner)
         dproj = torch.empty_like(proj)
         dproj[:, :ns].copy_(dB.view(rows, ns))
         dproj[:, ns:n2].copy_(dC.view(rows, ns))
@@ -1268,13 +1270,17 @@ def gated_delta_net_scan(q, k, v, beta, alpha):
     return _DeltaRule.apply(q, k, v, beta, alpha)
 
 
-def selective_scan(x, dt, a, b, c, d=None, z=None, *, dt_mode: str = "channel"):
+def selective_scan(x, dt, a, b, c, d=None, z=None, *, dt_mode: str = "channel", dt_softplus: bool = False):
     """``FusedScan.selective_scan/5`` (fused_scan.ex:370-384) plus optional D skip and silu(z) gate.
 
     x, dt (and z): [B, T, D]; a: [D, N]; b, c: [B, T, N]; d: [D].  dt is clipped to
     [1e-3, 0.1] inside the kernel.  dt_mode="channel" is the kernel semantics
     (B_bar = dt B per channel, fused_selective_scan.cu:68-90); "mean" is the Mamba
-    block CPU semantics (B_bar = mean_d(dt) B, common.ex:402-445).
+    block CPU semantics (B_bar = mean_d(dt) B, common.ex:402-445).  dt_softplus=True (mean
+    mode only; the library rejects it with "channel"): dt is the pre-activation and the kernels take softplus(dt) wherever they read it (the Mamba
+    block's dt = softplus(dt_proj(.)), common.ex:366), dt's gradient being with respect to
+    the pre-activation (no reference counterpart: the block glue's activation without a
+    pass and a tensor of its own).
     """
-    mode = {"channel": SS_DT_PER_CHANNEL, "mean": SS_DT_MEAN}[dt_mode]
+    mode = {"channel": SS_DT_PER_CHANNEL, "mean": SS_DT_MEAN}[dt_mode] | (SS_DT_SOFTPLUS if dt_softplus else 0)
     return _SelectiveScan.apply(x, dt, a, b, c, d, z, mode)

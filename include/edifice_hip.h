@@ -54,6 +54,13 @@ enum { EDF_F32 = 0, EDF_BF16 = 1 };
  * native/cuda/fused_selective_scan.cu:68-90) or mean over channels
  * (Mamba block CPU semantics, lib/edifice/ssm/common.ex:402-445). */
 enum { EDF_SS_DT_PER_CHANNEL = 0, EDF_SS_DT_MEAN = 1 };
+/* Flag OR-ed into EDF_SS_DT_MEAN (dt-mean mode only; with the per-channel mode the entry
+ * points return EDF_ERR_UNSUPPORTED) for the selective-scan entry points: dt holds the pre-activation,
+ * the kernels take softplus(dt) wherever they read dt (clip, dt mean, in-range masks), and
+ * grad_dt is the gradient with respect to that pre-activation.  No counterpart in the
+ * reference, whose callers pass softplus(dt_proj(.)) (common.ex:366): it is for the block
+ * callers, so the activation is not a pass (and a tensor) of its own. */
+enum { EDF_SS_DT_SOFTPLUS = 2 };
 
 int edf_version(void);
 const char* edf_last_error(void);

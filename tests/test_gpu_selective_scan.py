@@ -75,6 +75,61 @@ def test_selective_scan_fwd_bwd(case, rng):
         assert_close(host(t.grad), g[name], tol, name)
 
 
+SP_CASES = [
+    (2, 45, 32, 16, torch.float32, torch.float32, True, "mean"),
+    (2, 33, 24, 8, torch.float32, torch.float32, False, "mean"),
+    (2, 64, 48, 16, torch.bfloat16, torch.float32, True, "mean"),   # the Mamba block's form
+    (1, 40, 40, 4, torch.bfloat16, torch.bfloat16, True, "mean"),
+]
+
+
+@pytest.mark.parametrize("case", SP_CASES, ids=lambda c: "-".join(str(v).replace("torch.", "") for v in c))
+def test_selective_scan_dt_softplus(case, rng):
+    """dt given before its softplus (dt_softplus=True, the EDF_SS_DT_SOFTPLUS mode flag): y and
+    every gradient against the oracle run on softplus(dt_pre) in float64, dt's gradient chained
+    through sigmoid(dt_pre); dt_pre = N(0, 1) - 4 puts softplus(dt_pre) on both sides of
+    the clip range."""
+    from edifice_amd import fused_scan as fs
+    bsz, T, D, N, io, par, extras, mode = case
+    announce("selective_scan_dt_softplus", case=case)
+    x, _, A, B, C, Dv, z = make_inputs(rng, bsz, T, D, N)
+    if not extras:
+        Dv = z = None
+    dtp = rng.normal(size=x.shape) - 4.0
+    dy = rng.normal(size=x.shape)
+    tx, tdt = to_dev(x, io).requires_grad_(), to_dev(dtp, io).requires_grad_()
+    tz = to_dev(z, io).requires_grad_() if extras else None
+    tA, tB, tC = (to_dev(a, par).requires_grad_() for a in (A, B, C))
+    tD = to_dev(Dv, par).requires_grad_() if extras else None
+    out = fs.selective_scan(tx, tdt, tA, tB, tC, tD, tz, dt_mode=mode, dt_softplus=True)
+    out.backward(to_dev(dy, io))
+
+    xr, dtpr, zr, dyr = (None if a is None else rounded(a, io) for a in (x, dtp, z, dy))
+    Ar, Br, Cr, Dr = (None if a is None else rounded(a, par) for a in (A, B, C, Dv))
+    dtr = np.log1p(np.exp(dtpr))
+    tol = max(TOL[io], TOL[par])
+    assert_close(host(out), scans.selective_scan(xr, dtr, Ar, Br, Cr, Dr, zr, mode), tol, "y")
+    g = scans.selective_scan_backward(xr, dtr, Ar, Br, Cr, dyr, Dr, zr, mode)
+    g["ddt"] = g["ddt"] / (1.0 + np.exp(-dtpr))
+    pairs = [("dx", tx), ("ddt", tdt), ("dA", tA), ("dB", tB), ("dC", tC)]
+    if extras:
+        pairs += [("dD", tD), ("dz", tz)]
+    for name, t in pairs:
+        assert_close(host(t.grad), g[name], tol, name)
+
+
+def test_selective_scan_dt_softplus_needs_mean_mode(rng):
+    """The softplus flag is built for dt-mean mode: with the per-channel mode the library
+    refuses it (EDF_ERR_UNSUPPORTED) rather than reading dt as already activated."""
+    from edifice_amd import fused_scan as fs
+    from edifice_amd._native import EdificeHipError
+    announce("selective_scan_dt_softplus_channel")
+    x, dt, A, B, C, Dv, z = make_inputs(rng, 1, 8, 16, 4)
+    args = [to_dev(a, torch.float32) for a in (x, dt, A, B, C, Dv, z)]
+    with pytest.raises(EdificeHipError, match="dt-mean mode"):
+        fs.selective_scan(*args, dt_mode="channel", dt_softplus=True)
+
+
 def test_selective_scan_config2_full_size_properties(rng):
     """C2 shape (B=8, T=2048, D=1536, N=16, bf16 u/dt/z, f32 A/B/C/D): B == 0 gives
     y == D x silu(z) exactly (size-independent closed form), and one batch row agrees
