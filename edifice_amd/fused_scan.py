@@ -628,7 +628,7 @@ def _heads_split(x, parts, num_heads):
     d = width // (parts * num_heads)
     outs = [x.new_empty(bsz, num_heads, seq, d) for _ in range(parts)]
     if x.numel():
-        ptr, keep = _ptr_array(outs)
+        ptr, _keep = _ptr_array(outs)  # the host array lives until the call returns
         nat.call("edf_heads_split", _stream(), _p(x), ptr, bsz, seq, parts, num_heads, d, dtype_flag(x))
     return outs
 
@@ -637,7 +637,7 @@ def _heads_merge(ts):
     bsz, nh, seq, d = ts[0].shape
     y = ts[0].new_empty(bsz, seq, len(ts) * nh * d)
     if y.numel():
-        ptr, keep = _ptr_array(ts)
+        ptr, _keep = _ptr_array(ts)
         nat.call("edf_heads_merge", _stream(), ptr, _p(y), bsz, seq, len(ts), nh, d, dtype_flag(y))
     return y
 
